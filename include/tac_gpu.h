@@ -1,0 +1,165 @@
+/*
+ * tac_gpu.h — C ABI of the MI355X (gfx950) product-quantization build path.
+ *
+ * Drop-in boundary for the reference's `tac.index.pq` module (Zig):
+ *   pq.train        src/index/pq.zig:158-291   -> tac_pq_train / tac_pq_train_device
+ *   PQ.encode       src/index/pq.zig:59-76, batched the way storage.build drives
+ *                   it (src/index/storage.zig:280-295, :384-401)
+ *                                              -> tac_pq_encode / tac_pq_encode_device
+ *   PQ.decode       src/index/pq.zig:79-88     -> tac_pq_decode
+ *   kmeans.fit      src/tac/kmeans.zig:67-232  -> tac_kmeans_fit
+ *   PqError / KMeansError / RngError (src/index/pq.zig:32-38,
+ *   src/tac/kmeans.zig:56-60, src/util/rng.zig:14-18) -> tac_status
+ *
+ * Rules: plain C types; buffers are owned by the caller; the library never
+ * returns memory it allocated; 0 means success; no exception crosses the ABI.
+ * Calls are thread-safe and serialise per device.  Arguments are validated
+ * (with the reference's error precedence) before any device is touched, so
+ * argument errors are reported the same way on a host without a GPU.
+ *
+ * Shapes: `n` residual vectors of `dim` fp32 values, token-major [n][dim];
+ * `m` subspaces of dsub = dim / m values (1 <= dsub <= 8); `ksub` codewords
+ * per subspace (1 <= ksub <= 1024).  Codebooks are [m][ksub][dsub] fp32
+ * (codebook[((mm * ksub) + c) * dsub + k], src/index/pq.zig:14-15).  Codes are
+ * token-major [n][m], uint8_t when ksub <= 256 and uint16_t otherwise.
+ *
+ * Arithmetic is the reference's: distances are the unfused left fold of
+ * (x_k - c_k)^2, argmin keeps the first index, cluster sums fold members in
+ * ascending vector order from 0.0f and the centroid is sum * fl(1/fl(count)).
+ * Results are bit-identical to the reference for the same inputs.
+ */
+#ifndef TAC_GPU_H
+#define TAC_GPU_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+typedef enum tac_status {
+  TAC_OK = 0,
+  TAC_ERR_DIM_NOT_DIVISIBLE_BY_M = 1,  /* PqError.DimNotDivisibleByM */
+  TAC_ERR_DIM_MISMATCH = 2,            /* PqError.DimMismatch, KMeansError.DimMismatch */
+  TAC_ERR_EMPTY_CORPUS = 3,            /* PqError.EmptyCorpus */
+  TAC_ERR_OUT_BUFFER_WRONG_SIZE = 4,   /* PqError.OutBufferWrongSize */
+  TAC_ERR_NQ_MISMATCH = 5,             /* PqError.NQMismatch */
+  TAC_ERR_KMEANS_BUDGET_TOO_SMALL = 6, /* KMeansError.KmeansBudgetTooSmall */
+  TAC_ERR_EMPTY_VECTOR_SET = 7,        /* KMeansError.EmptyVectorSet */
+  TAC_ERR_RNG_EMPTY_DISTRIBUTION = 8,  /* RngError.EmptyDistribution */
+  TAC_ERR_RNG_NON_FINITE = 9,          /* RngError.NonFinite */
+  TAC_ERR_RNG_ALL_ZERO = 10,           /* RngError.AllZero */
+  TAC_ERR_OUT_OF_MEMORY = 11,          /* Allocator.Error.OutOfMemory */
+  TAC_ERR_NO_DEVICE = 12,              /* no usable HIP device */
+  TAC_ERR_HIP = 13,                    /* HIP runtime error; see tac_gpu_last_error */
+  TAC_ERR_INVALID_ARGUMENT = 14,       /* null pointer / shape outside the limits above */
+  TAC_ERR_UNSUPPORTED = 15             /* valid request this build does not implement */
+} tac_status;
+
+/* Never-break iteration control: pass as `tol` to run exactly max_iters. */
+#define TAC_TOL_NEVER (-__builtin_inff())
+
+/* Human-readable name of a status ("DimNotDivisibleByM", ...). */
+const char *tac_gpu_strerror(int status);
+/* Detail of the last TAC_ERR_HIP / TAC_ERR_OUT_OF_MEMORY on this thread. */
+const char *tac_gpu_last_error(void);
+
+/* ---- devices and memory (helpers for callers without a HIP binding) ---- */
+int tac_gpu_device_count(int *count);
+typedef struct tac_gpu_device_info {
+  char name[256];
+  char arch[64];            /* e.g. "gfx950:sramecc+:xnack-" */
+  int compute_units;
+  int clock_khz;
+  uint64_t global_mem_bytes;
+  uint64_t lds_bytes_per_block;
+} tac_gpu_device_info;
+int tac_gpu_get_device_info(int device, tac_gpu_device_info *info);
+int tac_gpu_set_device(int device);
+int tac_gpu_malloc(void **ptr, uint64_t bytes);
+int tac_gpu_free(void *ptr);
+int tac_gpu_memcpy_htod(void *dst, const void *src, uint64_t bytes);
+int tac_gpu_memcpy_dtoh(void *dst, const void *src, uint64_t bytes);
+int tac_gpu_memcpy_dtod(void *dst, const void *src, uint64_t bytes);
+int tac_gpu_synchronize(void);
+/* Release the per-device workspace the library caches between calls. */
+int tac_gpu_release_workspace(void);
+
+/* ---- optional outputs of training (every pointer may be NULL) ---------- */
+typedef struct tac_pq_train_extras {
+  uint32_t *iters_run; /* host [m]: Lloyd iterations run per subspace (KMeansResult.iters_run) */
+  float *wcss;         /* host [m]: wcss of each subspace's last iteration (KMeansResult.wcss) */
+  uint32_t *empties;   /* host [m]: empty clusters reseeded, summed over iterations */
+  float *trace;        /* host [max_iters][m][ksub][dsub]: codebooks after each iteration;
+                          iterations a subspace did not run repeat its final codebook */
+} tac_pq_train_extras;
+
+/*
+ * pq.train (src/index/pq.zig:158-291) with runtime m / ksub and iteration
+ * control.  Each subspace runs kmeans.fit with k = ksub
+ * (src/index/pq.zig:301-336):
+ *   - init_codebooks [m][ksub][dsub] seeds the Lloyd loop; NULL selects the
+ *     reference's k-means++ seeding with seed +% subspace (TAC_ERR_UNSUPPORTED
+ *     in this build);
+ *   - tol = 1e-4f, max_iters = 25 are the reference's values
+ *     (src/index/pq.zig:319-325); TAC_TOL_NEVER runs exactly max_iters;
+ *   - n <= ksub takes the degenerate branch (src/tac/kmeans.zig:88-104).
+ * Host pointers; the device copy of the residuals lives only for the call.
+ */
+int tac_pq_train(const float *residuals, uint64_t n, uint32_t dim, uint32_t m,
+                 uint32_t ksub, const float *init_codebooks, uint64_t seed,
+                 uint32_t max_iters, float tol, float *codebooks_out,
+                 tac_pq_train_extras *extras);
+
+/* Same, with residuals, init codebooks and the output in device memory.
+ * `stream` is a hipStream_t (NULL: the library's stream for the device). */
+int tac_pq_train_device(const float *d_residuals, uint64_t n, uint32_t dim,
+                        uint32_t m, uint32_t ksub, const float *d_init_codebooks,
+                        uint64_t seed, uint32_t max_iters, float tol,
+                        float *d_codebooks_out, tac_pq_train_extras *extras,
+                        void *stream);
+
+/*
+ * PQ.encode (src/index/pq.zig:59-76) for n residuals at once, as
+ * storage.build drives it (src/index/storage.zig:384-401): codes_out is
+ * token-major [n][m] (uint8_t for ksub <= 256, else uint16_t).
+ */
+int tac_pq_encode(const float *residuals, uint64_t n, uint32_t dim, uint32_t m,
+                  uint32_t ksub, const float *codebooks, void *codes_out);
+int tac_pq_encode_device(const float *d_residuals, uint64_t n, uint32_t dim,
+                         uint32_t m, uint32_t ksub, const float *d_codebooks,
+                         void *d_codes_out, void *stream);
+
+/* PQ.decode (src/index/pq.zig:79-88) for n code rows: out [n][dim]. */
+int tac_pq_decode(const void *codes, uint64_t n, uint32_t dim, uint32_t m,
+                  uint32_t ksub, const float *codebooks, float *out);
+
+/*
+ * kmeans.fit (src/tac/kmeans.zig:67-232) for one set of vectors of dim <= 8:
+ * centroids_out [k][dim], assignments_out [n] (the last iteration's
+ * assignment, KMeansResult.assignments), wcss_out and iters_run_out.
+ * init_centroids NULL selects k-means++ (TAC_ERR_UNSUPPORTED in this build).
+ */
+int tac_kmeans_fit(const float *vectors, uint64_t n, uint32_t dim, uint32_t k,
+                   uint32_t max_iters, float tol, uint64_t seed,
+                   const float *init_centroids, float *centroids_out,
+                   uint32_t *assignments_out, float *wcss_out,
+                   uint32_t *iters_run_out);
+
+/* ---- measurement -------------------------------------------------------- */
+/* When enabled, the library brackets its kernels with HIP events on the
+ * stream they run on and accumulates their durations. */
+typedef struct tac_gpu_profile {
+  double transpose_ms;   uint64_t transpose_launches;
+  double assign_ms;      uint64_t assign_launches;   /* Lloyd assignment kernel */
+  double update_ms;      uint64_t update_iters;      /* sort + fold + reseed + convergence */
+  double encode_ms;      uint64_t encode_launches;   /* encode kernel */
+} tac_gpu_profile;
+int tac_gpu_profile_enable(int enable);
+int tac_gpu_profile_read(tac_gpu_profile *out, int reset);
+
+#ifdef __cplusplus
+}
+#endif
+#endif /* TAC_GPU_H */

@@ -1,0 +1,806 @@
+// tac_gpu.hip — C ABI and host driver of the gfx950 PQ build path.
+//
+// Reference interfaces replaced (paths in the reference repository):
+//   pq.train     src/index/pq.zig:158-336
+//   PQ.encode    src/index/pq.zig:59-76 (batched as src/index/storage.zig:384-401)
+//   PQ.decode    src/index/pq.zig:79-88
+//   kmeans.fit   src/tac/kmeans.zig:67-365
+//
+// One training call keeps the residuals resident in HBM as a subspace-major
+// copy and runs every Lloyd iteration of all subspaces as a fixed sequence of
+// kernels on one stream:
+//   assign -> tile histogram -> scan -> stable scatter -> serial fold
+//   -> (wcss fold) -> empty reseed -> convergence flags
+// Subspaces that converged are skipped by every later kernel through a
+// per-subspace flag, so the host never waits inside the loop.
+#include "../../include/tac_gpu.h"
+#include "pq_kernels.hpp"
+
+#include <hip/hip_runtime.h>
+
+#include <cmath>
+#include <cstdio>
+#include <cstring>
+#include <mutex>
+#include <string>
+#include <vector>
+
+using namespace tacgpu;
+
+namespace {
+
+thread_local std::string g_last_error;
+
+constexpr uint32_t kMaxDsub = 8;
+constexpr uint32_t kMaxKsub = 1024;
+constexpr int kMaxDevices = 64;
+
+struct HipFailure {
+  hipError_t err;
+};
+
+void set_error(const char *what, hipError_t e) {
+  g_last_error = std::string(what) + ": " + hipGetErrorName(e) + " (" + hipGetErrorString(e) + ")";
+}
+
+int hip_status(const char *what, hipError_t e) {
+  set_error(what, e);
+  return e == hipErrorOutOfMemory ? TAC_ERR_OUT_OF_MEMORY : TAC_ERR_HIP;
+}
+
+#define HIP_TRY(expr)                                            \
+  do {                                                           \
+    hipError_t _e = (expr);                                      \
+    if (_e != hipSuccess) return hip_status(#expr, _e);          \
+  } while (0)
+
+#define LAUNCH_TRY(what)                                         \
+  do {                                                           \
+    hipError_t _e = hipGetLastError();                           \
+    if (_e != hipSuccess) return hip_status(what, _e);           \
+  } while (0)
+
+struct Buffer {
+  void *ptr = nullptr;
+  size_t bytes = 0;
+};
+
+struct EventPair {
+  hipEvent_t a = nullptr, b = nullptr;
+};
+
+struct DeviceState {
+  std::mutex mu;
+  hipStream_t own_stream = nullptr;
+  hipStream_t last_stream = nullptr;
+  hipEvent_t last_done = nullptr;
+  // training / encode workspace
+  Buffer xs, codes, e, hist, counts, start, sorted, flags, scal, trace, io_in, io_out, io_cb,
+      io_init;
+  // measurement
+  std::vector<hipEvent_t> events;
+};
+
+DeviceState *g_devices[kMaxDevices] = {};
+std::mutex g_devices_mu;
+bool g_profile = false;
+std::mutex g_profile_mu;
+tac_gpu_profile g_prof = {};
+
+int device_count() {
+  int c = 0;
+  const hipError_t e = hipGetDeviceCount(&c);
+  if (e != hipSuccess) {
+    set_error("hipGetDeviceCount", e);
+    return 0;
+  }
+  return c;
+}
+
+// Current device's state; NO_DEVICE when HIP reports none.
+int acquire_device(DeviceState **out, int *dev_out) {
+  if (device_count() <= 0) return TAC_ERR_NO_DEVICE;
+  int dev = 0;
+  HIP_TRY(hipGetDevice(&dev));
+  if (dev < 0 || dev >= kMaxDevices) return TAC_ERR_NO_DEVICE;
+  std::lock_guard<std::mutex> g(g_devices_mu);
+  if (!g_devices[dev]) g_devices[dev] = new DeviceState();
+  *out = g_devices[dev];
+  if (dev_out) *dev_out = dev;
+  return TAC_OK;
+}
+
+int ensure(DeviceState &ds, Buffer &b, size_t bytes) {
+  if (bytes <= b.bytes) return TAC_OK;
+  if (b.ptr) {
+    if (ds.last_stream) HIP_TRY(hipStreamSynchronize(ds.last_stream));
+    HIP_TRY(hipFree(b.ptr));
+    b.ptr = nullptr;
+    b.bytes = 0;
+  }
+  size_t want = bytes < 4096 ? 4096 : bytes;
+  want = (want + 4095) & ~size_t(4095);
+  const hipError_t e = hipMalloc(&b.ptr, want);
+  if (e != hipSuccess) {
+    b.ptr = nullptr;
+    return hip_status("hipMalloc(workspace)", e);
+  }
+  b.bytes = want;
+  return TAC_OK;
+}
+
+// Order this call after the previous one that used the workspace.
+int begin_call(DeviceState &ds, hipStream_t s) {
+  if (!ds.last_done) HIP_TRY(hipEventCreateWithFlags(&ds.last_done, hipEventDisableTiming));
+  if (ds.last_stream && ds.last_stream != s) HIP_TRY(hipStreamWaitEvent(s, ds.last_done, 0));
+  ds.last_stream = s;
+  return TAC_OK;
+}
+
+int end_call(DeviceState &ds, hipStream_t s) {
+  HIP_TRY(hipEventRecord(ds.last_done, s));
+  return TAC_OK;
+}
+
+int resolve_stream(DeviceState &ds, void *stream, hipStream_t *out) {
+  if (stream) {
+    *out = reinterpret_cast<hipStream_t>(stream);
+    return TAC_OK;
+  }
+  // A blocking stream: work on it is ordered with the null stream, so the
+  // synchronous tac_gpu_memcpy_* helpers see finished results.
+  if (!ds.own_stream) HIP_TRY(hipStreamCreateWithFlags(&ds.own_stream, hipStreamDefault));
+  *out = ds.own_stream;
+  return TAC_OK;
+}
+
+int event_at(DeviceState &ds, size_t idx, hipEvent_t *out) {
+  while (ds.events.size() <= idx) {
+    hipEvent_t ev;
+    HIP_TRY(hipEventCreate(&ev));
+    ds.events.push_back(ev);
+  }
+  *out = ds.events[idx];
+  return TAC_OK;
+}
+
+uint32_t pad_of(uint32_t d) { return d <= 1 ? 1 : d <= 2 ? 2 : d <= 4 ? 4 : 8; }
+
+uint32_t code_bits(uint32_t K) {
+  uint32_t b = 0;
+  while ((1u << b) < K) ++b;
+  return b;
+}
+
+// ---- argument validation with the reference's precedence ----------------
+
+// src/index/pq.zig:165-168, plus this build's shape limits.
+int validate_pq(uint64_t n, uint32_t dim, uint32_t m, uint32_t ksub) {
+  if (m == 0) return TAC_ERR_INVALID_ARGUMENT;
+  if (dim == 0) return TAC_ERR_DIM_MISMATCH;
+  if (dim % m != 0) return TAC_ERR_DIM_NOT_DIVISIBLE_BY_M;
+  if (n == 0) return TAC_ERR_EMPTY_CORPUS;
+  if (ksub == 0) return TAC_ERR_KMEANS_BUDGET_TOO_SMALL;
+  const uint32_t dsub = dim / m;
+  if (dsub > kMaxDsub || ksub > kMaxKsub) return TAC_ERR_UNSUPPORTED;
+  if (n > 0xFFFFFFFFull) return TAC_ERR_UNSUPPORTED;
+  return TAC_OK;
+}
+
+// ---- kernel launchers -------------------------------------------------------
+
+template <int D>
+struct Launch {
+  static constexpr int VPT = D <= 2 ? 8 : D <= 4 ? 4 : 2;
+
+  static void transpose(const float *x, float *xs, uint64_t n, uint32_t dim, uint32_t M,
+                        hipStream_t s) {
+    dim3 grid((unsigned)((n + kBlock - 1) / kBlock), M);
+    transpose_kernel<D><<<grid, kBlock, 0, s>>>(x, xs, n, dim);
+  }
+  static void assign(const float *xs, const float *cb, uint16_t *codes, float *e,
+                     const uint32_t *done, uint64_t n, uint32_t M, uint32_t K, hipStream_t s) {
+    dim3 grid((unsigned)((n + kBlock * VPT - 1) / (kBlock * VPT)), M);
+    const size_t lds = (size_t)K * Pad<D>::value * sizeof(float);
+    assign_kernel<D, VPT><<<grid, kBlock, lds, s>>>(xs, cb, codes, e, done, n, K);
+  }
+  static void scatter(const float *xs, const uint16_t *codes, const uint32_t *hist,
+                      const uint32_t *start, float *sorted, const uint32_t *done, uint64_t n,
+                      uint32_t M, uint32_t K, uint32_t T, hipStream_t s) {
+    dim3 grid(T, M);
+    scatter_kernel<D><<<grid, kBlock, 4 * K * sizeof(uint32_t), s>>>(
+        xs, codes, hist, start, sorted, done, n, K, T, code_bits(K));
+  }
+  static void fold(const float *sorted, const uint32_t *counts, const uint32_t *start,
+                   float *cb, const uint32_t *done, uint64_t n, uint32_t M, uint32_t K,
+                   hipStream_t s) {
+    const uint64_t lanes = (uint64_t)M * D * K;
+    fold_kernel<D><<<(unsigned)((lanes + kBlock - 1) / kBlock), kBlock, 0, s>>>(
+        sorted, counts, start, cb, done, n, M, K);
+  }
+  static void reseed(const float *xs, float *e, const uint32_t *counts, float *cb,
+                     uint32_t *empties, const uint32_t *done, uint64_t n, uint32_t M, uint32_t K,
+                     hipStream_t s) {
+    reseed_kernel<D><<<M, 1024, 0, s>>>(xs, e, counts, cb, empties, done, n, K);
+  }
+  template <typename CodeT>
+  static int encode(const float *x, const float *cb, CodeT *codes, uint64_t n, uint32_t dim,
+                    uint32_t M, uint32_t K, hipStream_t s) {
+    const size_t cb_lds = (size_t)K * Pad<D>::value * sizeof(float);
+    const size_t per_row = (size_t)M * sizeof(CodeT);
+    if (per_row * kBlock * 2 + cb_lds <= 65536) {
+      constexpr int V = 2;
+      const size_t lds = cb_lds + per_row * kBlock * V;
+      encode_kernel<D, V, CodeT><<<(unsigned)((n + kBlock * V - 1) / (kBlock * V)), kBlock, lds,
+                                   s>>>(x, cb, codes, n, dim, M, K);
+    } else if (per_row * kBlock + cb_lds <= 65536) {
+      const size_t lds = cb_lds + per_row * kBlock;
+      encode_kernel<D, 1, CodeT><<<(unsigned)((n + kBlock - 1) / kBlock), kBlock, lds, s>>>(
+          x, cb, codes, n, dim, M, K);
+    } else {
+      return TAC_ERR_UNSUPPORTED;
+    }
+    return TAC_OK;
+  }
+};
+
+#define DISPATCH_D_ST(D_, CALL)                          \
+  switch (D_) {                                          \
+    case 1: st = Launch<1>::CALL; break;                 \
+    case 2: st = Launch<2>::CALL; break;                 \
+    case 3: st = Launch<3>::CALL; break;                 \
+    case 4: st = Launch<4>::CALL; break;                 \
+    case 5: st = Launch<5>::CALL; break;                 \
+    case 6: st = Launch<6>::CALL; break;                 \
+    case 7: st = Launch<7>::CALL; break;                 \
+    case 8: st = Launch<8>::CALL; break;                 \
+    default: st = TAC_ERR_UNSUPPORTED;                   \
+  }
+
+#define DISPATCH_D(D_, CALL)                 \
+  switch (D_) {                              \
+    case 1: { Launch<1>::CALL; } break;      \
+    case 2: { Launch<2>::CALL; } break;      \
+    case 3: { Launch<3>::CALL; } break;      \
+    case 4: { Launch<4>::CALL; } break;      \
+    case 5: { Launch<5>::CALL; } break;      \
+    case 6: { Launch<6>::CALL; } break;      \
+    case 7: { Launch<7>::CALL; } break;      \
+    case 8: { Launch<8>::CALL; } break;      \
+    default: return TAC_ERR_UNSUPPORTED;     \
+  }
+
+template <typename T>
+T *as(Buffer &b) {
+  return reinterpret_cast<T *>(b.ptr);
+}
+
+struct TrainOut {
+  float *cb;                 // device [M][K][D]: init in, result out
+  uint32_t *d_assign;        // device [n] u32 (M == 1) or null
+  tac_pq_train_extras *ex;   // host extras or null
+  float *h_wcss_single;      // host scalar (kmeans.fit) or null
+  uint32_t *h_iters_single;  // host scalar (kmeans.fit) or null
+};
+
+// Lloyd training of all subspaces.  `out.cb` holds the initial codebooks on
+// entry and the trained ones on return.
+int train_core(DeviceState &ds, hipStream_t s, const float *d_x, uint64_t n, uint32_t dim,
+               uint32_t M, uint32_t K, uint32_t max_iters, float tol, const TrainOut &out) {
+  const uint32_t D = dim / M;
+  const uint32_t DP = pad_of(D);
+  tac_pq_train_extras *ex = out.ex;
+  const bool want_trace = ex && ex->trace && max_iters > 0;
+  const size_t cb_elems = (size_t)M * K * D;
+
+  // Degenerate branch: k >= n (src/tac/kmeans.zig:88-104).
+  if ((uint64_t)K >= n) {
+    const uint64_t total = cb_elems;
+    degenerate_kernel<<<(unsigned)((total + 255) / 256), 256, 0, s>>>(d_x, out.cb, n, dim, M, K,
+                                                                       D);
+    LAUNCH_TRY("degenerate_kernel");
+    if (out.d_assign) {
+      std::vector<uint32_t> iota(n);
+      for (uint64_t i = 0; i < n; ++i) iota[i] = (uint32_t)i;
+      HIP_TRY(hipMemcpyAsync(out.d_assign, iota.data(), n * sizeof(uint32_t),
+                             hipMemcpyHostToDevice, s));
+      HIP_TRY(hipStreamSynchronize(s));
+    }
+    if (ex) {
+      if (ex->iters_run) std::fill(ex->iters_run, ex->iters_run + M, 0u);
+      if (ex->wcss) std::fill(ex->wcss, ex->wcss + M, 0.0f);
+      if (ex->empties) std::fill(ex->empties, ex->empties + M, 0u);
+      if (want_trace) {
+        HIP_TRY(hipStreamSynchronize(s));
+        for (uint32_t t = 0; t < max_iters; ++t)
+          HIP_TRY(hipMemcpy(ex->trace + (size_t)t * cb_elems, out.cb, cb_elems * sizeof(float),
+                            hipMemcpyDeviceToHost));
+      }
+    }
+    if (out.h_wcss_single) *out.h_wcss_single = 0.0f;
+    if (out.h_iters_single) *out.h_iters_single = 0;
+    return TAC_OK;
+  }
+
+  const uint32_t T = (uint32_t)((n + kScatterTile - 1) / kScatterTile);
+  int st;
+  if ((st = ensure(ds, ds.xs, (size_t)M * n * DP * sizeof(float)))) return st;
+  if ((st = ensure(ds, ds.codes, (size_t)M * n * sizeof(uint16_t)))) return st;
+  if ((st = ensure(ds, ds.e, (size_t)M * n * sizeof(float)))) return st;
+  if ((st = ensure(ds, ds.hist, (size_t)M * T * K * sizeof(uint32_t)))) return st;
+  if ((st = ensure(ds, ds.counts, (size_t)M * K * sizeof(uint32_t)))) return st;
+  if ((st = ensure(ds, ds.start, (size_t)M * K * sizeof(uint32_t)))) return st;
+  if ((st = ensure(ds, ds.sorted, (size_t)M * D * n * sizeof(float)))) return st;
+  if ((st = ensure(ds, ds.flags, (size_t)3 * M * sizeof(uint32_t)))) return st;
+  if ((st = ensure(ds, ds.scal, (size_t)2 * M * sizeof(float)))) return st;
+  if (want_trace && (st = ensure(ds, ds.trace, (size_t)max_iters * cb_elems * sizeof(float))))
+    return st;
+
+  float *xs = as<float>(ds.xs);
+  uint16_t *codes = as<uint16_t>(ds.codes);
+  float *e = as<float>(ds.e);
+  uint32_t *hist = as<uint32_t>(ds.hist);
+  uint32_t *counts = as<uint32_t>(ds.counts);
+  uint32_t *start = as<uint32_t>(ds.start);
+  float *sorted = as<float>(ds.sorted);
+  uint32_t *done = as<uint32_t>(ds.flags);
+  uint32_t *iters_run = done + M;
+  uint32_t *empties = done + 2 * M;
+  float *wcss = as<float>(ds.scal);
+  float *prev = wcss + M;
+  HIP_TRY(hipMemsetAsync(done, 0, 3 * M * sizeof(uint32_t), s));
+  HIP_TRY(hipMemsetAsync(wcss, 0, 2 * M * sizeof(float), s));
+
+  const bool profile = g_profile;
+  size_t ev = 0;
+  hipEvent_t e0 = nullptr, e1 = nullptr;
+  if (profile) {
+    if ((st = event_at(ds, ev++, &e0))) return st;
+    HIP_TRY(hipEventRecord(e0, s));
+  }
+  DISPATCH_D(D, transpose(d_x, xs, n, dim, M, s));
+  LAUNCH_TRY("transpose_kernel");
+  if (profile) {
+    if ((st = event_at(ds, ev++, &e1))) return st;
+    HIP_TRY(hipEventRecord(e1, s));
+  }
+
+  // The reference breaks on rel < tol; only a tol above -inf can ever fire.
+  const bool check = tol > -INFINITY;
+  const bool want_wcss = (ex && ex->wcss) || out.h_wcss_single;
+  const size_t hist_lds = (size_t)K * sizeof(uint32_t);
+  std::vector<size_t> it_events;  // event index triples per iteration
+  for (uint32_t t = 0; t < max_iters; ++t) {
+    hipEvent_t a = nullptr, b = nullptr, c = nullptr;
+    if (profile) {
+      it_events.push_back(ev);
+      if ((st = event_at(ds, ev++, &a)) || (st = event_at(ds, ev++, &b)) ||
+          (st = event_at(ds, ev++, &c)))
+        return st;
+      HIP_TRY(hipEventRecord(a, s));
+    }
+    DISPATCH_D(D, assign(xs, out.cb, codes, e, done, n, M, K, s));
+    LAUNCH_TRY("assign_kernel");
+    if (profile) HIP_TRY(hipEventRecord(b, s));
+    hist_kernel<<<dim3(T, M), kBlock, hist_lds, s>>>(codes, hist, done, n, K, T);
+    LAUNCH_TRY("hist_kernel");
+    scan_kernel<<<M, 1024, 0, s>>>(hist, counts, start, done, K, T);
+    LAUNCH_TRY("scan_kernel");
+    DISPATCH_D(D, scatter(xs, codes, hist, start, sorted, done, n, M, K, T, s));
+    LAUNCH_TRY("scatter_kernel");
+    DISPATCH_D(D, fold(sorted, counts, start, out.cb, done, n, M, K, s));
+    LAUNCH_TRY("fold_kernel");
+    if (check || (want_wcss && t + 1 == max_iters)) {
+      wcss_kernel<<<M, kWave, 0, s>>>(e, wcss, done, n);
+      LAUNCH_TRY("wcss_kernel");
+    }
+    DISPATCH_D(D, reseed(xs, e, counts, out.cb, empties, done, n, M, K, s));
+    LAUNCH_TRY("reseed_kernel");
+    converge_kernel<<<(M + 63) / 64, 64, 0, s>>>(wcss, prev, done, iters_run, M, t, tol,
+                                                   check ? 1 : 0);
+    LAUNCH_TRY("converge_kernel");
+    if (want_trace)
+      HIP_TRY(hipMemcpyAsync(as<float>(ds.trace) + (size_t)t * cb_elems, out.cb,
+                             cb_elems * sizeof(float), hipMemcpyDeviceToDevice, s));
+    if (profile) HIP_TRY(hipEventRecord(c, s));
+  }
+  if (out.d_assign && max_iters == 0) HIP_TRY(hipMemsetAsync(codes, 0, n * sizeof(uint16_t), s));
+  if (out.d_assign) {
+    widen_codes_kernel<<<(unsigned)((n + 255) / 256), 256, 0, s>>>(codes, out.d_assign, n);
+    LAUNCH_TRY("widen_codes_kernel");
+  }
+
+  const bool need_host = profile || ex || out.h_wcss_single || out.h_iters_single;
+  if (need_host) {
+    std::vector<uint32_t> h_flags(3 * M);
+    std::vector<float> h_scal(2 * M);
+    HIP_TRY(hipMemcpyAsync(h_flags.data(), done, 3 * M * sizeof(uint32_t),
+                           hipMemcpyDeviceToHost, s));
+    HIP_TRY(hipMemcpyAsync(h_scal.data(), wcss, 2 * M * sizeof(float), hipMemcpyDeviceToHost,
+                           s));
+    HIP_TRY(hipStreamSynchronize(s));
+    if (ex) {
+      if (ex->iters_run) std::memcpy(ex->iters_run, &h_flags[M], M * sizeof(uint32_t));
+      if (ex->empties) std::memcpy(ex->empties, &h_flags[2 * M], M * sizeof(uint32_t));
+      if (ex->wcss) std::memcpy(ex->wcss, &h_scal[0], M * sizeof(float));
+      if (want_trace) {
+        HIP_TRY(hipMemcpy(ex->trace, ds.trace.ptr, (size_t)max_iters * cb_elems * sizeof(float),
+                          hipMemcpyDeviceToHost));
+        // Iterations a converged subspace skipped repeat its final codebook.
+        for (uint32_t m = 0; m < M; ++m) {
+          const uint32_t ran = h_flags[M + m];
+          for (uint32_t t = ran; t < max_iters; ++t)
+            if (ran > 0)
+              std::memcpy(ex->trace + ((size_t)t * M + m) * K * D,
+                          ex->trace + ((size_t)(ran - 1) * M + m) * K * D,
+                          (size_t)K * D * sizeof(float));
+        }
+      }
+    }
+    if (out.h_wcss_single) *out.h_wcss_single = h_scal[0];
+    if (out.h_iters_single) *out.h_iters_single = h_flags[M];
+    if (profile) {
+      std::lock_guard<std::mutex> g(g_profile_mu);
+      float ms = 0.0f;
+      HIP_TRY(hipEventElapsedTime(&ms, e0, e1));
+      g_prof.transpose_ms += ms;
+      g_prof.transpose_launches += 1;
+      for (size_t q : it_events) {
+        HIP_TRY(hipEventElapsedTime(&ms, ds.events[q], ds.events[q + 1]));
+        g_prof.assign_ms += ms;
+        g_prof.assign_launches += 1;
+        HIP_TRY(hipEventElapsedTime(&ms, ds.events[q + 1], ds.events[q + 2]));
+        g_prof.update_ms += ms;
+        g_prof.update_iters += 1;
+      }
+    }
+  }
+  return TAC_OK;
+}
+
+int encode_core(DeviceState &ds, hipStream_t s, const float *d_x, uint64_t n, uint32_t dim,
+                uint32_t M, uint32_t K, const float *d_cb, void *d_codes) {
+  const uint32_t D = dim / M;
+  const bool profile = g_profile;
+  hipEvent_t a = nullptr, b = nullptr;
+  int st;
+  if (profile) {
+    if ((st = event_at(ds, 0, &a)) || (st = event_at(ds, 1, &b))) return st;
+    HIP_TRY(hipEventRecord(a, s));
+  }
+  st = TAC_OK;
+  if (K <= 256) {
+    DISPATCH_D_ST(D, encode<uint8_t>(d_x, d_cb, (uint8_t *)d_codes, n, dim, M, K, s));
+  } else {
+    DISPATCH_D_ST(D, encode<uint16_t>(d_x, d_cb, (uint16_t *)d_codes, n, dim, M, K, s));
+  }
+  if (st) return st;
+  LAUNCH_TRY("encode_kernel");
+  if (profile) {
+    HIP_TRY(hipEventRecord(b, s));
+    HIP_TRY(hipEventSynchronize(b));
+    float ms = 0.0f;
+    HIP_TRY(hipEventElapsedTime(&ms, a, b));
+    std::lock_guard<std::mutex> g(g_profile_mu);
+    g_prof.encode_ms += ms;
+    g_prof.encode_launches += 1;
+  }
+  return TAC_OK;
+}
+
+const char *kNames[] = {"Ok",
+                        "DimNotDivisibleByM",
+                        "DimMismatch",
+                        "EmptyCorpus",
+                        "OutBufferWrongSize",
+                        "NQMismatch",
+                        "KmeansBudgetTooSmall",
+                        "EmptyVectorSet",
+                        "EmptyDistribution",
+                        "NonFinite",
+                        "AllZero",
+                        "OutOfMemory",
+                        "NoDevice",
+                        "HipError",
+                        "InvalidArgument",
+                        "Unsupported"};
+
+}  // namespace
+
+// ===========================================================================
+// C ABI
+// ===========================================================================
+extern "C" {
+
+const char *tac_gpu_strerror(int status) {
+  if (status < 0 || status >= (int)(sizeof(kNames) / sizeof(kNames[0]))) return "Unknown";
+  return kNames[status];
+}
+
+const char *tac_gpu_last_error(void) { return g_last_error.c_str(); }
+
+int tac_gpu_device_count(int *count) {
+  if (!count) return TAC_ERR_INVALID_ARGUMENT;
+  *count = device_count();
+  return *count > 0 ? TAC_OK : TAC_ERR_NO_DEVICE;
+}
+
+int tac_gpu_get_device_info(int device, tac_gpu_device_info *info) {
+  if (!info) return TAC_ERR_INVALID_ARGUMENT;
+  const int c = device_count();
+  if (c <= 0) return TAC_ERR_NO_DEVICE;
+  if (device < 0 || device >= c) return TAC_ERR_INVALID_ARGUMENT;
+  hipDeviceProp_t p;
+  HIP_TRY(hipGetDeviceProperties(&p, device));
+  std::memset(info, 0, sizeof(*info));
+  std::snprintf(info->name, sizeof(info->name), "%s", p.name);
+  std::snprintf(info->arch, sizeof(info->arch), "%s", p.gcnArchName);
+  info->compute_units = p.multiProcessorCount;
+  info->clock_khz = p.clockRate;
+  info->global_mem_bytes = p.totalGlobalMem;
+  info->lds_bytes_per_block = p.sharedMemPerBlock;
+  return TAC_OK;
+}
+
+int tac_gpu_set_device(int device) {
+  const int c = device_count();
+  if (c <= 0) return TAC_ERR_NO_DEVICE;
+  if (device < 0 || device >= c) return TAC_ERR_INVALID_ARGUMENT;
+  HIP_TRY(hipSetDevice(device));
+  return TAC_OK;
+}
+
+int tac_gpu_malloc(void **ptr, uint64_t bytes) {
+  if (!ptr) return TAC_ERR_INVALID_ARGUMENT;
+  *ptr = nullptr;
+  if (device_count() <= 0) return TAC_ERR_NO_DEVICE;
+  HIP_TRY(hipMalloc(ptr, bytes ? bytes : 1));
+  return TAC_OK;
+}
+
+int tac_gpu_free(void *ptr) {
+  if (!ptr) return TAC_OK;
+  if (device_count() <= 0) return TAC_ERR_NO_DEVICE;
+  HIP_TRY(hipFree(ptr));
+  return TAC_OK;
+}
+
+int tac_gpu_memcpy_htod(void *dst, const void *src, uint64_t bytes) {
+  if ((!dst || !src) && bytes) return TAC_ERR_INVALID_ARGUMENT;
+  if (device_count() <= 0) return TAC_ERR_NO_DEVICE;
+  if (bytes) HIP_TRY(hipMemcpy(dst, src, bytes, hipMemcpyHostToDevice));
+  return TAC_OK;
+}
+
+int tac_gpu_memcpy_dtoh(void *dst, const void *src, uint64_t bytes) {
+  if ((!dst || !src) && bytes) return TAC_ERR_INVALID_ARGUMENT;
+  if (device_count() <= 0) return TAC_ERR_NO_DEVICE;
+  if (bytes) HIP_TRY(hipMemcpy(dst, src, bytes, hipMemcpyDeviceToHost));
+  return TAC_OK;
+}
+
+int tac_gpu_memcpy_dtod(void *dst, const void *src, uint64_t bytes) {
+  if ((!dst || !src) && bytes) return TAC_ERR_INVALID_ARGUMENT;
+  if (device_count() <= 0) return TAC_ERR_NO_DEVICE;
+  if (bytes) HIP_TRY(hipMemcpy(dst, src, bytes, hipMemcpyDeviceToDevice));
+  return TAC_OK;
+}
+
+int tac_gpu_synchronize(void) {
+  if (device_count() <= 0) return TAC_ERR_NO_DEVICE;
+  HIP_TRY(hipDeviceSynchronize());
+  return TAC_OK;
+}
+
+int tac_gpu_release_workspace(void) {
+  DeviceState *ds = nullptr;
+  int st = acquire_device(&ds, nullptr);
+  if (st) return st;
+  std::lock_guard<std::mutex> g(ds->mu);
+  HIP_TRY(hipDeviceSynchronize());
+  Buffer *bufs[] = {&ds->xs,   &ds->codes,  &ds->e,     &ds->hist,  &ds->counts,
+                    &ds->start, &ds->sorted, &ds->flags, &ds->scal,  &ds->trace,
+                    &ds->io_in, &ds->io_out, &ds->io_cb, &ds->io_init};
+  for (Buffer *b : bufs) {
+    if (b->ptr) HIP_TRY(hipFree(b->ptr));
+    b->ptr = nullptr;
+    b->bytes = 0;
+  }
+  return TAC_OK;
+}
+
+int tac_gpu_profile_enable(int enable) {
+  g_profile = enable != 0;
+  return TAC_OK;
+}
+
+int tac_gpu_profile_read(tac_gpu_profile *out, int reset) {
+  if (!out) return TAC_ERR_INVALID_ARGUMENT;
+  std::lock_guard<std::mutex> g(g_profile_mu);
+  *out = g_prof;
+  if (reset) g_prof = tac_gpu_profile{};
+  return TAC_OK;
+}
+
+int tac_pq_train_device(const float *d_residuals, uint64_t n, uint32_t dim, uint32_t m,
+                        uint32_t ksub, const float *d_init_codebooks, uint64_t seed,
+                        uint32_t max_iters, float tol, float *d_codebooks_out,
+                        tac_pq_train_extras *extras, void *stream) {
+  (void)seed;
+  int st = validate_pq(n, dim, m, ksub);
+  if (st) return st;
+  if (!d_residuals || !d_codebooks_out) return TAC_ERR_INVALID_ARGUMENT;
+  if (!d_init_codebooks && (uint64_t)ksub < n) return TAC_ERR_UNSUPPORTED;
+  DeviceState *ds = nullptr;
+  if ((st = acquire_device(&ds, nullptr))) return st;
+  std::lock_guard<std::mutex> g(ds->mu);
+  hipStream_t s;
+  if ((st = resolve_stream(*ds, stream, &s))) return st;
+  if ((st = begin_call(*ds, s))) return st;
+  const size_t cb_bytes = (size_t)m * ksub * (dim / m) * sizeof(float);
+  if (d_init_codebooks && d_init_codebooks != d_codebooks_out)
+    HIP_TRY(hipMemcpyAsync(d_codebooks_out, d_init_codebooks, cb_bytes, hipMemcpyDeviceToDevice,
+                           s));
+  TrainOut out{d_codebooks_out, nullptr, extras, nullptr, nullptr};
+  st = train_core(*ds, s, d_residuals, n, dim, m, ksub, max_iters, tol, out);
+  if (st) return st;
+  return end_call(*ds, s);
+}
+
+int tac_pq_train(const float *residuals, uint64_t n, uint32_t dim, uint32_t m, uint32_t ksub,
+                 const float *init_codebooks, uint64_t seed, uint32_t max_iters, float tol,
+                 float *codebooks_out, tac_pq_train_extras *extras) {
+  (void)seed;
+  int st = validate_pq(n, dim, m, ksub);
+  if (st) return st;
+  if (!residuals || !codebooks_out) return TAC_ERR_INVALID_ARGUMENT;
+  if (!init_codebooks && (uint64_t)ksub < n) return TAC_ERR_UNSUPPORTED;
+  DeviceState *ds = nullptr;
+  if ((st = acquire_device(&ds, nullptr))) return st;
+  std::lock_guard<std::mutex> g(ds->mu);
+  hipStream_t s;
+  if ((st = resolve_stream(*ds, nullptr, &s))) return st;
+  if ((st = begin_call(*ds, s))) return st;
+  const size_t x_bytes = (size_t)n * dim * sizeof(float);
+  const size_t cb_bytes = (size_t)m * ksub * (dim / m) * sizeof(float);
+  if ((st = ensure(*ds, ds->io_in, x_bytes)) || (st = ensure(*ds, ds->io_cb, cb_bytes))) return st;
+  HIP_TRY(hipMemcpyAsync(ds->io_in.ptr, residuals, x_bytes, hipMemcpyHostToDevice, s));
+  if (init_codebooks)
+    HIP_TRY(hipMemcpyAsync(ds->io_cb.ptr, init_codebooks, cb_bytes, hipMemcpyHostToDevice, s));
+  TrainOut out{as<float>(ds->io_cb), nullptr, extras, nullptr, nullptr};
+  st = train_core(*ds, s, as<float>(ds->io_in), n, dim, m, ksub, max_iters, tol, out);
+  if (st) return st;
+  HIP_TRY(hipMemcpyAsync(codebooks_out, ds->io_cb.ptr, cb_bytes, hipMemcpyDeviceToHost, s));
+  HIP_TRY(hipStreamSynchronize(s));
+  return end_call(*ds, s);
+}
+
+int tac_pq_encode_device(const float *d_residuals, uint64_t n, uint32_t dim, uint32_t m,
+                         uint32_t ksub, const float *d_codebooks, void *d_codes_out,
+                         void *stream) {
+  if (m == 0 || ksub == 0) return TAC_ERR_INVALID_ARGUMENT;
+  if (dim == 0 || dim % m != 0) return TAC_ERR_DIM_MISMATCH;
+  if (dim / m > kMaxDsub || ksub > kMaxKsub) return TAC_ERR_UNSUPPORTED;
+  if (n == 0) return TAC_OK;
+  if (!d_residuals || !d_codebooks || !d_codes_out) return TAC_ERR_INVALID_ARGUMENT;
+  DeviceState *ds = nullptr;
+  int st = acquire_device(&ds, nullptr);
+  if (st) return st;
+  std::lock_guard<std::mutex> g(ds->mu);
+  hipStream_t s;
+  if ((st = resolve_stream(*ds, stream, &s))) return st;
+  if ((st = begin_call(*ds, s))) return st;
+  if ((st = encode_core(*ds, s, d_residuals, n, dim, m, ksub, d_codebooks, d_codes_out)))
+    return st;
+  return end_call(*ds, s);
+}
+
+int tac_pq_encode(const float *residuals, uint64_t n, uint32_t dim, uint32_t m, uint32_t ksub,
+                  const float *codebooks, void *codes_out) {
+  if (m == 0 || ksub == 0) return TAC_ERR_INVALID_ARGUMENT;
+  if (dim == 0 || dim % m != 0) return TAC_ERR_DIM_MISMATCH;
+  if (dim / m > kMaxDsub || ksub > kMaxKsub) return TAC_ERR_UNSUPPORTED;
+  if (n == 0) return TAC_OK;
+  if (!residuals || !codebooks || !codes_out) return TAC_ERR_INVALID_ARGUMENT;
+  DeviceState *ds = nullptr;
+  int st = acquire_device(&ds, nullptr);
+  if (st) return st;
+  std::lock_guard<std::mutex> g(ds->mu);
+  hipStream_t s;
+  if ((st = resolve_stream(*ds, nullptr, &s))) return st;
+  if ((st = begin_call(*ds, s))) return st;
+  const size_t x_bytes = (size_t)n * dim * sizeof(float);
+  const size_t cb_bytes = (size_t)ksub * dim * sizeof(float);
+  const size_t code_bytes = (size_t)n * m * (ksub <= 256 ? 1 : 2);
+  if ((st = ensure(*ds, ds->io_in, x_bytes)) || (st = ensure(*ds, ds->io_cb, cb_bytes)) ||
+      (st = ensure(*ds, ds->io_out, code_bytes)))
+    return st;
+  HIP_TRY(hipMemcpyAsync(ds->io_in.ptr, residuals, x_bytes, hipMemcpyHostToDevice, s));
+  HIP_TRY(hipMemcpyAsync(ds->io_cb.ptr, codebooks, cb_bytes, hipMemcpyHostToDevice, s));
+  if ((st = encode_core(*ds, s, as<float>(ds->io_in), n, dim, m, ksub, as<float>(ds->io_cb),
+                        ds->io_out.ptr)))
+    return st;
+  HIP_TRY(hipMemcpyAsync(codes_out, ds->io_out.ptr, code_bytes, hipMemcpyDeviceToHost, s));
+  HIP_TRY(hipStreamSynchronize(s));
+  return end_call(*ds, s);
+}
+
+int tac_pq_decode(const void *codes, uint64_t n, uint32_t dim, uint32_t m, uint32_t ksub,
+                  const float *codebooks, float *out) {
+  if (m == 0 || ksub == 0) return TAC_ERR_INVALID_ARGUMENT;
+  if (dim == 0 || dim % m != 0) return TAC_ERR_DIM_MISMATCH;
+  if (dim / m > kMaxDsub || ksub > kMaxKsub) return TAC_ERR_UNSUPPORTED;
+  if (n == 0) return TAC_OK;
+  if (!codes || !codebooks || !out) return TAC_ERR_INVALID_ARGUMENT;
+  DeviceState *ds = nullptr;
+  int st = acquire_device(&ds, nullptr);
+  if (st) return st;
+  std::lock_guard<std::mutex> g(ds->mu);
+  hipStream_t s;
+  if ((st = resolve_stream(*ds, nullptr, &s))) return st;
+  if ((st = begin_call(*ds, s))) return st;
+  const uint32_t D = dim / m;
+  const size_t code_bytes = (size_t)n * m * (ksub <= 256 ? 1 : 2);
+  const size_t cb_bytes = (size_t)ksub * dim * sizeof(float);
+  const size_t out_bytes = (size_t)n * dim * sizeof(float);
+  if ((st = ensure(*ds, ds->io_in, code_bytes)) || (st = ensure(*ds, ds->io_cb, cb_bytes)) ||
+      (st = ensure(*ds, ds->io_out, out_bytes)))
+    return st;
+  HIP_TRY(hipMemcpyAsync(ds->io_in.ptr, codes, code_bytes, hipMemcpyHostToDevice, s));
+  HIP_TRY(hipMemcpyAsync(ds->io_cb.ptr, codebooks, cb_bytes, hipMemcpyHostToDevice, s));
+  const uint64_t total = n * dim;
+  const unsigned blocks = (unsigned)((total + 255) / 256);
+  if (ksub <= 256)
+    decode_kernel<uint8_t><<<blocks, 256, 0, s>>>(as<uint8_t>(ds->io_in), as<float>(ds->io_cb),
+                                                  as<float>(ds->io_out), n, m, ksub, D);
+  else
+    decode_kernel<uint16_t><<<blocks, 256, 0, s>>>(as<uint16_t>(ds->io_in), as<float>(ds->io_cb),
+                                                   as<float>(ds->io_out), n, m, ksub, D);
+  LAUNCH_TRY("decode_kernel");
+  HIP_TRY(hipMemcpyAsync(out, ds->io_out.ptr, out_bytes, hipMemcpyDeviceToHost, s));
+  HIP_TRY(hipStreamSynchronize(s));
+  return end_call(*ds, s);
+}
+
+int tac_kmeans_fit(const float *vectors, uint64_t n, uint32_t dim, uint32_t k,
+                   uint32_t max_iters, float tol, uint64_t seed, const float *init_centroids,
+                   float *centroids_out, uint32_t *assignments_out, float *wcss_out,
+                   uint32_t *iters_run_out) {
+  (void)seed;
+  // src/tac/kmeans.zig:73-76
+  if (k == 0) return TAC_ERR_KMEANS_BUDGET_TOO_SMALL;
+  if (dim == 0) return TAC_ERR_DIM_MISMATCH;
+  if (n == 0) return TAC_ERR_EMPTY_VECTOR_SET;
+  if (dim > kMaxDsub || k > kMaxKsub || n > 0xFFFFFFFFull) return TAC_ERR_UNSUPPORTED;
+  if (!vectors || !centroids_out || !assignments_out) return TAC_ERR_INVALID_ARGUMENT;
+  if (!init_centroids && (uint64_t)k < n) return TAC_ERR_UNSUPPORTED;
+  DeviceState *ds = nullptr;
+  int st = acquire_device(&ds, nullptr);
+  if (st) return st;
+  std::lock_guard<std::mutex> g(ds->mu);
+  hipStream_t s;
+  if ((st = resolve_stream(*ds, nullptr, &s))) return st;
+  if ((st = begin_call(*ds, s))) return st;
+  const size_t x_bytes = (size_t)n * dim * sizeof(float);
+  const size_t cb_bytes = (size_t)k * dim * sizeof(float);
+  if ((st = ensure(*ds, ds->io_in, x_bytes)) || (st = ensure(*ds, ds->io_cb, cb_bytes)) ||
+      (st = ensure(*ds, ds->io_out, (size_t)n * sizeof(uint32_t))))
+    return st;
+  HIP_TRY(hipMemcpyAsync(ds->io_in.ptr, vectors, x_bytes, hipMemcpyHostToDevice, s));
+  if (init_centroids)
+    HIP_TRY(hipMemcpyAsync(ds->io_cb.ptr, init_centroids, cb_bytes, hipMemcpyHostToDevice, s));
+  float wcss = 0.0f;
+  uint32_t iters = 0;
+  TrainOut out{as<float>(ds->io_cb), as<uint32_t>(ds->io_out), nullptr, &wcss, &iters};
+  st = train_core(*ds, s, as<float>(ds->io_in), n, dim, 1, k, max_iters, tol, out);
+  if (st) return st;
+  HIP_TRY(hipMemcpyAsync(centroids_out, ds->io_cb.ptr, cb_bytes, hipMemcpyDeviceToHost, s));
+  HIP_TRY(hipMemcpyAsync(assignments_out, ds->io_out.ptr, (size_t)n * sizeof(uint32_t),
+                         hipMemcpyDeviceToHost, s));
+  HIP_TRY(hipStreamSynchronize(s));
+  if (wcss_out) *wcss_out = wcss;
+  if (iters_run_out) *iters_run_out = iters;
+  return end_call(*ds, s);
+}
+
+}  // extern "C"

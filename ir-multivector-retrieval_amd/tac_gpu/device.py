@@ -1,0 +1,120 @@
+"""Device memory, device-resident entry points and kernel timing.
+
+Used by callers that keep residuals resident in HBM across train and encode
+(the way storage.build chains them, src/index/storage.zig:378-401) and by
+the benchmark.  Memory comes from the library's own HIP runtime, so no other
+GPU framework has to be loaded in the process.
+"""
+from __future__ import annotations
+
+import ctypes
+from dataclasses import dataclass
+
+import numpy as np
+
+from . import errors
+from ._native import DeviceInfo, Profile, TrainExtras, lib
+from .pq import code_dtype
+
+
+def device_count() -> int:
+    c = ctypes.c_int(0)
+    lib.tac_gpu_device_count(ctypes.byref(c))
+    return int(c.value)
+
+
+def device_info(device: int = 0) -> dict:
+    info = DeviceInfo()
+    errors.check(lib.tac_gpu_get_device_info(device, ctypes.byref(info)))
+    return {
+        "name": info.name.decode(errors="replace"),
+        "arch": info.arch.decode(errors="replace"),
+        "compute_units": info.compute_units,
+        "clock_khz": info.clock_khz,
+        "global_mem_bytes": int(info.global_mem_bytes),
+    }
+
+
+def synchronize() -> None:
+    errors.check(lib.tac_gpu_synchronize())
+
+
+class DeviceArray:
+    """A flat device allocation with a numpy dtype and shape."""
+
+    def __init__(self, shape, dtype):
+        self.shape = tuple(int(s) for s in np.atleast_1d(shape)) if not isinstance(shape, tuple) \
+            else tuple(int(s) for s in shape)
+        self.dtype = np.dtype(dtype)
+        self.nbytes = int(np.prod(self.shape, dtype=np.int64)) * self.dtype.itemsize
+        p = ctypes.c_void_p()
+        errors.check(lib.tac_gpu_malloc(ctypes.byref(p), self.nbytes))
+        self.ptr = p
+
+    @classmethod
+    def from_host(cls, a: np.ndarray) -> "DeviceArray":
+        a = np.ascontiguousarray(a)
+        d = cls(a.shape, a.dtype)
+        errors.check(lib.tac_gpu_memcpy_htod(d.ptr, ctypes.c_void_p(a.ctypes.data), a.nbytes))
+        return d
+
+    def to_host(self) -> np.ndarray:
+        out = np.empty(self.shape, dtype=self.dtype)
+        errors.check(lib.tac_gpu_memcpy_dtoh(ctypes.c_void_p(out.ctypes.data), self.ptr,
+                                             self.nbytes))
+        return out
+
+    def free(self) -> None:
+        if self.ptr:
+            lib.tac_gpu_free(self.ptr)
+            self.ptr = ctypes.c_void_p()
+
+    def __del__(self):
+        try:
+            self.free()
+        except Exception:
+            pass
+
+
+def train_device(x: DeviceArray, n: int, dim: int, m: int, ksub: int, init: DeviceArray,
+                 out: DeviceArray, max_iters: int, tol: float, stats: bool = False):
+    """tac_pq_train_device on resident buffers; optional per-subspace stats."""
+    ex = None
+    arrays = None
+    if stats:
+        arrays = (np.zeros(m, np.uint32), np.zeros(m, np.float32), np.zeros(m, np.uint32))
+        ex = TrainExtras(arrays[0].ctypes.data_as(ctypes.POINTER(ctypes.c_uint32)),
+                         arrays[1].ctypes.data_as(ctypes.POINTER(ctypes.c_float)),
+                         arrays[2].ctypes.data_as(ctypes.POINTER(ctypes.c_uint32)), None)
+    errors.check(lib.tac_pq_train_device(x.ptr, n, dim, m, ksub, init.ptr, 0, max_iters, tol,
+                                         out.ptr, ctypes.byref(ex) if ex else None, None))
+    return arrays
+
+
+def encode_device(x: DeviceArray, n: int, dim: int, m: int, ksub: int, cb: DeviceArray,
+                  codes: DeviceArray) -> None:
+    assert codes.dtype == code_dtype(ksub)
+    errors.check(lib.tac_pq_encode_device(x.ptr, n, dim, m, ksub, cb.ptr, codes.ptr, None))
+
+
+@dataclass
+class KernelTimes:
+    transpose_ms: float
+    transpose_launches: int
+    assign_ms: float
+    assign_launches: int
+    update_ms: float
+    update_iters: int
+    encode_ms: float
+    encode_launches: int
+
+
+def profile_enable(on: bool = True) -> None:
+    lib.tac_gpu_profile_enable(1 if on else 0)
+
+
+def profile_read(reset: bool = True) -> KernelTimes:
+    p = Profile()
+    errors.check(lib.tac_gpu_profile_read(ctypes.byref(p), 1 if reset else 0))
+    return KernelTimes(p.transpose_ms, p.transpose_launches, p.assign_ms, p.assign_launches,
+                       p.update_ms, p.update_iters, p.encode_ms, p.encode_launches)

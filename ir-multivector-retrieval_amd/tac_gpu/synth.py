@@ -1,0 +1,120 @@
+"""Synthetic PQ build workloads (host generator ``libtac_synth.so``).
+
+Residual corpora follow one recipe: unit-sphere centres in R^dim, vectors
+``normalize(centre_j + N(0, sigma^2 I))`` with j uniform or Zipf(s), residual
+``vector - centre_j``.  Initial codebooks are the first ksub points of a
+seeded shuffle, per subspace.
+"""
+from __future__ import annotations
+
+import ctypes
+import os
+from dataclasses import dataclass
+
+import numpy as np
+
+from ._native import SYNTH_PATH
+
+
+@dataclass(frozen=True)
+class Workload:
+    name: str
+    n: int
+    dim: int
+    n_centers: int
+    zipf: float        # 0: uniform centre popularity
+    sigma: float
+    m: int
+    ksub: int
+    iters: int
+    seed: int = 0
+
+    @property
+    def dsub(self) -> int:
+        return self.dim // self.m
+
+
+# Small chunk (117,645 x 64, uniform over 10,240 centres) and the full corpus
+# shape (1,521,797 x 64, Zipf 1.1 over 32,768 centres); both m=16, ksub=256,
+# 20 Lloyd iterations.
+WORKLOADS = {
+    "chunk-117k": Workload("chunk-117k", 117_645, 64, 10_240, 0.0, 0.15, 16, 256, 20),
+    "corpus-1.52m": Workload("corpus-1.52m", 1_521_797, 64, 32_768, 1.1, 0.15, 16, 256, 20),
+    "corpus-1.52m-m32d2": Workload("corpus-1.52m-m32d2", 1_521_797, 64, 32_768, 1.1, 0.15, 32,
+                                   256, 20),
+    "corpus-1.52m-m8d8": Workload("corpus-1.52m-m8d8", 1_521_797, 64, 32_768, 1.1, 0.15, 8, 256,
+                                  20),
+    "corpus-1.52m-k1024": Workload("corpus-1.52m-k1024", 1_521_797, 64, 32_768, 1.1, 0.15, 16,
+                                   1024, 20),
+}
+
+
+def _lib() -> ctypes.CDLL:
+    if not SYNTH_PATH.exists():
+        raise ImportError(f"{SYNTH_PATH} is not built")
+    lib = ctypes.CDLL(os.fspath(SYNTH_PATH))
+    vp, u64, u32 = ctypes.c_void_p, ctypes.c_uint64, ctypes.c_uint32
+    lib.tac_synth_centers.argtypes = [u64, u32, u32, vp]
+    lib.tac_synth_residuals.argtypes = [u64, u64, u32, u32, vp, ctypes.c_double, ctypes.c_float,
+                                        u64, vp, vp, u32]
+    lib.tac_synth_shuffle_init.argtypes = [vp, u64, u32, u32, u32, u64, vp]
+    lib.tac_synth_gauss_codebooks.argtypes = [u64, u32, u32, u32, ctypes.c_float, vp]
+    for f in (lib.tac_synth_centers, lib.tac_synth_residuals, lib.tac_synth_shuffle_init,
+              lib.tac_synth_gauss_codebooks):
+        f.restype = ctypes.c_int
+    return lib
+
+
+_L = None
+
+
+def lib() -> ctypes.CDLL:
+    global _L
+    if _L is None:
+        _L = _lib()
+    return _L
+
+
+def _p(a: np.ndarray) -> ctypes.c_void_p:
+    return ctypes.c_void_p(a.ctypes.data)
+
+
+def centers(seed: int, n_centers: int, dim: int) -> np.ndarray:
+    out = np.empty((n_centers, dim), dtype=np.float32)
+    assert lib().tac_synth_centers(seed, n_centers, dim, _p(out)) == 0
+    return out
+
+
+def residuals(w: Workload, n: int | None = None, first: int = 0, threads: int | None = None,
+              with_ids: bool = False):
+    """Residual rows first .. first+n-1 of workload w (default: all of it)."""
+    n = w.n if n is None else n
+    c = centers(w.seed, w.n_centers, w.dim)
+    out = np.empty((n, w.dim), dtype=np.float32)
+    ids = np.empty(n, dtype=np.uint32) if with_ids else None
+    t = threads or min(16, os.cpu_count() or 1)
+    assert lib().tac_synth_residuals(w.seed, n, w.dim, w.n_centers, _p(c), w.zipf, w.sigma, first,
+                                     _p(out), _p(ids) if ids is not None else None, t) == 0
+    return (out, ids) if with_ids else out
+
+
+def shuffle_init(x: np.ndarray, m: int, ksub: int, seed: int) -> np.ndarray:
+    """[m][ksub][dsub] codebooks from the first ksub points of a seeded shuffle."""
+    n, dim = x.shape
+    out = np.empty((m, ksub, dim // m), dtype=np.float32)
+    x = np.ascontiguousarray(x, dtype=np.float32)
+    assert lib().tac_synth_shuffle_init(_p(x), n, dim, m, ksub, seed, _p(out)) == 0
+    return out
+
+
+def gauss_codebooks(seed: int, m: int, ksub: int, dsub: int, sigma: float) -> np.ndarray:
+    out = np.empty((m, ksub, dsub), dtype=np.float32)
+    assert lib().tac_synth_gauss_codebooks(seed, m, ksub, dsub, sigma, _p(out)) == 0
+    return out
+
+
+def workload(name: str, n: int | None = None):
+    """(residuals, init codebooks) of a named workload, optionally truncated to n rows."""
+    w = WORKLOADS[name]
+    x = residuals(w, n)
+    return w, x, shuffle_init(x, w.m, w.ksub, w.seed)

@@ -1,0 +1,231 @@
+"""ctypes binding of the CPU oracle (oracle/_build/libpq_oracle.so).
+
+TEST INFRASTRUCTURE ONLY: imported by tests/, __graft_entry__.smoke() and the
+cpu_baseline leg of bench.py, always as the checker or the timed CPU
+baseline, never as part of the product path.
+"""
+from __future__ import annotations
+
+import ctypes
+import os
+from dataclasses import dataclass
+from pathlib import Path
+
+import numpy as np
+
+ORACLE_DIR = Path(__file__).resolve().parent
+LIB_PATH = ORACLE_DIR / "_build" / "libpq_oracle.so"
+
+_vp, _u64, _u32, _f32 = ctypes.c_void_p, ctypes.c_uint64, ctypes.c_uint32, ctypes.c_float
+
+
+class FitExtras(ctypes.Structure):
+    _fields_ = [("trace", _vp), ("empties", _vp), ("wcss_trace", _vp)]
+
+
+class TrainExtras(ctypes.Structure):
+    _fields_ = [("trace", _vp), ("iters_run", _vp), ("wcss", _vp), ("empties", _vp)]
+
+
+class Xoshiro(ctypes.Structure):
+    _fields_ = [("s", _u64 * 4)]
+
+
+def _load():
+    if not LIB_PATH.exists():
+        raise ImportError(f"{LIB_PATH} is not built (make -C oracle)")
+    L = ctypes.CDLL(os.fspath(LIB_PATH))
+    L.orc_l2sq.restype = _f32
+    L.orc_l2sq.argtypes = [_vp, _vp, _u32]
+    L.orc_dot.restype = _f32
+    L.orc_dot.argtypes = [_vp, _vp, _u32]
+    L.orc_argmin.restype = _u64
+    L.orc_argmin.argtypes = [_vp, _u64]
+    L.orc_argmax.restype = _u64
+    L.orc_argmax.argtypes = [_vp, _u64]
+    L.orc_zig_prng_init.argtypes = [ctypes.POINTER(Xoshiro), _u64]
+    L.orc_zig_next.restype = _u64
+    L.orc_zig_next.argtypes = [ctypes.POINTER(Xoshiro)]
+    L.orc_zig_uint_less_than.restype = _u64
+    L.orc_zig_uint_less_than.argtypes = [ctypes.POINTER(Xoshiro), _u64]
+    L.orc_zig_float_f64.restype = ctypes.c_double
+    L.orc_zig_float_f64.argtypes = [ctypes.POINTER(Xoshiro)]
+    L.orc_weighted_sample.restype = ctypes.c_int
+    L.orc_weighted_sample.argtypes = [ctypes.POINTER(Xoshiro), _vp, _u64,
+                                      ctypes.POINTER(_u64)]
+    L.orc_kmeans_fit.restype = ctypes.c_int
+    L.orc_kmeans_fit.argtypes = [_vp, _u64, _u32, _u32, _u32, _f32, _u64, _u32, _vp, _vp, _vp,
+                                 ctypes.POINTER(_f32), ctypes.POINTER(_u32),
+                                 ctypes.POINTER(FitExtras)]
+    L.orc_pq_train.restype = ctypes.c_int
+    L.orc_pq_train.argtypes = [_vp, _u64, _u32, _u32, _u32, _vp, _u64, _u32, _f32, _u32, _vp,
+                               ctypes.POINTER(TrainExtras)]
+    L.orc_pq_encode.restype = ctypes.c_int
+    L.orc_pq_encode.argtypes = [_vp, _u64, _u32, _u32, _u32, _vp, _vp, _u32]
+    L.orc_pq_near_ties.restype = ctypes.c_int
+    L.orc_pq_near_ties.argtypes = [_vp, _u64, _u32, _u32, _u32, _vp, _f32,
+                                   ctypes.POINTER(_u64), _u32]
+    L.orc_pq_decode.restype = ctypes.c_int
+    L.orc_pq_decode.argtypes = [_vp, _u64, _u32, _u32, _u32, _vp, _vp]
+    L.orc_pq_distance_table.restype = ctypes.c_int
+    L.orc_pq_distance_table.argtypes = [_vp, _u32, _u32, _u32, _u32, _vp, _vp, _u64]
+    return L
+
+
+lib = _load()
+
+
+def _p(a):
+    return None if a is None else ctypes.c_void_p(a.ctypes.data)
+
+
+def _f32(a):
+    return np.ascontiguousarray(a, dtype=np.float32)
+
+
+def l2sq(a, b) -> np.float32:
+    a, b = _f32(a).reshape(-1), _f32(b).reshape(-1)
+    assert a.size == b.size
+    return np.float32(lib.orc_l2sq(_p(a), _p(b), a.size))
+
+
+def dot(a, b) -> np.float32:
+    a, b = _f32(a).reshape(-1), _f32(b).reshape(-1)
+    return np.float32(lib.orc_dot(_p(a), _p(b), a.size))
+
+
+def argmin(v) -> int:
+    v = _f32(v).reshape(-1)
+    return int(lib.orc_argmin(_p(v), v.size))
+
+
+def argmax(v) -> int:
+    v = _f32(v).reshape(-1)
+    return int(lib.orc_argmax(_p(v), v.size))
+
+
+class ZigPrng:
+    """Restated Zig std.Random.DefaultPrng (parity unpinned)."""
+
+    def __init__(self, seed: int):
+        self.state = Xoshiro()
+        lib.orc_zig_prng_init(ctypes.byref(self.state), seed & (2**64 - 1))
+
+    def next(self) -> int:
+        return int(lib.orc_zig_next(ctypes.byref(self.state)))
+
+    def uint_less_than(self, n: int) -> int:
+        return int(lib.orc_zig_uint_less_than(ctypes.byref(self.state), n))
+
+    def float_f64(self) -> float:
+        return float(lib.orc_zig_float_f64(ctypes.byref(self.state)))
+
+    def weighted_sample(self, w) -> tuple[int, int]:
+        w = _f32(w).reshape(-1)
+        out = _u64(0)
+        st = lib.orc_weighted_sample(ctypes.byref(self.state), _p(w), w.size, ctypes.byref(out))
+        return st, int(out.value)
+
+
+@dataclass
+class FitResult:
+    status: int
+    centroids: np.ndarray
+    assignments: np.ndarray
+    wcss: float
+    iters_run: int
+    trace: np.ndarray | None
+    empties: np.ndarray | None
+    wcss_trace: np.ndarray | None
+
+
+def kmeans_fit(vectors, dim: int, k: int, *, max_iters: int = 25, tol: float = 1e-4,
+               seed: int = 0, n_threads: int = 1, init=None, trace: bool = False) -> FitResult:
+    v = _f32(vectors).reshape(-1)
+    n = v.size // dim if dim else 0
+    cent = np.zeros(max(k, 1) * max(dim, 1), dtype=np.float32)
+    assign = np.zeros(max(n, 1), dtype=np.uint32)
+    init_a = None if init is None else _f32(init).reshape(-1)
+    tr = np.zeros((max_iters, k * dim), np.float32) if trace and max_iters else None
+    emp = np.zeros(max_iters, np.uint32) if trace and max_iters else None
+    wtr = np.zeros(max_iters, np.float32) if trace and max_iters else None
+    ex = FitExtras(_p(tr), _p(emp), _p(wtr))
+    wcss, iters = _f32_c(), _u32(0)
+    st = lib.orc_kmeans_fit(_p(v), n, dim, k, max_iters, tol, seed & (2**64 - 1), n_threads,
+                            _p(init_a), _p(cent), _p(assign), ctypes.byref(wcss),
+                            ctypes.byref(iters), ctypes.byref(ex))
+    return FitResult(st, cent[:k * dim], assign[:n], float(wcss.value), int(iters.value), tr, emp,
+                     wtr)
+
+
+def _f32_c():
+    return ctypes.c_float(0.0)
+
+
+@dataclass
+class TrainResult:
+    status: int
+    codebooks: np.ndarray
+    iters_run: np.ndarray
+    wcss: np.ndarray
+    empties: np.ndarray
+    trace: np.ndarray | None
+
+
+def pq_train(residuals, dim: int, m: int, ksub: int, *, init=None, seed: int = 0,
+             max_iters: int = 25, tol: float = 1e-4, n_threads: int = 1,
+             trace: bool = False) -> TrainResult:
+    r = _f32(residuals).reshape(-1)
+    n = r.size // dim if dim else 0
+    dsub = dim // m if m else 0
+    cb = np.zeros(max(m * ksub * dsub, 1), dtype=np.float32)
+    init_a = None if init is None else _f32(init).reshape(-1)
+    it = np.zeros(max(m, 1), np.uint32)
+    wc = np.zeros(max(m, 1), np.float32)
+    em = np.zeros(max(m, 1), np.uint32)
+    tr = np.zeros((max_iters, m * ksub * dsub), np.float32) if trace and max_iters else None
+    ex = TrainExtras(_p(tr), _p(it), _p(wc), _p(em))
+    st = lib.orc_pq_train(_p(r), n, dim, m, ksub, _p(init_a), seed & (2**64 - 1), max_iters, tol,
+                          n_threads, _p(cb), ctypes.byref(ex))
+    return TrainResult(st, cb[:m * ksub * dsub], it[:m], wc[:m], em[:m], tr)
+
+
+def pq_encode(residuals, dim: int, m: int, ksub: int, codebooks, n_threads: int = 1):
+    r = _f32(residuals).reshape(-1)
+    n = r.size // dim
+    out = np.zeros((n, m), dtype=np.uint8 if ksub <= 256 else np.uint16)
+    cb = _f32(codebooks).reshape(-1)
+    st = lib.orc_pq_encode(_p(r), n, dim, m, ksub, _p(cb), _p(out), n_threads)
+    assert st == 0, st
+    return out
+
+
+def pq_near_ties(residuals, dim: int, m: int, ksub: int, codebooks, rel_tol: float = 1e-5,
+                 n_threads: int = 1) -> int:
+    r = _f32(residuals).reshape(-1)
+    cb = _f32(codebooks).reshape(-1)
+    out = _u64(0)
+    st = lib.orc_pq_near_ties(_p(r), r.size // dim, dim, m, ksub, _p(cb), rel_tol,
+                              ctypes.byref(out), n_threads)
+    assert st == 0, st
+    return int(out.value)
+
+
+def pq_decode(codes, dim: int, m: int, ksub: int, codebooks):
+    c = np.ascontiguousarray(codes, dtype=np.uint8 if ksub <= 256 else np.uint16)
+    n = c.size // m
+    out = np.zeros((n, dim), np.float32)
+    cb = _f32(codebooks).reshape(-1)
+    st = lib.orc_pq_decode(_p(c), n, dim, m, ksub, _p(cb), _p(out))
+    assert st == 0, st
+    return out
+
+
+def pq_distance_table(queries, n_q: int, dim: int, m: int, ksub: int, codebooks,
+                      table_len: int | None = None):
+    q = _f32(queries).reshape(-1)
+    cb = _f32(codebooks).reshape(-1)
+    tl = m * ksub * n_q if table_len is None else table_len
+    out = np.zeros(max(tl, 1), np.float32)
+    st = lib.orc_pq_distance_table(_p(q), n_q, dim, m, ksub, _p(cb), _p(out), tl)
+    return st, out[:tl]

@@ -1,0 +1,120 @@
+/*
+ * pq_oracle.h — CPU restatement of the reference's product-quantization build
+ * path (Lloyd k-means per subspace + PQ encode), used ONLY as test
+ * infrastructure: the parity checker for the HIP library and the timed CPU
+ * baseline.  Nothing in the shipped library links or calls this code.
+ *
+ * Every function follows a reference location (paths relative to the
+ * reference repository root):
+ *   orc_l2sq / orc_dot      src/util/vec.zig:37-175   (operation order, no FMA)
+ *   orc_argmin / orc_argmax src/util/vec.zig:271-299  (first index wins ties)
+ *   orc_zig_*               src/util/rng.zig:22-82 and Zig std 0.16
+ *                           (std.Random.DefaultPrng = Xoshiro256++, SplitMix64
+ *                           seeding, uintLessThan, float(f64)) — "parity
+ *                           unpinned": no Zig toolchain exists here to check
+ *                           the stream against.
+ *   orc_kmeans_fit          src/tac/kmeans.zig:67-365
+ *   orc_pq_train            src/index/pq.zig:158-336
+ *   orc_pq_encode           src/index/pq.zig:59-76 driven as in
+ *                           src/index/storage.zig:201-244,280-295
+ *   orc_pq_decode           src/index/pq.zig:79-88
+ *   orc_pq_distance_table   src/index/pq.zig:92-123
+ *
+ * Status codes share their numbering with include/tac_gpu.h.
+ */
+#ifndef PQ_ORACLE_H
+#define PQ_ORACLE_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+enum {
+  ORC_OK = 0,
+  ORC_DIM_NOT_DIVISIBLE_BY_M = 1,
+  ORC_DIM_MISMATCH = 2,
+  ORC_EMPTY_CORPUS = 3,
+  ORC_OUT_BUFFER_WRONG_SIZE = 4,
+  ORC_NQ_MISMATCH = 5,
+  ORC_KMEANS_BUDGET_TOO_SMALL = 6,
+  ORC_EMPTY_VECTOR_SET = 7,
+  ORC_RNG_EMPTY_DISTRIBUTION = 8,
+  ORC_RNG_NON_FINITE = 9,
+  ORC_RNG_ALL_ZERO = 10,
+  ORC_OUT_OF_MEMORY = 11,
+  ORC_INVALID_ARGUMENT = 14,
+};
+
+/* Lane count the reference's generic vec path uses on the host it is built
+ * for (std.simd.suggestVectorLength(f32)): 16 on an AVX-512 x86-64 host. */
+#define ORC_HOST_LANES 16
+
+float orc_l2sq(const float *a, const float *b, uint32_t d);
+float orc_dot(const float *a, const float *b, uint32_t d);
+uint64_t orc_argmin(const float *v, uint64_t n);
+uint64_t orc_argmax(const float *v, uint64_t n);
+
+/* Zig std PRNG restatement (parity unpinned). */
+typedef struct { uint64_t s[4]; } orc_xoshiro;
+void orc_zig_prng_init(orc_xoshiro *r, uint64_t seed);
+uint64_t orc_zig_next(orc_xoshiro *r);
+uint64_t orc_zig_uint_less_than(orc_xoshiro *r, uint64_t less_than);
+double orc_zig_float_f64(orc_xoshiro *r);
+int orc_weighted_sample(orc_xoshiro *r, const float *w, uint64_t n, uint64_t *out);
+
+/* Optional per-iteration outputs. Any pointer may be NULL. */
+typedef struct {
+  float *trace;           /* [max_iters][k][dim]: centroids after iteration t */
+  uint32_t *empties;      /* [max_iters]: empty clusters reseeded in iteration t */
+  float *wcss_trace;      /* [max_iters]: wcss accumulated in iteration t */
+} orc_fit_extras;
+
+/* kmeans.fit. init_centroids == NULL selects k-means++ seeding with `seed`.
+ * tol = -INFINITY never breaks early.  Outputs: centroids [k][dim],
+ * assignments [n], wcss, iters_run. */
+int orc_kmeans_fit(const float *vectors, uint64_t n, uint32_t dim, uint32_t k,
+                   uint32_t max_iters, float tol, uint64_t seed,
+                   uint32_t n_threads, const float *init_centroids,
+                   float *centroids, uint32_t *assignments, float *wcss,
+                   uint32_t *iters_run, const orc_fit_extras *extras);
+
+typedef struct {
+  float *trace;          /* [max_iters][m][ksub][dsub] */
+  uint32_t *iters_run;   /* [m] */
+  float *wcss;           /* [m]  final wcss per subspace */
+  uint32_t *empties;     /* [m]  total empty reseeds per subspace */
+} orc_train_extras;
+
+/* pq.train with runtime m / ksub / iteration control.
+ * init_codebooks [m][ksub][dsub] or NULL (k-means++ with seed +% subspace). */
+int orc_pq_train(const float *residuals, uint64_t n, uint32_t dim, uint32_t m,
+                 uint32_t ksub, const float *init_codebooks, uint64_t seed,
+                 uint32_t max_iters, float tol, uint32_t n_threads,
+                 float *codebooks, const orc_train_extras *extras);
+
+/* Batched PQ.encode: codes token-major [n][m], u8 when ksub <= 256 else u16. */
+int orc_pq_encode(const float *residuals, uint64_t n, uint32_t dim, uint32_t m,
+                  uint32_t ksub, const float *codebooks, void *codes,
+                  uint32_t n_threads);
+
+/* Best-vs-second margin census of the exhaustive encode: number of
+ * (vector, subspace) pairs whose (second - best) / second <= rel_tol. */
+int orc_pq_near_ties(const float *residuals, uint64_t n, uint32_t dim,
+                     uint32_t m, uint32_t ksub, const float *codebooks,
+                     float rel_tol, uint64_t *count, uint32_t n_threads);
+
+int orc_pq_decode(const void *codes, uint64_t n, uint32_t dim, uint32_t m,
+                  uint32_t ksub, const float *codebooks, float *out);
+
+/* table[((mm * ksub) + c) * n_q + i] = dot(query_i[mm], codebook[mm][c]) */
+int orc_pq_distance_table(const float *queries, uint32_t n_q, uint32_t dim,
+                          uint32_t m, uint32_t ksub, const float *codebooks,
+                          float *table, uint64_t table_len);
+
+#ifdef __cplusplus
+}
+#endif
+#endif

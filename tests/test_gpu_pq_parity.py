@@ -1,0 +1,155 @@
+"""GPU parity: the HIP path against the CPU oracle, bit for bit.
+
+Every comparison is on bytes (codes) or float bit patterns (codebooks); the
+oracle restates src/index/pq.zig and src/tac/kmeans.zig.
+"""
+import numpy as np
+import pytest
+
+from oracle import binding as orc
+from tac_gpu import device, errors, kmeans, pq, synth
+
+NEVER = float("-inf")
+pytestmark = pytest.mark.gpu
+
+
+def _bits(a):
+    return np.ascontiguousarray(a, dtype=np.float32).view(np.uint32)
+
+
+def _workload_rows(n, seed=0, zipf=0.0, sigma=0.15):
+    w = synth.Workload("t", n, 64, 4096, zipf, sigma, 16, 256, 1, seed)
+    return synth.residuals(w, n)
+
+
+@pytest.mark.parametrize("m,ksub", [(16, 256), (32, 256), (8, 256), (64, 256), (16, 1024),
+                                    (16, 3), (21, 17)])
+def test_encode_matches_oracle(gpu, m, ksub):
+    dim = 64 if m != 21 else 63
+    n = 5003
+    x = _workload_rows(n, seed=3)[:, :dim].copy() if dim == 64 else \
+        np.random.default_rng(1).standard_normal((n, dim)).astype(np.float32) * 0.2
+    cb = synth.gauss_codebooks(7, m, ksub, dim // m, 0.05).reshape(-1)
+    p = pq.PQ(dim=dim, sub_dim=dim // m, codebooks=cb, m=m, ksub=ksub)
+    got = p.encode_many(x)
+    ref = orc.pq_encode(x, dim, m, ksub, cb, n_threads=8)
+    assert got.dtype == ref.dtype
+    assert np.array_equal(got, ref), f"{np.count_nonzero(got != ref)} codes differ"
+
+
+def test_encode_ties_pick_lowest_index(gpu):
+    # Codewords 5, 9 and 200 of every subspace are identical and nearest to
+    # every vector: the reference keeps the first (strict <), i.e. 5.
+    m, ksub, dim, n = 16, 256, 64, 777
+    rng = np.random.default_rng(5)
+    cb = (rng.standard_normal((m, ksub, 4)) * 3.0 + 10.0).astype(np.float32)
+    x = (rng.standard_normal((n, dim)) * 0.01).astype(np.float32)
+    for j in (5, 9, 200):
+        cb[:, j, :] = 0.0
+    got = pq.PQ(dim, 4, cb.reshape(-1), m, ksub).encode_many(x)
+    assert np.all(got == 5)
+    assert np.array_equal(got, orc.pq_encode(x, dim, m, ksub, cb))
+
+
+@pytest.mark.parametrize("n", [1, 63, 257, 4097, 16385])
+def test_encode_ragged_sizes(gpu, n):
+    x = _workload_rows(n, seed=11)
+    cb = synth.gauss_codebooks(2, 16, 256, 4, 0.05)
+    got = pq.PQ(64, 4, cb.reshape(-1), 16, 256).encode_many(x)
+    assert np.array_equal(got, orc.pq_encode(x, 64, 16, 256, cb))
+
+
+def test_train_chunk_matches_oracle_every_iteration(gpu):
+    """Full small-chunk workload: 117,645 x 64, m16 k256, 20 Lloyd iterations,
+    seeded-shuffle init; codebooks bit-exact after every iteration, codes
+    bit-exact."""
+    w, x, init = synth.workload("chunk-117k")
+    got = pq.train(x, w.dim, 0, m=w.m, ksub=w.ksub, max_iters=w.iters, tol=NEVER,
+                   init_codebooks=init, trace=True)
+    ref = orc.pq_train(x, w.dim, w.m, w.ksub, init=init, max_iters=w.iters, tol=NEVER,
+                       n_threads=16, trace=True)
+    assert ref.status == 0
+    for t in range(w.iters):
+        diff = np.count_nonzero(_bits(got.stats.trace[t]) != _bits(ref.trace[t]))
+        assert diff == 0, f"iteration {t}: {diff} codebook floats differ"
+    assert np.array_equal(_bits(got.codebooks), _bits(ref.codebooks))
+    assert np.array_equal(got.stats.iters_run, ref.iters_run)
+    assert np.array_equal(got.stats.empties, ref.empties)
+    codes = got.encode_many(x)
+    assert np.array_equal(codes, orc.pq_encode(x, w.dim, w.m, w.ksub, ref.codebooks, n_threads=16))
+
+
+@pytest.mark.parametrize("m,ksub,n", [(32, 256, 20000), (8, 256, 20000), (16, 1024, 30000),
+                                      (64, 16, 3000), (16, 256, 257)])
+def test_train_shapes_match_oracle(gpu, m, ksub, n):
+    x = _workload_rows(n, seed=9, zipf=1.1)
+    init = synth.shuffle_init(x, m, ksub, 4)
+    got = pq.train(x, 64, 0, m=m, ksub=ksub, max_iters=6, tol=NEVER, init_codebooks=init)
+    ref = orc.pq_train(x, 64, m, ksub, init=init, max_iters=6, tol=NEVER, n_threads=16)
+    assert np.array_equal(_bits(got.codebooks), _bits(ref.codebooks))
+
+
+def test_train_early_break_matches_oracle(gpu):
+    # Default tol = 1e-4: subspaces stop at different iterations.
+    x = _workload_rows(20000, seed=21)
+    init = synth.shuffle_init(x, 16, 64, 8)
+    got = pq.train(x, 64, 0, m=16, ksub=64, max_iters=25, tol=1e-4, init_codebooks=init)
+    ref = orc.pq_train(x, 64, 16, 64, init=init, max_iters=25, tol=1e-4, n_threads=16)
+    assert np.array_equal(got.stats.iters_run, ref.iters_run)
+    assert np.array_equal(_bits(got.stats.wcss), _bits(ref.wcss))
+    assert np.array_equal(_bits(got.codebooks), _bits(ref.codebooks))
+
+
+def test_train_forced_empty_clusters(gpu):
+    # Many init codewords sit on top of each other: most clusters empty in
+    # iteration 0 and get reseeded from the farthest points.
+    x = _workload_rows(5000, seed=4)
+    init = np.repeat(x[:4].reshape(4, 16, 4).transpose(1, 0, 2), 64, axis=1).copy()  # [16][256][4]
+    got = pq.train(x, 64, 0, m=16, ksub=256, max_iters=5, tol=NEVER, init_codebooks=init)
+    ref = orc.pq_train(x, 64, 16, 256, init=init, max_iters=5, tol=NEVER, n_threads=16)
+    assert ref.empties.sum() > 0
+    assert np.array_equal(got.stats.empties, ref.empties)
+    assert np.array_equal(_bits(got.codebooks), _bits(ref.codebooks))
+
+
+def test_train_degenerate_k_ge_n(gpu):
+    x = _workload_rows(200, seed=2)
+    got = pq.train(x, 64, 0, m=16, ksub=256, init_codebooks=None)
+    ref = orc.pq_train(x, 64, 16, 256, init=None)
+    assert np.array_equal(_bits(got.codebooks), _bits(ref.codebooks))
+    assert np.all(got.stats.iters_run == 0)
+
+
+def test_kmeans_fit_matches_oracle(gpu):
+    rng = np.random.default_rng(0xDE7E2)
+    v = rng.standard_normal(600 * 4).astype(np.float32)
+    init = v[: 32 * 4].copy()
+    got = kmeans.fit(v, 4, 32, max_iters=25, init_centroids=init)
+    ref = orc.kmeans_fit(v, 4, 32, max_iters=25, init=init)
+    assert got.iters_run == ref.iters_run
+    assert np.array_equal(got.assignments, ref.assignments)
+    assert np.array_equal(_bits(got.centroids), _bits(ref.centroids))
+    assert np.float32(got.wcss).view(np.uint32) == np.float32(ref.wcss).view(np.uint32)
+
+
+def test_device_resident_train_then_encode(gpu):
+    w, x, init = synth.workload("chunk-117k", n=40000)
+    dx = device.DeviceArray.from_host(x)
+    dinit = device.DeviceArray.from_host(init)
+    dcb = device.DeviceArray(init.shape, np.float32)
+    dcodes = device.DeviceArray((x.shape[0], w.m), np.uint8)
+    device.train_device(dx, x.shape[0], 64, w.m, w.ksub, dinit, dcb, 4, NEVER)
+    device.encode_device(dx, x.shape[0], 64, w.m, w.ksub, dcb, dcodes)
+    cb = dcb.to_host()
+    ref = orc.pq_train(x, 64, w.m, w.ksub, init=init, max_iters=4, tol=NEVER, n_threads=16)
+    assert np.array_equal(_bits(cb), _bits(ref.codebooks))
+    assert np.array_equal(dcodes.to_host(), orc.pq_encode(x, 64, w.m, w.ksub, ref.codebooks, 16))
+
+
+def test_argument_errors_on_device_path(gpu):
+    with pytest.raises(errors.DimNotDivisibleByM):
+        pq.train(np.zeros(33, np.float32), 33, 1)
+    with pytest.raises(errors.EmptyCorpus):
+        pq.train(np.zeros(0, np.float32), 32, 1)
+    with pytest.raises(errors.Unsupported):  # k-means++ seeding is not implemented
+        pq.train(np.zeros((300, 32), np.float32), 32, 1)
