@@ -182,6 +182,8 @@ def main() -> int:
                    "ksub": ksub, "lloyd_iters": iters, "init": "seeded-shuffle prefix",
                    "tol": "never (fixed iterations)", "codes": "u8 token-major"},
         "train_s": round(mean_train, 5),
+        "exact_rescans_per_pass": round(prof.exact_rescans / max(prof.assign_launches
+                                                                  + prof.encode_launches, 1)),
         "encode_s": round(mean_encode, 6),
         "encode_mvec_per_s": round(n / mean_encode / 1e6, 2),
         "roofline": {

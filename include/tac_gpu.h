@@ -155,6 +155,8 @@ typedef struct tac_gpu_profile {
   double assign_ms;      uint64_t assign_launches;   /* Lloyd assignment kernel */
   double update_ms;      uint64_t update_iters;      /* sort + fold + reseed + convergence */
   double encode_ms;      uint64_t encode_launches;   /* encode kernel */
+  uint64_t exact_rescans; /* (vector, subspace) searches the pruned pass left to a full
+                             reference scan (near ties across codeword blocks) */
 } tac_gpu_profile;
 int tac_gpu_profile_enable(int enable);
 int tac_gpu_profile_read(tac_gpu_profile *out, int reset);

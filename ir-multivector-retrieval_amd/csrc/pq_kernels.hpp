@@ -19,7 +19,7 @@
 //   e       [M][n] f32   distance to the assigned codeword (min_to_any)
 //   hist    [M][T][K]    per-tile histogram, then the tile's exclusive offset
 //   counts  [M][K]       cluster sizes; start [M][K] bucket starts
-//   sorted  [M][D][n]    residual components grouped by cluster, stable
+//   sorted  [M][n][DP]   residual records grouped by cluster, stable order
 #pragma once
 
 #include <hip/hip_runtime.h>
@@ -28,7 +28,8 @@
 namespace tacgpu {
 
 constexpr int kBlock = 256;        // threads per block for the streaming kernels
-constexpr int kScatterTile = 16384; // elements per stable-scatter tile (4 waves)
+constexpr int kSortTile = 2048;    // vectors per stable counting-sort tile (4 waves)
+constexpr int kFoldBatch = 8;      // 64-record loads in flight per fold wave
 constexpr int kWave = 64;
 
 template <int D>
@@ -77,59 +78,241 @@ __device__ __forceinline__ float exact_l2sq(const float (&x)[D], const float (&c
 }
 
 // ---------------------------------------------------------------------------
-// Layout transform: token-major residuals [n][dim] -> xs [M][n][DP].
+// Layout transform: token-major residuals [n][dim] -> xs [M][n][DP].  A block
+// moves `rows` consecutive rows: coalesced row loads into LDS, then one
+// contiguous [rows][DP] slab per subspace.
 // ---------------------------------------------------------------------------
 template <int D>
 __global__ __launch_bounds__(kBlock) void transpose_kernel(
-    const float* __restrict__ x, float* __restrict__ xs, uint64_t n, uint32_t dim) {
+    const float* __restrict__ x, float* __restrict__ xs, uint64_t n, uint32_t dim,
+    uint32_t rows) {
   constexpr int DP = Pad<D>::value;
-  const uint32_t m = blockIdx.y;
-  const uint64_t i = (uint64_t)blockIdx.x * kBlock + threadIdx.x;
-  if (i >= n) return;
-  const float* src = x + i * dim + (uint64_t)m * D;
-  float v[DP];
-#pragma unroll
-  for (int k = 0; k < DP; ++k) v[k] = k < D ? src[k] : 0.0f;
-  float* dst = xs + ((uint64_t)m * n + i) * DP;
-  if constexpr (DP == 1) {
-    dst[0] = v[0];
-  } else if constexpr (DP == 2) {
-    *reinterpret_cast<float2*>(dst) = make_float2(v[0], v[1]);
-  } else if constexpr (DP == 4) {
-    *reinterpret_cast<float4*>(dst) = make_float4(v[0], v[1], v[2], v[3]);
-  } else {
-    *reinterpret_cast<float4*>(dst) = make_float4(v[0], v[1], v[2], v[3]);
-    *reinterpret_cast<float4*>(dst + 4) = make_float4(v[4], v[5], v[6], v[7]);
+  extern __shared__ float tile[];  // [rows][dim + 1]
+  const uint32_t M = dim / D;
+  const uint64_t row0 = (uint64_t)blockIdx.x * rows;
+  const uint32_t nrows = row0 + rows <= n ? rows : (uint32_t)(n - row0);
+  const uint32_t ld = dim + 1;
+  const float* src = x + row0 * dim;
+  for (uint32_t f = threadIdx.x; f < nrows * dim; f += blockDim.x)
+    tile[(f / dim) * ld + f % dim] = src[f];
+  __syncthreads();
+  const uint32_t slab = nrows * DP;
+  for (uint32_t f = threadIdx.x; f < M * slab; f += blockDim.x) {
+    const uint32_t m = f / slab, r = (f % slab) / DP, k = f % DP;
+    xs[((uint64_t)m * n + row0 + r) * DP + k] = k < (uint32_t)D ? tile[r * ld + m * D + k] : 0.0f;
   }
 }
 
-// Stage one subspace codebook [K][D] into LDS as [K][DP] (pads = 0).
+// ---------------------------------------------------------------------------
+// Exact nearest-codeword search, pruned.
+//
+// The reference scans every codeword with the unfused distance
+// ref(c) = sum_k (x_k - c_k)^2 and keeps the first minimum.  Here a first
+// pass evaluates the expanded form a(c) = ||c||^2 - 2 x.c with FMAs (dsub
+// FMAs per pair) in blocks of kPruneBlock consecutive codewords and keeps,
+// per vector, the smallest block minimum best1 (block bblk) and the
+// smallest minimum of every other block best2.
+//
+// Rounding-error analysis bounds how far a(c) + ||x||^2 and ref(c) can each
+// stray from the true T(c) = ||x - c||^2, with g_n = n u / (1 - n u),
+// u = 2^-24:
+//   |a(c) + ||x||^2 - T(c)| <= Ea = 2 g_D (1 + g_D) (cmax^2 + 2 |x| cmax)
+//   |ref(c) - T(c)|         <= g_{D+2} T(c)
+// (||c||^2 is computed with error <= g_D ||c||^2 and the FMA chain adds
+// g_D (||c||^2 + sum |2 x_k c_k|), bounded by Cauchy-Schwarz).  Hence if
+// best2 - best1 > 2 Ea (1 + g_{D+2}) + g_{D+2} (|best1 + |x|^2| +
+// |best2 + |x|^2|) (the bound is doubled and given an absolute floor for
+// underflow), every codeword outside block bblk is strictly farther under
+// ref() than some codeword inside it, and the reference's first-index argmin
+// is the first-index argmin of block bblk, recomputed with ref().  Otherwise
+// (a near tie across blocks, or any non-finite or overflowing value) the
+// vector is resolved by the full reference scan.  Either way the result
+// equals the exhaustive reference scan bit for bit.
+// ---------------------------------------------------------------------------
+constexpr int kPruneBlock = 8;
+
+// Stage codebook [K][D] into LDS as lcb [Kp][DP] (pads 0) and lnc [Kp]
+// (squared norms, pads +inf); *lmax receives the bits of max ||c||^2 over
+// the real codewords (>= 0x7f800000 when any codeword is not finite).  The
+// caller zeroes *lmax and synchronises before, and synchronises after.
 template <int D>
-__device__ __forceinline__ void stage_codebook(float* lds, const float* __restrict__ cb,
-                                               uint32_t K) {
+__device__ __forceinline__ void stage_pruned(float* lcb, float* lnc, uint32_t* lmax,
+                                             const float* __restrict__ cb, uint32_t K,
+                                             uint32_t Kp) {
   constexpr int DP = Pad<D>::value;
-  for (uint32_t t = threadIdx.x; t < K * DP; t += blockDim.x) {
-    const uint32_t c = t / DP, k = t % DP;
-    lds[t] = k < (uint32_t)D ? cb[(uint64_t)c * D + k] : 0.0f;
+  for (uint32_t c = threadIdx.x; c < Kp; c += blockDim.x) {
+    float v[DP];
+#pragma unroll
+    for (int k = 0; k < DP; ++k) v[k] = (c < K && k < D) ? cb[(uint64_t)c * D + k] : 0.0f;
+    float s = 0.0f;
+#pragma unroll
+    for (int k = 0; k < D; ++k) s = s + v[k] * v[k];
+#pragma unroll
+    for (int k = 0; k < DP; ++k) lcb[c * DP + k] = v[k];
+    lnc[c] = c < K ? s : __builtin_inff();
+    if (c < K) atomicMax(lmax, __float_as_uint(s));
   }
+}
+
+// Reference scan over all K codewords: vec.argmin when SEED_FIRST
+// (src/util/vec.zig:271-283, best = dists[0]), PQ.encode otherwise
+// (src/index/pq.zig:64-73, best_d = +inf).  Strict < keeps the first index.
+template <int D, bool SEED_FIRST>
+__device__ __forceinline__ void reference_scan(const float (&x)[D], const float* lcb, uint32_t K,
+                                               uint32_t& idx, float& best) {
+  constexpr int DP = Pad<D>::value;
+  uint32_t c = 0;
+  if (SEED_FIRST) {
+    float c0[D];
+    load_padded<D>(lcb, c0);
+    best = exact_l2sq<D>(x, c0);
+    c = 1;
+  } else {
+    best = __builtin_inff();
+  }
+  idx = 0;
+  for (; c < K; ++c) {
+    float cv[D];
+    load_padded<D>(lcb + c * DP, cv);
+    const float d = exact_l2sq<D>(x, cv);
+    if (d < best) {
+      best = d;
+      idx = c;
+    }
+  }
+}
+
+template <int D, int VPT, bool SEED_FIRST>
+__device__ __forceinline__ void pruned_argmin(const float (&x)[VPT][D], const float* lcb,
+                                              const float* lnc, uint32_t K, uint32_t Kp,
+                                              uint32_t maxbits, uint32_t (&bidx)[VPT],
+                                              float (&bdist)[VPT], uint32_t& rescans) {
+  constexpr int DP = Pad<D>::value;
+  constexpr int B = kPruneBlock;
+  if (maxbits >= 0x7f800000u) {  // a non-finite codeword: reference scan for all
+#pragma unroll
+    for (int j = 0; j < VPT; ++j) reference_scan<D, SEED_FIRST>(x[j], lcb, K, bidx[j], bdist[j]);
+    rescans += VPT;
+    return;
+  }
+  float xp[VPT][D];
+#pragma unroll
+  for (int j = 0; j < VPT; ++j)
+#pragma unroll
+    for (int k = 0; k < D; ++k) xp[j][k] = -2.0f * x[j][k];
+  float best1[VPT], best2[VPT];
+  uint32_t bblk[VPT];
+#pragma unroll
+  for (int j = 0; j < VPT; ++j) {
+    best1[j] = __builtin_inff();
+    best2[j] = __builtin_inff();
+    bblk[j] = 0;
+  }
+  const uint32_t nb = Kp / B;
+  for (uint32_t b = 0; b < nb; ++b) {
+    float mb[VPT];
+#pragma unroll
+    for (int j = 0; j < VPT; ++j) mb[j] = __builtin_inff();
+#pragma unroll
+    for (int t = 0; t < B; ++t) {
+      const uint32_t c = b * B + t;
+      float cv[D];
+      load_padded<D>(lcb + c * DP, cv);
+      const float nc = lnc[c];
+#pragma unroll
+      for (int j = 0; j < VPT; ++j) {
+        float acc = nc;
+#pragma unroll
+        for (int k = 0; k < D; ++k) acc = __builtin_fmaf(xp[j][k], cv[k], acc);
+        mb[j] = fminf(mb[j], acc);
+      }
+    }
+    // Top-2 over block minima with compares and selects only (a min on these
+    // loop-carried values would add NaN-quieting instructions).
+#pragma unroll
+    for (int j = 0; j < VPT; ++j) {
+      const bool lt1 = mb[j] < best1[j];
+      const bool lt2 = mb[j] < best2[j];
+      best2[j] = lt1 ? best1[j] : (lt2 ? mb[j] : best2[j]);
+      best1[j] = lt1 ? mb[j] : best1[j];
+      bblk[j] = lt1 ? b : bblk[j];
+    }
+  }
+  constexpr float u = 5.9604644775390625e-8f;  // 2^-24
+  constexpr float gD = (float)D * u / (1.0f - (float)D * u);
+  constexpr float gR = (float)(D + 2) * u / (1.0f - (float)(D + 2) * u);
+  const float cmax2 = __uint_as_float(maxbits);
+  const float cmax = sqrtf(cmax2);
+#pragma unroll
+  for (int j = 0; j < VPT; ++j) {
+    float x2 = 0.0f;
+#pragma unroll
+    for (int k = 0; k < D; ++k) x2 = x2 + x[j][k] * x[j][k];
+    const float nx = sqrtf(x2);
+    const float ea = 2.0f * gD * (1.0f + gD) * (cmax2 + 2.0f * nx * cmax);
+    float thr = 2.0f * ea * (1.0f + gR) + gR * (fabsf(best2[j] + x2) + fabsf(best1[j] + x2));
+    thr = 2.0f * thr + 1e-30f;
+    // Below this magnitude no product or sum of the first pass overflows.
+    const bool tame = (cmax2 + 2.0f * nx * cmax) < 1e38f;
+    const bool ok = tame && (best2[j] - best1[j]) > thr;  // false on NaN
+    if (ok) {
+      float best = __builtin_inff();
+      uint32_t idx = bblk[j] * B;
+#pragma unroll
+      for (int t = 0; t < B; ++t) {
+        const uint32_t c = bblk[j] * B + t;
+        if (c < K) {
+          float cv[D];
+          load_padded<D>(lcb + c * DP, cv);
+          const float d = exact_l2sq<D>(x[j], cv);
+          if (d < best) {
+            best = d;
+            idx = c;
+          }
+        }
+      }
+      bidx[j] = idx;
+      bdist[j] = best;
+    } else {
+      reference_scan<D, SEED_FIRST>(x[j], lcb, K, bidx[j], bdist[j]);
+      ++rescans;
+    }
+  }
+}
+
+__device__ __forceinline__ void flush_rescans(uint32_t mine, uint32_t* lcount,
+                                              unsigned long long* __restrict__ rescans) {
+  if (mine) atomicAdd(lcount, mine);
+  __syncthreads();
+  if (threadIdx.x == 0 && *lcount) atomicAdd(rescans, (unsigned long long)*lcount);
 }
 
 // ---------------------------------------------------------------------------
 // Lloyd assignment (src/tac/kmeans.zig:344-365).  One block = one subspace
-// and kBlock*VPT consecutive vectors; every thread owns VPT vectors and
-// scans all K codewords, read from LDS as wave-wide broadcasts.
-// vec.argmin semantics: best starts at codeword 0, replaced on strict <.
+// and kBlock*VPT consecutive vectors; every thread owns VPT vectors.
+// vec.argmin semantics: the first index of the minimum.
 // ---------------------------------------------------------------------------
 template <int D, int VPT>
 __global__ __launch_bounds__(kBlock) void assign_kernel(
     const float* __restrict__ xs, const float* __restrict__ cb,
     uint16_t* __restrict__ codes, float* __restrict__ e,
-    const uint32_t* __restrict__ done, uint64_t n, uint32_t K) {
+    const uint32_t* __restrict__ done, uint64_t n, uint32_t K,
+    unsigned long long* __restrict__ rescans) {
   constexpr int DP = Pad<D>::value;
-  extern __shared__ float lds[];
+  extern __shared__ __attribute__((aligned(16))) float lds[];
   const uint32_t m = blockIdx.y;
   if (done[m]) return;
-  stage_codebook<D>(lds, cb + (uint64_t)m * K * D, K);
+  const uint32_t Kp = (K + kPruneBlock - 1) / kPruneBlock * kPruneBlock;
+  float* lcb = lds;                 // [Kp][DP], 16-byte aligned records
+  float* lnc = lds + Kp * DP;       // [Kp]
+  uint32_t& lmax = *reinterpret_cast<uint32_t*>(lnc + Kp);
+  uint32_t& lcount = *(&lmax + 1);
+  if (threadIdx.x == 0) {
+    lmax = 0;
+    lcount = 0;
+  }
+  __syncthreads();
+  stage_pruned<D>(lcb, lnc, &lmax, cb + (uint64_t)m * K * D, K, Kp);
   __syncthreads();
 
   const uint64_t base = (uint64_t)blockIdx.x * (kBlock * VPT) + threadIdx.x;
@@ -145,28 +328,10 @@ __global__ __launch_bounds__(kBlock) void assign_kernel(
       for (int k = 0; k < D; ++k) x[j][k] = 0.0f;
     }
   }
-  float best[VPT];
   uint32_t bidx[VPT];
-  {
-    float c0[D];
-    load_padded<D>(lds, c0);
-#pragma unroll
-    for (int j = 0; j < VPT; ++j) {
-      best[j] = exact_l2sq<D>(x[j], c0);
-      bidx[j] = 0;
-    }
-  }
-  for (uint32_t c = 1; c < K; ++c) {
-    float cv[D];
-    load_padded<D>(lds + c * DP, cv);
-#pragma unroll
-    for (int j = 0; j < VPT; ++j) {
-      const float d = exact_l2sq<D>(x[j], cv);
-      const bool lt = d < best[j];
-      best[j] = lt ? d : best[j];
-      bidx[j] = lt ? c : bidx[j];
-    }
-  }
+  float best[VPT];
+  uint32_t mine = 0;
+  pruned_argmin<D, VPT, true>(x, lcb, lnc, K, Kp, lmax, bidx, best, mine);
 #pragma unroll
   for (int j = 0; j < VPT; ++j) {
     const uint64_t i = base + (uint64_t)j * kBlock;
@@ -175,10 +340,15 @@ __global__ __launch_bounds__(kBlock) void assign_kernel(
       e[(uint64_t)m * n + i] = best[j];
     }
   }
+  flush_rescans(mine, &lcount, rescans);
 }
 
 // ---------------------------------------------------------------------------
-// Stable counting sort by code, step 1: per-tile histograms.
+// Stable counting sort by code.  The vectors of a subspace are cut into
+// tiles of kSortTile consecutive indices; a cluster's members end up in
+// sorted[m][start[c] ...] in ascending vector order.
+//
+// Step 1: per-tile histograms hist[m][t][c].
 // ---------------------------------------------------------------------------
 __global__ __launch_bounds__(kBlock) void hist_kernel(
     const uint16_t* __restrict__ codes, uint32_t* __restrict__ hist,
@@ -188,8 +358,8 @@ __global__ __launch_bounds__(kBlock) void hist_kernel(
   if (done[m]) return;
   for (uint32_t c = threadIdx.x; c < K; c += blockDim.x) h[c] = 0;
   __syncthreads();
-  const uint64_t lo = (uint64_t)t * kScatterTile;
-  const uint64_t hi = lo + kScatterTile < n ? lo + kScatterTile : n;
+  const uint64_t lo = (uint64_t)t * kSortTile;
+  const uint64_t hi = lo + kSortTile < n ? lo + kSortTile : n;
   const uint16_t* cm = codes + (uint64_t)m * n;
   for (uint64_t i = lo + threadIdx.x; i < hi; i += blockDim.x) atomicAdd(&h[cm[i]], 1u);
   __syncthreads();
@@ -197,15 +367,17 @@ __global__ __launch_bounds__(kBlock) void hist_kernel(
   for (uint32_t c = threadIdx.x; c < K; c += blockDim.x) out[c] = h[c];
 }
 
-// Step 2: per subspace, exclusive scan of every code's tile counts (in
-// place), cluster sizes, and bucket starts (exclusive scan over codes).
-// Block = 1024 threads = K codes x P tile ranges.
+// Step 2: per subspace, every code's tile counts become exclusive offsets
+// over tiles (in place); cluster sizes and bucket starts (exclusive scan
+// over codes) are written alongside.  Block = 1024 threads = K codes x P
+// contiguous tile ranges; loads are batched 8 deep.
 __global__ __launch_bounds__(1024) void scan_kernel(
     uint32_t* __restrict__ hist, uint32_t* __restrict__ counts,
     uint32_t* __restrict__ start, const uint32_t* __restrict__ done, uint32_t K,
     uint32_t T) {
   __shared__ uint32_t part_sum[1024];
   __shared__ uint32_t cnt[1024];
+  __shared__ uint32_t wsum[16];
   const uint32_t m = blockIdx.x;
   if (done[m]) return;
   const uint32_t P = blockDim.x / K;  // tile ranges per code (K <= 1024)
@@ -215,15 +387,36 @@ __global__ __launch_bounds__(1024) void scan_kernel(
   const uint32_t t0 = p * per < T ? p * per : T;
   const uint32_t t1 = t0 + per < T ? t0 + per : T;
   uint32_t* hm = hist + (uint64_t)m * T * K;
+  constexpr uint32_t B = 8;
   uint32_t s = 0;
-  if (active)
-    for (uint32_t t = t0; t < t1; ++t) s += hm[(uint64_t)t * K + c];
+  if (active) {
+    uint32_t t = t0;
+    for (; t + B <= t1; t += B) {
+      uint32_t v[B];
+#pragma unroll
+      for (uint32_t q = 0; q < B; ++q) v[q] = hm[(uint64_t)(t + q) * K + c];
+#pragma unroll
+      for (uint32_t q = 0; q < B; ++q) s += v[q];
+    }
+    for (; t < t1; ++t) s += hm[(uint64_t)t * K + c];
+  }
   part_sum[threadIdx.x] = s;
   __syncthreads();
   if (active) {
     uint32_t run = 0;
     for (uint32_t q = 0; q < p; ++q) run += part_sum[q * K + c];
-    for (uint32_t t = t0; t < t1; ++t) {
+    uint32_t t = t0;
+    for (; t + B <= t1; t += B) {
+      uint32_t v[B];
+#pragma unroll
+      for (uint32_t q = 0; q < B; ++q) v[q] = hm[(uint64_t)(t + q) * K + c];
+#pragma unroll
+      for (uint32_t q = 0; q < B; ++q) {
+        hm[(uint64_t)(t + q) * K + c] = run;
+        run += v[q];
+      }
+    }
+    for (; t < t1; ++t) {
       const uint32_t v = hm[(uint64_t)t * K + c];
       hm[(uint64_t)t * K + c] = run;
       run += v;
@@ -231,56 +424,119 @@ __global__ __launch_bounds__(1024) void scan_kernel(
     if (p == P - 1) cnt[c] = run;
   }
   __syncthreads();
-  if (threadIdx.x == 0) {
-    uint32_t acc = 0;
-    for (uint32_t q = 0; q < K; ++q) {
-      start[(uint64_t)m * K + q] = acc;
-      counts[(uint64_t)m * K + q] = cnt[q];
-      acc += cnt[q];
+  // exclusive scan of cnt[0..K) with the whole block
+  const uint32_t per_c = (K + blockDim.x - 1) / blockDim.x;
+  const uint32_t c0 = threadIdx.x * per_c;
+  uint32_t local = 0;
+  for (uint32_t q = 0; q < per_c; ++q)
+    if (c0 + q < K) local += cnt[c0 + q];
+  const uint32_t lane = threadIdx.x % kWave, w = threadIdx.x / kWave;
+  uint32_t incl = local;
+#pragma unroll
+  for (int off = 1; off < kWave; off <<= 1) {
+    const uint32_t o = __shfl_up(incl, off, kWave);
+    if (lane >= (uint32_t)off) incl += o;
+  }
+  if (lane == kWave - 1) wsum[w] = incl;
+  __syncthreads();
+  uint32_t before = 0;
+  for (uint32_t q = 0; q < w; ++q) before += wsum[q];
+  uint32_t acc = before + incl - local;
+  for (uint32_t q = 0; q < per_c; ++q) {
+    if (c0 + q < K) {
+      start[(uint64_t)m * K + c0 + q] = acc;
+      counts[(uint64_t)m * K + c0 + q] = cnt[c0 + q];
+      acc += cnt[c0 + q];
     }
   }
 }
 
-// Step 3: stable scatter.  Each of the 4 waves owns a quarter of the tile,
-// walks it in rounds of 64 in index order, and ranks equal codes inside a
-// round with ballots (match on every code bit).  Values land in
-// sorted[m][d][start[code] + tile offset + wave prefix + running rank].
+// Block-wide exclusive scan of one value per thread (blockDim.x <= 1024).
+__device__ __forceinline__ uint32_t block_exclusive_scan(uint32_t v, uint32_t* wsum) {
+  const uint32_t lane = threadIdx.x % kWave, w = threadIdx.x / kWave;
+  uint32_t incl = v;
+#pragma unroll
+  for (int off = 1; off < kWave; off <<= 1) {
+    const uint32_t o = __shfl_up(incl, off, kWave);
+    if (lane >= (uint32_t)off) incl += o;
+  }
+  if (lane == kWave - 1) wsum[w] = incl;
+  __syncthreads();
+  uint32_t before = 0;
+  for (uint32_t q = 0; q < w; ++q) before += wsum[q];
+  __syncthreads();
+  return before + incl - v;
+}
+
+// Workgroups are dispatched round-robin over the 8 XCDs; hand each XCD a
+// contiguous range of logical tiles so neighbouring tiles (which write
+// neighbouring runs of the same clusters) share one L2.
+__device__ __forceinline__ uint32_t xcd_contiguous(uint32_t linear, uint32_t total) {
+  const uint32_t per = (total + 7) / 8;
+  return (linear % 8) * per + linear / 8;
+}
+
+// Step 3: stable scatter through LDS.  Each of the 4 waves owns a quarter of
+// the tile and walks it in rounds of 64 in index order, ranking equal codes
+// inside a round with ballots (match on every code bit).  The tile is first
+// sorted by code in LDS, then every cluster's run leaves as consecutive
+// DP-float records: sorted[m][start[c] + tile offset + rank][0..DP).
 template <int D>
 __global__ __launch_bounds__(kBlock) void scatter_kernel(
     const float* __restrict__ xs, const uint16_t* __restrict__ codes,
     const uint32_t* __restrict__ hist, const uint32_t* __restrict__ start,
     float* __restrict__ sorted, const uint32_t* __restrict__ done, uint64_t n,
-    uint32_t K, uint32_t T, uint32_t code_bits) {
+    uint32_t K, uint32_t T, uint32_t M, uint32_t code_bits) {
   constexpr int DP = Pad<D>::value;
-  extern __shared__ uint32_t run[];  // [4][K]
-  const uint32_t m = blockIdx.y, t = blockIdx.x;
+  extern __shared__ __attribute__((aligned(16))) uint32_t smem[];
+  float* sx = reinterpret_cast<float*>(smem);  // [kSortTile][DP]
+  uint32_t* gdest = smem + kSortTile * DP;     // [kSortTile]
+  uint32_t* run = gdest + kSortTile;           // [4][K]
+  uint32_t* delta = run + 4 * K;               // [K]
+  __shared__ uint32_t wsum[kBlock / kWave];
+  const uint32_t logical = xcd_contiguous(blockIdx.x, gridDim.x);
+  if (logical >= M * T) return;
+  const uint32_t m = logical / T, t = logical % T;
   if (done[m]) return;
   const uint32_t w = threadIdx.x / kWave, lane = threadIdx.x % kWave;
-  constexpr uint32_t kQuarter = kScatterTile / 4;
-  const uint64_t tile_lo = (uint64_t)t * kScatterTile;
+  constexpr uint32_t kQuarter = kSortTile / 4;
+  const uint64_t tile_lo = (uint64_t)t * kSortTile;
+  const uint64_t tile_hi = tile_lo + kSortTile < n ? tile_lo + kSortTile : n;
   const uint64_t lo = tile_lo + (uint64_t)w * kQuarter;
-  const uint64_t hi_tile = tile_lo + kScatterTile < n ? tile_lo + kScatterTile : n;
-  const uint64_t hi = lo + kQuarter < hi_tile ? lo + kQuarter : hi_tile;
+  const uint64_t hi = lo + kQuarter < tile_hi ? lo + kQuarter : tile_hi;
   const uint16_t* cm = codes + (uint64_t)m * n;
 
   for (uint32_t c = threadIdx.x; c < 4 * K; c += blockDim.x) run[c] = 0;
   __syncthreads();
   for (uint64_t i = lo + lane; i < hi; i += kWave) atomicAdd(&run[w * K + cm[i]], 1u);
   __syncthreads();
+
+  // Per code: tile-local bucket start (scan over codes), wave prefixes, and
+  // delta = global start of the tile's run - local start.
+  const uint32_t per_c = (K + blockDim.x - 1) / blockDim.x;
+  const uint32_t c0 = threadIdx.x * per_c;
+  uint32_t tot = 0;
+  for (uint32_t q = 0; q < per_c; ++q)
+    if (c0 + q < K)
+      tot += run[c0 + q] + run[K + c0 + q] + run[2 * K + c0 + q] + run[3 * K + c0 + q];
+  uint32_t ls = block_exclusive_scan(tot, wsum);
   const uint32_t* hm = hist + ((uint64_t)m * T + t) * K;
-  for (uint32_t c = threadIdx.x; c < K; c += blockDim.x) {
-    uint32_t acc = start[(uint64_t)m * K + c] + hm[c];
-    for (uint32_t q = 0; q < 4; ++q) {
-      const uint32_t v = run[q * K + c];
-      run[q * K + c] = acc;
+  for (uint32_t q = 0; q < per_c; ++q) {
+    const uint32_t c = c0 + q;
+    if (c >= K) break;
+    delta[c] = start[(uint64_t)m * K + c] + hm[c] - ls;
+    uint32_t acc = ls;
+    for (uint32_t ww = 0; ww < 4; ++ww) {
+      const uint32_t v = run[ww * K + c];
+      run[ww * K + c] = acc;
       acc += v;
     }
+    ls = acc;
   }
   __syncthreads();
 
   const uint64_t lt_mask = (lane == 0) ? 0ull : (~0ull >> (64 - lane));
   const float* xm = xs + (uint64_t)m * n * DP;
-  float* sm = sorted + (uint64_t)m * D * n;
   uint32_t* myrun = run + w * K;
   for (uint64_t r = lo; r < hi; r += kWave) {
     const uint64_t i = r + lane;
@@ -294,51 +550,103 @@ __global__ __launch_bounds__(kBlock) void scatter_kernel(
     }
     const uint32_t rank = __popcll(match & lt_mask);
     const uint32_t total = __popcll(match);
-    uint32_t pos = 0;
-    if (valid) pos = myrun[code] + rank;
+    uint32_t lp = 0;
+    if (valid) lp = myrun[code] + rank;
     __builtin_amdgcn_wave_barrier();
-    if (valid && rank == total - 1) myrun[code] = pos + 1;
+    if (valid && rank == total - 1) myrun[code] = lp + 1;
     __builtin_amdgcn_wave_barrier();
     if (valid) {
-      float v[D];
-      load_padded<D>(xm + i * DP, v);
+      const float* src = xm + i * DP;
+      float* dst = sx + lp * DP;
 #pragma unroll
-      for (int k = 0; k < D; ++k) sm[(uint64_t)k * n + pos] = v[k];
+      for (int k = 0; k < DP; k += (DP >= 4 ? 4 : DP)) {
+        if constexpr (DP >= 4)
+          *reinterpret_cast<float4*>(dst + k) = *reinterpret_cast<const float4*>(src + k);
+        else if constexpr (DP == 2)
+          *reinterpret_cast<float2*>(dst) = *reinterpret_cast<const float2*>(src);
+        else
+          dst[0] = src[0];
+      }
+      gdest[lp] = lp + delta[code];
+    }
+  }
+  __syncthreads();
+
+  const uint32_t len = (uint32_t)(tile_hi - tile_lo);
+  float* sm = sorted + (uint64_t)m * n * DP;
+  for (uint32_t lp = threadIdx.x; lp < len; lp += blockDim.x) {
+    const float* src = sx + lp * DP;
+    float* dst = sm + (uint64_t)gdest[lp] * DP;
+#pragma unroll
+    for (int k = 0; k < DP; k += (DP >= 4 ? 4 : DP)) {
+      if constexpr (DP >= 4)
+        *reinterpret_cast<float4*>(dst + k) = *reinterpret_cast<const float4*>(src + k);
+      else if constexpr (DP == 2)
+        *reinterpret_cast<float2*>(dst) = *reinterpret_cast<const float2*>(src);
+      else
+        dst[0] = src[0];
     }
   }
 }
 
-// Step 4: one lane per (subspace, dim, cluster) chain folds the cluster's
-// members in ascending vector order and writes the centroid component
-// sum * fl(1 / fl(count)) (src/tac/kmeans.zig:177-198).  Empty clusters
-// are left for reseed_kernel.
+// Step 4: one wave per (subspace, cluster).  The wave streams the cluster's
+// contiguous records with coalesced loads (kFoldBatch x 64 records in
+// flight, staged through LDS) and lanes 0..D-1 fold dimension d in
+// ascending vector order from 0.0f, then write sum * fl(1 / fl(count))
+// (src/tac/kmeans.zig:177-198).  Empty clusters are left for reseed_kernel.
 template <int D>
-__global__ __launch_bounds__(kBlock) void fold_kernel(
+__global__ __launch_bounds__(kWave) void fold_kernel(
     const float* __restrict__ sorted, const uint32_t* __restrict__ counts,
     const uint32_t* __restrict__ start, float* __restrict__ cb,
-    const uint32_t* __restrict__ done, uint64_t n, uint32_t M, uint32_t K) {
-  const uint64_t g = (uint64_t)blockIdx.x * blockDim.x + threadIdx.x;
-  if (g >= (uint64_t)M * D * K) return;
-  const uint32_t c = g % K;
-  const uint32_t d = (g / K) % D;
-  const uint32_t m = g / ((uint64_t)K * D);
+    const uint32_t* __restrict__ done, uint64_t n, uint32_t K) {
+  constexpr int DP = Pad<D>::value;
+  constexpr uint32_t U = kFoldBatch;
+  __shared__ float buf[U * kWave * DP];
+  const uint32_t m = blockIdx.x / K, c = blockIdx.x % K;
   if (done[m]) return;
   const uint32_t cnt = counts[(uint64_t)m * K + c];
   if (cnt == 0) return;
-  const float* p = sorted + ((uint64_t)m * D + d) * n + start[(uint64_t)m * K + c];
-  float s = 0.0f;
-  uint32_t j = 0;
-  constexpr uint32_t U = 16;
-  for (; j + U <= cnt; j += U) {
-    float v[U];
+  const uint32_t lane = threadIdx.x;
+  const float* p = sorted + ((uint64_t)m * n + start[(uint64_t)m * K + c]) * DP;
+  float v[U][DP];
+  auto load_batch = [&](uint32_t j0) {
 #pragma unroll
-    for (uint32_t q = 0; q < U; ++q) v[q] = p[j + q];
+    for (uint32_t u = 0; u < U; ++u) {
+      const uint32_t j = j0 + u * kWave + lane;
+      if (j < cnt) {
+        const float* q = p + (uint64_t)j * DP;
 #pragma unroll
-    for (uint32_t q = 0; q < U; ++q) s = s + v[q];
+        for (int k = 0; k < DP; k += (DP >= 4 ? 4 : DP)) {
+          if constexpr (DP >= 4) {
+            const float4 a = *reinterpret_cast<const float4*>(q + k);
+            v[u][k] = a.x; v[u][k + 1] = a.y; v[u][k + 2] = a.z; v[u][k + 3] = a.w;
+          } else if constexpr (DP == 2) {
+            const float2 a = *reinterpret_cast<const float2*>(q);
+            v[u][0] = a.x; v[u][1] = a.y;
+          } else {
+            v[u][0] = q[0];
+          }
+        }
+      }
+    }
+  };
+  float acc = 0.0f;
+  load_batch(0);
+  for (uint32_t j0 = 0; j0 < cnt; j0 += U * kWave) {
+#pragma unroll
+    for (uint32_t u = 0; u < U; ++u)
+#pragma unroll
+      for (int k = 0; k < DP; ++k) buf[(u * kWave + lane) * DP + k] = v[u][k];
+    __syncthreads();
+    if (j0 + U * kWave < cnt) load_batch(j0 + U * kWave);
+    const uint32_t len = cnt - j0 < U * kWave ? cnt - j0 : U * kWave;
+    if (lane < (uint32_t)D) {
+#pragma unroll 8
+      for (uint32_t jj = 0; jj < len; ++jj) acc = acc + buf[jj * DP + lane];
+    }
+    __syncthreads();
   }
-  for (; j < cnt; ++j) s = s + p[j];
-  const float inv = 1.0f / (float)cnt;
-  cb[((uint64_t)m * K + c) * D + d] = s * inv;
+  if (lane < (uint32_t)D) cb[((uint64_t)m * K + c) * D + lane] = acc * (1.0f / (float)cnt);
 }
 
 // ---------------------------------------------------------------------------
@@ -474,21 +782,29 @@ __global__ void widen_codes_kernel(const uint16_t* __restrict__ codes, uint32_t*
 // PQ.encode (src/index/pq.zig:59-76) over token-major residuals.  A block
 // owns kBlock*VPT consecutive vectors and walks the M subspaces, staging one
 // codebook at a time in LDS; codes collect in LDS and leave as one
-// contiguous [tile][M] row block.  best starts at +inf, strict <.
+// contiguous [tile][M] row block.  best_d starts at +inf, strict <.
 // ---------------------------------------------------------------------------
 template <int D, int VPT, typename CodeT>
 __global__ __launch_bounds__(kBlock) void encode_kernel(
     const float* __restrict__ x, const float* __restrict__ cb, CodeT* __restrict__ codes,
-    uint64_t n, uint32_t dim, uint32_t M, uint32_t K) {
+    uint64_t n, uint32_t dim, uint32_t M, uint32_t K, unsigned long long* __restrict__ rescans) {
   constexpr int DP = Pad<D>::value;
   constexpr uint32_t kTile = kBlock * VPT;
-  extern __shared__ float lds[];
-  float* lcb = lds;
-  CodeT* lcodes = reinterpret_cast<CodeT*>(lds + K * DP);  // [kTile][M]
+  extern __shared__ __attribute__((aligned(16))) float lds[];
+  const uint32_t Kp = (K + kPruneBlock - 1) / kPruneBlock * kPruneBlock;
+  float* lcb = lds;                 // [Kp][DP], 16-byte aligned records
+  float* lnc = lds + Kp * DP;       // [Kp]
+  uint32_t& lmax = *reinterpret_cast<uint32_t*>(lnc + Kp);
+  uint32_t& lcount = *(&lmax + 1);
+  CodeT* lcodes = reinterpret_cast<CodeT*>(&lmax + 2);  // [kTile][M]
   const uint64_t tile_lo = (uint64_t)blockIdx.x * kTile;
+  uint32_t mine = 0;
+  if (threadIdx.x == 0) lcount = 0;
   for (uint32_t m = 0; m < M; ++m) {
     __syncthreads();
-    stage_codebook<D>(lcb, cb + (uint64_t)m * K * D, K);
+    if (threadIdx.x == 0) lmax = 0;
+    __syncthreads();
+    stage_pruned<D>(lcb, lnc, &lmax, cb + (uint64_t)m * K * D, K, Kp);
     __syncthreads();
     float xv[VPT][D];
 #pragma unroll
@@ -498,24 +814,9 @@ __global__ __launch_bounds__(kBlock) void encode_kernel(
 #pragma unroll
       for (int k = 0; k < D; ++k) xv[j][k] = src[k];
     }
-    float best[VPT];
     uint32_t bidx[VPT];
-#pragma unroll
-    for (int j = 0; j < VPT; ++j) {
-      best[j] = __builtin_inff();
-      bidx[j] = 0;
-    }
-    for (uint32_t c = 0; c < K; ++c) {
-      float cv[D];
-      load_padded<D>(lcb + c * DP, cv);
-#pragma unroll
-      for (int j = 0; j < VPT; ++j) {
-        const float d = exact_l2sq<D>(xv[j], cv);
-        const bool lt = d < best[j];
-        best[j] = lt ? d : best[j];
-        bidx[j] = lt ? c : bidx[j];
-      }
-    }
+    float best[VPT];
+    pruned_argmin<D, VPT, false>(xv, lcb, lnc, K, Kp, lmax, bidx, best, mine);
 #pragma unroll
     for (int j = 0; j < VPT; ++j)
       lcodes[((uint32_t)j * kBlock + threadIdx.x) * M + m] = (CodeT)bidx[j];
@@ -525,6 +826,7 @@ __global__ __launch_bounds__(kBlock) void encode_kernel(
   const uint64_t total = rows * M;
   CodeT* dst = codes + tile_lo * M;
   for (uint64_t q = threadIdx.x; q < total; q += kBlock) dst[q] = lcodes[q];
+  flush_rescans(mine, &lcount, rescans);
 }
 
 // PQ.decode (src/index/pq.zig:79-88): out[i][m*D + k] = cb[m][code[i][m]][k].

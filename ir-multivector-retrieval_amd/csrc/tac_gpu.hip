@@ -76,7 +76,7 @@ struct DeviceState {
   hipEvent_t last_done = nullptr;
   // training / encode workspace
   Buffer xs, codes, e, hist, counts, start, sorted, flags, scal, trace, io_in, io_out, io_cb,
-      io_init;
+      io_init, counter;
   // measurement
   std::vector<hipEvent_t> events;
 };
@@ -164,6 +164,25 @@ int event_at(DeviceState &ds, size_t idx, hipEvent_t *out) {
   return TAC_OK;
 }
 
+// Device counter of vectors the pruned search resolved by a full reference
+// scan; zeroed per call, added to the profile when measuring.
+int counter_begin(DeviceState &ds, hipStream_t s, unsigned long long **out) {
+  int st = ensure(ds, ds.counter, sizeof(unsigned long long));
+  if (st) return st;
+  HIP_TRY(hipMemsetAsync(ds.counter.ptr, 0, sizeof(unsigned long long), s));
+  *out = reinterpret_cast<unsigned long long *>(ds.counter.ptr);
+  return TAC_OK;
+}
+
+int counter_collect(DeviceState &ds, hipStream_t s) {
+  unsigned long long v = 0;
+  HIP_TRY(hipMemcpyAsync(&v, ds.counter.ptr, sizeof(v), hipMemcpyDeviceToHost, s));
+  HIP_TRY(hipStreamSynchronize(s));
+  std::lock_guard<std::mutex> g(g_profile_mu);
+  g_prof.exact_rescans += v;
+  return TAC_OK;
+}
+
 uint32_t pad_of(uint32_t d) { return d <= 1 ? 1 : d <= 2 ? 2 : d <= 4 ? 4 : 8; }
 
 uint32_t code_bits(uint32_t K) {
@@ -191,32 +210,50 @@ int validate_pq(uint64_t n, uint32_t dim, uint32_t m, uint32_t ksub) {
 
 template <int D>
 struct Launch {
-  static constexpr int VPT = D <= 2 ? 8 : D <= 4 ? 4 : 2;
+  static int transpose(const float *x, float *xs, uint64_t n, uint32_t dim, hipStream_t s) {
+    uint32_t rows = 16384 / (dim + 1);
+    if (rows > 64) rows = 64;
+    if (rows == 0) return TAC_ERR_UNSUPPORTED;
+    const size_t lds = (size_t)rows * (dim + 1) * sizeof(float);
+    transpose_kernel<D><<<(unsigned)((n + rows - 1) / rows), kBlock, lds, s>>>(x, xs, n, dim,
+                                                                            rows);
+    return TAC_OK;
+  }
+  static constexpr int VPT = D <= 4 ? 8 : 4;  // vectors per thread in assign / encode
 
-  static void transpose(const float *x, float *xs, uint64_t n, uint32_t dim, uint32_t M,
-                        hipStream_t s) {
-    dim3 grid((unsigned)((n + kBlock - 1) / kBlock), M);
-    transpose_kernel<D><<<grid, kBlock, 0, s>>>(x, xs, n, dim);
-  }
   static void assign(const float *xs, const float *cb, uint16_t *codes, float *e,
-                     const uint32_t *done, uint64_t n, uint32_t M, uint32_t K, hipStream_t s) {
+                     const uint32_t *done, uint64_t n, uint32_t M, uint32_t K,
+                     unsigned long long *rescans, hipStream_t s) {
     dim3 grid((unsigned)((n + kBlock * VPT - 1) / (kBlock * VPT)), M);
-    const size_t lds = (size_t)K * Pad<D>::value * sizeof(float);
-    assign_kernel<D, VPT><<<grid, kBlock, lds, s>>>(xs, cb, codes, e, done, n, K);
+    const uint32_t Kp = (K + kPruneBlock - 1) / kPruneBlock * kPruneBlock;
+    const size_t lds = (size_t)Kp * (Pad<D>::value + 1) * sizeof(float) + 2 * sizeof(uint32_t);
+    assign_kernel<D, VPT><<<grid, kBlock, lds, s>>>(xs, cb, codes, e, done, n, K, rescans);
   }
-  static void scatter(const float *xs, const uint16_t *codes, const uint32_t *hist,
-                      const uint32_t *start, float *sorted, const uint32_t *done, uint64_t n,
-                      uint32_t M, uint32_t K, uint32_t T, hipStream_t s) {
-    dim3 grid(T, M);
-    scatter_kernel<D><<<grid, kBlock, 4 * K * sizeof(uint32_t), s>>>(
-        xs, codes, hist, start, sorted, done, n, K, T, code_bits(K));
+  static int scatter(const float *xs, const uint16_t *codes, const uint32_t *hist,
+                     const uint32_t *start, float *sorted, const uint32_t *done, uint64_t n,
+                     uint32_t M, uint32_t K, uint32_t T, hipStream_t s) {
+    const size_t lds = (size_t)kSortTile * Pad<D>::value * sizeof(float) +
+                       (size_t)kSortTile * sizeof(uint32_t) + (size_t)5 * K * sizeof(uint32_t);
+    if (lds > 65536) {
+      static bool raised = false;
+      if (!raised) {
+        const hipError_t e = hipFuncSetAttribute((const void *)scatter_kernel<D>,
+                                                 hipFuncAttributeMaxDynamicSharedMemorySize,
+                                                 (int)lds);
+        if (e != hipSuccess) return hip_status("hipFuncSetAttribute(scatter_kernel)", e);
+        raised = true;
+      }
+    }
+    const uint32_t total = M * T;
+    const uint32_t blocks = 8 * ((total + 7) / 8);
+    scatter_kernel<D><<<blocks, kBlock, lds, s>>>(xs, codes, hist, start, sorted, done, n, K, T,
+                                                  M, code_bits(K));
+    return TAC_OK;
   }
   static void fold(const float *sorted, const uint32_t *counts, const uint32_t *start,
                    float *cb, const uint32_t *done, uint64_t n, uint32_t M, uint32_t K,
                    hipStream_t s) {
-    const uint64_t lanes = (uint64_t)M * D * K;
-    fold_kernel<D><<<(unsigned)((lanes + kBlock - 1) / kBlock), kBlock, 0, s>>>(
-        sorted, counts, start, cb, done, n, M, K);
+    fold_kernel<D><<<M * K, kWave, 0, s>>>(sorted, counts, start, cb, done, n, K);
   }
   static void reseed(const float *xs, float *e, const uint32_t *counts, float *cb,
                      uint32_t *empties, const uint32_t *done, uint64_t n, uint32_t M, uint32_t K,
@@ -225,18 +262,19 @@ struct Launch {
   }
   template <typename CodeT>
   static int encode(const float *x, const float *cb, CodeT *codes, uint64_t n, uint32_t dim,
-                    uint32_t M, uint32_t K, hipStream_t s) {
-    const size_t cb_lds = (size_t)K * Pad<D>::value * sizeof(float);
+                    uint32_t M, uint32_t K, unsigned long long *rescans, hipStream_t s) {
+    const uint32_t Kp = (K + kPruneBlock - 1) / kPruneBlock * kPruneBlock;
+    const size_t cb_lds = (size_t)Kp * (Pad<D>::value + 1) * sizeof(float) + 2 * sizeof(uint32_t);
     const size_t per_row = (size_t)M * sizeof(CodeT);
     if (per_row * kBlock * 2 + cb_lds <= 65536) {
       constexpr int V = 2;
       const size_t lds = cb_lds + per_row * kBlock * V;
       encode_kernel<D, V, CodeT><<<(unsigned)((n + kBlock * V - 1) / (kBlock * V)), kBlock, lds,
-                                   s>>>(x, cb, codes, n, dim, M, K);
+                                   s>>>(x, cb, codes, n, dim, M, K, rescans);
     } else if (per_row * kBlock + cb_lds <= 65536) {
       const size_t lds = cb_lds + per_row * kBlock;
       encode_kernel<D, 1, CodeT><<<(unsigned)((n + kBlock - 1) / kBlock), kBlock, lds, s>>>(
-          x, cb, codes, n, dim, M, K);
+          x, cb, codes, n, dim, M, K, rescans);
     } else {
       return TAC_ERR_UNSUPPORTED;
     }
@@ -322,7 +360,7 @@ int train_core(DeviceState &ds, hipStream_t s, const float *d_x, uint64_t n, uin
     return TAC_OK;
   }
 
-  const uint32_t T = (uint32_t)((n + kScatterTile - 1) / kScatterTile);
+  const uint32_t T = (uint32_t)((n + kSortTile - 1) / kSortTile);
   int st;
   if ((st = ensure(ds, ds.xs, (size_t)M * n * DP * sizeof(float)))) return st;
   if ((st = ensure(ds, ds.codes, (size_t)M * n * sizeof(uint16_t)))) return st;
@@ -330,7 +368,7 @@ int train_core(DeviceState &ds, hipStream_t s, const float *d_x, uint64_t n, uin
   if ((st = ensure(ds, ds.hist, (size_t)M * T * K * sizeof(uint32_t)))) return st;
   if ((st = ensure(ds, ds.counts, (size_t)M * K * sizeof(uint32_t)))) return st;
   if ((st = ensure(ds, ds.start, (size_t)M * K * sizeof(uint32_t)))) return st;
-  if ((st = ensure(ds, ds.sorted, (size_t)M * D * n * sizeof(float)))) return st;
+  if ((st = ensure(ds, ds.sorted, (size_t)M * n * DP * sizeof(float)))) return st;
   if ((st = ensure(ds, ds.flags, (size_t)3 * M * sizeof(uint32_t)))) return st;
   if ((st = ensure(ds, ds.scal, (size_t)2 * M * sizeof(float)))) return st;
   if (want_trace && (st = ensure(ds, ds.trace, (size_t)max_iters * cb_elems * sizeof(float))))
@@ -350,6 +388,8 @@ int train_core(DeviceState &ds, hipStream_t s, const float *d_x, uint64_t n, uin
   float *prev = wcss + M;
   HIP_TRY(hipMemsetAsync(done, 0, 3 * M * sizeof(uint32_t), s));
   HIP_TRY(hipMemsetAsync(wcss, 0, 2 * M * sizeof(float), s));
+  unsigned long long *rescans = nullptr;
+  if ((st = counter_begin(ds, s, &rescans))) return st;
 
   const bool profile = g_profile;
   size_t ev = 0;
@@ -358,7 +398,8 @@ int train_core(DeviceState &ds, hipStream_t s, const float *d_x, uint64_t n, uin
     if ((st = event_at(ds, ev++, &e0))) return st;
     HIP_TRY(hipEventRecord(e0, s));
   }
-  DISPATCH_D(D, transpose(d_x, xs, n, dim, M, s));
+  DISPATCH_D_ST(D, transpose(d_x, xs, n, dim, s));
+  if (st) return st;
   LAUNCH_TRY("transpose_kernel");
   if (profile) {
     if ((st = event_at(ds, ev++, &e1))) return st;
@@ -379,14 +420,15 @@ int train_core(DeviceState &ds, hipStream_t s, const float *d_x, uint64_t n, uin
         return st;
       HIP_TRY(hipEventRecord(a, s));
     }
-    DISPATCH_D(D, assign(xs, out.cb, codes, e, done, n, M, K, s));
+    DISPATCH_D(D, assign(xs, out.cb, codes, e, done, n, M, K, rescans, s));
     LAUNCH_TRY("assign_kernel");
     if (profile) HIP_TRY(hipEventRecord(b, s));
     hist_kernel<<<dim3(T, M), kBlock, hist_lds, s>>>(codes, hist, done, n, K, T);
     LAUNCH_TRY("hist_kernel");
     scan_kernel<<<M, 1024, 0, s>>>(hist, counts, start, done, K, T);
     LAUNCH_TRY("scan_kernel");
-    DISPATCH_D(D, scatter(xs, codes, hist, start, sorted, done, n, M, K, T, s));
+    DISPATCH_D_ST(D, scatter(xs, codes, hist, start, sorted, done, n, M, K, T, s));
+    if (st) return st;
     LAUNCH_TRY("scatter_kernel");
     DISPATCH_D(D, fold(sorted, counts, start, out.cb, done, n, M, K, s));
     LAUNCH_TRY("fold_kernel");
@@ -440,6 +482,7 @@ int train_core(DeviceState &ds, hipStream_t s, const float *d_x, uint64_t n, uin
     if (out.h_wcss_single) *out.h_wcss_single = h_scal[0];
     if (out.h_iters_single) *out.h_iters_single = h_flags[M];
     if (profile) {
+      if ((st = counter_collect(ds, s))) return st;
       std::lock_guard<std::mutex> g(g_profile_mu);
       float ms = 0.0f;
       HIP_TRY(hipEventElapsedTime(&ms, e0, e1));
@@ -464,15 +507,17 @@ int encode_core(DeviceState &ds, hipStream_t s, const float *d_x, uint64_t n, ui
   const bool profile = g_profile;
   hipEvent_t a = nullptr, b = nullptr;
   int st;
+  unsigned long long *rescans = nullptr;
+  if ((st = counter_begin(ds, s, &rescans))) return st;
   if (profile) {
     if ((st = event_at(ds, 0, &a)) || (st = event_at(ds, 1, &b))) return st;
     HIP_TRY(hipEventRecord(a, s));
   }
   st = TAC_OK;
   if (K <= 256) {
-    DISPATCH_D_ST(D, encode<uint8_t>(d_x, d_cb, (uint8_t *)d_codes, n, dim, M, K, s));
+    DISPATCH_D_ST(D, encode<uint8_t>(d_x, d_cb, (uint8_t *)d_codes, n, dim, M, K, rescans, s));
   } else {
-    DISPATCH_D_ST(D, encode<uint16_t>(d_x, d_cb, (uint16_t *)d_codes, n, dim, M, K, s));
+    DISPATCH_D_ST(D, encode<uint16_t>(d_x, d_cb, (uint16_t *)d_codes, n, dim, M, K, rescans, s));
   }
   if (st) return st;
   LAUNCH_TRY("encode_kernel");
@@ -481,6 +526,7 @@ int encode_core(DeviceState &ds, hipStream_t s, const float *d_x, uint64_t n, ui
     HIP_TRY(hipEventSynchronize(b));
     float ms = 0.0f;
     HIP_TRY(hipEventElapsedTime(&ms, a, b));
+    if ((st = counter_collect(ds, s))) return st;
     std::lock_guard<std::mutex> g(g_profile_mu);
     g_prof.encode_ms += ms;
     g_prof.encode_launches += 1;
@@ -600,7 +646,7 @@ int tac_gpu_release_workspace(void) {
   HIP_TRY(hipDeviceSynchronize());
   Buffer *bufs[] = {&ds->xs,   &ds->codes,  &ds->e,     &ds->hist,  &ds->counts,
                     &ds->start, &ds->sorted, &ds->flags, &ds->scal,  &ds->trace,
-                    &ds->io_in, &ds->io_out, &ds->io_cb, &ds->io_init};
+                    &ds->io_in, &ds->io_out, &ds->io_cb, &ds->io_init, &ds->counter};
   for (Buffer *b : bufs) {
     if (b->ptr) HIP_TRY(hipFree(b->ptr));
     b->ptr = nullptr;

@@ -52,6 +52,7 @@ class Profile(ctypes.Structure):
         ("update_iters", c_u64),
         ("encode_ms", ctypes.c_double),
         ("encode_launches", c_u64),
+        ("exact_rescans", c_u64),
     ]
 
 

@@ -107,6 +107,7 @@ class KernelTimes:
     update_iters: int
     encode_ms: float
     encode_launches: int
+    exact_rescans: int
 
 
 def profile_enable(on: bool = True) -> None:
@@ -117,4 +118,5 @@ def profile_read(reset: bool = True) -> KernelTimes:
     p = Profile()
     errors.check(lib.tac_gpu_profile_read(ctypes.byref(p), 1 if reset else 0))
     return KernelTimes(p.transpose_ms, p.transpose_launches, p.assign_ms, p.assign_launches,
-                       p.update_ms, p.update_iters, p.encode_ms, p.encode_launches)
+                       p.update_ms, p.update_iters, p.encode_ms, p.encode_launches,
+                       p.exact_rescans)

@@ -14,7 +14,7 @@ pytestmark = pytest.mark.gpu
 
 
 def _bits(a):
-    return np.ascontiguousarray(a, dtype=np.float32).view(np.uint32)
+    return np.ascontiguousarray(a, dtype=np.float32).reshape(-1).view(np.uint32)
 
 
 def _workload_rows(n, seed=0, zipf=0.0, sigma=0.15):
@@ -153,3 +153,86 @@ def test_argument_errors_on_device_path(gpu):
         pq.train(np.zeros(0, np.float32), 32, 1)
     with pytest.raises(errors.Unsupported):  # k-means++ seeding is not implemented
         pq.train(np.zeros((300, 32), np.float32), 32, 1)
+
+
+# ---- the pruned exact search against the exhaustive reference scan --------
+
+def _encode_both(x, cb, m, ksub):
+    dim = x.shape[1]
+    got = pq.PQ(dim, dim // m, np.ascontiguousarray(cb, np.float32).reshape(-1), m,
+                ksub).encode_many(x)
+    return got, orc.pq_encode(x, dim, m, ksub, cb)
+
+
+def test_pruned_search_near_ties_across_blocks(gpu):
+    # Codewords 3 and 200 (different blocks of 8) sit symmetrically around
+    # every vector's sub-vector, so their distances tie in exact arithmetic
+    # and differ by at most rounding; codeword 77 is a few ulps farther.
+    rng = np.random.default_rng(31)
+    n, m, ksub = 4096, 16, 256
+    x = (rng.standard_normal((n, 64)) * 0.2).astype(np.float32)
+    cb = (rng.standard_normal((m, ksub, 4)) * 0.2 + 3.0).astype(np.float32)
+    delta = np.float32(1e-3)
+    for mm in range(m):
+        centre = x[0, 4 * mm:4 * mm + 4]
+        cb[mm, 3] = centre + delta
+        cb[mm, 200] = centre - delta
+        cb[mm, 77] = centre + delta * np.float32(1.0000005)
+    x[:] = x[0]  # every vector equals the one the ties were built around
+    x += (rng.integers(-2, 3, x.shape) * np.float32(1e-9)).astype(np.float32)
+    got, ref = _encode_both(x, cb, m, ksub)
+    assert np.array_equal(got, ref)
+
+
+def test_pruned_search_duplicate_codewords_across_blocks(gpu):
+    rng = np.random.default_rng(32)
+    x = (rng.standard_normal((3000, 64)) * 0.2).astype(np.float32)
+    cb = (rng.standard_normal((16, 256, 4)) * 0.2).astype(np.float32)
+    cb[:, 8 * np.arange(32) + 5] = cb[:, 5:6]  # one codeword repeated in every block
+    got, ref = _encode_both(x, cb, 16, 256)
+    assert np.array_equal(got, ref)
+
+
+def test_pruned_search_wide_bounds(gpu):
+    # A few far-away codewords make cmax large, so the gap test is loose and
+    # many searches fall back to the full scan; results must not change.
+    rng = np.random.default_rng(33)
+    x = (rng.standard_normal((5000, 64)) * 0.2).astype(np.float32)
+    cb = (rng.standard_normal((16, 256, 4)) * 0.2).astype(np.float32)
+    cb[:, 255] = 1e6
+    got, ref = _encode_both(x, cb, 16, 256)
+    assert np.array_equal(got, ref)
+
+
+def test_pruned_search_non_finite_values(gpu):
+    rng = np.random.default_rng(34)
+    x = (rng.standard_normal((700, 64)) * 0.2).astype(np.float32)
+    cb = (rng.standard_normal((16, 64, 4)) * 0.2).astype(np.float32)
+    cb[0, 0, 0] = np.nan          # NaN codeword first: never wins under strict <
+    cb[1, 10, 2] = np.inf
+    cb[2, :, :] = np.float32(3e38)  # squared norms overflow
+    x[5, 0:4] = np.nan
+    x[6, 4:8] = np.inf
+    x[7, :] = np.float32(2e38)
+    got, ref = _encode_both(x, cb, 16, 64)
+    assert np.array_equal(got, ref)
+
+
+@pytest.mark.parametrize("ksub", [1, 2, 7, 8, 9, 100])
+def test_pruned_search_small_and_ragged_ksub(gpu, ksub):
+    x = _workload_rows(3001, seed=ksub)
+    cb = synth.gauss_codebooks(ksub, 16, ksub, 4, 0.1)
+    got, ref = _encode_both(x, cb, 16, ksub)
+    assert np.array_equal(got, ref)
+
+
+def test_train_with_duplicate_init_codewords_across_blocks(gpu):
+    # Lloyd assignment with exact ties spanning codeword blocks in every
+    # iteration's first pass.
+    x = _workload_rows(20000, seed=35, zipf=1.1)
+    init = synth.shuffle_init(x, 16, 256, 3)
+    init[:, 8 * np.arange(32) + 1] = init[:, 1:2]
+    got = pq.train(x, 64, 0, m=16, ksub=256, max_iters=4, tol=NEVER, init_codebooks=init)
+    ref = orc.pq_train(x, 64, 16, 256, init=init, max_iters=4, tol=NEVER, n_threads=16)
+    assert np.array_equal(got.stats.empties, ref.empties)
+    assert np.array_equal(_bits(got.codebooks), _bits(ref.codebooks))
