@@ -1,0 +1,151 @@
+"""The C ABI boundary and the host-side mirrors, without a GPU.
+
+Checks that the shared and static libraries export exactly what
+include/tac_gpu.h declares, that argument errors carry the reference's error
+names and precedence (src/index/pq.zig:165-168, src/tac/kmeans.zig:73-76)
+before any device is touched, and that the synthetic workload generator is
+deterministic.
+"""
+import re
+import subprocess
+from pathlib import Path
+
+import numpy as np
+import pytest
+
+import tac_gpu
+from tac_gpu import _native, device, errors, kmeans, pq, synth
+
+ROOT = Path(__file__).resolve().parent.parent
+HEADER = ROOT / "include" / "tac_gpu.h"
+PKG = ROOT / "ir-multivector-retrieval_amd"
+
+
+def header_functions():
+    text = HEADER.read_text()
+    text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
+    return set(re.findall(r"\b(tac_\w+)\s*\(", text)) - {"tac_status"}
+
+
+def exported(lib: Path):
+    out = subprocess.run(["nm", "-D" if lib.suffix == ".so" else "-g", "--defined-only",
+                          str(lib)], capture_output=True, text=True, check=True).stdout
+    return {line.split()[-1] for line in out.splitlines() if " T " in line}
+
+
+def test_header_matches_ctypes_table():
+    assert header_functions() == set(_native.SIGNATURES)
+
+
+@pytest.mark.parametrize("name", ["libtac_gpu.so", "libtac_gpu.a"])
+def test_libraries_export_every_declared_symbol(name):
+    syms = exported(PKG / "lib" / name)
+    missing = header_functions() - syms
+    assert not missing, missing
+    # nothing but the C ABI leaks out under the tac_ prefix
+    assert {s for s in syms if s.startswith("tac_")} == header_functions()
+
+
+def test_status_names_match_exception_classes():
+    for status, name in enumerate(_native.STATUS_NAMES):
+        assert tac_gpu.lib.tac_gpu_strerror(status).decode() == name
+        if status:
+            assert errors._BY_STATUS[status].__name__ in (name, {"HipError": "HipError"}.get(name))
+    assert tac_gpu.lib.tac_gpu_strerror(999).decode() == "Unknown"
+
+
+def test_train_argument_errors_follow_reference_precedence():
+    # pq.zig:165-168: dim 0, then dim % M, then empty, then len % dim
+    with pytest.raises(errors.DimMismatch):
+        pq.train(np.zeros(0, np.float32), 0, 1)
+    with pytest.raises(errors.DimNotDivisibleByM):
+        pq.train(np.zeros(0, np.float32), 33, 1)  # dim check precedes the empty check
+    with pytest.raises(errors.EmptyCorpus):
+        pq.train(np.zeros(0, np.float32), 32, 1)
+    with pytest.raises(errors.DimMismatch):
+        pq.train(np.zeros(65, np.float32), 32, 1)
+
+
+def test_kmeans_argument_errors_follow_reference_precedence():
+    with pytest.raises(errors.KmeansBudgetTooSmall):  # kmeans.zig:373-377
+        kmeans.fit(np.array([1, 0, 0, 1], np.float32), 2, 0)
+    with pytest.raises(errors.EmptyVectorSet):        # :379-383
+        kmeans.fit(np.zeros(0, np.float32), 2, 1)
+    with pytest.raises(errors.DimMismatch):           # :385-389
+        kmeans.fit(np.array([1, 2, 3], np.float32), 2, 1)
+
+
+def test_c_abi_validates_before_touching_a_device():
+    # Raw C ABI with NULL buffers: shape errors win over everything else.
+    L = tac_gpu.lib
+    assert L.tac_pq_train(None, 10, 33, 32, 256, None, 0, 25, 1e-4, None, None) == 1
+    assert L.tac_pq_train(None, 0, 32, 32, 256, None, 0, 25, 1e-4, None, None) == 3
+    assert L.tac_pq_train(None, 10, 0, 32, 256, None, 0, 25, 1e-4, None, None) == 2
+    assert L.tac_pq_train(None, 10, 32, 32, 0, None, 0, 25, 1e-4, None, None) == 6
+    assert L.tac_pq_train(None, 10, 32, 0, 256, None, 0, 25, 1e-4, None, None) == 14
+    assert L.tac_pq_train(None, 10, 64, 4, 256, None, 0, 25, 1e-4, None, None) == 15  # dsub 16
+    assert L.tac_pq_train(None, 10, 32, 32, 2048, None, 0, 25, 1e-4, None, None) == 15
+    assert L.tac_kmeans_fit(None, 5, 2, 0, 25, 1e-4, 0, None, None, None, None, None) == 6
+    assert L.tac_pq_encode(None, 10, 33, 32, 256, None, None) == 2
+    assert L.tac_pq_encode(None, 0, 32, 32, 256, None, None) == 0  # nothing to encode
+
+
+@pytest.mark.skipif(device.device_count() > 0, reason="a HIP device is present")
+def test_no_device_is_a_clean_error():
+    assert device.device_count() == 0
+    x = np.zeros((300, 32), np.float32)
+    init = np.zeros((32, 256, 1), np.float32)
+    with pytest.raises(errors.NoDevice):
+        pq.train(x, 32, 1, init_codebooks=init)
+    with pytest.raises(errors.NoDevice):
+        pq.PQ(32, 1, init.reshape(-1)).encode_many(x)
+    with pytest.raises(errors.NoDevice):
+        device.DeviceArray((4,), np.float32)
+
+
+def test_cpp_mirror_error_mapping():
+    exe = PKG / "lib" / "host_mirror_check"
+    r = subprocess.run([str(exe), "errors"], capture_output=True, text=True, timeout=60)
+    assert r.returncode == 0, r.stdout + r.stderr
+    assert "host mirror check passed" in r.stdout
+
+
+def test_synthetic_generator_is_deterministic_and_thread_independent():
+    w = synth.WORKLOADS["corpus-1.52m"]
+    a = synth.residuals(w, 5000, threads=1)
+    b = synth.residuals(w, 5000, threads=7)
+    assert a.tobytes() == b.tobytes()
+    # any chunk regenerates on its own
+    c = synth.residuals(w, 1000, first=2000, threads=3)
+    assert c.tobytes() == a[2000:3000].tobytes()
+
+
+def test_synthetic_residuals_follow_the_recipe():
+    # residual = normalize(centre + noise) - centre: adding the centre back
+    # gives a unit vector; Zipf popularity puts the most mass on centre 0.
+    w = synth.WORKLOADS["corpus-1.52m"]
+    r, ids = synth.residuals(w, 20000, with_ids=True)
+    cents = synth.centers(w.seed, w.n_centers, w.dim)
+    v = r.astype(np.float64) + cents[ids]
+    assert np.allclose(np.linalg.norm(v, axis=1), 1.0, atol=1e-5)
+    assert np.allclose(np.linalg.norm(cents, axis=1), 1.0, atol=1e-5)
+    counts = np.bincount(ids, minlength=w.n_centers)
+    assert counts[0] == counts.max() and counts[0] > 20000 / 20
+    # uniform popularity for the small chunk workload
+    w1 = synth.WORKLOADS["chunk-117k"]
+    _, ids1 = synth.residuals(w1, 20000, with_ids=True)
+    assert np.bincount(ids1, minlength=w1.n_centers).max() < 12
+
+
+def test_shuffle_init_picks_distinct_rows():
+    w = synth.WORKLOADS["chunk-117k"]
+    x = synth.residuals(w, 3000)
+    init = synth.shuffle_init(x, 16, 256, 0)
+    for m in (0, 7, 15):
+        rows = {tuple(v) for v in init[m]}
+        assert len(rows) == 256
+        # every codeword is a real sub-vector of the data
+        sub = {tuple(v) for v in x[:, 4 * m:4 * m + 4]}
+        assert rows <= sub
+    # per-subspace seeds differ
+    assert init[0].tobytes() != init[1].tobytes()

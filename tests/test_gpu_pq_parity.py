@@ -236,3 +236,12 @@ def test_train_with_duplicate_init_codewords_across_blocks(gpu):
     ref = orc.pq_train(x, 64, 16, 256, init=init, max_iters=4, tol=NEVER, n_threads=16)
     assert np.array_equal(got.stats.empties, ref.empties)
     assert np.array_equal(_bits(got.codebooks), _bits(ref.codebooks))
+
+
+def test_cpp_mirror_round_trip_on_gpu(gpu):
+    import subprocess
+    from pathlib import Path
+    exe = Path(__file__).resolve().parent.parent / "ir-multivector-retrieval_amd" / "lib" / \
+        "host_mirror_check"
+    r = subprocess.run([str(exe), "gpu"], capture_output=True, text=True, timeout=120)
+    assert r.returncode == 0, r.stdout + r.stderr
