@@ -15,6 +15,7 @@
 // per-subspace flag, so the host never waits inside the loop.
 #include "../../include/tac_gpu.h"
 #include "pq_kernels.hpp"
+#include "kmeanspp.hpp"
 
 #include <hip/hip_runtime.h>
 
@@ -76,7 +77,7 @@ struct DeviceState {
   hipEvent_t last_done = nullptr;
   // training / encode workspace
   Buffer xs, codes, e, hist, counts, start, sorted, flags, scal, trace, io_in, io_out, io_cb,
-      io_init, counter;
+      io_init, counter, kpp_state, kpp_w, kpp_bsum, kpp_bad;
   // measurement
   std::vector<hipEvent_t> events;
 };
@@ -250,6 +251,11 @@ struct Launch {
                                                   M, code_bits(K));
     return TAC_OK;
   }
+  static void kpp_update(const float *xs, float *w, double *bsum, uint32_t *bad,
+                         const KppState *st, float *cb, uint64_t n, uint32_t M, uint32_t K,
+                         uint32_t c, uint32_t NB, hipStream_t s) {
+    kpp_update_kernel<D><<<dim3(NB, M), 256, 0, s>>>(xs, w, bsum, bad, st, cb, n, K, c, NB);
+  }
   static void fold(const float *sorted, const uint32_t *counts, const uint32_t *start,
                    float *cb, const uint32_t *done, uint64_t n, uint32_t M, uint32_t K,
                    hipStream_t s) {
@@ -314,12 +320,49 @@ T *as(Buffer &b) {
 }
 
 struct TrainOut {
-  float *cb;                 // device [M][K][D]: init in, result out
+  float *cb;                 // device [M][K][D]: init in (unless kpp), result out
+  bool kpp;                  // seed with k-means++ (seed +% subspace) instead of cb
+  uint64_t seed;
   uint32_t *d_assign;        // device [n] u32 (M == 1) or null
   tac_pq_train_extras *ex;   // host extras or null
   float *h_wcss_single;      // host scalar (kmeans.fit) or null
   uint32_t *h_iters_single;  // host scalar (kmeans.fit) or null
 };
+
+// k-means++ seeding of all subspaces (src/tac/kmeans.zig:106-136) into
+// out.cb.  Returns the lowest subspace's error, as a serial run of the
+// reference (src/index/pq.zig:180-191) would.
+int kmeanspp(DeviceState &ds, hipStream_t s, const float *xs, uint64_t n, uint32_t M, uint32_t K,
+             uint32_t D, uint64_t seed, float *cb) {
+  const uint32_t NB = (uint32_t)((n + kKppBlock - 1) / kKppBlock);
+  int st;
+  if ((st = ensure(ds, ds.kpp_state, (size_t)M * sizeof(KppState))) ||
+      (st = ensure(ds, ds.kpp_w, (size_t)M * n * sizeof(float))) ||
+      (st = ensure(ds, ds.kpp_bsum, (size_t)M * NB * sizeof(double))) ||
+      (st = ensure(ds, ds.kpp_bad, (size_t)M * sizeof(uint32_t))))
+    return st;
+  KppState *state = as<KppState>(ds.kpp_state);
+  float *w = as<float>(ds.kpp_w);
+  double *bsum = as<double>(ds.kpp_bsum);
+  uint32_t *bad = as<uint32_t>(ds.kpp_bad);
+  kpp_init_kernel<<<(M + 63) / 64, 64, 0, s>>>(state, bad, seed, n, M);
+  LAUNCH_TRY("kpp_init_kernel");
+  for (uint32_t c = 0; c < K; ++c) {
+    DISPATCH_D(D, kpp_update(xs, w, bsum, bad, state, cb, n, M, K, c, NB, s));
+    LAUNCH_TRY("kpp_update_kernel");
+    if (c + 1 == K) break;
+    kpp_select_kernel<<<M, 1024, 0, s>>>(w, bsum, bad, state, n, NB);
+    LAUNCH_TRY("kpp_select_kernel");
+    kpp_fallback_kernel<<<M, 64, 0, s>>>(w, state, n);
+    LAUNCH_TRY("kpp_fallback_kernel");
+  }
+  std::vector<KppState> h(M);
+  HIP_TRY(hipMemcpyAsync(h.data(), state, M * sizeof(KppState), hipMemcpyDeviceToHost, s));
+  HIP_TRY(hipStreamSynchronize(s));
+  for (uint32_t m = 0; m < M; ++m)
+    if (h[m].err) return h[m].err;
+  return TAC_OK;
+}
 
 // Lloyd training of all subspaces.  `out.cb` holds the initial codebooks on
 // entry and the trained ones on return.
@@ -401,6 +444,7 @@ int train_core(DeviceState &ds, hipStream_t s, const float *d_x, uint64_t n, uin
   DISPATCH_D_ST(D, transpose(d_x, xs, n, dim, s));
   if (st) return st;
   LAUNCH_TRY("transpose_kernel");
+  if (out.kpp && (st = kmeanspp(ds, s, xs, n, M, K, D, out.seed, out.cb))) return st;
   if (profile) {
     if ((st = event_at(ds, ev++, &e1))) return st;
     HIP_TRY(hipEventRecord(e1, s));
@@ -646,7 +690,8 @@ int tac_gpu_release_workspace(void) {
   HIP_TRY(hipDeviceSynchronize());
   Buffer *bufs[] = {&ds->xs,   &ds->codes,  &ds->e,     &ds->hist,  &ds->counts,
                     &ds->start, &ds->sorted, &ds->flags, &ds->scal,  &ds->trace,
-                    &ds->io_in, &ds->io_out, &ds->io_cb, &ds->io_init, &ds->counter};
+                    &ds->io_in, &ds->io_out, &ds->io_cb, &ds->io_init, &ds->counter,
+                    &ds->kpp_state, &ds->kpp_w, &ds->kpp_bsum, &ds->kpp_bad};
   for (Buffer *b : bufs) {
     if (b->ptr) HIP_TRY(hipFree(b->ptr));
     b->ptr = nullptr;
@@ -672,11 +717,9 @@ int tac_pq_train_device(const float *d_residuals, uint64_t n, uint32_t dim, uint
                         uint32_t ksub, const float *d_init_codebooks, uint64_t seed,
                         uint32_t max_iters, float tol, float *d_codebooks_out,
                         tac_pq_train_extras *extras, void *stream) {
-  (void)seed;
   int st = validate_pq(n, dim, m, ksub);
   if (st) return st;
   if (!d_residuals || !d_codebooks_out) return TAC_ERR_INVALID_ARGUMENT;
-  if (!d_init_codebooks && (uint64_t)ksub < n) return TAC_ERR_UNSUPPORTED;
   DeviceState *ds = nullptr;
   if ((st = acquire_device(&ds, nullptr))) return st;
   std::lock_guard<std::mutex> g(ds->mu);
@@ -687,7 +730,8 @@ int tac_pq_train_device(const float *d_residuals, uint64_t n, uint32_t dim, uint
   if (d_init_codebooks && d_init_codebooks != d_codebooks_out)
     HIP_TRY(hipMemcpyAsync(d_codebooks_out, d_init_codebooks, cb_bytes, hipMemcpyDeviceToDevice,
                            s));
-  TrainOut out{d_codebooks_out, nullptr, extras, nullptr, nullptr};
+  TrainOut out{d_codebooks_out, d_init_codebooks == nullptr, seed, nullptr, extras, nullptr,
+               nullptr};
   st = train_core(*ds, s, d_residuals, n, dim, m, ksub, max_iters, tol, out);
   if (st) return st;
   return end_call(*ds, s);
@@ -696,11 +740,9 @@ int tac_pq_train_device(const float *d_residuals, uint64_t n, uint32_t dim, uint
 int tac_pq_train(const float *residuals, uint64_t n, uint32_t dim, uint32_t m, uint32_t ksub,
                  const float *init_codebooks, uint64_t seed, uint32_t max_iters, float tol,
                  float *codebooks_out, tac_pq_train_extras *extras) {
-  (void)seed;
   int st = validate_pq(n, dim, m, ksub);
   if (st) return st;
   if (!residuals || !codebooks_out) return TAC_ERR_INVALID_ARGUMENT;
-  if (!init_codebooks && (uint64_t)ksub < n) return TAC_ERR_UNSUPPORTED;
   DeviceState *ds = nullptr;
   if ((st = acquire_device(&ds, nullptr))) return st;
   std::lock_guard<std::mutex> g(ds->mu);
@@ -713,7 +755,8 @@ int tac_pq_train(const float *residuals, uint64_t n, uint32_t dim, uint32_t m, u
   HIP_TRY(hipMemcpyAsync(ds->io_in.ptr, residuals, x_bytes, hipMemcpyHostToDevice, s));
   if (init_codebooks)
     HIP_TRY(hipMemcpyAsync(ds->io_cb.ptr, init_codebooks, cb_bytes, hipMemcpyHostToDevice, s));
-  TrainOut out{as<float>(ds->io_cb), nullptr, extras, nullptr, nullptr};
+  TrainOut out{as<float>(ds->io_cb), init_codebooks == nullptr, seed, nullptr, extras, nullptr,
+               nullptr};
   st = train_core(*ds, s, as<float>(ds->io_in), n, dim, m, ksub, max_iters, tol, out);
   if (st) return st;
   HIP_TRY(hipMemcpyAsync(codebooks_out, ds->io_cb.ptr, cb_bytes, hipMemcpyDeviceToHost, s));
@@ -812,14 +855,12 @@ int tac_kmeans_fit(const float *vectors, uint64_t n, uint32_t dim, uint32_t k,
                    uint32_t max_iters, float tol, uint64_t seed, const float *init_centroids,
                    float *centroids_out, uint32_t *assignments_out, float *wcss_out,
                    uint32_t *iters_run_out) {
-  (void)seed;
   // src/tac/kmeans.zig:73-76
   if (k == 0) return TAC_ERR_KMEANS_BUDGET_TOO_SMALL;
   if (dim == 0) return TAC_ERR_DIM_MISMATCH;
   if (n == 0) return TAC_ERR_EMPTY_VECTOR_SET;
   if (dim > kMaxDsub || k > kMaxKsub || n > 0xFFFFFFFFull) return TAC_ERR_UNSUPPORTED;
   if (!vectors || !centroids_out || !assignments_out) return TAC_ERR_INVALID_ARGUMENT;
-  if (!init_centroids && (uint64_t)k < n) return TAC_ERR_UNSUPPORTED;
   DeviceState *ds = nullptr;
   int st = acquire_device(&ds, nullptr);
   if (st) return st;
@@ -837,7 +878,8 @@ int tac_kmeans_fit(const float *vectors, uint64_t n, uint32_t dim, uint32_t k,
     HIP_TRY(hipMemcpyAsync(ds->io_cb.ptr, init_centroids, cb_bytes, hipMemcpyHostToDevice, s));
   float wcss = 0.0f;
   uint32_t iters = 0;
-  TrainOut out{as<float>(ds->io_cb), as<uint32_t>(ds->io_out), nullptr, &wcss, &iters};
+  TrainOut out{as<float>(ds->io_cb), init_centroids == nullptr, seed, as<uint32_t>(ds->io_out),
+               nullptr, &wcss, &iters};
   st = train_core(*ds, s, as<float>(ds->io_in), n, dim, 1, k, max_iters, tol, out);
   if (st) return st;
   HIP_TRY(hipMemcpyAsync(centroids_out, ds->io_cb.ptr, cb_bytes, hipMemcpyDeviceToHost, s));

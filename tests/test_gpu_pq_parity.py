@@ -151,7 +151,7 @@ def test_argument_errors_on_device_path(gpu):
         pq.train(np.zeros(33, np.float32), 33, 1)
     with pytest.raises(errors.EmptyCorpus):
         pq.train(np.zeros(0, np.float32), 32, 1)
-    with pytest.raises(errors.Unsupported):  # k-means++ seeding is not implemented
+    with pytest.raises(errors.AllZero):  # k-means++ on identical points (rng.zig:65)
         pq.train(np.zeros((300, 32), np.float32), 32, 1)
 
 
@@ -245,3 +245,56 @@ def test_cpp_mirror_round_trip_on_gpu(gpu):
         "host_mirror_check"
     r = subprocess.run([str(exe), "gpu"], capture_output=True, text=True, timeout=120)
     assert r.returncode == 0, r.stdout + r.stderr
+
+
+# ---- k-means++ seeding (src/tac/kmeans.zig:106-136) ------------------------
+
+@pytest.mark.parametrize("m,ksub,n,seed", [(16, 256, 20000, 0xa1b2c3d4), (32, 64, 3000, 7),
+                                           (8, 256, 5000, 123)])
+def test_kmeanspp_train_matches_oracle(gpu, m, ksub, n, seed):
+    # The drop-in pq.train path: no initial codebooks, reference iteration
+    # control (25 iterations, tol 1e-4).
+    x = _workload_rows(n, seed=seed % 97, zipf=1.1)
+    got = pq.train(x, 64, seed, m=m, ksub=ksub)
+    ref = orc.pq_train(x, 64, m, ksub, seed=seed, n_threads=16)
+    assert ref.status == 0
+    assert np.array_equal(got.stats.iters_run, ref.iters_run)
+    assert np.array_equal(_bits(got.codebooks), _bits(ref.codebooks))
+
+
+def test_kmeanspp_first_iteration_is_the_seed_plus_one_update(gpu):
+    x = _workload_rows(8000, seed=5)
+    got = pq.train(x, 64, 99, m=16, ksub=128, max_iters=1, tol=NEVER, trace=True)
+    ref = orc.pq_train(x, 64, 16, 128, seed=99, max_iters=1, tol=NEVER, trace=True)
+    assert np.array_equal(_bits(got.stats.trace[0]), _bits(ref.trace[0]))
+
+
+def test_kmeanspp_all_zero_weights(gpu):
+    # 300 identical points, k = 256: after the first pick every weight is 0
+    # and weightedSample fails with AllZero (src/util/rng.zig:65).
+    x = np.tile(np.linspace(-1, 1, 64, dtype=np.float32), (300, 1))
+    assert orc.pq_train(x, 64, 16, 256, seed=1).status == 10
+    with pytest.raises(errors.AllZero):
+        pq.train(x, 64, 1, m=16, ksub=256)
+
+
+def test_kmeanspp_non_finite_weights(gpu):
+    # distances that overflow to +inf make weightedSample fail with NonFinite
+    x = _workload_rows(600, seed=8)
+    x[17] = 3e38
+    assert orc.pq_train(x, 64, 16, 256, seed=3).status == 9
+    with pytest.raises(errors.NonFinite):
+        pq.train(x, 64, 3, m=16, ksub=256)
+
+
+@pytest.mark.parametrize("k,seed", [(3, 42), (4, 7), (5, 0), (32, 42)])
+def test_kmeans_fit_kmeanspp_matches_oracle(gpu, k, seed):
+    # The reference's own seeded fit cases (src/tac/kmeans.zig:409-501) run
+    # end to end on the GPU and agree with the oracle bit for bit.
+    rng = np.random.default_rng(seed + k)
+    v = rng.standard_normal(600 * 2).astype(np.float32)
+    got = kmeans.fit(v, 2, k, seed=seed, max_iters=50)
+    ref = orc.kmeans_fit(v, 2, k, seed=seed, max_iters=50)
+    assert got.iters_run == ref.iters_run
+    assert np.array_equal(got.assignments, ref.assignments)
+    assert np.array_equal(_bits(got.centroids), _bits(ref.centroids))
