@@ -82,6 +82,9 @@ def main() -> int:
     ap.add_argument("--steps", type=int, default=5)
     ap.add_argument("--warmup", type=int, default=1)
     ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--traffic-pass", action="store_true",
+                    help="short run for hardware-counter passes: one 2-iteration train, one "
+                         "encode and a 1 GiB device-to-device copy (the calibration kernel)")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py measures one GPU only; --gpus {args.gpus} is not supported "
@@ -92,6 +95,7 @@ def main() -> int:
 
     errors.check(lib.tac_gpu_set_device(0))
     info = device.device_info(0)
+    info["name"] = info["name"] or info["arch"]
     w = synth.WORKLOADS[WORKLOAD]
     t0 = time.perf_counter()
     x = synth.residuals(w)
@@ -103,6 +107,17 @@ def main() -> int:
     dinit = device.DeviceArray.from_host(init)
     dcb = device.DeviceArray(init.shape, np.float32)
     dcodes = device.DeviceArray((n, m), np.uint8)
+
+    if args.traffic_pass:
+        device.train_device(dx, n, dim, m, ksub, dinit, dcb, 2, NEVER)
+        device.encode_device(dx, n, dim, m, ksub, dcb, dcodes)
+        a = device.DeviceArray((1 << 28,), np.float32)
+        b = device.DeviceArray((1 << 28,), np.float32)
+        errors.check(lib.tac_gpu_memcpy_dtod(b.ptr, a.ptr, a.nbytes))
+        device.synchronize()
+        print(json.dumps({"traffic_pass": WORKLOAD, "train_iters": 2, "encode": 1,
+                          "copy_bytes": a.nbytes}), flush=True)
+        return 0
 
     def step():
         device.train_device(dx, n, dim, m, ksub, dinit, dcb, iters, NEVER)
@@ -146,13 +161,16 @@ def main() -> int:
     update_avg_ms = prof.update_ms / max(prof.update_iters, 1)
     update_bytes = n * (4 * dim + m * 2)
 
-    traffic = None
-    tfile = ROOT / "profiles" / "assign_kernel_traffic.json"
+    # HBM bytes per launch from the committed FETCH_SIZE / WRITE_SIZE counter
+    # passes (scaled by a 1 GiB copy kernel); null if the summary is absent.
+    traffic = {}
+    tfile = ROOT / "profiles" / f"pq_build_{WORKLOAD}_hbm_traffic.json"
     if tfile.exists():
         try:
-            traffic = json.loads(tfile.read_text()).get("hbm_bytes_per_launch")
-        except (ValueError, OSError):
-            traffic = None
+            for k, v in json.loads(tfile.read_text())["kernels"].items():
+                traffic[k.split("<")[0]] = int(v["read_bytes"]) + int(v["write_bytes"])
+        except (ValueError, OSError, KeyError, TypeError):
+            traffic = {}
 
     # Full-size parity: 2 GPU iterations vs the oracle's 2 iterations.
     gpu_cb2 = None
@@ -190,7 +208,8 @@ def main() -> int:
             "kernel": "assign_kernel (Lloyd assignment, all subspaces, one iteration)",
             "bound": "mfma", "engine": "VALU fp32 (exact unfused distance + argmin)",
             "achieved": round(assign_tflops, 3), "peak": PEAK_FP32_TFLOPS, "unit": "TFLOP/s",
-            "frac": round(assign_tflops / PEAK_FP32_TFLOPS, 4), "traffic": traffic,
+            "frac": round(assign_tflops / PEAK_FP32_TFLOPS, 4),
+            "traffic": traffic.get("assign_kernel"),
             "avg_launch_ms": round(assign_avg_ms, 4), "algorithmic_flop_per_launch": assign_flop,
         },
         "encode_roofline": {
@@ -199,11 +218,16 @@ def main() -> int:
             "valu_frac": round(encode_flop / (encode_avg_ms * 1e-3) / 1e12 / PEAK_FP32_TFLOPS, 4),
             "hbm_gbs": round(encode_bytes / (encode_avg_ms * 1e-3) / 1e9, 1),
             "hbm_frac": round(encode_bytes / (encode_avg_ms * 1e-3) / 1e9 / PEAK_HBM_GBS, 4),
+            "traffic": traffic.get("encode_kernel"),
         },
         "update_roofline": {
             "avg_iter_ms": round(update_avg_ms, 4),
             "hbm_gbs": round(update_bytes / (update_avg_ms * 1e-3) / 1e9, 1),
             "hbm_frac": round(update_bytes / (update_avg_ms * 1e-3) / 1e9 / PEAK_HBM_GBS, 4),
+            "traffic": (sum(traffic.get(k, 0) for k in ("hist_kernel", "scan_kernel",
+                                                          "scatter_kernel", "fold_kernel",
+                                                          "reseed_kernel", "converge_kernel"))
+                        or None),
         },
         "cpu_baseline": None if cpu is None else {
             "value": round(cpu["train_s_per_20_iters"], 3), "unit": "s/20 iters",

@@ -100,8 +100,10 @@ typedef struct tac_pq_train_extras {
  * control.  Each subspace runs kmeans.fit with k = ksub
  * (src/index/pq.zig:301-336):
  *   - init_codebooks [m][ksub][dsub] seeds the Lloyd loop; NULL selects the
- *     reference's k-means++ seeding with seed +% subspace (TAC_ERR_UNSUPPORTED
- *     in this build);
+ *     reference's k-means++ seeding (src/tac/kmeans.zig:106-136) on the GPU,
+ *     subspace m drawing from std.Random.DefaultPrng seeded with seed +% m;
+ *     its errors are TAC_ERR_RNG_NON_FINITE and TAC_ERR_RNG_ALL_ZERO
+ *     (src/util/rng.zig:57-82), reported for the lowest failing subspace;
  *   - tol = 1e-4f, max_iters = 25 are the reference's values
  *     (src/index/pq.zig:319-325); TAC_TOL_NEVER runs exactly max_iters;
  *   - n <= ksub takes the degenerate branch (src/tac/kmeans.zig:88-104).
@@ -139,7 +141,7 @@ int tac_pq_decode(const void *codes, uint64_t n, uint32_t dim, uint32_t m,
  * kmeans.fit (src/tac/kmeans.zig:67-232) for one set of vectors of dim <= 8:
  * centroids_out [k][dim], assignments_out [n] (the last iteration's
  * assignment, KMeansResult.assignments), wcss_out and iters_run_out.
- * init_centroids NULL selects k-means++ (TAC_ERR_UNSUPPORTED in this build).
+ * init_centroids NULL selects k-means++ seeded with `seed`, as tac_pq_train.
  */
 int tac_kmeans_fit(const float *vectors, uint64_t n, uint32_t dim, uint32_t k,
                    uint32_t max_iters, float tol, uint64_t seed,

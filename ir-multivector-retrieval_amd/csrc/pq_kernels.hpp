@@ -779,53 +779,56 @@ __global__ void widen_codes_kernel(const uint16_t* __restrict__ codes, uint32_t*
 }
 
 // ---------------------------------------------------------------------------
-// PQ.encode (src/index/pq.zig:59-76) over token-major residuals.  A block
-// owns kBlock*VPT consecutive vectors and walks the M subspaces, staging one
-// codebook at a time in LDS; codes collect in LDS and leave as one
-// contiguous [tile][M] row block.  best_d starts at +inf, strict <.
+// PQ.encode (src/index/pq.zig:59-76) over token-major residuals.  One block =
+// one subspace m and kBlock*VPT consecutive vectors (the assignment kernel's
+// shape, reading sub-vector m of each row in place).  Block ids are laid out
+// XCD-contiguously with the M subspaces of a row tile adjacent, so the M
+// blocks that read the same rows run together on one XCD and share its L2:
+// each row crosses HBM once instead of once per subspace.  best_d starts at
+// +inf, strict <.
 // ---------------------------------------------------------------------------
 template <int D, int VPT, typename CodeT>
 __global__ __launch_bounds__(kBlock) void encode_kernel(
     const float* __restrict__ x, const float* __restrict__ cb, CodeT* __restrict__ codes,
-    uint64_t n, uint32_t dim, uint32_t M, uint32_t K, unsigned long long* __restrict__ rescans) {
-  constexpr int DP = Pad<D>::value;
+    uint64_t n, uint32_t dim, uint32_t M, uint32_t K, uint32_t tiles,
+    unsigned long long* __restrict__ rescans) {
   constexpr uint32_t kTile = kBlock * VPT;
+  constexpr int DP = Pad<D>::value;
   extern __shared__ __attribute__((aligned(16))) float lds[];
+  const uint32_t logical = xcd_contiguous(blockIdx.x, gridDim.x);
+  if (logical >= tiles * M) return;  // grid padding to a multiple of 8
+  const uint32_t t = logical / M, m = logical % M;
   const uint32_t Kp = (K + kPruneBlock - 1) / kPruneBlock * kPruneBlock;
   float* lcb = lds;                 // [Kp][DP], 16-byte aligned records
   float* lnc = lds + Kp * DP;       // [Kp]
   uint32_t& lmax = *reinterpret_cast<uint32_t*>(lnc + Kp);
   uint32_t& lcount = *(&lmax + 1);
-  CodeT* lcodes = reinterpret_cast<CodeT*>(&lmax + 2);  // [kTile][M]
-  const uint64_t tile_lo = (uint64_t)blockIdx.x * kTile;
-  uint32_t mine = 0;
-  if (threadIdx.x == 0) lcount = 0;
-  for (uint32_t m = 0; m < M; ++m) {
-    __syncthreads();
-    if (threadIdx.x == 0) lmax = 0;
-    __syncthreads();
-    stage_pruned<D>(lcb, lnc, &lmax, cb + (uint64_t)m * K * D, K, Kp);
-    __syncthreads();
-    float xv[VPT][D];
-#pragma unroll
-    for (int j = 0; j < VPT; ++j) {
-      const uint64_t i = tile_lo + (uint64_t)j * kBlock + threadIdx.x;
-      const float* src = x + (i < n ? i : 0) * dim + (uint64_t)m * D;
-#pragma unroll
-      for (int k = 0; k < D; ++k) xv[j][k] = src[k];
-    }
-    uint32_t bidx[VPT];
-    float best[VPT];
-    pruned_argmin<D, VPT, false>(xv, lcb, lnc, K, Kp, lmax, bidx, best, mine);
-#pragma unroll
-    for (int j = 0; j < VPT; ++j)
-      lcodes[((uint32_t)j * kBlock + threadIdx.x) * M + m] = (CodeT)bidx[j];
+  if (threadIdx.x == 0) {
+    lmax = 0;
+    lcount = 0;
   }
   __syncthreads();
-  const uint64_t rows = n - tile_lo < kTile ? n - tile_lo : kTile;
-  const uint64_t total = rows * M;
-  CodeT* dst = codes + tile_lo * M;
-  for (uint64_t q = threadIdx.x; q < total; q += kBlock) dst[q] = lcodes[q];
+  stage_pruned<D>(lcb, lnc, &lmax, cb + (uint64_t)m * K * D, K, Kp);
+  __syncthreads();
+
+  const uint64_t base = (uint64_t)t * kTile + threadIdx.x;
+  float xv[VPT][D];
+#pragma unroll
+  for (int j = 0; j < VPT; ++j) {
+    const uint64_t i = base + (uint64_t)j * kBlock;
+    const float* src = x + (i < n ? i : 0) * dim + (uint64_t)m * D;
+#pragma unroll
+    for (int k = 0; k < D; ++k) xv[j][k] = src[k];
+  }
+  uint32_t bidx[VPT];
+  float best[VPT];
+  uint32_t mine = 0;
+  pruned_argmin<D, VPT, false>(xv, lcb, lnc, K, Kp, lmax, bidx, best, mine);
+#pragma unroll
+  for (int j = 0; j < VPT; ++j) {
+    const uint64_t i = base + (uint64_t)j * kBlock;
+    if (i < n) codes[i * M + m] = (CodeT)bidx[j];
+  }
   flush_rescans(mine, &lcount, rescans);
 }
 

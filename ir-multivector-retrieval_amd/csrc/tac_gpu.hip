@@ -270,20 +270,13 @@ struct Launch {
   static int encode(const float *x, const float *cb, CodeT *codes, uint64_t n, uint32_t dim,
                     uint32_t M, uint32_t K, unsigned long long *rescans, hipStream_t s) {
     const uint32_t Kp = (K + kPruneBlock - 1) / kPruneBlock * kPruneBlock;
-    const size_t cb_lds = (size_t)Kp * (Pad<D>::value + 1) * sizeof(float) + 2 * sizeof(uint32_t);
-    const size_t per_row = (size_t)M * sizeof(CodeT);
-    if (per_row * kBlock * 2 + cb_lds <= 65536) {
-      constexpr int V = 2;
-      const size_t lds = cb_lds + per_row * kBlock * V;
-      encode_kernel<D, V, CodeT><<<(unsigned)((n + kBlock * V - 1) / (kBlock * V)), kBlock, lds,
-                                   s>>>(x, cb, codes, n, dim, M, K, rescans);
-    } else if (per_row * kBlock + cb_lds <= 65536) {
-      const size_t lds = cb_lds + per_row * kBlock;
-      encode_kernel<D, 1, CodeT><<<(unsigned)((n + kBlock - 1) / kBlock), kBlock, lds, s>>>(
-          x, cb, codes, n, dim, M, K, rescans);
-    } else {
-      return TAC_ERR_UNSUPPORTED;
-    }
+    const size_t lds = (size_t)Kp * (Pad<D>::value + 1) * sizeof(float) + 2 * sizeof(uint32_t);
+    const uint64_t tiles = (n + kBlock * VPT - 1) / (kBlock * VPT);
+    const uint64_t total = tiles * M;
+    if (total > 0xFFFFFFF0ull) return TAC_ERR_UNSUPPORTED;
+    const uint32_t blocks = (uint32_t)(8 * ((total + 7) / 8));
+    encode_kernel<D, VPT, CodeT><<<blocks, kBlock, lds, s>>>(x, cb, codes, n, dim, M, K,
+                                                              (uint32_t)tiles, rescans);
     return TAC_OK;
   }
 };

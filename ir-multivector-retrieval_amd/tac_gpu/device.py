@@ -58,6 +58,13 @@ class DeviceArray:
         errors.check(lib.tac_gpu_memcpy_htod(d.ptr, ctypes.c_void_p(a.ctypes.data), a.nbytes))
         return d
 
+    def copy_from_host(self, a: np.ndarray) -> None:
+        """Overwrite the leading a.nbytes bytes with host data."""
+        a = np.ascontiguousarray(a)
+        if a.nbytes > self.nbytes:
+            raise errors.OutBufferWrongSize(f"{a.nbytes} bytes into a {self.nbytes}-byte buffer")
+        errors.check(lib.tac_gpu_memcpy_htod(self.ptr, ctypes.c_void_p(a.ctypes.data), a.nbytes))
+
     def to_host(self) -> np.ndarray:
         out = np.empty(self.shape, dtype=self.dtype)
         errors.check(lib.tac_gpu_memcpy_dtoh(ctypes.c_void_p(out.ctypes.data), self.ptr,

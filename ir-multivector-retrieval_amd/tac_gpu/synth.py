@@ -8,6 +8,7 @@ seeded shuffle, per subspace.
 from __future__ import annotations
 
 import ctypes
+import functools
 import os
 from dataclasses import dataclass
 
@@ -46,6 +47,12 @@ WORKLOADS = {
                                   20),
     "corpus-1.52m-k1024": Workload("corpus-1.52m-k1024", 1_521_797, 64, 32_768, 1.1, 0.15, 16,
                                    1024, 20),
+    # Paper-scale training sample: 60M residuals, Zipf 1.05 over 262,144
+    # centres, sigma 0.12, 25 Lloyd iterations.
+    "paper-60m": Workload("paper-60m", 60_000_000, 64, 262_144, 1.05, 0.12, 16, 256, 25),
+    # Encode-only stream: 200M residuals generated as the paper-scale corpus,
+    # encoded in 10M-vector chunks against fixed N(0, 0.05^2) codebooks.
+    "stream-200m": Workload("stream-200m", 200_000_000, 64, 262_144, 1.05, 0.12, 16, 256, 0),
 }
 
 
@@ -79,17 +86,24 @@ def _p(a: np.ndarray) -> ctypes.c_void_p:
     return ctypes.c_void_p(a.ctypes.data)
 
 
-def centers(seed: int, n_centers: int, dim: int) -> np.ndarray:
+@functools.lru_cache(maxsize=4)
+def _centers(seed: int, n_centers: int, dim: int) -> np.ndarray:
     out = np.empty((n_centers, dim), dtype=np.float32)
     assert lib().tac_synth_centers(seed, n_centers, dim, _p(out)) == 0
+    out.setflags(write=False)
     return out
+
+
+def centers(seed: int, n_centers: int, dim: int) -> np.ndarray:
+    """Unit-sphere centres (cached: chunked generation reuses them)."""
+    return _centers(seed, n_centers, dim).copy()
 
 
 def residuals(w: Workload, n: int | None = None, first: int = 0, threads: int | None = None,
               with_ids: bool = False):
     """Residual rows first .. first+n-1 of workload w (default: all of it)."""
     n = w.n if n is None else n
-    c = centers(w.seed, w.n_centers, w.dim)
+    c = _centers(w.seed, w.n_centers, w.dim)
     out = np.empty((n, w.dim), dtype=np.float32)
     ids = np.empty(n, dtype=np.uint32) if with_ids else None
     t = threads or min(16, os.cpu_count() or 1)

@@ -1,0 +1,149 @@
+"""Every benchmark configuration at its full size on the GPU.
+
+Sizes the oracle finishes in seconds are compared bit for bit.  The
+60M-vector training sample and the 200M-vector encode stream are checked
+through properties that hold at any size: codes equal the oracle's on a
+sample, each centroid equals the serial fp32 mean of the points the previous
+codebook assigned to it, WCSS does not increase, and the stream's codes
+cover every vector.
+"""
+import time
+
+import numpy as np
+import pytest
+
+from oracle import binding as orc
+from tac_gpu import device, pq, synth
+
+NEVER = float("-inf")
+pytestmark = pytest.mark.gpu
+
+
+def _bits(a):
+    return np.ascontiguousarray(a, dtype=np.float32).reshape(-1).view(np.uint32)
+
+
+def _log(msg):
+    print(f"[configs] {msg}", flush=True)
+
+
+def _serial_mean(points):
+    """Centroid rule of src/tac/kmeans.zig:191-199: fp32 sums folded in
+    ascending row order from 0.0, times fl(1 / fl(count)).  np.cumsum
+    accumulates sequentially (np.sum would sum pairwise).  The reference
+    checks the same invariant at small size (kmeans.zig:545-626)."""
+    s = np.cumsum(points, axis=0, dtype=np.float32)[-1]
+    return s * (np.float32(1.0) / np.float32(len(points)))
+
+
+@pytest.fixture(scope="module")
+def corpus():
+    return synth.residuals(synth.WORKLOADS["corpus-1.52m"])
+
+
+@pytest.mark.parametrize("name", ["corpus-1.52m-m32d2", "corpus-1.52m-m8d8",
+                                  "corpus-1.52m-k1024"])
+def test_subspace_shape_sweep_full_corpus(gpu, corpus, name):
+    """(m=32, dsub=2), (m=8, dsub=8) and (m=16, ksub=1024) on all 1,521,797
+    residuals: codebooks bit-exact after 2 Lloyd iterations, codes bit-exact
+    on 50,000 vectors."""
+    w = synth.WORKLOADS[name]
+    x = corpus
+    init = synth.shuffle_init(x, w.m, w.ksub, w.seed)
+    _log(f"{name}: n={w.n} m={w.m} ksub={w.ksub}")
+    t0 = time.perf_counter()
+    got = pq.train(x, w.dim, 0, m=w.m, ksub=w.ksub, max_iters=2, tol=NEVER, init_codebooks=init)
+    t1 = time.perf_counter()
+    ref = orc.pq_train(x, w.dim, w.m, w.ksub, init=init, max_iters=2, tol=NEVER, n_threads=16)
+    _log(f"{name}: GPU {t1 - t0:.2f} s, oracle {time.perf_counter() - t1:.1f} s")
+    assert ref.status == 0
+    assert np.array_equal(_bits(got.codebooks), _bits(ref.codebooks))
+    sample = x[::30][:50000]
+    assert np.array_equal(got.encode_many(sample),
+                          orc.pq_encode(sample, w.dim, w.m, w.ksub, ref.codebooks, n_threads=16))
+
+
+@pytest.mark.timeout(300)
+def test_paper_scale_60m_resident(gpu):
+    """60,000,000 x 64 residuals resident in HBM, m16 k256, 25 iterations."""
+    w = synth.WORKLOADS["paper-60m"]
+    t0 = time.perf_counter()
+    x = synth.residuals(w)
+    init = synth.shuffle_init(x, w.m, w.ksub, w.seed)
+    _log(f"paper-60m: generated {w.n:,} x {w.dim} in {time.perf_counter() - t0:.1f} s")
+    dx = device.DeviceArray.from_host(x)
+    dinit = device.DeviceArray.from_host(init)
+    dcb = device.DeviceArray(init.shape, np.float32)
+    dcodes = device.DeviceArray((w.n, w.m), np.uint8)
+
+    def train(iters):
+        t = time.perf_counter()
+        it, wc, _ = device.train_device(dx, w.n, w.dim, w.m, w.ksub, dinit, dcb, iters, NEVER,
+                                        stats=True)
+        device.synchronize()
+        _log(f"paper-60m: {iters} iterations in {time.perf_counter() - t:.2f} s")
+        assert np.all(it == iters)
+        return wc.astype(np.float64), dcb.to_host()
+
+    wcss1, _ = train(1)
+    wcss5, _ = train(5)
+    _, cb24 = train(w.iters - 1)
+    device.encode_device(dx, w.n, w.dim, w.m, w.ksub, dcb, dcodes)
+    codes24 = dcodes.to_host()
+    wcss25, cb25 = train(w.iters)
+
+    # WCSS of Lloyd iterations does not increase (src/tac/kmeans.zig:503-521)
+    assert np.all(wcss5 <= wcss1) and np.all(wcss25 <= wcss5)
+
+    # encode with cb24 = the final iteration's assignment; oracle on a sample
+    sample = slice(17, None, 6007)
+    assert np.array_equal(codes24[sample], orc.pq_encode(x[sample], w.dim, w.m, w.ksub, cb24,
+                                                         n_threads=16))
+
+    # every non-empty cluster of the last update is the serial mean of its points
+    D = w.dsub
+    checked = 0
+    for m in (0, 9, 15):
+        cm = codes24[:, m]
+        counts = np.bincount(cm, minlength=w.ksub)
+        for c in (int(np.argmax(counts)), int(np.argmin(np.where(counts, counts, 1 << 40))), 77):
+            if counts[c] == 0:
+                continue
+            pts = x[cm == c, m * D:(m + 1) * D]
+            assert np.array_equal(_bits(cb25[m, c]), _bits(_serial_mean(pts))), (m, c)
+            checked += 1
+    assert checked >= 6
+
+    # training the same state further is deterministic
+    _, again = train(w.iters)
+    assert np.array_equal(_bits(again), _bits(cb25))
+
+
+@pytest.mark.timeout(300)
+def test_stream_encode_200m(gpu):
+    """200,000,000 residuals encoded in 10M-vector chunks against fixed
+    N(0, 0.05^2) codebooks: every chunk spot-checked bit for bit against the
+    oracle, and the codes of the whole stream account for every vector."""
+    w = synth.WORKLOADS["stream-200m"]
+    chunk = 10_000_000
+    cb = synth.gauss_codebooks(w.seed, w.m, w.ksub, w.dsub, 0.05)
+    dcb = device.DeviceArray.from_host(cb)
+    dx = device.DeviceArray((chunk, w.dim), np.float32)
+    dcodes = device.DeviceArray((chunk, w.m), np.uint8)
+    hist = np.zeros((w.m, w.ksub), np.int64)
+    t_enc = 0.0
+    for first in range(0, w.n, chunk):
+        x = synth.residuals(w, chunk, first=first)
+        dx.copy_from_host(x)
+        t0 = time.perf_counter()
+        device.encode_device(dx, chunk, w.dim, w.m, w.ksub, dcb, dcodes)
+        device.synchronize()
+        t_enc += time.perf_counter() - t0
+        codes = dcodes.to_host()
+        for m in range(w.m):
+            hist[m] += np.bincount(codes[:, m], minlength=w.ksub)
+        s = slice(first % 997, None, 20011)
+        assert np.array_equal(codes[s], orc.pq_encode(x[s], w.dim, w.m, w.ksub, cb,
+                                                      n_threads=16)), first
+    _log(f"stream-200m: {w.n:,} vectors, encode {t_enc:.2f} s ({w.n / t_enc / 1e6:.0f} Mvec/s)")
+    assert np.all(hist.sum(axis=1) == w.n)
