@@ -76,6 +76,36 @@ def cpu_baseline(x: np.ndarray, init: np.ndarray, w, gpu_cb3: np.ndarray | None)
     }
 
 
+def residual_stage(device, x, ids, w, reps: int):
+    """storage.build stage 2 on the corpus tokens (rebuilt as centre +
+    residual): average kernel time per call over `reps` timed calls."""
+    from tac_gpu import synth
+
+    cents = synth.centers(w.seed, w.n_centers, w.dim)
+    v = (x + cents[ids]).astype(np.float32)
+    dv = device.DeviceArray.from_host(v)
+    dc = device.DeviceArray.from_host(cents)
+    da = device.DeviceArray.from_host(ids)
+    dr = device.DeviceArray(v.shape, np.float32)
+    dn = device.DeviceArray((w.n,), np.float32)
+    device.residuals_device(dv, w.n, w.dim, dc, w.n_centers, da, dr, dn)  # warm
+    device.profile_enable(True)
+    device.profile_read(reset=True)
+    for _ in range(reps):
+        device.residuals_device(dv, w.n, w.dim, dc, w.n_centers, da, dr, dn)
+    p = device.profile_read(reset=True)
+    ms = p.residual_ms / max(p.residual_launches, 1)
+    for a in (dv, dc, da, dr, dn):
+        a.free()
+    nbytes = w.n * (8 * w.dim + 8) + w.n_centers * w.dim * 4
+    return {
+        "kernel": "residual_kernel (r = v - c[a], in-order norm, scale by 1/norm)",
+        "avg_call_ms": round(ms, 4), "algorithmic_bytes": nbytes,
+        "hbm_gbs": round(nbytes / (ms * 1e-3) / 1e9, 1),
+        "hbm_frac": round(nbytes / (ms * 1e-3) / 1e9 / PEAK_HBM_GBS, 4),
+    }
+
+
 def main() -> int:
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -98,7 +128,7 @@ def main() -> int:
     info["name"] = info["name"] or info["arch"]
     w = synth.WORKLOADS[WORKLOAD]
     t0 = time.perf_counter()
-    x = synth.residuals(w)
+    x, ids = synth.residuals(w, with_ids=True)
     init = synth.shuffle_init(x, w.m, w.ksub, w.seed)
     log(f"generated {w.n:,} x {w.dim} residuals in {time.perf_counter() - t0:.1f} s on {info['name']}")
 
@@ -111,6 +141,7 @@ def main() -> int:
     if args.traffic_pass:
         device.train_device(dx, n, dim, m, ksub, dinit, dcb, 2, NEVER)
         device.encode_device(dx, n, dim, m, ksub, dcb, dcodes)
+        residual_stage(device, x, ids, w, 1)
         a = device.DeviceArray((1 << 28,), np.float32)
         b = device.DeviceArray((1 << 28,), np.float32)
         errors.check(lib.tac_gpu_memcpy_dtod(b.ptr, a.ptr, a.nbytes))
@@ -149,6 +180,9 @@ def main() -> int:
     total = time.perf_counter() - t_all
     prof = device.profile_read(reset=True)
     device.profile_enable(False)
+    residual = residual_stage(device, x, ids, w, 5)
+    device.profile_enable(False)
+    log(f"residual stage: {residual['avg_call_ms']} ms per call")
 
     # Roofline of the dominant kernel (Lloyd assignment, VALU fp32): algorithmic
     # FLOP per launch = n * 2 * dim * ksub (one launch = one iteration, all m).
@@ -229,6 +263,7 @@ def main() -> int:
                                                           "reseed_kernel", "converge_kernel"))
                         or None),
         },
+        "residual_stage": residual,
         "cpu_baseline": None if cpu is None else {
             "value": round(cpu["train_s_per_20_iters"], 3), "unit": "s/20 iters",
             "encode_mvec_per_s": round(cpu["encode_mvec_per_s"], 3), "cores": cpu["cores"],

@@ -8,6 +8,9 @@
  *                                              -> tac_pq_encode / tac_pq_encode_device
  *   PQ.decode       src/index/pq.zig:79-88     -> tac_pq_decode
  *   kmeans.fit      src/tac/kmeans.zig:67-232  -> tac_kmeans_fit
+ *   storage.build stage 2, residualsAndNormsChunk
+ *                   src/index/storage.zig:255-278, :355-376
+ *                                              -> tac_residuals / tac_residuals_device
  *   PqError / KMeansError / RngError (src/index/pq.zig:32-38,
  *   src/tac/kmeans.zig:56-60, src/util/rng.zig:14-18) -> tac_status
  *
@@ -149,6 +152,30 @@ int tac_kmeans_fit(const float *vectors, uint64_t n, uint32_t dim, uint32_t k,
                    uint32_t *assignments_out, float *wcss_out,
                    uint32_t *iters_run_out);
 
+/* ---- storage.build stage 2: residuals and norms -------------------------- */
+/*
+ * residualsAndNormsChunk (src/index/storage.zig:255-278), run over every
+ * token as storage.build does at :355-376.  For token i with centroid
+ * a = assignments[i]:
+ *   diff_d = vectors[i][d] - centroids[a][d];
+ *   norms_out[i] = sqrt(((0 + diff_0^2) + diff_1^2) + ...), each operation
+ *                  rounded separately, in ascending d;
+ *   residuals_out[i][d] = diff_d * fl(1 / norm) if norm > 0, else diff_d.
+ * residuals_out may alias vectors.  An assignment >= n_centroids (a bounds
+ * trap in the reference) is TAC_ERR_INVALID_ARGUMENT and leaves the outputs
+ * unspecified.  dim <= 4096.
+ */
+int tac_residuals(const float *vectors, uint64_t n, uint32_t dim,
+                  const float *centroids, uint32_t n_centroids,
+                  const uint32_t *assignments, float *residuals_out,
+                  float *norms_out);
+/* Same on device buffers; ordered on `stream` (NULL: the library's stream).
+ * Returns after the kernel has finished (it reads back the range check). */
+int tac_residuals_device(const float *d_vectors, uint64_t n, uint32_t dim,
+                         const float *d_centroids, uint32_t n_centroids,
+                         const uint32_t *d_assignments, float *d_residuals_out,
+                         float *d_norms_out, void *stream);
+
 /* ---- measurement -------------------------------------------------------- */
 /* When enabled, the library brackets its kernels with HIP events on the
  * stream they run on and accumulates their durations. */
@@ -159,6 +186,7 @@ typedef struct tac_gpu_profile {
   double encode_ms;      uint64_t encode_launches;   /* encode kernel */
   uint64_t exact_rescans; /* (vector, subspace) searches the pruned pass left to a full
                              reference scan (near ties across codeword blocks) */
+  double residual_ms;    uint64_t residual_launches; /* residual + norm kernel */
 } tac_gpu_profile;
 int tac_gpu_profile_enable(int enable);
 int tac_gpu_profile_read(tac_gpu_profile *out, int reset);

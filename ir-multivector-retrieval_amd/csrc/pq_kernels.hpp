@@ -833,18 +833,23 @@ __global__ __launch_bounds__(kBlock) void encode_kernel(
 }
 
 // PQ.decode (src/index/pq.zig:79-88): out[i][m*D + k] = cb[m][code[i][m]][k].
+// A code >= K raises `status` and yields NaN instead of a read.
 template <typename CodeT>
 __global__ void decode_kernel(const CodeT* __restrict__ codes, const float* __restrict__ cb,
-                              float* __restrict__ out, uint64_t n, uint32_t M, uint32_t K,
-                              uint32_t D) {
+                              float* __restrict__ out, uint32_t* __restrict__ status,
+                              uint64_t n, uint32_t M, uint32_t K, uint32_t D) {
   const uint64_t g = (uint64_t)blockIdx.x * blockDim.x + threadIdx.x;
   const uint64_t dim = (uint64_t)M * D;
   if (g >= n * dim) return;
   const uint64_t i = g / dim;
   const uint32_t r = g % dim;
   const uint32_t m = r / D, k = r % D;
-  uint32_t code = codes[i * M + m];
-  if (code >= K) code = K - 1;
+  const uint32_t code = codes[i * M + m];
+  if (code >= K) {
+    atomicOr(status, 1u);
+    out[g] = __builtin_nanf("");
+    return;
+  }
   out[g] = cb[((uint64_t)m * K + code) * D + k];
 }
 

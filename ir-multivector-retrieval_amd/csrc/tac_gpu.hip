@@ -5,6 +5,7 @@
 //   PQ.encode    src/index/pq.zig:59-76 (batched as src/index/storage.zig:384-401)
 //   PQ.decode    src/index/pq.zig:79-88
 //   kmeans.fit   src/tac/kmeans.zig:67-365
+//   residuals    src/index/storage.zig:255-278,355-376 (storage.build stage 2)
 //
 // One training call keeps the residuals resident in HBM as a subspace-major
 // copy and runs every Lloyd iteration of all subspaces as a fixed sequence of
@@ -16,6 +17,7 @@
 #include "../../include/tac_gpu.h"
 #include "pq_kernels.hpp"
 #include "kmeanspp.hpp"
+#include "storage_kernels.hpp"
 
 #include <hip/hip_runtime.h>
 
@@ -77,7 +79,7 @@ struct DeviceState {
   hipEvent_t last_done = nullptr;
   // training / encode workspace
   Buffer xs, codes, e, hist, counts, start, sorted, flags, scal, trace, io_in, io_out, io_cb,
-      io_init, counter, kpp_state, kpp_w, kpp_bsum, kpp_bad;
+      io_init, counter, kpp_state, kpp_w, kpp_bsum, kpp_bad, status, io_aux, io_out2;
   // measurement
   std::vector<hipEvent_t> events;
 };
@@ -181,6 +183,27 @@ int counter_collect(DeviceState &ds, hipStream_t s) {
   HIP_TRY(hipStreamSynchronize(s));
   std::lock_guard<std::mutex> g(g_profile_mu);
   g_prof.exact_rescans += v;
+  return TAC_OK;
+}
+
+// Device word that kernels raise on invalid input (a centroid id or code out
+// of range); cleared before the launch, read back after it.
+int status_begin(DeviceState &ds, hipStream_t s, uint32_t **out) {
+  int st = ensure(ds, ds.status, sizeof(uint32_t));
+  if (st) return st;
+  HIP_TRY(hipMemsetAsync(ds.status.ptr, 0, sizeof(uint32_t), s));
+  *out = reinterpret_cast<uint32_t *>(ds.status.ptr);
+  return TAC_OK;
+}
+
+int status_collect(DeviceState &ds, hipStream_t s) {
+  uint32_t v = 0;
+  HIP_TRY(hipMemcpyAsync(&v, ds.status.ptr, sizeof(v), hipMemcpyDeviceToHost, s));
+  HIP_TRY(hipStreamSynchronize(s));
+  if (v) {
+    g_last_error = "input holds a centroid id or code out of range";
+    return TAC_ERR_INVALID_ARGUMENT;
+  }
   return TAC_OK;
 }
 
@@ -830,15 +853,18 @@ int tac_pq_decode(const void *codes, uint64_t n, uint32_t dim, uint32_t m, uint3
     return st;
   HIP_TRY(hipMemcpyAsync(ds->io_in.ptr, codes, code_bytes, hipMemcpyHostToDevice, s));
   HIP_TRY(hipMemcpyAsync(ds->io_cb.ptr, codebooks, cb_bytes, hipMemcpyHostToDevice, s));
+  uint32_t *status = nullptr;
+  if ((st = status_begin(*ds, s, &status))) return st;
   const uint64_t total = n * dim;
   const unsigned blocks = (unsigned)((total + 255) / 256);
   if (ksub <= 256)
     decode_kernel<uint8_t><<<blocks, 256, 0, s>>>(as<uint8_t>(ds->io_in), as<float>(ds->io_cb),
-                                                  as<float>(ds->io_out), n, m, ksub, D);
+                                                  as<float>(ds->io_out), status, n, m, ksub, D);
   else
     decode_kernel<uint16_t><<<blocks, 256, 0, s>>>(as<uint16_t>(ds->io_in), as<float>(ds->io_cb),
-                                                   as<float>(ds->io_out), n, m, ksub, D);
+                                                   as<float>(ds->io_out), status, n, m, ksub, D);
   LAUNCH_TRY("decode_kernel");
+  if ((st = status_collect(*ds, s))) return st;
   HIP_TRY(hipMemcpyAsync(out, ds->io_out.ptr, out_bytes, hipMemcpyDeviceToHost, s));
   HIP_TRY(hipStreamSynchronize(s));
   return end_call(*ds, s);
@@ -881,6 +907,117 @@ int tac_kmeans_fit(const float *vectors, uint64_t n, uint32_t dim, uint32_t k,
   HIP_TRY(hipStreamSynchronize(s));
   if (wcss_out) *wcss_out = wcss;
   if (iters_run_out) *iters_run_out = iters;
+  return end_call(*ds, s);
+}
+
+}  // extern "C"
+
+// ---- storage.build stage 2: residuals and norms ----------------------------
+
+namespace {
+
+int validate_residuals(uint64_t n, uint32_t dim) {
+  if (dim == 0) return TAC_ERR_DIM_MISMATCH;
+  if (dim > 4096) return TAC_ERR_UNSUPPORTED;
+  (void)n;
+  return TAC_OK;
+}
+
+int residuals_core(DeviceState &ds, hipStream_t s, const float *v, uint64_t n, uint32_t dim,
+                   const float *cent, uint32_t n_cent, const uint32_t *assign, float *out,
+                   float *norms) {
+  uint32_t *status = nullptr;
+  int st = status_begin(ds, s, &status);
+  if (st) return st;
+  const uint32_t R = residual_rows(dim);
+  const uint64_t blocks = (n + R - 1) / R;
+  if (blocks > 0x7FFFFFFFull) return TAC_ERR_UNSUPPORTED;
+  const size_t lds = ((size_t)R * (dim + 1) + 2 * R) * sizeof(float);
+  const bool vec4 = dim % 4 == 0 && ((uintptr_t)v % 16 == 0) && ((uintptr_t)cent % 16 == 0) &&
+                    ((uintptr_t)out % 16 == 0);
+  const bool profile = g_profile;
+  hipEvent_t a = nullptr, b = nullptr;
+  if (profile) {
+    if ((st = event_at(ds, 0, &a)) || (st = event_at(ds, 1, &b))) return st;
+    HIP_TRY(hipEventRecord(a, s));
+  }
+  if (vec4)
+    residual_kernel<4><<<(unsigned)blocks, kResBlock, lds, s>>>(v, cent, assign, out, norms,
+                                                                status, n, dim, n_cent, R);
+  else
+    residual_kernel<1><<<(unsigned)blocks, kResBlock, lds, s>>>(v, cent, assign, out, norms,
+                                                                status, n, dim, n_cent, R);
+  LAUNCH_TRY("residual_kernel");
+  if (profile) HIP_TRY(hipEventRecord(b, s));
+  if ((st = status_collect(ds, s))) return st;
+  if (profile) {
+    float ms = 0.0f;
+    HIP_TRY(hipEventElapsedTime(&ms, a, b));
+    std::lock_guard<std::mutex> g(g_profile_mu);
+    g_prof.residual_ms += ms;
+    g_prof.residual_launches += 1;
+  }
+  return TAC_OK;
+}
+
+}  // namespace
+
+extern "C" {
+
+int tac_residuals_device(const float *d_vectors, uint64_t n, uint32_t dim,
+                         const float *d_centroids, uint32_t n_centroids,
+                         const uint32_t *d_assignments, float *d_residuals_out,
+                         float *d_norms_out, void *stream) {
+  int st = validate_residuals(n, dim);
+  if (st) return st;
+  if (n == 0) return TAC_OK;
+  if (!d_vectors || !d_centroids || !d_assignments || !d_residuals_out || !d_norms_out)
+    return TAC_ERR_INVALID_ARGUMENT;
+  DeviceState *ds = nullptr;
+  if ((st = acquire_device(&ds, nullptr))) return st;
+  std::lock_guard<std::mutex> g(ds->mu);
+  hipStream_t s;
+  if ((st = resolve_stream(*ds, stream, &s))) return st;
+  if ((st = begin_call(*ds, s))) return st;
+  if ((st = residuals_core(*ds, s, d_vectors, n, dim, d_centroids, n_centroids, d_assignments,
+                           d_residuals_out, d_norms_out)))
+    return st;
+  return end_call(*ds, s);
+}
+
+int tac_residuals(const float *vectors, uint64_t n, uint32_t dim, const float *centroids,
+                  uint32_t n_centroids, const uint32_t *assignments, float *residuals_out,
+                  float *norms_out) {
+  int st = validate_residuals(n, dim);
+  if (st) return st;
+  if (n == 0) return TAC_OK;
+  if (!vectors || !centroids || !assignments || !residuals_out || !norms_out)
+    return TAC_ERR_INVALID_ARGUMENT;
+  DeviceState *ds = nullptr;
+  if ((st = acquire_device(&ds, nullptr))) return st;
+  std::lock_guard<std::mutex> g(ds->mu);
+  hipStream_t s;
+  if ((st = resolve_stream(*ds, nullptr, &s))) return st;
+  if ((st = begin_call(*ds, s))) return st;
+  const size_t x_bytes = (size_t)n * dim * sizeof(float);
+  const size_t c_bytes = (size_t)n_centroids * dim * sizeof(float);
+  const size_t a_bytes = (size_t)n * sizeof(uint32_t);
+  if ((st = ensure(*ds, ds->io_in, x_bytes)) || (st = ensure(*ds, ds->io_cb, c_bytes)) ||
+      (st = ensure(*ds, ds->io_aux, a_bytes)) || (st = ensure(*ds, ds->io_out, x_bytes)) ||
+      (st = ensure(*ds, ds->io_out2, (size_t)n * sizeof(float))))
+    return st;
+  HIP_TRY(hipMemcpyAsync(ds->io_in.ptr, vectors, x_bytes, hipMemcpyHostToDevice, s));
+  if (c_bytes)
+    HIP_TRY(hipMemcpyAsync(ds->io_cb.ptr, centroids, c_bytes, hipMemcpyHostToDevice, s));
+  HIP_TRY(hipMemcpyAsync(ds->io_aux.ptr, assignments, a_bytes, hipMemcpyHostToDevice, s));
+  if ((st = residuals_core(*ds, s, as<float>(ds->io_in), n, dim, as<float>(ds->io_cb),
+                           n_centroids, as<uint32_t>(ds->io_aux), as<float>(ds->io_out),
+                           as<float>(ds->io_out2))))
+    return st;
+  HIP_TRY(hipMemcpyAsync(residuals_out, ds->io_out.ptr, x_bytes, hipMemcpyDeviceToHost, s));
+  HIP_TRY(hipMemcpyAsync(norms_out, ds->io_out2.ptr, (size_t)n * sizeof(float),
+                         hipMemcpyDeviceToHost, s));
+  HIP_TRY(hipStreamSynchronize(s));
   return end_call(*ds, s);
 }
 

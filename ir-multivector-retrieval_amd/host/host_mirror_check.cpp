@@ -59,6 +59,9 @@ int errors_mode() {
     p.k = 1;
     tac::kmeans::fit(std::vector<float>{1, 2, 3}, 2, p);
   });
+  bad += expect_error("residuals ragged input", TAC_ERR_DIM_MISMATCH, [] {
+    tac::index::storage::residualsAndNorms(std::vector<float>(7, 0.0f), 2, {0.0f, 0.0f}, {0, 0});
+  });
   int count = 0;
   if (tac_gpu_device_count(&count) == TAC_ERR_NO_DEVICE) {
     bad += expect_error("valid train without a device", TAC_ERR_NO_DEVICE, [] {
@@ -94,7 +97,13 @@ int gpu_mode() {
   const bool same = codes_a == codes_b;
   std::printf("%s encode(decode(encode(x))) == encode(x) over %u subspaces\n", same ? "ok  " : "FAIL",
               pq.m);
-  return same ? 0 : 1;
+  // residual stage: centroids 0 and 1 of a 2-row table, (3, 4) -> norm 5
+  const auto res = tac::index::storage::residualsAndNorms({4, 6, 1, 1}, 2, {1, 2, 1, 1}, {0, 1});
+  const bool res_ok = res.norms[0] == 5.0f && res.norms[1] == 0.0f &&
+                      res.residuals[0] == 0.6f && res.residuals[1] == 0.8f &&
+                      res.residuals[2] == 0.0f && res.residuals[3] == 0.0f;
+  std::printf("%s residualsAndNorms (3,4) -> norm 5, zero row unscaled\n", res_ok ? "ok  " : "FAIL");
+  return (same && res_ok) ? 0 : 1;
 }
 
 }  // namespace

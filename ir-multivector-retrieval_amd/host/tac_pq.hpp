@@ -7,6 +7,9 @@
 //     .encode_many          <- the storage.build encode loop
 //                              src/index/storage.zig:280-295, :384-401
 //   tac::kmeans::fit        <- kmeans.fit     src/tac/kmeans.zig:67-232
+//   tac::index::storage::residualsAndNorms
+//                           <- residualsAndNormsChunk over every token
+//                              src/index/storage.zig:255-278, :355-376
 //
 // Zig error unions become exceptions of type tac::Error carrying the C-ABI
 // status; error names follow PqError / KMeansError / RngError.
@@ -117,6 +120,34 @@ inline PQ train(const std::vector<float>& residuals, uint32_t dim, uint64_t seed
 }
 
 }  // namespace pq
+
+namespace storage {
+
+struct Residuals {
+  std::vector<float> residuals;  // [n][dim], unit norm where norm > 0
+  std::vector<float> norms;      // [n]
+};
+
+// storage.build stage 2: residual = (vector - centroids[assignment]) scaled
+// by fl(1 / norm) when norm > 0.  An assignment outside the centroid table
+// throws InvalidArgument.
+inline Residuals residualsAndNorms(const std::vector<float>& vectors, uint32_t dim,
+                                   const std::vector<float>& centroids,
+                                   const std::vector<uint32_t>& assignments) {
+  if (dim == 0 || vectors.size() % dim != 0 || centroids.size() % dim != 0 ||
+      vectors.size() / dim != assignments.size())
+    throw Error(TAC_ERR_DIM_MISMATCH);
+  Residuals out;
+  out.residuals.resize(vectors.size());
+  out.norms.resize(assignments.size());
+  if (assignments.empty()) return out;
+  check(tac_residuals(vectors.data(), assignments.size(), dim, centroids.data(),
+                      static_cast<uint32_t>(centroids.size() / dim), assignments.data(),
+                      out.residuals.data(), out.norms.data()));
+  return out;
+}
+
+}  // namespace storage
 }  // namespace index
 
 namespace kmeans {

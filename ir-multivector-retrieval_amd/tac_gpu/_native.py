@@ -53,6 +53,8 @@ class Profile(ctypes.Structure):
         ("encode_ms", ctypes.c_double),
         ("encode_launches", c_u64),
         ("exact_rescans", c_u64),
+        ("residual_ms", ctypes.c_double),
+        ("residual_launches", c_u64),
     ]
 
 
@@ -90,6 +92,10 @@ SIGNATURES = {
         [c_void_p, c_u64, c_u32, c_u32, c_u32, ctypes.c_float, c_u64, c_void_p, c_void_p,
          c_void_p, c_f32_p, c_u32_p],
     ),
+    "tac_residuals": (
+        c_int, [c_void_p, c_u64, c_u32, c_void_p, c_u32, c_void_p, c_void_p, c_void_p]),
+    "tac_residuals_device": (
+        c_int, [c_void_p, c_u64, c_u32, c_void_p, c_u32, c_void_p, c_void_p, c_void_p, c_void_p]),
     "tac_gpu_profile_enable": (c_int, [c_int]),
     "tac_gpu_profile_read": (c_int, [ctypes.POINTER(Profile), c_int]),
 }

@@ -104,6 +104,13 @@ def encode_device(x: DeviceArray, n: int, dim: int, m: int, ksub: int, cb: Devic
     errors.check(lib.tac_pq_encode_device(x.ptr, n, dim, m, ksub, cb.ptr, codes.ptr, None))
 
 
+def residuals_device(v: DeviceArray, n: int, dim: int, cent: DeviceArray, n_cent: int,
+                     assign: DeviceArray, out: DeviceArray, norms: DeviceArray) -> None:
+    """tac_residuals_device on resident buffers (out may be v itself)."""
+    errors.check(lib.tac_residuals_device(v.ptr, n, dim, cent.ptr, n_cent, assign.ptr, out.ptr,
+                                          norms.ptr, None))
+
+
 @dataclass
 class KernelTimes:
     transpose_ms: float
@@ -115,6 +122,8 @@ class KernelTimes:
     encode_ms: float
     encode_launches: int
     exact_rescans: int
+    residual_ms: float = 0.0
+    residual_launches: int = 0
 
 
 def profile_enable(on: bool = True) -> None:
@@ -126,4 +135,4 @@ def profile_read(reset: bool = True) -> KernelTimes:
     errors.check(lib.tac_gpu_profile_read(ctypes.byref(p), 1 if reset else 0))
     return KernelTimes(p.transpose_ms, p.transpose_launches, p.assign_ms, p.assign_launches,
                        p.update_ms, p.update_iters, p.encode_ms, p.encode_launches,
-                       p.exact_rescans)
+                       p.exact_rescans, p.residual_ms, p.residual_launches)

@@ -69,6 +69,8 @@ def _load():
     L.orc_pq_decode.argtypes = [_vp, _u64, _u32, _u32, _u32, _vp, _vp]
     L.orc_pq_distance_table.restype = ctypes.c_int
     L.orc_pq_distance_table.argtypes = [_vp, _u32, _u32, _u32, _u32, _vp, _vp, _u64]
+    L.orc_residuals.restype = ctypes.c_int
+    L.orc_residuals.argtypes = [_vp, _u64, _u32, _vp, _u32, _vp, _vp, _vp]
     return L
 
 
@@ -229,3 +231,16 @@ def pq_distance_table(queries, n_q: int, dim: int, m: int, ksub: int, codebooks,
     out = np.zeros(max(tl, 1), np.float32)
     st = lib.orc_pq_distance_table(_p(q), n_q, dim, m, ksub, _p(cb), _p(out), tl)
     return st, out[:tl]
+
+
+def residuals(vectors, dim: int, centroids, assignments):
+    """(status, residuals [n][dim], norms [n]) of storage.zig:255-278."""
+    v = _f32(vectors).reshape(-1)
+    c = _f32(centroids).reshape(-1)
+    a = np.ascontiguousarray(assignments, dtype=np.uint32).reshape(-1)
+    n = a.size
+    r = np.zeros((n, dim), np.float32)
+    nr = np.zeros(n, np.float32)
+    st = lib.orc_residuals(_p(v), n, dim, _p(c), c.size // dim if dim else 0, _p(a), _p(r),
+                           _p(nr))
+    return st, r, nr

@@ -731,3 +731,36 @@ int orc_pq_distance_table(const float *queries, uint32_t n_q, uint32_t dim,
     }
   return ORC_OK;
 }
+
+/* src/index/storage.zig:255-278 (residualsAndNormsChunk).  Per token i with
+ * centroid a = assignments[i]: diff_d = v_d - c_d is stored, sum_sq folds
+ * diff_d * diff_d in ascending d from 0.0f, norm = sqrt(sum_sq) (correctly
+ * rounded), and only when norm > 0 every diff_d is multiplied by
+ * fl(1.0f / norm).  An assignment >= n_centroids (a bounds trap in the
+ * reference) is ORC_INVALID_ARGUMENT here. */
+int orc_residuals(const float *vectors, uint64_t n, uint32_t dim,
+                  const float *centroids, uint32_t n_centroids,
+                  const uint32_t *assignments, float *residuals, float *norms) {
+  if (dim == 0) return ORC_DIM_MISMATCH;
+  for (uint64_t i = 0; i < n; ++i)
+    if (assignments[i] >= n_centroids) return ORC_INVALID_ARGUMENT;
+  for (uint64_t i = 0; i < n; ++i) {
+    const float *v = vectors + i * dim;
+    const float *c = centroids + (uint64_t)assignments[i] * dim;
+    float *r = residuals + i * dim;
+    float sum_sq = 0.0f;
+    for (uint32_t d = 0; d < dim; ++d) {
+      const float diff = v[d] - c[d];
+      r[d] = diff;
+      const float sq = diff * diff;
+      sum_sq = sum_sq + sq;
+    }
+    const float norm = sqrtf(sum_sq);
+    norms[i] = norm;
+    if (norm > 0.0f) {
+      const float inv = 1.0f / norm;
+      for (uint32_t d = 0; d < dim; ++d) r[d] = r[d] * inv;
+    }
+  }
+  return ORC_OK;
+}

@@ -19,6 +19,7 @@
  *                           src/index/storage.zig:201-244,280-295
  *   orc_pq_decode           src/index/pq.zig:79-88
  *   orc_pq_distance_table   src/index/pq.zig:92-123
+ *   orc_residuals           src/index/storage.zig:255-278
  *
  * Status codes share their numbering with include/tac_gpu.h.
  */
@@ -113,6 +114,11 @@ int orc_pq_decode(const void *codes, uint64_t n, uint32_t dim, uint32_t m,
 int orc_pq_distance_table(const float *queries, uint32_t n_q, uint32_t dim,
                           uint32_t m, uint32_t ksub, const float *codebooks,
                           float *table, uint64_t table_len);
+
+/* Residuals and per-token norms (storage.build stage 2). */
+int orc_residuals(const float *vectors, uint64_t n, uint32_t dim,
+                  const float *centroids, uint32_t n_centroids,
+                  const uint32_t *assignments, float *residuals, float *norms);
 
 #ifdef __cplusplus
 }
