@@ -11,6 +11,15 @@
  *   storage.build stage 2, residualsAndNormsChunk
  *                   src/index/storage.zig:255-278, :355-376
  *                                              -> tac_residuals / tac_residuals_device
+ *   .tac doc layouts and footer checksum
+ *                   src/index/storage.zig:674-686, :705-749, :612-617
+ *                                              -> tac_doc_payload_bytes,
+ *                                                 tac_write_doc_layouts[_device],
+ *                                                 tac_crc32[_device]
+ *   PQ.buildDistanceTable src/index/pq.zig:92-123 -> tac_pq_distance_table[_device]
+ *   refine          src/retrieval/refine.zig:83-145 -> tac_refine / tac_refine_device
+ *   RefineError / StorageError (src/retrieval/refine.zig:37-42,
+ *   src/index/storage.zig:42-47) -> tac_status 16-20
  *   PqError / KMeansError / RngError (src/index/pq.zig:32-38,
  *   src/tac/kmeans.zig:56-60, src/util/rng.zig:14-18) -> tac_status
  *
@@ -57,7 +66,12 @@ typedef enum tac_status {
   TAC_ERR_NO_DEVICE = 12,              /* no usable HIP device */
   TAC_ERR_HIP = 13,                    /* HIP runtime error; see tac_gpu_last_error */
   TAC_ERR_INVALID_ARGUMENT = 14,       /* null pointer / shape outside the limits above */
-  TAC_ERR_UNSUPPORTED = 15             /* valid request this build does not implement */
+  TAC_ERR_UNSUPPORTED = 15,            /* valid request this build does not implement */
+  TAC_ERR_QUERY_SHAPE_MISMATCH = 16,   /* RefineError.QueryShapeMismatch */
+  TAC_ERR_TABLE_SIZE_MISMATCH = 17,    /* RefineError.TableSizeMismatch */
+  TAC_ERR_DOC_OUT_OF_RANGE = 18,       /* RefineError.DocOutOfRange */
+  TAC_ERR_DOC_LAYOUT_CORRUPT = 19,     /* RefineError.DocLayoutCorrupt */
+  TAC_ERR_BUFFER_TOO_SMALL = 20        /* StorageError.BufferTooSmall */
 } tac_status;
 
 /* Never-break iteration control: pass as `tol` to run exactly max_iters. */
@@ -176,6 +190,91 @@ int tac_residuals_device(const float *d_vectors, uint64_t n, uint32_t dim,
                          const uint32_t *d_assignments, float *d_residuals_out,
                          float *d_norms_out, void *stream);
 
+/* ---- .tac per-document layouts and image checksum ----------------------- */
+/*
+ * docPayloadSize (src/index/storage.zig:674-686) for m codes of code_bytes
+ * (1: ksub <= 256, 2: ksub <= 65536, little-endian) per token; a host-only
+ * computation over host doc_offsets [n_docs + 1].
+ */
+int tac_doc_payload_bytes(const uint64_t *doc_offsets, uint64_t n_docs, uint32_t m,
+                          uint32_t code_bytes, uint64_t *bytes_out);
+/*
+ * writeDocLayouts (src/index/storage.zig:705-749): doc_index_out [n_docs + 1]
+ * gets each document's payload offset (the last entry is the total) and
+ * payload_out the layouts: u32 n_d | u32 centroid id x n_d | n_d x m codes |
+ * zero padding to 8 bytes, all little-endian.  doc_offsets [n_docs + 1] must
+ * be non-decreasing with doc_offsets[n_docs] <= n_tokens (else
+ * TAC_ERR_INVALID_ARGUMENT); assignments [n_tokens]; codes [n_tokens][m].
+ * payload_len smaller than the layouts: TAC_ERR_BUFFER_TOO_SMALL.
+ */
+int tac_write_doc_layouts(const uint64_t *doc_offsets, uint64_t n_docs, uint64_t n_tokens,
+                          const uint32_t *assignments, const void *codes, uint32_t m,
+                          uint32_t code_bytes, uint64_t *doc_index_out, uint8_t *payload_out,
+                          uint64_t payload_len);
+/* Same on device buffers (payload_out 8-byte aligned); returns when done. */
+int tac_write_doc_layouts_device(const uint64_t *d_doc_offsets, uint64_t n_docs,
+                                 uint64_t n_tokens, const uint32_t *d_assignments,
+                                 const void *d_codes, uint32_t m, uint32_t code_bytes,
+                                 uint64_t *d_doc_index_out, uint8_t *d_payload_out,
+                                 uint64_t payload_len, void *stream);
+/*
+ * std.hash.Crc32 (CRC-32/ISO-HDLC) of len bytes, the footer checksum that
+ * serialise writes and parse verifies (src/index/storage.zig:612-617,
+ * :782-786).  tac_crc32 takes a host buffer, tac_crc32_device a device one;
+ * both store the checksum in *crc_out (host memory) and return when done.
+ */
+int tac_crc32(const void *bytes, uint64_t len, uint32_t *crc_out);
+int tac_crc32_device(const void *d_bytes, uint64_t len, uint32_t *crc_out, void *stream);
+
+/* ---- query side: distance table and refine ------------------------------ */
+/*
+ * PQ.buildDistanceTable (src/index/pq.zig:92-123): table_out [m][ksub][n_q],
+ * entry ((mm * ksub) + c) * n_q + i = dot(query_i[mm * dsub ..], codeword).
+ * n_q == 0: TAC_ERR_NQ_MISMATCH; table_len != m * ksub * n_q:
+ * TAC_ERR_OUT_BUFFER_WRONG_SIZE.
+ */
+int tac_pq_distance_table(const float *query_tokens, uint32_t n_q, uint32_t dim, uint32_t m,
+                          uint32_t ksub, const float *codebooks, float *table_out,
+                          uint64_t table_len);
+int tac_pq_distance_table_device(const float *d_query_tokens, uint32_t n_q, uint32_t dim,
+                                 uint32_t m, uint32_t ksub, const float *d_codebooks,
+                                 float *d_table_out, uint64_t table_len, void *stream);
+
+/* The parts of a parsed .tac Index (src/index/storage.zig:86-124) that refine
+ * reads.  Pointers are host or device memory to match the entry point. */
+typedef struct tac_doc_index {
+  uint32_t dim;                      /* token dim */
+  uint32_t kappa;                    /* centroids */
+  uint32_t m;                        /* PQ codes per token */
+  uint32_t ksub;                     /* codes are uint8 if <= 256, else uint16 LE */
+  uint64_t n_docs;
+  uint64_t n_tokens;
+  uint64_t payload_len;
+  const float *centroids;            /* [kappa][dim] */
+  const uint64_t *doc_index;         /* [n_docs + 1] payload offsets */
+  const uint8_t *doc_payload;        /* per-document layouts */
+  const uint64_t *doc_token_offsets; /* [n_docs + 1] */
+  const float *residual_norms;       /* [n_tokens] */
+} tac_doc_index;
+
+/*
+ * refine (src/retrieval/refine.zig:83-145) for n_candidates documents of one
+ * query: scores_out[j] = exact MaxSim of doc doc_ids[j],
+ *   sum_i max_k ( dot(q_i, centroid[c_k]) + norm_k * sum_m table[m][code_km][i] ).
+ * Errors, checked per candidate in order, return the first failing
+ * candidate's RefineError (n_q == 0: QueryShapeMismatch; table_len !=
+ * m * ksub * n_q: TableSizeMismatch; doc id >= n_docs: DocOutOfRange; a
+ * layout, token range, centroid id or code out of bounds: DocLayoutCorrupt).
+ * n_q * (dim + 1) + 4 * (dim + 64) floats must fit in 64 KB (else
+ * TAC_ERR_UNSUPPORTED).
+ */
+int tac_refine(const tac_doc_index *index, const float *table, uint64_t table_len,
+               const float *query_tokens, uint32_t n_q, const uint32_t *doc_ids,
+               uint32_t n_candidates, float *scores_out);
+int tac_refine_device(const tac_doc_index *d_index, const float *d_table, uint64_t table_len,
+                      const float *d_query_tokens, uint32_t n_q, const uint32_t *d_doc_ids,
+                      uint32_t n_candidates, float *d_scores_out, void *stream);
+
 /* ---- measurement -------------------------------------------------------- */
 /* When enabled, the library brackets its kernels with HIP events on the
  * stream they run on and accumulates their durations. */
@@ -187,6 +286,8 @@ typedef struct tac_gpu_profile {
   uint64_t exact_rescans; /* (vector, subspace) searches the pruned pass left to a full
                              reference scan (near ties across codeword blocks) */
   double residual_ms;    uint64_t residual_launches; /* residual + norm kernel */
+  double crc_ms;         uint64_t crc_launches;      /* CRC-32 kernels (+ 4-byte readback) */
+  double refine_ms;      uint64_t refine_launches;   /* refine kernel (+ status readback) */
 } tac_gpu_profile;
 int tac_gpu_profile_enable(int enable);
 int tac_gpu_profile_read(tac_gpu_profile *out, int reset);

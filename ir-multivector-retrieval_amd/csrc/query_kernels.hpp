@@ -1,0 +1,187 @@
+// query_kernels.hpp — gfx950 kernels of the query side that consumes PQ
+// codes: the per-query distance table (src/index/pq.zig:92-123) and refine's
+// exact MaxSim over candidate documents (src/retrieval/refine.zig:83-145).
+// Included once, by tac_gpu.hip.  Compiled with -ffp-contract=off: every
+// multiply and add is rounded separately, in the reference's order.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+namespace tacgpu {
+
+// vec.dot (src/util/vec.zig:37-103): dims 2 and 4 are left folds from 0,
+// dims 64 and 128 accumulate in 4 lanes chunk after chunk and reduce
+// ((a0 + a1) + a2) + a3, other dims accumulate in 16 lanes (the x86-64
+// AVX-512 lane count), reduce in lane order and fold the tail.
+// `a` and `b` may live in LDS or global memory.
+__device__ inline float ref_dot(const float* a, const float* b, uint32_t d) {
+  if (d == 2) return a[0] * b[0] + a[1] * b[1];
+  if (d == 4) {
+    float s = 0.0f;
+    for (int i = 0; i < 4; ++i) s = s + a[i] * b[i];
+    return s;
+  }
+  if (d == 64 || d == 128) {
+    float acc0 = 0.0f, acc1 = 0.0f, acc2 = 0.0f, acc3 = 0.0f;
+    for (uint32_t c = 0; c < d; c += 4) {
+      acc0 = acc0 + a[c] * b[c];
+      acc1 = acc1 + a[c + 1] * b[c + 1];
+      acc2 = acc2 + a[c + 2] * b[c + 2];
+      acc3 = acc3 + a[c + 3] * b[c + 3];
+    }
+    return ((acc0 + acc1) + acc2) + acc3;
+  }
+  float acc[16];
+#pragma unroll
+  for (int j = 0; j < 16; ++j) acc[j] = 0.0f;
+  uint32_t i = 0;
+  for (; i + 16 <= d; i += 16) {
+#pragma unroll
+    for (int j = 0; j < 16; ++j) acc[j] = acc[j] + a[i + j] * b[i + j];
+  }
+  float sum = acc[0];
+#pragma unroll
+  for (int j = 1; j < 16; ++j) sum = sum + acc[j];
+  for (; i < d; ++i) sum = sum + a[i] * b[i];
+  return sum;
+}
+
+// PQ.buildDistanceTable: table[((mm * K) + c) * n_q + i] =
+// dot(query_i[mm * D .. +D], codebook[mm][c]); one thread per entry, so
+// consecutive threads write consecutive i.
+__global__ __launch_bounds__(256) void distance_table_kernel(
+    const float* __restrict__ q, const float* __restrict__ cb, float* __restrict__ table,
+    uint32_t n_q, uint32_t dim, uint32_t M, uint32_t K, uint32_t D) {
+  const uint64_t g = (uint64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  const uint64_t total = (uint64_t)M * K * n_q;
+  if (g >= total) return;
+  const uint32_t i = (uint32_t)(g % n_q);
+  const uint64_t mc = g / n_q;
+  const uint32_t mm = (uint32_t)(mc / K);
+  table[g] = ref_dot(q + (uint64_t)i * dim + (uint64_t)mm * D, cb + mc * D, D);
+}
+
+// Refine status codes per candidate (tac_status values).
+constexpr uint32_t kRefineOk = 0;
+constexpr uint32_t kRefineDocOutOfRange = 18;
+constexpr uint32_t kRefineLayoutCorrupt = 19;
+
+struct RefineIndex {
+  const float* centroids;            // [kappa][dim]
+  const uint64_t* doc_index;         // [n_docs + 1]
+  const uint8_t* payload;            // per-doc layouts
+  const uint64_t* doc_token_offsets; // [n_docs + 1]
+  const float* norms;                // [n_tokens]
+  uint64_t n_docs, n_tokens, payload_len;
+  uint32_t dim, kappa, M, K;
+};
+
+__device__ __forceinline__ uint32_t load_u32_le(const uint8_t* p) {
+  return (uint32_t)p[0] | (uint32_t)p[1] << 8 | (uint32_t)p[2] << 16 | (uint32_t)p[3] << 24;
+}
+
+// One wave per candidate document (grid-stride over candidates).  Lane i
+// owns query token i (groups of 64 when n_q > 64): for every doc token k
+//   cent  = dot(q_i, centroid[c_k])            (centroid row staged in LDS)
+//   res   = sum over m of table[m][code_km][i]  (in m order, from 0)
+//   score = cent + norm_k * res;  best_i = max over k (strict >, from -inf)
+// and lane 0 folds best_0 + best_1 + ... in i order (0 for an empty doc).
+// Layout checks follow refine.zig:51-65,107-114; a failing candidate writes
+// its status and score 0, and `first_bad` keeps the lowest such index.
+constexpr int kRefineWaves = 4;
+
+__global__ __launch_bounds__(64 * kRefineWaves) void refine_kernel(
+    RefineIndex ix, const float* __restrict__ q, uint32_t n_q, const float* __restrict__ table,
+    const uint32_t* __restrict__ doc_ids, uint32_t n_cand, float* __restrict__ scores,
+    uint32_t* __restrict__ status, uint32_t* __restrict__ first_bad) {
+  extern __shared__ __attribute__((aligned(16))) float lds[];
+  const uint32_t w = threadIdx.x / 64, lane = threadIdx.x % 64;
+  const uint32_t ldq = ix.dim + 1;  // odd stride: lanes read distinct banks
+  float* qs = lds;                                          // [n_q][dim + 1]
+  float* crow = lds + (size_t)n_q * ldq + (size_t)w * (ix.dim + 64);  // [dim] per wave
+  float* best = crow + ix.dim;                              // [64] per wave
+  for (uint32_t f = threadIdx.x; f < n_q * ix.dim; f += blockDim.x)
+    qs[(f / ix.dim) * ldq + f % ix.dim] = q[f];
+  __syncthreads();
+  const uint32_t cb = ix.K <= 256 ? 1u : 2u;
+  const uint32_t stride = gridDim.x * kRefineWaves;
+  for (uint32_t cand = blockIdx.x * kRefineWaves + w; cand < n_cand; cand += stride) {
+    const uint64_t doc = doc_ids[cand];
+    uint32_t st = kRefineOk;
+    uint32_t n_d = 0;
+    uint64_t lo = 0, t_lo = 0;
+    if (doc >= ix.n_docs) {
+      st = kRefineDocOutOfRange;
+    } else {
+      lo = ix.doc_index[doc];
+      const uint64_t hi = ix.doc_index[doc + 1];
+      if (hi < lo || hi > ix.payload_len || hi - lo < 4) {
+        st = kRefineLayoutCorrupt;
+      } else {
+        n_d = load_u32_le(ix.payload + lo);
+        t_lo = ix.doc_token_offsets[doc];
+        const uint64_t t_hi = ix.doc_token_offsets[doc + 1];
+        if (hi - lo < 4 + 4ull * n_d + (uint64_t)n_d * ix.M * cb || t_hi - t_lo != n_d ||
+            t_hi > ix.n_tokens)
+          st = kRefineLayoutCorrupt;
+      }
+    }
+    float total = 0.0f;
+    for (uint32_t i0 = 0; st == kRefineOk && i0 < n_q; i0 += 64) {
+      const uint32_t i = i0 + lane;
+      float b = -__builtin_inff();
+      const uint8_t* lay = ix.payload + lo;
+      for (uint32_t k = 0; k < n_d; ++k) {
+        const uint32_t cid = load_u32_le(lay + 4 + 4ull * k);
+        if (cid >= ix.kappa) {
+          st = kRefineLayoutCorrupt;
+          break;
+        }
+        const float* cg = ix.centroids + (uint64_t)cid * ix.dim;
+        for (uint32_t d = lane; d < ix.dim; d += 64) crow[d] = cg[d];
+        __builtin_amdgcn_wave_barrier();
+        __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+        const uint8_t* codes = lay + 4 + 4ull * n_d + (uint64_t)k * ix.M * cb;
+        float res = 0.0f;
+        bool bad = false;
+        if (i < n_q) {
+          const float cent = ref_dot(qs + (size_t)i * ldq, crow, ix.dim);
+          for (uint32_t mm = 0; mm < ix.M; ++mm) {
+            const uint32_t code =
+                cb == 1 ? codes[mm] : (uint32_t)codes[2 * mm] | (uint32_t)codes[2 * mm + 1] << 8;
+            if (code >= ix.K) {
+              bad = true;
+              break;
+            }
+            res = res + table[((uint64_t)mm * ix.K + code) * n_q + i];
+          }
+          const float scaled = ix.norms[t_lo + k] * res;
+          const float score = cent + scaled;
+          if (score > b) b = score;
+        }
+        __builtin_amdgcn_wave_barrier();
+        if (__any(bad)) {
+          st = kRefineLayoutCorrupt;
+          break;
+        }
+      }
+      if (st != kRefineOk) break;
+      best[lane] = b;
+      __builtin_amdgcn_wave_barrier();
+      __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+      if (lane == 0 && n_d > 0) {
+        const uint32_t cnt = n_q - i0 < 64 ? n_q - i0 : 64;
+        for (uint32_t j = 0; j < cnt; ++j) total = total + best[j];
+      }
+      __builtin_amdgcn_wave_barrier();
+    }
+    if (lane == 0) {
+      scores[cand] = st == kRefineOk ? total : 0.0f;
+      status[cand] = st;
+      if (st != kRefineOk) atomicMin(first_bad, cand);
+    }
+  }
+}
+
+}  // namespace tacgpu

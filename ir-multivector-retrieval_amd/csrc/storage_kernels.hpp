@@ -133,3 +133,290 @@ __global__ __launch_bounds__(kResBlock) void residual_kernel(
 }
 
 }  // namespace tacgpu
+
+namespace tacgpu {
+
+// ---------------------------------------------------------------------------
+// .tac per-document layouts (src/index/storage.zig:674-686, :705-749).
+// Each doc d occupies align8(4 + 4 n_d + n_d m cb) payload bytes:
+//   u32 n_d | u32 centroid id x n_d | codes (n_d x m x cb bytes) | zeros.
+// doc_index[d] is the payload offset of doc d; doc_index[n_docs] the total.
+// ---------------------------------------------------------------------------
+__device__ __forceinline__ uint64_t doc_bytes(uint64_t n_d, uint32_t m, uint32_t cb) {
+  return (4 + 4 * n_d + n_d * m * cb + 7) & ~7ull;
+}
+
+constexpr int kScanBlock = 256;
+constexpr int kScanPer = 4;  // elements per thread in the u64 scan
+
+// Phase 1: per-block exclusive scan of doc sizes into doc_index, block totals
+// into `sums`.
+// Offsets that decrease or pass n_tokens raise `status` (the writer then
+// does not run) and count as empty documents.
+__global__ __launch_bounds__(kScanBlock) void doc_sizes_scan_kernel(
+    const uint64_t* __restrict__ doc_offsets, uint64_t n_docs, uint64_t n_tokens, uint32_t m,
+    uint32_t cb, uint64_t* __restrict__ doc_index, uint64_t* __restrict__ sums,
+    uint32_t* __restrict__ status) {
+  __shared__ uint64_t warp_tot[kScanBlock / 64];
+  const uint64_t base = (uint64_t)blockIdx.x * kScanBlock * kScanPer + threadIdx.x * kScanPer;
+  uint64_t v[kScanPer];
+  uint64_t local = 0;
+#pragma unroll
+  for (int q = 0; q < kScanPer; ++q) {
+    const uint64_t d = base + q;
+    v[q] = 0;
+    if (d < n_docs) {
+      const uint64_t a = doc_offsets[d], b = doc_offsets[d + 1];
+      if (b < a || b > n_tokens)
+        atomicOr(status, 1u);
+      else
+        v[q] = doc_bytes(b - a, m, cb);
+    }
+    local += v[q];
+  }
+  const uint32_t lane = threadIdx.x % 64, w = threadIdx.x / 64;
+  uint64_t incl = local;
+  for (int off = 1; off < 64; off <<= 1) {
+    const uint64_t o = __shfl_up(incl, off, 64);
+    if (lane >= (uint32_t)off) incl += o;
+  }
+  if (lane == 63) warp_tot[w] = incl;
+  __syncthreads();
+  uint64_t before = 0;
+  for (uint32_t q = 0; q < w; ++q) before += warp_tot[q];
+  uint64_t run = before + incl - local;
+#pragma unroll
+  for (int q = 0; q < kScanPer; ++q) {
+    const uint64_t d = base + q;
+    if (d < n_docs) doc_index[d] = run;
+    run += v[q];
+  }
+  if (threadIdx.x == kScanBlock - 1) sums[blockIdx.x] = before + incl;
+}
+
+// Phase 2 (one block): exclusive scan of the block totals in place; the
+// grand total lands in doc_index[n_docs].
+__global__ __launch_bounds__(kScanBlock) void doc_sums_scan_kernel(
+    uint64_t* __restrict__ sums, uint32_t nb, uint64_t* __restrict__ doc_index, uint64_t n_docs) {
+  __shared__ uint64_t warp_tot[kScanBlock / 64];
+  __shared__ uint64_t carry;
+  if (threadIdx.x == 0) carry = 0;
+  __syncthreads();
+  const uint32_t lane = threadIdx.x % 64, w = threadIdx.x / 64;
+  for (uint32_t b0 = 0; b0 < nb; b0 += kScanBlock) {
+    const uint32_t b = b0 + threadIdx.x;
+    const uint64_t x = b < nb ? sums[b] : 0;
+    uint64_t incl = x;
+    for (int off = 1; off < 64; off <<= 1) {
+      const uint64_t o = __shfl_up(incl, off, 64);
+      if (lane >= (uint32_t)off) incl += o;
+    }
+    if (lane == 63) warp_tot[w] = incl;
+    __syncthreads();
+    uint64_t before = carry;
+    for (uint32_t q = 0; q < w; ++q) before += warp_tot[q];
+    if (b < nb) sums[b] = before + incl - x;
+    __syncthreads();
+    if (threadIdx.x == kScanBlock - 1) carry = before + incl;
+    __syncthreads();
+  }
+  if (threadIdx.x == 0) doc_index[n_docs] = carry;
+}
+
+// Phase 3: add each block's carry-in.
+__global__ __launch_bounds__(kScanBlock) void doc_scan_add_kernel(
+    uint64_t* __restrict__ doc_index, const uint64_t* __restrict__ sums, uint64_t n_docs) {
+  const uint64_t base = (uint64_t)blockIdx.x * kScanBlock * kScanPer + threadIdx.x * kScanPer;
+  const uint64_t add = sums[blockIdx.x];
+#pragma unroll
+  for (int q = 0; q < kScanPer; ++q)
+    if (base + q < n_docs) doc_index[base + q] += add;
+}
+
+// One wave per document (grid-stride): n_d, the centroid ids and the codes,
+// then zero padding.  Doc starts are 8-aligned, so the id array is 4-aligned;
+// codes are copied as 32-bit words when source and destination allow.
+__global__ __launch_bounds__(256) void doc_write_kernel(
+    const uint64_t* __restrict__ doc_offsets, uint64_t n_docs, const uint32_t* __restrict__ assign,
+    const uint8_t* __restrict__ codes, uint32_t m, uint32_t cb,
+    const uint64_t* __restrict__ doc_index, uint8_t* __restrict__ payload) {
+  const uint32_t lane = threadIdx.x % 64;
+  const uint64_t waves = (uint64_t)gridDim.x * (blockDim.x / 64);
+  for (uint64_t d = (uint64_t)blockIdx.x * (blockDim.x / 64) + threadIdx.x / 64; d < n_docs;
+       d += waves) {
+    const uint64_t lo = doc_offsets[d], n_d = doc_offsets[d + 1] - lo;
+    uint8_t* p = payload + doc_index[d];
+    uint32_t* ids = reinterpret_cast<uint32_t*>(p + 4);
+    if (lane == 0) *reinterpret_cast<uint32_t*>(p) = (uint32_t)n_d;
+    for (uint64_t k = lane; k < n_d; k += 64) ids[k] = assign[lo + k];
+    const uint64_t nbytes = n_d * m * cb;
+    const uint8_t* src = codes + lo * m * cb;
+    uint8_t* dst = p + 4 + 4 * n_d;
+    if (((uintptr_t)src & 3) == 0 && (nbytes & 3) == 0) {
+      const uint32_t* s4 = reinterpret_cast<const uint32_t*>(src);
+      uint32_t* d4 = reinterpret_cast<uint32_t*>(dst);
+      for (uint64_t q = lane; q < nbytes / 4; q += 64) d4[q] = s4[q];
+    } else {
+      for (uint64_t q = lane; q < nbytes; q += 64) dst[q] = src[q];
+    }
+    const uint64_t used = 4 + 4 * n_d + nbytes;
+    const uint64_t total = doc_bytes(n_d, m, cb);
+    for (uint64_t q = used + lane; q < total; q += 64) p[q] = 0;
+  }
+}
+
+// ---------------------------------------------------------------------------
+// CRC-32/ISO-HDLC of a device buffer (std.hash.Crc32, as storage.zig applies
+// it to the whole image before the footer, :612-617, :782-786).
+//
+// Reflected representation: bit 31 holds the coefficient of x^0.  The
+// register after bytes B starting from register r is
+//   crc(r, B) = crc(0, B) ^ (r * x^(8|B|) mod P),
+// so zero-seeded CRCs of consecutive pieces combine left to right by one
+// modular multiplication each.  The buffer splits into an unaligned head
+// (< 16 bytes), a body of whole kCrcLeaf-byte leaves and a tail
+// (< kCrcLeaf bytes).  Every body leaf gets a thread, the 256 leaves of a
+// block combine in an LDS tree, the block results combine in one block, and
+// one thread adds head, tail and the all-ones preset.
+// ---------------------------------------------------------------------------
+constexpr uint32_t kCrcPoly = 0xEDB88320u;
+constexpr uint32_t kCrcLeaf = 1024;      // bytes per leaf (power of two)
+constexpr uint32_t kCrcLeafLog2 = 10;
+constexpr int kCrcBlock = 256;
+
+// x^(8 * 2^j) mod P for j = 0..63, reflected.
+struct CrcPowers {
+  uint32_t x8[64];
+};
+
+__host__ __device__ inline uint32_t crc_mulmod(uint32_t a, uint32_t b) {
+  uint32_t p = 0;
+  for (int i = 0; i < 32; ++i) {
+    if ((a >> (31 - i)) & 1u) p ^= b;
+    b = (b & 1u) ? (b >> 1) ^ kCrcPoly : b >> 1;
+  }
+  return p;
+}
+
+// r * x^(8 * count * 2^shift) mod P from the table of powers.
+__host__ __device__ inline uint32_t crc_shift(uint32_t r, uint64_t count, uint32_t shift,
+                                              const CrcPowers& pw) {
+  for (uint32_t j = 0; count; ++j, count >>= 1)
+    if (count & 1u) r = crc_mulmod(pw.x8[j + shift], r);
+  return r;
+}
+
+inline CrcPowers crc_powers_host() {
+  CrcPowers pw;
+  uint32_t t = 0x40000000u;  // x^1
+  for (int j = 0; j < 3; ++j) t = crc_mulmod(t, t);  // x^8
+  for (int j = 0; j < 64; ++j) {
+    pw.x8[j] = t;
+    t = crc_mulmod(t, t);
+  }
+  return pw;
+}
+
+// Slicing-by-4 tables in LDS: T[k][i] = CRC contribution of byte value i
+// followed by k zero bytes, from a zero register.
+__device__ inline void crc_tables(uint32_t (*T)[256]) {
+  for (uint32_t i = threadIdx.x; i < 256; i += blockDim.x) {
+    uint32_t r = i;
+    for (int k = 0; k < 8; ++k) r = (r & 1u) ? (r >> 1) ^ kCrcPoly : r >> 1;
+    T[0][i] = r;
+  }
+  __syncthreads();
+  for (int k = 1; k < 4; ++k) {
+    for (uint32_t i = threadIdx.x; i < 256; i += blockDim.x) {
+      const uint32_t v = T[k - 1][i];
+      T[k][i] = (v >> 8) ^ T[0][v & 0xFFu];
+    }
+    __syncthreads();
+  }
+}
+
+__device__ __forceinline__ uint32_t crc_word(uint32_t r, uint32_t w, const uint32_t (*T)[256]) {
+  r ^= w;
+  return T[3][r & 0xFFu] ^ T[2][(r >> 8) & 0xFFu] ^ T[1][(r >> 16) & 0xFFu] ^ T[0][r >> 24];
+}
+
+struct CrcNode {
+  uint32_t crc;
+  uint32_t leaves;
+};
+
+// Leaves of the 16-byte aligned body; one CrcNode per block.
+__global__ __launch_bounds__(kCrcBlock) void crc_leaf_kernel(const uint8_t* __restrict__ body,
+                                                             uint64_t n_leaves, CrcPowers pw,
+                                                             CrcNode* __restrict__ out) {
+  __shared__ uint32_t T[4][256];
+  __shared__ CrcNode node[kCrcBlock];
+  crc_tables(T);
+  const uint64_t leaf = (uint64_t)blockIdx.x * kCrcBlock + threadIdx.x;
+  uint32_t r = 0;
+  uint32_t have = 0;
+  if (leaf < n_leaves) {
+    const uint4* p = reinterpret_cast<const uint4*>(body + leaf * kCrcLeaf);
+#pragma unroll 4
+    for (uint32_t q = 0; q < kCrcLeaf / 16; ++q) {
+      const uint4 v = p[q];
+      r = crc_word(r, v.x, T);
+      r = crc_word(r, v.y, T);
+      r = crc_word(r, v.z, T);
+      r = crc_word(r, v.w, T);
+    }
+    have = 1;
+  }
+  node[threadIdx.x] = CrcNode{r, have};
+  __syncthreads();
+  for (uint32_t span = 1; span < kCrcBlock; span <<= 1) {
+    if (threadIdx.x % (2 * span) == 0) {
+      const CrcNode a = node[threadIdx.x], b = node[threadIdx.x + span];
+      if (b.leaves)
+        node[threadIdx.x] =
+            CrcNode{crc_shift(a.crc, b.leaves, kCrcLeafLog2, pw) ^ b.crc, a.leaves + b.leaves};
+    }
+    __syncthreads();
+  }
+  if (threadIdx.x == 0) out[blockIdx.x] = node[0];
+}
+
+// One block: folds the per-block nodes, then head, body and tail.
+__global__ __launch_bounds__(kCrcBlock) void crc_final_kernel(
+    const uint8_t* __restrict__ buf, uint64_t head, uint64_t body_leaves, uint64_t tail,
+    const CrcNode* __restrict__ nodes, uint32_t n_nodes, CrcPowers pw,
+    uint32_t* __restrict__ crc_out) {
+  __shared__ uint32_t T[4][256];
+  __shared__ CrcNode node[kCrcBlock];
+  __shared__ CrcNode acc;
+  crc_tables(T);
+  if (threadIdx.x == 0) acc = CrcNode{0, 0};
+  __syncthreads();
+  for (uint32_t b0 = 0; b0 < n_nodes; b0 += kCrcBlock) {
+    const uint32_t b = b0 + threadIdx.x;
+    node[threadIdx.x] = b < n_nodes ? nodes[b] : CrcNode{0, 0};
+    __syncthreads();
+    for (uint32_t span = 1; span < kCrcBlock; span <<= 1) {
+      if (threadIdx.x % (2 * span) == 0) {
+        const CrcNode a = node[threadIdx.x], c = node[threadIdx.x + span];
+        if (c.leaves)
+          node[threadIdx.x] =
+              CrcNode{crc_shift(a.crc, c.leaves, kCrcLeafLog2, pw) ^ c.crc, a.leaves + c.leaves};
+      }
+      __syncthreads();
+    }
+    if (threadIdx.x == 0 && node[0].leaves)
+      acc = CrcNode{crc_shift(acc.crc, node[0].leaves, kCrcLeafLog2, pw) ^ node[0].crc,
+                    acc.leaves + node[0].leaves};
+    __syncthreads();
+  }
+  if (threadIdx.x != 0) return;
+  uint32_t r = 0xFFFFFFFFu;
+  for (uint64_t i = 0; i < head; ++i) r = T[0][(r ^ buf[i]) & 0xFFu] ^ (r >> 8);
+  r = crc_shift(r, body_leaves, kCrcLeafLog2, pw) ^ acc.crc;
+  const uint8_t* t = buf + head + body_leaves * kCrcLeaf;
+  for (uint64_t i = 0; i < tail; ++i) r = T[0][(r ^ t[i]) & 0xFFu] ^ (r >> 8);
+  *crc_out = r ^ 0xFFFFFFFFu;
+}
+
+}  // namespace tacgpu

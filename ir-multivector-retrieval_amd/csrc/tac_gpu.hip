@@ -6,6 +6,8 @@
 //   PQ.decode    src/index/pq.zig:79-88
 //   kmeans.fit   src/tac/kmeans.zig:67-365
 //   residuals    src/index/storage.zig:255-278,355-376 (storage.build stage 2)
+//   doc layouts  src/index/storage.zig:674-686,705-749 and the image CRC-32
+//   distance table / refine  src/index/pq.zig:92-123, src/retrieval/refine.zig:83-145
 //
 // One training call keeps the residuals resident in HBM as a subspace-major
 // copy and runs every Lloyd iteration of all subspaces as a fixed sequence of
@@ -18,6 +20,7 @@
 #include "pq_kernels.hpp"
 #include "kmeanspp.hpp"
 #include "storage_kernels.hpp"
+#include "query_kernels.hpp"
 
 #include <hip/hip_runtime.h>
 
@@ -79,7 +82,8 @@ struct DeviceState {
   hipEvent_t last_done = nullptr;
   // training / encode workspace
   Buffer xs, codes, e, hist, counts, start, sorted, flags, scal, trace, io_in, io_out, io_cb,
-      io_init, counter, kpp_state, kpp_w, kpp_bsum, kpp_bad, status, io_aux, io_out2;
+      io_init, counter, kpp_state, kpp_w, kpp_bsum, kpp_bad, status, io_aux, io_out2, scan_sums,
+      io_x1, io_x2, io_x3;
   // measurement
   std::vector<hipEvent_t> events;
 };
@@ -609,7 +613,12 @@ const char *kNames[] = {"Ok",
                         "NoDevice",
                         "HipError",
                         "InvalidArgument",
-                        "Unsupported"};
+                        "Unsupported",
+                        "QueryShapeMismatch",
+                        "TableSizeMismatch",
+                        "DocOutOfRange",
+                        "DocLayoutCorrupt",
+                        "BufferTooSmall"};
 
 }  // namespace
 
@@ -1017,6 +1026,406 @@ int tac_residuals(const float *vectors, uint64_t n, uint32_t dim, const float *c
   HIP_TRY(hipMemcpyAsync(residuals_out, ds->io_out.ptr, x_bytes, hipMemcpyDeviceToHost, s));
   HIP_TRY(hipMemcpyAsync(norms_out, ds->io_out2.ptr, (size_t)n * sizeof(float),
                          hipMemcpyDeviceToHost, s));
+  HIP_TRY(hipStreamSynchronize(s));
+  return end_call(*ds, s);
+}
+
+}  // extern "C"
+
+// ---- .tac doc layouts, CRC-32, distance table, refine ----------------------
+
+namespace {
+
+uint64_t align8_host(uint64_t x) { return (x + 7u) & ~(uint64_t)7u; }
+
+int doc_layouts_core(DeviceState &ds, hipStream_t s, const uint64_t *d_off, uint64_t n_docs,
+                     uint64_t n_tokens, const uint32_t *d_assign, const uint8_t *d_codes,
+                     uint32_t m, uint32_t cb, uint64_t *d_index, uint8_t *d_payload,
+                     uint64_t payload_len, uint64_t *total_out) {
+  uint32_t *status = nullptr;
+  int st = status_begin(ds, s, &status);
+  if (st) return st;
+  if (n_docs == 0) {
+    HIP_TRY(hipMemsetAsync(d_index, 0, sizeof(uint64_t), s));
+    HIP_TRY(hipStreamSynchronize(s));
+    *total_out = 0;
+    return TAC_OK;
+  }
+  const uint64_t per = (uint64_t)kScanBlock * kScanPer;
+  const uint64_t nb = (n_docs + per - 1) / per;
+  if (nb > 0x7FFFFFFFull) return TAC_ERR_UNSUPPORTED;
+  if ((st = ensure(ds, ds.scan_sums, (size_t)nb * sizeof(uint64_t)))) return st;
+  uint64_t *sums = as<uint64_t>(ds.scan_sums);
+  doc_sizes_scan_kernel<<<(unsigned)nb, kScanBlock, 0, s>>>(d_off, n_docs, n_tokens, m, cb,
+                                                           d_index, sums, status);
+  doc_sums_scan_kernel<<<1, kScanBlock, 0, s>>>(sums, (uint32_t)nb, d_index, n_docs);
+  doc_scan_add_kernel<<<(unsigned)nb, kScanBlock, 0, s>>>(d_index, sums, n_docs);
+  LAUNCH_TRY("doc layout scan");
+  uint64_t total = 0;
+  HIP_TRY(hipMemcpyAsync(&total, d_index + n_docs, sizeof(total), hipMemcpyDeviceToHost, s));
+  if ((st = status_collect(ds, s))) return st;  // synchronises the stream
+  *total_out = total;
+  if (total > payload_len) {
+    g_last_error = "payload buffer smaller than the document layouts";
+    return TAC_ERR_BUFFER_TOO_SMALL;
+  }
+  const uint64_t waves_wanted = n_docs < (1ull << 20) ? n_docs : (1ull << 20);
+  const unsigned blocks = (unsigned)((waves_wanted + 3) / 4);
+  doc_write_kernel<<<blocks, 256, 0, s>>>(d_off, n_docs, d_assign, d_codes, m, cb, d_index,
+                                          d_payload);
+  LAUNCH_TRY("doc_write_kernel");
+  HIP_TRY(hipStreamSynchronize(s));
+  return TAC_OK;
+}
+
+int crc_core(DeviceState &ds, hipStream_t s, const uint8_t *d_buf, uint64_t len, uint32_t *out) {
+  const uint64_t mis = (uintptr_t)d_buf % 16;
+  const uint64_t head = mis ? ((16 - mis) < len ? (16 - mis) : len) : 0;
+  const uint64_t leaves = (len - head) / kCrcLeaf;
+  const uint64_t tail = len - head - leaves * kCrcLeaf;
+  const uint64_t nb = (leaves + kCrcBlock - 1) / kCrcBlock;
+  if (nb > 0x7FFFFFFFull) return TAC_ERR_UNSUPPORTED;
+  int st;
+  if ((st = ensure(ds, ds.scan_sums, (size_t)(nb ? nb : 1) * sizeof(CrcNode) + 16))) return st;
+  CrcNode *nodes = as<CrcNode>(ds.scan_sums);
+  uint32_t *d_crc = reinterpret_cast<uint32_t *>(nodes + (nb ? nb : 1));
+  static const CrcPowers pw = crc_powers_host();
+  if (nb) crc_leaf_kernel<<<(unsigned)nb, kCrcBlock, 0, s>>>(d_buf + head, leaves, pw, nodes);
+  crc_final_kernel<<<1, kCrcBlock, 0, s>>>(d_buf, head, leaves, tail, nodes, (uint32_t)nb, pw,
+                                           d_crc);
+  LAUNCH_TRY("crc kernels");
+  HIP_TRY(hipMemcpyAsync(out, d_crc, sizeof(uint32_t), hipMemcpyDeviceToHost, s));
+  HIP_TRY(hipStreamSynchronize(s));
+  return TAC_OK;
+}
+
+int refine_smem(uint32_t n_q, uint32_t dim, size_t *bytes) {
+  const uint64_t floats = (uint64_t)n_q * (dim + 1) + (uint64_t)kRefineWaves * (dim + 64);
+  if (floats * sizeof(float) > 65536) return TAC_ERR_UNSUPPORTED;
+  *bytes = (size_t)floats * sizeof(float);
+  return TAC_OK;
+}
+
+// refine.zig:99-105 argument checks, shared by both entry points.
+int validate_refine(const tac_doc_index *ix, uint64_t table_len, uint32_t n_q) {
+  if (!ix) return TAC_ERR_INVALID_ARGUMENT;
+  if (n_q == 0) return TAC_ERR_QUERY_SHAPE_MISMATCH;
+  if (table_len != (uint64_t)ix->m * ix->ksub * n_q) return TAC_ERR_TABLE_SIZE_MISMATCH;
+  if (ix->dim == 0 || ix->m == 0 || ix->ksub == 0 || ix->ksub > 65536)
+    return TAC_ERR_INVALID_ARGUMENT;
+  size_t smem;
+  return refine_smem(n_q, ix->dim, &smem);
+}
+
+int refine_core(DeviceState &ds, hipStream_t s, const tac_doc_index &ix, const float *d_table,
+                const float *d_q, uint32_t n_q, const uint32_t *d_ids, uint32_t n_cand,
+                float *d_scores) {
+  size_t smem = 0;
+  int st = refine_smem(n_q, ix.dim, &smem);
+  if (st) return st;
+  if ((st = ensure(ds, ds.io_x3, (size_t)n_cand * sizeof(uint32_t) + 16))) return st;
+  uint32_t *status = as<uint32_t>(ds.io_x3);
+  uint32_t *first_bad = status + n_cand;
+  HIP_TRY(hipMemsetAsync(first_bad, 0xFF, sizeof(uint32_t), s));
+  RefineIndex r{ix.centroids, ix.doc_index, ix.doc_payload, ix.doc_token_offsets,
+                ix.residual_norms, ix.n_docs, ix.n_tokens, ix.payload_len, ix.dim, ix.kappa,
+                ix.m, ix.ksub};
+  const uint32_t want = (n_cand + kRefineWaves - 1) / kRefineWaves;
+  const unsigned blocks = want < 8192 ? want : 8192;
+  refine_kernel<<<blocks, 64 * kRefineWaves, smem, s>>>(r, d_q, n_q, d_table, d_ids, n_cand,
+                                                       d_scores, status, first_bad);
+  LAUNCH_TRY("refine_kernel");
+  uint32_t bad = 0xFFFFFFFFu;
+  HIP_TRY(hipMemcpyAsync(&bad, first_bad, sizeof(bad), hipMemcpyDeviceToHost, s));
+  HIP_TRY(hipStreamSynchronize(s));
+  if (bad != 0xFFFFFFFFu) {
+    uint32_t code = 0;
+    HIP_TRY(hipMemcpy(&code, status + bad, sizeof(code), hipMemcpyDeviceToHost));
+    g_last_error = "refine failed at candidate " + std::to_string(bad);
+    return (int)code;
+  }
+  return TAC_OK;
+}
+
+}  // namespace
+
+extern "C" {
+
+int tac_doc_payload_bytes(const uint64_t *doc_offsets, uint64_t n_docs, uint32_t m,
+                          uint32_t code_bytes, uint64_t *bytes_out) {
+  if (!bytes_out || (n_docs && !doc_offsets) || m == 0 || (code_bytes != 1 && code_bytes != 2))
+    return TAC_ERR_INVALID_ARGUMENT;
+  uint64_t total = 0;
+  for (uint64_t d = 0; d < n_docs; ++d) {
+    if (doc_offsets[d + 1] < doc_offsets[d]) return TAC_ERR_INVALID_ARGUMENT;
+    const uint64_t n_d = doc_offsets[d + 1] - doc_offsets[d];
+    total += align8_host(4 + 4 * n_d + n_d * (uint64_t)m * code_bytes);
+  }
+  *bytes_out = total;
+  return TAC_OK;
+}
+
+int tac_write_doc_layouts_device(const uint64_t *d_doc_offsets, uint64_t n_docs,
+                                 uint64_t n_tokens, const uint32_t *d_assignments,
+                                 const void *d_codes, uint32_t m, uint32_t code_bytes,
+                                 uint64_t *d_doc_index_out, uint8_t *d_payload_out,
+                                 uint64_t payload_len, void *stream) {
+  if (m == 0 || (code_bytes != 1 && code_bytes != 2)) return TAC_ERR_INVALID_ARGUMENT;
+  if (!d_doc_offsets || !d_doc_index_out || (n_tokens && (!d_assignments || !d_codes)) ||
+      (payload_len && !d_payload_out) || ((uintptr_t)d_payload_out % 8))
+    return TAC_ERR_INVALID_ARGUMENT;
+  DeviceState *ds = nullptr;
+  int st = acquire_device(&ds, nullptr);
+  if (st) return st;
+  std::lock_guard<std::mutex> g(ds->mu);
+  hipStream_t s;
+  if ((st = resolve_stream(*ds, stream, &s))) return st;
+  if ((st = begin_call(*ds, s))) return st;
+  uint64_t total = 0;
+  if ((st = doc_layouts_core(*ds, s, d_doc_offsets, n_docs, n_tokens, d_assignments,
+                             static_cast<const uint8_t *>(d_codes), m, code_bytes,
+                             d_doc_index_out, d_payload_out, payload_len, &total)))
+    return st;
+  return end_call(*ds, s);
+}
+
+int tac_write_doc_layouts(const uint64_t *doc_offsets, uint64_t n_docs, uint64_t n_tokens,
+                          const uint32_t *assignments, const void *codes, uint32_t m,
+                          uint32_t code_bytes, uint64_t *doc_index_out, uint8_t *payload_out,
+                          uint64_t payload_len) {
+  if (m == 0 || (code_bytes != 1 && code_bytes != 2)) return TAC_ERR_INVALID_ARGUMENT;
+  if (!doc_offsets || !doc_index_out || (n_tokens && (!assignments || !codes)) ||
+      (payload_len && !payload_out))
+    return TAC_ERR_INVALID_ARGUMENT;
+  // Host-side checks first: the reference's BufferTooSmall precedes any write.
+  uint64_t need = 0;
+  int st = tac_doc_payload_bytes(doc_offsets, n_docs, m, code_bytes, &need);
+  if (st) return st;
+  if (n_docs && doc_offsets[n_docs] > n_tokens) return TAC_ERR_INVALID_ARGUMENT;
+  if (need > payload_len) return TAC_ERR_BUFFER_TOO_SMALL;
+  DeviceState *ds = nullptr;
+  if ((st = acquire_device(&ds, nullptr))) return st;
+  std::lock_guard<std::mutex> g(ds->mu);
+  hipStream_t s;
+  if ((st = resolve_stream(*ds, nullptr, &s))) return st;
+  if ((st = begin_call(*ds, s))) return st;
+  const size_t off_b = (size_t)(n_docs + 1) * sizeof(uint64_t);
+  const size_t a_b = (size_t)n_tokens * sizeof(uint32_t);
+  const size_t c_b = (size_t)n_tokens * m * code_bytes;
+  if ((st = ensure(*ds, ds->io_x1, off_b)) || (st = ensure(*ds, ds->io_aux, a_b + 4)) ||
+      (st = ensure(*ds, ds->io_in, c_b + 4)) || (st = ensure(*ds, ds->io_x2, off_b)) ||
+      (st = ensure(*ds, ds->io_out, need + 8)))
+    return st;
+  HIP_TRY(hipMemcpyAsync(ds->io_x1.ptr, doc_offsets, off_b, hipMemcpyHostToDevice, s));
+  if (a_b) HIP_TRY(hipMemcpyAsync(ds->io_aux.ptr, assignments, a_b, hipMemcpyHostToDevice, s));
+  if (c_b) HIP_TRY(hipMemcpyAsync(ds->io_in.ptr, codes, c_b, hipMemcpyHostToDevice, s));
+  uint64_t total = 0;
+  if ((st = doc_layouts_core(*ds, s, as<uint64_t>(ds->io_x1), n_docs, n_tokens,
+                             as<uint32_t>(ds->io_aux), as<uint8_t>(ds->io_in), m, code_bytes,
+                             as<uint64_t>(ds->io_x2), as<uint8_t>(ds->io_out), need + 8, &total)))
+    return st;
+  HIP_TRY(hipMemcpyAsync(doc_index_out, ds->io_x2.ptr, off_b, hipMemcpyDeviceToHost, s));
+  if (total) HIP_TRY(hipMemcpyAsync(payload_out, ds->io_out.ptr, total, hipMemcpyDeviceToHost, s));
+  HIP_TRY(hipStreamSynchronize(s));
+  return end_call(*ds, s);
+}
+
+int tac_crc32_device(const void *d_bytes, uint64_t len, uint32_t *crc_out, void *stream) {
+  if (!crc_out || (len && !d_bytes)) return TAC_ERR_INVALID_ARGUMENT;
+  if (len == 0) {
+    *crc_out = 0;
+    return TAC_OK;
+  }
+  DeviceState *ds = nullptr;
+  int st = acquire_device(&ds, nullptr);
+  if (st) return st;
+  std::lock_guard<std::mutex> g(ds->mu);
+  hipStream_t s;
+  if ((st = resolve_stream(*ds, stream, &s))) return st;
+  if ((st = begin_call(*ds, s))) return st;
+  const bool profile = g_profile;
+  hipEvent_t a = nullptr, b = nullptr;
+  if (profile) {
+    if ((st = event_at(*ds, 0, &a)) || (st = event_at(*ds, 1, &b))) return st;
+    HIP_TRY(hipEventRecord(a, s));
+  }
+  if ((st = crc_core(*ds, s, static_cast<const uint8_t *>(d_bytes), len, crc_out))) return st;
+  if (profile) {
+    HIP_TRY(hipEventRecord(b, s));
+    HIP_TRY(hipEventSynchronize(b));
+    float ms = 0.0f;
+    HIP_TRY(hipEventElapsedTime(&ms, a, b));
+    std::lock_guard<std::mutex> gp(g_profile_mu);
+    g_prof.crc_ms += ms;
+    g_prof.crc_launches += 1;
+  }
+  return end_call(*ds, s);
+}
+
+int tac_crc32(const void *bytes, uint64_t len, uint32_t *crc_out) {
+  if (!crc_out || (len && !bytes)) return TAC_ERR_INVALID_ARGUMENT;
+  if (len == 0) {
+    *crc_out = 0;
+    return TAC_OK;
+  }
+  DeviceState *ds = nullptr;
+  int st = acquire_device(&ds, nullptr);
+  if (st) return st;
+  std::lock_guard<std::mutex> g(ds->mu);
+  hipStream_t s;
+  if ((st = resolve_stream(*ds, nullptr, &s))) return st;
+  if ((st = begin_call(*ds, s))) return st;
+  if ((st = ensure(*ds, ds->io_in, len))) return st;
+  HIP_TRY(hipMemcpyAsync(ds->io_in.ptr, bytes, len, hipMemcpyHostToDevice, s));
+  if ((st = crc_core(*ds, s, as<uint8_t>(ds->io_in), len, crc_out))) return st;
+  return end_call(*ds, s);
+}
+
+int tac_pq_distance_table_device(const float *d_query_tokens, uint32_t n_q, uint32_t dim,
+                                 uint32_t m, uint32_t ksub, const float *d_codebooks,
+                                 float *d_table_out, uint64_t table_len, void *stream) {
+  if (m == 0 || ksub == 0) return TAC_ERR_INVALID_ARGUMENT;
+  if (n_q == 0) return TAC_ERR_NQ_MISMATCH;  // pq.zig:99
+  if (dim == 0 || dim % m != 0) return TAC_ERR_DIM_MISMATCH;
+  if (table_len != (uint64_t)m * ksub * n_q) return TAC_ERR_OUT_BUFFER_WRONG_SIZE;  // :106
+  if (!d_query_tokens || !d_codebooks || !d_table_out) return TAC_ERR_INVALID_ARGUMENT;
+  DeviceState *ds = nullptr;
+  int st = acquire_device(&ds, nullptr);
+  if (st) return st;
+  std::lock_guard<std::mutex> g(ds->mu);
+  hipStream_t s;
+  if ((st = resolve_stream(*ds, stream, &s))) return st;
+  if ((st = begin_call(*ds, s))) return st;
+  const uint64_t blocks = (table_len + 255) / 256;
+  if (blocks > 0x7FFFFFFFull) return TAC_ERR_UNSUPPORTED;
+  distance_table_kernel<<<(unsigned)blocks, 256, 0, s>>>(d_query_tokens, d_codebooks,
+                                                          d_table_out, n_q, dim, m, ksub,
+                                                          dim / m);
+  LAUNCH_TRY("distance_table_kernel");
+  return end_call(*ds, s);
+}
+
+int tac_pq_distance_table(const float *query_tokens, uint32_t n_q, uint32_t dim, uint32_t m,
+                          uint32_t ksub, const float *codebooks, float *table_out,
+                          uint64_t table_len) {
+  if (m == 0 || ksub == 0) return TAC_ERR_INVALID_ARGUMENT;
+  if (n_q == 0) return TAC_ERR_NQ_MISMATCH;
+  if (dim == 0 || dim % m != 0) return TAC_ERR_DIM_MISMATCH;
+  if (table_len != (uint64_t)m * ksub * n_q) return TAC_ERR_OUT_BUFFER_WRONG_SIZE;
+  if (!query_tokens || !codebooks || !table_out) return TAC_ERR_INVALID_ARGUMENT;
+  DeviceState *ds = nullptr;
+  int st = acquire_device(&ds, nullptr);
+  if (st) return st;
+  std::lock_guard<std::mutex> g(ds->mu);
+  hipStream_t s;
+  if ((st = resolve_stream(*ds, nullptr, &s))) return st;
+  if ((st = begin_call(*ds, s))) return st;
+  const size_t q_b = (size_t)n_q * dim * sizeof(float);
+  const size_t c_b = (size_t)ksub * dim * sizeof(float);
+  const size_t t_b = (size_t)table_len * sizeof(float);
+  if ((st = ensure(*ds, ds->io_in, q_b)) || (st = ensure(*ds, ds->io_cb, c_b)) ||
+      (st = ensure(*ds, ds->io_out, t_b)))
+    return st;
+  HIP_TRY(hipMemcpyAsync(ds->io_in.ptr, query_tokens, q_b, hipMemcpyHostToDevice, s));
+  HIP_TRY(hipMemcpyAsync(ds->io_cb.ptr, codebooks, c_b, hipMemcpyHostToDevice, s));
+  distance_table_kernel<<<(unsigned)((table_len + 255) / 256), 256, 0, s>>>(
+      as<float>(ds->io_in), as<float>(ds->io_cb), as<float>(ds->io_out), n_q, dim, m, ksub,
+      dim / m);
+  LAUNCH_TRY("distance_table_kernel");
+  HIP_TRY(hipMemcpyAsync(table_out, ds->io_out.ptr, t_b, hipMemcpyDeviceToHost, s));
+  HIP_TRY(hipStreamSynchronize(s));
+  return end_call(*ds, s);
+}
+
+int tac_refine_device(const tac_doc_index *d_index, const float *d_table, uint64_t table_len,
+                      const float *d_query_tokens, uint32_t n_q, const uint32_t *d_doc_ids,
+                      uint32_t n_candidates, float *d_scores_out, void *stream) {
+  int st = validate_refine(d_index, table_len, n_q);
+  if (st) return st;
+  if (n_candidates == 0) return TAC_OK;
+  const tac_doc_index &ix = *d_index;
+  if (!d_table || !d_query_tokens || !d_doc_ids || !d_scores_out || !ix.centroids ||
+      !ix.doc_index || !ix.doc_token_offsets || (ix.payload_len && !ix.doc_payload) ||
+      (ix.n_tokens && !ix.residual_norms))
+    return TAC_ERR_INVALID_ARGUMENT;
+  DeviceState *ds = nullptr;
+  if ((st = acquire_device(&ds, nullptr))) return st;
+  std::lock_guard<std::mutex> g(ds->mu);
+  hipStream_t s;
+  if ((st = resolve_stream(*ds, stream, &s))) return st;
+  if ((st = begin_call(*ds, s))) return st;
+  const bool profile = g_profile;
+  hipEvent_t a = nullptr, b = nullptr;
+  if (profile) {
+    if ((st = event_at(*ds, 0, &a)) || (st = event_at(*ds, 1, &b))) return st;
+    HIP_TRY(hipEventRecord(a, s));
+  }
+  if ((st = refine_core(*ds, s, ix, d_table, d_query_tokens, n_q, d_doc_ids, n_candidates,
+                        d_scores_out)))
+    return st;
+  if (profile) {
+    HIP_TRY(hipEventRecord(b, s));
+    HIP_TRY(hipEventSynchronize(b));
+    float ms = 0.0f;
+    HIP_TRY(hipEventElapsedTime(&ms, a, b));
+    std::lock_guard<std::mutex> gp(g_profile_mu);
+    g_prof.refine_ms += ms;
+    g_prof.refine_launches += 1;
+  }
+  return end_call(*ds, s);
+}
+
+int tac_refine(const tac_doc_index *index, const float *table, uint64_t table_len,
+               const float *query_tokens, uint32_t n_q, const uint32_t *doc_ids,
+               uint32_t n_candidates, float *scores_out) {
+  int st = validate_refine(index, table_len, n_q);
+  if (st) return st;
+  if (n_candidates == 0) return TAC_OK;
+  const tac_doc_index &h = *index;
+  if (!table || !query_tokens || !doc_ids || !scores_out || !h.centroids || !h.doc_index ||
+      !h.doc_token_offsets || (h.payload_len && !h.doc_payload) ||
+      (h.n_tokens && !h.residual_norms))
+    return TAC_ERR_INVALID_ARGUMENT;
+  DeviceState *ds = nullptr;
+  if ((st = acquire_device(&ds, nullptr))) return st;
+  std::lock_guard<std::mutex> g(ds->mu);
+  hipStream_t s;
+  if ((st = resolve_stream(*ds, nullptr, &s))) return st;
+  if ((st = begin_call(*ds, s))) return st;
+  // One staging allocation, 256-byte aligned pieces.
+  const size_t pieces[] = {(size_t)h.kappa * h.dim * sizeof(float),
+                           (size_t)(h.n_docs + 1) * sizeof(uint64_t),
+                           (size_t)h.payload_len,
+                           (size_t)(h.n_docs + 1) * sizeof(uint64_t),
+                           (size_t)h.n_tokens * sizeof(float),
+                           (size_t)table_len * sizeof(float),
+                           (size_t)n_q * h.dim * sizeof(float),
+                           (size_t)n_candidates * sizeof(uint32_t),
+                           (size_t)n_candidates * sizeof(float)};
+  const void *srcs[] = {h.centroids, h.doc_index, h.doc_payload, h.doc_token_offsets,
+                        h.residual_norms, table, query_tokens, doc_ids, nullptr};
+  size_t offs[9], total = 0;
+  for (int i = 0; i < 9; ++i) {
+    offs[i] = total;
+    total += (pieces[i] + 255) & ~size_t(255);
+  }
+  if ((st = ensure(*ds, ds->io_x1, total + 256))) return st;
+  uint8_t *base = as<uint8_t>(ds->io_x1);
+  for (int i = 0; i < 8; ++i)
+    if (pieces[i]) HIP_TRY(hipMemcpyAsync(base + offs[i], srcs[i], pieces[i], hipMemcpyHostToDevice, s));
+  tac_doc_index d = h;
+  d.centroids = reinterpret_cast<const float *>(base + offs[0]);
+  d.doc_index = reinterpret_cast<const uint64_t *>(base + offs[1]);
+  d.doc_payload = base + offs[2];
+  d.doc_token_offsets = reinterpret_cast<const uint64_t *>(base + offs[3]);
+  d.residual_norms = reinterpret_cast<const float *>(base + offs[4]);
+  float *d_scores = reinterpret_cast<float *>(base + offs[8]);
+  if ((st = refine_core(*ds, s, d, reinterpret_cast<const float *>(base + offs[5]),
+                        reinterpret_cast<const float *>(base + offs[6]), n_q,
+                        reinterpret_cast<const uint32_t *>(base + offs[7]), n_candidates,
+                        d_scores)))
+    return st;
+  HIP_TRY(hipMemcpyAsync(scores_out, d_scores, pieces[8], hipMemcpyDeviceToHost, s));
   HIP_TRY(hipStreamSynchronize(s));
   return end_call(*ds, s);
 }

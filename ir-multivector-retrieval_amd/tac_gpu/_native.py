@@ -55,6 +55,21 @@ class Profile(ctypes.Structure):
         ("exact_rescans", c_u64),
         ("residual_ms", ctypes.c_double),
         ("residual_launches", c_u64),
+        ("crc_ms", ctypes.c_double),
+        ("crc_launches", c_u64),
+        ("refine_ms", ctypes.c_double),
+        ("refine_launches", c_u64),
+    ]
+
+
+class DocIndex(ctypes.Structure):
+    """tac_doc_index: the parts of a parsed .tac Index that refine reads."""
+
+    _fields_ = [
+        ("dim", c_u32), ("kappa", c_u32), ("m", c_u32), ("ksub", c_u32),
+        ("n_docs", c_u64), ("n_tokens", c_u64), ("payload_len", c_u64),
+        ("centroids", c_void_p), ("doc_index", c_void_p), ("doc_payload", c_void_p),
+        ("doc_token_offsets", c_void_p), ("residual_norms", c_void_p),
     ]
 
 
@@ -96,6 +111,25 @@ SIGNATURES = {
         c_int, [c_void_p, c_u64, c_u32, c_void_p, c_u32, c_void_p, c_void_p, c_void_p]),
     "tac_residuals_device": (
         c_int, [c_void_p, c_u64, c_u32, c_void_p, c_u32, c_void_p, c_void_p, c_void_p, c_void_p]),
+    "tac_doc_payload_bytes": (c_int, [c_void_p, c_u64, c_u32, c_u32, ctypes.POINTER(c_u64)]),
+    "tac_write_doc_layouts": (
+        c_int, [c_void_p, c_u64, c_u64, c_void_p, c_void_p, c_u32, c_u32, c_void_p, c_void_p,
+                c_u64]),
+    "tac_write_doc_layouts_device": (
+        c_int, [c_void_p, c_u64, c_u64, c_void_p, c_void_p, c_u32, c_u32, c_void_p, c_void_p,
+                c_u64, c_void_p]),
+    "tac_crc32": (c_int, [c_void_p, c_u64, c_u32_p]),
+    "tac_crc32_device": (c_int, [c_void_p, c_u64, c_u32_p, c_void_p]),
+    "tac_pq_distance_table": (
+        c_int, [c_void_p, c_u32, c_u32, c_u32, c_u32, c_void_p, c_void_p, c_u64]),
+    "tac_pq_distance_table_device": (
+        c_int, [c_void_p, c_u32, c_u32, c_u32, c_u32, c_void_p, c_void_p, c_u64, c_void_p]),
+    "tac_refine": (
+        c_int, [ctypes.POINTER(DocIndex), c_void_p, c_u64, c_void_p, c_u32, c_void_p, c_u32,
+                c_void_p]),
+    "tac_refine_device": (
+        c_int, [ctypes.POINTER(DocIndex), c_void_p, c_u64, c_void_p, c_u32, c_void_p, c_u32,
+                c_void_p, c_void_p]),
     "tac_gpu_profile_enable": (c_int, [c_int]),
     "tac_gpu_profile_read": (c_int, [ctypes.POINTER(Profile), c_int]),
 }
@@ -104,6 +138,8 @@ STATUS_NAMES = [
     "Ok", "DimNotDivisibleByM", "DimMismatch", "EmptyCorpus", "OutBufferWrongSize",
     "NQMismatch", "KmeansBudgetTooSmall", "EmptyVectorSet", "EmptyDistribution", "NonFinite",
     "AllZero", "OutOfMemory", "NoDevice", "HipError", "InvalidArgument", "Unsupported",
+    "QueryShapeMismatch", "TableSizeMismatch", "DocOutOfRange", "DocLayoutCorrupt",
+    "BufferTooSmall",
 ]
 
 

@@ -75,6 +75,26 @@ class Unsupported(TacError):
     status = 15
 
 
+class QueryShapeMismatch(TacError):
+    status = 16
+
+
+class TableSizeMismatch(TacError):
+    status = 17
+
+
+class DocOutOfRange(TacError):
+    status = 18
+
+
+class DocLayoutCorrupt(TacError):
+    status = 19
+
+
+class BufferTooSmall(TacError):
+    status = 20
+
+
 _BY_STATUS = {cls.status: cls for cls in TacError.__subclasses__()}
 
 

@@ -101,6 +101,20 @@ class PQ:
             raise errors.DimMismatch("DimMismatch")
         return self.decode_many(c.reshape(1, self.m))[0]
 
+    def build_distance_table(self, query_tokens: np.ndarray, n_q: int) -> np.ndarray:
+        """PQ.buildDistanceTable (pq.zig:92-123): float32 [m][ksub][n_q] of
+        dot(query_i[m-th sub-vector], codeword)."""
+        if n_q == 0:
+            raise errors.NQMismatch("NQMismatch")
+        q = np.ascontiguousarray(query_tokens, dtype=np.float32).reshape(-1)
+        if q.size != n_q * self.dim:
+            raise errors.NQMismatch("NQMismatch")
+        out = np.empty((self.m, self.ksub, n_q), dtype=np.float32)
+        cb = np.ascontiguousarray(self.codebooks, dtype=np.float32)
+        errors.check(lib.tac_pq_distance_table(_ptr(q), n_q, self.dim, self.m, self.ksub,
+                                               _ptr(cb), _ptr(out), out.size))
+        return out
+
     def decode_many(self, codes: np.ndarray) -> np.ndarray:
         c = np.ascontiguousarray(codes, dtype=code_dtype(self.ksub))
         if c.size % self.m != 0:

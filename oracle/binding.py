@@ -71,6 +71,15 @@ def _load():
     L.orc_pq_distance_table.argtypes = [_vp, _u32, _u32, _u32, _u32, _vp, _vp, _u64]
     L.orc_residuals.restype = ctypes.c_int
     L.orc_residuals.argtypes = [_vp, _u64, _u32, _vp, _u32, _vp, _vp, _vp]
+    L.orc_doc_payload_bytes.restype = _u64
+    L.orc_doc_payload_bytes.argtypes = [_vp, _u64, _u32, _u32]
+    L.orc_write_doc_layouts.restype = ctypes.c_int
+    L.orc_write_doc_layouts.argtypes = [_vp, _u64, _vp, _vp, _u32, _u32, _vp, _vp, _u64]
+    L.orc_crc32.restype = _u32
+    L.orc_crc32.argtypes = [_vp, _u64]
+    L.orc_refine.restype = ctypes.c_int
+    L.orc_refine.argtypes = [_vp, _u32, _u32, _vp, _u32, _vp, _u64, _u32, _u32, _vp, _vp, _u64,
+                             _vp, _vp, _u64, _u64, _u64, ctypes.POINTER(_f32)]
     return L
 
 
@@ -244,3 +253,47 @@ def residuals(vectors, dim: int, centroids, assignments):
     st = lib.orc_residuals(_p(v), n, dim, _p(c), c.size // dim if dim else 0, _p(a), _p(r),
                            _p(nr))
     return st, r, nr
+
+
+def doc_payload_bytes(doc_offsets, m: int, code_bytes: int) -> int:
+    o = np.ascontiguousarray(doc_offsets, dtype=np.uint64)
+    return int(lib.orc_doc_payload_bytes(_p(o), o.size - 1, m, code_bytes))
+
+
+def write_doc_layouts(doc_offsets, assignments, codes, m: int, code_bytes: int,
+                      payload_len: int | None = None):
+    """(status, doc_index [n_docs+1] u64, payload bytes) of storage.zig:705-749."""
+    o = np.ascontiguousarray(doc_offsets, dtype=np.uint64)
+    a = np.ascontiguousarray(assignments, dtype=np.uint32)
+    c = np.ascontiguousarray(codes, dtype=np.uint8 if code_bytes == 1 else np.uint16)
+    n_docs = o.size - 1
+    need = doc_payload_bytes(o, m, code_bytes)
+    plen = need if payload_len is None else payload_len
+    idx = np.zeros(n_docs + 1, np.uint64)
+    pay = np.zeros(max(plen, 1), np.uint8)
+    st = lib.orc_write_doc_layouts(_p(o), n_docs, _p(a), _p(c), m, code_bytes, _p(idx), _p(pay),
+                                   plen)
+    return st, idx, pay[:plen]
+
+
+def crc32(data) -> int:
+    b = np.frombuffer(bytes(data), dtype=np.uint8) if not isinstance(data, np.ndarray) \
+        else np.ascontiguousarray(data).view(np.uint8).reshape(-1)
+    return int(lib.orc_crc32(_p(b) if b.size else None, b.size))
+
+
+def refine(query, n_q: int, dim: int, centroids, table, m: int, ksub: int, doc_index, payload,
+           doc_token_offsets, norms, doc_id: int):
+    """(status, score) of refine.zig:83-145 for one candidate document."""
+    q = _f32(query).reshape(-1)
+    c = _f32(centroids).reshape(-1)
+    t = _f32(table).reshape(-1)
+    di = np.ascontiguousarray(doc_index, dtype=np.uint64)
+    pay = np.ascontiguousarray(payload, dtype=np.uint8)
+    dto = np.ascontiguousarray(doc_token_offsets, dtype=np.uint64)
+    nr = _f32(norms).reshape(-1)
+    out = _f32_c()
+    st = lib.orc_refine(_p(q), n_q, dim, _p(c), c.size // dim, _p(t), t.size, m, ksub, _p(di),
+                        _p(pay), pay.size, _p(dto), _p(nr), nr.size, di.size - 1, doc_id,
+                        ctypes.byref(out))
+    return st, np.float32(out.value)

@@ -764,3 +764,131 @@ int orc_residuals(const float *vectors, uint64_t n, uint32_t dim,
   }
   return ORC_OK;
 }
+
+/* ------------------------------------------------------------------------ */
+/* .tac per-document layouts and footer checksum: src/index/storage.zig      */
+/* ------------------------------------------------------------------------ */
+
+static uint64_t align8(uint64_t x) { return (x + 7u) & ~(uint64_t)7u; }
+
+/* storage.zig:674-686 (docPayloadSize), with m codes of code_bytes each per
+ * token (the reference: m = PQ_M, one byte). */
+uint64_t orc_doc_payload_bytes(const uint64_t *doc_offsets, uint64_t n_docs,
+                               uint32_t m, uint32_t code_bytes) {
+  uint64_t total = 0;
+  for (uint64_t d = 0; d < n_docs; ++d) {
+    const uint64_t n_d = doc_offsets[d + 1] - doc_offsets[d];
+    total += align8(4 + n_d * 4 + n_d * (uint64_t)m * code_bytes);
+  }
+  return total;
+}
+
+/* storage.zig:705-749 (writeDocLayouts): doc_index[d] is the payload offset
+ * of doc d (doc_index[n_docs] = total); each doc is u32 n_d (LE), the n_d
+ * centroid ids (u32 LE), the n_d * m codes, zero padding to 8 bytes. */
+int orc_write_doc_layouts(const uint64_t *doc_offsets, uint64_t n_docs,
+                          const uint32_t *assignments, const void *codes,
+                          uint32_t m, uint32_t code_bytes, uint64_t *doc_index,
+                          uint8_t *payload, uint64_t payload_len) {
+  if (m == 0 || (code_bytes != 1 && code_bytes != 2)) return ORC_INVALID_ARGUMENT;
+  /* storage.zig:717: a payload buffer shorter than the layouts */
+  if (payload_len < orc_doc_payload_bytes(doc_offsets, n_docs, m, code_bytes))
+    return ORC_BUFFER_TOO_SMALL;
+  uint64_t off = 0;
+  for (uint64_t d = 0; d < n_docs; ++d) {
+    doc_index[d] = off;
+    const uint64_t lo = doc_offsets[d], n_d = doc_offsets[d + 1] - lo;
+    const uint64_t bytes = align8(4 + n_d * 4 + n_d * (uint64_t)m * code_bytes);
+    uint8_t *p = payload + off;
+    const uint32_t nd32 = (uint32_t)n_d;
+    for (int b = 0; b < 4; ++b) p[b] = (uint8_t)(nd32 >> (8 * b));
+    for (uint64_t k = 0; k < n_d; ++k)
+      for (int b = 0; b < 4; ++b) p[4 + 4 * k + b] = (uint8_t)(assignments[lo + k] >> (8 * b));
+    const uint64_t cb = n_d * (uint64_t)m * code_bytes;
+    memcpy(p + 4 + 4 * n_d, (const uint8_t *)codes + lo * (uint64_t)m * code_bytes, cb);
+    memset(p + 4 + 4 * n_d + cb, 0, bytes - (4 + 4 * n_d + cb));
+    off += bytes;
+  }
+  doc_index[n_docs] = off;
+  return ORC_OK;
+}
+
+/* std.hash.Crc32 as used by storage.zig:612-617 and :782-786: CRC-32/ISO-HDLC
+ * (reflected polynomial 0xEDB88320, register preset to all ones, result
+ * complemented), one byte at a time. */
+uint32_t orc_crc32(const uint8_t *bytes, uint64_t len) {
+  uint32_t table[256];
+  for (uint32_t i = 0; i < 256; ++i) {
+    uint32_t r = i;
+    for (int k = 0; k < 8; ++k) r = (r & 1u) ? (r >> 1) ^ 0xEDB88320u : r >> 1;
+    table[i] = r;
+  }
+  uint32_t r = 0xFFFFFFFFu;
+  for (uint64_t i = 0; i < len; ++i) r = table[(r ^ bytes[i]) & 0xFFu] ^ (r >> 8);
+  return r ^ 0xFFFFFFFFu;
+}
+
+/* ------------------------------------------------------------------------ */
+/* Query side: src/retrieval/refine.zig:83-145 for one candidate             */
+/* ------------------------------------------------------------------------ */
+
+int orc_refine(const float *query, uint32_t n_q, uint32_t dim,
+               const float *centroids, uint32_t kappa, const float *table,
+               uint64_t table_len, uint32_t m, uint32_t ksub,
+               const uint64_t *doc_index, const uint8_t *payload,
+               uint64_t payload_len, const uint64_t *doc_token_offsets,
+               const float *norms, uint64_t n_tokens, uint64_t n_docs,
+               uint64_t doc_id, float *score_out) {
+  if (n_q == 0) return ORC_QUERY_SHAPE_MISMATCH;                      /* :99-101 */
+  if (table_len != (uint64_t)m * ksub * n_q) return ORC_TABLE_SIZE_MISMATCH; /* :104 */
+  if (doc_id >= n_docs) return ORC_DOC_OUT_OF_RANGE;                  /* :107 */
+  const uint32_t code_bytes = ksub <= 256 ? 1 : 2;
+  /* storage.zig:112-116 docLayout, refine.zig:51-65 decodeDocLayout */
+  const uint64_t lo = doc_index[doc_id], hi = doc_index[doc_id + 1];
+  if (hi < lo || hi > payload_len || hi - lo < 4) return ORC_DOC_LAYOUT_CORRUPT;
+  const uint8_t *lay = payload + lo;
+  const uint32_t n_d = (uint32_t)lay[0] | (uint32_t)lay[1] << 8 | (uint32_t)lay[2] << 16 |
+                       (uint32_t)lay[3] << 24;
+  if (hi - lo < 4 + (uint64_t)n_d * 4 + (uint64_t)n_d * m * code_bytes)
+    return ORC_DOC_LAYOUT_CORRUPT;
+  const uint64_t t_lo = doc_token_offsets[doc_id], t_hi = doc_token_offsets[doc_id + 1];
+  if (t_hi - t_lo != n_d || t_hi > n_tokens) return ORC_DOC_LAYOUT_CORRUPT; /* :114 */
+  const uint8_t *ids = lay + 4;
+  const uint8_t *codes = lay + 4 + 4 * (uint64_t)n_d;
+  float *best = (float *)malloc(sizeof(float) * n_q);
+  if (!best) return ORC_OUT_OF_MEMORY;
+  for (uint32_t i = 0; i < n_q; ++i) best[i] = -INFINITY;
+  for (uint32_t k = 0; k < n_d; ++k) {
+    const uint32_t c_id = (uint32_t)ids[4 * k] | (uint32_t)ids[4 * k + 1] << 8 |
+                          (uint32_t)ids[4 * k + 2] << 16 | (uint32_t)ids[4 * k + 3] << 24;
+    if (c_id >= kappa) {  /* a bounds trap in the reference */
+      free(best);
+      return ORC_DOC_LAYOUT_CORRUPT;
+    }
+    const float *c_vec = centroids + (uint64_t)c_id * dim;
+    const float norm_k = norms[t_lo + k];
+    for (uint32_t i = 0; i < n_q; ++i) {
+      const float cent_term = orc_dot(query + (uint64_t)i * dim, c_vec, dim);
+      float res = 0.0f;
+      for (uint32_t mm = 0; mm < m; ++mm) {
+        const uint64_t cpos = ((uint64_t)k * m + mm) * code_bytes;
+        const uint32_t code = code_bytes == 1 ? codes[cpos]
+                                              : (uint32_t)codes[cpos] | (uint32_t)codes[cpos + 1] << 8;
+        if (code >= ksub) {
+          free(best);
+          return ORC_DOC_LAYOUT_CORRUPT;
+        }
+        res = res + table[((uint64_t)mm * ksub + code) * n_q + i];
+      }
+      const float scaled = norm_k * res;
+      const float score = cent_term + scaled;
+      if (score > best[i]) best[i] = score;
+    }
+  }
+  float sum = 0.0f;
+  if (n_d > 0)
+    for (uint32_t i = 0; i < n_q; ++i) sum = sum + best[i];
+  free(best);
+  *score_out = sum;
+  return ORC_OK;
+}

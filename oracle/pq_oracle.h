@@ -20,6 +20,11 @@
  *   orc_pq_decode           src/index/pq.zig:79-88
  *   orc_pq_distance_table   src/index/pq.zig:92-123
  *   orc_residuals           src/index/storage.zig:255-278
+ *   orc_doc_payload_bytes   src/index/storage.zig:674-686
+ *   orc_write_doc_layouts   src/index/storage.zig:705-749
+ *   orc_crc32               std.hash.Crc32 (CRC-32/ISO-HDLC) as storage.zig
+ *                           applies it to the image (:612-617, :782-786)
+ *   orc_refine              src/retrieval/refine.zig:51-145 (one candidate)
  *
  * Status codes share their numbering with include/tac_gpu.h.
  */
@@ -47,6 +52,11 @@ enum {
   ORC_RNG_ALL_ZERO = 10,
   ORC_OUT_OF_MEMORY = 11,
   ORC_INVALID_ARGUMENT = 14,
+  ORC_QUERY_SHAPE_MISMATCH = 16,  /* RefineError (src/retrieval/refine.zig:37-42) */
+  ORC_TABLE_SIZE_MISMATCH = 17,
+  ORC_DOC_OUT_OF_RANGE = 18,
+  ORC_DOC_LAYOUT_CORRUPT = 19,
+  ORC_BUFFER_TOO_SMALL = 20,      /* StorageError (src/index/storage.zig:42-47) */
 };
 
 /* Lane count the reference's generic vec path uses on the host it is built
@@ -119,6 +129,21 @@ int orc_pq_distance_table(const float *queries, uint32_t n_q, uint32_t dim,
 int orc_residuals(const float *vectors, uint64_t n, uint32_t dim,
                   const float *centroids, uint32_t n_centroids,
                   const uint32_t *assignments, float *residuals, float *norms);
+
+uint64_t orc_doc_payload_bytes(const uint64_t *doc_offsets, uint64_t n_docs,
+                               uint32_t m, uint32_t code_bytes);
+int orc_write_doc_layouts(const uint64_t *doc_offsets, uint64_t n_docs,
+                          const uint32_t *assignments, const void *codes,
+                          uint32_t m, uint32_t code_bytes, uint64_t *doc_index,
+                          uint8_t *payload, uint64_t payload_len);
+uint32_t orc_crc32(const uint8_t *bytes, uint64_t len);
+int orc_refine(const float *query, uint32_t n_q, uint32_t dim,
+               const float *centroids, uint32_t kappa, const float *table,
+               uint64_t table_len, uint32_t m, uint32_t ksub,
+               const uint64_t *doc_index, const uint8_t *payload,
+               uint64_t payload_len, const uint64_t *doc_token_offsets,
+               const float *norms, uint64_t n_tokens, uint64_t n_docs,
+               uint64_t doc_id, float *score_out);
 
 #ifdef __cplusplus
 }
