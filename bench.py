@@ -106,6 +106,101 @@ def residual_stage(device, x, ids, w, reps: int):
     }
 
 
+def storage_and_query(device, x, ids, w, cents):
+    """The .tac rows around the PQ build on the corpus workload: per-document
+    layouts of all tokens (documents of 1-100 tokens), the footer CRC-32 over
+    those layouts, one query's distance table and refine of 1,000 candidate
+    documents.  GPU call times (data resident), averaged over 5 calls."""
+    import ctypes
+    from tac_gpu import errors, lib, retrieval
+    from tac_gpu import pq as pqmod
+    from oracle import binding as orc
+
+    rng = np.random.default_rng(7)
+    lens = rng.integers(1, 101, w.n // 40)
+    off = np.concatenate([[0], np.cumsum(lens)]).astype(np.uint64)
+    off = off[off < w.n]
+    off = np.append(off, np.uint64(w.n))
+    n_docs = off.size - 1
+    codes = rng.integers(0, 256, (w.n, w.m)).astype(np.uint8)
+    total = int(orc.doc_payload_bytes(off, w.m, 1))
+    d_off = device.DeviceArray.from_host(off)
+    d_ids = device.DeviceArray.from_host(ids)
+    d_codes = device.DeviceArray.from_host(codes)
+    d_idx = device.DeviceArray((n_docs + 1,), np.uint64)
+    d_pay = device.DeviceArray((total,), np.uint8)
+
+    def timed(fn, reps=5):
+        fn()
+        device.synchronize()
+        t0 = time.perf_counter()
+        for _ in range(reps):
+            fn()
+        device.synchronize()
+        return (time.perf_counter() - t0) / reps
+
+    t_lay = timed(lambda: errors.check(lib.tac_write_doc_layouts_device(
+        d_off.ptr, n_docs, w.n, d_ids.ptr, d_codes.ptr, w.m, 1, d_idx.ptr, d_pay.ptr, total,
+        None)))
+    crc = ctypes.c_uint32(0)
+    device.profile_enable(True)
+    device.profile_read(reset=True)
+    t_crc = timed(lambda: errors.check(lib.tac_crc32_device(d_pay.ptr, total, ctypes.byref(crc),
+                                                             None)))
+    pc = device.profile_read(reset=True)
+    k_crc = pc.crc_ms / max(pc.crc_launches, 1) * 1e-3
+    # query side on the same documents: 32 query tokens, refine 1,000 candidates
+    n_q, dim = 32, w.dim
+    q = rng.standard_normal((n_q, dim)).astype(np.float32)
+    q /= np.linalg.norm(q, axis=1, keepdims=True)
+    cb = rng.standard_normal((w.m, w.ksub, w.dsub)).astype(np.float32) * 0.05
+    p = pqmod.PQ(dim=dim, sub_dim=w.dsub, codebooks=cb.reshape(-1), m=w.m, ksub=w.ksub)
+    d_q = device.DeviceArray.from_host(q)
+    d_cb = device.DeviceArray.from_host(cb)
+    d_tab = device.DeviceArray((w.m * w.ksub * n_q,), np.float32)
+    t_tab = timed(lambda: errors.check(lib.tac_pq_distance_table_device(
+        d_q.ptr, n_q, dim, w.m, w.ksub, d_cb.ptr, d_tab.ptr, w.m * w.ksub * n_q, None)))
+    norms = (1.0 + rng.random(w.n)).astype(np.float32)
+    d_cent = device.DeviceArray.from_host(cents)
+    d_norms = device.DeviceArray.from_host(norms)
+    view = retrieval._DocIndexC(dim, cents.shape[0], w.m, w.ksub, n_docs, w.n, total, d_cent.ptr,
+                                d_idx.ptr, d_pay.ptr, d_off.ptr, d_norms.ptr)
+    cand = rng.choice(n_docs, 1000, replace=False).astype(np.uint32)
+    d_cand = device.DeviceArray.from_host(cand)
+    d_scores = device.DeviceArray((1000,), np.float32)
+    device.profile_read(reset=True)
+    t_ref = timed(lambda: errors.check(lib.tac_refine_device(
+        ctypes.byref(view), d_tab.ptr, w.m * w.ksub * n_q, d_q.ptr, n_q, d_cand.ptr, 1000,
+        d_scores.ptr, None)))
+    pr = device.profile_read(reset=True)
+    k_ref = pr.refine_ms / max(pr.refine_launches, 1) * 1e-3
+    device.profile_enable(False)
+    cand_tokens = int(sum(int(off[c + 1] - off[c]) for c in cand))
+    # CPU reference for refine on the same candidates (oracle, one thread)
+    tab = d_tab.to_host()
+    idx_h, pay_h = d_idx.to_host(), d_pay.to_host()
+    t0 = time.perf_counter()
+    for c in cand[:100]:
+        orc.refine(q, n_q, dim, cents, tab, w.m, w.ksub, idx_h, pay_h, off, norms, int(c))
+    t_ref_cpu = (time.perf_counter() - t0) * 10
+    lay_bytes = w.n * (4 + w.m) + 16 * n_docs + total  # ids + codes + offsets in, layouts out
+    return {
+        "doc_layouts": {"tokens": w.n, "docs": n_docs, "payload_bytes": total,
+                        "ms": round(t_lay * 1e3, 4),
+                        "hbm_gbs": round(lay_bytes / t_lay / 1e9, 1)},
+        "crc32": {"bytes": total, "call_ms": round(t_crc * 1e3, 4),
+                  "kernel_ms": round(k_crc * 1e3, 4),
+                  "kernel_gbs": round(total / k_crc / 1e9, 1),
+                  "hbm_frac": round(total / k_crc / 1e9 / PEAK_HBM_GBS, 4)},
+        "distance_table": {"n_q": n_q, "m": w.m, "ksub": w.ksub, "us": round(t_tab * 1e6, 1)},
+        "refine": {"n_q": n_q, "candidates": 1000, "candidate_tokens": cand_tokens,
+                   "call_ms": round(t_ref * 1e3, 4), "kernel_ms": round(k_ref * 1e3, 4),
+                   "candidates_per_s": round(1000 / k_ref),
+                   "cpu_oracle_ms_1thread": round(t_ref_cpu * 1e3, 1)},
+        "note": "call times include launch, status readback and host synchronisation",
+    }
+
+
 def main() -> int:
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -183,6 +278,8 @@ def main() -> int:
     residual = residual_stage(device, x, ids, w, 5)
     device.profile_enable(False)
     log(f"residual stage: {residual['avg_call_ms']} ms per call")
+    sq = storage_and_query(device, x, ids, w, synth.centers(w.seed, w.n_centers, w.dim))
+    log(f"storage/query rows: {sq}")
 
     # Roofline of the dominant kernel (Lloyd assignment, VALU fp32): algorithmic
     # FLOP per launch = n * 2 * dim * ksub (one launch = one iteration, all m).
@@ -264,6 +361,7 @@ def main() -> int:
                         or None),
         },
         "residual_stage": residual,
+        "storage_query": sq,
         "cpu_baseline": None if cpu is None else {
             "value": round(cpu["train_s_per_20_iters"], 3), "unit": "s/20 iters",
             "encode_mvec_per_s": round(cpu["encode_mvec_per_s"], 3), "cores": cpu["cores"],

@@ -265,8 +265,8 @@ typedef struct tac_doc_index {
  * candidate's RefineError (n_q == 0: QueryShapeMismatch; table_len !=
  * m * ksub * n_q: TableSizeMismatch; doc id >= n_docs: DocOutOfRange; a
  * layout, token range, centroid id or code out of bounds: DocLayoutCorrupt).
- * n_q * (dim + 1) + 4 * (dim + 64) floats must fit in 64 KB (else
- * TAC_ERR_UNSUPPORTED).
+ * The query tokens (n_q * (dim + 1) floats) and per-wave staging must fit in
+ * 64 KB of LDS (about n_q * dim <= 14,000), else TAC_ERR_UNSUPPORTED.
  */
 int tac_refine(const tac_doc_index *index, const float *table, uint64_t table_len,
                const float *query_tokens, uint32_t n_q, const uint32_t *doc_ids,
@@ -286,8 +286,8 @@ typedef struct tac_gpu_profile {
   uint64_t exact_rescans; /* (vector, subspace) searches the pruned pass left to a full
                              reference scan (near ties across codeword blocks) */
   double residual_ms;    uint64_t residual_launches; /* residual + norm kernel */
-  double crc_ms;         uint64_t crc_launches;      /* CRC-32 kernels (+ 4-byte readback) */
-  double refine_ms;      uint64_t refine_launches;   /* refine kernel (+ status readback) */
+  double crc_ms;         uint64_t crc_launches;      /* CRC-32 kernels */
+  double refine_ms;      uint64_t refine_launches;   /* refine kernel */
 } tac_gpu_profile;
 int tac_gpu_profile_enable(int enable);
 int tac_gpu_profile_read(tac_gpu_profile *out, int reset);

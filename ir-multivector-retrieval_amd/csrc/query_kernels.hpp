@@ -81,15 +81,41 @@ __device__ __forceinline__ uint32_t load_u32_le(const uint8_t* p) {
   return (uint32_t)p[0] | (uint32_t)p[1] << 8 | (uint32_t)p[2] << 16 | (uint32_t)p[3] << 24;
 }
 
-// One wave per candidate document (grid-stride over candidates).  Lane i
-// owns query token i (groups of 64 when n_q > 64): for every doc token k
-//   cent  = dot(q_i, centroid[c_k])            (centroid row staged in LDS)
+// One wave per candidate document (grid-stride over candidates).  The wave
+// covers QP = n_q rounded up to a power of two (at most 64) query tokens and
+// S = 64 / QP document tokens at a time: lane (s, i) takes query token i0 + i
+// against document token k0 + s, for every k
+//   cent  = dot(q_i, centroid[c_k])            (centroid rows staged in LDS)
 //   res   = sum over m of table[m][code_km][i]  (in m order, from 0)
-//   score = cent + norm_k * res;  best_i = max over k (strict >, from -inf)
-// and lane 0 folds best_0 + best_1 + ... in i order (0 for an empty doc).
-// Layout checks follow refine.zig:51-65,107-114; a failing candidate writes
-// its status and score 0, and `first_bad` keeps the lowest such index.
+//   score = cent + norm_k * res
+// and keeps the first k of its running maximum (strict >, from -inf).  The S
+// slots of a query token then merge (larger value; on equal values the
+// earlier k, which keeps the sign of a zero maximum the reference would
+// keep), and lane 0 folds best_0 + best_1 + ... in i order (0 for an empty
+// document).  Layout checks follow refine.zig:51-65,107-114; a failing
+// candidate writes its status and score 0, and `first_bad` keeps the lowest
+// such index.
 constexpr int kRefineWaves = 4;
+constexpr uint32_t kRefineRowFloats = 640;  // per-wave LDS for centroid rows
+
+__host__ __device__ inline uint32_t refine_qp(uint32_t n_q) {
+  uint32_t qp = 1;
+  while (qp < n_q && qp < 64) qp <<= 1;
+  return qp;
+}
+
+__host__ __device__ inline uint32_t refine_slots(uint32_t n_q, uint32_t dim) {
+  uint32_t s = 64 / refine_qp(n_q);
+  while (s > 1 && s * (dim + 1) > kRefineRowFloats) s >>= 1;
+  return s;
+}
+
+// Per-block dynamic LDS floats: queries [n_q][dim + 1], then per wave the
+// centroid rows [S][dim + 1], 64 best values and 64 best token indices.
+__host__ __device__ inline uint32_t refine_lds_floats(uint32_t n_q, uint32_t dim) {
+  const uint32_t S = refine_slots(n_q, dim);
+  return n_q * (dim + 1) + kRefineWaves * (S * (dim + 1) + 128);
+}
 
 __global__ __launch_bounds__(64 * kRefineWaves) void refine_kernel(
     RefineIndex ix, const float* __restrict__ q, uint32_t n_q, const float* __restrict__ table,
@@ -97,12 +123,15 @@ __global__ __launch_bounds__(64 * kRefineWaves) void refine_kernel(
     uint32_t* __restrict__ status, uint32_t* __restrict__ first_bad) {
   extern __shared__ __attribute__((aligned(16))) float lds[];
   const uint32_t w = threadIdx.x / 64, lane = threadIdx.x % 64;
-  const uint32_t ldq = ix.dim + 1;  // odd stride: lanes read distinct banks
-  float* qs = lds;                                          // [n_q][dim + 1]
-  float* crow = lds + (size_t)n_q * ldq + (size_t)w * (ix.dim + 64);  // [dim] per wave
-  float* best = crow + ix.dim;                              // [64] per wave
+  const uint32_t ld = ix.dim + 1;  // odd stride: distinct rows hit distinct banks
+  const uint32_t QP = refine_qp(n_q), S = refine_slots(n_q, ix.dim);
+  const uint32_t slot = lane / QP, qi = lane % QP;
+  float* qs = lds;                                                  // [n_q][dim + 1]
+  float* crow = lds + (size_t)n_q * ld + (size_t)w * (S * ld + 128);  // [S][dim + 1]
+  float* bestv = crow + (size_t)S * ld;                             // [64]
+  uint32_t* bestk = reinterpret_cast<uint32_t*>(bestv + 64);        // [64]
   for (uint32_t f = threadIdx.x; f < n_q * ix.dim; f += blockDim.x)
-    qs[(f / ix.dim) * ldq + f % ix.dim] = q[f];
+    qs[(f / ix.dim) * ld + f % ix.dim] = q[f];
   __syncthreads();
   const uint32_t cb = ix.K <= 256 ? 1u : 2u;
   const uint32_t stride = gridDim.x * kRefineWaves;
@@ -127,26 +156,37 @@ __global__ __launch_bounds__(64 * kRefineWaves) void refine_kernel(
           st = kRefineLayoutCorrupt;
       }
     }
+    const uint8_t* lay = ix.payload + lo;
     float total = 0.0f;
-    for (uint32_t i0 = 0; st == kRefineOk && i0 < n_q; i0 += 64) {
-      const uint32_t i = i0 + lane;
+    for (uint32_t i0 = 0; st == kRefineOk && i0 < n_q; i0 += QP) {
+      const uint32_t i = i0 + qi;
       float b = -__builtin_inff();
-      const uint8_t* lay = ix.payload + lo;
-      for (uint32_t k = 0; k < n_d; ++k) {
-        const uint32_t cid = load_u32_le(lay + 4 + 4ull * k);
-        if (cid >= ix.kappa) {
+      uint32_t bk = 0xFFFFFFFFu;
+      for (uint32_t k0 = 0; k0 < n_d; k0 += S) {
+        // centroid rows of tokens k0 .. k0 + S - 1
+        bool bad_id = false;
+        for (uint32_t f = lane; f < S * ix.dim; f += 64) {
+          const uint32_t s = f / ix.dim, d = f % ix.dim;
+          if (k0 + s < n_d) {
+            const uint32_t cid = load_u32_le(lay + 4 + 4ull * (k0 + s));
+            if (cid >= ix.kappa)
+              bad_id = true;
+            else
+              crow[s * ld + d] = ix.centroids[(uint64_t)cid * ix.dim + d];
+          }
+        }
+        if (__any(bad_id)) {
           st = kRefineLayoutCorrupt;
           break;
         }
-        const float* cg = ix.centroids + (uint64_t)cid * ix.dim;
-        for (uint32_t d = lane; d < ix.dim; d += 64) crow[d] = cg[d];
         __builtin_amdgcn_wave_barrier();
         __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
-        const uint8_t* codes = lay + 4 + 4ull * n_d + (uint64_t)k * ix.M * cb;
-        float res = 0.0f;
+        const uint32_t k = k0 + slot;
         bool bad = false;
-        if (i < n_q) {
-          const float cent = ref_dot(qs + (size_t)i * ldq, crow, ix.dim);
+        if (slot < S && i < n_q && k < n_d) {  // S may be below 64 / QP
+          const float cent = ref_dot(qs + (size_t)i * ld, crow + (size_t)slot * ld, ix.dim);
+          const uint8_t* codes = lay + 4 + 4ull * n_d + (uint64_t)k * ix.M * cb;
+          float res = 0.0f;
           for (uint32_t mm = 0; mm < ix.M; ++mm) {
             const uint32_t code =
                 cb == 1 ? codes[mm] : (uint32_t)codes[2 * mm] | (uint32_t)codes[2 * mm + 1] << 8;
@@ -158,7 +198,10 @@ __global__ __launch_bounds__(64 * kRefineWaves) void refine_kernel(
           }
           const float scaled = ix.norms[t_lo + k] * res;
           const float score = cent + scaled;
-          if (score > b) b = score;
+          if (!bad && score > b) {
+            b = score;
+            bk = k;
+          }
         }
         __builtin_amdgcn_wave_barrier();
         if (__any(bad)) {
@@ -167,12 +210,25 @@ __global__ __launch_bounds__(64 * kRefineWaves) void refine_kernel(
         }
       }
       if (st != kRefineOk) break;
-      best[lane] = b;
+      bestv[lane] = b;
+      bestk[lane] = bk;
       __builtin_amdgcn_wave_barrier();
       __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
       if (lane == 0 && n_d > 0) {
-        const uint32_t cnt = n_q - i0 < 64 ? n_q - i0 : 64;
-        for (uint32_t j = 0; j < cnt; ++j) total = total + best[j];
+        const uint32_t cnt = n_q - i0 < QP ? n_q - i0 : QP;
+        for (uint32_t j = 0; j < cnt; ++j) {
+          float v = bestv[j];
+          uint32_t vk = bestk[j];
+          for (uint32_t s = 1; s < S; ++s) {
+            const float o = bestv[s * QP + j];
+            const uint32_t ok = bestk[s * QP + j];
+            if (o > v || (o == v && ok < vk)) {
+              v = o;
+              vk = ok;
+            }
+          }
+          total = total + v;
+        }
       }
       __builtin_amdgcn_wave_barrier();
     }

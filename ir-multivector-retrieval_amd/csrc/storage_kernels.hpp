@@ -275,19 +275,19 @@ __global__ __launch_bounds__(256) void doc_write_kernel(
 // so zero-seeded CRCs of consecutive pieces combine left to right by one
 // modular multiplication each.  The buffer splits into an unaligned head
 // (< 16 bytes), a body of whole kCrcLeaf-byte leaves and a tail
-// (< kCrcLeaf bytes).  Every body leaf gets a thread, the 256 leaves of a
-// block combine in an LDS tree, the block results combine in one block, and
-// one thread adds head, tail and the all-ones preset.
+// (< kCrcLeaf bytes).  A thread owns one leaf and runs kCrcWays interleaved
+// slicing-by-8 chains over its consecutive sub-leaves (independent LDS
+// lookups in flight), joins them, the 256 leaves of a block combine in an
+// LDS tree, one block combines the block results, and one thread adds head,
+// tail and the all-ones preset.
 // ---------------------------------------------------------------------------
 constexpr uint32_t kCrcPoly = 0xEDB88320u;
-constexpr uint32_t kCrcLeaf = 1024;      // bytes per leaf (power of two)
-constexpr uint32_t kCrcLeafLog2 = 10;
+constexpr uint32_t kCrcLeaf = 256;       // bytes per thread (power of two)
+constexpr uint32_t kCrcLeafLog2 = 8;
+constexpr uint32_t kCrcWays = 4;         // interleaved chains per thread
+constexpr uint32_t kCrcSub = kCrcLeaf / kCrcWays;  // 64 bytes per chain
+constexpr uint32_t kCrcSubLog2 = 6;
 constexpr int kCrcBlock = 256;
-
-// x^(8 * 2^j) mod P for j = 0..63, reflected.
-struct CrcPowers {
-  uint32_t x8[64];
-};
 
 __host__ __device__ inline uint32_t crc_mulmod(uint32_t a, uint32_t b) {
   uint32_t p = 0;
@@ -298,26 +298,54 @@ __host__ __device__ inline uint32_t crc_mulmod(uint32_t a, uint32_t b) {
   return p;
 }
 
-// r * x^(8 * count * 2^shift) mod P from the table of powers.
-__host__ __device__ inline uint32_t crc_shift(uint32_t r, uint64_t count, uint32_t shift,
-                                              const CrcPowers& pw) {
-  for (uint32_t j = 0; count; ++j, count >>= 1)
-    if (count & 1u) r = crc_mulmod(pw.x8[j + shift], r);
+// Multiplication tables for the shifts: tx[j][i] = x^(8 * 2^j) * x^i mod P
+// (j = 0..63, i = 0..31), so r * x^(8 * 2^j) is the XOR of tx[j][i] over the
+// coefficients i that r holds: 32 independent selects instead of a 32-step
+// serial chain.
+constexpr uint32_t kCrcTxRows = 64;
+
+inline void crc_tx_host(uint32_t* tx) {  // [kCrcTxRows][32]
+  uint32_t t = 0x40000000u;  // x^1
+  for (int j = 0; j < 3; ++j) t = crc_mulmod(t, t);  // x^8
+  for (uint32_t j = 0; j < kCrcTxRows; ++j) {
+    uint32_t v = t;  // x^(8 * 2^j) * x^0
+    for (int i = 0; i < 32; ++i) {
+      tx[j * 32 + i] = v;
+      v = (v & 1u) ? (v >> 1) ^ kCrcPoly : v >> 1;  // times x
+    }
+    t = crc_mulmod(t, t);
+  }
+}
+
+// Branch-free: every row entry is loaded (eight 16-byte LDS reads) and
+// masked by its coefficient bit.
+__device__ __forceinline__ uint32_t crc_mul_row(uint32_t r, const uint32_t* row) {
+  const uint4* row4 = reinterpret_cast<const uint4*>(row);
+  uint32_t p0 = 0, p1 = 0;
+#pragma unroll
+  for (int q = 0; q < 8; ++q) {
+    const uint4 v = row4[q];
+    const int i = 4 * q;
+    p0 ^= v.x & (0u - ((r >> (31 - i)) & 1u));
+    p1 ^= v.y & (0u - ((r >> (30 - i)) & 1u));
+    p0 ^= v.z & (0u - ((r >> (29 - i)) & 1u));
+    p1 ^= v.w & (0u - ((r >> (28 - i)) & 1u));
+  }
+  return p0 ^ p1;
+}
+
+// r * x^(8 * count * 2^shift) mod P with tx rows in LDS (one row per set bit).
+__device__ __forceinline__ uint32_t crc_shift_tx(uint32_t r, uint64_t count, uint32_t shift,
+                                                 const uint32_t* tx) {
+  while (count) {
+    const uint32_t j = (uint32_t)__builtin_ctzll(count);
+    r = crc_mul_row(r, tx + (j + shift) * 32);
+    count &= count - 1;
+  }
   return r;
 }
 
-inline CrcPowers crc_powers_host() {
-  CrcPowers pw;
-  uint32_t t = 0x40000000u;  // x^1
-  for (int j = 0; j < 3; ++j) t = crc_mulmod(t, t);  // x^8
-  for (int j = 0; j < 64; ++j) {
-    pw.x8[j] = t;
-    t = crc_mulmod(t, t);
-  }
-  return pw;
-}
-
-// Slicing-by-4 tables in LDS: T[k][i] = CRC contribution of byte value i
+// Slicing-by-8 tables in LDS: T[k][i] = CRC contribution of byte value i
 // followed by k zero bytes, from a zero register.
 __device__ inline void crc_tables(uint32_t (*T)[256]) {
   for (uint32_t i = threadIdx.x; i < 256; i += blockDim.x) {
@@ -326,7 +354,7 @@ __device__ inline void crc_tables(uint32_t (*T)[256]) {
     T[0][i] = r;
   }
   __syncthreads();
-  for (int k = 1; k < 4; ++k) {
+  for (int k = 1; k < 8; ++k) {
     for (uint32_t i = threadIdx.x; i < 256; i += blockDim.x) {
       const uint32_t v = T[k - 1][i];
       T[k][i] = (v >> 8) ^ T[0][v & 0xFFu];
@@ -335,9 +363,13 @@ __device__ inline void crc_tables(uint32_t (*T)[256]) {
   }
 }
 
-__device__ __forceinline__ uint32_t crc_word(uint32_t r, uint32_t w, const uint32_t (*T)[256]) {
-  r ^= w;
-  return T[3][r & 0xFFu] ^ T[2][(r >> 8) & 0xFFu] ^ T[1][(r >> 16) & 0xFFu] ^ T[0][r >> 24];
+// Eight bytes (lo = bytes 0-3, hi = bytes 4-7, little-endian): byte j needs
+// the table with 7 - j trailing zero bytes.
+__device__ __forceinline__ uint32_t crc_step8(uint32_t r, uint32_t lo, uint32_t hi,
+                                              const uint32_t (*T)[256]) {
+  r ^= lo;
+  return T[7][r & 0xFFu] ^ T[6][(r >> 8) & 0xFFu] ^ T[5][(r >> 16) & 0xFFu] ^ T[4][r >> 24] ^
+         T[3][hi & 0xFFu] ^ T[2][(hi >> 8) & 0xFFu] ^ T[1][(hi >> 16) & 0xFFu] ^ T[0][hi >> 24];
 }
 
 struct CrcNode {
@@ -345,78 +377,105 @@ struct CrcNode {
   uint32_t leaves;
 };
 
-// Leaves of the 16-byte aligned body; one CrcNode per block.
+__device__ __forceinline__ CrcNode crc_join(CrcNode a, CrcNode b, const uint32_t* tx) {
+  if (!b.leaves) return a;
+  return CrcNode{crc_shift_tx(a.crc, b.leaves, kCrcLeafLog2, tx) ^ b.crc, a.leaves + b.leaves};
+}
+
+// Combines the block's 256 nodes in order (one per thread, `mine`): a
+// shuffle tree inside each wave, then one thread joins the four wave results.
+// Every thread returns the block's combination.
+__device__ inline CrcNode crc_block_combine(CrcNode mine, CrcNode* wave_res, const uint32_t* tx) {
+  const uint32_t lane = threadIdx.x % 64, w = threadIdx.x / 64;
+  for (uint32_t span = 1; span < 64; span <<= 1) {
+    const CrcNode other{__shfl_down(mine.crc, span, 64), __shfl_down(mine.leaves, span, 64)};
+    if (lane % (2 * span) == 0 && lane + span < 64) mine = crc_join(mine, other, tx);
+  }
+  if (lane == 0) wave_res[w] = mine;
+  __syncthreads();
+  if (threadIdx.x == 0) {
+    CrcNode acc = wave_res[0];
+    for (uint32_t q = 1; q < kCrcBlock / 64; ++q) acc = crc_join(acc, wave_res[q], tx);
+    wave_res[0] = acc;
+  }
+  __syncthreads();
+  const CrcNode out = wave_res[0];
+  __syncthreads();
+  return out;
+}
+
+// Leaves of the 16-byte aligned body: every block reduces its 256 leaves to
+// one CrcNode.  g_tx is the [64][32] shift table in global memory.
 __global__ __launch_bounds__(kCrcBlock) void crc_leaf_kernel(const uint8_t* __restrict__ body,
-                                                             uint64_t n_leaves, CrcPowers pw,
-                                                             CrcNode* __restrict__ out) {
-  __shared__ uint32_t T[4][256];
-  __shared__ CrcNode node[kCrcBlock];
-  crc_tables(T);
+                                                             uint64_t n_leaves,
+                                                             const uint32_t* __restrict__ g_tx,
+                                                             CrcNode* __restrict__ nodes) {
+  __shared__ uint32_t T[8][256];
+  __shared__ __attribute__((aligned(16))) uint32_t tx[kCrcTxRows * 32];
+  __shared__ CrcNode node[kCrcBlock / 64];
+  for (uint32_t f = threadIdx.x; f < kCrcTxRows * 32; f += kCrcBlock) tx[f] = g_tx[f];
+  crc_tables(T);  // synchronises
   const uint64_t leaf = (uint64_t)blockIdx.x * kCrcBlock + threadIdx.x;
   uint32_t r = 0;
   uint32_t have = 0;
   if (leaf < n_leaves) {
     const uint4* p = reinterpret_cast<const uint4*>(body + leaf * kCrcLeaf);
-#pragma unroll 4
-    for (uint32_t q = 0; q < kCrcLeaf / 16; ++q) {
-      const uint4 v = p[q];
-      r = crc_word(r, v.x, T);
-      r = crc_word(r, v.y, T);
-      r = crc_word(r, v.z, T);
-      r = crc_word(r, v.w, T);
-    }
+    uint4 v[kCrcWays][kCrcSub / 16];
+#pragma unroll
+    for (uint32_t w = 0; w < kCrcWays; ++w)
+#pragma unroll
+      for (uint32_t q = 0; q < kCrcSub / 16; ++q) v[w][q] = p[w * (kCrcSub / 16) + q];
+    uint32_t rw[kCrcWays];
+#pragma unroll
+    for (uint32_t w = 0; w < kCrcWays; ++w) rw[w] = 0;
+#pragma unroll
+    for (uint32_t q = 0; q < kCrcSub / 16; ++q)
+#pragma unroll
+      for (uint32_t w = 0; w < kCrcWays; ++w) {
+        rw[w] = crc_step8(rw[w], v[w][q].x, v[w][q].y, T);
+        rw[w] = crc_step8(rw[w], v[w][q].z, v[w][q].w, T);
+      }
+    r = rw[0];
+#pragma unroll
+    for (uint32_t w = 1; w < kCrcWays; ++w) r = crc_mul_row(r, tx + kCrcSubLog2 * 32) ^ rw[w];
     have = 1;
   }
-  node[threadIdx.x] = CrcNode{r, have};
-  __syncthreads();
-  for (uint32_t span = 1; span < kCrcBlock; span <<= 1) {
-    if (threadIdx.x % (2 * span) == 0) {
-      const CrcNode a = node[threadIdx.x], b = node[threadIdx.x + span];
-      if (b.leaves)
-        node[threadIdx.x] =
-            CrcNode{crc_shift(a.crc, b.leaves, kCrcLeafLog2, pw) ^ b.crc, a.leaves + b.leaves};
-    }
-    __syncthreads();
-  }
-  if (threadIdx.x == 0) out[blockIdx.x] = node[0];
+  const CrcNode blk = crc_block_combine(CrcNode{r, have}, node, tx);
+  if (threadIdx.x == 0) nodes[blockIdx.x] = blk;
 }
 
-// One block: folds the per-block nodes, then head, body and tail.
+// One block: folds the block nodes in order, then head, body and tail.
 __global__ __launch_bounds__(kCrcBlock) void crc_final_kernel(
-    const uint8_t* __restrict__ buf, uint64_t head, uint64_t body_leaves, uint64_t tail,
-    const CrcNode* __restrict__ nodes, uint32_t n_nodes, CrcPowers pw,
+    const uint8_t* __restrict__ buf, uint64_t head, uint64_t n_leaves, uint64_t tail,
+    const CrcNode* __restrict__ nodes, uint32_t n_nodes, const uint32_t* __restrict__ g_tx,
     uint32_t* __restrict__ crc_out) {
-  __shared__ uint32_t T[4][256];
-  __shared__ CrcNode node[kCrcBlock];
-  __shared__ CrcNode acc;
-  crc_tables(T);
-  if (threadIdx.x == 0) acc = CrcNode{0, 0};
-  __syncthreads();
+  __shared__ uint32_t T[8][256];
+  __shared__ __attribute__((aligned(16))) uint32_t tx[kCrcTxRows * 32];
+  __shared__ CrcNode node[kCrcBlock / 64];
+  for (uint32_t f = threadIdx.x; f < kCrcTxRows * 32; f += kCrcBlock) tx[f] = g_tx[f];
+  crc_tables(T);  // synchronises
+  CrcNode acc{0, 0};
   for (uint32_t b0 = 0; b0 < n_nodes; b0 += kCrcBlock) {
     const uint32_t b = b0 + threadIdx.x;
-    node[threadIdx.x] = b < n_nodes ? nodes[b] : CrcNode{0, 0};
-    __syncthreads();
-    for (uint32_t span = 1; span < kCrcBlock; span <<= 1) {
-      if (threadIdx.x % (2 * span) == 0) {
-        const CrcNode a = node[threadIdx.x], c = node[threadIdx.x + span];
-        if (c.leaves)
-          node[threadIdx.x] =
-              CrcNode{crc_shift(a.crc, c.leaves, kCrcLeafLog2, pw) ^ c.crc, a.leaves + c.leaves};
-      }
-      __syncthreads();
-    }
-    if (threadIdx.x == 0 && node[0].leaves)
-      acc = CrcNode{crc_shift(acc.crc, node[0].leaves, kCrcLeafLog2, pw) ^ node[0].crc,
-                    acc.leaves + node[0].leaves};
-    __syncthreads();
+    const CrcNode part = crc_block_combine(b < n_nodes ? nodes[b] : CrcNode{0, 0}, node, tx);
+    acc = crc_join(acc, part, tx);
   }
   if (threadIdx.x != 0) return;
-  uint32_t r = 0xFFFFFFFFu;
-  for (uint64_t i = 0; i < head; ++i) r = T[0][(r ^ buf[i]) & 0xFFu] ^ (r >> 8);
-  r = crc_shift(r, body_leaves, kCrcLeafLog2, pw) ^ acc.crc;
-  const uint8_t* t = buf + head + body_leaves * kCrcLeaf;
-  for (uint64_t i = 0; i < tail; ++i) r = T[0][(r ^ t[i]) & 0xFFu] ^ (r >> 8);
-  *crc_out = r ^ 0xFFFFFFFFu;
+  uint32_t rr = 0xFFFFFFFFu;
+  for (uint64_t i = 0; i < head; ++i) rr = T[0][(rr ^ buf[i]) & 0xFFu] ^ (rr >> 8);
+  rr = crc_shift_tx(rr, n_leaves, kCrcLeafLog2, tx) ^ acc.crc;
+  // The tail starts 16-byte aligned (or at byte 0 when the head took all).
+  const uint8_t* t = buf + head + n_leaves * kCrcLeaf;
+  uint64_t i = 0;
+  if (((uintptr_t)t & 7) == 0) {
+    const uint2* t8 = reinterpret_cast<const uint2*>(t);
+    for (; i + 8 <= tail; i += 8) {
+      const uint2 v = t8[i / 8];
+      rr = crc_step8(rr, v.x, v.y, T);
+    }
+  }
+  for (; i < tail; ++i) rr = T[0][(rr ^ t[i]) & 0xFFu] ^ (rr >> 8);
+  *crc_out = rr ^ 0xFFFFFFFFu;
 }
 
 }  // namespace tacgpu

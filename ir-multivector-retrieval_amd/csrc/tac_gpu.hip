@@ -83,7 +83,8 @@ struct DeviceState {
   // training / encode workspace
   Buffer xs, codes, e, hist, counts, start, sorted, flags, scal, trace, io_in, io_out, io_cb,
       io_init, counter, kpp_state, kpp_w, kpp_bsum, kpp_bad, status, io_aux, io_out2, scan_sums,
-      io_x1, io_x2, io_x3;
+      io_x1, io_x2, io_x3, crc_tx;
+  bool crc_tx_ready = false;
   // measurement
   std::vector<hipEvent_t> events;
 };
@@ -713,10 +714,13 @@ int tac_gpu_release_workspace(void) {
   if (st) return st;
   std::lock_guard<std::mutex> g(ds->mu);
   HIP_TRY(hipDeviceSynchronize());
-  Buffer *bufs[] = {&ds->xs,   &ds->codes,  &ds->e,     &ds->hist,  &ds->counts,
-                    &ds->start, &ds->sorted, &ds->flags, &ds->scal,  &ds->trace,
-                    &ds->io_in, &ds->io_out, &ds->io_cb, &ds->io_init, &ds->counter,
-                    &ds->kpp_state, &ds->kpp_w, &ds->kpp_bsum, &ds->kpp_bad};
+  Buffer *bufs[] = {&ds->xs,        &ds->codes,   &ds->e,         &ds->hist,     &ds->counts,
+                    &ds->start,     &ds->sorted,  &ds->flags,     &ds->scal,     &ds->trace,
+                    &ds->io_in,     &ds->io_out,  &ds->io_cb,     &ds->io_init,  &ds->counter,
+                    &ds->kpp_state, &ds->kpp_w,   &ds->kpp_bsum,  &ds->kpp_bad,  &ds->status,
+                    &ds->io_aux,    &ds->io_out2, &ds->scan_sums, &ds->io_x1,    &ds->io_x2,
+                    &ds->io_x3,     &ds->crc_tx};
+  ds->crc_tx_ready = false;
   for (Buffer *b : bufs) {
     if (b->ptr) HIP_TRY(hipFree(b->ptr));
     b->ptr = nullptr;
@@ -1089,18 +1093,44 @@ int crc_core(DeviceState &ds, hipStream_t s, const uint8_t *d_buf, uint64_t len,
   if ((st = ensure(ds, ds.scan_sums, (size_t)(nb ? nb : 1) * sizeof(CrcNode) + 16))) return st;
   CrcNode *nodes = as<CrcNode>(ds.scan_sums);
   uint32_t *d_crc = reinterpret_cast<uint32_t *>(nodes + (nb ? nb : 1));
-  static const CrcPowers pw = crc_powers_host();
-  if (nb) crc_leaf_kernel<<<(unsigned)nb, kCrcBlock, 0, s>>>(d_buf + head, leaves, pw, nodes);
-  crc_final_kernel<<<1, kCrcBlock, 0, s>>>(d_buf, head, leaves, tail, nodes, (uint32_t)nb, pw,
+  if (!ds.crc_tx_ready) {  // the [64][32] shift table, uploaded once per device
+    static const std::vector<uint32_t> host_tx = [] {
+      std::vector<uint32_t> t(kCrcTxRows * 32);
+      crc_tx_host(t.data());
+      return t;
+    }();
+    if ((st = ensure(ds, ds.crc_tx, host_tx.size() * sizeof(uint32_t)))) return st;
+    HIP_TRY(hipMemcpy(ds.crc_tx.ptr, host_tx.data(), host_tx.size() * sizeof(uint32_t),
+                      hipMemcpyHostToDevice));
+    ds.crc_tx_ready = true;
+  }
+  const uint32_t *tx = as<uint32_t>(ds.crc_tx);
+  const bool profile = g_profile;
+  hipEvent_t a = nullptr, b = nullptr;
+  if (profile) {
+    if ((st = event_at(ds, 0, &a)) || (st = event_at(ds, 1, &b))) return st;
+    HIP_TRY(hipEventRecord(a, s));
+  }
+  if (nb) crc_leaf_kernel<<<(unsigned)nb, kCrcBlock, 0, s>>>(d_buf + head, leaves, tx, nodes);
+  crc_final_kernel<<<1, kCrcBlock, 0, s>>>(d_buf, head, leaves, tail, nodes, (uint32_t)nb, tx,
                                            d_crc);
   LAUNCH_TRY("crc kernels");
+  if (profile) HIP_TRY(hipEventRecord(b, s));
   HIP_TRY(hipMemcpyAsync(out, d_crc, sizeof(uint32_t), hipMemcpyDeviceToHost, s));
   HIP_TRY(hipStreamSynchronize(s));
+  if (profile) {
+    float ms = 0.0f;
+    HIP_TRY(hipEventElapsedTime(&ms, a, b));
+    std::lock_guard<std::mutex> g(g_profile_mu);
+    g_prof.crc_ms += ms;
+    g_prof.crc_launches += 1;
+  }
   return TAC_OK;
 }
 
 int refine_smem(uint32_t n_q, uint32_t dim, size_t *bytes) {
-  const uint64_t floats = (uint64_t)n_q * (dim + 1) + (uint64_t)kRefineWaves * (dim + 64);
+  if (dim > 4096 || n_q > 65536) return TAC_ERR_UNSUPPORTED;
+  const uint64_t floats = refine_lds_floats(n_q, dim);
   if (floats * sizeof(float) > 65536) return TAC_ERR_UNSUPPORTED;
   *bytes = (size_t)floats * sizeof(float);
   return TAC_OK;
@@ -1132,12 +1162,26 @@ int refine_core(DeviceState &ds, hipStream_t s, const tac_doc_index &ix, const f
                 ix.m, ix.ksub};
   const uint32_t want = (n_cand + kRefineWaves - 1) / kRefineWaves;
   const unsigned blocks = want < 8192 ? want : 8192;
+  const bool profile = g_profile;
+  hipEvent_t ea = nullptr, eb = nullptr;
+  if (profile) {
+    if ((st = event_at(ds, 0, &ea)) || (st = event_at(ds, 1, &eb))) return st;
+    HIP_TRY(hipEventRecord(ea, s));
+  }
   refine_kernel<<<blocks, 64 * kRefineWaves, smem, s>>>(r, d_q, n_q, d_table, d_ids, n_cand,
                                                        d_scores, status, first_bad);
   LAUNCH_TRY("refine_kernel");
+  if (profile) HIP_TRY(hipEventRecord(eb, s));
   uint32_t bad = 0xFFFFFFFFu;
   HIP_TRY(hipMemcpyAsync(&bad, first_bad, sizeof(bad), hipMemcpyDeviceToHost, s));
   HIP_TRY(hipStreamSynchronize(s));
+  if (profile) {
+    float ms = 0.0f;
+    HIP_TRY(hipEventElapsedTime(&ms, ea, eb));
+    std::lock_guard<std::mutex> g(g_profile_mu);
+    g_prof.refine_ms += ms;
+    g_prof.refine_launches += 1;
+  }
   if (bad != 0xFFFFFFFFu) {
     uint32_t code = 0;
     HIP_TRY(hipMemcpy(&code, status + bad, sizeof(code), hipMemcpyDeviceToHost));
@@ -1243,22 +1287,7 @@ int tac_crc32_device(const void *d_bytes, uint64_t len, uint32_t *crc_out, void 
   hipStream_t s;
   if ((st = resolve_stream(*ds, stream, &s))) return st;
   if ((st = begin_call(*ds, s))) return st;
-  const bool profile = g_profile;
-  hipEvent_t a = nullptr, b = nullptr;
-  if (profile) {
-    if ((st = event_at(*ds, 0, &a)) || (st = event_at(*ds, 1, &b))) return st;
-    HIP_TRY(hipEventRecord(a, s));
-  }
   if ((st = crc_core(*ds, s, static_cast<const uint8_t *>(d_bytes), len, crc_out))) return st;
-  if (profile) {
-    HIP_TRY(hipEventRecord(b, s));
-    HIP_TRY(hipEventSynchronize(b));
-    float ms = 0.0f;
-    HIP_TRY(hipEventElapsedTime(&ms, a, b));
-    std::lock_guard<std::mutex> gp(g_profile_mu);
-    g_prof.crc_ms += ms;
-    g_prof.crc_launches += 1;
-  }
   return end_call(*ds, s);
 }
 
@@ -1354,24 +1383,9 @@ int tac_refine_device(const tac_doc_index *d_index, const float *d_table, uint64
   hipStream_t s;
   if ((st = resolve_stream(*ds, stream, &s))) return st;
   if ((st = begin_call(*ds, s))) return st;
-  const bool profile = g_profile;
-  hipEvent_t a = nullptr, b = nullptr;
-  if (profile) {
-    if ((st = event_at(*ds, 0, &a)) || (st = event_at(*ds, 1, &b))) return st;
-    HIP_TRY(hipEventRecord(a, s));
-  }
   if ((st = refine_core(*ds, s, ix, d_table, d_query_tokens, n_q, d_doc_ids, n_candidates,
                         d_scores_out)))
     return st;
-  if (profile) {
-    HIP_TRY(hipEventRecord(b, s));
-    HIP_TRY(hipEventSynchronize(b));
-    float ms = 0.0f;
-    HIP_TRY(hipEventElapsedTime(&ms, a, b));
-    std::lock_guard<std::mutex> gp(g_profile_mu);
-    g_prof.refine_ms += ms;
-    g_prof.refine_launches += 1;
-  }
   return end_call(*ds, s);
 }
 

@@ -124,6 +124,10 @@ class KernelTimes:
     exact_rescans: int
     residual_ms: float = 0.0
     residual_launches: int = 0
+    crc_ms: float = 0.0
+    crc_launches: int = 0
+    refine_ms: float = 0.0
+    refine_launches: int = 0
 
 
 def profile_enable(on: bool = True) -> None:
@@ -135,4 +139,5 @@ def profile_read(reset: bool = True) -> KernelTimes:
     errors.check(lib.tac_gpu_profile_read(ctypes.byref(p), 1 if reset else 0))
     return KernelTimes(p.transpose_ms, p.transpose_launches, p.assign_ms, p.assign_launches,
                        p.update_ms, p.update_iters, p.encode_ms, p.encode_launches,
-                       p.exact_rescans, p.residual_ms, p.residual_launches)
+                       p.exact_rescans, p.residual_ms, p.residual_launches, p.crc_ms,
+                       p.crc_launches, p.refine_ms, p.refine_launches)

@@ -32,6 +32,13 @@ def test_crc_matches_zlib(gpu, n):
         assert _crc_device(data, mis) == want
 
 
+def test_crc_after_workspace_release(gpu):
+    data = np.random.default_rng(4).integers(0, 256, 100_003, dtype=np.uint8).tobytes()
+    assert storage.crc32(data) == zlib.crc32(data)
+    errors.check(lib.tac_gpu_release_workspace())
+    assert storage.crc32(data) == zlib.crc32(data)
+
+
 def test_crc_large_image(gpu):
     data = np.random.default_rng(1).integers(0, 256, 300 * 2**20 + 333, dtype=np.uint8)
     assert storage.crc32(data) == zlib.crc32(data.tobytes())

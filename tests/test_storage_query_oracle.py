@@ -76,15 +76,25 @@ def shift(r, count, sh, pw):
 
 @pytest.mark.parametrize("n,mis", [(0, 0), (5, 3), (5000, 0), (5000, 9), (70_000, 1)])
 def test_crc_decomposition_used_by_the_kernels(n, mis):
-    """head (to 16-byte alignment) + whole 1 KiB leaves combined pairwise by
-    x^(8 len) shifts + tail, from the all-ones preset, equals zlib's CRC."""
+    """head (to 16-byte alignment) + whole 256-byte leaves + tail, from the
+    all-ones preset, equals zlib's CRC.  Each leaf is four 64-byte chains
+    joined by x^(8*64) shifts, and leaves combine pairwise by x^(8 len)."""
     data = np.random.default_rng(n + mis).integers(0, 256, n, dtype=np.uint8).tobytes()
     pw = x8_powers()
-    L, LOG2 = 1024, 10
+    L, LOG2, SUB, SUB_LOG2 = 256, 8, 64, 6
     head = min((16 - mis) % 16, n)
     leaves = (n - head) // L
     tail = n - head - leaves * L
-    nodes = [(raw_crc(data[head + j * L: head + (j + 1) * L]), 1) for j in range(leaves)]
+
+    def leaf_crc(j):
+        base = head + j * L
+        ways = [raw_crc(data[base + w * SUB: base + (w + 1) * SUB]) for w in range(4)]
+        r = ways[0]
+        for w in range(1, 4):
+            r = mulmod(pw[SUB_LOG2], r) ^ ways[w]
+        return r
+
+    nodes = [(leaf_crc(j), 1) for j in range(leaves)]
     while len(nodes) > 1:  # pairwise tree, as the block reduction does
         nxt = []
         for k in range(0, len(nodes), 2):
@@ -99,6 +109,49 @@ def test_crc_decomposition_used_by_the_kernels(n, mis):
     r = shift(r, leaves, LOG2, pw) ^ body
     r = raw_crc(data[n - tail:], r) if tail else r
     assert r ^ 0xFFFFFFFF == zlib.crc32(data)
+
+
+def test_slicing_by_8_step():
+    """Eight bytes at once through tables T_k (byte then k zero bytes) equal
+    eight byte steps."""
+    T0 = []
+    for i in range(256):
+        r = i
+        for _ in range(8):
+            r = (r >> 1) ^ POLY if r & 1 else r >> 1
+        T0.append(r)
+    T = [T0]
+    for k in range(1, 8):
+        T.append([(v >> 8) ^ T0[v & 0xFF] for v in T[k - 1]])
+    rng = np.random.default_rng(3)
+    for _ in range(200):
+        reg = int(rng.integers(0, 2**32))
+        b = rng.integers(0, 256, 8, dtype=np.uint8).tobytes()
+        lo, hi = struct.unpack("<II", b)
+        x = reg ^ lo
+        got = (T[7][x & 0xFF] ^ T[6][(x >> 8) & 0xFF] ^ T[5][(x >> 16) & 0xFF] ^ T[4][x >> 24]
+               ^ T[3][hi & 0xFF] ^ T[2][(hi >> 8) & 0xFF] ^ T[1][(hi >> 16) & 0xFF]
+               ^ T[0][hi >> 24])
+        assert got == raw_crc(b, reg)
+
+
+def test_shift_table_rows_multiply():
+    """The kernels multiply by x^(8 * 2^j) as the XOR of table row j's
+    entries x^(8 * 2^j) * x^i over the coefficients i of the register."""
+    pw = x8_powers()
+    rng = np.random.default_rng(9)
+    for j in (0, 6, 8, 17, 40):
+        row, v = [], pw[j]
+        for _ in range(32):
+            row.append(v)
+            v = (v >> 1) ^ POLY if v & 1 else v >> 1
+        for reg in rng.integers(0, 2**32, 20):
+            reg = int(reg)
+            got = 0
+            for i in range(32):
+                if (reg >> (31 - i)) & 1:
+                    got ^= row[i]
+            assert got == mulmod(reg, pw[j])
 
 
 def test_shift_is_zero_bytes():
