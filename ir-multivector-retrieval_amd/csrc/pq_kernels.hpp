@@ -287,6 +287,23 @@ __device__ __forceinline__ void flush_rescans(uint32_t mine, uint32_t* lcount,
   if (threadIdx.x == 0 && *lcount) atomicAdd(rescans, (unsigned long long)*lcount);
 }
 
+// Exclusive scan of one value per thread over the block (all threads call).
+__device__ __forceinline__ uint32_t block_exclusive_scan(uint32_t v, uint32_t* wsum) {
+  const uint32_t lane = threadIdx.x % kWave, w = threadIdx.x / kWave;
+  uint32_t incl = v;
+#pragma unroll
+  for (int off = 1; off < kWave; off <<= 1) {
+    const uint32_t o = __shfl_up(incl, off, kWave);
+    if (lane >= (uint32_t)off) incl += o;
+  }
+  if (lane == kWave - 1) wsum[w] = incl;
+  __syncthreads();
+  uint32_t before = 0;
+  for (uint32_t q = 0; q < w; ++q) before += wsum[q];
+  __syncthreads();
+  return before + incl - v;
+}
+
 // ---------------------------------------------------------------------------
 // Lloyd assignment (src/tac/kmeans.zig:344-365).  One block = one subspace
 // and kBlock*VPT consecutive vectors; every thread owns VPT vectors.
@@ -367,29 +384,26 @@ __global__ __launch_bounds__(kBlock) void hist_kernel(
   for (uint32_t c = threadIdx.x; c < K; c += blockDim.x) out[c] = h[c];
 }
 
-// Step 2: per subspace, every code's tile counts become exclusive offsets
-// over tiles (in place); cluster sizes and bucket starts (exclusive scan
-// over codes) are written alongside.  Block = 1024 threads = K codes x P
-// contiguous tile ranges; loads are batched 8 deep.
-__global__ __launch_bounds__(1024) void scan_kernel(
-    uint32_t* __restrict__ hist, uint32_t* __restrict__ counts,
-    uint32_t* __restrict__ start, const uint32_t* __restrict__ done, uint32_t K,
-    uint32_t T) {
-  __shared__ uint32_t part_sum[1024];
-  __shared__ uint32_t cnt[1024];
-  __shared__ uint32_t wsum[16];
-  const uint32_t m = blockIdx.x;
+// Step 2: every code's tile counts become exclusive offsets over tiles (in
+// place); cluster sizes and bucket starts (exclusive scan over codes) are
+// written alongside.  The T tiles of a subspace split into G ranges:
+// scan_partial_kernel sums each range per code, scan_apply_kernel adds the
+// ranges before its own and rewrites its tiles; range 0 also writes counts
+// and starts.
+constexpr uint32_t kScanRanges = 32;
+
+__global__ __launch_bounds__(kBlock) void scan_partial_kernel(
+    const uint32_t* __restrict__ hist, uint32_t* __restrict__ part,
+    const uint32_t* __restrict__ done, uint32_t K, uint32_t T, uint32_t G) {
+  const uint32_t m = blockIdx.y, g = blockIdx.x;
   if (done[m]) return;
-  const uint32_t P = blockDim.x / K;  // tile ranges per code (K <= 1024)
-  const bool active = threadIdx.x < P * K;
-  const uint32_t c = threadIdx.x % K, p = threadIdx.x / K;
-  const uint32_t per = (T + P - 1) / P;
-  const uint32_t t0 = p * per < T ? p * per : T;
+  const uint32_t per = (T + G - 1) / G;
+  const uint32_t t0 = g * per < T ? g * per : T;
   const uint32_t t1 = t0 + per < T ? t0 + per : T;
-  uint32_t* hm = hist + (uint64_t)m * T * K;
+  const uint32_t* hm = hist + (uint64_t)m * T * K;
   constexpr uint32_t B = 8;
-  uint32_t s = 0;
-  if (active) {
+  for (uint32_t c = threadIdx.x; c < K; c += kBlock) {
+    uint32_t s = 0;
     uint32_t t = t0;
     for (; t + B <= t1; t += B) {
       uint32_t v[B];
@@ -399,74 +413,56 @@ __global__ __launch_bounds__(1024) void scan_kernel(
       for (uint32_t q = 0; q < B; ++q) s += v[q];
     }
     for (; t < t1; ++t) s += hm[(uint64_t)t * K + c];
+    part[((uint64_t)m * G + g) * K + c] = s;
   }
-  part_sum[threadIdx.x] = s;
-  __syncthreads();
-  if (active) {
-    uint32_t run = 0;
-    for (uint32_t q = 0; q < p; ++q) run += part_sum[q * K + c];
-    uint32_t t = t0;
-    for (; t + B <= t1; t += B) {
-      uint32_t v[B];
-#pragma unroll
-      for (uint32_t q = 0; q < B; ++q) v[q] = hm[(uint64_t)(t + q) * K + c];
-#pragma unroll
-      for (uint32_t q = 0; q < B; ++q) {
-        hm[(uint64_t)(t + q) * K + c] = run;
-        run += v[q];
-      }
+}
+
+__global__ __launch_bounds__(kBlock) void scan_apply_kernel(
+    uint32_t* __restrict__ hist, const uint32_t* __restrict__ part,
+    uint32_t* __restrict__ counts, uint32_t* __restrict__ start,
+    const uint32_t* __restrict__ done, uint32_t K, uint32_t T, uint32_t G) {
+  __shared__ uint32_t wsum[kBlock / kWave];
+  const uint32_t m = blockIdx.y, g = blockIdx.x;
+  if (done[m]) return;
+  const uint32_t per = (T + G - 1) / G;
+  const uint32_t t0 = g * per < T ? g * per : T;
+  const uint32_t t1 = t0 + per < T ? t0 + per : T;
+  uint32_t* hm = hist + (uint64_t)m * T * K;
+  const uint32_t* pm = part + (uint64_t)m * G * K;
+  const uint32_t per_c = (K + kBlock - 1) / kBlock;  // <= 4 codes per thread
+  const uint32_t c0 = threadIdx.x * per_c;
+  uint32_t tot[4] = {0, 0, 0, 0}, before[4] = {0, 0, 0, 0};
+  uint32_t local = 0;
+  for (uint32_t q = 0; q < per_c; ++q) {
+    const uint32_t c = c0 + q;
+    if (c >= K) break;
+    for (uint32_t gg = 0; gg < G; ++gg) {
+      const uint32_t v = pm[(uint64_t)gg * K + c];
+      if (gg < g) before[q] += v;
+      tot[q] += v;
     }
-    for (; t < t1; ++t) {
+    local += tot[q];
+  }
+  uint32_t st = block_exclusive_scan(local, wsum);
+  for (uint32_t q = 0; q < per_c; ++q) {
+    const uint32_t c = c0 + q;
+    if (c >= K) break;
+    if (g == 0) {
+      start[(uint64_t)m * K + c] = st;
+      counts[(uint64_t)m * K + c] = tot[q];
+    }
+    st += tot[q];
+    uint32_t run = before[q];
+    for (uint32_t t = t0; t < t1; ++t) {
       const uint32_t v = hm[(uint64_t)t * K + c];
       hm[(uint64_t)t * K + c] = run;
       run += v;
     }
-    if (p == P - 1) cnt[c] = run;
-  }
-  __syncthreads();
-  // exclusive scan of cnt[0..K) with the whole block
-  const uint32_t per_c = (K + blockDim.x - 1) / blockDim.x;
-  const uint32_t c0 = threadIdx.x * per_c;
-  uint32_t local = 0;
-  for (uint32_t q = 0; q < per_c; ++q)
-    if (c0 + q < K) local += cnt[c0 + q];
-  const uint32_t lane = threadIdx.x % kWave, w = threadIdx.x / kWave;
-  uint32_t incl = local;
-#pragma unroll
-  for (int off = 1; off < kWave; off <<= 1) {
-    const uint32_t o = __shfl_up(incl, off, kWave);
-    if (lane >= (uint32_t)off) incl += o;
-  }
-  if (lane == kWave - 1) wsum[w] = incl;
-  __syncthreads();
-  uint32_t before = 0;
-  for (uint32_t q = 0; q < w; ++q) before += wsum[q];
-  uint32_t acc = before + incl - local;
-  for (uint32_t q = 0; q < per_c; ++q) {
-    if (c0 + q < K) {
-      start[(uint64_t)m * K + c0 + q] = acc;
-      counts[(uint64_t)m * K + c0 + q] = cnt[c0 + q];
-      acc += cnt[c0 + q];
-    }
   }
 }
 
+
 // Block-wide exclusive scan of one value per thread (blockDim.x <= 1024).
-__device__ __forceinline__ uint32_t block_exclusive_scan(uint32_t v, uint32_t* wsum) {
-  const uint32_t lane = threadIdx.x % kWave, w = threadIdx.x / kWave;
-  uint32_t incl = v;
-#pragma unroll
-  for (int off = 1; off < kWave; off <<= 1) {
-    const uint32_t o = __shfl_up(incl, off, kWave);
-    if (lane >= (uint32_t)off) incl += o;
-  }
-  if (lane == kWave - 1) wsum[w] = incl;
-  __syncthreads();
-  uint32_t before = 0;
-  for (uint32_t q = 0; q < w; ++q) before += wsum[q];
-  __syncthreads();
-  return before + incl - v;
-}
 
 // Workgroups are dispatched round-robin over the 8 XCDs; hand each XCD a
 // contiguous range of logical tiles so neighbouring tiles (which write
@@ -505,10 +501,40 @@ __global__ __launch_bounds__(kBlock) void scatter_kernel(
   const uint64_t lo = tile_lo + (uint64_t)w * kQuarter;
   const uint64_t hi = lo + kQuarter < tile_hi ? lo + kQuarter : tile_hi;
   const uint16_t* cm = codes + (uint64_t)m * n;
+  const float* xm = xs + (uint64_t)m * n * DP;
+
+  // The wave's kRounds rounds of codes and records are loaded up front, so
+  // all of them are in flight while the counters and the scan run; the codes
+  // serve both the counting and the ranking pass.
+  constexpr uint32_t kRounds = kQuarter / kWave;
+  uint32_t code[kRounds];
+  float xv[kRounds][DP];
+#pragma unroll
+  for (uint32_t r = 0; r < kRounds; ++r) {
+    const uint64_t i = lo + (uint64_t)r * kWave + lane;
+    code[r] = i < hi ? cm[i] : 0u;
+    if (i < hi) {
+      const float* src = xm + i * DP;
+#pragma unroll
+      for (int k = 0; k < DP; k += (DP >= 4 ? 4 : DP)) {
+        if constexpr (DP >= 4) {
+          const float4 a = *reinterpret_cast<const float4*>(src + k);
+          xv[r][k] = a.x; xv[r][k + 1] = a.y; xv[r][k + 2] = a.z; xv[r][k + 3] = a.w;
+        } else if constexpr (DP == 2) {
+          const float2 a = *reinterpret_cast<const float2*>(src);
+          xv[r][0] = a.x; xv[r][1] = a.y;
+        } else {
+          xv[r][0] = src[0];
+        }
+      }
+    }
+  }
 
   for (uint32_t c = threadIdx.x; c < 4 * K; c += blockDim.x) run[c] = 0;
   __syncthreads();
-  for (uint64_t i = lo + lane; i < hi; i += kWave) atomicAdd(&run[w * K + cm[i]], 1u);
+#pragma unroll
+  for (uint32_t r = 0; r < kRounds; ++r)
+    if (lo + (uint64_t)r * kWave + lane < hi) atomicAdd(&run[w * K + code[r]], 1u);
   __syncthreads();
 
   // Per code: tile-local bucket start (scan over codes), wave prefixes, and
@@ -536,38 +562,37 @@ __global__ __launch_bounds__(kBlock) void scatter_kernel(
   __syncthreads();
 
   const uint64_t lt_mask = (lane == 0) ? 0ull : (~0ull >> (64 - lane));
-  const float* xm = xs + (uint64_t)m * n * DP;
   uint32_t* myrun = run + w * K;
-  for (uint64_t r = lo; r < hi; r += kWave) {
-    const uint64_t i = r + lane;
-    const bool valid = i < hi;
-    const uint32_t code = valid ? cm[i] : 0u;
+#pragma unroll
+  for (uint32_t r = 0; r < kRounds; ++r) {
+    const bool valid = lo + (uint64_t)r * kWave + lane < hi;
+    const uint32_t cd = code[r];
     uint64_t match = __ballot(valid);
     for (uint32_t b = 0; b < code_bits; ++b) {
-      const bool bit = (code >> b) & 1u;
+      const bool bit = (cd >> b) & 1u;
       const uint64_t bal = __ballot(bit);
       match &= bit ? bal : ~bal;
     }
     const uint32_t rank = __popcll(match & lt_mask);
     const uint32_t total = __popcll(match);
     uint32_t lp = 0;
-    if (valid) lp = myrun[code] + rank;
+    if (valid) lp = myrun[cd] + rank;
     __builtin_amdgcn_wave_barrier();
-    if (valid && rank == total - 1) myrun[code] = lp + 1;
+    if (valid && rank == total - 1) myrun[cd] = lp + 1;
     __builtin_amdgcn_wave_barrier();
     if (valid) {
-      const float* src = xm + i * DP;
       float* dst = sx + lp * DP;
 #pragma unroll
       for (int k = 0; k < DP; k += (DP >= 4 ? 4 : DP)) {
         if constexpr (DP >= 4)
-          *reinterpret_cast<float4*>(dst + k) = *reinterpret_cast<const float4*>(src + k);
+          *reinterpret_cast<float4*>(dst + k) =
+              make_float4(xv[r][k], xv[r][k + 1], xv[r][k + 2], xv[r][k + 3]);
         else if constexpr (DP == 2)
-          *reinterpret_cast<float2*>(dst) = *reinterpret_cast<const float2*>(src);
+          *reinterpret_cast<float2*>(dst) = make_float2(xv[r][0], xv[r][1]);
         else
-          dst[0] = src[0];
+          dst[0] = xv[r][0];
       }
-      gdest[lp] = lp + delta[code];
+      gdest[lp] = lp + delta[cd];
     }
   }
   __syncthreads();
@@ -591,9 +616,10 @@ __global__ __launch_bounds__(kBlock) void scatter_kernel(
 
 // Step 4: one wave per (subspace, cluster).  The wave streams the cluster's
 // contiguous records with coalesced loads (kFoldBatch x 64 records in
-// flight, staged through LDS) and lanes 0..D-1 fold dimension d in
-// ascending vector order from 0.0f, then write sum * fl(1 / fl(count))
-// (src/tac/kmeans.zig:177-198).  Empty clusters are left for reseed_kernel.
+// flight, staged through LDS dimension-major) and lanes 0..D-1 fold
+// dimension d in ascending vector order from 0.0f, then write
+// sum * fl(1 / fl(count)) (src/tac/kmeans.zig:177-198).  Empty clusters are
+// left for reseed_kernel.
 template <int D>
 __global__ __launch_bounds__(kWave) void fold_kernel(
     const float* __restrict__ sorted, const uint32_t* __restrict__ counts,
@@ -601,7 +627,8 @@ __global__ __launch_bounds__(kWave) void fold_kernel(
     const uint32_t* __restrict__ done, uint64_t n, uint32_t K) {
   constexpr int DP = Pad<D>::value;
   constexpr uint32_t U = kFoldBatch;
-  __shared__ float buf[U * kWave * DP];
+  constexpr uint32_t kCol = U * kWave + 4;  // padded: the D columns start on distinct banks
+  __shared__ __attribute__((aligned(16))) float buf[kCol * DP];
   const uint32_t m = blockIdx.x / K, c = blockIdx.x % K;
   if (done[m]) return;
   const uint32_t cnt = counts[(uint64_t)m * K + c];
@@ -630,19 +657,31 @@ __global__ __launch_bounds__(kWave) void fold_kernel(
       }
     }
   };
+  // buf is dimension-major, [DP][kCol]: lane d reads four consecutive
+  // members of its dimension with one 16-byte LDS read.
   float acc = 0.0f;
   load_batch(0);
   for (uint32_t j0 = 0; j0 < cnt; j0 += U * kWave) {
 #pragma unroll
     for (uint32_t u = 0; u < U; ++u)
 #pragma unroll
-      for (int k = 0; k < DP; ++k) buf[(u * kWave + lane) * DP + k] = v[u][k];
+      for (int k = 0; k < DP; ++k) buf[k * kCol + u * kWave + lane] = v[u][k];
     __syncthreads();
     if (j0 + U * kWave < cnt) load_batch(j0 + U * kWave);
     const uint32_t len = cnt - j0 < U * kWave ? cnt - j0 : U * kWave;
     if (lane < (uint32_t)D) {
-#pragma unroll 8
-      for (uint32_t jj = 0; jj < len; ++jj) acc = acc + buf[jj * DP + lane];
+      const float* col = buf + lane * kCol;
+      const float4* col4 = reinterpret_cast<const float4*>(col);
+      uint32_t jj = 0;
+#pragma unroll 4
+      for (; jj + 4 <= len; jj += 4) {
+        const float4 e = col4[jj / 4];
+        acc = acc + e.x;
+        acc = acc + e.y;
+        acc = acc + e.z;
+        acc = acc + e.w;
+      }
+      for (; jj < len; ++jj) acc = acc + col[jj];
     }
     __syncthreads();
   }
@@ -692,10 +731,17 @@ __global__ __launch_bounds__(1024) void reseed_kernel(
   const uint32_t* cm = counts + (uint64_t)m * K;
   const uint32_t lane = threadIdx.x % kWave, w = threadIdx.x / kWave;
   const uint32_t nw = blockDim.x / kWave;
+  // Empty clusters, listed in ascending order (K <= blockDim.x).
+  __shared__ uint32_t elist[1024];
+  __shared__ uint32_t ewsum[1024 / kWave];
+  const bool empty = threadIdx.x < K && cm[threadIdx.x] == 0;
+  const uint32_t pos = block_exclusive_scan(empty ? 1u : 0u, ewsum);
+  if (empty) elist[pos] = threadIdx.x;
   uint32_t found = 0;
-  for (uint32_t c = 0; c < K; ++c) {
-    if (cm[c] != 0) continue;  // uniform across the block
-    ++found;
+  for (uint32_t q = 0; q < nw; ++q) found += ewsum[q];  // wave totals: the count
+  __syncthreads();
+  for (uint32_t q = 0; q < found; ++q) {
+    const uint32_t c = elist[q];  // uniform across the block
     float bv = -__builtin_inff();
     uint64_t bi = ~0ull;
     for (uint64_t i = threadIdx.x; i < n; i += blockDim.x) {

@@ -432,6 +432,8 @@ int train_core(DeviceState &ds, hipStream_t s, const float *d_x, uint64_t n, uin
   if ((st = ensure(ds, ds.hist, (size_t)M * T * K * sizeof(uint32_t)))) return st;
   if ((st = ensure(ds, ds.counts, (size_t)M * K * sizeof(uint32_t)))) return st;
   if ((st = ensure(ds, ds.start, (size_t)M * K * sizeof(uint32_t)))) return st;
+  const uint32_t G = T < kScanRanges ? T : kScanRanges;
+  if ((st = ensure(ds, ds.scan_sums, (size_t)M * G * K * sizeof(uint32_t)))) return st;
   if ((st = ensure(ds, ds.sorted, (size_t)M * n * DP * sizeof(float)))) return st;
   if ((st = ensure(ds, ds.flags, (size_t)3 * M * sizeof(uint32_t)))) return st;
   if ((st = ensure(ds, ds.scal, (size_t)2 * M * sizeof(float)))) return st;
@@ -444,6 +446,7 @@ int train_core(DeviceState &ds, hipStream_t s, const float *d_x, uint64_t n, uin
   uint32_t *hist = as<uint32_t>(ds.hist);
   uint32_t *counts = as<uint32_t>(ds.counts);
   uint32_t *start = as<uint32_t>(ds.start);
+  uint32_t *scan_part = as<uint32_t>(ds.scan_sums);
   float *sorted = as<float>(ds.sorted);
   uint32_t *done = as<uint32_t>(ds.flags);
   uint32_t *iters_run = done + M;
@@ -490,8 +493,10 @@ int train_core(DeviceState &ds, hipStream_t s, const float *d_x, uint64_t n, uin
     if (profile) HIP_TRY(hipEventRecord(b, s));
     hist_kernel<<<dim3(T, M), kBlock, hist_lds, s>>>(codes, hist, done, n, K, T);
     LAUNCH_TRY("hist_kernel");
-    scan_kernel<<<M, 1024, 0, s>>>(hist, counts, start, done, K, T);
-    LAUNCH_TRY("scan_kernel");
+    scan_partial_kernel<<<dim3(G, M), kBlock, 0, s>>>(hist, scan_part, done, K, T, G);
+    scan_apply_kernel<<<dim3(G, M), kBlock, 0, s>>>(hist, scan_part, counts, start, done, K, T,
+                                                     G);
+    LAUNCH_TRY("scan kernels");
     DISPATCH_D_ST(D, scatter(xs, codes, hist, start, sorted, done, n, M, K, T, s));
     if (st) return st;
     LAUNCH_TRY("scatter_kernel");
