@@ -275,6 +275,18 @@ def main() -> int:
     total = time.perf_counter() - t_all
     prof = device.profile_read(reset=True)
     device.profile_enable(False)
+    # The drop-in call's defaults (src/index/pq.zig:319-325): k-means++ seeding,
+    # tol 1e-4, at most 25 iterations; the convergence test needs the serial
+    # wcss fold of every iteration.
+    device.synchronize()
+    t0 = time.perf_counter()
+    it_run, _, _ = device.train_device(dx, n, dim, m, ksub, None, dcb, 25, 1e-4, stats=True,
+                                       seed=0xa1b2c3d4)
+    device.synchronize()
+    drop_in = {"init": "k-means++ (GPU)", "tol": 1e-4, "max_iters": 25,
+               "iters_run_min": int(it_run.min()), "iters_run_max": int(it_run.max()),
+               "train_s": round(time.perf_counter() - t0, 5)}
+    log(f"drop-in defaults: {drop_in}")
     residual = residual_stage(device, x, ids, w, 5)
     device.profile_enable(False)
     log(f"residual stage: {residual['avg_call_ms']} ms per call")
@@ -360,6 +372,7 @@ def main() -> int:
                                                           "reseed_kernel", "converge_kernel"))
                         or None),
         },
+        "drop_in_defaults": drop_in,
         "residual_stage": residual,
         "storage_query": sq,
         "cpu_baseline": None if cpu is None else {

@@ -8,10 +8,12 @@
 #include <stdint.h>
 #include <string.h>
 
+#ifndef TAC_HD
 #if defined(__HIPCC__)
 #define TAC_HD __host__ __device__
 #else
 #define TAC_HD
+#endif
 #endif
 
 namespace tacgpu {

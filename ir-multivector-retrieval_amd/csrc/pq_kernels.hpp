@@ -25,6 +25,8 @@
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
+#include "fold_rules.hpp"
+
 namespace tacgpu {
 
 constexpr int kBlock = 256;        // threads per block for the streaming kernels
@@ -378,7 +380,18 @@ __global__ __launch_bounds__(kBlock) void hist_kernel(
   const uint64_t lo = (uint64_t)t * kSortTile;
   const uint64_t hi = lo + kSortTile < n ? lo + kSortTile : n;
   const uint16_t* cm = codes + (uint64_t)m * n;
-  for (uint64_t i = lo + threadIdx.x; i < hi; i += blockDim.x) atomicAdd(&h[cm[i]], 1u);
+  if (hi - lo == (uint64_t)kBlock * 8 && ((uintptr_t)(cm + lo) & 15) == 0) {
+    // a full, 16-byte aligned tile: eight codes per thread in one load
+    const uint4 v = reinterpret_cast<const uint4*>(cm + lo)[threadIdx.x];
+    const uint32_t w[4] = {v.x, v.y, v.z, v.w};
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+      atomicAdd(&h[w[q] & 0xFFFFu], 1u);
+      atomicAdd(&h[w[q] >> 16], 1u);
+    }
+  } else {
+    for (uint64_t i = lo + threadIdx.x; i < hi; i += blockDim.x) atomicAdd(&h[cm[i]], 1u);
+  }
   __syncthreads();
   uint32_t* out = hist + ((uint64_t)m * T + t) * K;
   for (uint32_t c = threadIdx.x; c < K; c += blockDim.x) out[c] = h[c];
@@ -690,26 +703,151 @@ __global__ __launch_bounds__(kWave) void fold_kernel(
 
 // ---------------------------------------------------------------------------
 // wcss = sequential fp32 fold of e over ascending vector index
-// (src/tac/kmeans.zig:179).  One wave per subspace: the wave stages 1024
-// values through LDS with coalesced loads, lane 0 folds them in order.
+// (src/tac/kmeans.zig:179), evaluated exactly in chunks of kFoldChunk terms
+// (fold_rules.hpp): f64 chunk sums -> prefix -> per-chunk quantized sums for
+// three candidate binades -> one wave per subspace applies the chunks in
+// order, folding term by term any chunk the rules do not cover.
 // ---------------------------------------------------------------------------
-__global__ __launch_bounds__(kWave) void wcss_kernel(
-    const float* __restrict__ e, float* __restrict__ wcss, const uint32_t* __restrict__ done,
-    uint64_t n) {
-  __shared__ float buf[1024];
-  const uint32_t m = blockIdx.x;
+__device__ __forceinline__ double wave_sum_f64(double v) {
+  for (int off = kWave / 2; off > 0; off >>= 1) v += __shfl_down(v, off, kWave);
+  return v;
+}
+__device__ __forceinline__ uint64_t wave_sum_u64(uint64_t v) {
+  for (int off = kWave / 2; off > 0; off >>= 1) v += __shfl_down(v, off, kWave);
+  return v;
+}
+
+// Chunk sums in f64 (any order: they only place the candidate binades).
+__global__ __launch_bounds__(kBlock) void wcss_chunk_sums_kernel(
+    const float* __restrict__ e, double* __restrict__ csum, const uint32_t* __restrict__ done,
+    uint64_t n, uint32_t nc) {
+  __shared__ double ws[kBlock / kWave];
+  const uint32_t m = blockIdx.y, j = blockIdx.x;
   if (done[m]) return;
   const float* em = e + (uint64_t)m * n;
-  float s = 0.0f;
-  for (uint64_t b = 0; b < n; b += 1024) {
-    const uint64_t len = n - b < 1024 ? n - b : 1024;
-    for (uint32_t q = threadIdx.x; q < len; q += kWave) buf[q] = em[b + q];
+  const uint64_t lo = (uint64_t)j * kFoldChunk;
+  double acc = 0.0;
+  for (uint32_t q = threadIdx.x; q < kFoldChunk; q += kBlock)
+    if (lo + q < n) acc += (double)em[lo + q];
+  acc = wave_sum_f64(acc);
+  if (threadIdx.x % kWave == 0) ws[threadIdx.x / kWave] = acc;
+  __syncthreads();
+  if (threadIdx.x == 0) csum[(uint64_t)m * nc + j] = (ws[0] + ws[1]) + (ws[2] + ws[3]);
+}
+
+// Exclusive prefix of the chunk sums (in place), one block per subspace.
+__global__ __launch_bounds__(kBlock) void wcss_prefix_kernel(double* __restrict__ csum,
+                                                             const uint32_t* __restrict__ done,
+                                                             uint32_t nc) {
+  __shared__ double ws[kBlock / kWave];
+  __shared__ double carry;
+  const uint32_t m = blockIdx.x;
+  if (done[m]) return;
+  double* cm = csum + (uint64_t)m * nc;
+  const uint32_t lane = threadIdx.x % kWave, w = threadIdx.x / kWave;
+  if (threadIdx.x == 0) carry = 0.0;
+  __syncthreads();
+  for (uint32_t j0 = 0; j0 < nc; j0 += kBlock) {
+    const uint32_t j = j0 + threadIdx.x;
+    const double x = j < nc ? cm[j] : 0.0;
+    double incl = x;
+    for (int off = 1; off < kWave; off <<= 1) {
+      const double o = __shfl_up(incl, off, kWave);
+      if (lane >= (uint32_t)off) incl += o;
+    }
+    if (lane == kWave - 1) ws[w] = incl;
     __syncthreads();
-    if (threadIdx.x == 0)
-      for (uint32_t q = 0; q < len; ++q) s = s + buf[q];
+    double before = carry;
+    for (uint32_t q = 0; q < w; ++q) before += ws[q];
+    if (j < nc) cm[j] = before + incl - x;
+    __syncthreads();
+    if (threadIdx.x == kBlock - 1) carry = before + incl;
     __syncthreads();
   }
-  if (threadIdx.x == 0) wcss[m] = s;
+}
+
+// Quantized sums of chunk j for the binades around its approximate start.
+__global__ __launch_bounds__(kBlock) void wcss_quantize_kernel(
+    const float* __restrict__ e, const double* __restrict__ pre, FoldChunk* __restrict__ chunks,
+    const uint32_t* __restrict__ done, uint64_t n, uint32_t nc) {
+  static_assert(kBlock / kWave == 4, "the block combines below assume four waves");
+  __shared__ uint64_t ws[kFoldCands][kBlock / kWave];
+  __shared__ uint32_t wbad[kBlock / kWave];
+  const uint32_t m = blockIdx.y, j = blockIdx.x;
+  if (done[m]) return;
+  const float ps = (float)pre[(uint64_t)m * nc + j];
+  const int32_t k0 = fold_is_normal_positive(ps) ? fold_exponent(ps) - 1 : -1000;
+  const float* em = e + (uint64_t)m * n;
+  const uint64_t lo = (uint64_t)j * kFoldChunk;
+  uint64_t q[kFoldCands] = {0, 0, 0};
+  uint32_t bad = 0;  // bit c: candidate c spoiled by one of this thread's terms
+  for (uint32_t t = threadIdx.x; t < kFoldChunk; t += kBlock) {
+    if (lo + t >= n) break;
+    const float v = em[lo + t];
+#pragma unroll
+    for (int c = 0; c < kFoldCands; ++c) {
+      const uint64_t qi = fold_quantize(v, k0 + c);
+      bad |= qi == kFoldBad ? 1u << c : 0u;
+      q[c] += qi == kFoldBad ? 0u : qi;
+    }
+  }
+  // spoiled candidates, OR-reduced over the block
+  for (int off = kWave / 2; off > 0; off >>= 1) bad |= __shfl_xor(bad, off, kWave);
+#pragma unroll
+  for (int c = 0; c < kFoldCands; ++c) {
+    const uint64_t sw = wave_sum_u64(q[c]);
+    if (threadIdx.x % kWave == 0) ws[c][threadIdx.x / kWave] = sw;
+  }
+  if (threadIdx.x % kWave == 0) wbad[threadIdx.x / kWave] = bad;
+  __syncthreads();
+  if (threadIdx.x == 0) {
+    FoldChunk ch;
+    ch.k0 = k0;
+    ch.clean = ~((wbad[0] | wbad[1]) | (wbad[2] | wbad[3])) & ((1u << kFoldCands) - 1u);
+#pragma unroll
+    for (int c = 0; c < kFoldCands; ++c) ch.q[c] = (ws[c][0] + ws[c][1]) + (ws[c][2] + ws[c][3]);
+    chunks[(uint64_t)m * nc + j] = ch;
+  }
+}
+
+// One wave per subspace: lane 0 applies the chunks in order (descriptors
+// staged through LDS 64 at a time); a chunk the rules do not cover is staged
+// through LDS and folded term by term.
+__global__ __launch_bounds__(kWave) void wcss_apply_kernel(
+    const float* __restrict__ e, const FoldChunk* __restrict__ chunks, float* __restrict__ wcss,
+    const uint32_t* __restrict__ done, uint64_t n, uint32_t nc) {
+  __shared__ FoldChunk lch[kWave];
+  __shared__ __attribute__((aligned(16))) float buf[kFoldChunk];
+  __shared__ uint32_t need;
+  const uint32_t m = blockIdx.x, lane = threadIdx.x;
+  if (done[m]) return;
+  const float* em = e + (uint64_t)m * n;
+  const FoldChunk* cm = chunks + (uint64_t)m * nc;
+  float s = 0.0f;  // lane 0's accumulator
+  for (uint32_t j0 = 0; j0 < nc; j0 += kWave) {
+    if (j0 + lane < nc) lch[lane] = cm[j0 + lane];
+    __syncthreads();
+    const uint32_t cnt = nc - j0 < kWave ? nc - j0 : kWave;
+    for (uint32_t q = 0; q < cnt; ++q) {
+      if (lane == 0) {
+        float out;
+        need = fold_apply(s, lch[q], &out) ? 0u : 1u;
+        if (!need) s = out;
+      }
+      __syncthreads();
+      if (need) {
+        const uint64_t lo = (uint64_t)(j0 + q) * kFoldChunk;
+        const uint32_t len = n - lo < kFoldChunk ? (uint32_t)(n - lo) : kFoldChunk;
+        for (uint32_t t = lane; t < len; t += kWave) buf[t] = em[lo + t];
+        __syncthreads();
+        if (lane == 0)
+          for (uint32_t t = 0; t < len; ++t) s = s + buf[t];
+        __syncthreads();
+      }
+    }
+    __syncthreads();
+  }
+  if (lane == 0) wcss[m] = s;
 }
 
 // ---------------------------------------------------------------------------

@@ -83,7 +83,7 @@ struct DeviceState {
   // training / encode workspace
   Buffer xs, codes, e, hist, counts, start, sorted, flags, scal, trace, io_in, io_out, io_cb,
       io_init, counter, kpp_state, kpp_w, kpp_bsum, kpp_bad, status, io_aux, io_out2, scan_sums,
-      io_x1, io_x2, io_x3, crc_tx;
+      io_x1, io_x2, io_x3, crc_tx, fold_pre, fold_chunks;
   bool crc_tx_ready = false;
   // measurement
   std::vector<hipEvent_t> events;
@@ -433,6 +433,9 @@ int train_core(DeviceState &ds, hipStream_t s, const float *d_x, uint64_t n, uin
   if ((st = ensure(ds, ds.counts, (size_t)M * K * sizeof(uint32_t)))) return st;
   if ((st = ensure(ds, ds.start, (size_t)M * K * sizeof(uint32_t)))) return st;
   const uint32_t G = T < kScanRanges ? T : kScanRanges;
+  const uint32_t nfc = (uint32_t)((n + kFoldChunk - 1) / kFoldChunk);  // wcss chunks
+  if ((st = ensure(ds, ds.fold_pre, (size_t)M * nfc * sizeof(double)))) return st;
+  if ((st = ensure(ds, ds.fold_chunks, (size_t)M * nfc * sizeof(FoldChunk)))) return st;
   if ((st = ensure(ds, ds.scan_sums, (size_t)M * G * K * sizeof(uint32_t)))) return st;
   if ((st = ensure(ds, ds.sorted, (size_t)M * n * DP * sizeof(float)))) return st;
   if ((st = ensure(ds, ds.flags, (size_t)3 * M * sizeof(uint32_t)))) return st;
@@ -447,6 +450,8 @@ int train_core(DeviceState &ds, hipStream_t s, const float *d_x, uint64_t n, uin
   uint32_t *counts = as<uint32_t>(ds.counts);
   uint32_t *start = as<uint32_t>(ds.start);
   uint32_t *scan_part = as<uint32_t>(ds.scan_sums);
+  double *fold_pre = as<double>(ds.fold_pre);
+  FoldChunk *fold_chunks = as<FoldChunk>(ds.fold_chunks);
   float *sorted = as<float>(ds.sorted);
   uint32_t *done = as<uint32_t>(ds.flags);
   uint32_t *iters_run = done + M;
@@ -503,8 +508,12 @@ int train_core(DeviceState &ds, hipStream_t s, const float *d_x, uint64_t n, uin
     DISPATCH_D(D, fold(sorted, counts, start, out.cb, done, n, M, K, s));
     LAUNCH_TRY("fold_kernel");
     if (check || (want_wcss && t + 1 == max_iters)) {
-      wcss_kernel<<<M, kWave, 0, s>>>(e, wcss, done, n);
-      LAUNCH_TRY("wcss_kernel");
+      wcss_chunk_sums_kernel<<<dim3(nfc, M), kBlock, 0, s>>>(e, fold_pre, done, n, nfc);
+      wcss_prefix_kernel<<<M, kBlock, 0, s>>>(fold_pre, done, nfc);
+      wcss_quantize_kernel<<<dim3(nfc, M), kBlock, 0, s>>>(e, fold_pre, fold_chunks, done, n,
+                                                            nfc);
+      wcss_apply_kernel<<<M, kWave, 0, s>>>(e, fold_chunks, wcss, done, n, nfc);
+      LAUNCH_TRY("wcss kernels");
     }
     DISPATCH_D(D, reseed(xs, e, counts, out.cb, empties, done, n, M, K, s));
     LAUNCH_TRY("reseed_kernel");
@@ -724,7 +733,7 @@ int tac_gpu_release_workspace(void) {
                     &ds->io_in,     &ds->io_out,  &ds->io_cb,     &ds->io_init,  &ds->counter,
                     &ds->kpp_state, &ds->kpp_w,   &ds->kpp_bsum,  &ds->kpp_bad,  &ds->status,
                     &ds->io_aux,    &ds->io_out2, &ds->scan_sums, &ds->io_x1,    &ds->io_x2,
-                    &ds->io_x3,     &ds->crc_tx};
+                    &ds->io_x3,     &ds->crc_tx,  &ds->fold_pre,  &ds->fold_chunks};
   ds->crc_tx_ready = false;
   for (Buffer *b : bufs) {
     if (b->ptr) HIP_TRY(hipFree(b->ptr));

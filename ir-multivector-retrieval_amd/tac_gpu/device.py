@@ -83,9 +83,11 @@ class DeviceArray:
             pass
 
 
-def train_device(x: DeviceArray, n: int, dim: int, m: int, ksub: int, init: DeviceArray,
-                 out: DeviceArray, max_iters: int, tol: float, stats: bool = False):
-    """tac_pq_train_device on resident buffers; optional per-subspace stats."""
+def train_device(x: DeviceArray, n: int, dim: int, m: int, ksub: int, init: DeviceArray | None,
+                 out: DeviceArray, max_iters: int, tol: float, stats: bool = False,
+                 seed: int = 0):
+    """tac_pq_train_device on resident buffers; optional per-subspace stats.
+    init None seeds every subspace with k-means++ (seed +% subspace)."""
     ex = None
     arrays = None
     if stats:
@@ -93,8 +95,10 @@ def train_device(x: DeviceArray, n: int, dim: int, m: int, ksub: int, init: Devi
         ex = TrainExtras(arrays[0].ctypes.data_as(ctypes.POINTER(ctypes.c_uint32)),
                          arrays[1].ctypes.data_as(ctypes.POINTER(ctypes.c_float)),
                          arrays[2].ctypes.data_as(ctypes.POINTER(ctypes.c_uint32)), None)
-    errors.check(lib.tac_pq_train_device(x.ptr, n, dim, m, ksub, init.ptr, 0, max_iters, tol,
-                                         out.ptr, ctypes.byref(ex) if ex else None, None))
+    errors.check(lib.tac_pq_train_device(x.ptr, n, dim, m, ksub,
+                                         init.ptr if init is not None else None,
+                                         seed & (2**64 - 1), max_iters, tol, out.ptr,
+                                         ctypes.byref(ex) if ex else None, None))
     return arrays
 
 

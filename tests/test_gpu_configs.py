@@ -58,9 +58,25 @@ def test_subspace_shape_sweep_full_corpus(gpu, corpus, name):
     _log(f"{name}: GPU {t1 - t0:.2f} s, oracle {time.perf_counter() - t1:.1f} s")
     assert ref.status == 0
     assert np.array_equal(_bits(got.codebooks), _bits(ref.codebooks))
+    assert np.array_equal(_bits(got.stats.wcss), _bits(ref.wcss))
     sample = x[::30][:50000]
     assert np.array_equal(got.encode_many(sample),
                           orc.pq_encode(sample, w.dim, w.m, w.ksub, ref.codebooks, n_threads=16))
+
+
+def test_convergence_and_wcss_full_corpus(gpu, corpus):
+    """The reference's defaults at full size: tol 1e-4 needs the serial fp32
+    wcss of every iteration (evaluated in chunks on the GPU); iterations run,
+    wcss and codebooks equal the oracle's bit for bit."""
+    w = synth.WORKLOADS["corpus-1.52m"]
+    x = corpus
+    init = synth.shuffle_init(x, w.m, w.ksub, w.seed)
+    got = pq.train(x, w.dim, 0, m=w.m, ksub=w.ksub, max_iters=6, tol=1e-4, init_codebooks=init)
+    ref = orc.pq_train(x, w.dim, w.m, w.ksub, init=init, max_iters=6, tol=1e-4, n_threads=16)
+    assert ref.status == 0
+    assert np.array_equal(got.stats.iters_run, ref.iters_run)
+    assert np.array_equal(_bits(got.stats.wcss), _bits(ref.wcss))
+    assert np.array_equal(_bits(got.codebooks), _bits(ref.codebooks))
 
 
 @pytest.mark.timeout(300)
