@@ -1,9 +1,12 @@
-// fold_rules.hpp — exact chunked evaluation of a serial fp32 sum of
-// non-negative terms, s_{i+1} = fl(s_i + e_i) from s_0 = 0 (the wcss fold of
-// src/tac/kmeans.zig:179).  Shared by the GPU kernels and a CPU check.
+// fold_rules.hpp — exact chunked evaluation of a serial sum of non-negative
+// float terms, s_{i+1} = fl(s_i + e_i) from s_0 = 0, with an fp32
+// accumulator (the wcss fold of src/tac/kmeans.zig:179) or an f64 one (the
+// weight folds of weightedSample, src/util/rng.zig:60-81).  Shared by the GPU
+// kernels and a CPU check.
 //
-// While the accumulator s lies in one binade [2^k, 2^(k+1)), the floats there
-// are exactly the multiples of U = 2^(k-23), so
+// Let the accumulator type carry F fraction bits (23 for fp32, 52 for f64).
+// While the accumulator s lies in one binade [2^k, 2^(k+1)), the values
+// there are exactly the multiples of U = 2^(k-F), so
 //   fl(s + e) = s + U * round(e / U)
 // whenever e / U is not exactly halfway between two integers (the tie would
 // be broken by the parity of s) and the exact sum stays below 2^(k+1) - U/2.
@@ -32,6 +35,7 @@ namespace tacgpu {
 
 constexpr uint32_t kFoldChunk = 1024;  // terms per chunk
 constexpr int kFoldCands = 3;          // candidate binades per chunk
+constexpr uint64_t kFoldBad = ~0ull;   // fold_quantize: the term spoils the binade
 
 struct FoldChunk {
   int32_t k0;          // candidate binade exponents k0, k0 + 1, k0 + 2
@@ -39,44 +43,76 @@ struct FoldChunk {
   uint64_t q[kFoldCands];
 };
 
-TAC_HD inline int32_t fold_exponent(float s) {  // k with 2^k <= s < 2^(k+1), s normal > 0
+template <typename Acc>
+struct FoldTraits;
+template <>
+struct FoldTraits<float> {
+  using Bits = uint32_t;
+  static constexpr int kFrac = 23, kExpBits = 8, kBias = 127;
+};
+template <>
+struct FoldTraits<double> {
+  using Bits = uint64_t;
+  static constexpr int kFrac = 52, kExpBits = 11, kBias = 1023;
+};
+
+template <typename Acc>
+TAC_HD inline typename FoldTraits<Acc>::Bits fold_bits(Acc s) {
   union {
-    float f;
-    uint32_t u;
+    Acc f;
+    typename FoldTraits<Acc>::Bits u;
   } v;
   v.f = s;
-  return (int32_t)((v.u >> 23) & 0xFFu) - 127;
+  return v.u;
 }
 
-TAC_HD inline bool fold_is_normal_positive(float s) {
+template <typename Acc>
+TAC_HD inline Acc fold_from_bits(typename FoldTraits<Acc>::Bits u) {
   union {
-    float f;
-    uint32_t u;
+    Acc f;
+    typename FoldTraits<Acc>::Bits u;
   } v;
-  v.f = s;
-  const uint32_t ex = (v.u >> 23) & 0xFFu;
-  return (v.u >> 31) == 0 && ex != 0 && ex != 0xFFu;
+  v.u = u;
+  return v.f;
 }
 
-constexpr uint64_t kFoldBad = ~0ull;  // fold_quantize: the term spoils the binade
+// k with 2^k <= s < 2^(k+1), for a normal s > 0.
+template <typename Acc>
+TAC_HD inline int32_t fold_exponent(Acc s) {
+  using T = FoldTraits<Acc>;
+  const uint32_t ex = (uint32_t)(fold_bits(s) >> T::kFrac) & ((1u << T::kExpBits) - 1u);
+  return (int32_t)ex - T::kBias;
+}
 
-// round(e / 2^(k-23)) for one term and one binade k, or kFoldBad when the
-// term spoils the chunk for that binade (k outside [-126, 127], e not finite,
-// negative, a tie, or so large that it alone would leave the binade).
-// Written without early returns: callers OR the failure into a mask and add
-// the value branch-free (a short-circuit `if (ok && quantize(&q)) ... else
-// ok = 0` form was compiled for gfx950 such that a failing term left `ok`
-// set).
+template <typename Acc>
+TAC_HD inline bool fold_is_normal_positive(Acc s) {
+  using T = FoldTraits<Acc>;
+  const auto u = fold_bits(s);
+  const uint32_t ex = (uint32_t)(u >> T::kFrac) & ((1u << T::kExpBits) - 1u);
+  return (u >> (T::kFrac + T::kExpBits)) == 0 && ex != 0 && ex != (1u << T::kExpBits) - 1u;
+}
+
+// round(e / 2^(k-F)) for one float term and one binade k of the accumulator,
+// or kFoldBad when the term spoils the chunk for that binade (k outside the
+// normal range, e not finite, negative, a tie, or so large that it alone
+// would leave the binade).  Written without early returns: callers OR the
+// failure into a mask and add the value branch-free (a short-circuit
+// `if (ok && quantize(&q)) ... else ok = 0` form was compiled for gfx950
+// such that a failing term left `ok` set).
+template <typename Acc>
 TAC_HD inline uint64_t fold_quantize(float e, int32_t k) {
-  const bool k_ok = k >= -126 && k <= 127;
+  using T = FoldTraits<Acc>;
+  constexpr int32_t kMin = 1 - T::kBias, kMax = T::kBias;
+  const bool k_ok = k >= kMin && k <= kMax;
   const bool e_ok = e >= 0.0f && e <= 3.402823466e38f;  // excludes NaN, negative, inf
-  // e / U exactly, in double: e has 24 significant bits and U is a power of
-  // two, and e * 2^(23-k) stays within double's normal range for every
-  // float e and every k in [-126, 127].
-  const double t = ldexp(e_ok ? (double)e : 0.0, k_ok ? 23 - k : 0);
-  const bool small = t < 16777216.0;  // < 2^24 units: cannot leave the binade alone
+  // e / U in double.  e has 24 significant bits and U is a power of two, so
+  // the scaling is exact unless it overflows (then t = inf: a term far
+  // beyond the binade) or underflows (then e / U < 2^-1022, which rounds to
+  // 0 and is no tie, and t rounds to a value below 0.5 as well).
+  const double t = ldexp(e_ok ? (double)e : 0.0, k_ok ? T::kFrac - k : 0);
+  const bool small = t < (double)(1ull << (T::kFrac + 1));  // cannot leave the binade alone
   const double fl = floor(small ? t : 0.0);
-  const double frac = t - fl;
+  const double frac = t - fl;  // exact: t < 2^53
   const bool tie = frac == 0.5;  // would depend on the parity of s
   const uint64_t q = (uint64_t)fl + (frac > 0.5 ? 1u : 0u);
   return (k_ok && e_ok && small && !tie) ? q : kFoldBad;
@@ -84,22 +120,20 @@ TAC_HD inline uint64_t fold_quantize(float e, int32_t k) {
 
 // Applies a chunk with quantized sums: true (and *out) when the chunk adds
 // exactly U * Q without leaving the accumulator's binade.
-TAC_HD inline bool fold_apply(float s, const FoldChunk& ch, float* out) {
+template <typename Acc>
+TAC_HD inline bool fold_apply(Acc s, const FoldChunk& ch, Acc* out) {
+  using T = FoldTraits<Acc>;
+  using Bits = typename T::Bits;
   if (!fold_is_normal_positive(s)) return false;
-  const int32_t k = fold_exponent(s);
-  const int32_t c = k - ch.k0;
+  const int32_t c = fold_exponent(s) - ch.k0;
   if (c < 0 || c >= kFoldCands || !((ch.clean >> c) & 1u)) return false;
   const uint64_t Q = ch.q[c];
-  // units of U: s = m * U with 2^23 <= m < 2^24; the binade ends at 2^24 U
-  union {
-    float f;
-    uint32_t u;
-  } v;
-  v.f = s;
-  const uint64_t m = (uint64_t)((v.u & 0x7FFFFFu) | 0x800000u);
-  if (Q > (1ull << 24) || m + Q > (1ull << 24) - 1) return false;
-  v.u = (v.u & 0xFF800000u) | (uint32_t)((m + Q) & 0x7FFFFFu);
-  *out = v.f;
+  // units of U: s = m * U with 2^F <= m < 2^(F+1); the binade ends at 2^(F+1) U
+  constexpr uint64_t kOne = 1ull << T::kFrac;
+  const Bits u = fold_bits(s);
+  const uint64_t m = (uint64_t)(u & (Bits)(kOne - 1)) | kOne;
+  if (Q > 2 * kOne || m + Q > 2 * kOne - 1) return false;
+  *out = fold_from_bits<Acc>((Bits)((u & ~(Bits)(kOne - 1)) | (Bits)((m + Q) & (kOne - 1))));
   return true;
 }
 

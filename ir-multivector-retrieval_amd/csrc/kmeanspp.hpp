@@ -81,10 +81,11 @@ __global__ __launch_bounds__(256) void kpp_update_kernel(
 
 // Round c draw: one block per subspace.  Checks the weights, draws u, finds
 // the candidate with the partial sums and a block-local prefix, and either
-// fixes `chosen` or raises `fallback`.
+// fixes `chosen` or raises `fallback` (always, with exact_only: every draw
+// then takes the exact sequential evaluation).
 __global__ __launch_bounds__(1024) void kpp_select_kernel(
     const float* __restrict__ w, const double* __restrict__ bsum, uint32_t* __restrict__ bad,
-    KppState* __restrict__ st, uint64_t n, uint32_t NB) {
+    KppState* __restrict__ st, uint64_t n, uint32_t NB, uint32_t exact_only) {
   __shared__ double s_before, s_total;
   __shared__ uint32_t s_block, s_first, s_stop;
   __shared__ double wsum[1024 / 64];
@@ -120,7 +121,7 @@ __global__ __launch_bounds__(1024) void kpp_select_kernel(
           s_block = blk;
           s_before = run;
           s_total = tot;
-          if (blk == NB) {
+          if (blk == NB || exact_only) {
             S.fallback = 1;  // u at or beyond the total: the tail rule decides
           } else {
             s_stop = 0;
@@ -188,56 +189,87 @@ __global__ __launch_bounds__(1024) void kpp_select_kernel(
   }
 }
 
-// Exact weightedSample on one wave for subspaces whose parallel decision was
-// inconclusive: lane 0 folds the weights in order, as rng.zig:60-81 does.
-__global__ __launch_bounds__(64) void kpp_fallback_kernel(const float* __restrict__ w,
-                                                          KppState* __restrict__ st, uint64_t n) {
-  __shared__ float buf[2048];
+// Exact weightedSample (rng.zig:60-81) for subspaces whose parallel decision
+// was inconclusive, one block per such subspace.  The reference folds the
+// f64 weights sequentially twice (the total, then the running cum up to the
+// first u < cum).  Here the first fold is evaluated exactly in chunks of
+// kFoldChunk weights (fold_rules.hpp with an f64 accumulator): all waves
+// form the chunk descriptors, then wave 0 applies them in order, recording
+// the exact running value before every chunk.  Because the weights are
+// non-negative the running value never decreases, so the first u < cum lies
+// in the first chunk whose end value exceeds u; wave 0 finds that chunk and
+// folds only it term by term from its exact start.
+// pre, chunks: [M][nc] scratch (nc = ceil(n / kFoldChunk)).
+constexpr uint32_t kKppFallbackThreads = 1024;
+
+__global__ __launch_bounds__(kKppFallbackThreads) void kpp_fallback_kernel(
+    const float* __restrict__ w, KppState* __restrict__ st, uint64_t n, double* __restrict__ pre,
+    FoldChunk* __restrict__ chunks, uint32_t nc) {
+  constexpr uint32_t kWaves = kKppFallbackThreads / kWave;
+  __shared__ double wsum[kWaves];
+  __shared__ double carry;
+  __shared__ FoldChunk lch[kWave];
+  __shared__ __attribute__((aligned(16))) float buf[kFoldChunk];
   const uint32_t m = blockIdx.x;
   KppState& S = st[m];
+  // Every thread reads the flags here; thread 0 rewrites them only at the
+  // end, after the block barriers below.
   if (S.err || !S.fallback) return;
   const float* wm = w + (uint64_t)m * n;
-  double total = 0.0;
-  for (uint64_t b = 0; b < n; b += 2048) {
-    const uint32_t len = n - b < 2048 ? (uint32_t)(n - b) : 2048u;
-    for (uint32_t q = threadIdx.x; q < len; q += 64) buf[q] = wm[b + q];
-    __syncthreads();
-    if (threadIdx.x == 0)
-      for (uint32_t q = 0; q < len; ++q) total += (double)buf[q];
-    __syncthreads();
-  }
-  __shared__ uint32_t found;
-  __shared__ double cum_s;
-  if (threadIdx.x == 0) {
-    found = 0xFFFFFFFFu;
-    cum_s = 0.0;
+  double* pm = pre + (uint64_t)m * nc;
+  FoldChunk* cm = chunks + (uint64_t)m * nc;
+  const uint32_t lane = threadIdx.x % kWave, wv = threadIdx.x / kWave;
+  for (uint32_t j = wv; j < nc; j += kWaves) {
+    const double cs = fold_chunk_sum_wave(wm, n, j);
+    if (lane == 0) pm[j] = cs;
   }
   __syncthreads();
+  block_prefix_f64<kKppFallbackThreads>(pm, nc, wsum, &carry);
+  for (uint32_t j = wv; j < nc; j += kWaves) fold_quantize_chunk_wave<double>(wm, n, j, pm[j], cm + j);
+  __syncthreads();
+  if (wv != 0) return;
+  // Wave 0 only from here: pm[j] becomes the exact value before chunk j.
+  const double total = fold_apply_wave<double>(wm, n, cm, nc, lch, buf, pm);
+  __threadfence_block();
   const double u = S.r * total;
-  for (uint64_t b = 0; b < n && found == 0xFFFFFFFFu; b += 2048) {
-    const uint32_t len = n - b < 2048 ? (uint32_t)(n - b) : 2048u;
-    for (uint32_t q = threadIdx.x; q < len; q += 64) buf[q] = wm[b + q];
-    __syncthreads();
-    if (threadIdx.x == 0) {
-      double cum = cum_s;
-      for (uint32_t q = 0; q < len; ++q) {
-        cum += (double)buf[q];
-        if (u < cum) {
-          found = (uint32_t)(b + q);
-          break;
-        }
-      }
-      cum_s = cum;
-    }
-    __syncthreads();
+  uint32_t jf = 0xFFFFFFFFu;
+  for (uint32_t j0 = 0; j0 < nc && jf == 0xFFFFFFFFu; j0 += kWave) {
+    const uint32_t j = j0 + lane;
+    const bool hit = j < nc && u < (j + 1 < nc ? pm[j + 1] : total);
+    const uint64_t ballot = __ballot(hit);
+    if (ballot) jf = j0 + (uint32_t)__ffsll((long long)ballot) - 1;
   }
-  if (threadIdx.x == 0) {
-    if (found == 0xFFFFFFFFu) {  // rng.zig:79-81: last positive weight
-      uint64_t last = n - 1;
-      while (last > 0 && wm[last] == 0.0f) --last;
-      found = (uint32_t)last;
+  uint64_t found = ~0ull;
+  if (jf != 0xFFFFFFFFu) {
+    const uint64_t lo = (uint64_t)jf * kFoldChunk;
+    const uint32_t len = fold_chunk_len(n, jf);
+    wave_lds_sync();
+    for (uint32_t t = lane; t < len; t += kWave) buf[t] = wm[lo + t];
+    wave_lds_sync();
+    double cum = pm[jf];
+    for (uint32_t t = 0; t < len; ++t) {
+      cum += (double)buf[t];
+      if (u < cum) {
+        found = lo + t;
+        break;
+      }
     }
-    S.chosen = found;
+  } else {
+    // rng.zig:79-81: no u < cum: the last positive weight (index 0 if none)
+    found = 0;
+    for (uint64_t b = n; b > 0;) {
+      const uint64_t lo = b > kWave ? b - kWave : 0;
+      const uint64_t i = lo + lane;
+      const uint64_t ballot = __ballot(i < b && wm[i] != 0.0f);
+      if (ballot) {
+        found = lo + 63 - (uint64_t)__clzll((long long)ballot);
+        break;
+      }
+      b = lo;
+    }
+  }
+  if (lane == 0) {
+    S.chosen = (uint32_t)found;
     S.fallback = 0;
   }
 }

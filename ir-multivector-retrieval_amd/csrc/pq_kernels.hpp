@@ -706,7 +706,8 @@ __global__ __launch_bounds__(kWave) void fold_kernel(
 // (src/tac/kmeans.zig:179), evaluated exactly in chunks of kFoldChunk terms
 // (fold_rules.hpp): f64 chunk sums -> prefix -> per-chunk quantized sums for
 // three candidate binades -> one wave per subspace applies the chunks in
-// order, folding term by term any chunk the rules do not cover.
+// order, folding term by term any chunk the rules do not cover.  The wave
+// helpers also serve the f64 weight folds of k-means++ (kmeanspp.hpp).
 // ---------------------------------------------------------------------------
 __device__ __forceinline__ double wave_sum_f64(double v) {
   for (int off = kWave / 2; off > 0; off >>= 1) v += __shfl_down(v, off, kWave);
@@ -717,22 +718,138 @@ __device__ __forceinline__ uint64_t wave_sum_u64(uint64_t v) {
   return v;
 }
 
-// Chunk sums in f64 (any order: they only place the candidate binades).
+// Orders one wave's LDS accesses before and after this point.
+__device__ __forceinline__ void wave_lds_sync() {
+  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+  __builtin_amdgcn_wave_barrier();
+  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+}
+
+constexpr int32_t kFoldNoBinade = -100000;  // k0 of a chunk whose start is not normal
+
+__host__ __device__ inline uint32_t fold_chunk_len(uint64_t n, uint32_t j) {
+  const uint64_t lo = (uint64_t)j * kFoldChunk;
+  return n - lo < kFoldChunk ? (uint32_t)(n - lo) : kFoldChunk;
+}
+
+// f64 sum of chunk j in any order (it only places the candidate binades);
+// the total lands in lane 0.
+__device__ inline double fold_chunk_sum_wave(const float* __restrict__ em, uint64_t n, uint32_t j) {
+  const uint32_t lane = threadIdx.x % kWave;
+  const uint64_t lo = (uint64_t)j * kFoldChunk;
+  const uint32_t len = fold_chunk_len(n, j);
+  double acc = 0.0;
+  for (uint32_t t = lane; t < len; t += kWave) acc += (double)em[lo + t];
+  return wave_sum_f64(acc);
+}
+
+// Exclusive prefix of a[0 .. cnt) in place, by a block of kThreads threads
+// (f64, any rounding: the values only place the candidate binades).
+template <uint32_t kThreads>
+__device__ inline void block_prefix_f64(double* __restrict__ a, uint32_t cnt, double* wsum,
+                                        double* carry) {
+  const uint32_t lane = threadIdx.x % kWave, w = threadIdx.x / kWave;
+  if (threadIdx.x == 0) *carry = 0.0;
+  __syncthreads();
+  for (uint32_t j0 = 0; j0 < cnt; j0 += kThreads) {
+    const uint32_t j = j0 + threadIdx.x;
+    const double x = j < cnt ? a[j] : 0.0;
+    double incl = x;
+    for (int off = 1; off < kWave; off <<= 1) {
+      const double o = __shfl_up(incl, off, kWave);
+      if (lane >= (uint32_t)off) incl += o;
+    }
+    if (lane == kWave - 1) wsum[w] = incl;
+    __syncthreads();
+    double before = *carry;
+    for (uint32_t q = 0; q < w; ++q) before += wsum[q];
+    if (j < cnt) a[j] = before + (incl - x);
+    __syncthreads();
+    if (threadIdx.x == kThreads - 1) *carry = before + incl;
+    __syncthreads();
+  }
+}
+
+// One wave: the descriptor of chunk j (quantized sums for the binades
+// around the approximate start `pre`), written by lane 0.
+template <typename Acc>
+__device__ inline void fold_quantize_chunk_wave(const float* __restrict__ em, uint64_t n,
+                                                uint32_t j, double pre,
+                                                FoldChunk* __restrict__ out) {
+  const uint32_t lane = threadIdx.x % kWave;
+  const Acc ps = (Acc)pre;
+  const int32_t k0 = fold_is_normal_positive(ps) ? fold_exponent(ps) - 1 : kFoldNoBinade;
+  const uint64_t lo = (uint64_t)j * kFoldChunk;
+  const uint32_t len = fold_chunk_len(n, j);
+  uint64_t q[kFoldCands] = {0, 0, 0};
+  uint32_t bad = 0;  // bit c: candidate c spoiled by one of this lane's terms
+  for (uint32_t t = lane; t < len; t += kWave) {
+    const float v = em[lo + t];
+#pragma unroll
+    for (int c = 0; c < kFoldCands; ++c) {
+      const uint64_t qi = fold_quantize<Acc>(v, k0 + c);
+      bad |= qi == kFoldBad ? 1u << c : 0u;
+      q[c] += qi == kFoldBad ? 0u : qi;
+    }
+  }
+  for (int off = kWave / 2; off > 0; off >>= 1) bad |= __shfl_xor(bad, off, kWave);
+#pragma unroll
+  for (int c = 0; c < kFoldCands; ++c) q[c] = wave_sum_u64(q[c]);
+  if (lane == 0) {
+    FoldChunk ch;
+    ch.k0 = k0;
+    ch.clean = ~bad & ((1u << kFoldCands) - 1u);
+#pragma unroll
+    for (int c = 0; c < kFoldCands; ++c) ch.q[c] = q[c];
+    *out = ch;
+  }
+}
+
+// One wave folds chunks 0 .. nc-1 of em in order from 0 with their
+// descriptors and returns the exact serial sum in every lane; every lane
+// computes the same values.  A chunk the rules do not cover is staged in
+// `buf` and folded term by term.  With `starts`, lane 0 stores the exact
+// accumulator value before each chunk.  lch: kWave descriptors of LDS;
+// buf: kFoldChunk floats of LDS.
+template <typename Acc>
+__device__ inline Acc fold_apply_wave(const float* __restrict__ em, uint64_t n,
+                                      const FoldChunk* __restrict__ cm, uint32_t nc,
+                                      FoldChunk* lch, float* buf, Acc* __restrict__ starts) {
+  const uint32_t lane = threadIdx.x % kWave;
+  Acc s = 0;
+  for (uint32_t j0 = 0; j0 < nc; j0 += kWave) {
+    wave_lds_sync();
+    if (j0 + lane < nc) lch[lane] = cm[j0 + lane];
+    wave_lds_sync();
+    const uint32_t cnt = nc - j0 < kWave ? nc - j0 : kWave;
+    for (uint32_t q = 0; q < cnt; ++q) {
+      const uint32_t j = j0 + q;
+      if (starts != nullptr && lane == 0) starts[j] = s;
+      Acc out;
+      if (!fold_apply(s, lch[q], &out)) {
+        const uint64_t lo = (uint64_t)j * kFoldChunk;
+        const uint32_t len = fold_chunk_len(n, j);
+        wave_lds_sync();
+        for (uint32_t t = lane; t < len; t += kWave) buf[t] = em[lo + t];
+        wave_lds_sync();
+        out = s;
+#pragma unroll 16
+        for (uint32_t t = 0; t < len; ++t) out = out + (Acc)buf[t];
+      }
+      s = out;
+    }
+  }
+  return s;
+}
+
+// Chunk sums, one wave per chunk, four chunks per block.
 __global__ __launch_bounds__(kBlock) void wcss_chunk_sums_kernel(
     const float* __restrict__ e, double* __restrict__ csum, const uint32_t* __restrict__ done,
     uint64_t n, uint32_t nc) {
-  __shared__ double ws[kBlock / kWave];
-  const uint32_t m = blockIdx.y, j = blockIdx.x;
-  if (done[m]) return;
-  const float* em = e + (uint64_t)m * n;
-  const uint64_t lo = (uint64_t)j * kFoldChunk;
-  double acc = 0.0;
-  for (uint32_t q = threadIdx.x; q < kFoldChunk; q += kBlock)
-    if (lo + q < n) acc += (double)em[lo + q];
-  acc = wave_sum_f64(acc);
-  if (threadIdx.x % kWave == 0) ws[threadIdx.x / kWave] = acc;
-  __syncthreads();
-  if (threadIdx.x == 0) csum[(uint64_t)m * nc + j] = (ws[0] + ws[1]) + (ws[2] + ws[3]);
+  const uint32_t m = blockIdx.y, j = blockIdx.x * (kBlock / kWave) + threadIdx.x / kWave;
+  if (done[m] || j >= nc) return;
+  const double s = fold_chunk_sum_wave(e + (uint64_t)m * n, n, j);
+  if (threadIdx.x % kWave == 0) csum[(uint64_t)m * nc + j] = s;
 }
 
 // Exclusive prefix of the chunk sums (in place), one block per subspace.
@@ -743,111 +860,30 @@ __global__ __launch_bounds__(kBlock) void wcss_prefix_kernel(double* __restrict_
   __shared__ double carry;
   const uint32_t m = blockIdx.x;
   if (done[m]) return;
-  double* cm = csum + (uint64_t)m * nc;
-  const uint32_t lane = threadIdx.x % kWave, w = threadIdx.x / kWave;
-  if (threadIdx.x == 0) carry = 0.0;
-  __syncthreads();
-  for (uint32_t j0 = 0; j0 < nc; j0 += kBlock) {
-    const uint32_t j = j0 + threadIdx.x;
-    const double x = j < nc ? cm[j] : 0.0;
-    double incl = x;
-    for (int off = 1; off < kWave; off <<= 1) {
-      const double o = __shfl_up(incl, off, kWave);
-      if (lane >= (uint32_t)off) incl += o;
-    }
-    if (lane == kWave - 1) ws[w] = incl;
-    __syncthreads();
-    double before = carry;
-    for (uint32_t q = 0; q < w; ++q) before += ws[q];
-    if (j < nc) cm[j] = before + incl - x;
-    __syncthreads();
-    if (threadIdx.x == kBlock - 1) carry = before + incl;
-    __syncthreads();
-  }
+  block_prefix_f64<kBlock>(csum + (uint64_t)m * nc, nc, ws, &carry);
 }
 
-// Quantized sums of chunk j for the binades around its approximate start.
+// Chunk descriptors, one wave per chunk, four chunks per block.
 __global__ __launch_bounds__(kBlock) void wcss_quantize_kernel(
     const float* __restrict__ e, const double* __restrict__ pre, FoldChunk* __restrict__ chunks,
     const uint32_t* __restrict__ done, uint64_t n, uint32_t nc) {
-  static_assert(kBlock / kWave == 4, "the block combines below assume four waves");
-  __shared__ uint64_t ws[kFoldCands][kBlock / kWave];
-  __shared__ uint32_t wbad[kBlock / kWave];
-  const uint32_t m = blockIdx.y, j = blockIdx.x;
-  if (done[m]) return;
-  const float ps = (float)pre[(uint64_t)m * nc + j];
-  const int32_t k0 = fold_is_normal_positive(ps) ? fold_exponent(ps) - 1 : -1000;
-  const float* em = e + (uint64_t)m * n;
-  const uint64_t lo = (uint64_t)j * kFoldChunk;
-  uint64_t q[kFoldCands] = {0, 0, 0};
-  uint32_t bad = 0;  // bit c: candidate c spoiled by one of this thread's terms
-  for (uint32_t t = threadIdx.x; t < kFoldChunk; t += kBlock) {
-    if (lo + t >= n) break;
-    const float v = em[lo + t];
-#pragma unroll
-    for (int c = 0; c < kFoldCands; ++c) {
-      const uint64_t qi = fold_quantize(v, k0 + c);
-      bad |= qi == kFoldBad ? 1u << c : 0u;
-      q[c] += qi == kFoldBad ? 0u : qi;
-    }
-  }
-  // spoiled candidates, OR-reduced over the block
-  for (int off = kWave / 2; off > 0; off >>= 1) bad |= __shfl_xor(bad, off, kWave);
-#pragma unroll
-  for (int c = 0; c < kFoldCands; ++c) {
-    const uint64_t sw = wave_sum_u64(q[c]);
-    if (threadIdx.x % kWave == 0) ws[c][threadIdx.x / kWave] = sw;
-  }
-  if (threadIdx.x % kWave == 0) wbad[threadIdx.x / kWave] = bad;
-  __syncthreads();
-  if (threadIdx.x == 0) {
-    FoldChunk ch;
-    ch.k0 = k0;
-    ch.clean = ~((wbad[0] | wbad[1]) | (wbad[2] | wbad[3])) & ((1u << kFoldCands) - 1u);
-#pragma unroll
-    for (int c = 0; c < kFoldCands; ++c) ch.q[c] = (ws[c][0] + ws[c][1]) + (ws[c][2] + ws[c][3]);
-    chunks[(uint64_t)m * nc + j] = ch;
-  }
+  const uint32_t m = blockIdx.y, j = blockIdx.x * (kBlock / kWave) + threadIdx.x / kWave;
+  if (done[m] || j >= nc) return;
+  const uint64_t at = (uint64_t)m * nc + j;
+  fold_quantize_chunk_wave<float>(e + (uint64_t)m * n, n, j, pre[at], chunks + at);
 }
 
-// One wave per subspace: lane 0 applies the chunks in order (descriptors
-// staged through LDS 64 at a time); a chunk the rules do not cover is staged
-// through LDS and folded term by term.
+// One wave per subspace applies the chunks in order.
 __global__ __launch_bounds__(kWave) void wcss_apply_kernel(
     const float* __restrict__ e, const FoldChunk* __restrict__ chunks, float* __restrict__ wcss,
     const uint32_t* __restrict__ done, uint64_t n, uint32_t nc) {
   __shared__ FoldChunk lch[kWave];
   __shared__ __attribute__((aligned(16))) float buf[kFoldChunk];
-  __shared__ uint32_t need;
-  const uint32_t m = blockIdx.x, lane = threadIdx.x;
+  const uint32_t m = blockIdx.x;
   if (done[m]) return;
-  const float* em = e + (uint64_t)m * n;
-  const FoldChunk* cm = chunks + (uint64_t)m * nc;
-  float s = 0.0f;  // lane 0's accumulator
-  for (uint32_t j0 = 0; j0 < nc; j0 += kWave) {
-    if (j0 + lane < nc) lch[lane] = cm[j0 + lane];
-    __syncthreads();
-    const uint32_t cnt = nc - j0 < kWave ? nc - j0 : kWave;
-    for (uint32_t q = 0; q < cnt; ++q) {
-      if (lane == 0) {
-        float out;
-        need = fold_apply(s, lch[q], &out) ? 0u : 1u;
-        if (!need) s = out;
-      }
-      __syncthreads();
-      if (need) {
-        const uint64_t lo = (uint64_t)(j0 + q) * kFoldChunk;
-        const uint32_t len = n - lo < kFoldChunk ? (uint32_t)(n - lo) : kFoldChunk;
-        for (uint32_t t = lane; t < len; t += kWave) buf[t] = em[lo + t];
-        __syncthreads();
-        if (lane == 0)
-          for (uint32_t t = 0; t < len; ++t) s = s + buf[t];
-        __syncthreads();
-      }
-    }
-    __syncthreads();
-  }
-  if (lane == 0) wcss[m] = s;
+  const float s = fold_apply_wave<float>(e + (uint64_t)m * n, n, chunks + (uint64_t)m * nc, nc,
+                                         lch, buf, static_cast<float*>(nullptr));
+  if (threadIdx.x == 0) wcss[m] = s;
 }
 
 // ---------------------------------------------------------------------------

@@ -26,6 +26,7 @@
 
 #include <cmath>
 #include <cstdio>
+#include <cstdlib>
 #include <cstring>
 #include <mutex>
 #include <string>
@@ -362,6 +363,18 @@ int kmeanspp(DeviceState &ds, hipStream_t s, const float *xs, uint64_t n, uint32
       (st = ensure(ds, ds.kpp_bsum, (size_t)M * NB * sizeof(double))) ||
       (st = ensure(ds, ds.kpp_bad, (size_t)M * sizeof(uint32_t))))
     return st;
+  // exact weight folds of the fallback: chunk prefixes / start values and
+  // descriptors (the same buffers, and sizes, as the wcss fold of training)
+  const uint32_t nfc = (uint32_t)((n + kFoldChunk - 1) / kFoldChunk);
+  if ((st = ensure(ds, ds.fold_pre, (size_t)M * nfc * sizeof(double))) ||
+      (st = ensure(ds, ds.fold_chunks, (size_t)M * nfc * sizeof(FoldChunk))))
+    return st;
+  double *fold_pre = as<double>(ds.fold_pre);
+  FoldChunk *fold_chunks = as<FoldChunk>(ds.fold_chunks);
+  // TAC_GPU_KPP_EXACT=1: every draw takes the exact sequential evaluation
+  // (the same picks, slower; the parallel band test is skipped).
+  const char *exact_env = getenv("TAC_GPU_KPP_EXACT");
+  const uint32_t exact_only = exact_env != nullptr && exact_env[0] == '1';
   KppState *state = as<KppState>(ds.kpp_state);
   float *w = as<float>(ds.kpp_w);
   double *bsum = as<double>(ds.kpp_bsum);
@@ -372,9 +385,10 @@ int kmeanspp(DeviceState &ds, hipStream_t s, const float *xs, uint64_t n, uint32
     DISPATCH_D(D, kpp_update(xs, w, bsum, bad, state, cb, n, M, K, c, NB, s));
     LAUNCH_TRY("kpp_update_kernel");
     if (c + 1 == K) break;
-    kpp_select_kernel<<<M, 1024, 0, s>>>(w, bsum, bad, state, n, NB);
+    kpp_select_kernel<<<M, 1024, 0, s>>>(w, bsum, bad, state, n, NB, exact_only);
     LAUNCH_TRY("kpp_select_kernel");
-    kpp_fallback_kernel<<<M, 64, 0, s>>>(w, state, n);
+    kpp_fallback_kernel<<<M, kKppFallbackThreads, 0, s>>>(w, state, n, fold_pre, fold_chunks,
+                                                          nfc);
     LAUNCH_TRY("kpp_fallback_kernel");
   }
   std::vector<KppState> h(M);
@@ -508,10 +522,11 @@ int train_core(DeviceState &ds, hipStream_t s, const float *d_x, uint64_t n, uin
     DISPATCH_D(D, fold(sorted, counts, start, out.cb, done, n, M, K, s));
     LAUNCH_TRY("fold_kernel");
     if (check || (want_wcss && t + 1 == max_iters)) {
-      wcss_chunk_sums_kernel<<<dim3(nfc, M), kBlock, 0, s>>>(e, fold_pre, done, n, nfc);
+      const uint32_t fgrid = (nfc + kBlock / kWave - 1) / (kBlock / kWave);
+      wcss_chunk_sums_kernel<<<dim3(fgrid, M), kBlock, 0, s>>>(e, fold_pre, done, n, nfc);
       wcss_prefix_kernel<<<M, kBlock, 0, s>>>(fold_pre, done, nfc);
-      wcss_quantize_kernel<<<dim3(nfc, M), kBlock, 0, s>>>(e, fold_pre, fold_chunks, done, n,
-                                                            nfc);
+      wcss_quantize_kernel<<<dim3(fgrid, M), kBlock, 0, s>>>(e, fold_pre, fold_chunks, done, n,
+                                                             nfc);
       wcss_apply_kernel<<<M, kWave, 0, s>>>(e, fold_chunks, wcss, done, n, nfc);
       LAUNCH_TRY("wcss kernels");
     }

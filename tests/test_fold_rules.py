@@ -1,7 +1,10 @@
-"""Host check of the chunked wcss evaluation the GPU kernels use (no GPU):
-the serial fp32 fold of non-negative terms (src/tac/kmeans.zig:179), taken a
-chunk at a time by quantizing the terms to the accumulator's ulp, equals the
-term-by-term fold bit for bit on random and adversarial sequences."""
+"""Host check of the chunked fold evaluation the GPU kernels use (no GPU):
+the serial fold of non-negative float terms with an fp32 accumulator (the
+wcss of src/tac/kmeans.zig:179) or an f64 one (weightedSample,
+src/util/rng.zig:60-81), taken a chunk at a time by quantizing the terms to
+the accumulator's ulp, equals the term-by-term fold bit for bit on random and
+adversarial sequences, and weightedSample's pick through the exact chunk
+start values equals the plain loop's."""
 import subprocess
 from pathlib import Path
 

@@ -262,6 +262,25 @@ def test_kmeanspp_train_matches_oracle(gpu, m, ksub, n, seed):
     assert np.array_equal(_bits(got.codebooks), _bits(ref.codebooks))
 
 
+@pytest.mark.parametrize("m,ksub,n,seed,dups", [(16, 256, 20000, 0xa1b2c3d4, False),
+                                                (8, 64, 777, 5, False),
+                                                (8, 128, 150_001, 9, False),
+                                                (16, 64, 6000, 31, True)])
+def test_kmeanspp_exact_evaluation_every_draw(gpu, monkeypatch, m, ksub, n, seed, dups):
+    # TAC_GPU_KPP_EXACT=1 sends every draw through the exact chunked
+    # evaluation of weightedSample (rng.zig:60-81) instead of only the
+    # inconclusive ones; the picks must not change.  `dups` repeats rows so
+    # that many weights are exactly zero.
+    x = _workload_rows(n, seed=seed % 89)
+    if dups:
+        x = x[np.random.default_rng(seed).integers(0, 400, n)]
+    monkeypatch.setenv("TAC_GPU_KPP_EXACT", "1")
+    got = pq.train(x, 64, seed, m=m, ksub=ksub, max_iters=2, tol=NEVER)
+    ref = orc.pq_train(x, 64, m, ksub, seed=seed, max_iters=2, tol=NEVER, n_threads=16)
+    assert ref.status == 0
+    assert np.array_equal(_bits(got.codebooks), _bits(ref.codebooks))
+
+
 def test_kmeanspp_first_iteration_is_the_seed_plus_one_update(gpu):
     x = _workload_rows(8000, seed=5)
     got = pq.train(x, 64, 99, m=16, ksub=128, max_iters=1, tol=NEVER, trace=True)
