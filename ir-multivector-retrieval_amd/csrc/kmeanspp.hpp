@@ -63,12 +63,14 @@ __global__ __launch_bounds__(256) void kpp_update_kernel(
     float xv[D];
     load_padded<D>(xm + i * DP, xv);
     const float d = exact_l2sq<D>(xv, cv);
+    bool store = true;
     float wi = d;
     if (c > 0) {
       const float old = wm[i];
-      wi = d < old ? d : old;  // kmeans.zig:134: replace on strict <
+      store = d < old;  // kmeans.zig:134: replace on strict <
+      wi = store ? d : old;
     }
-    wm[i] = wi;
+    if (store) wm[i] = wi;  // unchanged weights are not rewritten
     invalid |= !(wi >= 0.0f && wi <= 3.402823466e38f);  // rng.zig:62 NonFinite
     acc += (double)wi;
   }
@@ -86,53 +88,78 @@ __global__ __launch_bounds__(256) void kpp_update_kernel(
 __global__ __launch_bounds__(1024) void kpp_select_kernel(
     const float* __restrict__ w, const double* __restrict__ bsum, uint32_t* __restrict__ bad,
     KppState* __restrict__ st, uint64_t n, uint32_t NB, uint32_t exact_only) {
-  __shared__ double s_before, s_total;
+  __shared__ double s_before, s_total, s_u, s_r, carry;
   __shared__ uint32_t s_block, s_first, s_stop;
   __shared__ double wsum[1024 / 64];
   const uint32_t m = blockIdx.x;
   KppState& S = st[m];
-  // Thread 0 alone reads and writes the subspace state before the barrier;
-  // every thread then acts on the shared verdict.
+  const double* bm = bsum + (uint64_t)m * NB;
+  const uint32_t lane = threadIdx.x % 64, wv = threadIdx.x / 64;
+  // Thread 0 alone reads and writes the subspace state; every thread acts
+  // on the shared verdicts.
   if (threadIdx.x == 0) {
     s_stop = 1;
     s_first = 0xFFFFFFFFu;
+    s_block = NB;
+    carry = 0.0;
     if (!S.err) {
       S.fallback = 0;
-      if (bad[m]) {
+      if (bad[m])
         S.err = 9;  // NonFinite
-      } else {
-        double tot = 0.0;
-        for (uint32_t b = 0; b < NB; ++b) tot += bsum[(uint64_t)m * NB + b];
-        if (!(tot > 0.0)) {
-          S.err = 10;  // AllZero
-        } else {
-          S.r = kpp_float64(S.s);
-          const double u = S.r * tot;
-          double run = 0.0;
-          uint32_t blk = NB;
-          for (uint32_t b = 0; b < NB; ++b) {
-            const double next = run + bsum[(uint64_t)m * NB + b];
-            if (u < next) {
-              blk = b;
-              break;
-            }
-            run = next;
-          }
-          s_block = blk;
-          s_before = run;
-          s_total = tot;
-          if (blk == NB || exact_only) {
-            S.fallback = 1;  // u at or beyond the total: the tail rule decides
-          } else {
-            s_stop = 0;
-          }
-        }
-      }
+      else
+        s_stop = 0;
     }
   }
   __syncthreads();
   if (s_stop) return;
-  const double r = S.r;
+  // Total of the block sums, in any order: the bands cover every order.
+  double part = 0.0;
+  for (uint32_t b = threadIdx.x; b < NB; b += blockDim.x) part += bm[b];
+  for (int off = 32; off > 0; off >>= 1) part += __shfl_down(part, off, 64);
+  if (lane == 0) wsum[wv] = part;
+  __syncthreads();
+  if (threadIdx.x == 0) {
+    double tot = 0.0;
+    for (uint32_t q = 0; q < 1024 / 64; ++q) tot += wsum[q];
+    if (!(tot > 0.0)) {
+      S.err = 10;  // AllZero
+      s_stop = 1;
+    } else {
+      S.r = kpp_float64(S.s);
+      s_r = S.r;
+      s_total = tot;
+      s_u = S.r * tot;
+    }
+  }
+  __syncthreads();
+  if (s_stop) return;
+  // First block whose inclusive prefix exceeds u (a block-wide scan; any
+  // rounding: the candidate found below is verified against the bands).
+  const double ud = s_u;
+  for (uint32_t b0 = 0; b0 < NB; b0 += blockDim.x) {
+    const uint32_t b = b0 + threadIdx.x;
+    const double x = b < NB ? bm[b] : 0.0;
+    double incl = x;
+    for (int off = 1; off < 64; off <<= 1) {
+      const double o = __shfl_up(incl, off, 64);
+      if (lane >= (uint32_t)off) incl += o;
+    }
+    if (lane == 63) wsum[wv] = incl;
+    __syncthreads();
+    double before = carry;
+    for (uint32_t q = 0; q < wv; ++q) before += wsum[q];
+    if (b < NB && ud < before + incl) atomicMin(&s_block, b);
+    __syncthreads();
+    if (b == s_block) s_before = before + (incl - x);
+    if (threadIdx.x == blockDim.x - 1) carry = before + incl;
+    __syncthreads();
+    if (s_block != NB) break;
+  }
+  if (s_block == NB || exact_only) {
+    if (threadIdx.x == 0) S.fallback = 1;  // u at or beyond the total: the tail rule decides
+    return;
+  }
+  const double r = s_r;
   // Block-local inclusive prefix of kKppBlock weights: 4 per thread.
   const uint64_t lo = (uint64_t)s_block * kKppBlock;
   const float* wm = w + (uint64_t)m * n;
@@ -144,7 +171,6 @@ __global__ __launch_bounds__(1024) void kpp_select_kernel(
     v[q] = i < n ? (double)wm[i] : 0.0;
     local += v[q];
   }
-  const uint32_t lane = threadIdx.x % 64, wv = threadIdx.x / 64;
   double incl = local;
   for (int off = 1; off < 64; off <<= 1) {
     const double o = __shfl_up(incl, off, 64);
