@@ -27,6 +27,12 @@ class TrainExtras(ctypes.Structure):
     _fields_ = [("trace", _vp), ("iters_run", _vp), ("wcss", _vp), ("empties", _vp)]
 
 
+class TacParams(ctypes.Structure):
+    _fields_ = [("kappa_total", _u32), ("mu", _u32), ("tau", _u32), ("epsilon", _u32),
+                ("theta", _u32), ("max_iters", _u32), ("tol", _f32), ("seed", _u64),
+                ("n_threads", _u32)]
+
+
 class Xoshiro(ctypes.Structure):
     _fields_ = [("s", _u64 * 4)]
 
@@ -80,6 +86,21 @@ def _load():
     L.orc_refine.restype = ctypes.c_int
     L.orc_refine.argtypes = [_vp, _u32, _u32, _vp, _u32, _vp, _u64, _u32, _u32, _vp, _vp, _u64,
                              _vp, _vp, _u64, _u64, _u64, ctypes.POINTER(_f32)]
+    L.orc_tac_allocate_tail.restype = ctypes.c_int
+    L.orc_tac_allocate_tail.argtypes = [_vp, _u64, _vp, _u32, _u32, _u32, ctypes.POINTER(_u32)]
+    L.orc_tac_damped_phase2.restype = ctypes.c_int
+    L.orc_tac_damped_phase2.argtypes = [_vp, _vp, _u64, _vp, _vp, _u32, _u32, _u32]
+    L.orc_tac_bound_phase3.restype = ctypes.c_int
+    L.orc_tac_bound_phase3.argtypes = [_vp, _u64, _vp, _u32, _u32, _u32, _u32]
+    L.orc_tac_reconcile_phase4.restype = ctypes.c_int
+    L.orc_tac_reconcile_phase4.argtypes = [_vp, _u64, _vp, _vp, _u32, _u32, _u32, _u32, _u32]
+    L.orc_tac_allocate_budgets.restype = ctypes.c_int
+    L.orc_tac_allocate_budgets.argtypes = [_vp, _vp, _u64, _vp, _vp, ctypes.POINTER(TacParams)]
+    L.orc_tac_spreads.restype = None
+    L.orc_tac_spreads.argtypes = [_vp, _u32, _vp, _vp, _u64, _vp]
+    L.orc_tac_cluster_flat.restype = ctypes.c_int
+    L.orc_tac_cluster_flat.argtypes = [_vp, _u64, _vp, _u64, _u32, ctypes.POINTER(TacParams),
+                                       _vp, _vp, _vp, ctypes.POINTER(_f32), ctypes.POINTER(_u64)]
     return L
 
 
@@ -297,3 +318,92 @@ def refine(query, n_q: int, dim: int, centroids, table, m: int, ksub: int, doc_i
                         _p(pay), pay.size, _p(dto), _p(nr), nr.size, di.size - 1, doc_id,
                         ctypes.byref(out))
     return st, np.float32(out.value)
+
+
+# ---- TAC (src/tac/tac.zig) ---------------------------------------------------
+
+# Paper defaults (src/constants.zig TAC_MU / TAC_TAU / TAC_EPSILON / TAC_THETA).
+TAC_DEFAULTS = dict(mu=128, tau=256, epsilon=4, theta=39, max_iters=25, tol=1e-4)
+
+
+def tac_params(kappa_total: int, seed: int, **kw) -> TacParams:
+    d = dict(TAC_DEFAULTS, n_threads=1)
+    d.update(kw)
+    return TacParams(kappa_total, d["mu"], d["tau"], d["epsilon"], d["theta"], d["max_iters"],
+                     d["tol"], seed & (2**64 - 1), d["n_threads"])
+
+
+def _u32a(a):
+    return np.ascontiguousarray(a, dtype=np.uint32)
+
+
+def tac_allocate_tail(freqs, mu, tau, kappa_total):
+    f = _u32a(freqs)
+    kappa = np.zeros(max(f.size, 1), np.uint32)
+    b = _u32(0)
+    st = lib.orc_tac_allocate_tail(_p(f), f.size, _p(kappa), mu, tau, kappa_total,
+                                   ctypes.byref(b))
+    return st, kappa[:f.size], int(b.value)
+
+
+def tac_damped_phase2(freqs, spreads, kappa, budget_active, mu, tau):
+    f, sp = _u32a(freqs), _f32(spreads)
+    k = _u32a(kappa).copy()
+    frac = np.zeros(max(f.size, 1), np.float32)
+    st = lib.orc_tac_damped_phase2(_p(f), _p(sp), f.size, _p(k), _p(frac), budget_active, mu, tau)
+    return st, k, frac[:f.size]
+
+
+def tac_bound_phase3(freqs, kappa, mu, tau, epsilon, theta):
+    f = _u32a(freqs)
+    k = _u32a(kappa).copy()
+    st = lib.orc_tac_bound_phase3(_p(f), f.size, _p(k), mu, tau, epsilon, theta)
+    return st, k
+
+
+def tac_reconcile_phase4(freqs, kappa, frac, kappa_total, mu, tau, epsilon, theta):
+    f, fr = _u32a(freqs), _f32(frac)
+    k = _u32a(kappa).copy()
+    st = lib.orc_tac_reconcile_phase4(_p(f), f.size, _p(k), _p(fr), kappa_total, mu, tau,
+                                      epsilon, theta)
+    return st, k
+
+
+def tac_allocate_budgets(freqs, spreads, params: TacParams):
+    f, sp = _u32a(freqs), _f32(spreads)
+    k = np.zeros(max(f.size, 1), np.uint32)
+    frac = np.zeros(max(f.size, 1), np.float32)
+    st = lib.orc_tac_allocate_budgets(_p(f), _p(sp), f.size, _p(k), _p(frac), ctypes.byref(params))
+    return st, k[:f.size], frac[:f.size]
+
+
+def tac_spreads(vectors, dim, group_offsets, group_indices):
+    v = _f32(vectors).reshape(-1)
+    go, gi = _u32a(group_offsets), _u32a(group_indices)
+    nd = go.size - 1
+    out = np.zeros(max(nd, 1), np.float32)
+    lib.orc_tac_spreads(_p(v), dim, _p(go), _p(gi), nd, _p(out))
+    return out[:nd]
+
+
+@dataclass
+class TacResult:
+    status: int
+    centroids: np.ndarray
+    assignments: np.ndarray
+    kappa_per_token: np.ndarray
+    wcss_total: float
+
+
+def tac_cluster_flat(token_ids, vectors, dim: int, params: TacParams) -> TacResult:
+    ids = _u32a(token_ids).reshape(-1)
+    v = _f32(vectors).reshape(-1)
+    nd = int(ids.max()) + 1 if ids.size else 1
+    cent = np.zeros(max(params.kappa_total * max(dim, 1), 1), np.float32)
+    asg = np.zeros(max(ids.size, 1), np.uint32)
+    kpt = np.zeros(nd, np.uint32)
+    w, ndo = _f32_c(), _u64(0)
+    st = lib.orc_tac_cluster_flat(_p(ids), ids.size, _p(v), v.size, dim, ctypes.byref(params),
+                                  _p(cent), _p(asg), _p(kpt), ctypes.byref(w), ctypes.byref(ndo))
+    return TacResult(st, cent[:params.kappa_total * dim], asg[:ids.size], kpt,
+                     float(np.float32(w.value)))

@@ -25,6 +25,8 @@
  *   orc_crc32               std.hash.Crc32 (CRC-32/ISO-HDLC) as storage.zig
  *                           applies it to the image (:612-617, :782-786)
  *   orc_refine              src/retrieval/refine.zig:51-145 (one candidate)
+ *   orc_tac_*               src/tac/tac.zig:77-330 (phases 1-4) and
+ *                           :563-830 (clusterFlat), in tac_oracle.c
  *
  * Status codes share their numbering with include/tac_gpu.h.
  */
@@ -57,6 +59,10 @@ enum {
   ORC_DOC_OUT_OF_RANGE = 18,
   ORC_DOC_LAYOUT_CORRUPT = 19,
   ORC_BUFFER_TOO_SMALL = 20,      /* StorageError (src/index/storage.zig:42-47) */
+  ORC_BUDGET_TOO_SMALL = 21,      /* ClusteringError (src/tac/tac.zig:59-64) */
+  ORC_BUDGET_TOO_LARGE = 22,
+  ORC_INVALID_THRESHOLDS = 23,
+  ORC_EMPTY_TOKEN_DUMP = 24,
 };
 
 /* Lane count the reference's generic vec path uses on the host it is built
@@ -144,6 +150,46 @@ int orc_refine(const float *query, uint32_t n_q, uint32_t dim,
                uint64_t payload_len, const uint64_t *doc_token_offsets,
                const float *norms, uint64_t n_tokens, uint64_t n_docs,
                uint64_t doc_id, float *score_out);
+
+
+/* ---- TAC: token-aware clustering (src/tac/tac.zig) -------------------- */
+
+typedef struct {
+  uint32_t kappa_total, mu, tau, epsilon, theta, max_iters;
+  float tol;
+  uint64_t seed;
+  uint32_t n_threads; /* wcss_total grouping only (tac.zig:688-820) */
+} orc_tac_params;
+
+/* Phase 1 (tac.zig:97-126): tail kappa; *budget_active = kappa_total - tail. */
+int orc_tac_allocate_tail(const uint32_t *freqs, uint64_t n, uint32_t *kappa, uint32_t mu,
+                          uint32_t tau, uint32_t kappa_total, uint32_t *budget_active);
+/* Phase 2 (tac.zig:157-217). */
+int orc_tac_damped_phase2(const uint32_t *freqs, const float *spreads, uint64_t n,
+                          uint32_t *kappa, float *frac, uint32_t budget_active, uint32_t mu,
+                          uint32_t tau);
+/* Phase 3 (tac.zig:236-258). */
+int orc_tac_bound_phase3(const uint32_t *freqs, uint64_t n, uint32_t *kappa, uint32_t mu,
+                         uint32_t tau, uint32_t epsilon, uint32_t theta);
+/* Phase 4 (tac.zig:286-372). */
+int orc_tac_reconcile_phase4(const uint32_t *freqs, uint64_t n, uint32_t *kappa,
+                             const float *frac, uint32_t kappa_total, uint32_t mu, uint32_t tau,
+                             uint32_t epsilon, uint32_t theta);
+/* Phases 1-4 (tac.zig:388-401). */
+int orc_tac_allocate_budgets(const uint32_t *freqs, const float *spreads, uint64_t n,
+                             uint32_t *kappa, float *frac, const orc_tac_params *p);
+/* Per-token spread s_j by Welford (tac.zig:604-638); vectors grouped by token
+ * through offsets / indices (CSR, ascending input order within a token). */
+void orc_tac_spreads(const float *vectors, uint32_t dim, const uint32_t *group_offsets,
+                     const uint32_t *group_indices, uint64_t n_distinct, float *spreads);
+/* clusterFlat (tac.zig:563-830).  n_distinct = max(token_ids) + 1 is written
+ * to *n_distinct_out; kappa_per_token must hold it (callers size it from the
+ * ids).  centroids: kappa_total * dim; assignments: n_tokens. */
+int orc_tac_cluster_flat(const uint32_t *token_ids, uint64_t n_tokens, const float *vectors,
+                         uint64_t vectors_len, uint32_t dim, const orc_tac_params *p,
+                         float *centroids,
+                         uint32_t *assignments, uint32_t *kappa_per_token, float *wcss_total,
+                         uint64_t *n_distinct_out);
 
 #ifdef __cplusplus
 }
