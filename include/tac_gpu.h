@@ -18,6 +18,7 @@
  *                                                 tac_crc32[_device]
  *   PQ.buildDistanceTable src/index/pq.zig:92-123 -> tac_pq_distance_table[_device]
  *   refine          src/retrieval/refine.zig:83-145 -> tac_refine / tac_refine_device
+ *   TAC.clusterFlat src/tac/tac.zig:563-830    -> tac_cluster_flat
  *   RefineError / StorageError (src/retrieval/refine.zig:37-42,
  *   src/index/storage.zig:42-47) -> tac_status 16-20
  *   PqError / KMeansError / RngError (src/index/pq.zig:32-38,
@@ -71,7 +72,11 @@ typedef enum tac_status {
   TAC_ERR_TABLE_SIZE_MISMATCH = 17,    /* RefineError.TableSizeMismatch */
   TAC_ERR_DOC_OUT_OF_RANGE = 18,       /* RefineError.DocOutOfRange */
   TAC_ERR_DOC_LAYOUT_CORRUPT = 19,     /* RefineError.DocLayoutCorrupt */
-  TAC_ERR_BUFFER_TOO_SMALL = 20        /* StorageError.BufferTooSmall */
+  TAC_ERR_BUFFER_TOO_SMALL = 20,       /* StorageError.BufferTooSmall */
+  TAC_ERR_BUDGET_TOO_SMALL = 21,       /* ClusteringError.BudgetTooSmall */
+  TAC_ERR_BUDGET_TOO_LARGE = 22,       /* ClusteringError.BudgetTooLarge */
+  TAC_ERR_INVALID_THRESHOLDS = 23,     /* ClusteringError.InvalidThresholds */
+  TAC_ERR_EMPTY_TOKEN_DUMP = 24        /* ClusteringError.EmptyTokenDump */
 } tac_status;
 
 /* Never-break iteration control: pass as `tol` to run exactly max_iters. */
@@ -275,6 +280,45 @@ int tac_refine_device(const tac_doc_index *d_index, const float *d_table, uint64
                       const float *d_query_tokens, uint32_t n_q, const uint32_t *d_doc_ids,
                       uint32_t n_candidates, float *d_scores_out, void *stream);
 
+
+/* ---- token-aware clustering --------------------------------------------- */
+/* ClusteringParams (src/tac/tac.zig:35-58).  The paper defaults are
+ * mu 128, tau 256, epsilon 4, theta 39, max_iters 25, tol 1e-4
+ * (src/constants.zig TAC_MU / TAC_TAU / TAC_EPSILON / TAC_THETA). */
+typedef struct tac_cluster_params {
+  uint32_t kappa_total;
+  uint32_t mu, tau, epsilon, theta;
+  uint32_t max_iters;
+  float tol;
+  uint64_t seed;
+  uint32_t n_threads; /* only groups wcss_total: 1 folds the per-token wcss in token
+                         order (the serial path); T > 1 folds each of T contiguous
+                         slices of token ids, then the slices (tac.zig:688-820) */
+} tac_cluster_params;
+
+/*
+ * TAC.clusterFlat (src/tac/tac.zig:563-830): groups the n_tokens vectors
+ * (vectors_len = n_tokens * dim floats) by token id, computes every token's
+ * spread (Welford), allocates the kappa_total centroids over tokens (phases
+ * 1-4) and runs kmeans.fit per token with seed ^ token id, all tokens at once
+ * on the device.  Outputs, bit-identical to the reference:
+ *   centroids_out   kappa_total * dim, concatenated in token-id order;
+ *   assignments_out n_tokens global centroid ids;
+ *   kappa_per_token_out[j] for j < n_distinct = max(token id) + 1, written to
+ *     *n_distinct_out (kappa_per_token_len smaller: TAC_ERR_BUFFER_TOO_SMALL);
+ *   *wcss_total_out the per-token wcss folded as params->n_threads selects.
+ * Errors follow the reference's order: no tokens EmptyTokenDump; dim 0 or a
+ * length mismatch InvalidThresholds; kappa_total 0 BudgetTooSmall; then the
+ * phases' errors, and the first failing token's kmeans error (RngError).
+ * dim above 191 is TAC_ERR_UNSUPPORTED (rows are staged in LDS), as is a
+ * token given more than 12,288 centroids.
+ */
+int tac_cluster_flat(const uint32_t *token_ids, uint64_t n_tokens, const float *vectors,
+                     uint64_t vectors_len, uint32_t dim, const tac_cluster_params *params,
+                     float *centroids_out, uint32_t *assignments_out,
+                     uint32_t *kappa_per_token_out, uint64_t kappa_per_token_len,
+                     float *wcss_total_out, uint64_t *n_distinct_out);
+
 /* ---- measurement -------------------------------------------------------- */
 /* When enabled, the library brackets its kernels with HIP events on the
  * stream they run on and accumulates their durations. */
@@ -288,6 +332,9 @@ typedef struct tac_gpu_profile {
   double residual_ms;    uint64_t residual_launches; /* residual + norm kernel */
   double crc_ms;         uint64_t crc_launches;      /* CRC-32 kernels */
   double refine_ms;      uint64_t refine_launches;   /* refine kernel */
+  double cluster_kpp_ms;   /* tac_cluster_flat: degenerate init + k-means++ seeding */
+  double cluster_lloyd_ms; /* tac_cluster_flat: Lloyd iterations of every token */
+  uint64_t cluster_calls;
 } tac_gpu_profile;
 int tac_gpu_profile_enable(int enable);
 int tac_gpu_profile_read(tac_gpu_profile *out, int reset);

@@ -228,22 +228,17 @@ __global__ __launch_bounds__(1024) void kpp_select_kernel(
 // pre, chunks: [M][nc] scratch (nc = ceil(n / kFoldChunk)).
 constexpr uint32_t kKppFallbackThreads = 1024;
 
-__global__ __launch_bounds__(kKppFallbackThreads) void kpp_fallback_kernel(
-    const float* __restrict__ w, KppState* __restrict__ st, uint64_t n, double* __restrict__ pre,
-    FoldChunk* __restrict__ chunks, uint32_t nc) {
+// The body, for one weight vector wm[0 .. n) and its state S, run by a whole
+// block of kKppFallbackThreads threads (the caller has checked that S needs
+// it).  pm, cm: nc = ceil(n / kFoldChunk) entries of scratch.
+__device__ inline void kpp_fallback_block(const float* __restrict__ wm, uint64_t n, KppState& S,
+                                          double* __restrict__ pm, FoldChunk* __restrict__ cm,
+                                          uint32_t nc) {
   constexpr uint32_t kWaves = kKppFallbackThreads / kWave;
   __shared__ double wsum[kWaves];
   __shared__ double carry;
   __shared__ FoldChunk lch[kWave];
   __shared__ __attribute__((aligned(16))) float buf[kFoldChunk];
-  const uint32_t m = blockIdx.x;
-  KppState& S = st[m];
-  // Every thread reads the flags here; thread 0 rewrites them only at the
-  // end, after the block barriers below.
-  if (S.err || !S.fallback) return;
-  const float* wm = w + (uint64_t)m * n;
-  double* pm = pre + (uint64_t)m * nc;
-  FoldChunk* cm = chunks + (uint64_t)m * nc;
   const uint32_t lane = threadIdx.x % kWave, wv = threadIdx.x / kWave;
   for (uint32_t j = wv; j < nc; j += kWaves) {
     const double cs = fold_chunk_sum_wave(wm, n, j);
@@ -298,6 +293,18 @@ __global__ __launch_bounds__(kKppFallbackThreads) void kpp_fallback_kernel(
     S.chosen = (uint32_t)found;
     S.fallback = 0;
   }
+}
+
+__global__ __launch_bounds__(kKppFallbackThreads) void kpp_fallback_kernel(
+    const float* __restrict__ w, KppState* __restrict__ st, uint64_t n, double* __restrict__ pre,
+    FoldChunk* __restrict__ chunks, uint32_t nc) {
+  const uint32_t m = blockIdx.x;
+  KppState& S = st[m];
+  // Every thread reads the flags here; the body rewrites them only at the
+  // end, after its block barriers.
+  if (S.err || !S.fallback) return;
+  kpp_fallback_block(w + (uint64_t)m * n, n, S, pre + (uint64_t)m * nc,
+                     chunks + (uint64_t)m * nc, nc);
 }
 
 // Seeds every subspace's stream with seed +% m and draws the first row.

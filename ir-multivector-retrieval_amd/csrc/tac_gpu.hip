@@ -21,6 +21,8 @@
 #include "kmeanspp.hpp"
 #include "storage_kernels.hpp"
 #include "query_kernels.hpp"
+#include "tac_kernels.hpp"
+#include "tac_phases.hpp"
 
 #include <hip/hip_runtime.h>
 
@@ -85,6 +87,11 @@ struct DeviceState {
   Buffer xs, codes, e, hist, counts, start, sorted, flags, scal, trace, io_in, io_out, io_cb,
       io_init, counter, kpp_state, kpp_w, kpp_bsum, kpp_bad, status, io_aux, io_out2, scan_sums,
       io_x1, io_x2, io_x3, crc_tx, fold_pre, fold_chunks;
+  // token-aware clustering
+  Buffer tac_v, tac_idx, tac_offs, tac_G, tac_spreads, tac_w, tac_e, tac_code, tac_sorted,
+      tac_tsum, tac_hist, tac_counts, tac_start, tac_C, tac_pre, tac_fch, tac_st, tac_bad,
+      tac_done, tac_iters, tac_wcss, tac_prev, tac_empties, tac_assign, tac_probs, tac_tiles,
+      tac_chl, tac_cprob;
   bool crc_tx_ready = false;
   // measurement
   std::vector<hipEvent_t> events;
@@ -648,7 +655,11 @@ const char *kNames[] = {"Ok",
                         "TableSizeMismatch",
                         "DocOutOfRange",
                         "DocLayoutCorrupt",
-                        "BufferTooSmall"};
+                        "BufferTooSmall",
+                        "BudgetTooSmall",
+                        "BudgetTooLarge",
+                        "InvalidThresholds",
+                        "EmptyTokenDump"};
 
 }  // namespace
 
@@ -748,7 +759,14 @@ int tac_gpu_release_workspace(void) {
                     &ds->io_in,     &ds->io_out,  &ds->io_cb,     &ds->io_init,  &ds->counter,
                     &ds->kpp_state, &ds->kpp_w,   &ds->kpp_bsum,  &ds->kpp_bad,  &ds->status,
                     &ds->io_aux,    &ds->io_out2, &ds->scan_sums, &ds->io_x1,    &ds->io_x2,
-                    &ds->io_x3,     &ds->crc_tx,  &ds->fold_pre,  &ds->fold_chunks};
+                    &ds->io_x3,     &ds->crc_tx,  &ds->fold_pre,  &ds->fold_chunks,
+                    &ds->tac_v,     &ds->tac_idx, &ds->tac_offs,  &ds->tac_G,
+                    &ds->tac_spreads, &ds->tac_w, &ds->tac_e,     &ds->tac_code,
+                    &ds->tac_sorted, &ds->tac_tsum, &ds->tac_hist, &ds->tac_counts,
+                    &ds->tac_start, &ds->tac_C,   &ds->tac_pre,   &ds->tac_fch,
+                    &ds->tac_st,    &ds->tac_bad, &ds->tac_done,  &ds->tac_iters,
+                    &ds->tac_wcss,  &ds->tac_prev, &ds->tac_empties, &ds->tac_assign,
+                    &ds->tac_probs, &ds->tac_tiles, &ds->tac_chl, &ds->tac_cprob};
   ds->crc_tx_ready = false;
   for (Buffer *b : bufs) {
     if (b->ptr) HIP_TRY(hipFree(b->ptr));
@@ -1470,6 +1488,365 @@ int tac_refine(const tac_doc_index *index, const float *table, uint64_t table_le
     return st;
   HIP_TRY(hipMemcpyAsync(scores_out, d_scores, pieces[8], hipMemcpyDeviceToHost, s));
   HIP_TRY(hipStreamSynchronize(s));
+  return end_call(*ds, s);
+}
+
+}  // extern "C"
+
+// ---- token-aware clustering (src/tac/tac.zig:563-830) -------------------------
+
+namespace {
+
+template <typename T>
+int upload_vec(DeviceState &ds, Buffer &b, const std::vector<T> &v, hipStream_t s) {
+  const size_t bytes = (v.empty() ? 1 : v.size()) * sizeof(T);
+  if (int st = ensure(ds, b, bytes)) return st;
+  if (!v.empty())
+    HIP_TRY(hipMemcpyAsync(b.ptr, v.data(), v.size() * sizeof(T), hipMemcpyHostToDevice, s));
+  return TAC_OK;
+}
+
+// The batch of per-token fits: problems ordered by k descending (degenerate
+// problems, which skip seeding, last), their tiles and wcss chunks.
+struct TacPlan {
+  std::vector<TacProblem> probs;
+  std::vector<TacTile> tiles;
+  std::vector<TacChunk> chunks;
+  std::vector<uint32_t> cprob;       // problem of every centroid
+  std::vector<uint32_t> token;       // token id of every problem
+  std::vector<uint32_t> tiles_upto;  // [c]: tiles of problems still seeding in round c
+  std::vector<uint32_t> probs_upto;  // [c]: problems with more than c seeds
+  uint64_t hist_total = 0;
+  uint32_t kmax = 0;      // largest k of a non-degenerate problem
+};
+
+int tac_plan(const std::vector<uint32_t> &freqs, const std::vector<uint32_t> &offs,
+             const std::vector<uint32_t> &kappa, const std::vector<uint64_t> &goff,
+             uint64_t seed, uint32_t rt, uint64_t kappa_total, TacPlan *pl) {
+  for (uint32_t j = 0; j < (uint32_t)freqs.size(); ++j) {
+    if (kappa[j] == 0 || freqs[j] == 0) continue;
+    TacProblem p{};
+    p.off = offs[j];
+    p.n = freqs[j];
+    p.k = kappa[j];
+    p.goff = (uint32_t)goff[j];
+    p.seed = seed ^ (uint64_t)j;
+    p.degenerate = p.k >= p.n ? 1u : 0u;
+    pl->probs.push_back(p);
+    pl->token.push_back(j);
+  }
+  const size_t P = pl->probs.size();
+  std::vector<uint32_t> order(P);
+  for (size_t q = 0; q < P; ++q) order[q] = (uint32_t)q;
+  auto keff = [&](uint32_t q) { return pl->probs[q].degenerate ? 0u : pl->probs[q].k; };
+  std::stable_sort(order.begin(), order.end(),
+                   [&](uint32_t a, uint32_t b) { return keff(a) > keff(b); });
+  std::vector<TacProblem> probs(P);
+  std::vector<uint32_t> token(P);
+  for (size_t q = 0; q < P; ++q) {
+    probs[q] = pl->probs[order[q]];
+    token[q] = pl->token[order[q]];
+  }
+  pl->probs.swap(probs);
+  pl->token.swap(token);
+  pl->cprob.assign(kappa_total, 0);
+  uint32_t t0 = 0, c0 = 0;
+  for (uint32_t q = 0; q < (uint32_t)P; ++q) {
+    TacProblem &p = pl->probs[q];
+    p.tile0 = t0;
+    p.ntiles = (p.n + rt - 1) / rt;
+    p.chunk0 = c0;
+    p.nchunks = (p.n + kFoldChunk - 1) / kFoldChunk;
+    p.code_bits = p.k <= 1 ? 0u : 32u - (uint32_t)__builtin_clz(p.k - 1);
+    p.hist0 = pl->hist_total;
+    if (!p.degenerate) {
+      pl->hist_total += (uint64_t)p.ntiles * p.k;
+      if (p.k > pl->kmax) pl->kmax = p.k;
+    }
+    for (uint32_t t = 0; t < p.ntiles; ++t) pl->tiles.push_back(TacTile{q, t * rt});
+    for (uint32_t j = 0; j < p.nchunks; ++j) pl->chunks.push_back(TacChunk{q, j});
+    for (uint32_t c = 0; c < p.k; ++c) pl->cprob[(uint64_t)p.goff + c] = q;
+    t0 += p.ntiles;
+    c0 += p.nchunks;
+  }
+  // prefixes for the k-means++ rounds (k descending)
+  pl->tiles_upto.assign((size_t)pl->kmax + 1, 0);
+  pl->probs_upto.assign((size_t)pl->kmax + 1, 0);
+  for (uint32_t q = 0; q < (uint32_t)P; ++q) {
+    const TacProblem &p = pl->probs[q];
+    if (p.degenerate) break;
+    for (uint32_t c = 0; c < p.k && c <= pl->kmax; ++c) {
+      pl->tiles_upto[c] = p.tile0 + p.ntiles;
+      pl->probs_upto[c] = q + 1;
+    }
+  }
+  return TAC_OK;
+}
+
+int tac_cluster_core(DeviceState &ds, hipStream_t s, const uint32_t *ids, uint64_t N,
+                     const float *vectors, uint32_t dim, const tac_cluster_params &prm,
+                     uint64_t nd, float *cent_out, uint32_t *assign_out, uint32_t *kpt_out,
+                     float *wcss_out) {
+  const uint32_t rt = tac_rows_per_tile(dim);
+  if (rt < 64 || dim > 64u * kTacSpreadPer) return TAC_ERR_UNSUPPORTED;
+  // 32-bit row ids; the gather grid stays below 2^31 blocks
+  if (N > 0xFFFFFFFFull || (uint64_t)N * dim > (1ull << 38) || nd > 0x7FFFFFFFull)
+    return TAC_ERR_UNSUPPORTED;
+  int st;
+  // CSR grouping by token id, ascending input order inside a token (tac.zig:575-602)
+  std::vector<uint32_t> freqs(nd, 0), offs(nd + 1, 0), idx(N);
+  for (uint64_t i = 0; i < N; ++i) freqs[ids[i]] += 1;
+  for (uint64_t j = 0; j < nd; ++j) offs[j + 1] = offs[j] + freqs[j];
+  {
+    std::vector<uint32_t> cur(offs.begin(), offs.end() - 1);
+    for (uint64_t i = 0; i < N; ++i) idx[cur[ids[i]]++] = (uint32_t)i;
+  }
+  const size_t vbytes = (size_t)N * dim * sizeof(float);
+  if ((st = ensure(ds, ds.tac_v, vbytes)) || (st = ensure(ds, ds.tac_G, vbytes)) ||
+      (st = upload_vec(ds, ds.tac_idx, idx, s)) || (st = upload_vec(ds, ds.tac_offs, offs, s)) ||
+      (st = ensure(ds, ds.tac_spreads, nd * sizeof(float))))
+    return st;
+  HIP_TRY(hipMemcpyAsync(ds.tac_v.ptr, vectors, vbytes, hipMemcpyHostToDevice, s));
+  float *G = as<float>(ds.tac_G);
+  const uint64_t nf = (uint64_t)N * dim;
+  tac_gather_kernel<<<(unsigned)((nf + 255) / 256), 256, 0, s>>>(
+      as<float>(ds.tac_v), as<uint32_t>(ds.tac_idx), G, N, dim);
+  LAUNCH_TRY("tac_gather_kernel");
+  tac_spread_kernel<<<(unsigned)nd, kWave, dim * sizeof(float), s>>>(
+      G, as<uint32_t>(ds.tac_offs), dim, as<float>(ds.tac_spreads));
+  LAUNCH_TRY("tac_spread_kernel");
+  std::vector<float> spreads(nd);
+  HIP_TRY(hipMemcpyAsync(spreads.data(), ds.tac_spreads.ptr, nd * sizeof(float),
+                         hipMemcpyDeviceToHost, s));
+  HIP_TRY(hipStreamSynchronize(s));
+
+  // budgets (tac.zig:641-668)
+  std::vector<uint32_t> kappa(nd, 0);
+  const tacphase::Params pp{prm.kappa_total, prm.mu, prm.tau, prm.epsilon, prm.theta};
+  if ((st = tacphase::allocate(freqs, spreads, kappa, pp))) return st;
+  for (uint64_t j = 0; j < nd; ++j)
+    if (freqs[j] > 0 && kappa[j] == 0) return TAC_ERR_BUDGET_TOO_SMALL;
+  std::vector<uint64_t> goff(nd + 1, 0);
+  for (uint64_t j = 0; j < nd; ++j) goff[j + 1] = goff[j] + kappa[j];
+  if (goff[nd] != prm.kappa_total) return TAC_ERR_BUDGET_TOO_SMALL;
+  const uint64_t K = prm.kappa_total;
+
+  TacPlan pl;
+  if ((st = tac_plan(freqs, offs, kappa, goff, prm.seed, rt, K, &pl))) return st;
+  if (pl.kmax > kTacMaxCodes) return TAC_ERR_UNSUPPORTED;
+  const uint32_t P = (uint32_t)pl.probs.size();
+  const uint32_t NT = (uint32_t)pl.tiles.size(), NCH = (uint32_t)pl.chunks.size();
+  std::vector<uint32_t> done0(P);
+  for (uint32_t q = 0; q < P; ++q) done0[q] = pl.probs[q].degenerate;
+  if ((st = upload_vec(ds, ds.tac_probs, pl.probs, s)) ||
+      (st = upload_vec(ds, ds.tac_tiles, pl.tiles, s)) ||
+      (st = upload_vec(ds, ds.tac_chl, pl.chunks, s)) ||
+      (st = upload_vec(ds, ds.tac_cprob, pl.cprob, s)) ||
+      (st = upload_vec(ds, ds.tac_done, done0, s)) ||
+      (st = ensure(ds, ds.tac_w, N * sizeof(float))) ||
+      (st = ensure(ds, ds.tac_e, N * sizeof(float))) ||
+      (st = ensure(ds, ds.tac_code, N * sizeof(uint32_t))) ||
+      (st = ensure(ds, ds.tac_sorted, N * sizeof(uint32_t))) ||
+      (st = ensure(ds, ds.tac_assign, N * sizeof(uint32_t))) ||
+      (st = ensure(ds, ds.tac_tsum, (size_t)NT * sizeof(double))) ||
+      (st = ensure(ds, ds.tac_hist, (pl.hist_total + 1) * sizeof(uint32_t))) ||
+      (st = ensure(ds, ds.tac_counts, K * sizeof(uint32_t))) ||
+      (st = ensure(ds, ds.tac_start, K * sizeof(uint32_t))) ||
+      (st = ensure(ds, ds.tac_C, K * dim * sizeof(float))) ||
+      (st = ensure(ds, ds.tac_pre, (size_t)NCH * sizeof(double))) ||
+      (st = ensure(ds, ds.tac_fch, (size_t)NCH * sizeof(FoldChunk))) ||
+      (st = ensure(ds, ds.tac_st, (size_t)P * sizeof(KppState))) ||
+      (st = ensure(ds, ds.tac_bad, (size_t)P * sizeof(uint32_t))) ||
+      (st = ensure(ds, ds.tac_iters, (size_t)P * sizeof(uint32_t))) ||
+      (st = ensure(ds, ds.tac_wcss, (size_t)P * sizeof(float))) ||
+      (st = ensure(ds, ds.tac_prev, (size_t)P * sizeof(float))) ||
+      (st = ensure(ds, ds.tac_empties, (size_t)P * sizeof(uint32_t))))
+    return st;
+  float *w = as<float>(ds.tac_w), *e = as<float>(ds.tac_e), *C = as<float>(ds.tac_C);
+  uint32_t *code = as<uint32_t>(ds.tac_code), *sorted = as<uint32_t>(ds.tac_sorted);
+  uint32_t *done = as<uint32_t>(ds.tac_done), *bad = as<uint32_t>(ds.tac_bad);
+  uint32_t *hist = as<uint32_t>(ds.tac_hist), *counts = as<uint32_t>(ds.tac_counts);
+  uint32_t *start = as<uint32_t>(ds.tac_start), *iters = as<uint32_t>(ds.tac_iters);
+  float *wcss = as<float>(ds.tac_wcss), *prev = as<float>(ds.tac_prev);
+  double *tsum = as<double>(ds.tac_tsum), *pre = as<double>(ds.tac_pre);
+  FoldChunk *fch = as<FoldChunk>(ds.tac_fch);
+  KppState *kst = as<KppState>(ds.tac_st);
+  const TacProblem *probs = as<TacProblem>(ds.tac_probs);
+  const TacTile *tiles = as<TacTile>(ds.tac_tiles);
+  const TacChunk *chl = as<TacChunk>(ds.tac_chl);
+  HIP_TRY(hipMemsetAsync(code, 0, N * sizeof(uint32_t), s));
+  HIP_TRY(hipMemsetAsync(iters, 0, (size_t)P * sizeof(uint32_t), s));
+  HIP_TRY(hipMemsetAsync(ds.tac_empties.ptr, 0, (size_t)P * sizeof(uint32_t), s));
+  HIP_TRY(hipMemsetAsync(wcss, 0, (size_t)P * sizeof(float), s));
+  if (P == 0) return TAC_ERR_BUDGET_TOO_SMALL;  // unreachable: some token has rows
+
+  const size_t rows_lds = (size_t)rt * (dim + 1);
+  uint32_t chunk_c = (uint32_t)((16384 - rows_lds) / dim);
+  if (chunk_c > 64) chunk_c = 64;
+  const size_t upd_lds = (rows_lds + dim) * sizeof(float);
+  const size_t asg_lds = (rows_lds + (size_t)chunk_c * dim) * sizeof(float);
+  const size_t code_lds = (size_t)(pl.kmax ? pl.kmax : 1) * sizeof(uint32_t);
+  const bool profile = g_profile;
+  hipEvent_t ev0 = nullptr, ev1 = nullptr, ev2 = nullptr;
+  if (profile) {
+    if ((st = event_at(ds, 0, &ev0)) || (st = event_at(ds, 1, &ev1)) ||
+        (st = event_at(ds, 2, &ev2)))
+      return st;
+    HIP_TRY(hipEventRecord(ev0, s));
+  }
+
+  tac_degenerate_kernel<<<P, 256, 0, s>>>(G, probs, P, C, code, wcss, dim);
+  LAUNCH_TRY("tac_degenerate_kernel");
+  // k-means++ seeding (kmeans.zig:106-136), round c for every problem with k > c
+  tac_kpp_init_kernel<<<(P + 63) / 64, 64, 0, s>>>(probs, P, kst, bad);
+  LAUNCH_TRY("tac_kpp_init_kernel");
+  const char *exact_env = getenv("TAC_GPU_KPP_EXACT");
+  const uint32_t exact_only = exact_env != nullptr && exact_env[0] == '1';
+  for (uint32_t c = 0; c < pl.kmax; ++c) {
+    const uint32_t T = pl.tiles_upto[c];
+    if (T == 0) break;
+    if (dim == 64)
+      tac_kpp_update_kernel<64><<<T, rt, upd_lds, s>>>(G, w, tsum, bad, kst, probs, tiles, C, c,
+                                                       dim);
+    else if (dim == 128)
+      tac_kpp_update_kernel<128><<<T, rt, upd_lds, s>>>(G, w, tsum, bad, kst, probs, tiles, C,
+                                                        c, dim);
+    else
+      tac_kpp_update_kernel<0><<<T, rt, upd_lds, s>>>(G, w, tsum, bad, kst, probs, tiles, C, c,
+                                                      dim);
+    LAUNCH_TRY("tac_kpp_update_kernel");
+    const uint32_t P2 = c + 1 < pl.kmax ? pl.probs_upto[c + 1] : 0;
+    if (P2 == 0) continue;
+    tac_kpp_select_kernel<<<P2, rt, 0, s>>>(w, tsum, bad, kst, probs, exact_only);
+    LAUNCH_TRY("tac_kpp_select_kernel");
+    tac_kpp_fallback_kernel<<<P2, kKppFallbackThreads, 0, s>>>(w, kst, probs, pre, fch);
+    LAUNCH_TRY("tac_kpp_fallback_kernel");
+  }
+  {
+    std::vector<KppState> h(P);
+    HIP_TRY(hipMemcpyAsync(h.data(), kst, (size_t)P * sizeof(KppState), hipMemcpyDeviceToHost,
+                           s));
+    HIP_TRY(hipStreamSynchronize(s));
+    // the reference fits tokens in id order and stops at the first error
+    uint32_t first_tok = 0xFFFFFFFFu;
+    int first_err = 0;
+    for (uint32_t q = 0; q < P; ++q)
+      if (h[q].err && pl.token[q] < first_tok) {
+        first_tok = pl.token[q];
+        first_err = h[q].err;
+      }
+    if (first_err) return first_err;
+  }
+  if (profile) HIP_TRY(hipEventRecord(ev1, s));
+
+  // Lloyd iterations (kmeans.zig:149-224) for every problem not yet converged
+  for (uint32_t t = 0; t < prm.max_iters; ++t) {
+    if (dim == 64)
+      tac_assign_kernel<64><<<NT, rt, asg_lds, s>>>(G, C, probs, tiles, done, code, e, dim,
+                                                    chunk_c);
+    else if (dim == 128)
+      tac_assign_kernel<128><<<NT, rt, asg_lds, s>>>(G, C, probs, tiles, done, code, e, dim,
+                                                     chunk_c);
+    else
+      tac_assign_kernel<0><<<NT, rt, asg_lds, s>>>(G, C, probs, tiles, done, code, e, dim,
+                                                   chunk_c);
+    LAUNCH_TRY("tac_assign_kernel");
+    tac_hist_kernel<<<NT, rt, code_lds, s>>>(code, probs, tiles, done, hist);
+    LAUNCH_TRY("tac_hist_kernel");
+    tac_scan_kernel<<<P, 256, 0, s>>>(hist, probs, done, counts, start);
+    LAUNCH_TRY("tac_scan_kernel");
+    tac_scatter_kernel<<<NT, rt, code_lds, s>>>(code, hist, start, probs, tiles, done, sorted);
+    LAUNCH_TRY("tac_scatter_kernel");
+    tac_fold_kernel<<<(unsigned)((K + 3) / 4), 256, 0, s>>>(G, sorted, counts, start,
+                                                           as<uint32_t>(ds.tac_cprob), probs,
+                                                           done, C, (uint32_t)K, dim);
+    LAUNCH_TRY("tac_fold_kernel");
+    tac_chunk_sums_kernel<<<(NCH + 3) / 4, 256, 0, s>>>(e, probs, chl, NCH, done, pre);
+    tac_chunk_prefix_kernel<<<P, 256, 0, s>>>(pre, probs, done);
+    tac_quantize_kernel<<<(NCH + 3) / 4, 256, 0, s>>>(e, pre, probs, chl, NCH, done, fch);
+    tac_wcss_apply_kernel<<<P, kWave, 0, s>>>(e, fch, probs, done, wcss);
+    LAUNCH_TRY("tac wcss kernels");
+    tac_reseed_kernel<<<P, 256, 0, s>>>(G, e, counts, probs, done, C,
+                                        as<uint32_t>(ds.tac_empties), dim);
+    LAUNCH_TRY("tac_reseed_kernel");
+    tac_converge_kernel<<<(P + 255) / 256, 256, 0, s>>>(wcss, prev, done, iters, P, t, prm.tol);
+    LAUNCH_TRY("tac_converge_kernel");
+  }
+  if (profile) HIP_TRY(hipEventRecord(ev2, s));
+  tac_output_kernel<<<NT, rt, 0, s>>>(code, as<uint32_t>(ds.tac_idx), probs, tiles,
+                                     as<uint32_t>(ds.tac_assign));
+  LAUNCH_TRY("tac_output_kernel");
+  std::vector<float> pw(P);
+  HIP_TRY(hipMemcpyAsync(assign_out, ds.tac_assign.ptr, N * sizeof(uint32_t),
+                         hipMemcpyDeviceToHost, s));
+  HIP_TRY(hipMemcpyAsync(cent_out, C, K * dim * sizeof(float), hipMemcpyDeviceToHost, s));
+  HIP_TRY(hipMemcpyAsync(pw.data(), wcss, (size_t)P * sizeof(float), hipMemcpyDeviceToHost, s));
+  HIP_TRY(hipStreamSynchronize(s));
+  if (profile) {
+    float a = 0.0f, b = 0.0f;
+    HIP_TRY(hipEventElapsedTime(&a, ev0, ev1));
+    HIP_TRY(hipEventElapsedTime(&b, ev1, ev2));
+    std::lock_guard<std::mutex> g(g_profile_mu);
+    g_prof.cluster_kpp_ms += a;
+    g_prof.cluster_lloyd_ms += b;
+    g_prof.cluster_calls += 1;
+  }
+  for (uint64_t j = 0; j < nd; ++j) kpt_out[j] = kappa[j];
+  // wcss_total: the per-token wcss in token order, grouped by thread slices
+  std::vector<float> tok_w(nd, 0.0f);
+  std::vector<uint8_t> has(nd, 0);
+  for (uint32_t q = 0; q < P; ++q) {
+    tok_w[pl.token[q]] = pw[q];
+    has[pl.token[q]] = 1;
+  }
+  const uint32_t nt = prm.n_threads > 1 ? prm.n_threads : 1;
+  const uint64_t chunk = nt > 1 ? (nd + nt - 1) / nt : nd;
+  std::vector<float> parts(nt, 0.0f);
+  for (uint64_t j = 0; j < nd; ++j)
+    if (has[j]) parts[nt > 1 ? j / chunk : 0] += tok_w[j];
+  float total = 0.0f;
+  for (uint32_t q = 0; q < nt; ++q) total += parts[q];
+  *wcss_out = total;
+  return TAC_OK;
+}
+
+}  // namespace
+
+extern "C" {
+
+int tac_cluster_flat(const uint32_t *token_ids, uint64_t n_tokens, const float *vectors,
+                     uint64_t vectors_len, uint32_t dim, const tac_cluster_params *params,
+                     float *centroids_out, uint32_t *assignments_out,
+                     uint32_t *kappa_per_token_out, uint64_t kappa_per_token_len,
+                     float *wcss_total_out, uint64_t *n_distinct_out) {
+  if (!params) return TAC_ERR_INVALID_ARGUMENT;
+  // validation in the reference's order (tac.zig:570-573)
+  if (n_tokens == 0) return TAC_ERR_EMPTY_TOKEN_DUMP;
+  if (dim == 0) return TAC_ERR_INVALID_THRESHOLDS;
+  if (vectors_len != n_tokens * (uint64_t)dim) return TAC_ERR_INVALID_THRESHOLDS;
+  if (params->kappa_total == 0) return TAC_ERR_BUDGET_TOO_SMALL;
+  if (!token_ids || !vectors || !centroids_out || !assignments_out || !kappa_per_token_out ||
+      !wcss_total_out)
+    return TAC_ERR_INVALID_ARGUMENT;
+  uint32_t max_id = 0;
+  for (uint64_t i = 0; i < n_tokens; ++i)
+    if (token_ids[i] > max_id) max_id = token_ids[i];
+  const uint64_t nd = (uint64_t)max_id + 1;
+  if (n_distinct_out) *n_distinct_out = nd;
+  if (kappa_per_token_len < nd) return TAC_ERR_BUFFER_TOO_SMALL;
+  DeviceState *ds = nullptr;
+  int st;
+  if ((st = acquire_device(&ds, nullptr))) return st;
+  std::lock_guard<std::mutex> g(ds->mu);
+  hipStream_t s;
+  if ((st = resolve_stream(*ds, nullptr, &s))) return st;
+  if ((st = begin_call(*ds, s))) return st;
+  st = tac_cluster_core(*ds, s, token_ids, n_tokens, vectors, dim, *params, nd, centroids_out,
+                        assignments_out, kappa_per_token_out, wcss_total_out);
+  if (st) {
+    HIP_TRY(hipStreamSynchronize(s));
+    return st;
+  }
   return end_call(*ds, s);
 }
 

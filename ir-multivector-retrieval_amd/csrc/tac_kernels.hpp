@@ -1,0 +1,762 @@
+// tac_kernels.hpp — gfx950 kernels of token-aware clustering
+// (src/tac/tac.zig): the per-token Welford spreads (:604-638) and the batch of
+// per-token kmeans.fit calls (runOneTokenKmeans :458-513, kmeans.zig:67-242)
+// as one ragged engine.  Included once, by tac_gpu.hip, after kmeanspp.hpp.
+// Compiled with -ffp-contract=off: every operation rounds on its own.
+//
+// A problem is one token's fit: rows [off, off + n) of the token-grouped
+// matrix G (each token's vectors in ascending input order, as the reference
+// gathers them), centroids [goff, goff + k) of the global table.  Rows are
+// cut into tiles of rt rows and wcss chunks of kFoldChunk rows that never
+// cross a problem.  Problems are listed by k descending, so the problems (and
+// tiles) still seeding in k-means++ round c form a prefix of the lists.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+namespace tacgpu {
+
+struct TacProblem {
+  uint32_t off, n, k, goff;
+  uint32_t tile0, ntiles;    // tiles [tile0, tile0 + ntiles) of the tile list
+  uint32_t chunk0, nchunks;  // wcss chunks [chunk0, chunk0 + nchunks)
+  uint64_t hist0;            // ntiles * k tile-histogram counters
+  uint64_t seed;             // p.seed ^ token id
+  uint32_t code_bits;        // bits that tell the k codes apart
+  uint32_t degenerate;       // k >= n (kmeans.zig:88-104)
+};
+
+struct TacTile {
+  uint32_t prob, row0;  // row0: first row of the tile, relative to the problem
+};
+
+struct TacChunk {
+  uint32_t prob, j;  // j: chunk index within the problem
+};
+
+constexpr uint32_t kTacMaxCodes = 12288;   // k per problem: LDS counters of hist/scatter
+constexpr uint32_t kTacLdsFloats = 12288;  // staged rows: rt * (dim + 1) <= this
+
+// Rows per tile (= threads of the tile kernels) for a dimension; 0 beyond the
+// supported range.
+__host__ __device__ inline uint32_t tac_rows_per_tile(uint32_t dim) {
+  for (uint32_t rt = 128; rt >= 16; rt /= 2)
+    if (rt * (dim + 1) <= kTacLdsFloats) return rt;
+  return 0;
+}
+
+// vec.l2sq (src/util/vec.zig:109-175) in the reference's order: dim 2 and 4
+// are left folds, dims 64 and 128 accumulate in 4 lanes chunk after chunk and
+// reduce ((a0 + a1) + a2) + a3, other dims accumulate in 16 lanes (the
+// x86-64 AVX-512 lane count), reduce in lane order and fold the tail.  DIMC
+// fixes the dimension at compile time (0: runtime d).
+template <int DIMC>
+__device__ __forceinline__ float tac_l2sq(const float* a, const float* b, uint32_t d_rt) {
+  const uint32_t d = DIMC ? (uint32_t)DIMC : d_rt;
+  if (d == 2) {
+    const float d0 = a[0] - b[0];
+    const float d1 = a[1] - b[1];
+    return d0 * d0 + d1 * d1;
+  }
+  if (d == 4) {
+    float s = 0.0f;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const float t = a[i] - b[i];
+      s = s + t * t;
+    }
+    return s;
+  }
+  if (d == 64 || d == 128) {
+    float acc0 = 0.0f, acc1 = 0.0f, acc2 = 0.0f, acc3 = 0.0f;
+#pragma unroll
+    for (uint32_t c = 0; c < d; c += 4) {
+      const float t0 = a[c] - b[c], t1 = a[c + 1] - b[c + 1];
+      const float t2 = a[c + 2] - b[c + 2], t3 = a[c + 3] - b[c + 3];
+      acc0 = acc0 + t0 * t0;
+      acc1 = acc1 + t1 * t1;
+      acc2 = acc2 + t2 * t2;
+      acc3 = acc3 + t3 * t3;
+    }
+    return ((acc0 + acc1) + acc2) + acc3;
+  }
+  float acc[16];
+#pragma unroll
+  for (int j = 0; j < 16; ++j) acc[j] = 0.0f;
+  uint32_t i = 0;
+  for (; i + 16 <= d; i += 16) {
+#pragma unroll
+    for (int j = 0; j < 16; ++j) {
+      const float t = a[i + j] - b[i + j];
+      acc[j] = acc[j] + t * t;
+    }
+  }
+  float sum = acc[0];
+#pragma unroll
+  for (int j = 1; j < 16; ++j) sum = sum + acc[j];
+  for (; i < d; ++i) {
+    const float t = a[i] - b[i];
+    sum = sum + t * t;
+  }
+  return sum;
+}
+
+// ---------------------------------------------------------------------------
+// Gather: G[q] = vectors[idx[q]] (tac.zig:466-475), one thread per float.
+// ---------------------------------------------------------------------------
+__global__ __launch_bounds__(256) void tac_gather_kernel(const float* __restrict__ v,
+                                                         const uint32_t* __restrict__ idx,
+                                                         float* __restrict__ G, uint64_t rows,
+                                                         uint32_t dim) {
+  const uint64_t f = (uint64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (f >= rows * dim) return;
+  const uint64_t q = f / dim;
+  G[f] = v[(uint64_t)idx[q] * dim + f % dim];
+}
+
+// ---------------------------------------------------------------------------
+// Per-token spread by Welford (tac.zig:611-632): one wave per token, lane =
+// dimension (strided beyond 64); the trace folds the dimensions in order and
+// is divided by the f32 count of rows.  dim <= 64 * kTacSpreadPer.
+// ---------------------------------------------------------------------------
+constexpr int kTacSpreadPer = 12;
+
+__global__ __launch_bounds__(kWave) void tac_spread_kernel(const float* __restrict__ G,
+                                                           const uint32_t* __restrict__ offs,
+                                                           uint32_t dim,
+                                                           float* __restrict__ spreads) {
+  extern __shared__ float m2s[];  // [dim]
+  const uint32_t j = blockIdx.x, lane = threadIdx.x;
+  const uint32_t lo = offs[j], hi = offs[j + 1];
+  if (hi == lo) {
+    if (lane == 0) spreads[j] = 0.0f;
+    return;
+  }
+  float mean[kTacSpreadPer], m2[kTacSpreadPer];
+#pragma unroll
+  for (int u = 0; u < kTacSpreadPer; ++u) {
+    mean[u] = 0.0f;
+    m2[u] = 0.0f;
+  }
+  float count = 0.0f;
+  for (uint32_t q = lo; q < hi; ++q) {
+    const float* v = G + (uint64_t)q * dim;
+    count = count + 1.0f;
+    const float inv = 1.0f / count;
+#pragma unroll
+    for (int u = 0; u < kTacSpreadPer; ++u) {
+      const uint32_t d = lane + 64u * u;
+      if (d < dim) {
+        const float x = v[d];
+        const float old = mean[u];
+        const float delta = x - old;
+        mean[u] = old + delta * inv;
+        m2[u] = m2[u] + delta * (x - mean[u]);
+      }
+    }
+  }
+#pragma unroll
+  for (int u = 0; u < kTacSpreadPer; ++u) {
+    const uint32_t d = lane + 64u * u;
+    if (d < dim) m2s[d] = m2[u];
+  }
+  __syncthreads();
+  if (lane == 0) {
+    float trace = 0.0f;
+    for (uint32_t d = 0; d < dim; ++d) trace = trace + m2s[d];
+    spreads[j] = trace / (float)(hi - lo);
+  }
+}
+
+// ---------------------------------------------------------------------------
+// Degenerate problems (k >= n, kmeans.zig:88-104): centroid c = row
+// min(c, n - 1), assignment i = i, wcss 0, no iterations.  One block each.
+// ---------------------------------------------------------------------------
+__global__ __launch_bounds__(256) void tac_degenerate_kernel(
+    const float* __restrict__ G, const TacProblem* __restrict__ probs, uint32_t P,
+    float* __restrict__ C, uint32_t* __restrict__ code, float* __restrict__ wcss,
+    uint32_t dim) {
+  const uint32_t p = blockIdx.x;
+  if (p >= P || !probs[p].degenerate) return;
+  const TacProblem pr = probs[p];
+  for (uint64_t f = threadIdx.x; f < (uint64_t)pr.k * dim; f += blockDim.x) {
+    const uint32_t c = (uint32_t)(f / dim), d = (uint32_t)(f % dim);
+    const uint32_t src = c < pr.n ? c : pr.n - 1;
+    C[((uint64_t)pr.goff + c) * dim + d] = G[((uint64_t)pr.off + src) * dim + d];
+  }
+  for (uint32_t i = threadIdx.x; i < pr.n; i += blockDim.x) code[pr.off + i] = i;
+  if (threadIdx.x == 0) wcss[p] = 0.0f;
+}
+
+// Stage rows [row0, row0 + rt) of a problem (zeros past its end) into LDS
+// with stride ld; every thread of the block takes part.
+__device__ __forceinline__ void tac_stage_rows(const float* __restrict__ G, const TacProblem& pr,
+                                               uint32_t row0, uint32_t rt, uint32_t dim,
+                                               uint32_t ld, float* xr) {
+  const uint32_t rows = pr.n - row0 < rt ? pr.n - row0 : rt;
+  const float* src = G + ((uint64_t)pr.off + row0) * dim;
+  for (uint32_t f = threadIdx.x; f < rows * dim; f += blockDim.x)
+    xr[(f / dim) * ld + f % dim] = src[f];
+}
+
+// ---------------------------------------------------------------------------
+// k-means++ (kmeans.zig:106-136) per problem, with the PRNG seeded from
+// p.seed ^ token id.
+// ---------------------------------------------------------------------------
+__global__ void tac_kpp_init_kernel(const TacProblem* __restrict__ probs, uint32_t P,
+                                    KppState* __restrict__ st, uint32_t* __restrict__ bad) {
+  const uint32_t p = blockIdx.x * blockDim.x + threadIdx.x;
+  if (p >= P) return;
+  KppState S;
+  uint64_t sm = probs[p].seed;
+  for (int q = 0; q < 4; ++q) S.s[q] = kpp_splitmix(&sm);
+  S.chosen = probs[p].degenerate ? 0u : (uint32_t)kpp_uint_less_than(S.s, probs[p].n);
+  S.r = 0.0;
+  S.fallback = 0;
+  S.err = 0;
+  S.pad = 0;
+  st[p] = S;
+  bad[p] = 0;
+}
+
+// Round c over the tiles of problems with k > c (a prefix of the tile list):
+// centroid c = the chosen row; w = l2sq to it (round 0) or min(w, l2sq) on
+// strict < (kmeans.zig:129-135); weights validated (rng.zig:62); one f64
+// partial sum per tile.
+template <int DIMC>
+__global__ void tac_kpp_update_kernel(const float* __restrict__ G, float* __restrict__ w,
+                                      double* __restrict__ tsum, uint32_t* __restrict__ bad,
+                                      const KppState* __restrict__ st,
+                                      const TacProblem* __restrict__ probs,
+                                      const TacTile* __restrict__ tiles, float* __restrict__ C,
+                                      uint32_t c, uint32_t dim_rt) {
+  const uint32_t dim = DIMC ? (uint32_t)DIMC : dim_rt;
+  extern __shared__ __attribute__((aligned(16))) float tlds[];
+  const uint32_t rt = blockDim.x, ld = dim + 1;
+  float* xr = tlds;             // [rt][ld]
+  float* crow = tlds + rt * ld;  // [dim]
+  __shared__ double part[4];
+  const TacTile tl = tiles[blockIdx.x];
+  const TacProblem pr = probs[tl.prob];
+  if (st[tl.prob].err) return;
+  const uint32_t chosen = st[tl.prob].chosen;
+  for (uint32_t d = threadIdx.x; d < dim; d += rt) {
+    const float v = G[((uint64_t)pr.off + chosen) * dim + d];
+    crow[d] = v;
+    if (tl.row0 == 0) C[((uint64_t)pr.goff + c) * dim + d] = v;
+  }
+  tac_stage_rows(G, pr, tl.row0, rt, dim, ld, xr);
+  __syncthreads();
+  const uint32_t i = tl.row0 + threadIdx.x;
+  double acc = 0.0;
+  bool invalid = false;
+  if (i < pr.n) {
+    const float d = tac_l2sq<DIMC>(xr + threadIdx.x * ld, crow, dim);
+    float* wi = w + pr.off + i;
+    float v = d;
+    if (c > 0) {
+      const float old = *wi;
+      v = d < old ? d : old;
+      if (d < old) *wi = d;
+    } else {
+      *wi = d;
+    }
+    invalid = !(v >= 0.0f && v <= 3.402823466e38f);
+    acc = (double)v;
+  }
+  for (int off = 32; off > 0; off >>= 1) acc += __shfl_down(acc, off, 64);
+  if (threadIdx.x % 64 == 0) part[threadIdx.x / 64] = acc;
+  if (__any(invalid) && threadIdx.x % 64 == 0) atomicOr(&bad[tl.prob], 1u);
+  __syncthreads();
+  if (threadIdx.x == 0) {
+    double t = 0.0;
+    for (uint32_t q = 0; q < (rt + 63) / 64; ++q) t += part[q];
+    tsum[blockIdx.x] = t;
+  }
+}
+
+// Draw for round c + 1, one block of rt threads per problem with k > c + 1
+// (a prefix of the problem list): the same decision as kpp_select_kernel,
+// over the problem's tile sums and then one weight per thread inside the
+// candidate tile.  Order-free sums; the candidate is kept only when the draw
+// clears the error bands (kpp_decides), otherwise `fallback` is raised.
+__global__ __launch_bounds__(128) void tac_kpp_select_kernel(
+    const float* __restrict__ w, const double* __restrict__ tsum, uint32_t* __restrict__ bad,
+    KppState* __restrict__ st, const TacProblem* __restrict__ probs, uint32_t exact_only) {
+  __shared__ double s_before, s_total, s_u, s_r, carry;
+  __shared__ uint32_t s_tile, s_first, s_stop;
+  __shared__ double wsum[2];
+  const uint32_t p = blockIdx.x, rt = blockDim.x;
+  const TacProblem pr = probs[p];
+  KppState& S = st[p];
+  const uint32_t lane = threadIdx.x % 64, wv = threadIdx.x / 64, nw = (rt + 63) / 64;
+  const double* bm = tsum + pr.tile0;
+  const uint32_t NB = pr.ntiles;
+  if (threadIdx.x == 0) {
+    s_stop = 1;
+    s_first = 0xFFFFFFFFu;
+    s_tile = NB;
+    carry = 0.0;
+    if (!S.err) {
+      S.fallback = 0;
+      if (bad[p])
+        S.err = 9;  // NonFinite
+      else
+        s_stop = 0;
+    }
+  }
+  __syncthreads();
+  if (s_stop) return;
+  double part = 0.0;
+  for (uint32_t b = threadIdx.x; b < NB; b += rt) part += bm[b];
+  for (int off = 32; off > 0; off >>= 1) part += __shfl_down(part, off, 64);
+  if (lane == 0) wsum[wv] = part;
+  __syncthreads();
+  if (threadIdx.x == 0) {
+    double tot = 0.0;
+    for (uint32_t q = 0; q < nw; ++q) tot += wsum[q];
+    if (!(tot > 0.0)) {
+      S.err = 10;  // AllZero
+      s_stop = 1;
+    } else {
+      S.r = kpp_float64(S.s);
+      s_r = S.r;
+      s_total = tot;
+      s_u = S.r * tot;
+    }
+  }
+  __syncthreads();
+  if (s_stop) return;
+  const double ud = s_u;
+  for (uint32_t b0 = 0; b0 < NB; b0 += rt) {
+    const uint32_t b = b0 + threadIdx.x;
+    const double x = b < NB ? bm[b] : 0.0;
+    double incl = x;
+    for (int off = 1; off < 64; off <<= 1) {
+      const double o = __shfl_up(incl, off, 64);
+      if (lane >= (uint32_t)off) incl += o;
+    }
+    if (lane == 63 || threadIdx.x == rt - 1) wsum[wv] = incl;
+    __syncthreads();
+    double before = carry;
+    for (uint32_t q = 0; q < wv; ++q) before += wsum[q];
+    if (b < NB && ud < before + incl) atomicMin(&s_tile, b);
+    __syncthreads();
+    if (b == s_tile) s_before = before + (incl - x);
+    if (threadIdx.x == rt - 1) carry = before + incl;
+    __syncthreads();
+    if (s_tile != NB) break;
+  }
+  if (s_tile == NB || exact_only) {
+    if (threadIdx.x == 0) S.fallback = 1;  // u at or beyond the total: the tail rule decides
+    return;
+  }
+  const double r = s_r;
+  const uint64_t i = (uint64_t)s_tile * rt + threadIdx.x;  // tiles hold rt rows each
+  const double v = i < pr.n ? (double)w[pr.off + i] : 0.0;
+  double incl = v;
+  for (int off = 1; off < 64; off <<= 1) {
+    const double o = __shfl_up(incl, off, 64);
+    if (lane >= (uint32_t)off) incl += o;
+  }
+  if (lane == 63 || threadIdx.x == rt - 1) wsum[wv] = incl;
+  __syncthreads();
+  double base = s_before;
+  for (uint32_t q = 0; q < wv; ++q) base += wsum[q];
+  base += incl - v;  // exclusive prefix before weight i
+  const double u = r * s_total;
+  const double pi = base + v;
+  if (i < pr.n && u < pi) atomicMin(&s_first, threadIdx.x);
+  __syncthreads();
+  if (s_first == 0xFFFFFFFFu) {
+    if (threadIdx.x == 0) S.fallback = 1;
+    return;
+  }
+  if (threadIdx.x == s_first) {
+    if (kpp_decides(r, s_total, pr.n, i, base, pi))
+      S.chosen = (uint32_t)i;
+    else
+      S.fallback = 1;
+  }
+}
+
+// The exact sequential weightedSample for problems whose draw was
+// inconclusive (kpp_fallback_block over the problem's weights; the wcss
+// chunk scratch of the problem serves as its chunk scratch).
+__global__ __launch_bounds__(kKppFallbackThreads) void tac_kpp_fallback_kernel(
+    const float* __restrict__ w, KppState* __restrict__ st, const TacProblem* __restrict__ probs,
+    double* __restrict__ pre, FoldChunk* __restrict__ fchunks) {
+  const uint32_t p = blockIdx.x;
+  KppState& S = st[p];
+  if (S.err || !S.fallback) return;
+  const TacProblem pr = probs[p];
+  kpp_fallback_block(w + pr.off, pr.n, S, pre + pr.chunk0, fchunks + pr.chunk0, pr.nchunks);
+}
+
+// ---------------------------------------------------------------------------
+// Lloyd assignment (kmeans.zig:344-365): per row, vec.argmin over the
+// problem's centroids (first index on ties, strict <), min_to_any = that
+// distance.  One block per tile; the tile's rows sit in LDS (stride dim + 1),
+// centroids pass through LDS in chunks and are read as broadcasts.
+// ---------------------------------------------------------------------------
+template <int DIMC>
+__global__ void tac_assign_kernel(const float* __restrict__ G, const float* __restrict__ C,
+                                  const TacProblem* __restrict__ probs,
+                                  const TacTile* __restrict__ tiles,
+                                  const uint32_t* __restrict__ done, uint32_t* __restrict__ code,
+                                  float* __restrict__ e, uint32_t dim_rt, uint32_t chunk_c) {
+  const uint32_t dim = DIMC ? (uint32_t)DIMC : dim_rt;
+  extern __shared__ __attribute__((aligned(16))) float tlds[];
+  const uint32_t rt = blockDim.x, ld = dim + 1;
+  float* xr = tlds;             // [rt][ld]
+  float* cs = tlds + rt * ld;  // [chunk_c][dim]
+  const TacTile tl = tiles[blockIdx.x];
+  if (done[tl.prob]) return;
+  const TacProblem pr = probs[tl.prob];
+  tac_stage_rows(G, pr, tl.row0, rt, dim, ld, xr);
+  const float* xrow = xr + threadIdx.x * ld;
+  float best = 0.0f;
+  uint32_t bi = 0;
+  for (uint32_t c0 = 0; c0 < pr.k; c0 += chunk_c) {
+    const uint32_t cnt = pr.k - c0 < chunk_c ? pr.k - c0 : chunk_c;
+    __syncthreads();
+    const float* src = C + ((uint64_t)pr.goff + c0) * dim;
+    for (uint32_t f = threadIdx.x; f < cnt * dim; f += rt) cs[f] = src[f];
+    __syncthreads();
+    for (uint32_t q = 0; q < cnt; ++q) {
+      const float d = tac_l2sq<DIMC>(xrow, cs + q * dim, dim);
+      if (c0 + q == 0) {
+        best = d;  // vec.argmin starts from values[0]
+      } else if (d < best) {
+        best = d;
+        bi = c0 + q;
+      }
+    }
+  }
+  const uint32_t i = tl.row0 + threadIdx.x;
+  if (i < pr.n) {
+    code[pr.off + i] = bi;
+    e[pr.off + i] = best;
+  }
+}
+
+// ---------------------------------------------------------------------------
+// Stable grouping of each problem's rows by code, so that every cluster's
+// members are folded in ascending row order (kmeans.zig:177-184).
+// Step 1: tile histograms hist[hist0 + t * k + c].
+// ---------------------------------------------------------------------------
+__global__ void tac_hist_kernel(const uint32_t* __restrict__ code,
+                                const TacProblem* __restrict__ probs,
+                                const TacTile* __restrict__ tiles,
+                                const uint32_t* __restrict__ done, uint32_t* __restrict__ hist) {
+  extern __shared__ uint32_t hcnt[];  // [k]
+  const TacTile tl = tiles[blockIdx.x];
+  if (done[tl.prob]) return;
+  const TacProblem pr = probs[tl.prob];
+  for (uint32_t c = threadIdx.x; c < pr.k; c += blockDim.x) hcnt[c] = 0;
+  __syncthreads();
+  const uint32_t i = tl.row0 + threadIdx.x;
+  if (i < pr.n) atomicAdd(&hcnt[code[pr.off + i]], 1u);
+  __syncthreads();
+  uint32_t* out = hist + pr.hist0 + (uint64_t)(blockIdx.x - pr.tile0) * pr.k;
+  for (uint32_t c = threadIdx.x; c < pr.k; c += blockDim.x) out[c] = hcnt[c];
+}
+
+// Step 2, one block per problem: every code's tile counts become exclusive
+// offsets over the tiles (in place); cluster sizes go to counts and cluster
+// starts (relative to the problem's first row) to start.
+__global__ __launch_bounds__(256) void tac_scan_kernel(uint32_t* __restrict__ hist,
+                                                       const TacProblem* __restrict__ probs,
+                                                       const uint32_t* __restrict__ done,
+                                                       uint32_t* __restrict__ counts,
+                                                       uint32_t* __restrict__ start) {
+  __shared__ uint32_t wsum[256 / kWave];
+  __shared__ uint32_t carry;
+  const uint32_t p = blockIdx.x;
+  if (done[p]) return;
+  const TacProblem pr = probs[p];
+  if (threadIdx.x == 0) carry = 0;
+  __syncthreads();
+  for (uint32_t c0 = 0; c0 < pr.k; c0 += blockDim.x) {
+    const uint32_t c = c0 + threadIdx.x;
+    uint32_t run = 0;
+    if (c < pr.k) {
+      uint32_t* h = hist + pr.hist0 + c;
+      for (uint32_t t = 0; t < pr.ntiles; ++t) {
+        const uint32_t v = h[(uint64_t)t * pr.k];
+        h[(uint64_t)t * pr.k] = run;
+        run += v;
+      }
+      counts[pr.goff + c] = run;
+    }
+    const uint32_t ex = block_exclusive_scan(c < pr.k ? run : 0u, wsum);
+    if (c < pr.k) start[pr.goff + c] = carry + ex;
+    __syncthreads();
+    if (threadIdx.x == blockDim.x - 1) carry += ex + run;
+    __syncthreads();
+  }
+}
+
+// Step 3: stable scatter of row indices.  The tile's waves go in row order;
+// inside a wave equal codes are ranked with ballots (a match on every code
+// bit).  sorted[off + start[c] + tile offset + rank] = absolute row.
+__global__ void tac_scatter_kernel(const uint32_t* __restrict__ code,
+                                   const uint32_t* __restrict__ hist,
+                                   const uint32_t* __restrict__ start,
+                                   const TacProblem* __restrict__ probs,
+                                   const TacTile* __restrict__ tiles,
+                                   const uint32_t* __restrict__ done,
+                                   uint32_t* __restrict__ sorted) {
+  extern __shared__ uint32_t run[];  // [k]
+  const TacTile tl = tiles[blockIdx.x];
+  if (done[tl.prob]) return;
+  const TacProblem pr = probs[tl.prob];
+  const uint32_t* hm = hist + pr.hist0 + (uint64_t)(blockIdx.x - pr.tile0) * pr.k;
+  for (uint32_t c = threadIdx.x; c < pr.k; c += blockDim.x) run[c] = start[pr.goff + c] + hm[c];
+  const uint32_t i = tl.row0 + threadIdx.x;
+  const bool valid = i < pr.n;
+  const uint32_t cd = valid ? code[pr.off + i] : 0u;
+  const uint32_t lane = threadIdx.x % kWave, wv = threadIdx.x / kWave;
+  const uint64_t lt_mask = lane == 0 ? 0ull : (~0ull >> (64 - lane));
+  const uint32_t nw = (blockDim.x + kWave - 1) / kWave;
+  for (uint32_t r = 0; r < nw; ++r) {
+    __syncthreads();
+    if (wv == r) {
+      uint64_t match = __ballot(valid);
+      for (uint32_t b = 0; b < pr.code_bits; ++b) {
+        const bool bit = (cd >> b) & 1u;
+        const uint64_t bal = __ballot(bit);
+        match &= bit ? bal : ~bal;
+      }
+      const uint32_t rank = __popcll(match & lt_mask);
+      const uint32_t total = __popcll(match);
+      uint32_t pos = 0;
+      if (valid) pos = run[cd] + rank;
+      __builtin_amdgcn_wave_barrier();
+      __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+      if (valid && rank == total - 1) run[cd] = pos + 1;
+      if (valid) sorted[pr.off + pos] = pr.off + i;
+    }
+  }
+}
+
+// ---------------------------------------------------------------------------
+// Cluster sums and update (kmeans.zig:177-198): one wave per global cluster,
+// lane = dimension (strided beyond 64), members folded in ascending row order
+// from 0; centroid = sum * fl(1 / fl(count)).  Empty clusters are left to the
+// reseed kernel.  kTacFoldBatch member rows are loaded ahead of the adds.
+// ---------------------------------------------------------------------------
+constexpr int kTacFoldPer = 12;  // dimensions per lane: dim <= 768
+constexpr uint32_t kTacFoldBatch = 8;
+
+__global__ __launch_bounds__(256) void tac_fold_kernel(
+    const float* __restrict__ G, const uint32_t* __restrict__ sorted,
+    const uint32_t* __restrict__ counts, const uint32_t* __restrict__ start,
+    const uint32_t* __restrict__ cprob, const TacProblem* __restrict__ probs,
+    const uint32_t* __restrict__ done, float* __restrict__ C, uint32_t kappa, uint32_t dim) {
+  const uint32_t g = blockIdx.x * (256 / kWave) + threadIdx.x / kWave, lane = threadIdx.x % kWave;
+  if (g >= kappa) return;
+  const uint32_t p = cprob[g];
+  if (done[p]) return;
+  const uint32_t cnt = counts[g];
+  if (cnt == 0) return;
+  const uint32_t* mem = sorted + probs[p].off + start[g];
+  const uint32_t per = (dim + kWave - 1) / kWave;
+  float s[kTacFoldPer];
+#pragma unroll
+  for (int u = 0; u < kTacFoldPer; ++u) s[u] = 0.0f;
+  for (uint32_t q0 = 0; q0 < cnt; q0 += kTacFoldBatch) {
+    const uint32_t nb = cnt - q0 < kTacFoldBatch ? cnt - q0 : kTacFoldBatch;
+    uint32_t rows[kTacFoldBatch];
+#pragma unroll
+    for (uint32_t b = 0; b < kTacFoldBatch; ++b) rows[b] = b < nb ? mem[q0 + b] : 0u;
+#pragma unroll
+    for (int u = 0; u < kTacFoldPer; ++u) {
+      if ((uint32_t)u >= per) break;
+      const uint32_t d = lane + kWave * u;
+      float v[kTacFoldBatch];
+#pragma unroll
+      for (uint32_t b = 0; b < kTacFoldBatch; ++b)
+        v[b] = (b < nb && d < dim) ? G[(uint64_t)rows[b] * dim + d] : 0.0f;
+#pragma unroll
+      for (uint32_t b = 0; b < kTacFoldBatch; ++b)
+        if (b < nb) s[u] = s[u] + v[b];
+    }
+  }
+  const float inv = 1.0f / (float)cnt;
+#pragma unroll
+  for (int u = 0; u < kTacFoldPer; ++u) {
+    const uint32_t d = lane + kWave * u;
+    if ((uint32_t)u < per && d < dim) C[(uint64_t)g * dim + d] = s[u] * inv;
+  }
+}
+
+// ---------------------------------------------------------------------------
+// wcss per problem: the serial fp32 fold of min_to_any over its rows
+// (kmeans.zig:179), evaluated exactly in chunks (fold_rules.hpp).
+// ---------------------------------------------------------------------------
+__global__ __launch_bounds__(256) void tac_chunk_sums_kernel(
+    const float* __restrict__ e, const TacProblem* __restrict__ probs,
+    const TacChunk* __restrict__ chl, uint32_t nchl, const uint32_t* __restrict__ done,
+    double* __restrict__ pre) {
+  const uint32_t c = blockIdx.x * (256 / kWave) + threadIdx.x / kWave;
+  if (c >= nchl) return;
+  const TacChunk ch = chl[c];
+  if (done[ch.prob]) return;
+  const TacProblem pr = probs[ch.prob];
+  const double s = fold_chunk_sum_wave(e + pr.off, pr.n, ch.j);
+  if (threadIdx.x % kWave == 0) pre[c] = s;
+}
+
+__global__ __launch_bounds__(256) void tac_chunk_prefix_kernel(
+    double* __restrict__ pre, const TacProblem* __restrict__ probs,
+    const uint32_t* __restrict__ done) {
+  __shared__ double ws[256 / kWave];
+  __shared__ double carry;
+  const uint32_t p = blockIdx.x;
+  if (done[p]) return;
+  const TacProblem pr = probs[p];
+  block_prefix_f64<256>(pre + pr.chunk0, pr.nchunks, ws, &carry);
+}
+
+__global__ __launch_bounds__(256) void tac_quantize_kernel(
+    const float* __restrict__ e, const double* __restrict__ pre,
+    const TacProblem* __restrict__ probs, const TacChunk* __restrict__ chl, uint32_t nchl,
+    const uint32_t* __restrict__ done, FoldChunk* __restrict__ fchunks) {
+  const uint32_t c = blockIdx.x * (256 / kWave) + threadIdx.x / kWave;
+  if (c >= nchl) return;
+  const TacChunk ch = chl[c];
+  if (done[ch.prob]) return;
+  const TacProblem pr = probs[ch.prob];
+  fold_quantize_chunk_wave<float>(e + pr.off, pr.n, ch.j, pre[c], fchunks + c);
+}
+
+__global__ __launch_bounds__(kWave) void tac_wcss_apply_kernel(
+    const float* __restrict__ e, const FoldChunk* __restrict__ fchunks,
+    const TacProblem* __restrict__ probs, const uint32_t* __restrict__ done,
+    float* __restrict__ wcss) {
+  __shared__ FoldChunk lch[kWave];
+  __shared__ __attribute__((aligned(16))) float buf[kFoldChunk];
+  const uint32_t p = blockIdx.x;
+  if (done[p]) return;
+  const TacProblem pr = probs[p];
+  const float s = fold_apply_wave<float>(e + pr.off, pr.n, fchunks + pr.chunk0, pr.nchunks, lch,
+                                         buf, static_cast<float*>(nullptr));
+  if (threadIdx.x == 0) wcss[p] = s;
+}
+
+// ---------------------------------------------------------------------------
+// Empty-cluster reseed (kmeans.zig:199-211), one block per problem: empty
+// clusters in ascending order each take the row of argmax(min_to_any)
+// (first index on ties; index 0 when min_to_any[0] is NaN, as a strict >
+// scan from values[0] gives) and mark it claimed with -inf.
+// ---------------------------------------------------------------------------
+__global__ __launch_bounds__(256) void tac_reseed_kernel(
+    const float* __restrict__ G, float* __restrict__ e, const uint32_t* __restrict__ counts,
+    const TacProblem* __restrict__ probs, const uint32_t* __restrict__ done,
+    float* __restrict__ C, uint32_t* __restrict__ empties, uint32_t dim) {
+  __shared__ uint32_t elist[256];
+  __shared__ uint32_t ewsum[256 / kWave];
+  __shared__ float rv[256 / kWave];
+  __shared__ uint32_t ri[256 / kWave];
+  __shared__ uint32_t s_far;
+  const uint32_t p = blockIdx.x;
+  if (done[p]) return;
+  const TacProblem pr = probs[p];
+  const uint32_t lane = threadIdx.x % kWave, wv = threadIdx.x / kWave;
+  float* em = e + pr.off;
+  for (uint32_t c0 = 0; c0 < pr.k; c0 += blockDim.x) {
+    const uint32_t c = c0 + threadIdx.x;
+    const bool empty = c < pr.k && counts[pr.goff + c] == 0;
+    const uint32_t pos = block_exclusive_scan(empty ? 1u : 0u, ewsum);
+    if (empty) elist[pos] = c;
+    uint32_t found = 0;
+    for (uint32_t q = 0; q < blockDim.x / kWave; ++q) found += ewsum[q];
+    __syncthreads();
+    if (threadIdx.x == 0 && found) atomicAdd(&empties[p], found);
+    for (uint32_t q = 0; q < found; ++q) {
+      // argmax over em[0 .. n): first index of the largest value
+      float bv = -__builtin_inff();
+      uint32_t bidx = 0xFFFFFFFFu;
+      for (uint32_t i = threadIdx.x; i < pr.n; i += blockDim.x) {
+        const float v = em[i];
+        if (bidx == 0xFFFFFFFFu || v > bv) {
+          if (!(v != v)) {  // NaN never wins after index 0
+            bv = v;
+            bidx = i;
+          }
+        }
+      }
+      for (int off = 32; off > 0; off >>= 1) {
+        const float ov = __shfl_down(bv, off, kWave);
+        const uint32_t oi = __shfl_down(bidx, off, kWave);
+        if (oi != 0xFFFFFFFFu && (bidx == 0xFFFFFFFFu || ov > bv || (ov == bv && oi < bidx))) {
+          bv = ov;
+          bidx = oi;
+        }
+      }
+      if (lane == 0) {
+        rv[wv] = bv;
+        ri[wv] = bidx;
+      }
+      __syncthreads();
+      if (threadIdx.x == 0) {
+        float v = rv[0];
+        uint32_t ix = ri[0];
+        for (uint32_t ww = 1; ww < blockDim.x / kWave; ++ww)
+          if (ri[ww] != 0xFFFFFFFFu &&
+              (ix == 0xFFFFFFFFu || rv[ww] > v || (rv[ww] == v && ri[ww] < ix))) {
+            v = rv[ww];
+            ix = ri[ww];
+          }
+        const float e0 = em[0];
+        if (e0 != e0 || ix == 0xFFFFFFFFu) ix = 0;  // values[0] NaN: the scan keeps 0
+        // a value equal to values[0] never displaces index 0 (strict >)
+        if (ix != 0 && !(v > e0)) ix = 0;
+        s_far = ix;
+      }
+      __syncthreads();
+      const uint32_t far = s_far;
+      const uint32_t cc = elist[q];
+      for (uint32_t d = threadIdx.x; d < dim; d += blockDim.x)
+        C[((uint64_t)pr.goff + cc) * dim + d] = G[((uint64_t)pr.off + far) * dim + d];
+      __syncthreads();
+      if (threadIdx.x == 0) em[far] = -__builtin_inff();
+      __syncthreads();
+    }
+    __syncthreads();
+  }
+}
+
+// Convergence per problem (kmeans.zig:214-223): skipped at iteration 0;
+// rel = (prev - wcss) / (prev > 0 ? prev : 1); stop when rel < tol.
+__global__ void tac_converge_kernel(const float* __restrict__ wcss, float* __restrict__ prev,
+                                    uint32_t* __restrict__ done, uint32_t* __restrict__ iters,
+                                    uint32_t P, uint32_t t, float tol) {
+  const uint32_t p = blockIdx.x * blockDim.x + threadIdx.x;
+  if (p >= P || done[p]) return;
+  iters[p] = t + 1;
+  const float w = wcss[p];
+  if (t > 0) {
+    const float pv = prev[p];
+    const float denom = pv > 0.0f ? pv : 1.0f;
+    const float rel = (pv - w) / denom;
+    if (rel < tol) done[p] = 1;
+  }
+  prev[p] = w;
+}
+
+// Output: assignments[idx[off + i]] = goff + code[off + i] (tac.zig:504-510).
+__global__ void tac_output_kernel(const uint32_t* __restrict__ code,
+                                  const uint32_t* __restrict__ idx,
+                                  const TacProblem* __restrict__ probs,
+                                  const TacTile* __restrict__ tiles,
+                                  uint32_t* __restrict__ assign) {
+  const TacTile tl = tiles[blockIdx.x];
+  const TacProblem pr = probs[tl.prob];
+  const uint32_t i = tl.row0 + threadIdx.x;
+  if (i < pr.n) assign[idx[pr.off + i]] = pr.goff + code[pr.off + i];
+}
+
+}  // namespace tacgpu

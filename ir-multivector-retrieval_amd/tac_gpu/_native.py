@@ -59,6 +59,19 @@ class Profile(ctypes.Structure):
         ("crc_launches", c_u64),
         ("refine_ms", ctypes.c_double),
         ("refine_launches", c_u64),
+        ("cluster_kpp_ms", ctypes.c_double),
+        ("cluster_lloyd_ms", ctypes.c_double),
+        ("cluster_calls", c_u64),
+    ]
+
+
+class ClusterParams(ctypes.Structure):
+    """tac_cluster_params (ClusteringParams, src/tac/tac.zig:35-58)."""
+
+    _fields_ = [
+        ("kappa_total", c_u32), ("mu", c_u32), ("tau", c_u32), ("epsilon", c_u32),
+        ("theta", c_u32), ("max_iters", c_u32), ("tol", ctypes.c_float), ("seed", c_u64),
+        ("n_threads", c_u32),
     ]
 
 
@@ -130,6 +143,9 @@ SIGNATURES = {
     "tac_refine_device": (
         c_int, [ctypes.POINTER(DocIndex), c_void_p, c_u64, c_void_p, c_u32, c_void_p, c_u32,
                 c_void_p, c_void_p]),
+    "tac_cluster_flat": (
+        c_int, [c_void_p, c_u64, c_void_p, c_u64, c_u32, ctypes.POINTER(ClusterParams), c_void_p,
+                c_void_p, c_void_p, c_u64, c_f32_p, ctypes.POINTER(c_u64)]),
     "tac_gpu_profile_enable": (c_int, [c_int]),
     "tac_gpu_profile_read": (c_int, [ctypes.POINTER(Profile), c_int]),
 }
@@ -139,7 +155,7 @@ STATUS_NAMES = [
     "NQMismatch", "KmeansBudgetTooSmall", "EmptyVectorSet", "EmptyDistribution", "NonFinite",
     "AllZero", "OutOfMemory", "NoDevice", "HipError", "InvalidArgument", "Unsupported",
     "QueryShapeMismatch", "TableSizeMismatch", "DocOutOfRange", "DocLayoutCorrupt",
-    "BufferTooSmall",
+    "BufferTooSmall", "BudgetTooSmall", "BudgetTooLarge", "InvalidThresholds", "EmptyTokenDump",
 ]
 
 

@@ -95,6 +95,22 @@ class BufferTooSmall(TacError):
     status = 20
 
 
+class BudgetTooSmall(TacError):
+    status = 21
+
+
+class BudgetTooLarge(TacError):
+    status = 22
+
+
+class InvalidThresholds(TacError):
+    status = 23
+
+
+class EmptyTokenDump(TacError):
+    status = 24
+
+
 _BY_STATUS = {cls.status: cls for cls in TacError.__subclasses__()}
 
 

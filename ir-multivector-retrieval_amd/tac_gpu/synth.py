@@ -132,3 +132,31 @@ def workload(name: str, n: int | None = None):
     w = WORKLOADS[name]
     x = residuals(w, n)
     return w, x, shuffle_init(x, w.m, w.ksub, w.seed)
+
+
+# Token-aware clustering input: token id = a Zipf draw over `vocab` themes
+# (unit-sphere centres), vector = theme + residual noise scaled per token by
+# 0.5 + (id mod 7) / 4, so that token spreads differ.
+TAC_WORKLOADS = {
+    # 1.52M token vectors of dim 64 over a BERT-sized vocabulary (30,522 ids),
+    # Zipf 1.05, kappa_total 40,960: ~29k micro tokens, ~500 active tokens
+    # with up to ~1,000 centroids, 1.1e8 (row, centroid) pairs per iteration.
+    "tac-1.52m": dict(n=1_521_797, dim=64, vocab=30_522, zipf=1.05, sigma=0.15, seed=0,
+                      kappa_total=40_960),
+}
+
+
+def tac_vectors(n: int, dim: int, vocab: int, zipf: float, sigma: float, seed: int):
+    """(token_ids u32 [n], vectors f32 [n][dim]) of a synthetic token dump."""
+    w = Workload("tac", n, dim, vocab, zipf, sigma, 16, 256, 1, seed)
+    r, ids = residuals(w, n, with_ids=True)
+    c = _centers(seed, vocab, dim)
+    scale = (0.5 + (ids % 7).astype(np.float32) / 4.0).astype(np.float32)
+    v = (c[ids] + r * scale[:, None]).astype(np.float32)
+    return ids, v
+
+
+def tac_workload(name: str, n: int | None = None):
+    d = TAC_WORKLOADS[name]
+    ids, v = tac_vectors(n or d["n"], d["dim"], d["vocab"], d["zipf"], d["sigma"], d["seed"])
+    return d, ids, v

@@ -1,0 +1,138 @@
+"""GPU token-aware clustering (tac_cluster_flat) against the oracle's
+restatement of src/tac/tac.zig, bit for bit: centroids, assignments,
+kappa per token and wcss_total, and the same error for the same input."""
+import numpy as np
+import pytest
+
+from oracle import binding as orc
+from tac_gpu import errors, synth, tac
+
+pytestmark = pytest.mark.gpu
+
+
+def _params(kappa, seed, **kw):
+    return tac.ClusteringParams(kappa_total=kappa, seed=seed, **kw)
+
+
+def _check(ids, v, dim, kappa, seed, **kw):
+    ref = orc.tac_cluster_flat(ids, v, dim, orc.tac_params(kappa, seed, **kw))
+    assert ref.status == 0, ref.status
+    got = tac.cluster_flat(ids, v, dim, _params(kappa, seed, **kw))
+    assert np.array_equal(got.kappa_per_token, ref.kappa_per_token)
+    assert got.centroids.tobytes() == ref.centroids.tobytes()
+    assert np.array_equal(got.assignments, ref.assignments)
+    assert np.float32(got.wcss_total).tobytes() == np.float32(ref.wcss_total).tobytes()
+    return got
+
+
+def _feasible_kappa(ids, frac=0.6, mu=128, tau=256, theta=39):
+    f = np.bincount(ids)
+    tail = int(((f > 0) & (f < mu)).sum() + 2 * ((f >= mu) & (f < tau)).sum())
+    return tail + int(frac * (f[f >= tau] // theta).sum())
+
+
+def _themes(counts, themes, sigma, seed):
+    rng = np.random.default_rng(seed)
+    ids, vec = [], []
+    for tid, (c, t) in enumerate(zip(counts, themes)):
+        for _ in range(c):
+            ids.append(tid)
+            vec.append(np.asarray(t, np.float32) + rng.standard_normal(len(t)).astype(np.float32) * sigma)
+    return np.array(ids, np.uint32), np.array(vec, np.float32)
+
+
+def test_reference_test_inputs(gpu):
+    # The shapes of the reference's clusterFlat tests (tac.zig:1131-1306).
+    ids, v = _themes([10, 10, 6, 4], [(1, 0), (0, 1), (-1, 0), (0, -1)], 0.05, 7)
+    _check(ids, v, 2, 14, 42, mu=3, tau=5, epsilon=1, theta=1)
+    rng = np.random.default_rng(1)
+    _check((np.arange(40) % 5).astype(np.uint32), rng.standard_normal((40, 3)).astype(np.float32),
+           3, 18, 12345, mu=3, tau=5, epsilon=1, theta=1)
+    r = _check(np.array([1, 1, 1, 1, 2, 2, 2, 2, 3, 3, 3, 3], np.uint32),
+               np.arange(1, 13, dtype=np.float32) / 10, 1, 6, 0, mu=3, tau=5, epsilon=1, theta=1)
+    assert r.kappa_per_token.tolist() == [0, 2, 2, 2]
+    ids, v = _themes([6, 6, 6], [(10, 0), (0, 10), (-10, 0)], 0.05, 99)
+    r = _check(ids, v, 2, 3, 0, mu=2, tau=5, epsilon=1, theta=1)
+    assert np.array_equal(r.assignments, ids)
+
+
+@pytest.mark.parametrize("n,vocab,dim,seed", [(60_000, 2048, 64, 3), (30_000, 1024, 128, 4)])
+def test_synthetic_token_dumps(gpu, n, vocab, dim, seed):
+    ids, v = synth.tac_vectors(n, dim, vocab, 1.05, 0.15, seed)
+    _check(ids, v, dim, _feasible_kappa(ids), 5)
+
+
+def test_synthetic_200k(gpu):
+    """200,000 x 64 over 4,096 tokens: ~80 active tokens with up to ~500
+    centroids each, next to thousands of micro tokens."""
+    ids, v = synth.tac_vectors(200_000, 64, 4096, 1.05, 0.15, 3)
+    _check(ids, v, 64, _feasible_kappa(ids), 5)
+
+
+@pytest.mark.parametrize("dim", [3, 16, 33, 95, 96, 100, 191])
+def test_generic_dims(gpu, dim):
+    # generic 16-lane distances; 95 / 96 straddle the 128 / 64-row tiles
+    ids, v = synth.tac_vectors(6000, dim, 300, 1.0, 0.2, dim)
+    _check(ids, v, dim, _feasible_kappa(ids, mu=20, tau=40, theta=8), 9, mu=20, tau=40,
+           epsilon=4, theta=8)
+
+
+def test_thread_grouping_and_exact_draws(gpu, monkeypatch):
+    ids, v = synth.tac_vectors(60_000, 64, 2048, 1.05, 0.15, 8)
+    kap = _feasible_kappa(ids)
+    for nt in (3, 10):
+        _check(ids, v, 64, kap, 21, n_threads=nt)
+    monkeypatch.setenv("TAC_GPU_KPP_EXACT", "1")
+    _check(ids, v, 64, kap, 21)
+
+
+def test_degenerate_and_tiny_tokens(gpu):
+    # mu=2: tokens with one row are micro (k = 1 >= n = 1, the degenerate
+    # branch of kmeans.fit); small tokens of 2-3 rows get k = 2.
+    rng = np.random.default_rng(5)
+    ids = np.array([0, 1, 1, 2, 2, 2, 3, 4, 4, 4, 4, 4, 4, 4, 4] + [5] * 40, np.uint32)
+    v = rng.standard_normal((ids.size, 4)).astype(np.float32)
+    _check(ids, v, 4, 20, 3, mu=2, tau=4, epsilon=2, theta=2)
+
+
+def _expect(ids, v, dim, p_kw, exc):
+    ref = orc.tac_cluster_flat(ids, v, dim, orc.tac_params(**p_kw))
+    assert ref.status == exc.status
+    kw = dict(p_kw)
+    with pytest.raises(exc):
+        tac.cluster_flat(ids, v, dim, _params(kw.pop("kappa_total"), kw.pop("seed"), **kw))
+
+
+def test_errors_match_the_reference(gpu):
+    v2 = np.array([[1, 0], [0, 1]], np.float32)
+    _expect(np.zeros(0, np.uint32), np.zeros(0, np.float32), 2, dict(kappa_total=1, seed=0),
+            errors.EmptyTokenDump)
+    _expect([0, 0], v2, 2, dict(kappa_total=0, seed=0), errors.BudgetTooSmall)
+    _expect([0, 0, 0], v2, 2, dict(kappa_total=4, seed=0), errors.InvalidThresholds)
+    _expect([0, 0], v2, 2, dict(kappa_total=4, seed=0, mu=5, tau=5), errors.InvalidThresholds)
+    _expect([0, 1, 2], np.zeros((3, 2), np.float32), 2, dict(kappa_total=2, seed=0),
+            errors.BudgetTooSmall)
+    ids = np.zeros(300, np.uint32)
+    _expect(ids, np.random.default_rng(0).standard_normal((300, 2)).astype(np.float32), 2,
+            dict(kappa_total=50, seed=0), errors.BudgetTooLarge)
+    # k-means++ failures of small tokens (k = 2 from the tail tier, spreads
+    # unused): identical rows (AllZero) and a NaN row (NonFinite); the lowest
+    # failing token id decides.  An active token's NaN spread fails earlier,
+    # in phase 2 (InvalidThresholds).
+    same = np.tile(np.array([[0.5, 0.25]], np.float32), (4, 1))
+    nan = np.random.default_rng(1).standard_normal((4, 2)).astype(np.float32)
+    nan[2, 1] = np.nan
+    p = dict(kappa_total=4, seed=0, mu=3, tau=5, epsilon=1, theta=1)
+    _expect(np.array([0] * 4 + [1] * 4, np.uint32), np.vstack([same, nan]), 2, p, errors.AllZero)
+    _expect(np.array([1] * 4 + [0] * 4, np.uint32), np.vstack([same, nan]), 2, p,
+            errors.NonFinite)
+    nan6 = np.vstack([nan, nan[:2]])
+    _expect(np.zeros(6, np.uint32), nan6, 2, dict(kappa_total=2, seed=0, mu=3, tau=5, epsilon=1,
+                                                  theta=1), errors.InvalidThresholds)
+    with pytest.raises(errors.Unsupported):
+        tac.cluster_flat(np.zeros(4, np.uint32), np.zeros((4, 200), np.float32), 200,
+                         _params(1, 0))
+    # a clean call after the errors
+    ids, v = synth.tac_vectors(3000, 8, 100, 1.0, 0.2, 1)
+    _check(ids, v, 8, _feasible_kappa(ids, mu=5, tau=20, theta=4), 2, mu=5, tau=20, epsilon=4,
+           theta=4)
