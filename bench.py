@@ -201,6 +201,58 @@ def storage_and_query(device, x, ids, w, cents):
     }
 
 
+def tac_clustering(device, with_cpu: bool):
+    """Token-aware clustering (tac.clusterFlat) on the 1.52M-token synthetic
+    dump (dim 64, 30,522-id vocabulary, Zipf 1.05, kappa_total 40,960): call
+    time (host inputs, includes the upload and the host-side budget phases)
+    and the device time of seeding and Lloyd; the oracle and the GPU on the
+    first 200,000 rows (same generator) for a like-for-like CPU comparison."""
+    from oracle import binding as orc
+    from tac_gpu import synth, tac
+
+    d, ids, v = synth.tac_workload("tac-1.52m")
+    p = tac.ClusteringParams(kappa_total=d["kappa_total"], seed=0)
+    tac.cluster_flat(ids, v, d["dim"], p)  # warm-up: workspace allocation
+    device.profile_enable(True)
+    device.profile_read(reset=True)
+    reps = 2
+    t0 = time.perf_counter()
+    for _ in range(reps):
+        r = tac.cluster_flat(ids, v, d["dim"], p)
+    call_s = (time.perf_counter() - t0) / reps
+    pr = device.profile_read(reset=True)
+    device.profile_enable(False)
+    f = np.bincount(ids)
+    row = {
+        "workload": "tac-1.52m", "n": int(ids.size), "dim": d["dim"],
+        "distinct_tokens": int((f > 0).sum()), "kappa_total": d["kappa_total"],
+        "max_kappa_per_token": int(r.kappa_per_token.max()),
+        "pairs_per_iteration": int((f.astype(np.int64) * r.kappa_per_token[:f.size]).sum()),
+        "call_s": round(call_s, 4),
+        "device_kpp_ms": round(pr.cluster_kpp_ms / max(pr.cluster_calls, 1), 2),
+        "device_lloyd_ms": round(pr.cluster_lloyd_ms / max(pr.cluster_calls, 1), 2),
+        "kappa_sum_ok": bool(int(r.kappa_per_token.sum()) == d["kappa_total"]),
+    }
+    if with_cpu:
+        ns = 200_000
+        fs = np.bincount(ids[:ns])
+        kap = int(((fs > 0) & (fs < 128)).sum() + 2 * ((fs >= 128) & (fs < 256)).sum()
+                  + 0.6 * (fs[fs >= 256] // 39).sum())
+        t0 = time.perf_counter()
+        ref = orc.tac_cluster_flat(ids[:ns], v[:ns], d["dim"], orc.tac_params(kap, 0))
+        cpu_s = time.perf_counter() - t0
+        t0 = time.perf_counter()
+        got = tac.cluster_flat(ids[:ns], v[:ns], d["dim"], tac.ClusteringParams(kap, 0))
+        gpu_s = time.perf_counter() - t0
+        row["cpu_sample"] = {
+            "rows": ns, "kappa_total": kap, "oracle_s_1thread": round(cpu_s, 3),
+            "gpu_call_s": round(gpu_s, 4), "speedup": round(cpu_s / gpu_s, 1),
+            "bit_exact": bool(ref.status == 0 and got.centroids.tobytes() == ref.centroids.tobytes()
+                              and np.array_equal(got.assignments, ref.assignments)),
+        }
+    return row
+
+
 def main() -> int:
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -292,6 +344,8 @@ def main() -> int:
     log(f"residual stage: {residual['avg_call_ms']} ms per call")
     sq = storage_and_query(device, x, ids, w, synth.centers(w.seed, w.n_centers, w.dim))
     log(f"storage/query rows: {sq}")
+    tacrow = tac_clustering(device, not args.no_cpu_baseline)
+    log(f"token-aware clustering: {tacrow}")
 
     # Roofline of the dominant kernel (Lloyd assignment, VALU fp32): algorithmic
     # FLOP per launch = n * 2 * dim * ksub (one launch = one iteration, all m).
@@ -375,6 +429,7 @@ def main() -> int:
         "drop_in_defaults": drop_in,
         "residual_stage": residual,
         "storage_query": sq,
+        "tac_clustering": tacrow,
         "cpu_baseline": None if cpu is None else {
             "value": round(cpu["train_s_per_20_iters"], 3), "unit": "s/20 iters",
             "encode_mvec_per_s": round(cpu["encode_mvec_per_s"], 3), "cores": cpu["cores"],

@@ -132,6 +132,9 @@ class KernelTimes:
     crc_launches: int = 0
     refine_ms: float = 0.0
     refine_launches: int = 0
+    cluster_kpp_ms: float = 0.0
+    cluster_lloyd_ms: float = 0.0
+    cluster_calls: int = 0
 
 
 def profile_enable(on: bool = True) -> None:
@@ -144,4 +147,5 @@ def profile_read(reset: bool = True) -> KernelTimes:
     return KernelTimes(p.transpose_ms, p.transpose_launches, p.assign_ms, p.assign_launches,
                        p.update_ms, p.update_iters, p.encode_ms, p.encode_launches,
                        p.exact_rescans, p.residual_ms, p.residual_launches, p.crc_ms,
-                       p.crc_launches, p.refine_ms, p.refine_launches)
+                       p.crc_launches, p.refine_ms, p.refine_launches, p.cluster_kpp_ms,
+                       p.cluster_lloyd_ms, p.cluster_calls)

@@ -136,3 +136,33 @@ def test_errors_match_the_reference(gpu):
     ids, v = synth.tac_vectors(3000, 8, 100, 1.0, 0.2, 1)
     _check(ids, v, 8, _feasible_kappa(ids, mu=5, tau=20, theta=4), 2, mu=5, tau=20, epsilon=4,
            theta=4)
+
+
+def test_full_corpus_scale_properties(gpu):
+    """1,521,797 x 64 over a 30,522-id vocabulary, kappa_total 40,960, through
+    properties the reference fixes at any size: kappa sums to the budget,
+    every token's assignments lie in its own centroid range, and every
+    non-empty centroid is the serial fp32 fold of its final members times
+    fl(1 / fl(count)) (kmeans.zig:177-198: centroids are updated from the
+    assignments that fit returns)."""
+    d, ids, v = synth.tac_workload("tac-1.52m")
+    r = tac.cluster_flat(ids, v, d["dim"], _params(d["kappa_total"], 0))
+    k = r.kappa_per_token
+    assert int(k.sum()) == d["kappa_total"]
+    goff = np.concatenate([[0], np.cumsum(k.astype(np.int64))])
+    a = r.assignments.astype(np.int64)
+    assert np.all(a >= goff[ids]) and np.all(a < goff[ids + 1])
+    # serial member folds, all clusters at once, one member rank at a time
+    order = np.lexsort((np.arange(ids.size), a))
+    cnt = np.bincount(a, minlength=d["kappa_total"])
+    first = np.concatenate([[0], np.cumsum(cnt)[:-1]])
+    s = np.zeros((d["kappa_total"], d["dim"]), np.float32)
+    live = np.nonzero(cnt)[0]
+    for rank in range(int(cnt.max())):
+        live = live[cnt[live] > rank]
+        s[live] = (s[live] + v[order[first[live] + rank]]).astype(np.float32)
+    nz = cnt > 0
+    inv = (np.float32(1.0) / cnt[nz].astype(np.float32)).astype(np.float32)
+    want = (s[nz] * inv[:, None]).astype(np.float32)
+    assert want.tobytes() == r.centroids[nz].tobytes()
+    assert np.isfinite(r.wcss_total) and r.wcss_total > 0
