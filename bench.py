@@ -231,6 +231,8 @@ def tac_clustering(device, with_cpu: bool):
         "call_s": round(call_s, 4),
         "device_kpp_ms": round(pr.cluster_kpp_ms / max(pr.cluster_calls, 1), 2),
         "device_lloyd_ms": round(pr.cluster_lloyd_ms / max(pr.cluster_calls, 1), 2),
+        "host_prep_ms": round(pr.cluster_prep_ms / max(pr.cluster_calls, 1), 2),
+        "library_call_ms": round(pr.cluster_call_ms / max(pr.cluster_calls, 1), 2),
         "kappa_sum_ok": bool(int(r.kappa_per_token.sum()) == d["kappa_total"]),
     }
     if with_cpu:

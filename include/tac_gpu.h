@@ -335,6 +335,8 @@ typedef struct tac_gpu_profile {
   double cluster_kpp_ms;   /* tac_cluster_flat: degenerate init + k-means++ seeding */
   double cluster_lloyd_ms; /* tac_cluster_flat: Lloyd iterations of every token */
   uint64_t cluster_calls;
+  double cluster_prep_ms;  /* wall: grouping, upload, gather, spreads, budget phases, plan */
+  double cluster_call_ms;  /* wall: the whole tac_cluster_flat call */
 } tac_gpu_profile;
 int tac_gpu_profile_enable(int enable);
 int tac_gpu_profile_read(tac_gpu_profile *out, int reset);

@@ -26,6 +26,7 @@
 
 #include <hip/hip_runtime.h>
 
+#include <chrono>
 #include <cmath>
 #include <cstdio>
 #include <cstdlib>
@@ -91,7 +92,7 @@ struct DeviceState {
   Buffer tac_v, tac_idx, tac_offs, tac_G, tac_spreads, tac_w, tac_e, tac_code, tac_sorted,
       tac_tsum, tac_hist, tac_counts, tac_start, tac_C, tac_pre, tac_fch, tac_st, tac_bad,
       tac_done, tac_iters, tac_wcss, tac_prev, tac_empties, tac_assign, tac_probs, tac_tiles,
-      tac_chl, tac_cprob;
+      tac_chl, tac_cprob, tac_inv, tac_rsum, tac_ranges;
   bool crc_tx_ready = false;
   // measurement
   std::vector<hipEvent_t> events;
@@ -766,7 +767,8 @@ int tac_gpu_release_workspace(void) {
                     &ds->tac_start, &ds->tac_C,   &ds->tac_pre,   &ds->tac_fch,
                     &ds->tac_st,    &ds->tac_bad, &ds->tac_done,  &ds->tac_iters,
                     &ds->tac_wcss,  &ds->tac_prev, &ds->tac_empties, &ds->tac_assign,
-                    &ds->tac_probs, &ds->tac_tiles, &ds->tac_chl, &ds->tac_cprob};
+                    &ds->tac_probs, &ds->tac_tiles, &ds->tac_chl, &ds->tac_cprob,
+                    &ds->tac_inv,   &ds->tac_rsum, &ds->tac_ranges};
   ds->crc_tx_ready = false;
   for (Buffer *b : bufs) {
     if (b->ptr) HIP_TRY(hipFree(b->ptr));
@@ -1512,11 +1514,13 @@ struct TacPlan {
   std::vector<TacProblem> probs;
   std::vector<TacTile> tiles;
   std::vector<TacChunk> chunks;
+  std::vector<TacRange> ranges;      // scan ranges of the tile histograms
   std::vector<uint32_t> cprob;       // problem of every centroid
   std::vector<uint32_t> token;       // token id of every problem
   std::vector<uint32_t> tiles_upto;  // [c]: tiles of problems still seeding in round c
   std::vector<uint32_t> probs_upto;  // [c]: problems with more than c seeds
   uint64_t hist_total = 0;
+  uint64_t rsum_total = 0;
   uint32_t kmax = 0;      // largest k of a non-degenerate problem
 };
 
@@ -1559,10 +1563,15 @@ int tac_plan(const std::vector<uint32_t> &freqs, const std::vector<uint32_t> &of
     p.nchunks = (p.n + kFoldChunk - 1) / kFoldChunk;
     p.code_bits = p.k <= 1 ? 0u : 32u - (uint32_t)__builtin_clz(p.k - 1);
     p.hist0 = pl->hist_total;
+    p.range0 = (uint32_t)pl->ranges.size();
+    p.nranges = (p.ntiles + kTacScanTiles - 1) / kTacScanTiles;
+    p.rsum0 = pl->rsum_total;
     if (!p.degenerate) {
       pl->hist_total += (uint64_t)p.ntiles * p.k;
+      pl->rsum_total += (uint64_t)p.nranges * p.k;
       if (p.k > pl->kmax) pl->kmax = p.k;
     }
+    for (uint32_t r = 0; r < p.nranges; ++r) pl->ranges.push_back(TacRange{q, r});
     for (uint32_t t = 0; t < p.ntiles; ++t) pl->tiles.push_back(TacTile{q, t * rt});
     for (uint32_t j = 0; j < p.nchunks; ++j) pl->chunks.push_back(TacChunk{q, j});
     for (uint32_t c = 0; c < p.k; ++c) pl->cprob[(uint64_t)p.goff + c] = q;
@@ -1587,8 +1596,10 @@ int tac_cluster_core(DeviceState &ds, hipStream_t s, const uint32_t *ids, uint64
                      const float *vectors, uint32_t dim, const tac_cluster_params &prm,
                      uint64_t nd, float *cent_out, uint32_t *assign_out, uint32_t *kpt_out,
                      float *wcss_out) {
+  const auto wall0 = std::chrono::steady_clock::now();
   const uint32_t rt = tac_rows_per_tile(dim);
-  if (rt < 64 || dim > 64u * kTacSpreadPer) return TAC_ERR_UNSUPPORTED;
+  if (rt < 64 || dim > 192) return TAC_ERR_UNSUPPORTED;
+  const uint32_t per = (dim + 63) / 64;  // dimensions per lane in the wave kernels
   // 32-bit row ids; the gather grid stays below 2^31 blocks
   if (N > 0xFFFFFFFFull || (uint64_t)N * dim > (1ull << 38) || nd > 0x7FFFFFFFull)
     return TAC_ERR_UNSUPPORTED;
@@ -1612,9 +1623,25 @@ int tac_cluster_core(DeviceState &ds, hipStream_t s, const uint32_t *ids, uint64
   tac_gather_kernel<<<(unsigned)((nf + 255) / 256), 256, 0, s>>>(
       as<float>(ds.tac_v), as<uint32_t>(ds.tac_idx), G, N, dim);
   LAUNCH_TRY("tac_gather_kernel");
-  tac_spread_kernel<<<(unsigned)nd, kWave, dim * sizeof(float), s>>>(
-      G, as<uint32_t>(ds.tac_offs), dim, as<float>(ds.tac_spreads));
-  LAUNCH_TRY("tac_spread_kernel");
+  uint32_t max_n = 0;
+  for (uint64_t j = 0; j < nd; ++j) max_n = freqs[j] > max_n ? freqs[j] : max_n;
+  const uint32_t ninv = max_n < kTacInvMax ? max_n : kTacInvMax;
+  if ((st = ensure(ds, ds.tac_inv, (size_t)ninv * sizeof(float)))) return st;
+  tac_inv_table_kernel<<<(ninv + 255) / 256, 256, 0, s>>>(as<float>(ds.tac_inv), ninv);
+  LAUNCH_TRY("tac_inv_table_kernel");
+  {
+    const uint32_t *doffs = as<uint32_t>(ds.tac_offs);
+    const float *dinv = as<float>(ds.tac_inv);
+    float *dsp = as<float>(ds.tac_spreads);
+    const size_t lds = dim * sizeof(float);
+    if (per == 1)
+      tac_spread_kernel<1><<<(unsigned)nd, kWave, lds, s>>>(G, doffs, dinv, dim, dsp);
+    else if (per == 2)
+      tac_spread_kernel<2><<<(unsigned)nd, kWave, lds, s>>>(G, doffs, dinv, dim, dsp);
+    else
+      tac_spread_kernel<3><<<(unsigned)nd, kWave, lds, s>>>(G, doffs, dinv, dim, dsp);
+    LAUNCH_TRY("tac_spread_kernel");
+  }
   std::vector<float> spreads(nd);
   HIP_TRY(hipMemcpyAsync(spreads.data(), ds.tac_spreads.ptr, nd * sizeof(float),
                          hipMemcpyDeviceToHost, s));
@@ -1641,6 +1668,8 @@ int tac_cluster_core(DeviceState &ds, hipStream_t s, const uint32_t *ids, uint64
   if ((st = upload_vec(ds, ds.tac_probs, pl.probs, s)) ||
       (st = upload_vec(ds, ds.tac_tiles, pl.tiles, s)) ||
       (st = upload_vec(ds, ds.tac_chl, pl.chunks, s)) ||
+      (st = upload_vec(ds, ds.tac_ranges, pl.ranges, s)) ||
+      (st = ensure(ds, ds.tac_rsum, (pl.rsum_total + 1) * sizeof(uint32_t))) ||
       (st = upload_vec(ds, ds.tac_cprob, pl.cprob, s)) ||
       (st = upload_vec(ds, ds.tac_done, done0, s)) ||
       (st = ensure(ds, ds.tac_w, N * sizeof(float))) ||
@@ -1674,6 +1703,9 @@ int tac_cluster_core(DeviceState &ds, hipStream_t s, const uint32_t *ids, uint64
   const TacProblem *probs = as<TacProblem>(ds.tac_probs);
   const TacTile *tiles = as<TacTile>(ds.tac_tiles);
   const TacChunk *chl = as<TacChunk>(ds.tac_chl);
+  const TacRange *ranges = as<TacRange>(ds.tac_ranges);
+  uint32_t *rsum = as<uint32_t>(ds.tac_rsum);
+  const uint32_t NR = (uint32_t)pl.ranges.size();
   HIP_TRY(hipMemsetAsync(code, 0, N * sizeof(uint32_t), s));
   HIP_TRY(hipMemsetAsync(iters, 0, (size_t)P * sizeof(uint32_t), s));
   HIP_TRY(hipMemsetAsync(ds.tac_empties.ptr, 0, (size_t)P * sizeof(uint32_t), s));
@@ -1687,6 +1719,8 @@ int tac_cluster_core(DeviceState &ds, hipStream_t s, const uint32_t *ids, uint64
   const size_t asg_lds = (rows_lds + (size_t)chunk_c * dim) * sizeof(float);
   const size_t code_lds = (size_t)(pl.kmax ? pl.kmax : 1) * sizeof(uint32_t);
   const bool profile = g_profile;
+  const double prep_ms =
+      std::chrono::duration<double, std::milli>(std::chrono::steady_clock::now() - wall0).count();
   hipEvent_t ev0 = nullptr, ev1 = nullptr, ev2 = nullptr;
   if (profile) {
     if ((st = event_at(ds, 0, &ev0)) || (st = event_at(ds, 1, &ev1)) ||
@@ -1753,14 +1787,25 @@ int tac_cluster_core(DeviceState &ds, hipStream_t s, const uint32_t *ids, uint64
     LAUNCH_TRY("tac_assign_kernel");
     tac_hist_kernel<<<NT, rt, code_lds, s>>>(code, probs, tiles, done, hist);
     LAUNCH_TRY("tac_hist_kernel");
-    tac_scan_kernel<<<P, 256, 0, s>>>(hist, probs, done, counts, start);
-    LAUNCH_TRY("tac_scan_kernel");
+    tac_scan_partial_kernel<<<NR, 256, 0, s>>>(hist, probs, ranges, done, rsum);
+    tac_scan_apply_kernel<<<NR, 256, 0, s>>>(hist, probs, ranges, done, rsum, counts, start);
+    LAUNCH_TRY("tac scan kernels");
     tac_scatter_kernel<<<NT, rt, code_lds, s>>>(code, hist, start, probs, tiles, done, sorted);
     LAUNCH_TRY("tac_scatter_kernel");
-    tac_fold_kernel<<<(unsigned)((K + 3) / 4), 256, 0, s>>>(G, sorted, counts, start,
-                                                           as<uint32_t>(ds.tac_cprob), probs,
-                                                           done, C, (uint32_t)K, dim);
-    LAUNCH_TRY("tac_fold_kernel");
+    {
+      const uint32_t *cp = as<uint32_t>(ds.tac_cprob);
+      const unsigned fb = (unsigned)((K + 3) / 4);
+      if (per == 1)
+        tac_fold_kernel<1><<<fb, 256, 0, s>>>(G, sorted, counts, start, cp, probs, done, C,
+                                              (uint32_t)K, dim);
+      else if (per == 2)
+        tac_fold_kernel<2><<<fb, 256, 0, s>>>(G, sorted, counts, start, cp, probs, done, C,
+                                              (uint32_t)K, dim);
+      else
+        tac_fold_kernel<3><<<fb, 256, 0, s>>>(G, sorted, counts, start, cp, probs, done, C,
+                                              (uint32_t)K, dim);
+      LAUNCH_TRY("tac_fold_kernel");
+    }
     tac_chunk_sums_kernel<<<(NCH + 3) / 4, 256, 0, s>>>(e, probs, chl, NCH, done, pre);
     tac_chunk_prefix_kernel<<<P, 256, 0, s>>>(pre, probs, done);
     tac_quantize_kernel<<<(NCH + 3) / 4, 256, 0, s>>>(e, pre, probs, chl, NCH, done, fch);
@@ -1790,6 +1835,10 @@ int tac_cluster_core(DeviceState &ds, hipStream_t s, const uint32_t *ids, uint64
     g_prof.cluster_kpp_ms += a;
     g_prof.cluster_lloyd_ms += b;
     g_prof.cluster_calls += 1;
+    g_prof.cluster_prep_ms += prep_ms;
+    g_prof.cluster_call_ms +=
+        std::chrono::duration<double, std::milli>(std::chrono::steady_clock::now() - wall0)
+            .count();
   }
   for (uint64_t j = 0; j < nd; ++j) kpt_out[j] = kappa[j];
   // wcss_total: the per-token wcss in token order, grouped by thread slices

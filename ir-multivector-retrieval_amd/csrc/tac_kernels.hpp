@@ -25,6 +25,8 @@ struct TacProblem {
   uint64_t seed;             // p.seed ^ token id
   uint32_t code_bits;        // bits that tell the k codes apart
   uint32_t degenerate;       // k >= n (kmeans.zig:88-104)
+  uint32_t range0, nranges;  // scan ranges of kTacScanTiles tiles
+  uint64_t rsum0;            // nranges * k range sums
 };
 
 struct TacTile {
@@ -34,6 +36,12 @@ struct TacTile {
 struct TacChunk {
   uint32_t prob, j;  // j: chunk index within the problem
 };
+
+struct TacRange {
+  uint32_t prob, r;  // r: scan range index within the problem
+};
+
+constexpr uint32_t kTacScanTiles = 32;  // tiles per scan range
 
 constexpr uint32_t kTacMaxCodes = 12288;   // k per problem: LDS counters of hist/scatter
 constexpr uint32_t kTacLdsFloats = 12288;  // staged rows: rt * (dim + 1) <= this
@@ -117,13 +125,24 @@ __global__ __launch_bounds__(256) void tac_gather_kernel(const float* __restrict
 
 // ---------------------------------------------------------------------------
 // Per-token spread by Welford (tac.zig:611-632): one wave per token, lane =
-// dimension (strided beyond 64); the trace folds the dimensions in order and
-// is divided by the f32 count of rows.  dim <= 64 * kTacSpreadPer.
+// dimension (PER dimensions per lane); the trace folds the dimensions in
+// order and is divided by the f32 row count.  The f32 count after i rows is
+// min(i, 2^24) exactly (count + 1 stops growing at 2^24), so its reciprocal
+// comes from a table inv[i - 1] = fl(1 / min(i, 2^24)); rows and reciprocals
+// are loaded kTacSpreadBatch at a time, one batch ahead of the serial updates.
 // ---------------------------------------------------------------------------
-constexpr int kTacSpreadPer = 12;
+constexpr uint32_t kTacSpreadBatch = 32;
+constexpr uint32_t kTacInvMax = 1u << 24;
 
+__global__ void tac_inv_table_kernel(float* __restrict__ inv, uint32_t n) {
+  const uint32_t i = blockIdx.x * blockDim.x + threadIdx.x;
+  if (i < n) inv[i] = 1.0f / (float)(i + 1);  // i + 1 <= 2^24: exact in f32
+}
+
+template <int PER>
 __global__ __launch_bounds__(kWave) void tac_spread_kernel(const float* __restrict__ G,
                                                            const uint32_t* __restrict__ offs,
+                                                           const float* __restrict__ inv,
                                                            uint32_t dim,
                                                            float* __restrict__ spreads) {
   extern __shared__ float m2s[];  // [dim]
@@ -133,31 +152,55 @@ __global__ __launch_bounds__(kWave) void tac_spread_kernel(const float* __restri
     if (lane == 0) spreads[j] = 0.0f;
     return;
   }
-  float mean[kTacSpreadPer], m2[kTacSpreadPer];
+  float mean[PER], m2[PER];
 #pragma unroll
-  for (int u = 0; u < kTacSpreadPer; ++u) {
+  for (int u = 0; u < PER; ++u) {
     mean[u] = 0.0f;
     m2[u] = 0.0f;
   }
-  float count = 0.0f;
-  for (uint32_t q = lo; q < hi; ++q) {
-    const float* v = G + (uint64_t)q * dim;
-    count = count + 1.0f;
-    const float inv = 1.0f / count;
+  // double-buffered: batch q0 + B is in flight while batch q0 is folded
+  constexpr uint32_t B = kTacSpreadBatch;
+  float nx[B][PER], niv[B];
+  auto load = [&](uint32_t q0, float (&x)[B][PER], float (&v)[B]) {
 #pragma unroll
-    for (int u = 0; u < kTacSpreadPer; ++u) {
-      const uint32_t d = lane + 64u * u;
-      if (d < dim) {
-        const float x = v[d];
-        const float old = mean[u];
-        const float delta = x - old;
-        mean[u] = old + delta * inv;
-        m2[u] = m2[u] + delta * (x - mean[u]);
+    for (uint32_t b = 0; b < B; ++b) {
+      const uint32_t r = q0 - lo + b;  // rows folded before this one
+      const bool in = q0 + b < hi;
+      v[b] = in ? inv[r < kTacInvMax ? r : kTacInvMax - 1] : 0.0f;
+#pragma unroll
+      for (int u = 0; u < PER; ++u) {
+        const uint32_t d = lane + 64u * u;
+        x[b][u] = (in && d < dim) ? G[(uint64_t)(q0 + b) * dim + d] : 0.0f;
+      }
+    }
+  };
+  load(lo, nx, niv);
+  for (uint32_t q0 = lo; q0 < hi; q0 += B) {
+    const uint32_t nb = hi - q0 < B ? hi - q0 : B;
+    float xv[B][PER], iv[B];
+#pragma unroll
+    for (uint32_t b = 0; b < B; ++b) {
+      iv[b] = niv[b];
+#pragma unroll
+      for (int u = 0; u < PER; ++u) xv[b][u] = nx[b][u];
+    }
+    if (q0 + B < hi) load(q0 + B, nx, niv);
+#pragma unroll
+    for (uint32_t b = 0; b < B; ++b) {
+      if (b < nb) {
+#pragma unroll
+        for (int u = 0; u < PER; ++u) {
+          const float x = xv[b][u];
+          const float old = mean[u];
+          const float delta = x - old;
+          mean[u] = old + delta * iv[b];
+          m2[u] = m2[u] + delta * (x - mean[u]);
+        }
       }
     }
   }
 #pragma unroll
-  for (int u = 0; u < kTacSpreadPer; ++u) {
+  for (int u = 0; u < PER; ++u) {
     const uint32_t d = lane + 64u * u;
     if (d < dim) m2s[d] = m2[u];
   }
@@ -463,38 +506,68 @@ __global__ void tac_hist_kernel(const uint32_t* __restrict__ code,
   for (uint32_t c = threadIdx.x; c < pr.k; c += blockDim.x) out[c] = hcnt[c];
 }
 
-// Step 2, one block per problem: every code's tile counts become exclusive
-// offsets over the tiles (in place); cluster sizes go to counts and cluster
-// starts (relative to the problem's first row) to start.
-__global__ __launch_bounds__(256) void tac_scan_kernel(uint32_t* __restrict__ hist,
-                                                       const TacProblem* __restrict__ probs,
-                                                       const uint32_t* __restrict__ done,
-                                                       uint32_t* __restrict__ counts,
-                                                       uint32_t* __restrict__ start) {
+// Step 2: every code's tile counts become exclusive offsets over the tiles
+// (in place); cluster sizes go to counts and cluster starts (relative to the
+// problem's first row) to start.  A problem's tiles split into ranges of
+// kTacScanTiles: tac_scan_partial_kernel sums each range per code,
+// tac_scan_apply_kernel adds the ranges before its own and rewrites its
+// tiles; range 0 also writes counts and starts.  One block per range.
+__global__ __launch_bounds__(256) void tac_scan_partial_kernel(
+    const uint32_t* __restrict__ hist, const TacProblem* __restrict__ probs,
+    const TacRange* __restrict__ ranges, const uint32_t* __restrict__ done,
+    uint32_t* __restrict__ rsum) {
+  const TacRange rg = ranges[blockIdx.x];
+  if (done[rg.prob]) return;
+  const TacProblem pr = probs[rg.prob];
+  const uint32_t t0 = rg.r * kTacScanTiles;
+  const uint32_t t1 = t0 + kTacScanTiles < pr.ntiles ? t0 + kTacScanTiles : pr.ntiles;
+  for (uint32_t c = threadIdx.x; c < pr.k; c += blockDim.x) {
+    const uint32_t* h = hist + pr.hist0 + c;
+    uint32_t sum = 0;
+    for (uint32_t t = t0; t < t1; ++t) sum += h[(uint64_t)t * pr.k];
+    rsum[pr.rsum0 + (uint64_t)rg.r * pr.k + c] = sum;
+  }
+}
+
+__global__ __launch_bounds__(256) void tac_scan_apply_kernel(
+    uint32_t* __restrict__ hist, const TacProblem* __restrict__ probs,
+    const TacRange* __restrict__ ranges, const uint32_t* __restrict__ done,
+    const uint32_t* __restrict__ rsum, uint32_t* __restrict__ counts,
+    uint32_t* __restrict__ start) {
   __shared__ uint32_t wsum[256 / kWave];
   __shared__ uint32_t carry;
-  const uint32_t p = blockIdx.x;
-  if (done[p]) return;
-  const TacProblem pr = probs[p];
+  const TacRange rg = ranges[blockIdx.x];
+  if (done[rg.prob]) return;
+  const TacProblem pr = probs[rg.prob];
+  const uint32_t t0 = rg.r * kTacScanTiles;
+  const uint32_t t1 = t0 + kTacScanTiles < pr.ntiles ? t0 + kTacScanTiles : pr.ntiles;
+  const uint32_t* rs = rsum + pr.rsum0;
   if (threadIdx.x == 0) carry = 0;
   __syncthreads();
   for (uint32_t c0 = 0; c0 < pr.k; c0 += blockDim.x) {
     const uint32_t c = c0 + threadIdx.x;
-    uint32_t run = 0;
+    uint32_t total = 0;
     if (c < pr.k) {
+      uint32_t run = 0;
+      for (uint32_t r = 0; r < rg.r; ++r) run += rs[(uint64_t)r * pr.k + c];
       uint32_t* h = hist + pr.hist0 + c;
-      for (uint32_t t = 0; t < pr.ntiles; ++t) {
+      for (uint32_t t = t0; t < t1; ++t) {
         const uint32_t v = h[(uint64_t)t * pr.k];
         h[(uint64_t)t * pr.k] = run;
         run += v;
       }
-      counts[pr.goff + c] = run;
+      if (rg.r == 0) {
+        for (uint32_t r = 0; r < pr.nranges; ++r) total += rs[(uint64_t)r * pr.k + c];
+        counts[pr.goff + c] = total;
+      }
     }
-    const uint32_t ex = block_exclusive_scan(c < pr.k ? run : 0u, wsum);
-    if (c < pr.k) start[pr.goff + c] = carry + ex;
-    __syncthreads();
-    if (threadIdx.x == blockDim.x - 1) carry += ex + run;
-    __syncthreads();
+    if (rg.r == 0) {  // uniform over the block
+      const uint32_t ex = block_exclusive_scan(total, wsum);
+      if (c < pr.k) start[pr.goff + c] = carry + ex;
+      __syncthreads();
+      if (threadIdx.x == blockDim.x - 1) carry += ex + total;
+      __syncthreads();
+    }
   }
 }
 
@@ -543,13 +616,14 @@ __global__ void tac_scatter_kernel(const uint32_t* __restrict__ code,
 
 // ---------------------------------------------------------------------------
 // Cluster sums and update (kmeans.zig:177-198): one wave per global cluster,
-// lane = dimension (strided beyond 64), members folded in ascending row order
-// from 0; centroid = sum * fl(1 / fl(count)).  Empty clusters are left to the
-// reseed kernel.  kTacFoldBatch member rows are loaded ahead of the adds.
+// lane = dimension (PER dimensions per lane), members folded in ascending row
+// order from 0; centroid = sum * fl(1 / fl(count)).  Empty clusters are left
+// to the reseed kernel.  Member rows are loaded kTacFoldBatch at a time, and
+// the next batch's row indices are read while the current batch is added.
 // ---------------------------------------------------------------------------
-constexpr int kTacFoldPer = 12;  // dimensions per lane: dim <= 768
-constexpr uint32_t kTacFoldBatch = 8;
+constexpr uint32_t kTacFoldBatch = 16;
 
+template <int PER>
 __global__ __launch_bounds__(256) void tac_fold_kernel(
     const float* __restrict__ G, const uint32_t* __restrict__ sorted,
     const uint32_t* __restrict__ counts, const uint32_t* __restrict__ start,
@@ -562,33 +636,36 @@ __global__ __launch_bounds__(256) void tac_fold_kernel(
   const uint32_t cnt = counts[g];
   if (cnt == 0) return;
   const uint32_t* mem = sorted + probs[p].off + start[g];
-  const uint32_t per = (dim + kWave - 1) / kWave;
-  float s[kTacFoldPer];
+  float s[PER];
 #pragma unroll
-  for (int u = 0; u < kTacFoldPer; ++u) s[u] = 0.0f;
+  for (int u = 0; u < PER; ++u) s[u] = 0.0f;
+  // lane b < kTacFoldBatch holds member index b of the current batch
+  uint32_t idx = lane < kTacFoldBatch && lane < cnt ? mem[lane] : 0u;
   for (uint32_t q0 = 0; q0 < cnt; q0 += kTacFoldBatch) {
     const uint32_t nb = cnt - q0 < kTacFoldBatch ? cnt - q0 : kTacFoldBatch;
-    uint32_t rows[kTacFoldBatch];
+    float v[kTacFoldBatch][PER];
 #pragma unroll
-    for (uint32_t b = 0; b < kTacFoldBatch; ++b) rows[b] = b < nb ? mem[q0 + b] : 0u;
+    for (uint32_t b = 0; b < kTacFoldBatch; ++b) {
+      const uint32_t row = __shfl(idx, (int)b, kWave);
 #pragma unroll
-    for (int u = 0; u < kTacFoldPer; ++u) {
-      if ((uint32_t)u >= per) break;
-      const uint32_t d = lane + kWave * u;
-      float v[kTacFoldBatch];
-#pragma unroll
-      for (uint32_t b = 0; b < kTacFoldBatch; ++b)
-        v[b] = (b < nb && d < dim) ? G[(uint64_t)rows[b] * dim + d] : 0.0f;
-#pragma unroll
-      for (uint32_t b = 0; b < kTacFoldBatch; ++b)
-        if (b < nb) s[u] = s[u] + v[b];
+      for (int u = 0; u < PER; ++u) {
+        const uint32_t d = lane + kWave * u;
+        v[b][u] = (b < nb && d < dim) ? G[(uint64_t)row * dim + d] : 0.0f;
+      }
     }
+    const uint32_t nq = q0 + kTacFoldBatch + lane;
+    idx = lane < kTacFoldBatch && nq < cnt ? mem[nq] : 0u;
+#pragma unroll
+    for (uint32_t b = 0; b < kTacFoldBatch; ++b)
+      if (b < nb)
+#pragma unroll
+        for (int u = 0; u < PER; ++u) s[u] = s[u] + v[b][u];
   }
   const float inv = 1.0f / (float)cnt;
 #pragma unroll
-  for (int u = 0; u < kTacFoldPer; ++u) {
+  for (int u = 0; u < PER; ++u) {
     const uint32_t d = lane + kWave * u;
-    if ((uint32_t)u < per && d < dim) C[(uint64_t)g * dim + d] = s[u] * inv;
+    if (d < dim) C[(uint64_t)g * dim + d] = s[u] * inv;
   }
 }
 

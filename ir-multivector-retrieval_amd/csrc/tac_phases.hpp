@@ -7,6 +7,7 @@
 #include <math.h>
 #include <stdint.h>
 
+#include <algorithm>
 #include <vector>
 
 namespace tacgpu {
@@ -97,57 +98,57 @@ inline int bound(const std::vector<uint32_t>& f, std::vector<uint32_t>& kappa, c
 // the largest remainder below its cap (surplus), or from the active token
 // with the smallest remainder above the floor (deficit; then small 2 -> 1,
 // then micro 1 -> 0, lowest id first).  Ties go to the lowest token id.
+// The remainders never change and a token stays eligible until it reaches
+// its cap (floor), so the token chosen first keeps being chosen until then:
+// the loop is the same as walking the eligible tokens once, in order of
+// remainder (then id), each taking as many steps as it has room for.
 inline int reconcile(const std::vector<uint32_t>& f, std::vector<uint32_t>& kappa,
                      const std::vector<float>& frac, const Params& p) {
   uint64_t cur = 0;
   for (uint32_t k : kappa) cur += k;
   if (cur == p.kappa_total) return kOk;
   const size_t n = f.size();
+  std::vector<uint32_t> order;
   if (cur < p.kappa_total) {
-    for (uint32_t left = (uint32_t)(p.kappa_total - cur); left > 0; --left) {
-      int64_t best = -1;
-      float bf = -INFINITY;
-      for (size_t j = 0; j < n; ++j) {
-        if (classify(f[j], p.mu, p.tau) != kActive || kappa[j] >= f[j] / p.theta) continue;
-        if (frac[j] > bf || (frac[j] == bf && best < 0)) {
-          best = (int64_t)j;
-          bf = frac[j];
-        }
-      }
-      if (best < 0) return kBudgetTooLarge;
-      ++kappa[best];
+    uint64_t left = p.kappa_total - cur;
+    for (size_t j = 0; j < n; ++j)
+      if (classify(f[j], p.mu, p.tau) == kActive && kappa[j] < f[j] / p.theta)
+        order.push_back((uint32_t)j);
+    std::stable_sort(order.begin(), order.end(),
+                     [&](uint32_t a, uint32_t b) { return frac[a] > frac[b]; });
+    for (uint32_t j : order) {
+      if (left == 0) break;
+      const uint64_t room = f[j] / p.theta - kappa[j];
+      const uint64_t take = room < left ? room : left;
+      kappa[j] += (uint32_t)take;
+      left -= take;
     }
-    return kOk;
+    return left == 0 ? kOk : kBudgetTooLarge;
   }
-  for (uint32_t excess = (uint32_t)(cur - p.kappa_total); excess > 0; --excess) {
-    int64_t best = -1;
-    float bf = INFINITY;
-    for (size_t j = 0; j < n; ++j) {
-      if (classify(f[j], p.mu, p.tau) != kActive || kappa[j] <= p.epsilon) continue;
-      if (frac[j] < bf) {
-        best = (int64_t)j;
-        bf = frac[j];
-      }
-    }
-    if (best >= 0) {
-      --kappa[best];
-      continue;
-    }
-    for (size_t j = 0; j < n && best < 0; ++j)
-      if (classify(f[j], p.mu, p.tau) == kSmall && kappa[j] == 2) best = (int64_t)j;
-    if (best >= 0) {
-      kappa[best] = 1;
-      continue;
-    }
-    for (size_t j = 0; j < n && best < 0; ++j)
-      if (classify(f[j], p.mu, p.tau) == kMicro && kappa[j] == 1) best = (int64_t)j;
-    if (best >= 0) {
-      kappa[best] = 0;
-      continue;
-    }
-    return kBudgetTooSmall;
+  uint64_t excess = cur - p.kappa_total;
+  for (size_t j = 0; j < n; ++j)
+    if (classify(f[j], p.mu, p.tau) == kActive && kappa[j] > p.epsilon)
+      order.push_back((uint32_t)j);
+  std::stable_sort(order.begin(), order.end(),
+                   [&](uint32_t a, uint32_t b) { return frac[a] < frac[b]; });
+  for (uint32_t j : order) {
+    if (excess == 0) break;
+    const uint64_t room = kappa[j] - p.epsilon;
+    const uint64_t take = room < excess ? room : excess;
+    kappa[j] -= (uint32_t)take;
+    excess -= take;
   }
-  return kOk;
+  for (size_t j = 0; j < n && excess > 0; ++j)
+    if (classify(f[j], p.mu, p.tau) == kSmall && kappa[j] == 2) {
+      kappa[j] = 1;
+      --excess;
+    }
+  for (size_t j = 0; j < n && excess > 0; ++j)
+    if (classify(f[j], p.mu, p.tau) == kMicro && kappa[j] == 1) {
+      kappa[j] = 0;
+      --excess;
+    }
+  return excess == 0 ? kOk : kBudgetTooSmall;
 }
 
 // Phases 1-4 (tac.zig:388-401).

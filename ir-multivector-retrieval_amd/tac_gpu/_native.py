@@ -62,6 +62,8 @@ class Profile(ctypes.Structure):
         ("cluster_kpp_ms", ctypes.c_double),
         ("cluster_lloyd_ms", ctypes.c_double),
         ("cluster_calls", c_u64),
+        ("cluster_prep_ms", ctypes.c_double),
+        ("cluster_call_ms", ctypes.c_double),
     ]
 
 

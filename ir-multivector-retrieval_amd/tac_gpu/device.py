@@ -135,6 +135,8 @@ class KernelTimes:
     cluster_kpp_ms: float = 0.0
     cluster_lloyd_ms: float = 0.0
     cluster_calls: int = 0
+    cluster_prep_ms: float = 0.0
+    cluster_call_ms: float = 0.0
 
 
 def profile_enable(on: bool = True) -> None:
@@ -148,4 +150,5 @@ def profile_read(reset: bool = True) -> KernelTimes:
                        p.update_ms, p.update_iters, p.encode_ms, p.encode_launches,
                        p.exact_rescans, p.residual_ms, p.residual_launches, p.crc_ms,
                        p.crc_launches, p.refine_ms, p.refine_launches, p.cluster_kpp_ms,
-                       p.cluster_lloyd_ms, p.cluster_calls)
+                       p.cluster_lloyd_ms, p.cluster_calls, p.cluster_prep_ms,
+                       p.cluster_call_ms)
