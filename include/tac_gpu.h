@@ -337,6 +337,9 @@ typedef struct tac_gpu_profile {
   uint64_t cluster_calls;
   double cluster_prep_ms;  /* wall: grouping, upload, gather, spreads, budget phases, plan */
   double cluster_call_ms;  /* wall: the whole tac_cluster_flat call */
+  uint64_t cand_vectors;   /* (vector, subspace) assignments started from the previous code */
+  uint64_t cand_deferred;  /* of those, the ones left to the full search (candidate row
+                              exhausted, non-finite or huge values) */
 } tac_gpu_profile;
 int tac_gpu_profile_enable(int enable);
 int tac_gpu_profile_read(tac_gpu_profile *out, int reset);

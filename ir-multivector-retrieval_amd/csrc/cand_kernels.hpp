@@ -1,0 +1,393 @@
+// cand_kernels.hpp — exact candidate-set assignment for the Lloyd iterations
+// after the first (src/tac/kmeans.zig:344-365 semantics).  Included once, by
+// tac_gpu.hip, after pq_kernels.hpp.
+//
+// Why the result equals the exhaustive first-index argmin.
+//   Let a be the vector's code from the previous iteration (any valid index
+//   works: a is only an anchor) and U2 = ref(x, c_a), the reference distance
+//   to that codeword in the current codebook.  For every codeword c the
+//   reference fold (D squares and D-1 adds, separately rounded) satisfies
+//     |ref(x, c) - T(x, c)| <= g T(x, c) + eta,    g = gamma_{D+2},
+//   where T is the exact squared distance and eta < 1e-43 covers underflow.
+//   The reference's first-index argmin c* has ref(x, c*) <= U2, so T(x, c*)
+//   and T(x, c_a) are both at most rho^2 = (U2 + eta) / (1 - g), and by the
+//   triangle inequality ||c_a - c*||^2 <= 4 rho^2.  Hence c* lies in
+//     S = {a} + {c : lo(a, c) <= R2},   R2 >= 4 rho^2 (rounded up),
+//   for any lower bound lo(a, c) <= ||c_a - c||^2.  The kernel evaluates
+//   ref() on S exactly as the reference does and keeps the lexicographic
+//   minimum of (distance bits, index): c* has the global minimum and the
+//   smallest index among its ties, so that minimum is c*.
+//
+// Neighbour tables.  After every update, nbr_build_kernel sorts, for each
+// codeword a, the other codewords by lo(a, c) and keeps the first L of them
+// as one u32 key each: the bits of lo with the low 8 bits replaced by c
+// (K <= 256).  Clearing low bits of a non-negative float lowers it, so the
+// key's value part stays a lower bound, and sorted keys put S \ {a} in a
+// prefix of the row.  If the whole kept row lies inside R2 while codewords
+// are missing from it, S may be larger than the row: the vector goes to a
+// deferred list that the pruned full search (pq_kernels.hpp) resolves, as
+// do non-finite or huge distances and non-finite codebooks.
+//
+// Load balance.  A block assigns 1,024 vectors at a time.  Each vector's
+// candidates are cut into items of at most kCandItem; a block-wide scan of
+// the item counts lays the items out evenly over all threads, an item's
+// result folds into its vector's 64-bit LDS key with an atomic minimum, and
+// every thread then writes its own vector's result.  The work per thread
+// follows the mean candidate count, not the largest in a wave.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#include "pq_kernels.hpp"
+
+namespace tacgpu {
+
+constexpr uint32_t kCandList = 64;      // neighbours kept per codeword
+constexpr int kCandThreads = 1024;      // threads per assign_cand block
+constexpr int kCandWaves = kCandThreads / kWave;
+constexpr uint32_t kCandMaxK = 256;     // codeword ids fit the key's low 8 bits
+constexpr uint32_t kCandLdsMax = 160 * 1024;
+
+// gamma_n = n u / (1 - n u) with n = D + 2, u = 2^-24: relative error bound
+// of the reference fold at sub-dimension D.
+template <int D>
+__host__ __device__ constexpr float fold_gamma() {
+  return (float)(D + 2) * 5.9604644775390625e-8f / (1.0f - (float)(D + 2) * 5.9604644775390625e-8f);
+}
+
+constexpr uint32_t kCandItem = 8;  // candidates per work item
+
+// LDS layout of assign_cand_kernel, shared by the host launcher:
+//   lcb [K][DP] f32 | lnbr [K][L|1] u32 (an odd row stride puts the rows of
+//   different anchors in different banks) | group of kCandThreads vectors:
+//   gx [][DP] f32, gbest [] u64, gmeta [] u32 (a | count << 8),
+//   gitem [kCandThreads * 8] u16 (vector | item << 10) | wsum [16] u32 |
+//   lmax, lcnt u32
+struct CandLds {
+  uint32_t nbr_off, grp_off, item_off, wsum_off, total;
+};
+__host__ __device__ inline uint32_t cand_up16(uint32_t b) { return (b + 15u) & ~15u; }
+__host__ __device__ inline CandLds cand_lds(uint32_t K, uint32_t L, uint32_t DP) {
+  CandLds s;
+  s.nbr_off = cand_up16(K * DP * 4u);
+  s.grp_off = cand_up16(s.nbr_off + K * (L | 1u) * 4u);
+  s.item_off = s.grp_off + (uint32_t)kCandThreads * (DP * 4u + 8u + 4u);
+  s.wsum_off = cand_up16(s.item_off + (uint32_t)kCandThreads * 8u * 2u);
+  s.total = s.wsum_off + 16u * 4u + 16u;
+  return s;
+}
+
+// Block barrier that orders LDS only: outstanding global loads (the next
+// group's prefetch) and stores stay in flight across it.
+__device__ __forceinline__ void lds_barrier() {
+  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup", "local");
+  __builtin_amdgcn_s_barrier();
+  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup", "local");
+}
+
+// Value part of a neighbour key: a lower bound of ||c_a - c||^2.
+__device__ __forceinline__ float cand_key_value(uint32_t key) {
+  return __uint_as_float(key & 0xFFFFFF00u);
+}
+
+// One wave per (codeword a, subspace m): lo(a, c) for every c != a, a
+// bitonic sort of the 256 keys in LDS, the first L written to
+// nbr[m][a][0 .. L).
+template <int D>
+__global__ __launch_bounds__(kWave) void nbr_build_kernel(const float* __restrict__ cb,
+                                                          uint32_t* __restrict__ nbr,
+                                                          const uint32_t* __restrict__ done,
+                                                          uint32_t K, uint32_t L) {
+  __shared__ uint32_t keys[kCandMaxK];
+  const uint32_t a = blockIdx.x, m = blockIdx.y, lane = threadIdx.x;
+  if (done[m]) return;
+  constexpr float g = fold_gamma<D>();
+  const float* cbm = cb + (uint64_t)m * K * D;
+  float ca[D];
+#pragma unroll
+  for (int k = 0; k < D; ++k) ca[k] = cbm[(uint64_t)a * D + k];
+  for (uint32_t c = lane; c < kCandMaxK; c += kWave) {
+    uint32_t key = 0xFFFFFFFFu;
+    if (c < K && c != a) {
+      float cv[D];
+#pragma unroll
+      for (int k = 0; k < D; ++k) cv[k] = cbm[(uint64_t)c * D + k];
+      // ||c_a - c||^2 >= (s - eta) / (1 + g) >= s (1 - 2g) - 1e-38 (rounded).
+      const float s = exact_l2sq<D>(ca, cv);
+      float lo = s * (1.0f - 2.0f * g) - 1e-38f;
+      lo = fmaxf(lo, 0.0f);
+      key = (__float_as_uint(lo) & 0xFFFFFF00u) | c;
+    }
+    keys[c] = key;
+  }
+  wave_lds_sync();
+  for (uint32_t k = 2; k <= kCandMaxK; k <<= 1) {
+    for (uint32_t j = k >> 1; j > 0; j >>= 1) {
+      for (uint32_t q = lane; q < kCandMaxK / 2; q += kWave) {
+        const uint32_t i = ((q & ~(j - 1)) << 1) | (q & (j - 1));
+        const uint32_t p = i | j;
+        const uint32_t x = keys[i], y = keys[p];
+        const bool up = (i & k) == 0;
+        if ((x > y) == up) {
+          keys[i] = y;
+          keys[p] = x;
+        }
+      }
+      wave_lds_sync();
+    }
+  }
+  uint32_t* row = nbr + ((uint64_t)m * K + a) * L;
+  for (uint32_t j = lane; j < L; j += kWave) row[j] = keys[j];
+}
+
+// Lloyd assignment from the previous codes.  Block b = (chunk of vectors
+// [b*chunk, (b+1)*chunk), subspace m); codes[m][i] holds the previous
+// iteration's code on entry and the new one on exit, e[m][i] the reference
+// distance to it.  Vectors the candidate rule cannot settle are listed in
+// the block's own slice defer[m][b*chunk ..] (an LDS counter, so no global
+// atomics), their number in defer_count[m][b], for assign_list_kernel.
+template <int D>
+__global__ __launch_bounds__(kCandThreads) void assign_cand_kernel(
+    const float* __restrict__ xs, const float* __restrict__ cb, const uint32_t* __restrict__ nbr,
+    uint16_t* __restrict__ codes, float* __restrict__ e, uint32_t* __restrict__ defer,
+    uint32_t* __restrict__ defer_count, const uint32_t* __restrict__ done, uint64_t n,
+    uint32_t K, uint32_t L, uint32_t chunk) {
+  constexpr int DP = Pad<D>::value;
+  constexpr float g = fold_gamma<D>();
+  extern __shared__ __attribute__((aligned(16))) float lds[];
+  const uint32_t m = blockIdx.y;
+  if (done[m]) return;
+  const CandLds lay = cand_lds(K, L, DP);
+  uint8_t* base = reinterpret_cast<uint8_t*>(lds);
+  float* lcb = lds;
+  uint32_t* lnbr = reinterpret_cast<uint32_t*>(base + lay.nbr_off);
+  float* gx = reinterpret_cast<float*>(base + lay.grp_off);
+  unsigned long long* gbest = reinterpret_cast<unsigned long long*>(gx + kCandThreads * DP);
+  uint32_t* gmeta = reinterpret_cast<uint32_t*>(gbest + kCandThreads);
+  uint16_t* gitem = reinterpret_cast<uint16_t*>(base + lay.item_off);
+  uint32_t* wsum = reinterpret_cast<uint32_t*>(base + lay.wsum_off);
+  uint32_t* lmax = wsum + 16;
+  uint32_t* lcnt = lmax + 1;
+  const uint32_t t = threadIdx.x, lane = t % kWave, wave = t / kWave;
+
+  if (t == 0) {
+    *lmax = 0;
+    *lcnt = 0;
+  }
+  __syncthreads();
+  const float* cbm = cb + (uint64_t)m * K * D;
+  for (uint32_t c = t; c < K; c += blockDim.x) {
+    float v[DP];
+#pragma unroll
+    for (int k = 0; k < DP; ++k) v[k] = k < D ? cbm[(uint64_t)c * D + k] : 0.0f;
+    float s = 0.0f;
+#pragma unroll
+    for (int k = 0; k < D; ++k) s = s + v[k] * v[k];
+#pragma unroll
+    for (int k = 0; k < DP; ++k) lcb[c * DP + k] = v[k];
+    atomicMax(lmax, __float_as_uint(s));  // >= 0x7f800000: a non-finite codeword
+  }
+  const uint32_t Ls = L | 1u;  // LDS row stride
+  const uint32_t* nbm = nbr + (uint64_t)m * K * L;
+  for (uint32_t j = t; j < K * L; j += blockDim.x) lnbr[(j / L) * Ls + j % L] = nbm[j];
+  __syncthreads();
+  const bool all_deferred = *lmax >= 0x7f800000u;
+  const bool row_complete = L + 1 >= K;  // every other codeword is in the row
+
+  const uint64_t lo_i = (uint64_t)blockIdx.x * chunk;
+  const uint64_t hi_i = lo_i + chunk < n ? lo_i + chunk : n;
+  const float* xm = xs + (uint64_t)m * n * DP;
+  uint16_t* cm = codes + (uint64_t)m * n;
+  float* em = e + (uint64_t)m * n;
+  // Each group's vectors and previous codes are loaded one group ahead.
+  float xq[D];
+  uint32_t aq = 0;
+#pragma unroll
+  for (int k = 0; k < D; ++k) xq[k] = 0.0f;
+  if (lo_i + t < hi_i) {
+    load_padded<D>(xm + (lo_i + t) * DP, xq);
+    aq = cm[lo_i + t];
+  }
+  for (uint64_t g0 = lo_i; g0 < hi_i; g0 += kCandThreads) {
+    // Phase 1: anchor distance and candidate count of vector t.
+    const uint64_t i = g0 + t;
+    const bool valid = i < hi_i;
+    float x[D];
+#pragma unroll
+    for (int k = 0; k < D; ++k) x[k] = xq[k];
+    const uint32_t a = valid ? aq : 0u;
+    bool deferred = valid && (all_deferred || a >= K);
+    uint32_t cnt = 0;
+    float U2 = 0.0f;
+    if (valid && !deferred) {
+      float ca[D];
+      load_padded<D>(lcb + a * DP, ca);
+      U2 = exact_l2sq<D>(x, ca);
+      if (!(U2 < 1e37f)) {  // NaN, inf or too large for the bound arithmetic
+        deferred = true;
+      } else {
+        // R2 >= 4 (U2 + eta) / (1 - g): the x4 is exact, the factor covers g
+        // and the rounding of the product, the addend covers eta.
+        const float R2 = (U2 * 4.0f) * (1.0f + 8.0f * g) + 1e-38f;
+        const uint32_t* row = lnbr + a * Ls;
+        uint32_t lo = 0, len = L;  // first entry whose value exceeds R2
+        while (len > 0) {
+          const uint32_t half = len >> 1;
+          if (cand_key_value(row[lo + half]) <= R2) {
+            lo += half + 1;
+            len -= half + 1;
+          } else {
+            len = half;
+          }
+        }
+        cnt = lo;
+        if (cnt == L && !row_complete) {
+          deferred = true;
+          cnt = 0;
+        }
+      }
+    }
+    const bool live = valid && !deferred;
+    if (live) {
+#pragma unroll
+      for (int k = 0; k < DP; ++k) gx[t * DP + k] = k < D ? x[k] : 0.0f;
+      gbest[t] = ((unsigned long long)__float_as_uint(U2) << 32) | a;
+      gmeta[t] = a | (cnt << 8);
+    }
+    if (i + kCandThreads < hi_i) {
+      load_padded<D>(xm + (i + kCandThreads) * DP, xq);
+      aq = cm[i + kCandThreads];
+    }
+    const uint64_t dm = __ballot(valid && deferred);
+    if (dm) {
+      uint32_t at = 0;
+      if (lane == 0) at = atomicAdd(lcnt, (uint32_t)__popcll(dm));
+      at = __shfl(at, 0, kWave);
+      if (valid && deferred)
+        defer[(uint64_t)m * n + lo_i + at + (uint32_t)__popcll(dm & ((1ull << lane) - 1ull))] =
+            (uint32_t)i;
+    }
+    // Phase 2: block-wide exclusive scan of the item counts.
+    const uint32_t nit = (cnt + kCandItem - 1) / kCandItem;  // <= 8
+    uint32_t incl = nit;
+#pragma unroll
+    for (int off = 1; off < kWave; off <<= 1) {
+      const uint32_t o = __shfl_up(incl, off, kWave);
+      if (lane >= (uint32_t)off) incl += o;
+    }
+    if (lane == kWave - 1) wsum[wave] = incl;
+    lds_barrier();
+    uint32_t before = 0, total = 0;
+    for (uint32_t q = 0; q < (uint32_t)kCandWaves; ++q) {
+      const uint32_t w = wsum[q];
+      before += q < wave ? w : 0u;
+      total += w;
+    }
+    const uint32_t first = before + incl - nit;
+    for (uint32_t q = 0; q < nit; ++q) gitem[first + q] = (uint16_t)(t | (q << 10));
+    lds_barrier();
+    // Phase 3: items, kCandThreads at a time.
+    for (uint32_t w = t; w < total; w += kCandThreads) {
+      const uint32_t it = gitem[w];
+      const uint32_t u = it & 1023u, j0 = (it >> 10) * kCandItem;
+      const uint32_t meta = gmeta[u];
+      const uint32_t cu = meta >> 8;
+      const uint32_t jn = cu - j0 < kCandItem ? cu - j0 : kCandItem;
+      const uint32_t* row = lnbr + (meta & 0xFFu) * Ls + j0;
+      uint32_t cs[kCandItem];
+#pragma unroll
+      for (uint32_t k = 0; k < kCandItem; ++k) cs[k] = k < jn ? row[k] & 0xFFu : 0u;
+      float xv[D];
+      load_padded<D>(gx + u * DP, xv);
+      unsigned long long best = ~0ull;
+#pragma unroll
+      for (uint32_t k = 0; k < kCandItem; ++k) {
+        if (k < jn) {
+          float cv[D];
+          load_padded<D>(lcb + cs[k] * DP, cv);
+          const float d = exact_l2sq<D>(xv, cv);
+          const unsigned long long key = ((unsigned long long)__float_as_uint(d) << 32) | cs[k];
+          best = key < best ? key : best;
+        }
+      }
+      atomicMin(&gbest[u], best);
+    }
+    lds_barrier();
+    if (live) {
+      const unsigned long long k = gbest[t];
+      cm[i] = (uint16_t)(k & 0xFFFFu);
+      em[i] = __uint_as_float((uint32_t)(k >> 32));
+    }
+  }
+  lds_barrier();
+  if (t == 0) defer_count[(uint64_t)m * gridDim.x + blockIdx.x] = *lcnt;
+}
+
+// The deferred vectors: the pruned exact search over all K codewords
+// (pq_kernels.hpp), vectors gathered through the list slice of
+// assign_cand_kernel's block (blockIdx.x, m), in tiles of kBlock*VPT.
+// stats[0] += deferred vectors, stats[1] += vectors of the slice.
+template <int D, int VPT>
+__global__ __launch_bounds__(kBlock) void assign_list_kernel(
+    const float* __restrict__ xs, const float* __restrict__ cb, uint16_t* __restrict__ codes,
+    float* __restrict__ e, const uint32_t* __restrict__ defer,
+    const uint32_t* __restrict__ defer_count, const uint32_t* __restrict__ done, uint64_t n,
+    uint32_t K, uint32_t chunk, unsigned long long* __restrict__ rescans,
+    unsigned long long* __restrict__ stats) {
+  constexpr int DP = Pad<D>::value;
+  constexpr uint32_t kTile = kBlock * VPT;
+  extern __shared__ __attribute__((aligned(16))) float lds[];
+  const uint32_t m = blockIdx.y;
+  if (done[m]) return;
+  const uint32_t cnt = defer_count[(uint64_t)m * gridDim.x + blockIdx.x];
+  const uint64_t lo_i = (uint64_t)blockIdx.x * chunk;
+  if (threadIdx.x == 0) {
+    atomicAdd(&stats[0], (unsigned long long)cnt);
+    atomicAdd(&stats[1], (unsigned long long)((lo_i + chunk < n ? lo_i + chunk : n) - lo_i));
+  }
+  if (cnt == 0) return;
+  const uint32_t Kp = (K + kPruneBlock - 1) / kPruneBlock * kPruneBlock;
+  float* lcb = lds;
+  float* lnc = lds + Kp * DP;
+  uint32_t& lmax = *reinterpret_cast<uint32_t*>(lnc + Kp);
+  uint32_t& lcount = *(&lmax + 1);
+  if (threadIdx.x == 0) {
+    lmax = 0;
+    lcount = 0;
+  }
+  __syncthreads();
+  stage_pruned<D>(lcb, lnc, &lmax, cb + (uint64_t)m * K * D, K, Kp);
+  __syncthreads();
+  const float* xm = xs + (uint64_t)m * n * DP;
+  const uint32_t* lst = defer + (uint64_t)m * n + lo_i;
+  uint32_t mine = 0;
+  for (uint32_t t0 = 0; t0 < cnt; t0 += kTile) {
+    float x[VPT][D];
+    uint32_t idx[VPT];
+#pragma unroll
+    for (int j = 0; j < VPT; ++j) {
+      const uint64_t q = t0 + threadIdx.x + (uint64_t)j * kBlock;
+      idx[j] = q < cnt ? lst[q] : 0xFFFFFFFFu;
+      if (idx[j] != 0xFFFFFFFFu) {
+        load_padded<D>(xm + (uint64_t)idx[j] * DP, x[j]);
+      } else {
+#pragma unroll
+        for (int k = 0; k < D; ++k) x[j][k] = 0.0f;
+      }
+    }
+    uint32_t bidx[VPT];
+    float best[VPT];
+    pruned_argmin<D, VPT, true>(x, lcb, lnc, K, Kp, lmax, bidx, best, mine);
+#pragma unroll
+    for (int j = 0; j < VPT; ++j) {
+      if (idx[j] != 0xFFFFFFFFu) {
+        codes[(uint64_t)m * n + idx[j]] = (uint16_t)bidx[j];
+        e[(uint64_t)m * n + idx[j]] = best[j];
+      }
+    }
+  }
+  flush_rescans(mine, &lcount, rescans);
+}
+
+}  // namespace tacgpu

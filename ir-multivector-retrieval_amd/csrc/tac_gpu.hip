@@ -18,6 +18,7 @@
 // per-subspace flag, so the host never waits inside the loop.
 #include "../../include/tac_gpu.h"
 #include "pq_kernels.hpp"
+#include "cand_kernels.hpp"
 #include "kmeanspp.hpp"
 #include "storage_kernels.hpp"
 #include "query_kernels.hpp"
@@ -87,7 +88,7 @@ struct DeviceState {
   // training / encode workspace
   Buffer xs, codes, e, hist, counts, start, sorted, flags, scal, trace, io_in, io_out, io_cb,
       io_init, counter, kpp_state, kpp_w, kpp_bsum, kpp_bad, status, io_aux, io_out2, scan_sums,
-      io_x1, io_x2, io_x3, crc_tx, fold_pre, fold_chunks;
+      io_x1, io_x2, io_x3, crc_tx, fold_pre, fold_chunks, cand_nbr, cand_defer, cand_count;
   // token-aware clustering
   Buffer tac_v, tac_idx, tac_offs, tac_G, tac_spreads, tac_w, tac_e, tac_code, tac_sorted,
       tac_tsum, tac_hist, tac_counts, tac_start, tac_C, tac_pre, tac_fch, tac_st, tac_bad,
@@ -183,20 +184,24 @@ int event_at(DeviceState &ds, size_t idx, hipEvent_t *out) {
 
 // Device counter of vectors the pruned search resolved by a full reference
 // scan; zeroed per call, added to the profile when measuring.
+// Device counters: [0] exact rescans, [1] candidate-path deferrals,
+// [2] candidate-path assignments.
 int counter_begin(DeviceState &ds, hipStream_t s, unsigned long long **out) {
-  int st = ensure(ds, ds.counter, sizeof(unsigned long long));
+  int st = ensure(ds, ds.counter, 3 * sizeof(unsigned long long));
   if (st) return st;
-  HIP_TRY(hipMemsetAsync(ds.counter.ptr, 0, sizeof(unsigned long long), s));
+  HIP_TRY(hipMemsetAsync(ds.counter.ptr, 0, 3 * sizeof(unsigned long long), s));
   *out = reinterpret_cast<unsigned long long *>(ds.counter.ptr);
   return TAC_OK;
 }
 
 int counter_collect(DeviceState &ds, hipStream_t s) {
-  unsigned long long v = 0;
-  HIP_TRY(hipMemcpyAsync(&v, ds.counter.ptr, sizeof(v), hipMemcpyDeviceToHost, s));
+  unsigned long long v[3] = {0, 0, 0};
+  HIP_TRY(hipMemcpyAsync(v, ds.counter.ptr, sizeof(v), hipMemcpyDeviceToHost, s));
   HIP_TRY(hipStreamSynchronize(s));
   std::lock_guard<std::mutex> g(g_profile_mu);
-  g_prof.exact_rescans += v;
+  g_prof.exact_rescans += v[0];
+  g_prof.cand_deferred += v[1];
+  g_prof.cand_vectors += v[2];
   return TAC_OK;
 }
 
@@ -266,6 +271,40 @@ struct Launch {
     const uint32_t Kp = (K + kPruneBlock - 1) / kPruneBlock * kPruneBlock;
     const size_t lds = (size_t)Kp * (Pad<D>::value + 1) * sizeof(float) + 2 * sizeof(uint32_t);
     assign_kernel<D, VPT><<<grid, kBlock, lds, s>>>(xs, cb, codes, e, done, n, K, rescans);
+  }
+  // Candidate-set assignment (cand_kernels.hpp): neighbour tables of the
+  // current codebooks, the assignment from the previous codes, then the
+  // pruned full search of the deferred vectors.
+  static int assign_cand(const float *xs, const float *cb, uint32_t *nbr, uint16_t *codes,
+                         float *e, uint32_t *defer, uint32_t *defer_count, const uint32_t *done,
+                         uint64_t n, uint32_t M, uint32_t K, uint32_t L,
+                         unsigned long long *rescans, hipStream_t s) {
+    nbr_build_kernel<D><<<dim3(K, M), kWave, 0, s>>>(cb, nbr, done, K, L);
+    const CandLds lay = cand_lds(K, L, Pad<D>::value);
+    if (lay.total > 65536) {
+      static bool raised = false;
+      if (!raised) {
+        const hipError_t err = hipFuncSetAttribute((const void *)assign_cand_kernel<D>,
+                                                   hipFuncAttributeMaxDynamicSharedMemorySize,
+                                                   (int)cand_lds(kCandMaxK, kCandList,
+                                                                 Pad<D>::value).total);
+        if (err != hipSuccess) return hip_status("hipFuncSetAttribute(assign_cand_kernel)", err);
+        raised = true;
+      }
+    }
+    // About 1,024 blocks over all subspaces; a chunk is whole groups of
+    // kCandThreads vectors.
+    const uint64_t per_sub = std::max<uint64_t>(1, (1024 + M - 1) / M);
+    uint64_t chunk = (n + per_sub - 1) / per_sub;
+    chunk = (chunk + kCandThreads - 1) / kCandThreads * kCandThreads;
+    const uint64_t nblk = (n + chunk - 1) / chunk;
+    assign_cand_kernel<D><<<dim3((unsigned)nblk, M), kCandThreads, lay.total, s>>>(
+        xs, cb, nbr, codes, e, defer, defer_count, done, n, K, L, (uint32_t)chunk);
+    const uint32_t Kp = (K + kPruneBlock - 1) / kPruneBlock * kPruneBlock;
+    const size_t lds = (size_t)Kp * (Pad<D>::value + 1) * sizeof(float) + 2 * sizeof(uint32_t);
+    assign_list_kernel<D, VPT><<<dim3((unsigned)nblk, M), kBlock, lds, s>>>(
+        xs, cb, codes, e, defer, defer_count, done, n, K, (uint32_t)chunk, rescans, rescans + 1);
+    return TAC_OK;
   }
   static int scatter(const float *xs, const uint16_t *codes, const uint32_t *hist,
                      const uint32_t *start, float *sorted, const uint32_t *done, uint64_t n,
@@ -464,6 +503,17 @@ int train_core(DeviceState &ds, hipStream_t s, const float *d_x, uint64_t n, uin
   if ((st = ensure(ds, ds.scal, (size_t)2 * M * sizeof(float)))) return st;
   if (want_trace && (st = ensure(ds, ds.trace, (size_t)max_iters * cb_elems * sizeof(float))))
     return st;
+  // Iterations after the first start from the previous codes (cand_kernels.hpp)
+  // when the codeword ids fit the neighbour keys and the tables fit in LDS.
+  // TAC_GPU_FULL_SEARCH=1 keeps the full search in every iteration.
+  const char *full_env = getenv("TAC_GPU_FULL_SEARCH");
+  const uint32_t Lc = K >= 2 ? std::min<uint32_t>(kCandList, K - 1) : 0;
+  const bool cand = !(full_env && full_env[0] == '1') && K >= 2 && K <= kCandMaxK &&
+                    cand_lds(K, Lc, DP).total <= kCandLdsMax && max_iters > 1;
+  if (cand && ((st = ensure(ds, ds.cand_nbr, (size_t)M * K * Lc * sizeof(uint32_t))) ||
+               (st = ensure(ds, ds.cand_defer, (size_t)M * n * sizeof(uint32_t))) ||
+               (st = ensure(ds, ds.cand_count, (size_t)M * (1024 / M + 2) * sizeof(uint32_t)))))
+    return st;
 
   float *xs = as<float>(ds.xs);
   uint16_t *codes = as<uint16_t>(ds.codes);
@@ -515,8 +565,16 @@ int train_core(DeviceState &ds, hipStream_t s, const float *d_x, uint64_t n, uin
         return st;
       HIP_TRY(hipEventRecord(a, s));
     }
-    DISPATCH_D(D, assign(xs, out.cb, codes, e, done, n, M, K, rescans, s));
-    LAUNCH_TRY("assign_kernel");
+    if (cand && t > 0) {
+      DISPATCH_D_ST(D, assign_cand(xs, out.cb, as<uint32_t>(ds.cand_nbr), codes, e,
+                                   as<uint32_t>(ds.cand_defer), as<uint32_t>(ds.cand_count),
+                                   done, n, M, K, Lc, rescans, s));
+      if (st) return st;
+      LAUNCH_TRY("assign_cand kernels");
+    } else {
+      DISPATCH_D(D, assign(xs, out.cb, codes, e, done, n, M, K, rescans, s));
+      LAUNCH_TRY("assign_kernel");
+    }
     if (profile) HIP_TRY(hipEventRecord(b, s));
     hist_kernel<<<dim3(T, M), kBlock, hist_lds, s>>>(codes, hist, done, n, K, T);
     LAUNCH_TRY("hist_kernel");

@@ -64,6 +64,8 @@ class Profile(ctypes.Structure):
         ("cluster_calls", c_u64),
         ("cluster_prep_ms", ctypes.c_double),
         ("cluster_call_ms", ctypes.c_double),
+        ("cand_vectors", c_u64),
+        ("cand_deferred", c_u64),
     ]
 
 

@@ -1,0 +1,103 @@
+"""GPU parity of the candidate-set Lloyd assignment (iterations after the first).
+
+From the second iteration on, each vector is assigned by evaluating only the
+codewords that can tie or beat its previous code under the reference
+distance; the rest go to the pruned full search.  These tests train through
+both paths on inputs built to stress the rule: exact duplicate points and
+codewords (ties resolved by the first index), distances in the subnormal
+range, large magnitudes, every sub-dimension 1-8 and K from 2 to 256, and
+compare bit for bit with the oracle (src/tac/kmeans.zig:154-224 restated).
+"""
+import numpy as np
+import pytest
+
+from oracle import binding as orc
+from tac_gpu import device, kmeans, pq, synth
+
+NEVER = float("-inf")
+pytestmark = pytest.mark.gpu
+
+
+def _bits(a):
+    return np.ascontiguousarray(a, dtype=np.float32).reshape(-1).view(np.uint32)
+
+
+def _train_both(x, dim, m, ksub, init, iters):
+    got = pq.train(x, dim, 0, m=m, ksub=ksub, max_iters=iters, tol=NEVER, init_codebooks=init,
+                   trace=True)
+    ref = orc.pq_train(x, dim, m, ksub, init=init, max_iters=iters, tol=NEVER, n_threads=16,
+                       trace=True)
+    assert ref.status == 0
+    for t in range(iters):
+        diff = np.count_nonzero(_bits(got.stats.trace[t]) != _bits(ref.trace[t]))
+        assert diff == 0, f"iteration {t}: {diff} codebook floats differ"
+    assert np.array_equal(got.stats.empties, ref.empties)
+    return got, ref
+
+
+@pytest.mark.parametrize("dsub,ksub", [(1, 256), (2, 256), (3, 100), (4, 256), (5, 65),
+                                       (6, 17), (7, 2), (8, 256)])
+def test_sub_dimensions_and_codebook_sizes(gpu, dsub, ksub):
+    m = 4
+    dim = m * dsub
+    rng = np.random.default_rng(100 + dsub)
+    x = (rng.standard_normal((9000, dim)) * 0.2).astype(np.float32)
+    init = synth.shuffle_init(x, m, ksub, 5)
+    _train_both(x, dim, m, ksub, init, 6)
+
+
+def test_duplicate_points_and_codewords(gpu):
+    # 6,000 vectors drawn from 250 distinct points: every assignment has exact
+    # ties, clusters empty out and get reseeded onto duplicates.
+    rng = np.random.default_rng(7)
+    pts = (rng.standard_normal((250, 16)) * 0.3).astype(np.float32)
+    x = pts[rng.integers(0, 250, 6000)]
+    init = synth.shuffle_init(x, 4, 256, 1)
+    init[:, 128:] = init[:, :128]
+    _, ref = _train_both(x, 16, 4, 256, init, 6)
+    assert ref.empties.sum() > 0
+
+
+@pytest.mark.parametrize("scale", [1e-19, 1e-12, 1e15])
+def test_extreme_magnitudes(gpu, scale):
+    # 1e-19: squared distances are subnormal, the candidate rows cannot
+    # separate codewords and vectors go to the full search.  1e15: distances
+    # near 1e30, inside the bound arithmetic's range.
+    rng = np.random.default_rng(11)
+    x = (rng.standard_normal((5000, 16)) * scale).astype(np.float32)
+    init = synth.shuffle_init(x, 4, 256, 2)
+    _train_both(x, 16, 4, 256, init, 5)
+
+
+def test_matches_full_search_on_the_chunk_workload(gpu, monkeypatch):
+    # 117,645 x 64, m16 k256, 20 iterations: the default path (candidates
+    # from iteration 1) and TAC_GPU_FULL_SEARCH=1 give the same bytes, and
+    # the candidate path settles most vectors without the full search.
+    w, x, init = synth.workload("chunk-117k")
+    device.profile_enable(True)
+    device.profile_read(reset=True)
+    got = pq.train(x, w.dim, 0, m=w.m, ksub=w.ksub, max_iters=w.iters, tol=NEVER,
+                   init_codebooks=init)
+    prof = device.profile_read(reset=True)
+    monkeypatch.setenv("TAC_GPU_FULL_SEARCH", "1")
+    full = pq.train(x, w.dim, 0, m=w.m, ksub=w.ksub, max_iters=w.iters, tol=NEVER,
+                    init_codebooks=init)
+    prof_full = device.profile_read(reset=True)
+    device.profile_enable(False)
+    assert np.array_equal(_bits(got.codebooks), _bits(full.codebooks))
+    assert prof.cand_vectors == (w.iters - 1) * w.m * w.n
+    assert 0 < prof.cand_deferred < 0.1 * prof.cand_vectors
+    assert prof_full.cand_vectors == 0
+
+
+def test_kmeans_fit_assignments(gpu):
+    # M = 1 through kmeans.fit: assignments, wcss and iteration count.
+    rng = np.random.default_rng(0x5EED)
+    v = (rng.standard_normal((20000, 6)) * 0.5).astype(np.float32).reshape(-1)
+    init = v[: 200 * 6].copy()
+    got = kmeans.fit(v, 6, 200, max_iters=12, tol=1e-6, init_centroids=init)
+    ref = orc.kmeans_fit(v, 6, 200, max_iters=12, tol=1e-6, init=init)
+    assert got.iters_run == ref.iters_run
+    assert np.array_equal(got.assignments, ref.assignments)
+    assert np.array_equal(_bits(got.centroids), _bits(ref.centroids))
+    assert np.float32(got.wcss).view(np.uint32) == np.float32(ref.wcss).view(np.uint32)
