@@ -60,23 +60,29 @@ constexpr uint32_t kCandItem = 8;  // candidates per work item
 
 // LDS layout of assign_cand_kernel, shared by the host launcher:
 //   lcb [K][DP] f32 | lnbr [K][L|1] u32 (an odd row stride puts the rows of
-//   different anchors in different banks) | group of kCandThreads vectors:
-//   gx [][DP] f32, gbest [] u64, gmeta [] u32 (a | count << 8),
+//   different anchors in different banks) | lsamp [K][8] u32: the value bits
+//   of row entries 0, 7, 15, ..., 55 (all-ones past the row) | group of
+//   kCandThreads vectors: gx [][DP] f32, gbest [] u64, gR2 [] f32, ga [] u32,
 //   gitem [kCandThreads * 8] u16 (vector | item << 10) | wsum [16] u32 |
 //   lmax, lcnt u32
 struct CandLds {
-  uint32_t nbr_off, grp_off, item_off, wsum_off, total;
+  uint32_t nbr_off, samp_off, grp_off, item_off, wsum_off, total;
 };
 __host__ __device__ inline uint32_t cand_up16(uint32_t b) { return (b + 15u) & ~15u; }
 __host__ __device__ inline CandLds cand_lds(uint32_t K, uint32_t L, uint32_t DP) {
   CandLds s;
   s.nbr_off = cand_up16(K * DP * 4u);
-  s.grp_off = cand_up16(s.nbr_off + K * (L | 1u) * 4u);
-  s.item_off = s.grp_off + (uint32_t)kCandThreads * (DP * 4u + 8u + 4u);
+  s.samp_off = cand_up16(s.nbr_off + K * (L | 1u) * 4u);
+  s.grp_off = s.samp_off + K * 8u * 4u;
+  s.item_off = s.grp_off + (uint32_t)kCandThreads * (DP * 4u + 8u + 4u + 4u);
   s.wsum_off = cand_up16(s.item_off + (uint32_t)kCandThreads * 8u * 2u);
   s.total = s.wsum_off + 16u * 4u + 16u;
   return s;
 }
+
+// Row position of sample q: 0, 7, 15, ..., 55.  With b samples inside R2
+// the row's entries inside R2 all lie in [0, 8b): item q covers [8q, 8q+8).
+__host__ __device__ inline uint32_t cand_sample_pos(uint32_t q) { return q ? 8u * q - 1u : 0u; }
 
 // Block barrier that orders LDS only: outstanding global loads (the next
 // group's prefetch) and stores stay in flight across it.
@@ -162,9 +168,11 @@ __global__ __launch_bounds__(kCandThreads) void assign_cand_kernel(
   uint8_t* base = reinterpret_cast<uint8_t*>(lds);
   float* lcb = lds;
   uint32_t* lnbr = reinterpret_cast<uint32_t*>(base + lay.nbr_off);
+  uint32_t* lsamp = reinterpret_cast<uint32_t*>(base + lay.samp_off);
   float* gx = reinterpret_cast<float*>(base + lay.grp_off);
   unsigned long long* gbest = reinterpret_cast<unsigned long long*>(gx + kCandThreads * DP);
-  uint32_t* gmeta = reinterpret_cast<uint32_t*>(gbest + kCandThreads);
+  float* gR2 = reinterpret_cast<float*>(gbest + kCandThreads);
+  uint32_t* ga = reinterpret_cast<uint32_t*>(gR2 + kCandThreads);
   uint16_t* gitem = reinterpret_cast<uint16_t*>(base + lay.item_off);
   uint32_t* wsum = reinterpret_cast<uint32_t*>(base + lay.wsum_off);
   uint32_t* lmax = wsum + 16;
@@ -191,6 +199,10 @@ __global__ __launch_bounds__(kCandThreads) void assign_cand_kernel(
   const uint32_t Ls = L | 1u;  // LDS row stride
   const uint32_t* nbm = nbr + (uint64_t)m * K * L;
   for (uint32_t j = t; j < K * L; j += blockDim.x) lnbr[(j / L) * Ls + j % L] = nbm[j];
+  for (uint32_t j = t; j < K * 8; j += blockDim.x) {
+    const uint32_t pos = cand_sample_pos(j % 8);
+    lsamp[j] = pos < L ? nbm[(j / 8) * L + pos] & 0xFFFFFF00u : 0xFFFFFFFFu;
+  }
   __syncthreads();
   const bool all_deferred = *lmax >= 0x7f800000u;
   const bool row_complete = L + 1 >= K;  // every other codeword is in the row
@@ -210,7 +222,7 @@ __global__ __launch_bounds__(kCandThreads) void assign_cand_kernel(
     aq = cm[lo_i + t];
   }
   for (uint64_t g0 = lo_i; g0 < hi_i; g0 += kCandThreads) {
-    // Phase 1: anchor distance and candidate count of vector t.
+    // Phase 1: anchor distance, R2 and the number of items of vector t.
     const uint64_t i = g0 + t;
     const bool valid = i < hi_i;
     float x[D];
@@ -218,8 +230,8 @@ __global__ __launch_bounds__(kCandThreads) void assign_cand_kernel(
     for (int k = 0; k < D; ++k) x[k] = xq[k];
     const uint32_t a = valid ? aq : 0u;
     bool deferred = valid && (all_deferred || a >= K);
-    uint32_t cnt = 0;
-    float U2 = 0.0f;
+    uint32_t nit = 0;
+    float U2 = 0.0f, R2 = 0.0f;
     if (valid && !deferred) {
       float ca[D];
       load_padded<D>(lcb + a * DP, ca);
@@ -229,22 +241,17 @@ __global__ __launch_bounds__(kCandThreads) void assign_cand_kernel(
       } else {
         // R2 >= 4 (U2 + eta) / (1 - g): the x4 is exact, the factor covers g
         // and the rounding of the product, the addend covers eta.
-        const float R2 = (U2 * 4.0f) * (1.0f + 8.0f * g) + 1e-38f;
-        const uint32_t* row = lnbr + a * Ls;
-        uint32_t lo = 0, len = L;  // first entry whose value exceeds R2
-        while (len > 0) {
-          const uint32_t half = len >> 1;
-          if (cand_key_value(row[lo + half]) <= R2) {
-            lo += half + 1;
-            len -= half + 1;
-          } else {
-            len = half;
-          }
-        }
-        cnt = lo;
-        if (cnt == L && !row_complete) {
+        R2 = (U2 * 4.0f) * (1.0f + 8.0f * g) + 1e-38f;
+        const uint4 s0 = *reinterpret_cast<const uint4*>(lsamp + a * 8);
+        const uint4 s1 = *reinterpret_cast<const uint4*>(lsamp + a * 8 + 4);
+        const uint32_t sv[8] = {s0.x, s0.y, s0.z, s0.w, s1.x, s1.y, s1.z, s1.w};
+#pragma unroll
+        for (int q = 0; q < 8; ++q) nit += __uint_as_float(sv[q]) <= R2 ? 1u : 0u;
+        // All samples inside R2 and codewords missing from the row: the
+        // candidate set may extend past it.
+        if (nit == 8 && !row_complete && cand_key_value(lnbr[a * Ls + L - 1]) <= R2) {
           deferred = true;
-          cnt = 0;
+          nit = 0;
         }
       }
     }
@@ -253,7 +260,8 @@ __global__ __launch_bounds__(kCandThreads) void assign_cand_kernel(
 #pragma unroll
       for (int k = 0; k < DP; ++k) gx[t * DP + k] = k < D ? x[k] : 0.0f;
       gbest[t] = ((unsigned long long)__float_as_uint(U2) << 32) | a;
-      gmeta[t] = a | (cnt << 8);
+      gR2[t] = R2;
+      ga[t] = a;
     }
     if (i + kCandThreads < hi_i) {
       load_padded<D>(xm + (i + kCandThreads) * DP, xq);
@@ -269,7 +277,6 @@ __global__ __launch_bounds__(kCandThreads) void assign_cand_kernel(
             (uint32_t)i;
     }
     // Phase 2: block-wide exclusive scan of the item counts.
-    const uint32_t nit = (cnt + kCandItem - 1) / kCandItem;  // <= 8
     uint32_t incl = nit;
 #pragma unroll
     for (int off = 1; off < kWave; off <<= 1) {
@@ -278,40 +285,42 @@ __global__ __launch_bounds__(kCandThreads) void assign_cand_kernel(
     }
     if (lane == kWave - 1) wsum[wave] = incl;
     lds_barrier();
-    uint32_t before = 0, total = 0;
-    for (uint32_t q = 0; q < (uint32_t)kCandWaves; ++q) {
-      const uint32_t w = wsum[q];
-      before += q < wave ? w : 0u;
-      total += w;
+    uint32_t wv = lane < (uint32_t)kCandWaves ? wsum[lane] : 0u;  // wave totals, scanned
+#pragma unroll
+    for (int off = 1; off < kCandWaves; off <<= 1) {
+      const uint32_t o = __shfl_up(wv, off, kWave);
+      if (lane >= (uint32_t)off) wv += o;
     }
+    const uint32_t total = __shfl(wv, kCandWaves - 1, kWave);
+    const uint32_t before = wave ? __shfl(wv, wave - 1, kWave) : 0u;
     const uint32_t first = before + incl - nit;
     for (uint32_t q = 0; q < nit; ++q) gitem[first + q] = (uint16_t)(t | (q << 10));
     lds_barrier();
-    // Phase 3: items, kCandThreads at a time.
+    // Phase 3: items, kCandThreads at a time.  Entry j of the row is a
+    // candidate when j < L and its value is inside the vector's R2.
     for (uint32_t w = t; w < total; w += kCandThreads) {
       const uint32_t it = gitem[w];
       const uint32_t u = it & 1023u, j0 = (it >> 10) * kCandItem;
-      const uint32_t meta = gmeta[u];
-      const uint32_t cu = meta >> 8;
-      const uint32_t jn = cu - j0 < kCandItem ? cu - j0 : kCandItem;
-      const uint32_t* row = lnbr + (meta & 0xFFu) * Ls + j0;
-      uint32_t cs[kCandItem];
+      const float r2 = gR2[u];
+      const uint32_t* row = lnbr + ga[u] * Ls;
+      uint32_t keys[kCandItem];
 #pragma unroll
-      for (uint32_t k = 0; k < kCandItem; ++k) cs[k] = k < jn ? row[k] & 0xFFu : 0u;
+      for (uint32_t k = 0; k < kCandItem; ++k) keys[k] = j0 + k < L ? row[j0 + k] : 0xFFFFFFFFu;
       float xv[D];
       load_padded<D>(gx + u * DP, xv);
       unsigned long long best = ~0ull;
 #pragma unroll
       for (uint32_t k = 0; k < kCandItem; ++k) {
-        if (k < jn) {
+        if (cand_key_value(keys[k]) <= r2) {
+          const uint32_t c = keys[k] & 0xFFu;
           float cv[D];
-          load_padded<D>(lcb + cs[k] * DP, cv);
+          load_padded<D>(lcb + c * DP, cv);
           const float d = exact_l2sq<D>(xv, cv);
-          const unsigned long long key = ((unsigned long long)__float_as_uint(d) << 32) | cs[k];
+          const unsigned long long key = ((unsigned long long)__float_as_uint(d) << 32) | c;
           best = key < best ? key : best;
         }
       }
-      atomicMin(&gbest[u], best);
+      if (best != ~0ull) atomicMin(&gbest[u], best);
     }
     lds_barrier();
     if (live) {

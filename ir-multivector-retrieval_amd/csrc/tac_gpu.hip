@@ -302,7 +302,9 @@ struct Launch {
         xs, cb, nbr, codes, e, defer, defer_count, done, n, K, L, (uint32_t)chunk);
     const uint32_t Kp = (K + kPruneBlock - 1) / kPruneBlock * kPruneBlock;
     const size_t lds = (size_t)Kp * (Pad<D>::value + 1) * sizeof(float) + 2 * sizeof(uint32_t);
-    assign_list_kernel<D, VPT><<<dim3((unsigned)nblk, M), kBlock, lds, s>>>(
+    // A block's deferred slice holds about 2% of its chunk: two vectors per
+    // thread keep the tile full.
+    assign_list_kernel<D, 2><<<dim3((unsigned)nblk, M), kBlock, lds, s>>>(
         xs, cb, codes, e, defer, defer_count, done, n, K, (uint32_t)chunk, rescans, rescans + 1);
     return TAC_OK;
   }
