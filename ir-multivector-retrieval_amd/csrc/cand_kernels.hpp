@@ -99,14 +99,17 @@ __device__ __forceinline__ float cand_key_value(uint32_t key) {
 
 // One wave per (codeword a, subspace m): lo(a, c) for every c != a, a
 // bitonic sort of the 256 keys in LDS, the first L written to
-// nbr[m][a][0 .. L).
+// nbr[m][a][0 .. L).  Block (0, m) also clears the subspace's deferred
+// count for the assignment that follows on the same stream.
 template <int D>
 __global__ __launch_bounds__(kWave) void nbr_build_kernel(const float* __restrict__ cb,
                                                           uint32_t* __restrict__ nbr,
+                                                          uint32_t* __restrict__ defer_count,
                                                           const uint32_t* __restrict__ done,
                                                           uint32_t K, uint32_t L) {
   __shared__ uint32_t keys[kCandMaxK];
   const uint32_t a = blockIdx.x, m = blockIdx.y, lane = threadIdx.x;
+  if (a == 0 && lane == 0) defer_count[m] = 0;
   if (done[m]) return;
   constexpr float g = fold_gamma<D>();
   const float* cbm = cb + (uint64_t)m * K * D;
@@ -150,15 +153,16 @@ __global__ __launch_bounds__(kWave) void nbr_build_kernel(const float* __restric
 // Lloyd assignment from the previous codes.  Block b = (chunk of vectors
 // [b*chunk, (b+1)*chunk), subspace m); codes[m][i] holds the previous
 // iteration's code on entry and the new one on exit, e[m][i] the reference
-// distance to it.  Vectors the candidate rule cannot settle are listed in
-// the block's own slice defer[m][b*chunk ..] (an LDS counter, so no global
-// atomics), their number in defer_count[m][b], for assign_list_kernel.
+// distance to it.  Vectors the candidate rule cannot settle are first
+// listed in the block's own slice slice[m][b*chunk ..] (an LDS counter), then
+// appended to the subspace's dense list defer[m][0 .. defer_count[m]) with
+// one global atomic per block, for assign_list_kernel.
 template <int D>
 __global__ __launch_bounds__(kCandThreads) void assign_cand_kernel(
     const float* __restrict__ xs, const float* __restrict__ cb, const uint32_t* __restrict__ nbr,
-    uint16_t* __restrict__ codes, float* __restrict__ e, uint32_t* __restrict__ defer,
-    uint32_t* __restrict__ defer_count, const uint32_t* __restrict__ done, uint64_t n,
-    uint32_t K, uint32_t L, uint32_t chunk) {
+    uint16_t* __restrict__ codes, float* __restrict__ e, uint32_t* __restrict__ slice,
+    uint32_t* __restrict__ defer, uint32_t* __restrict__ defer_count,
+    const uint32_t* __restrict__ done, uint64_t n, uint32_t K, uint32_t L, uint32_t chunk) {
   constexpr int DP = Pad<D>::value;
   constexpr float g = fold_gamma<D>();
   extern __shared__ __attribute__((aligned(16))) float lds[];
@@ -273,7 +277,7 @@ __global__ __launch_bounds__(kCandThreads) void assign_cand_kernel(
       if (lane == 0) at = atomicAdd(lcnt, (uint32_t)__popcll(dm));
       at = __shfl(at, 0, kWave);
       if (valid && deferred)
-        defer[(uint64_t)m * n + lo_i + at + (uint32_t)__popcll(dm & ((1ull << lane) - 1ull))] =
+        slice[(uint64_t)m * n + lo_i + at + (uint32_t)__popcll(dm & ((1ull << lane) - 1ull))] =
             (uint32_t)i;
     }
     // Phase 2: block-wide exclusive scan of the item counts.
@@ -329,33 +333,39 @@ __global__ __launch_bounds__(kCandThreads) void assign_cand_kernel(
       em[i] = __uint_as_float((uint32_t)(k >> 32));
     }
   }
-  lds_barrier();
-  if (t == 0) defer_count[(uint64_t)m * gridDim.x + blockIdx.x] = *lcnt;
+  __syncthreads();  // the slice's global writes, and lcnt
+  const uint32_t nd = *lcnt;
+  if (nd == 0) return;
+  __syncthreads();  // every thread has read lcnt before it is reused
+  if (t == 0) *lcnt = atomicAdd(&defer_count[m], nd);
+  __syncthreads();
+  const uint32_t at = *lcnt;
+  for (uint32_t q = t; q < nd; q += kCandThreads)
+    defer[(uint64_t)m * n + at + q] = slice[(uint64_t)m * n + lo_i + q];
 }
 
 // The deferred vectors: the pruned exact search over all K codewords
-// (pq_kernels.hpp), vectors gathered through the list slice of
-// assign_cand_kernel's block (blockIdx.x, m), in tiles of kBlock*VPT.
-// stats[0] += deferred vectors, stats[1] += vectors of the slice.
+// (pq_kernels.hpp), vectors gathered through the dense list defer[m][..];
+// a persistent grid of gridDim.x blocks per subspace walks tiles of
+// kBlock*VPT entries.  With stats (profiling): stats[0] += deferred
+// vectors, stats[1] += n per subspace.
 template <int D, int VPT>
 __global__ __launch_bounds__(kBlock) void assign_list_kernel(
     const float* __restrict__ xs, const float* __restrict__ cb, uint16_t* __restrict__ codes,
     float* __restrict__ e, const uint32_t* __restrict__ defer,
     const uint32_t* __restrict__ defer_count, const uint32_t* __restrict__ done, uint64_t n,
-    uint32_t K, uint32_t chunk, unsigned long long* __restrict__ rescans,
-    unsigned long long* __restrict__ stats) {
+    uint32_t K, unsigned long long* __restrict__ rescans, unsigned long long* __restrict__ stats) {
   constexpr int DP = Pad<D>::value;
   constexpr uint32_t kTile = kBlock * VPT;
   extern __shared__ __attribute__((aligned(16))) float lds[];
   const uint32_t m = blockIdx.y;
   if (done[m]) return;
-  const uint32_t cnt = defer_count[(uint64_t)m * gridDim.x + blockIdx.x];
-  const uint64_t lo_i = (uint64_t)blockIdx.x * chunk;
-  if (threadIdx.x == 0) {
+  const uint32_t cnt = defer_count[m];
+  if (stats && blockIdx.x == 0 && threadIdx.x == 0) {
     atomicAdd(&stats[0], (unsigned long long)cnt);
-    atomicAdd(&stats[1], (unsigned long long)((lo_i + chunk < n ? lo_i + chunk : n) - lo_i));
+    atomicAdd(&stats[1], (unsigned long long)n);
   }
-  if (cnt == 0) return;
+  if ((uint64_t)blockIdx.x * kTile >= cnt) return;
   const uint32_t Kp = (K + kPruneBlock - 1) / kPruneBlock * kPruneBlock;
   float* lcb = lds;
   float* lnc = lds + Kp * DP;
@@ -369,9 +379,9 @@ __global__ __launch_bounds__(kBlock) void assign_list_kernel(
   stage_pruned<D>(lcb, lnc, &lmax, cb + (uint64_t)m * K * D, K, Kp);
   __syncthreads();
   const float* xm = xs + (uint64_t)m * n * DP;
-  const uint32_t* lst = defer + (uint64_t)m * n + lo_i;
+  const uint32_t* lst = defer + (uint64_t)m * n;
   uint32_t mine = 0;
-  for (uint32_t t0 = 0; t0 < cnt; t0 += kTile) {
+  for (uint64_t t0 = (uint64_t)blockIdx.x * kTile; t0 < cnt; t0 += (uint64_t)gridDim.x * kTile) {
     float x[VPT][D];
     uint32_t idx[VPT];
 #pragma unroll

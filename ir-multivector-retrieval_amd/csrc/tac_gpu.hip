@@ -276,10 +276,10 @@ struct Launch {
   // current codebooks, the assignment from the previous codes, then the
   // pruned full search of the deferred vectors.
   static int assign_cand(const float *xs, const float *cb, uint32_t *nbr, uint16_t *codes,
-                         float *e, uint32_t *defer, uint32_t *defer_count, const uint32_t *done,
-                         uint64_t n, uint32_t M, uint32_t K, uint32_t L,
+                         float *e, uint32_t *slice, uint32_t *defer, uint32_t *defer_count,
+                         const uint32_t *done, uint64_t n, uint32_t M, uint32_t K, uint32_t L,
                          unsigned long long *rescans, hipStream_t s) {
-    nbr_build_kernel<D><<<dim3(K, M), kWave, 0, s>>>(cb, nbr, done, K, L);
+    nbr_build_kernel<D><<<dim3(K, M), kWave, 0, s>>>(cb, nbr, defer_count, done, K, L);
     const CandLds lay = cand_lds(K, L, Pad<D>::value);
     if (lay.total > 65536) {
       static bool raised = false;
@@ -299,13 +299,18 @@ struct Launch {
     chunk = (chunk + kCandThreads - 1) / kCandThreads * kCandThreads;
     const uint64_t nblk = (n + chunk - 1) / chunk;
     assign_cand_kernel<D><<<dim3((unsigned)nblk, M), kCandThreads, lay.total, s>>>(
-        xs, cb, nbr, codes, e, defer, defer_count, done, n, K, L, (uint32_t)chunk);
+        xs, cb, nbr, codes, e, slice, defer, defer_count, done, n, K, L, (uint32_t)chunk);
     const uint32_t Kp = (K + kPruneBlock - 1) / kPruneBlock * kPruneBlock;
     const size_t lds = (size_t)Kp * (Pad<D>::value + 1) * sizeof(float) + 2 * sizeof(uint32_t);
-    // A block's deferred slice holds about 2% of its chunk: two vectors per
-    // thread keep the tile full.
-    assign_list_kernel<D, 2><<<dim3((unsigned)nblk, M), kBlock, lds, s>>>(
-        xs, cb, codes, e, defer, defer_count, done, n, K, (uint32_t)chunk, rescans, rescans + 1);
+    // About 2% of the vectors are deferred.  One vector per thread and about
+    // 4,096 blocks over all subspaces keep many short waves per SIMD (a full
+    // search is a long serial chain per lane); blocks loop when there are
+    // more.
+    const uint64_t g = std::max<uint64_t>(
+        1, std::min<uint64_t>((n + kBlock - 1) / kBlock, (4096 + M - 1) / M));
+    assign_list_kernel<D, 1><<<dim3((unsigned)g, M), kBlock, lds, s>>>(
+        xs, cb, codes, e, defer, defer_count, done, n, K, rescans,
+        g_profile ? rescans + 1 : nullptr);
     return TAC_OK;
   }
   static int scatter(const float *xs, const uint16_t *codes, const uint32_t *hist,
@@ -513,8 +518,8 @@ int train_core(DeviceState &ds, hipStream_t s, const float *d_x, uint64_t n, uin
   const bool cand = !(full_env && full_env[0] == '1') && K >= 2 && K <= kCandMaxK &&
                     cand_lds(K, Lc, DP).total <= kCandLdsMax && max_iters > 1;
   if (cand && ((st = ensure(ds, ds.cand_nbr, (size_t)M * K * Lc * sizeof(uint32_t))) ||
-               (st = ensure(ds, ds.cand_defer, (size_t)M * n * sizeof(uint32_t))) ||
-               (st = ensure(ds, ds.cand_count, (size_t)M * (1024 / M + 2) * sizeof(uint32_t)))))
+               (st = ensure(ds, ds.cand_defer, (size_t)2 * M * n * sizeof(uint32_t))) ||
+               (st = ensure(ds, ds.cand_count, (size_t)M * sizeof(uint32_t)))))
     return st;
 
   float *xs = as<float>(ds.xs);
@@ -568,9 +573,10 @@ int train_core(DeviceState &ds, hipStream_t s, const float *d_x, uint64_t n, uin
       HIP_TRY(hipEventRecord(a, s));
     }
     if (cand && t > 0) {
-      DISPATCH_D_ST(D, assign_cand(xs, out.cb, as<uint32_t>(ds.cand_nbr), codes, e,
-                                   as<uint32_t>(ds.cand_defer), as<uint32_t>(ds.cand_count),
-                                   done, n, M, K, Lc, rescans, s));
+      uint32_t *slices = as<uint32_t>(ds.cand_defer);
+      DISPATCH_D_ST(D, assign_cand(xs, out.cb, as<uint32_t>(ds.cand_nbr), codes, e, slices,
+                                   slices + (size_t)M * n, as<uint32_t>(ds.cand_count), done,
+                                   n, M, K, Lc, rescans, s));
       if (st) return st;
       LAUNCH_TRY("assign_cand kernels");
     } else {
