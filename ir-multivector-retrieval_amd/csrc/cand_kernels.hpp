@@ -28,12 +28,13 @@
 // deferred list that the pruned full search (pq_kernels.hpp) resolves, as
 // do non-finite or huge distances and non-finite codebooks.
 //
-// Load balance.  A block assigns 1,024 vectors at a time.  Each vector's
-// candidates are cut into items of at most kCandItem; a block-wide scan of
-// the item counts lays the items out evenly over all threads, an item's
-// result folds into its vector's 64-bit LDS key with an atomic minimum, and
-// every thread then writes its own vector's result.  The work per thread
-// follows the mean candidate count, not the largest in a wave.
+// Load balance.  Each wave assigns 64 vectors at a time.  A vector's
+// candidates are cut into items of at most kCandItem; a wave scan of the
+// item counts lays the items out over the wave's lanes, an item's result
+// folds into its vector's 64-bit LDS key with an atomic minimum, and every
+// lane then writes its own vector's result.  The work per lane follows the
+// mean candidate count, not the largest in the wave, and the waves of a
+// block never wait for one another.
 #pragma once
 
 #include <hip/hip_runtime.h>
@@ -61,36 +62,27 @@ constexpr uint32_t kCandItem = 8;  // candidates per work item
 // LDS layout of assign_cand_kernel, shared by the host launcher:
 //   lcb [K][DP] f32 | lnbr [K][L|1] u32 (an odd row stride puts the rows of
 //   different anchors in different banks) | lsamp [K][8] u32: the value bits
-//   of row entries 0, 7, 15, ..., 55 (all-ones past the row) | group of
-//   kCandThreads vectors: gx [][DP] f32, gbest [] u64, gR2 [] f32, ga [] u32,
-//   gitem [kCandThreads * 8] u16 (vector | item << 10) | wsum [16] u32 |
-//   lmax, lcnt u32
+//   of row entries 0, 7, 15, ..., 55 (all-ones past the row) | per wave:
+//   gx [64][DP] f32, gbest [64] u64, gR2 [64] f32, ga [64] u32,
+//   gitem [64 * 8] u16 (lane | item << 6) | lmax, lcnt u32
 struct CandLds {
-  uint32_t nbr_off, samp_off, grp_off, item_off, wsum_off, total;
+  uint32_t nbr_off, samp_off, wave_off, wave_bytes, scal_off, total;
 };
 __host__ __device__ inline uint32_t cand_up16(uint32_t b) { return (b + 15u) & ~15u; }
 __host__ __device__ inline CandLds cand_lds(uint32_t K, uint32_t L, uint32_t DP) {
   CandLds s;
   s.nbr_off = cand_up16(K * DP * 4u);
   s.samp_off = cand_up16(s.nbr_off + K * (L | 1u) * 4u);
-  s.grp_off = s.samp_off + K * 8u * 4u;
-  s.item_off = s.grp_off + (uint32_t)kCandThreads * (DP * 4u + 8u + 4u + 4u);
-  s.wsum_off = cand_up16(s.item_off + (uint32_t)kCandThreads * 8u * 2u);
-  s.total = s.wsum_off + 16u * 4u + 16u;
+  s.wave_off = s.samp_off + K * 8u * 4u;
+  s.wave_bytes = 64u * (DP * 4u + 8u + 4u + 4u) + 64u * 8u * 2u;
+  s.scal_off = s.wave_off + (uint32_t)kCandWaves * s.wave_bytes;
+  s.total = s.scal_off + 16u;
   return s;
 }
 
 // Row position of sample q: 0, 7, 15, ..., 55.  With b samples inside R2
 // the row's entries inside R2 all lie in [0, 8b): item q covers [8q, 8q+8).
 __host__ __device__ inline uint32_t cand_sample_pos(uint32_t q) { return q ? 8u * q - 1u : 0u; }
-
-// Block barrier that orders LDS only: outstanding global loads (the next
-// group's prefetch) and stores stay in flight across it.
-__device__ __forceinline__ void lds_barrier() {
-  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup", "local");
-  __builtin_amdgcn_s_barrier();
-  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup", "local");
-}
 
 // Value part of a neighbour key: a lower bound of ||c_a - c||^2.
 __device__ __forceinline__ float cand_key_value(uint32_t key) {
@@ -173,15 +165,15 @@ __global__ __launch_bounds__(kCandThreads) void assign_cand_kernel(
   float* lcb = lds;
   uint32_t* lnbr = reinterpret_cast<uint32_t*>(base + lay.nbr_off);
   uint32_t* lsamp = reinterpret_cast<uint32_t*>(base + lay.samp_off);
-  float* gx = reinterpret_cast<float*>(base + lay.grp_off);
-  unsigned long long* gbest = reinterpret_cast<unsigned long long*>(gx + kCandThreads * DP);
-  float* gR2 = reinterpret_cast<float*>(gbest + kCandThreads);
-  uint32_t* ga = reinterpret_cast<uint32_t*>(gR2 + kCandThreads);
-  uint16_t* gitem = reinterpret_cast<uint16_t*>(base + lay.item_off);
-  uint32_t* wsum = reinterpret_cast<uint32_t*>(base + lay.wsum_off);
-  uint32_t* lmax = wsum + 16;
-  uint32_t* lcnt = lmax + 1;
   const uint32_t t = threadIdx.x, lane = t % kWave, wave = t / kWave;
+  uint8_t* wb = base + lay.wave_off + wave * lay.wave_bytes;
+  float* gx = reinterpret_cast<float*>(wb);
+  unsigned long long* gbest = reinterpret_cast<unsigned long long*>(gx + 64 * DP);
+  float* gR2 = reinterpret_cast<float*>(gbest + 64);
+  uint32_t* ga = reinterpret_cast<uint32_t*>(gR2 + 64);
+  uint16_t* gitem = reinterpret_cast<uint16_t*>(ga + 64);
+  uint32_t* lmax = reinterpret_cast<uint32_t*>(base + lay.scal_off);
+  uint32_t* lcnt = lmax + 1;
 
   if (t == 0) {
     *lmax = 0;
@@ -216,23 +208,30 @@ __global__ __launch_bounds__(kCandThreads) void assign_cand_kernel(
   const float* xm = xs + (uint64_t)m * n * DP;
   uint16_t* cm = codes + (uint64_t)m * n;
   float* em = e + (uint64_t)m * n;
-  // Each group's vectors and previous codes are loaded one group ahead.
+  // Wave w takes the 64-vector groups w, w + kCandWaves, ... of the chunk;
+  // each group's vectors and previous codes are loaded one group ahead.
   float xq[D];
   uint32_t aq = 0;
 #pragma unroll
   for (int k = 0; k < D; ++k) xq[k] = 0.0f;
-  if (lo_i + t < hi_i) {
-    load_padded<D>(xm + (lo_i + t) * DP, xq);
-    aq = cm[lo_i + t];
+  const uint64_t first_i = lo_i + (uint64_t)wave * kWave + lane;
+  if (first_i < hi_i) {
+    load_padded<D>(xm + first_i * DP, xq);
+    aq = cm[first_i];
   }
-  for (uint64_t g0 = lo_i; g0 < hi_i; g0 += kCandThreads) {
-    // Phase 1: anchor distance, R2 and the number of items of vector t.
-    const uint64_t i = g0 + t;
+  constexpr uint64_t kStride = (uint64_t)kCandWaves * kWave;
+  for (uint64_t g0 = lo_i + (uint64_t)wave * kWave; g0 < hi_i; g0 += kStride) {
+    // Phase 1: anchor distance, R2 and the number of items of this lane's vector.
+    const uint64_t i = g0 + lane;
     const bool valid = i < hi_i;
     float x[D];
 #pragma unroll
     for (int k = 0; k < D; ++k) x[k] = xq[k];
     const uint32_t a = valid ? aq : 0u;
+    if (i + kStride < hi_i) {
+      load_padded<D>(xm + (i + kStride) * DP, xq);
+      aq = cm[i + kStride];
+    }
     bool deferred = valid && (all_deferred || a >= K);
     uint32_t nit = 0;
     float U2 = 0.0f, R2 = 0.0f;
@@ -260,17 +259,6 @@ __global__ __launch_bounds__(kCandThreads) void assign_cand_kernel(
       }
     }
     const bool live = valid && !deferred;
-    if (live) {
-#pragma unroll
-      for (int k = 0; k < DP; ++k) gx[t * DP + k] = k < D ? x[k] : 0.0f;
-      gbest[t] = ((unsigned long long)__float_as_uint(U2) << 32) | a;
-      gR2[t] = R2;
-      ga[t] = a;
-    }
-    if (i + kCandThreads < hi_i) {
-      load_padded<D>(xm + (i + kCandThreads) * DP, xq);
-      aq = cm[i + kCandThreads];
-    }
     const uint64_t dm = __ballot(valid && deferred);
     if (dm) {
       uint32_t at = 0;
@@ -280,31 +268,28 @@ __global__ __launch_bounds__(kCandThreads) void assign_cand_kernel(
         slice[(uint64_t)m * n + lo_i + at + (uint32_t)__popcll(dm & ((1ull << lane) - 1ull))] =
             (uint32_t)i;
     }
-    // Phase 2: block-wide exclusive scan of the item counts.
+    // Phase 2: the wave's items, laid out by an exclusive scan of the counts.
     uint32_t incl = nit;
 #pragma unroll
     for (int off = 1; off < kWave; off <<= 1) {
       const uint32_t o = __shfl_up(incl, off, kWave);
       if (lane >= (uint32_t)off) incl += o;
     }
-    if (lane == kWave - 1) wsum[wave] = incl;
-    lds_barrier();
-    uint32_t wv = lane < (uint32_t)kCandWaves ? wsum[lane] : 0u;  // wave totals, scanned
+    const uint32_t total = __shfl(incl, kWave - 1, kWave);  // <= 64 * 8
+    if (live) {
 #pragma unroll
-    for (int off = 1; off < kCandWaves; off <<= 1) {
-      const uint32_t o = __shfl_up(wv, off, kWave);
-      if (lane >= (uint32_t)off) wv += o;
+      for (int k = 0; k < DP; ++k) gx[lane * DP + k] = k < D ? x[k] : 0.0f;
+      gbest[lane] = ((unsigned long long)__float_as_uint(U2) << 32) | a;
+      gR2[lane] = R2;
+      ga[lane] = a;
     }
-    const uint32_t total = __shfl(wv, kCandWaves - 1, kWave);
-    const uint32_t before = wave ? __shfl(wv, wave - 1, kWave) : 0u;
-    const uint32_t first = before + incl - nit;
-    for (uint32_t q = 0; q < nit; ++q) gitem[first + q] = (uint16_t)(t | (q << 10));
-    lds_barrier();
-    // Phase 3: items, kCandThreads at a time.  Entry j of the row is a
-    // candidate when j < L and its value is inside the vector's R2.
-    for (uint32_t w = t; w < total; w += kCandThreads) {
+    for (uint32_t q = 0, f = incl - nit; q < nit; ++q) gitem[f + q] = (uint16_t)(lane | (q << 6));
+    wave_lds_sync();
+    // Phase 3: items, 64 at a time.  Entry j of the row is a candidate when
+    // j < L and its value is inside the vector's R2.
+    for (uint32_t w = lane; w < total; w += kWave) {
       const uint32_t it = gitem[w];
-      const uint32_t u = it & 1023u, j0 = (it >> 10) * kCandItem;
+      const uint32_t u = it & 63u, j0 = (it >> 6) * kCandItem;
       const float r2 = gR2[u];
       const uint32_t* row = lnbr + ga[u] * Ls;
       uint32_t keys[kCandItem];
@@ -326,12 +311,13 @@ __global__ __launch_bounds__(kCandThreads) void assign_cand_kernel(
       }
       if (best != ~0ull) atomicMin(&gbest[u], best);
     }
-    lds_barrier();
+    wave_lds_sync();
     if (live) {
-      const unsigned long long k = gbest[t];
+      const unsigned long long k = gbest[lane];
       cm[i] = (uint16_t)(k & 0xFFFFu);
       em[i] = __uint_as_float((uint32_t)(k >> 32));
     }
+    wave_lds_sync();  // the scratch is rewritten by the next group
   }
   __syncthreads();  // the slice's global writes, and lcnt
   const uint32_t nd = *lcnt;
