@@ -340,6 +340,9 @@ typedef struct tac_gpu_profile {
   uint64_t cand_vectors;   /* (vector, subspace) assignments started from the previous code */
   uint64_t cand_deferred;  /* of those, the ones left to the full search (candidate row
                               exhausted, non-finite or huge values) */
+  double cand_assign_ms;   /* assignment stages that started from the previous codes
+                              (included in assign_ms) */
+  uint64_t cand_assign_iters;
 } tac_gpu_profile;
 int tac_gpu_profile_enable(int enable);
 int tac_gpu_profile_read(tac_gpu_profile *out, int reset);

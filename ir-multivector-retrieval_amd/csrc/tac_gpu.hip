@@ -656,10 +656,15 @@ int train_core(DeviceState &ds, hipStream_t s, const float *d_x, uint64_t n, uin
       HIP_TRY(hipEventElapsedTime(&ms, e0, e1));
       g_prof.transpose_ms += ms;
       g_prof.transpose_launches += 1;
-      for (size_t q : it_events) {
+      for (size_t t = 0; t < it_events.size(); ++t) {
+        const size_t q = it_events[t];
         HIP_TRY(hipEventElapsedTime(&ms, ds.events[q], ds.events[q + 1]));
         g_prof.assign_ms += ms;
         g_prof.assign_launches += 1;
+        if (cand && t > 0) {
+          g_prof.cand_assign_ms += ms;
+          g_prof.cand_assign_iters += 1;
+        }
         HIP_TRY(hipEventElapsedTime(&ms, ds.events[q + 1], ds.events[q + 2]));
         g_prof.update_ms += ms;
         g_prof.update_iters += 1;

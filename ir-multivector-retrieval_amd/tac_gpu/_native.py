@@ -66,6 +66,8 @@ class Profile(ctypes.Structure):
         ("cluster_call_ms", ctypes.c_double),
         ("cand_vectors", c_u64),
         ("cand_deferred", c_u64),
+        ("cand_assign_ms", ctypes.c_double),
+        ("cand_assign_iters", c_u64),
     ]
 
 

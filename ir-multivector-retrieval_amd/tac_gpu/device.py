@@ -139,6 +139,8 @@ class KernelTimes:
     cluster_call_ms: float = 0.0
     cand_vectors: int = 0
     cand_deferred: int = 0
+    cand_assign_ms: float = 0.0
+    cand_assign_iters: int = 0
 
 
 def profile_enable(on: bool = True) -> None:
@@ -153,4 +155,5 @@ def profile_read(reset: bool = True) -> KernelTimes:
                        p.exact_rescans, p.residual_ms, p.residual_launches, p.crc_ms,
                        p.crc_launches, p.refine_ms, p.refine_launches, p.cluster_kpp_ms,
                        p.cluster_lloyd_ms, p.cluster_calls, p.cluster_prep_ms,
-                       p.cluster_call_ms, p.cand_vectors, p.cand_deferred)
+                       p.cluster_call_ms, p.cand_vectors, p.cand_deferred, p.cand_assign_ms,
+                       p.cand_assign_iters)
