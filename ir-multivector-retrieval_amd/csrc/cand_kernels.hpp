@@ -18,6 +18,12 @@
 //   minimum of (distance bits, index): c* has the global minimum and the
 //   smallest index among its ties, so that minimum is c*.
 //
+// Anchors.  Lloyd iterations after the first anchor each vector at its
+// previous code.  Encode anchors it at the codeword nearest the centre of its
+// cell in a grid over the codebook's bounding box (grid_build_kernel); a
+// vector outside the box takes the nearest cell.  The rule above holds for
+// any anchor, so the anchor only decides how many candidates are evaluated.
+//
 // Neighbour tables.  After every update, nbr_build_kernel sorts, for each
 // codeword a, the other codewords by lo(a, c) and keeps the first L of them
 // as one u32 key each: the bits of lo with the low 8 bits replaced by c
@@ -59,25 +65,42 @@ __host__ __device__ constexpr float fold_gamma() {
 
 constexpr uint32_t kCandItem = 8;  // candidates per work item
 
-// LDS layout of assign_cand_kernel, shared by the host launcher:
+constexpr uint32_t kCandCells = 10000;  // grid cells per subspace (encode anchors)
+
+// LDS layout of cand_kernel, shared by the host launcher:
 //   lcb [K][DP] f32 | lnbr [K][L|1] u32 (an odd row stride puts the rows of
 //   different anchors in different banks) | lsamp [K][8] u32: the value bits
-//   of row entries 0, 7, 15, ..., 55 (all-ones past the row) | per wave:
-//   gx [64][DP] f32, gbest [64] u64, gR2 [64] f32, ga [64] u32,
+//   of row entries 0, 7, 15, ..., 55 (all-ones past the row) | encode only:
+//   lanc [cells] u8 anchors, lgrid [2][8] f32 (cell origin, cells per unit) |
+//   per wave: gx [64][DP] f32, gbest [64] u64, gR2 [64] f32, ga [64] u32,
 //   gitem [64 * 8] u16 (lane | item << 6) | lmax, lcnt u32
 struct CandLds {
-  uint32_t nbr_off, samp_off, wave_off, wave_bytes, scal_off, total;
+  uint32_t nbr_off, samp_off, anc_off, grid_off, wave_off, wave_bytes, scal_off, total;
 };
 __host__ __device__ inline uint32_t cand_up16(uint32_t b) { return (b + 15u) & ~15u; }
-__host__ __device__ inline CandLds cand_lds(uint32_t K, uint32_t L, uint32_t DP) {
+__host__ __device__ inline CandLds cand_lds(uint32_t K, uint32_t L, uint32_t DP,
+                                            uint32_t cells = 0) {
   CandLds s;
   s.nbr_off = cand_up16(K * DP * 4u);
   s.samp_off = cand_up16(s.nbr_off + K * (L | 1u) * 4u);
-  s.wave_off = s.samp_off + K * 8u * 4u;
+  s.anc_off = s.samp_off + K * 8u * 4u;
+  s.grid_off = cand_up16(s.anc_off + cells);
+  s.wave_off = s.grid_off + (cells ? 64u : 0u);
   s.wave_bytes = 64u * (DP * 4u + 8u + 4u + 4u) + 64u * 8u * 2u;
   s.scal_off = s.wave_off + (uint32_t)kCandWaves * s.wave_bytes;
   s.total = s.scal_off + 16u;
   return s;
+}
+
+// Cells per dimension of the encode grid: the largest G with G^D <= kCandCells.
+__host__ __device__ inline uint32_t cand_grid_side(uint32_t D) {
+  uint32_t G = 1;
+  for (;;) {
+    uint64_t p = 1;
+    for (uint32_t k = 0; k < D; ++k) p *= (G + 1);
+    if (p > kCandCells) return G;
+    ++G;
+  }
 }
 
 // Row position of sample q: 0, 7, 15, ..., 55.  With b samples inside R2
@@ -102,7 +125,7 @@ __global__ __launch_bounds__(kWave) void nbr_build_kernel(const float* __restric
   __shared__ uint32_t keys[kCandMaxK];
   const uint32_t a = blockIdx.x, m = blockIdx.y, lane = threadIdx.x;
   if (a == 0 && lane == 0) defer_count[m] = 0;
-  if (done[m]) return;
+  if (done && done[m]) return;
   constexpr float g = fold_gamma<D>();
   const float* cbm = cb + (uint64_t)m * K * D;
   float ca[D];
@@ -142,29 +165,104 @@ __global__ __launch_bounds__(kWave) void nbr_build_kernel(const float* __restric
   for (uint32_t j = lane; j < L; j += kWave) row[j] = keys[j];
 }
 
-// Lloyd assignment from the previous codes.  Block b = (chunk of vectors
-// [b*chunk, (b+1)*chunk), subspace m); codes[m][i] holds the previous
-// iteration's code on entry and the new one on exit, e[m][i] the reference
-// distance to it.  Vectors the candidate rule cannot settle are first
-// listed in the block's own slice slice[m][b*chunk ..] (an LDS counter), then
-// appended to the subspace's dense list defer[m][0 .. defer_count[m]) with
-// one global atomic per block, for assign_list_kernel.
+// Encode anchors of subspace m = blockIdx.y: the bounding box of the
+// codewords (lo, hi per dimension), G cells per dimension, and for each cell
+// the codeword nearest its centre (any choice is valid; nearness only keeps
+// the candidate sets small).  grid[m] = {lo[8], G / (hi - lo)[8]}.
 template <int D>
-__global__ __launch_bounds__(kCandThreads) void assign_cand_kernel(
-    const float* __restrict__ xs, const float* __restrict__ cb, const uint32_t* __restrict__ nbr,
-    uint16_t* __restrict__ codes, float* __restrict__ e, uint32_t* __restrict__ slice,
-    uint32_t* __restrict__ defer, uint32_t* __restrict__ defer_count,
-    const uint32_t* __restrict__ done, uint64_t n, uint32_t K, uint32_t L, uint32_t chunk) {
+__global__ __launch_bounds__(kBlock) void grid_build_kernel(const float* __restrict__ cb,
+                                                            uint8_t* __restrict__ anchors,
+                                                            float* __restrict__ grid,
+                                                            uint32_t K, uint32_t G,
+                                                            uint32_t cells) {
+  __shared__ float lcb[kCandMaxK * D];
+  __shared__ float box[2 * D];
+  const uint32_t m = blockIdx.y;
+  const float* cbm = cb + (uint64_t)m * K * D;
+  for (uint32_t j = threadIdx.x; j < K * D; j += blockDim.x) lcb[j] = cbm[j];
+  __syncthreads();
+  if (threadIdx.x < D) {
+    float lo = lcb[threadIdx.x], hi = lcb[threadIdx.x];
+    for (uint32_t c = 1; c < K; ++c) {
+      lo = fminf(lo, lcb[c * D + threadIdx.x]);
+      hi = fmaxf(hi, lcb[c * D + threadIdx.x]);
+    }
+    const float inv = hi > lo ? (float)G / (hi - lo) : 0.0f;
+    box[threadIdx.x] = lo;
+    box[D + threadIdx.x] = inv;
+    if (blockIdx.x == 0) {
+      grid[m * 16 + threadIdx.x] = lo;
+      grid[m * 16 + 8 + threadIdx.x] = inv;
+    }
+  }
+  __syncthreads();
+  const uint32_t cell = blockIdx.x * blockDim.x + threadIdx.x;
+  if (cell >= cells) return;
+  float ctr[D];
+  uint32_t r = cell;
+#pragma unroll
+  for (int k = 0; k < D; ++k) {
+    const uint32_t ck = r % G;
+    r /= G;
+    ctr[k] = box[k] + ((float)ck + 0.5f) / (box[D + k] > 0.0f ? box[D + k] : 1.0f);
+  }
+  float best = __builtin_inff();
+  uint32_t bi = 0;
+  for (uint32_t c = 0; c < K; ++c) {
+    float d = 0.0f;
+#pragma unroll
+    for (int k = 0; k < D; ++k) {
+      const float u = ctr[k] - lcb[c * D + k];
+      d = d + u * u;
+    }
+    if (d < best) {
+      best = d;
+      bi = c;
+    }
+  }
+  anchors[(uint64_t)m * cells + cell] = (uint8_t)bi;
+}
+
+// The exact candidate-set assignment.  Training (ENCODE false): block
+// (chunk b, subspace m) of a 2-D grid; x = xs[m][i][DP]; the anchor is
+// codes[m][i] (the previous iteration's code) and the result goes back to
+// codes[m][i] with e[m][i], the reference distance.  Encode (ENCODE true):
+// a 1-D grid whose blocks run XCD-contiguously as (chunk, subspace) so that
+// the M blocks of a chunk share one L2; x = x[i][m*D ..] (token-major); the
+// anchor comes from the grid and the code goes to out[i][m].  Vectors the
+// rule cannot settle are first listed in the block's own slice
+// slice[m][b*chunk ..] (an LDS counter), then appended to the subspace's
+// dense list defer[m][0 .. defer_count[m]) with one global atomic per block.
+template <int D, bool ENCODE, typename CodeT>
+__global__ __launch_bounds__(kCandThreads) void cand_kernel(
+    const float* __restrict__ xin, const float* __restrict__ cb,
+    const uint32_t* __restrict__ nbr, const uint8_t* __restrict__ anchors,
+    const float* __restrict__ grid, uint16_t* __restrict__ codes, float* __restrict__ e,
+    CodeT* __restrict__ out, uint32_t* __restrict__ slice, uint32_t* __restrict__ defer,
+    uint32_t* __restrict__ defer_count, const uint32_t* __restrict__ done, uint64_t n,
+    uint32_t dim, uint32_t M, uint32_t K, uint32_t L, uint32_t chunk, uint32_t nchunks,
+    uint32_t G, uint32_t cells) {
   constexpr int DP = Pad<D>::value;
   constexpr float g = fold_gamma<D>();
   extern __shared__ __attribute__((aligned(16))) float lds[];
-  const uint32_t m = blockIdx.y;
-  if (done[m]) return;
-  const CandLds lay = cand_lds(K, L, DP);
+  uint32_t m, b;
+  if constexpr (ENCODE) {
+    const uint32_t logical = xcd_contiguous(blockIdx.x, gridDim.x);
+    if (logical >= nchunks * M) return;  // grid padding to a multiple of 8
+    b = logical / M;
+    m = logical % M;
+  } else {
+    b = blockIdx.x;
+    m = blockIdx.y;
+    if (done[m]) return;
+  }
+  const CandLds lay = cand_lds(K, L, DP, ENCODE ? cells : 0u);
   uint8_t* base = reinterpret_cast<uint8_t*>(lds);
   float* lcb = lds;
   uint32_t* lnbr = reinterpret_cast<uint32_t*>(base + lay.nbr_off);
   uint32_t* lsamp = reinterpret_cast<uint32_t*>(base + lay.samp_off);
+  uint8_t* lanc = base + lay.anc_off;
+  float* lgrid = reinterpret_cast<float*>(base + lay.grid_off);
   const uint32_t t = threadIdx.x, lane = t % kWave, wave = t / kWave;
   uint8_t* wb = base + lay.wave_off + wave * lay.wave_bytes;
   float* gx = reinterpret_cast<float*>(wb);
@@ -199,25 +297,38 @@ __global__ __launch_bounds__(kCandThreads) void assign_cand_kernel(
     const uint32_t pos = cand_sample_pos(j % 8);
     lsamp[j] = pos < L ? nbm[(j / 8) * L + pos] & 0xFFFFFF00u : 0xFFFFFFFFu;
   }
+  if constexpr (ENCODE) {
+    const uint8_t* am = anchors + (uint64_t)m * cells;
+    for (uint32_t j = t; j < cells; j += blockDim.x) lanc[j] = am[j];
+    if (t < 16) lgrid[t] = grid[m * 16 + t];
+  }
   __syncthreads();
   const bool all_deferred = *lmax >= 0x7f800000u;
   const bool row_complete = L + 1 >= K;  // every other codeword is in the row
 
-  const uint64_t lo_i = (uint64_t)blockIdx.x * chunk;
+  const uint64_t lo_i = (uint64_t)b * chunk;
   const uint64_t hi_i = lo_i + chunk < n ? lo_i + chunk : n;
-  const float* xm = xs + (uint64_t)m * n * DP;
   uint16_t* cm = codes + (uint64_t)m * n;
   float* em = e + (uint64_t)m * n;
+  auto load_x = [&](uint64_t i, float (&v)[D]) {
+    if constexpr (ENCODE) {
+      const float* src = xin + i * dim + (uint64_t)m * D;
+#pragma unroll
+      for (int k = 0; k < D; ++k) v[k] = src[k];
+    } else {
+      load_padded<D>(xin + ((uint64_t)m * n + i) * DP, v);
+    }
+  };
   // Wave w takes the 64-vector groups w, w + kCandWaves, ... of the chunk;
-  // each group's vectors and previous codes are loaded one group ahead.
+  // each group's vectors (and previous codes) are loaded one group ahead.
   float xq[D];
   uint32_t aq = 0;
 #pragma unroll
   for (int k = 0; k < D; ++k) xq[k] = 0.0f;
   const uint64_t first_i = lo_i + (uint64_t)wave * kWave + lane;
   if (first_i < hi_i) {
-    load_padded<D>(xm + first_i * DP, xq);
-    aq = cm[first_i];
+    load_x(first_i, xq);
+    if constexpr (!ENCODE) aq = cm[first_i];
   }
   constexpr uint64_t kStride = (uint64_t)kCandWaves * kWave;
   for (uint64_t g0 = lo_i + (uint64_t)wave * kWave; g0 < hi_i; g0 += kStride) {
@@ -227,10 +338,19 @@ __global__ __launch_bounds__(kCandThreads) void assign_cand_kernel(
     float x[D];
 #pragma unroll
     for (int k = 0; k < D; ++k) x[k] = xq[k];
-    const uint32_t a = valid ? aq : 0u;
+    uint32_t a = valid ? aq : 0u;
     if (i + kStride < hi_i) {
-      load_padded<D>(xm + (i + kStride) * DP, xq);
-      aq = cm[i + kStride];
+      load_x(i + kStride, xq);
+      if constexpr (!ENCODE) aq = cm[i + kStride];
+    }
+    if constexpr (ENCODE) {
+      uint32_t cell = 0;  // NaN coordinates land in cell 0 (fmaxf)
+#pragma unroll
+      for (int k = D - 1; k >= 0; --k) {
+        const float f = fminf(fmaxf((x[k] - lgrid[k]) * lgrid[8 + k], 0.0f), (float)(G - 1));
+        cell = cell * G + (uint32_t)f;
+      }
+      a = lanc[cell < cells ? cell : 0u];
     }
     bool deferred = valid && (all_deferred || a >= K);
     uint32_t nit = 0;
@@ -314,8 +434,12 @@ __global__ __launch_bounds__(kCandThreads) void assign_cand_kernel(
     wave_lds_sync();
     if (live) {
       const unsigned long long k = gbest[lane];
-      cm[i] = (uint16_t)(k & 0xFFFFu);
-      em[i] = __uint_as_float((uint32_t)(k >> 32));
+      if constexpr (ENCODE) {
+        out[i * M + m] = (CodeT)(k & 0xFFFFu);
+      } else {
+        cm[i] = (uint16_t)(k & 0xFFFFu);
+        em[i] = __uint_as_float((uint32_t)(k >> 32));
+      }
     }
     wave_lds_sync();  // the scratch is rewritten by the next group
   }
@@ -391,6 +515,54 @@ __global__ __launch_bounds__(kBlock) void assign_list_kernel(
         e[(uint64_t)m * n + idx[j]] = best[j];
       }
     }
+  }
+  flush_rescans(mine, &lcount, rescans);
+}
+
+// The deferred vectors of an encode: PQ.encode's scan semantics (best from
+// +inf, strict <; src/index/pq.zig:64-73) through the pruned exact search,
+// vectors gathered through defer[m][..] from the token-major input; codes
+// to out[i][m].  Grid as assign_list_kernel.
+template <int D, typename CodeT>
+__global__ __launch_bounds__(kBlock) void encode_list_kernel(
+    const float* __restrict__ x, const float* __restrict__ cb, CodeT* __restrict__ out,
+    const uint32_t* __restrict__ defer, const uint32_t* __restrict__ defer_count, uint64_t n,
+    uint32_t dim, uint32_t M, uint32_t K, unsigned long long* __restrict__ rescans,
+    unsigned long long* __restrict__ stats) {
+  constexpr int DP = Pad<D>::value;
+  extern __shared__ __attribute__((aligned(16))) float lds[];
+  const uint32_t m = blockIdx.y;
+  const uint32_t cnt = defer_count[m];
+  if (stats && blockIdx.x == 0 && threadIdx.x == 0) {
+    atomicAdd(&stats[0], (unsigned long long)cnt);
+    atomicAdd(&stats[1], (unsigned long long)n);
+  }
+  if ((uint64_t)blockIdx.x * kBlock >= cnt) return;
+  const uint32_t Kp = (K + kPruneBlock - 1) / kPruneBlock * kPruneBlock;
+  float* lcb = lds;
+  float* lnc = lds + Kp * DP;
+  uint32_t& lmax = *reinterpret_cast<uint32_t*>(lnc + Kp);
+  uint32_t& lcount = *(&lmax + 1);
+  if (threadIdx.x == 0) {
+    lmax = 0;
+    lcount = 0;
+  }
+  __syncthreads();
+  stage_pruned<D>(lcb, lnc, &lmax, cb + (uint64_t)m * K * D, K, Kp);
+  __syncthreads();
+  const uint32_t* lst = defer + (uint64_t)m * n;
+  uint32_t mine = 0;
+  for (uint64_t t0 = (uint64_t)blockIdx.x * kBlock; t0 < cnt; t0 += (uint64_t)gridDim.x * kBlock) {
+    const uint64_t q = t0 + threadIdx.x;
+    const uint32_t i = q < cnt ? lst[q] : 0xFFFFFFFFu;
+    float xv[1][D];
+    const float* src = x + (uint64_t)(i != 0xFFFFFFFFu ? i : 0u) * dim + (uint64_t)m * D;
+#pragma unroll
+    for (int k = 0; k < D; ++k) xv[0][k] = src[k];
+    uint32_t bidx[1];
+    float best[1];
+    pruned_argmin<D, 1, false>(xv, lcb, lnc, K, Kp, lmax, bidx, best, mine);
+    if (i != 0xFFFFFFFFu) out[(uint64_t)i * M + m] = (CodeT)bidx[0];
   }
   flush_rescans(mine, &lcount, rescans);
 }

@@ -88,7 +88,7 @@ struct DeviceState {
   // training / encode workspace
   Buffer xs, codes, e, hist, counts, start, sorted, flags, scal, trace, io_in, io_out, io_cb,
       io_init, counter, kpp_state, kpp_w, kpp_bsum, kpp_bad, status, io_aux, io_out2, scan_sums,
-      io_x1, io_x2, io_x3, crc_tx, fold_pre, fold_chunks, cand_nbr, cand_defer, cand_count;
+      io_x1, io_x2, io_x3, crc_tx, fold_pre, fold_chunks, cand_nbr, cand_defer, cand_count, cand_anchor, cand_grid;
   // token-aware clustering
   Buffer tac_v, tac_idx, tac_offs, tac_G, tac_spreads, tac_w, tac_e, tac_code, tac_sorted,
       tac_tsum, tac_hist, tac_counts, tac_start, tac_C, tac_pre, tac_fch, tac_st, tac_bad,
@@ -251,6 +251,24 @@ int validate_pq(uint64_t n, uint32_t dim, uint32_t m, uint32_t ksub) {
 
 // ---- kernel launchers -------------------------------------------------------
 
+// Raises a kernel's dynamic-LDS limit above the 64 KB default once per
+// function, to the largest layout it can be launched with (the candidate
+// kernels at K = 256, L = 64, and the given anchor-table size).
+int raise_lds(const void *fn, uint32_t bytes, uint32_t cells) {
+  if (bytes <= 65536) return TAC_OK;
+  static std::mutex mu;
+  static std::vector<const void *> raised;
+  std::lock_guard<std::mutex> g(mu);
+  for (const void *f : raised)
+    if (f == fn) return TAC_OK;
+  const uint32_t most = cand_lds(kCandMaxK, kCandList, 8, cells).total;
+  const hipError_t err = hipFuncSetAttribute(fn, hipFuncAttributeMaxDynamicSharedMemorySize,
+                                            (int)(most > bytes ? most : bytes));
+  if (err != hipSuccess) return hip_status("hipFuncSetAttribute(candidate kernel)", err);
+  raised.push_back(fn);
+  return TAC_OK;
+}
+
 template <int D>
 struct Launch {
   static int transpose(const float *x, float *xs, uint64_t n, uint32_t dim, hipStream_t s) {
@@ -281,25 +299,16 @@ struct Launch {
                          unsigned long long *rescans, hipStream_t s) {
     nbr_build_kernel<D><<<dim3(K, M), kWave, 0, s>>>(cb, nbr, defer_count, done, K, L);
     const CandLds lay = cand_lds(K, L, Pad<D>::value);
-    if (lay.total > 65536) {
-      static bool raised = false;
-      if (!raised) {
-        const hipError_t err = hipFuncSetAttribute((const void *)assign_cand_kernel<D>,
-                                                   hipFuncAttributeMaxDynamicSharedMemorySize,
-                                                   (int)cand_lds(kCandMaxK, kCandList,
-                                                                 Pad<D>::value).total);
-        if (err != hipSuccess) return hip_status("hipFuncSetAttribute(assign_cand_kernel)", err);
-        raised = true;
-      }
-    }
+    if (int st = raise_lds((const void *)cand_kernel<D, false, uint16_t>, lay.total, 0)) return st;
     // About 1,024 blocks over all subspaces; a chunk is whole groups of
     // kCandThreads vectors.
     const uint64_t per_sub = std::max<uint64_t>(1, (1024 + M - 1) / M);
     uint64_t chunk = (n + per_sub - 1) / per_sub;
     chunk = (chunk + kCandThreads - 1) / kCandThreads * kCandThreads;
     const uint64_t nblk = (n + chunk - 1) / chunk;
-    assign_cand_kernel<D><<<dim3((unsigned)nblk, M), kCandThreads, lay.total, s>>>(
-        xs, cb, nbr, codes, e, slice, defer, defer_count, done, n, K, L, (uint32_t)chunk);
+    cand_kernel<D, false, uint16_t><<<dim3((unsigned)nblk, M), kCandThreads, lay.total, s>>>(
+        xs, cb, nbr, nullptr, nullptr, codes, e, nullptr, slice, defer, defer_count, done, n, 0,
+        M, K, L, (uint32_t)chunk, (uint32_t)nblk, 0, 0);
     const uint32_t Kp = (K + kPruneBlock - 1) / kPruneBlock * kPruneBlock;
     const size_t lds = (size_t)Kp * (Pad<D>::value + 1) * sizeof(float) + 2 * sizeof(uint32_t);
     // About 2% of the vectors are deferred.  One vector per thread and about
@@ -310,6 +319,42 @@ struct Launch {
         1, std::min<uint64_t>((n + kBlock - 1) / kBlock, (4096 + M - 1) / M));
     assign_list_kernel<D, 1><<<dim3((unsigned)g, M), kBlock, lds, s>>>(
         xs, cb, codes, e, defer, defer_count, done, n, K, rescans,
+        g_profile ? rescans + 1 : nullptr);
+    return TAC_OK;
+  }
+  // Candidate-set encode: neighbour rows and grid anchors of the codebooks,
+  // the candidate pass over token-major input, then the reference scan of
+  // the deferred vectors.
+  template <typename CodeT>
+  static int encode_cand(const float *x, const float *cb, CodeT *codes, uint32_t *nbr,
+                         uint8_t *anchors, float *grid, uint32_t *slice, uint32_t *defer,
+                         uint32_t *defer_count, uint64_t n, uint32_t dim, uint32_t M, uint32_t K,
+                         uint32_t L, unsigned long long *rescans, hipStream_t s) {
+    const uint32_t G = cand_grid_side(D);
+    uint32_t cells = 1;
+    for (int k = 0; k < D; ++k) cells *= G;
+    nbr_build_kernel<D><<<dim3(K, M), kWave, 0, s>>>(cb, nbr, defer_count, nullptr, K, L);
+    grid_build_kernel<D><<<dim3((cells + kBlock - 1) / kBlock, M), kBlock, 0, s>>>(
+        cb, anchors, grid, K, G, cells);
+    const CandLds lay = cand_lds(K, L, Pad<D>::value, cells);
+    if (int st = raise_lds((const void *)cand_kernel<D, true, CodeT>, lay.total, cells))
+      return st;
+    // Chunks of 8,192 rows; the M blocks of a chunk run on one XCD, so a row
+    // crosses HBM once and its other subspaces come from L2.
+    const uint64_t chunk = 8192;
+    const uint64_t nchunks = (n + chunk - 1) / chunk;
+    const uint64_t total = nchunks * M;
+    if (total > 0xFFFFFFF0ull) return TAC_ERR_UNSUPPORTED;
+    const uint32_t blocks = (uint32_t)(8 * ((total + 7) / 8));
+    cand_kernel<D, true, CodeT><<<blocks, kCandThreads, lay.total, s>>>(
+        x, cb, nbr, anchors, grid, nullptr, nullptr, codes, slice, defer, defer_count, nullptr, n,
+        dim, M, K, L, (uint32_t)chunk, (uint32_t)nchunks, G, cells);
+    const uint32_t Kp = (K + kPruneBlock - 1) / kPruneBlock * kPruneBlock;
+    const size_t lds = (size_t)Kp * (Pad<D>::value + 1) * sizeof(float) + 2 * sizeof(uint32_t);
+    const uint64_t g = std::max<uint64_t>(
+        1, std::min<uint64_t>((n + kBlock - 1) / kBlock, (4096 + M - 1) / M));
+    encode_list_kernel<D, CodeT><<<dim3((unsigned)g, M), kBlock, lds, s>>>(
+        x, cb, codes, defer, defer_count, n, dim, M, K, rescans,
         g_profile ? rescans + 1 : nullptr);
     return TAC_OK;
   }
@@ -687,7 +732,26 @@ int encode_core(DeviceState &ds, hipStream_t s, const float *d_x, uint64_t n, ui
     HIP_TRY(hipEventRecord(a, s));
   }
   st = TAC_OK;
-  if (K <= 256) {
+  // Batches of 16,384 vectors or more take the candidate-set encode
+  // (cand_kernels.hpp); TAC_GPU_FULL_SEARCH=1 keeps the full search.
+  const char *full_env = getenv("TAC_GPU_FULL_SEARCH");
+  const uint32_t L = K >= 2 ? std::min<uint32_t>(kCandList, K - 1) : 0;
+  const bool cand = !(full_env && full_env[0] == '1') && K >= 2 && K <= kCandMaxK &&
+                    n >= 16384 && n <= 0xFFFFFFFFull;
+  if (cand) {
+    if ((st = ensure(ds, ds.cand_nbr, (size_t)M * K * L * sizeof(uint32_t))) ||
+        (st = ensure(ds, ds.cand_defer, (size_t)2 * M * n * sizeof(uint32_t))) ||
+        (st = ensure(ds, ds.cand_count, (size_t)M * sizeof(uint32_t))) ||
+        (st = ensure(ds, ds.cand_anchor, (size_t)M * kCandCells)) ||
+        (st = ensure(ds, ds.cand_grid, (size_t)M * 16 * sizeof(float))))
+      return st;
+    uint32_t *slices = as<uint32_t>(ds.cand_defer);
+    DISPATCH_D_ST(D, encode_cand<uint8_t>(d_x, d_cb, (uint8_t *)d_codes, as<uint32_t>(ds.cand_nbr),
+                                          as<uint8_t>(ds.cand_anchor), as<float>(ds.cand_grid),
+                                          slices, slices + (size_t)M * n,
+                                          as<uint32_t>(ds.cand_count), n, dim, M, K, L, rescans,
+                                          s));
+  } else if (K <= 256) {
     DISPATCH_D_ST(D, encode<uint8_t>(d_x, d_cb, (uint8_t *)d_codes, n, dim, M, K, rescans, s));
   } else {
     DISPATCH_D_ST(D, encode<uint16_t>(d_x, d_cb, (uint16_t *)d_codes, n, dim, M, K, rescans, s));

@@ -101,3 +101,75 @@ def test_kmeans_fit_assignments(gpu):
     assert np.array_equal(got.assignments, ref.assignments)
     assert np.array_equal(_bits(got.centroids), _bits(ref.centroids))
     assert np.float32(got.wcss).view(np.uint32) == np.float32(ref.wcss).view(np.uint32)
+
+
+# ---- encode: anchors from a grid over the codebook's bounding box ----------
+
+def _encode_both(x, cb, m, ksub):
+    dim = x.shape[1]
+    got = pq.PQ(dim, dim // m, np.ascontiguousarray(cb).reshape(-1), m, ksub).encode_many(x)
+    ref = orc.pq_encode(x, dim, m, ksub, cb, n_threads=16)
+    assert np.array_equal(got, ref), f"{np.count_nonzero(got != ref)} codes differ"
+    return got
+
+
+@pytest.mark.parametrize("dsub,ksub", [(1, 256), (2, 256), (3, 100), (4, 256), (5, 65),
+                                       (6, 17), (7, 2), (8, 256)])
+def test_encode_sub_dimensions_and_codebook_sizes(gpu, dsub, ksub):
+    m = 4
+    rng = np.random.default_rng(200 + dsub)
+    x = (rng.standard_normal((20000, m * dsub)) * 0.2).astype(np.float32)
+    cb = (rng.standard_normal((m, ksub, dsub)) * 0.2).astype(np.float32)
+    _encode_both(x, cb, m, ksub)
+
+
+def test_encode_ties_outliers_and_non_finite(gpu):
+    # Duplicate codewords (ties to the first index), vectors on codewords,
+    # vectors far outside the codebook's box (clamped to edge cells) and
+    # NaN / inf coordinates (PQ.encode keeps code 0 when every distance is
+    # NaN).
+    rng = np.random.default_rng(21)
+    m, ksub, dsub = 8, 256, 4
+    cb = (rng.standard_normal((m, ksub, dsub)) * 0.1).astype(np.float32)
+    cb[:, 200:] = cb[:, 10:66]
+    x = (rng.standard_normal((30000, m * dsub)) * 0.1).astype(np.float32)
+    on = cb[np.arange(m)[None, :], rng.integers(0, ksub, (5000, m))].reshape(5000, m * dsub)
+    x[:5000] = on
+    x[5000:6000] *= 1e4
+    x[6000, 3] = np.nan
+    x[6001, :] = np.nan
+    x[6002, 5] = np.inf
+    x[6003, 7] = -np.inf
+    _encode_both(x, cb, m, ksub)
+
+
+@pytest.mark.parametrize("scale", [1e-19, 1e15])
+def test_encode_extreme_magnitudes(gpu, scale):
+    rng = np.random.default_rng(23)
+    x = (rng.standard_normal((20000, 16)) * scale).astype(np.float32)
+    cb = (rng.standard_normal((4, 256, 4)) * scale).astype(np.float32)
+    _encode_both(x, cb, 4, 256)
+
+
+def test_encode_non_finite_codeword(gpu):
+    rng = np.random.default_rng(29)
+    x = (rng.standard_normal((20000, 16)) * 0.3).astype(np.float32)
+    cb = (rng.standard_normal((4, 256, 4)) * 0.3).astype(np.float32)
+    cb[1, 17, 2] = np.nan
+    cb[2, 99, 0] = np.inf
+    _encode_both(x, cb, 4, 256)
+
+
+def test_encode_matches_full_search_on_the_corpus(gpu, monkeypatch):
+    w, x, init = synth.workload("corpus-1.52m", n=200000)
+    p = pq.train(x, w.dim, 0, m=w.m, ksub=w.ksub, max_iters=3, tol=NEVER, init_codebooks=init)
+    device.profile_enable(True)
+    device.profile_read(reset=True)
+    got = p.encode_many(x)
+    prof = device.profile_read(reset=True)
+    device.profile_enable(False)
+    monkeypatch.setenv("TAC_GPU_FULL_SEARCH", "1")
+    full = p.encode_many(x)
+    assert np.array_equal(got, full)
+    assert prof.cand_vectors == w.m * x.shape[0]
+    assert 0 < prof.cand_deferred < 0.1 * prof.cand_vectors
