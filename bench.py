@@ -376,7 +376,7 @@ def main() -> int:
     if tfile.exists():
         try:
             for k, v in json.loads(tfile.read_text())["kernels"].items():
-                traffic[k.split("<")[0]] = int(v["read_bytes"]) + int(v["write_bytes"])
+                traffic[k] = int(v["read_bytes"]) + int(v["write_bytes"])
         except (ValueError, OSError, KeyError, TypeError):
             traffic = {}
 
@@ -418,8 +418,9 @@ def main() -> int:
             "bound": "mfma", "engine": "VALU fp32 (exact unfused distance + argmin)",
             "achieved": round(assign_tflops, 3), "peak": PEAK_FP32_TFLOPS, "unit": "TFLOP/s",
             "frac": round(assign_tflops / PEAK_FP32_TFLOPS, 4),
-            "traffic": (sum(traffic.get(k, 0) for k in ("nbr_build_kernel", "assign_cand_kernel",
-                                                          "assign_list_kernel")) or None),
+            "traffic": (sum(traffic.get(k, 0) for k in (
+                "nbr_build_kernel<4>", "cand_kernel<4, false, unsigned short>",
+                "assign_list_kernel<4, 1>")) or None),
             "avg_launch_ms": round(assign_avg_ms, 4), "algorithmic_flop_per_launch": assign_flop,
             "deferred_to_full_search": round(prof.cand_deferred / max(prof.cand_vectors, 1), 4),
         },
@@ -428,7 +429,7 @@ def main() -> int:
             "avg_launch_ms": round(full_avg_ms, 4),
             "achieved": round(assign_flop / (full_avg_ms * 1e-3) / 1e12, 3),
             "frac": round(assign_flop / (full_avg_ms * 1e-3) / 1e12 / PEAK_FP32_TFLOPS, 4),
-            "traffic": traffic.get("assign_kernel"),
+            "traffic": traffic.get("assign_kernel<4, 8>"),
         },
         "encode_roofline": {
             "avg_launch_ms": round(encode_avg_ms, 4),
@@ -436,16 +437,17 @@ def main() -> int:
             "valu_frac": round(encode_flop / (encode_avg_ms * 1e-3) / 1e12 / PEAK_FP32_TFLOPS, 4),
             "hbm_gbs": round(encode_bytes / (encode_avg_ms * 1e-3) / 1e9, 1),
             "hbm_frac": round(encode_bytes / (encode_avg_ms * 1e-3) / 1e9 / PEAK_HBM_GBS, 4),
-            "traffic": traffic.get("encode_kernel"),
+            "traffic": (sum(traffic.get(k, 0) for k in (
+                "nbr_build_kernel<4>", "grid_build_kernel<4>", "cand_kernel<4, true, unsigned char>",
+                "encode_list_kernel<4, unsigned char>")) or None),
         },
         "update_roofline": {
             "avg_iter_ms": round(update_avg_ms, 4),
             "hbm_gbs": round(update_bytes / (update_avg_ms * 1e-3) / 1e9, 1),
             "hbm_frac": round(update_bytes / (update_avg_ms * 1e-3) / 1e9 / PEAK_HBM_GBS, 4),
-            "traffic": (sum(traffic.get(k, 0) for k in ("hist_kernel", "scan_kernel",
-                                                          "scatter_kernel", "fold_kernel",
-                                                          "reseed_kernel", "converge_kernel"))
-                        or None),
+            "traffic": (sum(traffic.get(k, 0) for k in (
+                "hist_kernel", "scan_partial_kernel", "scan_apply_kernel", "scatter_kernel<4>",
+                "fold_kernel<4>", "reseed_kernel<4>", "converge_kernel")) or None),
         },
         "drop_in_defaults": drop_in,
         "residual_stage": residual,
