@@ -46,24 +46,14 @@
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
+#include "cand_rules.hpp"
 #include "pq_kernels.hpp"
 
 namespace tacgpu {
 
-constexpr uint32_t kCandList = 64;      // neighbours kept per codeword
-constexpr int kCandThreads = 1024;      // threads per assign_cand block
+constexpr int kCandThreads = 1024;      // threads per candidate block
 constexpr int kCandWaves = kCandThreads / kWave;
-constexpr uint32_t kCandMaxK = 256;     // codeword ids fit the key's low 8 bits
 constexpr uint32_t kCandLdsMax = 160 * 1024;
-
-// gamma_n = n u / (1 - n u) with n = D + 2, u = 2^-24: relative error bound
-// of the reference fold at sub-dimension D.
-template <int D>
-__host__ __device__ constexpr float fold_gamma() {
-  return (float)(D + 2) * 5.9604644775390625e-8f / (1.0f - (float)(D + 2) * 5.9604644775390625e-8f);
-}
-
-constexpr uint32_t kCandItem = 8;  // candidates per work item
 
 constexpr uint32_t kCandCells = 10000;  // grid cells per subspace (encode anchors)
 
@@ -103,15 +93,6 @@ __host__ __device__ inline uint32_t cand_grid_side(uint32_t D) {
   }
 }
 
-// Row position of sample q: 0, 7, 15, ..., 55.  With b samples inside R2
-// the row's entries inside R2 all lie in [0, 8b): item q covers [8q, 8q+8).
-__host__ __device__ inline uint32_t cand_sample_pos(uint32_t q) { return q ? 8u * q - 1u : 0u; }
-
-// Value part of a neighbour key: a lower bound of ||c_a - c||^2.
-__device__ __forceinline__ float cand_key_value(uint32_t key) {
-  return __uint_as_float(key & 0xFFFFFF00u);
-}
-
 // One wave per (codeword a, subspace m): lo(a, c) for every c != a, a
 // bitonic sort of the 256 keys in LDS, the first L written to
 // nbr[m][a][0 .. L).  Block (0, m) also clears the subspace's deferred
@@ -126,22 +107,18 @@ __global__ __launch_bounds__(kWave) void nbr_build_kernel(const float* __restric
   const uint32_t a = blockIdx.x, m = blockIdx.y, lane = threadIdx.x;
   if (a == 0 && lane == 0) defer_count[m] = 0;
   if (done && done[m]) return;
-  constexpr float g = fold_gamma<D>();
+  constexpr float g = cand_gamma(D);
   const float* cbm = cb + (uint64_t)m * K * D;
   float ca[D];
 #pragma unroll
   for (int k = 0; k < D; ++k) ca[k] = cbm[(uint64_t)a * D + k];
   for (uint32_t c = lane; c < kCandMaxK; c += kWave) {
-    uint32_t key = 0xFFFFFFFFu;
+    uint32_t key = kCandNoKey;
     if (c < K && c != a) {
       float cv[D];
 #pragma unroll
       for (int k = 0; k < D; ++k) cv[k] = cbm[(uint64_t)c * D + k];
-      // ||c_a - c||^2 >= (s - eta) / (1 + g) >= s (1 - 2g) - 1e-38 (rounded).
-      const float s = exact_l2sq<D>(ca, cv);
-      float lo = s * (1.0f - 2.0f * g) - 1e-38f;
-      lo = fmaxf(lo, 0.0f);
-      key = (__float_as_uint(lo) & 0xFFFFFF00u) | c;
+      key = cand_key(cand_lower_bound(exact_l2sq<D>(ca, cv), g), c);
     }
     keys[c] = key;
   }
@@ -243,7 +220,7 @@ __global__ __launch_bounds__(kCandThreads) void cand_kernel(
     uint32_t dim, uint32_t M, uint32_t K, uint32_t L, uint32_t chunk, uint32_t nchunks,
     uint32_t G, uint32_t cells) {
   constexpr int DP = Pad<D>::value;
-  constexpr float g = fold_gamma<D>();
+  constexpr float g = cand_gamma(D);
   extern __shared__ __attribute__((aligned(16))) float lds[];
   uint32_t m, b;
   if constexpr (ENCODE) {
@@ -293,10 +270,7 @@ __global__ __launch_bounds__(kCandThreads) void cand_kernel(
   const uint32_t Ls = L | 1u;  // LDS row stride
   const uint32_t* nbm = nbr + (uint64_t)m * K * L;
   for (uint32_t j = t; j < K * L; j += blockDim.x) lnbr[(j / L) * Ls + j % L] = nbm[j];
-  for (uint32_t j = t; j < K * 8; j += blockDim.x) {
-    const uint32_t pos = cand_sample_pos(j % 8);
-    lsamp[j] = pos < L ? nbm[(j / 8) * L + pos] & 0xFFFFFF00u : 0xFFFFFFFFu;
-  }
+  for (uint32_t j = t; j < K * 8; j += blockDim.x) lsamp[j] = cand_sample(nbm + (j / 8) * L, L, j % 8);
   if constexpr (ENCODE) {
     const uint8_t* am = anchors + (uint64_t)m * cells;
     for (uint32_t j = t; j < cells; j += blockDim.x) lanc[j] = am[j];
@@ -359,23 +333,18 @@ __global__ __launch_bounds__(kCandThreads) void cand_kernel(
       float ca[D];
       load_padded<D>(lcb + a * DP, ca);
       U2 = exact_l2sq<D>(x, ca);
-      if (!(U2 < 1e37f)) {  // NaN, inf or too large for the bound arithmetic
+      if (!cand_tame(U2)) {  // NaN, inf or too large for the bound arithmetic
         deferred = true;
       } else {
-        // R2 >= 4 (U2 + eta) / (1 - g): the x4 is exact, the factor covers g
-        // and the rounding of the product, the addend covers eta.
-        R2 = (U2 * 4.0f) * (1.0f + 8.0f * g) + 1e-38f;
+        R2 = cand_radius(U2, g);
         const uint4 s0 = *reinterpret_cast<const uint4*>(lsamp + a * 8);
         const uint4 s1 = *reinterpret_cast<const uint4*>(lsamp + a * 8 + 4);
         const uint32_t sv[8] = {s0.x, s0.y, s0.z, s0.w, s1.x, s1.y, s1.z, s1.w};
-#pragma unroll
-        for (int q = 0; q < 8; ++q) nit += __uint_as_float(sv[q]) <= R2 ? 1u : 0u;
-        // All samples inside R2 and codewords missing from the row: the
-        // candidate set may extend past it.
-        if (nit == 8 && !row_complete && cand_key_value(lnbr[a * Ls + L - 1]) <= R2) {
-          deferred = true;
-          nit = 0;
-        }
+        // The last kept entry is read only when every sample is inside R2.
+        const float last = __uint_as_float(sv[7]) <= R2 && !row_complete
+                               ? cand_key_value(lnbr[a * Ls + L - 1])
+                               : __builtin_inff();
+        nit = cand_items(sv, R2, last, row_complete, &deferred);
       }
     }
     const bool live = valid && !deferred;
@@ -399,7 +368,7 @@ __global__ __launch_bounds__(kCandThreads) void cand_kernel(
     if (live) {
 #pragma unroll
       for (int k = 0; k < DP; ++k) gx[lane * DP + k] = k < D ? x[k] : 0.0f;
-      gbest[lane] = ((unsigned long long)__float_as_uint(U2) << 32) | a;
+      gbest[lane] = cand_best_key(U2, a);
       gR2[lane] = R2;
       ga[lane] = a;
     }
@@ -414,18 +383,17 @@ __global__ __launch_bounds__(kCandThreads) void cand_kernel(
       const uint32_t* row = lnbr + ga[u] * Ls;
       uint32_t keys[kCandItem];
 #pragma unroll
-      for (uint32_t k = 0; k < kCandItem; ++k) keys[k] = j0 + k < L ? row[j0 + k] : 0xFFFFFFFFu;
+      for (uint32_t k = 0; k < kCandItem; ++k) keys[k] = j0 + k < L ? row[j0 + k] : kCandNoKey;
       float xv[D];
       load_padded<D>(gx + u * DP, xv);
       unsigned long long best = ~0ull;
 #pragma unroll
       for (uint32_t k = 0; k < kCandItem; ++k) {
-        if (cand_key_value(keys[k]) <= r2) {
+        if (cand_is_candidate(keys[k], j0 + k, L, r2)) {
           const uint32_t c = keys[k] & 0xFFu;
           float cv[D];
           load_padded<D>(lcb + c * DP, cv);
-          const float d = exact_l2sq<D>(xv, cv);
-          const unsigned long long key = ((unsigned long long)__float_as_uint(d) << 32) | c;
+          const unsigned long long key = cand_best_key(exact_l2sq<D>(xv, cv), c);
           best = key < best ? key : best;
         }
       }

@@ -1,0 +1,105 @@
+// cand_rules.hpp — the scalar rules of the exact candidate-set assignment,
+// shared by the GPU kernels (cand_kernels.hpp) and a host-side check
+// (tests/native/cand_rules_check.cpp).  Plain C++ when compiled by a host
+// compiler; compile with -ffp-contract=off either way.
+//
+// For an anchor codeword a and U2 = ref(x, c_a), the reference distance
+// (src/util/vec.zig:109-175: D squares and D-1 adds, separately rounded):
+//   * R2 = cand_radius(U2) >= 4 (U2 + eta) / (1 - g), g = gamma_{D+2};
+//   * a neighbour key stores cand_lower_bound(ref(c_a, c)) <= ||c_a - c||^2
+//     in its value bits and c in its low 8 bits;
+//   * every codeword that ties or beats c_a under ref() has a key value
+//     <= R2, so the reference's first-index argmin lies in
+//     {a} + {c : value(key(a, c)) <= R2}.
+#pragma once
+
+#include <stdint.h>
+#include <string.h>
+
+#ifndef TAC_HD
+#if defined(__HIPCC__)
+#define TAC_HD __host__ __device__
+#else
+#define TAC_HD
+#endif
+#endif
+
+namespace tacgpu {
+
+constexpr uint32_t kCandList = 64;  // neighbours kept per codeword
+constexpr uint32_t kCandItem = 8;   // candidates per work item
+constexpr uint32_t kCandMaxK = 256; // codeword ids fit the key's low 8 bits
+
+TAC_HD inline uint32_t cand_f2u(float f) {
+  uint32_t u;
+  memcpy(&u, &f, 4);
+  return u;
+}
+TAC_HD inline float cand_u2f(uint32_t u) {
+  float f;
+  memcpy(&f, &u, 4);
+  return f;
+}
+
+// gamma_n = n u / (1 - n u) with n = D + 2, u = 2^-24: relative error bound
+// of the reference fold at sub-dimension D.
+TAC_HD constexpr float cand_gamma(int D) {
+  return (float)(D + 2) * 5.9604644775390625e-8f / (1.0f - (float)(D + 2) * 5.9604644775390625e-8f);
+}
+
+// Radius of the candidate ball: R2 >= 4 (U2 + eta) / (1 - g).  The x4 is
+// exact, the factor covers g and the rounding of the product, the addend
+// covers eta (< 1e-43).  Valid for 0 <= U2 < 1e37 (cand_tame).
+TAC_HD inline float cand_radius(float U2, float g) { return (U2 * 4.0f) * (1.0f + 8.0f * g) + 1e-38f; }
+
+// The bound arithmetic stays finite; false on NaN and inf.
+TAC_HD inline bool cand_tame(float U2) { return U2 < 1e37f; }
+
+// Lower bound of ||c_a - c||^2 from s = ref(c_a, c): >= (s - eta) / (1 + g)
+// >= s (1 - 2g) - 1e-38 after rounding; clamped at 0 (NaN -> 0).
+TAC_HD inline float cand_lower_bound(float s, float g) {
+  const float lo = s * (1.0f - 2.0f * g) - 1e-38f;
+  return lo > 0.0f ? lo : 0.0f;
+}
+
+// Key of neighbour c: the bound's bits with the low 8 bits replaced by c.
+// Clearing low bits of a non-negative float lowers it, so the value part
+// stays a lower bound, and sorting keys sorts by bound, then by id.
+TAC_HD inline uint32_t cand_key(float lo, uint32_t c) { return (cand_f2u(lo) & 0xFFFFFF00u) | c; }
+TAC_HD inline float cand_key_value(uint32_t key) { return cand_u2f(key & 0xFFFFFF00u); }
+constexpr uint32_t kCandNoKey = 0xFFFFFFFFu;  // value part is NaN: never inside R2
+
+// Row position of sample q: 0, 7, 15, ..., 55.  With b samples inside R2,
+// every row entry inside R2 lies in [0, 8b): item q covers [8q, 8q + 8).
+TAC_HD inline uint32_t cand_sample_pos(uint32_t q) { return q ? 8u * q - 1u : 0u; }
+
+// Value bits of sample q of a row of L kept keys (all-ones past the row).
+TAC_HD inline uint32_t cand_sample(const uint32_t* row, uint32_t L, uint32_t q) {
+  const uint32_t pos = cand_sample_pos(q);
+  return pos < L ? row[pos] & 0xFFFFFF00u : kCandNoKey;
+}
+
+// Number of kCandItem-candidate items a vector needs from its anchor's row,
+// given the row's 8 samples; *deferred when all samples are inside R2, the
+// row is missing codewords (L + 1 < K) and its last kept entry is inside R2
+// too, so the candidate set may extend past the row.
+TAC_HD inline uint32_t cand_items(const uint32_t (&samples)[8], float R2, float last_value,
+                                  bool row_complete, bool* deferred) {
+  uint32_t nit = 0;
+  for (int q = 0; q < 8; ++q) nit += cand_u2f(samples[q]) <= R2 ? 1u : 0u;
+  *deferred = nit == 8 && !row_complete && last_value <= R2;
+  return *deferred ? 0u : nit;
+}
+
+// Entry j of the row is a candidate when j < L and its value is inside R2.
+TAC_HD inline bool cand_is_candidate(uint32_t key, uint32_t j, uint32_t L, float R2) {
+  return j < L && cand_key_value(key) <= R2;
+}
+
+// Lexicographic (distance bits, index) key: its minimum is the first-index
+// argmin among non-negative distances.
+TAC_HD inline uint64_t cand_best_key(float d, uint32_t c) {
+  return ((uint64_t)cand_f2u(d) << 32) | c;
+}
+
+}  // namespace tacgpu

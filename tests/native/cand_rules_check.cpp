@@ -1,0 +1,167 @@
+// Host check of the candidate-set rules used by the GPU assignment and encode
+// kernels (ir-multivector-retrieval_amd/csrc/cand_rules.hpp).  For random and
+// adversarial codebooks and vectors, and for any anchor codeword, the
+// candidate set that the rules select (neighbour rows of rounded-down bounds,
+// row samples, item counts, the R2 radius, deferral) must contain the
+// reference's first-index argmin (src/util/vec.zig:271-283 over the
+// unfused fold of vec.zig:109-175), and the lexicographic (distance bits,
+// index) minimum over it must equal that argmin and its distance bit for
+// bit.  Two planted mistakes must fail: a radius of rho instead of 2 rho, and
+// a tie rule that ignores the codeword index.
+// Build with -ffp-contract=off.
+#include <algorithm>
+#include <cmath>
+#include <cstdio>
+#include <vector>
+
+#include "../../ir-multivector-retrieval_amd/csrc/cand_rules.hpp"
+
+using namespace tacgpu;
+
+static uint64_t lcg = 0x2545F4914F6CDD1Dull;
+static uint64_t next_u64() {
+  lcg = lcg * 6364136223846793005ull + 1442695040888963407ull;
+  return lcg ^ (lcg >> 29);
+}
+static double unit() { return (double)(next_u64() >> 11) * (1.0 / 9007199254740992.0); }
+static float gauss() {
+  const double u1 = unit() + 1e-300, u2 = unit();
+  return (float)(std::sqrt(-2.0 * std::log(u1)) * std::cos(6.283185307179586 * u2));
+}
+
+// The reference distance: left fold, every operation rounded separately.
+static float fold(const float* x, const float* c, int D) {
+  float t = x[0] - c[0];
+  float s = t * t;
+  for (int k = 1; k < D; ++k) {
+    const float u = x[k] - c[k];
+    const float q = u * u;
+    s = s + q;
+  }
+  return s;
+}
+
+struct Counts {
+  long checks = 0, deferred = 0, wrong = 0, planted_radius = 0, planted_ties = 0;
+};
+
+static void run_case(const std::vector<float>& cb, int K, int D, const std::vector<float>& xs,
+                     int n, Counts& ct) {
+  const float g = cand_gamma(D);
+  const uint32_t L = std::min<uint32_t>(kCandList, (uint32_t)K - 1);
+  const bool row_complete = L + 1 >= (uint32_t)K;
+  std::vector<uint32_t> rows((size_t)K * L), samples((size_t)K * 8);
+  for (int a = 0; a < K; ++a) {
+    std::vector<uint32_t> keys;
+    for (int c = 0; c < K; ++c)
+      if (c != a) keys.push_back(cand_key(cand_lower_bound(fold(&cb[a * D], &cb[c * D], D), g), c));
+    std::sort(keys.begin(), keys.end());
+    for (uint32_t j = 0; j < L; ++j) rows[(size_t)a * L + j] = keys[j];
+    for (uint32_t q = 0; q < 8; ++q) samples[(size_t)a * 8 + q] = cand_sample(&rows[(size_t)a * L], L, q);
+  }
+  for (int i = 0; i < n; ++i) {
+    const float* x = &xs[(size_t)i * D];
+    // kmeans argmin: best = dists[0], strict < (vec.zig:271-283)
+    float best = fold(x, &cb[0], D);
+    int bi = 0;
+    for (int c = 1; c < K; ++c) {
+      const float d = fold(x, &cb[c * D], D);
+      if (d < best) {
+        best = d;
+        bi = c;
+      }
+    }
+    for (int rep = 0; rep < 3; ++rep) {
+      const int a = rep == 0 ? (int)(next_u64() % K) : rep == 1 ? bi : (int)(rows[(size_t)bi * L] & 0xFF);
+      const float U2 = fold(x, &cb[a * D], D);
+      ++ct.checks;
+      if (!cand_tame(U2)) {
+        ++ct.deferred;
+        continue;
+      }
+      const uint32_t* row = &rows[(size_t)a * L];
+      uint32_t sv[8];
+      for (int q = 0; q < 8; ++q) sv[q] = samples[(size_t)a * 8 + q];
+      const float R2 = cand_radius(U2, g);
+      bool deferred = false;
+      const uint32_t nit = cand_items(sv, R2, cand_key_value(row[L - 1]), row_complete, &deferred);
+      if (deferred) {
+        ++ct.deferred;
+        continue;
+      }
+      uint64_t key = cand_best_key(U2, a);
+      for (uint32_t j = 0; j < nit * kCandItem; ++j) {
+        const uint32_t k = j < L ? row[j] : kCandNoKey;
+        if (!cand_is_candidate(k, j, L, R2)) continue;
+        const uint32_t c = k & 0xFFu;
+        const uint64_t kk = cand_best_key(fold(x, &cb[c * D], D), c);
+        key = kk < key ? kk : key;
+      }
+      if ((int)(key & 0xFFFFFFFFu) != bi || (uint32_t)(key >> 32) != cand_f2u(best)) ++ct.wrong;
+      // Planted: radius rho^2 instead of 4 rho^2.
+      {
+        const float R2w = U2;
+        uint64_t kw = cand_best_key(U2, a);
+        for (uint32_t j = 0; j < L; ++j)
+          if (cand_key_value(row[j]) <= R2w) {
+            const uint32_t c = row[j] & 0xFFu;
+            const uint64_t kk = cand_best_key(fold(x, &cb[c * D], D), c);
+            kw = kk < kw ? kk : kw;
+          }
+        if ((int)(kw & 0xFFFFFFFFu) != bi) ++ct.planted_radius;
+      }
+      // Planted: ties resolved by scan order (row order) instead of the index.
+      {
+        float bd = U2;
+        uint32_t bc = a;
+        for (uint32_t j = 0; j < nit * kCandItem; ++j) {
+          const uint32_t k = j < L ? row[j] : kCandNoKey;
+          if (!cand_is_candidate(k, j, L, R2)) continue;
+          const uint32_t c = k & 0xFFu;
+          const float d = fold(x, &cb[c * D], D);
+          if (d < bd) {
+            bd = d;
+            bc = c;
+          }
+        }
+        if ((int)bc != bi) ++ct.planted_ties;
+      }
+    }
+  }
+}
+
+int main() {
+  Counts ct;
+  const int Ks[] = {2, 3, 17, 64, 65, 100, 256};
+  const double scales[] = {1.0, 1e-19, 1e-12, 1e15, 1e18};
+  for (int D = 1; D <= 8; ++D)
+    for (int K : Ks)
+      for (double sc : scales)
+        for (int pattern = 0; pattern < 3; ++pattern) {
+          std::vector<float> cb((size_t)K * D);
+          for (auto& v : cb) v = (float)(gauss() * 0.1 * sc);
+          if (pattern == 1)  // duplicates: the second half repeats the first
+            for (int c = K / 2; c < K; ++c)
+              for (int k = 0; k < D; ++k) cb[c * D + k] = cb[(c - K / 2) * D + k];
+          if (pattern == 2)  // few distinct points: many exact ties
+            for (int c = 0; c < K; ++c)
+              for (int k = 0; k < D; ++k) cb[c * D + k] = cb[(c % 5) * D + k];
+          const int n = 300;
+          std::vector<float> xs((size_t)n * D);
+          for (int i = 0; i < n; ++i) {
+            const int kind = i % 5;
+            for (int k = 0; k < D; ++k) {
+              float v = (float)(gauss() * 0.1 * sc);
+              if (kind == 1) v = cb[(next_u64() % K) * D + k];                       // on a codeword
+              if (kind == 2) v = (float)(cb[(i % K) * D + k] + gauss() * 1e-6 * sc);  // near one
+              if (kind == 3) v = (float)(v * 1e3);                                    // outlier
+              xs[(size_t)i * D + k] = v;
+            }
+          }
+          run_case(cb, K, D, xs, n, ct);
+        }
+  std::printf("cand rules: %ld checks, %ld deferred, %ld wrong; planted radius: %ld wrong, "
+              "planted ties: %ld wrong\n",
+              ct.checks, ct.deferred, ct.wrong, ct.planted_radius, ct.planted_ties);
+  return ct.wrong == 0 && ct.planted_radius > 0 && ct.planted_ties > 0 ? 0 : 1;
+}
