@@ -52,6 +52,12 @@
 namespace tacgpu {
 
 constexpr int kCandThreads = 1024;      // threads per candidate block
+// Training stages the neighbour rows in LDS (one block per CU).  Encode, which
+// also stages its anchor table, reads the rows from global memory (1 MB over
+// all subspaces, L2-resident) so that two blocks fit in a CU's LDS; the row
+// samples stay in LDS either way.
+template <bool ENCODE>
+constexpr bool cand_rows_in_lds() { return !ENCODE; }
 constexpr int kCandWaves = kCandThreads / kWave;
 constexpr uint32_t kCandLdsMax = 160 * 1024;
 
@@ -69,10 +75,10 @@ struct CandLds {
 };
 __host__ __device__ inline uint32_t cand_up16(uint32_t b) { return (b + 15u) & ~15u; }
 __host__ __device__ inline CandLds cand_lds(uint32_t K, uint32_t L, uint32_t DP,
-                                            uint32_t cells = 0) {
+                                            uint32_t cells = 0, bool rows_in_lds = true) {
   CandLds s;
   s.nbr_off = cand_up16(K * DP * 4u);
-  s.samp_off = cand_up16(s.nbr_off + K * (L | 1u) * 4u);
+  s.samp_off = cand_up16(s.nbr_off + (rows_in_lds ? K * (L | 1u) * 4u : 0u));
   s.anc_off = s.samp_off + K * 8u * 4u;
   s.grid_off = cand_up16(s.anc_off + cells);
   s.wave_off = s.grid_off + (cells ? 64u : 0u);
@@ -233,7 +239,8 @@ __global__ __launch_bounds__(kCandThreads) void cand_kernel(
     m = blockIdx.y;
     if (done[m]) return;
   }
-  const CandLds lay = cand_lds(K, L, DP, ENCODE ? cells : 0u);
+  constexpr bool kRowsInLds = cand_rows_in_lds<ENCODE>();
+  const CandLds lay = cand_lds(K, L, DP, ENCODE ? cells : 0u, kRowsInLds);
   uint8_t* base = reinterpret_cast<uint8_t*>(lds);
   float* lcb = lds;
   uint32_t* lnbr = reinterpret_cast<uint32_t*>(base + lay.nbr_off);
@@ -269,7 +276,10 @@ __global__ __launch_bounds__(kCandThreads) void cand_kernel(
   }
   const uint32_t Ls = L | 1u;  // LDS row stride
   const uint32_t* nbm = nbr + (uint64_t)m * K * L;
-  for (uint32_t j = t; j < K * L; j += blockDim.x) lnbr[(j / L) * Ls + j % L] = nbm[j];
+  if constexpr (kRowsInLds)
+    for (uint32_t j = t; j < K * L; j += blockDim.x) lnbr[(j / L) * Ls + j % L] = nbm[j];
+  const uint32_t* rows = kRowsInLds ? lnbr : nbm;  // row a at rows + a * rs
+  const uint32_t rs = kRowsInLds ? Ls : L;
   for (uint32_t j = t; j < K * 8; j += blockDim.x) lsamp[j] = cand_sample(nbm + (j / 8) * L, L, j % 8);
   if constexpr (ENCODE) {
     const uint8_t* am = anchors + (uint64_t)m * cells;
@@ -342,7 +352,7 @@ __global__ __launch_bounds__(kCandThreads) void cand_kernel(
         const uint32_t sv[8] = {s0.x, s0.y, s0.z, s0.w, s1.x, s1.y, s1.z, s1.w};
         // The last kept entry is read only when every sample is inside R2.
         const float last = __uint_as_float(sv[7]) <= R2 && !row_complete
-                               ? cand_key_value(lnbr[a * Ls + L - 1])
+                               ? cand_key_value(rows[a * rs + L - 1])
                                : __builtin_inff();
         nit = cand_items(sv, R2, last, row_complete, &deferred);
       }
@@ -380,10 +390,17 @@ __global__ __launch_bounds__(kCandThreads) void cand_kernel(
       const uint32_t it = gitem[w];
       const uint32_t u = it & 63u, j0 = (it >> 6) * kCandItem;
       const float r2 = gR2[u];
-      const uint32_t* row = lnbr + ga[u] * Ls;
+      const uint32_t* row = rows + ga[u] * rs;
       uint32_t keys[kCandItem];
+      if (!kRowsInLds && (L & 7u) == 0) {  // whole items: two 16-byte loads
+        const uint4 k0 = *reinterpret_cast<const uint4*>(row + j0);
+        const uint4 k1 = *reinterpret_cast<const uint4*>(row + j0 + 4);
+        keys[0] = k0.x; keys[1] = k0.y; keys[2] = k0.z; keys[3] = k0.w;
+        keys[4] = k1.x; keys[5] = k1.y; keys[6] = k1.z; keys[7] = k1.w;
+      } else {
 #pragma unroll
-      for (uint32_t k = 0; k < kCandItem; ++k) keys[k] = j0 + k < L ? row[j0 + k] : kCandNoKey;
+        for (uint32_t k = 0; k < kCandItem; ++k) keys[k] = j0 + k < L ? row[j0 + k] : kCandNoKey;
+      }
       float xv[D];
       load_padded<D>(gx + u * DP, xv);
       unsigned long long best = ~0ull;

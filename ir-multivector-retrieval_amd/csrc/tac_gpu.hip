@@ -336,7 +336,7 @@ struct Launch {
     nbr_build_kernel<D><<<dim3(K, M), kWave, 0, s>>>(cb, nbr, defer_count, nullptr, K, L);
     grid_build_kernel<D><<<dim3((cells + kBlock - 1) / kBlock, M), kBlock, 0, s>>>(
         cb, anchors, grid, K, G, cells);
-    const CandLds lay = cand_lds(K, L, Pad<D>::value, cells);
+    const CandLds lay = cand_lds(K, L, Pad<D>::value, cells, cand_rows_in_lds<true>());
     if (int st = raise_lds((const void *)cand_kernel<D, true, CodeT>, lay.total, cells))
       return st;
     // Chunks of 8,192 rows; the M blocks of a chunk run on one XCD, so a row
