@@ -96,6 +96,14 @@ TAC_HD inline bool cand_is_candidate(uint32_t key, uint32_t j, uint32_t L, float
   return j < L && cand_key_value(key) <= R2;
 }
 
+// True when a codeword whose anchor bound is lo (cand_lower_bound of its
+// reference distance to c_a) cannot tie or beat c_a for a vector with
+// U2 = ref(x, c_a): then ref(x, c) > U2.  k-means++ uses it to keep a weight
+// without reading the vector.
+TAC_HD inline bool cand_cannot_beat(float lo, float U2, float g) {
+  return cand_tame(U2) && lo > cand_radius(U2, g);
+}
+
 // Lexicographic (distance bits, index) key: its minimum is the first-index
 // argmin among non-negative distances.
 TAC_HD inline uint64_t cand_best_key(float d, uint32_t c) {

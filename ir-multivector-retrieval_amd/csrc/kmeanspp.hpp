@@ -22,6 +22,7 @@
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
+#include "cand_rules.hpp"
 #include "kpp_rules.hpp"
 
 namespace tacgpu {
@@ -40,37 +41,86 @@ constexpr int kKppBlock = 4096;  // weights per partial sum
 // Round c: write codeword c of every subspace from the row chosen last round,
 // update the weights w = min(w, l2sq(x, c_new)) (the first round assigns),
 // validate them, and emit f64 partial sums per block of kKppBlock rows.
+//
+// src[m][i] is the seed whose distance is w_i (w_i = l2sq(x_i, c_src)
+// exactly: it is the minimum so far).  A seed c_new can lower w_i only if
+// l2sq(x_i, c_new) < w_i, and by the candidate rule (cand_rules.hpp) it
+// cannot when a rounded-down bound of ||c_src - c_new||^2 exceeds
+// cand_radius(w_i): such weights are kept without reading the vector.
 template <int D>
 __global__ __launch_bounds__(256) void kpp_update_kernel(
-    const float* __restrict__ xs, float* __restrict__ w, double* __restrict__ bsum,
-    uint32_t* __restrict__ bad, const KppState* __restrict__ st, float* __restrict__ cb,
-    uint64_t n, uint32_t K, uint32_t c, uint32_t NB) {
+    const float* __restrict__ xs, float* __restrict__ w, uint16_t* __restrict__ src,
+    double* __restrict__ bsum, uint32_t* __restrict__ bad, const KppState* __restrict__ st,
+    float* __restrict__ cb, uint64_t n, uint32_t K, uint32_t c, uint32_t NB) {
   constexpr int DP = Pad<D>::value;
+  constexpr float g = cand_gamma(D);
   __shared__ double part[256 / 64];
+  __shared__ float lo_tab[1024];  // bound of ||c_j - c_new||^2 per earlier seed j
   const uint32_t m = blockIdx.y, b = blockIdx.x;
   if (st[m].err) return;
   const uint32_t chosen = st[m].chosen;
   float cv[D];
   load_padded<D>(xs + ((uint64_t)m * n + chosen) * DP, cv);
   if (b == 0 && threadIdx.x < (uint32_t)D) cb[((uint64_t)m * K + c) * D + threadIdx.x] = cv[threadIdx.x];
+  for (uint32_t j = threadIdx.x; j < c; j += blockDim.x) {
+    float cj[D];
+#pragma unroll
+    for (int k = 0; k < D; ++k) cj[k] = cb[((uint64_t)m * K + j) * D + k];
+    lo_tab[j] = cand_lower_bound(exact_l2sq<D>(cj, cv), g);
+  }
+  __syncthreads();
   const uint64_t lo = (uint64_t)b * kKppBlock;
   const uint64_t hi = lo + kKppBlock < n ? lo + kKppBlock : n;
   float* wm = w + (uint64_t)m * n;
+  uint16_t* sm = src + (uint64_t)m * n;
   const float* xm = xs + (uint64_t)m * n * DP;
   double acc = 0.0;
   bool invalid = false;
-  for (uint64_t i = lo + threadIdx.x; i < hi; i += blockDim.x) {
-    float xv[D];
-    load_padded<D>(xm + i * DP, xv);
-    const float d = exact_l2sq<D>(xv, cv);
-    bool store = true;
-    float wi = d;
-    if (c > 0) {
-      const float old = wm[i];
-      store = d < old;  // kmeans.zig:134: replace on strict <
-      wi = store ? d : old;
+  // Each thread owns kPer rows: weights and sources are loaded together, then
+  // only the rows the bound cannot settle load their vectors, so every load
+  // of a thread is in flight at once.
+  constexpr uint32_t kPer = kKppBlock / 256;
+  float wv[kPer];
+  uint32_t sv[kPer];
+  bool need[kPer];
+#pragma unroll
+  for (uint32_t j = 0; j < kPer; ++j) {
+    const uint64_t i = lo + j * 256 + threadIdx.x;
+    wv[j] = 0.0f;
+    sv[j] = 0;
+    if (c > 0 && i < hi) {
+      wv[j] = wm[i];
+      sv[j] = sm[i];
     }
-    if (store) wm[i] = wi;  // unchanged weights are not rewritten
+  }
+#pragma unroll
+  for (uint32_t j = 0; j < kPer; ++j) {
+    const uint64_t i = lo + j * 256 + threadIdx.x;
+    need[j] = i < hi && (c == 0 || !cand_cannot_beat(lo_tab[sv[j]], wv[j], g));
+  }
+  float xv[kPer][D];
+#pragma unroll
+  for (uint32_t j = 0; j < kPer; ++j) {
+    const uint64_t i = lo + j * 256 + threadIdx.x;
+    if (need[j]) load_padded<D>(xm + i * DP, xv[j]);
+  }
+#pragma unroll
+  for (uint32_t j = 0; j < kPer; ++j) {
+    const uint64_t i = lo + j * 256 + threadIdx.x;
+    if (i >= hi) continue;
+    float wi = wv[j];
+    if (need[j]) {
+      const float d = exact_l2sq<D>(xv[j], cv);
+      if (c == 0) {
+        wi = d;
+        wm[i] = d;
+        sm[i] = 0;
+      } else if (d < wi) {  // kmeans.zig:134: replace on strict <
+        wi = d;
+        wm[i] = d;  // unchanged weights are not rewritten
+        sm[i] = (uint16_t)c;
+      }
+    }
     invalid |= !(wi >= 0.0f && wi <= 3.402823466e38f);  // rng.zig:62 NonFinite
     acc += (double)wi;
   }

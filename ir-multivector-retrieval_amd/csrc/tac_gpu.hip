@@ -88,7 +88,7 @@ struct DeviceState {
   // training / encode workspace
   Buffer xs, codes, e, hist, counts, start, sorted, flags, scal, trace, io_in, io_out, io_cb,
       io_init, counter, kpp_state, kpp_w, kpp_bsum, kpp_bad, status, io_aux, io_out2, scan_sums,
-      io_x1, io_x2, io_x3, crc_tx, fold_pre, fold_chunks, cand_nbr, cand_defer, cand_count, cand_anchor, cand_grid;
+      io_x1, io_x2, io_x3, crc_tx, fold_pre, fold_chunks, cand_nbr, cand_defer, cand_count, cand_anchor, cand_grid, kpp_src;
   // token-aware clustering
   Buffer tac_v, tac_idx, tac_offs, tac_G, tac_spreads, tac_w, tac_e, tac_code, tac_sorted,
       tac_tsum, tac_hist, tac_counts, tac_start, tac_C, tac_pre, tac_fch, tac_st, tac_bad,
@@ -379,10 +379,10 @@ struct Launch {
                                                   M, code_bits(K));
     return TAC_OK;
   }
-  static void kpp_update(const float *xs, float *w, double *bsum, uint32_t *bad,
+  static void kpp_update(const float *xs, float *w, uint16_t *src, double *bsum, uint32_t *bad,
                          const KppState *st, float *cb, uint64_t n, uint32_t M, uint32_t K,
                          uint32_t c, uint32_t NB, hipStream_t s) {
-    kpp_update_kernel<D><<<dim3(NB, M), 256, 0, s>>>(xs, w, bsum, bad, st, cb, n, K, c, NB);
+    kpp_update_kernel<D><<<dim3(NB, M), 256, 0, s>>>(xs, w, src, bsum, bad, st, cb, n, K, c, NB);
   }
   static void fold(const float *sorted, const uint32_t *counts, const uint32_t *start,
                    float *cb, const uint32_t *done, uint64_t n, uint32_t M, uint32_t K,
@@ -459,6 +459,7 @@ int kmeanspp(DeviceState &ds, hipStream_t s, const float *xs, uint64_t n, uint32
   int st;
   if ((st = ensure(ds, ds.kpp_state, (size_t)M * sizeof(KppState))) ||
       (st = ensure(ds, ds.kpp_w, (size_t)M * n * sizeof(float))) ||
+      (st = ensure(ds, ds.kpp_src, (size_t)M * n * sizeof(uint16_t))) ||
       (st = ensure(ds, ds.kpp_bsum, (size_t)M * NB * sizeof(double))) ||
       (st = ensure(ds, ds.kpp_bad, (size_t)M * sizeof(uint32_t))))
     return st;
@@ -481,7 +482,8 @@ int kmeanspp(DeviceState &ds, hipStream_t s, const float *xs, uint64_t n, uint32
   kpp_init_kernel<<<(M + 63) / 64, 64, 0, s>>>(state, bad, seed, n, M);
   LAUNCH_TRY("kpp_init_kernel");
   for (uint32_t c = 0; c < K; ++c) {
-    DISPATCH_D(D, kpp_update(xs, w, bsum, bad, state, cb, n, M, K, c, NB, s));
+    DISPATCH_D(D, kpp_update(xs, w, as<uint16_t>(ds.kpp_src), bsum, bad, state, cb, n, M, K, c,
+                             NB, s));
     LAUNCH_TRY("kpp_update_kernel");
     if (c + 1 == K) break;
     kpp_select_kernel<<<M, 1024, 0, s>>>(w, bsum, bad, state, n, NB, exact_only);
@@ -903,7 +905,9 @@ int tac_gpu_release_workspace(void) {
                     &ds->tac_st,    &ds->tac_bad, &ds->tac_done,  &ds->tac_iters,
                     &ds->tac_wcss,  &ds->tac_prev, &ds->tac_empties, &ds->tac_assign,
                     &ds->tac_probs, &ds->tac_tiles, &ds->tac_chl, &ds->tac_cprob,
-                    &ds->tac_inv,   &ds->tac_rsum, &ds->tac_ranges};
+                    &ds->tac_inv,   &ds->tac_rsum, &ds->tac_ranges, &ds->cand_nbr,
+                    &ds->cand_defer, &ds->cand_count, &ds->cand_anchor, &ds->cand_grid,
+                    &ds->kpp_src};
   ds->crc_tx_ready = false;
   for (Buffer *b : bufs) {
     if (b->ptr) HIP_TRY(hipFree(b->ptr));

@@ -7,7 +7,9 @@
 // unfused fold of vec.zig:109-175), and the lexicographic (distance bits,
 // index) minimum over it must equal that argmin and its distance bit for
 // bit.  Two planted mistakes must fail: a radius of rho instead of 2 rho, and
-// a tie rule that ignores the codeword index.
+// a tie rule that ignores the codeword index.  The k-means++ skip
+// (cand_cannot_beat) is checked directly: whenever it holds for a codeword,
+// that codeword's reference distance is strictly greater than the anchor's.
 // Build with -ffp-contract=off.
 #include <algorithm>
 #include <cmath>
@@ -43,6 +45,7 @@ static float fold(const float* x, const float* c, int D) {
 
 struct Counts {
   long checks = 0, deferred = 0, wrong = 0, planted_radius = 0, planted_ties = 0;
+  long skip_checks = 0, skips = 0, skip_wrong = 0;
 };
 
 static void run_case(const std::vector<float>& cb, int K, int D, const std::vector<float>& xs,
@@ -75,6 +78,15 @@ static void run_case(const std::vector<float>& cb, int K, int D, const std::vect
       const int a = rep == 0 ? (int)(next_u64() % K) : rep == 1 ? bi : (int)(rows[(size_t)bi * L] & 0xFF);
       const float U2 = fold(x, &cb[a * D], D);
       ++ct.checks;
+      if (rep == 0)  // the k-means++ skip against every other codeword
+        for (int c = 0; c < K; ++c) {
+          if (c == a) continue;
+          ++ct.skip_checks;
+          if (cand_cannot_beat(cand_lower_bound(fold(&cb[a * D], &cb[c * D], D), g), U2, g)) {
+            ++ct.skips;
+            if (!(fold(x, &cb[c * D], D) > U2)) ++ct.skip_wrong;
+          }
+        }
       if (!cand_tame(U2)) {
         ++ct.deferred;
         continue;
@@ -163,5 +175,10 @@ int main() {
   std::printf("cand rules: %ld checks, %ld deferred, %ld wrong; planted radius: %ld wrong, "
               "planted ties: %ld wrong\n",
               ct.checks, ct.deferred, ct.wrong, ct.planted_radius, ct.planted_ties);
-  return ct.wrong == 0 && ct.planted_radius > 0 && ct.planted_ties > 0 ? 0 : 1;
+  std::printf("kmeans++ skip: %ld checks, %ld skips, %ld skip_wrong\n", ct.skip_checks, ct.skips,
+              ct.skip_wrong);
+  return ct.wrong == 0 && ct.skip_wrong == 0 && ct.skips > 0 && ct.planted_radius > 0 &&
+                 ct.planted_ties > 0
+             ? 0
+             : 1;
 }
