@@ -414,7 +414,7 @@ def main() -> int:
         "encode_mvec_per_s": round(n / mean_encode / 1e6, 2),
         "roofline": {
             "kernel": "Lloyd assignment from the previous codes (nbr_build_kernel + "
-                      "assign_cand_kernel + assign_list_kernel), iterations 1-19, all subspaces",
+                      "cand_kernel + assign_list_kernel), iterations 1-19, all subspaces",
             "bound": "mfma", "engine": "VALU fp32 (exact unfused distance + argmin)",
             "achieved": round(assign_tflops, 3), "peak": PEAK_FP32_TFLOPS, "unit": "TFLOP/s",
             "frac": round(assign_tflops / PEAK_FP32_TFLOPS, 4),
