@@ -31,7 +31,10 @@ namespace tacgpu {
 
 constexpr int kBlock = 256;        // threads per block for the streaming kernels
 constexpr int kSortTile = 2048;    // vectors per stable counting-sort tile (4 waves)
-constexpr int kFoldBatch = 8;      // 64-record loads in flight per fold wave
+// 64-record loads in flight per fold wave: 16 up to dsub 4 (one batch is
+// then long enough to cover the next batch's load), 8 above (registers).
+template <int D>
+constexpr int fold_batch() { return D <= 4 ? 16 : 8; }
 constexpr int kWave = 64;
 
 template <int D>
@@ -628,7 +631,7 @@ __global__ __launch_bounds__(kBlock) void scatter_kernel(
 }
 
 // Step 4: one wave per (subspace, cluster).  The wave streams the cluster's
-// contiguous records with coalesced loads (kFoldBatch x 64 records in
+// contiguous records with coalesced loads (fold_batch<D>() x 64 records in
 // flight, staged through LDS dimension-major) and lanes 0..D-1 fold
 // dimension d in ascending vector order from 0.0f, then write
 // sum * fl(1 / fl(count)) (src/tac/kmeans.zig:177-198).  Empty clusters are
@@ -639,7 +642,7 @@ __global__ __launch_bounds__(kWave) void fold_kernel(
     const uint32_t* __restrict__ start, float* __restrict__ cb,
     const uint32_t* __restrict__ done, uint64_t n, uint32_t K) {
   constexpr int DP = Pad<D>::value;
-  constexpr uint32_t U = kFoldBatch;
+  constexpr uint32_t U = fold_batch<D>();
   constexpr uint32_t kCol = U * kWave + 4;  // padded: the D columns start on distinct banks
   __shared__ __attribute__((aligned(16))) float buf[kCol * DP];
   const uint32_t m = blockIdx.x / K, c = blockIdx.x % K;
