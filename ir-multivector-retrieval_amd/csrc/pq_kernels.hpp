@@ -31,10 +31,7 @@ namespace tacgpu {
 
 constexpr int kBlock = 256;        // threads per block for the streaming kernels
 constexpr int kSortTile = 2048;    // vectors per stable counting-sort tile (4 waves)
-// 64-record loads in flight per fold wave: 16 up to dsub 4 (one batch is
-// then long enough to cover the next batch's load), 8 above (registers).
-template <int D>
-constexpr int fold_batch() { return D <= 4 ? 16 : 8; }
+constexpr int kFoldBatch = 8;      // 64-record loads in flight per fold wave
 constexpr int kWave = 64;
 
 template <int D>
@@ -631,7 +628,7 @@ __global__ __launch_bounds__(kBlock) void scatter_kernel(
 }
 
 // Step 4: one wave per (subspace, cluster).  The wave streams the cluster's
-// contiguous records with coalesced loads (fold_batch<D>() x 64 records in
+// contiguous records with coalesced loads (kFoldBatch x 64 records in
 // flight, staged through LDS dimension-major) and lanes 0..D-1 fold
 // dimension d in ascending vector order from 0.0f, then write
 // sum * fl(1 / fl(count)) (src/tac/kmeans.zig:177-198).  Empty clusters are
@@ -642,8 +639,10 @@ __global__ __launch_bounds__(kWave) void fold_kernel(
     const uint32_t* __restrict__ start, float* __restrict__ cb,
     const uint32_t* __restrict__ done, uint64_t n, uint32_t K) {
   constexpr int DP = Pad<D>::value;
-  constexpr uint32_t U = fold_batch<D>();
-  constexpr uint32_t kCol = U * kWave + 4;  // padded: the D columns start on distinct banks
+  constexpr uint32_t U = kFoldBatch;
+  // Padded: the D columns start on distinct banks, and the fold's reads of
+  // the next 32 members stay inside the column.
+  constexpr uint32_t kCol = U * kWave + 36;
   __shared__ __attribute__((aligned(16))) float buf[kCol * DP];
   const uint32_t m = blockIdx.x / K, c = blockIdx.x % K;
   if (done[m]) return;
@@ -686,16 +685,28 @@ __global__ __launch_bounds__(kWave) void fold_kernel(
     if (j0 + U * kWave < cnt) load_batch(j0 + U * kWave);
     const uint32_t len = cnt - j0 < U * kWave ? cnt - j0 : U * kWave;
     if (lane < (uint32_t)D) {
+      // One dependent add per member.  The reads of the next 32 members are
+      // issued before the current 32 are added, so their LDS latency hides
+      // behind the chain (they may read the column's padding, never past it).
       const float* col = buf + lane * kCol;
       const float4* col4 = reinterpret_cast<const float4*>(col);
       uint32_t jj = 0;
-#pragma unroll 4
-      for (; jj + 4 <= len; jj += 4) {
-        const float4 e = col4[jj / 4];
-        acc = acc + e.x;
-        acc = acc + e.y;
-        acc = acc + e.z;
-        acc = acc + e.w;
+      float4 a[8];
+#pragma unroll
+      for (int q = 0; q < 8; ++q) a[q] = col4[q];
+      for (; jj + 32 <= len; jj += 32) {
+        float4 b[8];
+#pragma unroll
+        for (int q = 0; q < 8; ++q) b[q] = col4[jj / 4 + 8 + q];
+#pragma unroll
+        for (int q = 0; q < 8; ++q) {
+          acc = acc + a[q].x;
+          acc = acc + a[q].y;
+          acc = acc + a[q].z;
+          acc = acc + a[q].w;
+        }
+#pragma unroll
+        for (int q = 0; q < 8; ++q) a[q] = b[q];
       }
       for (; jj < len; ++jj) acc = acc + col[jj];
     }
