@@ -19,9 +19,9 @@
 //   smallest index among its ties, so that minimum is c*.
 //
 // Anchors.  Lloyd iterations after the first anchor each vector at its
-// previous code.  Encode anchors it at the codeword nearest the centre of its
-// cell in a grid over the codebook's bounding box (grid_build_kernel); a
-// vector outside the box takes the nearest cell.  The rule above holds for
+// previous code.  Encode anchors it at the nearer of the two codewords
+// nearest the centre of its cell in a grid over the codebook's bounding box
+// (grid_build_kernel); a vector outside the box takes the nearest cell.  The rule above holds for
 // any anchor, so the anchor only decides how many candidates are evaluated.
 //
 // Neighbour tables.  After every update, nbr_build_kernel sorts, for each
@@ -61,13 +61,14 @@ constexpr bool cand_rows_in_lds() { return !ENCODE; }
 constexpr int kCandWaves = kCandThreads / kWave;
 constexpr uint32_t kCandLdsMax = 160 * 1024;
 
-constexpr uint32_t kCandCells = 10000;  // grid cells per subspace (encode anchors)
+constexpr uint32_t kCandCells = 6561;  // grid cells per subspace (encode anchors), 9^4
+constexpr uint32_t kCandAnchors = 2;   // anchor codewords per cell
 
 // LDS layout of cand_kernel, shared by the host launcher:
 //   lcb [K][DP] f32 | lnbr [K][L|1] u32 (an odd row stride puts the rows of
 //   different anchors in different banks) | lsamp [K][8] u32: the value bits
 //   of row entries 0, 7, 15, ..., 55 (all-ones past the row) | encode only:
-//   lanc [cells] u8 anchors, lgrid [2][8] f32 (cell origin, cells per unit) |
+//   lanc [cells][2] u8 anchors, lgrid [2][8] f32 (cell origin, cells per unit) |
 //   per wave: gx [64][DP] f32, gbest [64] u64, gR2 [64] f32, ga [64] u32,
 //   gitem [64 * 8] u16 (lane | item << 6) | lmax, lcnt u32
 struct CandLds {
@@ -80,7 +81,7 @@ __host__ __device__ inline CandLds cand_lds(uint32_t K, uint32_t L, uint32_t DP,
   s.nbr_off = cand_up16(K * DP * 4u);
   s.samp_off = cand_up16(s.nbr_off + (rows_in_lds ? K * (L | 1u) * 4u : 0u));
   s.anc_off = s.samp_off + K * 8u * 4u;
-  s.grid_off = cand_up16(s.anc_off + cells);
+  s.grid_off = cand_up16(s.anc_off + cells * kCandAnchors);
   s.wave_off = s.grid_off + (cells ? 64u : 0u);
   s.wave_bytes = 64u * (DP * 4u + 8u + 4u + 4u) + 64u * 8u * 2u;
   s.scal_off = s.wave_off + (uint32_t)kCandWaves * s.wave_bytes;
@@ -150,8 +151,9 @@ __global__ __launch_bounds__(kWave) void nbr_build_kernel(const float* __restric
 
 // Encode anchors of subspace m = blockIdx.y: the bounding box of the
 // codewords (lo, hi per dimension), G cells per dimension, and for each cell
-// the codeword nearest its centre (any choice is valid; nearness only keeps
-// the candidate sets small).  grid[m] = {lo[8], G / (hi - lo)[8]}.
+// the two codewords nearest its centre (any choice is valid; nearness only
+// keeps the candidate sets small).  grid[m] = {lo[8], G / (hi - lo)[8]},
+// anchors[m][cell][0..1].
 template <int D>
 __global__ __launch_bounds__(kBlock) void grid_build_kernel(const float* __restrict__ cb,
                                                             uint8_t* __restrict__ anchors,
@@ -189,8 +191,8 @@ __global__ __launch_bounds__(kBlock) void grid_build_kernel(const float* __restr
     r /= G;
     ctr[k] = box[k] + ((float)ck + 0.5f) / (box[D + k] > 0.0f ? box[D + k] : 1.0f);
   }
-  float best = __builtin_inff();
-  uint32_t bi = 0;
+  float best = __builtin_inff(), second = __builtin_inff();
+  uint32_t bi = 0, si = 0;
   for (uint32_t c = 0; c < K; ++c) {
     float d = 0.0f;
 #pragma unroll
@@ -199,11 +201,17 @@ __global__ __launch_bounds__(kBlock) void grid_build_kernel(const float* __restr
       d = d + u * u;
     }
     if (d < best) {
+      second = best;
+      si = bi;
       best = d;
       bi = c;
+    } else if (d < second) {
+      second = d;
+      si = c;
     }
   }
-  anchors[(uint64_t)m * cells + cell] = (uint8_t)bi;
+  anchors[((uint64_t)m * cells + cell) * kCandAnchors] = (uint8_t)bi;
+  anchors[((uint64_t)m * cells + cell) * kCandAnchors + 1] = (uint8_t)(K > 1 ? si : bi);
 }
 
 // The exact candidate-set assignment.  Training (ENCODE false): block
@@ -282,8 +290,8 @@ __global__ __launch_bounds__(kCandThreads) void cand_kernel(
   const uint32_t rs = kRowsInLds ? Ls : L;
   for (uint32_t j = t; j < K * 8; j += blockDim.x) lsamp[j] = cand_sample(nbm + (j / 8) * L, L, j % 8);
   if constexpr (ENCODE) {
-    const uint8_t* am = anchors + (uint64_t)m * cells;
-    for (uint32_t j = t; j < cells; j += blockDim.x) lanc[j] = am[j];
+    const uint8_t* am = anchors + (uint64_t)m * cells * kCandAnchors;
+    for (uint32_t j = t; j < cells * kCandAnchors; j += blockDim.x) lanc[j] = am[j];
     if (t < 16) lgrid[t] = grid[m * 16 + t];
   }
   __syncthreads();
@@ -327,14 +335,15 @@ __global__ __launch_bounds__(kCandThreads) void cand_kernel(
       load_x(i + kStride, xq);
       if constexpr (!ENCODE) aq = cm[i + kStride];
     }
+    uint32_t cell = 0;  // encode: NaN coordinates land in cell 0 (fmaxf)
     if constexpr (ENCODE) {
-      uint32_t cell = 0;  // NaN coordinates land in cell 0 (fmaxf)
 #pragma unroll
       for (int k = D - 1; k >= 0; --k) {
         const float f = fminf(fmaxf((x[k] - lgrid[k]) * lgrid[8 + k], 0.0f), (float)(G - 1));
         cell = cell * G + (uint32_t)f;
       }
-      a = lanc[cell < cells ? cell : 0u];
+      cell = cell < cells ? cell : 0u;
+      a = lanc[cell * kCandAnchors];
     }
     bool deferred = valid && (all_deferred || a >= K);
     uint32_t nit = 0;
@@ -343,6 +352,16 @@ __global__ __launch_bounds__(kCandThreads) void cand_kernel(
       float ca[D];
       load_padded<D>(lcb + a * DP, ca);
       U2 = exact_l2sq<D>(x, ca);
+      if constexpr (ENCODE) {  // the nearer of the cell's two anchors
+        const uint32_t a2 = lanc[cell * kCandAnchors + 1];
+        float cb2[D];
+        load_padded<D>(lcb + a2 * DP, cb2);
+        const float V2 = exact_l2sq<D>(x, cb2);
+        if (V2 < U2) {
+          U2 = V2;
+          a = a2;
+        }
+      }
       if (!cand_tame(U2)) {  // NaN, inf or too large for the bound arithmetic
         deferred = true;
       } else {

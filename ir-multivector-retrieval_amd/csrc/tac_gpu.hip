@@ -744,7 +744,7 @@ int encode_core(DeviceState &ds, hipStream_t s, const float *d_x, uint64_t n, ui
     if ((st = ensure(ds, ds.cand_nbr, (size_t)M * K * L * sizeof(uint32_t))) ||
         (st = ensure(ds, ds.cand_defer, (size_t)2 * M * n * sizeof(uint32_t))) ||
         (st = ensure(ds, ds.cand_count, (size_t)M * sizeof(uint32_t))) ||
-        (st = ensure(ds, ds.cand_anchor, (size_t)M * kCandCells)) ||
+        (st = ensure(ds, ds.cand_anchor, (size_t)M * kCandCells * kCandAnchors)) ||
         (st = ensure(ds, ds.cand_grid, (size_t)M * 16 * sizeof(float))))
       return st;
     uint32_t *slices = as<uint32_t>(ds.cand_defer);
