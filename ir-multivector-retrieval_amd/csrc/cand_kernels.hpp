@@ -65,11 +65,13 @@ constexpr uint32_t kCandCells = 6561;  // grid cells per subspace (encode anchor
 constexpr uint32_t kCandAnchors = 2;   // anchor codewords per cell
 
 // LDS layout of cand_kernel, shared by the host launcher:
-//   lcb [K][DP] f32 | lnbr [K][L|1] u32 (an odd row stride puts the rows of
-//   different anchors in different banks) | lsamp [K][8] u32: the value bits
+//   lcb [K][DP] f32 | lnbr [K][Lr|1] u32, Lr = cand_row_len(L) (an odd row
+//   stride puts the rows of different anchors in different banks) |
+//   lsamp [K][8] u32: the value bits
 //   of row entries 0, 7, 15, ..., 55 (all-ones past the row) | encode only:
 //   lanc [cells][2] u8 anchors, lgrid [2][8] f32 (cell origin, cells per unit) |
-//   per wave: gx [64][DP] f32, gbest [64] u64, gR2 [64] f32, ga [64] u32,
+//   per wave: gx [64][DP] f32, gbest [64] u64, gT [64] u32 (cand_threshold
+//   of R2), ga [64] u32,
 //   gitem [64 * 8] u16 (lane | item << 6) | lmax, lcnt u32
 struct CandLds {
   uint32_t nbr_off, samp_off, anc_off, grid_off, wave_off, wave_bytes, scal_off, total;
@@ -79,7 +81,7 @@ __host__ __device__ inline CandLds cand_lds(uint32_t K, uint32_t L, uint32_t DP,
                                             uint32_t cells = 0, bool rows_in_lds = true) {
   CandLds s;
   s.nbr_off = cand_up16(K * DP * 4u);
-  s.samp_off = cand_up16(s.nbr_off + (rows_in_lds ? K * (L | 1u) * 4u : 0u));
+  s.samp_off = cand_up16(s.nbr_off + (rows_in_lds ? K * (cand_row_len(L) | 1u) * 4u : 0u));
   s.anc_off = s.samp_off + K * 8u * 4u;
   s.grid_off = cand_up16(s.anc_off + cells * kCandAnchors);
   s.wave_off = s.grid_off + (cells ? 64u : 0u);
@@ -102,7 +104,8 @@ __host__ __device__ inline uint32_t cand_grid_side(uint32_t D) {
 
 // One wave per (codeword a, subspace m): lo(a, c) for every c != a, a
 // bitonic sort of the 256 keys in LDS, the first L written to
-// nbr[m][a][0 .. L).  Block (0, m) also clears the subspace's deferred
+// nbr[m][a][0 .. L) and kCandNoKey to the rest of the stored row
+// nbr[m][a][L .. cand_row_len(L)).  Block (0, m) also clears the subspace's deferred
 // count for the assignment that follows on the same stream.
 template <int D>
 __global__ __launch_bounds__(kWave) void nbr_build_kernel(const float* __restrict__ cb,
@@ -145,8 +148,9 @@ __global__ __launch_bounds__(kWave) void nbr_build_kernel(const float* __restric
       wave_lds_sync();
     }
   }
-  uint32_t* row = nbr + ((uint64_t)m * K + a) * L;
-  for (uint32_t j = lane; j < L; j += kWave) row[j] = keys[j];
+  const uint32_t Lr = cand_row_len(L);
+  uint32_t* row = nbr + ((uint64_t)m * K + a) * Lr;
+  for (uint32_t j = lane; j < Lr; j += kWave) row[j] = j < L ? keys[j] : kCandNoKey;
 }
 
 // Encode anchors of subspace m = blockIdx.y: the bounding box of the
@@ -214,6 +218,19 @@ __global__ __launch_bounds__(kBlock) void grid_build_kernel(const float* __restr
   anchors[((uint64_t)m * cells + cell) * kCandAnchors + 1] = (uint8_t)(K > 1 ? si : bi);
 }
 
+// Inclusive sum over the 64 lanes of a wave with DPP moves: shifts of 1, 2,
+// 4, 8 within each row of 16 lanes, then the row totals carried forward
+// with the row broadcasts of lanes 15 and 31.
+__device__ inline uint32_t wave_inclusive_sum(uint32_t v) {
+  v += (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, 0x111, 0xf, 0xf, false);  // row_shr:1
+  v += (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, 0x112, 0xf, 0xf, false);  // row_shr:2
+  v += (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, 0x114, 0xf, 0xf, false);  // row_shr:4
+  v += (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, 0x118, 0xf, 0xf, false);  // row_shr:8
+  v += (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, 0x142, 0xa, 0xf, false);  // row_bcast:15
+  v += (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, 0x143, 0xc, 0xf, false);  // row_bcast:31
+  return v;
+}
+
 // The exact candidate-set assignment.  Training (ENCODE false): block
 // (chunk b, subspace m) of a 2-D grid; x = xs[m][i][DP]; the anchor is
 // codes[m][i] (the previous iteration's code) and the result goes back to
@@ -259,8 +276,8 @@ __global__ __launch_bounds__(kCandThreads) void cand_kernel(
   uint8_t* wb = base + lay.wave_off + wave * lay.wave_bytes;
   float* gx = reinterpret_cast<float*>(wb);
   unsigned long long* gbest = reinterpret_cast<unsigned long long*>(gx + 64 * DP);
-  float* gR2 = reinterpret_cast<float*>(gbest + 64);
-  uint32_t* ga = reinterpret_cast<uint32_t*>(gR2 + 64);
+  uint32_t* gT = reinterpret_cast<uint32_t*>(gbest + 64);
+  uint32_t* ga = gT + 64;
   uint16_t* gitem = reinterpret_cast<uint16_t*>(ga + 64);
   uint32_t* lmax = reinterpret_cast<uint32_t*>(base + lay.scal_off);
   uint32_t* lcnt = lmax + 1;
@@ -282,13 +299,14 @@ __global__ __launch_bounds__(kCandThreads) void cand_kernel(
     for (int k = 0; k < DP; ++k) lcb[c * DP + k] = v[k];
     atomicMax(lmax, __float_as_uint(s));  // >= 0x7f800000: a non-finite codeword
   }
-  const uint32_t Ls = L | 1u;  // LDS row stride
-  const uint32_t* nbm = nbr + (uint64_t)m * K * L;
+  const uint32_t Lr = cand_row_len(L);  // stored row length
+  const uint32_t Ls = Lr | 1u;          // LDS row stride
+  const uint32_t* nbm = nbr + (uint64_t)m * K * Lr;
   if constexpr (kRowsInLds)
-    for (uint32_t j = t; j < K * L; j += blockDim.x) lnbr[(j / L) * Ls + j % L] = nbm[j];
+    for (uint32_t j = t; j < K * Lr; j += blockDim.x) lnbr[(j / Lr) * Ls + j % Lr] = nbm[j];
   const uint32_t* rows = kRowsInLds ? lnbr : nbm;  // row a at rows + a * rs
-  const uint32_t rs = kRowsInLds ? Ls : L;
-  for (uint32_t j = t; j < K * 8; j += blockDim.x) lsamp[j] = cand_sample(nbm + (j / 8) * L, L, j % 8);
+  const uint32_t rs = kRowsInLds ? Ls : Lr;
+  for (uint32_t j = t; j < K * 8; j += blockDim.x) lsamp[j] = cand_sample(nbm + (j / 8) * Lr, L, j % 8);
   if constexpr (ENCODE) {
     const uint8_t* am = anchors + (uint64_t)m * cells * kCandAnchors;
     for (uint32_t j = t; j < cells * kCandAnchors; j += blockDim.x) lanc[j] = am[j];
@@ -387,53 +405,60 @@ __global__ __launch_bounds__(kCandThreads) void cand_kernel(
             (uint32_t)i;
     }
     // Phase 2: the wave's items, laid out by an exclusive scan of the counts.
-    uint32_t incl = nit;
-#pragma unroll
-    for (int off = 1; off < kWave; off <<= 1) {
-      const uint32_t o = __shfl_up(incl, off, kWave);
-      if (lane >= (uint32_t)off) incl += o;
-    }
-    const uint32_t total = __shfl(incl, kWave - 1, kWave);  // <= 64 * 8
+    const uint32_t incl = wave_inclusive_sum(nit);
+    // At most 64 * 8; the bound also keeps a corrupted count inside the scratch.
+    const uint32_t total = min((uint32_t)__builtin_amdgcn_readlane((int)incl, kWave - 1), 64u * 8u);
     if (live) {
 #pragma unroll
       for (int k = 0; k < DP; ++k) gx[lane * DP + k] = k < D ? x[k] : 0.0f;
       gbest[lane] = cand_best_key(U2, a);
-      gR2[lane] = R2;
+      gT[lane] = cand_threshold(R2);
       ga[lane] = a;
     }
-    for (uint32_t q = 0, f = incl - nit; q < nit; ++q) gitem[f + q] = (uint16_t)(lane | (q << 6));
+    {
+      uint16_t* gi = gitem + (incl - nit);
+#pragma unroll
+      for (uint32_t q = 0; q < 8; ++q)
+        if (q < nit) gi[q] = (uint16_t)(lane | (q << 6));
+    }
     wave_lds_sync();
     // Phase 3: items, 64 at a time.  Entry j of the row is a candidate when
-    // j < L and its value is inside the vector's R2.
+    // it is inside the vector's R2 (key <= cand_threshold(R2)); entries past
+    // the L kept ones are kCandNoKey.  All 8 entries are evaluated without
+    // branches and the candidates' keys kept; a padding entry's codeword
+    // index (255) may lie past lcb when K < 256 and then reads other LDS
+    // data, which the candidate test discards.
     for (uint32_t w = lane; w < total; w += kWave) {
       const uint32_t it = gitem[w];
-      const uint32_t u = it & 63u, j0 = (it >> 6) * kCandItem;
-      const float r2 = gR2[u];
-      const uint32_t* row = rows + ga[u] * rs;
+      const uint32_t u = it & 63u, j0 = ((it >> 6) & 7u) * kCandItem;
+      const uint32_t T = gT[u];
+      const uint32_t* row = rows + ga[u] * rs + j0;
       uint32_t keys[kCandItem];
-      if (!kRowsInLds && (L & 7u) == 0) {  // whole items: two 16-byte loads
-        const uint4 k0 = *reinterpret_cast<const uint4*>(row + j0);
-        const uint4 k1 = *reinterpret_cast<const uint4*>(row + j0 + 4);
+      if constexpr (!kRowsInLds) {  // 16-byte aligned global rows: two 16-byte loads
+        const uint4 k0 = *reinterpret_cast<const uint4*>(row);
+        const uint4 k1 = *reinterpret_cast<const uint4*>(row + 4);
         keys[0] = k0.x; keys[1] = k0.y; keys[2] = k0.z; keys[3] = k0.w;
         keys[4] = k1.x; keys[5] = k1.y; keys[6] = k1.z; keys[7] = k1.w;
       } else {
 #pragma unroll
-        for (uint32_t k = 0; k < kCandItem; ++k) keys[k] = j0 + k < L ? row[j0 + k] : kCandNoKey;
+        for (uint32_t k = 0; k < kCandItem; ++k) keys[k] = row[k];
       }
       float xv[D];
       load_padded<D>(gx + u * DP, xv);
+      // A non-candidate's distance bits become all-ones: its key then lies
+      // above every real key (finite and infinite distances alike).
       unsigned long long best = ~0ull;
 #pragma unroll
       for (uint32_t k = 0; k < kCandItem; ++k) {
-        if (cand_is_candidate(keys[k], j0 + k, L, r2)) {
-          const uint32_t c = keys[k] & 0xFFu;
-          float cv[D];
-          load_padded<D>(lcb + c * DP, cv);
-          const unsigned long long key = cand_best_key(exact_l2sq<D>(xv, cv), c);
-          best = key < best ? key : best;
-        }
+        const uint32_t c = keys[k] & 0xFFu;
+        float cv[D];
+        load_padded<D>(lcb + c * DP, cv);
+        const uint32_t miss = 0u - (uint32_t)(keys[k] > T);  // all-ones off the candidates
+        const uint32_t db = cand_f2u(exact_l2sq<D>(xv, cv)) | miss;
+        const unsigned long long key = ((unsigned long long)db << 32) | c;
+        best = key < best ? key : best;
       }
-      if (best != ~0ull) atomicMin(&gbest[u], best);
+      if ((uint32_t)(best >> 32) != 0xFFFFFFFFu) atomicMin(&gbest[u], best);
     }
     wave_lds_sync();
     if (live) {

@@ -96,6 +96,19 @@ TAC_HD inline bool cand_is_candidate(uint32_t key, uint32_t j, uint32_t L, float
   return j < L && cand_key_value(key) <= R2;
 }
 
+// Stored row length: the L kept keys padded with kCandNoKey to the end of the
+// last item that the samples can select (8 items when L >= 56), so every item
+// reads 8 entries without a bound check.
+TAC_HD constexpr uint32_t cand_row_len(uint32_t L) {
+  return 8u * (L / 8u + 1u < 8u ? L / 8u + 1u : 8u);
+}
+
+// One unsigned compare for the candidate test: for 0 <= R2 < inf,
+// key <= cand_threshold(R2) exactly when cand_key_value(key) <= R2 (the
+// value part of a key is a multiple of 256 and non-negative floats order as
+// their bits); kCandNoKey is above every threshold.
+TAC_HD inline uint32_t cand_threshold(float R2) { return cand_f2u(R2) | 0xFFu; }
+
 // True when a codeword whose anchor bound is lo (cand_lower_bound of its
 // reference distance to c_a) cannot tie or beat c_a for a vector with
 // U2 = ref(x, c_a): then ref(x, c) > U2.  k-means++ uses it to keep a weight

@@ -564,7 +564,7 @@ int train_core(DeviceState &ds, hipStream_t s, const float *d_x, uint64_t n, uin
   const uint32_t Lc = K >= 2 ? std::min<uint32_t>(kCandList, K - 1) : 0;
   const bool cand = !(full_env && full_env[0] == '1') && K >= 2 && K <= kCandMaxK &&
                     cand_lds(K, Lc, DP).total <= kCandLdsMax && max_iters > 1;
-  if (cand && ((st = ensure(ds, ds.cand_nbr, (size_t)M * K * Lc * sizeof(uint32_t))) ||
+  if (cand && ((st = ensure(ds, ds.cand_nbr, (size_t)M * K * cand_row_len(Lc) * sizeof(uint32_t))) ||
                (st = ensure(ds, ds.cand_defer, (size_t)2 * M * n * sizeof(uint32_t))) ||
                (st = ensure(ds, ds.cand_count, (size_t)M * sizeof(uint32_t)))))
     return st;
@@ -741,7 +741,7 @@ int encode_core(DeviceState &ds, hipStream_t s, const float *d_x, uint64_t n, ui
   const bool cand = !(full_env && full_env[0] == '1') && K >= 2 && K <= kCandMaxK &&
                     n >= 16384 && n <= 0xFFFFFFFFull;
   if (cand) {
-    if ((st = ensure(ds, ds.cand_nbr, (size_t)M * K * L * sizeof(uint32_t))) ||
+    if ((st = ensure(ds, ds.cand_nbr, (size_t)M * K * cand_row_len(L) * sizeof(uint32_t))) ||
         (st = ensure(ds, ds.cand_defer, (size_t)2 * M * n * sizeof(uint32_t))) ||
         (st = ensure(ds, ds.cand_count, (size_t)M * sizeof(uint32_t))) ||
         (st = ensure(ds, ds.cand_anchor, (size_t)M * kCandCells * kCandAnchors)) ||

@@ -46,6 +46,7 @@ static float fold(const float* x, const float* c, int D) {
 struct Counts {
   long checks = 0, deferred = 0, wrong = 0, planted_radius = 0, planted_ties = 0;
   long skip_checks = 0, skips = 0, skip_wrong = 0;
+  long thr_checks = 0, thr_wrong = 0, row_overrun = 0;
 };
 
 static void run_case(const std::vector<float>& cb, int K, int D, const std::vector<float>& xs,
@@ -97,6 +98,16 @@ static void run_case(const std::vector<float>& cb, int K, int D, const std::vect
       const float R2 = cand_radius(U2, g);
       bool deferred = false;
       const uint32_t nit = cand_items(sv, R2, cand_key_value(row[L - 1]), row_complete, &deferred);
+      // The kernels test a key with one unsigned compare against
+      // cand_threshold(R2), and read whole items from rows padded to
+      // cand_row_len(L) with kCandNoKey.
+      const uint32_t T = cand_threshold(R2);
+      for (uint32_t j = 0; j <= L; ++j) {
+        const uint32_t k = j < L ? row[j] : kCandNoKey;
+        ++ct.thr_checks;
+        if ((k <= T) != (j < L && cand_key_value(k) <= R2)) ++ct.thr_wrong;
+      }
+      if (nit * kCandItem > cand_row_len(L)) ++ct.row_overrun;
       if (deferred) {
         ++ct.deferred;
         continue;
@@ -177,8 +188,10 @@ int main() {
               ct.checks, ct.deferred, ct.wrong, ct.planted_radius, ct.planted_ties);
   std::printf("kmeans++ skip: %ld checks, %ld skips, %ld skip_wrong\n", ct.skip_checks, ct.skips,
               ct.skip_wrong);
+  std::printf("threshold: %ld checks, %ld thr_wrong; row_overrun %ld\n", ct.thr_checks,
+              ct.thr_wrong, ct.row_overrun);
   return ct.wrong == 0 && ct.skip_wrong == 0 && ct.skips > 0 && ct.planted_radius > 0 &&
-                 ct.planted_ties > 0
+                 ct.planted_ties > 0 && ct.thr_wrong == 0 && ct.row_overrun == 0
              ? 0
              : 1;
 }
