@@ -26,7 +26,7 @@
 //
 // Neighbour tables.  After every update, nbr_build_kernel sorts, for each
 // codeword a, the other codewords by lo(a, c) and keeps the first L of them
-// as one u32 key each: the bits of lo with the low 8 bits replaced by c
+// as one u32 key each: the bits of lo with the low 12 bits replaced by c << 4
 // (K <= 256).  Clearing low bits of a non-negative float lowers it, so the
 // key's value part stays a lower bound, and sorted keys put S \ {a} in a
 // prefix of the row.  If the whole kept row lies inside R2 while codewords
@@ -70,8 +70,8 @@ constexpr uint32_t kCandAnchors = 2;   // anchor codewords per cell
 //   lsamp [K][8] u32: the value bits
 //   of row entries 0, 7, 15, ..., 55 (all-ones past the row) | encode only:
 //   lanc [cells][2] u8 anchors, lgrid [2][8] f32 (cell origin, cells per unit) |
-//   per wave: gx [64][DP] f32, gbest [64] u64, gT [64] u32 (cand_threshold
-//   of R2), ga [64] u32,
+//   per wave: gx [64][DP] f32, gbest [64] u64, ga [64] u32 (the anchor's
+//   row offset),
 //   gitem [64 * 8] u16 (lane | item << 6) | lmax, lcnt u32
 struct CandLds {
   uint32_t nbr_off, samp_off, anc_off, grid_off, wave_off, wave_bytes, scal_off, total;
@@ -85,7 +85,7 @@ __host__ __device__ inline CandLds cand_lds(uint32_t K, uint32_t L, uint32_t DP,
   s.anc_off = s.samp_off + K * 8u * 4u;
   s.grid_off = cand_up16(s.anc_off + cells * kCandAnchors);
   s.wave_off = s.grid_off + (cells ? 64u : 0u);
-  s.wave_bytes = 64u * (DP * 4u + 8u + 4u + 4u) + 64u * 8u * 2u;
+  s.wave_bytes = 64u * (DP * 4u + 8u + 4u) + 64u * 8u * 2u;
   s.scal_off = s.wave_off + (uint32_t)kCandWaves * s.wave_bytes;
   s.total = s.scal_off + 16u;
   return s;
@@ -104,7 +104,7 @@ __host__ __device__ inline uint32_t cand_grid_side(uint32_t D) {
 
 // One wave per (codeword a, subspace m): lo(a, c) for every c != a, a
 // bitonic sort of the 256 keys in LDS, the first L written to
-// nbr[m][a][0 .. L) and kCandNoKey to the rest of the stored row
+// nbr[m][a][0 .. L) and cand_pad_key(a) to the rest of the stored row
 // nbr[m][a][L .. cand_row_len(L)).  Block (0, m) also clears the subspace's deferred
 // count for the assignment that follows on the same stream.
 template <int D>
@@ -150,7 +150,7 @@ __global__ __launch_bounds__(kWave) void nbr_build_kernel(const float* __restric
   }
   const uint32_t Lr = cand_row_len(L);
   uint32_t* row = nbr + ((uint64_t)m * K + a) * Lr;
-  for (uint32_t j = lane; j < Lr; j += kWave) row[j] = j < L ? keys[j] : kCandNoKey;
+  for (uint32_t j = lane; j < Lr; j += kWave) row[j] = j < L ? keys[j] : cand_pad_key(a);
 }
 
 // Encode anchors of subspace m = blockIdx.y: the bounding box of the
@@ -276,8 +276,7 @@ __global__ __launch_bounds__(kCandThreads) void cand_kernel(
   uint8_t* wb = base + lay.wave_off + wave * lay.wave_bytes;
   float* gx = reinterpret_cast<float*>(wb);
   unsigned long long* gbest = reinterpret_cast<unsigned long long*>(gx + 64 * DP);
-  uint32_t* gT = reinterpret_cast<uint32_t*>(gbest + 64);
-  uint32_t* ga = gT + 64;
+  uint32_t* ga = reinterpret_cast<uint32_t*>(gbest + 64);
   uint16_t* gitem = reinterpret_cast<uint16_t*>(ga + 64);
   uint32_t* lmax = reinterpret_cast<uint32_t*>(base + lay.scal_off);
   uint32_t* lcnt = lmax + 1;
@@ -412,8 +411,7 @@ __global__ __launch_bounds__(kCandThreads) void cand_kernel(
 #pragma unroll
       for (int k = 0; k < DP; ++k) gx[lane * DP + k] = k < D ? x[k] : 0.0f;
       gbest[lane] = cand_best_key(U2, a);
-      gT[lane] = cand_threshold(R2);
-      ga[lane] = a;
+      ga[lane] = a * rs;  // the anchor's row offset
     }
     {
       uint16_t* gi = gitem + (incl - nit);
@@ -422,17 +420,15 @@ __global__ __launch_bounds__(kCandThreads) void cand_kernel(
         if (q < nit) gi[q] = (uint16_t)(lane | (q << 6));
     }
     wave_lds_sync();
-    // Phase 3: items, 64 at a time.  Entry j of the row is a candidate when
-    // it is inside the vector's R2 (key <= cand_threshold(R2)); entries past
-    // the L kept ones are kCandNoKey.  All 8 entries are evaluated without
-    // branches and the candidates' keys kept; a padding entry's codeword
-    // index (255) may lie past lcb when K < 256 and then reads other LDS
-    // data, which the candidate test discards.
+    // Phase 3: items, 64 at a time.  All 8 entries of an item are evaluated
+    // without branches and folded into the vector's key: the items cover the
+    // candidate set, and every entry (a kept neighbour or the anchor as
+    // padding) names a real codeword, so the extra (distance, index) keys
+    // leave the minimum unchanged.
     for (uint32_t w = lane; w < total; w += kWave) {
       const uint32_t it = gitem[w];
       const uint32_t u = it & 63u, j0 = ((it >> 6) & 7u) * kCandItem;
-      const uint32_t T = gT[u];
-      const uint32_t* row = rows + ga[u] * rs + j0;
+      const uint32_t* row = rows + ga[u] + j0;
       uint32_t keys[kCandItem];
       if constexpr (!kRowsInLds) {  // 16-byte aligned global rows: two 16-byte loads
         const uint4 k0 = *reinterpret_cast<const uint4*>(row);
@@ -445,28 +441,25 @@ __global__ __launch_bounds__(kCandThreads) void cand_kernel(
       }
       float xv[D];
       load_padded<D>(gx + u * DP, xv);
-      // A non-candidate's distance bits become all-ones: its key then lies
-      // above every real key (finite and infinite distances alike).
       unsigned long long best = ~0ull;
 #pragma unroll
       for (uint32_t k = 0; k < kCandItem; ++k) {
-        const uint32_t c = keys[k] & 0xFFu;
+        const uint32_t c16 = keys[k] & 0xFF0u;  // c << 4
         float cv[D];
-        load_padded<D>(lcb + c * DP, cv);
-        const uint32_t miss = 0u - (uint32_t)(keys[k] > T);  // all-ones off the candidates
-        const uint32_t db = cand_f2u(exact_l2sq<D>(xv, cv)) | miss;
-        const unsigned long long key = ((unsigned long long)db << 32) | c;
+        load_padded<D>(lcb + (c16 >> 4) * DP, cv);
+        const unsigned long long key =
+            ((unsigned long long)cand_f2u(exact_l2sq<D>(xv, cv)) << 32) | c16;
         best = key < best ? key : best;
       }
-      if ((uint32_t)(best >> 32) != 0xFFFFFFFFu) atomicMin(&gbest[u], best);
+      atomicMin(&gbest[u], best);
     }
     wave_lds_sync();
     if (live) {
       const unsigned long long k = gbest[lane];
       if constexpr (ENCODE) {
-        out[i * M + m] = (CodeT)(k & 0xFFFFu);
+        out[i * M + m] = (CodeT)cand_best_code(k);
       } else {
-        cm[i] = (uint16_t)(k & 0xFFFFu);
+        cm[i] = (uint16_t)cand_best_code(k);
         em[i] = __uint_as_float((uint32_t)(k >> 32));
       }
     }

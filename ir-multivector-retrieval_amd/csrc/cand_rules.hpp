@@ -7,7 +7,7 @@
 // (src/util/vec.zig:109-175: D squares and D-1 adds, separately rounded):
 //   * R2 = cand_radius(U2) >= 4 (U2 + eta) / (1 - g), g = gamma_{D+2};
 //   * a neighbour key stores cand_lower_bound(ref(c_a, c)) <= ||c_a - c||^2
-//     in its value bits and c in its low 8 bits;
+//     in its value bits and c << 4 in its low 12 bits;
 //   * every codeword that ties or beats c_a under ref() has a key value
 //     <= R2, so the reference's first-index argmin lies in
 //     {a} + {c : value(key(a, c)) <= R2}.
@@ -62,12 +62,21 @@ TAC_HD inline float cand_lower_bound(float s, float g) {
   return lo > 0.0f ? lo : 0.0f;
 }
 
-// Key of neighbour c: the bound's bits with the low 8 bits replaced by c.
-// Clearing low bits of a non-negative float lowers it, so the value part
-// stays a lower bound, and sorting keys sorts by bound, then by id.
-TAC_HD inline uint32_t cand_key(float lo, uint32_t c) { return (cand_f2u(lo) & 0xFFFFFF00u) | c; }
-TAC_HD inline float cand_key_value(uint32_t key) { return cand_u2f(key & 0xFFFFFF00u); }
+// Key of neighbour c: the bound's bits with the low 12 bits replaced by
+// c << 4, which is also the byte offset of codeword c in a table of 16-byte
+// codewords.  Clearing low bits of a non-negative float lowers it, so the
+// value part stays a lower bound, and sorting keys sorts by bound, then by id.
+constexpr uint32_t kCandValueMask = 0xFFFFF000u;
+TAC_HD inline uint32_t cand_key(float lo, uint32_t c) {
+  return (cand_f2u(lo) & kCandValueMask) | (c << 4);
+}
+TAC_HD inline float cand_key_value(uint32_t key) { return cand_u2f(key & kCandValueMask); }
+TAC_HD inline uint32_t cand_key_code(uint32_t key) { return (key >> 4) & 0xFFu; }
 constexpr uint32_t kCandNoKey = 0xFFFFFFFFu;  // value part is NaN: never inside R2
+// Padding entry of anchor a's stored row: its value part is NaN, so no
+// sample counts it, and its code is a, a real codeword, so an item that
+// reads it evaluates a valid (distance, index) key.
+TAC_HD inline uint32_t cand_pad_key(uint32_t a) { return kCandValueMask | (a << 4); }
 
 // Row position of sample q: 0, 7, 15, ..., 55.  With b samples inside R2,
 // every row entry inside R2 lies in [0, 8b): item q covers [8q, 8q + 8).
@@ -76,7 +85,7 @@ TAC_HD inline uint32_t cand_sample_pos(uint32_t q) { return q ? 8u * q - 1u : 0u
 // Value bits of sample q of a row of L kept keys (all-ones past the row).
 TAC_HD inline uint32_t cand_sample(const uint32_t* row, uint32_t L, uint32_t q) {
   const uint32_t pos = cand_sample_pos(q);
-  return pos < L ? row[pos] & 0xFFFFFF00u : kCandNoKey;
+  return pos < L ? row[pos] & kCandValueMask : kCandNoKey;
 }
 
 // Number of kCandItem-candidate items a vector needs from its anchor's row,
@@ -96,18 +105,12 @@ TAC_HD inline bool cand_is_candidate(uint32_t key, uint32_t j, uint32_t L, float
   return j < L && cand_key_value(key) <= R2;
 }
 
-// Stored row length: the L kept keys padded with kCandNoKey to the end of the
-// last item that the samples can select (8 items when L >= 56), so every item
-// reads 8 entries without a bound check.
+// Stored row length: the L kept keys padded with cand_pad_key to the end of
+// the last item that the samples can select (8 items when L >= 56), so every
+// item reads 8 entries without a bound check.
 TAC_HD constexpr uint32_t cand_row_len(uint32_t L) {
   return 8u * (L / 8u + 1u < 8u ? L / 8u + 1u : 8u);
 }
-
-// One unsigned compare for the candidate test: for 0 <= R2 < inf,
-// key <= cand_threshold(R2) exactly when cand_key_value(key) <= R2 (the
-// value part of a key is a multiple of 256 and non-negative floats order as
-// their bits); kCandNoKey is above every threshold.
-TAC_HD inline uint32_t cand_threshold(float R2) { return cand_f2u(R2) | 0xFFu; }
 
 // True when a codeword whose anchor bound is lo (cand_lower_bound of its
 // reference distance to c_a) cannot tie or beat c_a for a vector with
@@ -117,10 +120,13 @@ TAC_HD inline bool cand_cannot_beat(float lo, float U2, float g) {
   return cand_tame(U2) && lo > cand_radius(U2, g);
 }
 
-// Lexicographic (distance bits, index) key: its minimum is the first-index
-// argmin among non-negative distances.
+// Lexicographic (distance bits, index) key, the index stored as c << 4 as
+// in the neighbour keys: its minimum is the first-index argmin among
+// non-negative distances.  The minimum over any set of codewords that holds
+// the candidate set is the same, so evaluating extra codewords is harmless.
 TAC_HD inline uint64_t cand_best_key(float d, uint32_t c) {
-  return ((uint64_t)cand_f2u(d) << 32) | c;
+  return ((uint64_t)cand_f2u(d) << 32) | (c << 4);
 }
+TAC_HD inline uint32_t cand_best_code(uint64_t key) { return (uint32_t)key >> 4; }
 
 }  // namespace tacgpu

@@ -6,7 +6,8 @@
 // reference's first-index argmin (src/util/vec.zig:271-283 over the
 // unfused fold of vec.zig:109-175), and the lexicographic (distance bits,
 // index) minimum over it must equal that argmin and its distance bit for
-// bit.  Two planted mistakes must fail: a radius of rho instead of 2 rho, and
+// bit.  As the kernels do, every entry of every selected item is evaluated,
+// candidate or not, with rows padded to cand_row_len(L) by cand_pad_key.  Two planted mistakes must fail: a radius of rho instead of 2 rho, and
 // a tie rule that ignores the codeword index.  The k-means++ skip
 // (cand_cannot_beat) is checked directly: whenever it holds for a codeword,
 // that codeword's reference distance is strictly greater than the anchor's.
@@ -46,7 +47,7 @@ static float fold(const float* x, const float* c, int D) {
 struct Counts {
   long checks = 0, deferred = 0, wrong = 0, planted_radius = 0, planted_ties = 0;
   long skip_checks = 0, skips = 0, skip_wrong = 0;
-  long thr_checks = 0, thr_wrong = 0, row_overrun = 0;
+  long row_overrun = 0;
 };
 
 static void run_case(const std::vector<float>& cb, int K, int D, const std::vector<float>& xs,
@@ -54,14 +55,15 @@ static void run_case(const std::vector<float>& cb, int K, int D, const std::vect
   const float g = cand_gamma(D);
   const uint32_t L = std::min<uint32_t>(kCandList, (uint32_t)K - 1);
   const bool row_complete = L + 1 >= (uint32_t)K;
-  std::vector<uint32_t> rows((size_t)K * L), samples((size_t)K * 8);
+  const uint32_t Lr = cand_row_len(L);
+  std::vector<uint32_t> rows((size_t)K * Lr), samples((size_t)K * 8);
   for (int a = 0; a < K; ++a) {
     std::vector<uint32_t> keys;
     for (int c = 0; c < K; ++c)
       if (c != a) keys.push_back(cand_key(cand_lower_bound(fold(&cb[a * D], &cb[c * D], D), g), c));
     std::sort(keys.begin(), keys.end());
-    for (uint32_t j = 0; j < L; ++j) rows[(size_t)a * L + j] = keys[j];
-    for (uint32_t q = 0; q < 8; ++q) samples[(size_t)a * 8 + q] = cand_sample(&rows[(size_t)a * L], L, q);
+    for (uint32_t j = 0; j < Lr; ++j) rows[(size_t)a * Lr + j] = j < L ? keys[j] : cand_pad_key(a);
+    for (uint32_t q = 0; q < 8; ++q) samples[(size_t)a * 8 + q] = cand_sample(&rows[(size_t)a * Lr], L, q);
   }
   for (int i = 0; i < n; ++i) {
     const float* x = &xs[(size_t)i * D];
@@ -76,7 +78,7 @@ static void run_case(const std::vector<float>& cb, int K, int D, const std::vect
       }
     }
     for (int rep = 0; rep < 3; ++rep) {
-      const int a = rep == 0 ? (int)(next_u64() % K) : rep == 1 ? bi : (int)(rows[(size_t)bi * L] & 0xFF);
+      const int a = rep == 0 ? (int)(next_u64() % K) : rep == 1 ? bi : (int)cand_key_code(rows[(size_t)bi * Lr]);
       const float U2 = fold(x, &cb[a * D], D);
       ++ct.checks;
       if (rep == 0)  // the k-means++ skip against every other codeword
@@ -92,55 +94,45 @@ static void run_case(const std::vector<float>& cb, int K, int D, const std::vect
         ++ct.deferred;
         continue;
       }
-      const uint32_t* row = &rows[(size_t)a * L];
+      const uint32_t* row = &rows[(size_t)a * Lr];
       uint32_t sv[8];
       for (int q = 0; q < 8; ++q) sv[q] = samples[(size_t)a * 8 + q];
       const float R2 = cand_radius(U2, g);
       bool deferred = false;
       const uint32_t nit = cand_items(sv, R2, cand_key_value(row[L - 1]), row_complete, &deferred);
-      // The kernels test a key with one unsigned compare against
-      // cand_threshold(R2), and read whole items from rows padded to
-      // cand_row_len(L) with kCandNoKey.
-      const uint32_t T = cand_threshold(R2);
-      for (uint32_t j = 0; j <= L; ++j) {
-        const uint32_t k = j < L ? row[j] : kCandNoKey;
-        ++ct.thr_checks;
-        if ((k <= T) != (j < L && cand_key_value(k) <= R2)) ++ct.thr_wrong;
-      }
-      if (nit * kCandItem > cand_row_len(L)) ++ct.row_overrun;
+      if (nit * kCandItem > Lr) ++ct.row_overrun;  // items must stay inside the stored row
       if (deferred) {
         ++ct.deferred;
         continue;
       }
+      // Every entry of every selected item, candidate or not (the kernels).
       uint64_t key = cand_best_key(U2, a);
-      for (uint32_t j = 0; j < nit * kCandItem; ++j) {
-        const uint32_t k = j < L ? row[j] : kCandNoKey;
-        if (!cand_is_candidate(k, j, L, R2)) continue;
-        const uint32_t c = k & 0xFFu;
+      for (uint32_t j = 0; j < nit * kCandItem && j < Lr; ++j) {
+        const uint32_t c = cand_key_code(row[j]);
         const uint64_t kk = cand_best_key(fold(x, &cb[c * D], D), c);
         key = kk < key ? kk : key;
       }
-      if ((int)(key & 0xFFFFFFFFu) != bi || (uint32_t)(key >> 32) != cand_f2u(best)) ++ct.wrong;
+      if ((int)cand_best_code(key) != bi || (uint32_t)(key >> 32) != cand_f2u(best)) ++ct.wrong;
       // Planted: radius rho^2 instead of 4 rho^2.
       {
         const float R2w = U2;
         uint64_t kw = cand_best_key(U2, a);
         for (uint32_t j = 0; j < L; ++j)
           if (cand_key_value(row[j]) <= R2w) {
-            const uint32_t c = row[j] & 0xFFu;
+            const uint32_t c = cand_key_code(row[j]);
             const uint64_t kk = cand_best_key(fold(x, &cb[c * D], D), c);
             kw = kk < kw ? kk : kw;
           }
-        if ((int)(kw & 0xFFFFFFFFu) != bi) ++ct.planted_radius;
+        if ((int)cand_best_code(kw) != bi) ++ct.planted_radius;
       }
       // Planted: ties resolved by scan order (row order) instead of the index.
       {
         float bd = U2;
         uint32_t bc = a;
         for (uint32_t j = 0; j < nit * kCandItem; ++j) {
-          const uint32_t k = j < L ? row[j] : kCandNoKey;
+          const uint32_t k = row[j];
           if (!cand_is_candidate(k, j, L, R2)) continue;
-          const uint32_t c = k & 0xFFu;
+          const uint32_t c = cand_key_code(k);
           const float d = fold(x, &cb[c * D], D);
           if (d < bd) {
             bd = d;
@@ -188,10 +180,9 @@ int main() {
               ct.checks, ct.deferred, ct.wrong, ct.planted_radius, ct.planted_ties);
   std::printf("kmeans++ skip: %ld checks, %ld skips, %ld skip_wrong\n", ct.skip_checks, ct.skips,
               ct.skip_wrong);
-  std::printf("threshold: %ld checks, %ld thr_wrong; row_overrun %ld\n", ct.thr_checks,
-              ct.thr_wrong, ct.row_overrun);
+  std::printf("items: row_overrun %ld\n", ct.row_overrun);
   return ct.wrong == 0 && ct.skip_wrong == 0 && ct.skips > 0 && ct.planted_radius > 0 &&
-                 ct.planted_ties > 0 && ct.thr_wrong == 0 && ct.row_overrun == 0
+                 ct.planted_ties > 0 && ct.row_overrun == 0
              ? 0
              : 1;
 }
