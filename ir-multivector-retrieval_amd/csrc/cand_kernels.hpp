@@ -52,12 +52,10 @@
 namespace tacgpu {
 
 constexpr int kCandThreads = 1024;      // threads per candidate block
-// Training stages the neighbour rows in LDS (one block per CU).  Encode, which
-// also stages its anchor table, reads the rows from global memory (1 MB over
-// all subspaces, L2-resident) so that two blocks fit in a CU's LDS; the row
-// samples stay in LDS either way.
-template <bool ENCODE>
-constexpr bool cand_rows_in_lds() { return !ENCODE; }
+// The neighbour rows stay in global memory (64 KB per subspace at K = 256,
+// L2-resident) and are read as two 16-byte loads per item: staged in LDS they
+// took 66 KB of it, held the kernel to one block per CU and added bank
+// conflicts to the codeword gathers.  The row samples are staged in LDS.
 constexpr int kCandWaves = kCandThreads / kWave;
 constexpr uint32_t kCandLdsMax = 160 * 1024;
 
@@ -65,23 +63,19 @@ constexpr uint32_t kCandCells = 6561;  // grid cells per subspace (encode anchor
 constexpr uint32_t kCandAnchors = 2;   // anchor codewords per cell
 
 // LDS layout of cand_kernel, shared by the host launcher:
-//   lcb [K][DP] f32 | lnbr [K][Lr|1] u32, Lr = cand_row_len(L) (an odd row
-//   stride puts the rows of different anchors in different banks) |
-//   lsamp [K][8] u32: the value bits
-//   of row entries 0, 7, 15, ..., 55 (all-ones past the row) | encode only:
+//   lcb [K][DP] f32 | lsamp [K][8] u32: the value bits of row entries
+//   0, 7, 15, ..., 55 (all-ones past the row) | encode only:
 //   lanc [cells][2] u8 anchors, lgrid [2][8] f32 (cell origin, cells per unit) |
 //   per wave: gx [64][DP] f32, gbest [64] u64, ga [64] u32 (the anchor's
 //   row offset),
 //   gitem [64 * 8] u16 (lane | item << 6) | lmax, lcnt u32
 struct CandLds {
-  uint32_t nbr_off, samp_off, anc_off, grid_off, wave_off, wave_bytes, scal_off, total;
+  uint32_t samp_off, anc_off, grid_off, wave_off, wave_bytes, scal_off, total;
 };
 __host__ __device__ inline uint32_t cand_up16(uint32_t b) { return (b + 15u) & ~15u; }
-__host__ __device__ inline CandLds cand_lds(uint32_t K, uint32_t L, uint32_t DP,
-                                            uint32_t cells = 0, bool rows_in_lds = true) {
+__host__ __device__ inline CandLds cand_lds(uint32_t K, uint32_t DP, uint32_t cells = 0) {
   CandLds s;
-  s.nbr_off = cand_up16(K * DP * 4u);
-  s.samp_off = cand_up16(s.nbr_off + (rows_in_lds ? K * (cand_row_len(L) | 1u) * 4u : 0u));
+  s.samp_off = cand_up16(K * DP * 4u);
   s.anc_off = s.samp_off + K * 8u * 4u;
   s.grid_off = cand_up16(s.anc_off + cells * kCandAnchors);
   s.wave_off = s.grid_off + (cells ? 64u : 0u);
@@ -264,11 +258,9 @@ __global__ __launch_bounds__(kCandThreads) void cand_kernel(
     m = blockIdx.y;
     if (done[m]) return;
   }
-  constexpr bool kRowsInLds = cand_rows_in_lds<ENCODE>();
-  const CandLds lay = cand_lds(K, L, DP, ENCODE ? cells : 0u, kRowsInLds);
+  const CandLds lay = cand_lds(K, DP, ENCODE ? cells : 0u);
   uint8_t* base = reinterpret_cast<uint8_t*>(lds);
   float* lcb = lds;
-  uint32_t* lnbr = reinterpret_cast<uint32_t*>(base + lay.nbr_off);
   uint32_t* lsamp = reinterpret_cast<uint32_t*>(base + lay.samp_off);
   uint8_t* lanc = base + lay.anc_off;
   float* lgrid = reinterpret_cast<float*>(base + lay.grid_off);
@@ -299,12 +291,9 @@ __global__ __launch_bounds__(kCandThreads) void cand_kernel(
     atomicMax(lmax, __float_as_uint(s));  // >= 0x7f800000: a non-finite codeword
   }
   const uint32_t Lr = cand_row_len(L);  // stored row length
-  const uint32_t Ls = Lr | 1u;          // LDS row stride
   const uint32_t* nbm = nbr + (uint64_t)m * K * Lr;
-  if constexpr (kRowsInLds)
-    for (uint32_t j = t; j < K * Lr; j += blockDim.x) lnbr[(j / Lr) * Ls + j % Lr] = nbm[j];
-  const uint32_t* rows = kRowsInLds ? lnbr : nbm;  // row a at rows + a * rs
-  const uint32_t rs = kRowsInLds ? Ls : Lr;
+  const uint32_t* rows = nbm;  // row a at rows + a * rs
+  const uint32_t rs = Lr;
   for (uint32_t j = t; j < K * 8; j += blockDim.x) lsamp[j] = cand_sample(nbm + (j / 8) * Lr, L, j % 8);
   if constexpr (ENCODE) {
     const uint8_t* am = anchors + (uint64_t)m * cells * kCandAnchors;
@@ -430,14 +419,11 @@ __global__ __launch_bounds__(kCandThreads) void cand_kernel(
       const uint32_t u = it & 63u, j0 = ((it >> 6) & 7u) * kCandItem;
       const uint32_t* row = rows + ga[u] + j0;
       uint32_t keys[kCandItem];
-      if constexpr (!kRowsInLds) {  // 16-byte aligned global rows: two 16-byte loads
+      {  // rows of whole items, 32-byte aligned: two 16-byte loads
         const uint4 k0 = *reinterpret_cast<const uint4*>(row);
         const uint4 k1 = *reinterpret_cast<const uint4*>(row + 4);
         keys[0] = k0.x; keys[1] = k0.y; keys[2] = k0.z; keys[3] = k0.w;
         keys[4] = k1.x; keys[5] = k1.y; keys[6] = k1.z; keys[7] = k1.w;
-      } else {
-#pragma unroll
-        for (uint32_t k = 0; k < kCandItem; ++k) keys[k] = row[k];
       }
       float xv[D];
       load_padded<D>(gx + u * DP, xv);

@@ -253,7 +253,7 @@ int validate_pq(uint64_t n, uint32_t dim, uint32_t m, uint32_t ksub) {
 
 // Raises a kernel's dynamic-LDS limit above the 64 KB default once per
 // function, to the largest layout it can be launched with (the candidate
-// kernels at K = 256, L = 64, and the given anchor-table size).
+// kernels at K = 256 and the given anchor-table size).
 int raise_lds(const void *fn, uint32_t bytes, uint32_t cells) {
   if (bytes <= 65536) return TAC_OK;
   static std::mutex mu;
@@ -261,7 +261,7 @@ int raise_lds(const void *fn, uint32_t bytes, uint32_t cells) {
   std::lock_guard<std::mutex> g(mu);
   for (const void *f : raised)
     if (f == fn) return TAC_OK;
-  const uint32_t most = cand_lds(kCandMaxK, kCandList, 8, cells).total;
+  const uint32_t most = cand_lds(kCandMaxK, 8, cells).total;
   const hipError_t err = hipFuncSetAttribute(fn, hipFuncAttributeMaxDynamicSharedMemorySize,
                                             (int)(most > bytes ? most : bytes));
   if (err != hipSuccess) return hip_status("hipFuncSetAttribute(candidate kernel)", err);
@@ -298,7 +298,7 @@ struct Launch {
                          const uint32_t *done, uint64_t n, uint32_t M, uint32_t K, uint32_t L,
                          unsigned long long *rescans, hipStream_t s) {
     nbr_build_kernel<D><<<dim3(K, M), kWave, 0, s>>>(cb, nbr, defer_count, done, K, L);
-    const CandLds lay = cand_lds(K, L, Pad<D>::value);
+    const CandLds lay = cand_lds(K, Pad<D>::value);
     if (int st = raise_lds((const void *)cand_kernel<D, false, uint16_t>, lay.total, 0)) return st;
     // About 1,024 blocks over all subspaces; a chunk is whole groups of
     // kCandThreads vectors.
@@ -336,7 +336,7 @@ struct Launch {
     nbr_build_kernel<D><<<dim3(K, M), kWave, 0, s>>>(cb, nbr, defer_count, nullptr, K, L);
     grid_build_kernel<D><<<dim3((cells + kBlock - 1) / kBlock, M), kBlock, 0, s>>>(
         cb, anchors, grid, K, G, cells);
-    const CandLds lay = cand_lds(K, L, Pad<D>::value, cells, cand_rows_in_lds<true>());
+    const CandLds lay = cand_lds(K, Pad<D>::value, cells);
     if (int st = raise_lds((const void *)cand_kernel<D, true, CodeT>, lay.total, cells))
       return st;
     // Chunks of 8,192 rows; the M blocks of a chunk run on one XCD, so a row
@@ -563,7 +563,7 @@ int train_core(DeviceState &ds, hipStream_t s, const float *d_x, uint64_t n, uin
   const char *full_env = getenv("TAC_GPU_FULL_SEARCH");
   const uint32_t Lc = K >= 2 ? std::min<uint32_t>(kCandList, K - 1) : 0;
   const bool cand = !(full_env && full_env[0] == '1') && K >= 2 && K <= kCandMaxK &&
-                    cand_lds(K, Lc, DP).total <= kCandLdsMax && max_iters > 1;
+                    cand_lds(K, DP).total <= kCandLdsMax && max_iters > 1;
   if (cand && ((st = ensure(ds, ds.cand_nbr, (size_t)M * K * cand_row_len(Lc) * sizeof(uint32_t))) ||
                (st = ensure(ds, ds.cand_defer, (size_t)2 * M * n * sizeof(uint32_t))) ||
                (st = ensure(ds, ds.cand_count, (size_t)M * sizeof(uint32_t)))))
