@@ -353,10 +353,11 @@ def main() -> int:
     # which starts from the previous codes (neighbour rows, candidate
     # assignment, full search of the deferred vectors).  Algorithmic FLOP per
     # launch = n * 2 * dim * ksub, the reference's exhaustive search of one
-    # iteration over all m subspaces; the candidate path evaluates about 9
+    # iteration over all m subspaces; the candidate path evaluates about 13
     # codewords of 256 per vector-subspace, so the achieved figure is the
-    # exhaustive work delivered per second.  Iteration 0 runs the full search
-    # (assign_kernel) and is reported on its own.
+    # exhaustive work delivered per second, and can pass the VALU peak; the
+    # stage's measured HBM traffic rate is reported beside it.  Iteration 0
+    # runs the full search (assign_kernel) and is reported on its own.
     assign_flop = n * 2 * dim * ksub
     cand_avg_ms = prof.cand_assign_ms / max(prof.cand_assign_iters, 1)
     full_iters = prof.assign_launches - prof.cand_assign_iters
@@ -379,6 +380,11 @@ def main() -> int:
                 traffic[k] = int(v["read_bytes"]) + int(v["write_bytes"])
         except (ValueError, OSError, KeyError, TypeError):
             traffic = {}
+
+    cand_traffic = sum(traffic.get(k, 0) for k in (
+        "nbr_build_kernel<4>", "cand_kernel<4, false, unsigned short>",
+        "assign_list_kernel<4, 1>")) or None
+    cand_hbm_gbs = None if cand_traffic is None else cand_traffic / (assign_avg_ms * 1e-3) / 1e9
 
     # Full-size parity: 2 GPU iterations vs the oracle's 2 iterations.
     gpu_cb2 = None
@@ -418,11 +424,15 @@ def main() -> int:
             "bound": "mfma", "engine": "VALU fp32 (exact unfused distance + argmin)",
             "achieved": round(assign_tflops, 3), "peak": PEAK_FP32_TFLOPS, "unit": "TFLOP/s",
             "frac": round(assign_tflops / PEAK_FP32_TFLOPS, 4),
-            "traffic": (sum(traffic.get(k, 0) for k in (
-                "nbr_build_kernel<4>", "cand_kernel<4, false, unsigned short>",
-                "assign_list_kernel<4, 1>")) or None),
+            "traffic": cand_traffic,
             "avg_launch_ms": round(assign_avg_ms, 4), "algorithmic_flop_per_launch": assign_flop,
             "deferred_to_full_search": round(prof.cand_deferred / max(prof.cand_vectors, 1), 4),
+            "measured_hbm_gbs": None if cand_hbm_gbs is None else round(cand_hbm_gbs, 1),
+            "measured_hbm_frac": None if cand_hbm_gbs is None else round(cand_hbm_gbs / PEAK_HBM_GBS, 4),
+            "note": "achieved = iterations x n x 2 x dim x ksub / time, the exhaustive search's "
+                    "FLOP delivered per second; the exact candidate method evaluates about 13 of "
+                    "256 codewords per vector-subspace, so frac can pass 1; measured_hbm_* is the "
+                    "stage's counted HBM traffic over the same time",
         },
         "first_iteration_roofline": {
             "kernel": "assign_kernel (pruned full search, iteration 0)",
