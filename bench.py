@@ -382,7 +382,7 @@ def main() -> int:
             traffic = {}
 
     cand_traffic = sum(traffic.get(k, 0) for k in (
-        "nbr_build_kernel<4>", "cand_kernel<4, false, unsigned short>",
+        "nbr_build_kernel<4>", "cand_kernel<4, false, false, unsigned short>",
         "assign_list_kernel<4, 1>")) or None
     cand_hbm_gbs = None if cand_traffic is None else cand_traffic / (assign_avg_ms * 1e-3) / 1e9
 
@@ -435,11 +435,15 @@ def main() -> int:
                     "stage's counted HBM traffic over the same time",
         },
         "first_iteration_roofline": {
-            "kernel": "assign_kernel (pruned full search, iteration 0)",
+            "kernel": "Lloyd assignment of iteration 0 from grid anchors (nbr_build_kernel + "
+                      "grid_build_kernel + cand_kernel<4, true, false> + assign_list_kernel)",
             "avg_launch_ms": round(full_avg_ms, 4),
             "achieved": round(assign_flop / (full_avg_ms * 1e-3) / 1e12, 3),
             "frac": round(assign_flop / (full_avg_ms * 1e-3) / 1e12 / PEAK_FP32_TFLOPS, 4),
-            "traffic": traffic.get("assign_kernel<4, 8>"),
+            "traffic": (sum(traffic.get(k, 0) for k in (
+                "nbr_build_kernel<4>", "grid_build_kernel<4>",
+                "cand_kernel<4, true, false, unsigned short>", "assign_list_kernel<4, 1>"))
+                        or None),
         },
         "encode_roofline": {
             "avg_launch_ms": round(encode_avg_ms, 4),
@@ -448,7 +452,7 @@ def main() -> int:
             "hbm_gbs": round(encode_bytes / (encode_avg_ms * 1e-3) / 1e9, 1),
             "hbm_frac": round(encode_bytes / (encode_avg_ms * 1e-3) / 1e9 / PEAK_HBM_GBS, 4),
             "traffic": (sum(traffic.get(k, 0) for k in (
-                "nbr_build_kernel<4>", "grid_build_kernel<4>", "cand_kernel<4, true, unsigned char>",
+                "nbr_build_kernel<4>", "grid_build_kernel<4>", "cand_kernel<4, true, true, unsigned char>",
                 "encode_list_kernel<4, unsigned char>")) or None),
         },
         "update_roofline": {

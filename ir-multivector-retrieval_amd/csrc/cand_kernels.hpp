@@ -225,17 +225,20 @@ __device__ inline uint32_t wave_inclusive_sum(uint32_t v) {
   return v;
 }
 
-// The exact candidate-set assignment.  Training (ENCODE false): block
-// (chunk b, subspace m) of a 2-D grid; x = xs[m][i][DP]; the anchor is
-// codes[m][i] (the previous iteration's code) and the result goes back to
-// codes[m][i] with e[m][i], the reference distance.  Encode (ENCODE true):
-// a 1-D grid whose blocks run XCD-contiguously as (chunk, subspace) so that
-// the M blocks of a chunk share one L2; x = x[i][m*D ..] (token-major); the
-// anchor comes from the grid and the code goes to out[i][m].  Vectors the
-// rule cannot settle are first listed in the block's own slice
-// slice[m][b*chunk ..] (an LDS counter), then appended to the subspace's
-// dense list defer[m][0 .. defer_count[m]) with one global atomic per block.
-template <int D, bool ENCODE, typename CodeT>
+// The exact candidate-set assignment.  GRID picks the anchor: the nearer of
+// the vector's grid cell's two codewords (true), or codes[m][i], the
+// previous Lloyd iteration's code (false).  TOKENS picks the layout.
+// Training (TOKENS false): block (chunk b, subspace m) of a 2-D grid;
+// x = xs[m][i][DP]; the result goes to codes[m][i] with e[m][i], the
+// reference distance; iteration 0 runs with grid anchors, later iterations
+// from the previous codes.  Encode (TOKENS true, GRID true): a 1-D grid
+// whose blocks run XCD-contiguously as (chunk, subspace) so that the M
+// blocks of a chunk share one L2; x = x[i][m*D ..] (token-major) and the code
+// goes to out[i][m].  Vectors the rule cannot settle are first listed in the
+// block's own slice slice[m][b*chunk ..] (an LDS counter), then appended to
+// the subspace's dense list defer[m][0 .. defer_count[m]) with one global
+// atomic per block.
+template <int D, bool GRID, bool TOKENS, typename CodeT>
 __global__ __launch_bounds__(kCandThreads) void cand_kernel(
     const float* __restrict__ xin, const float* __restrict__ cb,
     const uint32_t* __restrict__ nbr, const uint8_t* __restrict__ anchors,
@@ -247,8 +250,9 @@ __global__ __launch_bounds__(kCandThreads) void cand_kernel(
   constexpr int DP = Pad<D>::value;
   constexpr float g = cand_gamma(D);
   extern __shared__ __attribute__((aligned(16))) float lds[];
+  static_assert(GRID || !TOKENS, "token-major input takes grid anchors");
   uint32_t m, b;
-  if constexpr (ENCODE) {
+  if constexpr (TOKENS) {
     const uint32_t logical = xcd_contiguous(blockIdx.x, gridDim.x);
     if (logical >= nchunks * M) return;  // grid padding to a multiple of 8
     b = logical / M;
@@ -258,7 +262,7 @@ __global__ __launch_bounds__(kCandThreads) void cand_kernel(
     m = blockIdx.y;
     if (done[m]) return;
   }
-  const CandLds lay = cand_lds(K, DP, ENCODE ? cells : 0u);
+  const CandLds lay = cand_lds(K, DP, GRID ? cells : 0u);
   uint8_t* base = reinterpret_cast<uint8_t*>(lds);
   float* lcb = lds;
   uint32_t* lsamp = reinterpret_cast<uint32_t*>(base + lay.samp_off);
@@ -295,7 +299,7 @@ __global__ __launch_bounds__(kCandThreads) void cand_kernel(
   const uint32_t* rows = nbm;  // row a at rows + a * rs
   const uint32_t rs = Lr;
   for (uint32_t j = t; j < K * 8; j += blockDim.x) lsamp[j] = cand_sample(nbm + (j / 8) * Lr, L, j % 8);
-  if constexpr (ENCODE) {
+  if constexpr (GRID) {
     const uint8_t* am = anchors + (uint64_t)m * cells * kCandAnchors;
     for (uint32_t j = t; j < cells * kCandAnchors; j += blockDim.x) lanc[j] = am[j];
     if (t < 16) lgrid[t] = grid[m * 16 + t];
@@ -309,7 +313,7 @@ __global__ __launch_bounds__(kCandThreads) void cand_kernel(
   uint16_t* cm = codes + (uint64_t)m * n;
   float* em = e + (uint64_t)m * n;
   auto load_x = [&](uint64_t i, float (&v)[D]) {
-    if constexpr (ENCODE) {
+    if constexpr (TOKENS) {
       const float* src = xin + i * dim + (uint64_t)m * D;
 #pragma unroll
       for (int k = 0; k < D; ++k) v[k] = src[k];
@@ -326,7 +330,7 @@ __global__ __launch_bounds__(kCandThreads) void cand_kernel(
   const uint64_t first_i = lo_i + (uint64_t)wave * kWave + lane;
   if (first_i < hi_i) {
     load_x(first_i, xq);
-    if constexpr (!ENCODE) aq = cm[first_i];
+    if constexpr (!GRID) aq = cm[first_i];
   }
   constexpr uint64_t kStride = (uint64_t)kCandWaves * kWave;
   for (uint64_t g0 = lo_i + (uint64_t)wave * kWave; g0 < hi_i; g0 += kStride) {
@@ -339,10 +343,10 @@ __global__ __launch_bounds__(kCandThreads) void cand_kernel(
     uint32_t a = valid ? aq : 0u;
     if (i + kStride < hi_i) {
       load_x(i + kStride, xq);
-      if constexpr (!ENCODE) aq = cm[i + kStride];
+      if constexpr (!GRID) aq = cm[i + kStride];
     }
-    uint32_t cell = 0;  // encode: NaN coordinates land in cell 0 (fmaxf)
-    if constexpr (ENCODE) {
+    uint32_t cell = 0;  // grid anchors: NaN coordinates land in cell 0 (fmaxf)
+    if constexpr (GRID) {
 #pragma unroll
       for (int k = D - 1; k >= 0; --k) {
         const float f = fminf(fmaxf((x[k] - lgrid[k]) * lgrid[8 + k], 0.0f), (float)(G - 1));
@@ -358,7 +362,7 @@ __global__ __launch_bounds__(kCandThreads) void cand_kernel(
       float ca[D];
       load_padded<D>(lcb + a * DP, ca);
       U2 = exact_l2sq<D>(x, ca);
-      if constexpr (ENCODE) {  // the nearer of the cell's two anchors
+      if constexpr (GRID) {  // the nearer of the cell's two anchors
         const uint32_t a2 = lanc[cell * kCandAnchors + 1];
         float cb2[D];
         load_padded<D>(lcb + a2 * DP, cb2);
@@ -442,7 +446,7 @@ __global__ __launch_bounds__(kCandThreads) void cand_kernel(
     wave_lds_sync();
     if (live) {
       const unsigned long long k = gbest[lane];
-      if constexpr (ENCODE) {
+      if constexpr (TOKENS) {
         out[i * M + m] = (CodeT)cand_best_code(k);
       } else {
         cm[i] = (uint16_t)cand_best_code(k);

@@ -291,24 +291,37 @@ struct Launch {
     assign_kernel<D, VPT><<<grid, kBlock, lds, s>>>(xs, cb, codes, e, done, n, K, rescans);
   }
   // Candidate-set assignment (cand_kernels.hpp): neighbour tables of the
-  // current codebooks, the assignment from the previous codes, then the
-  // pruned full search of the deferred vectors.
-  static int assign_cand(const float *xs, const float *cb, uint32_t *nbr, uint16_t *codes,
-                         float *e, uint32_t *slice, uint32_t *defer, uint32_t *defer_count,
-                         const uint32_t *done, uint64_t n, uint32_t M, uint32_t K, uint32_t L,
+  // current codebooks, the assignment from grid anchors (GRID, the first
+  // Lloyd iteration) or from the previous codes, then the pruned full search
+  // of the deferred vectors.
+  template <bool GRID>
+  static int assign_cand(const float *xs, const float *cb, uint32_t *nbr, uint8_t *anchors,
+                         float *grid, uint16_t *codes, float *e, uint32_t *slice,
+                         uint32_t *defer, uint32_t *defer_count, const uint32_t *done,
+                         uint64_t n, uint32_t M, uint32_t K, uint32_t L,
                          unsigned long long *rescans, hipStream_t s) {
     nbr_build_kernel<D><<<dim3(K, M), kWave, 0, s>>>(cb, nbr, defer_count, done, K, L);
-    const CandLds lay = cand_lds(K, Pad<D>::value);
-    if (int st = raise_lds((const void *)cand_kernel<D, false, uint16_t>, lay.total, 0)) return st;
+    uint32_t G = 0, cells = 0;
+    if (GRID) {
+      G = cand_grid_side(D);
+      cells = 1;
+      for (int k = 0; k < D; ++k) cells *= G;
+      grid_build_kernel<D><<<dim3((cells + kBlock - 1) / kBlock, M), kBlock, 0, s>>>(
+          cb, anchors, grid, K, G, cells);
+    }
+    const CandLds lay = cand_lds(K, Pad<D>::value, cells);
+    if (int st = raise_lds((const void *)cand_kernel<D, GRID, false, uint16_t>, lay.total, cells))
+      return st;
     // About 1,024 blocks over all subspaces; a chunk is whole groups of
     // kCandThreads vectors.
     const uint64_t per_sub = std::max<uint64_t>(1, (1024 + M - 1) / M);
     uint64_t chunk = (n + per_sub - 1) / per_sub;
     chunk = (chunk + kCandThreads - 1) / kCandThreads * kCandThreads;
     const uint64_t nblk = (n + chunk - 1) / chunk;
-    cand_kernel<D, false, uint16_t><<<dim3((unsigned)nblk, M), kCandThreads, lay.total, s>>>(
-        xs, cb, nbr, nullptr, nullptr, codes, e, nullptr, slice, defer, defer_count, done, n, 0,
-        M, K, L, (uint32_t)chunk, (uint32_t)nblk, 0, 0);
+    cand_kernel<D, GRID, false, uint16_t><<<dim3((unsigned)nblk, M), kCandThreads, lay.total,
+                                            s>>>(xs, cb, nbr, anchors, grid, codes, e, nullptr,
+                                                 slice, defer, defer_count, done, n, 0, M, K, L,
+                                                 (uint32_t)chunk, (uint32_t)nblk, G, cells);
     const uint32_t Kp = (K + kPruneBlock - 1) / kPruneBlock * kPruneBlock;
     const size_t lds = (size_t)Kp * (Pad<D>::value + 1) * sizeof(float) + 2 * sizeof(uint32_t);
     // About 2% of the vectors are deferred.  One vector per thread and about
@@ -337,7 +350,7 @@ struct Launch {
     grid_build_kernel<D><<<dim3((cells + kBlock - 1) / kBlock, M), kBlock, 0, s>>>(
         cb, anchors, grid, K, G, cells);
     const CandLds lay = cand_lds(K, Pad<D>::value, cells);
-    if (int st = raise_lds((const void *)cand_kernel<D, true, CodeT>, lay.total, cells))
+    if (int st = raise_lds((const void *)cand_kernel<D, true, true, CodeT>, lay.total, cells))
       return st;
     // Chunks of 8,192 rows; the M blocks of a chunk run on one XCD, so a row
     // crosses HBM once and its other subspaces come from L2.
@@ -346,7 +359,7 @@ struct Launch {
     const uint64_t total = nchunks * M;
     if (total > 0xFFFFFFF0ull) return TAC_ERR_UNSUPPORTED;
     const uint32_t blocks = (uint32_t)(8 * ((total + 7) / 8));
-    cand_kernel<D, true, CodeT><<<blocks, kCandThreads, lay.total, s>>>(
+    cand_kernel<D, true, true, CodeT><<<blocks, kCandThreads, lay.total, s>>>(
         x, cb, nbr, anchors, grid, nullptr, nullptr, codes, slice, defer, defer_count, nullptr, n,
         dim, M, K, L, (uint32_t)chunk, (uint32_t)nchunks, G, cells);
     const uint32_t Kp = (K + kPruneBlock - 1) / kPruneBlock * kPruneBlock;
@@ -557,16 +570,24 @@ int train_core(DeviceState &ds, hipStream_t s, const float *d_x, uint64_t n, uin
   if ((st = ensure(ds, ds.scal, (size_t)2 * M * sizeof(float)))) return st;
   if (want_trace && (st = ensure(ds, ds.trace, (size_t)max_iters * cb_elems * sizeof(float))))
     return st;
-  // Iterations after the first start from the previous codes (cand_kernels.hpp)
-  // when the codeword ids fit the neighbour keys and the tables fit in LDS.
-  // TAC_GPU_FULL_SEARCH=1 keeps the full search in every iteration.
+  // Candidate-set assignment (cand_kernels.hpp) when the codeword ids fit the
+  // neighbour keys and the tables fit in LDS: iterations after the first
+  // start from the previous codes, and the first, on 16,384 vectors or more,
+  // from grid anchors.  TAC_GPU_FULL_SEARCH=1 keeps the full search in every
+  // iteration.
   const char *full_env = getenv("TAC_GPU_FULL_SEARCH");
   const uint32_t Lc = K >= 2 ? std::min<uint32_t>(kCandList, K - 1) : 0;
-  const bool cand = !(full_env && full_env[0] == '1') && K >= 2 && K <= kCandMaxK &&
-                    cand_lds(K, DP).total <= kCandLdsMax && max_iters > 1;
-  if (cand && ((st = ensure(ds, ds.cand_nbr, (size_t)M * K * cand_row_len(Lc) * sizeof(uint32_t))) ||
-               (st = ensure(ds, ds.cand_defer, (size_t)2 * M * n * sizeof(uint32_t))) ||
-               (st = ensure(ds, ds.cand_count, (size_t)M * sizeof(uint32_t)))))
+  const bool cand_ok = !(full_env && full_env[0] == '1') && K >= 2 && K <= kCandMaxK &&
+                       cand_lds(K, DP, kCandCells).total <= kCandLdsMax && n <= 0xFFFFFFFFull;
+  const bool cand = cand_ok && max_iters > 1;
+  const bool cand_first = cand_ok && n >= 16384;
+  if ((cand || cand_first) &&
+      ((st = ensure(ds, ds.cand_nbr, (size_t)M * K * cand_row_len(Lc) * sizeof(uint32_t))) ||
+       (st = ensure(ds, ds.cand_defer, (size_t)2 * M * n * sizeof(uint32_t))) ||
+       (st = ensure(ds, ds.cand_count, (size_t)M * sizeof(uint32_t)))))
+    return st;
+  if (cand_first && ((st = ensure(ds, ds.cand_anchor, (size_t)M * kCandCells * kCandAnchors)) ||
+                     (st = ensure(ds, ds.cand_grid, (size_t)M * 16 * sizeof(float)))))
     return st;
 
   float *xs = as<float>(ds.xs);
@@ -619,11 +640,20 @@ int train_core(DeviceState &ds, hipStream_t s, const float *d_x, uint64_t n, uin
         return st;
       HIP_TRY(hipEventRecord(a, s));
     }
-    if (cand && t > 0) {
+    if ((cand && t > 0) || (cand_first && t == 0)) {
       uint32_t *slices = as<uint32_t>(ds.cand_defer);
-      DISPATCH_D_ST(D, assign_cand(xs, out.cb, as<uint32_t>(ds.cand_nbr), codes, e, slices,
-                                   slices + (size_t)M * n, as<uint32_t>(ds.cand_count), done,
-                                   n, M, K, Lc, rescans, s));
+      if (t == 0) {
+        DISPATCH_D_ST(D, assign_cand<true>(xs, out.cb, as<uint32_t>(ds.cand_nbr),
+                                           as<uint8_t>(ds.cand_anchor), as<float>(ds.cand_grid),
+                                           codes, e, slices, slices + (size_t)M * n,
+                                           as<uint32_t>(ds.cand_count), done, n, M, K, Lc,
+                                           rescans, s));
+      } else {
+        DISPATCH_D_ST(D, assign_cand<false>(xs, out.cb, as<uint32_t>(ds.cand_nbr), nullptr,
+                                            nullptr, codes, e, slices, slices + (size_t)M * n,
+                                            as<uint32_t>(ds.cand_count), done, n, M, K, Lc,
+                                            rescans, s));
+      }
       if (st) return st;
       LAUNCH_TRY("assign_cand kernels");
     } else {

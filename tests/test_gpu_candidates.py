@@ -1,8 +1,10 @@
-"""GPU parity of the candidate-set Lloyd assignment (iterations after the first).
+"""GPU parity of the candidate-set Lloyd assignment and encode.
 
 From the second iteration on, each vector is assigned by evaluating only the
 codewords that can tie or beat its previous code under the reference
-distance; the rest go to the pruned full search.  These tests train through
+distance; the rest go to the pruned full search.  The first iteration (on
+16,384 vectors or more) and encode anchor each vector at a grid cell's
+codeword instead.  These tests train through
 both paths on inputs built to stress the rule: exact duplicate points and
 codewords (ties resolved by the first index), distances in the subnormal
 range, large magnitudes, every sub-dimension 1-8 and K from 2 to 256, and
@@ -46,6 +48,32 @@ def test_sub_dimensions_and_codebook_sizes(gpu, dsub, ksub):
     _train_both(x, dim, m, ksub, init, 6)
 
 
+@pytest.mark.parametrize("dsub,ksub", [(1, 256), (2, 200), (3, 100), (4, 256), (5, 65),
+                                       (6, 17), (7, 2), (8, 256)])
+def test_first_iteration_grid_anchors(gpu, dsub, ksub):
+    # 20,000 vectors: iteration 0 takes the grid-anchored candidate pass.
+    m = 2
+    dim = m * dsub
+    rng = np.random.default_rng(300 + dsub)
+    x = (rng.standard_normal((20000, dim)) * 0.3).astype(np.float32)
+    init = synth.shuffle_init(x, m, ksub, 9)
+    _train_both(x, dim, m, ksub, init, 2)
+
+
+def test_first_iteration_grid_ties_and_magnitudes(gpu):
+    # Exact ties (vectors on duplicated codewords), subnormal and huge
+    # distances, all through the grid-anchored first iteration.
+    rng = np.random.default_rng(21)
+    pts = (rng.standard_normal((300, 16)) * 0.3).astype(np.float32)
+    x = pts[rng.integers(0, 300, 20000)]
+    init = synth.shuffle_init(x, 4, 256, 3)
+    init[:, 128:] = init[:, :128]
+    _train_both(x, 16, 4, 256, init, 2)
+    for scale in (1e-19, 1e15):
+        xs = (rng.standard_normal((20000, 16)) * scale).astype(np.float32)
+        _train_both(xs, 16, 4, 256, synth.shuffle_init(xs, 4, 256, 4), 2)
+
+
 def test_duplicate_points_and_codewords(gpu):
     # 6,000 vectors drawn from 250 distinct points: every assignment has exact
     # ties, clusters empty out and get reseeded onto duplicates.
@@ -70,9 +98,10 @@ def test_extreme_magnitudes(gpu, scale):
 
 
 def test_matches_full_search_on_the_chunk_workload(gpu, monkeypatch):
-    # 117,645 x 64, m16 k256, 20 iterations: the default path (candidates
-    # from iteration 1) and TAC_GPU_FULL_SEARCH=1 give the same bytes, and
-    # the candidate path settles most vectors without the full search.
+    # 117,645 x 64, m16 k256, 20 iterations: the default path (grid anchors
+    # in iteration 0, previous codes from iteration 1) and
+    # TAC_GPU_FULL_SEARCH=1 give the same bytes, and the candidate path
+    # settles most vectors without the full search.
     w, x, init = synth.workload("chunk-117k")
     device.profile_enable(True)
     device.profile_read(reset=True)
@@ -85,7 +114,7 @@ def test_matches_full_search_on_the_chunk_workload(gpu, monkeypatch):
     prof_full = device.profile_read(reset=True)
     device.profile_enable(False)
     assert np.array_equal(_bits(got.codebooks), _bits(full.codebooks))
-    assert prof.cand_vectors == (w.iters - 1) * w.m * w.n
+    assert prof.cand_vectors == w.iters * w.m * w.n
     assert 0 < prof.cand_deferred < 0.1 * prof.cand_vectors
     assert prof_full.cand_vectors == 0
 
