@@ -339,7 +339,8 @@ typedef struct tac_gpu_profile {
   double cluster_call_ms;  /* wall: the whole tac_cluster_flat call */
   uint64_t cand_vectors;   /* (vector, subspace) searches started from an anchor codeword:
                               the previous code (Lloyd iterations after the first) or a
-                              grid cell's codeword (encode of 16,384 vectors or more) */
+                              grid cell's codeword (the first Lloyd iteration and encode,
+                              on 16,384 vectors or more) */
   uint64_t cand_deferred;  /* of those, the ones left to the full search (candidate row
                               exhausted, non-finite or huge values) */
   double cand_assign_ms;   /* assignment stages that started from the previous codes
