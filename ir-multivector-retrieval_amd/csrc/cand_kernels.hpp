@@ -68,12 +68,15 @@ constexpr uint32_t kCandAnchors = 2;   // anchor codewords per cell
 //   lanc [cells][2] u8 anchors, lgrid [2][8] f32 (cell origin, cells per unit) |
 //   per wave: gx [64][DP] f32, gbest [64] u64, ga [64] u32 (the anchor's
 //   row offset),
-//   gitem [64 * 8] u16 (lane | item << 6) | lmax, lcnt u32
+//   gitem [64 * 8] u16 (lane | item << 6) | lmax, lcnt u32 | training only:
+//   lhist [tiles][(K + 1) / 2] u32, the block's sort-tile histograms of the
+//   new codes as u16 pairs (at most kSortTile per bin)
 struct CandLds {
-  uint32_t samp_off, anc_off, grid_off, wave_off, wave_bytes, scal_off, total;
+  uint32_t samp_off, anc_off, grid_off, wave_off, wave_bytes, scal_off, hist_off, total;
 };
 __host__ __device__ inline uint32_t cand_up16(uint32_t b) { return (b + 15u) & ~15u; }
-__host__ __device__ inline CandLds cand_lds(uint32_t K, uint32_t DP, uint32_t cells = 0) {
+__host__ __device__ inline CandLds cand_lds(uint32_t K, uint32_t DP, uint32_t cells = 0,
+                                            uint32_t hist_tiles = 0) {
   CandLds s;
   s.samp_off = cand_up16(K * DP * 4u);
   s.anc_off = s.samp_off + K * 8u * 4u;
@@ -81,9 +84,14 @@ __host__ __device__ inline CandLds cand_lds(uint32_t K, uint32_t DP, uint32_t ce
   s.wave_off = s.grid_off + (cells ? 64u : 0u);
   s.wave_bytes = 64u * (DP * 4u + 8u + 4u) + 64u * 8u * 2u;
   s.scal_off = s.wave_off + (uint32_t)kCandWaves * s.wave_bytes;
-  s.total = s.scal_off + 16u;
+  s.hist_off = s.scal_off + 16u;
+  s.total = s.hist_off + hist_tiles * ((K + 1u) / 2u) * 4u;
   return s;
 }
+
+// Sort tiles per training candidate block at most: the block's chunk is
+// whole tiles, so its histograms are complete.
+constexpr uint32_t kCandHistTiles = 16;
 
 // Cells per dimension of the encode grid: the largest G with G^D <= kCandCells.
 __host__ __device__ inline uint32_t cand_grid_side(uint32_t D) {
@@ -237,7 +245,10 @@ __device__ inline uint32_t wave_inclusive_sum(uint32_t v) {
 // goes to out[i][m].  Vectors the rule cannot settle are first listed in the
 // block's own slice slice[m][b*chunk ..] (an LDS counter), then appended to
 // the subspace's dense list defer[m][0 .. defer_count[m]) with one global
-// atomic per block.
+// atomic per block.  Training also counts the new codes per sort tile of
+// kSortTile vectors (the chunk is whole tiles) and writes
+// hist[m][tile][code] for the update's counting sort; the deferred vectors'
+// codes are added there by assign_list_kernel.
 template <int D, bool GRID, bool TOKENS, typename CodeT>
 __global__ __launch_bounds__(kCandThreads) void cand_kernel(
     const float* __restrict__ xin, const float* __restrict__ cb,
@@ -246,7 +257,7 @@ __global__ __launch_bounds__(kCandThreads) void cand_kernel(
     CodeT* __restrict__ out, uint32_t* __restrict__ slice, uint32_t* __restrict__ defer,
     uint32_t* __restrict__ defer_count, const uint32_t* __restrict__ done, uint64_t n,
     uint32_t dim, uint32_t M, uint32_t K, uint32_t L, uint32_t chunk, uint32_t nchunks,
-    uint32_t G, uint32_t cells) {
+    uint32_t G, uint32_t cells, uint32_t* __restrict__ hist, uint32_t T) {
   constexpr int DP = Pad<D>::value;
   constexpr float g = cand_gamma(D);
   extern __shared__ __attribute__((aligned(16))) float lds[];
@@ -262,7 +273,9 @@ __global__ __launch_bounds__(kCandThreads) void cand_kernel(
     m = blockIdx.y;
     if (done[m]) return;
   }
-  const CandLds lay = cand_lds(K, DP, GRID ? cells : 0u);
+  const uint32_t tiles = TOKENS ? 0u : chunk / kSortTile;  // the chunk is whole tiles
+  const uint32_t Kw = (K + 1u) / 2u;                       // u16 pairs per tile
+  const CandLds lay = cand_lds(K, DP, GRID ? cells : 0u, tiles);
   uint8_t* base = reinterpret_cast<uint8_t*>(lds);
   float* lcb = lds;
   uint32_t* lsamp = reinterpret_cast<uint32_t*>(base + lay.samp_off);
@@ -276,6 +289,8 @@ __global__ __launch_bounds__(kCandThreads) void cand_kernel(
   uint16_t* gitem = reinterpret_cast<uint16_t*>(ga + 64);
   uint32_t* lmax = reinterpret_cast<uint32_t*>(base + lay.scal_off);
   uint32_t* lcnt = lmax + 1;
+  uint32_t* lhist = reinterpret_cast<uint32_t*>(base + lay.hist_off);
+  for (uint32_t j = threadIdx.x; j < tiles * Kw; j += blockDim.x) lhist[j] = 0;
 
   if (t == 0) {
     *lmax = 0;
@@ -449,13 +464,23 @@ __global__ __launch_bounds__(kCandThreads) void cand_kernel(
       if constexpr (TOKENS) {
         out[i * M + m] = (CodeT)cand_best_code(k);
       } else {
-        cm[i] = (uint16_t)cand_best_code(k);
+        const uint32_t code = cand_best_code(k);
+        cm[i] = (uint16_t)code;
         em[i] = __uint_as_float((uint32_t)(k >> 32));
+        atomicAdd(&lhist[(uint32_t)((i - lo_i) / kSortTile) * Kw + code / 2u], 1u << (16u * (code & 1u)));
       }
     }
     wave_lds_sync();  // the scratch is rewritten by the next group
   }
-  __syncthreads();  // the slice's global writes, and lcnt
+  __syncthreads();  // the slice's global writes, lcnt and lhist
+  if constexpr (!TOKENS) {
+    const uint32_t tile0 = (uint32_t)(lo_i / kSortTile);
+    for (uint32_t j = t; j < tiles * K; j += blockDim.x) {
+      const uint32_t tt = j / K, c = j % K;
+      if (tile0 + tt < T)
+        hist[((uint64_t)m * T + tile0 + tt) * K + c] = (lhist[tt * Kw + c / 2u] >> (16u * (c & 1u))) & 0xFFFFu;
+    }
+  }
   const uint32_t nd = *lcnt;
   if (nd == 0) return;
   __syncthreads();  // every thread has read lcnt before it is reused
@@ -469,14 +494,16 @@ __global__ __launch_bounds__(kCandThreads) void cand_kernel(
 // The deferred vectors: the pruned exact search over all K codewords
 // (pq_kernels.hpp), vectors gathered through the dense list defer[m][..];
 // a persistent grid of gridDim.x blocks per subspace walks tiles of
-// kBlock*VPT entries.  With stats (profiling): stats[0] += deferred
+// kBlock*VPT entries; each new code is added to its sort tile's count in
+// hist[m][tile][code].  With stats (profiling): stats[0] += deferred
 // vectors, stats[1] += n per subspace.
 template <int D, int VPT>
 __global__ __launch_bounds__(kBlock) void assign_list_kernel(
     const float* __restrict__ xs, const float* __restrict__ cb, uint16_t* __restrict__ codes,
     float* __restrict__ e, const uint32_t* __restrict__ defer,
     const uint32_t* __restrict__ defer_count, const uint32_t* __restrict__ done, uint64_t n,
-    uint32_t K, unsigned long long* __restrict__ rescans, unsigned long long* __restrict__ stats) {
+    uint32_t K, unsigned long long* __restrict__ rescans, unsigned long long* __restrict__ stats,
+    uint32_t* __restrict__ hist, uint32_t T) {
   constexpr int DP = Pad<D>::value;
   constexpr uint32_t kTile = kBlock * VPT;
   extern __shared__ __attribute__((aligned(16))) float lds[];
@@ -525,6 +552,7 @@ __global__ __launch_bounds__(kBlock) void assign_list_kernel(
       if (idx[j] != 0xFFFFFFFFu) {
         codes[(uint64_t)m * n + idx[j]] = (uint16_t)bidx[j];
         e[(uint64_t)m * n + idx[j]] = best[j];
+        atomicAdd(&hist[((uint64_t)m * T + idx[j] / kSortTile) * K + bidx[j]], 1u);
       }
     }
   }

@@ -261,7 +261,7 @@ int raise_lds(const void *fn, uint32_t bytes, uint32_t cells) {
   std::lock_guard<std::mutex> g(mu);
   for (const void *f : raised)
     if (f == fn) return TAC_OK;
-  const uint32_t most = cand_lds(kCandMaxK, 8, cells).total;
+  const uint32_t most = cand_lds(kCandMaxK, 8, cells, kCandHistTiles).total;
   const hipError_t err = hipFuncSetAttribute(fn, hipFuncAttributeMaxDynamicSharedMemorySize,
                                             (int)(most > bytes ? most : bytes));
   if (err != hipSuccess) return hip_status("hipFuncSetAttribute(candidate kernel)", err);
@@ -293,13 +293,14 @@ struct Launch {
   // Candidate-set assignment (cand_kernels.hpp): neighbour tables of the
   // current codebooks, the assignment from grid anchors (GRID, the first
   // Lloyd iteration) or from the previous codes, then the pruned full search
-  // of the deferred vectors.
+  // of the deferred vectors.  Both passes also count the new codes per sort
+  // tile into hist[M][T][K] for the update.
   template <bool GRID>
   static int assign_cand(const float *xs, const float *cb, uint32_t *nbr, uint8_t *anchors,
                          float *grid, uint16_t *codes, float *e, uint32_t *slice,
                          uint32_t *defer, uint32_t *defer_count, const uint32_t *done,
-                         uint64_t n, uint32_t M, uint32_t K, uint32_t L,
-                         unsigned long long *rescans, hipStream_t s) {
+                         uint64_t n, uint32_t M, uint32_t K, uint32_t L, uint32_t *hist,
+                         uint32_t T, unsigned long long *rescans, hipStream_t s) {
     nbr_build_kernel<D><<<dim3(K, M), kWave, 0, s>>>(cb, nbr, defer_count, done, K, L);
     uint32_t G = 0, cells = 0;
     if (GRID) {
@@ -309,19 +310,21 @@ struct Launch {
       grid_build_kernel<D><<<dim3((cells + kBlock - 1) / kBlock, M), kBlock, 0, s>>>(
           cb, anchors, grid, K, G, cells);
     }
-    const CandLds lay = cand_lds(K, Pad<D>::value, cells);
-    if (int st = raise_lds((const void *)cand_kernel<D, GRID, false, uint16_t>, lay.total, cells))
-      return st;
-    // About 1,024 blocks over all subspaces; a chunk is whole groups of
-    // kCandThreads vectors.
+    // About 1,024 blocks over all subspaces; a chunk is whole sort tiles
+    // (whole groups of kCandThreads vectors), at most kCandHistTiles of them.
     const uint64_t per_sub = std::max<uint64_t>(1, (1024 + M - 1) / M);
     uint64_t chunk = (n + per_sub - 1) / per_sub;
-    chunk = (chunk + kCandThreads - 1) / kCandThreads * kCandThreads;
+    chunk = (chunk + kSortTile - 1) / kSortTile * kSortTile;
+    chunk = std::min<uint64_t>(chunk, (uint64_t)kCandHistTiles * kSortTile);
     const uint64_t nblk = (n + chunk - 1) / chunk;
+    const CandLds lay = cand_lds(K, Pad<D>::value, cells, (uint32_t)(chunk / kSortTile));
+    if (int st = raise_lds((const void *)cand_kernel<D, GRID, false, uint16_t>, lay.total, cells))
+      return st;
     cand_kernel<D, GRID, false, uint16_t><<<dim3((unsigned)nblk, M), kCandThreads, lay.total,
                                             s>>>(xs, cb, nbr, anchors, grid, codes, e, nullptr,
                                                  slice, defer, defer_count, done, n, 0, M, K, L,
-                                                 (uint32_t)chunk, (uint32_t)nblk, G, cells);
+                                                 (uint32_t)chunk, (uint32_t)nblk, G, cells, hist,
+                                                 T);
     const uint32_t Kp = (K + kPruneBlock - 1) / kPruneBlock * kPruneBlock;
     const size_t lds = (size_t)Kp * (Pad<D>::value + 1) * sizeof(float) + 2 * sizeof(uint32_t);
     // About 2% of the vectors are deferred.  One vector per thread and about
@@ -332,7 +335,7 @@ struct Launch {
         1, std::min<uint64_t>((n + kBlock - 1) / kBlock, (4096 + M - 1) / M));
     assign_list_kernel<D, 1><<<dim3((unsigned)g, M), kBlock, lds, s>>>(
         xs, cb, codes, e, defer, defer_count, done, n, K, rescans,
-        g_profile ? rescans + 1 : nullptr);
+        g_profile ? rescans + 1 : nullptr, hist, T);
     return TAC_OK;
   }
   // Candidate-set encode: neighbour rows and grid anchors of the codebooks,
@@ -361,7 +364,7 @@ struct Launch {
     const uint32_t blocks = (uint32_t)(8 * ((total + 7) / 8));
     cand_kernel<D, true, true, CodeT><<<blocks, kCandThreads, lay.total, s>>>(
         x, cb, nbr, anchors, grid, nullptr, nullptr, codes, slice, defer, defer_count, nullptr, n,
-        dim, M, K, L, (uint32_t)chunk, (uint32_t)nchunks, G, cells);
+        dim, M, K, L, (uint32_t)chunk, (uint32_t)nchunks, G, cells, nullptr, 0);
     const uint32_t Kp = (K + kPruneBlock - 1) / kPruneBlock * kPruneBlock;
     const size_t lds = (size_t)Kp * (Pad<D>::value + 1) * sizeof(float) + 2 * sizeof(uint32_t);
     const uint64_t g = std::max<uint64_t>(
@@ -578,7 +581,8 @@ int train_core(DeviceState &ds, hipStream_t s, const float *d_x, uint64_t n, uin
   const char *full_env = getenv("TAC_GPU_FULL_SEARCH");
   const uint32_t Lc = K >= 2 ? std::min<uint32_t>(kCandList, K - 1) : 0;
   const bool cand_ok = !(full_env && full_env[0] == '1') && K >= 2 && K <= kCandMaxK &&
-                       cand_lds(K, DP, kCandCells).total <= kCandLdsMax && n <= 0xFFFFFFFFull;
+                       cand_lds(K, DP, kCandCells, kCandHistTiles).total <= kCandLdsMax &&
+                       n <= 0xFFFFFFFFull;
   const bool cand = cand_ok && max_iters > 1;
   const bool cand_first = cand_ok && n >= 16384;
   if ((cand || cand_first) &&
@@ -640,19 +644,22 @@ int train_core(DeviceState &ds, hipStream_t s, const float *d_x, uint64_t n, uin
         return st;
       HIP_TRY(hipEventRecord(a, s));
     }
-    if ((cand && t > 0) || (cand_first && t == 0)) {
+    // The candidate passes count the sort tiles themselves; the full search
+    // leaves that to hist_kernel.
+    const bool cand_now = (cand && t > 0) || (cand_first && t == 0);
+    if (cand_now) {
       uint32_t *slices = as<uint32_t>(ds.cand_defer);
       if (t == 0) {
         DISPATCH_D_ST(D, assign_cand<true>(xs, out.cb, as<uint32_t>(ds.cand_nbr),
                                            as<uint8_t>(ds.cand_anchor), as<float>(ds.cand_grid),
                                            codes, e, slices, slices + (size_t)M * n,
-                                           as<uint32_t>(ds.cand_count), done, n, M, K, Lc,
-                                           rescans, s));
+                                           as<uint32_t>(ds.cand_count), done, n, M, K, Lc, hist,
+                                           T, rescans, s));
       } else {
         DISPATCH_D_ST(D, assign_cand<false>(xs, out.cb, as<uint32_t>(ds.cand_nbr), nullptr,
                                             nullptr, codes, e, slices, slices + (size_t)M * n,
-                                            as<uint32_t>(ds.cand_count), done, n, M, K, Lc,
-                                            rescans, s));
+                                            as<uint32_t>(ds.cand_count), done, n, M, K, Lc, hist,
+                                            T, rescans, s));
       }
       if (st) return st;
       LAUNCH_TRY("assign_cand kernels");
@@ -661,8 +668,10 @@ int train_core(DeviceState &ds, hipStream_t s, const float *d_x, uint64_t n, uin
       LAUNCH_TRY("assign_kernel");
     }
     if (profile) HIP_TRY(hipEventRecord(b, s));
-    hist_kernel<<<dim3(T, M), kBlock, hist_lds, s>>>(codes, hist, done, n, K, T);
-    LAUNCH_TRY("hist_kernel");
+    if (!cand_now) {
+      hist_kernel<<<dim3(T, M), kBlock, hist_lds, s>>>(codes, hist, done, n, K, T);
+      LAUNCH_TRY("hist_kernel");
+    }
     scan_partial_kernel<<<dim3(G, M), kBlock, 0, s>>>(hist, scan_part, done, K, T, G);
     scan_apply_kernel<<<dim3(G, M), kBlock, 0, s>>>(hist, scan_part, counts, start, done, K, T,
                                                      G);
