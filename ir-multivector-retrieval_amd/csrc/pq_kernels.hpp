@@ -465,8 +465,22 @@ __global__ __launch_bounds__(kBlock) void scan_apply_kernel(
       counts[(uint64_t)m * K + c] = tot[q];
     }
     st += tot[q];
+    // Eight tiles' counts are loaded before any is rewritten, so the loads
+    // overlap instead of waiting behind the stores one tile at a time.
+    constexpr uint32_t B = 8;
     uint32_t run = before[q];
-    for (uint32_t t = t0; t < t1; ++t) {
+    uint32_t t = t0;
+    for (; t + B <= t1; t += B) {
+      uint32_t v[B];
+#pragma unroll
+      for (uint32_t j = 0; j < B; ++j) v[j] = hm[(uint64_t)(t + j) * K + c];
+#pragma unroll
+      for (uint32_t j = 0; j < B; ++j) {
+        hm[(uint64_t)(t + j) * K + c] = run;
+        run += v[j];
+      }
+    }
+    for (; t < t1; ++t) {
       const uint32_t v = hm[(uint64_t)t * K + c];
       hm[(uint64_t)t * K + c] = run;
       run += v;
