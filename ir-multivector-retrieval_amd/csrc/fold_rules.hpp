@@ -118,6 +118,49 @@ TAC_HD inline uint64_t fold_quantize(float e, int32_t k) {
   return (k_ok && e_ok && small && !tie) ? q : kFoldBad;
 }
 
+// The accumulator in units of its ulp U: s = m * U with 2^F <= m < 2^(F+1)
+// (s normal and positive).
+template <typename Acc>
+TAC_HD inline uint64_t fold_units(Acc s) {
+  using T = FoldTraits<Acc>;
+  using Bits = typename T::Bits;
+  constexpr uint64_t kOne = 1ull << T::kFrac;
+  return (uint64_t)(fold_bits(s) & (Bits)(kOne - 1)) | kOne;
+}
+
+// m * U in the binade of s, for 2^F <= m < 2^(F+1).
+template <typename Acc>
+TAC_HD inline Acc fold_with_units(Acc s, uint64_t m) {
+  using T = FoldTraits<Acc>;
+  using Bits = typename T::Bits;
+  constexpr uint64_t kOne = 1ull << T::kFrac;
+  return fold_from_bits<Acc>((Bits)((fold_bits(s) & ~(Bits)(kOne - 1)) | (Bits)(m & (kOne - 1))));
+}
+
+// The chunk's quantized sum for the binade of s (normal, positive), or
+// kFoldBad when the chunk has no clean candidate there or the sum alone
+// would leave the binade.
+template <typename Acc>
+TAC_HD inline uint64_t fold_chunk_q(Acc s, const FoldChunk& ch) {
+  using T = FoldTraits<Acc>;
+  constexpr uint64_t kOne = 1ull << T::kFrac;
+  const int32_t c = fold_exponent(s) - ch.k0;
+  if (c < 0 || c >= kFoldCands || !((ch.clean >> c) & 1u)) return kFoldBad;
+  const uint64_t Q = c == 0 ? ch.q[0] : c == 1 ? ch.q[1] : ch.q[2];
+  return Q > 2 * kOne ? kFoldBad : Q;
+}
+
+// A run of chunks from s: with P_i the prefix sums of their fold_chunk_q,
+// chunk i adds U * Q_i exactly while fold_units(s) + P_i <= 2^(F+1) - 1, so
+// the run's partial sums are fold_with_units(s, fold_units(s) + P_i) and a
+// wave applies 64 chunks with one prefix sum (each Q_i <= 2^(F+1), so P
+// stays below 2^60).
+template <typename Acc>
+TAC_HD inline bool fold_run_fits(uint64_t m, uint64_t P) {
+  using T = FoldTraits<Acc>;
+  return m + P <= 2 * (1ull << T::kFrac) - 1;
+}
+
 // Applies a chunk with quantized sums: true (and *out) when the chunk adds
 // exactly U * Q without leaving the accumulator's binade.
 template <typename Acc>

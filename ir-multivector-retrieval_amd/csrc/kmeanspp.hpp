@@ -287,7 +287,6 @@ __device__ inline void kpp_fallback_block(const float* __restrict__ wm, uint64_t
   constexpr uint32_t kWaves = kKppFallbackThreads / kWave;
   __shared__ double wsum[kWaves];
   __shared__ double carry;
-  __shared__ FoldChunk lch[kWave];
   __shared__ __attribute__((aligned(16))) float buf[kFoldChunk];
   const uint32_t lane = threadIdx.x % kWave, wv = threadIdx.x / kWave;
   for (uint32_t j = wv; j < nc; j += kWaves) {
@@ -300,7 +299,7 @@ __device__ inline void kpp_fallback_block(const float* __restrict__ wm, uint64_t
   __syncthreads();
   if (wv != 0) return;
   // Wave 0 only from here: pm[j] becomes the exact value before chunk j.
-  const double total = fold_apply_wave<double>(wm, n, cm, nc, lch, buf, pm);
+  const double total = fold_apply_wave<double>(wm, n, cm, nc, buf, pm);
   __threadfence_block();
   const double u = S.r * total;
   uint32_t jf = 0xFFFFFFFFu;

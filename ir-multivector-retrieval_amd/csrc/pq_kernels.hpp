@@ -833,38 +833,56 @@ __device__ inline void fold_quantize_chunk_wave(const float* __restrict__ em, ui
   }
 }
 
+__device__ __forceinline__ uint64_t wave_inclusive_sum_u64(uint64_t v) {
+  const uint32_t lane = threadIdx.x % kWave;
+  for (int off = 1; off < kWave; off <<= 1) {
+    const uint64_t o = __shfl_up(v, off, kWave);
+    if (lane >= (uint32_t)off) v += o;
+  }
+  return v;
+}
+
 // One wave folds chunks 0 .. nc-1 of em in order from 0 with their
 // descriptors and returns the exact serial sum in every lane; every lane
-// computes the same values.  A chunk the rules do not cover is staged in
-// `buf` and folded term by term.  With `starts`, lane 0 stores the exact
-// accumulator value before each chunk.  lch: kWave descriptors of LDS;
-// buf: kFoldChunk floats of LDS.
+// computes the same values.  While the sum is normal, lane i takes chunk
+// j + i's quantized sum for the sum's binade and one prefix sum applies the
+// chunks up to the first one that does not fit (fold_run_fits), up to 64 at
+// a time.  That chunk, and any chunk while the sum is zero or subnormal, is
+// staged in `buf` (kFoldChunk floats of LDS) and folded term by term.  With
+// `starts`, the exact accumulator value before each chunk is stored.
 template <typename Acc>
 __device__ inline Acc fold_apply_wave(const float* __restrict__ em, uint64_t n,
-                                      const FoldChunk* __restrict__ cm, uint32_t nc,
-                                      FoldChunk* lch, float* buf, Acc* __restrict__ starts) {
+                                      const FoldChunk* __restrict__ cm, uint32_t nc, float* buf,
+                                      Acc* __restrict__ starts) {
   const uint32_t lane = threadIdx.x % kWave;
   Acc s = 0;
-  for (uint32_t j0 = 0; j0 < nc; j0 += kWave) {
-    wave_lds_sync();
-    if (j0 + lane < nc) lch[lane] = cm[j0 + lane];
-    wave_lds_sync();
-    const uint32_t cnt = nc - j0 < kWave ? nc - j0 : kWave;
-    for (uint32_t q = 0; q < cnt; ++q) {
-      const uint32_t j = j0 + q;
+  uint32_t j = 0;
+  while (j < nc) {
+    const uint32_t cnt = nc - j < kWave ? nc - j : kWave;
+    uint32_t b = 0;  // chunks applied through the prefix sum
+    if (fold_is_normal_positive(s)) {
+      const uint64_t m = fold_units(s);
+      const uint64_t Q = lane < cnt ? fold_chunk_q(s, cm[j + lane]) : kFoldBad;
+      const bool ok = Q != kFoldBad;
+      const uint64_t P = wave_inclusive_sum_u64(ok ? Q : 0u);
+      const uint64_t bad = __ballot(lane < cnt && !(ok && fold_run_fits<Acc>(m, P)));
+      b = bad ? (uint32_t)__builtin_ctzll(bad) : cnt;
+      if (starts != nullptr && lane < b) starts[j + lane] = fold_with_units(s, m + P - Q);
+      if (b > 0) s = fold_with_units(s, m + __shfl(P, (int)b - 1, kWave));
+    }
+    j += b;
+    if (b < cnt) {
       if (starts != nullptr && lane == 0) starts[j] = s;
-      Acc out;
-      if (!fold_apply(s, lch[q], &out)) {
-        const uint64_t lo = (uint64_t)j * kFoldChunk;
-        const uint32_t len = fold_chunk_len(n, j);
-        wave_lds_sync();
-        for (uint32_t t = lane; t < len; t += kWave) buf[t] = em[lo + t];
-        wave_lds_sync();
-        out = s;
+      const uint64_t lo = (uint64_t)j * kFoldChunk;
+      const uint32_t len = fold_chunk_len(n, j);
+      wave_lds_sync();
+      for (uint32_t t = lane; t < len; t += kWave) buf[t] = em[lo + t];
+      wave_lds_sync();
+      Acc out = s;
 #pragma unroll 16
-        for (uint32_t t = 0; t < len; ++t) out = out + (Acc)buf[t];
-      }
+      for (uint32_t t = 0; t < len; ++t) out = out + (Acc)buf[t];
       s = out;
+      ++j;
     }
   }
   return s;
@@ -905,12 +923,11 @@ __global__ __launch_bounds__(kBlock) void wcss_quantize_kernel(
 __global__ __launch_bounds__(kWave) void wcss_apply_kernel(
     const float* __restrict__ e, const FoldChunk* __restrict__ chunks, float* __restrict__ wcss,
     const uint32_t* __restrict__ done, uint64_t n, uint32_t nc) {
-  __shared__ FoldChunk lch[kWave];
   __shared__ __attribute__((aligned(16))) float buf[kFoldChunk];
   const uint32_t m = blockIdx.x;
   if (done[m]) return;
   const float s = fold_apply_wave<float>(e + (uint64_t)m * n, n, chunks + (uint64_t)m * nc, nc,
-                                         lch, buf, static_cast<float*>(nullptr));
+                                         buf, static_cast<float*>(nullptr));
   if (threadIdx.x == 0) wcss[m] = s;
 }
 

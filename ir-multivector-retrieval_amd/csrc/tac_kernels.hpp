@@ -713,13 +713,12 @@ __global__ __launch_bounds__(kWave) void tac_wcss_apply_kernel(
     const float* __restrict__ e, const FoldChunk* __restrict__ fchunks,
     const TacProblem* __restrict__ probs, const uint32_t* __restrict__ done,
     float* __restrict__ wcss) {
-  __shared__ FoldChunk lch[kWave];
   __shared__ __attribute__((aligned(16))) float buf[kFoldChunk];
   const uint32_t p = blockIdx.x;
   if (done[p]) return;
   const TacProblem pr = probs[p];
-  const float s = fold_apply_wave<float>(e + pr.off, pr.n, fchunks + pr.chunk0, pr.nchunks, lch,
-                                         buf, static_cast<float*>(nullptr));
+  const float s = fold_apply_wave<float>(e + pr.off, pr.n, fchunks + pr.chunk0, pr.nchunks, buf,
+                                         static_cast<float*>(nullptr));
   if (threadIdx.x == 0) wcss[p] = s;
 }
 

@@ -2,9 +2,12 @@
 // non-negative float terms, with an fp32 or an f64 accumulator, must equal
 // the plain serial fold bit for bit, on random and adversarial sequences
 // (exact ties, zeros, huge and tiny terms, NaN and inf, long absorbed
-// tails).  The f64 case also mirrors the k-means++ fallback's search (first
-// u < cum through the exact chunk start values) against the plain
-// weightedSample loop.  Built with -ffp-contract=off.
+// tails).  The chunk descriptors are applied both one by one and in runs of
+// 64 with one prefix sum per run, as the GPU wave applies them; the two must
+// agree with each other, chunk starts included, and with the serial fold.
+// The f64 case also mirrors the k-means++ fallback's search (first u < cum
+// through the exact chunk start values) against the plain weightedSample
+// loop.  Built with -ffp-contract=off.
 #include <algorithm>
 #include <cmath>
 #include <cstdint>
@@ -26,10 +29,9 @@ static Acc serial(const std::vector<float>& e) {
 
 // Host restatement of the GPU passes: f64 chunk prefix -> candidate binades
 // -> quantized sums (every term, spoiled candidates OR-ed into a mask, as
-// the quantize waves do) -> sequential application with term-by-term
-// fallback.  `starts` receives the exact value before every chunk.
+// the quantize waves do).
 template <typename Acc>
-static Acc chunked(const std::vector<float>& e, uint64_t* fallbacks, std::vector<Acc>* starts) {
+static std::vector<FoldChunk> describe(const std::vector<float>& e) {
   const size_t n = e.size();
   const size_t nc = (n + kFoldChunk - 1) / kFoldChunk;
   std::vector<double> pre(nc);
@@ -38,8 +40,7 @@ static Acc chunked(const std::vector<float>& e, uint64_t* fallbacks, std::vector
     pre[j] = acc;
     for (size_t i = j * kFoldChunk; i < std::min(n, (j + 1) * kFoldChunk); ++i) acc += (double)e[i];
   }
-  if (starts) starts->assign(nc, 0);
-  Acc s = 0;
+  std::vector<FoldChunk> out(nc);
   for (size_t j = 0; j < nc; ++j) {
     FoldChunk ch{};
     const Acc ps = (Acc)pre[j];
@@ -55,13 +56,63 @@ static Acc chunked(const std::vector<float>& e, uint64_t* fallbacks, std::vector
       ch.q[c] = q;
     }
     ch.clean = ~bad & ((1u << kFoldCands) - 1u);
+    out[j] = ch;
+  }
+  return out;
+}
+
+// Sequential application with term-by-term fallback; `starts` receives the
+// exact value before every chunk.
+template <typename Acc>
+static Acc chunked(const std::vector<float>& e, uint64_t* fallbacks, std::vector<Acc>* starts) {
+  const size_t n = e.size();
+  const std::vector<FoldChunk> chs = describe<Acc>(e);
+  const size_t nc = chs.size();
+  if (starts) starts->assign(nc, 0);
+  Acc s = 0;
+  for (size_t j = 0; j < nc; ++j) {
     if (starts) (*starts)[j] = s;
     Acc out;
-    if (fold_apply(s, ch, &out)) {
+    if (fold_apply(s, chs[j], &out)) {
       s = out;
     } else {
       ++*fallbacks;
       for (size_t i = j * kFoldChunk; i < std::min(n, (j + 1) * kFoldChunk); ++i) s = s + (Acc)e[i];
+    }
+  }
+  return s;
+}
+
+// The wave's procedure: from s, up to 64 chunks at once through the prefix
+// sums of fold_chunk_q while fold_run_fits holds; the first chunk that does
+// not fit (or any chunk while s is not normal) is folded term by term.
+template <typename Acc>
+static Acc chunked_runs(const std::vector<float>& e, std::vector<Acc>* starts) {
+  const size_t n = e.size();
+  const std::vector<FoldChunk> chs = describe<Acc>(e);
+  const size_t nc = chs.size();
+  if (starts) starts->assign(nc, 0);
+  Acc s = 0;
+  size_t j = 0;
+  while (j < nc) {
+    const size_t cnt = std::min<size_t>(64, nc - j);
+    size_t b = 0;
+    if (fold_is_normal_positive(s)) {
+      const uint64_t m = fold_units(s);
+      uint64_t P = 0;
+      for (; b < cnt; ++b) {
+        const uint64_t Q = fold_chunk_q(s, chs[j + b]);
+        if (Q == kFoldBad || !fold_run_fits<Acc>(m, P + Q)) break;
+        if (starts) (*starts)[j + b] = fold_with_units(s, m + P);
+        P += Q;
+      }
+      if (b > 0) s = fold_with_units(s, m + P);
+    }
+    j += b;
+    if (b < cnt) {
+      if (starts) (*starts)[j] = s;
+      for (size_t i = j * kFoldChunk; i < std::min(n, (j + 1) * kFoldChunk); ++i) s = s + (Acc)e[i];
+      ++j;
     }
   }
   return s;
@@ -123,6 +174,21 @@ int main() {
     const double c = serial<double>(e), d = chunked<double>(e, &fb64, nullptr);
     if (!same(c, d)) {
       std::printf("MISMATCH f64 %s n=%zu serial=%a chunked=%a\n", what, e.size(), c, d);
+      ++bad;
+    }
+    // runs of 64 chunks, with the chunk starts
+    std::vector<float> s32a, s32b;
+    std::vector<double> s64a, s64b;
+    uint64_t unused = 0;
+    (void)chunked<float>(e, &unused, &s32a);
+    (void)chunked<double>(e, &unused, &s64a);
+    const float r32 = chunked_runs<float>(e, &s32b);
+    const double r64 = chunked_runs<double>(e, &s64b);
+    bool starts_ok = s32a.size() == s32b.size() && s64a.size() == s64b.size();
+    for (size_t j = 0; starts_ok && j < s32a.size(); ++j) starts_ok = same(s32a[j], s32b[j]);
+    for (size_t j = 0; starts_ok && j < s64a.size(); ++j) starts_ok = same(s64a[j], s64b[j]);
+    if (!same(a, r32) || !same(c, r64) || !starts_ok) {
+      std::printf("MISMATCH runs %s n=%zu\n", what, e.size());
       ++bad;
     }
   };
