@@ -60,12 +60,18 @@ constexpr int kCandWaves = kCandThreads / kWave;
 constexpr uint32_t kCandLdsMax = 160 * 1024;
 
 constexpr uint32_t kCandCells = 6561;  // grid cells per subspace (encode anchors), 9^4
-constexpr uint32_t kCandAnchors = 2;   // anchor codewords per cell
+// Anchor codewords per grid cell: three for encode, two for the first Lloyd
+// iteration, whose block also holds the sort-tile counts (two blocks per CU
+// either way).
+template <bool TOKENS>
+constexpr uint32_t cand_anchors() { return TOKENS ? 3u : 2u; }
+constexpr uint32_t kCandAnchorsMax = 3;
 
 // LDS layout of cand_kernel, shared by the host launcher:
 //   lcb [K][DP] f32 | lsamp [K][8] u32: the value bits of row entries
-//   0, 7, 15, ..., 55 (all-ones past the row) | encode only:
-//   lanc [cells][2] u8 anchors, lgrid [2][8] f32 (cell origin, cells per unit) |
+//   0, 7, 15, ..., 55 (all-ones past the row) | grid anchors only:
+//   lanc [cells][na] u8 anchors (na = cand_anchors), lgrid [2][8] f32 (cell
+//   origin, cells per unit) |
 //   per wave: gx [64][DP] f32, gbest [64] u64, ga [64] u32 (the anchor's
 //   row offset),
 //   gitem [64 * 8] u16 (lane | item << 6) | lmax, lcnt u32 | training only:
@@ -76,11 +82,11 @@ struct CandLds {
 };
 __host__ __device__ inline uint32_t cand_up16(uint32_t b) { return (b + 15u) & ~15u; }
 __host__ __device__ inline CandLds cand_lds(uint32_t K, uint32_t DP, uint32_t cells = 0,
-                                            uint32_t hist_tiles = 0) {
+                                            uint32_t hist_tiles = 0, uint32_t na = 0) {
   CandLds s;
   s.samp_off = cand_up16(K * DP * 4u);
   s.anc_off = s.samp_off + K * 8u * 4u;
-  s.grid_off = cand_up16(s.anc_off + cells * kCandAnchors);
+  s.grid_off = cand_up16(s.anc_off + cells * na);
   s.wave_off = s.grid_off + (cells ? 64u : 0u);
   s.wave_bytes = 64u * (DP * 4u + 8u + 4u) + 64u * 8u * 2u;
   s.scal_off = s.wave_off + (uint32_t)kCandWaves * s.wave_bytes;
@@ -155,12 +161,12 @@ __global__ __launch_bounds__(kWave) void nbr_build_kernel(const float* __restric
   for (uint32_t j = lane; j < Lr; j += kWave) row[j] = j < L ? keys[j] : cand_pad_key(a);
 }
 
-// Encode anchors of subspace m = blockIdx.y: the bounding box of the
+// Grid anchors of subspace m = blockIdx.y: the bounding box of the
 // codewords (lo, hi per dimension), G cells per dimension, and for each cell
-// the two codewords nearest its centre (any choice is valid; nearness only
-// keeps the candidate sets small).  grid[m] = {lo[8], G / (hi - lo)[8]},
-// anchors[m][cell][0..1].
-template <int D>
+// the NA codewords nearest its centre (any choice is valid; nearness only
+// keeps the candidate sets small; with K < NA the nearest repeats).
+// grid[m] = {lo[8], G / (hi - lo)[8]}, anchors[m][cell][0 .. NA).
+template <int D, uint32_t NA>
 __global__ __launch_bounds__(kBlock) void grid_build_kernel(const float* __restrict__ cb,
                                                             uint8_t* __restrict__ anchors,
                                                             float* __restrict__ grid,
@@ -197,8 +203,13 @@ __global__ __launch_bounds__(kBlock) void grid_build_kernel(const float* __restr
     r /= G;
     ctr[k] = box[k] + ((float)ck + 0.5f) / (box[D + k] > 0.0f ? box[D + k] : 1.0f);
   }
-  float best = __builtin_inff(), second = __builtin_inff();
-  uint32_t bi = 0, si = 0;
+  float bd[NA];
+  uint32_t bc[NA];
+#pragma unroll
+  for (uint32_t q = 0; q < NA; ++q) {
+    bd[q] = __builtin_inff();
+    bc[q] = 0;
+  }
   for (uint32_t c = 0; c < K; ++c) {
     float d = 0.0f;
 #pragma unroll
@@ -206,18 +217,23 @@ __global__ __launch_bounds__(kBlock) void grid_build_kernel(const float* __restr
       const float u = ctr[k] - lcb[c * D + k];
       d = d + u * u;
     }
-    if (d < best) {
-      second = best;
-      si = bi;
-      best = d;
-      bi = c;
-    } else if (d < second) {
-      second = d;
-      si = c;
+    // Insert into the ascending list of the NA nearest (strict <: the
+    // earlier index stays ahead on ties).
+#pragma unroll
+    for (int q = (int)NA - 1; q >= 0; --q) {
+      if (d < bd[q]) {
+        if (q + 1 < (int)NA) {
+          bd[q + 1] = bd[q];
+          bc[q + 1] = bc[q];
+        }
+        bd[q] = d;
+        bc[q] = c;
+      }
     }
   }
-  anchors[((uint64_t)m * cells + cell) * kCandAnchors] = (uint8_t)bi;
-  anchors[((uint64_t)m * cells + cell) * kCandAnchors + 1] = (uint8_t)(K > 1 ? si : bi);
+#pragma unroll
+  for (uint32_t q = 0; q < NA; ++q)
+    anchors[((uint64_t)m * cells + cell) * NA + q] = (uint8_t)(q < K ? bc[q] : bc[0]);
 }
 
 // Inclusive sum over the 64 lanes of a wave with DPP moves: shifts of 1, 2,
@@ -275,7 +291,8 @@ __global__ __launch_bounds__(kCandThreads) void cand_kernel(
   }
   const uint32_t tiles = TOKENS ? 0u : chunk / kSortTile;  // the chunk is whole tiles
   const uint32_t Kw = (K + 1u) / 2u;                       // u16 pairs per tile
-  const CandLds lay = cand_lds(K, DP, GRID ? cells : 0u, tiles);
+  constexpr uint32_t NA = cand_anchors<TOKENS>();
+  const CandLds lay = cand_lds(K, DP, GRID ? cells : 0u, tiles, GRID ? NA : 0u);
   uint8_t* base = reinterpret_cast<uint8_t*>(lds);
   float* lcb = lds;
   uint32_t* lsamp = reinterpret_cast<uint32_t*>(base + lay.samp_off);
@@ -315,8 +332,8 @@ __global__ __launch_bounds__(kCandThreads) void cand_kernel(
   const uint32_t rs = Lr;
   for (uint32_t j = t; j < K * 8; j += blockDim.x) lsamp[j] = cand_sample(nbm + (j / 8) * Lr, L, j % 8);
   if constexpr (GRID) {
-    const uint8_t* am = anchors + (uint64_t)m * cells * kCandAnchors;
-    for (uint32_t j = t; j < cells * kCandAnchors; j += blockDim.x) lanc[j] = am[j];
+    const uint8_t* am = anchors + (uint64_t)m * cells * NA;
+    for (uint32_t j = t; j < cells * NA; j += blockDim.x) lanc[j] = am[j];
     if (t < 16) lgrid[t] = grid[m * 16 + t];
   }
   __syncthreads();
@@ -368,7 +385,7 @@ __global__ __launch_bounds__(kCandThreads) void cand_kernel(
         cell = cell * G + (uint32_t)f;
       }
       cell = cell < cells ? cell : 0u;
-      a = lanc[cell * kCandAnchors];
+      a = lanc[cell * NA];
     }
     bool deferred = valid && (all_deferred || a >= K);
     uint32_t nit = 0;
@@ -377,14 +394,17 @@ __global__ __launch_bounds__(kCandThreads) void cand_kernel(
       float ca[D];
       load_padded<D>(lcb + a * DP, ca);
       U2 = exact_l2sq<D>(x, ca);
-      if constexpr (GRID) {  // the nearer of the cell's two anchors
-        const uint32_t a2 = lanc[cell * kCandAnchors + 1];
-        float cb2[D];
-        load_padded<D>(lcb + a2 * DP, cb2);
-        const float V2 = exact_l2sq<D>(x, cb2);
-        if (V2 < U2) {
-          U2 = V2;
-          a = a2;
+      if constexpr (GRID) {  // the nearest of the cell's anchors
+#pragma unroll
+        for (uint32_t q = 1; q < NA; ++q) {
+          const uint32_t a2 = lanc[cell * NA + q];
+          float cb2[D];
+          load_padded<D>(lcb + a2 * DP, cb2);
+          const float V2 = exact_l2sq<D>(x, cb2);
+          if (V2 < U2) {
+            U2 = V2;
+            a = a2;
+          }
         }
       }
       if (!cand_tame(U2)) {  // NaN, inf or too large for the bound arithmetic

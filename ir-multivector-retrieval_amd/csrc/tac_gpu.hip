@@ -261,7 +261,7 @@ int raise_lds(const void *fn, uint32_t bytes, uint32_t cells) {
   std::lock_guard<std::mutex> g(mu);
   for (const void *f : raised)
     if (f == fn) return TAC_OK;
-  const uint32_t most = cand_lds(kCandMaxK, 8, cells, kCandHistTiles).total;
+  const uint32_t most = cand_lds(kCandMaxK, 8, cells, kCandHistTiles, kCandAnchorsMax).total;
   const hipError_t err = hipFuncSetAttribute(fn, hipFuncAttributeMaxDynamicSharedMemorySize,
                                             (int)(most > bytes ? most : bytes));
   if (err != hipSuccess) return hip_status("hipFuncSetAttribute(candidate kernel)", err);
@@ -307,7 +307,8 @@ struct Launch {
       G = cand_grid_side(D);
       cells = 1;
       for (int k = 0; k < D; ++k) cells *= G;
-      grid_build_kernel<D><<<dim3((cells + kBlock - 1) / kBlock, M), kBlock, 0, s>>>(
+      grid_build_kernel<D, cand_anchors<false>()><<<dim3((cells + kBlock - 1) / kBlock, M), kBlock,
+                                                     0, s>>>(
           cb, anchors, grid, K, G, cells);
     }
     // About 1,024 blocks over all subspaces; a chunk is whole sort tiles
@@ -317,7 +318,8 @@ struct Launch {
     chunk = (chunk + kSortTile - 1) / kSortTile * kSortTile;
     chunk = std::min<uint64_t>(chunk, (uint64_t)kCandHistTiles * kSortTile);
     const uint64_t nblk = (n + chunk - 1) / chunk;
-    const CandLds lay = cand_lds(K, Pad<D>::value, cells, (uint32_t)(chunk / kSortTile));
+    const CandLds lay = cand_lds(K, Pad<D>::value, cells, (uint32_t)(chunk / kSortTile),
+                                 GRID ? cand_anchors<false>() : 0u);
     if (int st = raise_lds((const void *)cand_kernel<D, GRID, false, uint16_t>, lay.total, cells))
       return st;
     cand_kernel<D, GRID, false, uint16_t><<<dim3((unsigned)nblk, M), kCandThreads, lay.total,
@@ -350,9 +352,10 @@ struct Launch {
     uint32_t cells = 1;
     for (int k = 0; k < D; ++k) cells *= G;
     nbr_build_kernel<D><<<dim3(K, M), kWave, 0, s>>>(cb, nbr, defer_count, nullptr, K, L);
-    grid_build_kernel<D><<<dim3((cells + kBlock - 1) / kBlock, M), kBlock, 0, s>>>(
+    grid_build_kernel<D, cand_anchors<true>()><<<dim3((cells + kBlock - 1) / kBlock, M), kBlock,
+                                                  0, s>>>(
         cb, anchors, grid, K, G, cells);
-    const CandLds lay = cand_lds(K, Pad<D>::value, cells);
+    const CandLds lay = cand_lds(K, Pad<D>::value, cells, 0, cand_anchors<true>());
     if (int st = raise_lds((const void *)cand_kernel<D, true, true, CodeT>, lay.total, cells))
       return st;
     // Chunks of 8,192 rows; the M blocks of a chunk run on one XCD, so a row
@@ -581,7 +584,8 @@ int train_core(DeviceState &ds, hipStream_t s, const float *d_x, uint64_t n, uin
   const char *full_env = getenv("TAC_GPU_FULL_SEARCH");
   const uint32_t Lc = K >= 2 ? std::min<uint32_t>(kCandList, K - 1) : 0;
   const bool cand_ok = !(full_env && full_env[0] == '1') && K >= 2 && K <= kCandMaxK &&
-                       cand_lds(K, DP, kCandCells, kCandHistTiles).total <= kCandLdsMax &&
+                       cand_lds(K, DP, kCandCells, kCandHistTiles, kCandAnchorsMax).total <=
+                           kCandLdsMax &&
                        n <= 0xFFFFFFFFull;
   const bool cand = cand_ok && max_iters > 1;
   const bool cand_first = cand_ok && n >= 16384;
@@ -590,7 +594,7 @@ int train_core(DeviceState &ds, hipStream_t s, const float *d_x, uint64_t n, uin
        (st = ensure(ds, ds.cand_defer, (size_t)2 * M * n * sizeof(uint32_t))) ||
        (st = ensure(ds, ds.cand_count, (size_t)M * sizeof(uint32_t)))))
     return st;
-  if (cand_first && ((st = ensure(ds, ds.cand_anchor, (size_t)M * kCandCells * kCandAnchors)) ||
+  if (cand_first && ((st = ensure(ds, ds.cand_anchor, (size_t)M * kCandCells * kCandAnchorsMax)) ||
                      (st = ensure(ds, ds.cand_grid, (size_t)M * 16 * sizeof(float)))))
     return st;
 
@@ -783,7 +787,7 @@ int encode_core(DeviceState &ds, hipStream_t s, const float *d_x, uint64_t n, ui
     if ((st = ensure(ds, ds.cand_nbr, (size_t)M * K * cand_row_len(L) * sizeof(uint32_t))) ||
         (st = ensure(ds, ds.cand_defer, (size_t)2 * M * n * sizeof(uint32_t))) ||
         (st = ensure(ds, ds.cand_count, (size_t)M * sizeof(uint32_t))) ||
-        (st = ensure(ds, ds.cand_anchor, (size_t)M * kCandCells * kCandAnchors)) ||
+        (st = ensure(ds, ds.cand_anchor, (size_t)M * kCandCells * kCandAnchorsMax)) ||
         (st = ensure(ds, ds.cand_grid, (size_t)M * 16 * sizeof(float))))
       return st;
     uint32_t *slices = as<uint32_t>(ds.cand_defer);
