@@ -57,28 +57,15 @@ __global__ __launch_bounds__(256) void kpp_update_kernel(
   __shared__ double part[256 / 64];
   __shared__ float lo_tab[1024];  // bound of ||c_j - c_new||^2 per earlier seed j
   const uint32_t m = blockIdx.y, b = blockIdx.x;
-  if (st[m].err) return;
-  const uint32_t chosen = st[m].chosen;
-  float cv[D];
-  load_padded<D>(xs + ((uint64_t)m * n + chosen) * DP, cv);
-  if (b == 0 && threadIdx.x < (uint32_t)D) cb[((uint64_t)m * K + c) * D + threadIdx.x] = cv[threadIdx.x];
-  for (uint32_t j = threadIdx.x; j < c; j += blockDim.x) {
-    float cj[D];
-#pragma unroll
-    for (int k = 0; k < D; ++k) cj[k] = cb[((uint64_t)m * K + j) * D + k];
-    lo_tab[j] = cand_lower_bound(exact_l2sq<D>(cj, cv), g);
-  }
-  __syncthreads();
   const uint64_t lo = (uint64_t)b * kKppBlock;
   const uint64_t hi = lo + kKppBlock < n ? lo + kKppBlock : n;
   float* wm = w + (uint64_t)m * n;
   uint16_t* sm = src + (uint64_t)m * n;
   const float* xm = xs + (uint64_t)m * n * DP;
-  double acc = 0.0;
-  bool invalid = false;
-  // Each thread owns kPer rows: weights and sources are loaded together, then
-  // only the rows the bound cannot settle load their vectors, so every load
-  // of a thread is in flight at once.
+  // Each thread owns kPer rows: weights and sources are loaded first (they
+  // do not depend on the draw, so they are in flight while the new seed and
+  // its bounds are read), then only the rows the bound cannot settle load
+  // their vectors.
   constexpr uint32_t kPer = kKppBlock / 256;
   float wv[kPer];
   uint32_t sv[kPer];
@@ -93,6 +80,20 @@ __global__ __launch_bounds__(256) void kpp_update_kernel(
       sv[j] = sm[i];
     }
   }
+  if (st[m].err) return;
+  const uint32_t chosen = st[m].chosen;
+  float cv[D];
+  load_padded<D>(xs + ((uint64_t)m * n + chosen) * DP, cv);
+  if (b == 0 && threadIdx.x < (uint32_t)D) cb[((uint64_t)m * K + c) * D + threadIdx.x] = cv[threadIdx.x];
+  for (uint32_t j = threadIdx.x; j < c; j += blockDim.x) {
+    float cj[D];
+#pragma unroll
+    for (int k = 0; k < D; ++k) cj[k] = cb[((uint64_t)m * K + j) * D + k];
+    lo_tab[j] = cand_lower_bound(exact_l2sq<D>(cj, cv), g);
+  }
+  __syncthreads();
+  double acc = 0.0;
+  bool invalid = false;
 #pragma unroll
   for (uint32_t j = 0; j < kPer; ++j) {
     const uint64_t i = lo + j * 256 + threadIdx.x;
