@@ -19,10 +19,11 @@
 //   smallest index among its ties, so that minimum is c*.
 //
 // Anchors.  Lloyd iterations after the first anchor each vector at its
-// previous code.  Encode anchors it at the nearer of the two codewords
-// nearest the centre of its cell in a grid over the codebook's bounding box
-// (grid_build_kernel); a vector outside the box takes the nearest cell.  The rule above holds for
-// any anchor, so the anchor only decides how many candidates are evaluated.
+// previous code.  The first iteration and encode anchor it at the nearest of
+// the codewords nearest the centre of its cell (cand_anchors of them) in a
+// grid over the codebook's bounding box (grid_build_kernel); a vector
+// outside the box takes the nearest cell.  The rule above holds for any
+// anchor, so the anchor only decides how many candidates are evaluated.
 //
 // Neighbour tables.  After every update, nbr_build_kernel sorts, for each
 // codeword a, the other codewords by lo(a, c) and keeps the first L of them

@@ -28,7 +28,7 @@ namespace tacgpu {
 
 constexpr uint32_t kCandList = 64;  // neighbours kept per codeword
 constexpr uint32_t kCandItem = 8;   // candidates per work item
-constexpr uint32_t kCandMaxK = 256; // codeword ids fit the key's low 8 bits
+constexpr uint32_t kCandMaxK = 256; // codeword ids fit the key's low 12 bits as id << 4
 
 TAC_HD inline uint32_t cand_f2u(float f) {
   uint32_t u;
