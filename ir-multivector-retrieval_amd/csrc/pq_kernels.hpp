@@ -641,7 +641,35 @@ __global__ __launch_bounds__(kBlock) void scatter_kernel(
   }
 }
 
-// Step 4: one wave per (subspace, cluster).  The wave streams the cluster's
+// Step 4a: the fold's launch order.  Clusters of all subspaces are binned by
+// size (bin = count / unit, 256 bins, the last taking every larger cluster)
+// and listed from the largest bin down, so the longest serial chains of
+// step 4 start first and the short ones fill the SIMDs around them.  The
+// sums do not depend on the order; within a bin it follows the atomics.
+// One block of 1024 threads.
+constexpr uint32_t kFoldOrderBins = 256;
+__global__ __launch_bounds__(1024) void fold_order_kernel(const uint32_t* __restrict__ counts,
+                                                          uint32_t* __restrict__ order, uint32_t E,
+                                                          uint32_t unit) {
+  __shared__ uint32_t bins[kFoldOrderBins];
+  __shared__ uint32_t wsum[1024 / kWave];
+  const uint32_t t = threadIdx.x;
+  if (t < kFoldOrderBins) bins[t] = 0;
+  __syncthreads();
+  auto bin_of = [&](uint32_t cnt) {  // 0 = the largest clusters
+    const uint32_t b = cnt / unit;
+    return kFoldOrderBins - 1u - (b < kFoldOrderBins - 1u ? b : kFoldOrderBins - 1u);
+  };
+  for (uint32_t j = t; j < E; j += blockDim.x) atomicAdd(&bins[bin_of(counts[j])], 1u);
+  __syncthreads();
+  const uint32_t first = block_exclusive_scan(t < kFoldOrderBins ? bins[t] : 0u, wsum);
+  __syncthreads();
+  if (t < kFoldOrderBins) bins[t] = first;
+  __syncthreads();
+  for (uint32_t j = t; j < E; j += blockDim.x) order[atomicAdd(&bins[bin_of(counts[j])], 1u)] = j;
+}
+
+// Step 4: one wave per (subspace, cluster), in the order of step 4a.  The wave streams the cluster's
 // contiguous records with coalesced loads (kFoldBatch x 64 records in
 // flight, staged through LDS dimension-major) and lanes 0..D-1 fold
 // dimension d in ascending vector order from 0.0f, then write
@@ -651,14 +679,16 @@ template <int D>
 __global__ __launch_bounds__(kWave) void fold_kernel(
     const float* __restrict__ sorted, const uint32_t* __restrict__ counts,
     const uint32_t* __restrict__ start, float* __restrict__ cb,
-    const uint32_t* __restrict__ done, uint64_t n, uint32_t K) {
+    const uint32_t* __restrict__ done, const uint32_t* __restrict__ order, uint64_t n,
+    uint32_t K) {
   constexpr int DP = Pad<D>::value;
   constexpr uint32_t U = kFoldBatch;
   // Padded: the D columns start on distinct banks, and the fold's reads of
   // the next 32 members stay inside the column.
   constexpr uint32_t kCol = U * kWave + 36;
   __shared__ __attribute__((aligned(16))) float buf[kCol * DP];
-  const uint32_t m = blockIdx.x / K, c = blockIdx.x % K;
+  const uint32_t id = order[blockIdx.x];
+  const uint32_t m = id / K, c = id % K;
   if (done[m]) return;
   const uint32_t cnt = counts[(uint64_t)m * K + c];
   if (cnt == 0) return;

@@ -88,7 +88,8 @@ struct DeviceState {
   // training / encode workspace
   Buffer xs, codes, e, hist, counts, start, sorted, flags, scal, trace, io_in, io_out, io_cb,
       io_init, counter, kpp_state, kpp_w, kpp_bsum, kpp_bad, status, io_aux, io_out2, scan_sums,
-      io_x1, io_x2, io_x3, crc_tx, fold_pre, fold_chunks, cand_nbr, cand_defer, cand_count, cand_anchor, cand_grid, kpp_src;
+      io_x1, io_x2, io_x3, crc_tx, fold_pre, fold_chunks, cand_nbr, cand_defer, cand_count, cand_anchor, cand_grid, kpp_src,
+      fold_order;
   // token-aware clustering
   Buffer tac_v, tac_idx, tac_offs, tac_G, tac_spreads, tac_w, tac_e, tac_code, tac_sorted,
       tac_tsum, tac_hist, tac_counts, tac_start, tac_C, tac_pre, tac_fch, tac_st, tac_bad,
@@ -404,9 +405,12 @@ struct Launch {
     kpp_update_kernel<D><<<dim3(NB, M), 256, 0, s>>>(xs, w, src, bsum, bad, st, cb, n, K, c, NB);
   }
   static void fold(const float *sorted, const uint32_t *counts, const uint32_t *start,
-                   float *cb, const uint32_t *done, uint64_t n, uint32_t M, uint32_t K,
-                   hipStream_t s) {
-    fold_kernel<D><<<M * K, kWave, 0, s>>>(sorted, counts, start, cb, done, n, K);
+                   float *cb, const uint32_t *done, uint32_t *order, uint64_t n, uint32_t M,
+                   uint32_t K, hipStream_t s) {
+    // Bins of 1/32 of the mean cluster size.
+    const uint32_t unit = (uint32_t)std::max<uint64_t>(1, n / K / 32);
+    fold_order_kernel<<<1, 1024, 0, s>>>(counts, order, M * K, unit);
+    fold_kernel<D><<<M * K, kWave, 0, s>>>(sorted, counts, start, cb, done, order, n, K);
   }
   static void reseed(const float *xs, float *e, const uint32_t *counts, float *cb,
                      uint32_t *empties, const uint32_t *done, uint64_t n, uint32_t M, uint32_t K,
@@ -566,6 +570,7 @@ int train_core(DeviceState &ds, hipStream_t s, const float *d_x, uint64_t n, uin
   if ((st = ensure(ds, ds.hist, (size_t)M * T * K * sizeof(uint32_t)))) return st;
   if ((st = ensure(ds, ds.counts, (size_t)M * K * sizeof(uint32_t)))) return st;
   if ((st = ensure(ds, ds.start, (size_t)M * K * sizeof(uint32_t)))) return st;
+  if ((st = ensure(ds, ds.fold_order, (size_t)M * K * sizeof(uint32_t)))) return st;
   const uint32_t G = T < kScanRanges ? T : kScanRanges;
   const uint32_t nfc = (uint32_t)((n + kFoldChunk - 1) / kFoldChunk);  // wcss chunks
   if ((st = ensure(ds, ds.fold_pre, (size_t)M * nfc * sizeof(double)))) return st;
@@ -683,7 +688,8 @@ int train_core(DeviceState &ds, hipStream_t s, const float *d_x, uint64_t n, uin
     DISPATCH_D_ST(D, scatter(xs, codes, hist, start, sorted, done, n, M, K, T, s));
     if (st) return st;
     LAUNCH_TRY("scatter_kernel");
-    DISPATCH_D(D, fold(sorted, counts, start, out.cb, done, n, M, K, s));
+    DISPATCH_D(D, fold(sorted, counts, start, out.cb, done, as<uint32_t>(ds.fold_order), n, M, K,
+                       s));
     LAUNCH_TRY("fold_kernel");
     if (check || (want_wcss && t + 1 == max_iters)) {
       const uint32_t fgrid = (nfc + kBlock / kWave - 1) / (kBlock / kWave);
@@ -950,7 +956,7 @@ int tac_gpu_release_workspace(void) {
                     &ds->tac_probs, &ds->tac_tiles, &ds->tac_chl, &ds->tac_cprob,
                     &ds->tac_inv,   &ds->tac_rsum, &ds->tac_ranges, &ds->cand_nbr,
                     &ds->cand_defer, &ds->cand_count, &ds->cand_anchor, &ds->cand_grid,
-                    &ds->kpp_src};
+                    &ds->kpp_src,   &ds->fold_order};
   ds->crc_tx_ready = false;
   for (Buffer *b : bufs) {
     if (b->ptr) HIP_TRY(hipFree(b->ptr));
