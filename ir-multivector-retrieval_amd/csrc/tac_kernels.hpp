@@ -618,10 +618,12 @@ __global__ void tac_scatter_kernel(const uint32_t* __restrict__ code,
 // Cluster sums and update (kmeans.zig:177-198): one wave per global cluster,
 // lane = dimension (PER dimensions per lane), members folded in ascending row
 // order from 0; centroid = sum * fl(1 / fl(count)).  Empty clusters are left
-// to the reseed kernel.  Member rows are loaded kTacFoldBatch at a time, and
-// the next batch's row indices are read while the current batch is added.
+// to the reseed kernel.  Member rows are loaded tac_fold_batch(PER) at a time
+// (one member per lane for dim <= 64, so a large cluster's chain waits on one
+// gather per 64 members), and the next batch's row indices are read while
+// the current batch is added.
 // ---------------------------------------------------------------------------
-constexpr uint32_t kTacFoldBatch = 16;
+__host__ __device__ constexpr uint32_t tac_fold_batch(int per) { return per == 1 ? 64u : per == 2 ? 32u : 16u; }
 
 template <int PER>
 __global__ __launch_bounds__(256) void tac_fold_kernel(
@@ -629,6 +631,7 @@ __global__ __launch_bounds__(256) void tac_fold_kernel(
     const uint32_t* __restrict__ counts, const uint32_t* __restrict__ start,
     const uint32_t* __restrict__ cprob, const TacProblem* __restrict__ probs,
     const uint32_t* __restrict__ done, float* __restrict__ C, uint32_t kappa, uint32_t dim) {
+  constexpr uint32_t kTacFoldBatch = tac_fold_batch(PER);
   const uint32_t g = blockIdx.x * (256 / kWave) + threadIdx.x / kWave, lane = threadIdx.x % kWave;
   if (g >= kappa) return;
   const uint32_t p = cprob[g];
