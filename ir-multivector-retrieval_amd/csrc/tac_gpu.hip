@@ -1801,7 +1801,10 @@ int tac_cluster_core(DeviceState &ds, hipStream_t s, const uint32_t *ids, uint64
     for (uint64_t i = 0; i < N; ++i) idx[cur[ids[i]]++] = (uint32_t)i;
   }
   const size_t vbytes = (size_t)N * dim * sizeof(float);
-  if ((st = ensure(ds, ds.tac_v, vbytes)) || (st = ensure(ds, ds.tac_G, vbytes)) ||
+  // G carries tac_spread_pad_floats of slack: the spread kernel's full-batch
+  // loads run up to one batch past a token's last row
+  const size_t gbytes = vbytes + tac_spread_pad_floats(dim) * sizeof(float);
+  if ((st = ensure(ds, ds.tac_v, vbytes)) || (st = ensure(ds, ds.tac_G, gbytes)) ||
       (st = upload_vec(ds, ds.tac_idx, idx, s)) || (st = upload_vec(ds, ds.tac_offs, offs, s)) ||
       (st = ensure(ds, ds.tac_spreads, nd * sizeof(float))))
     return st;
@@ -1813,9 +1816,10 @@ int tac_cluster_core(DeviceState &ds, hipStream_t s, const uint32_t *ids, uint64
   LAUNCH_TRY("tac_gather_kernel");
   uint32_t max_n = 0;
   for (uint64_t j = 0; j < nd; ++j) max_n = freqs[j] > max_n ? freqs[j] : max_n;
-  const uint32_t ninv = max_n < kTacInvMax ? max_n : kTacInvMax;
+  const uint64_t ninv = (uint64_t)max_n + kTacSpreadBatch;  // one batch of slack, as for G
   if ((st = ensure(ds, ds.tac_inv, (size_t)ninv * sizeof(float)))) return st;
-  tac_inv_table_kernel<<<(ninv + 255) / 256, 256, 0, s>>>(as<float>(ds.tac_inv), ninv);
+  tac_inv_table_kernel<<<(unsigned)((ninv + 255) / 256), 256, 0, s>>>(as<float>(ds.tac_inv),
+                                                                  (uint32_t)ninv);
   LAUNCH_TRY("tac_inv_table_kernel");
   {
     const uint32_t *doffs = as<uint32_t>(ds.tac_offs);

@@ -128,15 +128,30 @@ __global__ __launch_bounds__(256) void tac_gather_kernel(const float* __restrict
 // dimension (PER dimensions per lane); the trace folds the dimensions in
 // order and is divided by the f32 row count.  The f32 count after i rows is
 // min(i, 2^24) exactly (count + 1 stops growing at 2^24), so its reciprocal
-// comes from a table inv[i - 1] = fl(1 / min(i, 2^24)); rows and reciprocals
-// are loaded kTacSpreadBatch at a time, one batch ahead of the serial updates.
+// comes from a table inv[i - 1] = fl(1 / min(i, 2^24)).
+//
+// The largest token's serial chain is the whole kernel's time, and a lone
+// wave issues about one instruction per four cycles, so the loop is written
+// for the fewest instructions per row: rows and reciprocals are loaded
+// kTacSpreadBatch at a time into two register buffers used in turn, with no
+// bounds test on a full batch (G carries tac_spread_pad_floats of slack and
+// the table one batch of extra entries, so a batch may run past the token's
+// last row into memory it owns), and the six operations of each row's update
+// run without branches.  Only the token's last, partial batch tests the row
+// count.  Lanes past dim read neighbouring floats and never store them.
 // ---------------------------------------------------------------------------
 constexpr uint32_t kTacSpreadBatch = 32;
 constexpr uint32_t kTacInvMax = 1u << 24;
 
+// Floats of slack G needs past its last row for the spread kernel's loads.
+__host__ __device__ constexpr size_t tac_spread_pad_floats(uint32_t dim) {
+  return (size_t)kTacSpreadBatch * dim + 64u * ((dim + 63u) / 64u);
+}
+
 __global__ void tac_inv_table_kernel(float* __restrict__ inv, uint32_t n) {
   const uint32_t i = blockIdx.x * blockDim.x + threadIdx.x;
-  if (i < n) inv[i] = 1.0f / (float)(i + 1);  // i + 1 <= 2^24: exact in f32
+  // i + 1 <= 2^24 is exact in f32
+  if (i < n) inv[i] = 1.0f / (float)(i < kTacInvMax ? i + 1u : kTacInvMax);
 }
 
 template <int PER>
@@ -158,46 +173,87 @@ __global__ __launch_bounds__(kWave) void tac_spread_kernel(const float* __restri
     mean[u] = 0.0f;
     m2[u] = 0.0f;
   }
-  // double-buffered: batch q0 + B is in flight while batch q0 is folded
   constexpr uint32_t B = kTacSpreadBatch;
-  float nx[B][PER], niv[B];
-  auto load = [&](uint32_t q0, float (&x)[B][PER], float (&v)[B]) {
+  const float* gp = G + (uint64_t)lo * dim + lane;  // this lane's float of the next batch's row 0
+  const float* ip = inv;                            // reciprocal for the next batch's row 0
+  auto load = [&](float (&x)[B][PER], float (&v)[B]) {
+    const float* p = gp;
 #pragma unroll
     for (uint32_t b = 0; b < B; ++b) {
-      const uint32_t r = q0 - lo + b;  // rows folded before this one
-      const bool in = q0 + b < hi;
-      v[b] = in ? inv[r < kTacInvMax ? r : kTacInvMax - 1] : 0.0f;
+      v[b] = ip[b];
 #pragma unroll
-      for (int u = 0; u < PER; ++u) {
-        const uint32_t d = lane + 64u * u;
-        x[b][u] = (in && d < dim) ? G[(uint64_t)(q0 + b) * dim + d] : 0.0f;
-      }
+      for (int u = 0; u < PER; ++u) x[b][u] = p[64u * u];
+      p += dim;
+    }
+    gp += (uint64_t)B * dim;
+    ip += B;
+  };
+  auto fold_row = [&](const float (&x)[PER], float iv) {
+#pragma unroll
+    for (int u = 0; u < PER; ++u) {
+      const float old = mean[u];
+      const float delta = x[u] - old;
+      mean[u] = old + delta * iv;
+      m2[u] = m2[u] + delta * (x[u] - mean[u]);
     }
   };
-  load(lo, nx, niv);
-  for (uint32_t q0 = lo; q0 < hi; q0 += B) {
-    const uint32_t nb = hi - q0 < B ? hi - q0 : B;
-    float xv[B][PER], iv[B];
+  // A full batch issues row b's mean update beside row b - 1's m2 update (the
+  // same operations on the same operands as fold_row), so no operation waits
+  // on the one issued just before it.
+  auto fold = [&](const float (&x)[B][PER], const float (&v)[B]) {
+    float dp[PER];  // row b - 1's delta
 #pragma unroll
-    for (uint32_t b = 0; b < B; ++b) {
-      iv[b] = niv[b];
-#pragma unroll
-      for (int u = 0; u < PER; ++u) xv[b][u] = nx[b][u];
+    for (int u = 0; u < PER; ++u) {
+      dp[u] = x[0][u] - mean[u];
+      mean[u] = mean[u] + dp[u] * v[0];
     }
-    if (q0 + B < hi) load(q0 + B, nx, niv);
 #pragma unroll
-    for (uint32_t b = 0; b < B; ++b) {
-      if (b < nb) {
+    for (uint32_t b = 1; b < B; ++b) {
 #pragma unroll
-        for (int u = 0; u < PER; ++u) {
-          const float x = xv[b][u];
-          const float old = mean[u];
-          const float delta = x - old;
-          mean[u] = old + delta * iv[b];
-          m2[u] = m2[u] + delta * (x - mean[u]);
-        }
+      for (int u = 0; u < PER; ++u) {
+        // the scheduling barriers keep each pair together (left to itself
+        // the scheduler regroups the three mean operations back to back)
+        const float d = x[b][u] - mean[u];
+        const float e = x[b - 1][u] - mean[u];  // mean after row b - 1
+        __builtin_amdgcn_sched_barrier(0);
+        const float t = d * v[b];
+        const float q = dp[u] * e;
+        __builtin_amdgcn_sched_barrier(0);
+        mean[u] = mean[u] + t;
+        m2[u] = m2[u] + q;
+        __builtin_amdgcn_sched_barrier(0);
+        dp[u] = d;
       }
     }
+#pragma unroll
+    for (int u = 0; u < PER; ++u) m2[u] = m2[u] + dp[u] * (x[B - 1][u] - mean[u]);
+  };
+  auto fold_tail = [&](const float (&x)[B][PER], const float (&v)[B], uint32_t nb) {
+#pragma unroll
+    for (uint32_t b = 0; b < B; ++b)
+      if (b < nb) fold_row(x[b], v[b]);
+  };
+  // xa holds the batch at the fold position; the next batch goes to xb while
+  // xa is folded, then the roles swap.  A batch is loaded only when the batch
+  // before it is whole, so no load passes row hi - 1 + B.
+  float xa[B][PER], va[B], xb[B][PER], vb[B];
+  uint32_t left = hi - lo;
+  load(xa, va);
+  for (;;) {
+    if (left < B) {
+      fold_tail(xa, va, left);
+      break;
+    }
+    load(xb, vb);
+    fold(xa, va);
+    left -= B;
+    if (left < B) {
+      fold_tail(xb, vb, left);
+      break;
+    }
+    load(xa, va);
+    fold(xb, vb);
+    left -= B;
   }
 #pragma unroll
   for (int u = 0; u < PER; ++u) {

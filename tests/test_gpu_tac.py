@@ -77,6 +77,21 @@ def test_generic_dims(gpu, dim):
            epsilon=4, theta=8)
 
 
+@pytest.mark.parametrize("dim", [64, 96, 191])
+def test_spread_batch_edges(gpu, dim):
+    # token sizes on either side of one, two and three 32-row spread batches
+    # (the last, partial batch is the only one with a row test), in shuffled
+    # input order, with spreads that decide the budgets of tokens >= mu rows
+    sizes = [1, 31, 32, 33, 40, 63, 64, 65, 95, 96, 97, 128, 129]
+    rng = np.random.default_rng(dim)
+    ids = np.concatenate([np.full(c, t, np.uint32) for t, c in enumerate(sizes)])
+    ids = ids[rng.permutation(ids.size)]
+    scale = (1.0 + np.arange(len(sizes), dtype=np.float32))[ids, None]
+    v = (rng.standard_normal((ids.size, dim)).astype(np.float32) * scale).astype(np.float32)
+    _check(ids, v, dim, _feasible_kappa(ids, frac=0.9, mu=20, tau=40, theta=8), 4, mu=20,
+           tau=40, epsilon=4, theta=8)
+
+
 def test_thread_grouping_and_exact_draws(gpu, monkeypatch):
     ids, v = synth.tac_vectors(60_000, 64, 2048, 1.05, 0.15, 8)
     kap = _feasible_kappa(ids)
