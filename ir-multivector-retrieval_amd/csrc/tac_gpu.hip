@@ -1802,7 +1802,8 @@ int tac_cluster_core(DeviceState &ds, hipStream_t s, const uint32_t *ids, uint64
   }
   const size_t vbytes = (size_t)N * dim * sizeof(float);
   // G carries tac_spread_pad_floats of slack: the spread kernel's full-batch
-  // loads run up to one batch past a token's last row
+  // loads run up to one batch past a token's last row, and the fold kernel's
+  // lanes past dim up to 64 * per floats past a row
   const size_t gbytes = vbytes + tac_spread_pad_floats(dim) * sizeof(float);
   if ((st = ensure(ds, ds.tac_v, vbytes)) || (st = ensure(ds, ds.tac_G, gbytes)) ||
       (st = upload_vec(ds, ds.tac_idx, idx, s)) || (st = upload_vec(ds, ds.tac_offs, offs, s)) ||

@@ -677,7 +677,7 @@ __global__ void tac_scatter_kernel(const uint32_t* __restrict__ code,
 // to the reseed kernel.  Member rows are loaded tac_fold_batch(PER) at a time
 // (one member per lane for dim <= 64, so a large cluster's chain waits on one
 // gather per 64 members), and the next batch's row indices are read while
-// the current batch is added.
+// the current batch is added.  Only the last, partial batch tests members.
 // ---------------------------------------------------------------------------
 __host__ __device__ constexpr uint32_t tac_fold_batch(int per) { return per == 1 ? 64u : per == 2 ? 32u : 16u; }
 
@@ -700,9 +700,29 @@ __global__ __launch_bounds__(256) void tac_fold_kernel(
   for (int u = 0; u < PER; ++u) s[u] = 0.0f;
   // lane b < kTacFoldBatch holds member index b of the current batch
   uint32_t idx = lane < kTacFoldBatch && lane < cnt ? mem[lane] : 0u;
+  const float* gl = G + lane;
   for (uint32_t q0 = 0; q0 < cnt; q0 += kTacFoldBatch) {
     const uint32_t nb = cnt - q0 < kTacFoldBatch ? cnt - q0 : kTacFoldBatch;
     float v[kTacFoldBatch][PER];
+    if (nb == kTacFoldBatch) {
+      // a whole batch: no per-member tests, the row index read into a scalar
+      // register.  Lanes past dim read the next row's floats (G carries at
+      // least 64 * PER floats of slack) and never store their sums.
+#pragma unroll
+      for (uint32_t b = 0; b < kTacFoldBatch; ++b) {
+        const uint32_t row = __builtin_amdgcn_readlane(idx, (int)b);
+        const float* rp = gl + (uint64_t)row * dim;
+#pragma unroll
+        for (int u = 0; u < PER; ++u) v[b][u] = rp[kWave * u];
+      }
+      const uint32_t nq = q0 + kTacFoldBatch + lane;
+      idx = lane < kTacFoldBatch && nq < cnt ? mem[nq] : 0u;
+#pragma unroll
+      for (uint32_t b = 0; b < kTacFoldBatch; ++b)
+#pragma unroll
+        for (int u = 0; u < PER; ++u) s[u] = s[u] + v[b][u];
+      continue;
+    }
 #pragma unroll
     for (uint32_t b = 0; b < kTacFoldBatch; ++b) {
       const uint32_t row = __shfl(idx, (int)b, kWave);
