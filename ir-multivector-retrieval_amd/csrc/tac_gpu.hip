@@ -1820,7 +1820,7 @@ int tac_cluster_core(DeviceState &ds, hipStream_t s, const uint32_t *ids, uint64
   const uint64_t ninv = (uint64_t)max_n + kTacSpreadBatch;  // one batch of slack, as for G
   if ((st = ensure(ds, ds.tac_inv, (size_t)ninv * sizeof(float)))) return st;
   tac_inv_table_kernel<<<(unsigned)((ninv + 255) / 256), 256, 0, s>>>(as<float>(ds.tac_inv),
-                                                                  (uint32_t)ninv);
+                                                                  ninv);
   LAUNCH_TRY("tac_inv_table_kernel");
   {
     const uint32_t *doffs = as<uint32_t>(ds.tac_offs);

@@ -148,10 +148,10 @@ __host__ __device__ constexpr size_t tac_spread_pad_floats(uint32_t dim) {
   return (size_t)kTacSpreadBatch * dim + 64u * ((dim + 63u) / 64u);
 }
 
-__global__ void tac_inv_table_kernel(float* __restrict__ inv, uint32_t n) {
-  const uint32_t i = blockIdx.x * blockDim.x + threadIdx.x;
+__global__ void tac_inv_table_kernel(float* __restrict__ inv, uint64_t n) {
+  const uint64_t i = (uint64_t)blockIdx.x * blockDim.x + threadIdx.x;
   // i + 1 <= 2^24 is exact in f32
-  if (i < n) inv[i] = 1.0f / (float)(i < kTacInvMax ? i + 1u : kTacInvMax);
+  if (i < n) inv[i] = 1.0f / (float)(i < kTacInvMax ? (uint32_t)i + 1u : kTacInvMax);
 }
 
 template <int PER>
