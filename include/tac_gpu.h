@@ -39,7 +39,10 @@
  * Arithmetic is the reference's: distances are the unfused left fold of
  * (x_k - c_k)^2, argmin keeps the first index, cluster sums fold members in
  * ascending vector order from 0.0f and the centroid is sum * fl(1/fl(count)).
- * Results are bit-identical to the reference for the same inputs.
+ * Results are bit-identical to the oracle's restatement of the reference for
+ * the same inputs; they equal the reference's wherever that restatement's two
+ * unverifiable assumptions hold: the Zig std PRNG stream behind k-means++
+ * seeding, and 16 f32 lanes in the reference's generic distance path.
  */
 #ifndef TAC_GPU_H
 #define TAC_GPU_H
@@ -301,7 +304,8 @@ typedef struct tac_cluster_params {
  * (vectors_len = n_tokens * dim floats) by token id, computes every token's
  * spread (Welford), allocates the kappa_total centroids over tokens (phases
  * 1-4) and runs kmeans.fit per token with seed ^ token id, all tokens at once
- * on the device.  Outputs, bit-identical to the reference:
+ * on the device.  Outputs, bit-identical to the oracle (and to the reference
+ * under the assumptions stated at the top of this file):
  *   centroids_out   kappa_total * dim, concatenated in token-id order;
  *   assignments_out n_tokens global centroid ids;
  *   kappa_per_token_out[j] for j < n_distinct = max(token id) + 1, written to
@@ -311,7 +315,8 @@ typedef struct tac_cluster_params {
  * length mismatch InvalidThresholds; kappa_total 0 BudgetTooSmall; then the
  * phases' errors, and the first failing token's kmeans error (RngError).
  * dim above 191 is TAC_ERR_UNSUPPORTED (rows are staged in LDS), as is a
- * token given more than 12,288 centroids.
+ * token given more than 12,288 centroids, or a plan of 2^24 or more row
+ * tiles, tokens with centroids or wcss chunks (one block each).
  */
 int tac_cluster_flat(const uint32_t *token_ids, uint64_t n_tokens, const float *vectors,
                      uint64_t vectors_len, uint32_t dim, const tac_cluster_params *params,

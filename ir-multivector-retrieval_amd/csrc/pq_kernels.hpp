@@ -993,9 +993,12 @@ __global__ __launch_bounds__(1024) void reseed_kernel(
     const uint32_t c = elist[q];  // uniform across the block
     float bv = -__builtin_inff();
     uint64_t bi = ~0ull;
+    // vec.argmax starts from values[0] and moves only on a strict >, so a NaN
+    // past index 0 never wins and a NaN at index 0 keeps index 0: NaN terms
+    // are never candidates here, and index 0 is settled after the merge.
     for (uint64_t i = threadIdx.x; i < n; i += blockDim.x) {
       const float v = em[i];
-      if (bi == ~0ull || v > bv) {
+      if ((bi == ~0ull || v > bv) && !(v != v)) {
         bv = v;
         bi = i;
       }
@@ -1022,6 +1025,8 @@ __global__ __launch_bounds__(1024) void reseed_kernel(
           idx = si[q];
         }
       }
+      const float e0 = em[0];
+      if (e0 != e0 || idx == ~0ull) idx = 0;  // values[0] NaN: the scan keeps index 0
       const float* src = xs + ((uint64_t)m * n + idx) * DP;
       for (int k = 0; k < D; ++k) cb[((uint64_t)m * K + c) * D + k] = src[k];
       em[idx] = -__builtin_inff();

@@ -27,6 +27,7 @@
 
 #include <hip/hip_runtime.h>
 
+#include <algorithm>
 #include <chrono>
 #include <cmath>
 #include <cstdio>
@@ -1812,28 +1813,35 @@ int tac_cluster_core(DeviceState &ds, hipStream_t s, const uint32_t *ids, uint64
   HIP_TRY(hipMemcpyAsync(ds.tac_v.ptr, vectors, vbytes, hipMemcpyHostToDevice, s));
   float *G = as<float>(ds.tac_G);
   const uint64_t nf = (uint64_t)N * dim;
-  tac_gather_kernel<<<(unsigned)((nf + 255) / 256), 256, 0, s>>>(
+  // Grids stay far below a dispatch's 2^32 work-items: the gather and the
+  // reciprocal table are grid-stride loops, the spreads run in token slices.
+  constexpr uint64_t kMaxBlocks = 1ull << 20;
+  tac_gather_kernel<<<(unsigned)std::min<uint64_t>((nf + 255) / 256, kMaxBlocks), 256, 0, s>>>(
       as<float>(ds.tac_v), as<uint32_t>(ds.tac_idx), G, N, dim);
   LAUNCH_TRY("tac_gather_kernel");
   uint32_t max_n = 0;
   for (uint64_t j = 0; j < nd; ++j) max_n = freqs[j] > max_n ? freqs[j] : max_n;
   const uint64_t ninv = (uint64_t)max_n + kTacSpreadBatch;  // one batch of slack, as for G
   if ((st = ensure(ds, ds.tac_inv, (size_t)ninv * sizeof(float)))) return st;
-  tac_inv_table_kernel<<<(unsigned)((ninv + 255) / 256), 256, 0, s>>>(as<float>(ds.tac_inv),
-                                                                  ninv);
+  tac_inv_table_kernel<<<(unsigned)std::min<uint64_t>((ninv + 255) / 256, kMaxBlocks), 256, 0,
+                         s>>>(as<float>(ds.tac_inv), ninv);
   LAUNCH_TRY("tac_inv_table_kernel");
   {
     const uint32_t *doffs = as<uint32_t>(ds.tac_offs);
     const float *dinv = as<float>(ds.tac_inv);
     float *dsp = as<float>(ds.tac_spreads);
     const size_t lds = dim * sizeof(float);
-    if (per == 1)
-      tac_spread_kernel<1><<<(unsigned)nd, kWave, lds, s>>>(G, doffs, dinv, dim, dsp);
-    else if (per == 2)
-      tac_spread_kernel<2><<<(unsigned)nd, kWave, lds, s>>>(G, doffs, dinv, dim, dsp);
-    else
-      tac_spread_kernel<3><<<(unsigned)nd, kWave, lds, s>>>(G, doffs, dinv, dim, dsp);
-    LAUNCH_TRY("tac_spread_kernel");
+    constexpr uint64_t kSlice = 1ull << 24;  // tokens per launch (2^30 work-items)
+    for (uint64_t j0 = 0; j0 < nd; j0 += kSlice) {
+      const unsigned nb = (unsigned)std::min<uint64_t>(nd - j0, kSlice);
+      if (per == 1)
+        tac_spread_kernel<1><<<nb, kWave, lds, s>>>(G, doffs, dinv, dim, dsp, j0);
+      else if (per == 2)
+        tac_spread_kernel<2><<<nb, kWave, lds, s>>>(G, doffs, dinv, dim, dsp, j0);
+      else
+        tac_spread_kernel<3><<<nb, kWave, lds, s>>>(G, doffs, dinv, dim, dsp, j0);
+      LAUNCH_TRY("tac_spread_kernel");
+    }
   }
   std::vector<float> spreads(nd);
   HIP_TRY(hipMemcpyAsync(spreads.data(), ds.tac_spreads.ptr, nd * sizeof(float),
@@ -1854,6 +1862,12 @@ int tac_cluster_core(DeviceState &ds, hipStream_t s, const uint32_t *ids, uint64
   TacPlan pl;
   if ((st = tac_plan(freqs, offs, kappa, goff, prm.seed, rt, K, &pl))) return st;
   if (pl.kmax > kTacMaxCodes) return TAC_ERR_UNSUPPORTED;
+  // The Lloyd kernels launch one block of at most 256 work-items per tile,
+  // problem, chunk or scan range; a dispatch's grid holds under 2^32.
+  constexpr uint64_t kMaxUnits = (1ull << 32) / 256;
+  if (pl.tiles.size() >= kMaxUnits || pl.probs.size() >= kMaxUnits ||
+      pl.ranges.size() >= kMaxUnits || pl.chunks.size() >= kMaxUnits)
+    return TAC_ERR_UNSUPPORTED;
   const uint32_t P = (uint32_t)pl.probs.size();
   const uint32_t NT = (uint32_t)pl.tiles.size(), NCH = (uint32_t)pl.chunks.size();
   std::vector<uint32_t> done0(P);

@@ -117,10 +117,12 @@ __global__ __launch_bounds__(256) void tac_gather_kernel(const float* __restrict
                                                          const uint32_t* __restrict__ idx,
                                                          float* __restrict__ G, uint64_t rows,
                                                          uint32_t dim) {
-  const uint64_t f = (uint64_t)blockIdx.x * blockDim.x + threadIdx.x;
-  if (f >= rows * dim) return;
-  const uint64_t q = f / dim;
-  G[f] = v[(uint64_t)idx[q] * dim + f % dim];
+  // grid-stride, so rows * dim may exceed what one dispatch's grid can cover
+  const uint64_t total = rows * dim, stride = (uint64_t)gridDim.x * blockDim.x;
+  for (uint64_t f = (uint64_t)blockIdx.x * blockDim.x + threadIdx.x; f < total; f += stride) {
+    const uint64_t q = f / dim;
+    G[f] = v[(uint64_t)idx[q] * dim + f % dim];
+  }
 }
 
 // ---------------------------------------------------------------------------
@@ -149,9 +151,10 @@ __host__ __device__ constexpr size_t tac_spread_pad_floats(uint32_t dim) {
 }
 
 __global__ void tac_inv_table_kernel(float* __restrict__ inv, uint64_t n) {
-  const uint64_t i = (uint64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  const uint64_t stride = (uint64_t)gridDim.x * blockDim.x;
   // i + 1 <= 2^24 is exact in f32
-  if (i < n) inv[i] = 1.0f / (float)(i < kTacInvMax ? (uint32_t)i + 1u : kTacInvMax);
+  for (uint64_t i = (uint64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += stride)
+    inv[i] = 1.0f / (float)(i < kTacInvMax ? (uint32_t)i + 1u : kTacInvMax);
 }
 
 template <int PER>
@@ -159,9 +162,11 @@ __global__ __launch_bounds__(kWave) void tac_spread_kernel(const float* __restri
                                                            const uint32_t* __restrict__ offs,
                                                            const float* __restrict__ inv,
                                                            uint32_t dim,
-                                                           float* __restrict__ spreads) {
+                                                           float* __restrict__ spreads,
+                                                           uint64_t j0) {
   extern __shared__ float m2s[];  // [dim]
-  const uint32_t j = blockIdx.x, lane = threadIdx.x;
+  const uint64_t j = j0 + blockIdx.x;  // launched in slices of tokens
+  const uint32_t lane = threadIdx.x;
   const uint32_t lo = offs[j], hi = offs[j + 1];
   if (hi == lo) {
     if (lane == 0) spreads[j] = 0.0f;

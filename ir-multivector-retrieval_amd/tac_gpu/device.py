@@ -85,16 +85,23 @@ class DeviceArray:
 
 def train_device(x: DeviceArray, n: int, dim: int, m: int, ksub: int, init: DeviceArray | None,
                  out: DeviceArray, max_iters: int, tol: float, stats: bool = False,
-                 seed: int = 0):
-    """tac_pq_train_device on resident buffers; optional per-subspace stats.
+                 seed: int = 0, trace: bool = False):
+    """tac_pq_train_device on resident buffers; optional per-subspace stats
+    (iters_run, wcss, empties) and, with trace, the codebooks after every
+    iteration as a fourth array [max_iters][m][ksub][dsub].
     init None seeds every subspace with k-means++ (seed +% subspace)."""
     ex = None
     arrays = None
-    if stats:
+    if stats or trace:
         arrays = (np.zeros(m, np.uint32), np.zeros(m, np.float32), np.zeros(m, np.uint32))
+        tr = None
+        if trace:
+            tr = np.zeros((max_iters, m, ksub, dim // m), np.float32)
+            arrays = arrays + (tr,)
         ex = TrainExtras(arrays[0].ctypes.data_as(ctypes.POINTER(ctypes.c_uint32)),
                          arrays[1].ctypes.data_as(ctypes.POINTER(ctypes.c_float)),
-                         arrays[2].ctypes.data_as(ctypes.POINTER(ctypes.c_uint32)), None)
+                         arrays[2].ctypes.data_as(ctypes.POINTER(ctypes.c_uint32)),
+                         None if tr is None else tr.ctypes.data_as(ctypes.POINTER(ctypes.c_float)))
     errors.check(lib.tac_pq_train_device(x.ptr, n, dim, m, ksub,
                                          init.ptr if init is not None else None,
                                          seed & (2**64 - 1), max_iters, tol, out.ptr,

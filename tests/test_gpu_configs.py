@@ -41,6 +41,48 @@ def corpus():
     return synth.residuals(synth.WORKLOADS["corpus-1.52m"])
 
 
+def test_headline_corpus_as_benchmarked(gpu, corpus):
+    """The benchmark's workload as the benchmark runs it: all 1,521,797 x 64
+    residuals resident on the device, m16 k256, seeded-shuffle init, exactly
+    20 Lloyd iterations (tac_pq_train_device), then encode of every vector
+    (tac_pq_encode_device).  The codebooks after every iteration and all
+    24.3M codes equal the oracle's bit for bit (storage.build trains, then
+    encodes every token: src/index/storage.zig:380-401).  Near ties of the
+    final encode (best vs second within 1e-5 relative) are counted."""
+    w = synth.WORKLOADS["corpus-1.52m"]
+    x = corpus
+    init = synth.shuffle_init(x, w.m, w.ksub, w.seed)
+    dx = device.DeviceArray.from_host(x)
+    dinit = device.DeviceArray.from_host(init)
+    dcb = device.DeviceArray(init.shape, np.float32)
+    dcodes = device.DeviceArray((w.n, w.m), np.uint8)
+    t0 = time.perf_counter()
+    stats = device.train_device(dx, w.n, w.dim, w.m, w.ksub, dinit, dcb, w.iters, NEVER,
+                                trace=True)
+    device.encode_device(dx, w.n, w.dim, w.m, w.ksub, dcb, dcodes)
+    device.synchronize()
+    t1 = time.perf_counter()
+    cb, codes = dcb.to_host(), dcodes.to_host()
+    for a in (dx, dinit, dcb, dcodes):
+        a.free()
+    ref = orc.pq_train(x, w.dim, w.m, w.ksub, init=init, max_iters=w.iters, tol=NEVER,
+                       n_threads=16, trace=True)
+    t2 = time.perf_counter()
+    assert ref.status == 0
+    for t in range(w.iters):
+        diff = np.count_nonzero(_bits(stats[3][t]) != _bits(ref.trace[t]))
+        assert diff == 0, f"iteration {t}: {diff} codebook floats differ"
+    assert np.array_equal(_bits(cb), _bits(ref.codebooks))
+    assert np.all(stats[0] == w.iters)
+    ref_codes = orc.pq_encode(x, w.dim, w.m, w.ksub, ref.codebooks, n_threads=16)
+    t3 = time.perf_counter()
+    diff = int(np.count_nonzero(codes != ref_codes))
+    ties = orc.pq_near_ties(x, w.dim, w.m, w.ksub, ref.codebooks, 1e-5, n_threads=16)
+    _log(f"headline: GPU train+encode {t1 - t0:.3f} s (first call), oracle train {t2 - t1:.1f} s, "
+         f"encode {t3 - t2:.1f} s; {diff} of {codes.size} codes differ; near ties {ties}")
+    assert diff == 0
+
+
 @pytest.mark.parametrize("name", ["corpus-1.52m-m32d2", "corpus-1.52m-m8d8",
                                   "corpus-1.52m-k1024"])
 def test_subspace_shape_sweep_full_corpus(gpu, corpus, name):

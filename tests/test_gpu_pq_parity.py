@@ -112,6 +112,40 @@ def test_train_forced_empty_clusters(gpu):
     assert np.array_equal(_bits(got.codebooks), _bits(ref.codebooks))
 
 
+def _same_floats(a, b):
+    """Bit equality, with any NaN equal to any NaN (payloads are not compared)."""
+    a = np.ascontiguousarray(a, dtype=np.float32).reshape(-1)
+    b = np.ascontiguousarray(b, dtype=np.float32).reshape(-1)
+    na, nb = np.isnan(a), np.isnan(b)
+    return bool(np.array_equal(na, nb) and np.array_equal(a[~na].view(np.uint32),
+                                                          b[~nb].view(np.uint32)))
+
+
+@pytest.mark.parametrize("n", [5000, 40000])
+def test_train_reseed_skips_nan_distances(gpu, n):
+    # vec.argmax (src/util/vec.zig:285-299) starts from values[0] and moves on a
+    # strict >, so a NaN distance past index 0 never wins the empty-cluster
+    # reseed (src/tac/kmeans.zig:199-211).  Row 5 carries a NaN in subspace 3
+    # (its distance there is NaN) and row 1029, far from everything, holds the
+    # largest distance: it must seed the first empty cluster of every
+    # subspace, subspace 3 included.  Later iterations then run with the NaN
+    # codeword that row 5's cluster sum produces.
+    x = _workload_rows(n, seed=4)
+    x[5, 12:16] = np.nan
+    x[1029] = 50.0
+    init = np.repeat(x[:4].reshape(4, 16, 4).transpose(1, 0, 2), 64, axis=1).copy()
+    for iters in (1, 3):
+        got = pq.train(x, 64, 0, m=16, ksub=256, max_iters=iters, tol=NEVER,
+                       init_codebooks=init)
+        ref = orc.pq_train(x, 64, 16, 256, init=init, max_iters=iters, tol=NEVER, n_threads=16)
+        assert ref.status == 0
+        if iters == 1:
+            # every subspace reseeds its first empty cluster (index 1) from row 1029
+            assert np.all(ref.codebooks.reshape(16, 256, 4)[:, 1, :] == 50.0)
+        assert np.array_equal(got.stats.empties, ref.empties)
+        assert _same_floats(got.codebooks, ref.codebooks), f"{iters} iterations"
+
+
 def test_train_degenerate_k_ge_n(gpu):
     x = _workload_rows(200, seed=2)
     got = pq.train(x, 64, 0, m=16, ksub=256, init_codebooks=None)

@@ -110,6 +110,18 @@ def test_degenerate_and_tiny_tokens(gpu):
     _check(ids, v, 4, 20, 3, mu=2, tau=4, epsilon=2, theta=2)
 
 
+def test_token_id_past_2_pow_26(gpu):
+    # One row carries token id 70,000,000, so the vocabulary holds 70M ids:
+    # one spread wave per id is 4.5e9 work-items, more than one dispatch's
+    # grid, and the spreads run in slices of ids.
+    rng = np.random.default_rng(5)
+    ids = (np.arange(3000) % 7).astype(np.uint32)
+    ids[-1] = 70_000_000
+    v = rng.standard_normal((3000, 8)).astype(np.float32)
+    r = _check(ids, v, 8, 12, 3, mu=3, tau=5, epsilon=1, theta=1)
+    assert r.kappa_per_token.size == 70_000_001 and r.kappa_per_token[-1] == 1
+
+
 def _expect(ids, v, dim, p_kw, exc):
     ref = orc.tac_cluster_flat(ids, v, dim, orc.tac_params(**p_kw))
     assert ref.status == exc.status
