@@ -158,6 +158,24 @@ int tac_pq_encode_device(const float *d_residuals, uint64_t n, uint32_t dim,
                          uint32_t m, uint32_t ksub, const float *d_codebooks,
                          void *d_codes_out, void *stream);
 
+/*
+ * tac_pq_encode_device without any device allocation.  No counterpart in the
+ * reference: it is for callers that cannot allocate device memory (code under
+ * HIP graph capture, tight serving loops, harnesses that forbid hipMalloc).
+ * Same arguments, validation and codes as tac_pq_encode_device; stream NULL
+ * is the device's null stream, and the call returns once the work is
+ * enqueued.  Its scratch (counters, neighbour rows, grid anchors, deferred
+ * lists) is one static 128 MiB device array per GPU, held until the process
+ * ends; rows run in batches that fit it, so every n that
+ * tac_pq_encode_device accepts is accepted (codebooks whose tables leave no
+ * room for a 16,384-row batch take the full search).  All calls on one GPU
+ * share its array: calls that overlap on a GPU (other threads or streams)
+ * race, and the caller must serialise them.
+ */
+int tac_pq_encode_device_noalloc(const float *d_residuals, uint64_t n, uint32_t dim,
+                                 uint32_t m, uint32_t ksub, const float *d_codebooks,
+                                 void *d_codes_out, void *stream);
+
 /* PQ.decode (src/index/pq.zig:79-88) for n code rows: out [n][dim]. */
 int tac_pq_decode(const void *codes, uint64_t n, uint32_t dim, uint32_t m,
                   uint32_t ksub, const float *codebooks, float *out);

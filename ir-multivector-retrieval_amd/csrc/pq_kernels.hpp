@@ -1071,6 +1071,12 @@ __global__ void degenerate_kernel(const float* __restrict__ x, float* __restrict
   cb[g] = x[row * dim + (uint64_t)m * D + k];
 }
 
+// Clears n 32-bit words (a kernel rather than a memset, so the clear is an
+// ordinary dispatch in any stream or captured graph).
+__global__ void zero_words_kernel(uint32_t* __restrict__ p, uint32_t n) {
+  for (uint32_t i = threadIdx.x; i < n; i += blockDim.x) p[i] = 0u;
+}
+
 // Final codes [M][n] u16 -> caller's u32 assignments for kmeans.fit (M = 1).
 __global__ void widen_codes_kernel(const uint16_t* __restrict__ codes, uint32_t* __restrict__ out,
                                    uint64_t n) {

@@ -350,6 +350,14 @@ struct Launch {
                          uint8_t *anchors, float *grid, uint32_t *slice, uint32_t *defer,
                          uint32_t *defer_count, uint64_t n, uint32_t dim, uint32_t M, uint32_t K,
                          uint32_t L, unsigned long long *rescans, hipStream_t s) {
+    encode_tables(cb, nbr, anchors, grid, defer_count, M, K, L, s);
+    return encode_rows<CodeT>(x, cb, codes, nbr, anchors, grid, slice, defer, defer_count, n, dim,
+                              M, K, L, rescans, g_profile ? rescans + 1 : nullptr, s);
+  }
+  // The codebooks' neighbour rows and grid anchors (also clears defer_count).
+  static void encode_tables(const float *cb, uint32_t *nbr, uint8_t *anchors, float *grid,
+                            uint32_t *defer_count, uint32_t M, uint32_t K, uint32_t L,
+                            hipStream_t s) {
     const uint32_t G = cand_grid_side(D);
     uint32_t cells = 1;
     for (int k = 0; k < D; ++k) cells *= G;
@@ -357,6 +365,19 @@ struct Launch {
     grid_build_kernel<D, cand_anchors<true>()><<<dim3((cells + kBlock - 1) / kBlock, M), kBlock,
                                                   0, s>>>(
         cb, anchors, grid, K, G, cells);
+  }
+  // The candidate pass over n token-major rows from the tables, then the
+  // reference scan of the deferred vectors; defer_count must be zero, and
+  // slice / defer hold M * n words each.
+  template <typename CodeT>
+  static int encode_rows(const float *x, const float *cb, CodeT *codes, const uint32_t *nbr,
+                         const uint8_t *anchors, const float *grid, uint32_t *slice,
+                         uint32_t *defer, uint32_t *defer_count, uint64_t n, uint32_t dim,
+                         uint32_t M, uint32_t K, uint32_t L, unsigned long long *rescans,
+                         unsigned long long *stats, hipStream_t s) {
+    const uint32_t G = cand_grid_side(D);
+    uint32_t cells = 1;
+    for (int k = 0; k < D; ++k) cells *= G;
     const CandLds lay = cand_lds(K, Pad<D>::value, cells, 0, cand_anchors<true>());
     if (int st = raise_lds((const void *)cand_kernel<D, true, true, CodeT>, lay.total, cells))
       return st;
@@ -375,8 +396,7 @@ struct Launch {
     const uint64_t g = std::max<uint64_t>(
         1, std::min<uint64_t>((n + kBlock - 1) / kBlock, (4096 + M - 1) / M));
     encode_list_kernel<D, CodeT><<<dim3((unsigned)g, M), kBlock, lds, s>>>(
-        x, cb, codes, defer, defer_count, n, dim, M, K, rescans,
-        g_profile ? rescans + 1 : nullptr);
+        x, cb, codes, defer, defer_count, n, dim, M, K, rescans, stats);
     return TAC_OK;
   }
   static int scatter(const float *xs, const uint16_t *codes, const uint32_t *hist,
@@ -852,6 +872,39 @@ const char *kNames[] = {"Ok",
 }  // namespace
 
 // ===========================================================================
+// Scratch of the entry point that allocates nothing
+// ===========================================================================
+// tac_pq_encode_device_noalloc takes its counters, neighbour rows, grid
+// anchors and deferred-vector lists from this array instead of the cached
+// workspace.  Each GPU the library runs on holds its own copy, at its own
+// address, until the process ends.  The name is a host-side stand-in: host
+// code uses only the device address scratch_address returns.
+constexpr size_t kNoAllocScratchBytes = (size_t)128 << 20;
+static __device__ __align__(256) uint8_t scratch[kNoAllocScratchBytes];
+
+namespace {
+
+std::mutex g_scratch_mu;
+uint8_t *g_scratch[kMaxDevices] = {};
+
+// The scratch array's address on device `dev`, which must be current;
+// resolved on the first call on that device and kept.
+int scratch_address(int dev, uint8_t **out) {
+  std::lock_guard<std::mutex> g(g_scratch_mu);
+  if (!g_scratch[dev]) {
+    void *p = nullptr;
+    const hipError_t e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+    if (e != hipSuccess) return hip_status("hipGetSymbolAddress(scratch)", e);
+    if (!p) return TAC_ERR_HIP;
+    g_scratch[dev] = static_cast<uint8_t *>(p);
+  }
+  *out = g_scratch[dev];
+  return TAC_OK;
+}
+
+}  // namespace
+
+// ===========================================================================
 // C ABI
 // ===========================================================================
 extern "C" {
@@ -1049,6 +1102,92 @@ int tac_pq_encode_device(const float *d_residuals, uint64_t n, uint32_t dim, uin
   if ((st = encode_core(*ds, s, d_residuals, n, dim, m, ksub, d_codebooks, d_codes_out)))
     return st;
   return end_call(*ds, s);
+}
+
+// PQ.encode with no device allocation: the candidate encode's scratch comes
+// from one static device array per GPU (see scratch_address), and rows run
+// in batches that fit it.
+int tac_pq_encode_device_noalloc(const float *d_residuals, uint64_t n, uint32_t dim, uint32_t m,
+                                 uint32_t ksub, const float *d_codebooks, void *d_codes_out,
+                                 void *stream) {
+  if (m == 0 || ksub == 0) return TAC_ERR_INVALID_ARGUMENT;
+  if (dim == 0 || dim % m != 0) return TAC_ERR_DIM_MISMATCH;
+  if (dim / m > kMaxDsub || ksub > kMaxKsub) return TAC_ERR_UNSUPPORTED;
+  if (n == 0) return TAC_OK;
+  if (!d_residuals || !d_codebooks || !d_codes_out) return TAC_ERR_INVALID_ARGUMENT;
+  if (device_count() <= 0) return TAC_ERR_NO_DEVICE;
+  int dev = 0;
+  HIP_TRY(hipGetDevice(&dev));
+  if (dev < 0 || dev >= kMaxDevices) return TAC_ERR_NO_DEVICE;
+  uint8_t *base = nullptr;
+  int st = scratch_address(dev, &base);
+  if (st) return st;
+  hipStream_t s = reinterpret_cast<hipStream_t>(stream);  // NULL: the null stream
+  const uint32_t D = dim / m;
+  size_t off = 0;
+  auto take = [&](size_t bytes) {
+    uint8_t *p = base + off;
+    off += (bytes + 255) & ~(size_t)255;
+    return p;
+  };
+  // [0] exact rescans, [1] and [2] stay unused (no profiling here)
+  auto *counters = reinterpret_cast<unsigned long long *>(take(3 * sizeof(unsigned long long)));
+  zero_words_kernel<<<1, kWave, 0, s>>>(reinterpret_cast<uint32_t *>(counters), 6);
+  LAUNCH_TRY("zero_words_kernel");
+  const char *full_env = getenv("TAC_GPU_FULL_SEARCH");
+  const uint32_t L = ksub >= 2 ? std::min<uint32_t>(kCandList, ksub - 1) : 0;
+  bool cand = !(full_env && full_env[0] == '1') && ksub >= 2 && ksub <= kCandMaxK &&
+              n >= 16384;
+  uint64_t batch = 0;
+  uint32_t *count = nullptr, *nbr = nullptr, *lists = nullptr;
+  uint8_t *anchors = nullptr;
+  float *grid = nullptr;
+  if (cand) {
+    count = reinterpret_cast<uint32_t *>(take((size_t)m * sizeof(uint32_t)));
+    nbr = reinterpret_cast<uint32_t *>(
+        take((size_t)m * ksub * cand_row_len(L) * sizeof(uint32_t)));
+    anchors = take((size_t)m * kCandCells * kCandAnchorsMax);
+    grid = reinterpret_cast<float *>(take((size_t)m * 16 * sizeof(float)));
+    // the rest holds a batch's slices and deferred lists: 2 words per row and subspace
+    const size_t left = off < kNoAllocScratchBytes ? kNoAllocScratchBytes - off : 0;
+    batch = left / (2 * sizeof(uint32_t) * (size_t)m) / 8192 * 8192;
+    batch = std::min<uint64_t>(batch, 0xFFFF0000ull);
+    lists = reinterpret_cast<uint32_t *>(base + off);
+    cand = batch >= 16384;
+  }
+  if (!cand) {
+    if (ksub <= 256) {
+      DISPATCH_D_ST(D, encode<uint8_t>(d_residuals, d_codebooks, (uint8_t *)d_codes_out, n, dim,
+                                       m, ksub, counters, s));
+    } else {
+      DISPATCH_D_ST(D, encode<uint16_t>(d_residuals, d_codebooks, (uint16_t *)d_codes_out, n,
+                                        dim, m, ksub, counters, s));
+    }
+    if (st) return st;
+    LAUNCH_TRY("encode_kernel");
+    return TAC_OK;
+  }
+  DISPATCH_D(D, encode_tables(d_codebooks, nbr, anchors, grid, count, m, ksub, L, s));
+  LAUNCH_TRY("encode tables");
+  for (uint64_t r0 = 0; r0 < n; r0 += batch) {
+    const uint64_t nb = std::min<uint64_t>(batch, n - r0);
+    const float *x = d_residuals + r0 * dim;
+    uint8_t *codes = static_cast<uint8_t *>(d_codes_out) + r0 * m;
+    if (nb >= 16384) {
+      if (r0) {  // the tables' launch cleared the first batch's count
+        zero_words_kernel<<<1, kWave, 0, s>>>(count, m);
+        LAUNCH_TRY("zero_words_kernel");
+      }
+      DISPATCH_D_ST(D, encode_rows<uint8_t>(x, d_codebooks, codes, nbr, anchors, grid, lists,
+                                            lists + (size_t)m * nb, count, nb, dim, m, ksub, L,
+                                            counters, nullptr, s));
+    } else {
+      DISPATCH_D_ST(D, encode<uint8_t>(x, d_codebooks, codes, nb, dim, m, ksub, counters, s));
+    }
+    if (st) return st;
+    LAUNCH_TRY("encode_kernel");
+  }
+  return TAC_OK;
 }
 
 int tac_pq_encode(const float *residuals, uint64_t n, uint32_t dim, uint32_t m, uint32_t ksub,

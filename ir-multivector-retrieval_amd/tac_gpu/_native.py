@@ -120,6 +120,8 @@ SIGNATURES = {
     "tac_pq_encode": (c_int, [c_void_p, c_u64, c_u32, c_u32, c_u32, c_void_p, c_void_p]),
     "tac_pq_encode_device": (
         c_int, [c_void_p, c_u64, c_u32, c_u32, c_u32, c_void_p, c_void_p, c_void_p]),
+    "tac_pq_encode_device_noalloc": (
+        c_int, [c_void_p, c_u64, c_u32, c_u32, c_u32, c_void_p, c_void_p, c_void_p]),
     "tac_pq_decode": (c_int, [c_void_p, c_u64, c_u32, c_u32, c_u32, c_void_p, c_void_p]),
     "tac_kmeans_fit": (
         c_int,

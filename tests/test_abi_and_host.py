@@ -88,6 +88,14 @@ def test_c_abi_validates_before_touching_a_device():
     assert L.tac_kmeans_fit(None, 5, 2, 0, 25, 1e-4, 0, None, None, None, None, None) == 6
     assert L.tac_pq_encode(None, 10, 33, 32, 256, None, None) == 2
     assert L.tac_pq_encode(None, 0, 32, 32, 256, None, None) == 0  # nothing to encode
+    # the no-allocation encode validates exactly as tac_pq_encode_device
+    for f in (L.tac_pq_encode_device, L.tac_pq_encode_device_noalloc):
+        assert f(None, 10, 33, 32, 256, None, None, None) == 2
+        assert f(None, 10, 32, 0, 256, None, None, None) == 14
+        assert f(None, 10, 32, 2, 256, None, None, None) == 15  # dsub 16
+        assert f(None, 10, 32, 32, 2048, None, None, None) == 15
+        assert f(None, 0, 32, 32, 256, None, None, None) == 0
+        assert f(None, 10, 32, 32, 256, None, None, None) == 14
 
 
 @pytest.mark.skipif(device.device_count() > 0, reason="a HIP device is present")
@@ -101,6 +109,9 @@ def test_no_device_is_a_clean_error():
         pq.PQ(32, 1, init.reshape(-1)).encode_many(x)
     with pytest.raises(errors.NoDevice):
         device.DeviceArray((4,), np.float32)
+    fake = 0x1000  # never dereferenced: the device check comes first
+    assert tac_gpu.lib.tac_pq_encode_device_noalloc(fake, 300, 32, 32, 256, fake, fake,
+                                                    None) == errors.NoDevice.status
 
 
 def test_cpp_mirror_error_mapping():
