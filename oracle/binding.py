@@ -66,6 +66,8 @@ def _load():
     L.orc_pq_train.restype = ctypes.c_int
     L.orc_pq_train.argtypes = [_vp, _u64, _u32, _u32, _u32, _vp, _u64, _u32, _f32, _u32, _vp,
                                ctypes.POINTER(TrainExtras)]
+    L.orc_set_scalar.restype = None
+    L.orc_set_scalar.argtypes = [ctypes.c_int]
     L.orc_pq_encode.restype = ctypes.c_int
     L.orc_pq_encode.argtypes = [_vp, _u64, _u32, _u32, _u32, _vp, _vp, _u32]
     L.orc_pq_near_ties.restype = ctypes.c_int
@@ -407,3 +409,16 @@ def tac_cluster_flat(token_ids, vectors, dim: int, params: TacParams) -> TacResu
                                   _p(cent), _p(asg), _p(kpt), ctypes.byref(w), ctypes.byref(ndo))
     return TacResult(st, cent[:params.kappa_total * dim], asg[:ids.size], kpt,
                      float(np.float32(w.value)))
+
+
+class scalar_distances:
+    """Within the block, every oracle distance goes through orc_l2sq pair by
+    pair (the per-pair form the vectorized d <= 8 path is checked against)."""
+
+    def __enter__(self):
+        lib.orc_set_scalar(1)
+        return self
+
+    def __exit__(self, *exc):
+        lib.orc_set_scalar(0)
+        return False

@@ -125,6 +125,90 @@ uint64_t orc_argmax(const float *v, uint64_t n) {
 }
 
 /* ------------------------------------------------------------------------ */
+/* Distances to every codeword, the way the reference's loops write them     */
+/* ------------------------------------------------------------------------ */
+
+/* The reference's assignment writes dists[cc] = l2sq(v, c_cc) for every
+ * codeword and then takes vec.argmin (src/tac/kmeans.zig:356-364); PQ.encode
+ * scans the same distances from best = +inf (src/index/pq.zig:64-73).  For
+ * d <= 8 < ORC_HOST_LANES every arm of l2sq is the sequential fold
+ * ((x0-c0)^2 + (x1-c1)^2) + ..., so the distances below fold each codeword
+ * in that order, reading a transposed codebook cbt[k][cc] (row stride kp):
+ * the loop over codewords vectorizes, and each codeword's bits equal
+ * orc_l2sq's.  orc_set_scalar(1) forces the per-pair orc_l2sq path, against
+ * which the tests compare this one. */
+static int g_scalar = 0;
+void orc_set_scalar(int on) { g_scalar = on; }
+
+typedef void (*dists_fn)(const float *, const float *, uint32_t, uint32_t, float *);
+
+#define ORC_DISTS(D)                                                            \
+  static void dists_d##D(const float *x, const float *cbt, uint32_t k,        \
+                         uint32_t kp, float *out) {                           \
+    float xv[D];                                                              \
+    for (int j = 0; j < D; ++j) xv[j] = x[j];                                 \
+    for (uint32_t cc = 0; cc < k; ++cc) {                                     \
+      float t = xv[0] - cbt[cc];                                              \
+      float acc = t * t;                                                      \
+      for (int j = 1; j < D; ++j) {                                           \
+        t = xv[j] - cbt[(uint64_t)j * kp + cc];                               \
+        acc = acc + t * t;                                                    \
+      }                                                                       \
+      out[cc] = acc;                                                          \
+    }                                                                         \
+  }
+ORC_DISTS(1)
+ORC_DISTS(2)
+ORC_DISTS(3)
+ORC_DISTS(4)
+ORC_DISTS(5)
+ORC_DISTS(6)
+ORC_DISTS(7)
+ORC_DISTS(8)
+
+static dists_fn dists_for(uint32_t d) {
+  if (g_scalar) return NULL;
+  switch (d) {
+    case 1: return dists_d1;
+    case 2: return dists_d2;
+    case 3: return dists_d3;
+    case 4: return dists_d4;
+    case 5: return dists_d5;
+    case 6: return dists_d6;
+    case 7: return dists_d7;
+    case 8: return dists_d8;
+    default: return NULL;
+  }
+}
+
+/* cbt[j][cc] = cb[cc][j] for k codewords of d floats. */
+static void transpose_cb(const float *cb, uint32_t k, uint32_t d, float *cbt) {
+  for (uint32_t cc = 0; cc < k; ++cc)
+    for (uint32_t j = 0; j < d; ++j) cbt[(uint64_t)j * k + cc] = cb[(uint64_t)cc * d + j];
+}
+
+/* The scan `best = start; for i: if (v[i] < best) take i` (strict <, first
+ * index kept) as two passes that vectorize: the smallest value below start
+ * (NaN never compares below), then the first index holding a value equal to
+ * it (== makes -0.0 and +0.0 one class, as < does).  No value below start:
+ * index 0, which is where both of the reference's scans stay (vec.argmin
+ * with start = v[0], PQ.encode with start = +inf). */
+static uint64_t first_below(const float *v, uint64_t n, float start) {
+  float lane[8];
+  for (int j = 0; j < 8; ++j) lane[j] = start;
+  uint64_t i = 0;
+  for (; i + 8 <= n; i += 8)
+    for (int j = 0; j < 8; ++j) lane[j] = v[i + j] < lane[j] ? v[i + j] : lane[j];
+  for (; i < n; ++i) lane[0] = v[i] < lane[0] ? v[i] : lane[0];
+  float best = start;
+  for (int j = 0; j < 8; ++j) best = lane[j] < best ? lane[j] : best;
+  if (!(best < start)) return 0;
+  for (i = 0; i < n; ++i)
+    if (v[i] == best) return i;
+  return 0;
+}
+
+/* ------------------------------------------------------------------------ */
 /* Zig std PRNG (parity unpinned: restated from the published algorithms    */
 /* Xoshiro256++ / SplitMix64 and Zig std's Random helpers; no Zig toolchain   */
 /* is available to check the stream).  Reference call sites:                 */
@@ -245,15 +329,23 @@ typedef struct {
   float *dists;
   uint64_t lo, hi;
   uint32_t d, k;
+  const float *cbt; /* transposed centroids [d][k] for the vectorized distances, or NULL */
 } assign_ctx;
 
 /* src/tac/kmeans.zig:344-365 */
 static void assign_slice(const assign_ctx *c) {
+  const dists_fn f = c->cbt ? dists_for(c->d) : NULL;
   for (uint64_t i = c->lo; i < c->hi; ++i) {
     const float *v = c->vectors + i * c->d;
-    for (uint32_t cc = 0; cc < c->k; ++cc)
-      c->dists[cc] = orc_l2sq(v, c->centroids + (uint64_t)cc * c->d, c->d);
-    const uint64_t a = orc_argmin(c->dists, c->k);
+    uint64_t a;
+    if (f) {
+      f(v, c->cbt, c->k, c->k, c->dists);
+      a = first_below(c->dists, c->k, c->dists[0]);
+    } else {
+      for (uint32_t cc = 0; cc < c->k; ++cc)
+        c->dists[cc] = orc_l2sq(v, c->centroids + (uint64_t)cc * c->d, c->d);
+      a = orc_argmin(c->dists, c->k);
+    }
     c->assignments[i] = (uint32_t)a;
     c->min_to_any[i] = c->dists[a];
   }
@@ -270,12 +362,22 @@ static int assign_vectors(const float *vectors, uint64_t n, uint32_t d,
                           uint32_t *assignments, float *min_to_any,
                           uint32_t n_threads) {
   uint64_t real = n_threads <= 1 ? 1 : (n_threads < n ? n_threads : n);
+  float *cbt = NULL;
+  if (dists_for(d)) {
+    cbt = (float *)malloc(sizeof(float) * (uint64_t)k * d);
+    if (!cbt) return ORC_OUT_OF_MEMORY;
+    transpose_cb(centroids, k, d, cbt);
+  }
   if (real <= 1) {
     float *dists = (float *)malloc(sizeof(float) * k);
-    if (!dists) return ORC_OUT_OF_MEMORY;
-    assign_ctx c = {vectors, centroids, assignments, min_to_any, dists, 0, n, d, k};
+    if (!dists) {
+      free(cbt);
+      return ORC_OUT_OF_MEMORY;
+    }
+    assign_ctx c = {vectors, centroids, assignments, min_to_any, dists, 0, n, d, k, cbt};
     assign_slice(&c);
     free(dists);
+    free(cbt);
     return ORC_OK;
   }
   assign_ctx *ctx = (assign_ctx *)calloc(real, sizeof(assign_ctx));
@@ -285,6 +387,7 @@ static int assign_vectors(const float *vectors, uint64_t n, uint32_t d,
     free(ctx);
     free(th);
     free(dists);
+    free(cbt);
     return ORC_OUT_OF_MEMORY;
   }
   const uint64_t chunk = (n + real - 1) / real;
@@ -294,7 +397,7 @@ static int assign_vectors(const float *vectors, uint64_t n, uint32_t d,
     uint64_t hi = lo + chunk < n ? lo + chunk : n;
     if (lo > n) lo = n;
     ctx[t] = (assign_ctx){vectors, centroids, assignments, min_to_any,
-                          dists + t * k, lo, hi, d, k};
+                          dists + t * k, lo, hi, d, k, cbt};
     if (pthread_create(&th[t], NULL, assign_thread, &ctx[t]) != 0) break;
     ++spawned;
   }
@@ -304,6 +407,7 @@ static int assign_vectors(const float *vectors, uint64_t n, uint32_t d,
   free(ctx);
   free(th);
   free(dists);
+  free(cbt);
   return ORC_OK;
 }
 
@@ -578,22 +682,31 @@ typedef struct {
   uint32_t dim, m, ksub, dsub;
   float rel_tol;
   uint64_t near;
+  const float *cbt; /* per subspace, the transposed codebook [dsub][ksub], or NULL */
 } encode_ctx;
 
 /* src/index/pq.zig:59-76: best_d starts at +inf, strict < keeps the first. */
 static void encode_slice(encode_ctx *c) {
+  const dists_fn f = c->cbt ? dists_for(c->dsub) : NULL;
+  float *dists = f ? (float *)malloc(sizeof(float) * c->ksub) : NULL;
+  const dists_fn fn = dists ? f : NULL;
   for (uint64_t i = c->lo; i < c->hi; ++i) {
     const float *r = c->residuals + i * c->dim;
     for (uint32_t mm = 0; mm < c->m; ++mm) {
       const float *sub = r + (uint64_t)mm * c->dsub;
       const float *cb = c->codebooks + (uint64_t)mm * c->ksub * c->dsub;
       uint32_t best_c = 0;
-      float best_d = INFINITY;
-      for (uint32_t cc = 0; cc < c->ksub; ++cc) {
-        const float dd = orc_l2sq(sub, cb + (uint64_t)cc * c->dsub, c->dsub);
-        if (dd < best_d) {
-          best_d = dd;
-          best_c = cc;
+      if (fn) {
+        fn(sub, c->cbt + (uint64_t)mm * c->ksub * c->dsub, c->ksub, c->ksub, dists);
+        best_c = (uint32_t)first_below(dists, c->ksub, INFINITY);
+      } else {
+        float best_d = INFINITY;
+        for (uint32_t cc = 0; cc < c->ksub; ++cc) {
+          const float dd = orc_l2sq(sub, cb + (uint64_t)cc * c->dsub, c->dsub);
+          if (dd < best_d) {
+            best_d = dd;
+            best_c = cc;
+          }
         }
       }
       if (c->ksub <= 256)
@@ -602,6 +715,7 @@ static void encode_slice(encode_ctx *c) {
         ((uint16_t *)c->codes)[i * c->m + mm] = (uint16_t)best_c;
     }
   }
+  free(dists);
 }
 
 static void near_slice(encode_ctx *c) {
@@ -681,8 +795,19 @@ int orc_pq_encode(const float *residuals, uint64_t n, uint32_t dim, uint32_t m,
                   uint32_t n_threads) {
   if (m == 0 || ksub == 0 || ksub > 65536) return ORC_INVALID_ARGUMENT;
   if (dim == 0 || dim % m != 0) return ORC_DIM_MISMATCH;
-  encode_ctx base = {residuals, codebooks, codes, 0, n, dim, m, ksub, dim / m, 0.0f, 0};
-  return fan_out(base, n_threads, encode_thread, NULL);
+  const uint32_t dsub = dim / m;
+  float *cbt = NULL;
+  if (dists_for(dsub)) {
+    cbt = (float *)malloc(sizeof(float) * (uint64_t)m * ksub * dsub);
+    if (!cbt) return ORC_OUT_OF_MEMORY;
+    for (uint32_t mm = 0; mm < m; ++mm)
+      transpose_cb(codebooks + (uint64_t)mm * ksub * dsub, ksub, dsub,
+                   cbt + (uint64_t)mm * ksub * dsub);
+  }
+  encode_ctx base = {residuals, codebooks, codes, 0, n, dim, m, ksub, dsub, 0.0f, 0, cbt};
+  const int st = fan_out(base, n_threads, encode_thread, NULL);
+  free(cbt);
+  return st;
 }
 
 int orc_pq_near_ties(const float *residuals, uint64_t n, uint32_t dim,
@@ -690,7 +815,7 @@ int orc_pq_near_ties(const float *residuals, uint64_t n, uint32_t dim,
                      float rel_tol, uint64_t *count, uint32_t n_threads) {
   if (m == 0 || ksub == 0) return ORC_INVALID_ARGUMENT;
   if (dim == 0 || dim % m != 0) return ORC_DIM_MISMATCH;
-  encode_ctx base = {residuals, codebooks, NULL, 0, n, dim, m, ksub, dim / m, rel_tol, 0};
+  encode_ctx base = {residuals, codebooks, NULL, 0, n, dim, m, ksub, dim / m, rel_tol, 0, NULL};
   return fan_out(base, n_threads, near_thread, count);
 }
 

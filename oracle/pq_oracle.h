@@ -69,6 +69,11 @@ enum {
  * for (std.simd.suggestVectorLength(f32)): 16 on an AVX-512 x86-64 host. */
 #define ORC_HOST_LANES 16
 
+/* 1: every distance goes through orc_l2sq pair by pair (the per-pair form);
+ * 0 (default): for d <= 8 all K distances of a vector are formed at once from
+ * a transposed codebook, in the same per-codeword order.  Test hook. */
+void orc_set_scalar(int on);
+
 float orc_l2sq(const float *a, const float *b, uint32_t d);
 float orc_dot(const float *a, const float *b, uint32_t d);
 uint64_t orc_argmin(const float *v, uint64_t n);

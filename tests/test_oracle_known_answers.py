@@ -385,3 +385,66 @@ def test_distance_table_layout_and_values():  # pq.zig:344-349, :519-585
     assert abs(t[((m * 256) + c) * 4 + i] - q[i, m] * cb[m, c, 0]) < 1e-6
     st, _ = orc.pq_distance_table(q, 4, 32, 32, 256, cb, table_len=4)
     assert st == 4  # OutBufferWrongSize
+
+
+def _same_floats(a, b):
+    a, b = np.asarray(a, np.float32).reshape(-1), np.asarray(b, np.float32).reshape(-1)
+    na, nb = np.isnan(a), np.isnan(b)
+    return bool(np.array_equal(na, nb) and np.array_equal(a[~na].view(np.uint32),
+                                                          b[~nb].view(np.uint32)))
+
+
+@pytest.mark.parametrize("dsub", [1, 2, 3, 4, 5, 6, 7, 8])
+def test_vectorized_distances_equal_the_per_pair_form(dsub):
+    """For d <= 8 the oracle forms all K distances of a vector at once from a
+    transposed codebook and takes the first-index minimum in two passes; the
+    per-pair form (orc_l2sq, then the strict-< scan) must give the same codes,
+    codebooks, empties and wcss, on inputs with exact ties, duplicate
+    codewords, signed zeros, NaN and infinities."""
+    rng = np.random.default_rng(100 + dsub)
+    m, ksub, n = 4, 37, 3000
+    dim = m * dsub
+    cb = rng.standard_normal((m, ksub, dsub)).astype(np.float32)
+    cb[:, 3] = cb[:, 0]          # duplicates: the lower index wins
+    cb[:, 20] = 0.0
+    cb[:, 21] = -0.0             # equal to +0.0 under <
+    x = rng.standard_normal((n, dim)).astype(np.float32)
+    x[100:130] = cb[:, :30].transpose(1, 0, 2).reshape(30, dim)  # exact ties at distance 0
+    x[::97] = 0.0
+    x[5::101] = -0.0
+    x[7, :dsub] = np.nan
+    x[9, 0] = np.inf
+    x[11, -1] = -np.inf
+    x[13] = 3e19                 # squares overflow to +inf
+    bad = cb.copy()
+    bad[1, 5, 0] = np.nan
+    bad[2, 6, 0] = np.inf
+    for book in (cb, bad):
+        fast = orc.pq_encode(x, dim, m, ksub, book, n_threads=4)
+        with orc.scalar_distances():
+            slow = orc.pq_encode(x, dim, m, ksub, book, n_threads=4)
+        assert np.array_equal(fast, slow)
+    # Lloyd iterations: vec.argmin from values[0] (finite data, forced ties)
+    xt = x[14:].copy()
+    xt[~np.isfinite(xt)] = 0.0
+    xt[np.abs(xt) > 1e10] = 1.0
+    init = cb.copy()
+    a = orc.pq_train(xt, dim, m, ksub, init=init, max_iters=4, tol=float("-inf"), n_threads=3,
+                     trace=True)
+    with orc.scalar_distances():
+        b = orc.pq_train(xt, dim, m, ksub, init=init, max_iters=4, tol=float("-inf"),
+                         n_threads=3, trace=True)
+    assert a.status == b.status == 0
+    assert _same_floats(a.trace, b.trace)
+    assert np.array_equal(a.empties, b.empties)
+    assert _same_floats(a.wcss, b.wcss)
+    # a NaN row: its subspace's codeword 0 turns NaN, and argmin from values[0]
+    # then keeps 0 for every vector
+    xn = xt.copy()
+    xn[50, :dsub] = np.nan
+    a = orc.pq_train(xn, dim, m, ksub, init=init, max_iters=3, tol=float("-inf"), trace=True)
+    with orc.scalar_distances():
+        b = orc.pq_train(xn, dim, m, ksub, init=init, max_iters=3, tol=float("-inf"),
+                         trace=True)
+    assert _same_floats(a.trace, b.trace)
+    assert np.array_equal(a.empties, b.empties)
