@@ -1,21 +1,31 @@
 #!/usr/bin/env python3
 """PQ build benchmark on one MI355X: pq.train (20 Lloyd iterations) + pq.encode.
 
-Workload: the full-corpus shape — 1,521,797 synthetic fp32 residuals of
-dim 64 (Zipf 1.1 over 32,768 unit-sphere centres, sigma 0.15), m=16
-subspaces of dsub 4, ksub=256, seeded-shuffle initial codebooks, exactly 20
-Lloyd iterations, then encode of every vector.  One step = one full train +
-one full encode with residuals already resident in HBM.
+Headline workload: the full-corpus shape — 1,521,797 synthetic fp32
+residuals of dim 64 (Zipf 1.1 over 32,768 unit-sphere centres, sigma 0.15),
+m=16 subspaces of dsub 4, ksub=256, seeded-shuffle initial codebooks,
+exactly 20 Lloyd iterations, then encode of every vector.  One step = one
+full train + one full encode with residuals already resident in HBM.
 
 Prints ONE JSON line.  value = pq.train seconds per 20 iterations (lower is
-better); encode throughput, kernel rooflines, the CPU baseline and a
-full-size bit-exactness check ride along in the same line.
+better).  Beside it: encode throughput, the dominant kernel's roofline (live
+HIP-event time of every kernel over the timed steps, HBM traffic and VALU
+counters from the committed rocprofv3 summaries), the CPU baseline (the
+oracle on this host's cores), rows for the subspace-shape sweep, the 60M
+resident train and the 200M encode stream, and the stages around the path.
+
+Other modes:
+  --traffic-pass        a short run for rocprofv3 counter passes
+  --cpu-full            the CPU baseline protocol without extrapolation
+  --summarize-pmc OUT DIR...   per-kernel summary of rocprofv3 counter CSVs
 """
 from __future__ import annotations
 
 import argparse
+import csv
 import json
 import os
+import statistics
 import sys
 import time
 from pathlib import Path
@@ -28,54 +38,318 @@ sys.path.insert(0, str(ROOT))
 
 METRIC = "pq.train s/20 iters + pq.encode Mvec/s, 1.52M×64 fp32, m16×k256; % roofline"
 WORKLOAD = "corpus-1.52m"
-PEAK_FP32_TFLOPS = 157.3   # MI355X fp32 (vector / matrix) peak
+PEAK_FP32_TFLOPS = 157.3   # MI355X fp32 vector peak (packed)
 PEAK_HBM_GBS = 8000.0      # MI355X HBM3E
+# VALU issue: 256 CUs x 4 SIMDs, one wave64 VALU instruction per SIMD every 4
+# cycles (16 lanes), at 2.4 GHz.
+PEAK_VALU_GINSTR = 256 * 4 * 2.4 / 4
 NEVER = float("-inf")
+TRAFFIC_FILE = ROOT / "profiles" / f"pq_build_{WORKLOAD}_hbm_traffic.json"
+VALU_FILE = ROOT / "profiles" / f"pq_build_{WORKLOAD}_valu_counters.json"
+CPU_FULL_FILE = ROOT / "profiles" / f"cpu_baseline_{WORKLOAD}.json"
 
 
 def log(msg: str) -> None:
     print(f"[bench] {msg}", file=sys.stderr, flush=True)
 
 
-def cpu_threads() -> int:
+def host_threads() -> int:
     try:
-        n = len(os.sched_getaffinity(0))
+        return len(os.sched_getaffinity(0))
     except AttributeError:
-        n = os.cpu_count() or 1
-    return max(1, min(n, 16))
+        return os.cpu_count() or 1
 
 
-def cpu_baseline(x: np.ndarray, init: np.ndarray, w, gpu_cb3: np.ndarray | None):
-    """Oracle (CPU restatement of the reference) on a bounded sample of the
-    same workload: 2 Lloyd iterations of all 16 subspaces over the full
-    corpus, and encode of 200,000 vectors; extrapolated to the metric's units."""
+def host_cpu() -> str:
+    try:
+        for line in Path("/proc/cpuinfo").read_text().splitlines():
+            if line.startswith("model name"):
+                return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return "unknown"
+
+
+def median_of(fn, runs: int = 3):
+    """Median wall time of `runs` calls (the first call's result is returned)."""
+    times, first = [], None
+    for r in range(runs):
+        t0 = time.perf_counter()
+        out = fn()
+        times.append(time.perf_counter() - t0)
+        if r == 0:
+            first = out
+    return statistics.median(times), first
+
+
+# ---------------------------------------------------------------------------
+# CPU baseline: the oracle with the reference's threading
+# ---------------------------------------------------------------------------
+def cpu_baseline(x: np.ndarray, init: np.ndarray, w, gpu_cb2: np.ndarray | None,
+                 full: bool = False):
+    """The oracle (the C restatement of the reference, its threading: work
+    stealing over subspaces, static chunks inside a subspace and for encode)
+    on this host's cores, at T = every available thread and T = 1.
+
+    Protocol: one discarded warm-up (the 2-iteration run that also checks the
+    GPU's codebooks at full size), then the median of 3 runs of each timing.
+    Bounded mode (default) times 4 Lloyd iterations at T and extrapolates to
+    20, and 1 iteration of 2 subspaces at T = 1, extrapolated to 20
+    iterations of all subspaces; encode times the whole corpus at T and
+    100,000 vectors at T = 1.  Full mode times all 20 iterations at T."""
     from oracle import binding as orc
 
-    threads = cpu_threads()
-    iters = 2
+    T = host_threads()
     t0 = time.perf_counter()
-    ref = orc.pq_train(x, w.dim, w.m, w.ksub, init=init, max_iters=iters, tol=NEVER,
-                       n_threads=threads)
-    t_train = time.perf_counter() - t0
-    assert ref.status == 0
-    sample = 200_000
-    t0 = time.perf_counter()
-    orc.pq_encode(x[:sample], w.dim, w.m, w.ksub, ref.codebooks, n_threads=threads)
-    t_enc = time.perf_counter() - t0
+    ref2 = orc.pq_train(x, w.dim, w.m, w.ksub, init=init, max_iters=2, tol=NEVER, n_threads=T)
+    warm_s = time.perf_counter() - t0
+    assert ref2.status == 0
     parity = None
-    if gpu_cb3 is not None:
-        parity = bool(np.array_equal(gpu_cb3.view(np.uint32), ref.codebooks.view(np.uint32)))
+    if gpu_cb2 is not None:
+        parity = bool(np.array_equal(gpu_cb2.view(np.uint32), ref2.codebooks.view(np.uint32)))
+    iters = w.iters if full else 4
+    t_train, _ = median_of(lambda: orc.pq_train(x, w.dim, w.m, w.ksub, init=init,
+                                                 max_iters=iters, tol=NEVER, n_threads=T))
+    t_enc, _ = median_of(lambda: orc.pq_encode(x, w.dim, w.m, w.ksub, ref2.codebooks,
+                                               n_threads=T))
+    # T = 1: the first two subspaces (dim 2 * dsub) stand for all of them
+    dsub = w.dim // w.m
+    x2 = np.ascontiguousarray(x[:, :2 * dsub])
+    it1 = 2 if full else 1
+    t1_train, _ = median_of(lambda: orc.pq_train(x2, 2 * dsub, 2, w.ksub, init=init[:2],
+                                                  max_iters=it1, tol=NEVER, n_threads=1))
+    ns = 100_000
+    t1_enc, _ = median_of(lambda: orc.pq_encode(x[:ns], w.dim, w.m, w.ksub, ref2.codebooks,
+                                                n_threads=1))
     return {
-        "train_s_per_20_iters": t_train / iters * 20,
-        "encode_mvec_per_s": sample / t_enc / 1e6,
-        "cores": threads,
-        "sample": f"{iters} Lloyd iterations of all {w.m} subspaces over the full "
-                  f"{w.n:,}-vector corpus ({t_train:.1f} s) + encode of {sample:,} vectors "
-                  f"({t_enc:.1f} s); train extrapolated x{20 // iters}",
-        "parity_full_size": parity,
+        "value": round(t_train / iters * w.iters, 3), "unit": "s/20 iters",
+        "encode_mvec_per_s": round(w.n / t_enc / 1e6, 3),
+        "threads": T, "cores": T, "kind": "port",
+        "t1_train_s_per_20_iters": round(t1_train / it1 * w.iters * (w.m / 2), 2),
+        "t1_encode_mvec_per_s": round(ns / t1_enc / 1e6, 4),
+        "median_of": 3, "warmup_discarded": 1, "extrapolated": iters < w.iters,
+        "host_cpu": host_cpu(),
+        "sample": (f"T={T}: median of 3 runs of {iters} Lloyd iterations of all {w.m} "
+                   f"subspaces over the full {w.n:,}-vector corpus"
+                   + (f", scaled x{w.iters // iters} to {w.iters}" if iters < w.iters else "")
+                   + f"; encode of all {w.n:,} vectors, median of 3. T=1: {it1} iteration(s) "
+                     f"of 2 subspaces scaled to {w.iters} x {w.m}, encode of {ns:,} vectors. "
+                     f"Warm-up {warm_s:.1f} s discarded."),
+        "parity_full_size_2_iters": parity,
     }
 
 
+# ---------------------------------------------------------------------------
+# Counter summaries (rocprofv3 CSV -> profiles/*.json)
+# ---------------------------------------------------------------------------
+def _counter_rows(paths):
+    for p in paths:
+        p = Path(p)
+        files = [p] if p.is_file() else sorted(p.rglob("*counter_collection.csv"))
+        for f in files:
+            with open(f, newline="") as fh:
+                yield from csv.DictReader(fh)
+
+
+def _agent(paths):
+    for p in paths:
+        p = Path(p)
+        for f in ([p] if p.is_file() else sorted(p.rglob("*agent_info.csv"))):
+            if not f.name.endswith("agent_info.csv"):
+                continue
+            with open(f, newline="") as fh:
+                for r in csv.DictReader(fh):
+                    if r.get("Agent_Type") == "GPU":
+                        return {"cu": int(r["Cu_Count"]), "simd": int(r["Simd_Count"]),
+                                "xcc": int(r["Num_Xcc"])}
+    return {"cu": 256, "simd": 1024, "xcc": 8}
+
+
+def short_name(kernel: str) -> str:
+    """'void tacgpu::cand_kernel<4, false, ...>(float const*, ...)' ->
+    'cand_kernel<4, false, ...>'."""
+    k = kernel.replace("void ", "", 1) if kernel.startswith("void ") else kernel
+    depth, cut = 0, len(k)
+    for i, ch in enumerate(k):
+        if ch == "<":
+            depth += 1
+        elif ch == ">":
+            depth -= 1
+        elif ch == "(" and depth == 0:
+            cut = i
+            break
+    k = k[:cut]
+    return k.split("::")[-1] if "::" in k.split("<")[0] else k
+
+
+def _md_table(kernels: dict, cols) -> str:
+    lines = ["| kernel | " + " | ".join(c for c, _ in cols) + " |",
+             "|---|" + "---:|" * len(cols)]
+    for name, rec in kernels.items():
+        vals = []
+        for _, f in cols:
+            v = f(rec)
+            vals.append("-" if v is None else (f"{v:,.4g}" if isinstance(v, float) else f"{v:,}"))
+        lines.append(f"| {name} | " + " | ".join(vals) + " |")
+    return "\n".join(lines)
+
+
+def summarize_pmc(out_base: str, dirs, commands=()) -> None:
+    """Per-kernel averages of every counter over its launches, plus derived
+    figures: HBM bytes from FETCH_SIZE / WRITE_SIZE scaled by the 1 GiB copy
+    kernel (the largest __amd_rocclr_copyBuffer launch), and VALU issue use
+    from the SQ counters."""
+    agent = _agent(dirs)
+    per = {}  # kernel -> counter -> [values]
+    for r in _counter_rows(dirs):
+        name = short_name(r["Kernel_Name"])
+        per.setdefault(name, {}).setdefault(r["Counter_Name"], []).append(
+            float(r["Counter_Value"]))
+    copy = per.get("__amd_rocclr_copyBuffer", {})
+    gib_kib = float(1 << 20)
+    fscale = gib_kib / max(copy["FETCH_SIZE"]) if copy.get("FETCH_SIZE") else None
+    wscale = gib_kib / max(copy["WRITE_SIZE"]) if copy.get("WRITE_SIZE") else None
+    kernels = {}
+    for name, cs in sorted(per.items()):
+        avg = {c: sum(v) / len(v) for c, v in cs.items()}
+        rec = {"samples": max(len(v) for v in cs.values()), "counters": avg}
+        if "FETCH_SIZE" in avg and fscale:
+            rec["read_bytes"] = int(avg["FETCH_SIZE"] * 1024 * fscale)
+        if "WRITE_SIZE" in avg and wscale:
+            rec["write_bytes"] = int(avg["WRITE_SIZE"] * 1024 * wscale)
+        gui = avg.get("GRBM_GUI_ACTIVE")
+        if gui:
+            cyc = gui / agent["xcc"]  # summed over the XCDs
+            rec["cycles_per_xcd"] = round(cyc)
+            if "SQ_INSTS_VALU" in avg:
+                rec["valu_issue_frac"] = round(avg["SQ_INSTS_VALU"] / (agent["simd"] * cyc / 4), 4)
+            if "SQ_ACTIVE_INST_VALU" in avg:
+                rec["valu_busy"] = round(avg["SQ_ACTIVE_INST_VALU"] / (agent["cu"] * cyc), 4)
+            if "SQ_LDS_BANK_CONFLICT" in avg:
+                rec["lds_bank_conflict_frac"] = round(avg["SQ_LDS_BANK_CONFLICT"]
+                                                      / (agent["cu"] * cyc), 4)
+        if "SQ_THREAD_CYCLES_VALU" in avg and avg.get("SQ_ACTIVE_INST_VALU"):
+            rec["valu_lane_util"] = round(avg["SQ_THREAD_CYCLES_VALU"]
+                                          / (avg["SQ_ACTIVE_INST_VALU"] * 64), 4)
+        kernels[name] = rec
+    doc = {"agent": agent, "fetch_scale": fscale, "write_scale": wscale, "kernels": kernels}
+    Path(out_base + ".json").write_text(json.dumps(doc, indent=1, sort_keys=True) + "\n")
+    counters = sorted({c for rec in kernels.values() for c in rec["counters"]})
+    cols = [("samples", lambda r: r["samples"])]
+    if fscale:
+        cols.append(("HBM read MB", lambda r: r.get("read_bytes", 0) / 1e6 if "read_bytes" in r
+                     else None))
+    if wscale:
+        cols.append(("HBM write MB", lambda r: r.get("write_bytes", 0) / 1e6 if "write_bytes" in r
+                     else None))
+    for key, label in (("valu_issue_frac", "VALU issue"), ("valu_busy", "VALU busy"),
+                       ("valu_lane_util", "VALU lanes"),
+                       ("lds_bank_conflict_frac", "LDS conflict")):
+        if any(key in r for r in kernels.values()):
+            cols.append((label, lambda r, k=key: r.get(k)))
+    for c in counters:
+        cols.append((c, lambda r, k=c: (round(r["counters"][k]) if k in r["counters"] else None)))
+    md = [f"# rocprofv3 counters per kernel: {Path(out_base).name}", "",
+          "Values are averages over the samples of each kernel (one per launch per pass).",
+          f"Device: {agent['cu']} CUs, {agent['simd']} SIMDs, {agent['xcc']} XCDs.", ""]
+    if fscale or wscale:
+        md += [f"HBM bytes: FETCH_SIZE x {fscale and round(fscale, 4)}, WRITE_SIZE x "
+               f"{wscale and round(wscale, 4)} (KiB), the factors that make the 1 GiB "
+               "__amd_rocclr_copyBuffer launch read and write 1 GiB.", ""]
+    if any("valu_issue_frac" in r for r in kernels.values()):
+        md += ["VALU issue = SQ_INSTS_VALU / (SIMDs x GRBM_GUI_ACTIVE / XCDs / 4): the share of "
+               "the wave64 VALU issue slots (one per SIMD every 4 cycles) the kernel used. "
+               "VALU busy = SQ_ACTIVE_INST_VALU / (CUs x cycles); VALU lanes = "
+               "SQ_THREAD_CYCLES_VALU / (64 x SQ_ACTIVE_INST_VALU); LDS conflict = "
+               "SQ_LDS_BANK_CONFLICT / (CUs x cycles).", ""]
+    md += ["Commands:", "```", "cd /tmp && export TMPDIR=/tmp"] + list(commands) + [
+        "python3 bench.py --summarize-pmc " + " ".join([out_base] + [str(d) for d in dirs]),
+        "```", "", _md_table(kernels, cols), ""]
+    Path(out_base + ".md").write_text("\n".join(md))
+    log(f"wrote {out_base}.json and .md ({len(kernels)} kernels)")
+
+
+def _load_json(path: Path):
+    try:
+        return json.loads(path.read_text())
+    except (OSError, ValueError):
+        return None
+
+
+# ---------------------------------------------------------------------------
+# Roofline of the dominant kernel
+# ---------------------------------------------------------------------------
+def algorithmic_bytes(name: str, n: int, dim: int, m: int):
+    """Bytes a kernel must move per launch over the whole corpus: an
+    assignment or encode reads every residual once and writes one code per
+    vector and subspace (2 bytes during training, 1 in the encode output);
+    scatter reads the records and codes and writes the records; the fold
+    reads the records.  None for the small kernels."""
+    dsub = dim // m
+    dp = 1 if dsub <= 1 else 2 if dsub <= 2 else 4 if dsub <= 4 else 8
+    if name.startswith("cand_kernel") and ", true, true," in name:
+        return n * (4 * dim + m)
+    if name.startswith("encode_kernel"):
+        return n * (4 * dim + m)
+    if name.startswith(("cand_kernel", "assign_kernel")):
+        return n * (4 * dim + 2 * m)
+    if name.startswith("scatter_kernel"):
+        return n * m * (2 * 4 * dp + 2)
+    if name.startswith("fold_kernel"):
+        return n * m * 4 * dp
+    if name.startswith("transpose_kernel"):
+        return n * (4 * dim + 4 * m * dp)
+    return None
+
+
+def kernel_table(kt: dict, steps: int, train_ms: float):
+    rows = {}
+    for name, (ms, launches) in kt.items():
+        rows[name] = {"avg_ms": round(ms / max(launches, 1), 4),
+                      "launches_per_step": round(launches / steps, 2),
+                      "ms_per_step": round(ms / steps, 4),
+                      "share_of_step": round(ms / steps / train_ms, 4) if train_ms else None}
+    return dict(sorted(rows.items(), key=lambda kv: -kv[1]["ms_per_step"]))
+
+
+def roofline(name: str, row: dict, n: int, dim: int, m: int, traffic: dict, valu: dict):
+    ab = algorithmic_bytes(name, n, dim, m)
+    avg_s = row["avg_ms"] * 1e-3
+    achieved = ab / avg_s / 1e9 if ab else None
+    tr = traffic.get(name) if traffic else None
+    counted = None if not tr or "read_bytes" not in tr else tr["read_bytes"] + tr.get(
+        "write_bytes", 0)
+    out = {
+        "kernel": name, "bound": "hbm",
+        "achieved": None if achieved is None else round(achieved, 1),
+        "peak": PEAK_HBM_GBS, "unit": "GB/s",
+        "frac": None if achieved is None else round(achieved / PEAK_HBM_GBS, 4),
+        "traffic": counted,
+        "avg_launch_ms": row["avg_ms"], "algorithmic_bytes_per_launch": ab,
+        "launches_per_step": row["launches_per_step"], "share_of_step": row["share_of_step"],
+    }
+    if counted:
+        out["counted_hbm_gbs"] = round(counted / avg_s / 1e9, 1)
+        out["counted_over_algorithmic"] = round(counted / ab, 3) if ab else None
+    v = valu.get(name) if valu else None
+    if v:
+        c = v["counters"]
+        out["valu"] = {
+            "issue_frac": v.get("valu_issue_frac"), "busy": v.get("valu_busy"),
+            "lane_util": v.get("valu_lane_util"),
+            "lds_bank_conflict_frac": v.get("lds_bank_conflict_frac"),
+            "instr_per_launch": int(c["SQ_INSTS_VALU"]) if "SQ_INSTS_VALU" in c else None,
+            "live_ginstr_per_s": (round(c["SQ_INSTS_VALU"] / avg_s / 1e9, 1)
+                                  if "SQ_INSTS_VALU" in c else None),
+            "peak_ginstr_per_s": PEAK_VALU_GINSTR,
+            "source": str(VALU_FILE.relative_to(ROOT)),
+        }
+    return out
+
+
+# ---------------------------------------------------------------------------
+# Rows beside the headline
+# ---------------------------------------------------------------------------
 def residual_stage(device, x, ids, w, reps: int):
     """storage.build stage 2 on the corpus tokens (rebuilt as centre +
     residual): average kernel time per call over `reps` timed calls."""
@@ -94,6 +368,7 @@ def residual_stage(device, x, ids, w, reps: int):
     for _ in range(reps):
         device.residuals_device(dv, w.n, w.dim, dc, w.n_centers, da, dr, dn)
     p = device.profile_read(reset=True)
+    device.profile_enable(False)
     ms = p.residual_ms / max(p.residual_launches, 1)
     for a in (dv, dc, da, dr, dn):
         a.free()
@@ -106,7 +381,7 @@ def residual_stage(device, x, ids, w, reps: int):
     }
 
 
-def storage_and_query(device, x, ids, w, cents):
+def storage_and_query(device, x, ids, w, cents, with_cpu: bool):
     """The .tac rows around the PQ build on the corpus workload: per-document
     layouts of all tokens (documents of 1-100 tokens), the footer CRC-32 over
     those layouts, one query's distance table and refine of 1,000 candidate
@@ -114,7 +389,6 @@ def storage_and_query(device, x, ids, w, cents):
     import ctypes
     from tac_gpu import errors, lib, retrieval
     from tac_gpu import pq as pqmod
-    from oracle import binding as orc
 
     rng = np.random.default_rng(7)
     lens = rng.integers(1, 101, w.n // 40)
@@ -123,7 +397,10 @@ def storage_and_query(device, x, ids, w, cents):
     off = np.append(off, np.uint64(w.n))
     n_docs = off.size - 1
     codes = rng.integers(0, 256, (w.n, w.m)).astype(np.uint8)
-    total = int(orc.doc_payload_bytes(off, w.m, 1))
+    total_c = ctypes.c_uint64(0)
+    errors.check(lib.tac_doc_payload_bytes(off.ctypes.data_as(ctypes.c_void_p), n_docs, w.m, 1,
+                                           ctypes.byref(total_c)))
+    total = int(total_c.value)
     d_off = device.DeviceArray.from_host(off)
     d_ids = device.DeviceArray.from_host(ids)
     d_codes = device.DeviceArray.from_host(codes)
@@ -149,12 +426,10 @@ def storage_and_query(device, x, ids, w, cents):
                                                              None)))
     pc = device.profile_read(reset=True)
     k_crc = pc.crc_ms / max(pc.crc_launches, 1) * 1e-3
-    # query side on the same documents: 32 query tokens, refine 1,000 candidates
     n_q, dim = 32, w.dim
     q = rng.standard_normal((n_q, dim)).astype(np.float32)
     q /= np.linalg.norm(q, axis=1, keepdims=True)
     cb = rng.standard_normal((w.m, w.ksub, w.dsub)).astype(np.float32) * 0.05
-    p = pqmod.PQ(dim=dim, sub_dim=w.dsub, codebooks=cb.reshape(-1), m=w.m, ksub=w.ksub)
     d_q = device.DeviceArray.from_host(q)
     d_cb = device.DeviceArray.from_host(cb)
     d_tab = device.DeviceArray((w.m * w.ksub * n_q,), np.float32)
@@ -176,18 +451,11 @@ def storage_and_query(device, x, ids, w, cents):
     k_ref = pr.refine_ms / max(pr.refine_launches, 1) * 1e-3
     device.profile_enable(False)
     cand_tokens = int(sum(int(off[c + 1] - off[c]) for c in cand))
-    # CPU reference for refine on the same candidates (oracle, one thread)
-    tab = d_tab.to_host()
-    idx_h, pay_h = d_idx.to_host(), d_pay.to_host()
-    t0 = time.perf_counter()
-    for c in cand[:100]:
-        orc.refine(q, n_q, dim, cents, tab, w.m, w.ksub, idx_h, pay_h, off, norms, int(c))
-    t_ref_cpu = (time.perf_counter() - t0) * 10
-    lay_bytes = w.n * (4 + w.m) + 16 * n_docs + total  # ids + codes + offsets in, layouts out
-    return {
+    row = {
         "doc_layouts": {"tokens": w.n, "docs": n_docs, "payload_bytes": total,
                         "ms": round(t_lay * 1e3, 4),
-                        "hbm_gbs": round(lay_bytes / t_lay / 1e9, 1)},
+                        "hbm_gbs": round((w.n * (4 + w.m) + 16 * n_docs + total) / t_lay / 1e9,
+                                         1)},
         "crc32": {"bytes": total, "call_ms": round(t_crc * 1e3, 4),
                   "kernel_ms": round(k_crc * 1e3, 4),
                   "kernel_gbs": round(total / k_crc / 1e9, 1),
@@ -195,10 +463,21 @@ def storage_and_query(device, x, ids, w, cents):
         "distance_table": {"n_q": n_q, "m": w.m, "ksub": w.ksub, "us": round(t_tab * 1e6, 1)},
         "refine": {"n_q": n_q, "candidates": 1000, "candidate_tokens": cand_tokens,
                    "call_ms": round(t_ref * 1e3, 4), "kernel_ms": round(k_ref * 1e3, 4),
-                   "candidates_per_s": round(1000 / k_ref),
-                   "cpu_oracle_ms_1thread": round(t_ref_cpu * 1e3, 1)},
+                   "candidates_per_s": round(1000 / k_ref)},
         "note": "call times include launch, status readback and host synchronisation",
     }
+    if with_cpu:
+        from oracle import binding as orc
+        tab = d_tab.to_host()
+        idx_h, pay_h = d_idx.to_host(), d_pay.to_host()
+        t0 = time.perf_counter()
+        for c in cand[:100]:
+            orc.refine(q, n_q, dim, cents, tab, w.m, w.ksub, idx_h, pay_h, off, norms, int(c))
+        row["refine"]["cpu_oracle_ms_1thread"] = round((time.perf_counter() - t0) * 10 * 1e3, 1)
+    for a in (d_off, d_ids, d_codes, d_idx, d_pay, d_q, d_cb, d_tab, d_cent, d_norms, d_cand,
+              d_scores):
+        a.free()
+    return row
 
 
 def tac_clustering(device, with_cpu: bool):
@@ -255,27 +534,194 @@ def tac_clustering(device, with_cpu: bool):
     return row
 
 
+def train_encode_timing(device, dx, n, dim, m, ksub, dinit, steps, warmup):
+    """Median train and encode seconds over `steps` (after `warmup`) on
+    resident data, with the encode stage's device time."""
+    from tac_gpu import pq as pqmod
+    dcb = device.DeviceArray(dinit.shape, np.float32)
+    dcodes = device.DeviceArray((n, m), pqmod.code_dtype(ksub))
+    for _ in range(warmup):
+        device.train_device(dx, n, dim, m, ksub, dinit, dcb, 20, NEVER)
+        device.encode_device(dx, n, dim, m, ksub, dcb, dcodes)
+    device.synchronize()
+    tr, en = [], []
+    device.profile_enable(True)
+    device.profile_read(reset=True)
+    for _ in range(steps):
+        t0 = time.perf_counter()
+        device.train_device(dx, n, dim, m, ksub, dinit, dcb, 20, NEVER)
+        device.synchronize()
+        t1 = time.perf_counter()
+        device.encode_device(dx, n, dim, m, ksub, dcb, dcodes)
+        device.synchronize()
+        tr.append(t1 - t0)
+        en.append(time.perf_counter() - t1)
+    p = device.profile_read(reset=True)
+    device.profile_kernels(reset=True)
+    device.profile_enable(False)
+    dcb.free()
+    dcodes.free()
+    return statistics.median(tr), statistics.median(en), p
+
+
+def shape_sweep(device, dx, x, steps: int):
+    """(m32, dsub 2), (m8, dsub 8) and (m16, ksub 1024) on the resident
+    corpus: 20 Lloyd iterations from seeded-shuffle codebooks, then encode."""
+    from tac_gpu import synth
+    rows = {}
+    for name in ("corpus-1.52m-m32d2", "corpus-1.52m-m8d8", "corpus-1.52m-k1024"):
+        w = synth.WORKLOADS[name]
+        init = synth.shuffle_init(x, w.m, w.ksub, w.seed)
+        dinit = device.DeviceArray.from_host(init)
+        t_tr, t_en, p = train_encode_timing(device, dx, w.n, w.dim, w.m, w.ksub, dinit, steps, 1)
+        dinit.free()
+        cb = 1 if w.ksub <= 256 else 2
+        enc_ms = p.encode_ms / max(p.encode_launches, 1)
+        ebytes = w.n * (4 * w.dim + w.m * cb)
+        rows[name] = {
+            "m": w.m, "dsub": w.dim // w.m, "ksub": w.ksub, "lloyd_iters": 20,
+            "train_s": round(t_tr, 5),
+            "assign": "candidate sets" if w.ksub <= 256 else "pruned full search",
+            "encode_s": round(t_en, 6), "encode_mvec_per_s": round(w.n / t_en / 1e6, 1),
+            "encode_stage_ms": round(enc_ms, 4),
+            "encode_hbm_frac": round(ebytes / (enc_ms * 1e-3) / 1e9 / PEAK_HBM_GBS, 4),
+            "update_ms_per_iter": round(p.update_ms / max(p.update_iters, 1), 4),
+            "assign_ms_per_iter": round(p.assign_ms / max(p.assign_launches, 1), 4),
+        }
+        log(f"{name}: {rows[name]}")
+    return rows
+
+
+def paper_60m(device, steps: int):
+    """60,000,000 x 64 residuals generated on the device (Zipf 1.05 over
+    262,144 centres, sigma 0.12), resident; m16 k256, 25 Lloyd iterations
+    from seeded-shuffle codebooks."""
+    from tac_gpu import synth
+    w = synth.WORKLOADS["paper-60m"]
+    gen = synth.DeviceCorpus(w)
+    dx = device.DeviceArray((w.n, w.dim), np.float32)
+    t0 = time.perf_counter()
+    gen.fill(dx, w.n)
+    gen_s = time.perf_counter() - t0
+    init = gen.shuffle_init(dx, w.n, w.m, w.ksub, w.seed)
+    dinit = device.DeviceArray.from_host(init)
+    dcb = device.DeviceArray(init.shape, np.float32)
+    device.train_device(dx, w.n, w.dim, w.m, w.ksub, dinit, dcb, w.iters, NEVER)  # warm-up
+    device.synchronize()
+    times = []
+    device.profile_enable(True)
+    device.profile_read(reset=True)
+    for _ in range(steps):
+        t0 = time.perf_counter()
+        device.train_device(dx, w.n, w.dim, w.m, w.ksub, dinit, dcb, w.iters, NEVER)
+        device.synchronize()
+        times.append(time.perf_counter() - t0)
+    p = device.profile_read(reset=True)
+    device.profile_kernels(reset=True)
+    device.profile_enable(False)
+    for a in (dx, dinit, dcb):
+        a.free()
+    gen.free()
+    t = statistics.median(times)
+    return {"workload": "paper-60m", "n": w.n, "dim": w.dim, "m": w.m, "ksub": w.ksub,
+            "lloyd_iters": w.iters, "train_s": round(t, 4),
+            "ms_per_iter": round(t / w.iters * 1e3, 3),
+            "assign_ms_per_iter": round(p.assign_ms / max(p.assign_launches, 1), 3),
+            "update_ms_per_iter": round(p.update_ms / max(p.update_iters, 1), 3),
+            "resident_input_gb": round(w.n * w.dim * 4 / 1e9, 2),
+            "device_generation_s": round(gen_s, 2), "timed_runs": steps,
+            "data": "synthetic, generated on the device"}
+
+
+def stream_200m(device):
+    """200,000,000 residuals in 10M-vector chunks (generated on the device as
+    the 60M corpus is), encoded against fixed N(0, 0.05^2) codebooks, m16
+    k256: device encode time per chunk and the whole stream's HBM rate."""
+    from tac_gpu import synth
+    w = synth.WORKLOADS["stream-200m"]
+    chunk = 10_000_000
+    gen = synth.DeviceCorpus(w)
+    cb = synth.gauss_codebooks(w.seed, w.m, w.ksub, w.dsub, 0.05)
+    dcb = device.DeviceArray.from_host(cb)
+    dx = device.DeviceArray((chunk, w.dim), np.float32)
+    dcodes = device.DeviceArray((chunk, w.m), np.uint8)
+    gen.fill(dx, chunk, 0)
+    device.encode_device(dx, chunk, w.dim, w.m, w.ksub, dcb, dcodes)  # warm-up
+    device.synchronize()
+    enc = []
+    hist = np.zeros(w.ksub, np.int64)
+    t_all = time.perf_counter()
+    for k in range(w.n // chunk):
+        gen.fill(dx, chunk, k * chunk)
+        device.profile_enable(True)
+        device.profile_read(reset=True)
+        device.encode_device(dx, chunk, w.dim, w.m, w.ksub, dcb, dcodes)
+        p = device.profile_read(reset=True)
+        device.profile_enable(False)
+        enc.append(p.encode_ms)
+        if k == 0:
+            hist += np.bincount(dcodes.to_host().reshape(-1), minlength=w.ksub)
+    wall = time.perf_counter() - t_all
+    device.profile_kernels(reset=True)
+    for a in (dcb, dx, dcodes):
+        a.free()
+    gen.free()
+    tot_ms = float(sum(enc))
+    nbytes = w.n * (4 * w.dim + w.m)
+    return {"workload": "stream-200m", "n": w.n, "chunk": chunk, "chunks": len(enc),
+            "encode_ms_per_chunk": round(statistics.median(enc), 4),
+            "encode_s_total": round(tot_ms * 1e-3, 4),
+            "encode_mvec_per_s": round(w.n / (tot_ms * 1e-3) / 1e6, 1),
+            "hbm_gbs": round(nbytes / (tot_ms * 1e-3) / 1e9, 1),
+            "hbm_frac": round(nbytes / (tot_ms * 1e-3) / 1e9 / PEAK_HBM_GBS, 4),
+            "stream_wall_s": round(wall, 2),
+            "codes_in_range_chunk0": int(hist.sum()) == chunk * w.m,
+            "data": "synthetic, generated on the device chunk by chunk"}
+
+
+# ---------------------------------------------------------------------------
 def main() -> int:
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=5)
     ap.add_argument("--warmup", type=int, default=1)
     ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--headline-only", action="store_true",
+                    help="skip the shape sweep, 60M, 200M and the rows around the path")
     ap.add_argument("--traffic-pass", action="store_true",
                     help="short run for hardware-counter passes: one 2-iteration train, one "
-                         "encode and a 1 GiB device-to-device copy (the calibration kernel)")
+                         "encode, one residual-stage call and a 1 GiB device-to-device copy "
+                         "(the calibration kernel)")
+    ap.add_argument("--cpu-full", action="store_true",
+                    help="the CPU baseline protocol over all 20 iterations, printed as JSON")
+    ap.add_argument("--summarize-pmc", nargs="+", metavar=("OUT", "DIR"),
+                    help="write OUT.json and OUT.md: per-kernel averages of rocprofv3 counter "
+                         "CSVs in DIRs")
+    ap.add_argument("--pmc-command", action="append", default=[],
+                    help="a command line that produced the counters, quoted in OUT.md")
     args = ap.parse_args()
+    if args.summarize_pmc:
+        if len(args.summarize_pmc) < 2:
+            ap.error("--summarize-pmc OUT DIR [DIR ...]")
+        summarize_pmc(args.summarize_pmc[0], args.summarize_pmc[1:], args.pmc_command)
+        return 0
     if args.gpus != 1:
         print(f"bench.py measures one GPU only; --gpus {args.gpus} is not supported "
-              "(the PQ build path runs on a single MI355X).", file=sys.stderr)
+              "(this build runs the PQ path on a single MI355X).", file=sys.stderr)
         return 2
 
     from tac_gpu import device, errors, lib, synth
 
+    w = synth.WORKLOADS[WORKLOAD]
+    if args.cpu_full:
+        x = synth.residuals(w)
+        init = synth.shuffle_init(x, w.m, w.ksub, w.seed)
+        print(json.dumps(cpu_baseline(x, init, w, None, full=True)), flush=True)
+        return 0
+
     errors.check(lib.tac_gpu_set_device(0))
     info = device.device_info(0)
     info["name"] = info["name"] or info["arch"]
-    w = synth.WORKLOADS[WORKLOAD]
     t0 = time.perf_counter()
     x, ids = synth.residuals(w, with_ids=True)
     init = synth.shuffle_init(x, w.m, w.ksub, w.seed)
@@ -299,19 +745,13 @@ def main() -> int:
                           "copy_bytes": a.nbytes}), flush=True)
         return 0
 
-    def step():
-        device.train_device(dx, n, dim, m, ksub, dinit, dcb, iters, NEVER)
-        t_mid = time.perf_counter()
-        device.encode_device(dx, n, dim, m, ksub, dcb, dcodes)
-        return t_mid
-
     for i in range(args.warmup):
-        step()
+        device.train_device(dx, n, dim, m, ksub, dinit, dcb, iters, NEVER)
+        device.encode_device(dx, n, dim, m, ksub, dcb, dcodes)
         device.synchronize()
         log(f"warmup step {i + 1}/{args.warmup} done")
 
-    device.profile_enable(True)
-    device.profile_read(reset=True)
+    # Timed region: host clock around each synchronised train and encode.
     train_s, encode_s = [], []
     device.synchronize()
     t_all = time.perf_counter()
@@ -325,78 +765,36 @@ def main() -> int:
         te = time.perf_counter()
         train_s.append(tm - ts)
         encode_s.append(te - tm)
-        log(f"step {i + 1}/{args.steps}: train {1e3 * (tm - ts):.1f} ms, encode {1e3 * (te - tm):.2f} ms")
+        log(f"step {i + 1}/{args.steps}: train {1e3 * (tm - ts):.2f} ms, encode {1e3 * (te - tm):.3f} ms")
     total = time.perf_counter() - t_all
+    # The same steps again with every kernel bracketed by HIP events on the
+    # library's stream (the events themselves lengthen a step, so the value
+    # above is timed without them).
+    device.profile_enable(True)
+    device.profile_read(reset=True)
+    device.profile_kernels(reset=True)
+    for i in range(args.steps):
+        device.train_device(dx, n, dim, m, ksub, dinit, dcb, iters, NEVER)
+        device.encode_device(dx, n, dim, m, ksub, dcb, dcodes)
+    device.synchronize()
     prof = device.profile_read(reset=True)
+    kt = device.profile_kernels(reset=True)
     device.profile_enable(False)
-    # The drop-in call's defaults (src/index/pq.zig:319-325): k-means++ seeding,
-    # tol 1e-4, at most 25 iterations; the convergence test needs the serial
-    # wcss fold of every iteration.
-    device.synchronize()
-    t0 = time.perf_counter()
-    it_run, _, _ = device.train_device(dx, n, dim, m, ksub, None, dcb, 25, 1e-4, stats=True,
-                                       seed=0xa1b2c3d4)
-    device.synchronize()
-    drop_in = {"init": "k-means++ (GPU)", "tol": 1e-4, "max_iters": 25,
-               "iters_run_min": int(it_run.min()), "iters_run_max": int(it_run.max()),
-               "train_s": round(time.perf_counter() - t0, 5)}
-    log(f"drop-in defaults: {drop_in}")
-    residual = residual_stage(device, x, ids, w, 5)
-    device.profile_enable(False)
-    log(f"residual stage: {residual['avg_call_ms']} ms per call")
-    sq = storage_and_query(device, x, ids, w, synth.centers(w.seed, w.n_centers, w.dim))
-    log(f"storage/query rows: {sq}")
-    tacrow = tac_clustering(device, not args.no_cpu_baseline)
-    log(f"token-aware clustering: {tacrow}")
-
-    # Roofline of the dominant stage: the Lloyd assignment of iterations 1-19,
-    # which starts from the previous codes (neighbour rows, candidate
-    # assignment, full search of the deferred vectors).  Algorithmic FLOP per
-    # launch = n * 2 * dim * ksub, the reference's exhaustive search of one
-    # iteration over all m subspaces; the candidate path evaluates about 13
-    # codewords of 256 per vector-subspace, so the achieved figure is the
-    # exhaustive work delivered per second, and can pass the VALU peak; the
-    # stage's measured HBM traffic rate is reported beside it.  Iteration 0
-    # runs the full search (assign_kernel) and is reported on its own.
-    assign_flop = n * 2 * dim * ksub
-    cand_avg_ms = prof.cand_assign_ms / max(prof.cand_assign_iters, 1)
-    full_iters = prof.assign_launches - prof.cand_assign_iters
-    full_avg_ms = (prof.assign_ms - prof.cand_assign_ms) / max(full_iters, 1)
-    assign_avg_ms = cand_avg_ms
-    assign_tflops = assign_flop / (assign_avg_ms * 1e-3) / 1e12
-    encode_avg_ms = prof.encode_ms / max(prof.encode_launches, 1)
-    encode_flop = n * 2 * dim * ksub
-    encode_bytes = n * (4 * dim + m * 1)
-    update_avg_ms = prof.update_ms / max(prof.update_iters, 1)
-    update_bytes = n * (4 * dim + m * 2)
-
-    # HBM bytes per launch from the committed FETCH_SIZE / WRITE_SIZE counter
-    # passes (scaled by a 1 GiB copy kernel); null if the summary is absent.
-    traffic = {}
-    tfile = ROOT / "profiles" / f"pq_build_{WORKLOAD}_hbm_traffic.json"
-    if tfile.exists():
-        try:
-            for k, v in json.loads(tfile.read_text())["kernels"].items():
-                traffic[k] = int(v["read_bytes"]) + int(v["write_bytes"])
-        except (ValueError, OSError, KeyError, TypeError):
-            traffic = {}
-
-    cand_traffic = sum(traffic.get(k, 0) for k in (
-        "nbr_build_kernel<4>", "cand_kernel<4, false, false, unsigned short>",
-        "assign_list_kernel<4, 1>")) or None
-    cand_hbm_gbs = None if cand_traffic is None else cand_traffic / (assign_avg_ms * 1e-3) / 1e9
-
-    # Full-size parity: 2 GPU iterations vs the oracle's 2 iterations.
-    gpu_cb2 = None
-    cpu = None
-    if not args.no_cpu_baseline:
-        device.train_device(dx, n, dim, m, ksub, dinit, dcb, 2, NEVER)
-        gpu_cb2 = dcb.to_host().reshape(-1)
-        log("running the CPU baseline (oracle) sample")
-        cpu = cpu_baseline(x, init, w, gpu_cb2)
-
     mean_train = float(np.mean(train_s))
     mean_encode = float(np.mean(encode_s))
+    step_ms = 1e3 * (mean_train + mean_encode)
+    kernels = kernel_table(kt, args.steps, step_ms)
+    traffic = (_load_json(TRAFFIC_FILE) or {}).get("kernels", {})
+    valu = (_load_json(VALU_FILE) or {}).get("kernels", {})
+    dominant = next(iter(kernels)) if kernels else None
+    roof = roofline(dominant, kernels[dominant], n, dim, m, traffic, valu) if dominant else None
+    enc_names = [k for k in kernels if ", true, true," in k or k.startswith(
+        ("encode_kernel", "encode_list_kernel"))]
+    enc_ms = prof.encode_ms / max(prof.encode_launches, 1)
+    ebytes = n * (4 * dim + m)
+    update_ms = prof.update_ms / max(prof.update_iters, 1)
+    ubytes = n * (4 * dim + 2 * m)
+    assign_ms = prof.assign_ms / max(prof.assign_launches, 1)
     out = {
         "metric": METRIC,
         "value": round(mean_train, 5),
@@ -414,70 +812,87 @@ def main() -> int:
                    "ksub": ksub, "lloyd_iters": iters, "init": "seeded-shuffle prefix",
                    "tol": "never (fixed iterations)", "codes": "u8 token-major"},
         "train_s": round(mean_train, 5),
-        "exact_rescans_per_pass": round(prof.exact_rescans / max(prof.assign_launches
-                                                                  + prof.encode_launches, 1)),
         "encode_s": round(mean_encode, 6),
         "encode_mvec_per_s": round(n / mean_encode / 1e6, 2),
-        "roofline": {
-            "kernel": "Lloyd assignment from the previous codes (nbr_build_kernel + "
-                      "cand_kernel + assign_list_kernel), iterations 1-19, all subspaces",
-            "bound": "mfma", "engine": "VALU fp32 (exact unfused distance + argmin)",
-            "achieved": round(assign_tflops, 3), "peak": PEAK_FP32_TFLOPS, "unit": "TFLOP/s",
-            "frac": round(assign_tflops / PEAK_FP32_TFLOPS, 4),
-            "traffic": cand_traffic,
-            "avg_launch_ms": round(assign_avg_ms, 4), "algorithmic_flop_per_launch": assign_flop,
-            "deferred_to_full_search": round(prof.cand_deferred / max(prof.cand_vectors, 1), 4),
-            "measured_hbm_gbs": None if cand_hbm_gbs is None else round(cand_hbm_gbs, 1),
-            "measured_hbm_frac": None if cand_hbm_gbs is None else round(cand_hbm_gbs / PEAK_HBM_GBS, 4),
-            "note": "achieved = iterations x n x 2 x dim x ksub / time, the exhaustive search's "
-                    "FLOP delivered per second; the exact candidate method evaluates about 13 of "
-                    "256 codewords per vector-subspace, so frac can pass 1; measured_hbm_* is the "
-                    "stage's counted HBM traffic over the same time",
-        },
-        "first_iteration_roofline": {
-            "kernel": "Lloyd assignment of iteration 0 from grid anchors (nbr_build_kernel + "
-                      "grid_build_kernel + cand_kernel<4, true, false> + assign_list_kernel)",
-            "avg_launch_ms": round(full_avg_ms, 4),
-            "achieved": round(assign_flop / (full_avg_ms * 1e-3) / 1e12, 3),
-            "frac": round(assign_flop / (full_avg_ms * 1e-3) / 1e12 / PEAK_FP32_TFLOPS, 4),
-            "traffic": (sum(traffic.get(k, 0) for k in (
-                "nbr_build_kernel<4>", "grid_build_kernel<4>",
-                "cand_kernel<4, true, false, unsigned short>", "assign_list_kernel<4, 1>"))
-                        or None),
-        },
+        "roofline": roof,
         "encode_roofline": {
-            "avg_launch_ms": round(encode_avg_ms, 4),
-            "valu_tflops": round(encode_flop / (encode_avg_ms * 1e-3) / 1e12, 3),
-            "valu_frac": round(encode_flop / (encode_avg_ms * 1e-3) / 1e12 / PEAK_FP32_TFLOPS, 4),
-            "hbm_gbs": round(encode_bytes / (encode_avg_ms * 1e-3) / 1e9, 1),
-            "hbm_frac": round(encode_bytes / (encode_avg_ms * 1e-3) / 1e9 / PEAK_HBM_GBS, 4),
-            "traffic": (sum(traffic.get(k, 0) for k in (
-                "nbr_build_kernel<4>", "grid_build_kernel<4>", "cand_kernel<4, true, true, unsigned char>",
-                "encode_list_kernel<4, unsigned char>")) or None),
+            "stage": " + ".join(enc_names) if enc_names else None,
+            "avg_stage_ms": round(enc_ms, 4), "algorithmic_bytes": ebytes,
+            "hbm_gbs": round(ebytes / (enc_ms * 1e-3) / 1e9, 1),
+            "hbm_frac": round(ebytes / (enc_ms * 1e-3) / 1e9 / PEAK_HBM_GBS, 4),
+            "traffic": sum(traffic[k]["read_bytes"] + traffic[k].get("write_bytes", 0)
+                           for k in enc_names if k in traffic and "read_bytes" in traffic[k])
+                       or None,
         },
+        "assign_stage_ms_per_iter": round(assign_ms, 4),
         "update_roofline": {
-            "avg_iter_ms": round(update_avg_ms, 4),
-            "hbm_gbs": round(update_bytes / (update_avg_ms * 1e-3) / 1e9, 1),
-            "hbm_frac": round(update_bytes / (update_avg_ms * 1e-3) / 1e9 / PEAK_HBM_GBS, 4),
-            "traffic": (sum(traffic.get(k, 0) for k in (
-                "hist_kernel", "scan_partial_kernel", "scan_apply_kernel", "scatter_kernel<4>",
-                "fold_kernel<4>", "reseed_kernel<4>", "converge_kernel")) or None),
+            "avg_iter_ms": round(update_ms, 4), "algorithmic_bytes": ubytes,
+            "hbm_gbs": round(ubytes / (update_ms * 1e-3) / 1e9, 1),
+            "hbm_frac": round(ubytes / (update_ms * 1e-3) / 1e9 / PEAK_HBM_GBS, 4),
+            "traffic": sum(traffic[k]["read_bytes"] + traffic[k].get("write_bytes", 0)
+                           for k in traffic if "read_bytes" in traffic[k] and k.startswith(
+                               ("hist_kernel", "scan_partial", "scan_apply", "scatter_kernel",
+                                "fold_order", "fold_kernel", "reseed_kernel", "converge_kernel")))
+                       or None,
         },
-        "drop_in_defaults": drop_in,
-        "residual_stage": residual,
-        "storage_query": sq,
-        "tac_clustering": tacrow,
-        "cpu_baseline": None if cpu is None else {
-            "value": round(cpu["train_s_per_20_iters"], 3), "unit": "s/20 iters",
-            "encode_mvec_per_s": round(cpu["encode_mvec_per_s"], 3), "cores": cpu["cores"],
-            "kind": "port", "sample": cpu["sample"],
-        },
-        "parity_full_size_2_iters_bit_exact": None if cpu is None else cpu["parity_full_size"],
+        "kernels": {k: v for k, v in list(kernels.items())[:12]},
+        "kernel_timing": (f"HIP events around every kernel on the library's stream over "
+                          f"{args.steps} further steps of the same workload"),
+        "candidate_deferred_frac": round(prof.cand_deferred / max(prof.cand_vectors, 1), 4),
         "device": info["name"],
     }
-    if cpu is not None:
-        out["speedup_vs_cpu_train"] = round(cpu["train_s_per_20_iters"] / mean_train, 1)
-        out["speedup_vs_cpu_encode"] = round(out["encode_mvec_per_s"] / cpu["encode_mvec_per_s"], 1)
+    log(f"train {mean_train * 1e3:.3f} ms, encode {mean_encode * 1e3:.3f} ms; dominant {dominant}")
+
+    # The reference's drop-in defaults (src/index/pq.zig:319-325): k-means++,
+    # tol 1e-4, at most 25 iterations.
+    device.synchronize()
+    t0 = time.perf_counter()
+    it_run, _, _ = device.train_device(dx, n, dim, m, ksub, None, dcb, 25, 1e-4, stats=True,
+                                       seed=0xa1b2c3d4)
+    device.synchronize()
+    out["drop_in_defaults"] = {"init": "k-means++ (GPU)", "tol": 1e-4, "max_iters": 25,
+                               "iters_run_min": int(it_run.min()),
+                               "iters_run_max": int(it_run.max()),
+                               "train_s": round(time.perf_counter() - t0, 5)}
+
+    # Full-size parity: 2 GPU iterations, checked inside the CPU baseline.
+    device.train_device(dx, n, dim, m, ksub, dinit, dcb, 2, NEVER)
+    gpu_cb2 = dcb.to_host().reshape(-1)
+    if not args.headline_only:
+        out["shape_sweep"] = shape_sweep(device, dx, x, 3)
+    for a in (dinit, dcb, dcodes):
+        a.free()
+    dx.free()
+    device.synchronize()
+    errors.check(lib.tac_gpu_release_workspace())
+    if not args.headline_only:
+        out["paper_60m"] = paper_60m(device, 2)
+        log(f"paper-60m: {out['paper_60m']}")
+        errors.check(lib.tac_gpu_release_workspace())
+        out["stream_200m"] = stream_200m(device)
+        log(f"stream-200m: {out['stream_200m']}")
+        errors.check(lib.tac_gpu_release_workspace())
+        out["residual_stage"] = residual_stage(device, x, ids, w, 5)
+        out["storage_query"] = storage_and_query(device, x, ids, w,
+                                                 synth.centers(w.seed, w.n_centers, w.dim),
+                                                 not args.no_cpu_baseline)
+        out["tac_clustering"] = tac_clustering(device, not args.no_cpu_baseline)
+        log("rows around the path done")
+
+    if not args.no_cpu_baseline:
+        log(f"CPU baseline (oracle) on {host_threads()} threads")
+        cpu = cpu_baseline(x, init, w, gpu_cb2)
+        out["parity_full_size_2_iters_bit_exact"] = cpu.pop("parity_full_size_2_iters")
+        full = _load_json(CPU_FULL_FILE)
+        if full:
+            cpu["full_protocol"] = {k: full.get(k) for k in (
+                "value", "encode_mvec_per_s", "threads", "t1_train_s_per_20_iters",
+                "t1_encode_mvec_per_s", "host_cpu", "extrapolated")}
+            cpu["full_protocol"]["source"] = str(CPU_FULL_FILE.relative_to(ROOT))
+        out["cpu_baseline"] = cpu
+        out["speedup_vs_cpu_train"] = round(cpu["value"] / mean_train, 1)
+        out["speedup_vs_cpu_encode"] = round(out["encode_mvec_per_s"] / cpu["encode_mvec_per_s"],
+                                             1)
     print(json.dumps(out), flush=True)
     return 0
 

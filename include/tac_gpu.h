@@ -373,6 +373,19 @@ typedef struct tac_gpu_profile {
 int tac_gpu_profile_enable(int enable);
 int tac_gpu_profile_read(tac_gpu_profile *out, int reset);
 
+/* Per-kernel times: while profiling is enabled, training and encode bracket
+ * each kernel launch with HIP events on the stream it runs on.  `name` is the
+ * kernel as rocprofv3 reports it, without the namespace (for example
+ * "cand_kernel<4, false, false, unsigned short>"). */
+typedef struct tac_gpu_kernel_time {
+  char name[96];
+  double ms;          /* summed over launches */
+  uint64_t launches;
+} tac_gpu_kernel_time;
+/* Writes up to cap entries to out (sorted by name) and the number of
+ * distinct kernels timed to *count; reset clears the tallies. */
+int tac_gpu_profile_kernels(tac_gpu_kernel_time *out, uint32_t cap, uint32_t *count, int reset);
+
 #ifdef __cplusplus
 }
 #endif

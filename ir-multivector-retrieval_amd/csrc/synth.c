@@ -215,6 +215,14 @@ static int shuffle_prefix(uint64_t seed, uint64_t n, uint32_t ksub,
   return 0;
 }
 
+/* The rows tac_synth_shuffle_init takes for subspace mm are
+ * tac_synth_shuffle_prefix(seed + mm, n, ksub): for callers whose residuals
+ * live in device memory. */
+int tac_synth_shuffle_prefix(uint64_t seed, uint64_t n, uint32_t ksub, uint64_t *prefix) {
+  if (!prefix || ksub == 0 || (uint64_t)ksub > n) return 14;
+  return shuffle_prefix(seed, n, ksub, prefix);
+}
+
 int tac_synth_shuffle_init(const float *residuals, uint64_t n, uint32_t dim,
                            uint32_t m, uint32_t ksub, uint64_t seed,
                            float *codebooks) {

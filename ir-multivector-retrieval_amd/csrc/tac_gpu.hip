@@ -29,6 +29,8 @@
 
 #include <algorithm>
 #include <chrono>
+#include <cstdarg>
+#include <map>
 #include <cmath>
 #include <cstdio>
 #include <cstdlib>
@@ -99,6 +101,7 @@ struct DeviceState {
   bool crc_tx_ready = false;
   // measurement
   std::vector<hipEvent_t> events;
+  std::vector<hipEvent_t> kevents;  // per-kernel timers
 };
 
 DeviceState *g_devices[kMaxDevices] = {};
@@ -173,6 +176,93 @@ int resolve_stream(DeviceState &ds, void *stream, hipStream_t *out) {
   *out = ds.own_stream;
   return TAC_OK;
 }
+
+// ---- per-kernel timers (profiling only) ------------------------------------
+// While profiling is on, a call installs a KernelClock for its thread; every
+// instrumented launch is bracketed by two HIP events on its stream, and the
+// call adds the elapsed times to g_kernel_times by kernel name (the name
+// rocprofv3 reports, without the namespace) once its stream is synchronised.
+struct KernelMark {
+  char name[96];
+  size_t ev;
+};
+struct KernelClock {
+  DeviceState *ds = nullptr;
+  hipStream_t s = nullptr;
+  std::vector<KernelMark> marks;
+};
+thread_local KernelClock *tl_clock = nullptr;
+std::map<std::string, std::pair<double, uint64_t>> g_kernel_times;  // under g_profile_mu
+
+hipEvent_t kevent(DeviceState &ds, size_t idx) {
+  while (ds.kevents.size() <= idx) {
+    hipEvent_t ev = nullptr;
+    if (hipEventCreate(&ev) != hipSuccess) return nullptr;
+    ds.kevents.push_back(ev);
+  }
+  return ds.kevents[idx];
+}
+
+// Start of an instrumented launch; the name is printf-formatted.
+void kt_begin(const char *fmt, ...) {
+  KernelClock *c = tl_clock;
+  if (!c) return;
+  KernelMark mk;
+  va_list ap;
+  va_start(ap, fmt);
+  vsnprintf(mk.name, sizeof mk.name, fmt, ap);
+  va_end(ap);
+  mk.ev = 2 * c->marks.size();
+  hipEvent_t a = kevent(*c->ds, mk.ev);
+  if (!a || hipEventRecord(a, c->s) != hipSuccess) return;
+  c->marks.push_back(mk);
+}
+
+void kt_end() {
+  KernelClock *c = tl_clock;
+  if (!c || c->marks.empty()) return;
+  hipEvent_t b = kevent(*c->ds, c->marks.back().ev + 1);
+  if (!b || hipEventRecord(b, c->s) != hipSuccess) c->marks.pop_back();
+}
+
+// Brackets one launch statement (which may hold commas) with the timer.
+#define KT(...) kt_begin(__VA_ARGS__)
+#define KT_END() kt_end()
+
+template <typename T> constexpr const char *code_name();
+template <> constexpr const char *code_name<uint8_t>() { return "unsigned char"; }
+template <> constexpr const char *code_name<uint16_t>() { return "unsigned short"; }
+
+// Installs a clock on this thread for one call when profiling is on.
+struct ClockScope {
+  KernelClock clock;
+  bool on;
+  ClockScope(DeviceState &ds, hipStream_t s) : on(g_profile && !tl_clock) {
+    if (on) {
+      clock.ds = &ds;
+      clock.s = s;
+      tl_clock = &clock;
+    }
+  }
+  ~ClockScope() {
+    if (on) tl_clock = nullptr;
+  }
+  // Adds the call's kernel times; synchronises the stream.
+  int collect() {
+    if (!on || clock.marks.empty()) return TAC_OK;
+    HIP_TRY(hipStreamSynchronize(clock.s));
+    std::lock_guard<std::mutex> g(g_profile_mu);
+    for (const KernelMark &mk : clock.marks) {
+      float ms = 0.0f;
+      HIP_TRY(hipEventElapsedTime(&ms, clock.ds->kevents[mk.ev], clock.ds->kevents[mk.ev + 1]));
+      auto &t = g_kernel_times[mk.name];
+      t.first += ms;
+      t.second += 1;
+    }
+    clock.marks.clear();
+    return TAC_OK;
+  }
+};
 
 int event_at(DeviceState &ds, size_t idx, hipEvent_t *out) {
   while (ds.events.size() <= idx) {
@@ -278,8 +368,10 @@ struct Launch {
     if (rows > 64) rows = 64;
     if (rows == 0) return TAC_ERR_UNSUPPORTED;
     const size_t lds = (size_t)rows * (dim + 1) * sizeof(float);
+    KT("transpose_kernel<%d>", D);
     transpose_kernel<D><<<(unsigned)((n + rows - 1) / rows), kBlock, lds, s>>>(x, xs, n, dim,
                                                                             rows);
+    KT_END();
     return TAC_OK;
   }
   static constexpr int VPT = D <= 4 ? 8 : 4;  // vectors per thread in assign / encode
@@ -290,7 +382,9 @@ struct Launch {
     dim3 grid((unsigned)((n + kBlock * VPT - 1) / (kBlock * VPT)), M);
     const uint32_t Kp = (K + kPruneBlock - 1) / kPruneBlock * kPruneBlock;
     const size_t lds = (size_t)Kp * (Pad<D>::value + 1) * sizeof(float) + 2 * sizeof(uint32_t);
+    KT("assign_kernel<%d, %d>", D, VPT);
     assign_kernel<D, VPT><<<grid, kBlock, lds, s>>>(xs, cb, codes, e, done, n, K, rescans);
+    KT_END();
   }
   // Candidate-set assignment (cand_kernels.hpp): neighbour tables of the
   // current codebooks, the assignment from grid anchors (GRID, the first
@@ -303,15 +397,19 @@ struct Launch {
                          uint32_t *defer, uint32_t *defer_count, const uint32_t *done,
                          uint64_t n, uint32_t M, uint32_t K, uint32_t L, uint32_t *hist,
                          uint32_t T, unsigned long long *rescans, hipStream_t s) {
+    KT("nbr_build_kernel<%d>", D);
     nbr_build_kernel<D><<<dim3(K, M), kWave, 0, s>>>(cb, nbr, defer_count, done, K, L);
+    KT_END();
     uint32_t G = 0, cells = 0;
     if (GRID) {
       G = cand_grid_side(D);
       cells = 1;
       for (int k = 0; k < D; ++k) cells *= G;
+      KT("grid_build_kernel<%d, %uu>", D, cand_anchors<false>());
       grid_build_kernel<D, cand_anchors<false>()><<<dim3((cells + kBlock - 1) / kBlock, M), kBlock,
                                                      0, s>>>(
           cb, anchors, grid, K, G, cells);
+      KT_END();
     }
     // About 1,024 blocks over all subspaces; a chunk is whole sort tiles
     // (whole groups of kCandThreads vectors), at most kCandHistTiles of them.
@@ -324,11 +422,13 @@ struct Launch {
                                  GRID ? cand_anchors<false>() : 0u);
     if (int st = raise_lds((const void *)cand_kernel<D, GRID, false, uint16_t>, lay.total, cells))
       return st;
+    KT("cand_kernel<%d, %s, false, unsigned short>", D, GRID ? "true" : "false");
     cand_kernel<D, GRID, false, uint16_t><<<dim3((unsigned)nblk, M), kCandThreads, lay.total,
                                             s>>>(xs, cb, nbr, anchors, grid, codes, e, nullptr,
                                                  slice, defer, defer_count, done, n, 0, M, K, L,
                                                  (uint32_t)chunk, (uint32_t)nblk, G, cells, hist,
                                                  T);
+    KT_END();
     const uint32_t Kp = (K + kPruneBlock - 1) / kPruneBlock * kPruneBlock;
     const size_t lds = (size_t)Kp * (Pad<D>::value + 1) * sizeof(float) + 2 * sizeof(uint32_t);
     // About 2% of the vectors are deferred.  One vector per thread and about
@@ -337,9 +437,11 @@ struct Launch {
     // more.
     const uint64_t g = std::max<uint64_t>(
         1, std::min<uint64_t>((n + kBlock - 1) / kBlock, (4096 + M - 1) / M));
+    KT("assign_list_kernel<%d, 1>", D);
     assign_list_kernel<D, 1><<<dim3((unsigned)g, M), kBlock, lds, s>>>(
         xs, cb, codes, e, defer, defer_count, done, n, K, rescans,
         g_profile ? rescans + 1 : nullptr, hist, T);
+    KT_END();
     return TAC_OK;
   }
   // Candidate-set encode: neighbour rows and grid anchors of the codebooks,
@@ -361,10 +463,14 @@ struct Launch {
     const uint32_t G = cand_grid_side(D);
     uint32_t cells = 1;
     for (int k = 0; k < D; ++k) cells *= G;
+    KT("nbr_build_kernel<%d>", D);
     nbr_build_kernel<D><<<dim3(K, M), kWave, 0, s>>>(cb, nbr, defer_count, nullptr, K, L);
+    KT_END();
+    KT("grid_build_kernel<%d, %uu>", D, cand_anchors<true>());
     grid_build_kernel<D, cand_anchors<true>()><<<dim3((cells + kBlock - 1) / kBlock, M), kBlock,
                                                   0, s>>>(
         cb, anchors, grid, K, G, cells);
+    KT_END();
   }
   // The candidate pass over n token-major rows from the tables, then the
   // reference scan of the deferred vectors; defer_count must be zero, and
@@ -388,15 +494,19 @@ struct Launch {
     const uint64_t total = nchunks * M;
     if (total > 0xFFFFFFF0ull) return TAC_ERR_UNSUPPORTED;
     const uint32_t blocks = (uint32_t)(8 * ((total + 7) / 8));
+    KT("cand_kernel<%d, true, true, %s>", D, code_name<CodeT>());
     cand_kernel<D, true, true, CodeT><<<blocks, kCandThreads, lay.total, s>>>(
         x, cb, nbr, anchors, grid, nullptr, nullptr, codes, slice, defer, defer_count, nullptr, n,
         dim, M, K, L, (uint32_t)chunk, (uint32_t)nchunks, G, cells, nullptr, 0);
+    KT_END();
     const uint32_t Kp = (K + kPruneBlock - 1) / kPruneBlock * kPruneBlock;
     const size_t lds = (size_t)Kp * (Pad<D>::value + 1) * sizeof(float) + 2 * sizeof(uint32_t);
     const uint64_t g = std::max<uint64_t>(
         1, std::min<uint64_t>((n + kBlock - 1) / kBlock, (4096 + M - 1) / M));
+    KT("encode_list_kernel<%d, %s>", D, code_name<CodeT>());
     encode_list_kernel<D, CodeT><<<dim3((unsigned)g, M), kBlock, lds, s>>>(
         x, cb, codes, defer, defer_count, n, dim, M, K, rescans, stats);
+    KT_END();
     return TAC_OK;
   }
   static int scatter(const float *xs, const uint16_t *codes, const uint32_t *hist,
@@ -416,8 +526,10 @@ struct Launch {
     }
     const uint32_t total = M * T;
     const uint32_t blocks = 8 * ((total + 7) / 8);
+    KT("scatter_kernel<%d>", D);
     scatter_kernel<D><<<blocks, kBlock, lds, s>>>(xs, codes, hist, start, sorted, done, n, K, T,
                                                   M, code_bits(K));
+    KT_END();
     return TAC_OK;
   }
   static void kpp_update(const float *xs, float *w, uint16_t *src, double *bsum, uint32_t *bad,
@@ -430,13 +542,19 @@ struct Launch {
                    uint32_t K, hipStream_t s) {
     // Bins of 1/32 of the mean cluster size.
     const uint32_t unit = (uint32_t)std::max<uint64_t>(1, n / K / 32);
+    KT("fold_order_kernel");
     fold_order_kernel<<<1, 1024, 0, s>>>(counts, order, M * K, unit);
+    KT_END();
+    KT("fold_kernel<%d>", D);
     fold_kernel<D><<<M * K, kWave, 0, s>>>(sorted, counts, start, cb, done, order, n, K);
+    KT_END();
   }
   static void reseed(const float *xs, float *e, const uint32_t *counts, float *cb,
                      uint32_t *empties, const uint32_t *done, uint64_t n, uint32_t M, uint32_t K,
                      hipStream_t s) {
+    KT("reseed_kernel<%d>", D);
     reseed_kernel<D><<<M, 1024, 0, s>>>(xs, e, counts, cb, empties, done, n, K);
+    KT_END();
   }
   template <typename CodeT>
   static int encode(const float *x, const float *cb, CodeT *codes, uint64_t n, uint32_t dim,
@@ -447,8 +565,10 @@ struct Launch {
     const uint64_t total = tiles * M;
     if (total > 0xFFFFFFF0ull) return TAC_ERR_UNSUPPORTED;
     const uint32_t blocks = (uint32_t)(8 * ((total + 7) / 8));
+    KT("encode_kernel<%d, %d, %s>", D, VPT, code_name<CodeT>());
     encode_kernel<D, VPT, CodeT><<<blocks, kBlock, lds, s>>>(x, cb, codes, n, dim, M, K,
                                                               (uint32_t)tiles, rescans);
+    KT_END();
     return TAC_OK;
   }
 };
@@ -645,6 +765,7 @@ int train_core(DeviceState &ds, hipStream_t s, const float *d_x, uint64_t n, uin
   if ((st = counter_begin(ds, s, &rescans))) return st;
 
   const bool profile = g_profile;
+  ClockScope clock(ds, s);
   size_t ev = 0;
   hipEvent_t e0 = nullptr, e1 = nullptr;
   if (profile) {
@@ -699,12 +820,18 @@ int train_core(DeviceState &ds, hipStream_t s, const float *d_x, uint64_t n, uin
     }
     if (profile) HIP_TRY(hipEventRecord(b, s));
     if (!cand_now) {
+      KT("hist_kernel");
       hist_kernel<<<dim3(T, M), kBlock, hist_lds, s>>>(codes, hist, done, n, K, T);
+      KT_END();
       LAUNCH_TRY("hist_kernel");
     }
+    KT("scan_partial_kernel");
     scan_partial_kernel<<<dim3(G, M), kBlock, 0, s>>>(hist, scan_part, done, K, T, G);
+    KT_END();
+    KT("scan_apply_kernel");
     scan_apply_kernel<<<dim3(G, M), kBlock, 0, s>>>(hist, scan_part, counts, start, done, K, T,
                                                      G);
+    KT_END();
     LAUNCH_TRY("scan kernels");
     DISPATCH_D_ST(D, scatter(xs, codes, hist, start, sorted, done, n, M, K, T, s));
     if (st) return st;
@@ -714,17 +841,27 @@ int train_core(DeviceState &ds, hipStream_t s, const float *d_x, uint64_t n, uin
     LAUNCH_TRY("fold_kernel");
     if (check || (want_wcss && t + 1 == max_iters)) {
       const uint32_t fgrid = (nfc + kBlock / kWave - 1) / (kBlock / kWave);
+      KT("wcss_chunk_sums_kernel");
       wcss_chunk_sums_kernel<<<dim3(fgrid, M), kBlock, 0, s>>>(e, fold_pre, done, n, nfc);
+      KT_END();
+      KT("wcss_prefix_kernel");
       wcss_prefix_kernel<<<M, kBlock, 0, s>>>(fold_pre, done, nfc);
+      KT_END();
+      KT("wcss_quantize_kernel");
       wcss_quantize_kernel<<<dim3(fgrid, M), kBlock, 0, s>>>(e, fold_pre, fold_chunks, done, n,
                                                              nfc);
+      KT_END();
+      KT("wcss_apply_kernel");
       wcss_apply_kernel<<<M, kWave, 0, s>>>(e, fold_chunks, wcss, done, n, nfc);
+      KT_END();
       LAUNCH_TRY("wcss kernels");
     }
     DISPATCH_D(D, reseed(xs, e, counts, out.cb, empties, done, n, M, K, s));
     LAUNCH_TRY("reseed_kernel");
+    KT("converge_kernel");
     converge_kernel<<<(M + 63) / 64, 64, 0, s>>>(wcss, prev, done, iters_run, M, t, tol,
                                                    check ? 1 : 0);
+    KT_END();
     LAUNCH_TRY("converge_kernel");
     if (want_trace)
       HIP_TRY(hipMemcpyAsync(as<float>(ds.trace) + (size_t)t * cb_elems, out.cb,
@@ -768,6 +905,7 @@ int train_core(DeviceState &ds, hipStream_t s, const float *d_x, uint64_t n, uin
     if (out.h_iters_single) *out.h_iters_single = h_flags[M];
     if (profile) {
       if ((st = counter_collect(ds, s))) return st;
+      if ((st = clock.collect())) return st;
       std::lock_guard<std::mutex> g(g_profile_mu);
       float ms = 0.0f;
       HIP_TRY(hipEventElapsedTime(&ms, e0, e1));
@@ -795,6 +933,7 @@ int encode_core(DeviceState &ds, hipStream_t s, const float *d_x, uint64_t n, ui
                 uint32_t M, uint32_t K, const float *d_cb, void *d_codes) {
   const uint32_t D = dim / M;
   const bool profile = g_profile;
+  ClockScope clock(ds, s);
   hipEvent_t a = nullptr, b = nullptr;
   int st;
   unsigned long long *rescans = nullptr;
@@ -836,6 +975,7 @@ int encode_core(DeviceState &ds, hipStream_t s, const float *d_x, uint64_t n, ui
     float ms = 0.0f;
     HIP_TRY(hipEventElapsedTime(&ms, a, b));
     if ((st = counter_collect(ds, s))) return st;
+    if ((st = clock.collect())) return st;
     std::lock_guard<std::mutex> g(g_profile_mu);
     g_prof.encode_ms += ms;
     g_prof.encode_launches += 1;
@@ -1030,6 +1170,23 @@ int tac_gpu_profile_read(tac_gpu_profile *out, int reset) {
   std::lock_guard<std::mutex> g(g_profile_mu);
   *out = g_prof;
   if (reset) g_prof = tac_gpu_profile{};
+  return TAC_OK;
+}
+
+int tac_gpu_profile_kernels(tac_gpu_kernel_time *out, uint32_t cap, uint32_t *count, int reset) {
+  if (!count || (cap && !out)) return TAC_ERR_INVALID_ARGUMENT;
+  std::lock_guard<std::mutex> g(g_profile_mu);
+  uint32_t i = 0;
+  for (const auto &kv : g_kernel_times) {
+    if (i < cap) {
+      std::snprintf(out[i].name, sizeof out[i].name, "%s", kv.first.c_str());
+      out[i].ms = kv.second.first;
+      out[i].launches = kv.second.second;
+    }
+    ++i;
+  }
+  *count = i;
+  if (reset) g_kernel_times.clear();
   return TAC_OK;
 }
 

@@ -31,6 +31,10 @@ class TrainExtras(ctypes.Structure):
     ]
 
 
+class KernelTime(ctypes.Structure):
+    _fields_ = [("name", ctypes.c_char * 96), ("ms", ctypes.c_double), ("launches", c_u64)]
+
+
 class DeviceInfo(ctypes.Structure):
     _fields_ = [
         ("name", ctypes.c_char * 256),
@@ -156,6 +160,8 @@ SIGNATURES = {
                 c_void_p, c_void_p, c_u64, c_f32_p, ctypes.POINTER(c_u64)]),
     "tac_gpu_profile_enable": (c_int, [c_int]),
     "tac_gpu_profile_read": (c_int, [ctypes.POINTER(Profile), c_int]),
+    "tac_gpu_profile_kernels": (
+        c_int, [ctypes.POINTER(KernelTime), c_u32, ctypes.POINTER(c_u32), c_int]),
 }
 
 STATUS_NAMES = [

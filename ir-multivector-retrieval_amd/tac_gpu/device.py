@@ -65,6 +65,12 @@ class DeviceArray:
             raise errors.OutBufferWrongSize(f"{a.nbytes} bytes into a {self.nbytes}-byte buffer")
         errors.check(lib.tac_gpu_memcpy_htod(self.ptr, ctypes.c_void_p(a.ctypes.data), a.nbytes))
 
+    def read_row(self, i: int, out: np.ndarray) -> None:
+        """Copy row i of a 2-D array into the host array `out`."""
+        nb = out.nbytes
+        errors.check(lib.tac_gpu_memcpy_dtoh(ctypes.c_void_p(out.ctypes.data),
+                                             ctypes.c_void_p(self.ptr.value + i * nb), nb))
+
     def to_host(self) -> np.ndarray:
         out = np.empty(self.shape, dtype=self.dtype)
         errors.check(lib.tac_gpu_memcpy_dtoh(ctypes.c_void_p(out.ctypes.data), self.ptr,
@@ -164,3 +170,15 @@ def profile_read(reset: bool = True) -> KernelTimes:
                        p.cluster_lloyd_ms, p.cluster_calls, p.cluster_prep_ms,
                        p.cluster_call_ms, p.cand_vectors, p.cand_deferred, p.cand_assign_ms,
                        p.cand_assign_iters)
+
+
+def profile_kernels(reset: bool = True) -> dict:
+    """Per-kernel HIP-event times recorded while profiling was enabled:
+    {kernel name: (total ms, launches)}."""
+    from ._native import KernelTime
+    count = ctypes.c_uint32(0)
+    errors.check(lib.tac_gpu_profile_kernels(None, 0, ctypes.byref(count), 0))
+    arr = (KernelTime * max(count.value, 1))()
+    errors.check(lib.tac_gpu_profile_kernels(arr, count.value, ctypes.byref(count),
+                                             1 if reset else 0))
+    return {k.name.decode(): (float(k.ms), int(k.launches)) for k in arr[:count.value]}

@@ -66,8 +66,9 @@ def _lib() -> ctypes.CDLL:
                                         u64, vp, vp, u32]
     lib.tac_synth_shuffle_init.argtypes = [vp, u64, u32, u32, u32, u64, vp]
     lib.tac_synth_gauss_codebooks.argtypes = [u64, u32, u32, u32, ctypes.c_float, vp]
+    lib.tac_synth_shuffle_prefix.argtypes = [u64, u64, u32, vp]
     for f in (lib.tac_synth_centers, lib.tac_synth_residuals, lib.tac_synth_shuffle_init,
-              lib.tac_synth_gauss_codebooks):
+              lib.tac_synth_gauss_codebooks, lib.tac_synth_shuffle_prefix):
         f.restype = ctypes.c_int
     return lib
 
@@ -119,6 +120,75 @@ def shuffle_init(x: np.ndarray, m: int, ksub: int, seed: int) -> np.ndarray:
     x = np.ascontiguousarray(x, dtype=np.float32)
     assert lib().tac_synth_shuffle_init(_p(x), n, dim, m, ksub, seed, _p(out)) == 0
     return out
+
+
+def _gpu_lib() -> ctypes.CDLL:
+    path = SYNTH_PATH.with_name("libtac_synth_gpu.so")
+    if not path.exists():
+        raise ImportError(f"{path} is not built")
+    lib = ctypes.CDLL(os.fspath(path))
+    vp, u64, u32 = ctypes.c_void_p, ctypes.c_uint64, ctypes.c_uint32
+    lib.tac_synth_residuals_device.argtypes = [u64, u64, u32, u32, vp, vp, ctypes.c_float, u64,
+                                               vp, vp]
+    lib.tac_synth_residuals_device.restype = ctypes.c_int
+    return lib
+
+
+_GL = None
+
+
+def zipf_cdf(n_centers: int, s: float) -> np.ndarray:
+    """Normalised Zipf(s) CDF over centres, accumulated in index order as
+    synth.c does."""
+    acc = np.cumsum(np.power(np.arange(1, n_centers + 1, dtype=np.float64), -s))
+    cdf = acc / acc[-1]
+    cdf[-1] = 1.0
+    return cdf
+
+
+class DeviceCorpus:
+    """Residual rows of a workload generated on the device (the kernel form of
+    the same generator), for inputs too large to generate on the host."""
+
+    def __init__(self, w: Workload):
+        global _GL
+        from . import device
+        if _GL is None:
+            _GL = _gpu_lib()
+        self.w = w
+        self.centers = device.DeviceArray.from_host(
+            np.ascontiguousarray(_centers(w.seed, w.n_centers, w.dim)))
+        self.cdf = (device.DeviceArray.from_host(zipf_cdf(w.n_centers, w.zipf))
+                    if w.zipf > 0 else None)
+
+    def fill(self, out, n: int, first: int = 0) -> None:
+        """Rows first .. first+n-1 into the device array `out` ([>= n][dim] f32)."""
+        from . import device
+        assert out.nbytes >= n * self.w.dim * 4
+        st = _GL.tac_synth_residuals_device(
+            self.w.seed, n, self.w.dim, self.w.n_centers, self.centers.ptr,
+            self.cdf.ptr if self.cdf is not None else None, self.w.sigma, first, out.ptr, None)
+        assert st == 0, st
+        device.synchronize()
+
+    def shuffle_init(self, x, n: int, m: int, ksub: int, seed: int) -> np.ndarray:
+        """shuffle_init's codebooks, read from the device rows x[0 .. n)."""
+        dim = self.w.dim
+        dsub = dim // m
+        out = np.empty((m, ksub, dsub), np.float32)
+        pre = np.empty(ksub, np.uint64)
+        row = np.empty(dim, np.float32)
+        for mm in range(m):
+            assert lib().tac_synth_shuffle_prefix(seed + mm, n, ksub, _p(pre)) == 0
+            for c in range(ksub):
+                x.read_row(int(pre[c]), row)
+                out[mm, c] = row[mm * dsub:(mm + 1) * dsub]
+        return out
+
+    def free(self) -> None:
+        self.centers.free()
+        if self.cdf is not None:
+            self.cdf.free()
 
 
 def gauss_codebooks(seed: int, m: int, ksub: int, dsub: int, sigma: float) -> np.ndarray:
