@@ -111,7 +111,21 @@ class EmptyTokenDump(TacError):
     status = 24
 
 
-_BY_STATUS = {cls.status: cls for cls in TacError.__subclasses__()}
+# StorageError (src/index/storage.zig:40-47) raised by the host-side .tac
+# header and layout parser; no C-ABI status carries them.
+class InvalidIndex(TacError):
+    status = None
+
+
+class UnsupportedVersion(TacError):
+    status = None
+
+
+class IndexCorrupt(TacError):
+    status = None
+
+
+_BY_STATUS = {cls.status: cls for cls in TacError.__subclasses__() if cls.status is not None}
 
 
 def check(status: int) -> None:
