@@ -581,7 +581,7 @@ def shape_sweep(device, dx, x, steps: int):
         rows[name] = {
             "m": w.m, "dsub": w.dim // w.m, "ksub": w.ksub, "lloyd_iters": 20,
             "train_s": round(t_tr, 5),
-            "assign": "candidate sets" if w.ksub <= 256 else "pruned full search",
+            "assign": "candidate sets",
             "encode_s": round(t_en, 6), "encode_mvec_per_s": round(w.n / t_en / 1e6, 1),
             "encode_stage_ms": round(enc_ms, 4),
             "encode_hbm_frac": round(ebytes / (enc_ms * 1e-3) / 1e9 / PEAK_HBM_GBS, 4),

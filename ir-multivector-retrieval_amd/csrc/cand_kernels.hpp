@@ -71,7 +71,8 @@ constexpr uint32_t kCandAnchorsMax = 3;
 // LDS layout of cand_kernel, shared by the host launcher:
 //   lcb [K][DP] f32 | lsamp [K][8] u32: the value bits of row entries
 //   0, 7, 15, ..., 55 (all-ones past the row) | grid anchors only:
-//   lanc [cells][na] u8 anchors (na = cand_anchors), lgrid [2][8] f32 (cell
+//   lanc [cells][na] anchors (na = cand_anchors; u8 up to K = 256, else u16),
+//   lgrid [2][8] f32 (cell
 //   origin, cells per unit) |
 //   per wave: gx [64][DP] f32, gbest [64] u64, ga [64] u32 (the anchor's
 //   row offset),
@@ -83,11 +84,11 @@ struct CandLds {
 };
 __host__ __device__ inline uint32_t cand_up16(uint32_t b) { return (b + 15u) & ~15u; }
 __host__ __device__ inline CandLds cand_lds(uint32_t K, uint32_t DP, uint32_t cells = 0,
-                                            uint32_t hist_tiles = 0, uint32_t na = 0) {
+                                            uint32_t hist_tiles = 0, uint32_t anchor_bytes = 0) {
   CandLds s;
   s.samp_off = cand_up16(K * DP * 4u);
   s.anc_off = s.samp_off + K * 8u * 4u;
-  s.grid_off = cand_up16(s.anc_off + cells * na);
+  s.grid_off = cand_up16(s.anc_off + cells * anchor_bytes);
   s.wave_off = s.grid_off + (cells ? 64u : 0u);
   s.wave_bytes = 64u * (DP * 4u + 8u + 4u) + 64u * 8u * 2u;
   s.scal_off = s.wave_off + (uint32_t)kCandWaves * s.wave_bytes;
@@ -111,27 +112,30 @@ __host__ __device__ inline uint32_t cand_grid_side(uint32_t D) {
   }
 }
 
-// One wave per (codeword a, subspace m): lo(a, c) for every c != a, a
-// bitonic sort of the 256 keys in LDS, the first L written to
-// nbr[m][a][0 .. L) and cand_pad_key(a) to the rest of the stored row
-// nbr[m][a][L .. cand_row_len(L)).  Block (0, m) also clears the subspace's deferred
-// count for the assignment that follows on the same stream.
+// One block per (codeword a, subspace m) (one wave up to K = 256, four
+// beyond): lo(a, c) for every c != a, a bitonic sort of the next power of two
+// >= K keys in LDS, the first L written to nbr[m][a][0 .. L) and
+// cand_pad_key(a) to the rest of the stored row nbr[m][a][L .. cand_row_len(L)).
+// Block (0, m) also clears the subspace's deferred count for the assignment
+// that follows on the same stream.
 template <int D>
-__global__ __launch_bounds__(kWave) void nbr_build_kernel(const float* __restrict__ cb,
-                                                          uint32_t* __restrict__ nbr,
-                                                          uint32_t* __restrict__ defer_count,
-                                                          const uint32_t* __restrict__ done,
-                                                          uint32_t K, uint32_t L) {
+__global__ __launch_bounds__(256) void nbr_build_kernel(const float* __restrict__ cb,
+                                                        uint32_t* __restrict__ nbr,
+                                                        uint32_t* __restrict__ defer_count,
+                                                        const uint32_t* __restrict__ done,
+                                                        uint32_t K, uint32_t L) {
   __shared__ uint32_t keys[kCandMaxK];
-  const uint32_t a = blockIdx.x, m = blockIdx.y, lane = threadIdx.x;
-  if (a == 0 && lane == 0) defer_count[m] = 0;
+  const uint32_t a = blockIdx.x, m = blockIdx.y, t = threadIdx.x;
+  if (a == 0 && t == 0) defer_count[m] = 0;
   if (done && done[m]) return;
   constexpr float g = cand_gamma(D);
+  uint32_t P = kWave;  // keys sorted: the next power of two >= K, at least 64
+  while (P < K) P <<= 1;
   const float* cbm = cb + (uint64_t)m * K * D;
   float ca[D];
 #pragma unroll
   for (int k = 0; k < D; ++k) ca[k] = cbm[(uint64_t)a * D + k];
-  for (uint32_t c = lane; c < kCandMaxK; c += kWave) {
+  for (uint32_t c = t; c < P; c += blockDim.x) {
     uint32_t key = kCandNoKey;
     if (c < K && c != a) {
       float cv[D];
@@ -141,10 +145,10 @@ __global__ __launch_bounds__(kWave) void nbr_build_kernel(const float* __restric
     }
     keys[c] = key;
   }
-  wave_lds_sync();
-  for (uint32_t k = 2; k <= kCandMaxK; k <<= 1) {
+  __syncthreads();
+  for (uint32_t k = 2; k <= P; k <<= 1) {
     for (uint32_t j = k >> 1; j > 0; j >>= 1) {
-      for (uint32_t q = lane; q < kCandMaxK / 2; q += kWave) {
+      for (uint32_t q = t; q < P / 2; q += blockDim.x) {
         const uint32_t i = ((q & ~(j - 1)) << 1) | (q & (j - 1));
         const uint32_t p = i | j;
         const uint32_t x = keys[i], y = keys[p];
@@ -154,12 +158,12 @@ __global__ __launch_bounds__(kWave) void nbr_build_kernel(const float* __restric
           keys[p] = x;
         }
       }
-      wave_lds_sync();
+      __syncthreads();
     }
   }
   const uint32_t Lr = cand_row_len(L);
   uint32_t* row = nbr + ((uint64_t)m * K + a) * Lr;
-  for (uint32_t j = lane; j < Lr; j += kWave) row[j] = j < L ? keys[j] : cand_pad_key(a);
+  for (uint32_t j = t; j < Lr; j += blockDim.x) row[j] = j < L ? keys[j] : cand_pad_key(a);
 }
 
 // Grid anchors of subspace m = blockIdx.y: the bounding box of the
@@ -167,9 +171,9 @@ __global__ __launch_bounds__(kWave) void nbr_build_kernel(const float* __restric
 // the NA codewords nearest its centre (any choice is valid; nearness only
 // keeps the candidate sets small; with K < NA the nearest repeats).
 // grid[m] = {lo[8], G / (hi - lo)[8]}, anchors[m][cell][0 .. NA).
-template <int D, uint32_t NA>
+template <int D, uint32_t NA, typename AnchorT>
 __global__ __launch_bounds__(kBlock) void grid_build_kernel(const float* __restrict__ cb,
-                                                            uint8_t* __restrict__ anchors,
+                                                            AnchorT* __restrict__ anchors,
                                                             float* __restrict__ grid,
                                                             uint32_t K, uint32_t G,
                                                             uint32_t cells) {
@@ -234,7 +238,7 @@ __global__ __launch_bounds__(kBlock) void grid_build_kernel(const float* __restr
   }
 #pragma unroll
   for (uint32_t q = 0; q < NA; ++q)
-    anchors[((uint64_t)m * cells + cell) * NA + q] = (uint8_t)(q < K ? bc[q] : bc[0]);
+    anchors[((uint64_t)m * cells + cell) * NA + q] = (AnchorT)(q < K ? bc[q] : bc[0]);
 }
 
 // Inclusive sum over the 64 lanes of a wave with DPP moves: shifts of 1, 2,
@@ -266,10 +270,10 @@ __device__ inline uint32_t wave_inclusive_sum(uint32_t v) {
 // kSortTile vectors (the chunk is whole tiles) and writes
 // hist[m][tile][code] for the update's counting sort; the deferred vectors'
 // codes are added there by assign_list_kernel.
-template <int D, bool GRID, bool TOKENS, typename CodeT>
+template <int D, bool GRID, bool TOKENS, typename CodeT, typename AnchorT>
 __global__ __launch_bounds__(kCandThreads) void cand_kernel(
     const float* __restrict__ xin, const float* __restrict__ cb,
-    const uint32_t* __restrict__ nbr, const uint8_t* __restrict__ anchors,
+    const uint32_t* __restrict__ nbr, const AnchorT* __restrict__ anchors,
     const float* __restrict__ grid, uint16_t* __restrict__ codes, float* __restrict__ e,
     CodeT* __restrict__ out, uint32_t* __restrict__ slice, uint32_t* __restrict__ defer,
     uint32_t* __restrict__ defer_count, const uint32_t* __restrict__ done, uint64_t n,
@@ -293,11 +297,11 @@ __global__ __launch_bounds__(kCandThreads) void cand_kernel(
   const uint32_t tiles = TOKENS ? 0u : chunk / kSortTile;  // the chunk is whole tiles
   const uint32_t Kw = (K + 1u) / 2u;                       // u16 pairs per tile
   constexpr uint32_t NA = cand_anchors<TOKENS>();
-  const CandLds lay = cand_lds(K, DP, GRID ? cells : 0u, tiles, GRID ? NA : 0u);
+  const CandLds lay = cand_lds(K, DP, GRID ? cells : 0u, tiles, GRID ? NA * (uint32_t)sizeof(AnchorT) : 0u);
   uint8_t* base = reinterpret_cast<uint8_t*>(lds);
   float* lcb = lds;
   uint32_t* lsamp = reinterpret_cast<uint32_t*>(base + lay.samp_off);
-  uint8_t* lanc = base + lay.anc_off;
+  AnchorT* lanc = reinterpret_cast<AnchorT*>(base + lay.anc_off);
   float* lgrid = reinterpret_cast<float*>(base + lay.grid_off);
   const uint32_t t = threadIdx.x, lane = t % kWave, wave = t / kWave;
   uint8_t* wb = base + lay.wave_off + wave * lay.wave_bytes;
@@ -333,7 +337,7 @@ __global__ __launch_bounds__(kCandThreads) void cand_kernel(
   const uint32_t rs = Lr;
   for (uint32_t j = t; j < K * 8; j += blockDim.x) lsamp[j] = cand_sample(nbm + (j / 8) * Lr, L, j % 8);
   if constexpr (GRID) {
-    const uint8_t* am = anchors + (uint64_t)m * cells * NA;
+    const AnchorT* am = anchors + (uint64_t)m * cells * NA;
     for (uint32_t j = t; j < cells * NA; j += blockDim.x) lanc[j] = am[j];
     if (t < 16) lgrid[t] = grid[m * 16 + t];
   }
@@ -470,7 +474,7 @@ __global__ __launch_bounds__(kCandThreads) void cand_kernel(
       unsigned long long best = ~0ull;
 #pragma unroll
       for (uint32_t k = 0; k < kCandItem; ++k) {
-        const uint32_t c16 = keys[k] & 0xFF0u;  // c << 4
+        const uint32_t c16 = keys[k] & kCandIdField;  // c << 4
         float cv[D];
         load_padded<D>(lcb + (c16 >> 4) * DP, cv);
         const unsigned long long key =

@@ -7,7 +7,7 @@
 // (src/util/vec.zig:109-175: D squares and D-1 adds, separately rounded):
 //   * R2 = cand_radius(U2) >= 4 (U2 + eta) / (1 - g), g = gamma_{D+2};
 //   * a neighbour key stores cand_lower_bound(ref(c_a, c)) <= ||c_a - c||^2
-//     in its value bits and c << 4 in its low 12 bits;
+//     in its value bits and c << 4 in its low 14 bits (K <= 1024);
 //   * every codeword that ties or beats c_a under ref() has a key value
 //     <= R2, so the reference's first-index argmin lies in
 //     {a} + {c : value(key(a, c)) <= R2}.
@@ -28,7 +28,7 @@ namespace tacgpu {
 
 constexpr uint32_t kCandList = 64;  // neighbours kept per codeword
 constexpr uint32_t kCandItem = 8;   // candidates per work item
-constexpr uint32_t kCandMaxK = 256; // codeword ids fit the key's low 12 bits as id << 4
+constexpr uint32_t kCandMaxK = 1024; // codeword ids fit the key's low 14 bits as id << 4
 
 TAC_HD inline uint32_t cand_f2u(float f) {
   uint32_t u;
@@ -62,16 +62,17 @@ TAC_HD inline float cand_lower_bound(float s, float g) {
   return lo > 0.0f ? lo : 0.0f;
 }
 
-// Key of neighbour c: the bound's bits with the low 12 bits replaced by
-// c << 4, which is also the byte offset of codeword c in a table of 16-byte
-// codewords.  Clearing low bits of a non-negative float lowers it, so the
-// value part stays a lower bound, and sorting keys sorts by bound, then by id.
-constexpr uint32_t kCandValueMask = 0xFFFFF000u;
+// Key of neighbour c: the bound's bits with the low 14 bits replaced by
+// c << 4 (the bound keeps 9 mantissa bits).  Clearing low bits of a
+// non-negative float lowers it, so the value part stays a lower bound, and
+// sorting keys sorts by bound, then by id.
+constexpr uint32_t kCandValueMask = 0xFFFFC000u;
+constexpr uint32_t kCandIdField = 0x3FF0u;  // c << 4
 TAC_HD inline uint32_t cand_key(float lo, uint32_t c) {
   return (cand_f2u(lo) & kCandValueMask) | (c << 4);
 }
 TAC_HD inline float cand_key_value(uint32_t key) { return cand_u2f(key & kCandValueMask); }
-TAC_HD inline uint32_t cand_key_code(uint32_t key) { return (key >> 4) & 0xFFu; }
+TAC_HD inline uint32_t cand_key_code(uint32_t key) { return (key & kCandIdField) >> 4; }
 constexpr uint32_t kCandNoKey = 0xFFFFFFFFu;  // value part is NaN: never inside R2
 // Padding entry of anchor a's stored row: its value part is NaN, so no
 // sample counts it, and its code is a, a real codeword, so an item that

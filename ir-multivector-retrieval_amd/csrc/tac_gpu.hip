@@ -343,23 +343,37 @@ int validate_pq(uint64_t n, uint32_t dim, uint32_t m, uint32_t ksub) {
 
 // ---- kernel launchers -------------------------------------------------------
 
-// Raises a kernel's dynamic-LDS limit above the 64 KB default once per
-// function, to the largest layout it can be launched with (the candidate
-// kernels at K = 256 and the given anchor-table size).
+// Raises a kernel's dynamic-LDS limit above the 64 KB default to the largest
+// layout it has been launched with (at most kCandLdsMax).
 int raise_lds(const void *fn, uint32_t bytes, uint32_t cells) {
+  (void)cells;
   if (bytes <= 65536) return TAC_OK;
+  if (bytes > kCandLdsMax) return TAC_ERR_UNSUPPORTED;
   static std::mutex mu;
-  static std::vector<const void *> raised;
+  static std::vector<std::pair<const void *, uint32_t>> raised;
   std::lock_guard<std::mutex> g(mu);
-  for (const void *f : raised)
-    if (f == fn) return TAC_OK;
-  const uint32_t most = cand_lds(kCandMaxK, 8, cells, kCandHistTiles, kCandAnchorsMax).total;
-  const hipError_t err = hipFuncSetAttribute(fn, hipFuncAttributeMaxDynamicSharedMemorySize,
-                                            (int)(most > bytes ? most : bytes));
+  for (auto &f : raised)
+    if (f.first == fn && f.second >= bytes) return TAC_OK;
+  const hipError_t err =
+      hipFuncSetAttribute(fn, hipFuncAttributeMaxDynamicSharedMemorySize, (int)bytes);
   if (err != hipSuccess) return hip_status("hipFuncSetAttribute(candidate kernel)", err);
-  raised.push_back(fn);
+  for (auto &f : raised)
+    if (f.first == fn) {
+      f.second = bytes;
+      return TAC_OK;
+    }
+  raised.push_back({fn, bytes});
   return TAC_OK;
 }
+
+// Sort tiles a training candidate block counts (its chunk is whole tiles):
+// kCandHistTiles, fewer when the tile histograms would not fit the LDS.
+inline uint32_t cand_hist_tiles(uint32_t K, uint32_t DP, uint32_t cells, uint32_t anchor_bytes) {
+  uint32_t tiles = kCandHistTiles;
+  while (tiles > 1 && cand_lds(K, DP, cells, tiles, anchor_bytes).total > kCandLdsMax) tiles >>= 1;
+  return tiles;
+}
+inline uint32_t nbr_threads(uint32_t K) { return K > 256 ? 256u : (uint32_t)kWave; }
 
 template <int D>
 struct Launch {
@@ -391,43 +405,45 @@ struct Launch {
   // Lloyd iteration) or from the previous codes, then the pruned full search
   // of the deferred vectors.  Both passes also count the new codes per sort
   // tile into hist[M][T][K] for the update.
-  template <bool GRID>
-  static int assign_cand(const float *xs, const float *cb, uint32_t *nbr, uint8_t *anchors,
+  template <bool GRID, typename AnchorT>
+  static int assign_cand(const float *xs, const float *cb, uint32_t *nbr, AnchorT *anchors,
                          float *grid, uint16_t *codes, float *e, uint32_t *slice,
                          uint32_t *defer, uint32_t *defer_count, const uint32_t *done,
                          uint64_t n, uint32_t M, uint32_t K, uint32_t L, uint32_t *hist,
                          uint32_t T, unsigned long long *rescans, hipStream_t s) {
     KT("nbr_build_kernel<%d>", D);
-    nbr_build_kernel<D><<<dim3(K, M), kWave, 0, s>>>(cb, nbr, defer_count, done, K, L);
+    nbr_build_kernel<D><<<dim3(K, M), nbr_threads(K), 0, s>>>(cb, nbr, defer_count, done, K, L);
     KT_END();
     uint32_t G = 0, cells = 0;
+    constexpr uint32_t NA = cand_anchors<false>();
     if (GRID) {
       G = cand_grid_side(D);
       cells = 1;
       for (int k = 0; k < D; ++k) cells *= G;
-      KT("grid_build_kernel<%d, %uu>", D, cand_anchors<false>());
-      grid_build_kernel<D, cand_anchors<false>()><<<dim3((cells + kBlock - 1) / kBlock, M), kBlock,
-                                                     0, s>>>(
+      KT("grid_build_kernel<%d, %uu>", D, NA);
+      grid_build_kernel<D, NA, AnchorT><<<dim3((cells + kBlock - 1) / kBlock, M), kBlock, 0, s>>>(
           cb, anchors, grid, K, G, cells);
       KT_END();
     }
     // About 1,024 blocks over all subspaces; a chunk is whole sort tiles
-    // (whole groups of kCandThreads vectors), at most kCandHistTiles of them.
+    // (whole groups of kCandThreads vectors), at most as many as the block's
+    // tile histograms can hold in LDS.
+    const uint32_t abytes = GRID ? NA * (uint32_t)sizeof(AnchorT) : 0u;
+    const uint32_t max_tiles = cand_hist_tiles(K, Pad<D>::value, cells, abytes);
     const uint64_t per_sub = std::max<uint64_t>(1, (1024 + M - 1) / M);
     uint64_t chunk = (n + per_sub - 1) / per_sub;
     chunk = (chunk + kSortTile - 1) / kSortTile * kSortTile;
-    chunk = std::min<uint64_t>(chunk, (uint64_t)kCandHistTiles * kSortTile);
+    chunk = std::min<uint64_t>(chunk, (uint64_t)max_tiles * kSortTile);
     const uint64_t nblk = (n + chunk - 1) / chunk;
-    const CandLds lay = cand_lds(K, Pad<D>::value, cells, (uint32_t)(chunk / kSortTile),
-                                 GRID ? cand_anchors<false>() : 0u);
-    if (int st = raise_lds((const void *)cand_kernel<D, GRID, false, uint16_t>, lay.total, cells))
+    const CandLds lay = cand_lds(K, Pad<D>::value, cells, (uint32_t)(chunk / kSortTile), abytes);
+    if (int st = raise_lds((const void *)cand_kernel<D, GRID, false, uint16_t, AnchorT>,
+                           lay.total, cells))
       return st;
     KT("cand_kernel<%d, %s, false, unsigned short>", D, GRID ? "true" : "false");
-    cand_kernel<D, GRID, false, uint16_t><<<dim3((unsigned)nblk, M), kCandThreads, lay.total,
-                                            s>>>(xs, cb, nbr, anchors, grid, codes, e, nullptr,
-                                                 slice, defer, defer_count, done, n, 0, M, K, L,
-                                                 (uint32_t)chunk, (uint32_t)nblk, G, cells, hist,
-                                                 T);
+    cand_kernel<D, GRID, false, uint16_t, AnchorT><<<dim3((unsigned)nblk, M), kCandThreads,
+                                                     lay.total, s>>>(
+        xs, cb, nbr, anchors, grid, codes, e, nullptr, slice, defer, defer_count, done, n, 0, M, K,
+        L, (uint32_t)chunk, (uint32_t)nblk, G, cells, hist, T);
     KT_END();
     const uint32_t Kp = (K + kPruneBlock - 1) / kPruneBlock * kPruneBlock;
     const size_t lds = (size_t)Kp * (Pad<D>::value + 1) * sizeof(float) + 2 * sizeof(uint32_t);
@@ -449,26 +465,28 @@ struct Launch {
   // the deferred vectors.
   template <typename CodeT>
   static int encode_cand(const float *x, const float *cb, CodeT *codes, uint32_t *nbr,
-                         uint8_t *anchors, float *grid, uint32_t *slice, uint32_t *defer,
+                         CodeT *anchors, float *grid, uint32_t *slice, uint32_t *defer,
                          uint32_t *defer_count, uint64_t n, uint32_t dim, uint32_t M, uint32_t K,
                          uint32_t L, unsigned long long *rescans, hipStream_t s) {
-    encode_tables(cb, nbr, anchors, grid, defer_count, M, K, L, s);
+    encode_tables<CodeT>(cb, nbr, anchors, grid, defer_count, M, K, L, s);
     return encode_rows<CodeT>(x, cb, codes, nbr, anchors, grid, slice, defer, defer_count, n, dim,
                               M, K, L, rescans, g_profile ? rescans + 1 : nullptr, s);
   }
   // The codebooks' neighbour rows and grid anchors (also clears defer_count).
-  static void encode_tables(const float *cb, uint32_t *nbr, uint8_t *anchors, float *grid,
+  template <typename AnchorT>
+  static void encode_tables(const float *cb, uint32_t *nbr, AnchorT *anchors, float *grid,
                             uint32_t *defer_count, uint32_t M, uint32_t K, uint32_t L,
                             hipStream_t s) {
     const uint32_t G = cand_grid_side(D);
     uint32_t cells = 1;
     for (int k = 0; k < D; ++k) cells *= G;
     KT("nbr_build_kernel<%d>", D);
-    nbr_build_kernel<D><<<dim3(K, M), kWave, 0, s>>>(cb, nbr, defer_count, nullptr, K, L);
+    nbr_build_kernel<D><<<dim3(K, M), nbr_threads(K), 0, s>>>(cb, nbr, defer_count, nullptr, K,
+                                                               L);
     KT_END();
     KT("grid_build_kernel<%d, %uu>", D, cand_anchors<true>());
-    grid_build_kernel<D, cand_anchors<true>()><<<dim3((cells + kBlock - 1) / kBlock, M), kBlock,
-                                                  0, s>>>(
+    grid_build_kernel<D, cand_anchors<true>(), AnchorT><<<dim3((cells + kBlock - 1) / kBlock, M),
+                                                          kBlock, 0, s>>>(
         cb, anchors, grid, K, G, cells);
     KT_END();
   }
@@ -477,15 +495,16 @@ struct Launch {
   // slice / defer hold M * n words each.
   template <typename CodeT>
   static int encode_rows(const float *x, const float *cb, CodeT *codes, const uint32_t *nbr,
-                         const uint8_t *anchors, const float *grid, uint32_t *slice,
+                         const CodeT *anchors, const float *grid, uint32_t *slice,
                          uint32_t *defer, uint32_t *defer_count, uint64_t n, uint32_t dim,
                          uint32_t M, uint32_t K, uint32_t L, unsigned long long *rescans,
                          unsigned long long *stats, hipStream_t s) {
     const uint32_t G = cand_grid_side(D);
     uint32_t cells = 1;
     for (int k = 0; k < D; ++k) cells *= G;
-    const CandLds lay = cand_lds(K, Pad<D>::value, cells, 0, cand_anchors<true>());
-    if (int st = raise_lds((const void *)cand_kernel<D, true, true, CodeT>, lay.total, cells))
+    const CandLds lay =
+        cand_lds(K, Pad<D>::value, cells, 0, cand_anchors<true>() * (uint32_t)sizeof(CodeT));
+    if (int st = raise_lds((const void *)cand_kernel<D, true, true, CodeT, CodeT>, lay.total, cells))
       return st;
     // Chunks of 8,192 rows; the M blocks of a chunk run on one XCD, so a row
     // crosses HBM once and its other subspaces come from L2.
@@ -495,7 +514,7 @@ struct Launch {
     if (total > 0xFFFFFFF0ull) return TAC_ERR_UNSUPPORTED;
     const uint32_t blocks = (uint32_t)(8 * ((total + 7) / 8));
     KT("cand_kernel<%d, true, true, %s>", D, code_name<CodeT>());
-    cand_kernel<D, true, true, CodeT><<<blocks, kCandThreads, lay.total, s>>>(
+    cand_kernel<D, true, true, CodeT, CodeT><<<blocks, kCandThreads, lay.total, s>>>(
         x, cb, nbr, anchors, grid, nullptr, nullptr, codes, slice, defer, defer_count, nullptr, n,
         dim, M, K, L, (uint32_t)chunk, (uint32_t)nchunks, G, cells, nullptr, 0);
     KT_END();
@@ -729,8 +748,11 @@ int train_core(DeviceState &ds, hipStream_t s, const float *d_x, uint64_t n, uin
   // iteration.
   const char *full_env = getenv("TAC_GPU_FULL_SEARCH");
   const uint32_t Lc = K >= 2 ? std::min<uint32_t>(kCandList, K - 1) : 0;
+  // Anchors (first iteration) are u8 ids up to K = 256, u16 beyond; the
+  // block's tables must fit the LDS with at least one sort tile.
+  const uint32_t anchor_size = K <= 256 ? 1u : 2u;
   const bool cand_ok = !(full_env && full_env[0] == '1') && K >= 2 && K <= kCandMaxK &&
-                       cand_lds(K, DP, kCandCells, kCandHistTiles, kCandAnchorsMax).total <=
+                       cand_lds(K, DP, kCandCells, 1, cand_anchors<false>() * anchor_size).total <=
                            kCandLdsMax &&
                        n <= 0xFFFFFFFFull;
   const bool cand = cand_ok && max_iters > 1;
@@ -740,7 +762,8 @@ int train_core(DeviceState &ds, hipStream_t s, const float *d_x, uint64_t n, uin
        (st = ensure(ds, ds.cand_defer, (size_t)2 * M * n * sizeof(uint32_t))) ||
        (st = ensure(ds, ds.cand_count, (size_t)M * sizeof(uint32_t)))))
     return st;
-  if (cand_first && ((st = ensure(ds, ds.cand_anchor, (size_t)M * kCandCells * kCandAnchorsMax)) ||
+  if (cand_first && ((st = ensure(ds, ds.cand_anchor,
+                                  (size_t)M * kCandCells * kCandAnchorsMax * anchor_size)) ||
                      (st = ensure(ds, ds.cand_grid, (size_t)M * 16 * sizeof(float)))))
     return st;
 
@@ -801,16 +824,24 @@ int train_core(DeviceState &ds, hipStream_t s, const float *d_x, uint64_t n, uin
     if (cand_now) {
       uint32_t *slices = as<uint32_t>(ds.cand_defer);
       if (t == 0) {
-        DISPATCH_D_ST(D, assign_cand<true>(xs, out.cb, as<uint32_t>(ds.cand_nbr),
-                                           as<uint8_t>(ds.cand_anchor), as<float>(ds.cand_grid),
-                                           codes, e, slices, slices + (size_t)M * n,
-                                           as<uint32_t>(ds.cand_count), done, n, M, K, Lc, hist,
-                                           T, rescans, s));
+        if (anchor_size == 1) {
+          DISPATCH_D_ST(D, assign_cand<true>(xs, out.cb, as<uint32_t>(ds.cand_nbr),
+                                             as<uint8_t>(ds.cand_anchor), as<float>(ds.cand_grid),
+                                             codes, e, slices, slices + (size_t)M * n,
+                                             as<uint32_t>(ds.cand_count), done, n, M, K, Lc,
+                                             hist, T, rescans, s));
+        } else {
+          DISPATCH_D_ST(D, assign_cand<true>(xs, out.cb, as<uint32_t>(ds.cand_nbr),
+                                             as<uint16_t>(ds.cand_anchor), as<float>(ds.cand_grid),
+                                             codes, e, slices, slices + (size_t)M * n,
+                                             as<uint32_t>(ds.cand_count), done, n, M, K, Lc,
+                                             hist, T, rescans, s));
+        }
       } else {
-        DISPATCH_D_ST(D, assign_cand<false>(xs, out.cb, as<uint32_t>(ds.cand_nbr), nullptr,
-                                            nullptr, codes, e, slices, slices + (size_t)M * n,
-                                            as<uint32_t>(ds.cand_count), done, n, M, K, Lc, hist,
-                                            T, rescans, s));
+        DISPATCH_D_ST(D, assign_cand<false>(xs, out.cb, as<uint32_t>(ds.cand_nbr),
+                                            (uint8_t *)nullptr, nullptr, codes, e, slices,
+                                            slices + (size_t)M * n, as<uint32_t>(ds.cand_count),
+                                            done, n, M, K, Lc, hist, T, rescans, s));
       }
       if (st) return st;
       LAUNCH_TRY("assign_cand kernels");
@@ -947,21 +978,37 @@ int encode_core(DeviceState &ds, hipStream_t s, const float *d_x, uint64_t n, ui
   // (cand_kernels.hpp); TAC_GPU_FULL_SEARCH=1 keeps the full search.
   const char *full_env = getenv("TAC_GPU_FULL_SEARCH");
   const uint32_t L = K >= 2 ? std::min<uint32_t>(kCandList, K - 1) : 0;
+  // Codes and grid anchors share one width: u8 up to K = 256, u16 beyond.
+  const uint32_t code_size = K <= 256 ? 1u : 2u;
+  const uint32_t G = cand_grid_side(D), D_pad = pad_of(D);
+  uint32_t cells = 1;
+  for (uint32_t k = 0; k < D; ++k) cells *= G;
   const bool cand = !(full_env && full_env[0] == '1') && K >= 2 && K <= kCandMaxK &&
-                    n >= 16384 && n <= 0xFFFFFFFFull;
+                    n >= 16384 && n <= 0xFFFFFFFFull &&
+                    cand_lds(K, D_pad, cells, 0, cand_anchors<true>() * code_size).total <=
+                        kCandLdsMax;
   if (cand) {
     if ((st = ensure(ds, ds.cand_nbr, (size_t)M * K * cand_row_len(L) * sizeof(uint32_t))) ||
         (st = ensure(ds, ds.cand_defer, (size_t)2 * M * n * sizeof(uint32_t))) ||
         (st = ensure(ds, ds.cand_count, (size_t)M * sizeof(uint32_t))) ||
-        (st = ensure(ds, ds.cand_anchor, (size_t)M * kCandCells * kCandAnchorsMax)) ||
+        (st = ensure(ds, ds.cand_anchor, (size_t)M * kCandCells * kCandAnchorsMax * code_size)) ||
         (st = ensure(ds, ds.cand_grid, (size_t)M * 16 * sizeof(float))))
       return st;
     uint32_t *slices = as<uint32_t>(ds.cand_defer);
-    DISPATCH_D_ST(D, encode_cand<uint8_t>(d_x, d_cb, (uint8_t *)d_codes, as<uint32_t>(ds.cand_nbr),
-                                          as<uint8_t>(ds.cand_anchor), as<float>(ds.cand_grid),
-                                          slices, slices + (size_t)M * n,
-                                          as<uint32_t>(ds.cand_count), n, dim, M, K, L, rescans,
-                                          s));
+    if (code_size == 1) {
+      DISPATCH_D_ST(D, encode_cand<uint8_t>(d_x, d_cb, (uint8_t *)d_codes,
+                                            as<uint32_t>(ds.cand_nbr), as<uint8_t>(ds.cand_anchor),
+                                            as<float>(ds.cand_grid), slices,
+                                            slices + (size_t)M * n, as<uint32_t>(ds.cand_count),
+                                            n, dim, M, K, L, rescans, s));
+    } else {
+      DISPATCH_D_ST(D, encode_cand<uint16_t>(d_x, d_cb, (uint16_t *)d_codes,
+                                             as<uint32_t>(ds.cand_nbr),
+                                             as<uint16_t>(ds.cand_anchor),
+                                             as<float>(ds.cand_grid), slices,
+                                             slices + (size_t)M * n, as<uint32_t>(ds.cand_count),
+                                             n, dim, M, K, L, rescans, s));
+    }
   } else if (K <= 256) {
     DISPATCH_D_ST(D, encode<uint8_t>(d_x, d_cb, (uint8_t *)d_codes, n, dim, M, K, rescans, s));
   } else {
@@ -1293,8 +1340,7 @@ int tac_pq_encode_device_noalloc(const float *d_residuals, uint64_t n, uint32_t 
   LAUNCH_TRY("zero_words_kernel");
   const char *full_env = getenv("TAC_GPU_FULL_SEARCH");
   const uint32_t L = ksub >= 2 ? std::min<uint32_t>(kCandList, ksub - 1) : 0;
-  bool cand = !(full_env && full_env[0] == '1') && ksub >= 2 && ksub <= kCandMaxK &&
-              n >= 16384;
+  bool cand = !(full_env && full_env[0] == '1') && ksub >= 2 && ksub <= 256 && n >= 16384;
   uint64_t batch = 0;
   uint32_t *count = nullptr, *nbr = nullptr, *lists = nullptr;
   uint8_t *anchors = nullptr;
@@ -1324,7 +1370,7 @@ int tac_pq_encode_device_noalloc(const float *d_residuals, uint64_t n, uint32_t 
     LAUNCH_TRY("encode_kernel");
     return TAC_OK;
   }
-  DISPATCH_D(D, encode_tables(d_codebooks, nbr, anchors, grid, count, m, ksub, L, s));
+  DISPATCH_D(D, encode_tables<uint8_t>(d_codebooks, nbr, anchors, grid, count, m, ksub, L, s));
   LAUNCH_TRY("encode tables");
   for (uint64_t r0 = 0; r0 < n; r0 += batch) {
     const uint64_t nb = std::min<uint64_t>(batch, n - r0);

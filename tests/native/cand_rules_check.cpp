@@ -147,7 +147,7 @@ static void run_case(const std::vector<float>& cb, int K, int D, const std::vect
 
 int main() {
   Counts ct;
-  const int Ks[] = {2, 3, 17, 64, 65, 100, 256};
+  const int Ks[] = {2, 3, 17, 64, 65, 100, 256, 300, 1024};
   const double scales[] = {1.0, 1e-19, 1e-12, 1e15, 1e18};
   for (int D = 1; D <= 8; ++D)
     for (int K : Ks)

@@ -38,7 +38,8 @@ def _train_both(x, dim, m, ksub, init, iters):
 
 
 @pytest.mark.parametrize("dsub,ksub", [(1, 256), (2, 256), (3, 100), (4, 256), (5, 65),
-                                       (6, 17), (7, 2), (8, 256)])
+                                       (6, 17), (7, 2), (8, 256), (4, 1024), (2, 512), (8, 1024),
+                                       (1, 700), (3, 1000)])
 def test_sub_dimensions_and_codebook_sizes(gpu, dsub, ksub):
     m = 4
     dim = m * dsub
@@ -49,7 +50,7 @@ def test_sub_dimensions_and_codebook_sizes(gpu, dsub, ksub):
 
 
 @pytest.mark.parametrize("dsub,ksub", [(1, 256), (2, 200), (3, 100), (4, 256), (5, 65),
-                                       (6, 17), (7, 2), (8, 256)])
+                                       (6, 17), (7, 2), (8, 256), (4, 1024), (2, 777), (8, 1024)])
 def test_first_iteration_grid_anchors(gpu, dsub, ksub):
     # 20,000 vectors: iteration 0 takes the grid-anchored candidate pass.
     m = 2
@@ -143,7 +144,8 @@ def _encode_both(x, cb, m, ksub):
 
 
 @pytest.mark.parametrize("dsub,ksub", [(1, 256), (2, 256), (3, 100), (4, 256), (5, 65),
-                                       (6, 17), (7, 2), (8, 256)])
+                                       (6, 17), (7, 2), (8, 256), (4, 1024), (2, 512), (8, 1024),
+                                       (3, 1000)])
 def test_encode_sub_dimensions_and_codebook_sizes(gpu, dsub, ksub):
     m = 4
     rng = np.random.default_rng(200 + dsub)
@@ -202,3 +204,23 @@ def test_encode_matches_full_search_on_the_corpus(gpu, monkeypatch):
     assert np.array_equal(got, full)
     assert prof.cand_vectors == w.m * x.shape[0]
     assert 0 < prof.cand_deferred < 0.1 * prof.cand_vectors
+
+
+def test_k1024_matches_full_search_on_the_corpus(gpu, monkeypatch):
+    """m16 x k1024 on 200,000 corpus rows: 3 candidate iterations (the first
+    from u16 grid anchors) and the candidate encode give the full search's
+    codebooks and codes."""
+    w = synth.WORKLOADS["corpus-1.52m-k1024"]
+    x = synth.residuals(w, 200000)
+    init = synth.shuffle_init(x, w.m, w.ksub, 0)
+    device.profile_enable(True)
+    device.profile_read(reset=True)
+    p = pq.train(x, w.dim, 0, m=w.m, ksub=w.ksub, max_iters=3, tol=NEVER, init_codebooks=init)
+    got = p.encode_many(x)
+    prof = device.profile_read(reset=True)
+    device.profile_enable(False)
+    assert prof.cand_vectors > 0 and prof.cand_deferred < 0.2 * prof.cand_vectors
+    monkeypatch.setenv("TAC_GPU_FULL_SEARCH", "1")
+    q = pq.train(x, w.dim, 0, m=w.m, ksub=w.ksub, max_iters=3, tol=NEVER, init_codebooks=init)
+    assert np.array_equal(_bits(p.codebooks), _bits(q.codebooks))
+    assert got.dtype == np.uint16 and np.array_equal(got, q.encode_many(x))
