@@ -587,22 +587,30 @@ __global__ __launch_bounds__(kBlock) void assign_list_kernel(
 // The deferred vectors of an encode: PQ.encode's scan semantics (best from
 // +inf, strict <; src/index/pq.zig:64-73) through the pruned exact search,
 // vectors gathered through defer[m][..] from the token-major input; codes
-// to out[i][m].  Grid as assign_list_kernel.
-template <int D, typename CodeT>
+// to out[i][m].  Each thread takes VPT deferred vectors (their searches
+// interleave), a persistent grid of gridDim.x blocks per subspace walks
+// tiles of kBlock * VPT entries.  Two widths are launched back to back and a
+// subspace's deferred count picks one: VPT 1 (many short waves) below a
+// quarter of the rows, VPT 8 (the full search's interleave) above; the other
+// launch returns at once.
+template <int D, int VPT, typename CodeT>
 __global__ __launch_bounds__(kBlock) void encode_list_kernel(
     const float* __restrict__ x, const float* __restrict__ cb, CodeT* __restrict__ out,
     const uint32_t* __restrict__ defer, const uint32_t* __restrict__ defer_count, uint64_t n,
     uint32_t dim, uint32_t M, uint32_t K, unsigned long long* __restrict__ rescans,
     unsigned long long* __restrict__ stats) {
   constexpr int DP = Pad<D>::value;
+  constexpr uint32_t kTile = kBlock * VPT;
   extern __shared__ __attribute__((aligned(16))) float lds[];
   const uint32_t m = blockIdx.y;
   const uint32_t cnt = defer_count[m];
+  const bool wide = 4ull * cnt > n;
+  if ((VPT > 1) != wide) return;  // the other width serves this subspace
   if (stats && blockIdx.x == 0 && threadIdx.x == 0) {
     atomicAdd(&stats[0], (unsigned long long)cnt);
     atomicAdd(&stats[1], (unsigned long long)n);
   }
-  if ((uint64_t)blockIdx.x * kBlock >= cnt) return;
+  if ((uint64_t)blockIdx.x * kTile >= cnt) return;
   const uint32_t Kp = (K + kPruneBlock - 1) / kPruneBlock * kPruneBlock;
   float* lcb = lds;
   float* lnc = lds + Kp * DP;
@@ -617,17 +625,24 @@ __global__ __launch_bounds__(kBlock) void encode_list_kernel(
   __syncthreads();
   const uint32_t* lst = defer + (uint64_t)m * n;
   uint32_t mine = 0;
-  for (uint64_t t0 = (uint64_t)blockIdx.x * kBlock; t0 < cnt; t0 += (uint64_t)gridDim.x * kBlock) {
-    const uint64_t q = t0 + threadIdx.x;
-    const uint32_t i = q < cnt ? lst[q] : 0xFFFFFFFFu;
-    float xv[1][D];
-    const float* src = x + (uint64_t)(i != 0xFFFFFFFFu ? i : 0u) * dim + (uint64_t)m * D;
+  for (uint64_t t0 = (uint64_t)blockIdx.x * kTile; t0 < cnt; t0 += (uint64_t)gridDim.x * kTile) {
+    float xv[VPT][D];
+    uint32_t idx[VPT];
 #pragma unroll
-    for (int k = 0; k < D; ++k) xv[0][k] = src[k];
-    uint32_t bidx[1];
-    float best[1];
-    pruned_argmin<D, 1, false>(xv, lcb, lnc, K, Kp, lmax, bidx, best, mine);
-    if (i != 0xFFFFFFFFu) out[(uint64_t)i * M + m] = (CodeT)bidx[0];
+    for (int j = 0; j < VPT; ++j) {
+      const uint64_t q = t0 + threadIdx.x + (uint64_t)j * kBlock;
+      idx[j] = q < cnt ? lst[q] : 0xFFFFFFFFu;
+      const float* src = x + (uint64_t)(idx[j] != 0xFFFFFFFFu ? idx[j] : 0u) * dim +
+                         (uint64_t)m * D;
+#pragma unroll
+      for (int k = 0; k < D; ++k) xv[j][k] = src[k];
+    }
+    uint32_t bidx[VPT];
+    float best[VPT];
+    pruned_argmin<D, VPT, false>(xv, lcb, lnc, K, Kp, lmax, bidx, best, mine);
+#pragma unroll
+    for (int j = 0; j < VPT; ++j)
+      if (idx[j] != 0xFFFFFFFFu) out[(uint64_t)idx[j] * M + m] = (CodeT)bidx[j];
   }
   flush_rescans(mine, &lcount, rescans);
 }

@@ -520,10 +520,20 @@ struct Launch {
     KT_END();
     const uint32_t Kp = (K + kPruneBlock - 1) / kPruneBlock * kPruneBlock;
     const size_t lds = (size_t)Kp * (Pad<D>::value + 1) * sizeof(float) + 2 * sizeof(uint32_t);
-    const uint64_t g = std::max<uint64_t>(
+    // The deferred vectors: one per thread on about 4,096 blocks over all
+    // subspaces when they are few, eight per thread when more than a quarter
+    // of a subspace's rows were deferred (each launch serves the subspaces of
+    // its width, blocks loop when there are more).
+    const uint64_t g1 = std::max<uint64_t>(
         1, std::min<uint64_t>((n + kBlock - 1) / kBlock, (4096 + M - 1) / M));
-    KT("encode_list_kernel<%d, %s>", D, code_name<CodeT>());
-    encode_list_kernel<D, CodeT><<<dim3((unsigned)g, M), kBlock, lds, s>>>(
+    const uint64_t g8 = std::max<uint64_t>(
+        1, std::min<uint64_t>((n + kBlock * 8 - 1) / (kBlock * 8), (4096 + M - 1) / M));
+    KT("encode_list_kernel<%d, 1, %s>", D, code_name<CodeT>());
+    encode_list_kernel<D, 1, CodeT><<<dim3((unsigned)g1, M), kBlock, lds, s>>>(
+        x, cb, codes, defer, defer_count, n, dim, M, K, rescans, stats);
+    KT_END();
+    KT("encode_list_kernel<%d, 8, %s>", D, code_name<CodeT>());
+    encode_list_kernel<D, 8, CodeT><<<dim3((unsigned)g8, M), kBlock, lds, s>>>(
         x, cb, codes, defer, defer_count, n, dim, M, K, rescans, stats);
     KT_END();
     return TAC_OK;
