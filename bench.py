@@ -279,26 +279,27 @@ def _load_json(path: Path):
 # ---------------------------------------------------------------------------
 # Roofline of the dominant kernel
 # ---------------------------------------------------------------------------
-def algorithmic_bytes(name: str, n: int, dim: int, m: int):
-    """Bytes a kernel must move per launch over the whole corpus: an
-    assignment or encode reads every residual once and writes one code per
-    vector and subspace (2 bytes during training, 1 in the encode output);
-    scatter reads the records and codes and writes the records; the fold
-    reads the records.  None for the small kernels."""
+def algorithmic_bytes(name: str, n: int, dim: int, m: int, parts: int = 1):
+    """Bytes a kernel must move per launch: an assignment or encode reads
+    every residual once and writes one code per vector and subspace (2 bytes
+    during training, 1 in the encode output); scatter reads the records and
+    codes and writes the records; the fold reads the records.  Training
+    launches cover m / parts subspaces each (parts = the streams the Lloyd
+    loop splits the subspaces over).  None for the small kernels."""
     dsub = dim // m
     dp = 1 if dsub <= 1 else 2 if dsub <= 2 else 4 if dsub <= 4 else 8
     if name.startswith("cand_kernel") and ", true, true," in name:
         return n * (4 * dim + m)
     if name.startswith("encode_kernel"):
         return n * (4 * dim + m)
-    if name.startswith(("cand_kernel", "assign_kernel")):
-        return n * (4 * dim + 2 * m)
-    if name.startswith("scatter_kernel"):
-        return n * m * (2 * 4 * dp + 2)
-    if name.startswith("fold_kernel"):
-        return n * m * 4 * dp
     if name.startswith("transpose_kernel"):
         return n * (4 * dim + 4 * m * dp)
+    if name.startswith(("cand_kernel", "assign_kernel")):
+        return n * (4 * dim + 2 * m) // parts
+    if name.startswith("scatter_kernel"):
+        return n * m * (2 * 4 * dp + 2) // parts
+    if name.startswith("fold_kernel"):
+        return n * m * 4 * dp // parts
     return None
 
 
@@ -312,8 +313,9 @@ def kernel_table(kt: dict, steps: int, train_ms: float):
     return dict(sorted(rows.items(), key=lambda kv: -kv[1]["ms_per_step"]))
 
 
-def roofline(name: str, row: dict, n: int, dim: int, m: int, traffic: dict, valu: dict):
-    ab = algorithmic_bytes(name, n, dim, m)
+def roofline(name: str, row: dict, n: int, dim: int, m: int, traffic: dict, valu: dict,
+             parts: int = 1):
+    ab = algorithmic_bytes(name, n, dim, m, parts)
     avg_s = row["avg_ms"] * 1e-3
     achieved = ab / avg_s / 1e9 if ab else None
     tr = traffic.get(name) if traffic else None
@@ -587,6 +589,7 @@ def shape_sweep(device, dx, x, steps: int):
             "encode_hbm_frac": round(ebytes / (enc_ms * 1e-3) / 1e9 / PEAK_HBM_GBS, 4),
             "update_ms_per_iter": round(p.update_ms / max(p.update_iters, 1), 4),
             "assign_ms_per_iter": round(p.assign_ms / max(p.assign_launches, 1), 4),
+            "train_streams": int(p.train_streams),
         }
         log(f"{name}: {rows[name]}")
     return rows
@@ -628,6 +631,7 @@ def paper_60m(device, steps: int):
             "ms_per_iter": round(t / w.iters * 1e3, 3),
             "assign_ms_per_iter": round(p.assign_ms / max(p.assign_launches, 1), 3),
             "update_ms_per_iter": round(p.update_ms / max(p.update_iters, 1), 3),
+            "train_streams": int(p.train_streams),
             "resident_input_gb": round(w.n * w.dim * 4 / 1e9, 2),
             "device_generation_s": round(gen_s, 2), "timed_runs": steps,
             "data": "synthetic, generated on the device"}
@@ -787,13 +791,17 @@ def main() -> int:
     traffic = (_load_json(TRAFFIC_FILE) or {}).get("kernels", {})
     valu = (_load_json(VALU_FILE) or {}).get("kernels", {})
     dominant = next(iter(kernels)) if kernels else None
-    roof = roofline(dominant, kernels[dominant], n, dim, m, traffic, valu) if dominant else None
+    parts = max(1, int(prof.train_streams))
+    roof = (roofline(dominant, kernels[dominant], n, dim, m, traffic, valu, parts)
+            if dominant else None)
     enc_names = [k for k in kernels if ", true, true," in k or k.startswith(
         ("encode_kernel", "encode_list_kernel"))]
     enc_ms = prof.encode_ms / max(prof.encode_launches, 1)
     ebytes = n * (4 * dim + m)
+    # With two training streams the stage timers cover the first half of the
+    # subspaces (the second runs beside it), and so do the stage bytes.
     update_ms = prof.update_ms / max(prof.update_iters, 1)
-    ubytes = n * (4 * dim + 2 * m)
+    ubytes = n * (4 * dim + 2 * m) // parts
     assign_ms = prof.assign_ms / max(prof.assign_launches, 1)
     out = {
         "metric": METRIC,
@@ -825,6 +833,7 @@ def main() -> int:
                        or None,
         },
         "assign_stage_ms_per_iter": round(assign_ms, 4),
+        "train_streams": parts,
         "update_roofline": {
             "avg_iter_ms": round(update_ms, 4), "algorithmic_bytes": ubytes,
             "hbm_gbs": round(ubytes / (update_ms * 1e-3) / 1e9, 1),
@@ -836,8 +845,10 @@ def main() -> int:
                        or None,
         },
         "kernels": {k: v for k, v in list(kernels.items())[:12]},
-        "kernel_timing": (f"HIP events around every kernel on the library's stream over "
-                          f"{args.steps} further steps of the same workload"),
+        "kernel_timing": (f"HIP events around every kernel on the stream it runs on over "
+                          f"{args.steps} further steps of the same workload; training "
+                          f"launches cover {m // parts} of the {m} subspaces each, "
+                          f"{parts} streams side by side"),
         "candidate_deferred_frac": round(prof.cand_deferred / max(prof.cand_vectors, 1), 4),
         "device": info["name"],
     }

@@ -347,7 +347,7 @@ int tac_cluster_flat(const uint32_t *token_ids, uint64_t n_tokens, const float *
  * stream they run on and accumulates their durations. */
 typedef struct tac_gpu_profile {
   double transpose_ms;   uint64_t transpose_launches;
-  double assign_ms;      uint64_t assign_launches;   /* Lloyd assignment kernel */
+  double assign_ms;      uint64_t assign_launches;   /* Lloyd assignment stage */
   double update_ms;      uint64_t update_iters;      /* sort + fold + reseed + convergence */
   double encode_ms;      uint64_t encode_launches;   /* encode kernel */
   uint64_t exact_rescans; /* (vector, subspace) searches the pruned pass left to a full
@@ -369,6 +369,10 @@ typedef struct tac_gpu_profile {
   double cand_assign_ms;   /* assignment stages that started from the previous codes
                               (included in assign_ms) */
   uint64_t cand_assign_iters;
+  uint64_t train_streams;  /* streams the last training call split its subspaces over: 2 when
+                              M is even (halves m < M/2 and m >= M/2 side by side), else 1.
+                              With 2, assign_ms and update_ms time the first half while the
+                              second runs beside it */
 } tac_gpu_profile;
 int tac_gpu_profile_enable(int enable);
 int tac_gpu_profile_read(tac_gpu_profile *out, int reset);

@@ -99,6 +99,9 @@ struct DeviceState {
       tac_done, tac_iters, tac_wcss, tac_prev, tac_empties, tac_assign, tac_probs, tac_tiles,
       tac_chl, tac_cprob, tac_inv, tac_rsum, tac_ranges;
   bool crc_tx_ready = false;
+  // training's second stream (two halves of the subspaces) and its events
+  hipStream_t aux_stream[1] = {};
+  hipEvent_t aux_fork = nullptr, aux_join[1] = {};
   // measurement
   std::vector<hipEvent_t> events;
   std::vector<hipEvent_t> kevents;  // per-kernel timers
@@ -192,6 +195,8 @@ struct KernelClock {
   std::vector<KernelMark> marks;
 };
 thread_local KernelClock *tl_clock = nullptr;
+// The stream of the launches being timed when it is not the call's own.
+thread_local hipStream_t tl_kt_stream = nullptr;
 std::map<std::string, std::pair<double, uint64_t>> g_kernel_times;  // under g_profile_mu
 
 hipEvent_t kevent(DeviceState &ds, size_t idx) {
@@ -214,7 +219,7 @@ void kt_begin(const char *fmt, ...) {
   va_end(ap);
   mk.ev = 2 * c->marks.size();
   hipEvent_t a = kevent(*c->ds, mk.ev);
-  if (!a || hipEventRecord(a, c->s) != hipSuccess) return;
+  if (!a || hipEventRecord(a, tl_kt_stream ? tl_kt_stream : c->s) != hipSuccess) return;
   c->marks.push_back(mk);
 }
 
@@ -222,7 +227,8 @@ void kt_end() {
   KernelClock *c = tl_clock;
   if (!c || c->marks.empty()) return;
   hipEvent_t b = kevent(*c->ds, c->marks.back().ev + 1);
-  if (!b || hipEventRecord(b, c->s) != hipSuccess) c->marks.pop_back();
+  if (!b || hipEventRecord(b, tl_kt_stream ? tl_kt_stream : c->s) != hipSuccess)
+    c->marks.pop_back();
 }
 
 // Brackets one launch statement (which may hold commas) with the timer.
@@ -819,96 +825,162 @@ int train_core(DeviceState &ds, hipStream_t s, const float *d_x, uint64_t n, uin
   const bool want_wcss = (ex && ex->wcss) || out.h_wcss_single;
   const size_t hist_lds = (size_t)K * sizeof(uint32_t);
   std::vector<size_t> it_events;  // event index triples per iteration
-  for (uint32_t t = 0; t < max_iters; ++t) {
+  uint32_t gcells = 1;
+  for (uint32_t k = 0; k < D; ++k) gcells *= cand_grid_side(D);
+
+  // Two halves of the subspaces on two streams (M even): every subspace's
+  // kernels see only its own buffers, so each half runs the same arithmetic
+  // as one stream would, and one half's latency-bound steps (the fold's
+  // longest chains, the deferred-vector scans, the small scans) overlap the
+  // other half's VALU-bound assignment.  TAC_GPU_TRAIN_STREAMS=1 keeps one
+  // stream.
+  const char *streams_env = getenv("TAC_GPU_TRAIN_STREAMS");
+  const bool one_stream = streams_env && streams_env[0] == '1';
+  const uint32_t H = (!one_stream && M >= 2 && M % 2 == 0) ? 2u : 1u;
+  struct Half {
+    uint32_t m0, Mh;
+    hipStream_t s;
+  };
+  Half halves[2];
+  for (uint32_t h = 0; h < H; ++h) halves[h] = {h * (M / H), M / H, s};
+  if (H > 1) {
+    if (!ds.aux_fork) HIP_TRY(hipEventCreateWithFlags(&ds.aux_fork, hipEventDisableTiming));
+    HIP_TRY(hipEventRecord(ds.aux_fork, s));
+    for (uint32_t h = 1; h < H; ++h) {
+      if (!ds.aux_stream[h - 1])
+        HIP_TRY(hipStreamCreateWithFlags(&ds.aux_stream[h - 1], hipStreamNonBlocking));
+      if (!ds.aux_join[h - 1])
+        HIP_TRY(hipEventCreateWithFlags(&ds.aux_join[h - 1], hipEventDisableTiming));
+      halves[h].s = ds.aux_stream[h - 1];
+      HIP_TRY(hipStreamWaitEvent(halves[h].s, ds.aux_fork, 0));
+    }
+  }
+  struct StreamScope {
+    explicit StreamScope(hipStream_t hs) { tl_kt_stream = hs; }
+    ~StreamScope() { tl_kt_stream = nullptr; }
+  };
+  uint32_t *slices_all = (cand || cand_first) ? as<uint32_t>(ds.cand_defer) : nullptr;
+
+  // One Lloyd iteration t of the subspaces m0 .. m0+Mh-1 on stream hs.
+  auto iterate = [&](const Half &h, uint32_t t) -> int {
+    int st = TAC_OK;
+    const uint32_t m0 = h.m0, Mh = h.Mh;
+    hipStream_t hs = h.s;
+    StreamScope scope(hs);
+    float *xs_h = xs + (size_t)m0 * n * DP;
+    uint16_t *codes_h = codes + (size_t)m0 * n;
+    float *e_h = e + (size_t)m0 * n;
+    uint32_t *hist_h = hist + (size_t)m0 * T * K;
+    uint32_t *counts_h = counts + (size_t)m0 * K;
+    uint32_t *start_h = start + (size_t)m0 * K;
+    uint32_t *scan_h = scan_part + (size_t)m0 * G * K;
+    double *pre_h = fold_pre + (size_t)m0 * nfc;
+    FoldChunk *chunks_h = fold_chunks + (size_t)m0 * nfc;
+    float *sorted_h = sorted + (size_t)m0 * n * DP;
+    uint32_t *done_h = done + m0;
+    float *cb_h = out.cb + (size_t)m0 * K * D;
+    uint32_t *order_h = as<uint32_t>(ds.fold_order) + (size_t)m0 * K;
     hipEvent_t a = nullptr, b = nullptr, c = nullptr;
-    if (profile) {
+    const bool timed = profile && m0 == 0;
+    if (timed) {
       it_events.push_back(ev);
       if ((st = event_at(ds, ev++, &a)) || (st = event_at(ds, ev++, &b)) ||
           (st = event_at(ds, ev++, &c)))
         return st;
-      HIP_TRY(hipEventRecord(a, s));
+      HIP_TRY(hipEventRecord(a, hs));
     }
     // The candidate passes count the sort tiles themselves; the full search
     // leaves that to hist_kernel.
     const bool cand_now = (cand && t > 0) || (cand_first && t == 0);
     if (cand_now) {
-      uint32_t *slices = as<uint32_t>(ds.cand_defer);
+      uint32_t *nbr_h = as<uint32_t>(ds.cand_nbr) + (size_t)m0 * K * cand_row_len(Lc);
+      uint32_t *slices_h = slices_all + (size_t)m0 * n;
+      uint32_t *defer_h = slices_all + (size_t)M * n + (size_t)m0 * n;
+      uint32_t *count_h = as<uint32_t>(ds.cand_count) + m0;
       if (t == 0) {
+        const size_t aoff = (size_t)m0 * gcells * cand_anchors<false>();
+        float *grid_h = as<float>(ds.cand_grid) + (size_t)m0 * 16;
         if (anchor_size == 1) {
-          DISPATCH_D_ST(D, assign_cand<true>(xs, out.cb, as<uint32_t>(ds.cand_nbr),
-                                             as<uint8_t>(ds.cand_anchor), as<float>(ds.cand_grid),
-                                             codes, e, slices, slices + (size_t)M * n,
-                                             as<uint32_t>(ds.cand_count), done, n, M, K, Lc,
-                                             hist, T, rescans, s));
+          DISPATCH_D_ST(D, assign_cand<true>(xs_h, cb_h, nbr_h, as<uint8_t>(ds.cand_anchor) + aoff,
+                                             grid_h, codes_h, e_h, slices_h, defer_h, count_h,
+                                             done_h, n, Mh, K, Lc, hist_h, T, rescans, hs));
         } else {
-          DISPATCH_D_ST(D, assign_cand<true>(xs, out.cb, as<uint32_t>(ds.cand_nbr),
-                                             as<uint16_t>(ds.cand_anchor), as<float>(ds.cand_grid),
-                                             codes, e, slices, slices + (size_t)M * n,
-                                             as<uint32_t>(ds.cand_count), done, n, M, K, Lc,
-                                             hist, T, rescans, s));
+          DISPATCH_D_ST(D, assign_cand<true>(xs_h, cb_h, nbr_h, as<uint16_t>(ds.cand_anchor) + aoff,
+                                             grid_h, codes_h, e_h, slices_h, defer_h, count_h,
+                                             done_h, n, Mh, K, Lc, hist_h, T, rescans, hs));
         }
       } else {
-        DISPATCH_D_ST(D, assign_cand<false>(xs, out.cb, as<uint32_t>(ds.cand_nbr),
-                                            (uint8_t *)nullptr, nullptr, codes, e, slices,
-                                            slices + (size_t)M * n, as<uint32_t>(ds.cand_count),
-                                            done, n, M, K, Lc, hist, T, rescans, s));
+        DISPATCH_D_ST(D, assign_cand<false>(xs_h, cb_h, nbr_h, (uint8_t *)nullptr, nullptr,
+                                            codes_h, e_h, slices_h, defer_h, count_h, done_h, n,
+                                            Mh, K, Lc, hist_h, T, rescans, hs));
       }
       if (st) return st;
       LAUNCH_TRY("assign_cand kernels");
     } else {
-      DISPATCH_D(D, assign(xs, out.cb, codes, e, done, n, M, K, rescans, s));
+      DISPATCH_D(D, assign(xs_h, cb_h, codes_h, e_h, done_h, n, Mh, K, rescans, hs));
       LAUNCH_TRY("assign_kernel");
     }
-    if (profile) HIP_TRY(hipEventRecord(b, s));
+    if (timed) HIP_TRY(hipEventRecord(b, hs));
     if (!cand_now) {
       KT("hist_kernel");
-      hist_kernel<<<dim3(T, M), kBlock, hist_lds, s>>>(codes, hist, done, n, K, T);
+      hist_kernel<<<dim3(T, Mh), kBlock, hist_lds, hs>>>(codes_h, hist_h, done_h, n, K, T);
       KT_END();
       LAUNCH_TRY("hist_kernel");
     }
     KT("scan_partial_kernel");
-    scan_partial_kernel<<<dim3(G, M), kBlock, 0, s>>>(hist, scan_part, done, K, T, G);
+    scan_partial_kernel<<<dim3(G, Mh), kBlock, 0, hs>>>(hist_h, scan_h, done_h, K, T, G);
     KT_END();
     KT("scan_apply_kernel");
-    scan_apply_kernel<<<dim3(G, M), kBlock, 0, s>>>(hist, scan_part, counts, start, done, K, T,
-                                                     G);
+    scan_apply_kernel<<<dim3(G, Mh), kBlock, 0, hs>>>(hist_h, scan_h, counts_h, start_h, done_h,
+                                                      K, T, G);
     KT_END();
     LAUNCH_TRY("scan kernels");
-    DISPATCH_D_ST(D, scatter(xs, codes, hist, start, sorted, done, n, M, K, T, s));
+    DISPATCH_D_ST(D, scatter(xs_h, codes_h, hist_h, start_h, sorted_h, done_h, n, Mh, K, T, hs));
     if (st) return st;
     LAUNCH_TRY("scatter_kernel");
-    DISPATCH_D(D, fold(sorted, counts, start, out.cb, done, as<uint32_t>(ds.fold_order), n, M, K,
-                       s));
+    DISPATCH_D(D, fold(sorted_h, counts_h, start_h, cb_h, done_h, order_h, n, Mh, K, hs));
     LAUNCH_TRY("fold_kernel");
     if (check || (want_wcss && t + 1 == max_iters)) {
       const uint32_t fgrid = (nfc + kBlock / kWave - 1) / (kBlock / kWave);
       KT("wcss_chunk_sums_kernel");
-      wcss_chunk_sums_kernel<<<dim3(fgrid, M), kBlock, 0, s>>>(e, fold_pre, done, n, nfc);
+      wcss_chunk_sums_kernel<<<dim3(fgrid, Mh), kBlock, 0, hs>>>(e_h, pre_h, done_h, n, nfc);
       KT_END();
       KT("wcss_prefix_kernel");
-      wcss_prefix_kernel<<<M, kBlock, 0, s>>>(fold_pre, done, nfc);
+      wcss_prefix_kernel<<<Mh, kBlock, 0, hs>>>(pre_h, done_h, nfc);
       KT_END();
       KT("wcss_quantize_kernel");
-      wcss_quantize_kernel<<<dim3(fgrid, M), kBlock, 0, s>>>(e, fold_pre, fold_chunks, done, n,
-                                                             nfc);
+      wcss_quantize_kernel<<<dim3(fgrid, Mh), kBlock, 0, hs>>>(e_h, pre_h, chunks_h, done_h, n,
+                                                                nfc);
       KT_END();
       KT("wcss_apply_kernel");
-      wcss_apply_kernel<<<M, kWave, 0, s>>>(e, fold_chunks, wcss, done, n, nfc);
+      wcss_apply_kernel<<<Mh, kWave, 0, hs>>>(e_h, chunks_h, wcss + m0, done_h, n, nfc);
       KT_END();
       LAUNCH_TRY("wcss kernels");
     }
-    DISPATCH_D(D, reseed(xs, e, counts, out.cb, empties, done, n, M, K, s));
+    DISPATCH_D(D, reseed(xs_h, e_h, counts_h, cb_h, empties + m0, done_h, n, Mh, K, hs));
     LAUNCH_TRY("reseed_kernel");
     KT("converge_kernel");
-    converge_kernel<<<(M + 63) / 64, 64, 0, s>>>(wcss, prev, done, iters_run, M, t, tol,
-                                                   check ? 1 : 0);
+    converge_kernel<<<(Mh + 63) / 64, 64, 0, hs>>>(wcss + m0, prev + m0, done_h, iters_run + m0,
+                                                    Mh, t, tol, check ? 1 : 0);
     KT_END();
     LAUNCH_TRY("converge_kernel");
     if (want_trace)
-      HIP_TRY(hipMemcpyAsync(as<float>(ds.trace) + (size_t)t * cb_elems, out.cb,
-                             cb_elems * sizeof(float), hipMemcpyDeviceToDevice, s));
-    if (profile) HIP_TRY(hipEventRecord(c, s));
+      HIP_TRY(hipMemcpyAsync(as<float>(ds.trace) + (size_t)t * cb_elems + (size_t)m0 * K * D,
+                             cb_h, (size_t)Mh * K * D * sizeof(float), hipMemcpyDeviceToDevice,
+                             hs));
+    if (timed) HIP_TRY(hipEventRecord(c, hs));
+    return TAC_OK;
+  };
+
+  st = TAC_OK;
+  for (uint32_t t = 0; t < max_iters && !st; ++t)
+    for (uint32_t h = 0; h < H && !st; ++h) st = iterate(halves[h], t);
+  // The caller's stream waits for the other half, also after an error.
+  for (uint32_t h = 1; h < H; ++h) {
+    HIP_TRY(hipEventRecord(ds.aux_join[h - 1], halves[h].s));
+    HIP_TRY(hipStreamWaitEvent(s, ds.aux_join[h - 1], 0));
   }
+  if (st) return st;
   if (out.d_assign && max_iters == 0) HIP_TRY(hipMemsetAsync(codes, 0, n * sizeof(uint16_t), s));
   if (out.d_assign) {
     widen_codes_kernel<<<(unsigned)((n + 255) / 256), 256, 0, s>>>(codes, out.d_assign, n);
@@ -952,6 +1024,7 @@ int train_core(DeviceState &ds, hipStream_t s, const float *d_x, uint64_t n, uin
       HIP_TRY(hipEventElapsedTime(&ms, e0, e1));
       g_prof.transpose_ms += ms;
       g_prof.transpose_launches += 1;
+      g_prof.train_streams = H;
       for (size_t t = 0; t < it_events.size(); ++t) {
         const size_t q = it_events[t];
         HIP_TRY(hipEventElapsedTime(&ms, ds.events[q], ds.events[q + 1]));

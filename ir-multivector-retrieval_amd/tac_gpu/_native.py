@@ -72,6 +72,7 @@ class Profile(ctypes.Structure):
         ("cand_deferred", c_u64),
         ("cand_assign_ms", ctypes.c_double),
         ("cand_assign_iters", c_u64),
+        ("train_streams", c_u64),
     ]
 
 

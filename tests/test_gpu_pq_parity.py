@@ -37,6 +37,32 @@ def test_encode_matches_oracle(gpu, m, ksub):
     assert np.array_equal(got, ref), f"{np.count_nonzero(got != ref)} codes differ"
 
 
+@pytest.mark.parametrize("tol", [NEVER, 1e-3])
+def test_train_two_streams_match_one(gpu, monkeypatch, tol):
+    """The Lloyd loop runs the two halves of the subspaces on two streams
+    when m is even; one stream (TAC_GPU_TRAIN_STREAMS=1) gives the same bits,
+    also when subspaces of either half converge at different iterations."""
+    w, x, init = synth.workload("chunk-117k", n=60000)
+
+    def run():
+        return pq.train(x, w.dim, 0, m=w.m, ksub=w.ksub, max_iters=12, tol=tol,
+                        init_codebooks=init, trace=True)
+
+    two = run()
+    monkeypatch.setenv("TAC_GPU_TRAIN_STREAMS", "1")
+    one = run()
+    assert np.array_equal(_bits(two.stats.trace), _bits(one.stats.trace))
+    assert np.array_equal(_bits(two.codebooks), _bits(one.codebooks))
+    assert np.array_equal(two.stats.iters_run, one.stats.iters_run)
+    assert np.array_equal(two.stats.empties, one.stats.empties)
+    assert np.array_equal(_bits(two.stats.wcss), _bits(one.stats.wcss))
+    if tol != NEVER:
+        ref = orc.pq_train(x, w.dim, w.m, w.ksub, init=init, max_iters=12, tol=tol,
+                           n_threads=16)
+        assert np.array_equal(two.stats.iters_run, ref.iters_run)
+        assert np.array_equal(_bits(two.codebooks), _bits(ref.codebooks))
+
+
 def test_encode_ties_pick_lowest_index(gpu):
     # Codewords 5, 9 and 200 of every subspace are identical and nearest to
     # every vector: the reference keeps the first (strict <), i.e. 5.
