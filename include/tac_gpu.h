@@ -341,6 +341,18 @@ int tac_cluster_flat(const uint32_t *token_ids, uint64_t n_tokens, const float *
                      float *centroids_out, uint32_t *assignments_out,
                      uint32_t *kappa_per_token_out, uint64_t kappa_per_token_len,
                      float *wcss_total_out, uint64_t *n_distinct_out);
+/* tac_cluster_flat over token vectors already resident on the device
+ * (d_vectors: n_tokens * dim floats); token ids and every output stay in host
+ * memory, results and errors are those of tac_cluster_flat.  No counterpart in
+ * the reference: it is for callers whose token vectors are on the GPU already
+ * (the storage build holds them there for the residual and encode stages), and
+ * skips the n_tokens * dim * 4-byte upload. */
+int tac_cluster_flat_device(const uint32_t *token_ids, uint64_t n_tokens,
+                            const float *d_vectors, uint64_t vectors_len, uint32_t dim,
+                            const tac_cluster_params *params, float *centroids_out,
+                            uint32_t *assignments_out, uint32_t *kappa_per_token_out,
+                            uint64_t kappa_per_token_len, float *wcss_total_out,
+                            uint64_t *n_distinct_out);
 
 /* ---- measurement -------------------------------------------------------- */
 /* When enabled, the library brackets its kernels with HIP events on the

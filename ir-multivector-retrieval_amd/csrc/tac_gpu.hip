@@ -2207,9 +2207,9 @@ int tac_plan(const std::vector<uint32_t> &freqs, const std::vector<uint32_t> &of
 }
 
 int tac_cluster_core(DeviceState &ds, hipStream_t s, const uint32_t *ids, uint64_t N,
-                     const float *vectors, uint32_t dim, const tac_cluster_params &prm,
-                     uint64_t nd, float *cent_out, uint32_t *assign_out, uint32_t *kpt_out,
-                     float *wcss_out) {
+                     const float *vectors, bool vectors_on_device, uint32_t dim,
+                     const tac_cluster_params &prm, uint64_t nd, float *cent_out,
+                     uint32_t *assign_out, uint32_t *kpt_out, float *wcss_out) {
   const auto wall0 = std::chrono::steady_clock::now();
   const uint32_t rt = tac_rows_per_tile(dim);
   if (rt < 64 || dim > 192) return TAC_ERR_UNSUPPORTED;
@@ -2231,18 +2231,24 @@ int tac_cluster_core(DeviceState &ds, hipStream_t s, const uint32_t *ids, uint64
   // loads run up to one batch past a token's last row, and the fold kernel's
   // lanes past dim up to 64 * per floats past a row
   const size_t gbytes = vbytes + tac_spread_pad_floats(dim) * sizeof(float);
-  if ((st = ensure(ds, ds.tac_v, vbytes)) || (st = ensure(ds, ds.tac_G, gbytes)) ||
-      (st = upload_vec(ds, ds.tac_idx, idx, s)) || (st = upload_vec(ds, ds.tac_offs, offs, s)) ||
+  if ((!vectors_on_device && (st = ensure(ds, ds.tac_v, vbytes))) ||
+      (st = ensure(ds, ds.tac_G, gbytes)) || (st = upload_vec(ds, ds.tac_idx, idx, s)) ||
+      (st = upload_vec(ds, ds.tac_offs, offs, s)) ||
       (st = ensure(ds, ds.tac_spreads, nd * sizeof(float))))
     return st;
-  HIP_TRY(hipMemcpyAsync(ds.tac_v.ptr, vectors, vbytes, hipMemcpyHostToDevice, s));
+  // Host vectors go up once; device-resident ones are gathered in place.
+  const float *dv = vectors;
+  if (!vectors_on_device) {
+    HIP_TRY(hipMemcpyAsync(ds.tac_v.ptr, vectors, vbytes, hipMemcpyHostToDevice, s));
+    dv = as<float>(ds.tac_v);
+  }
   float *G = as<float>(ds.tac_G);
   const uint64_t nf = (uint64_t)N * dim;
   // Grids stay far below a dispatch's 2^32 work-items: the gather and the
   // reciprocal table are grid-stride loops, the spreads run in token slices.
   constexpr uint64_t kMaxBlocks = 1ull << 20;
   tac_gather_kernel<<<(unsigned)std::min<uint64_t>((nf + 255) / 256, kMaxBlocks), 256, 0, s>>>(
-      as<float>(ds.tac_v), as<uint32_t>(ds.tac_idx), G, N, dim);
+      dv, as<uint32_t>(ds.tac_idx), G, N, dim);
   LAUNCH_TRY("tac_gather_kernel");
   uint32_t max_n = 0;
   for (uint64_t j = 0; j < nd; ++j) max_n = freqs[j] > max_n ? freqs[j] : max_n;
@@ -2495,11 +2501,13 @@ int tac_cluster_core(DeviceState &ds, hipStream_t s, const uint32_t *ids, uint64
 
 extern "C" {
 
-int tac_cluster_flat(const uint32_t *token_ids, uint64_t n_tokens, const float *vectors,
-                     uint64_t vectors_len, uint32_t dim, const tac_cluster_params *params,
-                     float *centroids_out, uint32_t *assignments_out,
-                     uint32_t *kappa_per_token_out, uint64_t kappa_per_token_len,
-                     float *wcss_total_out, uint64_t *n_distinct_out) {
+namespace {
+int cluster_flat_entry(const uint32_t *token_ids, uint64_t n_tokens, const float *vectors,
+                       bool on_device, uint64_t vectors_len, uint32_t dim,
+                       const tac_cluster_params *params, float *centroids_out,
+                       uint32_t *assignments_out, uint32_t *kappa_per_token_out,
+                       uint64_t kappa_per_token_len, float *wcss_total_out,
+                       uint64_t *n_distinct_out) {
   if (!params) return TAC_ERR_INVALID_ARGUMENT;
   // validation in the reference's order (tac.zig:570-573)
   if (n_tokens == 0) return TAC_ERR_EMPTY_TOKEN_DUMP;
@@ -2522,13 +2530,35 @@ int tac_cluster_flat(const uint32_t *token_ids, uint64_t n_tokens, const float *
   hipStream_t s;
   if ((st = resolve_stream(*ds, nullptr, &s))) return st;
   if ((st = begin_call(*ds, s))) return st;
-  st = tac_cluster_core(*ds, s, token_ids, n_tokens, vectors, dim, *params, nd, centroids_out,
-                        assignments_out, kappa_per_token_out, wcss_total_out);
+  st = tac_cluster_core(*ds, s, token_ids, n_tokens, vectors, on_device, dim, *params, nd,
+                        centroids_out, assignments_out, kappa_per_token_out, wcss_total_out);
   if (st) {
     HIP_TRY(hipStreamSynchronize(s));
     return st;
   }
   return end_call(*ds, s);
+}
+}  // namespace
+
+int tac_cluster_flat(const uint32_t *token_ids, uint64_t n_tokens, const float *vectors,
+                     uint64_t vectors_len, uint32_t dim, const tac_cluster_params *params,
+                     float *centroids_out, uint32_t *assignments_out,
+                     uint32_t *kappa_per_token_out, uint64_t kappa_per_token_len,
+                     float *wcss_total_out, uint64_t *n_distinct_out) {
+  return cluster_flat_entry(token_ids, n_tokens, vectors, false, vectors_len, dim, params,
+                            centroids_out, assignments_out, kappa_per_token_out,
+                            kappa_per_token_len, wcss_total_out, n_distinct_out);
+}
+
+int tac_cluster_flat_device(const uint32_t *token_ids, uint64_t n_tokens,
+                            const float *d_vectors, uint64_t vectors_len, uint32_t dim,
+                            const tac_cluster_params *params, float *centroids_out,
+                            uint32_t *assignments_out, uint32_t *kappa_per_token_out,
+                            uint64_t kappa_per_token_len, float *wcss_total_out,
+                            uint64_t *n_distinct_out) {
+  return cluster_flat_entry(token_ids, n_tokens, d_vectors, true, vectors_len, dim, params,
+                            centroids_out, assignments_out, kappa_per_token_out,
+                            kappa_per_token_len, wcss_total_out, n_distinct_out);
 }
 
 }  // extern "C"

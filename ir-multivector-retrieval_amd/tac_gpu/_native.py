@@ -159,6 +159,9 @@ SIGNATURES = {
     "tac_cluster_flat": (
         c_int, [c_void_p, c_u64, c_void_p, c_u64, c_u32, ctypes.POINTER(ClusterParams), c_void_p,
                 c_void_p, c_void_p, c_u64, c_f32_p, ctypes.POINTER(c_u64)]),
+    "tac_cluster_flat_device": (
+        c_int, [c_void_p, c_u64, c_void_p, c_u64, c_u32, ctypes.POINTER(ClusterParams), c_void_p,
+                c_void_p, c_void_p, c_u64, c_f32_p, ctypes.POINTER(c_u64)]),
     "tac_gpu_profile_enable": (c_int, [c_int]),
     "tac_gpu_profile_read": (c_int, [ctypes.POINTER(Profile), c_int]),
     "tac_gpu_profile_kernels": (

@@ -44,9 +44,16 @@ class ClusteringResult:
 
 
 def cluster_flat(token_ids, vectors, dim: int, p: ClusteringParams) -> ClusteringResult:
-    """clusterFlat: per-token budgets, then kmeans.fit per token, on the GPU."""
+    """clusterFlat: per-token budgets, then kmeans.fit per token, on the GPU.
+    `vectors` may also be a device.DeviceArray of n_tokens * dim floats
+    (tac_cluster_flat_device: no upload)."""
     ids = np.ascontiguousarray(token_ids, dtype=np.uint32).reshape(-1)
-    v = np.ascontiguousarray(vectors, dtype=np.float32).reshape(-1)
+    on_device = hasattr(vectors, "ptr") and hasattr(vectors, "nbytes")
+    if on_device:
+        vptr, vlen = vectors.ptr, vectors.nbytes // 4
+    else:
+        v = np.ascontiguousarray(vectors, dtype=np.float32).reshape(-1)
+        vptr, vlen = v.ctypes.data_as(ctypes.c_void_p), v.size
     nd = int(ids.max()) + 1 if ids.size else 1
     cent = np.zeros(max(p.kappa_total * max(dim, 1), 1), np.float32)
     asg = np.zeros(max(ids.size, 1), np.uint32)
@@ -54,8 +61,9 @@ def cluster_flat(token_ids, vectors, dim: int, p: ClusteringParams) -> Clusterin
     wcss = ctypes.c_float(0.0)
     nd_out = ctypes.c_uint64(0)
     prm = p.native()
-    errors.check(lib.tac_cluster_flat(
-        ids.ctypes.data_as(ctypes.c_void_p), ids.size, v.ctypes.data_as(ctypes.c_void_p), v.size,
+    fn = lib.tac_cluster_flat_device if on_device else lib.tac_cluster_flat
+    errors.check(fn(
+        ids.ctypes.data_as(ctypes.c_void_p), ids.size, vptr, vlen,
         dim, ctypes.byref(prm), cent.ctypes.data_as(ctypes.c_void_p),
         asg.ctypes.data_as(ctypes.c_void_p), kpt.ctypes.data_as(ctypes.c_void_p), nd,
         ctypes.byref(wcss), ctypes.byref(nd_out)))

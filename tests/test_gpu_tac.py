@@ -122,6 +122,25 @@ def test_token_id_past_2_pow_26(gpu):
     assert r.kappa_per_token.size == 70_000_001 and r.kappa_per_token[-1] == 1
 
 
+def test_device_resident_vectors(gpu):
+    """tac_cluster_flat_device: the same token dump resident on the device
+    gives the oracle's bits, as the host entry point does."""
+    from tac_gpu import device
+    ids, v = synth.tac_vectors(40_000, 64, 1024, 1.05, 0.15, 6)
+    kap = _feasible_kappa(ids)
+    ref = orc.tac_cluster_flat(ids, v, 64, orc.tac_params(kap, 9))
+    assert ref.status == 0
+    dv = device.DeviceArray.from_host(np.ascontiguousarray(v))
+    try:
+        got = tac.cluster_flat(ids, dv, 64, _params(kap, 9))
+    finally:
+        dv.free()
+    assert np.array_equal(got.kappa_per_token, ref.kappa_per_token)
+    assert got.centroids.tobytes() == ref.centroids.tobytes()
+    assert np.array_equal(got.assignments, ref.assignments)
+    assert np.float32(got.wcss_total).tobytes() == np.float32(ref.wcss_total).tobytes()
+
+
 def _expect(ids, v, dim, p_kw, exc):
     ref = orc.tac_cluster_flat(ids, v, dim, orc.tac_params(**p_kw))
     assert ref.status == exc.status
