@@ -97,7 +97,7 @@ struct DeviceState {
   Buffer tac_v, tac_idx, tac_offs, tac_G, tac_spreads, tac_w, tac_e, tac_code, tac_sorted,
       tac_tsum, tac_hist, tac_counts, tac_start, tac_C, tac_pre, tac_fch, tac_st, tac_bad,
       tac_done, tac_iters, tac_wcss, tac_prev, tac_empties, tac_assign, tac_probs, tac_tiles,
-      tac_chl, tac_cprob, tac_inv, tac_rsum, tac_ranges;
+      tac_chl, tac_cprob, tac_inv, tac_rsum, tac_ranges, tac_h;
   bool crc_tx_ready = false;
   // training's second stream (two halves of the subspaces) and its events
   hipStream_t aux_stream[1] = {};
@@ -1280,7 +1280,7 @@ int tac_gpu_release_workspace(void) {
                     &ds->tac_probs, &ds->tac_tiles, &ds->tac_chl, &ds->tac_cprob,
                     &ds->tac_inv,   &ds->tac_rsum, &ds->tac_ranges, &ds->cand_nbr,
                     &ds->cand_defer, &ds->cand_count, &ds->cand_anchor, &ds->cand_grid,
-                    &ds->kpp_src,   &ds->fold_order};
+                    &ds->kpp_src,   &ds->fold_order, &ds->tac_h};
   ds->crc_tx_ready = false;
   for (Buffer *b : bufs) {
     if (b->ptr) HIP_TRY(hipFree(b->ptr));
@@ -2329,6 +2329,17 @@ int tac_cluster_core(DeviceState &ds, hipStream_t s, const uint32_t *ids, uint64
       (st = ensure(ds, ds.tac_prev, (size_t)P * sizeof(float))) ||
       (st = ensure(ds, ds.tac_empties, (size_t)P * sizeof(uint32_t))))
     return st;
+  // 64-float rows take the matrix-core assignment (tac_assign_mfma_kernel);
+  // TAC_GPU_TAC_VALU_ASSIGN=1 keeps the exact search for every row.
+  const char *valu_env = getenv("TAC_GPU_TAC_VALU_ASSIGN");
+  const bool mfma = dim == 64 && rt == kTacMfmaRows && !(valu_env && valu_env[0] == '1');
+  // Problems are sorted by k, descending: the tiles of those with at least
+  // kmin centroids (a prefix) take the matrix cores, the rest the exact
+  // search, which costs less for a few centroids.
+  const char *kmin_env = getenv("TAC_GPU_TAC_MFMA_KMIN");
+  const uint32_t kmin = kmin_env ? (uint32_t)std::max(1, atoi(kmin_env)) : 8u;
+  const uint32_t mfma_tiles = !mfma ? 0u : pl.kmax >= kmin ? pl.tiles_upto[kmin - 1] : 0u;
+  if (mfma_tiles > 0 && (st = ensure(ds, ds.tac_h, K * sizeof(float)))) return st;
   float *w = as<float>(ds.tac_w), *e = as<float>(ds.tac_e), *C = as<float>(ds.tac_C);
   uint32_t *code = as<uint32_t>(ds.tac_code), *sorted = as<uint32_t>(ds.tac_sorted);
   uint32_t *done = as<uint32_t>(ds.tac_done), *bad = as<uint32_t>(ds.tac_bad);
@@ -2413,16 +2424,28 @@ int tac_cluster_core(DeviceState &ds, hipStream_t s, const uint32_t *ids, uint64
 
   // Lloyd iterations (kmeans.zig:149-224) for every problem not yet converged
   for (uint32_t t = 0; t < prm.max_iters; ++t) {
-    if (dim == 64)
-      tac_assign_kernel<64><<<NT, rt, asg_lds, s>>>(G, C, probs, tiles, done, code, e, dim,
-                                                    chunk_c);
-    else if (dim == 128)
-      tac_assign_kernel<128><<<NT, rt, asg_lds, s>>>(G, C, probs, tiles, done, code, e, dim,
+    if (mfma_tiles > 0) {
+      tac_cnorm_kernel<<<(unsigned)((K + 255) / 256), 256, 0, s>>>(
+          C, as<uint32_t>(ds.tac_cprob), done, (uint32_t)K, as<float>(ds.tac_h));
+      LAUNCH_TRY("tac_cnorm_kernel");
+      tac_assign_mfma_kernel<<<mfma_tiles, kTacMfmaThreads, 0, s>>>(
+          G, C, as<float>(ds.tac_h), probs, tiles, done, code, e);
+      LAUNCH_TRY("tac_assign_mfma_kernel");
+    }
+    if (mfma_tiles < NT) {
+      const uint32_t nt = NT - mfma_tiles;
+      const TacTile *rest = tiles + mfma_tiles;
+      if (dim == 64)
+        tac_assign_kernel<64><<<nt, rt, asg_lds, s>>>(G, C, probs, rest, done, code, e, dim,
+                                                      chunk_c);
+      else if (dim == 128)
+        tac_assign_kernel<128><<<nt, rt, asg_lds, s>>>(G, C, probs, rest, done, code, e, dim,
+                                                       chunk_c);
+      else
+        tac_assign_kernel<0><<<nt, rt, asg_lds, s>>>(G, C, probs, rest, done, code, e, dim,
                                                      chunk_c);
-    else
-      tac_assign_kernel<0><<<NT, rt, asg_lds, s>>>(G, C, probs, tiles, done, code, e, dim,
-                                                   chunk_c);
-    LAUNCH_TRY("tac_assign_kernel");
+      LAUNCH_TRY("tac_assign_kernel");
+    }
     tac_hist_kernel<<<NT, rt, code_lds, s>>>(code, probs, tiles, done, hist);
     LAUNCH_TRY("tac_hist_kernel");
     tac_scan_partial_kernel<<<NR, 256, 0, s>>>(hist, probs, ranges, done, rsum);

@@ -546,6 +546,292 @@ __global__ void tac_assign_kernel(const float* __restrict__ G, const float* __re
 }
 
 // ---------------------------------------------------------------------------
+// Lloyd assignment for 64-float rows on the matrix cores: the same result as
+// tac_assign_kernel, with most of the arithmetic moved to MFMA.
+//
+// Screen.  s(x, c) = h_c - x.c with h_c = ||c||^2 / 2 (fp32, any order) and
+// x.c from v_mfma_f32_16x16x4_f32 (16 steps of 4 dimensions).  Whatever the
+// order and rounding of the products and sums inside the matrix core,
+// |s - (||c||^2 / 2 - x.c)| <= E = Gm (||x||^2 + 2 cmax2) + 1e-35 with
+// Gm = 512 u (u = 2^-24), cmax2 >= ||c||^2 for every centroid of the
+// problem, and the addend covering products in the subnormal range.
+// Candidates.  The reference distance (tac_l2sq<64>: four 16-term lane sums
+// and three adds, g = gamma_20 relative) of the winner c* is at most that of
+// the screen's minimum c_m, so s(c*) <= s_min + 2E + 1.01 g ||x - c_m||^2
+// and ||x - c_m||^2 <= ||x||^2 + 2 (s_min + E).  tac_screen_threshold
+// bounds this with the factors doubled and 1e-30 added, which covers the
+// rounding of its own arithmetic.  Every centroid whose screen value is at
+// most the threshold gets the reference distance; the lexicographic minimum
+// of (distance bits, index) over them is the reference's first-index argmin
+// (non-negative finite distances).
+// Lanes.  A 16-row group x 16 centroids: lane l feeds row l % 16 and
+// centroid l % 16 at dimension 4 s + l / 16 and holds the dot products of
+// rows 4 (l / 16) + i, i < 4, with centroid l % 16.  Each lane keeps the two
+// smallest screen values of its centroids per row; when the second is at
+// most the threshold the lane may hold more candidates, and the row gets the
+// reference distance to every centroid instead.  A block whose rows or
+// centroids have non-finite, subnormal or huge components (where the bounds
+// do not hold) takes tac_assign_kernel's exact search for all its rows.
+// One block of 256 work-items per tile of 128 rows; wave w takes rows
+// 32 w .. 32 w + 31 as two row groups, four accumulator chains at a time.
+// ---------------------------------------------------------------------------
+constexpr uint32_t kTacMfmaRows = 128;     // rows per tile (tac_rows_per_tile(64))
+constexpr uint32_t kTacMfmaThreads = 256;
+constexpr uint32_t kTacMfmaChunk = 64;     // centroids staged in LDS at a time
+constexpr uint32_t kTacMfmaLd = 65;        // LDS row stride (floats)
+
+// Components for which the screen's bounds hold: finite, |v| < 1e18 and not
+// subnormal.
+__device__ __forceinline__ bool tac_screen_tame(float v) {
+  const float a = fabsf(v);
+  return a < 1e18f && (a == 0.0f || a >= 1.17549435e-38f);
+}
+
+__device__ __forceinline__ float tac_screen_threshold(float s_min, float x2, float cmax2) {
+  constexpr float u = 5.9604644775390625e-8f;
+  const float E = 512.0f * u * (x2 + 2.0f * cmax2) + 1e-35f;
+  return s_min + 2.0f * E + 2.0f * (32.0f * u) * (x2 + 2.0f * fabsf(s_min) + 2.0f * E) + 1e-30f;
+}
+
+// Per Lloyd iteration, before the assignment: h[c] = ||c||^2 / 2 for every
+// centroid of an unfinished problem, NaN when a component breaks
+// tac_screen_tame (the assignment then takes the exact search).
+__global__ __launch_bounds__(256) void tac_cnorm_kernel(const float* __restrict__ C,
+                                                        const uint32_t* __restrict__ cprob,
+                                                        const uint32_t* __restrict__ done,
+                                                        uint32_t K, float* __restrict__ h) {
+  const uint32_t c = blockIdx.x * blockDim.x + threadIdx.x;
+  if (c >= K) return;
+  if (done[cprob[c]]) return;
+  const float4* row = reinterpret_cast<const float4*>(C + (uint64_t)c * 64);
+  float n = 0.0f;
+  bool tame = true;
+#pragma unroll 4
+  for (int q = 0; q < 16; ++q) {
+    const float4 v = row[q];
+    tame = tame && tac_screen_tame(v.x) && tac_screen_tame(v.y) && tac_screen_tame(v.z) &&
+           tac_screen_tame(v.w);
+    n = n + v.x * v.x;
+    n = n + v.y * v.y;
+    n = n + v.z * v.z;
+    n = n + v.w * v.w;
+  }
+  h[c] = tame ? 0.5f * n : __builtin_nanf("");
+}
+
+typedef float tac_floatx4 __attribute__((ext_vector_type(4)));
+
+__global__ __launch_bounds__(kTacMfmaThreads) void tac_assign_mfma_kernel(
+    const float* __restrict__ G, const float* __restrict__ C, const float* __restrict__ h,
+    const TacProblem* __restrict__ probs, const TacTile* __restrict__ tiles,
+    const uint32_t* __restrict__ done, uint32_t* __restrict__ code, float* __restrict__ e) {
+  constexpr uint32_t R = kTacMfmaRows, LD = kTacMfmaLd, CH = kTacMfmaChunk;
+  __shared__ float xr[R * LD];
+  __shared__ float cs[CH * LD];
+  __shared__ float hs[CH];
+  __shared__ float x2s[R];
+  __shared__ unsigned long long rowkey[R];
+  __shared__ uint32_t queue[R * 16];
+  __shared__ uint32_t full[R];  // rows whose candidates a lane may not hold
+  __shared__ uint32_t qn, nfull, exact, hmax;
+  const TacTile tl = tiles[blockIdx.x];
+  if (done[tl.prob]) return;
+  const TacProblem pr = probs[tl.prob];
+  const uint32_t t = threadIdx.x, lane = t % 64, w = t / 64, li = lane % 16, lq = lane / 16;
+  const uint32_t rows = pr.n - tl.row0 < R ? pr.n - tl.row0 : R;
+  if (t == 0) {
+    qn = 0;
+    nfull = 0;
+    exact = 0;
+    hmax = 0;  // bits of the largest h of the problem (NaN: an untame centroid)
+  }
+  tac_stage_rows(G, pr, tl.row0, R, 64, LD, xr);
+  __syncthreads();
+  if (t < R) {
+    float x2 = 0.0f;
+    bool tame = true;
+    if (t < rows) {
+      for (int d = 0; d < 64; ++d) {
+        const float v = xr[t * LD + d];
+        tame = tame && tac_screen_tame(v);
+        x2 = x2 + v * v;
+      }
+      if (!tame) atomicOr(&exact, 1u);
+    }
+    x2s[t] = x2;
+    rowkey[t] = ~0ull;
+  }
+  __syncthreads();
+  const float* Cp = C + (uint64_t)pr.goff * 64;
+  if (!exact) {
+    // A operands of the wave's two row groups (rows past the tile read 0).
+    float a[2][16];
+#pragma unroll
+    for (int g = 0; g < 2; ++g) {
+      const uint32_t r = 32 * w + 16 * g + li;
+#pragma unroll
+      for (int s = 0; s < 16; ++s) a[g][s] = r < rows ? xr[r * LD + 4 * s + lq] : 0.0f;
+    }
+    float b1[2][4], b2[2][4];
+    uint32_t i1[2][4], i2[2][4];
+#pragma unroll
+    for (int g = 0; g < 2; ++g)
+#pragma unroll
+      for (int v = 0; v < 4; ++v) {
+        b1[g][v] = __builtin_inff();
+        b2[g][v] = __builtin_inff();
+        i1[g][v] = 0;
+        i2[g][v] = 0;
+      }
+    // Chunks of CH centroids pass through LDS; each work-item holds its 16
+    // floats (and h) of the next chunk in registers while the current one is
+    // worked on.
+    constexpr uint32_t PF = CH * 64 / kTacMfmaThreads;
+    float pf[PF];
+    float ph = __builtin_inff();
+    auto fetch = [&](uint32_t c0) {
+      const uint32_t cnt = pr.k - c0 < CH ? pr.k - c0 : CH;
+#pragma unroll
+      for (uint32_t j = 0; j < PF; ++j) {
+        const uint32_t f = t + j * kTacMfmaThreads, cc = f / 64;
+        pf[j] = cc < cnt ? Cp[(uint64_t)c0 * 64 + f] : 0.0f;
+      }
+      if (t < CH) ph = t < cnt ? h[pr.goff + c0 + t] : __builtin_inff();
+    };
+    fetch(0);
+    for (uint32_t c0 = 0; c0 < pr.k; c0 += CH) {
+      const uint32_t cnt = pr.k - c0 < CH ? pr.k - c0 : CH;
+      __syncthreads();
+#pragma unroll
+      for (uint32_t j = 0; j < PF; ++j) {
+        const uint32_t f = t + j * kTacMfmaThreads;
+        cs[(f / 64) * LD + f % 64] = pf[j];
+      }
+      if (t < CH) {
+        hs[t] = ph;
+        // NaN bits exceed every finite value's, so a NaN h shows in hmax.
+        if (t < cnt) atomicMax(&hmax, __float_as_uint(ph) & 0x7FFFFFFFu);
+      }
+      __syncthreads();
+      if (c0 + CH < pr.k) fetch(c0 + CH);
+      // Two centroid groups at a time: four independent accumulator chains
+      // (2 row groups x 2 centroid groups) keep the matrix core busy.  A
+      // group past the chunk's centroids reads the padding (h = inf).
+      for (uint32_t cg = 0; cg < CH / 16 && cg * 16 < cnt; cg += 2) {
+        float bv[2][16], hv[2];
+        uint32_t cidx[2];
+#pragma unroll
+        for (int j = 0; j < 2; ++j) {
+          const uint32_t cc = (cg + j) * 16 + li;
+#pragma unroll
+          for (int s = 0; s < 16; ++s) bv[j][s] = cs[cc * LD + 4 * s + lq];
+          hv[j] = hs[cc];
+          cidx[j] = c0 + cc;
+        }
+        tac_floatx4 acc[2][2];
+#pragma unroll
+        for (int g = 0; g < 2; ++g)
+#pragma unroll
+          for (int j = 0; j < 2; ++j) acc[g][j] = tac_floatx4{0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+        for (int s = 0; s < 16; ++s)
+#pragma unroll
+          for (int g = 0; g < 2; ++g)
+#pragma unroll
+            for (int j = 0; j < 2; ++j)
+              acc[g][j] = __builtin_amdgcn_mfma_f32_16x16x4f32(a[g][s], bv[j][s], acc[g][j], 0, 0,
+                                                               0);
+        // Two smallest screen values per (row group, row) without branches;
+        // centroids arrive in ascending index order.
+#pragma unroll
+        for (int j = 0; j < 2; ++j)
+#pragma unroll
+          for (int g = 0; g < 2; ++g)
+#pragma unroll
+            for (int v = 0; v < 4; ++v) {
+              const float sv = hv[j] - acc[g][j][v];
+              const bool lt1 = sv < b1[g][v], lt2 = sv < b2[g][v];
+              b2[g][v] = lt1 ? b1[g][v] : (lt2 ? sv : b2[g][v]);
+              i2[g][v] = lt1 ? i1[g][v] : (lt2 ? cidx[j] : i2[g][v]);
+              b1[g][v] = lt1 ? sv : b1[g][v];
+              i1[g][v] = lt1 ? cidx[j] : i1[g][v];
+            }
+      }
+    }
+    if (hmax >= 0x7F800000u) exact = 1;  // an untame centroid (uniform: read after a barrier)
+    const float cmax2 = 2.0f * __uint_as_float(hmax);
+#pragma unroll
+    for (int g = 0; g < 2; ++g)
+#pragma unroll
+      for (int v = 0; v < 4; ++v) {
+        float m = b1[g][v];
+#pragma unroll
+        for (int off = 1; off < 16; off <<= 1) m = fminf(m, __shfl_xor(m, off, 64));
+        const uint32_t r = 32 * w + 16 * g + 4 * lq + v;
+        const float thr = tac_screen_threshold(m, x2s[r], cmax2);
+        // A NaN screen value (or threshold) cannot occur with tame inputs;
+        // it sends the row to the full search all the same.  The row's 16
+        // lanes agree through the reduction, and lane 16 q lists it.
+        uint32_t over = (!(m <= thr) || b2[g][v] <= thr) ? 1u : 0u;
+#pragma unroll
+        for (int off = 1; off < 16; off <<= 1) over |= __shfl_xor(over, off, 64);
+        if (r < rows) {
+          if (b1[g][v] <= thr) queue[atomicAdd(&qn, 1u)] = (r << 16) | i1[g][v];
+          if (li == 0 && over) full[atomicAdd(&nfull, 1u)] = r;
+        }
+      }
+    __syncthreads();
+    if (!exact) {
+      for (uint32_t q = t; q < qn; q += kTacMfmaThreads) {
+        const uint32_t r = queue[q] >> 16, c = queue[q] & 0xFFFFu;
+        const float d = tac_l2sq<64>(xr + r * LD, Cp + (uint64_t)c * 64, 64);
+        atomicMin(&rowkey[r], ((unsigned long long)__float_as_uint(d) << 32) | c);
+      }
+      // Rows a lane's two kept values could not settle: every centroid, the
+      // block's work-items side by side.
+      for (uint32_t j = 0; j < nfull; ++j) {
+        const uint32_t r = full[j];
+        for (uint32_t c = t; c < pr.k; c += kTacMfmaThreads) {
+          const float d = tac_l2sq<64>(xr + r * LD, Cp + (uint64_t)c * 64, 64);
+          atomicMin(&rowkey[r], ((unsigned long long)__float_as_uint(d) << 32) | c);
+        }
+      }
+      __syncthreads();
+      if (t < rows) {
+        const unsigned long long k = rowkey[t];
+        code[pr.off + tl.row0 + t] = (uint32_t)k;
+        e[pr.off + tl.row0 + t] = __uint_as_float((uint32_t)(k >> 32));
+      }
+      return;
+    }
+  }
+  // The exact search of tac_assign_kernel: vec.argmin from values[0], strict <.
+  float best = 0.0f;
+  uint32_t bi = 0;
+  for (uint32_t c0 = 0; c0 < pr.k; c0 += CH) {
+    const uint32_t cnt = pr.k - c0 < CH ? pr.k - c0 : CH;
+    __syncthreads();
+    for (uint32_t f = t; f < cnt * 64; f += kTacMfmaThreads)
+      cs[(f / 64) * LD + f % 64] = Cp[(uint64_t)c0 * 64 + f];
+    __syncthreads();
+    if (t < rows)
+      for (uint32_t q = 0; q < cnt; ++q) {
+        const float d = tac_l2sq<64>(xr + t * LD, cs + q * LD, 64);
+        if (c0 + q == 0) {
+          best = d;
+        } else if (d < best) {
+          best = d;
+          bi = c0 + q;
+        }
+      }
+  }
+  if (t < rows) {
+    code[pr.off + tl.row0 + t] = bi;
+    e[pr.off + tl.row0 + t] = best;
+  }
+}
+
+// ---------------------------------------------------------------------------
 // Stable grouping of each problem's rows by code, so that every cluster's
 // members are folded in ascending row order (kmeans.zig:177-184).
 // Step 1: tile histograms hist[hist0 + t * k + c].

@@ -122,6 +122,30 @@ def test_token_id_past_2_pow_26(gpu):
     assert r.kappa_per_token.size == 70_000_001 and r.kappa_per_token[-1] == 1
 
 
+@pytest.mark.parametrize("case", ["dump", "ties", "untame"])
+def test_matrix_core_assignment(gpu, monkeypatch, case):
+    """64-float rows: the MFMA-screened assignment on every problem (a k
+    threshold of 1) gives the oracle's bits, also with exact ties between
+    centroids (rows the screen cannot settle) and with subnormal or huge
+    components (blocks that fall back to the exact search)."""
+    monkeypatch.setenv("TAC_GPU_TAC_MFMA_KMIN", "1")
+    if case == "dump":
+        ids, v = synth.tac_vectors(60_000, 64, 2048, 1.05, 0.15, 8)
+        _check(ids, v, 64, _feasible_kappa(ids), 5)
+        return
+    rng = np.random.default_rng(11 if case == "ties" else 12)
+    ids = (np.arange(6000) % 3).astype(np.uint32)
+    if case == "ties":
+        # small-integer rows: the first assignment (centroids are seeded rows)
+        # has exact distance ties, some of them inside one lane's centroids
+        v = rng.integers(0, 3, (ids.size, 64)).astype(np.float32)
+    else:
+        v = rng.standard_normal((ids.size, 64)).astype(np.float32)
+        v[::97, 5] = np.float32(1e-40)  # subnormal
+        v[::389, 9] = np.float32(3e18)  # beyond the screen's bound
+    _check(ids, v.astype(np.float32), 64, 60, 21, mu=3, tau=5, epsilon=1, theta=1)
+
+
 def test_device_resident_vectors(gpu):
     """tac_cluster_flat_device: the same token dump resident on the device
     gives the oracle's bits, as the host entry point does."""
