@@ -426,7 +426,7 @@ struct Launch {
       G = cand_grid_side(D);
       cells = 1;
       for (int k = 0; k < D; ++k) cells *= G;
-      KT("grid_build_kernel<%d, %uu>", D, NA);
+      KT("grid_build_kernel<%d, %uu, %s>", D, NA, code_name<AnchorT>());
       grid_build_kernel<D, NA, AnchorT><<<dim3((cells + kBlock - 1) / kBlock, M), kBlock, 0, s>>>(
           cb, anchors, grid, K, G, cells);
       KT_END();
@@ -445,7 +445,8 @@ struct Launch {
     if (int st = raise_lds((const void *)cand_kernel<D, GRID, false, uint16_t, AnchorT>,
                            lay.total, cells))
       return st;
-    KT("cand_kernel<%d, %s, false, unsigned short>", D, GRID ? "true" : "false");
+    KT("cand_kernel<%d, %s, false, unsigned short, %s>", D, GRID ? "true" : "false",
+       code_name<AnchorT>());
     cand_kernel<D, GRID, false, uint16_t, AnchorT><<<dim3((unsigned)nblk, M), kCandThreads,
                                                      lay.total, s>>>(
         xs, cb, nbr, anchors, grid, codes, e, nullptr, slice, defer, defer_count, done, n, 0, M, K,
@@ -490,7 +491,7 @@ struct Launch {
     nbr_build_kernel<D><<<dim3(K, M), nbr_threads(K), 0, s>>>(cb, nbr, defer_count, nullptr, K,
                                                                L);
     KT_END();
-    KT("grid_build_kernel<%d, %uu>", D, cand_anchors<true>());
+    KT("grid_build_kernel<%d, %uu, %s>", D, cand_anchors<true>(), code_name<AnchorT>());
     grid_build_kernel<D, cand_anchors<true>(), AnchorT><<<dim3((cells + kBlock - 1) / kBlock, M),
                                                           kBlock, 0, s>>>(
         cb, anchors, grid, K, G, cells);
@@ -519,7 +520,7 @@ struct Launch {
     const uint64_t total = nchunks * M;
     if (total > 0xFFFFFFF0ull) return TAC_ERR_UNSUPPORTED;
     const uint32_t blocks = (uint32_t)(8 * ((total + 7) / 8));
-    KT("cand_kernel<%d, true, true, %s>", D, code_name<CodeT>());
+    KT("cand_kernel<%d, true, true, %s, %s>", D, code_name<CodeT>(), code_name<CodeT>());
     cand_kernel<D, true, true, CodeT, CodeT><<<blocks, kCandThreads, lay.total, s>>>(
         x, cb, nbr, anchors, grid, nullptr, nullptr, codes, slice, defer, defer_count, nullptr, n,
         dim, M, K, L, (uint32_t)chunk, (uint32_t)nchunks, G, cells, nullptr, 0);
