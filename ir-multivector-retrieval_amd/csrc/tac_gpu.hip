@@ -650,12 +650,22 @@ struct TrainOut {
   uint32_t *h_iters_single;  // host scalar (kmeans.fit) or null
 };
 
-// k-means++ seeding of all subspaces (src/tac/kmeans.zig:106-136) into
-// out.cb.  Returns the lowest subspace's error, as a serial run of the
-// reference (src/index/pq.zig:180-191) would.
-int kmeanspp(DeviceState &ds, hipStream_t s, const float *xs, uint64_t n, uint32_t M, uint32_t K,
-             uint32_t D, uint64_t seed, float *cb) {
+// A run of consecutive subspaces [m0, m0 + Mh) and the stream it runs on.
+struct SubspaceGroup {
+  uint32_t m0, Mh;
+  hipStream_t s;
+};
+
+// k-means++ seeding of all subspaces (src/tac/kmeans.zig:106-136) into cb,
+// each group of subspaces on its own stream (groups[0] on s, the call's
+// stream, which waits for the others before the states are read back).
+// Returns the lowest subspace's error, as a serial run of the reference
+// (src/index/pq.zig:180-191) would.
+int kmeanspp(DeviceState &ds, hipStream_t s, const SubspaceGroup *groups, uint32_t H,
+             const float *xs, uint64_t n, uint32_t M, uint32_t K, uint32_t D, uint64_t seed,
+             float *cb) {
   const uint32_t NB = (uint32_t)((n + kKppBlock - 1) / kKppBlock);
+  const uint32_t DP = pad_of(D);
   int st;
   if ((st = ensure(ds, ds.kpp_state, (size_t)M * sizeof(KppState))) ||
       (st = ensure(ds, ds.kpp_w, (size_t)M * n * sizeof(float))) ||
@@ -677,26 +687,46 @@ int kmeanspp(DeviceState &ds, hipStream_t s, const float *xs, uint64_t n, uint32
   const uint32_t exact_only = exact_env != nullptr && exact_env[0] == '1';
   KppState *state = as<KppState>(ds.kpp_state);
   float *w = as<float>(ds.kpp_w);
+  uint16_t *src = as<uint16_t>(ds.kpp_src);
   double *bsum = as<double>(ds.kpp_bsum);
   uint32_t *bad = as<uint32_t>(ds.kpp_bad);
-  kpp_init_kernel<<<(M + 63) / 64, 64, 0, s>>>(state, bad, seed, n, M);
-  LAUNCH_TRY("kpp_init_kernel");
-  for (uint32_t c = 0; c < K; ++c) {
-    DISPATCH_D(D, kpp_update(xs, w, as<uint16_t>(ds.kpp_src), bsum, bad, state, cb, n, M, K, c,
-                             NB, s));
-    LAUNCH_TRY("kpp_update_kernel");
-    if (c + 1 == K) break;
-    kpp_select_kernel<<<M, 1024, 0, s>>>(w, bsum, bad, state, n, NB, exact_only);
-    LAUNCH_TRY("kpp_select_kernel");
-    kpp_fallback_kernel<<<M, kKppFallbackThreads, 0, s>>>(w, state, n, fold_pre, fold_chunks,
-                                                          nfc);
-    LAUNCH_TRY("kpp_fallback_kernel");
+  auto launch_all = [&]() -> int {
+    for (uint32_t h = 0; h < H; ++h) {
+      const SubspaceGroup &g = groups[h];
+      kpp_init_kernel<<<(g.Mh + 63) / 64, 64, 0, g.s>>>(state + g.m0, bad + g.m0, seed + g.m0,
+                                                       n, g.Mh);
+      LAUNCH_TRY("kpp_init_kernel");
+    }
+    for (uint32_t c = 0; c < K; ++c) {
+      for (uint32_t h = 0; h < H; ++h) {
+        const SubspaceGroup &g = groups[h];
+        const uint64_t m0 = g.m0;
+        DISPATCH_D(D, kpp_update(xs + m0 * n * DP, w + m0 * n, src + m0 * n, bsum + m0 * NB,
+                                 bad + m0, state + m0, cb + m0 * K * D, n, g.Mh, K, c, NB, g.s));
+        LAUNCH_TRY("kpp_update_kernel");
+        if (c + 1 == K) continue;
+        kpp_select_kernel<<<g.Mh, 1024, 0, g.s>>>(w + m0 * n, bsum + m0 * NB, bad + m0,
+                                                  state + m0, n, NB, exact_only);
+        LAUNCH_TRY("kpp_select_kernel");
+        kpp_fallback_kernel<<<g.Mh, kKppFallbackThreads, 0, g.s>>>(
+            w + m0 * n, state + m0, n, fold_pre + m0 * nfc, fold_chunks + m0 * nfc, nfc);
+        LAUNCH_TRY("kpp_fallback_kernel");
+      }
+    }
+    return TAC_OK;
+  };
+  st = launch_all();
+  // The call's stream waits for the other groups, also after an error.
+  for (uint32_t h = 1; h < H; ++h) {
+    HIP_TRY(hipEventRecord(ds.aux_join[h - 1], groups[h].s));
+    HIP_TRY(hipStreamWaitEvent(s, ds.aux_join[h - 1], 0));
   }
-  std::vector<KppState> h(M);
-  HIP_TRY(hipMemcpyAsync(h.data(), state, M * sizeof(KppState), hipMemcpyDeviceToHost, s));
+  if (st) return st;
+  std::vector<KppState> hs(M);
+  HIP_TRY(hipMemcpyAsync(hs.data(), state, M * sizeof(KppState), hipMemcpyDeviceToHost, s));
   HIP_TRY(hipStreamSynchronize(s));
   for (uint32_t m = 0; m < M; ++m)
-    if (h[m].err) return h[m].err;
+    if (hs[m].err) return hs[m].err;
   return TAC_OK;
 }
 
@@ -815,34 +845,17 @@ int train_core(DeviceState &ds, hipStream_t s, const float *d_x, uint64_t n, uin
   DISPATCH_D_ST(D, transpose(d_x, xs, n, dim, s));
   if (st) return st;
   LAUNCH_TRY("transpose_kernel");
-  if (out.kpp && (st = kmeanspp(ds, s, xs, n, M, K, D, out.seed, out.cb))) return st;
-  if (profile) {
-    if ((st = event_at(ds, ev++, &e1))) return st;
-    HIP_TRY(hipEventRecord(e1, s));
-  }
-
-  // The reference breaks on rel < tol; only a tol above -inf can ever fire.
-  const bool check = tol > -INFINITY;
-  const bool want_wcss = (ex && ex->wcss) || out.h_wcss_single;
-  const size_t hist_lds = (size_t)K * sizeof(uint32_t);
-  std::vector<size_t> it_events;  // event index triples per iteration
-  uint32_t gcells = 1;
-  for (uint32_t k = 0; k < D; ++k) gcells *= cand_grid_side(D);
-
-  // Two halves of the subspaces on two streams (M even): every subspace's
-  // kernels see only its own buffers, so each half runs the same arithmetic
-  // as one stream would, and one half's latency-bound steps (the fold's
-  // longest chains, the deferred-vector scans, the small scans) overlap the
-  // other half's VALU-bound assignment.  TAC_GPU_TRAIN_STREAMS=1 keeps one
+  // Two halves of the subspaces on two streams (M even), for the k-means++
+  // seeding and the Lloyd loop: every subspace's kernels see only its own
+  // buffers, so each half runs the same arithmetic as one stream would, and
+  // one half's latency-bound steps (the fold's longest chains, the
+  // deferred-vector scans, the draws, the small scans) overlap the other
+  // half's VALU- or HBM-bound work.  TAC_GPU_TRAIN_STREAMS=1 keeps one
   // stream.
   const char *streams_env = getenv("TAC_GPU_TRAIN_STREAMS");
   const bool one_stream = streams_env && streams_env[0] == '1';
   const uint32_t H = (!one_stream && M >= 2 && M % 2 == 0) ? 2u : 1u;
-  struct Half {
-    uint32_t m0, Mh;
-    hipStream_t s;
-  };
-  Half halves[2];
+  SubspaceGroup halves[2];
   for (uint32_t h = 0; h < H; ++h) halves[h] = {h * (M / H), M / H, s};
   if (H > 1) {
     if (!ds.aux_fork) HIP_TRY(hipEventCreateWithFlags(&ds.aux_fork, hipEventDisableTiming));
@@ -856,6 +869,23 @@ int train_core(DeviceState &ds, hipStream_t s, const float *d_x, uint64_t n, uin
       HIP_TRY(hipStreamWaitEvent(halves[h].s, ds.aux_fork, 0));
     }
   }
+  if (out.kpp && (st = kmeanspp(ds, s, halves, H, xs, n, M, K, D, out.seed, out.cb))) {
+    // the other half joins the call's stream inside kmeanspp
+    return st;
+  }
+  if (profile) {
+    if ((st = event_at(ds, ev++, &e1))) return st;
+    HIP_TRY(hipEventRecord(e1, s));
+  }
+
+  // The reference breaks on rel < tol; only a tol above -inf can ever fire.
+  const bool check = tol > -INFINITY;
+  const bool want_wcss = (ex && ex->wcss) || out.h_wcss_single;
+  const size_t hist_lds = (size_t)K * sizeof(uint32_t);
+  std::vector<size_t> it_events;  // event index triples per iteration
+  uint32_t gcells = 1;
+  for (uint32_t k = 0; k < D; ++k) gcells *= cand_grid_side(D);
+
   struct StreamScope {
     explicit StreamScope(hipStream_t hs) { tl_kt_stream = hs; }
     ~StreamScope() { tl_kt_stream = nullptr; }
@@ -863,7 +893,7 @@ int train_core(DeviceState &ds, hipStream_t s, const float *d_x, uint64_t n, uin
   uint32_t *slices_all = (cand || cand_first) ? as<uint32_t>(ds.cand_defer) : nullptr;
 
   // One Lloyd iteration t of the subspaces m0 .. m0+Mh-1 on stream hs.
-  auto iterate = [&](const Half &h, uint32_t t) -> int {
+  auto iterate = [&](const SubspaceGroup &h, uint32_t t) -> int {
     int st = TAC_OK;
     const uint32_t m0 = h.m0, Mh = h.Mh;
     hipStream_t hs = h.s;

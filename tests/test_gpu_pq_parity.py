@@ -37,16 +37,19 @@ def test_encode_matches_oracle(gpu, m, ksub):
     assert np.array_equal(got, ref), f"{np.count_nonzero(got != ref)} codes differ"
 
 
-@pytest.mark.parametrize("tol", [NEVER, 1e-3])
-def test_train_two_streams_match_one(gpu, monkeypatch, tol):
-    """The Lloyd loop runs the two halves of the subspaces on two streams
-    when m is even; one stream (TAC_GPU_TRAIN_STREAMS=1) gives the same bits,
-    also when subspaces of either half converge at different iterations."""
+@pytest.mark.parametrize("tol,kpp", [(NEVER, False), (1e-3, False), (1e-4, True)])
+def test_train_two_streams_match_one(gpu, monkeypatch, tol, kpp):
+    """The k-means++ seeding and the Lloyd loop run the two halves of the
+    subspaces on two streams when m is even; one stream
+    (TAC_GPU_TRAIN_STREAMS=1) gives the same bits, also when subspaces of
+    either half converge at different iterations."""
     w, x, init = synth.workload("chunk-117k", n=60000)
+    if kpp:
+        init = None
 
     def run():
-        return pq.train(x, w.dim, 0, m=w.m, ksub=w.ksub, max_iters=12, tol=tol,
-                        init_codebooks=init, trace=True)
+        return pq.train(x, w.dim, 0xa1b2c3d4 if kpp else 0, m=w.m, ksub=w.ksub, max_iters=12,
+                        tol=tol, init_codebooks=init, trace=True)
 
     two = run()
     monkeypatch.setenv("TAC_GPU_TRAIN_STREAMS", "1")
@@ -58,7 +61,7 @@ def test_train_two_streams_match_one(gpu, monkeypatch, tol):
     assert np.array_equal(_bits(two.stats.wcss), _bits(one.stats.wcss))
     if tol != NEVER:
         ref = orc.pq_train(x, w.dim, w.m, w.ksub, init=init, max_iters=12, tol=tol,
-                           n_threads=16)
+                           n_threads=16, seed=0xa1b2c3d4 if kpp else 0)
         assert np.array_equal(two.stats.iters_run, ref.iters_run)
         assert np.array_equal(_bits(two.codebooks), _bits(ref.codebooks))
 
