@@ -333,8 +333,8 @@ typedef struct tac_cluster_params {
  * length mismatch InvalidThresholds; kappa_total 0 BudgetTooSmall; then the
  * phases' errors, and the first failing token's kmeans error (RngError).
  * dim above 191 is TAC_ERR_UNSUPPORTED (rows are staged in LDS), as is a
- * token given more than 12,288 centroids, or a plan of 2^24 or more row
- * tiles, tokens with centroids or wcss chunks (one block each).
+ * plan of 2^24 or more row tiles, tokens with centroids or wcss chunks (one
+ * block each).
  */
 int tac_cluster_flat(const uint32_t *token_ids, uint64_t n_tokens, const float *vectors,
                      uint64_t vectors_len, uint32_t dim, const tac_cluster_params *params,

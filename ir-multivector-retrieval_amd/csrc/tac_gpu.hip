@@ -2323,7 +2323,6 @@ int tac_cluster_core(DeviceState &ds, hipStream_t s, const uint32_t *ids, uint64
 
   TacPlan pl;
   if ((st = tac_plan(freqs, offs, kappa, goff, prm.seed, rt, K, &pl))) return st;
-  if (pl.kmax > kTacMaxCodes) return TAC_ERR_UNSUPPORTED;
   // The Lloyd kernels launch one block of at most 256 work-items per tile,
   // problem, chunk or scan range; a dispatch's grid holds under 2^32.
   constexpr uint64_t kMaxUnits = (1ull << 32) / 256;
@@ -2397,7 +2396,12 @@ int tac_cluster_core(DeviceState &ds, hipStream_t s, const uint32_t *ids, uint64
   if (chunk_c > 64) chunk_c = 64;
   const size_t upd_lds = (rows_lds + dim) * sizeof(float);
   const size_t asg_lds = (rows_lds + (size_t)chunk_c * dim) * sizeof(float);
-  const size_t code_lds = (size_t)(pl.kmax ? pl.kmax : 1) * sizeof(uint32_t);
+  // hist / scatter: per-code counters up to kTacMaxCodes codes, the tile's
+  // codes beyond
+  const size_t code_lds =
+      (size_t)std::max<uint32_t>(std::min<uint32_t>(std::max<uint32_t>(pl.kmax, 1u), kTacMaxCodes),
+                                 rt) *
+      sizeof(uint32_t);
   const bool profile = g_profile;
   const double prep_ms =
       std::chrono::duration<double, std::milli>(std::chrono::steady_clock::now() - wall0).count();

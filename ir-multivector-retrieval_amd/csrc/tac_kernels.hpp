@@ -43,7 +43,9 @@ struct TacRange {
 
 constexpr uint32_t kTacScanTiles = 32;  // tiles per scan range
 
-constexpr uint32_t kTacMaxCodes = 12288;   // k per problem: LDS counters of hist/scatter
+// k per problem up to which hist and scatter keep per-code counters in LDS;
+// larger problems count and rank codes within the tile's rows instead.
+constexpr uint32_t kTacMaxCodes = 12288;
 constexpr uint32_t kTacLdsFloats = 12288;  // staged rows: rt * (dim + 1) <= this
 
 // Rows per tile (= threads of the tile kernels) for a dimension; 0 beyond the
@@ -644,6 +646,8 @@ __global__ __launch_bounds__(kTacMfmaThreads) void tac_assign_mfma_kernel(
     nfull = 0;
     exact = 0;
     hmax = 0;  // bits of the largest h of the problem (NaN: an untame centroid)
+    // the candidate queue holds 16-bit centroid indices
+    if (pr.k > 0xFFFFu) exact = 1;
   }
   tac_stage_rows(G, pr, tl.row0, R, 64, LD, xr);
   __syncthreads();
@@ -840,10 +844,27 @@ __global__ void tac_hist_kernel(const uint32_t* __restrict__ code,
                                 const TacProblem* __restrict__ probs,
                                 const TacTile* __restrict__ tiles,
                                 const uint32_t* __restrict__ done, uint32_t* __restrict__ hist) {
-  extern __shared__ uint32_t hcnt[];  // [k]
+  extern __shared__ uint32_t hcnt[];  // [k], or the tile's codes when k > kTacMaxCodes
   const TacTile tl = tiles[blockIdx.x];
   if (done[tl.prob]) return;
   const TacProblem pr = probs[tl.prob];
+  if (pr.k > kTacMaxCodes) {
+    // The tile's row of counters is cleared, then the first row of each code
+    // in the tile writes that code's count.
+    uint32_t* out = hist + pr.hist0 + (uint64_t)(blockIdx.x - pr.tile0) * pr.k;
+    const uint32_t i = tl.row0 + threadIdx.x;
+    hcnt[threadIdx.x] = i < pr.n ? code[pr.off + i] : 0xFFFFFFFFu;
+    for (uint32_t c = threadIdx.x; c < pr.k; c += blockDim.x) out[c] = 0;
+    __syncthreads();
+    const uint32_t cd = hcnt[threadIdx.x];
+    if (cd == 0xFFFFFFFFu) return;
+    for (uint32_t j = 0; j < threadIdx.x; ++j)
+      if (hcnt[j] == cd) return;
+    uint32_t cnt = 0;
+    for (uint32_t j = threadIdx.x; j < blockDim.x; ++j) cnt += hcnt[j] == cd ? 1u : 0u;
+    out[cd] = cnt;
+    return;
+  }
   for (uint32_t c = threadIdx.x; c < pr.k; c += blockDim.x) hcnt[c] = 0;
   __syncthreads();
   const uint32_t i = tl.row0 + threadIdx.x;
@@ -928,15 +949,25 @@ __global__ void tac_scatter_kernel(const uint32_t* __restrict__ code,
                                    const TacTile* __restrict__ tiles,
                                    const uint32_t* __restrict__ done,
                                    uint32_t* __restrict__ sorted) {
-  extern __shared__ uint32_t run[];  // [k]
+  extern __shared__ uint32_t run[];  // [k], or the tile's codes when k > kTacMaxCodes
   const TacTile tl = tiles[blockIdx.x];
   if (done[tl.prob]) return;
   const TacProblem pr = probs[tl.prob];
   const uint32_t* hm = hist + pr.hist0 + (uint64_t)(blockIdx.x - pr.tile0) * pr.k;
-  for (uint32_t c = threadIdx.x; c < pr.k; c += blockDim.x) run[c] = start[pr.goff + c] + hm[c];
   const uint32_t i = tl.row0 + threadIdx.x;
   const bool valid = i < pr.n;
   const uint32_t cd = valid ? code[pr.off + i] : 0u;
+  if (pr.k > kTacMaxCodes) {
+    // rank = earlier rows of the tile with the same code
+    run[threadIdx.x] = valid ? cd : 0xFFFFFFFFu;
+    __syncthreads();
+    if (!valid) return;
+    uint32_t rank = 0;
+    for (uint32_t j = 0; j < threadIdx.x; ++j) rank += run[j] == cd ? 1u : 0u;
+    sorted[pr.off + start[pr.goff + cd] + hm[cd] + rank] = pr.off + i;
+    return;
+  }
+  for (uint32_t c = threadIdx.x; c < pr.k; c += blockDim.x) run[c] = start[pr.goff + c] + hm[c];
   const uint32_t lane = threadIdx.x % kWave, wv = threadIdx.x / kWave;
   const uint64_t lt_mask = lane == 0 ? 0ull : (~0ull >> (64 - lane));
   const uint32_t nw = (blockDim.x + kWave - 1) / kWave;

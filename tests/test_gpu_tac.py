@@ -146,6 +146,18 @@ def test_matrix_core_assignment(gpu, monkeypatch, case):
     _check(ids, v.astype(np.float32), 64, 60, 21, mu=3, tau=5, epsilon=1, theta=1)
 
 
+def test_token_beyond_the_lds_code_counters(gpu):
+    """A token with 12,600 centroids (more than the 12,288 per-code LDS
+    counters of the grouping kernels) groups its rows by counting and
+    ranking codes within each tile instead; same bits as the oracle."""
+    rng = np.random.default_rng(31)
+    ids = np.zeros(40000, np.uint32)
+    ids[:500] = 1
+    v = rng.standard_normal((40000, 2)).astype(np.float32)
+    r = _check(ids, v, 2, 13100, 5, mu=3, tau=5, epsilon=1, theta=1, max_iters=3)
+    assert r.kappa_per_token[0] > 12288
+
+
 def test_device_resident_vectors(gpu):
     """tac_cluster_flat_device: the same token dump resident on the device
     gives the oracle's bits, as the host entry point does."""
