@@ -6,6 +6,7 @@ names and precedence (src/index/pq.zig:165-168, src/tac/kmeans.zig:73-76)
 before any device is touched, and that the synthetic workload generator is
 deterministic.
 """
+import ctypes
 import re
 import subprocess
 from pathlib import Path
@@ -96,6 +97,39 @@ def test_c_abi_validates_before_touching_a_device():
         assert f(None, 10, 32, 32, 2048, None, None, None) == 15
         assert f(None, 0, 32, 32, 256, None, None, None) == 0
         assert f(None, 10, 32, 32, 256, None, None, None) == 14
+
+
+def test_cluster_entries_validate_before_touching_a_device():
+    # tac_cluster_flat and its device-resident variant check in the reference's
+    # order (tac.zig:570-573) before any device is looked up: empty dump, zero
+    # dimension, length mismatch, zero budget, then NULL buffers.
+    L = tac_gpu.lib
+    p = _native.ClusterParams(kappa_total=8, mu=1, tau=1, epsilon=1, theta=1, max_iters=5,
+                              tol=1e-4, seed=0, n_threads=1)
+    zero = _native.ClusterParams(kappa_total=0, mu=1, tau=1, epsilon=1, theta=1, max_iters=5,
+                                 tol=1e-4, seed=0, n_threads=1)
+    ids = np.zeros(4, np.uint32)
+    fake = 0x1000  # never dereferenced: every case fails before a pointer is read
+    ref = ctypes.byref
+    for f in (L.tac_cluster_flat, L.tac_cluster_flat_device):
+        assert f(None, 4, None, 8, 2, None, None, None, None, 0, None, None) == \
+            errors.InvalidArgument.status
+        assert f(None, 0, None, 0, 2, ref(p), None, None, None, 0, None, None) == \
+            errors.EmptyTokenDump.status
+        assert f(None, 4, None, 0, 0, ref(p), None, None, None, 0, None, None) == \
+            errors.InvalidThresholds.status
+        assert f(None, 4, None, 7, 2, ref(p), None, None, None, 0, None, None) == \
+            errors.InvalidThresholds.status
+        assert f(None, 4, None, 8, 2, ref(zero), None, None, None, 0, None, None) == \
+            errors.BudgetTooSmall.status
+        assert f(None, 4, None, 8, 2, ref(p), None, None, None, 0, None, None) == \
+            errors.InvalidArgument.status
+        # one distinct token id needs a kappa_per_token buffer of at least one entry
+        nd = ctypes.c_uint64(0)
+        wcss = ctypes.c_float(0)
+        assert f(ids.ctypes.data, 4, fake, 8, 2, ref(p), fake, fake, fake, 0, ref(wcss),
+                 ref(nd)) == errors.BufferTooSmall.status
+        assert nd.value == 1
 
 
 @pytest.mark.skipif(device.device_count() > 0, reason="a HIP device is present")
