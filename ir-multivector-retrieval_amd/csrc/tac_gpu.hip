@@ -97,7 +97,7 @@ struct DeviceState {
   Buffer tac_v, tac_idx, tac_offs, tac_G, tac_spreads, tac_w, tac_e, tac_code, tac_sorted,
       tac_tsum, tac_hist, tac_counts, tac_start, tac_C, tac_pre, tac_fch, tac_st, tac_bad,
       tac_done, tac_iters, tac_wcss, tac_prev, tac_empties, tac_assign, tac_probs, tac_tiles,
-      tac_chl, tac_cprob, tac_inv, tac_rsum, tac_ranges, tac_h;
+      tac_chl, tac_cprob, tac_inv, tac_rsum, tac_ranges, tac_h, tac_ktiles;
   bool crc_tx_ready = false;
   // training's second stream (two halves of the subspaces) and its events
   hipStream_t aux_stream[1] = {};
@@ -1311,7 +1311,7 @@ int tac_gpu_release_workspace(void) {
                     &ds->tac_probs, &ds->tac_tiles, &ds->tac_chl, &ds->tac_cprob,
                     &ds->tac_inv,   &ds->tac_rsum, &ds->tac_ranges, &ds->cand_nbr,
                     &ds->cand_defer, &ds->cand_count, &ds->cand_anchor, &ds->cand_grid,
-                    &ds->kpp_src,   &ds->fold_order, &ds->tac_h};
+                    &ds->kpp_src,   &ds->fold_order, &ds->tac_h, &ds->tac_ktiles};
   ds->crc_tx_ready = false;
   for (Buffer *b : bufs) {
     if (b->ptr) HIP_TRY(hipFree(b->ptr));
@@ -2333,26 +2333,35 @@ int tac_cluster_core(DeviceState &ds, hipStream_t s, const uint32_t *ids, uint64
   const uint32_t NT = (uint32_t)pl.tiles.size(), NCH = (uint32_t)pl.chunks.size();
   std::vector<uint32_t> done0(P);
   for (uint32_t q = 0; q < P; ++q) done0[q] = pl.probs[q].degenerate;
+  // the tiles of the k-means++ rounds (problems in k-descending order, so
+  // round c covers the first tiles_upto[c])
+  std::vector<KppTile> ktiles(std::max<uint32_t>(pl.tiles_upto.empty() ? 0u : pl.tiles_upto[0], 1u));
+  for (uint32_t b = 0; b < (pl.tiles_upto.empty() ? 0u : pl.tiles_upto[0]); ++b) {
+    const TacTile &tl = pl.tiles[b];
+    const TacProblem &pq = pl.probs[tl.prob];
+    ktiles[b] = KppTile{tl.prob, tl.row0, pq.off, pq.n, pq.goff, pq.tile0, pq.ntiles, 0u};
+  }
   if ((st = upload_vec(ds, ds.tac_probs, pl.probs, s)) ||
       (st = upload_vec(ds, ds.tac_tiles, pl.tiles, s)) ||
+      (st = upload_vec(ds, ds.tac_ktiles, ktiles, s)) ||
       (st = upload_vec(ds, ds.tac_chl, pl.chunks, s)) ||
       (st = upload_vec(ds, ds.tac_ranges, pl.ranges, s)) ||
       (st = ensure(ds, ds.tac_rsum, (pl.rsum_total + 1) * sizeof(uint32_t))) ||
       (st = upload_vec(ds, ds.tac_cprob, pl.cprob, s)) ||
       (st = upload_vec(ds, ds.tac_done, done0, s)) ||
-      (st = ensure(ds, ds.tac_w, N * sizeof(float))) ||
+      (st = ensure(ds, ds.tac_w, 2 * N * sizeof(float))) ||
       (st = ensure(ds, ds.tac_e, N * sizeof(float))) ||
       (st = ensure(ds, ds.tac_code, N * sizeof(uint32_t))) ||
       (st = ensure(ds, ds.tac_sorted, N * sizeof(uint32_t))) ||
       (st = ensure(ds, ds.tac_assign, N * sizeof(uint32_t))) ||
-      (st = ensure(ds, ds.tac_tsum, (size_t)NT * sizeof(double))) ||
+      (st = ensure(ds, ds.tac_tsum, 2 * (size_t)NT * sizeof(double))) ||
       (st = ensure(ds, ds.tac_hist, (pl.hist_total + 1) * sizeof(uint32_t))) ||
       (st = ensure(ds, ds.tac_counts, K * sizeof(uint32_t))) ||
       (st = ensure(ds, ds.tac_start, K * sizeof(uint32_t))) ||
       (st = ensure(ds, ds.tac_C, K * dim * sizeof(float))) ||
       (st = ensure(ds, ds.tac_pre, (size_t)NCH * sizeof(double))) ||
       (st = ensure(ds, ds.tac_fch, (size_t)NCH * sizeof(FoldChunk))) ||
-      (st = ensure(ds, ds.tac_st, (size_t)P * sizeof(KppState))) ||
+      (st = ensure(ds, ds.tac_st, 2 * (size_t)P * sizeof(KppState))) ||
       (st = ensure(ds, ds.tac_bad, (size_t)P * sizeof(uint32_t))) ||
       (st = ensure(ds, ds.tac_iters, (size_t)P * sizeof(uint32_t))) ||
       (st = ensure(ds, ds.tac_wcss, (size_t)P * sizeof(float))) ||
@@ -2416,43 +2425,97 @@ int tac_cluster_core(DeviceState &ds, hipStream_t s, const uint32_t *ids, uint64
   tac_degenerate_kernel<<<P, 256, 0, s>>>(G, probs, P, C, code, wcss, dim);
   LAUNCH_TRY("tac_degenerate_kernel");
   // k-means++ seeding (kmeans.zig:106-136), round c for every problem with k > c
-  tac_kpp_init_kernel<<<(P + 63) / 64, 64, 0, s>>>(probs, P, kst, bad);
+  // states, weights and tile sums alternate between two halves by round
+  // parity; the states "after round -1" (the first draws) go to half 1
+  tac_kpp_init_kernel<<<(P + 63) / 64, 64, 0, s>>>(probs, P, kst + P, bad);
   LAUNCH_TRY("tac_kpp_init_kernel");
+  // TAC_GPU_KPP_EXACT=v: the draws of round c for problem q with (c + q) % v
+  // == 0 take the exact sequential evaluation (v = 1: every draw; the same
+  // picks, through the stall-and-replay path)
   const char *exact_env = getenv("TAC_GPU_KPP_EXACT");
-  const uint32_t exact_only = exact_env != nullptr && exact_env[0] == '1';
-  for (uint32_t c = 0; c < pl.kmax; ++c) {
+  const uint32_t exact_every = exact_env != nullptr ? (uint32_t)std::max(0, atoi(exact_env)) : 0u;
+  const size_t round_lds = dim == 64 ? ((size_t)rt * 64 + 64) * sizeof(float) : upd_lds;
+  const KppTile *ktl = as<KppTile>(ds.tac_ktiles);
+  auto round = [&](uint32_t c, uint32_t replay) -> int {
     const uint32_t T = pl.tiles_upto[c];
-    if (T == 0) break;
+    const uint32_t in = (c + 1) & 1u, out = c & 1u;
+    const KppRound rb{w + in * N,      w + out * N,  tsum + in * NT,
+                      tsum + out * NT, kst + in * P, kst + out * P};
     if (dim == 64)
-      tac_kpp_update_kernel<64><<<T, rt, upd_lds, s>>>(G, w, tsum, bad, kst, probs, tiles, C, c,
-                                                       dim);
+      tac_kpp_round_kernel<64><<<T, rt, round_lds, s>>>(G, rb, bad, ktl, C, c, dim, exact_every,
+                                                        replay);
     else if (dim == 128)
-      tac_kpp_update_kernel<128><<<T, rt, upd_lds, s>>>(G, w, tsum, bad, kst, probs, tiles, C,
-                                                        c, dim);
+      tac_kpp_round_kernel<128><<<T, rt, round_lds, s>>>(G, rb, bad, ktl, C, c, dim,
+                                                         exact_every, replay);
     else
-      tac_kpp_update_kernel<0><<<T, rt, upd_lds, s>>>(G, w, tsum, bad, kst, probs, tiles, C, c,
-                                                      dim);
-    LAUNCH_TRY("tac_kpp_update_kernel");
-    const uint32_t P2 = c + 1 < pl.kmax ? pl.probs_upto[c + 1] : 0;
-    if (P2 == 0) continue;
-    tac_kpp_select_kernel<<<P2, rt, 0, s>>>(w, tsum, bad, kst, probs, exact_only);
-    LAUNCH_TRY("tac_kpp_select_kernel");
-    tac_kpp_fallback_kernel<<<P2, kKppFallbackThreads, 0, s>>>(w, kst, probs, pre, fch);
-    LAUNCH_TRY("tac_kpp_fallback_kernel");
+      tac_kpp_round_kernel<0><<<T, rt, round_lds, s>>>(G, rb, bad, ktl, C, c, dim, exact_every,
+                                                       replay);
+    LAUNCH_TRY("tac_kpp_round_kernel");
+    return TAC_OK;
+  };
+  auto exact_round = [&](uint32_t c) -> int {
+    const uint32_t Pc = pl.probs_upto[c];
+    const uint32_t in = (c + 1) & 1u, out = c & 1u;
+    const KppRound rb{w + in * N,      w + out * N,  tsum + in * NT,
+                      tsum + out * NT, kst + in * P, kst + out * P};
+    const size_t ex_lds = (size_t)dim * sizeof(float);
+    if (dim == 64)
+      tac_kpp_exact_round_kernel<64><<<Pc, kKppFallbackThreads, ex_lds, s>>>(
+          G, rb, bad, probs, C, pre, fch, c, dim, rt);
+    else if (dim == 128)
+      tac_kpp_exact_round_kernel<128><<<Pc, kKppFallbackThreads, ex_lds, s>>>(
+          G, rb, bad, probs, C, pre, fch, c, dim, rt);
+    else
+      tac_kpp_exact_round_kernel<0><<<Pc, kKppFallbackThreads, ex_lds, s>>>(
+          G, rb, bad, probs, C, pre, fch, c, dim, rt);
+    LAUNCH_TRY("tac_kpp_exact_round_kernel");
+    return TAC_OK;
+  };
+  // a problem's state after its last round k - 1 sits in half (k - 1) & 1;
+  // returns the earliest pending round (kmax if none)
+  std::vector<KppState> hst(2 * (size_t)P);
+  auto final_states = [&](uint32_t *pending) -> int {
+    HIP_TRY(hipMemcpyAsync(hst.data(), kst, 2 * (size_t)P * sizeof(KppState),
+                           hipMemcpyDeviceToHost, s));
+    HIP_TRY(hipStreamSynchronize(s));
+    *pending = pl.kmax;
+    for (uint32_t q = 0; q < P; ++q) {
+      const TacProblem &pq = pl.probs[q];
+      if (pq.degenerate || pq.k == 0) continue;
+      const KppState &hq = hst[(size_t)((pq.k - 1) & 1u) * P + q];
+      if (!hq.err && hq.fallback) *pending = std::min(*pending, hq.pad);
+    }
+    return TAC_OK;
+  };
+  for (uint32_t c = 0; c < pl.kmax && pl.tiles_upto[c] > 0; ++c)
+    if ((st = round(c, 0))) return st;
+  uint32_t pending;
+  if ((st = final_states(&pending))) return st;
+  if (pending < pl.kmax) {
+    // replay the stalled problems from their earliest pending draw
+    for (uint32_t c = pending; c < pl.kmax; ++c) {
+      if ((st = exact_round(c))) return st;
+      if (c + 1 < pl.kmax && pl.tiles_upto[c + 1] > 0 && (st = round(c + 1, 1))) return st;
+    }
+    if ((st = final_states(&pending))) return st;
+    if (pending < pl.kmax) {
+      g_last_error = "k-means++ replay left a draw pending";
+      return TAC_ERR_HIP;
+    }
   }
   {
-    std::vector<KppState> h(P);
-    HIP_TRY(hipMemcpyAsync(h.data(), kst, (size_t)P * sizeof(KppState), hipMemcpyDeviceToHost,
-                           s));
-    HIP_TRY(hipStreamSynchronize(s));
     // the reference fits tokens in id order and stops at the first error
     uint32_t first_tok = 0xFFFFFFFFu;
     int first_err = 0;
-    for (uint32_t q = 0; q < P; ++q)
-      if (h[q].err && pl.token[q] < first_tok) {
+    for (uint32_t q = 0; q < P; ++q) {
+      const TacProblem &pq = pl.probs[q];
+      if (pq.degenerate || pq.k == 0) continue;
+      const KppState &hq = hst[(size_t)((pq.k - 1) & 1u) * P + q];
+      if (hq.err && pl.token[q] < first_tok) {
         first_tok = pl.token[q];
-        first_err = h[q].err;
+        first_err = hq.err;
       }
+    }
     if (first_err) return first_err;
   }
   if (profile) HIP_TRY(hipEventRecord(ev1, s));

@@ -308,8 +308,51 @@ __device__ __forceinline__ void tac_stage_rows(const float* __restrict__ G, cons
 
 // ---------------------------------------------------------------------------
 // k-means++ (kmeans.zig:106-136) per problem, with the PRNG seeded from
-// p.seed ^ token id.
+// p.seed ^ token id.  One launch per round.
+//
+// Round c runs over the tiles of the problems with k > c (a prefix of the
+// tile list).  For c >= 1 each block first draws centroid c from the weights
+// the previous round left (weightedSample, rng.zig:57-82); then it writes
+// centroid c, sets w = l2sq to it (round 0) or min(w, l2sq) on strict <
+// (kmeans.zig:129-135), validates the weights (rng.zig:62) and leaves one f64
+// sum per tile.  Every block of a problem makes the same draw from the same
+// inputs in the same order, so no block waits for another: the weights, tile
+// sums and states of round c - 1 are read from one half of two buffers while
+// round c writes the other (KppRound).  The sums are order-free; a candidate
+// is kept only when the draw clears the error bands (kpp_decides).  Otherwise
+// (rare: the draw lands within rounding of a boundary) the problem stalls:
+// its draw of round c stays pending (fallback raised, pad = c), its weights
+// and tile sums stay as round c - 1 left them, and later rounds only forward
+// its state.  After the last round the host replays the stalled problems from
+// the earliest pending round: tac_kpp_exact_round_kernel resolves a pending
+// draw exactly and makes that round's update, then this kernel runs the next
+// round with `replay` set, where only replaying problems (pad ==
+// kKppReplaying) act.  Non-finite weights of round c stamp bad[p] with c
+// (atomicMin); a draw fails with NonFinite when a stamp of an earlier round
+// is present, so a stamp made while a round runs never changes its draws.
 // ---------------------------------------------------------------------------
+constexpr uint32_t kKppNoBad = 0xFFFFFFFFu;
+// KppState.pad of a problem: 0 in the first pass; the round of its pending
+// draw while fallback is raised; kKppReplaying once the exact draw has
+// resolved it, for the rest of its rounds.
+constexpr uint32_t kKppReplaying = 0xFFFFFFFFu;
+
+typedef float tac_floatx4 __attribute__((ext_vector_type(4)));
+
+// What a round's block needs of its tile and problem, in one load.
+struct KppTile {
+  uint32_t prob, row0, off, n, goff, tile0, ntiles, pad;
+};
+
+struct KppRound {
+  const float* w_in;      // weights after round c - 1
+  float* w_out;           // weights after round c
+  const double* tsum_in;  // tile sums after round c - 1 (one per tile of the list)
+  double* tsum_out;
+  const KppState* st_in;  // states after the draw of round c - 1 (one per problem)
+  KppState* st_out;
+};
+
 __global__ void tac_kpp_init_kernel(const TacProblem* __restrict__ probs, uint32_t P,
                                     KppState* __restrict__ st, uint32_t* __restrict__ bad) {
   const uint32_t p = blockIdx.x * blockDim.x + threadIdx.x;
@@ -323,181 +366,295 @@ __global__ void tac_kpp_init_kernel(const TacProblem* __restrict__ probs, uint32
   S.err = 0;
   S.pad = 0;
   st[p] = S;
-  bad[p] = 0;
+  bad[p] = kKppNoBad;
 }
 
-// Round c over the tiles of problems with k > c (a prefix of the tile list):
-// centroid c = the chosen row; w = l2sq to it (round 0) or min(w, l2sq) on
-// strict < (kmeans.zig:129-135); weights validated (rng.zig:62); one f64
-// partial sum per tile.
+// Inclusive and exclusive prefix of one f64 per thread over a block of
+// rt <= 128 threads, in a fixed order (the exclusive value of thread t + 1 is
+// the inclusive value of thread t, bit for bit).  Returns the block total.
+// Ends with the block barrier that makes ws reusable only after the caller's
+// next barrier.
+__device__ inline double kpp_block_scan(double x, uint32_t rt, double* ws, double* incl,
+                                        double* excl) {
+  const uint32_t lane = threadIdx.x % kWave, wv = threadIdx.x / kWave;
+  double in = x;
+  for (int off = 1; off < kWave; off <<= 1) {
+    const double o = __shfl_up(in, off, kWave);
+    if (lane >= (uint32_t)off) in += o;
+  }
+  const double up = __shfl_up(in, 1, kWave);
+  if (lane == kWave - 1 || threadIdx.x == rt - 1) ws[wv] = in;
+  __syncthreads();
+  double before = 0.0;
+  for (uint32_t q = 0; q < wv; ++q) before += ws[q];
+  double total = 0.0;
+  for (uint32_t q = 0; q < (rt + kWave - 1) / kWave; ++q) total += ws[q];
+  *incl = before + in;
+  *excl = lane == 0 ? before : before + up;
+  return total;
+}
+
+// Row staging for 64-float rows: coalesced 16-byte loads, stored in LDS
+// without padding with the 16-byte chunks of row r permuted by r & 15, so
+// that a thread reading its own row chunk by chunk hits distinct banks.
+__device__ __forceinline__ uint32_t tac_swz64(uint32_t row, uint32_t chunk) {
+  return row * 64u + ((chunk ^ (row & 15u)) << 2);
+}
+
 template <int DIMC>
-__global__ void tac_kpp_update_kernel(const float* __restrict__ G, float* __restrict__ w,
-                                      double* __restrict__ tsum, uint32_t* __restrict__ bad,
-                                      const KppState* __restrict__ st,
-                                      const TacProblem* __restrict__ probs,
-                                      const TacTile* __restrict__ tiles, float* __restrict__ C,
-                                      uint32_t c, uint32_t dim_rt) {
+__global__ void tac_kpp_round_kernel(const float* __restrict__ G, KppRound b,
+                                     uint32_t* __restrict__ bad,
+                                     const KppTile* __restrict__ ktiles, float* __restrict__ C,
+                                     uint32_t c, uint32_t dim_rt, uint32_t exact_every,
+                                     uint32_t replay) {
   const uint32_t dim = DIMC ? (uint32_t)DIMC : dim_rt;
   extern __shared__ __attribute__((aligned(16))) float tlds[];
-  const uint32_t rt = blockDim.x, ld = dim + 1;
-  float* xr = tlds;             // [rt][ld]
+  const uint32_t rt = blockDim.x, t = threadIdx.x;
+  const uint32_t ld = DIMC == 64 ? 64u : dim + 1;
+  float* xr = tlds;             // rt rows
   float* crow = tlds + rt * ld;  // [dim]
-  __shared__ double part[4];
-  const TacTile tl = tiles[blockIdx.x];
-  const TacProblem pr = probs[tl.prob];
-  if (st[tl.prob].err) return;
-  const uint32_t chosen = st[tl.prob].chosen;
-  for (uint32_t d = threadIdx.x; d < dim; d += rt) {
-    const float v = G[((uint64_t)pr.off + chosen) * dim + d];
+  __shared__ double ws_a[2], ws_b[2], wsum[2], s_before;
+  __shared__ uint32_t s_thr, s_tile, s_first, s_chosen;
+  const KppTile tl = ktiles[blockIdx.x];
+  const uint32_t p = tl.prob;
+  const KppTile& pr = tl;
+  const uint32_t i = tl.row0 + t;
+  const bool row_ok = i < pr.n;
+  const float old = (c > 0 && row_ok) ? b.w_in[pr.off + i] : 0.0f;
+  // stage the tile's rows (independent of the draw)
+  if (DIMC == 64) {
+    const uint32_t rows = pr.n - tl.row0 < rt ? pr.n - tl.row0 : rt;
+    const tac_floatx4* src =
+        reinterpret_cast<const tac_floatx4*>(G + ((uint64_t)pr.off + tl.row0) * 64);
+    const uint32_t nq = rows * 16u;
+    tac_floatx4 v[16];
+#pragma unroll
+    for (int j = 0; j < 16; ++j) {
+      const uint32_t q = t + (uint32_t)j * rt;
+      v[j] = q < nq ? src[q] : tac_floatx4{0.0f, 0.0f, 0.0f, 0.0f};
+    }
+#pragma unroll
+    for (int j = 0; j < 16; ++j) {
+      const uint32_t q = t + (uint32_t)j * rt;
+      if (q < nq) *reinterpret_cast<tac_floatx4*>(xr + tac_swz64(q >> 4, q & 15u)) = v[j];
+    }
+  } else {
+    const uint32_t rows = pr.n - tl.row0 < rt ? pr.n - tl.row0 : rt;
+    const float* src = G + ((uint64_t)pr.off + tl.row0) * dim;
+    for (uint32_t f = t; f < rows * dim; f += rt) xr[(f / dim) * ld + f % dim] = src[f];
+  }
+  KppState S = b.st_in[p];
+  if (replay && S.pad != kKppReplaying) return;  // uniform; writes nothing
+  if (t == 0) {
+    s_thr = 0xFFFFFFFFu;
+    s_first = 0xFFFFFFFFu;
+    s_tile = pr.ntiles;
+    s_chosen = S.chosen;
+  }
+  // a problem whose draw is pending (an earlier round's) only forwards its state
+  const bool draws = c > 0 && !S.err && !S.fallback;
+  if (draws) {
+    if (bad[p] < c) {
+      S.err = 9;  // NonFinite
+    } else {
+      // total and the tile holding the draw: thread t sums a contiguous run
+      // of the problem's tile sums
+      const uint32_t NB = pr.ntiles;
+      const double* tb = b.tsum_in + pr.tile0;
+      const uint32_t per = (NB + rt - 1) / rt;
+      const uint32_t b0 = t * per < NB ? t * per : NB;
+      const uint32_t b1 = b0 + per < NB ? b0 + per : NB;
+      constexpr uint32_t kRegTiles = 16;  // runs up to this long stay in registers
+      const bool in_regs = per <= kRegTiles;
+      double tv[kRegTiles];
+      double part = 0.0;
+      if (in_regs) {
+#pragma unroll
+        for (uint32_t j = 0; j < kRegTiles; ++j) tv[j] = b0 + j < b1 ? tb[b0 + j] : 0.0;
+#pragma unroll
+        for (uint32_t j = 0; j < kRegTiles; ++j)
+          if (b0 + j < b1) part += tv[j];
+      } else {
+        for (uint32_t q = b0; q < b1; ++q) part += tb[q];
+      }
+      double incl, excl;
+      const double total = kpp_block_scan(part, rt, ws_a, &incl, &excl);
+      if (!(total > 0.0)) {
+        S.err = 10;  // AllZero
+      } else {
+        const double r = kpp_float64(S.s);
+        S.r = r;
+        const double u = r * total;
+        if (b0 < b1 && u < incl) atomicMin(&s_thr, t);
+        __syncthreads();
+        if (t == s_thr) {
+          double run = excl;
+          if (in_regs) {
+            bool found = false;
+#pragma unroll
+            for (uint32_t j = 0; j < kRegTiles; ++j) {
+              if (!found && b0 + j < b1) {
+                const double nx = run + tv[j];
+                if (u < nx) {
+                  found = true;
+                  s_tile = b0 + j;
+                  s_before = run;
+                }
+                run = nx;
+              }
+            }
+          } else {
+            for (uint32_t q = b0; q < b1; ++q) {
+              const double nx = run + tb[q];
+              if (u < nx) {
+                s_tile = q;
+                s_before = run;
+                break;
+              }
+              run = nx;
+            }
+          }
+        }
+        __syncthreads();
+        if (s_tile == NB || (exact_every && (c + p) % exact_every == 0)) {
+          S.fallback = 1;  // u at or beyond the total: the tail rule decides
+        } else {
+          // one weight per thread inside the candidate tile (tiles hold rt rows)
+          const uint64_t ci = (uint64_t)s_tile * rt + t;
+          const double wv = ci < pr.n ? (double)b.w_in[pr.off + ci] : 0.0;
+          double wi, we;
+          kpp_block_scan(wv, rt, ws_b, &wi, &we);
+          const double pi = s_before + wi, pprev = s_before + we;
+          if (ci < pr.n && u < pi) atomicMin(&s_first, t);
+          __syncthreads();
+          if (s_first == 0xFFFFFFFFu) {
+            S.fallback = 1;
+          } else {
+            if (t == s_first)
+              s_chosen = kpp_decides(r, total, pr.n, ci, pprev, pi) ? (uint32_t)ci : 0xFFFFFFFFu;
+            __syncthreads();
+            if (s_chosen == 0xFFFFFFFFu)
+              S.fallback = 1;
+            else
+              S.chosen = s_chosen;
+          }
+        }
+      }
+    }
+  }
+  if (draws && S.fallback) S.pad = c;  // the draw of round c is pending
+  if (t == 0 && tl.row0 == 0) b.st_out[p] = S;  // every round forwards the state
+  if (S.err || S.fallback) return;               // uniform over the block
+  const float* cg = G + ((uint64_t)pr.off + S.chosen) * dim;
+  for (uint32_t d = t; d < dim; d += rt) {
+    const float v = cg[d];
     crow[d] = v;
     if (tl.row0 == 0) C[((uint64_t)pr.goff + c) * dim + d] = v;
   }
-  tac_stage_rows(G, pr, tl.row0, rt, dim, ld, xr);
   __syncthreads();
-  const uint32_t i = tl.row0 + threadIdx.x;
   double acc = 0.0;
   bool invalid = false;
-  if (i < pr.n) {
-    const float d = tac_l2sq<DIMC>(xr + threadIdx.x * ld, crow, dim);
-    float* wi = w + pr.off + i;
-    float v = d;
-    if (c > 0) {
-      const float old = *wi;
-      v = d < old ? d : old;
-      if (d < old) *wi = d;
+  if (row_ok) {
+    float d;
+    if (DIMC == 64) {
+      float a0 = 0.0f, a1 = 0.0f, a2 = 0.0f, a3 = 0.0f;
+#pragma unroll
+      for (uint32_t j = 0; j < 16; ++j) {
+        const tac_floatx4 x = *reinterpret_cast<const tac_floatx4*>(xr + tac_swz64(t, j));
+        const tac_floatx4 y = *reinterpret_cast<const tac_floatx4*>(crow + 4 * j);
+        const float t0 = x.x - y.x, t1 = x.y - y.y, t2 = x.z - y.z, t3 = x.w - y.w;
+        a0 = a0 + t0 * t0;
+        a1 = a1 + t1 * t1;
+        a2 = a2 + t2 * t2;
+        a3 = a3 + t3 * t3;
+      }
+      d = ((a0 + a1) + a2) + a3;  // tac_l2sq<64>'s order
     } else {
-      *wi = d;
+      d = tac_l2sq<DIMC>(xr + t * ld, crow, dim);
     }
+    const float v = c > 0 ? (d < old ? d : old) : d;
+    b.w_out[pr.off + i] = v;
     invalid = !(v >= 0.0f && v <= 3.402823466e38f);
     acc = (double)v;
   }
   for (int off = 32; off > 0; off >>= 1) acc += __shfl_down(acc, off, 64);
-  if (threadIdx.x % 64 == 0) part[threadIdx.x / 64] = acc;
-  if (__any(invalid) && threadIdx.x % 64 == 0) atomicOr(&bad[tl.prob], 1u);
+  if (t % 64 == 0) wsum[t / 64] = acc;
+  if (__any(invalid) && t % 64 == 0) atomicMin(&bad[p], c);
   __syncthreads();
-  if (threadIdx.x == 0) {
-    double t = 0.0;
-    for (uint32_t q = 0; q < (rt + 63) / 64; ++q) t += part[q];
-    tsum[blockIdx.x] = t;
+  if (t == 0) {
+    double s = 0.0;
+    for (uint32_t q = 0; q < (rt + 63) / 64; ++q) s += wsum[q];
+    b.tsum_out[blockIdx.x] = s;
   }
 }
 
-// Draw for round c + 1, one block of rt threads per problem with k > c + 1
-// (a prefix of the problem list): the same decision as kpp_select_kernel,
-// over the problem's tile sums and then one weight per thread inside the
-// candidate tile.  Order-free sums; the candidate is kept only when the draw
-// clears the error bands (kpp_decides), otherwise `fallback` is raised.
-__global__ __launch_bounds__(128) void tac_kpp_select_kernel(
-    const float* __restrict__ w, const double* __restrict__ tsum, uint32_t* __restrict__ bad,
-    KppState* __restrict__ st, const TacProblem* __restrict__ probs, uint32_t exact_only) {
-  __shared__ double s_before, s_total, s_u, s_r, carry;
-  __shared__ uint32_t s_tile, s_first, s_stop;
-  __shared__ double wsum[2];
-  const uint32_t p = blockIdx.x, rt = blockDim.x;
+// The exact sequential weightedSample for problems whose draw in round c is
+// pending (kpp_fallback_block over the weights after round c - 1; the wcss
+// chunk scratch of the problem serves as its chunk scratch), followed by
+// round c's update of that problem by this one block, which marks the problem
+// as replaying.  Only launched in the replay pass; blocks of problems without
+// a draw pending in round c return at once.
+template <int DIMC>
+__global__ __launch_bounds__(kKppFallbackThreads) void tac_kpp_exact_round_kernel(
+    const float* __restrict__ G, KppRound b, uint32_t* __restrict__ bad,
+    const TacProblem* __restrict__ probs, float* __restrict__ C, double* __restrict__ pre,
+    FoldChunk* __restrict__ fchunks, uint32_t c, uint32_t dim_rt, uint32_t rt) {
+  const uint32_t dim = DIMC ? (uint32_t)DIMC : dim_rt;
+  extern __shared__ __attribute__((aligned(16))) float crow[];  // [dim]
+  __shared__ double wpart[kKppFallbackThreads / kWave];
+  __shared__ KppState S;  // the draw works on this copy; thread 0 writes it back
+  const uint32_t p = blockIdx.x, t = threadIdx.x, lane = t % kWave, wv = t / kWave;
+  if (t == 0) S = b.st_out[p];
+  __syncthreads();
+  if (S.err || !S.fallback || S.pad != c) return;  // uniform over the block
   const TacProblem pr = probs[p];
-  KppState& S = st[p];
-  const uint32_t lane = threadIdx.x % 64, wv = threadIdx.x / 64, nw = (rt + 63) / 64;
-  const double* bm = tsum + pr.tile0;
-  const uint32_t NB = pr.ntiles;
-  if (threadIdx.x == 0) {
-    s_stop = 1;
-    s_first = 0xFFFFFFFFu;
-    s_tile = NB;
-    carry = 0.0;
-    if (!S.err) {
-      S.fallback = 0;
-      if (bad[p])
-        S.err = 9;  // NonFinite
-      else
-        s_stop = 0;
-    }
+  kpp_fallback_block(b.w_in + pr.off, pr.n, S, pre + pr.chunk0, fchunks + pr.chunk0,
+                     pr.nchunks);
+  __syncthreads();
+  const uint32_t chosen = S.chosen;
+  if (t == 0) {
+    S.pad = kKppReplaying;
+    b.st_out[p] = S;
+  }
+  const float* cg = G + ((uint64_t)pr.off + chosen) * dim;
+  for (uint32_t d = t; d < dim; d += kKppFallbackThreads) {
+    const float v = cg[d];
+    crow[d] = v;
+    C[((uint64_t)pr.goff + c) * dim + d] = v;
   }
   __syncthreads();
-  if (s_stop) return;
-  double part = 0.0;
-  for (uint32_t b = threadIdx.x; b < NB; b += rt) part += bm[b];
-  for (int off = 32; off > 0; off >>= 1) part += __shfl_down(part, off, 64);
-  if (lane == 0) wsum[wv] = part;
-  __syncthreads();
-  if (threadIdx.x == 0) {
-    double tot = 0.0;
-    for (uint32_t q = 0; q < nw; ++q) tot += wsum[q];
-    if (!(tot > 0.0)) {
-      S.err = 10;  // AllZero
-      s_stop = 1;
+  const uint32_t per_pass = kKppFallbackThreads / rt;  // rt divides the block
+  for (uint32_t i0 = 0; i0 < pr.n; i0 += kKppFallbackThreads) {
+    const uint32_t i = i0 + t;
+    double acc = 0.0;
+    bool invalid = false;
+    if (i < pr.n) {
+      const float d = tac_l2sq<DIMC>(G + ((uint64_t)pr.off + i) * dim, crow, dim);
+      const float old = b.w_in[pr.off + i];
+      const float v = d < old ? d : old;  // rounds with a draw have c >= 1
+      b.w_out[pr.off + i] = v;
+      invalid = !(v >= 0.0f && v <= 3.402823466e38f);
+      acc = (double)v;
+    }
+    if (__any(invalid) && lane == 0) atomicMin(&bad[p], c);
+    const uint32_t seg = rt < kWave ? rt : kWave;
+    for (uint32_t off = seg / 2; off > 0; off >>= 1) acc += __shfl_down(acc, off, kWave);
+    const uint32_t tile0 = i0 / rt;
+    if (rt < kWave) {
+      const uint32_t tile = tile0 + t / rt;
+      if (t % rt == 0 && tile < pr.ntiles) b.tsum_out[pr.tile0 + tile] = acc;
     } else {
-      S.r = kpp_float64(S.s);
-      s_r = S.r;
-      s_total = tot;
-      s_u = S.r * tot;
+      if (lane == 0) wpart[wv] = acc;
+      __syncthreads();
+      const uint32_t wpt = rt / kWave;
+      if (t < per_pass && tile0 + t < pr.ntiles) {
+        double s = 0.0;
+        for (uint32_t q = 0; q < wpt; ++q) s += wpart[t * wpt + q];
+        b.tsum_out[pr.tile0 + tile0 + t] = s;
+      }
+      __syncthreads();
     }
   }
-  __syncthreads();
-  if (s_stop) return;
-  const double ud = s_u;
-  for (uint32_t b0 = 0; b0 < NB; b0 += rt) {
-    const uint32_t b = b0 + threadIdx.x;
-    const double x = b < NB ? bm[b] : 0.0;
-    double incl = x;
-    for (int off = 1; off < 64; off <<= 1) {
-      const double o = __shfl_up(incl, off, 64);
-      if (lane >= (uint32_t)off) incl += o;
-    }
-    if (lane == 63 || threadIdx.x == rt - 1) wsum[wv] = incl;
-    __syncthreads();
-    double before = carry;
-    for (uint32_t q = 0; q < wv; ++q) before += wsum[q];
-    if (b < NB && ud < before + incl) atomicMin(&s_tile, b);
-    __syncthreads();
-    if (b == s_tile) s_before = before + (incl - x);
-    if (threadIdx.x == rt - 1) carry = before + incl;
-    __syncthreads();
-    if (s_tile != NB) break;
-  }
-  if (s_tile == NB || exact_only) {
-    if (threadIdx.x == 0) S.fallback = 1;  // u at or beyond the total: the tail rule decides
-    return;
-  }
-  const double r = s_r;
-  const uint64_t i = (uint64_t)s_tile * rt + threadIdx.x;  // tiles hold rt rows each
-  const double v = i < pr.n ? (double)w[pr.off + i] : 0.0;
-  double incl = v;
-  for (int off = 1; off < 64; off <<= 1) {
-    const double o = __shfl_up(incl, off, 64);
-    if (lane >= (uint32_t)off) incl += o;
-  }
-  if (lane == 63 || threadIdx.x == rt - 1) wsum[wv] = incl;
-  __syncthreads();
-  double base = s_before;
-  for (uint32_t q = 0; q < wv; ++q) base += wsum[q];
-  base += incl - v;  // exclusive prefix before weight i
-  const double u = r * s_total;
-  const double pi = base + v;
-  if (i < pr.n && u < pi) atomicMin(&s_first, threadIdx.x);
-  __syncthreads();
-  if (s_first == 0xFFFFFFFFu) {
-    if (threadIdx.x == 0) S.fallback = 1;
-    return;
-  }
-  if (threadIdx.x == s_first) {
-    if (kpp_decides(r, s_total, pr.n, i, base, pi))
-      S.chosen = (uint32_t)i;
-    else
-      S.fallback = 1;
-  }
-}
-
-// The exact sequential weightedSample for problems whose draw was
-// inconclusive (kpp_fallback_block over the problem's weights; the wcss
-// chunk scratch of the problem serves as its chunk scratch).
-__global__ __launch_bounds__(kKppFallbackThreads) void tac_kpp_fallback_kernel(
-    const float* __restrict__ w, KppState* __restrict__ st, const TacProblem* __restrict__ probs,
-    double* __restrict__ pre, FoldChunk* __restrict__ fchunks) {
-  const uint32_t p = blockIdx.x;
-  KppState& S = st[p];
-  if (S.err || !S.fallback) return;
-  const TacProblem pr = probs[p];
-  kpp_fallback_block(w + pr.off, pr.n, S, pre + pr.chunk0, fchunks + pr.chunk0, pr.nchunks);
 }
 
 // ---------------------------------------------------------------------------
@@ -621,7 +778,6 @@ __global__ __launch_bounds__(256) void tac_cnorm_kernel(const float* __restrict_
   h[c] = tame ? 0.5f * n : __builtin_nanf("");
 }
 
-typedef float tac_floatx4 __attribute__((ext_vector_type(4)));
 
 __global__ __launch_bounds__(kTacMfmaThreads) void tac_assign_mfma_kernel(
     const float* __restrict__ G, const float* __restrict__ C, const float* __restrict__ h,

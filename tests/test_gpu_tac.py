@@ -97,8 +97,14 @@ def test_thread_grouping_and_exact_draws(gpu, monkeypatch):
     kap = _feasible_kappa(ids)
     for nt in (3, 10):
         _check(ids, v, 64, kap, 21, n_threads=nt)
-    monkeypatch.setenv("TAC_GPU_KPP_EXACT", "1")
-    _check(ids, v, 64, kap, 21)
+    # Draws sent to the exact sequential evaluation: every draw ("1"), and
+    # the draws of round c of problem q with (c + q) % 7 == 0 ("7"), so that
+    # tokens stall at different rounds and are replayed beside tokens that
+    # finished, some stalling again while they replay.
+    for every in ("1", "7"):
+        monkeypatch.setenv("TAC_GPU_KPP_EXACT", every)
+        _check(ids, v, 64, kap, 21)
+        _check(ids, v, 64, kap, 21, n_threads=3)
 
 
 def test_degenerate_and_tiny_tokens(gpu):
