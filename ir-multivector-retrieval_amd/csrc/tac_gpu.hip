@@ -2434,7 +2434,9 @@ int tac_cluster_core(DeviceState &ds, hipStream_t s, const uint32_t *ids, uint64
   // picks, through the stall-and-replay path)
   const char *exact_env = getenv("TAC_GPU_KPP_EXACT");
   const uint32_t exact_every = exact_env != nullptr ? (uint32_t)std::max(0, atoi(exact_env)) : 0u;
-  const size_t round_lds = dim == 64 ? ((size_t)rt * 64 + 64) * sizeof(float) : upd_lds;
+  // dim 64: one 128-row tile per block of 128 threads, staged 64 rows at a time
+  if (dim == 64 && rt != 128) return TAC_ERR_UNSUPPORTED;
+  const size_t round_lds = dim == 64 ? (64 * 64 + 64) * sizeof(float) : upd_lds;
   const KppTile *ktl = as<KppTile>(ds.tac_ktiles);
   auto round = [&](uint32_t c, uint32_t replay) -> int {
     const uint32_t T = pl.tiles_upto[c];

@@ -402,17 +402,18 @@ __device__ __forceinline__ uint32_t tac_swz64(uint32_t row, uint32_t chunk) {
 }
 
 template <int DIMC>
-__global__ void tac_kpp_round_kernel(const float* __restrict__ G, KppRound b,
-                                     uint32_t* __restrict__ bad,
-                                     const KppTile* __restrict__ ktiles, float* __restrict__ C,
-                                     uint32_t c, uint32_t dim_rt, uint32_t exact_every,
-                                     uint32_t replay) {
+__global__ __launch_bounds__(128) void tac_kpp_round_kernel(
+    const float* __restrict__ G, KppRound b, uint32_t* __restrict__ bad,
+    const KppTile* __restrict__ ktiles, float* __restrict__ C, uint32_t c, uint32_t dim_rt,
+    uint32_t exact_every, uint32_t replay) {
   const uint32_t dim = DIMC ? (uint32_t)DIMC : dim_rt;
   extern __shared__ __attribute__((aligned(16))) float tlds[];
   const uint32_t rt = blockDim.x, t = threadIdx.x;
   const uint32_t ld = DIMC == 64 ? 64u : dim + 1;
-  float* xr = tlds;             // rt rows
-  float* crow = tlds + rt * ld;  // [dim]
+  // 64-float rows pass through LDS 64 at a time (the block has 128 threads,
+  // one row each); other dims stage the whole tile
+  float* xr = tlds;
+  float* crow = tlds + (DIMC == 64 ? 64u * 64u : rt * ld);  // [dim]
   __shared__ double ws_a[2], ws_b[2], wsum[2], s_before;
   __shared__ uint32_t s_thr, s_tile, s_first, s_chosen;
   const KppTile tl = ktiles[blockIdx.x];
@@ -420,22 +421,40 @@ __global__ void tac_kpp_round_kernel(const float* __restrict__ G, KppRound b,
   const KppTile& pr = tl;
   const uint32_t i = tl.row0 + t;
   const bool row_ok = i < pr.n;
+  // Issue every load that does not wait on the draw first: the state, the
+  // run of tile sums this thread adds up, the weights and the tile's rows.
+  KppState S = b.st_in[p];
+  const uint32_t badp = bad[p];
+  const uint32_t NB = pr.ntiles;
+  const double* tb = b.tsum_in + pr.tile0;
+  const uint32_t per = (NB + rt - 1) / rt;
+  const uint32_t b0 = t * per < NB ? t * per : NB;
+  const uint32_t b1 = b0 + per < NB ? b0 + per : NB;
+  constexpr uint32_t kRegTiles = 16;  // runs up to this long stay in registers
+  const bool in_regs = per <= kRegTiles;
+  double tv[kRegTiles];
+  if (c > 0 && in_regs) {
+#pragma unroll
+    for (uint32_t j = 0; j < kRegTiles; ++j) tv[j] = b0 + j < b1 ? tb[b0 + j] : 0.0;
+  }
   const float old = (c > 0 && row_ok) ? b.w_in[pr.off + i] : 0.0f;
-  // stage the tile's rows (independent of the draw)
+  // 64-float rows: coalesced 16-byte loads (chunk t & 15 of rows (t >> 4) +
+  // 8 j); rows 0-63 go to LDS at once, rows 64-127 wait in registers
+  tac_floatx4 v[16];
+  uint32_t nq = 0;
   if (DIMC == 64) {
-    const uint32_t rows = pr.n - tl.row0 < rt ? pr.n - tl.row0 : rt;
+    const uint32_t rows = pr.n - tl.row0 < 128u ? pr.n - tl.row0 : 128u;
     const tac_floatx4* src =
         reinterpret_cast<const tac_floatx4*>(G + ((uint64_t)pr.off + tl.row0) * 64);
-    const uint32_t nq = rows * 16u;
-    tac_floatx4 v[16];
+    nq = rows * 16u;
 #pragma unroll
     for (int j = 0; j < 16; ++j) {
-      const uint32_t q = t + (uint32_t)j * rt;
+      const uint32_t q = t + (uint32_t)j * 128u;
       v[j] = q < nq ? src[q] : tac_floatx4{0.0f, 0.0f, 0.0f, 0.0f};
     }
 #pragma unroll
-    for (int j = 0; j < 16; ++j) {
-      const uint32_t q = t + (uint32_t)j * rt;
+    for (int j = 0; j < 8; ++j) {
+      const uint32_t q = t + (uint32_t)j * 128u;
       if (q < nq) *reinterpret_cast<tac_floatx4*>(xr + tac_swz64(q >> 4, q & 15u)) = v[j];
     }
   } else {
@@ -443,7 +462,6 @@ __global__ void tac_kpp_round_kernel(const float* __restrict__ G, KppRound b,
     const float* src = G + ((uint64_t)pr.off + tl.row0) * dim;
     for (uint32_t f = t; f < rows * dim; f += rt) xr[(f / dim) * ld + f % dim] = src[f];
   }
-  KppState S = b.st_in[p];
   if (replay && S.pad != kKppReplaying) return;  // uniform; writes nothing
   if (t == 0) {
     s_thr = 0xFFFFFFFFu;
@@ -454,23 +472,13 @@ __global__ void tac_kpp_round_kernel(const float* __restrict__ G, KppRound b,
   // a problem whose draw is pending (an earlier round's) only forwards its state
   const bool draws = c > 0 && !S.err && !S.fallback;
   if (draws) {
-    if (bad[p] < c) {
+    if (badp < c) {
       S.err = 9;  // NonFinite
     } else {
-      // total and the tile holding the draw: thread t sums a contiguous run
-      // of the problem's tile sums
-      const uint32_t NB = pr.ntiles;
-      const double* tb = b.tsum_in + pr.tile0;
-      const uint32_t per = (NB + rt - 1) / rt;
-      const uint32_t b0 = t * per < NB ? t * per : NB;
-      const uint32_t b1 = b0 + per < NB ? b0 + per : NB;
-      constexpr uint32_t kRegTiles = 16;  // runs up to this long stay in registers
-      const bool in_regs = per <= kRegTiles;
-      double tv[kRegTiles];
+      // total and the tile holding the draw: thread t adds up a contiguous
+      // run of the problem's tile sums
       double part = 0.0;
       if (in_regs) {
-#pragma unroll
-        for (uint32_t j = 0; j < kRegTiles; ++j) tv[j] = b0 + j < b1 ? tb[b0 + j] : 0.0;
 #pragma unroll
         for (uint32_t j = 0; j < kRegTiles; ++j)
           if (b0 + j < b1) part += tv[j];
@@ -554,24 +562,42 @@ __global__ void tac_kpp_round_kernel(const float* __restrict__ G, KppRound b,
   __syncthreads();
   double acc = 0.0;
   bool invalid = false;
-  if (row_ok) {
-    float d;
-    if (DIMC == 64) {
-      float a0 = 0.0f, a1 = 0.0f, a2 = 0.0f, a3 = 0.0f;
+  float d = 0.0f;
+  if (DIMC == 64) {
+    // pass 0: rows 0-63, already in LDS; pass 1: rows 64-127 (v[8..15]); wave
+    // h reads in pass h
 #pragma unroll
-      for (uint32_t j = 0; j < 16; ++j) {
-        const tac_floatx4 x = *reinterpret_cast<const tac_floatx4*>(xr + tac_swz64(t, j));
-        const tac_floatx4 y = *reinterpret_cast<const tac_floatx4*>(crow + 4 * j);
-        const float t0 = x.x - y.x, t1 = x.y - y.y, t2 = x.z - y.z, t3 = x.w - y.w;
-        a0 = a0 + t0 * t0;
-        a1 = a1 + t1 * t1;
-        a2 = a2 + t2 * t2;
-        a3 = a3 + t3 * t3;
+    for (int h = 0; h < 2; ++h) {
+      if (h) {
+        __syncthreads();
+#pragma unroll
+        for (int j = 8; j < 16; ++j) {
+          const uint32_t q = t + (uint32_t)j * 128u;
+          if (q < nq)
+            *reinterpret_cast<tac_floatx4*>(xr + tac_swz64((q >> 4) - 64u, q & 15u)) = v[j];
+        }
+        __syncthreads();
       }
-      d = ((a0 + a1) + a2) + a3;  // tac_l2sq<64>'s order
-    } else {
-      d = tac_l2sq<DIMC>(xr + t * ld, crow, dim);
+      if (t / 64 == (uint32_t)h && row_ok) {
+        const uint32_t r = t - 64u * h;
+        float a0 = 0.0f, a1 = 0.0f, a2 = 0.0f, a3 = 0.0f;
+#pragma unroll
+        for (uint32_t j = 0; j < 16; ++j) {
+          const tac_floatx4 x = *reinterpret_cast<const tac_floatx4*>(xr + tac_swz64(r, j));
+          const tac_floatx4 y = *reinterpret_cast<const tac_floatx4*>(crow + 4 * j);
+          const float t0 = x.x - y.x, t1 = x.y - y.y, t2 = x.z - y.z, t3 = x.w - y.w;
+          a0 = a0 + t0 * t0;
+          a1 = a1 + t1 * t1;
+          a2 = a2 + t2 * t2;
+          a3 = a3 + t3 * t3;
+        }
+        d = ((a0 + a1) + a2) + a3;  // tac_l2sq<64>'s order
+      }
     }
+  } else if (row_ok) {
+    d = tac_l2sq<DIMC>(xr + t * ld, crow, dim);
+  }
+  if (row_ok) {
     const float v = c > 0 ? (d < old ? d : old) : d;
     b.w_out[pr.off + i] = v;
     invalid = !(v >= 0.0f && v <= 3.402823466e38f);
