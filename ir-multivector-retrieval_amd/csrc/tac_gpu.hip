@@ -37,6 +37,7 @@
 #include <cstring>
 #include <mutex>
 #include <string>
+#include <thread>
 #include <vector>
 
 using namespace tacgpu;
@@ -2251,28 +2252,37 @@ int tac_cluster_core(DeviceState &ds, hipStream_t s, const uint32_t *ids, uint64
   int st;
   // CSR grouping by token id, ascending input order inside a token (tac.zig:575-602)
   std::vector<uint32_t> freqs(nd, 0), offs(nd + 1, 0), idx(N);
-  for (uint64_t i = 0; i < N; ++i) freqs[ids[i]] += 1;
-  for (uint64_t j = 0; j < nd; ++j) offs[j + 1] = offs[j] + freqs[j];
-  {
+  auto group = [&] {
+    for (uint64_t i = 0; i < N; ++i) freqs[ids[i]] += 1;
+    for (uint64_t j = 0; j < nd; ++j) offs[j + 1] = offs[j] + freqs[j];
     std::vector<uint32_t> cur(offs.begin(), offs.end() - 1);
     for (uint64_t i = 0; i < N; ++i) idx[cur[ids[i]]++] = (uint32_t)i;
-  }
+  };
   const size_t vbytes = (size_t)N * dim * sizeof(float);
   // G carries tac_spread_pad_floats of slack: the spread kernel's full-batch
   // loads run up to one batch past a token's last row, and the fold kernel's
   // lanes past dim up to 64 * per floats past a row
   const size_t gbytes = vbytes + tac_spread_pad_floats(dim) * sizeof(float);
   if ((!vectors_on_device && (st = ensure(ds, ds.tac_v, vbytes))) ||
-      (st = ensure(ds, ds.tac_G, gbytes)) || (st = upload_vec(ds, ds.tac_idx, idx, s)) ||
-      (st = upload_vec(ds, ds.tac_offs, offs, s)) ||
-      (st = ensure(ds, ds.tac_spreads, nd * sizeof(float))))
+      (st = ensure(ds, ds.tac_G, gbytes)))
     return st;
-  // Host vectors go up once; device-resident ones are gathered in place.
+  // Host vectors go up once (the grouping runs on a second thread meanwhile,
+  // the copy from pageable memory holding this one); device-resident ones
+  // are gathered in place.
   const float *dv = vectors;
   if (!vectors_on_device) {
-    HIP_TRY(hipMemcpyAsync(ds.tac_v.ptr, vectors, vbytes, hipMemcpyHostToDevice, s));
+    std::thread grouper(group);
+    const hipError_t upload =
+        hipMemcpyAsync(ds.tac_v.ptr, vectors, vbytes, hipMemcpyHostToDevice, s);
+    grouper.join();
+    HIP_TRY(upload);
     dv = as<float>(ds.tac_v);
+  } else {
+    group();
   }
+  if ((st = upload_vec(ds, ds.tac_idx, idx, s)) || (st = upload_vec(ds, ds.tac_offs, offs, s)) ||
+      (st = ensure(ds, ds.tac_spreads, nd * sizeof(float))))
+    return st;
   float *G = as<float>(ds.tac_G);
   const uint64_t nf = (uint64_t)N * dim;
   // Grids stay far below a dispatch's 2^32 work-items: the gather and the
@@ -2283,7 +2293,7 @@ int tac_cluster_core(DeviceState &ds, hipStream_t s, const uint32_t *ids, uint64
   LAUNCH_TRY("tac_gather_kernel");
   uint32_t max_n = 0;
   for (uint64_t j = 0; j < nd; ++j) max_n = freqs[j] > max_n ? freqs[j] : max_n;
-  const uint64_t ninv = (uint64_t)max_n + kTacSpreadBatch;  // one batch of slack, as for G
+  const uint64_t ninv = (uint64_t)max_n + kTacSpreadSlackRows;  // slack, as for G
   if ((st = ensure(ds, ds.tac_inv, (size_t)ninv * sizeof(float)))) return st;
   tac_inv_table_kernel<<<(unsigned)std::min<uint64_t>((ninv + 255) / 256, kMaxBlocks), 256, 0,
                          s>>>(as<float>(ds.tac_inv), ninv);
@@ -2296,7 +2306,9 @@ int tac_cluster_core(DeviceState &ds, hipStream_t s, const uint32_t *ids, uint64
     constexpr uint64_t kSlice = 1ull << 24;  // tokens per launch (2^30 work-items)
     for (uint64_t j0 = 0; j0 < nd; j0 += kSlice) {
       const unsigned nb = (unsigned)std::min<uint64_t>(nd - j0, kSlice);
-      if (per == 1)
+      if (dim == 64)
+        tac_spread64_kernel<<<nb, kTacSpread64Threads, 0, s>>>(G, doffs, dinv, dsp, j0);
+      else if (per == 1)
         tac_spread_kernel<1><<<nb, kWave, lds, s>>>(G, doffs, dinv, dim, dsp, j0);
       else if (per == 2)
         tac_spread_kernel<2><<<nb, kWave, lds, s>>>(G, doffs, dinv, dim, dsp, j0);
@@ -2311,6 +2323,7 @@ int tac_cluster_core(DeviceState &ds, hipStream_t s, const uint32_t *ids, uint64
   HIP_TRY(hipStreamSynchronize(s));
 
   // budgets (tac.zig:641-668)
+
   std::vector<uint32_t> kappa(nd, 0);
   const tacphase::Params pp{prm.kappa_total, prm.mu, prm.tau, prm.epsilon, prm.theta};
   if ((st = tacphase::allocate(freqs, spreads, kappa, pp))) return st;
@@ -2323,6 +2336,7 @@ int tac_cluster_core(DeviceState &ds, hipStream_t s, const uint32_t *ids, uint64
 
   TacPlan pl;
   if ((st = tac_plan(freqs, offs, kappa, goff, prm.seed, rt, K, &pl))) return st;
+
   // The Lloyd kernels launch one block of at most 256 work-items per tile,
   // problem, chunk or scan range; a dispatch's grid holds under 2^32.
   constexpr uint64_t kMaxUnits = (1ull << 32) / 256;
@@ -2414,6 +2428,7 @@ int tac_cluster_core(DeviceState &ds, hipStream_t s, const uint32_t *ids, uint64
   const bool profile = g_profile;
   const double prep_ms =
       std::chrono::duration<double, std::milli>(std::chrono::steady_clock::now() - wall0).count();
+
   hipEvent_t ev0 = nullptr, ev1 = nullptr, ev2 = nullptr;
   if (profile) {
     if ((st = event_at(ds, 0, &ev0)) || (st = event_at(ds, 1, &ev1)) ||

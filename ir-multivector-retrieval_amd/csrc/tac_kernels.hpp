@@ -144,12 +144,19 @@ __global__ __launch_bounds__(256) void tac_gather_kernel(const float* __restrict
 // run without branches.  Only the token's last, partial batch tests the row
 // count.  Lanes past dim read neighbouring floats and never store them.
 // ---------------------------------------------------------------------------
+typedef float tac_floatx4 __attribute__((ext_vector_type(4)));
+
 constexpr uint32_t kTacSpreadBatch = 32;
+constexpr uint32_t kTacSpread64Rows = 64;  // rows per batch of tac_spread64_kernel
 constexpr uint32_t kTacInvMax = 1u << 24;
 
-// Floats of slack G needs past its last row for the spread kernel's loads.
+// Rows of slack G and the reciprocal table need past a token's last row: a
+// spread kernel's batch may run that far.
+constexpr uint32_t kTacSpreadSlackRows = kTacSpread64Rows;
+
+// Floats of slack G needs past its last row for the spread kernels' loads.
 __host__ __device__ constexpr size_t tac_spread_pad_floats(uint32_t dim) {
-  return (size_t)kTacSpreadBatch * dim + 64u * ((dim + 63u) / 64u);
+  return (size_t)kTacSpreadSlackRows * dim + 64u * ((dim + 63u) / 64u);
 }
 
 __global__ void tac_inv_table_kernel(float* __restrict__ inv, uint64_t n) {
@@ -275,6 +282,160 @@ __global__ __launch_bounds__(kWave) void tac_spread_kernel(const float* __restri
   }
 }
 
+// The same spread for 64-float rows, built for memory latency.  A block of
+// one folding wave and kTacSpread64Loaders loading waves serves one token:
+// the loaders fetch batches of 64 rows (one 16-byte load per lane brings four
+// rows, 1 KB per instruction), each a quarter of every batch, four batches
+// ahead of the fold, and store a batch into one of two LDS buffers a step
+// before it is folded; wave 0 folds the other buffer, one dimension per lane.  One block barrier per
+// batch.  The fold is tac_spread_kernel's, operation for operation.  Loads
+// past a token's last batch repeat that batch (the same lines, so no new
+// memory traffic), which keeps every step's loads unconditional.
+constexpr uint32_t kTacSpread64Loaders = 4;
+constexpr uint32_t kTacSpread64Threads = (kTacSpread64Loaders + 1) * kWave;
+
+__global__ __launch_bounds__(kTacSpread64Threads) void tac_spread64_kernel(
+    const float* __restrict__ G, const uint32_t* __restrict__ offs,
+    const float* __restrict__ inv, float* __restrict__ spreads, uint64_t j0) {
+  constexpr uint32_t R = kTacSpread64Rows;
+  constexpr uint32_t GW = R / 4 / kTacSpread64Loaders;  // 16-byte groups per loader per batch
+  constexpr int NR = 4;                               // batches in flight per loader
+  constexpr uint32_t C = 16;                          // rows read from LDS ahead of the fold
+  __shared__ __attribute__((aligned(16))) float xs[2][R * 64];  // row-major batches
+  __shared__ __attribute__((aligned(16))) float is[2][R];
+  __shared__ float m2s[64];
+  const uint64_t j = j0 + blockIdx.x;  // launched in slices of tokens
+  const uint32_t lane = threadIdx.x % kWave;
+  const uint32_t w = __builtin_amdgcn_readfirstlane(threadIdx.x / kWave);  // wave-uniform
+  const uint32_t lo = offs[j], hi = offs[j + 1];
+  if (hi == lo) {
+    if (threadIdx.x == 0) spreads[j] = 0.0f;
+    return;
+  }
+  const uint32_t n = hi - lo, nb = (n + R - 1) / R;
+  const tac_floatx4* g4 = reinterpret_cast<const tac_floatx4*>(G + (uint64_t)lo * 64);
+  tac_floatx4 buf[NR][GW];
+  float ivb[NR];
+  // batch k (at most the last) into register slot `slot`: group q of a batch
+  // holds rows 4q .. 4q + 3 (lane l: row 4q + l / 16, dimensions 4 (l % 16)
+  // ..); G and inv carry a batch of slack, so a partial last batch loads whole
+  // loader index (wave 0 only folds); wave-uniform, so the batch and quarter
+  // offsets stay scalar and every load and store is a fixed lane offset plus
+  // an immediate
+  const uint32_t lw = w - 1u;
+  const char* gq = reinterpret_cast<const char*>(g4) + (uint64_t)lw * GW * 1024u;
+  const uint32_t voff = lane * 16u;
+  auto load = [&](int slot, uint32_t k) {
+    k = k < nb ? k : nb - 1;
+    const char* p = gq + (uint64_t)k * (R * 256u) + voff;
+#pragma unroll
+    for (uint32_t g = 0; g < GW; ++g)
+      buf[slot][g] = *reinterpret_cast<const tac_floatx4*>(p + g * 1024u);
+    ivb[slot] = inv[(uint64_t)k * R + lane];
+  };
+  auto store = [&](int slot, uint32_t k) {
+    char* x = reinterpret_cast<char*>(xs[k & 1u]) + lw * GW * 1024u + voff;
+#pragma unroll
+    for (uint32_t g = 0; g < GW; ++g)
+      *reinterpret_cast<tac_floatx4*>(x + g * 1024u) = buf[slot][g];
+    is[k & 1u][lane] = ivb[slot];  // every loader writes the same values
+  };
+  float mean = 0.0f, m2 = 0.0f;
+  auto fold = [&](uint32_t k) {
+    const float* x = xs[k & 1u];
+    const float* iv = is[k & 1u];
+    const uint32_t m = n - k * R < R ? n - k * R : R;
+    if (m == R) {
+      // row b's mean update beside row b - 1's m2 update, as tac_spread_kernel;
+      // the next C rows are read from LDS while C rows fold
+      float xc[2][C], ic[2][C];
+      auto read = [&](int h, uint32_t c0) {
+#pragma unroll
+        for (uint32_t b = 0; b < C; ++b) xc[h][b] = x[(c0 + b) * 64u + lane];
+#pragma unroll
+        for (uint32_t q = 0; q < C / 4; ++q) {
+          const tac_floatx4 v4 = *reinterpret_cast<const tac_floatx4*>(iv + c0 + 4u * q);
+          ic[h][4 * q] = v4.x;
+          ic[h][4 * q + 1] = v4.y;
+          ic[h][4 * q + 2] = v4.z;
+          ic[h][4 * q + 3] = v4.w;
+        }
+      };
+      float xp = 0.0f, dp = 0.0f;
+      read(0, 0);
+#pragma unroll
+      for (uint32_t cc = 0; cc < R / C; ++cc) {
+        const int h = (int)(cc & 1u);
+        if (cc + 1 < R / C) read(h ^ 1, (cc + 1) * C);
+#pragma unroll
+        for (uint32_t b = 0; b < C; ++b) {
+          const float xb = xc[h][b], ivv = ic[h][b];
+          if (cc == 0 && b == 0) {
+            dp = xb - mean;
+            mean = mean + dp * ivv;
+          } else {
+            const float d = xb - mean;
+            const float e = xp - mean;  // mean after the previous row
+            __builtin_amdgcn_sched_barrier(0);
+            const float t = d * ivv;
+            const float q = dp * e;
+            __builtin_amdgcn_sched_barrier(0);
+            mean = mean + t;
+            m2 = m2 + q;
+            __builtin_amdgcn_sched_barrier(0);
+            dp = d;
+          }
+          xp = xb;
+        }
+      }
+      m2 = m2 + dp * (xp - mean);
+    } else {
+      for (uint32_t b = 0; b < m; ++b) {
+        const float xb = x[b * 64u + lane];
+        const float old = mean;
+        const float delta = xb - old;
+        mean = old + delta * iv[b];
+        m2 = m2 + delta * (xb - mean);
+      }
+    }
+  };
+  // step k: batch k sits in LDS buffer k & 1 and is folded; batches k + 1 ..
+  // k + NR - 1 wait in registers; batch k + NR is loaded into the register
+  // slot of batch k; batch k + 1 goes to the other LDS buffer
+  // The loaders and the folding wave run separate loops with the same
+  // number of block barriers (one before step 0, one after each step).
+  if (w > 0) {
+#pragma unroll
+    for (int q = 0; q < NR; ++q) load(q, (uint32_t)q);
+    store(0, 0);
+    __syncthreads();
+    uint32_t k = 0;
+    for (;;) {
+#pragma unroll
+      for (int sl = 0; sl < NR; ++sl) {
+        load(sl, k + NR);
+        store((sl + 1) % NR, k + 1);
+        __syncthreads();
+        if (++k == nb) break;
+      }
+      if (k == nb) break;
+    }
+  } else {
+    __syncthreads();
+    for (uint32_t k = 0; k < nb; ++k) {
+      fold(k);
+      __syncthreads();
+    }
+  }
+  if (w == 0) m2s[lane] = m2;
+  __syncthreads();
+  if (threadIdx.x == 0) {
+    float trace = 0.0f;
+    for (uint32_t d = 0; d < 64; ++d) trace = trace + m2s[d];
+    spreads[j] = trace / (float)n;
+  }
+}
+
 // ---------------------------------------------------------------------------
 // Degenerate problems (k >= n, kmeans.zig:88-104): centroid c = row
 // min(c, n - 1), assignment i = i, wcss 0, no iterations.  One block each.
@@ -337,7 +498,6 @@ constexpr uint32_t kKppNoBad = 0xFFFFFFFFu;
 // resolved it, for the rest of its rounds.
 constexpr uint32_t kKppReplaying = 0xFFFFFFFFu;
 
-typedef float tac_floatx4 __attribute__((ext_vector_type(4)));
 
 // What a round's block needs of its tile and problem, in one load.
 struct KppTile {

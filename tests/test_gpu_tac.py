@@ -80,9 +80,12 @@ def test_generic_dims(gpu, dim):
 @pytest.mark.parametrize("dim", [64, 96, 191])
 def test_spread_batch_edges(gpu, dim):
     # token sizes on either side of one, two and three 32-row spread batches
-    # (the last, partial batch is the only one with a row test), in shuffled
-    # input order, with spreads that decide the budgets of tokens >= mu rows
-    sizes = [1, 31, 32, 33, 40, 63, 64, 65, 95, 96, 97, 128, 129]
+    # and of the 64-row batches of the dim-64 kernel, up to past its ring of
+    # four (the last, partial batch is the only one with a row test), in
+    # shuffled input order, with spreads that decide the budgets of tokens >=
+    # mu rows
+    sizes = [1, 31, 32, 33, 40, 63, 64, 65, 95, 96, 97, 128, 129, 191, 192, 193, 255, 256,
+             257, 319, 320, 321, 449, 512, 577]
     rng = np.random.default_rng(dim)
     ids = np.concatenate([np.full(c, t, np.uint32) for t, c in enumerate(sizes)])
     ids = ids[rng.permutation(ids.size)]
