@@ -2242,32 +2242,43 @@ struct TacPlan {
 int tac_plan(const std::vector<uint32_t> &freqs, const std::vector<uint32_t> &offs,
              const std::vector<uint32_t> &kappa, const std::vector<uint64_t> &goff,
              uint64_t seed, uint32_t rt, uint64_t kappa_total, TacPlan *pl) {
-  for (uint32_t j = 0; j < (uint32_t)freqs.size(); ++j) {
+  // Problems in order of effective k (0 for degenerate ones), descending,
+  // ties in token order: a stable counting sort over the tokens in id order.
+  const uint32_t nd = (uint32_t)freqs.size();
+  auto keff = [&](uint32_t j) { return kappa[j] >= freqs[j] ? 0u : kappa[j]; };
+  size_t P = 0;
+  uint32_t kx = 0;
+  for (uint32_t j = 0; j < nd; ++j) {
     if (kappa[j] == 0 || freqs[j] == 0) continue;
-    TacProblem p{};
+    ++P;
+    kx = std::max(kx, keff(j));
+  }
+  std::vector<uint32_t> slot((size_t)kx + 2, 0);  // bucket kx - keff, descending k
+  for (uint32_t j = 0; j < nd; ++j)
+    if (kappa[j] != 0 && freqs[j] != 0) ++slot[kx - keff(j) + 1];
+  for (size_t b = 1; b < slot.size(); ++b) slot[b] += slot[b - 1];
+  pl->probs.assign(P, TacProblem{});
+  pl->token.assign(P, 0u);
+  size_t n_tiles = 0, n_chunks = 0, n_ranges = 0;
+  for (uint32_t j = 0; j < nd; ++j) {
+    if (kappa[j] == 0 || freqs[j] == 0) continue;
+    const uint32_t q = slot[kx - keff(j)]++;
+    TacProblem &p = pl->probs[q];
     p.off = offs[j];
     p.n = freqs[j];
     p.k = kappa[j];
     p.goff = (uint32_t)goff[j];
     p.seed = seed ^ (uint64_t)j;
     p.degenerate = p.k >= p.n ? 1u : 0u;
-    pl->probs.push_back(p);
-    pl->token.push_back(j);
+    pl->token[q] = j;
+    const size_t nt = (p.n + rt - 1) / rt;
+    n_tiles += nt;
+    n_chunks += (p.n + kFoldChunk - 1) / kFoldChunk;
+    n_ranges += (nt + kTacScanTiles - 1) / kTacScanTiles;
   }
-  const size_t P = pl->probs.size();
-  std::vector<uint32_t> order(P);
-  for (size_t q = 0; q < P; ++q) order[q] = (uint32_t)q;
-  auto keff = [&](uint32_t q) { return pl->probs[q].degenerate ? 0u : pl->probs[q].k; };
-  std::stable_sort(order.begin(), order.end(),
-                   [&](uint32_t a, uint32_t b) { return keff(a) > keff(b); });
-  std::vector<TacProblem> probs(P);
-  std::vector<uint32_t> token(P);
-  for (size_t q = 0; q < P; ++q) {
-    probs[q] = pl->probs[order[q]];
-    token[q] = pl->token[order[q]];
-  }
-  pl->probs.swap(probs);
-  pl->token.swap(token);
+  pl->tiles.reserve(n_tiles);
+  pl->chunks.reserve(n_chunks);
+  pl->ranges.reserve(n_ranges);
   pl->cprob.assign(kappa_total, 0);
   uint32_t t0 = 0, c0 = 0;
   for (uint32_t q = 0; q < (uint32_t)P; ++q) {
