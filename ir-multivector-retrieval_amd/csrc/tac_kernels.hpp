@@ -922,7 +922,7 @@ __global__ void tac_assign_kernel(const float* __restrict__ G, const float* __re
 // ---------------------------------------------------------------------------
 constexpr uint32_t kTacMfmaRows = 128;     // rows per tile (tac_rows_per_tile(64))
 constexpr uint32_t kTacMfmaThreads = 256;
-constexpr uint32_t kTacMfmaChunk = 64;     // centroids staged in LDS at a time
+constexpr uint32_t kTacMfmaChunk = 128;    // centroids staged in LDS at a time
 constexpr uint32_t kTacMfmaLd = 65;        // LDS row stride (floats)
 
 // Components for which the screen's bounds hold: finite, |v| < 1e18 and not
