@@ -33,7 +33,7 @@
 
 namespace tacgpu {
 
-constexpr uint32_t kFoldChunk = 1024;  // terms per chunk
+constexpr uint32_t kFoldChunk = 256;  // terms per chunk
 constexpr int kFoldCands = 3;          // candidate binades per chunk
 constexpr uint64_t kFoldBad = ~0ull;   // fold_quantize: the term spoils the binade
 
