@@ -108,7 +108,8 @@ int tac_gpu_memcpy_htod(void *dst, const void *src, uint64_t bytes);
 int tac_gpu_memcpy_dtoh(void *dst, const void *src, uint64_t bytes);
 int tac_gpu_memcpy_dtod(void *dst, const void *src, uint64_t bytes);
 int tac_gpu_synchronize(void);
-/* Release the per-device workspace the library caches between calls. */
+/* Release the per-device workspace the library caches between calls (device
+ * buffers and the pinned host staging buffers of large uploads). */
 int tac_gpu_release_workspace(void);
 
 /* ---- optional outputs of training (every pointer may be NULL) ---------- */
