@@ -98,7 +98,7 @@ struct DeviceState {
   Buffer tac_v, tac_idx, tac_offs, tac_G, tac_spreads, tac_w, tac_e, tac_code, tac_sorted,
       tac_tsum, tac_hist, tac_counts, tac_start, tac_C, tac_pre, tac_fch, tac_st, tac_bad,
       tac_done, tac_iters, tac_wcss, tac_prev, tac_empties, tac_assign, tac_probs, tac_tiles,
-      tac_chl, tac_cprob, tac_inv, tac_rsum, tac_ranges, tac_h, tac_ktiles;
+      tac_chl, tac_cprob, tac_inv, tac_rsum, tac_ranges, tac_h, tac_ktiles, tac_big;
   bool crc_tx_ready = false;
   // training's second stream (two halves of the subspaces) and its events
   hipStream_t aux_stream[1] = {};
@@ -1374,7 +1374,8 @@ int tac_gpu_release_workspace(void) {
                     &ds->tac_probs, &ds->tac_tiles, &ds->tac_chl, &ds->tac_cprob,
                     &ds->tac_inv,   &ds->tac_rsum, &ds->tac_ranges, &ds->cand_nbr,
                     &ds->cand_defer, &ds->cand_count, &ds->cand_anchor, &ds->cand_grid,
-                    &ds->kpp_src,   &ds->fold_order, &ds->tac_h, &ds->tac_ktiles};
+                    &ds->kpp_src,   &ds->fold_order, &ds->tac_h, &ds->tac_ktiles,
+                    &ds->tac_big};
   ds->crc_tx_ready = false;
   for (Buffer *b : bufs) {
     if (b->ptr) HIP_TRY(hipFree(b->ptr));
@@ -2455,6 +2456,7 @@ int tac_cluster_core(DeviceState &ds, hipStream_t s, const uint32_t *ids, uint64
       (st = ensure(ds, ds.tac_pre, (size_t)NCH * sizeof(double))) ||
       (st = ensure(ds, ds.tac_fch, (size_t)NCH * sizeof(FoldChunk))) ||
       (st = ensure(ds, ds.tac_st, 2 * (size_t)P * sizeof(KppState))) ||
+      (st = ensure(ds, ds.tac_big, (K + 1) * sizeof(uint32_t))) ||
       (st = ensure(ds, ds.tac_bad, (size_t)P * sizeof(uint32_t))) ||
       (st = ensure(ds, ds.tac_iters, (size_t)P * sizeof(uint32_t))) ||
       (st = ensure(ds, ds.tac_wcss, (size_t)P * sizeof(float))) ||
@@ -2650,16 +2652,24 @@ int tac_cluster_core(DeviceState &ds, hipStream_t s, const uint32_t *ids, uint64
     {
       const uint32_t *cp = as<uint32_t>(ds.tac_cprob);
       const unsigned fb = (unsigned)((K + 3) / 4);
+      // dim 64: clusters of kTacFoldBig members or more go to the block kernel
+      uint32_t *big = dim == 64 ? as<uint32_t>(ds.tac_big) : nullptr;
+      if (big) HIP_TRY(hipMemsetAsync(big, 0, sizeof(uint32_t), s));
       if (per == 1)
         tac_fold_kernel<1><<<fb, 256, 0, s>>>(G, sorted, counts, start, cp, probs, done, C,
-                                              (uint32_t)K, dim);
+                                              (uint32_t)K, dim, big);
       else if (per == 2)
         tac_fold_kernel<2><<<fb, 256, 0, s>>>(G, sorted, counts, start, cp, probs, done, C,
-                                              (uint32_t)K, dim);
+                                              (uint32_t)K, dim, nullptr);
       else
         tac_fold_kernel<3><<<fb, 256, 0, s>>>(G, sorted, counts, start, cp, probs, done, C,
-                                              (uint32_t)K, dim);
+                                              (uint32_t)K, dim, nullptr);
       LAUNCH_TRY("tac_fold_kernel");
+      if (big) {
+        tac_fold_big_kernel<<<kTacFoldBigBlocks, kTacFoldBigThreads, 0, s>>>(
+            G, sorted, counts, start, cp, probs, C, big);
+        LAUNCH_TRY("tac_fold_big_kernel");
+      }
     }
     tac_chunk_sums_kernel<<<(NCH + 3) / 4, 256, 0, s>>>(e, probs, chl, NCH, done, pre);
     tac_chunk_prefix_kernel<<<P, 256, 0, s>>>(pre, probs, done);

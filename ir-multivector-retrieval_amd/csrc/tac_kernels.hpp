@@ -1343,6 +1343,10 @@ __global__ void tac_scatter_kernel(const uint32_t* __restrict__ code,
 // gather per 64 members), and the next batch's row indices are read while
 // the current batch is added.  Only the last, partial batch tests members.
 // ---------------------------------------------------------------------------
+// Clusters of at least kTacFoldBig members (64-float rows) are folded by
+// tac_fold_big_kernel from a list the wave kernel builds (big[0] = count).
+constexpr uint32_t kTacFoldBig = 512;
+
 __host__ __device__ constexpr uint32_t tac_fold_batch(int per) { return per == 1 ? 64u : per == 2 ? 32u : 16u; }
 
 template <int PER>
@@ -1350,7 +1354,8 @@ __global__ __launch_bounds__(256) void tac_fold_kernel(
     const float* __restrict__ G, const uint32_t* __restrict__ sorted,
     const uint32_t* __restrict__ counts, const uint32_t* __restrict__ start,
     const uint32_t* __restrict__ cprob, const TacProblem* __restrict__ probs,
-    const uint32_t* __restrict__ done, float* __restrict__ C, uint32_t kappa, uint32_t dim) {
+    const uint32_t* __restrict__ done, float* __restrict__ C, uint32_t kappa, uint32_t dim,
+    uint32_t* __restrict__ big) {
   constexpr uint32_t kTacFoldBatch = tac_fold_batch(PER);
   const uint32_t g = blockIdx.x * (256 / kWave) + threadIdx.x / kWave, lane = threadIdx.x % kWave;
   if (g >= kappa) return;
@@ -1358,6 +1363,10 @@ __global__ __launch_bounds__(256) void tac_fold_kernel(
   if (done[p]) return;
   const uint32_t cnt = counts[g];
   if (cnt == 0) return;
+  if (big != nullptr && cnt >= kTacFoldBig) {  // left to tac_fold_big_kernel
+    if (lane == 0) big[1 + atomicAdd(&big[0], 1u)] = g;
+    return;
+  }
   const uint32_t* mem = sorted + probs[p].off + start[g];
   float s[PER];
 #pragma unroll
@@ -1409,6 +1418,114 @@ __global__ __launch_bounds__(256) void tac_fold_kernel(
   for (int u = 0; u < PER; ++u) {
     const uint32_t d = lane + kWave * u;
     if (d < dim) C[(uint64_t)g * dim + d] = s[u] * inv;
+  }
+}
+
+// The same cluster sums for clusters of at least kTacFoldBig members, one
+// block per listed cluster (blocks stride over the list): a wave folding 64
+// members per gathered batch waits a full memory round trip per batch, so
+// four loader waves gather the member rows instead (one 16-byte piece per
+// lane, four rows per load instruction), four batches ahead, and store each
+// batch into one of two LDS buffers a step before wave 0 folds it, lane =
+// dimension, in member order from 0.0f.  Member indices are staged in LDS a
+// segment of kTacFoldBigSeg at a time by the whole block, so the loaders'
+// only global loads are rows.  One block barrier per batch; loader and folder
+// loops count the same barriers.
+constexpr uint32_t kTacFoldBigLoaders = 4;
+constexpr uint32_t kTacFoldBigThreads = (kTacFoldBigLoaders + 1) * kWave;
+constexpr uint32_t kTacFoldBigBlocks = 512;
+constexpr uint32_t kTacFoldBigSeg = 4096;  // member indices staged at a time
+
+__global__ __launch_bounds__(kTacFoldBigThreads) void tac_fold_big_kernel(
+    const float* __restrict__ G, const uint32_t* __restrict__ sorted,
+    const uint32_t* __restrict__ counts, const uint32_t* __restrict__ start,
+    const uint32_t* __restrict__ cprob, const TacProblem* __restrict__ probs,
+    float* __restrict__ C, const uint32_t* __restrict__ big) {
+  constexpr uint32_t B = 64;                           // members per batch
+  constexpr uint32_t RW = B / kTacFoldBigLoaders;      // members per loader per batch
+  constexpr uint32_t GW = RW / 4;                      // load instructions per loader per batch
+  constexpr int NR = 4;                                // batches in flight per loader
+  constexpr uint32_t CR = 16;                          // rows read from LDS ahead of the fold
+  __shared__ __attribute__((aligned(16))) float xs[2][B * 64];
+  __shared__ uint32_t ids[kTacFoldBigSeg];
+  const uint32_t lane = threadIdx.x % kWave;
+  const uint32_t w = __builtin_amdgcn_readfirstlane(threadIdx.x / kWave);  // wave-uniform
+  const uint32_t nbig = big[0];
+  for (uint32_t li = blockIdx.x; li < nbig; li += gridDim.x) {
+    const uint32_t g = big[1 + li];
+    const uint32_t cnt = counts[g];
+    const uint32_t* mem = sorted + probs[cprob[g]].off + start[g];
+    float sum = 0.0f;
+    for (uint32_t s0 = 0; s0 < cnt; s0 += kTacFoldBigSeg) {
+      const uint32_t sn = cnt - s0 < kTacFoldBigSeg ? cnt - s0 : kTacFoldBigSeg;
+      for (uint32_t t = threadIdx.x; t < sn; t += kTacFoldBigThreads) ids[t] = mem[s0 + t];
+      __syncthreads();
+      const uint32_t nb = (sn + B - 1) / B;
+      if (w > 0) {
+        const uint32_t lw = w - 1u;
+        tac_floatx4 buf[NR][GW];
+        // batch k into register slot `slot`; lane l fetches piece l % 16 of
+        // member RW lw + 4 q + l / 16 (past the segment: its last member again,
+        // which the fold never reads, so every load is unconditional)
+        auto load = [&](int slot, uint32_t k) {
+#pragma unroll
+          for (uint32_t q = 0; q < GW; ++q) {
+            uint32_t m = k * B + RW * lw + 4u * q + lane / 16u;
+            m = m < sn ? m : sn - 1u;
+            buf[slot][q] = *reinterpret_cast<const tac_floatx4*>(G + (uint64_t)ids[m] * 64u +
+                                                                  4u * (lane % 16u));
+          }
+        };
+        auto store = [&](int slot, uint32_t k) {
+          char* x = reinterpret_cast<char*>(xs[k & 1u]) + lw * RW * 256u + lane * 16u;
+#pragma unroll
+          for (uint32_t q = 0; q < GW; ++q)
+            *reinterpret_cast<tac_floatx4*>(x + q * 1024u) = buf[slot][q];
+        };
+#pragma unroll
+        for (int q = 0; q < NR; ++q) load(q, (uint32_t)q);
+        store(0, 0);
+        __syncthreads();
+        uint32_t k = 0;
+        for (;;) {
+#pragma unroll
+          for (int sl = 0; sl < NR; ++sl) {
+            load(sl, k + NR);
+            store((sl + 1) % NR, k + 1);
+            __syncthreads();
+            if (++k == nb) break;
+          }
+          if (k == nb) break;
+        }
+      } else {
+        __syncthreads();
+        for (uint32_t k = 0; k < nb; ++k) {
+          const float* x = xs[k & 1u];
+          const uint32_t m = sn - k * B < B ? sn - k * B : B;
+          if (m == B) {
+            float xc[2][CR];
+#pragma unroll
+            for (uint32_t b = 0; b < CR; ++b) xc[0][b] = x[b * 64u + lane];
+#pragma unroll
+            for (uint32_t cc = 0; cc < B / CR; ++cc) {
+              const int h = (int)(cc & 1u);
+              if (cc + 1 < B / CR) {
+#pragma unroll
+                for (uint32_t b = 0; b < CR; ++b)
+                  xc[h ^ 1][b] = x[((cc + 1) * CR + b) * 64u + lane];
+              }
+#pragma unroll
+              for (uint32_t b = 0; b < CR; ++b) sum = sum + xc[h][b];
+            }
+          } else {
+            for (uint32_t b = 0; b < m; ++b) sum = sum + x[b * 64u + lane];
+          }
+          __syncthreads();
+        }
+      }
+      __syncthreads();  // ids and the buffers are reused by the next segment or cluster
+    }
+    if (w == 0) C[(uint64_t)g * 64u + lane] = sum * (1.0f / (float)cnt);
   }
 }
 
