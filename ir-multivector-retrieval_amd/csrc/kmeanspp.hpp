@@ -199,7 +199,12 @@ __global__ __launch_bounds__(1024) void kpp_select_kernel(
     __syncthreads();
     double before = carry;
     for (uint32_t q = 0; q < wv; ++q) before += wsum[q];
-    if (b < NB && ud < before + incl) atomicMin(&s_block, b);
+    {
+      // the first such block: a wave ballot and one LDS atomic per wave (an
+      // atomic from every lane to one address serializes)
+      const uint64_t bl = __ballot(b < NB && ud < before + incl);
+      if (lane == 0 && bl) atomicMin(&s_block, b + (uint32_t)__ffsll((long long)bl) - 1u);
+    }
     __syncthreads();
     if (b == s_block) s_before = before + (incl - x);
     if (threadIdx.x == blockDim.x - 1) carry = before + incl;
@@ -234,13 +239,19 @@ __global__ __launch_bounds__(1024) void kpp_select_kernel(
   base += incl - local;
   const double u = r * s_total;
   double p = base;
+  uint32_t cand = 0xFFFFFFFFu;
 #pragma unroll
   for (int q = 0; q < 4; ++q) {
     p += v[q];
     const uint64_t i = lo + threadIdx.x * 4 + q;
-    if (i < n && u < p) {
-      atomicMin(&s_first, (uint32_t)(i - lo));
-      break;
+    if (cand == 0xFFFFFFFFu && i < n && u < p) cand = (uint32_t)(i - lo);
+  }
+  {
+    // indices grow with the lane, so the wave's first candidate is its least
+    const uint64_t bl = __ballot(cand != 0xFFFFFFFFu);
+    if (bl) {
+      const uint32_t c0 = __shfl(cand, __ffsll((long long)bl) - 1, 64);
+      if (lane == 0) atomicMin(&s_first, c0);
     }
   }
   __syncthreads();

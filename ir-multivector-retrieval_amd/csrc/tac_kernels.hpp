@@ -653,7 +653,12 @@ __global__ __launch_bounds__(128) void tac_kpp_round_kernel(
         const double r = kpp_float64(S.s);
         S.r = r;
         const double u = r * total;
-        if (b0 < b1 && u < incl) atomicMin(&s_thr, t);
+        {
+          // the first such thread: one ballot per wave, one LDS atomic per wave
+          // (an atomic from every lane to one address serializes)
+          const uint64_t bl = __ballot(b0 < b1 && u < incl);
+          if (t % kWave == 0 && bl) atomicMin(&s_thr, t + (uint32_t)__ffsll((long long)bl) - 1u);
+        }
         __syncthreads();
         if (t == s_thr) {
           double run = excl;
@@ -693,7 +698,11 @@ __global__ __launch_bounds__(128) void tac_kpp_round_kernel(
           double wi, we;
           kpp_block_scan(wv, rt, ws_b, &wi, &we);
           const double pi = s_before + wi, pprev = s_before + we;
-          if (ci < pr.n && u < pi) atomicMin(&s_first, t);
+          {
+            const uint64_t bl = __ballot(ci < pr.n && u < pi);
+            if (t % kWave == 0 && bl)
+              atomicMin(&s_first, t + (uint32_t)__ffsll((long long)bl) - 1u);
+          }
           __syncthreads();
           if (s_first == 0xFFFFFFFFu) {
             S.fallback = 1;
@@ -920,6 +929,22 @@ __global__ void tac_assign_kernel(const float* __restrict__ G, const float* __re
 // One block of 256 work-items per tile of 128 rows; wave w takes rows
 // 32 w .. 32 w + 31 as two row groups, four accumulator chains at a time.
 // ---------------------------------------------------------------------------
+// This lane's slot in a shared LDS list when `take` (every lane of the wave
+// calls it): the wave's ballot, one atomic add by its first taking lane, and
+// the rank among the taking lanes below.
+__device__ __forceinline__ uint32_t tac_wave_append(bool take, uint32_t* counter) {
+  const uint64_t bl = __ballot(take);
+  const uint32_t lane = threadIdx.x % kWave;
+  uint32_t base = 0;
+  if (bl) {
+    const int leader = __ffsll((long long)bl) - 1;
+    if ((int)lane == leader) base = atomicAdd(counter, (uint32_t)__popcll(bl));
+    base = __shfl(base, leader, kWave);
+  }
+  const uint64_t below = bl & ((1ull << lane) - 1ull);
+  return base + (uint32_t)__popcll(below);
+}
+
 constexpr uint32_t kTacMfmaRows = 128;     // rows per tile (tac_rows_per_tile(64))
 constexpr uint32_t kTacMfmaThreads = 256;
 constexpr uint32_t kTacMfmaChunk = 128;    // centroids staged in LDS at a time
@@ -1056,7 +1081,11 @@ __global__ __launch_bounds__(kTacMfmaThreads) void tac_assign_mfma_kernel(
       if (t < CH) {
         hs[t] = ph;
         // NaN bits exceed every finite value's, so a NaN h shows in hmax.
-        if (t < cnt) atomicMax(&hmax, __float_as_uint(ph) & 0x7FFFFFFFu);
+        // hmax only grows, so a value at or below what it already holds
+        // cannot change it: only the larger ones take the (serializing)
+        // atomic, after the first chunk few do.
+        const uint32_t hb = __float_as_uint(ph) & 0x7FFFFFFFu;
+        if (t < cnt && hb > hmax) atomicMax(&hmax, hb);
       }
       __syncthreads();
       if (c0 + CH < pr.k) fetch(c0 + CH);
@@ -1135,12 +1164,22 @@ __global__ __launch_bounds__(kTacMfmaThreads) void tac_assign_mfma_kernel(
       }
       // Rows a lane's two kept values could not settle: every centroid, the
       // block's work-items side by side.
+      // (each work-item keeps its own minimum, the wave reduces it, and one
+      // LDS atomic per wave and row merges them)
       for (uint32_t j = 0; j < nfull; ++j) {
         const uint32_t r = full[j];
+        unsigned long long best = ~0ull;
         for (uint32_t c = t; c < pr.k; c += kTacMfmaThreads) {
           const float d = tac_l2sq<64>(xr + r * LD, Cp + (uint64_t)c * 64, 64);
-          atomicMin(&rowkey[r], ((unsigned long long)__float_as_uint(d) << 32) | c);
+          const unsigned long long key = ((unsigned long long)__float_as_uint(d) << 32) | c;
+          best = key < best ? key : best;
         }
+#pragma unroll
+        for (int off = 1; off < 64; off <<= 1) {
+          const unsigned long long o = __shfl_xor(best, off, 64);
+          best = o < best ? o : best;
+        }
+        if (lane == 0) atomicMin(&rowkey[r], best);
       }
       __syncthreads();
       if (t < rows) {
