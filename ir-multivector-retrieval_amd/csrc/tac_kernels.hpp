@@ -990,7 +990,7 @@ __global__ __launch_bounds__(256) void tac_cnorm_kernel(const float* __restrict_
 }
 
 
-__global__ __launch_bounds__(kTacMfmaThreads) void tac_assign_mfma_kernel(
+__global__ __launch_bounds__(kTacMfmaThreads) __attribute__((amdgpu_waves_per_eu(2))) void tac_assign_mfma_kernel(
     const float* __restrict__ G, const float* __restrict__ C, const float* __restrict__ h,
     const TacProblem* __restrict__ probs, const TacTile* __restrict__ tiles,
     const uint32_t* __restrict__ done, uint32_t* __restrict__ code, float* __restrict__ e) {
@@ -1016,7 +1016,31 @@ __global__ __launch_bounds__(kTacMfmaThreads) void tac_assign_mfma_kernel(
     // the candidate queue holds 16-bit centroid indices
     if (pr.k > 0xFFFFu) exact = 1;
   }
-  tac_stage_rows(G, pr, tl.row0, R, 64, LD, xr);
+  {
+    // the tile's rows: every 16-byte load issued before the first is used
+    // (a load-store loop waited a round trip per step: 5-12 us per tile)
+    constexpr uint32_t Q = R * 16 / kTacMfmaThreads;  // 16-byte pieces per work-item
+    const tac_floatx4* src =
+        reinterpret_cast<const tac_floatx4*>(G + ((uint64_t)pr.off + tl.row0) * 64);
+    const uint32_t nq = rows * 16u;
+    tac_floatx4 v4[Q];
+#pragma unroll
+    for (uint32_t j = 0; j < Q; ++j) {
+      const uint32_t q = t + j * kTacMfmaThreads;
+      v4[j] = q < nq ? src[q] : tac_floatx4{0.0f, 0.0f, 0.0f, 0.0f};
+    }
+#pragma unroll
+    for (uint32_t j = 0; j < Q; ++j) {
+      const uint32_t q = t + j * kTacMfmaThreads;
+      if (q < nq) {
+        float* d = xr + (q >> 4) * LD + 4u * (q & 15u);
+        d[0] = v4[j].x;
+        d[1] = v4[j].y;
+        d[2] = v4[j].z;
+        d[3] = v4[j].w;
+      }
+    }
+  }
   __syncthreads();
   if (t < R) {
     float x2 = 0.0f;
@@ -1150,10 +1174,14 @@ __global__ __launch_bounds__(kTacMfmaThreads) void tac_assign_mfma_kernel(
         uint32_t over = (!(m <= thr) || b2[g][v] <= thr) ? 1u : 0u;
 #pragma unroll
         for (int off = 1; off < 16; off <<= 1) over |= __shfl_xor(over, off, 64);
-        if (r < rows) {
-          if (b1[g][v] <= thr) queue[atomicAdd(&qn, 1u)] = (r << 16) | i1[g][v];
-          if (li == 0 && over) full[atomicAdd(&nfull, 1u)] = r;
-        }
+        // list slots by a wave ballot and one LDS atomic per wave (lanes
+        // adding to one counter one by one serialize)
+        const bool cand = r < rows && b1[g][v] <= thr;
+        const uint32_t qs = tac_wave_append(cand, &qn);
+        if (cand) queue[qs] = (r << 16) | i1[g][v];
+        const bool fr = r < rows && li == 0 && over;
+        const uint32_t fs = tac_wave_append(fr, &nfull);
+        if (fr) full[fs] = r;
       }
     __syncthreads();
     if (!exact) {
