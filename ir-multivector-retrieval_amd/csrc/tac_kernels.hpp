@@ -458,13 +458,28 @@ __global__ __launch_bounds__(256) void tac_degenerate_kernel(
 
 // Stage rows [row0, row0 + rt) of a problem (zeros past its end) into LDS
 // with stride ld; every thread of the block takes part.
+// Loads go out U at a time before their stores, so a step waits one round
+// trip for U floats rather than one.
 __device__ __forceinline__ void tac_stage_rows(const float* __restrict__ G, const TacProblem& pr,
                                                uint32_t row0, uint32_t rt, uint32_t dim,
                                                uint32_t ld, float* xr) {
+  constexpr uint32_t U = 16;
   const uint32_t rows = pr.n - row0 < rt ? pr.n - row0 : rt;
+  const uint32_t total = rows * dim;
   const float* src = G + ((uint64_t)pr.off + row0) * dim;
-  for (uint32_t f = threadIdx.x; f < rows * dim; f += blockDim.x)
-    xr[(f / dim) * ld + f % dim] = src[f];
+  for (uint32_t f0 = threadIdx.x; f0 < total; f0 += U * blockDim.x) {
+    float v[U];
+#pragma unroll
+    for (uint32_t u = 0; u < U; ++u) {
+      const uint32_t f = f0 + u * blockDim.x;
+      v[u] = f < total ? src[f] : 0.0f;
+    }
+#pragma unroll
+    for (uint32_t u = 0; u < U; ++u) {
+      const uint32_t f = f0 + u * blockDim.x;
+      if (f < total) xr[(f / dim) * ld + f % dim] = v[u];
+    }
+  }
 }
 
 // ---------------------------------------------------------------------------
@@ -880,7 +895,24 @@ __global__ void tac_assign_kernel(const float* __restrict__ G, const float* __re
     const uint32_t cnt = pr.k - c0 < chunk_c ? pr.k - c0 : chunk_c;
     __syncthreads();
     const float* src = C + ((uint64_t)pr.goff + c0) * dim;
-    for (uint32_t f = threadIdx.x; f < cnt * dim; f += rt) cs[f] = src[f];
+    {
+      // up to U loads out before their stores
+      constexpr uint32_t U = 8;
+      const uint32_t total = cnt * dim;
+      for (uint32_t f0 = threadIdx.x; f0 < total; f0 += U * rt) {
+        float v[U];
+#pragma unroll
+        for (uint32_t u = 0; u < U; ++u) {
+          const uint32_t f = f0 + u * rt;
+          v[u] = f < total ? src[f] : 0.0f;
+        }
+#pragma unroll
+        for (uint32_t u = 0; u < U; ++u) {
+          const uint32_t f = f0 + u * rt;
+          if (f < total) cs[f] = v[u];
+        }
+      }
+    }
     __syncthreads();
     for (uint32_t q = 0; q < cnt; ++q) {
       const float d = tac_l2sq<DIMC>(xrow, cs + q * dim, dim);
