@@ -557,39 +557,27 @@ __global__ __launch_bounds__(kBlock) void scatter_kernel(
     }
   }
 
-  for (uint32_t c = threadIdx.x; c < 4 * K; c += blockDim.x) run[c] = 0;
-  __syncthreads();
-#pragma unroll
-  for (uint32_t r = 0; r < kRounds; ++r)
-    if (lo + (uint64_t)r * kWave + lane < hi) atomicAdd(&run[w * K + code[r]], 1u);
-  __syncthreads();
-
-  // Per code: tile-local bucket start (scan over codes), wave prefixes, and
-  // delta = global start of the tile's run - local start.
+  // This thread's codes' global run starts (start + the tile's offset),
+  // loaded now so that the scan below does not wait for them.
   const uint32_t per_c = (K + blockDim.x - 1) / blockDim.x;
   const uint32_t c0 = threadIdx.x * per_c;
-  uint32_t tot = 0;
-  for (uint32_t q = 0; q < per_c; ++q)
-    if (c0 + q < K)
-      tot += run[c0 + q] + run[K + c0 + q] + run[2 * K + c0 + q] + run[3 * K + c0 + q];
-  uint32_t ls = block_exclusive_scan(tot, wsum);
   const uint32_t* hm = hist + ((uint64_t)m * T + t) * K;
-  for (uint32_t q = 0; q < per_c; ++q) {
-    const uint32_t c = c0 + q;
-    if (c >= K) break;
-    delta[c] = start[(uint64_t)m * K + c] + hm[c] - ls;
-    uint32_t acc = ls;
-    for (uint32_t ww = 0; ww < 4; ++ww) {
-      const uint32_t v = run[ww * K + c];
-      run[ww * K + c] = acc;
-      acc += v;
-    }
-    ls = acc;
-  }
-  __syncthreads();
+  constexpr uint32_t kPre = 4;
+  uint32_t pre[kPre];
+#pragma unroll
+  for (uint32_t q = 0; q < kPre; ++q)
+    pre[q] = q < per_c && c0 + q < K ? start[(uint64_t)m * K + c0 + q] + hm[c0 + q] : 0u;
 
+  for (uint32_t c = threadIdx.x; c < 4 * K; c += blockDim.x) run[c] = 0;
+  __syncthreads();
+  // Ranking inside each round of 64: the lanes holding the same code (a
+  // match on every code bit), this lane's rank among them and their number,
+  // kept as rank | total << 16 for the placement pass.  The last lane of
+  // each code adds the number to the wave's count: one plain add per
+  // distinct code and round (the wave's LDS operations run in order).
   const uint64_t lt_mask = (lane == 0) ? 0ull : (~0ull >> (64 - lane));
   uint32_t* myrun = run + w * K;
+  uint32_t rk[kRounds];
 #pragma unroll
   for (uint32_t r = 0; r < kRounds; ++r) {
     const bool valid = lo + (uint64_t)r * kWave + lane < hi;
@@ -602,6 +590,42 @@ __global__ __launch_bounds__(kBlock) void scatter_kernel(
     }
     const uint32_t rank = __popcll(match & lt_mask);
     const uint32_t total = __popcll(match);
+    rk[r] = rank | (total << 16);
+    if (valid && rank == total - 1) myrun[cd] += total;
+    __builtin_amdgcn_wave_barrier();
+  }
+  __syncthreads();
+
+  // Per code: tile-local bucket start (scan over codes), wave prefixes, and
+  // delta = global start of the tile's run - local start.
+  uint32_t tot = 0;
+  for (uint32_t q = 0; q < per_c; ++q)
+    if (c0 + q < K)
+      tot += run[c0 + q] + run[K + c0 + q] + run[2 * K + c0 + q] + run[3 * K + c0 + q];
+  uint32_t ls = block_exclusive_scan(tot, wsum);
+  for (uint32_t q = 0; q < per_c; ++q) {
+    const uint32_t c = c0 + q;
+    if (c >= K) break;
+    uint32_t g0 = 0;
+#pragma unroll
+    for (uint32_t j = 0; j < kPre; ++j) g0 = j == q ? pre[j] : g0;
+    delta[c] = (q < kPre ? g0 : start[(uint64_t)m * K + c] + hm[c]) - ls;
+    uint32_t acc = ls;
+    for (uint32_t ww = 0; ww < 4; ++ww) {
+      const uint32_t v = run[ww * K + c];
+      run[ww * K + c] = acc;
+      acc += v;
+    }
+    ls = acc;
+  }
+  __syncthreads();
+
+#pragma unroll
+  for (uint32_t r = 0; r < kRounds; ++r) {
+    const bool valid = lo + (uint64_t)r * kWave + lane < hi;
+    const uint32_t cd = code[r];
+    const uint32_t rank = rk[r] & 0xFFFFu;
+    const uint32_t total = rk[r] >> 16;
     uint32_t lp = 0;
     if (valid) lp = myrun[cd] + rank;
     __builtin_amdgcn_wave_barrier();
