@@ -2339,6 +2339,38 @@ int tac_cluster_core(DeviceState &ds, hipStream_t s, const uint32_t *ids, uint64
     std::vector<uint32_t> cur(offs.begin(), offs.end() - 1);
     for (uint64_t i = 0; i < N; ++i) idx[cur[ids[i]]++] = (uint32_t)i;
   };
+  // The same grouping on T host threads, each over a contiguous slice of the
+  // rows: per-slice counts, then each slice's run of token j placed after the
+  // runs of the slices before it, so the order inside a token stays the
+  // input order and idx, offs and freqs equal the one-thread result.
+  auto group_threads = [&](uint32_t T) {
+    std::vector<uint32_t> cnt((size_t)T * nd, 0);
+    auto each = [&](auto fn) {
+      std::vector<std::thread> th;
+      for (uint32_t t = 1; t < T; ++t) th.emplace_back(fn, t);
+      fn(0u);
+      for (auto &x : th) x.join();
+    };
+    each([&](uint32_t t) {
+      uint32_t *c = cnt.data() + (size_t)t * nd;
+      for (uint64_t i = N * t / T, e = N * (t + 1) / T; i < e; ++i) c[ids[i]] += 1;
+    });
+    uint32_t at = 0;
+    for (uint64_t j = 0; j < nd; ++j) {
+      offs[j] = at;
+      for (uint32_t t = 0; t < T; ++t) {
+        const uint32_t v = cnt[(size_t)t * nd + j];
+        cnt[(size_t)t * nd + j] = at;
+        at += v;
+      }
+      freqs[j] = at - offs[j];
+    }
+    offs[nd] = at;
+    each([&](uint32_t t) {
+      uint32_t *c = cnt.data() + (size_t)t * nd;
+      for (uint64_t i = N * t / T, e = N * (t + 1) / T; i < e; ++i) idx[c[ids[i]]++] = (uint32_t)i;
+    });
+  };
   const size_t vbytes = (size_t)N * dim * sizeof(float);
   // G carries tac_spread_pad_floats of slack: the spread kernel's full-batch
   // loads run up to one batch past a token's last row, and the fold kernel's
@@ -2358,7 +2390,14 @@ int tac_cluster_core(DeviceState &ds, hipStream_t s, const uint32_t *ids, uint64
     if (up) return up;
     dv = as<float>(ds.tac_v);
   } else {
-    group();
+    // Nothing to overlap with here: the grouping runs on up to 8 threads when
+    // the rows are many and the per-thread counts stay small.
+    const uint32_t hc = std::thread::hardware_concurrency();
+    const uint32_t T = std::max<uint32_t>(1u, std::min<uint32_t>(8u, hc));
+    if (T > 1 && N >= (1u << 16) && (uint64_t)nd * T <= (1ull << 24))
+      group_threads(T);
+    else
+      group();
   }
   if ((st = upload_vec(ds, ds.tac_idx, idx, s)) || (st = upload_vec(ds, ds.tac_offs, offs, s)) ||
       (st = ensure(ds, ds.tac_spreads, nd * sizeof(float))))
