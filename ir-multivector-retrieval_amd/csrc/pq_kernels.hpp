@@ -707,8 +707,7 @@ __global__ __launch_bounds__(kWave) void fold_kernel(
     uint32_t K) {
   constexpr int DP = Pad<D>::value;
   constexpr uint32_t U = kFoldBatch;
-  // Padded: the D columns start on distinct banks, and the fold's reads of
-  // the next 32 members stay inside the column.
+  // Padded: the D columns start on distinct banks.
   constexpr uint32_t kCol = U * kWave + 36;
   __shared__ __attribute__((aligned(16))) float buf[kCol * DP];
   const uint32_t id = order[blockIdx.x];
@@ -753,19 +752,28 @@ __global__ __launch_bounds__(kWave) void fold_kernel(
     if (j0 + U * kWave < cnt) load_batch(j0 + U * kWave);
     const uint32_t len = cnt - j0 < U * kWave ? cnt - j0 : U * kWave;
     if (lane < (uint32_t)D) {
-      // One dependent add per member.  The reads of the next 32 members are
-      // issued before the current 32 are added, so their LDS latency hides
-      // behind the chain (they may read the column's padding, never past it).
+      // One dependent add per member, in ascending member order.  A step
+      // issues the LDS reads of 128 members together (32 16-byte reads), so
+      // their latency is paid once per 128 adds; then steps of 32, then one.
       const float* col = buf + lane * kCol;
       const float4* col4 = reinterpret_cast<const float4*>(col);
       uint32_t jj = 0;
-      float4 a[8];
+      for (; jj + 128 <= len; jj += 128) {
+        float4 a[32];
 #pragma unroll
-      for (int q = 0; q < 8; ++q) a[q] = col4[q];
+        for (int q = 0; q < 32; ++q) a[q] = col4[jj / 4 + q];
+#pragma unroll
+        for (int q = 0; q < 32; ++q) {
+          acc = acc + a[q].x;
+          acc = acc + a[q].y;
+          acc = acc + a[q].z;
+          acc = acc + a[q].w;
+        }
+      }
       for (; jj + 32 <= len; jj += 32) {
-        float4 b[8];
+        float4 a[8];
 #pragma unroll
-        for (int q = 0; q < 8; ++q) b[q] = col4[jj / 4 + 8 + q];
+        for (int q = 0; q < 8; ++q) a[q] = col4[jj / 4 + q];
 #pragma unroll
         for (int q = 0; q < 8; ++q) {
           acc = acc + a[q].x;
@@ -773,8 +781,6 @@ __global__ __launch_bounds__(kWave) void fold_kernel(
           acc = acc + a[q].z;
           acc = acc + a[q].w;
         }
-#pragma unroll
-        for (int q = 0; q < 8; ++q) a[q] = b[q];
       }
       for (; jj < len; ++jj) acc = acc + col[jj];
     }
