@@ -333,7 +333,7 @@ typedef struct tac_cluster_params {
  * Errors follow the reference's order: no tokens EmptyTokenDump; dim 0 or a
  * length mismatch InvalidThresholds; kappa_total 0 BudgetTooSmall; then the
  * phases' errors, and the first failing token's kmeans error (RngError).
- * dim above 191 is TAC_ERR_UNSUPPORTED (rows are staged in LDS), as is a
+ * dim above 512 is TAC_ERR_UNSUPPORTED (rows are staged in LDS), as is a
  * plan of 2^24 or more row tiles, tokens with centroids or wcss chunks (one
  * block each).
  */

@@ -2325,7 +2325,7 @@ int tac_cluster_core(DeviceState &ds, hipStream_t s, const uint32_t *ids, uint64
                      uint32_t *assign_out, uint32_t *kpt_out, float *wcss_out) {
   const auto wall0 = std::chrono::steady_clock::now();
   const uint32_t rt = tac_rows_per_tile(dim);
-  if (rt < 64 || dim > 192) return TAC_ERR_UNSUPPORTED;
+  if (rt < 64 || dim > kTacMaxDim) return TAC_ERR_UNSUPPORTED;
   const uint32_t per = (dim + 63) / 64;  // dimensions per lane in the wave kernels
   // 32-bit row ids; the gather grid stays below 2^31 blocks
   if (N > 0xFFFFFFFFull || (uint64_t)N * dim > (1ull << 38) || nd > 0x7FFFFFFFull)
@@ -2425,14 +2425,22 @@ int tac_cluster_core(DeviceState &ds, hipStream_t s, const uint32_t *ids, uint64
     constexpr uint64_t kSlice = 1ull << 24;  // tokens per launch (2^30 work-items)
     for (uint64_t j0 = 0; j0 < nd; j0 += kSlice) {
       const unsigned nb = (unsigned)std::min<uint64_t>(nd - j0, kSlice);
-      if (dim == 64)
+#define TAC_SPREAD(P) tac_spread_kernel<P><<<nb, kWave, lds, s>>>(G, doffs, dinv, dim, dsp, j0)
+      if (dim == 64) {
         tac_spread64_kernel<<<nb, kTacSpread64Threads, 0, s>>>(G, doffs, dinv, dsp, j0);
-      else if (per == 1)
-        tac_spread_kernel<1><<<nb, kWave, lds, s>>>(G, doffs, dinv, dim, dsp, j0);
-      else if (per == 2)
-        tac_spread_kernel<2><<<nb, kWave, lds, s>>>(G, doffs, dinv, dim, dsp, j0);
-      else
-        tac_spread_kernel<3><<<nb, kWave, lds, s>>>(G, doffs, dinv, dim, dsp, j0);
+      } else {
+        switch (per) {  // dim <= kTacMaxDim: at most 8 dimensions per lane
+          case 1: TAC_SPREAD(1); break;
+          case 2: TAC_SPREAD(2); break;
+          case 3: TAC_SPREAD(3); break;
+          case 4: TAC_SPREAD(4); break;
+          case 5: TAC_SPREAD(5); break;
+          case 6: TAC_SPREAD(6); break;
+          case 7: TAC_SPREAD(7); break;
+          default: TAC_SPREAD(8); break;
+        }
+      }
+#undef TAC_SPREAD
       LAUNCH_TRY("tac_spread_kernel");
     }
   }
@@ -2535,10 +2543,21 @@ int tac_cluster_core(DeviceState &ds, hipStream_t s, const uint32_t *ids, uint64
   if (P == 0) return TAC_ERR_BUDGET_TOO_SMALL;  // unreachable: some token has rows
 
   const size_t rows_lds = (size_t)rt * (dim + 1);
-  uint32_t chunk_c = (uint32_t)((16384 - rows_lds) / dim);
+  // the rows of a tile, then (assignment) a chunk of centroids or (k-means++
+  // round) the drawn row; rt and the budget leave room for one centroid at least
+  uint32_t chunk_c = (uint32_t)((tac_tile_lds_floats(dim) - rows_lds) / dim);
   if (chunk_c > 64) chunk_c = 64;
   const size_t upd_lds = (rows_lds + dim) * sizeof(float);
   const size_t asg_lds = (rows_lds + (size_t)chunk_c * dim) * sizeof(float);
+  // Wide rows take more than the 64 KB of dynamic LDS a launch gets by default.
+  if (upd_lds > 65536 || asg_lds > 65536) {
+    hipError_t e = hipFuncSetAttribute((const void *)tac_kpp_round_kernel<0>,
+                                       hipFuncAttributeMaxDynamicSharedMemorySize, (int)upd_lds);
+    if (e == hipSuccess)
+      e = hipFuncSetAttribute((const void *)tac_assign_kernel<0>,
+                              hipFuncAttributeMaxDynamicSharedMemorySize, (int)asg_lds);
+    if (e != hipSuccess) return hip_status("hipFuncSetAttribute(tac tile kernels)", e);
+  }
   // hist / scatter: per-code counters up to kTacMaxCodes codes, the tile's
   // codes beyond
   const size_t code_lds =
@@ -2694,15 +2713,19 @@ int tac_cluster_core(DeviceState &ds, hipStream_t s, const uint32_t *ids, uint64
       // dim 64: clusters of kTacFoldBig members or more go to the block kernel
       uint32_t *big = dim == 64 ? as<uint32_t>(ds.tac_big) : nullptr;
       if (big) HIP_TRY(hipMemsetAsync(big, 0, sizeof(uint32_t), s));
-      if (per == 1)
-        tac_fold_kernel<1><<<fb, 256, 0, s>>>(G, sorted, counts, start, cp, probs, done, C,
-                                              (uint32_t)K, dim, big);
-      else if (per == 2)
-        tac_fold_kernel<2><<<fb, 256, 0, s>>>(G, sorted, counts, start, cp, probs, done, C,
-                                              (uint32_t)K, dim, nullptr);
-      else
-        tac_fold_kernel<3><<<fb, 256, 0, s>>>(G, sorted, counts, start, cp, probs, done, C,
-                                              (uint32_t)K, dim, nullptr);
+#define TAC_FOLD(P, BIG) \
+  tac_fold_kernel<P><<<fb, 256, 0, s>>>(G, sorted, counts, start, cp, probs, done, C, (uint32_t)K, dim, BIG)
+      switch (per) {  // dim <= kTacMaxDim: at most 8 dimensions per lane
+        case 1: TAC_FOLD(1, big); break;
+        case 2: TAC_FOLD(2, nullptr); break;
+        case 3: TAC_FOLD(3, nullptr); break;
+        case 4: TAC_FOLD(4, nullptr); break;
+        case 5: TAC_FOLD(5, nullptr); break;
+        case 6: TAC_FOLD(6, nullptr); break;
+        case 7: TAC_FOLD(7, nullptr); break;
+        default: TAC_FOLD(8, nullptr); break;
+      }
+#undef TAC_FOLD
       LAUNCH_TRY("tac_fold_kernel");
       if (big) {
         tac_fold_big_kernel<<<kTacFoldBigBlocks, kTacFoldBigThreads, 0, s>>>(

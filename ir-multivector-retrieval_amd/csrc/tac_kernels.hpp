@@ -47,13 +47,26 @@ constexpr uint32_t kTacScanTiles = 32;  // tiles per scan range
 // larger problems count and rank codes within the tile's rows instead.
 constexpr uint32_t kTacMaxCodes = 12288;
 constexpr uint32_t kTacLdsFloats = 12288;  // staged rows: rt * (dim + 1) <= this
+// Rows of more than 191 floats: 64-row tiles whose staged rows (and, for the
+// assignment, a chunk of centroids) take up to kTacLdsWideFloats of LDS, which
+// holds a tile and one centroid up to kTacMaxDim floats a row (the rest of
+// the 160 KB is left to the kernels' static LDS).
+constexpr uint32_t kTacMaxDim = 512;
+constexpr uint32_t kTacLdsWideFloats = 40704;
+static_assert(64u * (kTacMaxDim + 1u) + kTacMaxDim <= kTacLdsWideFloats, "a wide tile fits");
 
 // Rows per tile (= threads of the tile kernels) for a dimension; 0 beyond the
 // supported range.
 __host__ __device__ inline uint32_t tac_rows_per_tile(uint32_t dim) {
-  for (uint32_t rt = 128; rt >= 16; rt /= 2)
+  for (uint32_t rt = 128; rt >= 64; rt /= 2)
     if (rt * (dim + 1) <= kTacLdsFloats) return rt;
-  return 0;
+  return dim <= kTacMaxDim ? 64u : 0u;
+}
+
+// LDS floats the tile kernels may take for a dimension: 64 KB up to 191
+// floats a row, kTacLdsWideFloats beyond.
+__host__ __device__ inline uint32_t tac_tile_lds_floats(uint32_t dim) {
+  return 64u * (dim + 1u) <= kTacLdsFloats ? 16384u : kTacLdsWideFloats;
 }
 
 // vec.l2sq (src/util/vec.zig:109-175) in the reference's order: dim 2 and 4
@@ -147,6 +160,11 @@ __global__ __launch_bounds__(256) void tac_gather_kernel(const float* __restrict
 typedef float tac_floatx4 __attribute__((ext_vector_type(4)));
 
 constexpr uint32_t kTacSpreadBatch = 32;
+// Rows per batch of tac_spread_kernel<PER>: two batches of B x PER floats
+// stay in registers, so wider rows take shorter batches.
+__host__ __device__ constexpr uint32_t tac_spread_batch(int per) {
+  return per <= 3 ? kTacSpreadBatch : per <= 6 ? 16u : 8u;
+}
 constexpr uint32_t kTacSpread64Rows = 64;  // rows per batch of tac_spread64_kernel
 constexpr uint32_t kTacInvMax = 1u << 24;
 
@@ -187,7 +205,7 @@ __global__ __launch_bounds__(kWave) void tac_spread_kernel(const float* __restri
     mean[u] = 0.0f;
     m2[u] = 0.0f;
   }
-  constexpr uint32_t B = kTacSpreadBatch;
+  constexpr uint32_t B = tac_spread_batch(PER);
   const float* gp = G + (uint64_t)lo * dim + lane;  // this lane's float of the next batch's row 0
   const float* ip = inv;                            // reciprocal for the next batch's row 0
   auto load = [&](float (&x)[B][PER], float (&v)[B]) {

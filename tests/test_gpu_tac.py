@@ -69,17 +69,20 @@ def test_synthetic_200k(gpu):
     _check(ids, v, 64, _feasible_kappa(ids), 5)
 
 
-@pytest.mark.parametrize("dim", [3, 16, 33, 95, 96, 100, 191])
+@pytest.mark.parametrize("dim", [3, 16, 33, 95, 96, 100, 191, 192, 256, 257, 384, 448, 512])
 def test_generic_dims(gpu, dim):
-    # generic 16-lane distances; 95 / 96 straddle the 128 / 64-row tiles
+    # generic 16-lane distances; 95 / 96 straddle the 128 / 64-row tiles, 191 /
+    # 192 the 64 KB and the wide-row LDS budgets; 4 to 8 dimensions per lane
+    # in the spread and fold waves past 192
     ids, v = synth.tac_vectors(6000, dim, 300, 1.0, 0.2, dim)
     _check(ids, v, dim, _feasible_kappa(ids, mu=20, tau=40, theta=8), 9, mu=20, tau=40,
            epsilon=4, theta=8)
 
 
-@pytest.mark.parametrize("dim", [64, 96, 191])
+@pytest.mark.parametrize("dim", [64, 96, 191, 320, 512])
 def test_spread_batch_edges(gpu, dim):
     # token sizes on either side of one, two and three 32-row spread batches
+    # (16 rows at 4 to 6 dimensions per lane, 8 rows beyond)
     # and of the 64-row batches of the dim-64 kernel, up to past its ring of
     # four (the last, partial batch is the only one with a row test), in
     # shuffled input order, with spreads that decide the budgets of tokens >=
@@ -221,7 +224,7 @@ def test_errors_match_the_reference(gpu):
     _expect(np.zeros(6, np.uint32), nan6, 2, dict(kappa_total=2, seed=0, mu=3, tau=5, epsilon=1,
                                                   theta=1), errors.InvalidThresholds)
     with pytest.raises(errors.Unsupported):
-        tac.cluster_flat(np.zeros(4, np.uint32), np.zeros((4, 200), np.float32), 200,
+        tac.cluster_flat(np.zeros(4, np.uint32), np.zeros((4, 513), np.float32), 513,
                          _params(1, 0))
     # a clean call after the errors
     ids, v = synth.tac_vectors(3000, 8, 100, 1.0, 0.2, 1)
