@@ -118,19 +118,27 @@ __host__ __device__ inline uint32_t cand_grid_side(uint32_t D) {
 // cand_pad_key(a) to the rest of the stored row nbr[m][a][L .. cand_row_len(L)).
 // Block (0, m) also clears the subspace's deferred count for the assignment
 // that follows on the same stream.
+// Keys a neighbour-table block sorts: the next power of two >= K, at least
+// 64.  They take P * 4 bytes of dynamic LDS (1 KB at K = 256), so the blocks
+// still fit on a CU beside the candidate kernel of the other stream.
+__host__ __device__ inline uint32_t nbr_keys(uint32_t K) {
+  uint32_t P = kWave;
+  while (P < K) P <<= 1;
+  return P;
+}
+
 template <int D>
 __global__ __launch_bounds__(256) void nbr_build_kernel(const float* __restrict__ cb,
                                                         uint32_t* __restrict__ nbr,
                                                         uint32_t* __restrict__ defer_count,
                                                         const uint32_t* __restrict__ done,
                                                         uint32_t K, uint32_t L) {
-  __shared__ uint32_t keys[kCandMaxK];
+  extern __shared__ uint32_t keys[];  // [nbr_keys(K)]
   const uint32_t a = blockIdx.x, m = blockIdx.y, t = threadIdx.x;
   if (a == 0 && t == 0) defer_count[m] = 0;
   if (done && done[m]) return;
   constexpr float g = cand_gamma(D);
-  uint32_t P = kWave;  // keys sorted: the next power of two >= K, at least 64
-  while (P < K) P <<= 1;
+  const uint32_t P = nbr_keys(K);
   const float* cbm = cb + (uint64_t)m * K * D;
   float ca[D];
 #pragma unroll

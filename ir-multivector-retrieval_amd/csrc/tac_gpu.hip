@@ -481,7 +481,8 @@ struct Launch {
                          uint64_t n, uint32_t M, uint32_t K, uint32_t L, uint32_t *hist,
                          uint32_t T, unsigned long long *rescans, hipStream_t s) {
     KT("nbr_build_kernel<%d>", D);
-    nbr_build_kernel<D><<<dim3(K, M), nbr_threads(K), 0, s>>>(cb, nbr, defer_count, done, K, L);
+    nbr_build_kernel<D><<<dim3(K, M), nbr_threads(K), nbr_keys(K) * sizeof(uint32_t), s>>>(
+        cb, nbr, defer_count, done, K, L);
     KT_END();
     uint32_t G = 0, cells = 0;
     constexpr uint32_t NA = cand_anchors<false>();
@@ -551,8 +552,8 @@ struct Launch {
     uint32_t cells = 1;
     for (int k = 0; k < D; ++k) cells *= G;
     KT("nbr_build_kernel<%d>", D);
-    nbr_build_kernel<D><<<dim3(K, M), nbr_threads(K), 0, s>>>(cb, nbr, defer_count, nullptr, K,
-                                                               L);
+    nbr_build_kernel<D><<<dim3(K, M), nbr_threads(K), nbr_keys(K) * sizeof(uint32_t), s>>>(
+        cb, nbr, defer_count, nullptr, K, L);
     KT_END();
     KT("grid_build_kernel<%d, %uu, %s>", D, cand_anchors<true>(), code_name<AnchorT>());
     grid_build_kernel<D, cand_anchors<true>(), AnchorT><<<dim3((cells + kBlock - 1) / kBlock, M),
