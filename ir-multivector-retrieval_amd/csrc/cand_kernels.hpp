@@ -69,8 +69,9 @@ constexpr uint32_t cand_anchors() { return TOKENS ? 3u : 2u; }
 constexpr uint32_t kCandAnchorsMax = 3;
 
 // LDS layout of cand_kernel, shared by the host launcher:
-//   lcb [K][DP] f32 | lsamp [K][8] u32: the value bits of row entries
-//   0, 7, 15, ..., 55 (all-ones past the row) | grid anchors only:
+//   lcb [K][DP] f32 | lsamp [K][8] u32: the top 16 bits of the value bits
+//   of row entries 0, 7, 15, ..., 119 (the 16 samples, two per word; all-ones
+//   past the row) | grid anchors only:
 //   lanc [cells][na] anchors (na = cand_anchors; u8 up to K = 256, else u16),
 //   lgrid [2][8] f32 (cell
 //   origin, cells per unit) |
@@ -343,7 +344,12 @@ __global__ __launch_bounds__(kCandThreads) void cand_kernel(
   const uint32_t* nbm = nbr + (uint64_t)m * K * Lr;
   const uint32_t* rows = nbm;  // row a at rows + a * rs
   const uint32_t rs = Lr;
-  for (uint32_t j = t; j < K * 8; j += blockDim.x) lsamp[j] = cand_sample(nbm + (j / 8) * Lr, L, j % 8);
+  // The 16 truncated samples of a row as 8 words, sample 2w in the low half of word w.
+  for (uint32_t j = t; j < K * 8; j += blockDim.x) {
+    const uint32_t* row = nbm + (j / 8) * Lr;
+    const uint32_t q = 2u * (j % 8u);
+    lsamp[j] = (uint32_t)cand_sample16(row, L, q) | ((uint32_t)cand_sample16(row, L, q + 1u) << 16);
+  }
   if constexpr (GRID) {
     const AnchorT* am = anchors + (uint64_t)m * cells * NA;
     for (uint32_t j = t; j < cells * NA; j += blockDim.x) lanc[j] = am[j];
@@ -426,14 +432,41 @@ __global__ __launch_bounds__(kCandThreads) void cand_kernel(
         R2 = cand_radius(U2, g);
         const uint4 s0 = *reinterpret_cast<const uint4*>(lsamp + a * 8);
         const uint4 s1 = *reinterpret_cast<const uint4*>(lsamp + a * 8 + 4);
-        const uint32_t sv[8] = {s0.x, s0.y, s0.z, s0.w, s1.x, s1.y, s1.z, s1.w};
-        // The last kept entry is read only when every sample is inside R2.
-        const float last = __uint_as_float(sv[7]) <= R2 && !row_complete
-                               ? cand_key_value(rows[a * rs + L - 1])
-                               : __builtin_inff();
-        nit = cand_items(sv, R2, last, row_complete, &deferred);
+        const uint32_t sw[8] = {s0.x, s0.y, s0.z, s0.w, s1.x, s1.y, s1.z, s1.w};
+        uint16_t sv[kCandSamples];
+#pragma unroll
+        for (uint32_t q = 0; q < 8; ++q) {
+          sv[2 * q] = (uint16_t)(sw[q] & 0xFFFFu);
+          sv[2 * q + 1] = (uint16_t)(sw[q] >> 16);
+        }
+        nit = cand_items16(sv, R2, L, row_complete, &deferred);
+        if constexpr (GRID) {
+          // A grid anchor sits farther from its vector than a previous code:
+          // the long rows' items 8-15 cost more there than the full search
+          // they would save, so such a vector is deferred past 8 items.
+          if (nit > 8u && !row_complete) {
+            nit = 0;
+            deferred = true;
+          }
+        }
       }
     }
+    // Phase 2: the wave's items, laid out by an exclusive scan of the counts.
+    // The wave's scratch holds 64 * 8 items; a vector may take up to 16, so
+    // in the rare wave whose total passes 512 the vectors above 8 items go
+    // to the deferred list (the full search) instead.
+    uint32_t incl = wave_inclusive_sum(nit);
+    uint32_t total = (uint32_t)__builtin_amdgcn_readlane((int)incl, kWave - 1);
+    if (total > 64u * 8u) {
+      if (nit > 8u) {
+        nit = 0;
+        deferred = true;
+      }
+      incl = wave_inclusive_sum(nit);
+      total = (uint32_t)__builtin_amdgcn_readlane((int)incl, kWave - 1);
+    }
+    // The bound also keeps a corrupted count inside the scratch.
+    total = min(total, 64u * 8u);
     const bool live = valid && !deferred;
     const uint64_t dm = __ballot(valid && deferred);
     if (dm) {
@@ -444,10 +477,6 @@ __global__ __launch_bounds__(kCandThreads) void cand_kernel(
         slice[(uint64_t)m * n + lo_i + at + (uint32_t)__popcll(dm & ((1ull << lane) - 1ull))] =
             (uint32_t)i;
     }
-    // Phase 2: the wave's items, laid out by an exclusive scan of the counts.
-    const uint32_t incl = wave_inclusive_sum(nit);
-    // At most 64 * 8; the bound also keeps a corrupted count inside the scratch.
-    const uint32_t total = min((uint32_t)__builtin_amdgcn_readlane((int)incl, kWave - 1), 64u * 8u);
     if (live) {
 #pragma unroll
       for (int k = 0; k < DP; ++k) gx[lane * DP + k] = k < D ? x[k] : 0.0f;
@@ -457,7 +486,7 @@ __global__ __launch_bounds__(kCandThreads) void cand_kernel(
     {
       uint16_t* gi = gitem + (incl - nit);
 #pragma unroll
-      for (uint32_t q = 0; q < 8; ++q)
+      for (uint32_t q = 0; q < kCandSamples; ++q)
         if (q < nit) gi[q] = (uint16_t)(lane | (q << 6));
     }
     wave_lds_sync();
@@ -468,7 +497,7 @@ __global__ __launch_bounds__(kCandThreads) void cand_kernel(
     // leave the minimum unchanged.
     for (uint32_t w = lane; w < total; w += kWave) {
       const uint32_t it = gitem[w];
-      const uint32_t u = it & 63u, j0 = ((it >> 6) & 7u) * kCandItem;
+      const uint32_t u = it & 63u, j0 = ((it >> 6) & 15u) * kCandItem;
       const uint32_t* row = rows + ga[u] + j0;
       uint32_t keys[kCandItem];
       {  // rows of whole items, 32-byte aligned: two 16-byte loads

@@ -26,7 +26,9 @@
 
 namespace tacgpu {
 
-constexpr uint32_t kCandList = 64;  // neighbours kept per codeword
+constexpr uint32_t kCandList = 128;   // neighbours kept per codeword (Lloyd iterations)
+constexpr uint32_t kCandListEncode = 64;  // the same for encode (grid anchors)
+constexpr uint32_t kCandSamples = 16; // row samples: entries 0, 7, 15, ..., 119
 constexpr uint32_t kCandItem = 8;   // candidates per work item
 constexpr uint32_t kCandMaxK = 1024; // codeword ids fit the key's low 14 bits as id << 4
 
@@ -79,8 +81,10 @@ constexpr uint32_t kCandNoKey = 0xFFFFFFFFu;  // value part is NaN: never inside
 // reads it evaluates a valid (distance, index) key.
 TAC_HD inline uint32_t cand_pad_key(uint32_t a) { return kCandValueMask | (a << 4); }
 
-// Row position of sample q: 0, 7, 15, ..., 55.  With b samples inside R2,
+// Row position of sample q: 0, 7, 15, ..., 119.  With b samples inside R2,
 // every row entry inside R2 lies in [0, 8b): item q covers [8q, 8q + 8).
+// Sample values never decrease along a row (keys are sorted, padding is NaN),
+// so when sample 7 lies outside R2 so do samples 8-15.
 TAC_HD inline uint32_t cand_sample_pos(uint32_t q) { return q ? 8u * q - 1u : 0u; }
 
 // Value bits of sample q of a row of L kept keys (all-ones past the row).
@@ -89,15 +93,32 @@ TAC_HD inline uint32_t cand_sample(const uint32_t* row, uint32_t L, uint32_t q) 
   return pos < L ? row[pos] & kCandValueMask : kCandNoKey;
 }
 
+// Sample q as the top 16 bits of its value bits.  Clearing low bits of a
+// non-negative float lowers it, so the truncated sample is a lower bound of
+// the entry's value (NaN padding stays NaN): a count of truncated samples
+// inside R2 is never below the count of the samples themselves.
+TAC_HD inline uint16_t cand_sample16(const uint32_t* row, uint32_t L, uint32_t q) {
+  return (uint16_t)(cand_sample(row, L, q) >> 16);
+}
+TAC_HD inline float cand_u16f(uint16_t h) { return cand_u2f((uint32_t)h << 16); }
+
+// Samples a row of L kept keys has (positions below L): 1 + L / 8, at most
+// kCandSamples.  Its items, 8 per sample, cover the stored row.
+TAC_HD constexpr uint32_t cand_row_samples(uint32_t L) {
+  return 1u + L / 8u < kCandSamples ? 1u + L / 8u : kCandSamples;
+}
+
 // Number of kCandItem-candidate items a vector needs from its anchor's row,
-// given the row's 8 samples; *deferred when all samples are inside R2, the
-// row is missing codewords (L + 1 < K) and its last kept entry is inside R2
-// too, so the candidate set may extend past the row.
-TAC_HD inline uint32_t cand_items(const uint32_t (&samples)[8], float R2, float last_value,
-                                  bool row_complete, bool* deferred) {
+// given the row's kCandSamples truncated samples.  When b truncated samples
+// are inside R2, at most b of the samples themselves are, so every row entry
+// inside R2 lies in [0, 8b).  *deferred when every sample the row has counts
+// as inside and the row is missing codewords (L + 1 < K): the candidate set
+// may then extend past the row.
+TAC_HD inline uint32_t cand_items16(const uint16_t (&samples)[kCandSamples], float R2,
+                                    uint32_t L, bool row_complete, bool* deferred) {
   uint32_t nit = 0;
-  for (int q = 0; q < 8; ++q) nit += cand_u2f(samples[q]) <= R2 ? 1u : 0u;
-  *deferred = nit == 8 && !row_complete && last_value <= R2;
+  for (uint32_t q = 0; q < kCandSamples; ++q) nit += cand_u16f(samples[q]) <= R2 ? 1u : 0u;
+  *deferred = nit >= cand_row_samples(L) && !row_complete;
   return *deferred ? 0u : nit;
 }
 
@@ -107,10 +128,10 @@ TAC_HD inline bool cand_is_candidate(uint32_t key, uint32_t j, uint32_t L, float
 }
 
 // Stored row length: the L kept keys padded with cand_pad_key to the end of
-// the last item that the samples can select (8 items when L >= 56), so every
-// item reads 8 entries without a bound check.
+// the last item that the samples can select (16 items when L >= 120), so
+// every item reads 8 entries without a bound check.
 TAC_HD constexpr uint32_t cand_row_len(uint32_t L) {
-  return 8u * (L / 8u + 1u < 8u ? L / 8u + 1u : 8u);
+  return 8u * (L / 8u + 1u < kCandSamples ? L / 8u + 1u : kCandSamples);
 }
 
 // True when a codeword whose anchor bound is lo (cand_lower_bound of its

@@ -1155,7 +1155,7 @@ int encode_core(DeviceState &ds, hipStream_t s, const float *d_x, uint64_t n, ui
   // Batches of 16,384 vectors or more take the candidate-set encode
   // (cand_kernels.hpp); TAC_GPU_FULL_SEARCH=1 keeps the full search.
   const char *full_env = getenv("TAC_GPU_FULL_SEARCH");
-  const uint32_t L = K >= 2 ? std::min<uint32_t>(kCandList, K - 1) : 0;
+  const uint32_t L = K >= 2 ? std::min<uint32_t>(kCandListEncode, K - 1) : 0;
   // Codes and grid anchors share one width: u8 up to K = 256, u16 beyond.
   const uint32_t code_size = K <= 256 ? 1u : 2u;
   const uint32_t G = cand_grid_side(D), D_pad = pad_of(D);
@@ -1525,7 +1525,7 @@ int tac_pq_encode_device_noalloc(const float *d_residuals, uint64_t n, uint32_t 
   zero_words_kernel<<<1, kWave, 0, s>>>(reinterpret_cast<uint32_t *>(counters), 6);
   LAUNCH_TRY("zero_words_kernel");
   const char *full_env = getenv("TAC_GPU_FULL_SEARCH");
-  const uint32_t L = ksub >= 2 ? std::min<uint32_t>(kCandList, ksub - 1) : 0;
+  const uint32_t L = ksub >= 2 ? std::min<uint32_t>(kCandListEncode, ksub - 1) : 0;
   bool cand = !(full_env && full_env[0] == '1') && ksub >= 2 && ksub <= 256 && n >= 16384;
   uint64_t batch = 0;
   uint32_t *count = nullptr, *nbr = nullptr, *lists = nullptr;

@@ -2,7 +2,8 @@
 // kernels (ir-multivector-retrieval_amd/csrc/cand_rules.hpp).  For random and
 // adversarial codebooks and vectors, and for any anchor codeword, the
 // candidate set that the rules select (neighbour rows of rounded-down bounds,
-// row samples, item counts, the R2 radius, deferral) must contain the
+// 16 row samples truncated to 16 bits, item counts, the R2 radius, deferral)
+// must contain the
 // reference's first-index argmin (src/util/vec.zig:271-283 over the
 // unfused fold of vec.zig:109-175), and the lexicographic (distance bits,
 // index) minimum over it must equal that argmin and its distance bit for
@@ -51,19 +52,21 @@ struct Counts {
 };
 
 static void run_case(const std::vector<float>& cb, int K, int D, const std::vector<float>& xs,
-                     int n, Counts& ct) {
+                     int n, uint32_t Lmax, Counts& ct) {
   const float g = cand_gamma(D);
-  const uint32_t L = std::min<uint32_t>(kCandList, (uint32_t)K - 1);
+  const uint32_t L = std::min<uint32_t>(Lmax, (uint32_t)K - 1);
   const bool row_complete = L + 1 >= (uint32_t)K;
   const uint32_t Lr = cand_row_len(L);
-  std::vector<uint32_t> rows((size_t)K * Lr), samples((size_t)K * 8);
+  std::vector<uint32_t> rows((size_t)K * Lr);
+  std::vector<uint16_t> samples((size_t)K * kCandSamples);
   for (int a = 0; a < K; ++a) {
     std::vector<uint32_t> keys;
     for (int c = 0; c < K; ++c)
       if (c != a) keys.push_back(cand_key(cand_lower_bound(fold(&cb[a * D], &cb[c * D], D), g), c));
     std::sort(keys.begin(), keys.end());
     for (uint32_t j = 0; j < Lr; ++j) rows[(size_t)a * Lr + j] = j < L ? keys[j] : cand_pad_key(a);
-    for (uint32_t q = 0; q < 8; ++q) samples[(size_t)a * 8 + q] = cand_sample(&rows[(size_t)a * Lr], L, q);
+    for (uint32_t q = 0; q < kCandSamples; ++q)
+      samples[(size_t)a * kCandSamples + q] = cand_sample16(&rows[(size_t)a * Lr], L, q);
   }
   for (int i = 0; i < n; ++i) {
     const float* x = &xs[(size_t)i * D];
@@ -95,11 +98,11 @@ static void run_case(const std::vector<float>& cb, int K, int D, const std::vect
         continue;
       }
       const uint32_t* row = &rows[(size_t)a * Lr];
-      uint32_t sv[8];
-      for (int q = 0; q < 8; ++q) sv[q] = samples[(size_t)a * 8 + q];
+      uint16_t sv[kCandSamples];
+      for (uint32_t q = 0; q < kCandSamples; ++q) sv[q] = samples[(size_t)a * kCandSamples + q];
       const float R2 = cand_radius(U2, g);
       bool deferred = false;
-      const uint32_t nit = cand_items(sv, R2, cand_key_value(row[L - 1]), row_complete, &deferred);
+      const uint32_t nit = cand_items16(sv, R2, L, row_complete, &deferred);
       if (nit * kCandItem > Lr) ++ct.row_overrun;  // items must stay inside the stored row
       if (deferred) {
         ++ct.deferred;
@@ -173,7 +176,9 @@ int main() {
               xs[(size_t)i * D + k] = v;
             }
           }
-          run_case(cb, K, D, xs, n, ct);
+          // the Lloyd iterations' rows and encode's shorter ones
+          run_case(cb, K, D, xs, n, kCandList, ct);
+          run_case(cb, K, D, xs, n, kCandListEncode, ct);
         }
   std::printf("cand rules: %ld checks, %ld deferred, %ld wrong; planted radius: %ld wrong, "
               "planted ties: %ld wrong\n",
