@@ -170,17 +170,19 @@ def test_token_beyond_the_lds_code_counters(gpu):
     assert r.kappa_per_token[0] > 12288
 
 
-def test_device_resident_vectors(gpu):
+@pytest.mark.parametrize("n,dim", [(40_000, 64), (70_000, 320)])
+def test_device_resident_vectors(gpu, n, dim):
     """tac_cluster_flat_device: the same token dump resident on the device
-    gives the oracle's bits, as the host entry point does."""
+    gives the oracle's bits, as the host entry point does (70,000 rows: the
+    grouping runs on several host threads; dim 320: wide-row tiles)."""
     from tac_gpu import device
-    ids, v = synth.tac_vectors(40_000, 64, 1024, 1.05, 0.15, 6)
+    ids, v = synth.tac_vectors(n, dim, 1024, 1.05, 0.15, 6)
     kap = _feasible_kappa(ids)
-    ref = orc.tac_cluster_flat(ids, v, 64, orc.tac_params(kap, 9))
+    ref = orc.tac_cluster_flat(ids, v, dim, orc.tac_params(kap, 9))
     assert ref.status == 0
     dv = device.DeviceArray.from_host(np.ascontiguousarray(v))
     try:
-        got = tac.cluster_flat(ids, dv, 64, _params(kap, 9))
+        got = tac.cluster_flat(ids, dv, dim, _params(kap, 9))
     finally:
         dv.free()
     assert np.array_equal(got.kappa_per_token, ref.kappa_per_token)
