@@ -279,8 +279,10 @@ __device__ inline uint32_t wave_inclusive_sum(uint32_t v) {
 // kSortTile vectors (the chunk is whole tiles) and writes
 // hist[m][tile][code] for the update's counting sort; the deferred vectors'
 // codes are added there by assign_list_kernel.
+// Up to dsub 4 the kernel is held to 64 VGPRs (8 waves per SIMD): two
+// 16-wave blocks then share a CU, as the LDS allows; past 64 only one fits.
 template <int D, bool GRID, bool TOKENS, typename CodeT, typename AnchorT>
-__global__ __launch_bounds__(kCandThreads) void cand_kernel(
+__global__ __launch_bounds__(kCandThreads, D <= 4 ? 8 : 4) void cand_kernel(
     const float* __restrict__ xin, const float* __restrict__ cb,
     const uint32_t* __restrict__ nbr, const AnchorT* __restrict__ anchors,
     const float* __restrict__ grid, uint16_t* __restrict__ codes, float* __restrict__ e,

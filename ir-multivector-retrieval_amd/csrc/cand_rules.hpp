@@ -26,7 +26,8 @@
 
 namespace tacgpu {
 
-constexpr uint32_t kCandList = 128;   // neighbours kept per codeword (Lloyd iterations)
+constexpr uint32_t kCandList = 128;   // neighbours kept per codeword (Lloyd iterations, dsub <= 4)
+constexpr uint32_t kCandListWide = 64;  // the same past dsub 4, where items cost more
 constexpr uint32_t kCandListEncode = 64;  // the same for encode (grid anchors)
 constexpr uint32_t kCandSamples = 16; // row samples: entries 0, 7, 15, ..., 119
 constexpr uint32_t kCandItem = 8;   // candidates per work item

@@ -858,7 +858,7 @@ int train_core(DeviceState &ds, hipStream_t s, const float *d_x, uint64_t n, uin
   // from grid anchors.  TAC_GPU_FULL_SEARCH=1 keeps the full search in every
   // iteration.
   const char *full_env = getenv("TAC_GPU_FULL_SEARCH");
-  const uint32_t Lc = K >= 2 ? std::min<uint32_t>(kCandList, K - 1) : 0;
+  const uint32_t Lc = K >= 2 ? std::min<uint32_t>(dim / M <= 4 ? kCandList : kCandListWide, K - 1) : 0;
   // Anchors (first iteration) are u8 ids up to K = 256, u16 beyond; the
   // block's tables must fit the LDS with at least one sort tile.
   const uint32_t anchor_size = K <= 256 ? 1u : 2u;
