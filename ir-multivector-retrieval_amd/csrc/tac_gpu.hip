@@ -2677,18 +2677,51 @@ int tac_cluster_core(DeviceState &ds, hipStream_t s, const uint32_t *ids, uint64
   }
   if (profile) HIP_TRY(hipEventRecord(ev1, s));
 
-  // Lloyd iterations (kmeans.zig:149-224) for every problem not yet converged
+  // Lloyd iterations (kmeans.zig:149-224) for every problem not yet converged.
+  // Problems are sorted by k, descending, and their tiles, scan ranges and
+  // wcss chunks are listed in problem order, so the problems still running
+  // lie in a prefix of each list.  At a few iterations the done flags are
+  // read back once and the per-tile, per-range, per-chunk and per-problem
+  // launches shrink to the prefix up to the last problem still running
+  // (the one-centroid tail converges within the first iterations); when
+  // none is left the loop ends.  The kernels skip finished problems
+  // themselves, so the results are those of the full launches.
+  std::vector<uint32_t> range_upto(P + 1, 0), chunk_upto(P + 1, 0);
+  for (uint32_t q = 0; q < P; ++q) {
+    range_upto[q + 1] = range_upto[q] + pl.probs[q].nranges;
+    chunk_upto[q + 1] = chunk_upto[q] + pl.probs[q].nchunks;
+  }
+  uint32_t Pa = P, NTa = NT, NRa = NR, NCHa = NCH;
+  std::vector<uint32_t> hdone;
   for (uint32_t t = 0; t < prm.max_iters; ++t) {
-    if (mfma_tiles > 0) {
+    if (t == 3 || t == 6 || t == 10 || t == 15 || t == 21) {
+      hdone.resize(P);
+      HIP_TRY(hipMemcpyAsync(hdone.data(), done, (size_t)P * sizeof(uint32_t),
+                             hipMemcpyDeviceToHost, s));
+      HIP_TRY(hipStreamSynchronize(s));
+      uint32_t qa = 0;
+      for (uint32_t q = Pa; q > 0; --q)
+        if (!hdone[q - 1]) {
+          qa = q;
+          break;
+        }
+      if (qa == 0) break;  // every problem has converged
+      Pa = qa;
+      NTa = pl.probs[qa - 1].tile0 + pl.probs[qa - 1].ntiles;
+      NRa = range_upto[qa];
+      NCHa = chunk_upto[qa];
+    }
+    const uint32_t mt = std::min(mfma_tiles, NTa);
+    if (mt > 0) {
       tac_cnorm_kernel<<<(unsigned)((K + 255) / 256), 256, 0, s>>>(
           C, as<uint32_t>(ds.tac_cprob), done, (uint32_t)K, as<float>(ds.tac_h));
       LAUNCH_TRY("tac_cnorm_kernel");
-      tac_assign_mfma_kernel<<<mfma_tiles, kTacMfmaThreads, 0, s>>>(
+      tac_assign_mfma_kernel<<<mt, kTacMfmaThreads, 0, s>>>(
           G, C, as<float>(ds.tac_h), probs, tiles, done, code, e);
       LAUNCH_TRY("tac_assign_mfma_kernel");
     }
-    if (mfma_tiles < NT) {
-      const uint32_t nt = NT - mfma_tiles;
+    if (mfma_tiles < NTa) {
+      const uint32_t nt = NTa - mfma_tiles;
       const TacTile *rest = tiles + mfma_tiles;
       if (dim == 64)
         tac_assign_kernel<64><<<nt, rt, asg_lds, s>>>(G, C, probs, rest, done, code, e, dim,
@@ -2701,12 +2734,12 @@ int tac_cluster_core(DeviceState &ds, hipStream_t s, const uint32_t *ids, uint64
                                                      chunk_c);
       LAUNCH_TRY("tac_assign_kernel");
     }
-    tac_hist_kernel<<<NT, rt, code_lds, s>>>(code, probs, tiles, done, hist);
+    tac_hist_kernel<<<NTa, rt, code_lds, s>>>(code, probs, tiles, done, hist);
     LAUNCH_TRY("tac_hist_kernel");
-    tac_scan_partial_kernel<<<NR, 256, 0, s>>>(hist, probs, ranges, done, rsum);
-    tac_scan_apply_kernel<<<NR, 256, 0, s>>>(hist, probs, ranges, done, rsum, counts, start);
+    tac_scan_partial_kernel<<<NRa, 256, 0, s>>>(hist, probs, ranges, done, rsum);
+    tac_scan_apply_kernel<<<NRa, 256, 0, s>>>(hist, probs, ranges, done, rsum, counts, start);
     LAUNCH_TRY("tac scan kernels");
-    tac_scatter_kernel<<<NT, rt, code_lds, s>>>(code, hist, start, probs, tiles, done, sorted);
+    tac_scatter_kernel<<<NTa, rt, code_lds, s>>>(code, hist, start, probs, tiles, done, sorted);
     LAUNCH_TRY("tac_scatter_kernel");
     {
       const uint32_t *cp = as<uint32_t>(ds.tac_cprob);
@@ -2734,15 +2767,15 @@ int tac_cluster_core(DeviceState &ds, hipStream_t s, const uint32_t *ids, uint64
         LAUNCH_TRY("tac_fold_big_kernel");
       }
     }
-    tac_chunk_sums_kernel<<<(NCH + 3) / 4, 256, 0, s>>>(e, probs, chl, NCH, done, pre);
-    tac_chunk_prefix_kernel<<<P, 256, 0, s>>>(pre, probs, done);
-    tac_quantize_kernel<<<(NCH + 3) / 4, 256, 0, s>>>(e, pre, probs, chl, NCH, done, fch);
-    tac_wcss_apply_kernel<<<P, kWave, 0, s>>>(e, fch, probs, done, wcss);
+    tac_chunk_sums_kernel<<<(NCHa + 3) / 4, 256, 0, s>>>(e, probs, chl, NCHa, done, pre);
+    tac_chunk_prefix_kernel<<<Pa, 256, 0, s>>>(pre, probs, done);
+    tac_quantize_kernel<<<(NCHa + 3) / 4, 256, 0, s>>>(e, pre, probs, chl, NCHa, done, fch);
+    tac_wcss_apply_kernel<<<Pa, kWave, 0, s>>>(e, fch, probs, done, wcss);
     LAUNCH_TRY("tac wcss kernels");
-    tac_reseed_kernel<<<P, 256, 0, s>>>(G, e, counts, probs, done, C,
-                                        as<uint32_t>(ds.tac_empties), dim);
+    tac_reseed_kernel<<<Pa, 256, 0, s>>>(G, e, counts, probs, done, C,
+                                         as<uint32_t>(ds.tac_empties), dim);
     LAUNCH_TRY("tac_reseed_kernel");
-    tac_converge_kernel<<<(P + 255) / 256, 256, 0, s>>>(wcss, prev, done, iters, P, t, prm.tol);
+    tac_converge_kernel<<<(Pa + 255) / 256, 256, 0, s>>>(wcss, prev, done, iters, Pa, t, prm.tol);
     LAUNCH_TRY("tac_converge_kernel");
   }
   if (profile) HIP_TRY(hipEventRecord(ev2, s));
