@@ -313,31 +313,65 @@ def kernel_table(kt: dict, steps: int, train_ms: float):
     return dict(sorted(rows.items(), key=lambda kv: -kv[1]["ms_per_step"]))
 
 
-def roofline(name: str, row: dict, n: int, dim: int, m: int, traffic: dict, valu: dict,
-             parts: int = 1):
+def algorithmic_flops(name: str, n: int, dim: int, m: int, ksub: int, parts: int = 1):
+    """FLOP a launch stands for in the reference's exhaustive scan: dsub
+    multiply-adds per (vector, subspace, codeword) pair, 2 * dim * ksub per
+    vector over all subspaces (the candidate kernels evaluate a pruned subset
+    of the pairs; the figure counts the work they replace).  None for kernels
+    that compute no distances."""
+    if name.startswith("cand_kernel") and ", true, true," in name:
+        return 2 * n * dim * ksub
+    if name.startswith("encode_kernel"):
+        return 2 * n * dim * ksub
+    if name.startswith(("cand_kernel", "assign_kernel")):
+        return 2 * n * dim * ksub // parts
+    return None
+
+
+def roofline(name: str, row: dict, n: int, dim: int, m: int, ksub: int, traffic: dict,
+             valu: dict, parts: int = 1):
+    """The dominant kernel against the roof its counters show it is bound by:
+    'valu' (fp32 vector, algorithmic FLOP against 157.3 TFLOP/s) when its
+    measured VALU issue share exceeds its HBM share, else 'hbm' (algorithmic
+    bytes against 8 TB/s).  Both shares are reported under their own names."""
     ab = algorithmic_bytes(name, n, dim, m, parts)
+    af = algorithmic_flops(name, n, dim, m, ksub, parts)
     avg_s = row["avg_ms"] * 1e-3
-    achieved = ab / avg_s / 1e9 if ab else None
+    hbm_gbs = ab / avg_s / 1e9 if ab else None
+    hbm_frac = None if hbm_gbs is None else hbm_gbs / PEAK_HBM_GBS
+    tflops = af / avg_s / 1e12 if af else None
+    v = valu.get(name) if valu else None
+    issue = v.get("valu_issue_frac") if v else None
+    valu_bound = (issue is not None and tflops is not None and hbm_frac is not None
+                  and issue > hbm_frac)
     tr = traffic.get(name) if traffic else None
     counted = None if not tr or "read_bytes" not in tr else tr["read_bytes"] + tr.get(
         "write_bytes", 0)
-    out = {
-        "kernel": name, "bound": "hbm",
-        "achieved": None if achieved is None else round(achieved, 1),
-        "peak": PEAK_HBM_GBS, "unit": "GB/s",
-        "frac": None if achieved is None else round(achieved / PEAK_HBM_GBS, 4),
+    if valu_bound:
+        out = {"kernel": name, "bound": "valu", "achieved": round(tflops, 2),
+               "peak": PEAK_FP32_TFLOPS, "unit": "TFLOP/s",
+               "frac": round(tflops / PEAK_FP32_TFLOPS, 4)}
+    else:
+        out = {"kernel": name, "bound": "hbm",
+               "achieved": None if hbm_gbs is None else round(hbm_gbs, 1),
+               "peak": PEAK_HBM_GBS, "unit": "GB/s",
+               "frac": None if hbm_frac is None else round(hbm_frac, 4)}
+    out.update({
         "traffic": counted,
+        "valu_issue_frac": issue,
+        "hbm_achieved_gbs": None if hbm_gbs is None else round(hbm_gbs, 1),
+        "hbm_frac": None if hbm_frac is None else round(hbm_frac, 4),
+        "algorithmic_flop_per_launch": af,
         "avg_launch_ms": row["avg_ms"], "algorithmic_bytes_per_launch": ab,
         "launches_per_step": row["launches_per_step"], "share_of_step": row["share_of_step"],
-    }
+    })
     if counted:
         out["counted_hbm_gbs"] = round(counted / avg_s / 1e9, 1)
         out["counted_over_algorithmic"] = round(counted / ab, 3) if ab else None
-    v = valu.get(name) if valu else None
     if v:
         c = v["counters"]
         out["valu"] = {
-            "issue_frac": v.get("valu_issue_frac"), "busy": v.get("valu_busy"),
+            "issue_frac": issue, "busy": v.get("valu_busy"),
             "lane_util": v.get("valu_lane_util"),
             "lds_bank_conflict_frac": v.get("lds_bank_conflict_frac"),
             "instr_per_launch": int(c["SQ_INSTS_VALU"]) if "SQ_INSTS_VALU" in c else None,
@@ -808,7 +842,7 @@ def main() -> int:
     valu = (_load_json(VALU_FILE) or {}).get("kernels", {})
     dominant = next(iter(kernels)) if kernels else None
     parts = max(1, int(prof.train_streams))
-    roof = (roofline(dominant, kernels[dominant], n, dim, m, traffic, valu, parts)
+    roof = (roofline(dominant, kernels[dominant], n, dim, m, ksub, traffic, valu, parts)
             if dominant else None)
     enc_names = [k for k in kernels if ", true, true," in k or k.startswith(
         ("encode_kernel", "encode_list_kernel"))]

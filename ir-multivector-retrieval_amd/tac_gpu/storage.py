@@ -144,7 +144,7 @@ def parse_header(image) -> dict:
     """parse's header checks (:764-797) with the PQ shape read from the header:
     magic, version, 1 <= pq_bits <= 16, sub_dim * pq_M == dim, dim and kappa
     non-zero, section offsets monotonic from 128 and inside the image, the
-    codebook section large enough, and the footer CRC-32.  Raises
+    footer CRC-32, then the centroid and codebook sections large enough.  Raises
     InvalidIndex / UnsupportedVersion / IndexCorrupt as the reference does."""
     b = np.frombuffer(bytes(image), np.uint8)
     if b.size < HEADER_REGION_SIZE + 8:
@@ -168,11 +168,15 @@ def parse_header(image) -> dict:
     footer = offs[-1]
     if footer + 8 > b.size:
         raise errors.InvalidIndex("footer")
-    if int(h["ilist_off"]) - int(h["pq_off"]) < pq_section_bytes(m, bits, sub):
-        raise errors.InvalidIndex("codebook section")
     stored = int(np.frombuffer(b[footer:footer + 4].tobytes(), "<u4")[0])
     if zlib.crc32(b[:footer].tobytes()) != stored:  # host CRC-32, std.hash.Crc32's
         raise errors.IndexCorrupt("footer CRC-32")
+    # Section sizes after the CRC, in parse's order: centroids (:799-802),
+    # then (past the HNSW section, not read here) parsePq's codebooks (:942).
+    if int(h["hnsw_off"]) - int(h["centroids_off"]) < int(h["kappa"]) * dim * 4:
+        raise errors.InvalidIndex("centroid section")
+    if int(h["ilist_off"]) - int(h["pq_off"]) < pq_section_bytes(m, bits, sub):
+        raise errors.InvalidIndex("codebook section")
     out = {f: int(h[f]) for f in _HEADER_DTYPE.names if f not in ("magic", "_pad0")}
     out["code_bytes"] = code_bytes_of(bits)
     out["ksub"] = 1 << bits

@@ -50,6 +50,12 @@ def cluster_flat(token_ids, vectors, dim: int, p: ClusteringParams) -> Clusterin
     ids = np.ascontiguousarray(token_ids, dtype=np.uint32).reshape(-1)
     on_device = hasattr(vectors, "ptr") and hasattr(vectors, "nbytes")
     if on_device:
+        # the device entry point reads f32 values (its length check, in the
+        # reference's error order, sees nbytes / 4 of them); an array of
+        # another dtype is refused before any call, since an f64 or integer
+        # array would otherwise be read as f32 bits
+        if np.dtype(getattr(vectors, "dtype", np.float32)) != np.float32:
+            raise errors.InvalidArgument("device vectors must be float32")
         vptr, vlen = vectors.ptr, vectors.nbytes // 4
     else:
         v = np.ascontiguousarray(vectors, dtype=np.float32).reshape(-1)

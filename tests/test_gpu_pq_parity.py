@@ -380,3 +380,36 @@ def test_kmeans_fit_kmeanspp_matches_oracle(gpu, k, seed):
     assert got.iters_run == ref.iters_run
     assert np.array_equal(got.assignments, ref.assignments)
     assert np.array_equal(_bits(got.centroids), _bits(ref.centroids))
+
+
+@pytest.mark.timeout(300)
+def test_cluster_past_2_pow_24_members(gpu):
+    """One cluster of about 16.9M members (more than 2^24): its centroid is
+    sum * fl(1.0 / fl(count)) with fl(count) rounded (src/tac/kmeans.zig:194),
+    and its fp32 sum is a serial fold of 16.9M terms in ascending row order
+    (kmeans.zig:177-184) whose running value passes 2^23, where a float's
+    spacing exceeds the terms' scale and any other order rounds differently.
+    dim 4, m 1, ksub 4, three blobs of 33,334 rows beside the big one,
+    rows interleaved; 3 Lloyd iterations with every codebook and wcss
+    compared with the oracle bit for bit."""
+    rng = np.random.default_rng(24)
+    big, small = 16_900_001, 33_334
+    n = big + 3 * small
+    centres = np.array([[0.5, 0.25, 0.75, 1.5], [-3, 0, 0, 0], [0, -3, 0, 0], [0, 0, -3, 0]],
+                       np.float32)
+    blob = np.concatenate([np.zeros(big, np.int64), np.repeat([1, 2, 3], small)])
+    blob = blob[rng.permutation(n)]
+    x = (centres[blob] + rng.standard_normal((n, 4), dtype=np.float32) * np.float32(0.01))
+    x = x.astype(np.float32)
+    init = np.stack([x[np.nonzero(blob == b)[0][0]] for b in range(4)])[None].astype(np.float32)
+    got = pq.train(x, 4, 0, m=1, ksub=4, max_iters=3, tol=NEVER, init_codebooks=init,
+                   trace=True)
+    ref = orc.pq_train(x, 4, 1, 4, init=init, max_iters=3, tol=NEVER, n_threads=16, trace=True)
+    assert ref.status == 0
+    codes = orc.pq_encode(x, 4, 1, 4, ref.trace[1], n_threads=16)
+    counts = np.bincount(codes[:, 0], minlength=4)
+    assert counts.max() > 2 ** 24 and int(np.float32(counts.max())) != counts.max()
+    for t in range(3):
+        assert np.array_equal(_bits(got.stats.trace[t]), _bits(ref.trace[t])), t
+    assert np.array_equal(_bits(got.stats.wcss), _bits(ref.wcss))
+    assert np.array_equal(_bits(got.codebooks), _bits(ref.codebooks))

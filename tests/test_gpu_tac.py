@@ -262,3 +262,15 @@ def test_full_corpus_scale_properties(gpu):
     want = (s[nz] * inv[:, None]).astype(np.float32)
     assert want.tobytes() == r.centroids[nz].tobytes()
     assert np.isfinite(r.wcss_total) and r.wcss_total > 0
+
+
+@pytest.mark.parametrize("tol,dim", [(1e-2, 64), (2e-3, 64), (5e-4, 8)])
+def test_problems_converging_around_the_readbacks(gpu, tol, dim):
+    """Loose tolerances make tokens of different k converge at different
+    iterations, on both sides of the points where the Lloyd loop reads the
+    done flags back and shrinks its launches to the unfinished problems
+    (iterations 3, 6, 10, 15 and 21), and let the loop end early through
+    the all-converged exit: centroids, assignments, kappa and wcss_total
+    equal the oracle's (kmeans.zig:214-223 per token)."""
+    ids, v = synth.tac_vectors(60_000, dim, 2048, 1.05, 0.15, 17)
+    _check(ids, v, dim, _feasible_kappa(ids), 23, max_iters=25, tol=tol)

@@ -96,8 +96,21 @@ def test_header_rejections():
         storage.parse_header(patched(20, np.uint32(8).tobytes()))
     with pytest.raises(errors.InvalidIndex):        # pq_bits out of range
         storage.parse_header(patched(24, bytes([17])))
-    with pytest.raises(errors.InvalidIndex):        # codebook section too small for 2^11
+    def recrc(image):
+        b = bytearray(image)
+        f = offs["footer_off"]
+        b[f:f + 4] = np.uint32(zlib.crc32(bytes(b[:f]))).astype("<u4").tobytes()
+        return bytes(b)
+
+    # The section sizes are checked after the footer CRC, as parse does
+    # (storage.zig:793-797, then :799-802 and parsePq :942): a short codebook
+    # section under a stale CRC is IndexCorrupt, under a valid one InvalidIndex.
+    with pytest.raises(errors.IndexCorrupt):
         storage.parse_header(patched(24, bytes([11])))
+    with pytest.raises(errors.InvalidIndex, match="codebook section"):
+        storage.parse_header(recrc(patched(24, bytes([11]))))
+    with pytest.raises(errors.InvalidIndex, match="centroid section"):  # kappa 10 -> 11
+        storage.parse_header(recrc(patched(16, np.uint32(11).tobytes())))
     with pytest.raises(errors.IndexCorrupt):        # one payload byte flipped
         pos = offs["doc_off"] + 8 * (off.size) + 5
         storage.parse_header(patched(pos, bytes([img[pos] ^ 1])))
