@@ -16,7 +16,7 @@ resident train and the 200M encode stream, and the stages around the path.
 
 Other modes:
   --traffic-pass        a short run for rocprofv3 counter passes
-  --cpu-full            the CPU baseline protocol without extrapolation
+  --cpu-protocol OUT W...   the CPU baseline protocol of workloads W (profiles)
   --summarize-pmc OUT DIR...   per-kernel summary of rocprofv3 counter CSVs
 """
 from __future__ import annotations
@@ -46,7 +46,6 @@ PEAK_VALU_GINSTR = 256 * 4 * 2.4 / 4
 NEVER = float("-inf")
 TRAFFIC_FILE = ROOT / "profiles" / f"pq_build_{WORKLOAD}_hbm_traffic.json"
 VALU_FILE = ROOT / "profiles" / f"pq_build_{WORKLOAD}_valu_counters.json"
-CPU_FULL_FILE = ROOT / "profiles" / f"cpu_baseline_{WORKLOAD}.json"
 
 
 def log(msg: str) -> None:
@@ -137,6 +136,149 @@ def cpu_baseline(x: np.ndarray, init: np.ndarray, w, gpu_cb2: np.ndarray | None,
                      f"Warm-up {warm_s:.1f} s discarded."),
         "parity_full_size_2_iters": parity,
     }
+
+
+# The CPU protocol of every workload: how much of it is timed (Lloyd
+# iterations at T, at T = 1 on 2 subspaces, vectors encoded at T = 1) and
+# for the encode stream the chunk that stands for the whole of it.
+CPU_PLAN = {
+    "chunk-117k": dict(iters_T=20, iters_T1=20, enc_T1=117_645),
+    "corpus-1.52m": dict(iters_T=20, iters_T1=2, enc_T1=100_000),
+    "corpus-1.52m-m32d2": dict(iters_T=20, iters_T1=2, enc_T1=100_000),
+    "corpus-1.52m-m8d8": dict(iters_T=20, iters_T1=2, enc_T1=100_000),
+    "corpus-1.52m-k1024": dict(iters_T=20, iters_T1=1, enc_T1=50_000),
+    "paper-60m": dict(iters_T=1, iters_T1=1, enc_T1=100_000),
+    "stream-200m": dict(chunk=10_000_000, enc_T1=100_000),
+}
+
+
+def cpu_protocol(name: str) -> dict:
+    """The CPU baseline protocol for one workload: the oracle on this host at
+    T = every available thread and T = 1, one discarded warm-up, median of 3.
+    Training workloads time CPU_PLAN's iterations of all subspaces at T
+    (all of them up to the 1.52M corpus; one for the 60M sample, scaled to
+    its 25) and iterations of the first 2 subspaces at T = 1, scaled to all
+    subspaces and iterations (subspaces train independently,
+    src/index/pq.zig:200-205); encode runs the whole workload at T and a
+    prefix at T = 1.  The 200M stream times the encode of its first 10M
+    chunk, scaled x20.  Every scaled figure is labelled."""
+    from oracle import binding as orc
+    from tac_gpu import synth
+
+    w = synth.WORKLOADS[name]
+    plan = CPU_PLAN[name]
+    T = host_threads()
+    t0 = time.perf_counter()
+    rec = {"workload": name, "n": w.n, "dim": w.dim, "m": w.m, "dsub": w.dsub, "ksub": w.ksub,
+           "threads": T, "cores": T, "kind": "port", "host_cpu": host_cpu(), "median_of": 3,
+           "warmup_discarded": 1}
+    if name == "stream-200m":
+        chunk = plan["chunk"]
+        x = synth.residuals(w, chunk)
+        rec["generate_s"] = round(time.perf_counter() - t0, 1)
+        cb = synth.gauss_codebooks(w.seed, w.m, w.ksub, w.dsub, 0.05)
+        orc.pq_encode(x, w.dim, w.m, w.ksub, cb, n_threads=T)  # warm-up
+        t_enc, _ = median_of(lambda: orc.pq_encode(x, w.dim, w.m, w.ksub, cb, n_threads=T))
+        ns = plan["enc_T1"]
+        t1_enc, _ = median_of(lambda: orc.pq_encode(x[:ns], w.dim, w.m, w.ksub, cb,
+                                                    n_threads=1))
+        scale = w.n / chunk
+        rec.update({
+            "value": round(t_enc * scale, 2), "unit": "s per 200M-vector encode",
+            "encode_mvec_per_s": round(chunk / t_enc / 1e6, 3),
+            "t1_encode_mvec_per_s": round(ns / t1_enc / 1e6, 4),
+            "t1_s_per_200m": round(t1_enc / ns * w.n, 1),
+            "extrapolated": True,
+            "sample": (f"T={T}: encode of the first {chunk:,}-vector chunk (median of 3), "
+                       f"scaled x{scale:.0f} to {w.n:,}; T=1: {ns:,} vectors, scaled.")})
+        return rec
+    x = synth.residuals(w)
+    init = synth.shuffle_init(x, w.m, w.ksub, w.seed)
+    rec["generate_s"] = round(time.perf_counter() - t0, 1)
+    it_T, it_1 = plan["iters_T"], plan["iters_T1"]
+    ref = orc.pq_train(x, w.dim, w.m, w.ksub, init=init, max_iters=min(2, w.iters), tol=NEVER,
+                       n_threads=T)  # warm-up; its codebooks serve the encode timing
+    assert ref.status == 0
+    t_train, _ = median_of(lambda: orc.pq_train(x, w.dim, w.m, w.ksub, init=init,
+                                                 max_iters=it_T, tol=NEVER, n_threads=T))
+    t_enc, _ = median_of(lambda: orc.pq_encode(x, w.dim, w.m, w.ksub, ref.codebooks,
+                                               n_threads=T))
+    d2 = 2 * w.dsub
+    x2 = np.ascontiguousarray(x[:, :d2])
+    t1_train, _ = median_of(lambda: orc.pq_train(x2, d2, 2, w.ksub, init=init[:2],
+                                                  max_iters=it_1, tol=NEVER, n_threads=1))
+    del x2
+    ns = min(plan["enc_T1"], w.n)
+    t1_enc, _ = median_of(lambda: orc.pq_encode(x[:ns], w.dim, w.m, w.ksub, ref.codebooks,
+                                                n_threads=1))
+    rec.update({
+        "lloyd_iters": w.iters,
+        "value": round(t_train / it_T * w.iters, 3), "unit": f"s/{w.iters} iters",
+        "encode_mvec_per_s": round(w.n / t_enc / 1e6, 3),
+        "t1_train_s": round(t1_train / it_1 * w.iters * (w.m / 2), 2),
+        "t1_encode_mvec_per_s": round(ns / t1_enc / 1e6, 4),
+        "extrapolated": it_T < w.iters,
+        "sample": (f"T={T}: median of 3 runs of {it_T} Lloyd iteration(s) of all {w.m} "
+                   f"subspaces over all {w.n:,} vectors"
+                   + (f", scaled x{w.iters / it_T:g} to {w.iters}" if it_T < w.iters else
+                      " (not extrapolated)")
+                   + f"; encode of all {w.n:,} vectors. T=1: {it_1} iteration(s) of the "
+                     f"first 2 subspaces, scaled to {w.iters} iterations x {w.m} subspaces"
+                     f"; encode of {ns:,} vectors.")})
+    return rec
+
+
+def cpu_profile_row(name: str, gpu_s: float | None = None, gpu_enc_mvec: float | None = None):
+    """The committed CPU protocol record of a workload
+    (profiles/cpu_baseline_<name>.json, written by --cpu-protocol on the GPU
+    box's host), with the speed-ups of this run's GPU figures over it."""
+    rec = _load_json(ROOT / "profiles" / f"cpu_baseline_{name}.json")
+    if not rec:
+        return None
+    keys = ("value", "unit", "encode_mvec_per_s", "threads", "t1_train_s",
+            "t1_encode_mvec_per_s", "t1_s_per_200m", "kind", "host_cpu", "extrapolated",
+            "sample")
+    row = {k: rec[k] for k in keys if k in rec}
+    row["source"] = f"profiles/cpu_baseline_{name}.json"
+    if gpu_s and "value" in rec:
+        row["speedup_train_or_stream"] = round(rec["value"] / gpu_s, 1)
+    if gpu_enc_mvec and rec.get("encode_mvec_per_s"):
+        row["speedup_encode"] = round(gpu_enc_mvec / rec["encode_mvec_per_s"], 1)
+    return row
+
+
+def write_cpu_profile(out_dir: Path, rec: dict, command: str) -> None:
+    """profiles-style JSON and Markdown summary of one cpu_protocol record."""
+    out_dir.mkdir(parents=True, exist_ok=True)
+    stem = f"cpu_baseline_{rec['workload']}"
+    (out_dir / f"{stem}.json").write_text(json.dumps(rec, indent=1) + "\n")
+    stream = rec["workload"] == "stream-200m"
+    lines = [
+        f"# CPU baseline, {rec['workload']} ({rec['n']:,} x {rec['dim']} fp32, "
+        f"m{rec['m']} dsub {rec['dsub']} k{rec['ksub']})", "",
+        "The oracle (`oracle/pq_oracle.c`, the C restatement of the reference's `pq.train` / "
+        "`PQ.encode` with its threading: work stealing over subspaces, static chunks inside a "
+        "subspace and for encode; built `-O3 -march=x86-64-v3 -ffp-contract=off`) on the GPU "
+        "box's host cores. No Zig toolchain exists in this image, so the reference itself "
+        "cannot be timed (`kind: port`).", "",
+        f"Protocol: {rec['sample']} One discarded warm-up, median of 3 runs of each timing.", "",
+        f"Command (on the GPU box): `{command}`", ""]
+    if stream:
+        lines += ["| host CPU | threads | s per 200M encode (scaled) | encode Mvec/s | "
+                  "T=1 encode Mvec/s | T=1 s per 200M (scaled) |",
+                  "|---|---:|---:|---:|---:|---:|",
+                  f"| {rec['host_cpu']} | {rec['threads']} | {rec['value']} | "
+                  f"{rec['encode_mvec_per_s']} | {rec['t1_encode_mvec_per_s']} | "
+                  f"{rec['t1_s_per_200m']} |"]
+    else:
+        lines += [f"| host CPU | threads | pq.train {rec['unit']}"
+                  f"{' (scaled)' if rec['extrapolated'] else ''} | pq.encode Mvec/s | "
+                  f"T=1 pq.train s (scaled) | T=1 pq.encode Mvec/s |",
+                  "|---|---:|---:|---:|---:|---:|",
+                  f"| {rec['host_cpu']} | {rec['threads']} | {rec['value']} | "
+                  f"{rec['encode_mvec_per_s']} | {rec['t1_train_s']} | "
+                  f"{rec['t1_encode_mvec_per_s']} |"]
+    (out_dir / f"{stem}.md").write_text("\n".join(lines) + "\n")
 
 
 # ---------------------------------------------------------------------------
@@ -609,6 +751,21 @@ def train_encode_timing(device, dx, n, dim, m, ksub, dinit, steps, warmup):
         tr.append(t1 - t0)
         en.append(time.perf_counter() - t1)
     p = device.profile_read(reset=True)
+    # one more encode alone: the share of vectors its candidate pass deferred
+    device.encode_device(dx, n, dim, m, ksub, dcb, dcodes)
+    device.synchronize()
+    pe = device.profile_read(reset=True)
+    p.encode_deferred_frac = pe.cand_deferred / max(pe.cand_vectors, 1)
+    # the train-then-encode entry: its encode stage is one candidate pass
+    # anchored at the last Lloyd codes (device time of that pass)
+    te = []
+    for _ in range(steps):
+        device.profile_read(reset=True)
+        device.train_encode_device(dx, n, dim, m, ksub, dinit, dcb, dcodes, 20, NEVER)
+        device.synchronize()
+        q = device.profile_read(reset=True)
+        te.append(q.encode_ms / max(q.encode_launches, 1))
+    p.train_encode_stage_ms = statistics.median(te)
     device.profile_kernels(reset=True)
     device.profile_enable(False)
     dcb.free()
@@ -637,10 +794,16 @@ def shape_sweep(device, dx, x, steps: int):
             "encode_s": round(t_en, 6), "encode_mvec_per_s": round(w.n / t_en / 1e6, 1),
             "encode_stage_ms": round(enc_ms, 4),
             "encode_hbm_frac": round(ebytes / (enc_ms * 1e-3) / 1e9 / PEAK_HBM_GBS, 4),
+            "train_encode_entry_stage_ms": round(p.train_encode_stage_ms, 4),
+            "train_encode_entry_hbm_frac": round(
+                ebytes / (p.train_encode_stage_ms * 1e-3) / 1e9 / PEAK_HBM_GBS, 4),
             "update_ms_per_iter": round(p.update_ms / max(p.update_iters, 1), 4),
             "assign_ms_per_iter": round(p.assign_ms / max(p.assign_launches, 1), 4),
             "train_streams": int(p.train_streams),
+            "candidate_deferred_frac_train": round(p.cand_deferred / max(p.cand_vectors, 1), 5),
+            "candidate_deferred_frac_encode": round(p.encode_deferred_frac, 5),
         }
+        rows[name]["cpu_baseline"] = cpu_profile_row(name, t_tr, w.n / t_en / 1e6)
         log(f"{name}: {rows[name]}")
     return rows
 
@@ -684,7 +847,8 @@ def paper_60m(device, steps: int):
             "train_streams": int(p.train_streams),
             "resident_input_gb": round(w.n * w.dim * 4 / 1e9, 2),
             "device_generation_s": round(gen_s, 2), "timed_runs": steps,
-            "data": "synthetic, generated on the device"}
+            "data": "synthetic, generated on the device",
+            "cpu_baseline": cpu_profile_row("paper-60m", t)}
 
 
 def stream_200m(device):
@@ -703,6 +867,7 @@ def stream_200m(device):
     device.encode_device(dx, chunk, w.dim, w.m, w.ksub, dcb, dcodes)  # warm-up
     device.synchronize()
     enc = []
+    deferred = vectors = 0
     hist = np.zeros(w.ksub, np.int64)
     t_all = time.perf_counter()
     for k in range(w.n // chunk):
@@ -713,6 +878,8 @@ def stream_200m(device):
         p = device.profile_read(reset=True)
         device.profile_enable(False)
         enc.append(p.encode_ms)
+        deferred += p.cand_deferred
+        vectors += p.cand_vectors
         if k == 0:
             hist += np.bincount(dcodes.to_host().reshape(-1), minlength=w.ksub)
     wall = time.perf_counter() - t_all
@@ -730,7 +897,10 @@ def stream_200m(device):
             "hbm_frac": round(nbytes / (tot_ms * 1e-3) / 1e9 / PEAK_HBM_GBS, 4),
             "stream_wall_s": round(wall, 2),
             "codes_in_range_chunk0": int(hist.sum()) == chunk * w.m,
-            "data": "synthetic, generated on the device chunk by chunk"}
+            "candidate_deferred_frac": round(deferred / max(vectors, 1), 5),
+            "data": "synthetic, generated on the device chunk by chunk",
+            "cpu_baseline": cpu_profile_row("stream-200m", tot_ms * 1e-3,
+                                            w.n / (tot_ms * 1e-3) / 1e6)}
 
 
 # ---------------------------------------------------------------------------
@@ -746,8 +916,9 @@ def main() -> int:
                     help="short run for hardware-counter passes: one 2-iteration train, one "
                          "encode, one residual-stage call and a 1 GiB device-to-device copy "
                          "(the calibration kernel)")
-    ap.add_argument("--cpu-full", action="store_true",
-                    help="the CPU baseline protocol over all 20 iterations, printed as JSON")
+    ap.add_argument("--cpu-protocol", nargs="+", metavar=("OUT_DIR", "WORKLOAD"),
+                    help="the CPU baseline protocol of each named workload; writes "
+                         "OUT_DIR/cpu_baseline_<workload>.json and .md")
     ap.add_argument("--summarize-pmc", nargs="+", metavar=("OUT", "DIR"),
                     help="write OUT.json and OUT.md: per-kernel averages of rocprofv3 counter "
                          "CSVs in DIRs")
@@ -766,13 +937,18 @@ def main() -> int:
 
     from tac_gpu import device, errors, lib, synth
 
-    w = synth.WORKLOADS[WORKLOAD]
-    if args.cpu_full:
-        x = synth.residuals(w)
-        init = synth.shuffle_init(x, w.m, w.ksub, w.seed)
-        print(json.dumps(cpu_baseline(x, init, w, None, full=True)), flush=True)
+    if args.cpu_protocol:
+        if len(args.cpu_protocol) < 2:
+            ap.error("--cpu-protocol OUT_DIR WORKLOAD [WORKLOAD ...]")
+        out_dir = Path(args.cpu_protocol[0])
+        for name in args.cpu_protocol[1:]:
+            t0 = time.perf_counter()
+            rec = cpu_protocol(name)
+            write_cpu_profile(out_dir, rec, f"python3 bench.py --cpu-protocol profiles {name}")
+            log(f"cpu protocol {name}: {json.dumps(rec)} ({time.perf_counter() - t0:.0f} s)")
         return 0
 
+    w = synth.WORKLOADS[WORKLOAD]
     errors.check(lib.tac_gpu_set_device(0))
     info = device.device_info(0)
     info["name"] = info["name"] or info["arch"]
@@ -833,7 +1009,22 @@ def main() -> int:
     device.synchronize()
     prof = device.profile_read(reset=True)
     kt = device.profile_kernels(reset=True)
+    # The train-then-encode entry (storage.build's chain): whole-call wall
+    # time and the device time of its encode pass, which is anchored at the
+    # last Lloyd codes instead of grid cells.
+    te_wall, te_stage = [], []
+    for i in range(args.steps):
+        device.train_encode_device(dx, n, dim, m, ksub, dinit, dcb, dcodes, iters, NEVER)
+        device.synchronize()
+        q = device.profile_read(reset=True)
+        te_stage.append(q.encode_ms / max(q.encode_launches, 1))
+    device.profile_kernels(reset=True)
     device.profile_enable(False)
+    for i in range(args.steps):  # wall time without the per-kernel events
+        t0 = time.perf_counter()
+        device.train_encode_device(dx, n, dim, m, ksub, dinit, dcb, dcodes, iters, NEVER)
+        device.synchronize()
+        te_wall.append(time.perf_counter() - t0)
     mean_train = float(np.mean(train_s))
     mean_encode = float(np.mean(encode_s))
     step_ms = 1e3 * (mean_train + mean_encode)
@@ -873,6 +1064,12 @@ def main() -> int:
         "encode_s": round(mean_encode, 6),
         "encode_mvec_per_s": round(n / mean_encode / 1e6, 2),
         "roofline": roof,
+        "train_encode_entry": {
+            "call_s": round(statistics.median(te_wall), 5),
+            "encode_stage_ms": round(statistics.median(te_stage), 4),
+            "encode_hbm_frac": round(n * (4 * dim + m) / (statistics.median(te_stage) * 1e-3)
+                                     / 1e9 / PEAK_HBM_GBS, 4),
+            "anchors": "last Lloyd codes (tac_pq_train_encode_device)"},
         "encode_roofline": {
             "stage": " + ".join(enc_names) if enc_names else None,
             "avg_stage_ms": round(enc_ms, 4), "algorithmic_bytes": ebytes,
@@ -944,12 +1141,9 @@ def main() -> int:
         log(f"CPU baseline (oracle) on {host_threads()} threads")
         cpu = cpu_baseline(x, init, w, gpu_cb2)
         out["parity_full_size_2_iters_bit_exact"] = cpu.pop("parity_full_size_2_iters")
-        full = _load_json(CPU_FULL_FILE)
+        full = cpu_profile_row(WORKLOAD)
         if full:
-            cpu["full_protocol"] = {k: full.get(k) for k in (
-                "value", "encode_mvec_per_s", "threads", "t1_train_s_per_20_iters",
-                "t1_encode_mvec_per_s", "host_cpu", "extrapolated")}
-            cpu["full_protocol"]["source"] = str(CPU_FULL_FILE.relative_to(ROOT))
+            cpu["full_protocol"] = full
         out["cpu_baseline"] = cpu
         out["speedup_vs_cpu_train"] = round(cpu["value"] / mean_train, 1)
         out["speedup_vs_cpu_encode"] = round(out["encode_mvec_per_s"] / cpu["encode_mvec_per_s"],

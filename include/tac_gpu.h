@@ -149,6 +149,23 @@ int tac_pq_train_device(const float *d_residuals, uint64_t n, uint32_t dim,
                         void *stream);
 
 /*
+ * pq.train followed by PQ.encode of the same residuals, the way
+ * storage.build chains them (src/index/storage.zig:380-401; train at :380,
+ * the token-major encode loop at :384-401): d_codebooks_out as
+ * tac_pq_train_device, and d_codes_out [n][m] (uint8_t, uint16_t past
+ * ksub 256) equal to tac_pq_encode_device's codes for those codebooks.  The
+ * encode runs as one more candidate pass anchored at the last Lloyd codes
+ * (no grid anchors; the argmin is exact for any anchor); configurations
+ * without the candidate tables (ksub > 1024, n < 16,384 with one
+ * iteration, n <= ksub, max_iters 0) run tac_pq_encode_device's path.
+ */
+int tac_pq_train_encode_device(const float *d_residuals, uint64_t n, uint32_t dim,
+                               uint32_t m, uint32_t ksub, const float *d_init_codebooks,
+                               uint64_t seed, uint32_t max_iters, float tol,
+                               float *d_codebooks_out, void *d_codes_out,
+                               tac_pq_train_extras *extras, void *stream);
+
+/*
  * PQ.encode (src/index/pq.zig:59-76) for n residuals at once, as
  * storage.build drives it (src/index/storage.zig:384-401): codes_out is
  * token-major [n][m] (uint8_t for ksub <= 256, else uint16_t).
@@ -182,10 +199,14 @@ int tac_pq_decode(const void *codes, uint64_t n, uint32_t dim, uint32_t m,
                   uint32_t ksub, const float *codebooks, float *out);
 
 /*
- * kmeans.fit (src/tac/kmeans.zig:67-232) for one set of vectors of dim <= 8:
+ * kmeans.fit (src/tac/kmeans.zig:67-232) for one set of vectors:
  * centroids_out [k][dim], assignments_out [n] (the last iteration's
  * assignment, KMeansResult.assignments), wcss_out and iters_run_out.
  * init_centroids NULL selects k-means++ seeded with `seed`, as tac_pq_train.
+ * Distances are vec.l2sq at the vectors' dim (src/util/vec.zig:109-175).
+ * dim <= 8 (k <= 1024) runs on the PQ kernels; 9 <= dim <= 512 (any k) on
+ * the token-clustering engine as one problem; wider rows are
+ * TAC_ERR_UNSUPPORTED.
  */
 int tac_kmeans_fit(const float *vectors, uint64_t n, uint32_t dim, uint32_t k,
                    uint32_t max_iters, float tol, uint64_t seed,

@@ -1114,6 +1114,17 @@ __global__ void widen_codes_kernel(const uint16_t* __restrict__ codes, uint32_t*
   if (i < n) out[i] = codes[i];
 }
 
+// Codes [M][n] u16 -> token-major rows [n][M] of CodeT (PQ.encode's layout,
+// src/index/storage.zig:384-401): reads coalesced per subspace, each thread
+// writes its row's M codes.
+template <typename CodeT>
+__global__ void codes_to_tokens_kernel(const uint16_t* __restrict__ codes, CodeT* __restrict__ out,
+                                       uint64_t n, uint32_t M) {
+  const uint64_t i = (uint64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (i >= n) return;
+  for (uint32_t m = 0; m < M; ++m) out[i * M + m] = (CodeT)codes[(uint64_t)m * n + i];
+}
+
 // ---------------------------------------------------------------------------
 // PQ.encode (src/index/pq.zig:59-76) over token-major residuals.  One block =
 // one subspace m and kBlock*VPT consecutive vectors (the assignment kernel's

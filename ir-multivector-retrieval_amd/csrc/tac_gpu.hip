@@ -712,6 +712,8 @@ struct TrainOut {
   tac_pq_train_extras *ex;   // host extras or null
   float *h_wcss_single;      // host scalar (kmeans.fit) or null
   uint32_t *h_iters_single;  // host scalar (kmeans.fit) or null
+  void *codes_out = nullptr;  // device token-major [n][M] codes (u8, u16 past K = 256) or null
+  bool *encoded = nullptr;    // set when train_core wrote codes_out itself
 };
 
 // A run of consecutive subspaces [m0, m0 + Mh) and the stream it runs on.
@@ -1076,6 +1078,60 @@ int train_core(DeviceState &ds, hipStream_t s, const float *d_x, uint64_t n, uin
     HIP_TRY(hipStreamWaitEvent(s, ds.aux_join[h - 1], 0));
   }
   if (st) return st;
+  // Encode of the residuals just trained on, as storage.build chains train
+  // and encode (src/index/storage.zig:380-401): one more candidate pass with
+  // the final codebooks, anchored at the last Lloyd codes (any anchor gives
+  // the exact argmin; these are the nearest at hand), over every subspace,
+  // then the codes turned token-major.  Without the candidate tables the
+  // caller runs the ordinary encode.
+  if (out.codes_out && (cand || cand_first) && max_iters >= 1) {
+    hipEvent_t ea = nullptr, eb = nullptr;
+    if (profile) {
+      if ((st = event_at(ds, ev++, &ea)) || (st = event_at(ds, ev++, &eb))) return st;
+      HIP_TRY(hipEventRecord(ea, s));
+    }
+    if (H > 1) {
+      HIP_TRY(hipEventRecord(ds.aux_fork, s));
+      for (uint32_t h = 1; h < H; ++h) HIP_TRY(hipStreamWaitEvent(halves[h].s, ds.aux_fork, 0));
+    }
+    for (uint32_t h = 0; h < H && !st; ++h) {
+      const uint32_t m0 = halves[h].m0, Mh = halves[h].Mh;
+      hipStream_t hs = halves[h].s;
+      StreamScope scope(hs);
+      uint32_t *done_h = done + m0;
+      HIP_TRY(hipMemsetAsync(done_h, 0, Mh * sizeof(uint32_t), hs));  // every subspace
+      uint32_t *nbr_h = as<uint32_t>(ds.cand_nbr) + (size_t)m0 * K * cand_row_len(Lc);
+      uint32_t *slices_h = slices_all + (size_t)m0 * n;
+      uint32_t *defer_h = slices_all + (size_t)M * n + (size_t)m0 * n;
+      DISPATCH_D_ST(D, assign_cand<false>(xs + (size_t)m0 * n * DP, out.cb + (size_t)m0 * K * D,
+                                          nbr_h, (uint8_t *)nullptr, nullptr,
+                                          codes + (size_t)m0 * n, e + (size_t)m0 * n, slices_h,
+                                          defer_h, as<uint32_t>(ds.cand_count) + m0, done_h, n,
+                                          Mh, K, Lc, hist + (size_t)m0 * T * K, T, rescans, hs));
+    }
+    for (uint32_t h = 1; h < H; ++h) {
+      HIP_TRY(hipEventRecord(ds.aux_join[h - 1], halves[h].s));
+      HIP_TRY(hipStreamWaitEvent(s, ds.aux_join[h - 1], 0));
+    }
+    if (st) return st;
+    LAUNCH_TRY("final candidate pass");
+    const unsigned tb = (unsigned)((n + 255) / 256);
+    if (K <= 256)
+      codes_to_tokens_kernel<uint8_t><<<tb, 256, 0, s>>>(codes, (uint8_t *)out.codes_out, n, M);
+    else
+      codes_to_tokens_kernel<uint16_t><<<tb, 256, 0, s>>>(codes, (uint16_t *)out.codes_out, n, M);
+    LAUNCH_TRY("codes_to_tokens_kernel");
+    if (profile) {
+      HIP_TRY(hipEventRecord(eb, s));
+      HIP_TRY(hipEventSynchronize(eb));
+      float ms = 0.0f;
+      HIP_TRY(hipEventElapsedTime(&ms, ea, eb));
+      std::lock_guard<std::mutex> g(g_profile_mu);
+      g_prof.encode_ms += ms;
+      g_prof.encode_launches += 1;
+    }
+    if (out.encoded) *out.encoded = true;
+  }
   if (out.d_assign && max_iters == 0) HIP_TRY(hipMemsetAsync(codes, 0, n * sizeof(uint16_t), s));
   if (out.d_assign) {
     widen_codes_kernel<<<(unsigned)((n + 255) / 256), 256, 0, s>>>(codes, out.d_assign, n);
@@ -1272,6 +1328,25 @@ int scratch_address(int dev, uint8_t **out) {
 // ===========================================================================
 // C ABI
 // ===========================================================================
+namespace {
+// One kmeans.fit problem run through the token engine (tac_kmeans_fit at
+// dims past the PQ kernels'): every row belongs to token 0, which gets k
+// centroids without the spreads and budget phases; init (k x dim, host),
+// when given, replaces k-means++; the problem's iteration count goes to
+// *iters_out.
+struct TacFixedFit {
+  uint32_t k;
+  const float *init;
+  uint32_t *iters_out;
+};
+
+int tac_cluster_core(DeviceState &ds, hipStream_t s, const uint32_t *ids, uint64_t N,
+                     const float *vectors, bool vectors_on_device, uint32_t dim,
+                     const tac_cluster_params &prm, uint64_t nd, float *cent_out,
+                     uint32_t *assign_out, uint32_t *kpt_out, float *wcss_out,
+                     const TacFixedFit *fixed = nullptr);
+}  // namespace
+
 extern "C" {
 
 const char *tac_gpu_strerror(int status) {
@@ -1444,6 +1519,34 @@ int tac_pq_train_device(const float *d_residuals, uint64_t n, uint32_t dim, uint
                nullptr};
   st = train_core(*ds, s, d_residuals, n, dim, m, ksub, max_iters, tol, out);
   if (st) return st;
+  return end_call(*ds, s);
+}
+
+int tac_pq_train_encode_device(const float *d_residuals, uint64_t n, uint32_t dim, uint32_t m,
+                               uint32_t ksub, const float *d_init_codebooks, uint64_t seed,
+                               uint32_t max_iters, float tol, float *d_codebooks_out,
+                               void *d_codes_out, tac_pq_train_extras *extras, void *stream) {
+  int st = validate_pq(n, dim, m, ksub);
+  if (st) return st;
+  if (!d_residuals || !d_codebooks_out || !d_codes_out) return TAC_ERR_INVALID_ARGUMENT;
+  DeviceState *ds = nullptr;
+  if ((st = acquire_device(&ds, nullptr))) return st;
+  std::lock_guard<std::mutex> g(ds->mu);
+  hipStream_t s;
+  if ((st = resolve_stream(*ds, stream, &s))) return st;
+  if ((st = begin_call(*ds, s))) return st;
+  const size_t cb_bytes = (size_t)m * ksub * (dim / m) * sizeof(float);
+  if (d_init_codebooks && d_init_codebooks != d_codebooks_out)
+    HIP_TRY(hipMemcpyAsync(d_codebooks_out, d_init_codebooks, cb_bytes, hipMemcpyDeviceToDevice,
+                           s));
+  bool encoded = false;
+  TrainOut out{d_codebooks_out, d_init_codebooks == nullptr, seed, nullptr, extras, nullptr,
+               nullptr, d_codes_out, &encoded};
+  st = train_core(*ds, s, d_residuals, n, dim, m, ksub, max_iters, tol, out);
+  if (st) return st;
+  if (!encoded &&
+      (st = encode_core(*ds, s, d_residuals, n, dim, m, ksub, d_codebooks_out, d_codes_out)))
+    return st;
   return end_call(*ds, s);
 }
 
@@ -1657,7 +1760,11 @@ int tac_kmeans_fit(const float *vectors, uint64_t n, uint32_t dim, uint32_t k,
   if (k == 0) return TAC_ERR_KMEANS_BUDGET_TOO_SMALL;
   if (dim == 0) return TAC_ERR_DIM_MISMATCH;
   if (n == 0) return TAC_ERR_EMPTY_VECTOR_SET;
-  if (dim > kMaxDsub || k > kMaxKsub || n > 0xFFFFFFFFull) return TAC_ERR_UNSUPPORTED;
+  // dims up to 8 run on the PQ kernels (one subspace of the whole vector);
+  // wider rows, up to 512 floats, on the token-clustering engine as a single
+  // problem.  Both compute vec.l2sq in the reference's form for the dim.
+  const bool wide = dim > kMaxDsub;
+  if ((wide ? dim > kTacMaxDim : k > kMaxKsub) || n > 0xFFFFFFFFull) return TAC_ERR_UNSUPPORTED;
   if (!vectors || !centroids_out || !assignments_out) return TAC_ERR_INVALID_ARGUMENT;
   DeviceState *ds = nullptr;
   int st = acquire_device(&ds, nullptr);
@@ -1666,6 +1773,23 @@ int tac_kmeans_fit(const float *vectors, uint64_t n, uint32_t dim, uint32_t k,
   hipStream_t s;
   if ((st = resolve_stream(*ds, nullptr, &s))) return st;
   if ((st = begin_call(*ds, s))) return st;
+  if (wide) {
+    tac_cluster_params prm{};
+    prm.kappa_total = k;
+    prm.max_iters = max_iters;
+    prm.tol = tol;
+    prm.seed = seed;  // token 0: the problem's seed is seed ^ 0
+    prm.n_threads = 1;
+    uint32_t kpt = 0, iters = 0;
+    float wcss = 0.0f;
+    const TacFixedFit fx{k, init_centroids, &iters};
+    st = tac_cluster_core(*ds, s, nullptr, n, vectors, false, dim, prm, 1, centroids_out,
+                          assignments_out, &kpt, &wcss, &fx);
+    if (st) return st;
+    if (wcss_out) *wcss_out = wcss;
+    if (iters_run_out) *iters_run_out = iters;
+    return end_call(*ds, s);
+  }
   const size_t x_bytes = (size_t)n * dim * sizeof(float);
   const size_t cb_bytes = (size_t)k * dim * sizeof(float);
   if ((st = ensure(*ds, ds->io_in, x_bytes)) || (st = ensure(*ds, ds->io_cb, cb_bytes)) ||
@@ -2323,7 +2447,8 @@ int tac_plan(const std::vector<uint32_t> &freqs, const std::vector<uint32_t> &of
 int tac_cluster_core(DeviceState &ds, hipStream_t s, const uint32_t *ids, uint64_t N,
                      const float *vectors, bool vectors_on_device, uint32_t dim,
                      const tac_cluster_params &prm, uint64_t nd, float *cent_out,
-                     uint32_t *assign_out, uint32_t *kpt_out, float *wcss_out) {
+                     uint32_t *assign_out, uint32_t *kpt_out, float *wcss_out,
+                     const TacFixedFit *fixed) {
   const auto wall0 = std::chrono::steady_clock::now();
   const uint32_t rt = tac_rows_per_tile(dim);
   if (rt < 64 || dim > kTacMaxDim) return TAC_ERR_UNSUPPORTED;
@@ -2335,6 +2460,12 @@ int tac_cluster_core(DeviceState &ds, hipStream_t s, const uint32_t *ids, uint64
   // CSR grouping by token id, ascending input order inside a token (tac.zig:575-602)
   std::vector<uint32_t> freqs(nd, 0), offs(nd + 1, 0), idx(N);
   auto group = [&] {
+    if (fixed) {  // one token: the rows in input order
+      freqs[0] = (uint32_t)N;
+      offs[1] = (uint32_t)N;
+      for (uint64_t i = 0; i < N; ++i) idx[i] = (uint32_t)i;
+      return;
+    }
     for (uint64_t i = 0; i < N; ++i) freqs[ids[i]] += 1;
     for (uint64_t j = 0; j < nd; ++j) offs[j + 1] = offs[j] + freqs[j];
     std::vector<uint32_t> cur(offs.begin(), offs.end() - 1);
@@ -2395,7 +2526,7 @@ int tac_cluster_core(DeviceState &ds, hipStream_t s, const uint32_t *ids, uint64
     // the rows are many and the per-thread counts stay small.
     const uint32_t hc = std::thread::hardware_concurrency();
     const uint32_t T = std::max<uint32_t>(1u, std::min<uint32_t>(8u, hc));
-    if (T > 1 && N >= (1u << 16) && (uint64_t)nd * T <= (1ull << 24))
+    if (!fixed && T > 1 && N >= (1u << 16) && (uint64_t)nd * T <= (1ull << 24))
       group_threads(T);
     else
       group();
@@ -2418,7 +2549,7 @@ int tac_cluster_core(DeviceState &ds, hipStream_t s, const uint32_t *ids, uint64
   tac_inv_table_kernel<<<(unsigned)std::min<uint64_t>((ninv + 255) / 256, kMaxBlocks), 256, 0,
                          s>>>(as<float>(ds.tac_inv), ninv);
   LAUNCH_TRY("tac_inv_table_kernel");
-  {
+  if (!fixed) {  // a fixed problem needs no spreads: its k is given
     const uint32_t *doffs = as<uint32_t>(ds.tac_offs);
     const float *dinv = as<float>(ds.tac_inv);
     float *dsp = as<float>(ds.tac_spreads);
@@ -2445,16 +2576,19 @@ int tac_cluster_core(DeviceState &ds, hipStream_t s, const uint32_t *ids, uint64
       LAUNCH_TRY("tac_spread_kernel");
     }
   }
-  std::vector<float> spreads(nd);
-  HIP_TRY(hipMemcpyAsync(spreads.data(), ds.tac_spreads.ptr, nd * sizeof(float),
-                         hipMemcpyDeviceToHost, s));
-  HIP_TRY(hipStreamSynchronize(s));
-
-  // budgets (tac.zig:641-668)
-
   std::vector<uint32_t> kappa(nd, 0);
-  const tacphase::Params pp{prm.kappa_total, prm.mu, prm.tau, prm.epsilon, prm.theta};
-  if ((st = tacphase::allocate(freqs, spreads, kappa, pp))) return st;
+  if (fixed) {
+    kappa[0] = fixed->k;
+  } else {
+    std::vector<float> spreads(nd);
+    HIP_TRY(hipMemcpyAsync(spreads.data(), ds.tac_spreads.ptr, nd * sizeof(float),
+                           hipMemcpyDeviceToHost, s));
+    HIP_TRY(hipStreamSynchronize(s));
+
+    // budgets (tac.zig:641-668)
+    const tacphase::Params pp{prm.kappa_total, prm.mu, prm.tau, prm.epsilon, prm.theta};
+    if ((st = tacphase::allocate(freqs, spreads, kappa, pp))) return st;
+  }
   for (uint64_t j = 0; j < nd; ++j)
     if (freqs[j] > 0 && kappa[j] == 0) return TAC_ERR_BUDGET_TOO_SMALL;
   std::vector<uint64_t> goff(nd + 1, 0);
@@ -2644,10 +2778,16 @@ int tac_cluster_core(DeviceState &ds, hipStream_t s, const uint32_t *ids, uint64
     }
     return TAC_OK;
   };
-  for (uint32_t c = 0; c < pl.kmax && pl.tiles_upto[c] > 0; ++c)
+  // Caller-supplied centroids (a fixed problem with init) replace the
+  // seeding; a degenerate problem keeps the rows the degenerate kernel wrote.
+  const bool given_init = fixed && fixed->init && !pl.probs[0].degenerate;
+  if (given_init)
+    HIP_TRY(hipMemcpyAsync(C, fixed->init, (size_t)fixed->k * dim * sizeof(float),
+                           hipMemcpyHostToDevice, s));
+  for (uint32_t c = 0; !given_init && c < pl.kmax && pl.tiles_upto[c] > 0; ++c)
     if ((st = round(c, 0))) return st;
-  uint32_t pending;
-  if ((st = final_states(&pending))) return st;
+  uint32_t pending = pl.kmax;
+  if (!given_init && (st = final_states(&pending))) return st;
   if (pending < pl.kmax) {
     // replay the stalled problems from their earliest pending draw
     for (uint32_t c = pending; c < pl.kmax; ++c) {
@@ -2660,7 +2800,7 @@ int tac_cluster_core(DeviceState &ds, hipStream_t s, const uint32_t *ids, uint64
       return TAC_ERR_HIP;
     }
   }
-  {
+  if (!given_init) {
     // the reference fits tokens in id order and stops at the first error
     uint32_t first_tok = 0xFFFFFFFFu;
     int first_err = 0;
@@ -2787,6 +2927,8 @@ int tac_cluster_core(DeviceState &ds, hipStream_t s, const uint32_t *ids, uint64
                          hipMemcpyDeviceToHost, s));
   HIP_TRY(hipMemcpyAsync(cent_out, C, K * dim * sizeof(float), hipMemcpyDeviceToHost, s));
   HIP_TRY(hipMemcpyAsync(pw.data(), wcss, (size_t)P * sizeof(float), hipMemcpyDeviceToHost, s));
+  if (fixed && fixed->iters_out)
+    HIP_TRY(hipMemcpyAsync(fixed->iters_out, iters, sizeof(uint32_t), hipMemcpyDeviceToHost, s));
   HIP_TRY(hipStreamSynchronize(s));
   if (profile) {
     float a = 0.0f, b = 0.0f;

@@ -122,6 +122,11 @@ SIGNATURES = {
         [c_void_p, c_u64, c_u32, c_u32, c_u32, c_void_p, c_u64, c_u32, ctypes.c_float,
          c_void_p, ctypes.POINTER(TrainExtras), c_void_p],
     ),
+    "tac_pq_train_encode_device": (
+        c_int,
+        [c_void_p, c_u64, c_u32, c_u32, c_u32, c_void_p, c_u64, c_u32, ctypes.c_float,
+         c_void_p, c_void_p, ctypes.POINTER(TrainExtras), c_void_p],
+    ),
     "tac_pq_encode": (c_int, [c_void_p, c_u64, c_u32, c_u32, c_u32, c_void_p, c_void_p]),
     "tac_pq_encode_device": (
         c_int, [c_void_p, c_u64, c_u32, c_u32, c_u32, c_void_p, c_void_p, c_void_p]),

@@ -115,6 +115,29 @@ def train_device(x: DeviceArray, n: int, dim: int, m: int, ksub: int, init: Devi
     return arrays
 
 
+def train_encode_device(x: DeviceArray, n: int, dim: int, m: int, ksub: int,
+                        init: DeviceArray | None, out: DeviceArray, codes: DeviceArray,
+                        max_iters: int, tol: float, seed: int = 0, trace: bool = False):
+    """tac_pq_train_encode_device: train (as train_device) and encode the same
+    resident residuals into `codes` [n][m], as storage.build chains them.
+    Returns the per-subspace stats (and trace) as train_device does."""
+    assert codes.dtype == code_dtype(ksub)
+    arrays = (np.zeros(m, np.uint32), np.zeros(m, np.float32), np.zeros(m, np.uint32))
+    tr = None
+    if trace:
+        tr = np.zeros((max_iters, m, ksub, dim // m), np.float32)
+        arrays = arrays + (tr,)
+    ex = TrainExtras(arrays[0].ctypes.data_as(ctypes.POINTER(ctypes.c_uint32)),
+                     arrays[1].ctypes.data_as(ctypes.POINTER(ctypes.c_float)),
+                     arrays[2].ctypes.data_as(ctypes.POINTER(ctypes.c_uint32)),
+                     None if tr is None else tr.ctypes.data_as(ctypes.POINTER(ctypes.c_float)))
+    errors.check(lib.tac_pq_train_encode_device(x.ptr, n, dim, m, ksub,
+                                                init.ptr if init is not None else None,
+                                                seed & (2**64 - 1), max_iters, tol, out.ptr,
+                                                codes.ptr, ctypes.byref(ex), None))
+    return arrays
+
+
 def encode_device(x: DeviceArray, n: int, dim: int, m: int, ksub: int, cb: DeviceArray,
                   codes: DeviceArray) -> None:
     assert codes.dtype == code_dtype(ksub)

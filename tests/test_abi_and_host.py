@@ -87,6 +87,11 @@ def test_c_abi_validates_before_touching_a_device():
     assert L.tac_pq_train(None, 10, 64, 4, 256, None, 0, 25, 1e-4, None, None) == 15  # dsub 16
     assert L.tac_pq_train(None, 10, 32, 32, 2048, None, 0, 25, 1e-4, None, None) == 15
     assert L.tac_kmeans_fit(None, 5, 2, 0, 25, 1e-4, 0, None, None, None, None, None) == 6
+    # rows of up to 512 floats (the token engine past dim 8), any k there
+    assert L.tac_kmeans_fit(None, 5, 513, 3, 25, 1e-4, 0, None, None, None, None, None) == 15
+    assert L.tac_kmeans_fit(None, 5, 512, 3, 25, 1e-4, 0, None, None, None, None, None) == 14
+    assert L.tac_kmeans_fit(None, 5, 8, 2048, 25, 1e-4, 0, None, None, None, None, None) == 15
+    assert L.tac_kmeans_fit(None, 5, 9, 2048, 25, 1e-4, 0, None, None, None, None, None) == 14
     assert L.tac_pq_encode(None, 10, 33, 32, 256, None, None) == 2
     assert L.tac_pq_encode(None, 0, 32, 32, 256, None, None) == 0  # nothing to encode
     # the no-allocation encode validates exactly as tac_pq_encode_device

@@ -36,6 +36,24 @@ def _serial_mean(points):
     return s * (np.float32(1.0) / np.float32(len(points)))
 
 
+def _check_train_encode(x, w, init, ref, ref_codes):
+    """tac_pq_train_encode_device on the same input: the codebooks and every
+    code equal the oracle's train and encode (storage.build's chain,
+    src/index/storage.zig:380-401)."""
+    dx = device.DeviceArray.from_host(x)
+    dinit = device.DeviceArray.from_host(init)
+    dcb = device.DeviceArray(init.shape, np.float32)
+    dcodes = device.DeviceArray((w.n, w.m), pq.code_dtype(w.ksub))
+    device.train_encode_device(dx, w.n, w.dim, w.m, w.ksub, dinit, dcb, dcodes, w.iters, NEVER)
+    cb, codes = dcb.to_host(), dcodes.to_host()
+    for a in (dx, dinit, dcb, dcodes):
+        a.free()
+    assert np.array_equal(_bits(cb), _bits(ref.codebooks))
+    diff = int(np.count_nonzero(codes != ref_codes))
+    _log(f"{w.name}: train+encode entry, {diff} of {codes.size} codes differ")
+    assert diff == 0
+
+
 @pytest.fixture(scope="module")
 def corpus():
     return synth.residuals(synth.WORKLOADS["corpus-1.52m"])
@@ -76,6 +94,7 @@ def test_headline_corpus_as_benchmarked(gpu, corpus):
     assert np.all(stats[0] == w.iters)
     ref_codes = orc.pq_encode(x, w.dim, w.m, w.ksub, ref.codebooks, n_threads=16)
     t3 = time.perf_counter()
+    _check_train_encode(x, w, init, ref, ref_codes)
     diff = int(np.count_nonzero(codes != ref_codes))
     ties = orc.pq_near_ties(x, w.dim, w.m, w.ksub, ref.codebooks, 1e-5, n_threads=16)
     _log(f"headline: GPU train+encode {t1 - t0:.3f} s (first call), oracle train {t2 - t1:.1f} s, "
@@ -120,6 +139,7 @@ def test_subspace_shape_sweep_full_corpus(gpu, corpus, name):
     assert np.all(stats[0] == w.iters)
     ref_codes = orc.pq_encode(x, w.dim, w.m, w.ksub, ref.codebooks, n_threads=16)
     assert ref_codes.dtype == codes.dtype
+    _check_train_encode(x, w, init, ref, ref_codes)
     diff = int(np.count_nonzero(codes != ref_codes))
     _log(f"{name}: GPU {t1 - t0:.2f} s, oracle train {t2 - t1:.1f} s, encode "
          f"{time.perf_counter() - t2:.1f} s; {diff} of {codes.size} codes differ")

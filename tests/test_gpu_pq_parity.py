@@ -195,6 +195,79 @@ def test_kmeans_fit_matches_oracle(gpu):
     assert np.float32(got.wcss).view(np.uint32) == np.float32(ref.wcss).view(np.uint32)
 
 
+@pytest.mark.parametrize("dim,k,n,init", [(9, 12, 3000, False), (16, 40, 5000, True),
+                                          (33, 17, 4000, False), (64, 50, 6000, False),
+                                          (64, 30, 4000, True), (128, 9, 2500, False),
+                                          (100, 3000, 2000, False), (512, 5, 700, True)])
+def test_kmeans_fit_wide_rows(gpu, dim, k, n, init):
+    """kmeans.fit past dim 8 (the token-clustering engine as one problem):
+    vec.l2sq's 4-lane form at 64 and 128 and its generic form otherwise,
+    k-means++ from `seed` or caller centroids, tol 1e-4 (the reference's
+    default, so wcss decides the stop), and k >= n (the degenerate branch,
+    kmeans.zig:88-104).  Centroids, assignments, wcss and iterations equal
+    the oracle's bit for bit."""
+    rng = np.random.default_rng(dim * 1000 + k)
+    centres = rng.standard_normal((7, dim)).astype(np.float32)
+    v = (centres[rng.integers(0, 7, n)] + 0.3 * rng.standard_normal((n, dim))).astype(np.float32)
+    ini = v[rng.permutation(n)[:k]].copy() if init and k < n else None
+    got = kmeans.fit(v, dim, k, seed=77, max_iters=25, tol=1e-4, init_centroids=ini)
+    ref = orc.kmeans_fit(v, dim, k, max_iters=25, tol=1e-4, seed=77, init=ini)
+    assert ref.status == 0
+    assert got.iters_run == ref.iters_run
+    assert np.array_equal(got.assignments, ref.assignments)
+    assert np.array_equal(_bits(got.centroids), _bits(ref.centroids))
+    assert np.float32(got.wcss).view(np.uint32) == np.float32(ref.wcss).view(np.uint32)
+
+
+@pytest.mark.parametrize("case", ["tol", "one_stream", "k1024", "m8", "small_one_iter",
+                                  "degenerate", "zero_iters"])
+def test_train_encode_entry(gpu, monkeypatch, case):
+    """tac_pq_train_encode_device: its codebooks equal tac_pq_train_device's
+    and its codes tac_pq_encode_device's on those codebooks, and both equal
+    the oracle: with tol 1e-3 (subspaces that stop early still encode), on
+    one stream, with u16 codes, at dsub 8, and on the shapes that take the
+    ordinary encode (one iteration of fewer than 16,384 vectors, n <= ksub,
+    no iteration)."""
+    m, ksub, n, iters, tol = 16, 256, 40_000, 8, NEVER
+    if case == "tol":
+        tol = 1e-3
+    if case == "one_stream":
+        monkeypatch.setenv("TAC_GPU_TRAIN_STREAMS", "1")
+    if case == "k1024":
+        ksub = 1024
+    if case == "m8":
+        m = 8
+    if case == "small_one_iter":
+        n, iters = 9000, 1
+    if case == "degenerate":
+        n = 200
+    if case == "zero_iters":
+        iters = 0
+    x = _workload_rows(n, seed=5)
+    init = synth.shuffle_init(x, m, ksub, 3) if ksub <= n else None
+    dx = device.DeviceArray.from_host(x)
+    dinit = device.DeviceArray.from_host(init) if init is not None else None
+    dcb = device.DeviceArray((m, ksub, 64 // m), np.float32)
+    dcodes = device.DeviceArray((n, m), pq.code_dtype(ksub))
+    st = device.train_encode_device(dx, n, 64, m, ksub, dinit, dcb, dcodes, iters, tol, seed=11)
+    cb, codes = dcb.to_host(), dcodes.to_host()
+    # the separate entry points on the same input
+    dcb2 = device.DeviceArray((m, ksub, 64 // m), np.float32)
+    dcodes2 = device.DeviceArray((n, m), pq.code_dtype(ksub))
+    st2 = device.train_device(dx, n, 64, m, ksub, dinit, dcb2, iters, tol, stats=True, seed=11)
+    device.encode_device(dx, n, 64, m, ksub, dcb2, dcodes2)
+    assert np.array_equal(_bits(cb), _bits(dcb2.to_host()))
+    assert np.array_equal(codes, dcodes2.to_host())
+    assert np.array_equal(st[0], st2[0]) and np.array_equal(_bits(st[1]), _bits(st2[1]))
+    for a in (dx, dinit, dcb, dcodes, dcb2, dcodes2):
+        if a is not None:
+            a.free()
+    ref = orc.pq_train(x, 64, m, ksub, init=init, seed=11, max_iters=iters, tol=tol, n_threads=8)
+    assert ref.status == 0
+    assert np.array_equal(_bits(cb), _bits(ref.codebooks))
+    assert np.array_equal(codes, orc.pq_encode(x, 64, m, ksub, ref.codebooks, n_threads=8))
+
+
 def test_device_resident_train_then_encode(gpu):
     w, x, init = synth.workload("chunk-117k", n=40000)
     dx = device.DeviceArray.from_host(x)
