@@ -101,6 +101,21 @@ typedef struct tac_gpu_device_info {
   uint64_t lds_bytes_per_block;
 } tac_gpu_device_info;
 int tac_gpu_get_device_info(int device, tac_gpu_device_info *info);
+/*
+ * vec.lane_count of the host the reference is built for,
+ * std.simd.suggestVectorLength(f32) (src/util/vec.zig:16): 16 on AVX-512
+ * x86-64 (the default), 8 on AVX2, 4 on NEON (aarch64).  It orders the
+ * reference's generic l2sq / dot (vec.zig:90-103, :159-175), used at PQ
+ * sub-dimension 8 (4 lanes pair elements j and j + 4) and by token
+ * clustering at dims other than 2, 4, 64 and 128; every other distance is
+ * unaffected.  Process-wide; takes effect on a device at the next call there
+ * (calls already running keep the value they started with).  lanes must be
+ * 4, 8 or 16 (else TAC_ERR_INVALID_ARGUMENT).  No counterpart call in the
+ * reference, where it is a build-time constant.
+ */
+int tac_gpu_set_lane_count(uint32_t lanes);
+int tac_gpu_get_lane_count(uint32_t *lanes);
+
 int tac_gpu_set_device(int device);
 int tac_gpu_malloc(void **ptr, uint64_t bytes);
 int tac_gpu_free(void *ptr);

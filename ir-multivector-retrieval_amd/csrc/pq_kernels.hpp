@@ -63,11 +63,78 @@ __device__ __forceinline__ void load_padded(const float* __restrict__ p, float (
   }
 }
 
-// Reference distance: sequential left fold, separate roundings.  The fold
-// starts from 0.0f in the reference; 0.0f + (x0-c0)^2 equals (x0-c0)^2
-// bit for bit because a square is never -0.0.
+// vec.lane_count of the host the reference is built for
+// (std.simd.suggestVectorLength(f32), src/util/vec.zig:16): 16 on AVX-512,
+// 8 on AVX2, 4 on NEON.  It sets the order of the generic vec path
+// (:90-103, :159-175) and is set per device from the host
+// (tac_gpu_set_lane_count).
+__constant__ uint32_t c_vec_lanes = 16;
+
+// The generic vec path at L lanes: lane j accumulates the products of
+// elements j, j + L, ... of the whole L-element chunks from 0.0f, the lanes
+// are added in order, then the tail elements one by one.
+template <int L, bool DOT>
+__device__ __forceinline__ float generic_vec_lanes(const float* a, const float* b, uint32_t d) {
+  float acc[L];
+#pragma unroll
+  for (int j = 0; j < L; ++j) acc[j] = 0.0f;
+  uint32_t i = 0;
+  for (; i + L <= d; i += L) {
+#pragma unroll
+    for (int j = 0; j < L; ++j) {
+      if constexpr (DOT) {
+        acc[j] = acc[j] + a[i + j] * b[i + j];
+      } else {
+        const float t = a[i + j] - b[i + j];
+        acc[j] = acc[j] + t * t;
+      }
+    }
+  }
+  float sum = acc[0];
+#pragma unroll
+  for (int j = 1; j < L; ++j) sum = sum + acc[j];
+  for (; i < d; ++i) {
+    if constexpr (DOT) {
+      sum = sum + a[i] * b[i];
+    } else {
+      const float t = a[i] - b[i];
+      sum = sum + t * t;
+    }
+  }
+  return sum;
+}
+
+// vec.l2sqGeneric / vec.dotGeneric at the device's lane count.
+template <bool DOT>
+__device__ __forceinline__ float generic_vec(const float* a, const float* b, uint32_t d) {
+  const uint32_t L = c_vec_lanes;
+  if (L == 4) return generic_vec_lanes<4, DOT>(a, b, d);
+  if (L == 8) return generic_vec_lanes<8, DOT>(a, b, d);
+  return generic_vec_lanes<16, DOT>(a, b, d);
+}
+
+// Reference distance at sub-dimension D <= 8 (src/util/vec.zig:109-175):
+// the sequential left fold with separate roundings (the reference's
+// explicit dim 2 / dim 4 folds, and its generic path for every D below two
+// lane widths); at D = 8 on a 4-lane host the generic path's lane j holds
+// (x_j - c_j)^2 + (x_{j+4} - c_{j+4})^2 and the lanes are added in order.
+// The fold starts from 0.0f in the reference; 0.0f + (x0-c0)^2 equals
+// (x0-c0)^2 bit for bit because a square is never -0.0.
 template <int D>
 __device__ __forceinline__ float exact_l2sq(const float (&x)[D], const float (&c)[D]) {
+  if constexpr (D == 8) {
+    if (c_vec_lanes == 4) {
+      float l[4];
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        const float t0 = x[j] - c[j];
+        const float t1 = x[j + 4] - c[j + 4];
+        l[j] = t0 * t0;
+        l[j] = l[j] + t1 * t1;
+      }
+      return ((l[0] + l[1]) + l[2]) + l[3];
+    }
+  }
   float t = x[0] - c[0];
   float s = t * t;
 #pragma unroll

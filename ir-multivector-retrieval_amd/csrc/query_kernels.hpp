@@ -8,12 +8,14 @@
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
+#include "pq_kernels.hpp"
+
 namespace tacgpu {
 
 // vec.dot (src/util/vec.zig:37-103): dims 2 and 4 are left folds from 0,
 // dims 64 and 128 accumulate in 4 lanes chunk after chunk and reduce
-// ((a0 + a1) + a2) + a3, other dims accumulate in 16 lanes (the x86-64
-// AVX-512 lane count), reduce in lane order and fold the tail.
+// ((a0 + a1) + a2) + a3, other dims take the generic path at the device's
+// lane count (generic_vec: lanes, lane-order reduce, tail).
 // `a` and `b` may live in LDS or global memory.
 __device__ inline float ref_dot(const float* a, const float* b, uint32_t d) {
   if (d == 2) return a[0] * b[0] + a[1] * b[1];
@@ -32,19 +34,7 @@ __device__ inline float ref_dot(const float* a, const float* b, uint32_t d) {
     }
     return ((acc0 + acc1) + acc2) + acc3;
   }
-  float acc[16];
-#pragma unroll
-  for (int j = 0; j < 16; ++j) acc[j] = 0.0f;
-  uint32_t i = 0;
-  for (; i + 16 <= d; i += 16) {
-#pragma unroll
-    for (int j = 0; j < 16; ++j) acc[j] = acc[j] + a[i + j] * b[i + j];
-  }
-  float sum = acc[0];
-#pragma unroll
-  for (int j = 1; j < 16; ++j) sum = sum + acc[j];
-  for (; i < d; ++i) sum = sum + a[i] * b[i];
-  return sum;
+  return generic_vec<true>(a, b, d);
 }
 
 // PQ.buildDistanceTable: table[((mm * K) + c) * n_q + i] =

@@ -28,6 +28,7 @@
 #include <hip/hip_runtime.h>
 
 #include <algorithm>
+#include <atomic>
 #include <chrono>
 #include <cstdarg>
 #include <map>
@@ -219,7 +220,29 @@ int upload_host(DeviceState &ds, void *dst, const void *src, size_t bytes, hipSt
 }
 
 // Order this call after the previous one that used the workspace.
+// The reference host's vector lane count (tac_gpu_set_lane_count), and the
+// value each device's c_vec_lanes last received (0: never written).
+std::atomic<uint32_t> g_vec_lanes{16};
+std::atomic<uint32_t> g_dev_lanes[kMaxDevices] = {};
+const uint32_t kLaneValues[3] = {4, 8, 16};  // copy sources that outlive the copies
+
+// Brings the current device's c_vec_lanes up to the setting, ordered before
+// the work the call enqueues on s.  No allocation.
+int sync_lanes(hipStream_t s) {
+  int dev = 0;
+  HIP_TRY(hipGetDevice(&dev));
+  if (dev < 0 || dev >= kMaxDevices) return TAC_ERR_NO_DEVICE;
+  const uint32_t want = g_vec_lanes.load();
+  if (g_dev_lanes[dev].load() == want) return TAC_OK;
+  const uint32_t *src = want == 4 ? &kLaneValues[0] : want == 8 ? &kLaneValues[1] : &kLaneValues[2];
+  HIP_TRY(hipMemcpyToSymbolAsync(HIP_SYMBOL(c_vec_lanes), src, sizeof(uint32_t), 0,
+                                 hipMemcpyHostToDevice, s));
+  g_dev_lanes[dev].store(want);
+  return TAC_OK;
+}
+
 int begin_call(DeviceState &ds, hipStream_t s) {
+  if (int st = sync_lanes(s)) return st;
   if (!ds.last_done) HIP_TRY(hipEventCreateWithFlags(&ds.last_done, hipEventDisableTiming));
   if (ds.last_stream && ds.last_stream != s) HIP_TRY(hipStreamWaitEvent(s, ds.last_done, 0));
   ds.last_stream = s;
@@ -1379,6 +1402,18 @@ int tac_gpu_get_device_info(int device, tac_gpu_device_info *info) {
   return TAC_OK;
 }
 
+int tac_gpu_set_lane_count(uint32_t lanes) {
+  if (lanes != 4 && lanes != 8 && lanes != 16) return TAC_ERR_INVALID_ARGUMENT;
+  g_vec_lanes.store(lanes);
+  return TAC_OK;
+}
+
+int tac_gpu_get_lane_count(uint32_t *lanes) {
+  if (!lanes) return TAC_ERR_INVALID_ARGUMENT;
+  *lanes = g_vec_lanes.load();
+  return TAC_OK;
+}
+
 int tac_gpu_set_device(int device) {
   const int c = device_count();
   if (c <= 0) return TAC_ERR_NO_DEVICE;
@@ -1616,6 +1651,7 @@ int tac_pq_encode_device_noalloc(const float *d_residuals, uint64_t n, uint32_t 
   int st = scratch_address(dev, &base);
   if (st) return st;
   hipStream_t s = reinterpret_cast<hipStream_t>(stream);  // NULL: the null stream
+  if ((st = sync_lanes(s))) return st;
   const uint32_t D = dim / m;
   size_t off = 0;
   auto take = [&](size_t bytes) {

@@ -15,6 +15,8 @@
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
+#include "pq_kernels.hpp"
+
 namespace tacgpu {
 
 struct TacProblem {
@@ -71,8 +73,8 @@ __host__ __device__ inline uint32_t tac_tile_lds_floats(uint32_t dim) {
 
 // vec.l2sq (src/util/vec.zig:109-175) in the reference's order: dim 2 and 4
 // are left folds, dims 64 and 128 accumulate in 4 lanes chunk after chunk and
-// reduce ((a0 + a1) + a2) + a3, other dims accumulate in 16 lanes (the
-// x86-64 AVX-512 lane count), reduce in lane order and fold the tail.  DIMC
+// reduce ((a0 + a1) + a2) + a3, other dims take the generic path at the
+// device's lane count (generic_vec: lanes, lane-order reduce, tail).  DIMC
 // fixes the dimension at compile time (0: runtime d).
 template <int DIMC>
 __device__ __forceinline__ float tac_l2sq(const float* a, const float* b, uint32_t d_rt) {
@@ -104,25 +106,7 @@ __device__ __forceinline__ float tac_l2sq(const float* a, const float* b, uint32
     }
     return ((acc0 + acc1) + acc2) + acc3;
   }
-  float acc[16];
-#pragma unroll
-  for (int j = 0; j < 16; ++j) acc[j] = 0.0f;
-  uint32_t i = 0;
-  for (; i + 16 <= d; i += 16) {
-#pragma unroll
-    for (int j = 0; j < 16; ++j) {
-      const float t = a[i + j] - b[i + j];
-      acc[j] = acc[j] + t * t;
-    }
-  }
-  float sum = acc[0];
-#pragma unroll
-  for (int j = 1; j < 16; ++j) sum = sum + acc[j];
-  for (; i < d; ++i) {
-    const float t = a[i] - b[i];
-    sum = sum + t * t;
-  }
-  return sum;
+  return generic_vec<false>(a, b, d);
 }
 
 // ---------------------------------------------------------------------------

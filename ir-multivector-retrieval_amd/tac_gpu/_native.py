@@ -105,6 +105,8 @@ SIGNATURES = {
     "tac_gpu_device_count": (c_int, [ctypes.POINTER(c_int)]),
     "tac_gpu_get_device_info": (c_int, [c_int, ctypes.POINTER(DeviceInfo)]),
     "tac_gpu_set_device": (c_int, [c_int]),
+    "tac_gpu_set_lane_count": (c_int, [c_u32]),
+    "tac_gpu_get_lane_count": (c_int, [ctypes.POINTER(c_u32)]),
     "tac_gpu_malloc": (c_int, [ctypes.POINTER(c_void_p), c_u64]),
     "tac_gpu_free": (c_int, [c_void_p]),
     "tac_gpu_memcpy_htod": (c_int, [c_void_p, c_void_p, c_u64]),

@@ -35,6 +35,34 @@ def device_info(device: int = 0) -> dict:
     }
 
 
+def set_lane_count(lanes: int) -> None:
+    """vec.lane_count of the host whose reference build is being matched
+    (src/util/vec.zig:16): 16 (AVX-512, the default), 8 (AVX2) or 4 (NEON)."""
+    errors.check(lib.tac_gpu_set_lane_count(lanes))
+
+
+def lane_count() -> int:
+    v = ctypes.c_uint32(0)
+    errors.check(lib.tac_gpu_get_lane_count(ctypes.byref(v)))
+    return int(v.value)
+
+
+class lanes:
+    """Within the block the library's generic vec path uses `n` lanes."""
+
+    def __init__(self, n: int):
+        self.n = n
+
+    def __enter__(self):
+        self.prev = lane_count()
+        set_lane_count(self.n)
+        return self
+
+    def __exit__(self, *exc):
+        set_lane_count(self.prev)
+        return False
+
+
 def synchronize() -> None:
     errors.check(lib.tac_gpu_synchronize())
 

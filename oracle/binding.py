@@ -68,6 +68,10 @@ def _load():
                                ctypes.POINTER(TrainExtras)]
     L.orc_set_scalar.restype = None
     L.orc_set_scalar.argtypes = [ctypes.c_int]
+    L.orc_set_lane_count.restype = ctypes.c_int
+    L.orc_set_lane_count.argtypes = [_u32]
+    L.orc_lane_count.restype = _u32
+    L.orc_lane_count.argtypes = []
     L.orc_pq_encode.restype = ctypes.c_int
     L.orc_pq_encode.argtypes = [_vp, _u64, _u32, _u32, _u32, _vp, _vp, _u32]
     L.orc_pq_near_ties.restype = ctypes.c_int
@@ -421,4 +425,23 @@ class scalar_distances:
 
     def __exit__(self, *exc):
         lib.orc_set_scalar(0)
+        return False
+
+
+class lane_count:
+    """Within the block the oracle's generic vec path (src/util/vec.zig:16,
+    :90-103, :159-175) runs with `lanes` vector lanes (4, 8 or 16), the
+    value of std.simd.suggestVectorLength(f32) on the host being matched."""
+
+    def __init__(self, lanes: int):
+        self.lanes = lanes
+
+    def __enter__(self):
+        self.prev = int(lib.orc_lane_count())
+        st = lib.orc_set_lane_count(self.lanes)
+        assert st == 0, f"lane count {self.lanes} rejected"
+        return self
+
+    def __exit__(self, *exc):
+        lib.orc_set_lane_count(self.prev)
         return False

@@ -23,11 +23,22 @@
 /* vec primitives: src/util/vec.zig                                          */
 /* ------------------------------------------------------------------------ */
 
+/* vec.lane_count (src/util/vec.zig:16), settable to the reference host's. */
+static uint32_t g_lanes = 16;
+int orc_set_lane_count(uint32_t lanes) {
+  if (lanes != 4 && lanes != 8 && lanes != 16) return ORC_INVALID_ARGUMENT;
+  g_lanes = lanes;
+  return ORC_OK;
+}
+uint32_t orc_lane_count(void) { return g_lanes; }
+
 /* src/util/vec.zig:109-175.  dim 2 and 4 are explicit left folds (:114-118,
  * :133-139); dims 64 and 128 use four vector lanes that accumulate chunk
  * after chunk and an ordered reduce (:142-155); other dims use the host
- * lane count with an ordered reduce and a scalar tail (:159-175).  For every
- * dim below ORC_HOST_LANES the generic path equals the sequential fold. */
+ * lane count L with an ordered reduce and a scalar tail (:159-175): lane j
+ * accumulates elements j, j + L, ... of the whole L-chunks from 0.0, the
+ * lanes are summed in order, then the tail elements one by one.  Below 2 L
+ * elements that is the sequential fold (0 + x = x for a square). */
 float orc_l2sq(const float *a, const float *b, uint32_t d) {
   if (d == 2) {
     const float d0 = a[0] - b[0];
@@ -52,18 +63,19 @@ float orc_l2sq(const float *a, const float *b, uint32_t d) {
     }
     return ((acc[0] + acc[1]) + acc[2]) + acc[3];
   }
-  float acc[ORC_HOST_LANES];
-  for (int j = 0; j < ORC_HOST_LANES; ++j) acc[j] = 0.0f;
+  const uint32_t L = g_lanes;
+  float acc[ORC_MAX_LANES];
+  for (uint32_t j = 0; j < L; ++j) acc[j] = 0.0f;
   uint32_t i = 0;
-  while (i + ORC_HOST_LANES <= d) {
-    for (int j = 0; j < ORC_HOST_LANES; ++j) {
+  while (i + L <= d) {
+    for (uint32_t j = 0; j < L; ++j) {
       const float t = a[i + j] - b[i + j];
       acc[j] += t * t;
     }
-    i += ORC_HOST_LANES;
+    i += L;
   }
   float sum = acc[0];
-  for (int j = 1; j < ORC_HOST_LANES; ++j) sum += acc[j];
+  for (uint32_t j = 1; j < L; ++j) sum += acc[j];
   for (; i < d; ++i) {
     const float t = a[i] - b[i];
     sum += t * t;
@@ -85,15 +97,16 @@ float orc_dot(const float *a, const float *b, uint32_t d) {
       for (int j = 0; j < 4; ++j) acc[j] += a[c + j] * b[c + j];
     return ((acc[0] + acc[1]) + acc[2]) + acc[3];
   }
-  float acc[ORC_HOST_LANES];
-  for (int j = 0; j < ORC_HOST_LANES; ++j) acc[j] = 0.0f;
+  const uint32_t L = g_lanes;
+  float acc[ORC_MAX_LANES];
+  for (uint32_t j = 0; j < L; ++j) acc[j] = 0.0f;
   uint32_t i = 0;
-  while (i + ORC_HOST_LANES <= d) {
-    for (int j = 0; j < ORC_HOST_LANES; ++j) acc[j] += a[i + j] * b[i + j];
-    i += ORC_HOST_LANES;
+  while (i + L <= d) {
+    for (uint32_t j = 0; j < L; ++j) acc[j] += a[i + j] * b[i + j];
+    i += L;
   }
   float sum = acc[0];
-  for (int j = 1; j < ORC_HOST_LANES; ++j) sum += acc[j];
+  for (uint32_t j = 1; j < L; ++j) sum += acc[j];
   for (; i < d; ++i) sum += a[i] * b[i];
   return sum;
 }
@@ -131,12 +144,13 @@ uint64_t orc_argmax(const float *v, uint64_t n) {
 /* The reference's assignment writes dists[cc] = l2sq(v, c_cc) for every
  * codeword and then takes vec.argmin (src/tac/kmeans.zig:356-364); PQ.encode
  * scans the same distances from best = +inf (src/index/pq.zig:64-73).  For
- * d <= 8 < ORC_HOST_LANES every arm of l2sq is the sequential fold
- * ((x0-c0)^2 + (x1-c1)^2) + ..., so the distances below fold each codeword
- * in that order, reading a transposed codebook cbt[k][cc] (row stride kp):
- * the loop over codewords vectorizes, and each codeword's bits equal
- * orc_l2sq's.  orc_set_scalar(1) forces the per-pair orc_l2sq path, against
- * which the tests compare this one. */
+ * d <= 8 every arm of l2sq is the sequential fold ((x0-c0)^2 + (x1-c1)^2)
+ * + ..., except d = 8 at 4 lanes, whose lanes j = 0..3 hold
+ * (x_j-c_j)^2 + (x_{j+4}-c_{j+4})^2 and are summed in order; the distances
+ * below fold each codeword in that order, reading a transposed codebook
+ * cbt[k][cc] (row stride kp): the loop over codewords vectorizes, and each
+ * codeword's bits equal orc_l2sq's.  orc_set_scalar(1) forces the per-pair
+ * orc_l2sq path, against which the tests compare this one. */
 static int g_scalar = 0;
 void orc_set_scalar(int on) { g_scalar = on; }
 
@@ -166,6 +180,21 @@ ORC_DISTS(6)
 ORC_DISTS(7)
 ORC_DISTS(8)
 
+static void dists_d8_l4(const float *x, const float *cbt, uint32_t k, uint32_t kp, float *out) {
+  float xv[8];
+  for (int j = 0; j < 8; ++j) xv[j] = x[j];
+  for (uint32_t cc = 0; cc < k; ++cc) {
+    float lane[4];
+    for (int j = 0; j < 4; ++j) {
+      const float t0 = xv[j] - cbt[(uint64_t)j * kp + cc];
+      const float t1 = xv[j + 4] - cbt[(uint64_t)(j + 4) * kp + cc];
+      lane[j] = t0 * t0;
+      lane[j] = lane[j] + t1 * t1;
+    }
+    out[cc] = ((lane[0] + lane[1]) + lane[2]) + lane[3];
+  }
+}
+
 static dists_fn dists_for(uint32_t d) {
   if (g_scalar) return NULL;
   switch (d) {
@@ -176,7 +205,7 @@ static dists_fn dists_for(uint32_t d) {
     case 5: return dists_d5;
     case 6: return dists_d6;
     case 7: return dists_d7;
-    case 8: return dists_d8;
+    case 8: return g_lanes == 4 ? dists_d8_l4 : dists_d8;
     default: return NULL;
   }
 }

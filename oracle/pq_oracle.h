@@ -65,9 +65,14 @@ enum {
   ORC_EMPTY_TOKEN_DUMP = 24,
 };
 
-/* Lane count the reference's generic vec path uses on the host it is built
- * for (std.simd.suggestVectorLength(f32)): 16 on an AVX-512 x86-64 host. */
-#define ORC_HOST_LANES 16
+/* Lane count of the reference's generic vec path, vec.lane_count =
+ * std.simd.suggestVectorLength(f32) of the host it is built for
+ * (src/util/vec.zig:16): 16 on AVX-512 x86-64 (the default here), 8 on AVX2,
+ * 4 on NEON (aarch64).  orc_set_lane_count takes 4, 8 or 16 and returns 0,
+ * or 14 (invalid argument) and keeps the current value. */
+#define ORC_MAX_LANES 16
+int orc_set_lane_count(uint32_t lanes);
+uint32_t orc_lane_count(void);
 
 /* 1: every distance goes through orc_l2sq pair by pair (the per-pair form);
  * 0 (default): for d <= 8 all K distances of a vector are formed at once from

@@ -36,6 +36,86 @@ def test_l2sq_tail_beyond_lane():  # vec.zig:379-388
     assert orc.l2sq(a, a + 1) == 9.0
 
 
+def _np_generic(a, b, lanes, dot=False):
+    """vec.l2sqGeneric / dotGeneric (vec.zig:90-103, :159-175) in numpy
+    float32, every operation rounded: lane j adds the products of elements
+    j, j + lanes, ... of the whole chunks to 0.0, the lanes are added in
+    order, then the tail elements one by one."""
+    a, b = f32(*a), f32(*b)
+    p = a * b if dot else (a - b) * (a - b)
+    acc = np.zeros(lanes, np.float32)
+    i = 0
+    while i + lanes <= a.size:
+        acc = acc + p[i:i + lanes]
+        i += lanes
+    s = acc[0]
+    for j in range(1, lanes):
+        s = np.float32(s + acc[j])
+    for k in range(i, a.size):
+        s = np.float32(s + p[k])
+    return s
+
+
+@pytest.mark.parametrize("lanes", [4, 8, 16])
+@pytest.mark.parametrize("dim", [3, 8, 9, 16, 20, 33, 100])
+def test_generic_vec_lane_count(lanes, dim):
+    """The generic path at each host lane count (vec.zig:16), pinned three
+    ways: against the chunked form above; at 8 and 16 lanes for dims below
+    two lane widths against the plain sequential fold (a different
+    formula); and, at 4 lanes and dim 8, against the pairing of element j
+    with j + 4, while a planted pairing of neighbours (j with j + 1) and the
+    sequential fold both disagree on some of the same inputs."""
+    rng = np.random.default_rng(dim * 31 + lanes)
+    seq_diff = adj_diff = 0
+    with orc.lane_count(lanes):
+        for _ in range(400):
+            a = rng.standard_normal(dim).astype(np.float32)
+            b = rng.standard_normal(dim).astype(np.float32)
+            got = orc.l2sq(a, b)
+            if dim not in (2, 4, 64, 128):
+                assert got == _np_generic(a, b, lanes), (a, b)
+                assert orc.dot(a, b) == _np_generic(a, b, lanes, dot=True)
+            sq = ((a - b) * (a - b)).astype(np.float32)
+            seq = np.float32(0.0)
+            for v in sq:
+                seq = np.float32(seq + v)
+            if dim < 2 * lanes:
+                assert got == seq
+            if lanes == 4 and dim == 8:
+                lane = (sq[:4] + sq[4:]).astype(np.float32)
+                assert got == np.float32(np.float32(np.float32(lane[0] + lane[1]) + lane[2]) + lane[3])
+                adj = (sq[0::2] + sq[1::2]).astype(np.float32)
+                planted = np.float32(np.float32(np.float32(adj[0] + adj[1]) + adj[2]) + adj[3])
+                seq_diff += int(got != seq)
+                adj_diff += int(got != planted)
+    if lanes == 4 and dim == 8:
+        assert seq_diff > 0 and adj_diff > 0
+
+
+def test_lane_count_rejects_other_values():
+    assert orc.lib.orc_set_lane_count(5) != 0
+    assert orc.lib.orc_set_lane_count(32) != 0
+    assert orc.lib.orc_lane_count() == 16
+
+
+@pytest.mark.parametrize("lanes", [4, 16])
+def test_vectorized_dsub8_matches_per_pair_path(lanes):
+    """PQ at sub-dimension 8: the oracle's vectorized all-codeword distance
+    form (the 4-lane pairing at 4 lanes) against its per-pair orc_l2sq
+    path, on the train trace and the codes."""
+    rng = np.random.default_rng(lanes)
+    x = rng.standard_normal((3000, 64)).astype(np.float32) * np.float32(0.3)
+    init = x[rng.permutation(3000)[:64]].reshape(64, 8, 8).transpose(1, 0, 2).copy()
+    with orc.lane_count(lanes):
+        fast = orc.pq_train(x, 64, 8, 64, init=init, max_iters=4, tol=NEVER, trace=True)
+        fcodes = orc.pq_encode(x, 64, 8, 64, fast.codebooks)
+        with orc.scalar_distances():
+            slow = orc.pq_train(x, 64, 8, 64, init=init, max_iters=4, tol=NEVER, trace=True)
+            scodes = orc.pq_encode(x, 64, 8, 64, fast.codebooks)
+    assert fast.trace.tobytes() == slow.trace.tobytes()
+    assert np.array_equal(fcodes, scodes)
+
+
 def test_l2sq_dim4_hand_checked():  # vec.zig:513-519
     assert orc.l2sq(f32(1, 2, 3, 4), f32(5, 6, 7, 8)) == 64.0
 
