@@ -15,7 +15,8 @@ oracle on this host's cores), rows for the subspace-shape sweep, the 60M
 resident train and the 200M encode stream, and the stages around the path.
 
 Other modes:
-  --traffic-pass        a short run for rocprofv3 counter passes
+  --counter-pass W      one run of workload W's GPU work for rocprofv3 counter passes
+  --summarize-trace OUT DIR   kernel table of a rocprofv3 --kernel-trace --stats run
   --cpu-protocol OUT W...   the CPU baseline protocol of workloads W (profiles)
   --summarize-pmc OUT DIR...   per-kernel summary of rocprofv3 counter CSVs
 """
@@ -472,27 +473,35 @@ def algorithmic_flops(name: str, n: int, dim: int, m: int, ksub: int, parts: int
 
 def roofline(name: str, row: dict, n: int, dim: int, m: int, ksub: int, traffic: dict,
              valu: dict, parts: int = 1):
-    """The dominant kernel against the roof its counters show it is bound by:
-    'valu' (fp32 vector, algorithmic FLOP against 157.3 TFLOP/s) when its
-    measured VALU issue share exceeds its HBM share, else 'hbm' (algorithmic
-    bytes against 8 TB/s).  Both shares are reported under their own names."""
+    """The dominant kernel against the roof its counters show it is bound by.
+    'valu': the kernel's wave64 VALU instructions per launch (committed
+    rocprofv3 counters, taken on the two-stream default, scaled to this run's
+    launch size) over its live average launch time, against the issue peak
+    of one wave64 VALU instruction per SIMD every 4 cycles (614.4 G/s); used
+    when that share exceeds the HBM share.  'hbm': algorithmic bytes over the
+    live launch time against 8 TB/s.  Both shares are reported under their
+    own names, with the exhaustive-scan FLOP rate (which a pruned search can
+    push past the FLOP peak, so it is no roof for this kernel)."""
     ab = algorithmic_bytes(name, n, dim, m, parts)
     af = algorithmic_flops(name, n, dim, m, ksub, parts)
     avg_s = row["avg_ms"] * 1e-3
     hbm_gbs = ab / avg_s / 1e9 if ab else None
     hbm_frac = None if hbm_gbs is None else hbm_gbs / PEAK_HBM_GBS
-    tflops = af / avg_s / 1e12 if af else None
     v = valu.get(name) if valu else None
-    issue = v.get("valu_issue_frac") if v else None
-    valu_bound = (issue is not None and tflops is not None and hbm_frac is not None
-                  and issue > hbm_frac)
+    instr = None
+    if v and "SQ_INSTS_VALU" in v["counters"]:
+        # training kernels were counted as half launches (two streams)
+        training = name.startswith(("cand_kernel", "assign_kernel")) and ", true, true," not in name
+        instr = v["counters"]["SQ_INSTS_VALU"] * (2 / max(parts, 1) if training else 1)
+    ginstr = instr / avg_s / 1e9 if instr else None
+    issue_frac = None if ginstr is None else ginstr / PEAK_VALU_GINSTR
     tr = traffic.get(name) if traffic else None
     counted = None if not tr or "read_bytes" not in tr else tr["read_bytes"] + tr.get(
         "write_bytes", 0)
-    if valu_bound:
-        out = {"kernel": name, "bound": "valu", "achieved": round(tflops, 2),
-               "peak": PEAK_FP32_TFLOPS, "unit": "TFLOP/s",
-               "frac": round(tflops / PEAK_FP32_TFLOPS, 4)}
+    if issue_frac is not None and hbm_frac is not None and issue_frac > hbm_frac:
+        out = {"kernel": name, "bound": "valu", "achieved": round(ginstr, 1),
+               "peak": PEAK_VALU_GINSTR, "unit": "G wave64 VALU instr/s",
+               "frac": round(issue_frac, 4)}
     else:
         out = {"kernel": name, "bound": "hbm",
                "achieved": None if hbm_gbs is None else round(hbm_gbs, 1),
@@ -500,10 +509,10 @@ def roofline(name: str, row: dict, n: int, dim: int, m: int, ksub: int, traffic:
                "frac": None if hbm_frac is None else round(hbm_frac, 4)}
     out.update({
         "traffic": counted,
-        "valu_issue_frac": issue,
         "hbm_achieved_gbs": None if hbm_gbs is None else round(hbm_gbs, 1),
         "hbm_frac": None if hbm_frac is None else round(hbm_frac, 4),
-        "algorithmic_flop_per_launch": af,
+        "valu_issue_frac_live": None if issue_frac is None else round(issue_frac, 4),
+        "exhaustive_scan_tflops": None if not af else round(af / avg_s / 1e12, 2),
         "avg_launch_ms": row["avg_ms"], "algorithmic_bytes_per_launch": ab,
         "launches_per_step": row["launches_per_step"], "share_of_step": row["share_of_step"],
     })
@@ -513,7 +522,7 @@ def roofline(name: str, row: dict, n: int, dim: int, m: int, ksub: int, traffic:
     if v:
         c = v["counters"]
         out["valu"] = {
-            "issue_frac": issue, "busy": v.get("valu_busy"),
+            "issue_frac_counters": v.get("valu_issue_frac"), "busy": v.get("valu_busy"),
             "lane_util": v.get("valu_lane_util"),
             "lds_bank_conflict_frac": v.get("lds_bank_conflict_frac"),
             "instr_per_launch": int(c["SQ_INSTS_VALU"]) if "SQ_INSTS_VALU" in c else None,
@@ -904,6 +913,81 @@ def stream_200m(device):
 
 
 # ---------------------------------------------------------------------------
+# Counter passes and trace summaries
+# ---------------------------------------------------------------------------
+COUNTER_PASSES = {
+    "corpus": "corpus-1.52m: the benchmarked train (20 Lloyd iterations from seeded-shuffle "
+              "codebooks) and encode, one residual-stage call",
+    "m8d8": "corpus-1.52m-m8d8: 20-iteration train and encode",
+    "k1024": "corpus-1.52m-k1024: 20-iteration train and encode",
+    "stream-chunk": "stream-200m: encode of its first 10M-vector chunk (device-generated rows, "
+                    "fixed N(0, 0.05^2) codebooks)",
+}
+
+
+def counter_pass(device, errors, lib, synth, which, x, ids, dx):
+    """One run of a workload's benchmarked GPU work, for one rocprofv3 counter
+    pass, then a 1 GiB device-to-device copy whose counters calibrate the
+    byte counts."""
+    from tac_gpu import pq as pqmod
+    if which == "stream-chunk":
+        ws = synth.WORKLOADS["stream-200m"]
+        chunk = 10_000_000
+        gen = synth.DeviceCorpus(ws)
+        xs = device.DeviceArray((chunk, ws.dim), np.float32)
+        gen.fill(xs, chunk, 0)
+        dcb = device.DeviceArray.from_host(synth.gauss_codebooks(ws.seed, ws.m, ws.ksub,
+                                                                 ws.dsub, 0.05))
+        codes = device.DeviceArray((chunk, ws.m), np.uint8)
+        device.encode_device(xs, chunk, ws.dim, ws.m, ws.ksub, dcb, codes)
+        for a in (xs, dcb, codes):
+            a.free()
+        gen.free()
+    else:
+        name = {"corpus": WORKLOAD, "m8d8": "corpus-1.52m-m8d8",
+                "k1024": "corpus-1.52m-k1024"}[which]
+        w = synth.WORKLOADS[name]
+        init = synth.shuffle_init(x, w.m, w.ksub, w.seed)
+        dinit = device.DeviceArray.from_host(init)
+        dcb = device.DeviceArray(init.shape, np.float32)
+        codes = device.DeviceArray((w.n, w.m), pqmod.code_dtype(w.ksub))
+        device.train_device(dx, w.n, w.dim, w.m, w.ksub, dinit, dcb, w.iters, NEVER)
+        device.encode_device(dx, w.n, w.dim, w.m, w.ksub, dcb, codes)
+        for a in (dinit, dcb, codes):
+            a.free()
+        if which == "corpus":
+            residual_stage(device, x, ids, synth.WORKLOADS[WORKLOAD], 1)
+    a = device.DeviceArray((1 << 28,), np.float32)
+    b = device.DeviceArray((1 << 28,), np.float32)
+    errors.check(lib.tac_gpu_memcpy_dtod(b.ptr, a.ptr, a.nbytes))
+    device.synchronize()
+    print(json.dumps({"counter_pass": which, "work": COUNTER_PASSES[which],
+                      "copy_bytes": a.nbytes}), flush=True)
+
+
+def summarize_trace(out_base: str, trace_dir: str, title: str, commands=()) -> None:
+    """OUT.md: every kernel of a rocprofv3 --kernel-trace --stats run (its
+    *kernel_stats.csv), with calls, total and average duration."""
+    paths = sorted(Path(trace_dir).rglob("*kernel_stats.csv"))
+    if not paths:
+        raise SystemExit(f"no kernel_stats.csv under {trace_dir}")
+    rows = []
+    with open(paths[0], newline="") as f:
+        for r in csv.DictReader(f):
+            name = r["Name"].split("(")[0].removeprefix("void ").removeprefix("tacgpu::")
+            rows.append((name, int(r["Calls"]), float(r["TotalDurationNs"]),
+                         float(r["AverageNs"])))
+    rows.sort(key=lambda t: -t[2])
+    total = sum(t[2] for t in rows)
+    md = [f"# Kernel trace: {title}", "", "Command:", "```"] + list(commands) + ["```", "",
+          "| kernel | calls | total ms | share | average us |", "|---|---:|---:|---:|---:|"]
+    for name, calls, tot, avg in rows:
+        md.append(f"| {name} | {calls} | {tot / 1e6:.3f} | {tot / total:.4f} | {avg / 1e3:.2f} |")
+    Path(out_base + ".md").write_text("\n".join(md) + "\n")
+    log(f"wrote {out_base}.md ({len(rows)} kernels)")
+
+
+# ---------------------------------------------------------------------------
 def main() -> int:
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -912,10 +996,13 @@ def main() -> int:
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--headline-only", action="store_true",
                     help="skip the shape sweep, 60M, 200M and the rows around the path")
-    ap.add_argument("--traffic-pass", action="store_true",
-                    help="short run for hardware-counter passes: one 2-iteration train, one "
-                         "encode, one residual-stage call and a 1 GiB device-to-device copy "
-                         "(the calibration kernel)")
+    ap.add_argument("--counter-pass", choices=sorted(COUNTER_PASSES),
+                    help="one run of a workload's benchmarked work for rocprofv3 counter "
+                         "passes, then a 1 GiB device-to-device copy (the calibration kernel)")
+    ap.add_argument("--summarize-trace", nargs=2, metavar=("OUT", "DIR"),
+                    help="write OUT.md: the per-kernel table of a rocprofv3 --kernel-trace "
+                         "--stats run in DIR")
+    ap.add_argument("--trace-title", default="", help="title line for --summarize-trace")
     ap.add_argument("--cpu-protocol", nargs="+", metavar=("OUT_DIR", "WORKLOAD"),
                     help="the CPU baseline protocol of each named workload; writes "
                          "OUT_DIR/cpu_baseline_<workload>.json and .md")
@@ -925,6 +1012,10 @@ def main() -> int:
     ap.add_argument("--pmc-command", action="append", default=[],
                     help="a command line that produced the counters, quoted in OUT.md")
     args = ap.parse_args()
+    if args.summarize_trace:
+        summarize_trace(args.summarize_trace[0], args.summarize_trace[1], args.trace_title,
+                        args.pmc_command)
+        return 0
     if args.summarize_pmc:
         if len(args.summarize_pmc) < 2:
             ap.error("--summarize-pmc OUT DIR [DIR ...]")
@@ -963,16 +1054,8 @@ def main() -> int:
     dcb = device.DeviceArray(init.shape, np.float32)
     dcodes = device.DeviceArray((n, m), np.uint8)
 
-    if args.traffic_pass:
-        device.train_device(dx, n, dim, m, ksub, dinit, dcb, 2, NEVER)
-        device.encode_device(dx, n, dim, m, ksub, dcb, dcodes)
-        residual_stage(device, x, ids, w, 1)
-        a = device.DeviceArray((1 << 28,), np.float32)
-        b = device.DeviceArray((1 << 28,), np.float32)
-        errors.check(lib.tac_gpu_memcpy_dtod(b.ptr, a.ptr, a.nbytes))
-        device.synchronize()
-        print(json.dumps({"traffic_pass": WORKLOAD, "train_iters": 2, "encode": 1,
-                          "copy_bytes": a.nbytes}), flush=True)
+    if args.counter_pass:
+        counter_pass(device, errors, lib, synth, args.counter_pass, x, ids, dx)
         return 0
 
     for i in range(args.warmup):
