@@ -422,6 +422,8 @@ typedef struct tac_gpu_profile {
                               M is even (halves m < M/2 and m >= M/2 side by side), else 1.
                               With 2, assign_ms and update_ms time the first half while the
                               second runs beside it */
+  uint64_t cell_subspaces; /* encode subspaces that took the cell-list pass (rows wider than
+                              the codebook's box); the others took the anchored pass */
 } tac_gpu_profile;
 int tac_gpu_profile_enable(int enable);
 int tac_gpu_profile_read(tac_gpu_profile *out, int reset);

@@ -185,10 +185,12 @@ __global__ __launch_bounds__(kBlock) void grid_build_kernel(const float* __restr
                                                             AnchorT* __restrict__ anchors,
                                                             float* __restrict__ grid,
                                                             uint32_t K, uint32_t G,
-                                                            uint32_t cells) {
+                                                            uint32_t cells,
+                                                            const uint32_t* __restrict__ skip) {
   __shared__ float lcb[kCandMaxK * D];
   __shared__ float box[2 * D];
   const uint32_t m = blockIdx.y;
+  if (skip && skip[m]) return;  // a subspace another encode pass serves
   const float* cbm = cb + (uint64_t)m * K * D;
   for (uint32_t j = threadIdx.x; j < K * D; j += blockDim.x) lcb[j] = cbm[j];
   __syncthreads();
@@ -300,6 +302,7 @@ __global__ __launch_bounds__(kCandThreads, D <= 4 ? 8 : 4) void cand_kernel(
     if (logical >= nchunks * M) return;  // grid padding to a multiple of 8
     b = logical / M;
     m = logical % M;
+    if (done && done[m]) return;  // a subspace another encode pass serves
   } else {
     b = blockIdx.x;
     m = blockIdx.y;

@@ -19,6 +19,7 @@
 #include "../../include/tac_gpu.h"
 #include "pq_kernels.hpp"
 #include "cand_kernels.hpp"
+#include "cell_kernels.hpp"
 #include "kmeanspp.hpp"
 #include "storage_kernels.hpp"
 #include "query_kernels.hpp"
@@ -94,7 +95,7 @@ struct DeviceState {
   Buffer xs, codes, e, hist, counts, start, sorted, flags, scal, trace, io_in, io_out, io_cb,
       io_init, counter, kpp_state, kpp_w, kpp_bsum, kpp_bad, status, io_aux, io_out2, scan_sums,
       io_x1, io_x2, io_x3, crc_tx, fold_pre, fold_chunks, cand_nbr, cand_defer, cand_count, cand_anchor, cand_grid, kpp_src,
-      fold_order;
+      fold_order, cell_par, cell_cids, cell_ccnt, cell_rec, cell_list;
   // token-aware clustering
   Buffer tac_v, tac_idx, tac_offs, tac_G, tac_spreads, tac_w, tac_e, tac_code, tac_sorted,
       tac_tsum, tac_hist, tac_counts, tac_start, tac_C, tac_pre, tac_fch, tac_st, tac_bad,
@@ -371,21 +372,22 @@ int event_at(DeviceState &ds, size_t idx, hipEvent_t *out) {
 // Device counters: [0] exact rescans, [1] candidate-path deferrals,
 // [2] candidate-path assignments.
 int counter_begin(DeviceState &ds, hipStream_t s, unsigned long long **out) {
-  int st = ensure(ds, ds.counter, 3 * sizeof(unsigned long long));
+  int st = ensure(ds, ds.counter, 4 * sizeof(unsigned long long));
   if (st) return st;
-  HIP_TRY(hipMemsetAsync(ds.counter.ptr, 0, 3 * sizeof(unsigned long long), s));
+  HIP_TRY(hipMemsetAsync(ds.counter.ptr, 0, 4 * sizeof(unsigned long long), s));
   *out = reinterpret_cast<unsigned long long *>(ds.counter.ptr);
   return TAC_OK;
 }
 
 int counter_collect(DeviceState &ds, hipStream_t s) {
-  unsigned long long v[3] = {0, 0, 0};
+  unsigned long long v[4] = {0, 0, 0, 0};
   HIP_TRY(hipMemcpyAsync(v, ds.counter.ptr, sizeof(v), hipMemcpyDeviceToHost, s));
   HIP_TRY(hipStreamSynchronize(s));
   std::lock_guard<std::mutex> g(g_profile_mu);
   g_prof.exact_rescans += v[0];
   g_prof.cand_deferred += v[1];
   g_prof.cand_vectors += v[2];
+  g_prof.cell_subspaces += v[3];
   return TAC_OK;
 }
 
@@ -515,7 +517,7 @@ struct Launch {
       for (int k = 0; k < D; ++k) cells *= G;
       KT("grid_build_kernel<%d, %uu, %s>", D, NA, code_name<AnchorT>());
       grid_build_kernel<D, NA, AnchorT><<<dim3((cells + kBlock - 1) / kBlock, M), kBlock, 0, s>>>(
-          cb, anchors, grid, K, G, cells);
+          cb, anchors, grid, K, G, cells, nullptr);
       KT_END();
     }
     // About 1,024 blocks over all subspaces; a chunk is whole sort tiles
@@ -570,18 +572,18 @@ struct Launch {
   template <typename AnchorT>
   static void encode_tables(const float *cb, uint32_t *nbr, AnchorT *anchors, float *grid,
                             uint32_t *defer_count, uint32_t M, uint32_t K, uint32_t L,
-                            hipStream_t s) {
+                            hipStream_t s, const uint32_t *skip = nullptr) {
     const uint32_t G = cand_grid_side(D);
     uint32_t cells = 1;
     for (int k = 0; k < D; ++k) cells *= G;
     KT("nbr_build_kernel<%d>", D);
     nbr_build_kernel<D><<<dim3(K, M), nbr_threads(K), nbr_keys(K) * sizeof(uint32_t), s>>>(
-        cb, nbr, defer_count, nullptr, K, L);
+        cb, nbr, defer_count, skip, K, L);
     KT_END();
     KT("grid_build_kernel<%d, %uu, %s>", D, cand_anchors<true>(), code_name<AnchorT>());
     grid_build_kernel<D, cand_anchors<true>(), AnchorT><<<dim3((cells + kBlock - 1) / kBlock, M),
                                                           kBlock, 0, s>>>(
-        cb, anchors, grid, K, G, cells);
+        cb, anchors, grid, K, G, cells, skip);
     KT_END();
   }
   // The candidate pass over n token-major rows from the tables, then the
@@ -592,7 +594,8 @@ struct Launch {
                          const CodeT *anchors, const float *grid, uint32_t *slice,
                          uint32_t *defer, uint32_t *defer_count, uint64_t n, uint32_t dim,
                          uint32_t M, uint32_t K, uint32_t L, unsigned long long *rescans,
-                         unsigned long long *stats, hipStream_t s) {
+                         unsigned long long *stats, hipStream_t s,
+                         const uint32_t *skip = nullptr, bool deferred_pass = true) {
     const uint32_t G = cand_grid_side(D);
     uint32_t cells = 1;
     for (int k = 0; k < D; ++k) cells *= G;
@@ -609,15 +612,23 @@ struct Launch {
     const uint32_t blocks = (uint32_t)(8 * ((total + 7) / 8));
     KT("cand_kernel<%d, true, true, %s, %s>", D, code_name<CodeT>(), code_name<CodeT>());
     cand_kernel<D, true, true, CodeT, CodeT><<<blocks, kCandThreads, lay.total, s>>>(
-        x, cb, nbr, anchors, grid, nullptr, nullptr, codes, slice, defer, defer_count, nullptr, n,
+        x, cb, nbr, anchors, grid, nullptr, nullptr, codes, slice, defer, defer_count, skip, n,
         dim, M, K, L, (uint32_t)chunk, (uint32_t)nchunks, G, cells, nullptr, 0);
     KT_END();
+    if (!deferred_pass) return TAC_OK;
+    return encode_deferred<CodeT>(x, cb, codes, defer, defer_count, n, dim, M, K, rescans, stats, s);
+  }
+  // The deferred vectors of an encode pass: one per thread on about 4,096
+  // blocks over all subspaces when they are few, eight per thread when more
+  // than a quarter of a subspace's rows were deferred (each launch serves the
+  // subspaces of its width, blocks loop when there are more).
+  template <typename CodeT>
+  static int encode_deferred(const float *x, const float *cb, CodeT *codes,
+                             const uint32_t *defer, const uint32_t *defer_count, uint64_t n,
+                             uint32_t dim, uint32_t M, uint32_t K, unsigned long long *rescans,
+                             unsigned long long *stats, hipStream_t s) {
     const uint32_t Kp = (K + kPruneBlock - 1) / kPruneBlock * kPruneBlock;
     const size_t lds = (size_t)Kp * (Pad<D>::value + 1) * sizeof(float) + 2 * sizeof(uint32_t);
-    // The deferred vectors: one per thread on about 4,096 blocks over all
-    // subspaces when they are few, eight per thread when more than a quarter
-    // of a subspace's rows were deferred (each launch serves the subspaces of
-    // its width, blocks loop when there are more).
     const uint64_t g1 = std::max<uint64_t>(
         1, std::min<uint64_t>((n + kBlock - 1) / kBlock, (4096 + M - 1) / M));
     const uint64_t g8 = std::max<uint64_t>(
@@ -631,6 +642,61 @@ struct Launch {
         x, cb, codes, defer, defer_count, n, dim, M, K, rescans, stats);
     KT_END();
     return TAC_OK;
+  }
+  // Encode at sub-dimensions 1-4 with K <= 256: per subspace, the box
+  // kernel picks the cell-list encode (cell_kernels.hpp) when more than
+  // kCellOutside of a sample of the rows lies outside the codebook's box (the
+  // anchored encode would leave them to the full search), else the anchored
+  // candidate encode; every kernel of the other pass returns at once for that
+  // subspace.  mode 1 / 0 forces the cell lists / the anchored pass.  Then
+  // the reference scan of the deferred vectors of both.  slice / defer hold
+  // M * n words each.
+  template <typename CodeT>
+  static int encode_auto(const float *x, const float *cb, CodeT *codes, uint32_t *nbr,
+                         CodeT *anchors, float *grid, uint32_t *par, uint32_t *sel,
+                         uint8_t *cids, uint32_t *ccnt, uint32_t *rec, uint8_t *lists,
+                         uint32_t cap_items, uint32_t *slice, uint32_t *defer,
+                         uint32_t *defer_count, uint64_t n, uint32_t dim, uint32_t M, uint32_t K,
+                         uint32_t L, int mode, unsigned long long *rescans,
+                         unsigned long long *stats, unsigned long long *cells_stat,
+                         hipStream_t s) {
+    if constexpr (D > 4) {
+      return TAC_ERR_UNSUPPORTED;
+    } else {
+      constexpr uint32_t Cc = cell_coarse_count(D), F = cell_fine_per_coarse(D), CPB = 256 / F;
+      KT("cell_box_kernel<%d>", D);
+      cell_box_kernel<D><<<M, 256, 0, s>>>(x, cb, par, sel, defer_count, n, dim, K, mode,
+                                           cells_stat);
+      KT_END();
+      encode_tables<CodeT>(cb, nbr, anchors, grid, defer_count, M, K, L, s, sel);
+      if (int st = encode_rows<CodeT>(x, cb, codes, nbr, anchors, grid, slice, defer,
+                                      defer_count, n, dim, M, K, L, rescans, stats, s, sel,
+                                      false))
+        return st;
+      KT("cell_coarse_kernel<%d>", D);
+      cell_coarse_kernel<D><<<dim3((Cc + 3) / 4, M), 256, 0, s>>>(cb, par, cids, ccnt, K);
+      KT_END();
+      KT("cell_fine_kernel<%d>", D);
+      cell_fine_kernel<D><<<dim3((Cc + CPB - 1) / CPB, M), CPB * F, 0, s>>>(
+          cb, par, cids, ccnt, rec, lists, K, cap_items);
+      KT_END();
+      const CellLds lay = cell_lds(K, Pad<D>::value);
+      if (int st = raise_lds((const void *)cell_encode_kernel<D, CodeT>, lay.total, 0)) return st;
+      // Chunks of 8,192 rows; the M blocks of a chunk run on one XCD, so a
+      // row crosses HBM once and its other subspaces come from L2.
+      const uint64_t chunk = 8192;
+      const uint64_t nchunks = (n + chunk - 1) / chunk;
+      const uint64_t total = nchunks * M;
+      if (total > 0xFFFFFFF0ull) return TAC_ERR_UNSUPPORTED;
+      const uint32_t blocks = (uint32_t)(8 * ((total + 7) / 8));
+      KT("cell_encode_kernel<%d, %s>", D, code_name<CodeT>());
+      cell_encode_kernel<D, CodeT><<<blocks, kCandThreads, lay.total, s>>>(
+          x, cb, par, rec, lists, codes, slice, defer, defer_count, n, dim, M, K,
+          (uint32_t)chunk, (uint32_t)nchunks, cap_items);
+      KT_END();
+      return encode_deferred<CodeT>(x, cb, codes, defer, defer_count, n, dim, M, K, rescans,
+                                    stats, s);
+    }
   }
   static int scatter(const float *xs, const uint16_t *codes, const uint32_t *hist,
                      const uint32_t *start, float *sorted, const uint32_t *done, uint64_t n,
@@ -1217,6 +1283,18 @@ int train_core(DeviceState &ds, hipStream_t s, const float *d_x, uint64_t n, uin
   return TAC_OK;
 }
 
+// Fine and coarse cells per subspace of the cell-list encode at a runtime
+// sub-dimension (1-4).
+inline uint32_t cell_count_of(uint32_t D) {
+  return D == 1 ? cell_count(1) : D == 2 ? cell_count(2) : D == 3 ? cell_count(3) : cell_count(4);
+}
+inline uint32_t cell_coarse_count_of(uint32_t D) {
+  return D == 1   ? cell_coarse_count(1)
+         : D == 2 ? cell_coarse_count(2)
+         : D == 3 ? cell_coarse_count(3)
+                  : cell_coarse_count(4);
+}
+
 int encode_core(DeviceState &ds, hipStream_t s, const float *d_x, uint64_t n, uint32_t dim,
                 uint32_t M, uint32_t K, const float *d_cb, void *d_codes) {
   const uint32_t D = dim / M;
@@ -1244,7 +1322,38 @@ int encode_core(DeviceState &ds, hipStream_t s, const float *d_x, uint64_t n, ui
                     n >= 16384 && n <= 0xFFFFFFFFull &&
                     cand_lds(K, D_pad, cells, 0, cand_anchors<true>() * code_size).total <=
                         kCandLdsMax;
-  if (cand) {
+  // Sub-dimensions 1-4 with K <= 256 on kCellMinRows rows or more choose per
+  // subspace between the cell-list and the anchored encode (encode_auto).
+  // TAC_GPU_ENCODE_CELLS=1 or 0 forces one of them, =auto makes the choice
+  // at any size.
+  const char *cells_env = getenv("TAC_GPU_ENCODE_CELLS");
+  const int cell_mode = !cells_env ? -1 : cells_env[0] == '1' ? 1 : cells_env[0] == '0' ? 0 : -1;
+  const bool by_cells = cand && D >= 1 && D <= 4 && K <= 256 && (cells_env || n >= kCellMinRows);
+  if (by_cells) {
+    const uint32_t ncell = cell_count_of(D), ncoarse = cell_coarse_count_of(D);
+    const uint32_t cap_items = ncell * kCellItemsPerCell;
+    if ((st = ensure(ds, ds.cand_nbr, (size_t)M * K * cand_row_len(L) * sizeof(uint32_t))) ||
+        (st = ensure(ds, ds.cand_defer, (size_t)2 * M * n * sizeof(uint32_t))) ||
+        (st = ensure(ds, ds.cand_count, (size_t)M * sizeof(uint32_t))) ||
+        (st = ensure(ds, ds.cand_anchor, (size_t)M * kCandCells * kCandAnchorsMax * code_size)) ||
+        (st = ensure(ds, ds.cand_grid, (size_t)M * 16 * sizeof(float))) ||
+        (st = ensure(ds, ds.cell_par, (size_t)M * (kCellParWords + 1) * sizeof(uint32_t))) ||
+        (st = ensure(ds, ds.cell_cids, (size_t)M * ncoarse * K)) ||
+        (st = ensure(ds, ds.cell_ccnt, (size_t)M * ncoarse * sizeof(uint32_t))) ||
+        (st = ensure(ds, ds.cell_rec, (size_t)M * ncell * sizeof(uint32_t))) ||
+        (st = ensure(ds, ds.cell_list, (size_t)M * cap_items * kCellItem)))
+      return st;
+    uint32_t *slices = as<uint32_t>(ds.cand_defer);
+    uint32_t *par = as<uint32_t>(ds.cell_par);
+    DISPATCH_D_ST(D, encode_auto<uint8_t>(
+                         d_x, d_cb, (uint8_t *)d_codes, as<uint32_t>(ds.cand_nbr),
+                         as<uint8_t>(ds.cand_anchor), as<float>(ds.cand_grid), par,
+                         par + (size_t)M * kCellParWords, as<uint8_t>(ds.cell_cids),
+                         as<uint32_t>(ds.cell_ccnt), as<uint32_t>(ds.cell_rec),
+                         as<uint8_t>(ds.cell_list), cap_items, slices, slices + (size_t)M * n,
+                         as<uint32_t>(ds.cand_count), n, dim, M, K, L, cell_mode, rescans,
+                         g_profile ? rescans + 1 : nullptr, g_profile ? rescans + 3 : nullptr, s));
+  } else if (cand) {
     if ((st = ensure(ds, ds.cand_nbr, (size_t)M * K * cand_row_len(L) * sizeof(uint32_t))) ||
         (st = ensure(ds, ds.cand_defer, (size_t)2 * M * n * sizeof(uint32_t))) ||
         (st = ensure(ds, ds.cand_count, (size_t)M * sizeof(uint32_t))) ||

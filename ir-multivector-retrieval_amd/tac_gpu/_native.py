@@ -73,6 +73,7 @@ class Profile(ctypes.Structure):
         ("cand_assign_ms", ctypes.c_double),
         ("cand_assign_iters", c_u64),
         ("train_streams", c_u64),
+        ("cell_subspaces", c_u64),
     ]
 
 
