@@ -876,7 +876,7 @@ def stream_200m(device):
     device.encode_device(dx, chunk, w.dim, w.m, w.ksub, dcb, dcodes)  # warm-up
     device.synchronize()
     enc = []
-    deferred = vectors = 0
+    deferred = vectors = cell_subspaces = 0
     hist = np.zeros(w.ksub, np.int64)
     t_all = time.perf_counter()
     for k in range(w.n // chunk):
@@ -889,6 +889,7 @@ def stream_200m(device):
         enc.append(p.encode_ms)
         deferred += p.cand_deferred
         vectors += p.cand_vectors
+        cell_subspaces += p.cell_subspaces
         if k == 0:
             hist += np.bincount(dcodes.to_host().reshape(-1), minlength=w.ksub)
     wall = time.perf_counter() - t_all
@@ -907,6 +908,7 @@ def stream_200m(device):
             "stream_wall_s": round(wall, 2),
             "codes_in_range_chunk0": int(hist.sum()) == chunk * w.m,
             "candidate_deferred_frac": round(deferred / max(vectors, 1), 5),
+            "cell_list_subspaces_per_chunk": round(cell_subspaces / max(len(enc), 1), 2),
             "data": "synthetic, generated on the device chunk by chunk",
             "cpu_baseline": cpu_profile_row("stream-200m", tot_ms * 1e-3,
                                             w.n / (tot_ms * 1e-3) / 1e6)}
