@@ -312,6 +312,7 @@ def short_name(kernel: str) -> str:
     """'void tacgpu::cand_kernel<4, false, ...>(float const*, ...)' ->
     'cand_kernel<4, false, ...>'."""
     k = kernel.replace("void ", "", 1) if kernel.startswith("void ") else kernel
+    k = k.removeprefix("(anonymous namespace)::")
     depth, cut = 0, len(k)
     for i, ch in enumerate(k):
         if ch == "<":
@@ -976,7 +977,8 @@ def summarize_trace(out_base: str, trace_dir: str, title: str, commands=()) -> N
     rows = []
     with open(paths[0], newline="") as f:
         for r in csv.DictReader(f):
-            name = r["Name"].split("(")[0].removeprefix("void ").removeprefix("tacgpu::")
+            name = (r["Name"].removeprefix("(anonymous namespace)::").split("(")[0]
+                    .removeprefix("void ").removeprefix("tacgpu::"))
             rows.append((name, int(r["Calls"]), float(r["TotalDurationNs"]),
                          float(r["AverageNs"])))
     rows.sort(key=lambda t: -t[2])
@@ -1012,7 +1014,7 @@ def main() -> int:
                     help="write OUT.json and OUT.md: per-kernel averages of rocprofv3 counter "
                          "CSVs in DIRs")
     ap.add_argument("--pmc-command", action="append", default=[],
-                    help="a command line that produced the counters, quoted in OUT.md")
+                    help="a command line that produced the counters or the trace, quoted in OUT.md")
     args = ap.parse_args()
     if args.summarize_trace:
         summarize_trace(args.summarize_trace[0], args.summarize_trace[1], args.trace_title,
