@@ -1175,7 +1175,7 @@ def main() -> int:
             "traffic": sum(traffic[k]["read_bytes"] + traffic[k].get("write_bytes", 0)
                            for k in traffic if "read_bytes" in traffic[k] and k.startswith(
                                ("hist_kernel", "scan_partial", "scan_apply", "scatter_kernel",
-                                "fold_order", "fold_kernel", "reseed_kernel", "converge_kernel")))
+                                "fold_kernel", "reseed_kernel")))
                        or None,
         },
         "kernels": {k: v for k, v in list(kernels.items())[:12]},

@@ -472,6 +472,37 @@ __global__ __launch_bounds__(kBlock) void hist_kernel(
 // and starts.
 constexpr uint32_t kScanRanges = 32;
 
+// The fold's launch order of one subspace, from the block that holds its
+// cluster sizes (thread t holds codes c0 .. c0 + per_c - 1): clusters binned
+// by size (bin = count / unit, kFoldOrderBins bins, the last taking every
+// larger cluster) and listed from the largest bin down into order[0 .. K),
+// so the longest serial chains of the fold start first and the short ones
+// fill the SIMDs around them.  The sums do not depend on the order; within a
+// bin it follows the atomics.
+constexpr uint32_t kFoldOrderBins = 256;
+__device__ inline void fold_order_block(const uint32_t (&tot)[4], uint32_t per_c, uint32_t c0,
+                                        uint32_t K, uint32_t* __restrict__ order,
+                                        uint32_t unit) {
+  __shared__ uint32_t bins[kFoldOrderBins];
+  __shared__ uint32_t osum[kBlock / kWave];
+  auto bin_of = [&](uint32_t cnt) {  // 0 = the largest clusters
+    const uint32_t b = cnt / unit;
+    return kFoldOrderBins - 1u - (b < kFoldOrderBins - 1u ? b : kFoldOrderBins - 1u);
+  };
+  for (uint32_t j = threadIdx.x; j < kFoldOrderBins; j += blockDim.x) bins[j] = 0;
+  __syncthreads();
+  for (uint32_t q = 0; q < per_c; ++q)
+    if (c0 + q < K) atomicAdd(&bins[bin_of(tot[q])], 1u);
+  __syncthreads();
+  const uint32_t first =
+      block_exclusive_scan(threadIdx.x < kFoldOrderBins ? bins[threadIdx.x] : 0u, osum);
+  __syncthreads();
+  if (threadIdx.x < kFoldOrderBins) bins[threadIdx.x] = first;
+  __syncthreads();
+  for (uint32_t q = 0; q < per_c; ++q)
+    if (c0 + q < K) order[atomicAdd(&bins[bin_of(tot[q])], 1u)] = c0 + q;
+}
+
 __global__ __launch_bounds__(kBlock) void scan_partial_kernel(
     const uint32_t* __restrict__ hist, uint32_t* __restrict__ part,
     const uint32_t* __restrict__ done, uint32_t K, uint32_t T, uint32_t G) {
@@ -499,8 +530,8 @@ __global__ __launch_bounds__(kBlock) void scan_partial_kernel(
 
 __global__ __launch_bounds__(kBlock) void scan_apply_kernel(
     uint32_t* __restrict__ hist, const uint32_t* __restrict__ part,
-    uint32_t* __restrict__ counts, uint32_t* __restrict__ start,
-    const uint32_t* __restrict__ done, uint32_t K, uint32_t T, uint32_t G) {
+    uint32_t* __restrict__ counts, uint32_t* __restrict__ start, uint32_t* __restrict__ order,
+    const uint32_t* __restrict__ done, uint32_t K, uint32_t T, uint32_t G, uint32_t unit) {
   __shared__ uint32_t wsum[kBlock / kWave];
   const uint32_t m = blockIdx.y, g = blockIdx.x;
   if (done[m]) return;
@@ -524,6 +555,7 @@ __global__ __launch_bounds__(kBlock) void scan_apply_kernel(
     local += tot[q];
   }
   uint32_t st = block_exclusive_scan(local, wsum);
+  if (g == 0) fold_order_block(tot, per_c, c0, K, order + (uint64_t)m * K, unit);
   for (uint32_t q = 0; q < per_c; ++q) {
     const uint32_t c = c0 + q;
     if (c >= K) break;
@@ -732,35 +764,9 @@ __global__ __launch_bounds__(kBlock) void scatter_kernel(
   }
 }
 
-// Step 4a: the fold's launch order.  Clusters of all subspaces are binned by
-// size (bin = count / unit, 256 bins, the last taking every larger cluster)
-// and listed from the largest bin down, so the longest serial chains of
-// step 4 start first and the short ones fill the SIMDs around them.  The
-// sums do not depend on the order; within a bin it follows the atomics.
-// One block of 1024 threads.
-constexpr uint32_t kFoldOrderBins = 256;
-__global__ __launch_bounds__(1024) void fold_order_kernel(const uint32_t* __restrict__ counts,
-                                                          uint32_t* __restrict__ order, uint32_t E,
-                                                          uint32_t unit) {
-  __shared__ uint32_t bins[kFoldOrderBins];
-  __shared__ uint32_t wsum[1024 / kWave];
-  const uint32_t t = threadIdx.x;
-  if (t < kFoldOrderBins) bins[t] = 0;
-  __syncthreads();
-  auto bin_of = [&](uint32_t cnt) {  // 0 = the largest clusters
-    const uint32_t b = cnt / unit;
-    return kFoldOrderBins - 1u - (b < kFoldOrderBins - 1u ? b : kFoldOrderBins - 1u);
-  };
-  for (uint32_t j = t; j < E; j += blockDim.x) atomicAdd(&bins[bin_of(counts[j])], 1u);
-  __syncthreads();
-  const uint32_t first = block_exclusive_scan(t < kFoldOrderBins ? bins[t] : 0u, wsum);
-  __syncthreads();
-  if (t < kFoldOrderBins) bins[t] = first;
-  __syncthreads();
-  for (uint32_t j = t; j < E; j += blockDim.x) order[atomicAdd(&bins[bin_of(counts[j])], 1u)] = j;
-}
-
-// Step 4: one wave per (subspace, cluster), in the order of step 4a.  The wave streams the cluster's
+// Step 4: one wave per (subspace, cluster): block r * M + m folds the cluster
+// of rank r in subspace m's size order (fold_order_block), so every
+// subspace's largest clusters start first.  The wave streams the cluster's
 // contiguous records with coalesced loads (kFoldBatch x 64 records in
 // flight, staged through LDS dimension-major) and lanes 0..D-1 fold
 // dimension d in ascending vector order from 0.0f, then write
@@ -771,14 +777,13 @@ __global__ __launch_bounds__(kWave) void fold_kernel(
     const float* __restrict__ sorted, const uint32_t* __restrict__ counts,
     const uint32_t* __restrict__ start, float* __restrict__ cb,
     const uint32_t* __restrict__ done, const uint32_t* __restrict__ order, uint64_t n,
-    uint32_t K) {
+    uint32_t M, uint32_t K) {
   constexpr int DP = Pad<D>::value;
   constexpr uint32_t U = kFoldBatch;
   // Padded: the D columns start on distinct banks.
   constexpr uint32_t kCol = U * kWave + 36;
   __shared__ __attribute__((aligned(16))) float buf[kCol * DP];
-  const uint32_t id = order[blockIdx.x];
-  const uint32_t m = id / K, c = id % K;
+  const uint32_t m = blockIdx.x % M, c = order[(uint64_t)m * K + blockIdx.x / M];
   if (done[m]) return;
   const uint32_t cnt = counts[(uint64_t)m * K + c];
   if (cnt == 0) return;
@@ -1066,8 +1071,9 @@ __global__ __launch_bounds__(kWave) void wcss_apply_kernel(
 template <int D>
 __global__ __launch_bounds__(1024) void reseed_kernel(
     const float* __restrict__ xs, float* __restrict__ e, const uint32_t* __restrict__ counts,
-    float* __restrict__ cb, uint32_t* __restrict__ empties, const uint32_t* __restrict__ done,
-    uint64_t n, uint32_t K) {
+    float* __restrict__ cb, uint32_t* __restrict__ empties, uint32_t* __restrict__ done,
+    const float* __restrict__ wcss, float* __restrict__ prev, uint32_t* __restrict__ iters_run,
+    uint64_t n, uint32_t K, uint32_t iter, float tol, int check) {
   constexpr int DP = Pad<D>::value;
   __shared__ float sv[1024 / kWave];
   __shared__ uint64_t si[1024 / kWave];
@@ -1130,29 +1136,23 @@ __global__ __launch_bounds__(1024) void reseed_kernel(
     }
     __syncthreads();
   }
-  if (threadIdx.x == 0) empties[m] += found;
-}
-
-// Convergence bookkeeping (src/tac/kmeans.zig:186, :214-223), run after the
-// update of iteration `iter`.
-__global__ void converge_kernel(const float* __restrict__ wcss, float* __restrict__ prev,
-                                uint32_t* __restrict__ done, uint32_t* __restrict__ iters_run,
-                                uint32_t M, uint32_t iter, float tol, int check) {
-  const uint32_t m = blockIdx.x * blockDim.x + threadIdx.x;
-  if (m >= M || done[m]) return;
+  if (threadIdx.x != 0) return;
+  empties[m] += found;
+  // Convergence bookkeeping (src/tac/kmeans.zig:186, :214-223) of iteration
+  // `iter`, whose wcss the update computed before the reseed.
   iters_run[m] = iter + 1;
   if (!check) return;
-  const float w = wcss[m];
+  const float ws = wcss[m];
   if (iter > 0) {
     const float p = prev[m];
     const float denom = p > 0.0f ? p : 1.0f;
-    const float rel = (p - w) / denom;
+    const float rel = (p - ws) / denom;
     if (rel < tol) {
       done[m] = 1;
       return;
     }
   }
-  prev[m] = w;
+  prev[m] = ws;
 }
 
 // Degenerate k >= n (src/tac/kmeans.zig:88-104): codeword c of subspace m is

@@ -727,22 +727,19 @@ struct Launch {
     kpp_update_kernel<D><<<dim3(NB, M), 256, 0, s>>>(xs, w, src, bsum, bad, st, cb, n, K, c, NB);
   }
   static void fold(const float *sorted, const uint32_t *counts, const uint32_t *start,
-                   float *cb, const uint32_t *done, uint32_t *order, uint64_t n, uint32_t M,
+                   float *cb, const uint32_t *done, const uint32_t *order, uint64_t n, uint32_t M,
                    uint32_t K, hipStream_t s) {
-    // Bins of 1/32 of the mean cluster size.
-    const uint32_t unit = (uint32_t)std::max<uint64_t>(1, n / K / 32);
-    KT("fold_order_kernel");
-    fold_order_kernel<<<1, 1024, 0, s>>>(counts, order, M * K, unit);
-    KT_END();
     KT("fold_kernel<%d>", D);
-    fold_kernel<D><<<M * K, kWave, 0, s>>>(sorted, counts, start, cb, done, order, n, K);
+    fold_kernel<D><<<M * K, kWave, 0, s>>>(sorted, counts, start, cb, done, order, n, M, K);
     KT_END();
   }
   static void reseed(const float *xs, float *e, const uint32_t *counts, float *cb,
-                     uint32_t *empties, const uint32_t *done, uint64_t n, uint32_t M, uint32_t K,
-                     hipStream_t s) {
+                     uint32_t *empties, uint32_t *done, const float *wcss, float *prev,
+                     uint32_t *iters_run, uint64_t n, uint32_t M, uint32_t K, uint32_t iter,
+                     float tol, int check, hipStream_t s) {
     KT("reseed_kernel<%d>", D);
-    reseed_kernel<D><<<M, 1024, 0, s>>>(xs, e, counts, cb, empties, done, n, K);
+    reseed_kernel<D><<<M, 1024, 0, s>>>(xs, e, counts, cb, empties, done, wcss, prev, iters_run,
+                                        n, K, iter, tol, check);
     KT_END();
   }
   template <typename CodeT>
@@ -1117,8 +1114,10 @@ int train_core(DeviceState &ds, hipStream_t s, const float *d_x, uint64_t n, uin
     scan_partial_kernel<<<dim3(G, Mh), kBlock, 0, hs>>>(hist_h, scan_h, done_h, K, T, G);
     KT_END();
     KT("scan_apply_kernel");
-    scan_apply_kernel<<<dim3(G, Mh), kBlock, 0, hs>>>(hist_h, scan_h, counts_h, start_h, done_h,
-                                                      K, T, G);
+    // the fold's order: bins of 1/32 of the mean cluster size
+    scan_apply_kernel<<<dim3(G, Mh), kBlock, 0, hs>>>(
+        hist_h, scan_h, counts_h, start_h, order_h, done_h, K, T, G,
+        (uint32_t)std::max<uint64_t>(1, n / K / 32));
     KT_END();
     LAUNCH_TRY("scan kernels");
     DISPATCH_D_ST(D, scatter(xs_h, codes_h, hist_h, start_h, sorted_h, done_h, n, Mh, K, T, hs));
@@ -1143,13 +1142,9 @@ int train_core(DeviceState &ds, hipStream_t s, const float *d_x, uint64_t n, uin
       KT_END();
       LAUNCH_TRY("wcss kernels");
     }
-    DISPATCH_D(D, reseed(xs_h, e_h, counts_h, cb_h, empties + m0, done_h, n, Mh, K, hs));
+    DISPATCH_D(D, reseed(xs_h, e_h, counts_h, cb_h, empties + m0, done_h, wcss + m0, prev + m0,
+                         iters_run + m0, n, Mh, K, t, tol, check ? 1 : 0, hs));
     LAUNCH_TRY("reseed_kernel");
-    KT("converge_kernel");
-    converge_kernel<<<(Mh + 63) / 64, 64, 0, hs>>>(wcss + m0, prev + m0, done_h, iters_run + m0,
-                                                    Mh, t, tol, check ? 1 : 0);
-    KT_END();
-    LAUNCH_TRY("converge_kernel");
     if (want_trace)
       HIP_TRY(hipMemcpyAsync(as<float>(ds.trace) + (size_t)t * cb_elems + (size_t)m0 * K * D,
                              cb_h, (size_t)Mh * K * D * sizeof(float), hipMemcpyDeviceToDevice,
