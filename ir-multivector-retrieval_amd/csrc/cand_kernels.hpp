@@ -438,13 +438,7 @@ __global__ __launch_bounds__(kCandThreads, D <= 4 ? 8 : 4) void cand_kernel(
         const uint4 s0 = *reinterpret_cast<const uint4*>(lsamp + a * 8);
         const uint4 s1 = *reinterpret_cast<const uint4*>(lsamp + a * 8 + 4);
         const uint32_t sw[8] = {s0.x, s0.y, s0.z, s0.w, s1.x, s1.y, s1.z, s1.w};
-        uint16_t sv[kCandSamples];
-#pragma unroll
-        for (uint32_t q = 0; q < 8; ++q) {
-          sv[2 * q] = (uint16_t)(sw[q] & 0xFFFFu);
-          sv[2 * q + 1] = (uint16_t)(sw[q] >> 16);
-        }
-        nit = cand_items16(sv, R2, L, row_complete, &deferred);
+        nit = cand_items_words(sw, R2, L, row_complete, &deferred);
         if constexpr (GRID) {
           // A grid anchor sits farther from its vector than a previous code:
           // the long rows' items 8-15 cost more there than the full search

@@ -123,6 +123,33 @@ TAC_HD inline uint32_t cand_items16(const uint16_t (&samples)[kCandSamples], flo
   return *deferred ? 0u : nit;
 }
 
+// The same count from the 8 words that hold the samples two to a word
+// (sample 2w in the low half of word w).  A truncated sample h is inside R2
+// exactly when h <= bits(R2) >> 16: h << 16 is a non-negative float or the
+// NaN padding (0xFFFF, never inside), non-negative floats order as their
+// bits, and R2 is finite and non-negative.  Samples never decrease along a
+// row, so the count is found by a binary search: four probes find it up to
+// 15, a fifth tells 15 from 16.  Every probe picks its word with selects on
+// the bits found so far (no indexed register reads).
+TAC_HD inline uint32_t cand_items_words(const uint32_t (&w)[8], float R2, uint32_t L,
+                                        bool row_complete, bool* deferred) {
+  const uint32_t lim = cand_f2u(R2) >> 16;
+  uint32_t b = (w[3] >> 16) <= lim ? 8u : 0u;                     // sample 7
+  const uint32_t w2 = b ? w[5] : w[1];                            // sample b + 3
+  b += (w2 >> 16) <= lim ? 4u : 0u;
+  const uint32_t lo3 = (b & 4u) ? w[2] : w[0], hi3 = (b & 4u) ? w[6] : w[4];
+  const uint32_t w3 = (b & 8u) ? hi3 : lo3;                       // sample b + 1
+  b += (w3 >> 16) <= lim ? 2u : 0u;
+  const uint32_t a0 = (b & 2u) ? w[1] : w[0], a1 = (b & 2u) ? w[3] : w[2];
+  const uint32_t a2 = (b & 2u) ? w[5] : w[4], a3 = (b & 2u) ? w[7] : w[6];
+  const uint32_t a01 = (b & 4u) ? a1 : a0, a23 = (b & 4u) ? a3 : a2;
+  const uint32_t w4 = (b & 8u) ? a23 : a01;                       // sample b
+  b += (w4 & 0xFFFFu) <= lim ? 1u : 0u;
+  b += (b == 15u && (w[7] >> 16) <= lim) ? 1u : 0u;               // sample 15
+  *deferred = b >= cand_row_samples(L) && !row_complete;
+  return *deferred ? 0u : b;
+}
+
 // Entry j of the row is a candidate when j < L and its value is inside R2.
 TAC_HD inline bool cand_is_candidate(uint32_t key, uint32_t j, uint32_t L, float R2) {
   return j < L && cand_key_value(key) <= R2;

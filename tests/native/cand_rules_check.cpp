@@ -49,7 +49,40 @@ struct Counts {
   long checks = 0, deferred = 0, wrong = 0, planted_radius = 0, planted_ties = 0;
   long skip_checks = 0, skips = 0, skip_wrong = 0;
   long row_overrun = 0;
+  long search_mismatch = 0, search_checks = 0;
 };
+
+// The binary search against the linear count on sorted sample rows built to
+// put R2 on, just below and just above every sample (and NaN tails).
+static void search_cases(Counts& ct) {
+  for (int rep = 0; rep < 200000; ++rep) {
+    uint16_t sv[kCandSamples];
+    const uint32_t valid = (uint32_t)(next_u64() % 17);  // samples before the NaN tail
+    uint16_t v = (uint16_t)(next_u64() % 0x7F00);
+    for (uint32_t q = 0; q < kCandSamples; ++q) {
+      if (q < valid) {
+        v = (uint16_t)std::min<uint32_t>(0x7F7Fu, v + (uint32_t)(next_u64() % 3 == 0 ? 0 : next_u64() % 300));
+        sv[q] = v;
+      } else {
+        sv[q] = 0xFFFF;
+      }
+    }
+    const uint32_t pick = (uint32_t)(next_u64() % kCandSamples);
+    const uint32_t base = valid ? sv[std::min(pick, valid - 1)] : (uint32_t)(next_u64() % 0x7F00);
+    const int delta = (int)(next_u64() % 3) - 1;
+    const uint32_t hi = (uint32_t)std::min<int64_t>(0x7F7F, std::max<int64_t>(0, (int64_t)base + delta));
+    const float R2 = cand_u2f((hi << 16) | (uint32_t)(next_u64() & 0xFFFF));
+    const uint32_t L = (uint32_t)(next_u64() % 200);
+    const bool complete = next_u64() % 4 == 0;
+    bool d1 = false, d2 = false;
+    const uint32_t n1 = cand_items16(sv, R2, L, complete, &d1);
+    uint32_t words[8];
+    for (uint32_t q = 0; q < 8; ++q) words[q] = (uint32_t)sv[2 * q] | ((uint32_t)sv[2 * q + 1] << 16);
+    const uint32_t n2 = cand_items_words(words, R2, L, complete, &d2);
+    ++ct.search_checks;
+    if (n1 != n2 || d1 != d2) ++ct.search_mismatch;
+  }
+}
 
 static void run_case(const std::vector<float>& cb, int K, int D, const std::vector<float>& xs,
                      int n, uint32_t Lmax, Counts& ct) {
@@ -103,6 +136,13 @@ static void run_case(const std::vector<float>& cb, int K, int D, const std::vect
       const float R2 = cand_radius(U2, g);
       bool deferred = false;
       const uint32_t nit = cand_items16(sv, R2, L, row_complete, &deferred);
+      {  // the kernels' binary search over the packed words gives the same count
+        uint32_t words[8];
+        for (uint32_t q = 0; q < 8; ++q) words[q] = (uint32_t)sv[2 * q] | ((uint32_t)sv[2 * q + 1] << 16);
+        bool d2 = false;
+        const uint32_t n2 = cand_items_words(words, R2, L, row_complete, &d2);
+        if (n2 != nit || d2 != deferred) ++ct.search_mismatch;
+      }
       if (nit * kCandItem > Lr) ++ct.row_overrun;  // items must stay inside the stored row
       if (deferred) {
         ++ct.deferred;
@@ -185,9 +225,11 @@ int main() {
               ct.checks, ct.deferred, ct.wrong, ct.planted_radius, ct.planted_ties);
   std::printf("kmeans++ skip: %ld checks, %ld skips, %ld skip_wrong\n", ct.skip_checks, ct.skips,
               ct.skip_wrong);
+  search_cases(ct);
   std::printf("items: row_overrun %ld\n", ct.row_overrun);
+  std::printf("binary search: %ld checks, %ld search_mismatch\n", ct.search_checks, ct.search_mismatch);
   return ct.wrong == 0 && ct.skip_wrong == 0 && ct.skips > 0 && ct.planted_radius > 0 &&
-                 ct.planted_ties > 0 && ct.row_overrun == 0
+                 ct.planted_ties > 0 && ct.row_overrun == 0 && ct.search_mismatch == 0
              ? 0
              : 1;
 }

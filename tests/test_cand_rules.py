@@ -19,3 +19,4 @@ def test_cand_rules(tmp_path):
     assert r.returncode == 0, r.stdout + r.stderr
     assert " 0 wrong;" in r.stdout, r.stdout
     assert "row_overrun 0" in r.stdout, r.stdout
+    assert " 0 search_mismatch" in r.stdout, r.stdout
