@@ -882,6 +882,23 @@ int kmeanspp(DeviceState &ds, hipStream_t s, const SubspaceGroup *groups, uint32
   return TAC_OK;
 }
 
+// Whether the candidate-set passes serve a shape.  Past a few dimensions the
+// candidate ball around an anchor holds most of a 256-codeword book (its
+// volume grows as 2^D): the rows run out and most vectors fall through to the
+// full search anyway.  On 1.52M corpus rows at m8 K256 the Lloyd loop ran
+// faster with the pruned full search from dsub 7 on (19.7 against 24.4 ms at
+// dsub 8; a tie at 6) and encode from dsub 5 on (0.83 against 1.14 ms at 8).
+// Larger books keep the candidate passes: the full search costs K per vector.
+// TAC_GPU_FULL_SEARCH=1 turns the candidate passes off everywhere,
+// TAC_GPU_CANDIDATES=1 keeps them at every dsub (both for auditing).
+bool cand_wanted(uint32_t D, uint32_t K, bool encode) {
+  const char *full_env = getenv("TAC_GPU_FULL_SEARCH");
+  if (full_env && full_env[0] == '1') return false;
+  const char *cand_env = getenv("TAC_GPU_CANDIDATES");
+  if (cand_env && cand_env[0] == '1') return true;
+  return K > 256 || D <= (encode ? 4u : 6u);
+}
+
 // Lloyd training of all subspaces.  `out.cb` holds the initial codebooks on
 // entry and the trained ones on return.
 int train_core(DeviceState &ds, hipStream_t s, const float *d_x, uint64_t n, uint32_t dim,
@@ -943,14 +960,12 @@ int train_core(DeviceState &ds, hipStream_t s, const float *d_x, uint64_t n, uin
   // Candidate-set assignment (cand_kernels.hpp) when the codeword ids fit the
   // neighbour keys and the tables fit in LDS: iterations after the first
   // start from the previous codes, and the first, on 16,384 vectors or more,
-  // from grid anchors.  TAC_GPU_FULL_SEARCH=1 keeps the full search in every
-  // iteration.
-  const char *full_env = getenv("TAC_GPU_FULL_SEARCH");
+  // from grid anchors; cand_wanted decides the sub-dimensions and switches.
   const uint32_t Lc = K >= 2 ? std::min<uint32_t>(dim / M <= 4 ? kCandList : kCandListWide, K - 1) : 0;
   // Anchors (first iteration) are u8 ids up to K = 256, u16 beyond; the
   // block's tables must fit the LDS with at least one sort tile.
   const uint32_t anchor_size = K <= 256 ? 1u : 2u;
-  const bool cand_ok = !(full_env && full_env[0] == '1') && K >= 2 && K <= kCandMaxK &&
+  const bool cand_ok = cand_wanted(D, K, false) && K >= 2 && K <= kCandMaxK &&
                        cand_lds(K, DP, kCandCells, 1, cand_anchors<false>() * anchor_size).total <=
                            kCandLdsMax &&
                        n <= 0xFFFFFFFFull;
@@ -1168,7 +1183,7 @@ int train_core(DeviceState &ds, hipStream_t s, const float *d_x, uint64_t n, uin
   // the exact argmin; these are the nearest at hand), over every subspace,
   // then the codes turned token-major.  Without the candidate tables the
   // caller runs the ordinary encode.
-  if (out.codes_out && (cand || cand_first) && max_iters >= 1) {
+  if (out.codes_out && (cand || cand_first) && max_iters >= 1 && cand_wanted(D, K, true)) {
     hipEvent_t ea = nullptr, eb = nullptr;
     if (profile) {
       if ((st = event_at(ds, ev++, &ea)) || (st = event_at(ds, ev++, &eb))) return st;
@@ -1305,15 +1320,14 @@ int encode_core(DeviceState &ds, hipStream_t s, const float *d_x, uint64_t n, ui
   }
   st = TAC_OK;
   // Batches of 16,384 vectors or more take the candidate-set encode
-  // (cand_kernels.hpp); TAC_GPU_FULL_SEARCH=1 keeps the full search.
-  const char *full_env = getenv("TAC_GPU_FULL_SEARCH");
+  // (cand_kernels.hpp) where cand_wanted says so.
   const uint32_t L = K >= 2 ? std::min<uint32_t>(kCandListEncode, K - 1) : 0;
   // Codes and grid anchors share one width: u8 up to K = 256, u16 beyond.
   const uint32_t code_size = K <= 256 ? 1u : 2u;
   const uint32_t G = cand_grid_side(D), D_pad = pad_of(D);
   uint32_t cells = 1;
   for (uint32_t k = 0; k < D; ++k) cells *= G;
-  const bool cand = !(full_env && full_env[0] == '1') && K >= 2 && K <= kCandMaxK &&
+  const bool cand = cand_wanted(D, K, true) && K >= 2 && K <= kCandMaxK &&
                     n >= 16384 && n <= 0xFFFFFFFFull &&
                     cand_lds(K, D_pad, cells, 0, cand_anchors<true>() * code_size).total <=
                         kCandLdsMax;
@@ -1767,9 +1781,8 @@ int tac_pq_encode_device_noalloc(const float *d_residuals, uint64_t n, uint32_t 
   auto *counters = reinterpret_cast<unsigned long long *>(take(3 * sizeof(unsigned long long)));
   zero_words_kernel<<<1, kWave, 0, s>>>(reinterpret_cast<uint32_t *>(counters), 6);
   LAUNCH_TRY("zero_words_kernel");
-  const char *full_env = getenv("TAC_GPU_FULL_SEARCH");
   const uint32_t L = ksub >= 2 ? std::min<uint32_t>(kCandListEncode, ksub - 1) : 0;
-  bool cand = !(full_env && full_env[0] == '1') && ksub >= 2 && ksub <= 256 && n >= 16384;
+  bool cand = cand_wanted(D, ksub, true) && ksub >= 2 && ksub <= 256 && n >= 16384;
   uint64_t batch = 0;
   uint32_t *count = nullptr, *nbr = nullptr, *lists = nullptr;
   uint8_t *anchors = nullptr;

@@ -20,6 +20,14 @@ NEVER = float("-inf")
 pytestmark = pytest.mark.gpu
 
 
+@pytest.fixture(autouse=True)
+def _candidate_passes(monkeypatch):
+    # By default the library keeps the candidate passes for dsub <= 6 in the
+    # Lloyd loop and dsub <= 4 in encode (K <= 256); these tests exercise
+    # them at every dsub.  TAC_GPU_FULL_SEARCH=1 still wins where a test sets it.
+    monkeypatch.setenv("TAC_GPU_CANDIDATES", "1")
+
+
 def _bits(a):
     return np.ascontiguousarray(a, dtype=np.float32).reshape(-1).view(np.uint32)
 
@@ -224,3 +232,28 @@ def test_k1024_matches_full_search_on_the_corpus(gpu, monkeypatch):
     q = pq.train(x, w.dim, 0, m=w.m, ksub=w.ksub, max_iters=3, tol=NEVER, init_codebooks=init)
     assert np.array_equal(_bits(p.codebooks), _bits(q.codebooks))
     assert got.dtype == np.uint16 and np.array_equal(got, q.encode_many(x))
+
+
+@pytest.mark.parametrize("dsub,train_cand,encode_cand", [(4, True, True), (5, True, False),
+                                                          (7, False, False), (8, False, False)])
+def test_default_pass_by_sub_dimension(gpu, monkeypatch, dsub, train_cand, encode_cand):
+    # Without the switch: the candidate passes where they are faster (Lloyd up
+    # to dsub 6, encode up to dsub 4, K <= 256), the pruned full search past
+    # that; the bytes are the oracle's either way.
+    monkeypatch.delenv("TAC_GPU_CANDIDATES")
+    m, ksub, n = 2, 256, 20000
+    dim = m * dsub
+    rng = np.random.default_rng(600 + dsub)
+    x = (rng.standard_normal((n, dim)) * 0.3).astype(np.float32)
+    init = synth.shuffle_init(x, m, ksub, 3)
+    device.profile_enable(True)
+    device.profile_read(reset=True)
+    got, _ = _train_both(x, dim, m, ksub, init, 3)
+    prof_train = device.profile_read(reset=True)
+    codes = got.encode_many(x)
+    prof_enc = device.profile_read(reset=True)
+    device.profile_enable(False)
+    assert (prof_train.cand_vectors > 0) == train_cand
+    assert (prof_enc.cand_vectors > 0) == encode_cand
+    ref = orc.pq_encode(x, dim, m, ksub, got.codebooks, n_threads=16)
+    assert np.array_equal(codes, ref)
