@@ -10,7 +10,7 @@ wider than the codebook (most vectors outside the codebook's box but inside
 the grid), lattice codebooks with exact ties on the bisectors, vectors on
 and beside cell edges (the grid's origin and scale recomputed here the way
 the box kernel sets them when the codebook's box holds the sample's
-mean +- 3 sigma), duplicate codewords whose lists pass the 16-item limit,
+mean +- 3 sigma), duplicate codewords whose lists pass the 32-item (128-codeword) limit,
 lists that overflow the list space, and K below one item of 8.
 """
 import numpy as np
@@ -110,7 +110,8 @@ def test_vectors_on_cell_edges(gpu, monkeypatch, dsub):
 
 def test_duplicates_past_the_item_limit(gpu, monkeypatch):
     # 200 copies of one codeword: lists near it hold all 200 (ties), past the
-    # 16-item limit, so those cells defer; the first copy must win.
+    # 32-item (128-codeword) limit, so those cells defer; the first copy must
+    # win.
     rng = np.random.default_rng(31)
     m, ksub, dsub = 4, 256, 4
     cb = (rng.standard_normal((m, ksub, dsub)) * 0.2).astype(np.float32)
@@ -120,9 +121,9 @@ def test_duplicates_past_the_item_limit(gpu, monkeypatch):
 
 
 def test_list_space_overflow(gpu, monkeypatch):
-    # Two points, 128 copies each: every list holds one point's copies (ties)
-    # and some the other's, 16 items or close, past the space of 4 items per
-    # cell on average: later blocks defer their cells.  A second call reuses
+    # Two points, 128 copies each: every list holds one point's copies (ties,
+    # 32 items) and some the other's too (past the item limit), far past the
+    # space of 8 items per cell on average: later blocks defer their cells.  A second call reuses
     # the space from its start.
     rng = np.random.default_rng(37)
     m, ksub, dsub = 2, 256, 4
