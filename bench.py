@@ -925,6 +925,8 @@ COUNTER_PASSES = {
     "k1024": "corpus-1.52m-k1024: 20-iteration train and encode",
     "stream-chunk": "stream-200m: encode of its first 10M-vector chunk (device-generated rows, "
                     "fixed N(0, 0.05^2) codebooks)",
+    "paper-60m": "paper-60m: one 25-iteration train of the 60M-vector corpus (device-generated, "
+                 "resident; the generator's launches come first)",
 }
 
 
@@ -944,6 +946,18 @@ def counter_pass(device, errors, lib, synth, which, x, ids, dx):
         codes = device.DeviceArray((chunk, ws.m), np.uint8)
         device.encode_device(xs, chunk, ws.dim, ws.m, ws.ksub, dcb, codes)
         for a in (xs, dcb, codes):
+            a.free()
+        gen.free()
+    elif which == "paper-60m":
+        w = synth.WORKLOADS["paper-60m"]
+        gen = synth.DeviceCorpus(w)
+        xs = device.DeviceArray((w.n, w.dim), np.float32)
+        gen.fill(xs, w.n)
+        dinit = device.DeviceArray.from_host(gen.shuffle_init(xs, w.n, w.m, w.ksub, w.seed))
+        dcb = device.DeviceArray((w.m, w.ksub, w.dsub), np.float32)
+        device.train_device(xs, w.n, w.dim, w.m, w.ksub, dinit, dcb, w.iters, NEVER)
+        device.synchronize()
+        for a in (xs, dinit, dcb):
             a.free()
         gen.free()
     else:
