@@ -113,20 +113,84 @@ __host__ __device__ inline uint32_t cand_grid_side(uint32_t D) {
   }
 }
 
-// One block per (codeword a, subspace m) (one wave up to K = 256, four
-// beyond): lo(a, c) for every c != a, a bitonic sort of the next power of two
-// >= K keys in LDS, the first L written to nbr[m][a][0 .. L) and
-// cand_pad_key(a) to the rest of the stored row nbr[m][a][L .. cand_row_len(L)).
+// Exchange partner of lane ^ LX within a wave: DPP moves for 1, 2 and 8
+// (quad permutes and a row rotation by 8), a swizzle for 4 and 16, a
+// permute for 32.
+template <uint32_t LX>
+__device__ inline uint32_t lane_xor(uint32_t v) {
+  if constexpr (LX == 1) {
+    return (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, 0xB1, 0xf, 0xf, false);  // quad_perm 1,0,3,2
+  } else if constexpr (LX == 2) {
+    return (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, 0x4E, 0xf, 0xf, false);  // quad_perm 2,3,0,1
+  } else if constexpr (LX == 8) {
+    return (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, 0x128, 0xf, 0xf, false);  // row_ror:8
+  } else if constexpr (LX == 4 || LX == 16) {
+    return (uint32_t)__builtin_amdgcn_ds_swizzle((int)v, (int)(0x1Fu | (LX << 10)));  // xor mask
+  } else {
+    static_assert(LX == 32, "lane_xor: 1, 2, 4, 8, 16 or 32");
+    return (uint32_t)__shfl_xor((int)v, 32, kWave);
+  }
+}
+
+// Stage (2^KB, 2^JB) of a bitonic network over the 64 R keys of a wave, key
+// e = lane R + r in v[r]: keys e and e ^ 2^JB end in ascending order when
+// e & 2^KB is 0, in descending order otherwise.
+template <int R, int KB, int JB>
+__device__ inline void bitonic_stage(uint32_t (&v)[R], uint32_t lane) {
+  constexpr uint32_t k = 1u << KB, j = 1u << JB;
+  if constexpr (j >= (uint32_t)R) {
+    const bool lower = (lane & (j / R)) == 0;
+#pragma unroll
+    for (int r = 0; r < R; ++r) {
+      const uint32_t o = lane_xor<j / R>(v[r]);
+      const bool up = ((lane * R + r) & k) == 0;
+      v[r] = up == lower ? min(v[r], o) : max(v[r], o);
+    }
+  } else {
+#pragma unroll
+    for (int r = 0; r < R; ++r) {
+      if ((r & j) == 0) {
+        const bool up = ((lane * R + r) & k) == 0;
+        const uint32_t lo = min(v[r], v[r | j]), hi = max(v[r], v[r | j]);
+        v[r] = up ? lo : hi;
+        v[r | j] = up ? hi : lo;
+      }
+    }
+  }
+}
+template <int R, int KB, int JB>
+__device__ inline void bitonic_stages(uint32_t (&v)[R], uint32_t lane) {
+  bitonic_stage<R, KB, JB>(v, lane);
+  if constexpr (JB > 0) bitonic_stages<R, KB, JB - 1>(v, lane);
+}
+template <int R>
+constexpr int wave_log_keys() { return R == 4 ? 8 : R == 2 ? 7 : 6; }
+// Sorts the wave's 64 R keys ascending (key e = lane R + r).
+template <int R, int KB = 1>
+__device__ inline void wave_bitonic_sort(uint32_t (&v)[R], uint32_t lane) {
+  bitonic_stages<R, KB, KB - 1>(v, lane);
+  if constexpr (KB < wave_log_keys<R>()) wave_bitonic_sort<R, KB + 1>(v, lane);
+}
+// Sorts a bitonic sequence of the wave's 64 R keys ascending.
+template <int R>
+__device__ inline void wave_bitonic_merge(uint32_t (&v)[R], uint32_t lane) {
+  constexpr int LOG = wave_log_keys<R>();
+  bitonic_stages<R, LOG, LOG - 1>(v, lane);  // e & 2^LOG is 0: ascending everywhere
+}
+
+// One block per (codeword a, subspace m), one wave up to K = 256, four
+// beyond: lo(a, c) for every c != a as a key (all-ones for a and past K),
+// and the first L <= 128 keys in ascending order written to nbr[m][a][0 ..
+// L), cand_pad_key(a) to the rest of the stored row nbr[m][a][L ..
+// cand_row_len(L)).  Keys are distinct (the codeword id is part of the key),
+// so the row is the unique sorted prefix.  Each wave sorts its 256 keys in
+// registers (bitonic network, lane exchanges without LDS); with four waves
+// the four sorted runs meet in LDS, where the 128 smallest of two runs are
+// the element-wise minimum of the first 128 of one and the first 128 of the
+// other reversed (a bitonic sequence, merged in registers), twice.
 // Block (0, m) also clears the subspace's deferred count for the assignment
 // that follows on the same stream.
-// Keys a neighbour-table block sorts: the next power of two >= K, at least
-// 64.  They take P * 4 bytes of dynamic LDS (1 KB at K = 256), so the blocks
-// still fit on a CU beside the candidate kernel of the other stream.
-__host__ __device__ inline uint32_t nbr_keys(uint32_t K) {
-  uint32_t P = kWave;
-  while (P < K) P <<= 1;
-  return P;
-}
+__host__ __device__ inline uint32_t nbr_lds_bytes(uint32_t K) { return K > 256 ? 4096u : 0u; }
 
 template <int D>
 __global__ __launch_bounds__(256) void nbr_build_kernel(const float* __restrict__ cb,
@@ -134,17 +198,20 @@ __global__ __launch_bounds__(256) void nbr_build_kernel(const float* __restrict_
                                                         uint32_t* __restrict__ defer_count,
                                                         const uint32_t* __restrict__ done,
                                                         uint32_t K, uint32_t L) {
-  extern __shared__ uint32_t keys[];  // [nbr_keys(K)]
+  extern __shared__ uint32_t runs[];  // [4][256], four waves only
   const uint32_t a = blockIdx.x, m = blockIdx.y, t = threadIdx.x;
+  const uint32_t lane = t % kWave, w = t / kWave;
   if (a == 0 && t == 0) defer_count[m] = 0;
   if (done && done[m]) return;
   constexpr float g = cand_gamma(D);
-  const uint32_t P = nbr_keys(K);
   const float* cbm = cb + (uint64_t)m * K * D;
   float ca[D];
 #pragma unroll
   for (int k = 0; k < D; ++k) ca[k] = cbm[(uint64_t)a * D + k];
-  for (uint32_t c = t; c < P; c += blockDim.x) {
+  uint32_t v[4];
+#pragma unroll
+  for (int r = 0; r < 4; ++r) {
+    const uint32_t c = w * 256u + (uint32_t)r * kWave + lane;
     uint32_t key = kCandNoKey;
     if (c < K && c != a) {
       float cv[D];
@@ -152,27 +219,49 @@ __global__ __launch_bounds__(256) void nbr_build_kernel(const float* __restrict_
       for (int k = 0; k < D; ++k) cv[k] = cbm[(uint64_t)c * D + k];
       key = cand_key(cand_lower_bound(exact_l2sq<D>(ca, cv), g), c);
     }
-    keys[c] = key;
+    v[r] = key;
+  }
+  wave_bitonic_sort<4>(v, lane);
+  const uint32_t Lr = cand_row_len(L);  // <= 128
+  uint32_t* row = nbr + ((uint64_t)m * K + a) * Lr;
+  if (blockDim.x == kWave) {
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+      const uint32_t e = lane * 4u + (uint32_t)r;
+      if (e < Lr) row[e] = e < L ? v[r] : cand_pad_key(a);
+    }
+    return;
+  }
+#pragma unroll
+  for (int r = 0; r < 4; ++r) runs[w * 256u + lane * 4u + (uint32_t)r] = v[r];
+  __syncthreads();
+  uint32_t h[2];
+  if (w < 2) {  // runs 2w and 2w + 1 -> their 128 smallest, into run 2w's first half
+    const uint32_t* A = runs + 2u * w * 256u;
+    const uint32_t* B = A + 256u;
+#pragma unroll
+    for (int r = 0; r < 2; ++r) {
+      const uint32_t e = lane * 2u + (uint32_t)r;
+      h[r] = min(A[e], B[127u - e]);
+    }
+    wave_bitonic_merge<2>(h, lane);
+#pragma unroll
+    for (int r = 0; r < 2; ++r) runs[2u * w * 256u + lane * 2u + (uint32_t)r] = h[r];
   }
   __syncthreads();
-  for (uint32_t k = 2; k <= P; k <<= 1) {
-    for (uint32_t j = k >> 1; j > 0; j >>= 1) {
-      for (uint32_t q = t; q < P / 2; q += blockDim.x) {
-        const uint32_t i = ((q & ~(j - 1)) << 1) | (q & (j - 1));
-        const uint32_t p = i | j;
-        const uint32_t x = keys[i], y = keys[p];
-        const bool up = (i & k) == 0;
-        if ((x > y) == up) {
-          keys[i] = y;
-          keys[p] = x;
-        }
-      }
-      __syncthreads();
+  if (w == 0) {
+#pragma unroll
+    for (int r = 0; r < 2; ++r) {
+      const uint32_t e = lane * 2u + (uint32_t)r;
+      h[r] = min(runs[e], runs[512u + 127u - e]);
+    }
+    wave_bitonic_merge<2>(h, lane);
+#pragma unroll
+    for (int r = 0; r < 2; ++r) {
+      const uint32_t e = lane * 2u + (uint32_t)r;
+      if (e < Lr) row[e] = e < L ? h[r] : cand_pad_key(a);
     }
   }
-  const uint32_t Lr = cand_row_len(L);
-  uint32_t* row = nbr + ((uint64_t)m * K + a) * Lr;
-  for (uint32_t j = t; j < Lr; j += blockDim.x) row[j] = j < L ? keys[j] : cand_pad_key(a);
 }
 
 // Grid anchors of subspace m = blockIdx.y: the bounding box of the

@@ -14,8 +14,8 @@
 // for every vector inside the grid, all entries of its cell's list with the
 // reference distance and keeps the lexicographic (distance bits, index)
 // minimum, which is the reference's code.  Lists are padded with the fine
-// anchor to whole items of 8 entries and laid out over the wave's lanes as
-// the candidate encode lays out its items (cand_kernels.hpp).  Vectors
+// anchor to whole items of kCellItem (4) entries, and a wave's vectors have
+// their items laid out over its lanes by a scan of their counts.  Vectors
 // outside the grid (and NaN) and cells whose list passes kCellMaxItems items
 // take the pruned full search through the deferred list.  A subspace takes
 // this pass when many of its rows lie outside the codebook's box and its

@@ -506,7 +506,7 @@ struct Launch {
                          uint64_t n, uint32_t M, uint32_t K, uint32_t L, uint32_t *hist,
                          uint32_t T, unsigned long long *rescans, hipStream_t s) {
     KT("nbr_build_kernel<%d>", D);
-    nbr_build_kernel<D><<<dim3(K, M), nbr_threads(K), nbr_keys(K) * sizeof(uint32_t), s>>>(
+    nbr_build_kernel<D><<<dim3(K, M), nbr_threads(K), nbr_lds_bytes(K), s>>>(
         cb, nbr, defer_count, done, K, L);
     KT_END();
     uint32_t G = 0, cells = 0;
@@ -577,7 +577,7 @@ struct Launch {
     uint32_t cells = 1;
     for (int k = 0; k < D; ++k) cells *= G;
     KT("nbr_build_kernel<%d>", D);
-    nbr_build_kernel<D><<<dim3(K, M), nbr_threads(K), nbr_keys(K) * sizeof(uint32_t), s>>>(
+    nbr_build_kernel<D><<<dim3(K, M), nbr_threads(K), nbr_lds_bytes(K), s>>>(
         cb, nbr, defer_count, skip, K, L);
     KT_END();
     KT("grid_build_kernel<%d, %uu, %s>", D, cand_anchors<true>(), code_name<AnchorT>());

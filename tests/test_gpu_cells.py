@@ -10,8 +10,9 @@ wider than the codebook (most vectors outside the codebook's box but inside
 the grid), lattice codebooks with exact ties on the bisectors, vectors on
 and beside cell edges (the grid's origin and scale recomputed here the way
 the box kernel sets them when the codebook's box holds the sample's
-mean +- 3 sigma), duplicate codewords whose lists pass the 32-item (128-codeword) limit,
-lists that overflow the list space, and K below one item of 8.
+mean +- 3 sigma), duplicate codewords whose lists pass the 32-item
+(128-codeword) limit, lists that overflow the list space, and K below one
+item of 4 codewords.
 """
 import numpy as np
 import pytest
