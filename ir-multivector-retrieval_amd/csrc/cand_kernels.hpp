@@ -641,21 +641,190 @@ __global__ __launch_bounds__(kCandThreads, D <= 4 ? 8 : 4) void cand_kernel(
     defer[(uint64_t)m * n + at + q] = slice[(uint64_t)m * n + lo_i + q];
 }
 
+// pruned_argmin (pq_kernels.hpp) for one vector x held by the S consecutive
+// lanes of a group (sub = lane % S; every lane of the group passes the same
+// x), with Kp / kPruneBlock a multiple of S.  Lane sub takes blocks [sub nb /
+// S, (sub + 1) nb / S) of the first pass, walking each block from entry sub
+// (mod kPruneBlock) so that the group's lanes read distinct LDS banks; a
+// block's minimum does not depend on that order (fminf over the entries).
+// The group's block minima then meet in a top-2 merge: the smaller best1
+// wins, best2 is the smaller of the loser's best1 and the winner's best2,
+// and equal best1 values make best2 equal best1 (no gap, so a rescan), as
+// one lane's top-2 over all blocks makes them.  The winning block's entries
+// and a rescan's codewords are spread over the lanes and their (distance,
+// index) minima merged lexicographically, which keeps the first index of
+// the reference scan's minimum; with SEED_FIRST a NaN distance to codeword
+// 0 is the result (vec.argmin keeps dists[0] when nothing compares below
+// it).  Every lane returns the result; rescans counts on lane sub 0.
+template <int S>
+__device__ inline float group_xor_f(float v, uint32_t o) {
+  if constexpr (S >= 2) {
+    if (o == 1) return __uint_as_float(lane_xor<1>(__float_as_uint(v)));
+  }
+  if constexpr (S >= 4) {
+    if (o == 2) return __uint_as_float(lane_xor<2>(__float_as_uint(v)));
+  }
+  return v;
+}
+template <int S>
+__device__ inline uint32_t group_xor_u(uint32_t v, uint32_t o) {
+  if constexpr (S >= 2) {
+    if (o == 1) return lane_xor<1>(v);
+  }
+  if constexpr (S >= 4) {
+    if (o == 2) return lane_xor<2>(v);
+  }
+  return v;
+}
+// (d, c) <- the lexicographic minimum of the group's (distance, index) pairs
+// (distances non-negative or +inf; NaN never wins).
+template <int S>
+__device__ inline void group_lex_min(float& d, uint32_t& c) {
+#pragma unroll
+  for (uint32_t o = 1; o < (uint32_t)S; o <<= 1) {
+    const float od = group_xor_f<S>(d, o);
+    const uint32_t oc = group_xor_u<S>(c, o);
+    if (od < d || (od == d && oc < c)) {
+      d = od;
+      c = oc;
+    }
+  }
+}
+
+template <int D, int S, bool SEED_FIRST>
+__device__ __forceinline__ void pruned_argmin_lanes(const float (&x)[D], const float* lcb,
+                                                    const float* lnc, uint32_t K, uint32_t Kp,
+                                                    uint32_t maxbits, uint32_t sub,
+                                                    uint32_t& bidx, float& bdist,
+                                                    uint32_t& rescans) {
+  static_assert(S == 2 || S == 4, "lanes per vector: 2 or 4");
+  constexpr int DP = Pad<D>::value;
+  constexpr int B = kPruneBlock;
+  bool rescan = maxbits >= 0x7f800000u;  // a non-finite codeword: reference scan
+  if (!rescan) {
+    float xp[D];
+#pragma unroll
+    for (int k = 0; k < D; ++k) xp[k] = -2.0f * x[k];
+    const uint32_t per = Kp / B / S, b0 = sub * per;
+    float best1 = __builtin_inff(), best2 = __builtin_inff();
+    uint32_t bblk = b0;
+    for (uint32_t b = b0; b < b0 + per; ++b) {
+      float mb = __builtin_inff();
+#pragma unroll
+      for (int t = 0; t < B; ++t) {
+        const uint32_t c = b * B + (((uint32_t)t + sub) & (B - 1));
+        float cv[D];
+        load_padded<D>(lcb + c * DP, cv);
+        float acc = lnc[c];
+#pragma unroll
+        for (int k = 0; k < D; ++k) acc = __builtin_fmaf(xp[k], cv[k], acc);
+        mb = fminf(mb, acc);
+      }
+      const bool lt1 = mb < best1;
+      const bool lt2 = mb < best2;
+      best2 = lt1 ? best1 : (lt2 ? mb : best2);
+      best1 = lt1 ? mb : best1;
+      bblk = lt1 ? b : bblk;
+    }
+#pragma unroll
+    for (uint32_t o = 1; o < (uint32_t)S; o <<= 1) {
+      const float o1 = group_xor_f<S>(best1, o), o2 = group_xor_f<S>(best2, o);
+      const uint32_t ob = group_xor_u<S>(bblk, o);
+      if (o1 < best1) {
+        best2 = best1 < o2 ? best1 : o2;
+        best1 = o1;
+        bblk = ob;
+      } else if (best1 < o1) {
+        best2 = best2 < o1 ? best2 : o1;
+      } else {
+        best2 = best1;
+        bblk = ob < bblk ? ob : bblk;
+      }
+    }
+    constexpr float u = 5.9604644775390625e-8f;  // 2^-24
+    constexpr float gD = (float)D * u / (1.0f - (float)D * u);
+    constexpr float gR = (float)(D + 2) * u / (1.0f - (float)(D + 2) * u);
+    const float cmax2 = __uint_as_float(maxbits);
+    const float cmax = sqrtf(cmax2);
+    float x2 = 0.0f;
+#pragma unroll
+    for (int k = 0; k < D; ++k) x2 = x2 + x[k] * x[k];
+    const float nx = sqrtf(x2);
+    const float ea = 2.0f * gD * (1.0f + gD) * (cmax2 + 2.0f * nx * cmax);
+    float thr = 2.0f * ea * (1.0f + gR) + gR * (fabsf(best2 + x2) + fabsf(best1 + x2));
+    thr = 2.0f * thr + 1e-30f;
+    const bool tame = (cmax2 + 2.0f * nx * cmax) < 1e38f;
+    if (tame && (best2 - best1) > thr) {  // false on NaN
+      float best = __builtin_inff();
+      uint32_t idx = bblk * B;
+#pragma unroll
+      for (int t = 0; t < B / S; ++t) {
+        const uint32_t c = bblk * B + (uint32_t)t * S + sub;
+        if (c < K) {
+          float cv[D];
+          load_padded<D>(lcb + c * DP, cv);
+          const float d = exact_l2sq<D>(x, cv);
+          if (d < best) {
+            best = d;
+            idx = c;
+          }
+        }
+      }
+      group_lex_min<S>(best, idx);
+      bidx = idx;
+      bdist = best;
+      return;
+    }
+    rescan = true;
+  }
+  // Reference scan: lane sub takes codewords sub, sub + S, ...
+  if (sub == 0) ++rescans;
+  float d0 = 0.0f;
+  if (SEED_FIRST) {
+    float c0[D];
+    load_padded<D>(lcb, c0);
+    d0 = exact_l2sq<D>(x, c0);
+  }
+  float best = __builtin_inff();
+  uint32_t idx = 0xFFFFFFFFu;
+  for (uint32_t c = sub; c < K; c += S) {
+    float cv[D];
+    load_padded<D>(lcb + c * DP, cv);
+    const float d = exact_l2sq<D>(x, cv);
+    if (d < best) {
+      best = d;
+      idx = c;
+    }
+  }
+  group_lex_min<S>(best, idx);
+  if (idx == 0xFFFFFFFFu) idx = 0;  // nothing below +inf: index 0, +inf
+  if (SEED_FIRST && d0 != d0) {     // NaN at codeword 0 stays the minimum
+    idx = 0;
+    best = d0;
+  }
+  bidx = idx;
+  bdist = best;
+}
+
 // The deferred vectors: the pruned exact search over all K codewords
 // (pq_kernels.hpp), vectors gathered through the dense list defer[m][..];
 // a persistent grid of gridDim.x blocks per subspace walks tiles of
-// kBlock*VPT entries; each new code is added to its sort tile's count in
-// hist[m][tile][code].  With stats (profiling): stats[0] += deferred
-// vectors, stats[1] += n per subspace.
-template <int D, int VPT>
+// kBlock * VPT / S entries; each new code is added to its sort tile's count
+// in hist[m][tile][code].  S > 1 (with VPT 1): S lanes share a vector's
+// search (pruned_argmin_lanes), for K with Kp / kPruneBlock a multiple of
+// S: a search is a serial chain over its codewords, and few deferred
+// vectors leave few waves per SIMD to hide it.  With stats (profiling):
+// stats[0] += deferred vectors, stats[1] += n per subspace.
+template <int D, int VPT, int S = 1>
 __global__ __launch_bounds__(kBlock) void assign_list_kernel(
     const float* __restrict__ xs, const float* __restrict__ cb, uint16_t* __restrict__ codes,
     float* __restrict__ e, const uint32_t* __restrict__ defer,
     const uint32_t* __restrict__ defer_count, const uint32_t* __restrict__ done, uint64_t n,
     uint32_t K, unsigned long long* __restrict__ rescans, unsigned long long* __restrict__ stats,
     uint32_t* __restrict__ hist, uint32_t T) {
+  static_assert(S == 1 || VPT == 1, "lane groups take one vector each");
   constexpr int DP = Pad<D>::value;
-  constexpr uint32_t kTile = kBlock * VPT;
+  constexpr uint32_t kTile = kBlock * VPT / S;
   extern __shared__ __attribute__((aligned(16))) float lds[];
   const uint32_t m = blockIdx.y;
   if (done[m]) return;
@@ -680,6 +849,30 @@ __global__ __launch_bounds__(kBlock) void assign_list_kernel(
   const float* xm = xs + (uint64_t)m * n * DP;
   const uint32_t* lst = defer + (uint64_t)m * n;
   uint32_t mine = 0;
+  if constexpr (S > 1) {
+    const uint32_t sub = threadIdx.x % S;
+    for (uint64_t t0 = (uint64_t)blockIdx.x * kTile; t0 < cnt; t0 += (uint64_t)gridDim.x * kTile) {
+      const uint64_t q = t0 + threadIdx.x / S;
+      const uint32_t idx = q < cnt ? lst[q] : 0xFFFFFFFFu;
+      float x[D];
+      if (idx != 0xFFFFFFFFu) {
+        load_padded<D>(xm + (uint64_t)idx * DP, x);
+      } else {
+#pragma unroll
+        for (int k = 0; k < D; ++k) x[k] = 0.0f;
+      }
+      uint32_t bidx;
+      float best;
+      pruned_argmin_lanes<D, S, true>(x, lcb, lnc, K, Kp, lmax, sub, bidx, best, mine);
+      if (sub == 0 && idx != 0xFFFFFFFFu) {
+        codes[(uint64_t)m * n + idx] = (uint16_t)bidx;
+        e[(uint64_t)m * n + idx] = best;
+        atomicAdd(&hist[((uint64_t)m * T + idx / kSortTile) * K + bidx], 1u);
+      }
+    }
+    flush_rescans(mine, &lcount, rescans);
+    return;
+  }
   for (uint64_t t0 = (uint64_t)blockIdx.x * kTile; t0 < cnt; t0 += (uint64_t)gridDim.x * kTile) {
     float x[VPT][D];
     uint32_t idx[VPT];
@@ -717,15 +910,17 @@ __global__ __launch_bounds__(kBlock) void assign_list_kernel(
 // tiles of kBlock * VPT entries.  Two widths are launched back to back and a
 // subspace's deferred count picks one: VPT 1 (many short waves) below a
 // quarter of the rows, VPT 8 (the full search's interleave) above; the other
-// launch returns at once.
-template <int D, int VPT, typename CodeT>
+// launch returns at once.  S > 1 (with VPT 1): S lanes share a vector's
+// search, as in assign_list_kernel.
+template <int D, int VPT, typename CodeT, int S = 1>
 __global__ __launch_bounds__(kBlock) void encode_list_kernel(
     const float* __restrict__ x, const float* __restrict__ cb, CodeT* __restrict__ out,
     const uint32_t* __restrict__ defer, const uint32_t* __restrict__ defer_count, uint64_t n,
     uint32_t dim, uint32_t M, uint32_t K, unsigned long long* __restrict__ rescans,
     unsigned long long* __restrict__ stats) {
+  static_assert(S == 1 || VPT == 1, "lane groups take one vector each");
   constexpr int DP = Pad<D>::value;
-  constexpr uint32_t kTile = kBlock * VPT;
+  constexpr uint32_t kTile = kBlock * VPT / S;
   extern __shared__ __attribute__((aligned(16))) float lds[];
   const uint32_t m = blockIdx.y;
   const uint32_t cnt = defer_count[m];
@@ -750,6 +945,23 @@ __global__ __launch_bounds__(kBlock) void encode_list_kernel(
   __syncthreads();
   const uint32_t* lst = defer + (uint64_t)m * n;
   uint32_t mine = 0;
+  if constexpr (S > 1) {
+    const uint32_t sub = threadIdx.x % S;
+    for (uint64_t t0 = (uint64_t)blockIdx.x * kTile; t0 < cnt; t0 += (uint64_t)gridDim.x * kTile) {
+      const uint64_t q = t0 + threadIdx.x / S;
+      const uint32_t idx = q < cnt ? lst[q] : 0xFFFFFFFFu;
+      const float* src = x + (uint64_t)(idx != 0xFFFFFFFFu ? idx : 0u) * dim + (uint64_t)m * D;
+      float xv[D];
+#pragma unroll
+      for (int k = 0; k < D; ++k) xv[k] = src[k];
+      uint32_t bidx;
+      float best;
+      pruned_argmin_lanes<D, S, false>(xv, lcb, lnc, K, Kp, lmax, sub, bidx, best, mine);
+      if (sub == 0 && idx != 0xFFFFFFFFu) out[(uint64_t)idx * M + m] = (CodeT)bidx;
+    }
+    flush_rescans(mine, &lcount, rescans);
+    return;
+  }
   for (uint64_t t0 = (uint64_t)blockIdx.x * kTile; t0 < cnt; t0 += (uint64_t)gridDim.x * kTile) {
     float xv[VPT][D];
     uint32_t idx[VPT];

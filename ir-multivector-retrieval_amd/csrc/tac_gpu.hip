@@ -468,6 +468,16 @@ inline uint32_t cand_hist_tiles(uint32_t K, uint32_t DP, uint32_t cells, uint32_
   return tiles;
 }
 inline uint32_t nbr_threads(uint32_t K) { return K > 256 ? 256u : (uint32_t)kWave; }
+// The deferred-vector kernels give each vector four lanes from K = 128 on,
+// where the blocks of kPruneBlock codewords split evenly over four lanes
+// (TAC_GPU_LIST_LANES=1 keeps one lane per vector, for the tests that
+// compare the two).
+inline bool list_lanes4(uint32_t K) {
+  const char *v = getenv("TAC_GPU_LIST_LANES");
+  const bool one = v != nullptr && v[0] == '1';
+  const uint32_t Kp = (K + kPruneBlock - 1) / kPruneBlock * kPruneBlock;
+  return !one && K >= 128 && (Kp / kPruneBlock) % 4 == 0;
+}
 
 template <int D>
 struct Launch {
@@ -543,16 +553,26 @@ struct Launch {
     KT_END();
     const uint32_t Kp = (K + kPruneBlock - 1) / kPruneBlock * kPruneBlock;
     const size_t lds = (size_t)Kp * (Pad<D>::value + 1) * sizeof(float) + 2 * sizeof(uint32_t);
-    // About 2% of the vectors are deferred.  One vector per thread and about
-    // 4,096 blocks over all subspaces keep many short waves per SIMD (a full
-    // search is a long serial chain per lane); blocks loop when there are
-    // more.
-    const uint64_t g = std::max<uint64_t>(
-        1, std::min<uint64_t>((n + kBlock - 1) / kBlock, (4096 + M - 1) / M));
-    KT("assign_list_kernel<%d, 1>", D);
-    assign_list_kernel<D, 1><<<dim3((unsigned)g, M), kBlock, lds, s>>>(
-        xs, cb, codes, e, defer, defer_count, done, n, K, rescans,
-        g_profile ? rescans + 1 : nullptr, hist, T);
+    // About 2% of the vectors are deferred, each a serial chain over all K
+    // codewords: four lanes share a vector's search when the blocks of
+    // kPruneBlock codewords split evenly over them (list_lanes4), so that
+    // four times as many waves hide the chains, else one vector per thread;
+    // about 4,096 blocks over all subspaces, looping when there are more.
+    const bool lanes4 = list_lanes4(K);
+    const uint64_t per = lanes4 ? kBlock / 4 : kBlock;
+    const uint64_t g =
+        std::max<uint64_t>(1, std::min<uint64_t>((n + per - 1) / per, (4096 + M - 1) / M));
+    if (lanes4) {
+      KT("assign_list_kernel<%d, 1, 4>", D);
+      assign_list_kernel<D, 1, 4><<<dim3((unsigned)g, M), kBlock, lds, s>>>(
+          xs, cb, codes, e, defer, defer_count, done, n, K, rescans,
+          g_profile ? rescans + 1 : nullptr, hist, T);
+    } else {
+      KT("assign_list_kernel<%d, 1>", D);
+      assign_list_kernel<D, 1><<<dim3((unsigned)g, M), kBlock, lds, s>>>(
+          xs, cb, codes, e, defer, defer_count, done, n, K, rescans,
+          g_profile ? rescans + 1 : nullptr, hist, T);
+    }
     KT_END();
     return TAC_OK;
   }
@@ -629,13 +649,21 @@ struct Launch {
                              unsigned long long *stats, hipStream_t s) {
     const uint32_t Kp = (K + kPruneBlock - 1) / kPruneBlock * kPruneBlock;
     const size_t lds = (size_t)Kp * (Pad<D>::value + 1) * sizeof(float) + 2 * sizeof(uint32_t);
+    const bool lanes4 = list_lanes4(K);
+    const uint64_t per1 = lanes4 ? kBlock / 4 : kBlock;
     const uint64_t g1 = std::max<uint64_t>(
-        1, std::min<uint64_t>((n + kBlock - 1) / kBlock, (4096 + M - 1) / M));
+        1, std::min<uint64_t>((n + per1 - 1) / per1, (4096 + M - 1) / M));
     const uint64_t g8 = std::max<uint64_t>(
         1, std::min<uint64_t>((n + kBlock * 8 - 1) / (kBlock * 8), (4096 + M - 1) / M));
-    KT("encode_list_kernel<%d, 1, %s>", D, code_name<CodeT>());
-    encode_list_kernel<D, 1, CodeT><<<dim3((unsigned)g1, M), kBlock, lds, s>>>(
-        x, cb, codes, defer, defer_count, n, dim, M, K, rescans, stats);
+    if (lanes4) {
+      KT("encode_list_kernel<%d, 1, %s, 4>", D, code_name<CodeT>());
+      encode_list_kernel<D, 1, CodeT, 4><<<dim3((unsigned)g1, M), kBlock, lds, s>>>(
+          x, cb, codes, defer, defer_count, n, dim, M, K, rescans, stats);
+    } else {
+      KT("encode_list_kernel<%d, 1, %s>", D, code_name<CodeT>());
+      encode_list_kernel<D, 1, CodeT><<<dim3((unsigned)g1, M), kBlock, lds, s>>>(
+          x, cb, codes, defer, defer_count, n, dim, M, K, rescans, stats);
+    }
     KT_END();
     KT("encode_list_kernel<%d, 8, %s>", D, code_name<CodeT>());
     encode_list_kernel<D, 8, CodeT><<<dim3((unsigned)g8, M), kBlock, lds, s>>>(

@@ -257,3 +257,30 @@ def test_default_pass_by_sub_dimension(gpu, monkeypatch, dsub, train_cand, encod
     assert (prof_enc.cand_vectors > 0) == encode_cand
     ref = orc.pq_encode(x, dim, m, ksub, got.codebooks, n_threads=16)
     assert np.array_equal(codes, ref)
+
+
+@pytest.mark.parametrize("ksub", [256, 1024])
+def test_deferred_search_lane_groups_match_one_lane(gpu, monkeypatch, ksub):
+    """The deferred vectors' pruned full search with four lanes per vector
+    (K >= 128) gives the one-lane search's codebooks and codes, on corpus rows
+    whose candidate passes defer a few percent of the vector-subspaces."""
+    w = synth.WORKLOADS["corpus-1.52m-k1024" if ksub == 1024 else "corpus-1.52m"]
+    x = synth.residuals(w, 60000)
+    init = synth.shuffle_init(x, w.m, w.ksub, 0)
+
+    def run():
+        device.profile_enable(True)
+        device.profile_read(reset=True)
+        p = pq.train(x, w.dim, 0, m=w.m, ksub=w.ksub, max_iters=3, tol=NEVER,
+                     init_codebooks=init)
+        codes = p.encode_many(x)
+        prof = device.profile_read(reset=True)
+        device.profile_enable(False)
+        return p, codes, prof
+
+    p4, c4, prof = run()
+    assert prof.cand_deferred > 0
+    monkeypatch.setenv("TAC_GPU_LIST_LANES", "1")
+    p1, c1, _ = run()
+    assert np.array_equal(_bits(p4.codebooks), _bits(p1.codebooks))
+    assert np.array_equal(c4, c1)
