@@ -922,6 +922,7 @@ COUNTER_PASSES = {
     "corpus": "corpus-1.52m: the benchmarked train (20 Lloyd iterations from seeded-shuffle "
               "codebooks) and encode, one residual-stage call",
     "m8d8": "corpus-1.52m-m8d8: 20-iteration train and encode",
+    "m32d2": "corpus-1.52m-m32d2: 20-iteration train and encode",
     "k1024": "corpus-1.52m-k1024: 20-iteration train and encode",
     "stream-chunk": "stream-200m: encode of its first 10M-vector chunk (device-generated rows, "
                     "fixed N(0, 0.05^2) codebooks)",
@@ -961,7 +962,7 @@ def counter_pass(device, errors, lib, synth, which, x, ids, dx):
             a.free()
         gen.free()
     else:
-        name = {"corpus": WORKLOAD, "m8d8": "corpus-1.52m-m8d8",
+        name = {"corpus": WORKLOAD, "m8d8": "corpus-1.52m-m8d8", "m32d2": "corpus-1.52m-m32d2",
                 "k1024": "corpus-1.52m-k1024"}[which]
         w = synth.WORKLOADS[name]
         init = synth.shuffle_init(x, w.m, w.ksub, w.seed)

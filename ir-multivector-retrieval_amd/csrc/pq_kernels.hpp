@@ -503,6 +503,11 @@ __device__ inline void fold_order_block(const uint32_t (&tot)[4], uint32_t per_c
     if (c0 + q < K) order[atomicAdd(&bins[bin_of(tot[q])], 1u)] = c0 + q;
 }
 
+// Each thread of the scan kernels takes per_c = ceil(K / kBlock) <= PER
+// consecutive codes c0 .. c0 + per_c - 1 (PER = 1, 2 or 4 by K), and the
+// loads of all its codes go out together (per code one after another would
+// pay every round trip per_c times at K = 1,024).
+template <uint32_t PER>
 __global__ __launch_bounds__(kBlock) void scan_partial_kernel(
     const uint32_t* __restrict__ hist, uint32_t* __restrict__ part,
     const uint32_t* __restrict__ done, uint32_t K, uint32_t T, uint32_t G) {
@@ -512,22 +517,34 @@ __global__ __launch_bounds__(kBlock) void scan_partial_kernel(
   const uint32_t t0 = g * per < T ? g * per : T;
   const uint32_t t1 = t0 + per < T ? t0 + per : T;
   const uint32_t* hm = hist + (uint64_t)m * T * K;
+  const uint32_t per_c = (K + kBlock - 1) / kBlock;
+  const uint32_t c0 = threadIdx.x * per_c;
+  const uint32_t nq = c0 < K ? (K - c0 < per_c ? K - c0 : per_c) : 0u;
+  if (nq == 0) return;
   constexpr uint32_t B = 8;
-  for (uint32_t c = threadIdx.x; c < K; c += kBlock) {
-    uint32_t s = 0;
-    uint32_t t = t0;
-    for (; t + B <= t1; t += B) {
-      uint32_t v[B];
+  uint32_t s[PER] = {};
+  uint32_t t = t0;
+  for (; t + B <= t1; t += B) {
+    uint32_t v[B][PER];
 #pragma unroll
-      for (uint32_t q = 0; q < B; ++q) v[q] = hm[(uint64_t)(t + q) * K + c];
+    for (uint32_t j = 0; j < B; ++j)
 #pragma unroll
-      for (uint32_t q = 0; q < B; ++q) s += v[q];
-    }
-    for (; t < t1; ++t) s += hm[(uint64_t)t * K + c];
-    part[((uint64_t)m * G + g) * K + c] = s;
+      for (uint32_t q = 0; q < PER; ++q) v[j][q] = q < nq ? hm[(uint64_t)(t + j) * K + c0 + q] : 0u;
+#pragma unroll
+    for (uint32_t j = 0; j < B; ++j)
+#pragma unroll
+      for (uint32_t q = 0; q < PER; ++q) s[q] += v[j][q];
   }
+  for (; t < t1; ++t)
+#pragma unroll
+    for (uint32_t q = 0; q < PER; ++q)
+      if (q < nq) s[q] += hm[(uint64_t)t * K + c0 + q];
+#pragma unroll
+  for (uint32_t q = 0; q < PER; ++q)
+    if (q < nq) part[((uint64_t)m * G + g) * K + c0 + q] = s[q];
 }
 
+template <uint32_t PER>
 __global__ __launch_bounds__(kBlock) void scan_apply_kernel(
     uint32_t* __restrict__ hist, const uint32_t* __restrict__ part,
     uint32_t* __restrict__ counts, uint32_t* __restrict__ start, uint32_t* __restrict__ order,
@@ -542,53 +559,59 @@ __global__ __launch_bounds__(kBlock) void scan_apply_kernel(
   const uint32_t* pm = part + (uint64_t)m * G * K;
   const uint32_t per_c = (K + kBlock - 1) / kBlock;  // <= 4 codes per thread
   const uint32_t c0 = threadIdx.x * per_c;
-  uint32_t tot[4] = {0, 0, 0, 0}, before[4] = {0, 0, 0, 0};
-  uint32_t local = 0;
-  for (uint32_t q = 0; q < per_c; ++q) {
-    const uint32_t c = c0 + q;
-    if (c >= K) break;
-    for (uint32_t gg = 0; gg < G; ++gg) {
-      const uint32_t v = pm[(uint64_t)gg * K + c];
-      if (gg < g) before[q] += v;
+  const uint32_t nq = c0 < K ? (K - c0 < per_c ? K - c0 : per_c) : 0u;
+  uint32_t tot[4] = {0, 0, 0, 0}, before[PER] = {};
+  for (uint32_t gg = 0; gg < G; ++gg)
+#pragma unroll
+    for (uint32_t q = 0; q < PER; ++q) {
+      const uint32_t v = q < nq ? pm[(uint64_t)gg * K + c0 + q] : 0u;
+      before[q] += gg < g ? v : 0u;
       tot[q] += v;
     }
-    local += tot[q];
-  }
+  uint32_t local = 0;
+#pragma unroll
+  for (uint32_t q = 0; q < PER; ++q) local += tot[q];
   uint32_t st = block_exclusive_scan(local, wsum);
   if (g == 0) fold_order_block(tot, per_c, c0, K, order + (uint64_t)m * K, unit);
-  for (uint32_t q = 0; q < per_c; ++q) {
-    const uint32_t c = c0 + q;
-    if (c >= K) break;
-    if (g == 0) {
-      start[(uint64_t)m * K + c] = st;
-      counts[(uint64_t)m * K + c] = tot[q];
+  uint32_t run[PER];
+#pragma unroll
+  for (uint32_t q = 0; q < PER; ++q) {
+    if (q < nq && g == 0) {
+      start[(uint64_t)m * K + c0 + q] = st;
+      counts[(uint64_t)m * K + c0 + q] = tot[q];
     }
     st += tot[q];
-    // Eight tiles' counts are loaded before any is rewritten, so the loads
-    // overlap instead of waiting behind the stores one tile at a time.
-    constexpr uint32_t B = 8;
-    uint32_t run = before[q];
-    uint32_t t = t0;
-    for (; t + B <= t1; t += B) {
-      uint32_t v[B];
-#pragma unroll
-      for (uint32_t j = 0; j < B; ++j) v[j] = hm[(uint64_t)(t + j) * K + c];
-#pragma unroll
-      for (uint32_t j = 0; j < B; ++j) {
-        hm[(uint64_t)(t + j) * K + c] = run;
-        run += v[j];
-      }
-    }
-    for (; t < t1; ++t) {
-      const uint32_t v = hm[(uint64_t)t * K + c];
-      hm[(uint64_t)t * K + c] = run;
-      run += v;
-    }
+    run[q] = before[q];
   }
+  // Eight tiles' counts of every code of the thread are loaded before any is
+  // rewritten, so the loads overlap instead of waiting behind the stores.
+  constexpr uint32_t B = 8;
+  uint32_t t = t0;
+  for (; t + B <= t1; t += B) {
+    uint32_t v[B][PER];
+#pragma unroll
+    for (uint32_t j = 0; j < B; ++j)
+#pragma unroll
+      for (uint32_t q = 0; q < PER; ++q) v[j][q] = q < nq ? hm[(uint64_t)(t + j) * K + c0 + q] : 0u;
+#pragma unroll
+    for (uint32_t j = 0; j < B; ++j)
+#pragma unroll
+      for (uint32_t q = 0; q < PER; ++q)
+        if (q < nq) {
+          hm[(uint64_t)(t + j) * K + c0 + q] = run[q];
+          run[q] += v[j][q];
+        }
+  }
+  for (; t < t1; ++t)
+#pragma unroll
+    for (uint32_t q = 0; q < PER; ++q)
+      if (q < nq) {
+        const uint32_t v = hm[(uint64_t)t * K + c0 + q];
+        hm[(uint64_t)t * K + c0 + q] = run[q];
+        run[q] += v;
+      }
 }
 
-
-// Block-wide exclusive scan of one value per thread (blockDim.x <= 1024).
 
 // Workgroups are dispatched round-robin over the 8 XCDs; hand each XCD a
 // contiguous range of logical tiles so neighbouring tiles (which write

@@ -1153,15 +1153,28 @@ int train_core(DeviceState &ds, hipStream_t s, const float *d_x, uint64_t n, uin
       KT_END();
       LAUNCH_TRY("hist_kernel");
     }
-    KT("scan_partial_kernel");
-    scan_partial_kernel<<<dim3(G, Mh), kBlock, 0, hs>>>(hist_h, scan_h, done_h, K, T, G);
-    KT_END();
-    KT("scan_apply_kernel");
+    // codes per scan thread: ceil(K / kBlock), rounded up to 1, 2 or 4
+    const uint32_t scan_per = K <= kBlock ? 1u : K <= 2u * kBlock ? 2u : 4u;
     // the fold's order: bins of 1/32 of the mean cluster size
-    scan_apply_kernel<<<dim3(G, Mh), kBlock, 0, hs>>>(
-        hist_h, scan_h, counts_h, start_h, order_h, done_h, K, T, G,
-        (uint32_t)std::max<uint64_t>(1, n / K / 32));
-    KT_END();
+    const uint32_t order_unit = (uint32_t)std::max<uint64_t>(1, n / K / 32);
+#define SCAN_PASSES(P)                                                                    \
+  do {                                                                                    \
+    KT("scan_partial_kernel<%uu>", P);                                                    \
+    scan_partial_kernel<P><<<dim3(G, Mh), kBlock, 0, hs>>>(hist_h, scan_h, done_h, K, T, G); \
+    KT_END();                                                                             \
+    KT("scan_apply_kernel<%uu>", P);                                                      \
+    scan_apply_kernel<P><<<dim3(G, Mh), kBlock, 0, hs>>>(hist_h, scan_h, counts_h, start_h,  \
+                                                         order_h, done_h, K, T, G,        \
+                                                         order_unit);                     \
+    KT_END();                                                                             \
+  } while (0)
+    if (scan_per == 1)
+      SCAN_PASSES(1u);
+    else if (scan_per == 2)
+      SCAN_PASSES(2u);
+    else
+      SCAN_PASSES(4u);
+#undef SCAN_PASSES
     LAUNCH_TRY("scan kernels");
     DISPATCH_D_ST(D, scatter(xs_h, codes_h, hist_h, start_h, sorted_h, done_h, n, Mh, K, T, hs));
     if (st) return st;
