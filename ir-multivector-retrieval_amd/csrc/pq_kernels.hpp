@@ -787,14 +787,23 @@ __global__ __launch_bounds__(kBlock) void scatter_kernel(
   }
 }
 
-// Step 4: one wave per (subspace, cluster): block r * M + m folds the cluster
-// of rank r in subspace m's size order (fold_order_block), so every
-// subspace's largest clusters start first.  The wave streams the cluster's
-// contiguous records with coalesced loads (kFoldBatch x 64 records in
-// flight, staged through LDS dimension-major) and lanes 0..D-1 fold
-// dimension d in ascending vector order from 0.0f, then write
+// Step 4: one wave per (subspace, FP consecutive ranks of its size order):
+// block g * M + m folds the clusters of ranks g FP .. g FP + FP - 1 in
+// subspace m's size order (fold_order_block), so every subspace's largest
+// clusters start first, and clusters that share a wave have similar sizes.
+// FP = 4 / DP below four padded dimensions (two clusters at dsub 2, four at
+// dsub 1), else 1, so that lane p DP + d folds dimension d of the wave's
+// cluster p and one add serves FP clusters.  The wave streams each
+// cluster's contiguous records with coalesced loads (kFoldBatch x 64 records
+// in flight, staged through LDS dimension-major) and each lane folds its
+// dimension in ascending vector order from 0.0f, then writes
 // sum * fl(1 / fl(count)) (src/tac/kmeans.zig:177-198).  Empty clusters are
 // left for reseed_kernel.
+template <int D>
+constexpr uint32_t fold_per_wave() {
+  return Pad<D>::value < 4 ? 4u / (uint32_t)Pad<D>::value : 1u;
+}
+
 template <int D>
 __global__ __launch_bounds__(kWave) void fold_kernel(
     const float* __restrict__ sorted, const uint32_t* __restrict__ counts,
@@ -802,51 +811,74 @@ __global__ __launch_bounds__(kWave) void fold_kernel(
     const uint32_t* __restrict__ done, const uint32_t* __restrict__ order, uint64_t n,
     uint32_t M, uint32_t K) {
   constexpr int DP = Pad<D>::value;
+  constexpr uint32_t FP = fold_per_wave<D>();
   constexpr uint32_t U = kFoldBatch;
-  // Padded: the D columns start on distinct banks.
+  // Padded: the FP * DP columns start on distinct banks.
   constexpr uint32_t kCol = U * kWave + 36;
-  __shared__ __attribute__((aligned(16))) float buf[kCol * DP];
-  const uint32_t m = blockIdx.x % M, c = order[(uint64_t)m * K + blockIdx.x / M];
+  __shared__ __attribute__((aligned(16))) float buf[kCol * DP * FP];
+  const uint32_t m = blockIdx.x % M, r0 = (blockIdx.x / M) * FP;
   if (done[m]) return;
-  const uint32_t cnt = counts[(uint64_t)m * K + c];
-  if (cnt == 0) return;
   const uint32_t lane = threadIdx.x;
-  const float* p = sorted + ((uint64_t)m * n + start[(uint64_t)m * K + c]) * DP;
-  float v[U][DP];
+  uint32_t cl[FP], cnt[FP];
+  const float* src[FP];
+  uint32_t most = 0;
+#pragma unroll
+  for (uint32_t f = 0; f < FP; ++f) {
+    cl[f] = r0 + f < K ? order[(uint64_t)m * K + r0 + f] : 0u;
+    cnt[f] = r0 + f < K ? counts[(uint64_t)m * K + cl[f]] : 0u;
+    src[f] = sorted + ((uint64_t)m * n + (cnt[f] ? start[(uint64_t)m * K + cl[f]] : 0u)) * DP;
+    most = cnt[f] > most ? cnt[f] : most;
+  }
+  if (most == 0) return;
+  float v[FP][U][DP];
   auto load_batch = [&](uint32_t j0) {
 #pragma unroll
-    for (uint32_t u = 0; u < U; ++u) {
-      const uint32_t j = j0 + u * kWave + lane;
-      if (j < cnt) {
-        const float* q = p + (uint64_t)j * DP;
+    for (uint32_t f = 0; f < FP; ++f)
 #pragma unroll
-        for (int k = 0; k < DP; k += (DP >= 4 ? 4 : DP)) {
-          if constexpr (DP >= 4) {
-            const float4 a = *reinterpret_cast<const float4*>(q + k);
-            v[u][k] = a.x; v[u][k + 1] = a.y; v[u][k + 2] = a.z; v[u][k + 3] = a.w;
-          } else if constexpr (DP == 2) {
-            const float2 a = *reinterpret_cast<const float2*>(q);
-            v[u][0] = a.x; v[u][1] = a.y;
-          } else {
-            v[u][0] = q[0];
+      for (uint32_t u = 0; u < U; ++u) {
+        const uint32_t j = j0 + u * kWave + lane;
+        if (j < cnt[f]) {
+          const float* q = src[f] + (uint64_t)j * DP;
+#pragma unroll
+          for (int k = 0; k < DP; k += (DP >= 4 ? 4 : DP)) {
+            if constexpr (DP >= 4) {
+              const float4 a = *reinterpret_cast<const float4*>(q + k);
+              v[f][u][k] = a.x; v[f][u][k + 1] = a.y; v[f][u][k + 2] = a.z; v[f][u][k + 3] = a.w;
+            } else if constexpr (DP == 2) {
+              const float2 a = *reinterpret_cast<const float2*>(q);
+              v[f][u][0] = a.x; v[f][u][1] = a.y;
+            } else {
+              v[f][u][0] = q[0];
+            }
           }
         }
       }
-    }
   };
-  // buf is dimension-major, [DP][kCol]: lane d reads four consecutive
-  // members of its dimension with one 16-byte LDS read.
+  // buf is column-major, [FP][DP][kCol]: lane f DP + d reads four
+  // consecutive members of dimension d of cluster f with one 16-byte LDS
+  // read.
+  const uint32_t f_of = lane / DP, d_of = lane % DP;
+  const bool folds = f_of < FP && d_of < (uint32_t)D;
+  uint32_t mine = 0, my_cl = 0;  // this lane's cluster, by selects (no indexed registers)
+#pragma unroll
+  for (uint32_t f = 0; f < FP; ++f) {
+    mine = f == f_of ? cnt[f] : mine;
+    my_cl = f == f_of ? cl[f] : my_cl;
+  }
+  mine = folds ? mine : 0u;
   float acc = 0.0f;
   load_batch(0);
-  for (uint32_t j0 = 0; j0 < cnt; j0 += U * kWave) {
+  for (uint32_t j0 = 0; j0 < most; j0 += U * kWave) {
 #pragma unroll
-    for (uint32_t u = 0; u < U; ++u)
+    for (uint32_t f = 0; f < FP; ++f)
 #pragma unroll
-      for (int k = 0; k < DP; ++k) buf[k * kCol + u * kWave + lane] = v[u][k];
+      for (uint32_t u = 0; u < U; ++u)
+#pragma unroll
+        for (int k = 0; k < DP; ++k) buf[(f * DP + k) * kCol + u * kWave + lane] = v[f][u][k];
     __syncthreads();
-    if (j0 + U * kWave < cnt) load_batch(j0 + U * kWave);
-    const uint32_t len = cnt - j0 < U * kWave ? cnt - j0 : U * kWave;
-    if (lane < (uint32_t)D) {
+    if (j0 + U * kWave < most) load_batch(j0 + U * kWave);
+    const uint32_t len = mine > j0 ? (mine - j0 < U * kWave ? mine - j0 : U * kWave) : 0u;
+    if (folds) {
       // One dependent add per member, in ascending member order.  A step
       // issues the LDS reads of 128 members together (32 16-byte reads), so
       // their latency is paid once per 128 adds; then steps of 32, then one.
@@ -881,7 +913,7 @@ __global__ __launch_bounds__(kWave) void fold_kernel(
     }
     __syncthreads();
   }
-  if (lane < (uint32_t)D) cb[((uint64_t)m * K + c) * D + lane] = acc * (1.0f / (float)cnt);
+  if (folds && mine > 0) cb[((uint64_t)m * K + my_cl) * D + d_of] = acc * (1.0f / (float)mine);
 }
 
 // ---------------------------------------------------------------------------

@@ -758,7 +758,9 @@ struct Launch {
                    float *cb, const uint32_t *done, const uint32_t *order, uint64_t n, uint32_t M,
                    uint32_t K, hipStream_t s) {
     KT("fold_kernel<%d>", D);
-    fold_kernel<D><<<M * K, kWave, 0, s>>>(sorted, counts, start, cb, done, order, n, M, K);
+    constexpr uint32_t FP = fold_per_wave<D>();
+    fold_kernel<D><<<M * ((K + FP - 1) / FP), kWave, 0, s>>>(sorted, counts, start, cb, done,
+                                                             order, n, M, K);
     KT_END();
   }
   static void reseed(const float *xs, float *e, const uint32_t *counts, float *cb,
