@@ -791,9 +791,9 @@ __global__ __launch_bounds__(kBlock) void scatter_kernel(
 // block g * M + m folds the clusters of ranks g FP .. g FP + FP - 1 in
 // subspace m's size order (fold_order_block), so every subspace's largest
 // clusters start first, and clusters that share a wave have similar sizes.
-// FP = 8 / DP up to four padded dimensions (two clusters at dsub 3-4, four
-// at dsub 2, eight at dsub 1), else 1, so that lane p DP + d folds
-// dimension d of the wave's cluster p and one add serves FP clusters.  The wave streams each
+// FP = 8 / DP below four padded dimensions (four clusters at dsub 2, eight
+// at dsub 1), else 1, so that lane p DP + d folds dimension d of the wave's
+// cluster p and one add serves FP clusters.  The wave streams each
 // cluster's contiguous records with coalesced loads (kFoldBatch x 64 records
 // in flight, staged through LDS dimension-major) and each lane folds its
 // dimension in ascending vector order from 0.0f, then writes
@@ -801,7 +801,7 @@ __global__ __launch_bounds__(kBlock) void scatter_kernel(
 // left for reseed_kernel.
 template <int D>
 constexpr uint32_t fold_per_wave() {
-  return Pad<D>::value <= 4 ? 8u / (uint32_t)Pad<D>::value : 1u;
+  return Pad<D>::value < 4 ? 8u / (uint32_t)Pad<D>::value : 1u;
 }
 
 template <int D>
