@@ -813,22 +813,26 @@ __device__ __forceinline__ void pruned_argmin_lanes(const float (&x)[D], const f
 // in hist[m][tile][code].  S > 1 (with VPT 1): S lanes share a vector's
 // search (pruned_argmin_lanes), for K with Kp / kPruneBlock a multiple of
 // S: a search is a serial chain over its codewords, and few deferred
-// vectors leave few waves per SIMD to hide it.  With stats (profiling):
-// stats[0] += deferred vectors, stats[1] += n per subspace.
+// vectors leave few waves per SIMD to hide it; many deferred vectors keep
+// the SIMDs busy anyway, and there one lane per vector costs less, so a
+// subspace with `split` deferred vectors or more takes one lane per vector
+// (the grid is sized for the S-lane tiles, which are smaller).  With stats
+// (profiling): stats[0] += deferred vectors, stats[1] += n per subspace.
 template <int D, int VPT, int S = 1>
 __global__ __launch_bounds__(kBlock) void assign_list_kernel(
     const float* __restrict__ xs, const float* __restrict__ cb, uint16_t* __restrict__ codes,
     float* __restrict__ e, const uint32_t* __restrict__ defer,
     const uint32_t* __restrict__ defer_count, const uint32_t* __restrict__ done, uint64_t n,
     uint32_t K, unsigned long long* __restrict__ rescans, unsigned long long* __restrict__ stats,
-    uint32_t* __restrict__ hist, uint32_t T) {
+    uint32_t* __restrict__ hist, uint32_t T, uint32_t split) {
   static_assert(S == 1 || VPT == 1, "lane groups take one vector each");
   constexpr int DP = Pad<D>::value;
-  constexpr uint32_t kTile = kBlock * VPT / S;
   extern __shared__ __attribute__((aligned(16))) float lds[];
   const uint32_t m = blockIdx.y;
   if (done[m]) return;
   const uint32_t cnt = defer_count[m];
+  const bool lanes = S > 1 && cnt < split;  // uniform over the grid's subspace
+  const uint32_t kTile = lanes ? kBlock * VPT / S : kBlock * VPT;
   if (stats && blockIdx.x == 0 && threadIdx.x == 0) {
     atomicAdd(&stats[0], (unsigned long long)cnt);
     atomicAdd(&stats[1], (unsigned long long)n);
@@ -850,28 +854,30 @@ __global__ __launch_bounds__(kBlock) void assign_list_kernel(
   const uint32_t* lst = defer + (uint64_t)m * n;
   uint32_t mine = 0;
   if constexpr (S > 1) {
-    const uint32_t sub = threadIdx.x % S;
-    for (uint64_t t0 = (uint64_t)blockIdx.x * kTile; t0 < cnt; t0 += (uint64_t)gridDim.x * kTile) {
-      const uint64_t q = t0 + threadIdx.x / S;
-      const uint32_t idx = q < cnt ? lst[q] : 0xFFFFFFFFu;
-      float x[D];
-      if (idx != 0xFFFFFFFFu) {
-        load_padded<D>(xm + (uint64_t)idx * DP, x);
-      } else {
+    if (lanes) {
+      const uint32_t sub = threadIdx.x % S;
+      for (uint64_t t0 = (uint64_t)blockIdx.x * kTile; t0 < cnt; t0 += (uint64_t)gridDim.x * kTile) {
+        const uint64_t q = t0 + threadIdx.x / S;
+        const uint32_t idx = q < cnt ? lst[q] : 0xFFFFFFFFu;
+        float x[D];
+        if (idx != 0xFFFFFFFFu) {
+          load_padded<D>(xm + (uint64_t)idx * DP, x);
+        } else {
 #pragma unroll
-        for (int k = 0; k < D; ++k) x[k] = 0.0f;
+          for (int k = 0; k < D; ++k) x[k] = 0.0f;
+        }
+        uint32_t bidx;
+        float best;
+        pruned_argmin_lanes<D, S, true>(x, lcb, lnc, K, Kp, lmax, sub, bidx, best, mine);
+        if (sub == 0 && idx != 0xFFFFFFFFu) {
+          codes[(uint64_t)m * n + idx] = (uint16_t)bidx;
+          e[(uint64_t)m * n + idx] = best;
+          atomicAdd(&hist[((uint64_t)m * T + idx / kSortTile) * K + bidx], 1u);
+        }
       }
-      uint32_t bidx;
-      float best;
-      pruned_argmin_lanes<D, S, true>(x, lcb, lnc, K, Kp, lmax, sub, bidx, best, mine);
-      if (sub == 0 && idx != 0xFFFFFFFFu) {
-        codes[(uint64_t)m * n + idx] = (uint16_t)bidx;
-        e[(uint64_t)m * n + idx] = best;
-        atomicAdd(&hist[((uint64_t)m * T + idx / kSortTile) * K + bidx], 1u);
-      }
+      flush_rescans(mine, &lcount, rescans);
+      return;
     }
-    flush_rescans(mine, &lcount, rescans);
-    return;
   }
   for (uint64_t t0 = (uint64_t)blockIdx.x * kTile; t0 < cnt; t0 += (uint64_t)gridDim.x * kTile) {
     float x[VPT][D];
@@ -907,25 +913,26 @@ __global__ __launch_bounds__(kBlock) void assign_list_kernel(
 // vectors gathered through defer[m][..] from the token-major input; codes
 // to out[i][m].  Each thread takes VPT deferred vectors (their searches
 // interleave), a persistent grid of gridDim.x blocks per subspace walks
-// tiles of kBlock * VPT entries.  Two widths are launched back to back and a
-// subspace's deferred count picks one: VPT 1 (many short waves) below a
-// quarter of the rows, VPT 8 (the full search's interleave) above; the other
-// launch returns at once.  S > 1 (with VPT 1): S lanes share a vector's
-// search, as in assign_list_kernel.
+// tiles of kBlock * VPT / S entries.  Two widths are launched back to back
+// and a subspace's deferred count picks one: VPT 1 below a quarter of the
+// rows, VPT 8 (the full search's interleave) above; the other launch returns
+// at once.  S > 1 (with VPT 1): S lanes share a vector's search below
+// `split` deferred vectors, one lane from there, as in assign_list_kernel.
 template <int D, int VPT, typename CodeT, int S = 1>
 __global__ __launch_bounds__(kBlock) void encode_list_kernel(
     const float* __restrict__ x, const float* __restrict__ cb, CodeT* __restrict__ out,
     const uint32_t* __restrict__ defer, const uint32_t* __restrict__ defer_count, uint64_t n,
     uint32_t dim, uint32_t M, uint32_t K, unsigned long long* __restrict__ rescans,
-    unsigned long long* __restrict__ stats) {
+    unsigned long long* __restrict__ stats, uint32_t split) {
   static_assert(S == 1 || VPT == 1, "lane groups take one vector each");
   constexpr int DP = Pad<D>::value;
-  constexpr uint32_t kTile = kBlock * VPT / S;
   extern __shared__ __attribute__((aligned(16))) float lds[];
   const uint32_t m = blockIdx.y;
   const uint32_t cnt = defer_count[m];
   const bool wide = 4ull * cnt > n;
   if ((VPT > 1) != wide) return;  // the other width serves this subspace
+  const bool lanes = S > 1 && cnt < split;
+  const uint32_t kTile = lanes ? kBlock * VPT / S : kBlock * VPT;
   if (stats && blockIdx.x == 0 && threadIdx.x == 0) {
     atomicAdd(&stats[0], (unsigned long long)cnt);
     atomicAdd(&stats[1], (unsigned long long)n);
@@ -946,21 +953,23 @@ __global__ __launch_bounds__(kBlock) void encode_list_kernel(
   const uint32_t* lst = defer + (uint64_t)m * n;
   uint32_t mine = 0;
   if constexpr (S > 1) {
-    const uint32_t sub = threadIdx.x % S;
-    for (uint64_t t0 = (uint64_t)blockIdx.x * kTile; t0 < cnt; t0 += (uint64_t)gridDim.x * kTile) {
-      const uint64_t q = t0 + threadIdx.x / S;
-      const uint32_t idx = q < cnt ? lst[q] : 0xFFFFFFFFu;
-      const float* src = x + (uint64_t)(idx != 0xFFFFFFFFu ? idx : 0u) * dim + (uint64_t)m * D;
-      float xv[D];
+    if (lanes) {
+      const uint32_t sub = threadIdx.x % S;
+      for (uint64_t t0 = (uint64_t)blockIdx.x * kTile; t0 < cnt; t0 += (uint64_t)gridDim.x * kTile) {
+        const uint64_t q = t0 + threadIdx.x / S;
+        const uint32_t idx = q < cnt ? lst[q] : 0xFFFFFFFFu;
+        const float* src = x + (uint64_t)(idx != 0xFFFFFFFFu ? idx : 0u) * dim + (uint64_t)m * D;
+        float xv[D];
 #pragma unroll
-      for (int k = 0; k < D; ++k) xv[k] = src[k];
-      uint32_t bidx;
-      float best;
-      pruned_argmin_lanes<D, S, false>(xv, lcb, lnc, K, Kp, lmax, sub, bidx, best, mine);
-      if (sub == 0 && idx != 0xFFFFFFFFu) out[(uint64_t)idx * M + m] = (CodeT)bidx;
+        for (int k = 0; k < D; ++k) xv[k] = src[k];
+        uint32_t bidx;
+        float best;
+        pruned_argmin_lanes<D, S, false>(xv, lcb, lnc, K, Kp, lmax, sub, bidx, best, mine);
+        if (sub == 0 && idx != 0xFFFFFFFFu) out[(uint64_t)idx * M + m] = (CodeT)bidx;
+      }
+      flush_rescans(mine, &lcount, rescans);
+      return;
     }
-    flush_rescans(mine, &lcount, rescans);
-    return;
   }
   for (uint64_t t0 = (uint64_t)blockIdx.x * kTile; t0 < cnt; t0 += (uint64_t)gridDim.x * kTile) {
     float xv[VPT][D];

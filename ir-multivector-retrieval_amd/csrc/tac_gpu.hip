@@ -468,15 +468,21 @@ inline uint32_t cand_hist_tiles(uint32_t K, uint32_t DP, uint32_t cells, uint32_
   return tiles;
 }
 inline uint32_t nbr_threads(uint32_t K) { return K > 256 ? 256u : (uint32_t)kWave; }
-// The deferred-vector kernels give each vector four lanes from K = 128 on,
-// where the blocks of kPruneBlock codewords split evenly over four lanes
+// The deferred-vector kernels can give each vector four lanes from K = 128
+// on, where the blocks of kPruneBlock codewords split evenly over four lanes
 // (TAC_GPU_LIST_LANES=1 keeps one lane per vector, for the tests that
-// compare the two).
+// compare the two).  Four lanes serve a subspace with fewer than
+// list_split(K) deferred vectors (one lane costs less once the many vectors
+// fill the SIMDs: measured 118 against 133 us for 100,000 vectors per
+// subspace at K = 256); 0 when they are not used.
 inline bool list_lanes4(uint32_t K) {
   const char *v = getenv("TAC_GPU_LIST_LANES");
   const bool one = v != nullptr && v[0] == '1';
   const uint32_t Kp = (K + kPruneBlock - 1) / kPruneBlock * kPruneBlock;
   return !one && K >= 128 && (Kp / kPruneBlock) % 4 == 0;
+}
+inline uint32_t list_split(uint32_t K) {
+  return !list_lanes4(K) ? 0u : K >= 512 ? 0xFFFFFFFFu : 32768u;
 }
 
 template <int D>
@@ -558,20 +564,20 @@ struct Launch {
     // kPruneBlock codewords split evenly over them (list_lanes4), so that
     // four times as many waves hide the chains, else one vector per thread;
     // about 4,096 blocks over all subspaces, looping when there are more.
-    const bool lanes4 = list_lanes4(K);
-    const uint64_t per = lanes4 ? kBlock / 4 : kBlock;
+    const uint32_t split = list_split(K);
+    const uint64_t per = split ? kBlock / 4 : kBlock;  // the smaller tiles of the two widths
     const uint64_t g =
         std::max<uint64_t>(1, std::min<uint64_t>((n + per - 1) / per, (4096 + M - 1) / M));
-    if (lanes4) {
+    if (split) {
       KT("assign_list_kernel<%d, 1, 4>", D);
       assign_list_kernel<D, 1, 4><<<dim3((unsigned)g, M), kBlock, lds, s>>>(
           xs, cb, codes, e, defer, defer_count, done, n, K, rescans,
-          g_profile ? rescans + 1 : nullptr, hist, T);
+          g_profile ? rescans + 1 : nullptr, hist, T, split);
     } else {
-      KT("assign_list_kernel<%d, 1>", D);
-      assign_list_kernel<D, 1><<<dim3((unsigned)g, M), kBlock, lds, s>>>(
+      KT("assign_list_kernel<%d, 1, 1>", D);
+      assign_list_kernel<D, 1, 1><<<dim3((unsigned)g, M), kBlock, lds, s>>>(
           xs, cb, codes, e, defer, defer_count, done, n, K, rescans,
-          g_profile ? rescans + 1 : nullptr, hist, T);
+          g_profile ? rescans + 1 : nullptr, hist, T, 0u);
     }
     KT_END();
     return TAC_OK;
@@ -649,25 +655,25 @@ struct Launch {
                              unsigned long long *stats, hipStream_t s) {
     const uint32_t Kp = (K + kPruneBlock - 1) / kPruneBlock * kPruneBlock;
     const size_t lds = (size_t)Kp * (Pad<D>::value + 1) * sizeof(float) + 2 * sizeof(uint32_t);
-    const bool lanes4 = list_lanes4(K);
-    const uint64_t per1 = lanes4 ? kBlock / 4 : kBlock;
+    const uint32_t split = list_split(K);
+    const uint64_t per1 = split ? kBlock / 4 : kBlock;  // the smaller tiles of the two widths
     const uint64_t g1 = std::max<uint64_t>(
         1, std::min<uint64_t>((n + per1 - 1) / per1, (4096 + M - 1) / M));
     const uint64_t g8 = std::max<uint64_t>(
         1, std::min<uint64_t>((n + kBlock * 8 - 1) / (kBlock * 8), (4096 + M - 1) / M));
-    if (lanes4) {
+    if (split) {
       KT("encode_list_kernel<%d, 1, %s, 4>", D, code_name<CodeT>());
       encode_list_kernel<D, 1, CodeT, 4><<<dim3((unsigned)g1, M), kBlock, lds, s>>>(
-          x, cb, codes, defer, defer_count, n, dim, M, K, rescans, stats);
+          x, cb, codes, defer, defer_count, n, dim, M, K, rescans, stats, split);
     } else {
-      KT("encode_list_kernel<%d, 1, %s>", D, code_name<CodeT>());
-      encode_list_kernel<D, 1, CodeT><<<dim3((unsigned)g1, M), kBlock, lds, s>>>(
-          x, cb, codes, defer, defer_count, n, dim, M, K, rescans, stats);
+      KT("encode_list_kernel<%d, 1, %s, 1>", D, code_name<CodeT>());
+      encode_list_kernel<D, 1, CodeT, 1><<<dim3((unsigned)g1, M), kBlock, lds, s>>>(
+          x, cb, codes, defer, defer_count, n, dim, M, K, rescans, stats, 0u);
     }
     KT_END();
-    KT("encode_list_kernel<%d, 8, %s>", D, code_name<CodeT>());
+    KT("encode_list_kernel<%d, 8, %s, 1>", D, code_name<CodeT>());
     encode_list_kernel<D, 8, CodeT><<<dim3((unsigned)g8, M), kBlock, lds, s>>>(
-        x, cb, codes, defer, defer_count, n, dim, M, K, rescans, stats);
+        x, cb, codes, defer, defer_count, n, dim, M, K, rescans, stats, split);
     KT_END();
     return TAC_OK;
   }
