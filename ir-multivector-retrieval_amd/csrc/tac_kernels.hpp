@@ -955,9 +955,10 @@ __global__ void tac_assign_kernel(const float* __restrict__ G, const float* __re
 // Lanes.  A 16-row group x 16 centroids: lane l feeds row l % 16 and
 // centroid l % 16 at dimension 4 s + l / 16 and holds the dot products of
 // rows 4 (l / 16) + i, i < 4, with centroid l % 16.  Each lane keeps the two
-// smallest screen values of its centroids per row; when the second is at
-// most the threshold the lane may hold more candidates, and the row gets the
-// reference distance to every centroid instead.  A block whose rows or
+// smallest screen values of its centroids (those with c % 16 = l % 16) per
+// row; when the second is at most the threshold the lane may hold more
+// candidates, and every centroid of its class gets the reference distance
+// (a row with a NaN screen value gets it for every centroid).  A block whose rows or
 // centroids have non-finite, subnormal or huge components (where the bounds
 // do not hold) takes tac_assign_kernel's exact search for all its rows.
 // One block of 256 work-items per tile of 128 rows; wave w takes rows
@@ -1034,9 +1035,11 @@ __global__ __launch_bounds__(kTacMfmaThreads) __attribute__((amdgpu_waves_per_eu
   __shared__ float hs[CH];
   __shared__ float x2s[R];
   __shared__ unsigned long long rowkey[R];
+  // (row, centroid) candidates from the front; (row, column class) entries
+  // from the back: a row's lane contributes at most one of the two
   __shared__ uint32_t queue[R * 16];
-  __shared__ uint32_t full[R];  // rows whose candidates a lane may not hold
-  __shared__ uint32_t qn, nfull, exact, hmax;
+  __shared__ uint32_t full[R];  // rows whose screen values are not all numbers
+  __shared__ uint32_t qn, cn, nfull, exact, hmax;
   const TacTile tl = tiles[blockIdx.x];
   if (done[tl.prob]) return;
   const TacProblem pr = probs[tl.prob];
@@ -1044,6 +1047,7 @@ __global__ __launch_bounds__(kTacMfmaThreads) __attribute__((amdgpu_waves_per_eu
   const uint32_t rows = pr.n - tl.row0 < R ? pr.n - tl.row0 : R;
   if (t == 0) {
     qn = 0;
+    cn = 0;
     nfull = 0;
     exact = 0;
     hmax = 0;  // bits of the largest h of the problem (NaN: an untame centroid)
@@ -1205,14 +1209,21 @@ __global__ __launch_bounds__(kTacMfmaThreads) __attribute__((amdgpu_waves_per_eu
         // A NaN screen value (or threshold) cannot occur with tame inputs;
         // it sends the row to the full search all the same.  The row's 16
         // lanes agree through the reduction, and lane 16 q lists it.
-        uint32_t over = (!(m <= thr) || b2[g][v] <= thr) ? 1u : 0u;
-#pragma unroll
-        for (int off = 1; off < 16; off <<= 1) over |= __shfl_xor(over, off, 64);
-        // list slots by a wave ballot and one LDS atomic per wave (lanes
-        // adding to one counter one by one serialize)
-        const bool cand = r < rows && b1[g][v] <= thr;
+        const bool over = !(m <= thr);
+        // This lane sees the centroids of its column class li (c % 16 == li)
+        // only, and keeps their two smallest screen values.  With the second
+        // above the threshold, its only possible candidate is the first;
+        // with the second at or below it the class may hold more, and every
+        // centroid of the class gets the reference distance.  Other classes
+        // are settled by their own lanes.  List slots by a wave ballot and
+        // one LDS atomic per wave (lanes adding to one counter one by one
+        // serialize).
+        const bool cls = r < rows && !over && b2[g][v] <= thr;
+        const bool cand = r < rows && !over && !cls && b1[g][v] <= thr;
         const uint32_t qs = tac_wave_append(cand, &qn);
         if (cand) queue[qs] = (r << 16) | i1[g][v];
+        const uint32_t cs_ = tac_wave_append(cls, &cn);
+        if (cls) queue[R * 16 - 1 - cs_] = (r << 16) | li;
         const bool fr = r < rows && li == 0 && over;
         const uint32_t fs = tac_wave_append(fr, &nfull);
         if (fr) full[fs] = r;
@@ -1224,8 +1235,19 @@ __global__ __launch_bounds__(kTacMfmaThreads) __attribute__((amdgpu_waves_per_eu
         const float d = tac_l2sq<64>(xr + r * LD, Cp + (uint64_t)c * 64, 64);
         atomicMin(&rowkey[r], ((unsigned long long)__float_as_uint(d) << 32) | c);
       }
-      // Rows a lane's two kept values could not settle: every centroid, the
-      // block's work-items side by side.
+      // Column classes: per = ceil(k / 16) centroids each, the work-items
+      // over all (entry, centroid) pairs.
+      const uint32_t per = (pr.k + 15) / 16;
+      for (uint32_t q = t; q < cn * per; q += kTacMfmaThreads) {
+        const uint32_t ent = queue[R * 16 - 1 - q / per];
+        const uint32_t r = ent >> 16, c = (ent & 15u) + 16u * (q % per);
+        if (c < pr.k) {
+          const float d = tac_l2sq<64>(xr + r * LD, Cp + (uint64_t)c * 64, 64);
+          atomicMin(&rowkey[r], ((unsigned long long)__float_as_uint(d) << 32) | c);
+        }
+      }
+      // Rows with a NaN screen value: every centroid, the block's
+      // work-items side by side.
       // (each work-item keeps its own minimum, the wave reduces it, and one
       // LDS atomic per wave and row merges them)
       for (uint32_t j = 0; j < nfull; ++j) {
