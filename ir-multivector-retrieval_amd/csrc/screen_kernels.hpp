@@ -1,0 +1,324 @@
+// screen_kernels.hpp — the Lloyd assignment's full search for sub-dimensions
+// 5-8 (records of 8 floats) and K <= 256 with its first pass on the matrix
+// cores.  Included once, by tac_gpu.hip, after cand_kernels.hpp.
+//
+// Screen.  For a vector x and codeword c (dimensions past D are 0), the
+// search ranks codewords by s(c) = ||c||^2 - 2 x.c.  Here s comes from one
+// v_mfma_f32_16x16x32_bf16 per 16 codewords x 16 vectors, over 32 terms:
+//   A = [-2 c_hi, -2 c_lo, -2 c_hi, n_hi, n_lo, 0 ...],  B = [x_hi, x_hi, x_lo, 1, 1, 0 ...]
+// with v_hi = bf16(v), v_lo = bf16(v - v_hi) (round to nearest even) and
+// n = fl(sum_d c_d^2).  For a finite v, |v - v_hi| <= 2^-8 |v| + 2^-126 and
+// |v - v_hi - v_lo| <= 2^-16 |v| + 2^-125 (the absolute terms cover
+// subnormal or flushed pieces), so per dimension, with a = -2 c_d, the three
+// products miss a x_d by at most 3.02 * 2^-16 |a| |x_d| + 2^-123 (|a| + |x_d|);
+// n_hi + n_lo is within (2^-16 + gamma_8) ||c||^2 + 2^-124 of ||c||^2; the
+// bf16 products are exact in fp32 but for underflow (2^-126 each); and the
+// matrix core adds the 32 terms in fp32 in some order (gamma_31 of their
+// absolute sum).  Altogether
+//   |s~ - s| <= 2^-14 (||c||^2 + 2 ||x|| ||c||) + 2^-121 (2 ||c|| + ||x||) + 2^-120,
+// and the kernel uses four times that with cmax^2 = max_c fl(||c||^2) in
+// place of ||c||^2.  It needs fl(||x||^2) <= 2^120 and cmax^2 <= 2^120
+// (false for a NaN or infinite component): every component is then below
+// 2^60 (times 1 + 4u), so no product or partial sum overflows.  A codebook
+// past that sends every vector to the deferred list below, a vector past it
+// goes there alone.
+//
+// Layout and the exact result.  The codeword pieces are the A operand and
+// the vector pieces the B operand, so lane l of a wave holds the screen
+// values of vector l % 16 of a 16-vector group against codewords
+// 16 g + 4 (l / 16) + i, i < 4, of codeword group g.  It folds them into the
+// minimum of blocks of two consecutive groups (8 codewords) and keeps the
+// two smallest block minima; the blocks of the vector's four lanes
+// partition the codewords.  After the four lanes merge their top-2
+// (permlane swaps: every lane of the vector ends with the same result), the
+// argument of pruned_argmin (pq_kernels.hpp) applies unchanged: when the gap
+// between the two smallest block minima exceeds the threshold built from the
+// screen bound and the reference distance's gamma_{D+2}, the reference's
+// first-index argmin lies in the winning block, whose codewords then get the
+// reference distance (two per lane, merged by (distance, index)).  Equal
+// block minima leave no gap.  A vector without the gap joins the subspace's
+// deferred list, whose pruned exact search (assign_list_kernel,
+// cand_kernels.hpp) follows: about 3% of the corpus rows at m8/d8, far fewer
+// than the waves that would stall on an in-wave scan of all K codewords.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#include "cand_kernels.hpp"
+
+namespace tacgpu {
+
+typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
+typedef float floatx4 __attribute__((ext_vector_type(4)));
+
+constexpr uint32_t kScreenMaxK = 256;     // codewords in the kernel's LDS table
+constexpr uint32_t kScreenVecGroups = 4;  // 16-vector groups per wave pass
+constexpr float kScreenTame = 1.329227995784916e36f;  // 2^120
+
+// Minimum, median and maximum without the canonicalising moves IEEE mode adds
+// to fminf / fmaxf; the screen's operands are never NaN where the results
+// count (tame vectors and codebooks, +inf padding).
+__device__ __forceinline__ float min3_raw(float a, float b, float c) {
+  float r;
+  asm("v_min3_f32 %0, %1, %2, %3" : "=v"(r) : "v"(a), "v"(b), "v"(c));
+  return r;
+}
+__device__ __forceinline__ float med3_raw(float a, float b, float c) {
+  float r;
+  asm("v_med3_f32 %0, %1, %2, %3" : "=v"(r) : "v"(a), "v"(b), "v"(c));
+  return r;
+}
+__device__ __forceinline__ float min_raw(float a, float b) {
+  float r;
+  asm("v_min_f32 %0, %1, %2" : "=v"(r) : "v"(a), "v"(b));
+  return r;
+}
+__device__ __forceinline__ float max_raw(float a, float b) {
+  float r;
+  asm("v_max_f32 %0, %1, %2" : "=v"(r) : "v"(a), "v"(b));
+  return r;
+}
+
+// The values of lanes l and l ^ 16 (R = 16) or l and l ^ 32 (R = 32), as a
+// pair that is the same in both lanes (v_permlane16_swap / v_permlane32_swap
+// of v with itself); reductions over the pair are symmetric in it.
+template <int R>
+__device__ __forceinline__ void pair_of(uint32_t v, uint32_t& a, uint32_t& b) {
+  static_assert(R == 16 || R == 32, "row pairs");
+  if constexpr (R == 16) {
+    const auto s = __builtin_amdgcn_permlane16_swap(v, v, false, false);
+    a = s[0];
+    b = s[1];
+  } else {
+    const auto s = __builtin_amdgcn_permlane32_swap(v, v, false, false);
+    a = s[0];
+    b = s[1];
+  }
+}
+
+// Merge the top-2 block minima (b1 <= b2, block bb of b1) of lanes l and l ^ R.
+template <int R>
+__device__ __forceinline__ void screen_merge(float& b1, float& b2, uint32_t& bb) {
+  uint32_t d1, s1, d2, s2, db, sb;
+  pair_of<R>(__float_as_uint(b1), d1, s1);
+  pair_of<R>(__float_as_uint(b2), d2, s2);
+  pair_of<R>(bb, db, sb);
+  const float D1 = __uint_as_float(d1), S1 = __uint_as_float(s1);
+  // second smallest of {D1, D2, S1, S2} with D1 <= D2, S1 <= S2
+  b2 = min3_raw(max_raw(D1, S1), __uint_as_float(d2), __uint_as_float(s2));
+  bb = S1 < D1 ? sb : db;  // ties leave b2 == b1: no gap
+  b1 = min_raw(D1, S1);
+}
+
+// (d, c) <- the smaller of the (distance, index) pairs of lanes l and l ^ R.
+template <int R>
+__device__ __forceinline__ void screen_lex_min(float& d, uint32_t& c) {
+  uint32_t dd, sd, dc, sc;
+  pair_of<R>(__float_as_uint(d), dd, sd);
+  pair_of<R>(c, dc, sc);
+  const float Dv = __uint_as_float(dd), Sv = __uint_as_float(sd);
+  const bool s_wins = Sv < Dv || (Sv == Dv && sc < dc);
+  d = s_wins ? Sv : Dv;
+  c = s_wins ? sc : dc;
+}
+
+// Lloyd assignment for D in 5..8 (vec.argmin: first index); xs = [M][n][8]
+// records, one block of 4 waves per sort tile of kSortTile rows
+// (blockIdx.x) of a subspace (blockIdx.y), 64 vectors per wave pass; K <=
+// kScreenMaxK = blockDim.x.  codes[m][i], e[m][i] = reference distance for
+// the vectors the screen settles; the others go to defer[m][..]
+// (defer_count[m] must be zero at the launch, and assign_list_kernel must
+// follow).  hist[m][tile][c] = the settled vectors of the tile with code c
+// (assign_list_kernel adds the deferred ones).
+template <int D>
+__global__ __launch_bounds__(256) void assign_screen_kernel(
+    const float* __restrict__ xs, const float* __restrict__ cb, uint16_t* __restrict__ codes,
+    float* __restrict__ e, uint32_t* __restrict__ defer, uint32_t* __restrict__ defer_count,
+    const uint32_t* __restrict__ done, uint64_t n, uint32_t K, uint32_t* __restrict__ hist,
+    uint32_t T) {
+  static_assert(D >= 5 && D <= 8, "records of 8 floats");
+  static_assert(kSortTile % (4 * 16 * kScreenVecGroups) == 0, "whole wave passes per tile");
+  constexpr uint32_t VG = kScreenVecGroups;
+  __shared__ bf16x8 lA[kScreenMaxK * 4];  // [c][q]: the codeword pieces
+  __shared__ __attribute__((aligned(16))) float lcb[kScreenMaxK * 8];  // fp32 codewords
+  __shared__ uint32_t s_hist[kScreenMaxK];
+  __shared__ uint32_t s_list[kSortTile];  // the tile's deferred rows
+  __shared__ uint32_t s_max, s_cnt, s_base;
+  const uint32_t m = blockIdx.y;
+  if (done[m]) return;
+  const uint32_t t = threadIdx.x, lane = t % kWave, w = t / kWave;
+  const uint32_t p = lane % 16, q = lane / 16;
+  const uint32_t ngroups = (K + 15u) / 16u;
+  if (t == 0) {
+    s_max = 0;
+    s_cnt = 0;
+  }
+  if (t < K) s_hist[t] = 0;
+  {
+    // The pieces of codeword c = t, padding past K.
+    const uint32_t c = t;
+    const float* cbm = cb + (uint64_t)m * K * D;
+    float v[8];
+#pragma unroll
+    for (int d = 0; d < 8; ++d) v[d] = (c < K && d < D) ? cbm[(uint64_t)c * D + d] : 0.0f;
+    float n2 = v[0] * v[0];
+#pragma unroll
+    for (int d = 1; d < D; ++d) n2 = n2 + v[d] * v[d];
+    bf16x8 ch, cl, nn;
+#pragma unroll
+    for (int d = 0; d < 8; ++d) {
+      const float a = -2.0f * v[d];  // exact
+      const __bf16 hi = (__bf16)a;
+      ch[d] = hi;
+      cl[d] = (__bf16)(a - (float)hi);
+      nn[d] = (__bf16)0.0f;
+      lcb[c * 8 + d] = v[d];
+    }
+    const __bf16 nh = (__bf16)n2;
+    nn[0] = c < K ? nh : (__bf16)__builtin_inff();  // padding: screen +inf
+    nn[1] = c < K ? (__bf16)(n2 - (float)nh) : (__bf16)0.0f;
+    lA[c * 4 + 0] = ch;
+    lA[c * 4 + 1] = cl;
+    lA[c * 4 + 2] = ch;
+    lA[c * 4 + 3] = nn;
+    // the largest norm's bits (norms are non-negative or NaN, and a NaN's
+    // bits sort above +inf's)
+    uint32_t mx = c < K ? __float_as_uint(n2) : 0u;
+#pragma unroll
+    for (int o = 1; o < kWave; o <<= 1) {
+      const uint32_t other = (uint32_t)__shfl_xor((int)mx, o, kWave);
+      mx = other > mx ? other : mx;
+    }
+    __syncthreads();  // s_max cleared
+    if (lane == 0) atomicMax(&s_max, mx);
+  }
+  __syncthreads();
+  const float cmax2 = __uint_as_float(s_max);
+  const bool cb_ok = cmax2 <= kScreenTame;  // false on NaN
+  const float cmax = sqrtf(cmax2);
+  constexpr float u = 5.9604644775390625e-8f;  // 2^-24
+  constexpr float gR = (float)(D + 2) * u / (1.0f - (float)(D + 2) * u);
+  constexpr float k12 = 2.44140625e-4f;           // 2^-12
+  constexpr float k119 = 1.504632769052528e-36f;  // 2^-119
+  constexpr float k118 = 3.009265538105056e-36f;  // 2^-118
+  const float* xm = xs + (uint64_t)m * n * 8;
+  const uint64_t tile0 = (uint64_t)blockIdx.x * kSortTile;
+  const uint64_t tile1 = tile0 + kSortTile < n ? tile0 + kSortTile : n;
+  const bf16x8* arow = lA + p * 4 + q;  // + 64 per codeword group
+  const floatx4 zero = {0.0f, 0.0f, 0.0f, 0.0f};
+  for (uint64_t row0 = tile0 + w * (16 * VG); row0 < tile1; row0 += 4 * 16 * VG) {
+    // B operands: vector row0 + 16 vg + p, pieces q (x_hi, x_hi, x_lo, ones);
+    // rows past the tile repeat its last row and are not written.
+    bf16x8 X[VG];
+    float x[VG][D], x2[VG];
+#pragma unroll
+    for (uint32_t vg = 0; vg < VG; ++vg) {
+      const uint64_t r = row0 + 16 * vg + p;
+      const uint64_t rr = r < tile1 ? r : tile1 - 1;
+      const float4 a0 = *reinterpret_cast<const float4*>(xm + rr * 8);
+      const float4 a1 = *reinterpret_cast<const float4*>(xm + rr * 8 + 4);
+      const float xv[8] = {a0.x, a0.y, a0.z, a0.w, a1.x, a1.y, a1.z, a1.w};
+#pragma unroll
+      for (int d = 0; d < D; ++d) x[vg][d] = xv[d];
+      float s2 = xv[0] * xv[0];
+#pragma unroll
+      for (int d = 1; d < D; ++d) s2 = s2 + xv[d] * xv[d];
+      x2[vg] = s2;
+      bf16x8 hi, lo, one;
+#pragma unroll
+      for (int d = 0; d < 8; ++d) {
+        const float xd = d < D ? xv[d] : 0.0f;
+        hi[d] = (__bf16)xd;
+        lo[d] = (__bf16)(xd - (float)hi[d]);
+        one[d] = (__bf16)(d < 2 ? 1.0f : 0.0f);
+      }
+      X[vg] = q == 3 ? one : q == 2 ? lo : hi;
+    }
+    // First pass: block minima over this lane's codewords (4 per group, two
+    // groups per block), the two smallest of them per vector; blocks are
+    // numbered b * 4 + q.
+    float b1[VG], b2[VG];
+    uint32_t bb[VG];
+#pragma unroll
+    for (uint32_t vg = 0; vg < VG; ++vg) {
+      b1[vg] = __builtin_inff();
+      b2[vg] = __builtin_inff();
+      bb[vg] = q;
+    }
+    for (uint32_t g = 0; g < ngroups; g += 2) {
+      const bf16x8 A0 = arow[g * 64];
+      const bf16x8 A1 = g + 1 < ngroups ? arow[(g + 1) * 64] : A0;  // A0 again: same minimum
+      const uint32_t blk = (g / 2) * 4 + q;
+#pragma unroll
+      for (uint32_t vg = 0; vg < VG; ++vg) {
+        const floatx4 c0 = __builtin_amdgcn_mfma_f32_16x16x32_bf16(A0, X[vg], zero, 0, 0, 0);
+        const floatx4 c1 = __builtin_amdgcn_mfma_f32_16x16x32_bf16(A1, X[vg], zero, 0, 0, 0);
+        const float v0 = min3_raw(c0[0], c0[1], c0[2]);
+        const float v1 = min3_raw(c1[0], c1[1], c1[2]);
+        const float v = min3_raw(min_raw(v0, c0[3]), v1, c1[3]);
+        b2[vg] = med3_raw(b1[vg], b2[vg], v);
+        bb[vg] = v < b1[vg] ? blk : bb[vg];
+        b1[vg] = min_raw(b1[vg], v);
+      }
+    }
+#pragma unroll
+    for (uint32_t vg = 0; vg < VG; ++vg) {
+      screen_merge<16>(b1[vg], b2[vg], bb[vg]);
+      screen_merge<32>(b1[vg], b2[vg], bb[vg]);
+    }
+    // The threshold test, then the reference distance to the winning block
+    // (lane q takes its codewords 16 g + 4 qw + q), or the deferred list.
+#pragma unroll
+    for (uint32_t vg = 0; vg < VG; ++vg) {
+      const uint64_t r = row0 + 16 * vg + p;
+      const float nx = sqrtf(x2[vg]);
+      const float ea = k12 * (cmax2 + 2.0f * nx * cmax) + k119 * (2.0f * cmax + nx) + k118;
+      float thr = 2.0f * ea * (1.0f + gR) +
+                  gR * (fabsf(b2[vg] + x2[vg]) + fabsf(b1[vg] + x2[vg]));
+      thr = 2.0f * thr + 1e-30f;
+      // b2 = +inf: every other block holds padding only (a tame codeword's
+      // screen value is finite), so the winning block holds every codeword.
+      const bool ok = cb_ok && x2[vg] <= kScreenTame &&
+                      (b2[vg] == __builtin_inff() || (b2[vg] - b1[vg]) > thr);
+      if (ok) {
+        float best = __builtin_inff();
+        uint32_t idx = 0xFFFFFFFFu;
+        const uint32_t b = bb[vg] / 4, qw = bb[vg] % 4;
+#pragma unroll
+        for (uint32_t j = 0; j < 2; ++j) {
+          const uint32_t c = 16 * (b * 2 + j) + 4 * qw + q;
+          if (c < K) {
+            float cv[D];
+            load_padded<D>(lcb + c * 8, cv);
+            const float d2 = exact_l2sq<D>(x[vg], cv);
+            if (d2 < best) {  // c rises with j: the first of this lane's ties stays
+              best = d2;
+              idx = c;
+            }
+          }
+        }
+        screen_lex_min<16>(best, idx);
+        screen_lex_min<32>(best, idx);
+        if (q == 0 && r < tile1) {
+          codes[(uint64_t)m * n + r] = (uint16_t)idx;
+          e[(uint64_t)m * n + r] = best;
+          atomicAdd(&s_hist[idx], 1u);
+        }
+      } else if (q == 0 && r < tile1) {
+        s_list[atomicAdd(&s_cnt, 1u)] = (uint32_t)r;  // at most kSortTile rows
+      }
+    }
+  }
+  __syncthreads();
+  uint32_t* out = hist + ((uint64_t)m * T + blockIdx.x) * K;
+  if (t < K) out[t] = s_hist[t];
+  const uint32_t cnt = s_cnt;
+  if (cnt == 0) return;
+  if (t == 0) s_base = atomicAdd(&defer_count[m], cnt);
+  __syncthreads();
+  uint32_t* lst = defer + (uint64_t)m * n + s_base;
+  for (uint32_t i = t; i < cnt; i += blockDim.x) lst[i] = s_list[i];
+}
+
+}  // namespace tacgpu

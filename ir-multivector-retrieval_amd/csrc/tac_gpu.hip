@@ -20,6 +20,7 @@
 #include "pq_kernels.hpp"
 #include "cand_kernels.hpp"
 #include "cell_kernels.hpp"
+#include "screen_kernels.hpp"
 #include "kmeanspp.hpp"
 #include "storage_kernels.hpp"
 #include "query_kernels.hpp"
@@ -468,6 +469,15 @@ inline uint32_t cand_hist_tiles(uint32_t K, uint32_t DP, uint32_t cells, uint32_
   return tiles;
 }
 inline uint32_t nbr_threads(uint32_t K) { return K > 256 ? 256u : (uint32_t)kWave; }
+// The full search at sub-dimensions 5-8 takes its first pass on the matrix
+// cores (screen_kernels.hpp) up to K = 256: on 1.52M corpus rows at m8 K256
+// the Lloyd loop took 15.7 ms against 19.8 with the vector-unit search.
+// TAC_GPU_SCREEN=0 keeps the vector-unit search (for the tests that compare
+// the two).
+inline bool screen_wanted(uint32_t K) {
+  const char *v = getenv("TAC_GPU_SCREEN");
+  return K <= kScreenMaxK && !(v && v[0] == '0');
+}
 // The deferred-vector kernels can give each vector four lanes from K = 128
 // on, where the blocks of kPruneBlock codewords split evenly over four lanes
 // (TAC_GPU_LIST_LANES=1 keeps one lane per vector, for the tests that
@@ -509,6 +519,26 @@ struct Launch {
     KT("assign_kernel<%d, %d>", D, VPT);
     assign_kernel<D, VPT><<<grid, kBlock, lds, s>>>(xs, cb, codes, e, done, n, K, rescans);
     KT_END();
+  }
+  // The full search with its first pass on the matrix cores (sub-dimensions
+  // 5-8, K <= 256; screen_kernels.hpp): one block per sort tile settles the
+  // vectors the screen separates and counts them into hist[M][T][K], the
+  // others take the pruned exact search of the deferred list.
+  static int assign_screen(const float *xs, const float *cb, uint16_t *codes, float *e,
+                           uint32_t *defer, uint32_t *defer_count, const uint32_t *done,
+                           uint64_t n, uint32_t M, uint32_t K, uint32_t *hist, uint32_t T,
+                           unsigned long long *rescans, hipStream_t s) {
+    if constexpr (D >= 5 && D <= 8) {
+      HIP_TRY(hipMemsetAsync(defer_count, 0, M * sizeof(uint32_t), s));
+      KT("assign_screen_kernel<%d>", D);
+      assign_screen_kernel<D><<<dim3(T, M), 256, 0, s>>>(xs, cb, codes, e, defer, defer_count,
+                                                         done, n, K, hist, T);
+      KT_END();
+      assign_deferred(xs, cb, codes, e, defer, defer_count, done, n, M, K, hist, T, rescans, s);
+      return TAC_OK;
+    } else {
+      return TAC_ERR_INVALID_ARGUMENT;  // no matrix-core screen outside 5-8 sub-dimensions
+    }
   }
   // Candidate-set assignment (cand_kernels.hpp): neighbour tables of the
   // current codebooks, the assignment from grid anchors (GRID, the first
@@ -557,6 +587,16 @@ struct Launch {
         xs, cb, nbr, anchors, grid, codes, e, nullptr, slice, defer, defer_count, done, n, 0, M, K,
         L, (uint32_t)chunk, (uint32_t)nblk, G, cells, hist, T);
     KT_END();
+    assign_deferred(xs, cb, codes, e, defer, defer_count, done, n, M, K, hist, T, rescans, s);
+    return TAC_OK;
+  }
+  // The pruned exact search of the deferred vectors defer[m][..], which also
+  // counts their codes into hist[M][T][K].
+  static void assign_deferred(const float *xs, const float *cb, uint16_t *codes, float *e,
+                              const uint32_t *defer, const uint32_t *defer_count,
+                              const uint32_t *done, uint64_t n, uint32_t M, uint32_t K,
+                              uint32_t *hist, uint32_t T, unsigned long long *rescans,
+                              hipStream_t s) {
     const uint32_t Kp = (K + kPruneBlock - 1) / kPruneBlock * kPruneBlock;
     const size_t lds = (size_t)Kp * (Pad<D>::value + 1) * sizeof(float) + 2 * sizeof(uint32_t);
     // About 2% of the vectors are deferred, each a serial chain over all K
@@ -580,7 +620,6 @@ struct Launch {
           g_profile ? rescans + 1 : nullptr, hist, T, 0u);
     }
     KT_END();
-    return TAC_OK;
   }
   // Candidate-set encode: neighbour rows and grid anchors of the codebooks,
   // the candidate pass over token-major input, then the reference scan of
@@ -1007,9 +1046,13 @@ int train_core(DeviceState &ds, hipStream_t s, const float *d_x, uint64_t n, uin
                        n <= 0xFFFFFFFFull;
   const bool cand = cand_ok && max_iters > 1;
   const bool cand_first = cand_ok && n >= 16384;
+  // The full search's iterations take the matrix-core screen where it applies.
+  const bool screen = D >= 5 && D <= 8 && screen_wanted(K) && n <= 0xFFFFFFFFull;
   if ((cand || cand_first) &&
-      ((st = ensure(ds, ds.cand_nbr, (size_t)M * K * cand_row_len(Lc) * sizeof(uint32_t))) ||
-       (st = ensure(ds, ds.cand_defer, (size_t)2 * M * n * sizeof(uint32_t))) ||
+      (st = ensure(ds, ds.cand_nbr, (size_t)M * K * cand_row_len(Lc) * sizeof(uint32_t))))
+    return st;
+  if ((cand || cand_first || screen) &&
+      ((st = ensure(ds, ds.cand_defer, (size_t)2 * M * n * sizeof(uint32_t))) ||
        (st = ensure(ds, ds.cand_count, (size_t)M * sizeof(uint32_t)))))
     return st;
   if (cand_first && ((st = ensure(ds, ds.cand_anchor,
@@ -1093,7 +1136,8 @@ int train_core(DeviceState &ds, hipStream_t s, const float *d_x, uint64_t n, uin
     explicit StreamScope(hipStream_t hs) { tl_kt_stream = hs; }
     ~StreamScope() { tl_kt_stream = nullptr; }
   };
-  uint32_t *slices_all = (cand || cand_first) ? as<uint32_t>(ds.cand_defer) : nullptr;
+  uint32_t *slices_all =
+      (cand || cand_first || screen) ? as<uint32_t>(ds.cand_defer) : nullptr;
 
   // One Lloyd iteration t of the subspaces m0 .. m0+Mh-1 on stream hs.
   auto iterate = [&](const SubspaceGroup &h, uint32_t t) -> int {
@@ -1123,9 +1167,10 @@ int train_core(DeviceState &ds, hipStream_t s, const float *d_x, uint64_t n, uin
         return st;
       HIP_TRY(hipEventRecord(a, hs));
     }
-    // The candidate passes count the sort tiles themselves; the full search
-    // leaves that to hist_kernel.
+    // The candidate passes and the screened full search count the sort
+    // tiles themselves; the vector-unit full search leaves that to hist_kernel.
     const bool cand_now = (cand && t > 0) || (cand_first && t == 0);
+    const bool screen_now = !cand_now && screen;
     if (cand_now) {
       uint32_t *nbr_h = as<uint32_t>(ds.cand_nbr) + (size_t)m0 * K * cand_row_len(Lc);
       uint32_t *slices_h = slices_all + (size_t)m0 * n;
@@ -1150,12 +1195,19 @@ int train_core(DeviceState &ds, hipStream_t s, const float *d_x, uint64_t n, uin
       }
       if (st) return st;
       LAUNCH_TRY("assign_cand kernels");
+    } else if (screen_now) {
+      uint32_t *defer_h = slices_all + (size_t)M * n + (size_t)m0 * n;
+      uint32_t *count_h = as<uint32_t>(ds.cand_count) + m0;
+      DISPATCH_D_ST(D, assign_screen(xs_h, cb_h, codes_h, e_h, defer_h, count_h, done_h, n, Mh, K,
+                                     hist_h, T, rescans, hs));
+      if (st) return st;
+      LAUNCH_TRY("assign_screen kernels");
     } else {
       DISPATCH_D(D, assign(xs_h, cb_h, codes_h, e_h, done_h, n, Mh, K, rescans, hs));
       LAUNCH_TRY("assign_kernel");
     }
     if (timed) HIP_TRY(hipEventRecord(b, hs));
-    if (!cand_now) {
+    if (!cand_now && !screen_now) {
       KT("hist_kernel");
       hist_kernel<<<dim3(T, Mh), kBlock, hist_lds, hs>>>(codes_h, hist_h, done_h, n, K, T);
       KT_END();
