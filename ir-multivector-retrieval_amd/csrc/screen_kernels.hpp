@@ -4,20 +4,22 @@
 //
 // Screen.  For a vector x and codeword c (dimensions past D are 0), the
 // search ranks codewords by s(c) = ||c||^2 - 2 x.c.  Here s comes from one
-// v_mfma_f32_16x16x32_bf16 per 16 codewords x 16 vectors, over 32 terms:
-//   A = [-2 c_hi, -2 c_lo, -2 c_hi, n_hi, n_lo, 0 ...],  B = [x_hi, x_hi, x_lo, 1, 1, 0 ...]
-// with v_hi = bf16(v), v_lo = bf16(v - v_hi) (round to nearest even) and
-// n = fl(sum_d c_d^2).  For a finite v, |v - v_hi| <= 2^-8 |v| + 2^-126 and
-// |v - v_hi - v_lo| <= 2^-16 |v| + 2^-125 (the absolute terms cover
-// subnormal or flushed pieces), so per dimension, with a = -2 c_d, the three
-// products miss a x_d by at most 3.02 * 2^-16 |a| |x_d| + 2^-123 (|a| + |x_d|);
-// n_hi + n_lo is within (2^-16 + gamma_8) ||c||^2 + 2^-124 of ||c||^2; the
-// bf16 products are exact in fp32 but for underflow (2^-126 each); and the
-// matrix core adds the 32 terms in fp32 in some order (gamma_31 of their
-// absolute sum).  Altogether
-//   |s~ - s| <= 2^-14 (||c||^2 + 2 ||x|| ||c||) + 2^-121 (2 ||c|| + ||x||) + 2^-120,
-// and the kernel uses four times that with cmax^2 = max_c fl(||c||^2) in
-// place of ||c||^2.  It needs fl(||x||^2) <= 2^120 and cmax^2 <= 2^120
+// v_mfma_f32_16x16x32_bf16 per 16 codewords x 16 vectors, over 32 products
+// added to the accumulator input n = fl(sum_d c_d^2):
+//   A = [a_hi, a_lo, a_hi, a_lo],  B = [x_hi, x_hi, x_lo, x_lo]  (8 slots each)
+// with a = -2 c (exact), v_hi = bf16(v), v_lo = bf16(v - v_hi) (round to
+// nearest even), so the products sum to (a_hi + a_lo) . (x_hi + x_lo).  For a
+// finite v, |v - v_hi - v_lo| <= 2^-16 |v| + 2^-125 (the absolute term covers
+// subnormal or flushed pieces), so per dimension the products miss a x_d by
+// at most 2.0001 * 2^-16 |a| |x_d| + 2^-124.9 (|a| + |x_d|); n is within
+// gamma_8 ||c||^2 of ||c||^2; the bf16 products are exact in fp32 but for
+// underflow (2^-126 each); and the matrix core adds the 33 terms in fp32 in
+// some order (gamma_32 of their absolute sum, at most
+// 2^-19 (2.032 ||x|| ||c|| + ||c||^2), plus 2^-126 per addition if partial
+// sums flush).  Altogether
+//   |s~ - s| <= 2^-14 (1.07 ||x|| ||c|| + 0.04 ||c||^2) + 2^-123 (2 ||c|| + ||x||) + 2^-120,
+// and the kernel uses twice that with cmax^2 = max_c fl(||c||^2) in place of
+// ||c||^2.  It needs fl(||x||^2) <= 2^120 and cmax^2 <= 2^120
 // (false for a NaN or infinite component): every component is then below
 // 2^60 (times 1 + 4u), so no product or partial sum overflows.  A codebook
 // past that sends every vector to the deferred list below, a vector past it
@@ -56,29 +58,13 @@ constexpr uint32_t kScreenMaxK = 256;     // codewords in the kernel's LDS table
 constexpr uint32_t kScreenVecGroups = 4;  // 16-vector groups per wave pass
 constexpr float kScreenTame = 1.329227995784916e36f;  // 2^120
 
-// Minimum, median and maximum without the canonicalising moves IEEE mode adds
-// to fminf / fmaxf; the screen's operands are never NaN where the results
-// count (tame vectors and codebooks, +inf padding).
-__device__ __forceinline__ float min3_raw(float a, float b, float c) {
-  float r;
-  asm("v_min3_f32 %0, %1, %2, %3" : "=v"(r) : "v"(a), "v"(b), "v"(c));
-  return r;
-}
-__device__ __forceinline__ float med3_raw(float a, float b, float c) {
-  float r;
-  asm("v_med3_f32 %0, %1, %2, %3" : "=v"(r) : "v"(a), "v"(b), "v"(c));
-  return r;
-}
-__device__ __forceinline__ float min_raw(float a, float b) {
-  float r;
-  asm("v_min_f32 %0, %1, %2" : "=v"(r) : "v"(a), "v"(b));
-  return r;
-}
-__device__ __forceinline__ float max_raw(float a, float b) {
-  float r;
-  asm("v_max_f32 %0, %1, %2" : "=v"(r) : "v"(a), "v"(b));
-  return r;
-}
+// Minimum and maximum in the IEEE 754-2019 sense (v_minimum3_f32 /
+// v_maximum3_f32: no canonicalising moves, which fminf / fmaxf add in IEEE
+// mode); the screen's operands are never NaN where the results count (tame
+// vectors and codebooks, +inf padding).
+__device__ __forceinline__ float min2f(float a, float b) { return __builtin_elementwise_minimum(a, b); }
+__device__ __forceinline__ float max2f(float a, float b) { return __builtin_elementwise_maximum(a, b); }
+__device__ __forceinline__ float min3f(float a, float b, float c) { return min2f(min2f(a, b), c); }
 
 // The values of lanes l and l ^ 16 (R = 16) or l and l ^ 32 (R = 32), as a
 // pair that is the same in both lanes (v_permlane16_swap / v_permlane32_swap
@@ -106,9 +92,9 @@ __device__ __forceinline__ void screen_merge(float& b1, float& b2, uint32_t& bb)
   pair_of<R>(bb, db, sb);
   const float D1 = __uint_as_float(d1), S1 = __uint_as_float(s1);
   // second smallest of {D1, D2, S1, S2} with D1 <= D2, S1 <= S2
-  b2 = min3_raw(max_raw(D1, S1), __uint_as_float(d2), __uint_as_float(s2));
+  b2 = min3f(max2f(D1, S1), __uint_as_float(d2), __uint_as_float(s2));
   bb = S1 < D1 ? sb : db;  // ties leave b2 == b1: no gap
-  b1 = min_raw(D1, S1);
+  b1 = min2f(D1, S1);
 }
 
 // (d, c) <- the smaller of the (distance, index) pairs of lanes l and l ^ R.
@@ -141,6 +127,7 @@ __global__ __launch_bounds__(256) void assign_screen_kernel(
   static_assert(kSortTile % (4 * 16 * kScreenVecGroups) == 0, "whole wave passes per tile");
   constexpr uint32_t VG = kScreenVecGroups;
   __shared__ bf16x8 lA[kScreenMaxK * 4];  // [c][q]: the codeword pieces
+  __shared__ __attribute__((aligned(16))) float lnorm[kScreenMaxK];  // +inf past K
   __shared__ __attribute__((aligned(16))) float lcb[kScreenMaxK * 8];  // fp32 codewords
   __shared__ uint32_t s_hist[kScreenMaxK];
   __shared__ uint32_t s_list[kSortTile];  // the tile's deferred rows
@@ -149,7 +136,9 @@ __global__ __launch_bounds__(256) void assign_screen_kernel(
   if (done[m]) return;
   const uint32_t t = threadIdx.x, lane = t % kWave, w = t / kWave;
   const uint32_t p = lane % 16, q = lane / 16;
-  const uint32_t ngroups = (K + 15u) / 16u;
+  // codeword groups of 16, rounded up to whole blocks of two: the tables
+  // hold all kScreenMaxK entries, padding (screen +inf) past K
+  const uint32_t ngroups = (K + 31u) / 32u * 2u;
   if (t == 0) {
     s_max = 0;
     s_cnt = 0;
@@ -165,23 +154,20 @@ __global__ __launch_bounds__(256) void assign_screen_kernel(
     float n2 = v[0] * v[0];
 #pragma unroll
     for (int d = 1; d < D; ++d) n2 = n2 + v[d] * v[d];
-    bf16x8 ch, cl, nn;
+    bf16x8 ch, cl;
 #pragma unroll
     for (int d = 0; d < 8; ++d) {
       const float a = -2.0f * v[d];  // exact
       const __bf16 hi = (__bf16)a;
       ch[d] = hi;
       cl[d] = (__bf16)(a - (float)hi);
-      nn[d] = (__bf16)0.0f;
       lcb[c * 8 + d] = v[d];
     }
-    const __bf16 nh = (__bf16)n2;
-    nn[0] = c < K ? nh : (__bf16)__builtin_inff();  // padding: screen +inf
-    nn[1] = c < K ? (__bf16)(n2 - (float)nh) : (__bf16)0.0f;
+    lnorm[c] = c < K ? n2 : __builtin_inff();  // padding: screen +inf
     lA[c * 4 + 0] = ch;
     lA[c * 4 + 1] = cl;
     lA[c * 4 + 2] = ch;
-    lA[c * 4 + 3] = nn;
+    lA[c * 4 + 3] = cl;
     // the largest norm's bits (norms are non-negative or NaN, and a NaN's
     // bits sort above +inf's)
     uint32_t mx = c < K ? __float_as_uint(n2) : 0u;
@@ -199,16 +185,18 @@ __global__ __launch_bounds__(256) void assign_screen_kernel(
   const float cmax = sqrtf(cmax2);
   constexpr float u = 5.9604644775390625e-8f;  // 2^-24
   constexpr float gR = (float)(D + 2) * u / (1.0f - (float)(D + 2) * u);
-  constexpr float k12 = 2.44140625e-4f;           // 2^-12
+  // twice the bound: 2^-13 (1.07 nx cmax + 0.04 cmax^2) + 2^-122 (2 cmax + nx) + 2^-119
+  constexpr float kxc = 1.31e-4f;                 // >= 1.07 * 2^-13
+  constexpr float kcc = 4.9e-6f;                  // >= 0.04 * 2^-13
+  constexpr float k122 = 1.880790961315660e-37f;  // 2^-122
   constexpr float k119 = 1.504632769052528e-36f;  // 2^-119
-  constexpr float k118 = 3.009265538105056e-36f;  // 2^-118
   const float* xm = xs + (uint64_t)m * n * 8;
   const uint64_t tile0 = (uint64_t)blockIdx.x * kSortTile;
   const uint64_t tile1 = tile0 + kSortTile < n ? tile0 + kSortTile : n;
   const bf16x8* arow = lA + p * 4 + q;  // + 64 per codeword group
-  const floatx4 zero = {0.0f, 0.0f, 0.0f, 0.0f};
+  const floatx4* nrow = reinterpret_cast<const floatx4*>(lnorm) + q;  // + 4 per group
   for (uint64_t row0 = tile0 + w * (16 * VG); row0 < tile1; row0 += 4 * 16 * VG) {
-    // B operands: vector row0 + 16 vg + p, pieces q (x_hi, x_hi, x_lo, ones);
+    // B operands: vector row0 + 16 vg + p, pieces q (x_hi, x_hi, x_lo, x_lo);
     // rows past the tile repeat its last row and are not written.
     bf16x8 X[VG];
     float x[VG][D], x2[VG];
@@ -225,15 +213,14 @@ __global__ __launch_bounds__(256) void assign_screen_kernel(
 #pragma unroll
       for (int d = 1; d < D; ++d) s2 = s2 + xv[d] * xv[d];
       x2[vg] = s2;
-      bf16x8 hi, lo, one;
+      bf16x8 hi, lo;
 #pragma unroll
       for (int d = 0; d < 8; ++d) {
         const float xd = d < D ? xv[d] : 0.0f;
         hi[d] = (__bf16)xd;
         lo[d] = (__bf16)(xd - (float)hi[d]);
-        one[d] = (__bf16)(d < 2 ? 1.0f : 0.0f);
       }
-      X[vg] = q == 3 ? one : q == 2 ? lo : hi;
+      X[vg] = q >= 2 ? lo : hi;
     }
     // First pass: block minima over this lane's codewords (4 per group, two
     // groups per block), the two smallest of them per vector; blocks are
@@ -248,18 +235,20 @@ __global__ __launch_bounds__(256) void assign_screen_kernel(
     }
     for (uint32_t g = 0; g < ngroups; g += 2) {
       const bf16x8 A0 = arow[g * 64];
-      const bf16x8 A1 = g + 1 < ngroups ? arow[(g + 1) * 64] : A0;  // A0 again: same minimum
+      const bf16x8 A1 = arow[(g + 1) * 64];
+      const floatx4 N0 = nrow[g * 4];
+      const floatx4 N1 = nrow[(g + 1) * 4];
       const uint32_t blk = (g / 2) * 4 + q;
 #pragma unroll
       for (uint32_t vg = 0; vg < VG; ++vg) {
-        const floatx4 c0 = __builtin_amdgcn_mfma_f32_16x16x32_bf16(A0, X[vg], zero, 0, 0, 0);
-        const floatx4 c1 = __builtin_amdgcn_mfma_f32_16x16x32_bf16(A1, X[vg], zero, 0, 0, 0);
-        const float v0 = min3_raw(c0[0], c0[1], c0[2]);
-        const float v1 = min3_raw(c1[0], c1[1], c1[2]);
-        const float v = min3_raw(min_raw(v0, c0[3]), v1, c1[3]);
-        b2[vg] = med3_raw(b1[vg], b2[vg], v);
+        const floatx4 c0 = __builtin_amdgcn_mfma_f32_16x16x32_bf16(A0, X[vg], N0, 0, 0, 0);
+        const floatx4 c1 = __builtin_amdgcn_mfma_f32_16x16x32_bf16(A1, X[vg], N1, 0, 0, 0);
+        const float v0 = min3f(c0[0], c0[1], c0[2]);
+        const float v1 = min3f(c1[0], c1[1], c1[2]);
+        const float v = min3f(min2f(v0, c0[3]), v1, c1[3]);
+        b2[vg] = min2f(b2[vg], max2f(b1[vg], v));  // second smallest (b1 <= b2)
         bb[vg] = v < b1[vg] ? blk : bb[vg];
-        b1[vg] = min_raw(b1[vg], v);
+        b1[vg] = min2f(b1[vg], v);
       }
     }
 #pragma unroll
@@ -273,7 +262,7 @@ __global__ __launch_bounds__(256) void assign_screen_kernel(
     for (uint32_t vg = 0; vg < VG; ++vg) {
       const uint64_t r = row0 + 16 * vg + p;
       const float nx = sqrtf(x2[vg]);
-      const float ea = k12 * (cmax2 + 2.0f * nx * cmax) + k119 * (2.0f * cmax + nx) + k118;
+      const float ea = kxc * nx * cmax + kcc * cmax2 + k122 * (2.0f * cmax + nx) + k119;
       float thr = 2.0f * ea * (1.0f + gR) +
                   gR * (fabsf(b2[vg] + x2[vg]) + fabsf(b1[vg] + x2[vg]));
       thr = 2.0f * thr + 1e-30f;
