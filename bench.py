@@ -783,6 +783,15 @@ def train_encode_timing(device, dx, n, dim, m, ksub, dinit, steps, warmup):
     return statistics.median(tr), statistics.median(en), p
 
 
+def search_kind(dsub: int, ksub: int, encode: bool) -> str:
+    """The first pass the library picks (cand_wanted / screen_wanted in
+    tac_gpu.hip): candidate sets up to dsub 6 in the Lloyd loop and dsub 4 in
+    encode (and beyond K = 256), the matrix-core screen from there."""
+    if ksub > 256 or dsub <= (4 if encode else 6):
+        return "candidate sets"
+    return "matrix-core screen"
+
+
 def shape_sweep(device, dx, x, steps: int):
     """(m32, dsub 2), (m8, dsub 8) and (m16, ksub 1024) on the resident
     corpus: 20 Lloyd iterations from seeded-shuffle codebooks, then encode."""
@@ -800,7 +809,8 @@ def shape_sweep(device, dx, x, steps: int):
         rows[name] = {
             "m": w.m, "dsub": w.dim // w.m, "ksub": w.ksub, "lloyd_iters": 20,
             "train_s": round(t_tr, 5),
-            "assign": "candidate sets",
+            "assign": search_kind(w.dim // w.m, w.ksub, False),
+            "encode_search": search_kind(w.dim // w.m, w.ksub, True),
             "encode_s": round(t_en, 6), "encode_mvec_per_s": round(w.n / t_en / 1e6, 1),
             "encode_stage_ms": round(enc_ms, 4),
             "encode_hbm_frac": round(ebytes / (enc_ms * 1e-3) / 1e9 / PEAK_HBM_GBS, 4),

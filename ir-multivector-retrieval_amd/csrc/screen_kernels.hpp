@@ -109,20 +109,27 @@ __device__ __forceinline__ void screen_lex_min(float& d, uint32_t& c) {
   c = s_wins ? sc : dc;
 }
 
-// Lloyd assignment for D in 5..8 (vec.argmin: first index); xs = [M][n][8]
-// records, one block of 4 waves per sort tile of kSortTile rows
-// (blockIdx.x) of a subspace (blockIdx.y), 64 vectors per wave pass; K <=
-// kScreenMaxK = blockDim.x.  codes[m][i], e[m][i] = reference distance for
-// the vectors the screen settles; the others go to defer[m][..]
-// (defer_count[m] must be zero at the launch, and assign_list_kernel must
-// follow).  hist[m][tile][c] = the settled vectors of the tile with code c
-// (assign_list_kernel adds the deferred ones).
-template <int D>
-__global__ __launch_bounds__(256) void assign_screen_kernel(
-    const float* __restrict__ xs, const float* __restrict__ cb, uint16_t* __restrict__ codes,
+// The full search for D in 5..8 and K <= kScreenMaxK = blockDim.x, one
+// block of 4 waves per (tile of kSortTile rows, subspace m), 64 vectors per
+// wave pass.  The vectors the screen settles get their code (the first index
+// of the minimum: vec.argmin's and PQ.encode's scan agree on finite
+// distances); the others go to defer[m][..] (defer_count[m] must be zero at
+// the launch, and the deferred-list kernel of the same semantics must
+// follow).
+//  - Lloyd assignment (ENCODE false; CodeT uint16_t): x = xs [M][n][8]
+//    records, blockIdx.x = tile, blockIdx.y = m; codes[m][i], e[m][i] =
+//    reference distance; hist[m][tile][c] = the settled vectors of the tile
+//    with code c (assign_list_kernel adds the deferred ones).
+//  - Encode (ENCODE true): x = token-major rows [n][dim], sub-vector m at
+//    m * D; the M blocks of a tile are adjacent in an XCD's share of the
+//    grid (xcd_contiguous), so a row crosses HBM once; codes[i * M + m];
+//    encode_list_kernel follows.
+template <int D, bool ENCODE, typename CodeT>
+__global__ __launch_bounds__(256) void screen_kernel(
+    const float* __restrict__ x_in, const float* __restrict__ cb, CodeT* __restrict__ codes,
     float* __restrict__ e, uint32_t* __restrict__ defer, uint32_t* __restrict__ defer_count,
-    const uint32_t* __restrict__ done, uint64_t n, uint32_t K, uint32_t* __restrict__ hist,
-    uint32_t T) {
+    const uint32_t* __restrict__ done, uint64_t n, uint32_t dim, uint32_t M, uint32_t K,
+    uint32_t* __restrict__ hist, uint32_t T) {
   static_assert(D >= 5 && D <= 8, "records of 8 floats");
   static_assert(kSortTile % (4 * 16 * kScreenVecGroups) == 0, "whole wave passes per tile");
   constexpr uint32_t VG = kScreenVecGroups;
@@ -132,8 +139,17 @@ __global__ __launch_bounds__(256) void assign_screen_kernel(
   __shared__ uint32_t s_hist[kScreenMaxK];
   __shared__ uint32_t s_list[kSortTile];  // the tile's deferred rows
   __shared__ uint32_t s_max, s_cnt, s_base;
-  const uint32_t m = blockIdx.y;
-  if (done[m]) return;
+  uint32_t m, tile;
+  if constexpr (ENCODE) {
+    const uint32_t logical = xcd_contiguous(blockIdx.x, gridDim.x);
+    if (logical >= T * M) return;  // grid padding to a multiple of 8
+    tile = logical / M;
+    m = logical % M;
+  } else {
+    tile = blockIdx.x;
+    m = blockIdx.y;
+    if (done[m]) return;
+  }
   const uint32_t t = threadIdx.x, lane = t % kWave, w = t / kWave;
   const uint32_t p = lane % 16, q = lane / 16;
   // codeword groups of 16, rounded up to whole blocks of two: the tables
@@ -143,7 +159,7 @@ __global__ __launch_bounds__(256) void assign_screen_kernel(
     s_max = 0;
     s_cnt = 0;
   }
-  if (t < K) s_hist[t] = 0;
+  if (!ENCODE && t < K) s_hist[t] = 0;
   {
     // The pieces of codeword c = t, padding past K.
     const uint32_t c = t;
@@ -190,8 +206,10 @@ __global__ __launch_bounds__(256) void assign_screen_kernel(
   constexpr float kcc = 4.9e-6f;                  // >= 0.04 * 2^-13
   constexpr float k122 = 1.880790961315660e-37f;  // 2^-122
   constexpr float k119 = 1.504632769052528e-36f;  // 2^-119
-  const float* xm = xs + (uint64_t)m * n * 8;
-  const uint64_t tile0 = (uint64_t)blockIdx.x * kSortTile;
+  const float* xm = ENCODE ? x_in + (uint64_t)m * D : x_in + (uint64_t)m * n * 8;
+  const bool vec4 = !ENCODE || (D == 8 && dim % 4 == 0 &&
+                                 ((uintptr_t)x_in & 15u) == 0);  // 16-byte aligned rows
+  const uint64_t tile0 = (uint64_t)tile * kSortTile;
   const uint64_t tile1 = tile0 + kSortTile < n ? tile0 + kSortTile : n;
   const bf16x8* arow = lA + p * 4 + q;  // + 64 per codeword group
   const floatx4* nrow = reinterpret_cast<const floatx4*>(lnorm) + q;  // + 4 per group
@@ -204,14 +222,23 @@ __global__ __launch_bounds__(256) void assign_screen_kernel(
     for (uint32_t vg = 0; vg < VG; ++vg) {
       const uint64_t r = row0 + 16 * vg + p;
       const uint64_t rr = r < tile1 ? r : tile1 - 1;
-      const float4 a0 = *reinterpret_cast<const float4*>(xm + rr * 8);
-      const float4 a1 = *reinterpret_cast<const float4*>(xm + rr * 8 + 4);
-      const float xv[8] = {a0.x, a0.y, a0.z, a0.w, a1.x, a1.y, a1.z, a1.w};
+      const float* src = xm + rr * (ENCODE ? (uint64_t)dim : 8u);
+      float xv[8];
+      if (vec4) {
+        const float4 a0 = *reinterpret_cast<const float4*>(src);
+        const float4 a1 = *reinterpret_cast<const float4*>(src + 4);
+        xv[0] = a0.x; xv[1] = a0.y; xv[2] = a0.z; xv[3] = a0.w;
+        xv[4] = a1.x; xv[5] = a1.y; xv[6] = a1.z; xv[7] = a1.w;
+      } else {
+#pragma unroll
+        for (int d = 0; d < 8; ++d) xv[d] = d < D ? src[d] : 0.0f;
+      }
 #pragma unroll
       for (int d = 0; d < D; ++d) x[vg][d] = xv[d];
+      // ||x||^2 for the bound and the tameness test (any rounding order does)
       float s2 = xv[0] * xv[0];
 #pragma unroll
-      for (int d = 1; d < D; ++d) s2 = s2 + xv[d] * xv[d];
+      for (int d = 1; d < D; ++d) s2 = __builtin_fmaf(xv[d], xv[d], s2);
       x2[vg] = s2;
       bf16x8 hi, lo;
 #pragma unroll
@@ -290,9 +317,13 @@ __global__ __launch_bounds__(256) void assign_screen_kernel(
         screen_lex_min<16>(best, idx);
         screen_lex_min<32>(best, idx);
         if (q == 0 && r < tile1) {
-          codes[(uint64_t)m * n + r] = (uint16_t)idx;
-          e[(uint64_t)m * n + r] = best;
-          atomicAdd(&s_hist[idx], 1u);
+          if constexpr (ENCODE) {
+            codes[r * M + m] = (CodeT)idx;
+          } else {
+            codes[(uint64_t)m * n + r] = (CodeT)idx;
+            e[(uint64_t)m * n + r] = best;
+            atomicAdd(&s_hist[idx], 1u);
+          }
         }
       } else if (q == 0 && r < tile1) {
         s_list[atomicAdd(&s_cnt, 1u)] = (uint32_t)r;  // at most kSortTile rows
@@ -300,8 +331,10 @@ __global__ __launch_bounds__(256) void assign_screen_kernel(
     }
   }
   __syncthreads();
-  uint32_t* out = hist + ((uint64_t)m * T + blockIdx.x) * K;
-  if (t < K) out[t] = s_hist[t];
+  if constexpr (!ENCODE) {
+    uint32_t* out = hist + ((uint64_t)m * T + tile) * K;
+    if (t < K) out[t] = s_hist[t];
+  }
   const uint32_t cnt = s_cnt;
   if (cnt == 0) return;
   if (t == 0) s_base = atomicAdd(&defer_count[m], cnt);

@@ -530,9 +530,9 @@ struct Launch {
                            unsigned long long *rescans, hipStream_t s) {
     if constexpr (D >= 5 && D <= 8) {
       HIP_TRY(hipMemsetAsync(defer_count, 0, M * sizeof(uint32_t), s));
-      KT("assign_screen_kernel<%d>", D);
-      assign_screen_kernel<D><<<dim3(T, M), 256, 0, s>>>(xs, cb, codes, e, defer, defer_count,
-                                                         done, n, K, hist, T);
+      KT("screen_kernel<%d, false, unsigned short>", D);
+      screen_kernel<D, false, uint16_t><<<dim3(T, M), 256, 0, s>>>(
+          xs, cb, codes, e, defer, defer_count, done, n, 0, M, K, hist, T);
       KT_END();
       assign_deferred(xs, cb, codes, e, defer, defer_count, done, n, M, K, hist, T, rescans, s);
       return TAC_OK;
@@ -620,6 +620,31 @@ struct Launch {
           g_profile ? rescans + 1 : nullptr, hist, T, 0u);
     }
     KT_END();
+  }
+  // Encode through the matrix-core screen (sub-dimensions 5-8, K <= 256;
+  // screen_kernels.hpp), then the deferred rows' pruned exact search with
+  // PQ.encode's scan; defer holds M * n words.
+  template <typename CodeT>
+  static int encode_screen(const float *x, const float *cb, CodeT *codes, uint32_t *defer,
+                           uint32_t *defer_count, uint64_t n, uint32_t dim, uint32_t M,
+                           uint32_t K, unsigned long long *rescans, unsigned long long *stats,
+                           hipStream_t s) {
+    if constexpr (D >= 5 && D <= 8) {
+      const uint64_t tiles = (n + kSortTile - 1) / kSortTile;
+      const uint64_t total = tiles * M;
+      if (total > 0xFFFFFFF0ull) return TAC_ERR_UNSUPPORTED;
+      HIP_TRY(hipMemsetAsync(defer_count, 0, M * sizeof(uint32_t), s));
+      const uint32_t blocks = (uint32_t)(8 * ((total + 7) / 8));
+      KT("screen_kernel<%d, true, %s>", D, code_name<CodeT>());
+      screen_kernel<D, true, CodeT><<<blocks, 256, 0, s>>>(x, cb, codes, nullptr, defer,
+                                                           defer_count, nullptr, n, dim, M, K,
+                                                           nullptr, (uint32_t)tiles);
+      KT_END();
+      return encode_deferred<CodeT>(x, cb, codes, defer, defer_count, n, dim, M, K, rescans,
+                                    stats, s);
+    } else {
+      return TAC_ERR_INVALID_ARGUMENT;  // no matrix-core screen outside 5-8 sub-dimensions
+    }
   }
   // Candidate-set encode: neighbour rows and grid anchors of the codebooks,
   // the candidate pass over token-major input, then the reference scan of
@@ -1485,6 +1510,14 @@ int encode_core(DeviceState &ds, hipStream_t s, const float *d_x, uint64_t n, ui
                                              slices + (size_t)M * n, as<uint32_t>(ds.cand_count),
                                              n, dim, M, K, L, rescans, s));
     }
+  } else if (D >= 5 && D <= 8 && screen_wanted(K) && n <= 0xFFFFFFFFull) {
+    if ((st = ensure(ds, ds.cand_defer, (size_t)2 * M * n * sizeof(uint32_t))) ||
+        (st = ensure(ds, ds.cand_count, (size_t)M * sizeof(uint32_t))))
+      return st;
+    DISPATCH_D_ST(D, encode_screen<uint8_t>(d_x, d_cb, (uint8_t *)d_codes,
+                                            as<uint32_t>(ds.cand_defer) + (size_t)M * n,
+                                            as<uint32_t>(ds.cand_count), n, dim, M, K, rescans,
+                                            g_profile ? rescans + 1 : nullptr, s));
   } else if (K <= 256) {
     DISPATCH_D_ST(D, encode<uint8_t>(d_x, d_cb, (uint8_t *)d_codes, n, dim, M, K, rescans, s));
   } else {

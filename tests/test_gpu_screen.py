@@ -1,5 +1,5 @@
 """GPU parity of the matrix-core first pass of the full search (sub-dimensions
-5-8, K <= 256, screen_kernels.hpp).
+5-8, K <= 256, screen_kernels.hpp), in the Lloyd assignment and in encode.
 
 The full search at these sub-dimensions ranks codewords by a bf16
 hi/lo screen on v_mfma_f32_16x16x32_bf16 and gives the reference distance to
@@ -102,3 +102,64 @@ def test_non_finite_components(gpu, monkeypatch):
     old, _ = _train(x, 32, 4, 64, init, 3, monkeypatch, False)
     for t in range(3):
         assert np.array_equal(_bits(got.stats.trace[t]), _bits(old.stats.trace[t]))
+
+
+def _encode(x, dim, m, ksub, cb, monkeypatch, screen):
+    monkeypatch.setenv("TAC_GPU_SCREEN", "1" if screen else "0")
+    device.profile_enable(True)
+    device.profile_read(reset=True)
+    p = pq.PQ(dim=dim, sub_dim=dim // m, codebooks=cb, m=m, ksub=ksub)
+    got = p.encode_many(x)
+    prof = device.profile_read(reset=True)
+    device.profile_enable(False)
+    return got, prof
+
+
+def _check_encode(x, dim, m, ksub, cb, monkeypatch):
+    got, prof = _encode(x, dim, m, ksub, cb, monkeypatch, True)
+    ref = orc.pq_encode(x, dim, m, ksub, cb, n_threads=16)
+    assert got.dtype == ref.dtype
+    assert np.array_equal(got, ref), f"{np.count_nonzero(got != ref)} codes differ"
+    old, _ = _encode(x, dim, m, ksub, cb, monkeypatch, False)
+    assert np.array_equal(got, old)
+    return prof
+
+
+@pytest.mark.parametrize("dsub,m,ksub", [(8, 8, 256), (8, 3, 100), (5, 4, 256), (6, 5, 31),
+                                         (7, 3, 17), (7, 4, 256), (5, 2, 2), (6, 4, 129)])
+def test_encode_sub_dimensions(gpu, monkeypatch, dsub, m, ksub):
+    # PQ.encode through the screen: token-major rows, 16-byte loads at dsub 8
+    # with dim % 4 == 0, element loads otherwise (dim 24, 20, 30, 21, 28, 10).
+    dim = m * dsub
+    rng = np.random.default_rng(900 + 10 * dsub + ksub)
+    x = (rng.standard_normal((12_345, dim)) * 0.2).astype(np.float32)
+    cb = synth.shuffle_init(x, m, ksub, 7).reshape(-1)
+    prof = _check_encode(x, dim, m, ksub, cb, monkeypatch)
+    assert prof.cand_vectors == m * x.shape[0]
+    assert prof.cand_deferred < 0.2 * prof.cand_vectors
+
+
+def test_encode_ties_and_non_finite(gpu, monkeypatch):
+    # duplicated codewords (exact ties: lowest index), rows equal to
+    # codewords, and rows with inf / NaN components (the deferred scan keeps
+    # PQ.encode's best-from-+inf rule)
+    rng = np.random.default_rng(23)
+    dim, m, ksub = 64, 8, 256
+    x = (rng.standard_normal((9000, dim)) * 0.2).astype(np.float32)
+    cb = synth.shuffle_init(x, m, ksub, 4)
+    cb[:, 200:] = cb[:, 100:156]
+    x[:50] = cb[np.arange(8), np.arange(50)[:, None] % ksub].reshape(50, dim)
+    x[60, 3] = np.inf
+    x[61, 9] = np.nan
+    x[62, :8] = np.nan
+    _check_encode(x, dim, m, ksub, cb.reshape(-1), monkeypatch)
+
+
+@pytest.mark.parametrize("scale", [1e-25, 1e15, 1e20])
+def test_encode_magnitudes(gpu, monkeypatch, scale):
+    rng = np.random.default_rng(29)
+    x = (rng.standard_normal((6000, 64)) * scale).astype(np.float32)
+    cb = synth.shuffle_init(x, 8, 256, 6).reshape(-1)
+    prof = _check_encode(x, 64, 8, 256, cb, monkeypatch)
+    if scale < 1e-18 or scale > 1e18:
+        assert prof.cand_deferred == prof.cand_vectors
