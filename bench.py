@@ -761,11 +761,12 @@ def train_encode_timing(device, dx, n, dim, m, ksub, dinit, steps, warmup):
         tr.append(t1 - t0)
         en.append(time.perf_counter() - t1)
     p = device.profile_read(reset=True)
-    # one more encode alone: the share of vectors its candidate pass deferred
+    # one more encode alone: the share of vectors its first pass (candidate
+    # sets or the matrix-core screen) deferred
     device.encode_device(dx, n, dim, m, ksub, dcb, dcodes)
     device.synchronize()
     pe = device.profile_read(reset=True)
-    p.encode_deferred_frac = pe.cand_deferred / max(pe.cand_vectors, 1)
+    p.encode_deferred_frac = deferred_frac(pe)
     # the train-then-encode entry: its encode stage is one candidate pass
     # anchored at the last Lloyd codes (device time of that pass)
     te = []
@@ -783,11 +784,17 @@ def train_encode_timing(device, dx, n, dim, m, ksub, dinit, steps, warmup):
     return statistics.median(tr), statistics.median(en), p
 
 
-def search_kind(dsub: int, ksub: int, encode: bool) -> str:
-    """The first pass the library picks (cand_wanted / screen_wanted in
-    tac_gpu.hip): candidate sets up to dsub 6 in the Lloyd loop and dsub 4 in
-    encode (and beyond K = 256), the matrix-core screen from there."""
-    if ksub > 256 or dsub <= (4 if encode else 6):
+def deferred_frac(p) -> float:
+    """The share of (vector, subspace) searches the first pass (candidate
+    sets or the matrix-core screen) left to the pruned exact search."""
+    return (p.cand_deferred + p.screen_deferred) / max(p.cand_vectors + p.screen_vectors, 1)
+
+
+def search_kind(dsub: int, ksub: int) -> str:
+    """The first pass the library picks in the Lloyd loop and in encode
+    (cand_wanted / screen_wanted in tac_gpu.hip): candidate sets up to dsub 4
+    (and beyond K = 256), the matrix-core screen from dsub 5 on."""
+    if ksub > 256 or dsub <= 4:
         return "candidate sets"
     return "matrix-core screen"
 
@@ -809,8 +816,7 @@ def shape_sweep(device, dx, x, steps: int):
         rows[name] = {
             "m": w.m, "dsub": w.dim // w.m, "ksub": w.ksub, "lloyd_iters": 20,
             "train_s": round(t_tr, 5),
-            "assign": search_kind(w.dim // w.m, w.ksub, False),
-            "encode_search": search_kind(w.dim // w.m, w.ksub, True),
+            "assign": search_kind(w.dim // w.m, w.ksub),
             "encode_s": round(t_en, 6), "encode_mvec_per_s": round(w.n / t_en / 1e6, 1),
             "encode_stage_ms": round(enc_ms, 4),
             "encode_hbm_frac": round(ebytes / (enc_ms * 1e-3) / 1e9 / PEAK_HBM_GBS, 4),
@@ -820,7 +826,7 @@ def shape_sweep(device, dx, x, steps: int):
             "update_ms_per_iter": round(p.update_ms / max(p.update_iters, 1), 4),
             "assign_ms_per_iter": round(p.assign_ms / max(p.assign_launches, 1), 4),
             "train_streams": int(p.train_streams),
-            "candidate_deferred_frac_train": round(p.cand_deferred / max(p.cand_vectors, 1), 5),
+            "candidate_deferred_frac_train": round(deferred_frac(p), 5),
             "candidate_deferred_frac_encode": round(p.encode_deferred_frac, 5),
         }
         rows[name]["cpu_baseline"] = cpu_profile_row(name, t_tr, w.n / t_en / 1e6)

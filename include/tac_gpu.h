@@ -424,6 +424,10 @@ typedef struct tac_gpu_profile {
                               second runs beside it */
   uint64_t cell_subspaces; /* encode subspaces that took the cell-list pass (rows wider than
                               the codebook's box); the others took the anchored pass */
+  uint64_t screen_vectors;  /* (vector, subspace) searches through the matrix-core screen
+                               (sub-dimensions 5-8, K <= 256: Lloyd assignment and encode) */
+  uint64_t screen_deferred; /* of those, the ones the screen could not settle (left to the
+                               pruned exact search) */
 } tac_gpu_profile;
 int tac_gpu_profile_enable(int enable);
 int tac_gpu_profile_read(tac_gpu_profile *out, int reset);

@@ -371,17 +371,19 @@ int event_at(DeviceState &ds, size_t idx, hipEvent_t *out) {
 // Device counter of vectors the pruned search resolved by a full reference
 // scan; zeroed per call, added to the profile when measuring.
 // Device counters: [0] exact rescans, [1] candidate-path deferrals,
-// [2] candidate-path assignments.
+// [2] candidate-path assignments, [3] cell-list encode subspaces,
+// [4] screen deferrals, [5] screen searches.
+constexpr int kCounters = 6;
 int counter_begin(DeviceState &ds, hipStream_t s, unsigned long long **out) {
-  int st = ensure(ds, ds.counter, 4 * sizeof(unsigned long long));
+  int st = ensure(ds, ds.counter, kCounters * sizeof(unsigned long long));
   if (st) return st;
-  HIP_TRY(hipMemsetAsync(ds.counter.ptr, 0, 4 * sizeof(unsigned long long), s));
+  HIP_TRY(hipMemsetAsync(ds.counter.ptr, 0, kCounters * sizeof(unsigned long long), s));
   *out = reinterpret_cast<unsigned long long *>(ds.counter.ptr);
   return TAC_OK;
 }
 
 int counter_collect(DeviceState &ds, hipStream_t s) {
-  unsigned long long v[4] = {0, 0, 0, 0};
+  unsigned long long v[kCounters] = {0, 0, 0, 0, 0, 0};
   HIP_TRY(hipMemcpyAsync(v, ds.counter.ptr, sizeof(v), hipMemcpyDeviceToHost, s));
   HIP_TRY(hipStreamSynchronize(s));
   std::lock_guard<std::mutex> g(g_profile_mu);
@@ -389,6 +391,8 @@ int counter_collect(DeviceState &ds, hipStream_t s) {
   g_prof.cand_deferred += v[1];
   g_prof.cand_vectors += v[2];
   g_prof.cell_subspaces += v[3];
+  g_prof.screen_deferred += v[4];
+  g_prof.screen_vectors += v[5];
   return TAC_OK;
 }
 
@@ -534,7 +538,8 @@ struct Launch {
       screen_kernel<D, false, uint16_t><<<dim3(T, M), 256, 0, s>>>(
           xs, cb, codes, e, defer, defer_count, done, n, 0, M, K, hist, T);
       KT_END();
-      assign_deferred(xs, cb, codes, e, defer, defer_count, done, n, M, K, hist, T, rescans, s);
+      assign_deferred(xs, cb, codes, e, defer, defer_count, done, n, M, K, hist, T, rescans,
+                      g_profile ? rescans + 4 : nullptr, s);
       return TAC_OK;
     } else {
       return TAC_ERR_INVALID_ARGUMENT;  // no matrix-core screen outside 5-8 sub-dimensions
@@ -587,16 +592,18 @@ struct Launch {
         xs, cb, nbr, anchors, grid, codes, e, nullptr, slice, defer, defer_count, done, n, 0, M, K,
         L, (uint32_t)chunk, (uint32_t)nblk, G, cells, hist, T);
     KT_END();
-    assign_deferred(xs, cb, codes, e, defer, defer_count, done, n, M, K, hist, T, rescans, s);
+    assign_deferred(xs, cb, codes, e, defer, defer_count, done, n, M, K, hist, T, rescans,
+                    g_profile ? rescans + 1 : nullptr, s);
     return TAC_OK;
   }
   // The pruned exact search of the deferred vectors defer[m][..], which also
-  // counts their codes into hist[M][T][K].
+  // counts their codes into hist[M][T][K]; stats (profiling): [0] += the
+  // deferred vectors, [1] += n per subspace.
   static void assign_deferred(const float *xs, const float *cb, uint16_t *codes, float *e,
                               const uint32_t *defer, const uint32_t *defer_count,
                               const uint32_t *done, uint64_t n, uint32_t M, uint32_t K,
                               uint32_t *hist, uint32_t T, unsigned long long *rescans,
-                              hipStream_t s) {
+                              unsigned long long *stats, hipStream_t s) {
     const uint32_t Kp = (K + kPruneBlock - 1) / kPruneBlock * kPruneBlock;
     const size_t lds = (size_t)Kp * (Pad<D>::value + 1) * sizeof(float) + 2 * sizeof(uint32_t);
     // About 2% of the vectors are deferred, each a serial chain over all K
@@ -612,12 +619,12 @@ struct Launch {
       KT("assign_list_kernel<%d, 1, 4>", D);
       assign_list_kernel<D, 1, 4><<<dim3((unsigned)g, M), kBlock, lds, s>>>(
           xs, cb, codes, e, defer, defer_count, done, n, K, rescans,
-          g_profile ? rescans + 1 : nullptr, hist, T, split);
+          stats, hist, T, split);
     } else {
       KT("assign_list_kernel<%d, 1, 1>", D);
       assign_list_kernel<D, 1, 1><<<dim3((unsigned)g, M), kBlock, lds, s>>>(
           xs, cb, codes, e, defer, defer_count, done, n, K, rescans,
-          g_profile ? rescans + 1 : nullptr, hist, T, 0u);
+          stats, hist, T, 0u);
     }
     KT_END();
   }
@@ -985,10 +992,15 @@ int kmeanspp(DeviceState &ds, hipStream_t s, const SubspaceGroup *groups, uint32
 // Whether the candidate-set passes serve a shape.  Past a few dimensions the
 // candidate ball around an anchor holds most of a 256-codeword book (its
 // volume grows as 2^D): the rows run out and most vectors fall through to the
-// full search anyway.  On 1.52M corpus rows at m8 K256 the Lloyd loop ran
-// faster with the pruned full search from dsub 7 on (19.7 against 24.4 ms at
-// dsub 8; a tie at 6) and encode from dsub 5 on (0.83 against 1.14 ms at 8).
-// Larger books keep the candidate passes: the full search costs K per vector.
+// full search anyway.  With the vector-unit pruned search the Lloyd loop on
+// 1.52M corpus rows at m8 K256 was faster through the full search from dsub
+// 7 on (19.7 against 24.4 ms at dsub 8; a tie at 6) and encode from dsub 5
+// on (0.83 against 1.14 ms at 8).  With the full search's first pass on the
+// matrix cores (screen_kernels.hpp, K <= 256) the Lloyd loop is faster
+// through it from dsub 5 on (corpus columns, 20 iterations: 19.5 against
+// 20.9 ms at m12 dsub 5, 13.3 against 16.7 ms at m8 dsub 6); without the
+// screen (TAC_GPU_SCREEN=0) the candidate passes keep dsub 5-6.  Larger
+// books keep the candidate passes: the full search costs K per vector.
 // TAC_GPU_FULL_SEARCH=1 turns the candidate passes off everywhere,
 // TAC_GPU_CANDIDATES=1 keeps them at every dsub (both for auditing).
 bool cand_wanted(uint32_t D, uint32_t K, bool encode) {
@@ -996,7 +1008,8 @@ bool cand_wanted(uint32_t D, uint32_t K, bool encode) {
   if (full_env && full_env[0] == '1') return false;
   const char *cand_env = getenv("TAC_GPU_CANDIDATES");
   if (cand_env && cand_env[0] == '1') return true;
-  return K > 256 || D <= (encode ? 4u : 6u);
+  if (K > 256 || D <= 4u) return true;
+  return !encode && D <= 6u && !screen_wanted(K);
 }
 
 // Lloyd training of all subspaces.  `out.cb` holds the initial codebooks on
@@ -1517,7 +1530,7 @@ int encode_core(DeviceState &ds, hipStream_t s, const float *d_x, uint64_t n, ui
     DISPATCH_D_ST(D, encode_screen<uint8_t>(d_x, d_cb, (uint8_t *)d_codes,
                                             as<uint32_t>(ds.cand_defer) + (size_t)M * n,
                                             as<uint32_t>(ds.cand_count), n, dim, M, K, rescans,
-                                            g_profile ? rescans + 1 : nullptr, s));
+                                            g_profile ? rescans + 4 : nullptr, s));
   } else if (K <= 256) {
     DISPATCH_D_ST(D, encode<uint8_t>(d_x, d_cb, (uint8_t *)d_codes, n, dim, M, K, rescans, s));
   } else {

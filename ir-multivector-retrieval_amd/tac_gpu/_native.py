@@ -74,6 +74,8 @@ class Profile(ctypes.Structure):
         ("cand_assign_iters", c_u64),
         ("train_streams", c_u64),
         ("cell_subspaces", c_u64),
+        ("screen_vectors", c_u64),
+        ("screen_deferred", c_u64),
     ]
 
 

@@ -207,6 +207,8 @@ class KernelTimes:
     cand_assign_iters: int = 0
     train_streams: int = 1
     cell_subspaces: int = 0
+    screen_vectors: int = 0
+    screen_deferred: int = 0
 
 
 def profile_enable(on: bool = True) -> None:
@@ -222,7 +224,8 @@ def profile_read(reset: bool = True) -> KernelTimes:
                        p.crc_launches, p.refine_ms, p.refine_launches, p.cluster_kpp_ms,
                        p.cluster_lloyd_ms, p.cluster_calls, p.cluster_prep_ms,
                        p.cluster_call_ms, p.cand_vectors, p.cand_deferred, p.cand_assign_ms,
-                       p.cand_assign_iters, p.train_streams, p.cell_subspaces)
+                       p.cand_assign_iters, p.train_streams, p.cell_subspaces,
+                       p.screen_vectors, p.screen_deferred)
 
 
 def profile_kernels(reset: bool = True) -> dict:

@@ -22,9 +22,8 @@ pytestmark = pytest.mark.gpu
 
 @pytest.fixture(autouse=True)
 def _candidate_passes(monkeypatch):
-    # By default the library keeps the candidate passes for dsub <= 6 in the
-    # Lloyd loop and dsub <= 4 in encode (K <= 256); these tests exercise
-    # them at every dsub.  TAC_GPU_FULL_SEARCH=1 still wins where a test sets it.
+    # By default the library keeps the candidate passes for dsub <= 4
+    # (K <= 256); these tests exercise them at every dsub.  TAC_GPU_FULL_SEARCH=1 still wins where a test sets it.
     monkeypatch.setenv("TAC_GPU_CANDIDATES", "1")
 
 
@@ -234,13 +233,20 @@ def test_k1024_matches_full_search_on_the_corpus(gpu, monkeypatch):
     assert got.dtype == np.uint16 and np.array_equal(got, q.encode_many(x))
 
 
-@pytest.mark.parametrize("dsub,train_cand,encode_cand", [(4, True, True), (5, True, False),
-                                                          (7, False, False), (8, False, False)])
-def test_default_pass_by_sub_dimension(gpu, monkeypatch, dsub, train_cand, encode_cand):
-    # Without the switch: the candidate passes where they are faster (Lloyd up
-    # to dsub 6, encode up to dsub 4, K <= 256), the pruned full search past
-    # that; the bytes are the oracle's either way.
+@pytest.mark.parametrize("dsub,screen_off,train_cand,encode_cand",
+                         [(4, False, True, True), (5, False, False, False),
+                          (6, False, False, False), (8, False, False, False),
+                          (5, True, True, False), (7, True, False, False)])
+def test_default_pass_by_sub_dimension(gpu, monkeypatch, dsub, screen_off, train_cand,
+                                       encode_cand):
+    # Without the switch: the candidate passes where they are faster (up to
+    # dsub 4, K <= 256), the full search through the matrix-core screen from
+    # dsub 5 on; without the screen the Lloyd loop keeps the candidate passes
+    # up to dsub 6 and the full search is the vector unit's.  The bytes are the
+    # oracle's either way.
     monkeypatch.delenv("TAC_GPU_CANDIDATES")
+    if screen_off:
+        monkeypatch.setenv("TAC_GPU_SCREEN", "0")
     m, ksub, n = 2, 256, 20000
     dim = m * dsub
     rng = np.random.default_rng(600 + dsub)
@@ -255,6 +261,8 @@ def test_default_pass_by_sub_dimension(gpu, monkeypatch, dsub, train_cand, encod
     device.profile_enable(False)
     assert (prof_train.cand_vectors > 0) == train_cand
     assert (prof_enc.cand_vectors > 0) == encode_cand
+    assert (prof_train.screen_vectors > 0) == (not train_cand and not screen_off)
+    assert (prof_enc.screen_vectors > 0) == (not encode_cand and not screen_off)
     ref = orc.pq_encode(x, dim, m, ksub, got.codebooks, n_threads=16)
     assert np.array_equal(codes, ref)
 

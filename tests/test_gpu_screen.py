@@ -64,8 +64,8 @@ def test_sub_dimensions_and_codebook_sizes(gpu, monkeypatch, dsub, ksub):
     init = synth.shuffle_init(x, m, ksub, 5)
     prof = _check(x, dim, m, ksub, init, 6, monkeypatch)
     # every vector went through the screen, which settled most of them
-    assert prof.cand_vectors == 6 * m * x.shape[0]
-    assert prof.cand_deferred < 0.2 * prof.cand_vectors
+    assert prof.screen_vectors == 6 * m * x.shape[0]
+    assert prof.screen_deferred < 0.2 * prof.screen_vectors
 
 
 def test_duplicate_points_and_codewords(gpu, monkeypatch):
@@ -88,7 +88,7 @@ def test_magnitudes(gpu, monkeypatch, scale):
     init = synth.shuffle_init(x, 4, 256, 2)
     prof = _check(x, 32, 4, 256, init, 4, monkeypatch)
     if scale < 1e-18 or scale > 1e18:
-        assert prof.cand_deferred == prof.cand_vectors
+        assert prof.screen_deferred == prof.screen_vectors
 
 
 def test_non_finite_components(gpu, monkeypatch):
@@ -135,8 +135,8 @@ def test_encode_sub_dimensions(gpu, monkeypatch, dsub, m, ksub):
     x = (rng.standard_normal((12_345, dim)) * 0.2).astype(np.float32)
     cb = synth.shuffle_init(x, m, ksub, 7).reshape(-1)
     prof = _check_encode(x, dim, m, ksub, cb, monkeypatch)
-    assert prof.cand_vectors == m * x.shape[0]
-    assert prof.cand_deferred < 0.2 * prof.cand_vectors
+    assert prof.screen_vectors == m * x.shape[0]
+    assert prof.screen_deferred < 0.2 * prof.screen_vectors
 
 
 def test_encode_ties_and_non_finite(gpu, monkeypatch):
@@ -162,4 +162,4 @@ def test_encode_magnitudes(gpu, monkeypatch, scale):
     cb = synth.shuffle_init(x, 8, 256, 6).reshape(-1)
     prof = _check_encode(x, 64, 8, 256, cb, monkeypatch)
     if scale < 1e-18 or scale > 1e18:
-        assert prof.cand_deferred == prof.cand_vectors
+        assert prof.screen_deferred == prof.screen_vectors
