@@ -53,9 +53,10 @@ namespace tacgpu {
 
 typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
 typedef float floatx4 __attribute__((ext_vector_type(4)));
+typedef float floatx16 __attribute__((ext_vector_type(16)));
 
 constexpr uint32_t kScreenMaxK = 256;     // codewords in the kernel's LDS table
-constexpr uint32_t kScreenVecGroups = 4;  // 16-vector groups per wave pass
+constexpr uint32_t kScreenVecGroups = 2;  // 32-vector groups per wave pass
 constexpr float kScreenTame = 1.329227995784916e36f;  // 2^120
 
 // Minimum and maximum in the IEEE 754-2019 sense (v_minimum3_f32 /
@@ -131,10 +132,12 @@ __global__ __launch_bounds__(256) void screen_kernel(
     const uint32_t* __restrict__ done, uint64_t n, uint32_t dim, uint32_t M, uint32_t K,
     uint32_t* __restrict__ hist, uint32_t T) {
   static_assert(D >= 5 && D <= 8, "records of 8 floats");
-  static_assert(kSortTile % (4 * 16 * kScreenVecGroups) == 0, "whole wave passes per tile");
+  static_assert(kSortTile % (4 * 32 * kScreenVecGroups) == 0, "whole wave passes per tile");
   constexpr uint32_t VG = kScreenVecGroups;
-  __shared__ bf16x8 lA[kScreenMaxK * 4];  // [c][q]: the codeword pieces
-  __shared__ __attribute__((aligned(16))) float lnorm[kScreenMaxK];  // +inf past K
+  __shared__ bf16x8 lA[kScreenMaxK * 2];  // [c][h]: the pieces a_hi (h 0), a_lo (h 1)
+  // norms in accumulator order: codeword 32 g + 8 j + 4 h + i at 32 g + 16 h + 4 j + i,
+  // +inf past K
+  __shared__ __attribute__((aligned(16))) float lnorm[kScreenMaxK];
   __shared__ __attribute__((aligned(16))) float lcb[kScreenMaxK * 8];  // fp32 codewords
   __shared__ uint32_t s_hist[kScreenMaxK];
   __shared__ uint32_t s_list[kSortTile];  // the tile's deferred rows
@@ -151,10 +154,8 @@ __global__ __launch_bounds__(256) void screen_kernel(
     if (done[m]) return;
   }
   const uint32_t t = threadIdx.x, lane = t % kWave, w = t / kWave;
-  const uint32_t p = lane % 16, q = lane / 16;
-  // codeword groups of 16, rounded up to whole blocks of two: the tables
-  // hold all kScreenMaxK entries, padding (screen +inf) past K
-  const uint32_t ngroups = (K + 31u) / 32u * 2u;
+  const uint32_t col = lane % 32, h = lane / 32;
+  const uint32_t ngroups = (K + 31u) / 32u;  // codeword groups of 32 (padding past K)
   if (t == 0) {
     s_max = 0;
     s_cnt = 0;
@@ -179,11 +180,10 @@ __global__ __launch_bounds__(256) void screen_kernel(
       cl[d] = (__bf16)(a - (float)hi);
       lcb[c * 8 + d] = v[d];
     }
-    lnorm[c] = c < K ? n2 : __builtin_inff();  // padding: screen +inf
-    lA[c * 4 + 0] = ch;
-    lA[c * 4 + 1] = cl;
-    lA[c * 4 + 2] = ch;
-    lA[c * 4 + 3] = cl;
+    const uint32_t r = c % 32;
+    lnorm[(c - r) + 16 * ((r / 4) % 2) + 4 * (r / 8) + r % 4] = c < K ? n2 : __builtin_inff();
+    lA[c * 2 + 0] = ch;
+    lA[c * 2 + 1] = cl;
     // the largest norm's bits (norms are non-negative or NaN, and a NaN's
     // bits sort above +inf's)
     uint32_t mx = c < K ? __float_as_uint(n2) : 0u;
@@ -211,16 +211,16 @@ __global__ __launch_bounds__(256) void screen_kernel(
                                  ((uintptr_t)x_in & 15u) == 0);  // 16-byte aligned rows
   const uint64_t tile0 = (uint64_t)tile * kSortTile;
   const uint64_t tile1 = tile0 + kSortTile < n ? tile0 + kSortTile : n;
-  const bf16x8* arow = lA + p * 4 + q;  // + 64 per codeword group
-  const floatx4* nrow = reinterpret_cast<const floatx4*>(lnorm) + q;  // + 4 per group
-  for (uint64_t row0 = tile0 + w * (16 * VG); row0 < tile1; row0 += 4 * 16 * VG) {
-    // B operands: vector row0 + 16 vg + p, pieces q (x_hi, x_hi, x_lo, x_lo);
+  const bf16x8* arow = lA + col * 2 + h;                               // + 64 per group
+  const floatx4* nrow = reinterpret_cast<const floatx4*>(lnorm) + h * 4;  // + 8 per group
+  for (uint64_t row0 = tile0 + w * (32 * VG); row0 < tile1; row0 += 4 * 32 * VG) {
+    // B operands of vector row0 + 32 vg + col: [x_hi | x_hi] and [x_lo | x_lo];
     // rows past the tile repeat its last row and are not written.
-    bf16x8 X[VG];
+    bf16x8 Xh[VG], Xl[VG];
     float x[VG][D], x2[VG];
 #pragma unroll
     for (uint32_t vg = 0; vg < VG; ++vg) {
-      const uint64_t r = row0 + 16 * vg + p;
+      const uint64_t r = row0 + 32 * vg + col;
       const uint64_t rr = r < tile1 ? r : tile1 - 1;
       const float* src = xm + rr * (ENCODE ? (uint64_t)dim : 8u);
       float xv[8];
@@ -240,55 +240,58 @@ __global__ __launch_bounds__(256) void screen_kernel(
 #pragma unroll
       for (int d = 1; d < D; ++d) s2 = __builtin_fmaf(xv[d], xv[d], s2);
       x2[vg] = s2;
-      bf16x8 hi, lo;
 #pragma unroll
       for (int d = 0; d < 8; ++d) {
         const float xd = d < D ? xv[d] : 0.0f;
-        hi[d] = (__bf16)xd;
-        lo[d] = (__bf16)(xd - (float)hi[d]);
+        Xh[vg][d] = (__bf16)xd;
+        Xl[vg][d] = (__bf16)(xd - (float)Xh[vg][d]);
       }
-      X[vg] = q >= 2 ? lo : hi;
     }
-    // First pass: block minima over this lane's codewords (4 per group, two
-    // groups per block), the two smallest of them per vector; blocks are
-    // numbered b * 4 + q.
+    // First pass: this lane holds codewords 32 g + 8 j + 4 h + i (j, i < 4) of
+    // its vector; blocks of 8 (j 0-1 and j 2-3) numbered (2 g + s) 2 + h, the
+    // two smallest block minima per vector.
     float b1[VG], b2[VG];
     uint32_t bb[VG];
 #pragma unroll
     for (uint32_t vg = 0; vg < VG; ++vg) {
       b1[vg] = __builtin_inff();
       b2[vg] = __builtin_inff();
-      bb[vg] = q;
+      bb[vg] = h;
     }
-    for (uint32_t g = 0; g < ngroups; g += 2) {
-      const bf16x8 A0 = arow[g * 64];
-      const bf16x8 A1 = arow[(g + 1) * 64];
-      const floatx4 N0 = nrow[g * 4];
-      const floatx4 N1 = nrow[(g + 1) * 4];
-      const uint32_t blk = (g / 2) * 4 + q;
+    for (uint32_t g = 0; g < ngroups; ++g) {
+      const bf16x8 A = arow[g * 64];
+      const floatx4 n0 = nrow[g * 8 + 0], n1 = nrow[g * 8 + 1];
+      const floatx4 n2 = nrow[g * 8 + 2], n3 = nrow[g * 8 + 3];
+      const floatx16 N = {n0[0], n0[1], n0[2], n0[3], n1[0], n1[1], n1[2], n1[3],
+                          n2[0], n2[1], n2[2], n2[3], n3[0], n3[1], n3[2], n3[3]};
 #pragma unroll
       for (uint32_t vg = 0; vg < VG; ++vg) {
-        const floatx4 c0 = __builtin_amdgcn_mfma_f32_16x16x32_bf16(A0, X[vg], N0, 0, 0, 0);
-        const floatx4 c1 = __builtin_amdgcn_mfma_f32_16x16x32_bf16(A1, X[vg], N1, 0, 0, 0);
-        const float v0 = min3f(c0[0], c0[1], c0[2]);
-        const float v1 = min3f(c1[0], c1[1], c1[2]);
-        const float v = min3f(min2f(v0, c0[3]), v1, c1[3]);
-        b2[vg] = min2f(b2[vg], max2f(b1[vg], v));  // second smallest (b1 <= b2)
-        bb[vg] = v < b1[vg] ? blk : bb[vg];
-        b1[vg] = min2f(b1[vg], v);
+        floatx16 c = __builtin_amdgcn_mfma_f32_32x32x16_bf16(A, Xh[vg], N, 0, 0, 0);
+        c = __builtin_amdgcn_mfma_f32_32x32x16_bf16(A, Xl[vg], c, 0, 0, 0);
+#pragma unroll
+        for (uint32_t sb = 0; sb < 2; ++sb) {
+          const float v = min2f(min3f(min3f(c[8 * sb], c[8 * sb + 1], c[8 * sb + 2]),
+                                      min2f(c[8 * sb + 3], c[8 * sb + 4]),
+                                      min2f(c[8 * sb + 5], c[8 * sb + 6])),
+                                c[8 * sb + 7]);
+          const uint32_t blk = (2 * g + sb) * 2 + h;
+          b2[vg] = min2f(b2[vg], max2f(b1[vg], v));  // second smallest (b1 <= b2)
+          bb[vg] = v < b1[vg] ? blk : bb[vg];
+          b1[vg] = min2f(b1[vg], v);
+        }
       }
     }
 #pragma unroll
-    for (uint32_t vg = 0; vg < VG; ++vg) {
-      screen_merge<16>(b1[vg], b2[vg], bb[vg]);
-      screen_merge<32>(b1[vg], b2[vg], bb[vg]);
-    }
+    for (uint32_t vg = 0; vg < VG; ++vg) screen_merge<32>(b1[vg], b2[vg], bb[vg]);
     // The threshold test, then the reference distance to the winning block
-    // (lane q takes its codewords 16 g + 4 qw + q), or the deferred list.
+    // (lane h takes its codewords 32 g + 8 (2 s + h) + 4 hw + i), or the
+    // deferred list.
 #pragma unroll
     for (uint32_t vg = 0; vg < VG; ++vg) {
-      const uint64_t r = row0 + 16 * vg + p;
-      const float nx = sqrtf(x2[vg]);
+      const uint64_t r = row0 + 32 * vg + col;
+      // an upper bound of ||x|| from the raw square root (1 ulp, so the
+      // factor), floored at 2^-50: the bound needs no more precision
+      const float nx = __builtin_amdgcn_sqrtf(max2f(x2[vg], 7.888609052210118e-31f)) * 1.000001f;
       const float ea = kxc * nx * cmax + kcc * cmax2 + k122 * (2.0f * cmax + nx) + k119;
       float thr = 2.0f * ea * (1.0f + gR) +
                   gR * (fabsf(b2[vg] + x2[vg]) + fabsf(b1[vg] + x2[vg]));
@@ -300,23 +303,23 @@ __global__ __launch_bounds__(256) void screen_kernel(
       if (ok) {
         float best = __builtin_inff();
         uint32_t idx = 0xFFFFFFFFu;
-        const uint32_t b = bb[vg] / 4, qw = bb[vg] % 4;
+        const uint32_t g = bb[vg] / 4, sb = (bb[vg] / 2) % 2, hw = bb[vg] % 2;
+        const uint32_t c0 = 32 * g + 8 * (2 * sb + h) + 4 * hw;
 #pragma unroll
-        for (uint32_t j = 0; j < 2; ++j) {
-          const uint32_t c = 16 * (b * 2 + j) + 4 * qw + q;
+        for (uint32_t i = 0; i < 4; ++i) {
+          const uint32_t c = c0 + i;
           if (c < K) {
             float cv[D];
             load_padded<D>(lcb + c * 8, cv);
             const float d2 = exact_l2sq<D>(x[vg], cv);
-            if (d2 < best) {  // c rises with j: the first of this lane's ties stays
+            if (d2 < best) {  // c rises with i: the first of this lane's ties stays
               best = d2;
               idx = c;
             }
           }
         }
-        screen_lex_min<16>(best, idx);
         screen_lex_min<32>(best, idx);
-        if (q == 0 && r < tile1) {
+        if (h == 0 && r < tile1) {
           if constexpr (ENCODE) {
             codes[r * M + m] = (CodeT)idx;
           } else {
@@ -325,7 +328,7 @@ __global__ __launch_bounds__(256) void screen_kernel(
             atomicAdd(&s_hist[idx], 1u);
           }
         }
-      } else if (q == 0 && r < tile1) {
+      } else if (h == 0 && r < tile1) {
         s_list[atomicAdd(&s_cnt, 1u)] = (uint32_t)r;  // at most kSortTile rows
       }
     }
