@@ -1,22 +1,23 @@
-// screen_kernels.hpp — the Lloyd assignment's full search for sub-dimensions
-// 5-8 (records of 8 floats) and K <= 256 with its first pass on the matrix
-// cores.  Included once, by tac_gpu.hip, after cand_kernels.hpp.
+// screen_kernels.hpp — the full search for sub-dimensions 5-8 (records of 8
+// floats) and K <= 256 with its first pass on the matrix cores, for the Lloyd
+// assignment and for encode.  Included once, by tac_gpu.hip, after
+// cand_kernels.hpp.
 //
 // Screen.  For a vector x and codeword c (dimensions past D are 0), the
-// search ranks codewords by s(c) = ||c||^2 - 2 x.c.  Here s comes from one
-// v_mfma_f32_16x16x32_bf16 per 16 codewords x 16 vectors, over 32 products
-// added to the accumulator input n = fl(sum_d c_d^2):
-//   A = [a_hi, a_lo, a_hi, a_lo],  B = [x_hi, x_hi, x_lo, x_lo]  (8 slots each)
-// with a = -2 c (exact), v_hi = bf16(v), v_lo = bf16(v - v_hi) (round to
-// nearest even), so the products sum to (a_hi + a_lo) . (x_hi + x_lo).  For a
-// finite v, |v - v_hi - v_lo| <= 2^-16 |v| + 2^-125 (the absolute term covers
-// subnormal or flushed pieces), so per dimension the products miss a x_d by
-// at most 2.0001 * 2^-16 |a| |x_d| + 2^-124.9 (|a| + |x_d|); n is within
-// gamma_8 ||c||^2 of ||c||^2; the bf16 products are exact in fp32 but for
-// underflow (2^-126 each); and the matrix core adds the 33 terms in fp32 in
-// some order (gamma_32 of their absolute sum, at most
-// 2^-19 (2.032 ||x|| ||c|| + ||c||^2), plus 2^-126 per addition if partial
-// sums flush).  Altogether
+// search ranks codewords by s(c) = ||c||^2 - 2 x.c.  Here s comes from two
+// chained v_mfma_f32_32x32x16_bf16 per 32 codewords x 32 vectors, 32
+// products added to the accumulator input n = fl(sum_d c_d^2):
+//   A = [a_hi | a_lo] with B = [x_hi | x_hi], then A with B = [x_lo | x_lo]
+// (8 slots each half) with a = -2 c (exact), v_hi = bf16(v), v_lo =
+// bf16(v - v_hi) (round to nearest even), so the products sum to
+// (a_hi + a_lo) . (x_hi + x_lo).  For a finite v, |v - v_hi - v_lo| <=
+// 2^-16 |v| + 2^-125 (the absolute term covers subnormal or flushed pieces),
+// so per dimension the products miss a x_d by at most
+// 2.0001 * 2^-16 |a| |x_d| + 2^-124.9 (|a| + |x_d|); n is within gamma_8 ||c||^2
+// of ||c||^2; the bf16 products are exact in fp32 but for underflow (2^-126
+// each); and the matrix core adds the 33 terms in fp32 in some order
+// (gamma_32 of their absolute sum, at most 2^-19 (2.032 ||x|| ||c|| + ||c||^2),
+// plus 2^-126 per addition if partial sums flush).  Altogether
 //   |s~ - s| <= 2^-14 (1.07 ||x|| ||c|| + 0.04 ||c||^2) + 2^-123 (2 ||c|| + ||x||) + 2^-120,
 // and the kernel uses twice that with cmax^2 = max_c fl(||c||^2) in place of
 // ||c||^2.  It needs fl(||x||^2) <= 2^120 and cmax^2 <= 2^120
@@ -25,23 +26,24 @@
 // past that sends every vector to the deferred list below, a vector past it
 // goes there alone.
 //
-// Layout and the exact result.  The codeword pieces are the A operand and
-// the vector pieces the B operand, so lane l of a wave holds the screen
-// values of vector l % 16 of a 16-vector group against codewords
-// 16 g + 4 (l / 16) + i, i < 4, of codeword group g.  It folds them into the
-// minimum of blocks of two consecutive groups (8 codewords) and keeps the
-// two smallest block minima; the blocks of the vector's four lanes
-// partition the codewords.  After the four lanes merge their top-2
-// (permlane swaps: every lane of the vector ends with the same result), the
+// Layout and the exact result.  The codeword pieces are the A operand
+// (lane l: codeword 32 g + l % 32, piece l / 32) and the vector pieces the B
+// operand (lane l: vector l % 32 of a 32-vector group), so lane l holds the
+// screen values of its vector against codewords 32 g + 8 j + 4 (l / 32) + i,
+// j, i < 4, of codeword group g.  It folds them into the minima of blocks of
+// 8 (j 0-1 and j 2-3) and keeps the two smallest block minima; the blocks of
+// the vector's two lanes partition the codewords.  After the two lanes merge
+// their top-2 (a permlane swap: both lanes end with the same result), the
 // argument of pruned_argmin (pq_kernels.hpp) applies unchanged: when the gap
 // between the two smallest block minima exceeds the threshold built from the
 // screen bound and the reference distance's gamma_{D+2}, the reference's
 // first-index argmin lies in the winning block, whose codewords then get the
-// reference distance (two per lane, merged by (distance, index)).  Equal
+// reference distance (four per lane, merged by (distance, index)).  Equal
 // block minima leave no gap.  A vector without the gap joins the subspace's
-// deferred list, whose pruned exact search (assign_list_kernel,
-// cand_kernels.hpp) follows: about 3% of the corpus rows at m8/d8, far fewer
-// than the waves that would stall on an in-wave scan of all K codewords.
+// deferred list, whose pruned exact search (assign_list_kernel or
+// encode_list_kernel, cand_kernels.hpp) follows: about 0.5% of the corpus
+// rows at m8/d8, far fewer than the waves that would stall on an in-wave
+// scan of all K codewords.
 #pragma once
 
 #include <hip/hip_runtime.h>
@@ -134,7 +136,9 @@ __global__ __launch_bounds__(256) void screen_kernel(
   static_assert(D >= 5 && D <= 8, "records of 8 floats");
   static_assert(kSortTile % (4 * 32 * kScreenVecGroups) == 0, "whole wave passes per tile");
   constexpr uint32_t VG = kScreenVecGroups;
-  __shared__ bf16x8 lA[kScreenMaxK * 2];  // [c][h]: the pieces a_hi (h 0), a_lo (h 1)
+  // [g][h][c % 32]: the pieces a_hi (h 0), a_lo (h 1) of codeword c in group g
+  // (each half-wave reads 32 consecutive entries)
+  __shared__ bf16x8 lA[kScreenMaxK * 2];
   // norms in accumulator order: codeword 32 g + 8 j + 4 h + i at 32 g + 16 h + 4 j + i,
   // +inf past K
   __shared__ __attribute__((aligned(16))) float lnorm[kScreenMaxK];
@@ -182,8 +186,8 @@ __global__ __launch_bounds__(256) void screen_kernel(
     }
     const uint32_t r = c % 32;
     lnorm[(c - r) + 16 * ((r / 4) % 2) + 4 * (r / 8) + r % 4] = c < K ? n2 : __builtin_inff();
-    lA[c * 2 + 0] = ch;
-    lA[c * 2 + 1] = cl;
+    lA[(c - r) * 2 + r] = ch;
+    lA[(c - r) * 2 + 32 + r] = cl;
     // the largest norm's bits (norms are non-negative or NaN, and a NaN's
     // bits sort above +inf's)
     uint32_t mx = c < K ? __float_as_uint(n2) : 0u;
@@ -211,7 +215,7 @@ __global__ __launch_bounds__(256) void screen_kernel(
                                  ((uintptr_t)x_in & 15u) == 0);  // 16-byte aligned rows
   const uint64_t tile0 = (uint64_t)tile * kSortTile;
   const uint64_t tile1 = tile0 + kSortTile < n ? tile0 + kSortTile : n;
-  const bf16x8* arow = lA + col * 2 + h;                               // + 64 per group
+  const bf16x8* arow = lA + h * 32 + col;                              // + 64 per group
   const floatx4* nrow = reinterpret_cast<const floatx4*>(lnorm) + h * 4;  // + 8 per group
   for (uint64_t row0 = tile0 + w * (32 * VG); row0 < tile1; row0 += 4 * 32 * VG) {
     // B operands of vector row0 + 32 vg + col: [x_hi | x_hi] and [x_lo | x_lo];
