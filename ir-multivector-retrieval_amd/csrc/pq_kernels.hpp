@@ -928,9 +928,41 @@ __device__ __forceinline__ double wave_sum_f64(double v) {
   for (int off = kWave / 2; off > 0; off >>= 1) v += __shfl_down(v, off, kWave);
   return v;
 }
-__device__ __forceinline__ uint64_t wave_sum_u64(uint64_t v) {
-  for (int off = kWave / 2; off > 0; off >>= 1) v += __shfl_down(v, off, kWave);
+// v of the lane the DPP control CTRL names (0 where it names none or the
+// row is outside ROW_MASK), both halves of a 64-bit value.
+template <int CTRL, int ROW_MASK>
+__device__ __forceinline__ uint64_t dpp_u64(uint64_t v) {
+  const uint32_t lo = (uint32_t)__builtin_amdgcn_update_dpp(0, (int)(uint32_t)v, CTRL, ROW_MASK,
+                                                            0xf, true);
+  const uint32_t hi = (uint32_t)__builtin_amdgcn_update_dpp(0, (int)(uint32_t)(v >> 32), CTRL,
+                                                            ROW_MASK, 0xf, true);
+  return ((uint64_t)hi << 32) | lo;
+}
+
+// Inclusive prefix sum over the wave's lanes by DPP moves (VALU, no LDS
+// round trips): shifts by 1, 2, 4, 8 inside each row of 16 lanes, then row
+// 0's total into row 1 and row 2's into row 3 (row_bcast:15), then rows
+// 0-1's into rows 2-3 (row_bcast:31).
+__device__ __forceinline__ uint64_t wave_inclusive_sum_u64(uint64_t v) {
+  v += dpp_u64<0x111, 0xf>(v);  // row_shr:1
+  v += dpp_u64<0x112, 0xf>(v);  // row_shr:2
+  v += dpp_u64<0x114, 0xf>(v);  // row_shr:4
+  v += dpp_u64<0x118, 0xf>(v);  // row_shr:8
+  v += dpp_u64<0x142, 0xa>(v);  // row_bcast:15 into rows 1 and 3
+  v += dpp_u64<0x143, 0xc>(v);  // row_bcast:31 into rows 2 and 3
   return v;
+}
+
+// v of lane `l` (uniform) in every lane.
+__device__ __forceinline__ uint64_t readlane_u64(uint64_t v, uint32_t l) {
+  const uint32_t lo = (uint32_t)__builtin_amdgcn_readlane((int)(uint32_t)v, (int)l);
+  const uint32_t hi = (uint32_t)__builtin_amdgcn_readlane((int)(uint32_t)(v >> 32), (int)l);
+  return ((uint64_t)hi << 32) | lo;
+}
+
+// The sum over the wave's lanes, in every lane.
+__device__ __forceinline__ uint64_t wave_sum_u64(uint64_t v) {
+  return readlane_u64(wave_inclusive_sum_u64(v), kWave - 1);
 }
 
 // Orders one wave's LDS accesses before and after this point.
@@ -1020,15 +1052,6 @@ __device__ inline void fold_quantize_chunk_wave(const float* __restrict__ em, ui
   }
 }
 
-__device__ __forceinline__ uint64_t wave_inclusive_sum_u64(uint64_t v) {
-  const uint32_t lane = threadIdx.x % kWave;
-  for (int off = 1; off < kWave; off <<= 1) {
-    const uint64_t o = __shfl_up(v, off, kWave);
-    if (lane >= (uint32_t)off) v += o;
-  }
-  return v;
-}
-
 // One wave folds chunks 0 .. nc-1 of em in order from 0 with their
 // descriptors and returns the exact serial sum in every lane; every lane
 // computes the same values.  While the sum is normal, lane i takes chunk
@@ -1055,7 +1078,7 @@ __device__ inline Acc fold_apply_wave(const float* __restrict__ em, uint64_t n,
       const uint64_t bad = __ballot(lane < cnt && !(ok && fold_run_fits<Acc>(m, P)));
       b = bad ? (uint32_t)__builtin_ctzll(bad) : cnt;
       if (starts != nullptr && lane < b) starts[j + lane] = fold_with_units(s, m + P - Q);
-      if (b > 0) s = fold_with_units(s, m + __shfl(P, (int)b - 1, kWave));
+      if (b > 0) s = fold_with_units(s, m + readlane_u64(P, b - 1));
     }
     j += b;
     if (b < cnt) {
