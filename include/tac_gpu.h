@@ -198,7 +198,7 @@ int tac_pq_encode_device(const float *d_residuals, uint64_t n, uint32_t dim,
  * Same arguments, validation and codes as tac_pq_encode_device; stream NULL
  * is the device's null stream, and the call returns once the work is
  * enqueued.  Its scratch (counters, neighbour rows, grid anchors, deferred
- * lists) is one static 128 MiB device array per GPU, held until the process
+ * lists) is one static 32 MiB device array per GPU, held until the process
  * ends; rows run in batches that fit it, so every n that
  * tac_pq_encode_device accepts is accepted (codebooks whose tables leave no
  * room for a 16,384-row batch take the full search).  All calls on one GPU

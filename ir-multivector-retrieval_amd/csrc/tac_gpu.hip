@@ -1588,7 +1588,8 @@ const char *kNames[] = {"Ok",
 // workspace.  Each GPU the library runs on holds its own copy, at its own
 // address, until the process ends.  The name is a host-side stand-in: host
 // code uses only the device address scratch_address returns.
-constexpr size_t kNoAllocScratchBytes = (size_t)128 << 20;
+// 32 MiB: batches of 245,760 rows at m16 (49,152 at m64).
+constexpr size_t kNoAllocScratchBytes = (size_t)32 << 20;
 static __device__ __align__(256) uint8_t scratch[kNoAllocScratchBytes];
 
 namespace {
