@@ -37,6 +37,10 @@ struct KppState {
 };
 
 constexpr int kKppBlock = 4096;  // weights per partial sum
+// Work-items of a kpp_update_kernel block: 8 rows each, so the kernel keeps
+// four waves per SIMD at dsub 8 (16 rows each held it to two) and eight at
+// dsub 4, for the rounds' dependent loads.
+constexpr uint32_t kKppThreads = 512;
 
 // Round c: write codeword c of every subspace from the row chosen last round,
 // update the weights w = min(w, l2sq(x, c_new)) (the first round assigns),
@@ -48,13 +52,13 @@ constexpr int kKppBlock = 4096;  // weights per partial sum
 // cannot when a rounded-down bound of ||c_src - c_new||^2 exceeds
 // cand_radius(w_i): such weights are kept without reading the vector.
 template <int D>
-__global__ __launch_bounds__(256) void kpp_update_kernel(
+__global__ __launch_bounds__(kKppThreads) void kpp_update_kernel(
     const float* __restrict__ xs, float* __restrict__ w, uint16_t* __restrict__ src,
     double* __restrict__ bsum, uint32_t* __restrict__ bad, const KppState* __restrict__ st,
     float* __restrict__ cb, uint64_t n, uint32_t K, uint32_t c, uint32_t NB) {
   constexpr int DP = Pad<D>::value;
   constexpr float g = cand_gamma(D);
-  __shared__ double part[256 / 64];
+  __shared__ double part[kKppThreads / 64];
   __shared__ float lo_tab[1024];  // bound of ||c_j - c_new||^2 per earlier seed j
   const uint32_t m = blockIdx.y, b = blockIdx.x;
   const uint64_t lo = (uint64_t)b * kKppBlock;
@@ -66,13 +70,13 @@ __global__ __launch_bounds__(256) void kpp_update_kernel(
   // do not depend on the draw, so they are in flight while the new seed and
   // its bounds are read), then only the rows the bound cannot settle load
   // their vectors.
-  constexpr uint32_t kPer = kKppBlock / 256;
+  constexpr uint32_t kPer = kKppBlock / kKppThreads;
   float wv[kPer];
   uint32_t sv[kPer];
   bool need[kPer];
 #pragma unroll
   for (uint32_t j = 0; j < kPer; ++j) {
-    const uint64_t i = lo + j * 256 + threadIdx.x;
+    const uint64_t i = lo + j * kKppThreads + threadIdx.x;
     wv[j] = 0.0f;
     sv[j] = 0;
     if (c > 0 && i < hi) {
@@ -96,18 +100,18 @@ __global__ __launch_bounds__(256) void kpp_update_kernel(
   bool invalid = false;
 #pragma unroll
   for (uint32_t j = 0; j < kPer; ++j) {
-    const uint64_t i = lo + j * 256 + threadIdx.x;
+    const uint64_t i = lo + j * kKppThreads + threadIdx.x;
     need[j] = i < hi && (c == 0 || !cand_cannot_beat(lo_tab[sv[j]], wv[j], g));
   }
   float xv[kPer][D];
 #pragma unroll
   for (uint32_t j = 0; j < kPer; ++j) {
-    const uint64_t i = lo + j * 256 + threadIdx.x;
+    const uint64_t i = lo + j * kKppThreads + threadIdx.x;
     if (need[j]) load_padded<D>(xm + i * DP, xv[j]);
   }
 #pragma unroll
   for (uint32_t j = 0; j < kPer; ++j) {
-    const uint64_t i = lo + j * 256 + threadIdx.x;
+    const uint64_t i = lo + j * kKppThreads + threadIdx.x;
     if (i >= hi) continue;
     float wi = wv[j];
     if (need[j]) {
@@ -129,7 +133,12 @@ __global__ __launch_bounds__(256) void kpp_update_kernel(
   if (threadIdx.x % 64 == 0) part[threadIdx.x / 64] = acc;
   if (invalid) atomicOr(&bad[m], 1u);
   __syncthreads();
-  if (threadIdx.x == 0) bsum[(uint64_t)m * NB + b] = (part[0] + part[1]) + (part[2] + part[3]);
+  if (threadIdx.x == 0) {
+    double t = 0.0;
+#pragma unroll
+    for (uint32_t q = 0; q < kKppThreads / 64; ++q) t += part[q];
+    bsum[(uint64_t)m * NB + b] = t;
+  }
 }
 
 // Round c draw: one block per subspace.  Checks the weights, draws u, finds
@@ -293,7 +302,7 @@ constexpr uint32_t kKppFallbackThreads = 1024;
 // The body, for one weight vector wm[0 .. n) and its state S, run by a whole
 // block of kKppFallbackThreads threads (the caller has checked that S needs
 // it).  pm, cm: nc = ceil(n / kFoldChunk) entries of scratch.
-__device__ inline void kpp_fallback_block(const float* __restrict__ wm, uint64_t n, KppState& S,
+__device__ __forceinline__ void kpp_fallback_block(const float* __restrict__ wm, uint64_t n, KppState& S,
                                           double* __restrict__ pm, FoldChunk* __restrict__ cm,
                                           uint32_t nc) {
   constexpr uint32_t kWaves = kKppFallbackThreads / kWave;
@@ -301,13 +310,25 @@ __device__ inline void kpp_fallback_block(const float* __restrict__ wm, uint64_t
   __shared__ double carry;
   __shared__ __attribute__((aligned(16))) float buf[kFoldChunk];
   const uint32_t lane = threadIdx.x % kWave, wv = threadIdx.x / kWave;
-  for (uint32_t j = wv; j < nc; j += kWaves) {
-    const double cs = fold_chunk_sum_wave(wm, n, j);
-    if (lane == 0) pm[j] = cs;
+  // Chunk sums and descriptors, each wave kFallbackBatch chunks at a time
+  // (all their loads in flight together).
+  constexpr uint32_t kFallbackBatch = 4;
+  for (uint32_t j0 = wv * kFallbackBatch; j0 < nc; j0 += kWaves * kFallbackBatch) {
+    double cs[kFallbackBatch];
+    fold_chunk_sums_wave<kFallbackBatch>(wm, n, j0, nc, cs);
+    if (lane == 0)
+#pragma unroll
+      for (uint32_t b = 0; b < kFallbackBatch; ++b)
+        if (j0 + b < nc) pm[j0 + b] = cs[b];
   }
   __syncthreads();
   block_prefix_f64<kKppFallbackThreads>(pm, nc, wsum, &carry);
-  for (uint32_t j = wv; j < nc; j += kWaves) fold_quantize_chunk_wave<double>(wm, n, j, pm[j], cm + j);
+  for (uint32_t j0 = wv * kFallbackBatch; j0 < nc; j0 += kWaves * kFallbackBatch) {
+    double pre[kFallbackBatch];
+#pragma unroll
+    for (uint32_t b = 0; b < kFallbackBatch; ++b) pre[b] = j0 + b < nc ? pm[j0 + b] : 0.0;
+    fold_quantize_chunks_wave<double, kFallbackBatch>(wm, n, j0, nc, pre, cm + j0);
+  }
   __syncthreads();
   if (wv != 0) return;
   // Wave 0 only from here: pm[j] becomes the exact value before chunk j.

@@ -1052,6 +1052,85 @@ __device__ inline void fold_quantize_chunk_wave(const float* __restrict__ em, ui
   }
 }
 
+// fold_chunk_sum_wave and fold_quantize_chunk_wave for the B chunks
+// j0 .. j0 + B - 1 below nc at once (each chunk's terms in the same lanes and
+// order), every load issued before any arithmetic: one wave working through
+// many chunks pays a memory round trip per B chunks instead of per chunk.
+template <uint32_t B>
+__device__ inline void fold_load_chunks_wave(const float* __restrict__ em, uint64_t n,
+                                             uint32_t j0, uint32_t nc,
+                                             float (&v)[B][kFoldChunk / kWave],
+                                             uint32_t (&len)[B]) {
+  const uint32_t lane = threadIdx.x % kWave;
+#pragma unroll
+  for (uint32_t b = 0; b < B; ++b) {
+    const uint32_t j = j0 + b;
+    len[b] = j < nc ? fold_chunk_len(n, j) : 0u;
+    const uint64_t lo = (uint64_t)j * kFoldChunk;
+#pragma unroll
+    for (uint32_t t = 0; t < kFoldChunk / kWave; ++t) {
+      const uint32_t i = lane + t * kWave;
+      v[b][t] = i < len[b] ? em[lo + i] : 0.0f;
+    }
+  }
+}
+
+template <uint32_t B>
+__device__ inline void fold_chunk_sums_wave(const float* __restrict__ em, uint64_t n, uint32_t j0,
+                                            uint32_t nc, double (&cs)[B]) {
+  const uint32_t lane = threadIdx.x % kWave;
+  float v[B][kFoldChunk / kWave];
+  uint32_t len[B];
+  fold_load_chunks_wave<B>(em, n, j0, nc, v, len);
+#pragma unroll
+  for (uint32_t b = 0; b < B; ++b) {
+    double acc = 0.0;
+#pragma unroll
+    for (uint32_t t = 0; t < kFoldChunk / kWave; ++t)
+      if (lane + t * kWave < len[b]) acc += (double)v[b][t];
+    cs[b] = wave_sum_f64(acc);
+  }
+}
+
+template <typename Acc, uint32_t B>
+__device__ inline void fold_quantize_chunks_wave(const float* __restrict__ em, uint64_t n,
+                                                 uint32_t j0, uint32_t nc,
+                                                 const double (&pre)[B],
+                                                 FoldChunk* __restrict__ out) {
+  const uint32_t lane = threadIdx.x % kWave;
+  float v[B][kFoldChunk / kWave];
+  uint32_t len[B];
+  fold_load_chunks_wave<B>(em, n, j0, nc, v, len);
+#pragma unroll
+  for (uint32_t b = 0; b < B; ++b) {
+    const Acc ps = (Acc)pre[b];
+    const int32_t k0 = fold_is_normal_positive(ps) ? fold_exponent(ps) - 1 : kFoldNoBinade;
+    uint64_t q[kFoldCands] = {0, 0, 0};
+    uint32_t bad = 0;  // bit c: candidate c spoiled by one of this lane's terms
+#pragma unroll
+    for (uint32_t t = 0; t < kFoldChunk / kWave; ++t) {
+      if (lane + t * kWave >= len[b]) continue;
+#pragma unroll
+      for (int c = 0; c < kFoldCands; ++c) {
+        const uint64_t qi = fold_quantize<Acc>(v[b][t], k0 + c);
+        bad |= qi == kFoldBad ? 1u << c : 0u;
+        q[c] += qi == kFoldBad ? 0u : qi;
+      }
+    }
+    for (int off = kWave / 2; off > 0; off >>= 1) bad |= __shfl_xor(bad, off, kWave);
+#pragma unroll
+    for (int c = 0; c < kFoldCands; ++c) q[c] = wave_sum_u64(q[c]);
+    if (lane == 0 && j0 + b < nc) {
+      FoldChunk ch;
+      ch.k0 = k0;
+      ch.clean = ~bad & ((1u << kFoldCands) - 1u);
+#pragma unroll
+      for (int c = 0; c < kFoldCands; ++c) ch.q[c] = q[c];
+      out[b] = ch;
+    }
+  }
+}
+
 // One wave folds chunks 0 .. nc-1 of em in order from 0 with their
 // descriptors and returns the exact serial sum in every lane; every lane
 // computes the same values.  While the sum is normal, lane i takes chunk

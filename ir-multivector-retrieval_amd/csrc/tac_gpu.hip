@@ -829,7 +829,8 @@ struct Launch {
   static void kpp_update(const float *xs, float *w, uint16_t *src, double *bsum, uint32_t *bad,
                          const KppState *st, float *cb, uint64_t n, uint32_t M, uint32_t K,
                          uint32_t c, uint32_t NB, hipStream_t s) {
-    kpp_update_kernel<D><<<dim3(NB, M), 256, 0, s>>>(xs, w, src, bsum, bad, st, cb, n, K, c, NB);
+    kpp_update_kernel<D><<<dim3(NB, M), kKppThreads, 0, s>>>(xs, w, src, bsum, bad, st, cb, n,
+                                                              K, c, NB);
   }
   static void fold(const float *sorted, const uint32_t *counts, const uint32_t *start,
                    float *cb, const uint32_t *done, const uint32_t *order, uint64_t n, uint32_t M,
