@@ -533,7 +533,7 @@ struct Launch {
                            uint64_t n, uint32_t M, uint32_t K, uint32_t *hist, uint32_t T,
                            unsigned long long *rescans, hipStream_t s) {
     if constexpr (D >= 5 && D <= 8) {
-      HIP_TRY(hipMemsetAsync(defer_count, 0, M * sizeof(uint32_t), s));
+      zero_words_kernel<<<1, kWave, 0, s>>>(defer_count, M);  // a dispatch, also in a graph
       KT("screen_kernel<%d, false, unsigned short>", D);
       screen_kernel<D, false, uint16_t><<<dim3(T, M), 256, 0, s>>>(
           xs, cb, codes, e, defer, defer_count, done, n, 0, M, K, hist, T);
@@ -640,7 +640,7 @@ struct Launch {
       const uint64_t tiles = (n + kSortTile - 1) / kSortTile;
       const uint64_t total = tiles * M;
       if (total > 0xFFFFFFF0ull) return TAC_ERR_UNSUPPORTED;
-      HIP_TRY(hipMemsetAsync(defer_count, 0, M * sizeof(uint32_t), s));
+      zero_words_kernel<<<1, kWave, 0, s>>>(defer_count, M);  // a dispatch, also in a graph
       const uint32_t blocks = (uint32_t)(8 * ((total + 7) / 8));
       KT("screen_kernel<%d, true, %s>", D, code_name<CodeT>());
       screen_kernel<D, true, CodeT><<<blocks, 256, 0, s>>>(x, cb, codes, nullptr, defer,
@@ -1930,6 +1930,28 @@ int tac_pq_encode_device_noalloc(const float *d_residuals, uint64_t n, uint32_t 
   auto *counters = reinterpret_cast<unsigned long long *>(take(3 * sizeof(unsigned long long)));
   zero_words_kernel<<<1, kWave, 0, s>>>(reinterpret_cast<uint32_t *>(counters), 6);
   LAUNCH_TRY("zero_words_kernel");
+  // Sub-dimensions 5-8 with ksub <= 256: the matrix-core screen, its
+  // deferred list (one word per row and subspace) and count in the scratch,
+  // in batches of whole sort tiles that fit.
+  if (D >= 5 && D <= 8 && screen_wanted(ksub)) {
+    uint32_t *dcount = reinterpret_cast<uint32_t *>(take((size_t)m * sizeof(uint32_t)));
+    const size_t left = off < kNoAllocScratchBytes ? kNoAllocScratchBytes - off : 0;
+    uint64_t sb = left / (sizeof(uint32_t) * (size_t)m) / kSortTile * kSortTile;
+    sb = std::min<uint64_t>(sb, 0xFFFF0000ull / kSortTile * kSortTile);
+    uint32_t *dlist = reinterpret_cast<uint32_t *>(base + off);
+    if (sb > 0) {
+      for (uint64_t r0 = 0; r0 < n; r0 += sb) {
+        const uint64_t nb = std::min<uint64_t>(sb, n - r0);
+        DISPATCH_D_ST(D, encode_screen<uint8_t>(d_residuals + r0 * dim, d_codebooks,
+                                                static_cast<uint8_t *>(d_codes_out) + r0 * m,
+                                                dlist, dcount, nb, dim, m, ksub, counters,
+                                                nullptr, s));
+        if (st) return st;
+        LAUNCH_TRY("screen encode");
+      }
+      return TAC_OK;
+    }
+  }
   const uint32_t L = ksub >= 2 ? std::min<uint32_t>(kCandListEncode, ksub - 1) : 0;
   bool cand = cand_wanted(D, ksub, true) && ksub >= 2 && ksub <= 256 && n >= 16384;
   uint64_t batch = 0;

@@ -24,9 +24,9 @@ def _encode(fn, dx, n, dim, m, ksub, dcb, fill):
 
 # (m, ksub, rows of the first call, rows of the second call).  At m16 the
 # scratch holds batches of 245,760 rows: the first call runs two full
-# batches and a 5,000-row tail (full search); m64 batches are 49,152 rows, m8
-# batches 507,904; ksub 1024 and calls under 16,384 rows take the full search
-# throughout.
+# batches and a 5,000-row tail (full search); m64 batches are 49,152 rows; m8
+# (dsub 8) takes the matrix-core screen in batches of 1,046,528 rows; ksub
+# 1024 and calls under 16,384 rows take the full search throughout.
 CASES = [
     (16, 256, 2 * 245_760 + 5_000, 40_000),
     (64, 256, 300_000, 20_000),
