@@ -142,6 +142,7 @@ __global__ __launch_bounds__(256) void tac_gather_kernel(const float* __restrict
 // count.  Lanes past dim read neighbouring floats and never store them.
 // ---------------------------------------------------------------------------
 typedef float tac_floatx4 __attribute__((ext_vector_type(4)));
+typedef __bf16 tac_bf16x8 __attribute__((ext_vector_type(8)));
 
 constexpr uint32_t kTacSpreadBatch = 32;
 // Rows per batch of tac_spread_kernel<PER>: two batches of B x PER floats
@@ -938,11 +939,18 @@ __global__ void tac_assign_kernel(const float* __restrict__ G, const float* __re
 // tac_assign_kernel, with most of the arithmetic moved to MFMA.
 //
 // Screen.  s(x, c) = h_c - x.c with h_c = ||c||^2 / 2 (fp32, any order) and
-// x.c from v_mfma_f32_16x16x4_f32 (16 steps of 4 dimensions).  Whatever the
-// order and rounding of the products and sums inside the matrix core,
-// |s - (||c||^2 / 2 - x.c)| <= E = Gm (||x||^2 + 2 cmax2) + 1e-35 with
-// Gm = 512 u (u = 2^-24), cmax2 >= ||c||^2 for every centroid of the
-// problem, and the addend covering products in the subnormal range.
+// x.c from eight v_mfma_f32_16x16x32_bf16 per 16 rows x 16 centroids over
+// bf16 hi/lo pieces (v_hi = bf16(v), v_lo = bf16(v - v_hi), round to nearest
+// even): (x_hi + x_lo) . (c_hi + c_lo) as four exact bf16 products per
+// dimension, 256 terms added in fp32 in some order.  For the tame components
+// below, |v - v_hi - v_lo| <= 2^-16 |v| + 2^-125, so the products miss x.c by
+// at most 2.0001 * 2^-16 ||x|| ||c|| plus underflow, the sum adds gamma_256
+// (2^-16) of 1.016 ||x|| ||c||, and h carries gamma_64 of ||c||^2 / 2:
+// altogether at most 2^-15 (0.76 ||x||^2 + 0.82 ||c||^2) plus terms below
+// 2^-120 (||x|| + ||c||), inside E = Gm (||x||^2 + 2 cmax2) + 1e-35 with
+// Gm = 512 u (u = 2^-24) = 2^-15, cmax2 >= ||c||^2 for every centroid of the
+// problem, and the addend covering products in the subnormal range (the
+// bound the fp32 matrix-core screen this replaced was given).
 // Candidates.  The reference distance (tac_l2sq<64>: four 16-term lane sums
 // and three adds, g = gamma_20 relative) of the winner c* is at most that of
 // the screen's minimum c_m, so s(c*) <= s_min + 2E + 1.01 g ||x - c_m||^2
@@ -963,6 +971,13 @@ __global__ void tac_assign_kernel(const float* __restrict__ G, const float* __re
 // do not hold) takes tac_assign_kernel's exact search for all its rows.
 // One block of 256 work-items per tile of 128 rows; wave w takes rows
 // 32 w .. 32 w + 31 as two row groups, four accumulator chains at a time.
+// Lane layout of v_mfma_f32_16x16x32_bf16: lane l supplies row (A) or
+// centroid (B) l % 16 at k = 8 (l / 16) + i, i < 8, and holds the dot
+// products of rows 4 (l / 16) + i, i < 4, with centroid l % 16; MFMA t of a
+// tile takes dimensions 32 (t % 2) + k of the pieces (x_hi or x_lo) x (c_hi
+// or c_lo) that t / 2 names.  The chunk's centroids sit in LDS as bf16 rows
+// [c_hi x 64 | c_lo x 64 | 8 pad], 272 bytes, so the 16 centroids a
+// half-wave reads fall in distinct banks.
 // ---------------------------------------------------------------------------
 // This lane's slot in a shared LDS list when `take` (every lane of the wave
 // calls it): the wave's ballot, one atomic add by its first taking lane, and
@@ -984,6 +999,7 @@ constexpr uint32_t kTacMfmaRows = 128;     // rows per tile (tac_rows_per_tile(6
 constexpr uint32_t kTacMfmaThreads = 256;
 constexpr uint32_t kTacMfmaChunk = 128;    // centroids staged in LDS at a time
 constexpr uint32_t kTacMfmaLd = 65;        // LDS row stride (floats)
+constexpr uint32_t kTacMfmaLd16 = 136;     // LDS row stride of the bf16 centroid pieces
 
 // Components for which the screen's bounds hold: finite, |v| < 1e18 and not
 // subnormal.
@@ -1031,7 +1047,13 @@ __global__ __launch_bounds__(kTacMfmaThreads) __attribute__((amdgpu_waves_per_eu
     const uint32_t* __restrict__ done, uint32_t* __restrict__ code, float* __restrict__ e) {
   constexpr uint32_t R = kTacMfmaRows, LD = kTacMfmaLd, CH = kTacMfmaChunk;
   __shared__ float xr[R * LD];
-  __shared__ float cs[CH * LD];
+  // the chunk's centroids: bf16 pieces for the screen, fp32 rows for the
+  // exact search (which restages them)
+  constexpr uint32_t kCsBytes = CH * LD * 4 > CH * kTacMfmaLd16 * 2 ? CH * LD * 4
+                                                                    : CH * kTacMfmaLd16 * 2;
+  __shared__ __attribute__((aligned(16))) uint8_t cbuf[kCsBytes];
+  float* cs = reinterpret_cast<float*>(cbuf);
+  __bf16* cb16 = reinterpret_cast<__bf16*>(cbuf);
   __shared__ float hs[CH];
   __shared__ float x2s[R];
   __shared__ unsigned long long rowkey[R];
@@ -1097,13 +1119,21 @@ __global__ __launch_bounds__(kTacMfmaThreads) __attribute__((amdgpu_waves_per_eu
   __syncthreads();
   const float* Cp = C + (uint64_t)pr.goff * 64;
   if (!exact) {
-    // A operands of the wave's two row groups (rows past the tile read 0).
-    float a[2][16];
+    // A operands of the wave's two row groups (rows past the tile read 0):
+    // the hi and lo pieces of dimensions 32 dh + 8 lq + i.
+    tac_bf16x8 xh[2][2], xl[2][2];
 #pragma unroll
     for (int g = 0; g < 2; ++g) {
       const uint32_t r = 32 * w + 16 * g + li;
 #pragma unroll
-      for (int s = 0; s < 16; ++s) a[g][s] = r < rows ? xr[r * LD + 4 * s + lq] : 0.0f;
+      for (int dh = 0; dh < 2; ++dh)
+#pragma unroll
+        for (int i = 0; i < 8; ++i) {
+          const float v = r < rows ? xr[r * LD + 32 * dh + 8 * lq + i] : 0.0f;
+          const __bf16 hi = (__bf16)v;
+          xh[g][dh][i] = hi;
+          xl[g][dh][i] = (__bf16)(v - (float)hi);
+        }
     }
     float b1[2][4], b2[2][4];
     uint32_t i1[2][4], i2[2][4];
@@ -1116,18 +1146,21 @@ __global__ __launch_bounds__(kTacMfmaThreads) __attribute__((amdgpu_waves_per_eu
         i1[g][v] = 0;
         i2[g][v] = 0;
       }
-    // Chunks of CH centroids pass through LDS; each work-item holds its 16
-    // floats (and h) of the next chunk in registers while the current one is
-    // worked on.
-    constexpr uint32_t PF = CH * 64 / kTacMfmaThreads;
-    float pf[PF];
+    // Chunks of CH centroids pass through LDS; each work-item holds its
+    // four runs of 8 floats (and h) of the next chunk in registers while the
+    // current one is worked on, and stores them as bf16 pieces.
+    constexpr uint32_t PF = CH * 64 / 8 / kTacMfmaThreads;  // runs of 8 floats
+    tac_floatx4 pf[PF][2];
     float ph = __builtin_inff();
     auto fetch = [&](uint32_t c0) {
       const uint32_t cnt = pr.k - c0 < CH ? pr.k - c0 : CH;
 #pragma unroll
       for (uint32_t j = 0; j < PF; ++j) {
-        const uint32_t f = t + j * kTacMfmaThreads, cc = f / 64;
-        pf[j] = cc < cnt ? Cp[(uint64_t)c0 * 64 + f] : 0.0f;
+        const uint32_t f = t + j * kTacMfmaThreads, cc = f / 8;
+        const tac_floatx4* src =
+            reinterpret_cast<const tac_floatx4*>(Cp + (uint64_t)c0 * 64 + 8ull * f);
+        pf[j][0] = cc < cnt ? src[0] : tac_floatx4{0.0f, 0.0f, 0.0f, 0.0f};
+        pf[j][1] = cc < cnt ? src[1] : tac_floatx4{0.0f, 0.0f, 0.0f, 0.0f};
       }
       if (t < CH) ph = t < cnt ? h[pr.goff + c0 + t] : __builtin_inff();
     };
@@ -1137,8 +1170,17 @@ __global__ __launch_bounds__(kTacMfmaThreads) __attribute__((amdgpu_waves_per_eu
       __syncthreads();
 #pragma unroll
       for (uint32_t j = 0; j < PF; ++j) {
-        const uint32_t f = t + j * kTacMfmaThreads;
-        cs[(f / 64) * LD + f % 64] = pf[j];
+        const uint32_t f = t + j * kTacMfmaThreads, cc = f / 8, d0 = 8 * (f % 8);
+        tac_bf16x8 hi8, lo8;
+#pragma unroll
+        for (int i = 0; i < 8; ++i) {
+          const float v = pf[j][i / 4][i % 4];
+          const __bf16 hi = (__bf16)v;
+          hi8[i] = hi;
+          lo8[i] = (__bf16)(v - (float)hi);
+        }
+        *reinterpret_cast<tac_bf16x8*>(cb16 + cc * kTacMfmaLd16 + d0) = hi8;
+        *reinterpret_cast<tac_bf16x8*>(cb16 + cc * kTacMfmaLd16 + 64 + d0) = lo8;
       }
       if (t < CH) {
         hs[t] = ph;
@@ -1155,13 +1197,18 @@ __global__ __launch_bounds__(kTacMfmaThreads) __attribute__((amdgpu_waves_per_eu
       // (2 row groups x 2 centroid groups) keep the matrix core busy.  A
       // group past the chunk's centroids reads the padding (h = inf).
       for (uint32_t cg = 0; cg < CH / 16 && cg * 16 < cnt; cg += 2) {
-        float bv[2][16], hv[2];
+        tac_bf16x8 ch[2][2], cl[2][2];
+        float hv[2];
         uint32_t cidx[2];
 #pragma unroll
         for (int j = 0; j < 2; ++j) {
           const uint32_t cc = (cg + j) * 16 + li;
 #pragma unroll
-          for (int s = 0; s < 16; ++s) bv[j][s] = cs[cc * LD + 4 * s + lq];
+          for (int dh = 0; dh < 2; ++dh) {
+            const __bf16* row = cb16 + cc * kTacMfmaLd16 + 32 * dh + 8 * lq;
+            ch[j][dh] = *reinterpret_cast<const tac_bf16x8*>(row);
+            cl[j][dh] = *reinterpret_cast<const tac_bf16x8*>(row + 64);
+          }
           hv[j] = hs[cc];
           cidx[j] = c0 + cc;
         }
@@ -1171,13 +1218,16 @@ __global__ __launch_bounds__(kTacMfmaThreads) __attribute__((amdgpu_waves_per_eu
 #pragma unroll
           for (int j = 0; j < 2; ++j) acc[g][j] = tac_floatx4{0.0f, 0.0f, 0.0f, 0.0f};
 #pragma unroll
-        for (int s = 0; s < 16; ++s)
+        for (int dh = 0; dh < 2; ++dh)
 #pragma unroll
-          for (int g = 0; g < 2; ++g)
+          for (int pc = 0; pc < 4; ++pc)
 #pragma unroll
-            for (int j = 0; j < 2; ++j)
-              acc[g][j] = __builtin_amdgcn_mfma_f32_16x16x4f32(a[g][s], bv[j][s], acc[g][j], 0, 0,
-                                                               0);
+            for (int g = 0; g < 2; ++g)
+#pragma unroll
+              for (int j = 0; j < 2; ++j)
+                acc[g][j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(
+                    pc < 2 ? xh[g][dh] : xl[g][dh], pc % 2 == 0 ? ch[j][dh] : cl[j][dh],
+                    acc[g][j], 0, 0, 0);
         // Two smallest screen values per (row group, row) without branches;
         // centroids arrive in ascending index order.
 #pragma unroll
