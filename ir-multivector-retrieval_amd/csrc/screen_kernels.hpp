@@ -50,6 +50,7 @@
 #include <stdint.h>
 
 #include "cand_kernels.hpp"
+#include "screen_rules.hpp"
 
 namespace tacgpu {
 
@@ -59,7 +60,6 @@ typedef float floatx16 __attribute__((ext_vector_type(16)));
 
 constexpr uint32_t kScreenMaxK = 256;     // codewords in the kernel's LDS table
 constexpr uint32_t kScreenVecGroups = 2;  // 32-vector groups per wave pass
-constexpr float kScreenTame = 1.329227995784916e36f;  // 2^120
 
 // Minimum and maximum in the IEEE 754-2019 sense (v_minimum3_f32 /
 // v_maximum3_f32: no canonicalising moves, which fminf / fmaxf add in IEEE
@@ -203,13 +203,6 @@ __global__ __launch_bounds__(256) void screen_kernel(
   const float cmax2 = __uint_as_float(s_max);
   const bool cb_ok = cmax2 <= kScreenTame;  // false on NaN
   const float cmax = sqrtf(cmax2);
-  constexpr float u = 5.9604644775390625e-8f;  // 2^-24
-  constexpr float gR = (float)(D + 2) * u / (1.0f - (float)(D + 2) * u);
-  // twice the bound: 2^-13 (1.07 nx cmax + 0.04 cmax^2) + 2^-122 (2 cmax + nx) + 2^-119
-  constexpr float kxc = 1.31e-4f;                 // >= 1.07 * 2^-13
-  constexpr float kcc = 4.9e-6f;                  // >= 0.04 * 2^-13
-  constexpr float k122 = 1.880790961315660e-37f;  // 2^-122
-  constexpr float k119 = 1.504632769052528e-36f;  // 2^-119
   const float* xm = ENCODE ? x_in + (uint64_t)m * D : x_in + (uint64_t)m * n * 8;
   const bool vec4 = !ENCODE || (D == 8 && dim % 4 == 0 &&
                                  ((uintptr_t)x_in & 15u) == 0);  // 16-byte aligned rows
@@ -296,14 +289,10 @@ __global__ __launch_bounds__(256) void screen_kernel(
       // an upper bound of ||x|| from the raw square root (1 ulp, so the
       // factor), floored at 2^-50: the bound needs no more precision
       const float nx = __builtin_amdgcn_sqrtf(max2f(x2[vg], 7.888609052210118e-31f)) * 1.000001f;
-      const float ea = kxc * nx * cmax + kcc * cmax2 + k122 * (2.0f * cmax + nx) + k119;
-      float thr = 2.0f * ea * (1.0f + gR) +
-                  gR * (fabsf(b2[vg] + x2[vg]) + fabsf(b1[vg] + x2[vg]));
-      thr = 2.0f * thr + 1e-30f;
       // b2 = +inf: every other block holds padding only (a tame codeword's
       // screen value is finite), so the winning block holds every codeword.
       const bool ok = cb_ok && x2[vg] <= kScreenTame &&
-                      (b2[vg] == __builtin_inff() || (b2[vg] - b1[vg]) > thr);
+                      screen_separates<D>(b1[vg], b2[vg], x2[vg], screen_err(nx, cmax, cmax2));
       if (ok) {
         float best = __builtin_inff();
         uint32_t idx = 0xFFFFFFFFu;

@@ -2,10 +2,10 @@
 5-8, K <= 256, screen_kernels.hpp), in the Lloyd assignment and in encode.
 
 The full search at these sub-dimensions ranks codewords by a bf16
-hi/lo screen on v_mfma_f32_16x16x32_bf16 and gives the reference distance to
-the winning block; a vector whose blocks the screen cannot separate goes to
-the deferred list and its pruned exact search.  These cases train through it (TAC_GPU_FULL_SEARCH=1: every
-iteration takes the full search) and compare every iteration's codebook
+hi/lo screen on v_mfma_f32_32x32x16_bf16 and gives the reference distance to
+the winning block of 8; a vector whose blocks the screen cannot separate goes
+to the deferred list and its pruned exact search.  These cases train through
+it (TAC_GPU_FULL_SEARCH=1: every iteration takes the full search) and compare every iteration's codebook
 bit for bit with the oracle (src/tac/kmeans.zig:154-224 restated) and with
 the vector-unit first pass (TAC_GPU_SCREEN=0): every sub-dimension 5-8, K
 from 2 to 256 (codeword padding inside the 16-wide groups), exact ties from
