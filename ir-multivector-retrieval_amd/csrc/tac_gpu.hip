@@ -38,6 +38,7 @@
 #include <cstdio>
 #include <cstdlib>
 #include <cstring>
+#include <functional>
 #include <mutex>
 #include <string>
 #include <thread>
@@ -101,7 +102,9 @@ struct DeviceState {
   Buffer tac_v, tac_idx, tac_offs, tac_G, tac_spreads, tac_w, tac_e, tac_code, tac_sorted,
       tac_tsum, tac_hist, tac_counts, tac_start, tac_C, tac_pre, tac_fch, tac_st, tac_bad,
       tac_done, tac_iters, tac_wcss, tac_prev, tac_empties, tac_assign, tac_probs, tac_tiles,
-      tac_chl, tac_cprob, tac_inv, tac_rsum, tac_ranges, tac_h, tac_ktiles, tac_big;
+      tac_chl, tac_cprob, tac_inv, tac_rsum, tac_ranges, tac_h, tac_ktiles, tac_big, tac_ids,
+      tac_pcnt, tac_pslots;
+  hipEvent_t tac_pre_ev[16] = {};  // chunk arrivals for the early spreads (a ring)
   bool crc_tx_ready = false;
   // training's second stream (two halves of the subspaces) and its events
   hipStream_t aux_stream[1] = {};
@@ -173,10 +176,14 @@ constexpr size_t kStageMin = 32u << 20;   // smaller uploads copy from pageable 
 // memcpy of the next: about 49 GB/s on an MI355X host, against 27 GB/s for a
 // hipMemcpyAsync from the same pageable memory.  The source may be reused
 // once this returns; a staging buffer is waited on before its next fill.
-int upload_host(DeviceState &ds, void *dst, const void *src, size_t bytes, hipStream_t s) {
+// With after_chunk, the chunks' copies are enqueued in order, and
+// after_chunk(end) runs right after each (end: the bytes enqueued so far),
+// from the thread that enqueued it; a non-zero status ends the upload.
+int upload_host(DeviceState &ds, void *dst, const void *src, size_t bytes, hipStream_t s,
+                const std::function<int(size_t)> *after_chunk = nullptr) {
   if (bytes < kStageMin) {
     HIP_TRY(hipMemcpyAsync(dst, src, bytes, hipMemcpyHostToDevice, s));
-    return TAC_OK;
+    return after_chunk ? (*after_chunk)(bytes) : TAC_OK;
   }
   constexpr int T = DeviceState::kStageThreads;
   for (int b = 0; b < DeviceState::kStageBufs; ++b) {
@@ -186,6 +193,9 @@ int upload_host(DeviceState &ds, void *dst, const void *src, size_t bytes, hipSt
   const size_t nch = (bytes + kStageChunk - 1) / kStageChunk;
   hipError_t errs[T] = {};
   const char *what[T] = {};
+  int cb_status[T] = {};
+  std::atomic<size_t> next{0};  // the next chunk to enqueue (ordered mode)
+  std::atomic<bool> failed{false};
   auto work = [&](int tid) {
     uint32_t k = 0;
     for (size_t c = (size_t)tid; c < nch; c += T, ++k) {
@@ -194,22 +204,38 @@ int upload_host(DeviceState &ds, void *dst, const void *src, size_t bytes, hipSt
       if (ds.stage_pending[b] && (e = hipEventSynchronize(ds.stage_ev[b])) != hipSuccess) {
         errs[tid] = e;
         what[tid] = "hipEventSynchronize";
+        failed = true;
         return;
       }
       const size_t off = c * kStageChunk, len = std::min(bytes - off, kStageChunk);
       memcpy(ds.stage[b], static_cast<const char *>(src) + off, len);
+      if (after_chunk) {
+        while (next.load(std::memory_order_acquire) != c) {
+          if (failed.load(std::memory_order_acquire)) return;
+          std::this_thread::yield();
+        }
+      }
       if ((e = hipMemcpyAsync(static_cast<char *>(dst) + off, ds.stage[b], len,
                               hipMemcpyHostToDevice, s)) != hipSuccess) {
         errs[tid] = e;
         what[tid] = "hipMemcpyAsync";
+        failed = true;
         return;
       }
       if ((e = hipEventRecord(ds.stage_ev[b], s)) != hipSuccess) {
         errs[tid] = e;
         what[tid] = "hipEventRecord";
+        failed = true;
         return;
       }
       ds.stage_pending[b] = true;
+      if (after_chunk) {
+        if ((cb_status[tid] = (*after_chunk)(off + len)) != TAC_OK) {
+          failed = true;
+          return;
+        }
+        next.store(c + 1, std::memory_order_release);
+      }
     }
   };
   std::thread helpers[T - 1];
@@ -218,6 +244,8 @@ int upload_host(DeviceState &ds, void *dst, const void *src, size_t bytes, hipSt
   for (auto &h : helpers) h.join();
   for (int t = 0; t < T; ++t)
     if (errs[t] != hipSuccess) return hip_status(what[t], errs[t]);
+  for (int t = 0; t < T; ++t)
+    if (cb_status[t] != TAC_OK) return cb_status[t];
   return TAC_OK;
 }
 
@@ -2835,17 +2863,99 @@ int tac_cluster_core(DeviceState &ds, hipStream_t s, const uint32_t *ids, uint64
   if ((!vectors_on_device && (st = ensure(ds, ds.tac_v, vbytes))) ||
       (st = ensure(ds, ds.tac_G, gbytes)))
     return st;
+  // Early spreads of the largest tokens (64-float rows): on the second
+  // stream the ids go up, the kTacPreSlots tokens with the most rows (at
+  // least pre_min) take slots, and as the rows arrive (each staged chunk of a
+  // host upload, or all at once when they are resident) those tokens' rows
+  // are copied into G and their Welford chains advance, beside the upload
+  // and the host grouping.  The main gather waits for the second stream.
+  // TAC_GPU_TAC_PRESPREAD=0 turns it off; TAC_GPU_TAC_PRESPREAD_MIN sets
+  // pre_min (16,384 rows).
+  const char *pre_env = getenv("TAC_GPU_TAC_PRESPREAD");
+  const char *pre_min_env = getenv("TAC_GPU_TAC_PRESPREAD_MIN");
+  const uint32_t pre_min = pre_min_env ? (uint32_t)std::max(1, atoi(pre_min_env)) : 16384u;
+  // (resident rows need 16-byte alignment: the copies move 16-byte pieces)
+  const bool early = dim == 64 && !fixed && nd <= (1ull << 17) && N >= pre_min &&
+                     (vectors_on_device ? ((uintptr_t)vectors & 15u) == 0 : vbytes >= kStageMin) &&
+                     !(pre_env && pre_env[0] == '0');
+  hipStream_t s2 = nullptr;
+  TacPreSlot *slots = nullptr;
+  uint64_t pre_rows = 0;  // input rows the slots have been advanced over
+  if (early) {
+    const uint64_t ninv_pre = N + kTacSpreadSlackRows;  // covers any token's rows
+    if ((st = ensure(ds, ds.tac_ids, N * sizeof(uint32_t))) ||
+        (st = ensure(ds, ds.tac_pcnt, (nd + kTacPreMaxSegs * kTacPreSlots) * sizeof(uint32_t))) ||
+        (st = ensure(ds, ds.tac_pslots, kTacPreSlots * sizeof(TacPreSlot))) ||
+        (st = ensure(ds, ds.tac_inv, ninv_pre * sizeof(float))))
+      return st;
+    if (!ds.aux_stream[0])
+      HIP_TRY(hipStreamCreateWithFlags(&ds.aux_stream[0], hipStreamNonBlocking));
+    if (!ds.aux_fork) HIP_TRY(hipEventCreateWithFlags(&ds.aux_fork, hipEventDisableTiming));
+    if (!ds.aux_join[0]) HIP_TRY(hipEventCreateWithFlags(&ds.aux_join[0], hipEventDisableTiming));
+    for (hipEvent_t &ev : ds.tac_pre_ev)
+      if (!ev) HIP_TRY(hipEventCreateWithFlags(&ev, hipEventDisableTiming));
+    s2 = ds.aux_stream[0];
+    slots = as<TacPreSlot>(ds.tac_pslots);
+    HIP_TRY(hipEventRecord(ds.aux_fork, s));
+    HIP_TRY(hipStreamWaitEvent(s2, ds.aux_fork, 0));
+    HIP_TRY(hipMemcpyAsync(ds.tac_ids.ptr, ids, N * sizeof(uint32_t), hipMemcpyHostToDevice, s2));
+    HIP_TRY(hipMemsetAsync(ds.tac_pcnt.ptr, 0, nd * sizeof(uint32_t), s2));
+    const dim3 hgrid((unsigned)std::min<uint64_t>((N + 16383) / 16384, 128),
+                     (unsigned)((nd + kTacHistTile - 1) / kTacHistTile));
+    tac_id_hist_kernel<<<hgrid, 1024, 0, s2>>>(as<uint32_t>(ds.tac_ids), N, (uint32_t)nd,
+                                              as<uint32_t>(ds.tac_pcnt));
+    LAUNCH_TRY("tac_id_hist_kernel");
+    tac_pre_select_kernel<<<1, 1024, 0, s2>>>(as<uint32_t>(ds.tac_pcnt), (uint32_t)nd, pre_min,
+                                              slots);
+    LAUNCH_TRY("tac_pre_select_kernel");
+    tac_inv_table_kernel<<<(unsigned)std::min<uint64_t>((ninv_pre + 255) / 256, 1u << 20), 256, 0,
+                           s2>>>(as<float>(ds.tac_inv), ninv_pre);
+    LAUNCH_TRY("tac_inv_table_kernel");
+  }
+  // advance the slots over input rows [pre_rows, r1) of rows (on the device),
+  // in pieces of kTacPreMaxSegs segments: count, copy, fold
+  auto pre_advance = [&](const float *rows, uint64_t r1) -> int {
+    constexpr uint64_t piece = (uint64_t)kTacPreSeg * kTacPreMaxSegs;
+    uint32_t *segcnt = as<uint32_t>(ds.tac_pcnt) + nd;  // past the id counts
+    const uint32_t *dids = as<uint32_t>(ds.tac_ids);
+    for (; pre_rows < r1;) {
+      const uint64_t e = std::min<uint64_t>(r1, pre_rows + piece);
+      const uint32_t a = (uint32_t)pre_rows, b = (uint32_t)e;
+      const uint32_t nseg = (uint32_t)((e - pre_rows + kTacPreSeg - 1) / kTacPreSeg);
+      tac_pre_count_kernel<<<nseg, 256, 0, s2>>>(dids, a, b, slots, segcnt);
+      LAUNCH_TRY("tac_pre_count_kernel");
+      tac_pre_copy_kernel<<<nseg, 256, 0, s2>>>(rows, dids, a, b, slots, segcnt,
+                                                as<float>(ds.tac_G));
+      LAUNCH_TRY("tac_pre_copy_kernel");
+      tac_spread64_kernel<<<kTacPreSlots, kTacSpread64Threads, 0, s2>>>(
+          as<float>(ds.tac_G), nullptr, as<float>(ds.tac_inv), nullptr, 0, slots, 1u, segcnt,
+          nseg);
+      LAUNCH_TRY("tac_spread64_kernel (resume)");
+      pre_rows = e;
+    }
+    return TAC_OK;
+  };
+  // after each staged chunk (in order): the second stream waits for its copy
+  uint32_t pre_chunk = 0;
+  const std::function<int(size_t)> after_chunk = [&](size_t end) -> int {
+    hipEvent_t ev = ds.tac_pre_ev[pre_chunk++ % 16u];
+    HIP_TRY(hipEventRecord(ev, s));
+    HIP_TRY(hipStreamWaitEvent(s2, ev, 0));
+    return pre_advance(as<float>(ds.tac_v), end / ((size_t)dim * sizeof(float)));
+  };
   // Host vectors go up once (the grouping runs on a second thread meanwhile,
   // the copy from pageable memory holding this one); device-resident ones
   // are gathered in place.
   const float *dv = vectors;
   if (!vectors_on_device) {
     std::thread grouper(group);
-    const int up = upload_host(ds, ds.tac_v.ptr, vectors, vbytes, s);
+    const int up =
+        upload_host(ds, ds.tac_v.ptr, vectors, vbytes, s, early ? &after_chunk : nullptr);
     grouper.join();
     if (up) return up;
     dv = as<float>(ds.tac_v);
   } else {
+    if (early && (st = pre_advance(vectors, N))) return st;
     // Nothing to overlap with here: the grouping runs on up to 8 threads when
     // the rows are many and the per-thread counts stay small.
     const uint32_t hc = std::thread::hardware_concurrency();
@@ -2860,6 +2970,10 @@ int tac_cluster_core(DeviceState &ds, hipStream_t s, const uint32_t *ids, uint64
     return st;
   float *G = as<float>(ds.tac_G);
   const uint64_t nf = (uint64_t)N * dim;
+  if (early) {  // the early spreads are done with G before the gather fills it
+    HIP_TRY(hipEventRecord(ds.aux_join[0], s2));
+    HIP_TRY(hipStreamWaitEvent(s, ds.aux_join[0], 0));
+  }
   // Grids stay far below a dispatch's 2^32 work-items: the gather and the
   // reciprocal table are grid-stride loops, the spreads run in token slices.
   constexpr uint64_t kMaxBlocks = 1ull << 20;
@@ -2883,7 +2997,8 @@ int tac_cluster_core(DeviceState &ds, hipStream_t s, const uint32_t *ids, uint64
       const unsigned nb = (unsigned)std::min<uint64_t>(nd - j0, kSlice);
 #define TAC_SPREAD(P) tac_spread_kernel<P><<<nb, kWave, lds, s>>>(G, doffs, dinv, dim, dsp, j0)
       if (dim == 64) {
-        tac_spread64_kernel<<<nb, kTacSpread64Threads, 0, s>>>(G, doffs, dinv, dsp, j0);
+        tac_spread64_kernel<<<nb, kTacSpread64Threads, 0, s>>>(G, doffs, dinv, dsp, j0, slots,
+                                                               0u);
       } else {
         switch (per) {  // dim <= kTacMaxDim: at most 8 dimensions per lane
           case 1: TAC_SPREAD(1); break;

@@ -297,9 +297,224 @@ __global__ __launch_bounds__(kWave) void tac_spread_kernel(const float* __restri
 constexpr uint32_t kTacSpread64Loaders = 4;
 constexpr uint32_t kTacSpread64Threads = (kTacSpread64Loaders + 1) * kWave;
 
+// Spreads of the largest tokens ahead of the grouping (64-float rows).  Up to
+// kTacPreSlots tokens with the most rows (at least a threshold) get a slot:
+// while the rows reach the device (chunk by chunk, in input order), their
+// rows are copied to their places in G, the grouped copy (in input order,
+// which is their order in G), and their Welford chains advance over the rows
+// copied so far (tac_spread64_kernel in resume mode).  The chain is the same
+// chain in the same order, so the spread launch that follows the grouping
+// only finishes these tokens from their slots.
+constexpr uint32_t kTacPreSlots = 8;
+constexpr uint32_t kTacPreNone = 0xFFFFFFFFu;
+struct TacPreSlot {
+  float mean[64], m2[64];  // the chain's state, one dimension per entry
+  uint32_t tok;            // token id, or kTacPreNone for an empty slot
+  uint32_t lo;             // the token's first row in G
+  uint32_t rows;           // rows copied to G so far
+  uint32_t folded;         // rows folded into mean and m2 so far
+};
+
+// Rows per token id (ids < nd).  Block (x, y) counts the ids of tile y
+// (kTacHistTile ids) among its share of the rows in LDS, then adds its
+// non-zero counters to cnt: a hot id takes one device atomic per block, not
+// one per row.
+constexpr uint32_t kTacHistTile = 16384;
+__global__ __launch_bounds__(1024) void tac_id_hist_kernel(const uint32_t* __restrict__ ids,
+                                                           uint64_t n, uint32_t nd,
+                                                           uint32_t* __restrict__ cnt) {
+  __shared__ uint32_t h[kTacHistTile];
+  const uint32_t id0 = blockIdx.y * kTacHistTile;
+  const uint32_t span = nd - id0 < kTacHistTile ? nd - id0 : kTacHistTile;
+  for (uint32_t i = threadIdx.x; i < span; i += blockDim.x) h[i] = 0u;
+  __syncthreads();
+  const uint64_t per = (n + gridDim.x - 1) / gridDim.x;
+  const uint64_t a = (uint64_t)blockIdx.x * per;
+  const uint64_t b = a + per < n ? a + per : n;
+  for (uint64_t i = a + threadIdx.x; i < b; i += blockDim.x) {
+    const uint32_t d = ids[i] - id0;  // ids below id0 wrap past span
+    if (d < span) atomicAdd(&h[d], 1u);
+  }
+  __syncthreads();
+  for (uint32_t i = threadIdx.x; i < span; i += blockDim.x)
+    if (h[i] != 0u) atomicAdd(&cnt[id0 + i], h[i]);
+}
+
+// One block of 1024: the kTacPreSlots tokens with the most rows (ties: the
+// lower id), those with at least nmin rows, each with its first row in G
+// (the rows of every lower id); the slots' chains start empty.
+__global__ __launch_bounds__(1024) void tac_pre_select_kernel(const uint32_t* __restrict__ cnt,
+                                                              uint32_t nd, uint32_t nmin,
+                                                              TacPreSlot* __restrict__ slots) {
+  __shared__ uint64_t s_red[1024 / kWave];
+  __shared__ uint32_t s_tok[kTacPreSlots];
+  const uint32_t t = threadIdx.x, lane = t % kWave, wv = t / kWave;
+  constexpr uint32_t NW = 1024 / kWave;
+  for (uint32_t q = 0; q < kTacPreSlots; ++q) {
+    // key = rows << 32 | ~id: the largest key is the most rows, then the lowest id
+    uint64_t best = 0;
+    for (uint32_t j = t; j < nd; j += 1024) {
+      bool taken = false;
+      for (uint32_t r = 0; r < q; ++r) taken = taken || s_tok[r] == j;
+      const uint64_t key = taken ? 0ull : ((uint64_t)cnt[j] << 32) | (uint32_t)~j;
+      best = key > best ? key : best;
+    }
+    for (int o = kWave / 2; o > 0; o >>= 1) {
+      const uint64_t v = __shfl_xor(best, o, kWave);
+      best = v > best ? v : best;
+    }
+    if (lane == 0) s_red[wv] = best;
+    __syncthreads();
+    if (t == 0) {
+      uint64_t b = 0;
+      for (uint32_t r = 0; r < NW; ++r) b = s_red[r] > b ? s_red[r] : b;
+      s_tok[q] = (uint32_t)(b >> 32) >= nmin && nmin > 0 ? ~(uint32_t)b : kTacPreNone;
+    }
+    __syncthreads();
+  }
+  for (uint32_t q = 0; q < kTacPreSlots; ++q) {
+    const uint32_t tok = s_tok[q];  // block-uniform
+    uint64_t part = 0;
+    if (tok != kTacPreNone)
+      for (uint32_t j = t; j < tok; j += 1024) part += cnt[j];
+    for (int o = kWave / 2; o > 0; o >>= 1) part += __shfl_xor(part, o, kWave);
+    if (lane == 0) s_red[wv] = part;
+    __syncthreads();
+    if (t < 64) {
+      slots[q].mean[t] = 0.0f;
+      slots[q].m2[t] = 0.0f;
+    }
+    if (t == 0) {
+      uint64_t lo = 0;
+      for (uint32_t r = 0; r < NW; ++r) lo += s_red[r];
+      slots[q].tok = tok;
+      slots[q].lo = (uint32_t)lo;
+      slots[q].rows = 0;
+      slots[q].folded = 0;
+    }
+    __syncthreads();
+  }
+}
+
+// The slots' rows among input rows [r0, r1) of V (64 floats each) go to G
+// after the rows copied before, in input order, in two launches over
+// segments of kTacPreSeg rows (at most kTacPreMaxSegs per range): a count of
+// each slot's rows per segment, then each segment's copy at the count of the
+// segments before it.  Rows in a segment are taken in four 256-row groups.
+constexpr uint32_t kTacPreSeg = 1024;
+constexpr uint32_t kTacPreMaxSegs = 128;
+
+__global__ __launch_bounds__(256) void tac_pre_count_kernel(const uint32_t* __restrict__ ids,
+                                                            uint32_t r0, uint32_t r1,
+                                                            const TacPreSlot* __restrict__ slots,
+                                                            uint32_t* __restrict__ segcnt) {
+  __shared__ uint32_t s_wc[kTacPreSlots][4];
+  const uint32_t seg0 = r0 + blockIdx.x * kTacPreSeg;
+  const uint32_t lane = threadIdx.x % kWave, wv = threadIdx.x / kWave;
+  uint32_t id[4];
+#pragma unroll
+  for (uint32_t q = 0; q < 4; ++q) {
+    const uint32_t r = seg0 + q * 256u + threadIdx.x;
+    id[q] = r < r1 ? ids[r] : kTacPreNone;
+  }
+#pragma unroll
+  for (uint32_t sl = 0; sl < kTacPreSlots; ++sl) {
+    const uint32_t tok = slots[sl].tok;
+    uint32_t c = 0;
+#pragma unroll
+    for (uint32_t q = 0; q < 4; ++q)
+      c += (uint32_t)__popcll(__ballot(tok != kTacPreNone && id[q] == tok));
+    if (lane == 0) s_wc[sl][wv] = c;
+  }
+  __syncthreads();
+  if (threadIdx.x < kTacPreSlots) {
+    const uint32_t sl = threadIdx.x;
+    segcnt[blockIdx.x * kTacPreSlots + sl] = s_wc[sl][0] + s_wc[sl][1] + s_wc[sl][2] + s_wc[sl][3];
+  }
+}
+
+__global__ __launch_bounds__(256) void tac_pre_copy_kernel(const float* __restrict__ V,
+                                                           const uint32_t* __restrict__ ids,
+                                                           uint32_t r0, uint32_t r1,
+                                                           const TacPreSlot* __restrict__ slots,
+                                                           const uint32_t* __restrict__ segcnt,
+                                                           float* __restrict__ G) {
+  __shared__ uint32_t s_src[kTacPreSeg];
+  __shared__ uint64_t s_dst[kTacPreSeg];
+  __shared__ uint32_t s_wc[kTacPreSlots][4][4];  // hits per slot, 256-row group, wave
+  __shared__ uint32_t s_hc[4][4];                // hits of any slot per group, wave
+  __shared__ uint64_t s_at[kTacPreSlots];        // the segment's first place per slot
+  const uint32_t seg0 = r0 + blockIdx.x * kTacPreSeg;
+  const uint32_t t = threadIdx.x, lane = t % kWave, wv = t / kWave;
+  const uint64_t below = (1ull << lane) - 1ull;
+  if (t < kTacPreSlots) {
+    uint64_t at = (uint64_t)slots[t].lo + slots[t].rows;
+    for (uint32_t g = 0; g < blockIdx.x; ++g) at += segcnt[g * kTacPreSlots + t];
+    s_at[t] = at;
+  }
+  // the slot of each of this thread's rows (each row has at most one), its
+  // rank among the slot's rows in its wave, and its place among the hits
+  int sl_of[4];
+  uint32_t rk[4], hp[4];
+#pragma unroll
+  for (uint32_t q = 0; q < 4; ++q) {
+    const uint32_t r = seg0 + q * 256u + t;
+    const uint32_t id = r < r1 ? ids[r] : kTacPreNone;
+    sl_of[q] = -1;
+#pragma unroll
+    for (uint32_t sl = 0; sl < kTacPreSlots; ++sl) {
+      const uint32_t tok = slots[sl].tok;
+      if (tok != kTacPreNone && id == tok) sl_of[q] = (int)sl;
+    }
+  }
+#pragma unroll
+  for (uint32_t q = 0; q < 4; ++q) {
+    rk[q] = 0;
+#pragma unroll
+    for (uint32_t sl = 0; sl < kTacPreSlots; ++sl) {
+      const uint64_t b = __ballot(sl_of[q] == (int)sl);
+      if (sl_of[q] == (int)sl) rk[q] = (uint32_t)__popcll(b & below);
+      if (lane == 0) s_wc[sl][q][wv] = (uint32_t)__popcll(b);
+    }
+    const uint64_t hb = __ballot(sl_of[q] >= 0);
+    hp[q] = (uint32_t)__popcll(hb & below);
+    if (lane == 0) s_hc[q][wv] = (uint32_t)__popcll(hb);
+  }
+  __syncthreads();
+  uint32_t m = 0;
+#pragma unroll
+  for (uint32_t q = 0; q < 4; ++q) {
+    uint32_t hbefore = m;
+    for (uint32_t w = 0; w < wv; ++w) hbefore += s_hc[q][w];
+    if (sl_of[q] >= 0) {
+      const uint32_t sl = (uint32_t)sl_of[q];
+      uint64_t dst = s_at[sl] + rk[q];
+      for (uint32_t qq = 0; qq < q; ++qq)
+        dst += s_wc[sl][qq][0] + s_wc[sl][qq][1] + s_wc[sl][qq][2] + s_wc[sl][qq][3];
+      for (uint32_t w = 0; w < wv; ++w) dst += s_wc[sl][q][w];
+      s_src[hbefore + hp[q]] = seg0 + q * 256u + t;
+      s_dst[hbefore + hp[q]] = dst;
+    }
+    m += s_hc[q][0] + s_hc[q][1] + s_hc[q][2] + s_hc[q][3];
+  }
+  __syncthreads();
+  // 16 float4 per row, 16 rows per pass
+  for (uint32_t f = t; f < m * 16u; f += 256u) {
+    const uint32_t c4 = f % 16u;
+    const tac_floatx4 v = reinterpret_cast<const tac_floatx4*>(V + (uint64_t)s_src[f / 16u] * 64u)[c4];
+    reinterpret_cast<tac_floatx4*>(G + s_dst[f / 16u] * 64u)[c4] = v;
+  }
+}
+
+// With resume set, block q advances slot q's chain over the rows the last
+// copy added (segcnt: its nseg segment counts; offs, spreads and j0 unused);
+// otherwise a token that holds a slot of pre (nullable) only takes its
+// finished chain from it.
 __global__ __launch_bounds__(kTacSpread64Threads) void tac_spread64_kernel(
     const float* __restrict__ G, const uint32_t* __restrict__ offs,
-    const float* __restrict__ inv, float* __restrict__ spreads, uint64_t j0) {
+    const float* __restrict__ inv, float* __restrict__ spreads, uint64_t j0,
+    TacPreSlot* __restrict__ pre, uint32_t resume, const uint32_t* __restrict__ segcnt = nullptr,
+    uint32_t nseg = 0) {
   constexpr uint32_t R = kTacSpread64Rows;
   constexpr uint32_t GW = R / 4 / kTacSpread64Loaders;  // 16-byte groups per loader per batch
   constexpr int NR = 4;                               // batches in flight per loader
@@ -310,12 +525,44 @@ __global__ __launch_bounds__(kTacSpread64Threads) void tac_spread64_kernel(
   const uint64_t j = j0 + blockIdx.x;  // launched in slices of tokens
   const uint32_t lane = threadIdx.x % kWave;
   const uint32_t w = __builtin_amdgcn_readfirstlane(threadIdx.x / kWave);  // wave-uniform
-  const uint32_t lo = offs[j], hi = offs[j + 1];
-  if (hi == lo) {
-    if (threadIdx.x == 0) spreads[j] = 0.0f;
-    return;
+  // rows [lo, lo + n) of G fold, their reciprocals from inv[ib]; a finished
+  // token skips the fold
+  uint32_t lo, n, ib = 0, rows_end = 0;
+  bool finished = false;
+  float mean = 0.0f, m2 = 0.0f;
+  TacPreSlot* ps = nullptr;
+  if (resume) {
+    ps = pre + blockIdx.x;
+    if (ps->tok == kTacPreNone) return;  // block-uniform
+    rows_end = ps->rows;
+    for (uint32_t g = 0; g < nseg; ++g) rows_end += segcnt[g * kTacPreSlots + blockIdx.x];
+    ib = ps->folded;
+    lo = ps->lo + ib;
+    n = rows_end - ib;
+    if (n == 0) {
+      if (threadIdx.x == 0) ps->rows = rows_end;  // (= folded)
+      return;
+    }
+    mean = ps->mean[lane];
+    m2 = ps->m2[lane];
+  } else {
+    lo = offs[j];
+    const uint32_t hi = offs[j + 1];
+    if (hi == lo) {
+      if (threadIdx.x == 0) spreads[j] = 0.0f;
+      return;
+    }
+    n = hi - lo;
+    if (pre) {
+#pragma unroll
+      for (uint32_t q = 0; q < kTacPreSlots; ++q)
+        if (pre[q].tok == (uint32_t)j && pre[q].folded == n) {  // its chain covered all n rows
+          finished = true;
+          m2 = pre[q].m2[lane];
+        }
+    }
   }
-  const uint32_t n = hi - lo, nb = (n + R - 1) / R;
+  const uint32_t nb = (n + R - 1) / R;
   const tac_floatx4* g4 = reinterpret_cast<const tac_floatx4*>(G + (uint64_t)lo * 64);
   tac_floatx4 buf[NR][GW];
   float ivb[NR];
@@ -334,7 +581,7 @@ __global__ __launch_bounds__(kTacSpread64Threads) void tac_spread64_kernel(
 #pragma unroll
     for (uint32_t g = 0; g < GW; ++g)
       buf[slot][g] = *reinterpret_cast<const tac_floatx4*>(p + g * 1024u);
-    ivb[slot] = inv[(uint64_t)k * R + lane];
+    ivb[slot] = inv[(uint64_t)ib + (uint64_t)k * R + lane];
   };
   auto store = [&](int slot, uint32_t k) {
     char* x = reinterpret_cast<char*>(xs[k & 1u]) + lw * GW * 1024u + voff;
@@ -343,7 +590,6 @@ __global__ __launch_bounds__(kTacSpread64Threads) void tac_spread64_kernel(
       *reinterpret_cast<tac_floatx4*>(x + g * 1024u) = buf[slot][g];
     is[k & 1u][lane] = ivb[slot];  // every loader writes the same values
   };
-  float mean = 0.0f, m2 = 0.0f;
   auto fold = [&](uint32_t k) {
     const float* x = xs[k & 1u];
     const float* iv = is[k & 1u];
@@ -407,7 +653,9 @@ __global__ __launch_bounds__(kTacSpread64Threads) void tac_spread64_kernel(
   // slot of batch k; batch k + 1 goes to the other LDS buffer
   // The loaders and the folding wave run separate loops with the same
   // number of block barriers (one before step 0, one after each step).
-  if (w > 0) {
+  if (finished) {
+    // nothing to fold
+  } else if (w > 0) {
 #pragma unroll
     for (int q = 0; q < NR; ++q) load(q, (uint32_t)q);
     store(0, 0);
@@ -429,6 +677,17 @@ __global__ __launch_bounds__(kTacSpread64Threads) void tac_spread64_kernel(
       fold(k);
       __syncthreads();
     }
+  }
+  if (resume) {
+    if (w == 0) {
+      ps->mean[lane] = mean;
+      ps->m2[lane] = m2;
+    }
+    if (threadIdx.x == 0) {
+      ps->rows = rows_end;
+      ps->folded = rows_end;
+    }
+    return;
   }
   if (w == 0) m2s[lane] = m2;
   __syncthreads();

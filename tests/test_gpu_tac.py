@@ -191,6 +191,34 @@ def test_device_resident_vectors(gpu, n, dim):
     assert np.float32(got.wcss_total).tobytes() == np.float32(ref.wcss_total).tobytes()
 
 
+@pytest.mark.parametrize("resident", [False, True])
+def test_early_spreads(gpu, monkeypatch, resident):
+    """The spreads of the largest tokens advanced while the rows arrive: each
+    8 MB staged chunk of the 51 MB host upload, or all rows at once when they
+    are resident on the device.  TAC_GPU_TAC_PRESPREAD_MIN=500 gives all 8
+    slots a token (chunks end inside their runs of rows).  Both that path and
+    the one with it off (TAC_GPU_TAC_PRESPREAD=0) give the oracle's bits."""
+    from tac_gpu import device
+    ids, v = synth.tac_vectors(200_000, 64, 4096, 1.05, 0.15, 3)
+    assert np.sort(np.bincount(ids))[-8] >= 500
+    kap = _feasible_kappa(ids)
+    ref = orc.tac_cluster_flat(ids, v, 64, orc.tac_params(kap, 5))
+    assert ref.status == 0
+    monkeypatch.setenv("TAC_GPU_TAC_PRESPREAD_MIN", "500")
+    dv = device.DeviceArray.from_host(np.ascontiguousarray(v)) if resident else None
+    try:
+        for on in ("1", "0"):
+            monkeypatch.setenv("TAC_GPU_TAC_PRESPREAD", on)
+            got = tac.cluster_flat(ids, dv if resident else v, 64, _params(kap, 5))
+            assert np.array_equal(got.kappa_per_token, ref.kappa_per_token), on
+            assert got.centroids.tobytes() == ref.centroids.tobytes(), on
+            assert np.array_equal(got.assignments, ref.assignments), on
+            assert np.float32(got.wcss_total).tobytes() == np.float32(ref.wcss_total).tobytes()
+    finally:
+        if dv is not None:
+            dv.free()
+
+
 def _expect(ids, v, dim, p_kw, exc):
     ref = orc.tac_cluster_flat(ids, v, dim, orc.tac_params(**p_kw))
     assert ref.status == exc.status
