@@ -39,6 +39,8 @@
 #include <cstdlib>
 #include <cstring>
 #include <functional>
+#include <deque>
+#include <condition_variable>
 #include <mutex>
 #include <string>
 #include <thread>
@@ -2935,13 +2937,48 @@ int tac_cluster_core(DeviceState &ds, hipStream_t s, const uint32_t *ids, uint64
     }
     return TAC_OK;
   };
-  // after each staged chunk (in order): the second stream waits for its copy
+  // Host upload: after the last staged chunk of each piece of rows (the
+  // callback runs in chunk order) an event goes on the upload stream, and a
+  // launcher thread makes the second stream wait for it and advances the
+  // slots, so the upload threads make one extra call per piece.  Re-recording
+  // one of the 16 ring events before its wait is issued only makes that wait
+  // later.
+  constexpr uint64_t kPrePieceRows = (uint64_t)kTacPreSeg * kTacPreMaxSegs;
   uint32_t pre_chunk = 0;
+  uint64_t pre_mark = 0;  // rows covered by the pieces handed over so far
+  std::mutex pre_mu;
+  std::condition_variable pre_cv;
+  std::deque<std::pair<hipEvent_t, uint64_t>> pre_q;
+  bool pre_end = false;
+  int pre_st = TAC_OK;
   const std::function<int(size_t)> after_chunk = [&](size_t end) -> int {
+    const uint64_t r1 = end / ((size_t)dim * sizeof(float));
+    if (r1 < pre_mark + kPrePieceRows && end < vbytes) return TAC_OK;
+    pre_mark = r1;
     hipEvent_t ev = ds.tac_pre_ev[pre_chunk++ % 16u];
     HIP_TRY(hipEventRecord(ev, s));
-    HIP_TRY(hipStreamWaitEvent(s2, ev, 0));
-    return pre_advance(as<float>(ds.tac_v), end / ((size_t)dim * sizeof(float)));
+    {
+      std::lock_guard<std::mutex> g(pre_mu);
+      pre_q.emplace_back(ev, r1);
+    }
+    pre_cv.notify_one();
+    return TAC_OK;
+  };
+  auto launcher = [&] {
+    for (;;) {
+      std::pair<hipEvent_t, uint64_t> item;
+      {
+        std::unique_lock<std::mutex> g(pre_mu);
+        pre_cv.wait(g, [&] { return pre_end || !pre_q.empty(); });
+        if (pre_q.empty()) return;  // pre_end
+        item = pre_q.front();
+        pre_q.pop_front();
+      }
+      if (pre_st != TAC_OK) continue;  // drain after a failure
+      const hipError_t e = hipStreamWaitEvent(s2, item.first, 0);
+      pre_st = e != hipSuccess ? hip_status("hipStreamWaitEvent", e)
+                               : pre_advance(as<float>(ds.tac_v), item.second);
+    }
   };
   // Host vectors go up once (the grouping runs on a second thread meanwhile,
   // the copy from pageable memory holding this one); device-resident ones
@@ -2949,10 +2986,21 @@ int tac_cluster_core(DeviceState &ds, hipStream_t s, const uint32_t *ids, uint64
   const float *dv = vectors;
   if (!vectors_on_device) {
     std::thread grouper(group);
+    std::thread pre_launcher;
+    if (early) pre_launcher = std::thread(launcher);
     const int up =
         upload_host(ds, ds.tac_v.ptr, vectors, vbytes, s, early ? &after_chunk : nullptr);
+    if (early) {
+      {
+        std::lock_guard<std::mutex> g(pre_mu);
+        pre_end = true;
+      }
+      pre_cv.notify_one();
+      pre_launcher.join();
+    }
     grouper.join();
     if (up) return up;
+    if (pre_st) return pre_st;
     dv = as<float>(ds.tac_v);
   } else {
     if (early && (st = pre_advance(vectors, N))) return st;
