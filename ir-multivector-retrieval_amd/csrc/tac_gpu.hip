@@ -112,7 +112,7 @@ struct DeviceState {
   hipStream_t aux_stream[1] = {};
   hipEvent_t aux_fork = nullptr, aux_join[1] = {};
   // pinned staging for large uploads from pageable host memory (upload_host)
-  static constexpr int kStageThreads = 4, kStageBufs = 2 * kStageThreads;
+  static constexpr int kStageThreads = 8, kStageBufs = 2 * kStageThreads;
   void *stage[kStageBufs] = {};
   hipEvent_t stage_ev[kStageBufs] = {};
   bool stage_pending[kStageBufs] = {};
@@ -175,7 +175,8 @@ constexpr size_t kStageMin = 32u << 20;   // smaller uploads copy from pageable 
 // Host-to-device copy of `bytes` from pageable memory, enqueued on s.  Large
 // copies pass through pinned staging buffers that kStageThreads host threads
 // fill (two buffers each, used in turn), so the DMA of one chunk overlaps the
-// memcpy of the next: about 49 GB/s on an MI355X host, against 27 GB/s for a
+// memcpy of the next: about 56 GB/s with eight threads on an MI355X host (49
+// with four), against 27 GB/s for a
 // hipMemcpyAsync from the same pageable memory.  The source may be reused
 // once this returns; a staging buffer is waited on before its next fill.
 // With after_chunk, the chunks' copies are enqueued in order, and
