@@ -2718,6 +2718,18 @@ struct TacPlan {
   uint64_t hist_total = 0;
   uint64_t rsum_total = 0;
   uint32_t kmax = 0;      // largest k of a non-degenerate problem
+  void reset() {  // empty, keeping the lists' capacity
+    probs.clear();
+    tiles.clear();
+    chunks.clear();
+    ranges.clear();
+    cprob.clear();
+    token.clear();
+    tiles_upto.clear();
+    probs_upto.clear();
+    hist_total = rsum_total = 0;
+    kmax = 0;
+  }
 };
 
 int tac_plan(const std::vector<uint32_t> &freqs, const std::vector<uint32_t> &offs,
@@ -2725,6 +2737,7 @@ int tac_plan(const std::vector<uint32_t> &freqs, const std::vector<uint32_t> &of
              uint64_t seed, uint32_t rt, uint64_t kappa_total, TacPlan *pl) {
   // Problems in order of effective k (0 for degenerate ones), descending,
   // ties in token order: a stable counting sort over the tokens in id order.
+  pl->reset();
   const uint32_t nd = (uint32_t)freqs.size();
   auto keff = [&](uint32_t j) { return kappa[j] >= freqs[j] ? 0u : kappa[j]; };
   size_t P = 0;
@@ -2812,8 +2825,17 @@ int tac_cluster_core(DeviceState &ds, hipStream_t s, const uint32_t *ids, uint64
   if (N > 0xFFFFFFFFull || (uint64_t)N * dim > (1ull << 38) || nd > 0x7FFFFFFFull)
     return TAC_ERR_UNSUPPORTED;
   int st;
-  // CSR grouping by token id, ascending input order inside a token (tac.zig:575-602)
-  std::vector<uint32_t> freqs(nd, 0), offs(nd + 1, 0), idx(N);
+  // CSR grouping by token id, ascending input order inside a token (tac.zig:575-602).
+  // The call's large host lists live in per-thread caches that keep their
+  // capacity, so repeated calls do not fault in fresh pages for them.
+  static thread_local std::vector<uint32_t> idx_cache, cnt_cache;
+  static thread_local std::vector<uint64_t> goff_cache;
+  static thread_local std::vector<KppState> hst_cache;
+  static thread_local std::vector<KppTile> ktiles_cache;
+  static thread_local TacPlan plan_cache;
+  std::vector<uint32_t> freqs(nd, 0), offs(nd + 1, 0);
+  std::vector<uint32_t> &idx = idx_cache;
+  idx.resize(N);
   auto group = [&] {
     if (fixed) {  // one token: the rows in input order
       freqs[0] = (uint32_t)N;
@@ -2831,7 +2853,8 @@ int tac_cluster_core(DeviceState &ds, hipStream_t s, const uint32_t *ids, uint64
   // runs of the slices before it, so the order inside a token stays the
   // input order and idx, offs and freqs equal the one-thread result.
   auto group_threads = [&](uint32_t T) {
-    std::vector<uint32_t> cnt((size_t)T * nd, 0);
+    std::vector<uint32_t> &cnt = cnt_cache;
+    cnt.assign((size_t)T * nd, 0u);
     auto each = [&](auto fn) {
       std::vector<std::thread> th;
       for (uint32_t t = 1; t < T; ++t) th.emplace_back(fn, t);
@@ -3079,12 +3102,13 @@ int tac_cluster_core(DeviceState &ds, hipStream_t s, const uint32_t *ids, uint64
   }
   for (uint64_t j = 0; j < nd; ++j)
     if (freqs[j] > 0 && kappa[j] == 0) return TAC_ERR_BUDGET_TOO_SMALL;
-  std::vector<uint64_t> goff(nd + 1, 0);
+  std::vector<uint64_t> &goff = goff_cache;
+  goff.assign(nd + 1, 0);
   for (uint64_t j = 0; j < nd; ++j) goff[j + 1] = goff[j] + kappa[j];
   if (goff[nd] != prm.kappa_total) return TAC_ERR_BUDGET_TOO_SMALL;
   const uint64_t K = prm.kappa_total;
 
-  TacPlan pl;
+  TacPlan &pl = plan_cache;
   if ((st = tac_plan(freqs, offs, kappa, goff, prm.seed, rt, K, &pl))) return st;
 
   // The Lloyd kernels launch one block of at most 256 work-items per tile,
@@ -3099,7 +3123,8 @@ int tac_cluster_core(DeviceState &ds, hipStream_t s, const uint32_t *ids, uint64
   for (uint32_t q = 0; q < P; ++q) done0[q] = pl.probs[q].degenerate;
   // the tiles of the k-means++ rounds (problems in k-descending order, so
   // round c covers the first tiles_upto[c])
-  std::vector<KppTile> ktiles(std::max<uint32_t>(pl.tiles_upto.empty() ? 0u : pl.tiles_upto[0], 1u));
+  std::vector<KppTile> &ktiles = ktiles_cache;
+  ktiles.assign(std::max<uint32_t>(pl.tiles_upto.empty() ? 0u : pl.tiles_upto[0], 1u), KppTile{});
   for (uint32_t b = 0; b < (pl.tiles_upto.empty() ? 0u : pl.tiles_upto[0]); ++b) {
     const TacTile &tl = pl.tiles[b];
     const TacProblem &pq = pl.probs[tl.prob];
@@ -3252,7 +3277,8 @@ int tac_cluster_core(DeviceState &ds, hipStream_t s, const uint32_t *ids, uint64
   };
   // a problem's state after its last round k - 1 sits in half (k - 1) & 1;
   // returns the earliest pending round (kmax if none)
-  std::vector<KppState> hst(2 * (size_t)P);
+  std::vector<KppState> &hst = hst_cache;
+  hst.resize(2 * (size_t)P);
   auto final_states = [&](uint32_t *pending) -> int {
     HIP_TRY(hipMemcpyAsync(hst.data(), kst, 2 * (size_t)P * sizeof(KppState),
                            hipMemcpyDeviceToHost, s));
